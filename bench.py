@@ -1,0 +1,245 @@
+"""Benchmark of the needle.js decode hot path on one MI355X.
+
+Prints ONE JSON line.  `value` is the int8 matvec throughput (GB/s of
+algorithmic bytes) on the isolated matvec workload: W int8 [4096][4096] with
+fp32 scales per group of 32, x fp32 [4096], batch 1.  The inputs are resident
+in HBM before timing starts; the timed launches rotate over enough weight
+replicas (> 256 MB) that every launch streams its weights from HBM rather
+than from the 256 MB Infinity Cache.  Launches are captured in one HIP graph
+and replayed; HIP events on the replay stream bracket the timed region.
+
+`parts` adds the other headline numbers: batch-8 matvec and single-query
+int8-KV decode attention (8 heads x 64, contexts 512/2048/8192), each with
+its HBM roofline fraction (peak 8 TB/s) and, for reference, the same kernel
+on an Infinity-Cache-resident working set.
+
+`cpu_baseline` times the oracle (the C restatement of the reference CPU
+path, one thread) on a bounded sample of the same matvec workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT, ROOT / "needle.js_amd"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+ROTATE_BYTES = 640 << 20  # rotation set well above the Infinity Cache
+
+
+def matvec_bytes(n, k, g, batch):
+    """Algorithmic bytes of one int8 matvec launch: codes + scales + x + y."""
+    return n * k + n * (k // g) * 4 + batch * k * 4 + batch * n * 4
+
+
+def attention_bytes(length, heads):
+    """K and V codes (64 B each per token-head), their f32 scales, q and out."""
+    return heads * length * (64 + 64 + 4 + 4) + 2 * heads * 64 * 4
+
+
+class GraphTimer:
+    """Captures `launch(stream)` calls into one HIP graph and times replays."""
+
+    def __init__(self, torch, launches):
+        self.torch = torch
+        self.graph = torch.cuda.CUDAGraph()
+        self.stream = torch.cuda.Stream()
+        self.n = len(launches)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(self.stream):
+            handle = self.stream.cuda_stream
+            for f in launches:  # one eager pass before capture
+                f(handle)
+        self.stream.synchronize()
+        with torch.cuda.graph(self.graph, stream=self.stream):
+            handle = torch.cuda.current_stream().cuda_stream
+            for f in launches:
+                f(handle)
+        torch.cuda.synchronize()
+
+    def time(self, replays, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            self.graph.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(self.stream):
+            start.record(self.stream)
+            for _ in range(replays):
+                self.graph.replay()
+            stop.record(self.stream)
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(stop)
+        return ms / (replays * self.n)  # ms per launch
+
+
+def bench_matvec(torch, hip, n, k, g, batch, steps, warmup, rotate=True):
+    import ctypes as C
+
+    import numpy as np
+
+    from needle_hip import lib as L
+    from needle_hip import synth
+
+    per = matvec_bytes(n, k, g, batch)
+    replicas = max(1, math.ceil(ROTATE_BYTES / per)) if rotate else 1
+    w, s = synth.int8_matrix(2026, f"bench-w{n}x{k}", n, k, g)
+    mats = []
+    for _ in range(replicas):
+        h = C.c_void_p()
+        hip._check(hip.lib.nd_mat_upload_i8(hip.ctx, L.ptr(w), L.ptr(s), n, k, g, C.byref(h)))
+        mats.append(h)
+    x = torch.from_numpy(synth.Stream(2026, "bench-x").normal((batch, k))).cuda()
+    y = torch.empty((batch, n), dtype=torch.float32, device="cuda")
+
+    def make(h):
+        return lambda stream: hip._check(hip.lib.nd_matvec_d(
+            hip.ctx, h, x.data_ptr(), batch, 0, n, y.data_ptr(), C.c_void_p(stream)))
+
+    timer = GraphTimer(torch, [make(h) for h in mats])
+    replays = max(1, math.ceil(steps / timer.n))
+    ms = timer.time(replays, warmup)
+    for h in mats:
+        hip.lib.nd_mat_free(hip.ctx, h)
+    gbs = per / (ms * 1e-3) / 1e9
+    return {"bytes_per_launch": per, "replicas": replicas, "launches": replays * timer.n,
+            "ms_per_launch": ms, "GBps": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
+
+
+def bench_attention(torch, hip, length, heads, steps, warmup, rotate=True):
+    import ctypes as C
+
+    from needle_hip import HipKvCache, synth
+
+    per = attention_bytes(length, heads)
+    replicas = max(1, math.ceil(ROTATE_BYTES / per)) if rotate else 1
+    st = synth.Stream(7, f"bench-att{length}")
+    K, V = st.normal((length, heads, 64)), st.normal((length, heads, 64))
+    caches = []
+    for _ in range(replicas):
+        kv = HipKvCache(hip, 1, heads, max_length=length)
+        kv.store(0, 0, K, V)
+        caches.append(kv)
+    q = torch.from_numpy(st.normal((heads * 64,))).cuda()
+    out = torch.empty(heads * 64, dtype=torch.float32, device="cuda")
+
+    def make(kv):
+        return lambda stream: hip._check(hip.lib.nd_attention_d(
+            hip.ctx, kv.handle, 0, length - 1, q.data_ptr(), heads, out.data_ptr(),
+            C.c_void_p(stream)))
+
+    timer = GraphTimer(torch, [make(kv) for kv in caches])
+    replays = max(1, math.ceil(steps / timer.n))
+    ms = timer.time(replays, warmup)
+    for kv in caches:
+        kv.free()
+    gbs = per / (ms * 1e-3) / 1e9
+    return {"bytes_per_call": per, "replicas": replicas, "calls": replays * timer.n,
+            "ms_per_call": ms, "GBps": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
+
+
+def cpu_baseline_matvec(n, k, g, seconds):
+    """The oracle (one thread) on the same matvec workload, timed on this host."""
+    import numpy as np
+
+    import oracle
+    from needle_hip import synth
+
+    w, s = synth.int8_matrix(2026, f"bench-w{n}x{k}", n, k, g)
+    x = synth.Stream(2026, "bench-x").normal((1, k))
+    oracle.matvec_i8(w, s, g, x)  # warm
+    calls = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.matvec_i8(w, s, g, x)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    per = matvec_bytes(n, k, g, 1)
+    return {"value": per * calls / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{calls} calls of the oracle int8 matvec N={n} K={k} G={g} batch 1 "
+                      f"({el:.1f} s, host has {os.cpu_count()} cores)"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3200, help="timed matvec launches")
+    ap.add_argument("--warmup", type=int, default=3, help="untimed graph replays")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--skip-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
+              "design is documented but not built.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from needle_hip import HipBackend
+
+    hip = HipBackend(device=0)
+    n = k = 4096
+    g = 32
+    main_mv = bench_matvec(torch, hip, n, k, g, 1, args.steps, args.warmup)
+    print(f"[bench] matvec b1 HBM {main_mv['GBps']:.0f} GB/s "
+          f"{main_mv['ms_per_launch'] * 1e3:.2f} us/launch", file=sys.stderr, flush=True)
+    parts = {"matvec_b1_hbm": main_mv}
+    parts["matvec_b8_hbm"] = bench_matvec(torch, hip, n, k, g, 8, args.steps, args.warmup)
+    parts["matvec_b1_mall"] = bench_matvec(torch, hip, n, k, g, 1, args.steps, args.warmup,
+                                           rotate=False)
+    print(f"[bench] matvec b8 {parts['matvec_b8_hbm']['GBps']:.0f} GB/s, b1 MALL "
+          f"{parts['matvec_b1_mall']['GBps']:.0f} GB/s", file=sys.stderr, flush=True)
+    for length in (512, 2048, 8192):
+        parts[f"attention_L{length}_hbm"] = bench_attention(torch, hip, length, 8,
+                                                            args.steps // 2, args.warmup)
+        print(f"[bench] attention L={length} "
+              f"{parts[f'attention_L{length}_hbm']['GBps']:.0f} GB/s", file=sys.stderr, flush=True)
+    parts["attention_L8192_mall"] = bench_attention(torch, hip, 8192, 8, args.steps // 2,
+                                                    args.warmup, rotate=False)
+
+    cpu = None
+    if not args.skip_cpu:
+        cpu = cpu_baseline_matvec(n, k, g, args.cpu_seconds)
+
+    ms = main_mv["ms_per_launch"]
+    line = {
+        "metric": "decode tok/s (batch 1 & 64) + int8 matvec/attn GB/s as % of HBM peak",
+        "value": round(main_mv["GBps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": main_mv["launches"],
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8xf32",
+        "data": "synthetic",
+        "config": {"workload": "int8 matvec N=4096 K=4096 G=32 batch 1 (fp32 scales, fp32 x/y)",
+                   "rotation_replicas": main_mv["replicas"]},
+        "roofline": {"bound": "hbm", "achieved": round(main_mv["GBps"], 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(main_mv["frac_hbm"], 4), "traffic": None,
+                     "kernel": "matvec_i8_kernel<1,1,64,4>",
+                     "bytes_per_launch": main_mv["bytes_per_launch"]},
+        "cpu_baseline": cpu,
+        "parts": parts,
+    }
+    hip.dispose()
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

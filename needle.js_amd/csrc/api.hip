@@ -1,0 +1,550 @@
+// C ABI of libneedle_hip.so: argument validation, HBM ownership, staging of
+// host buffers, and dispatch to the kernels.  Validation mirrors the
+// reference's invariants (backends/cq.ts:113-126, model/runtime.ts:150-160,
+// 289-299, 885-891) so that the host binding can raise the same NeedleError
+// codes.
+#include <cstdarg>
+#include <cstring>
+#include <vector>
+
+#include "nd_internal.hpp"
+
+static thread_local std::string g_create_error;
+
+nd_status nd_fail(nd_ctx* ctx, nd_status code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (ctx) ctx->error = buf;
+  else g_create_error = buf;
+  return code;
+}
+
+nd_status nd_hip_fail(nd_ctx* ctx, hipError_t err, const char* what) {
+  return nd_fail(ctx, err == hipErrorOutOfMemory ? ND_ERR_NOMEM : ND_ERR_BACKEND, "%s: %s (%d)",
+                 what, hipGetErrorString(err), (int)err);
+}
+
+static nd_status ensure_stage(nd_ctx* ctx, size_t bytes) {
+  if (ctx->stage_bytes >= bytes) return ND_OK;
+  if (ctx->stage) {
+    ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    ND_HIP(ctx, hipFree(ctx->stage));
+    ctx->stage = nullptr;
+    ctx->stage_bytes = 0;
+  }
+  size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+  ND_HIP(ctx, hipMalloc(&ctx->stage, want));
+  ctx->stage_bytes = want;
+  return ND_OK;
+}
+
+static nd_status ensure_partials(nd_ctx* ctx, size_t floats) {
+  if (ctx->attn_partial_floats >= floats) return ND_OK;
+  if (ctx->attn_partials) {
+    ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    ND_HIP(ctx, hipFree(ctx->attn_partials));
+    ctx->attn_partials = nullptr;
+    ctx->attn_partial_floats = 0;
+  }
+  ND_HIP(ctx, hipMalloc(&ctx->attn_partials, floats * sizeof(float)));
+  ctx->attn_partial_floats = floats;
+  return ND_OK;
+}
+
+static inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+extern "C" {
+
+nd_status nd_create(int32_t device, nd_ctx** out) {
+  if (!out) return nd_fail(nullptr, ND_ERR_INVALID, "nd_create: out is NULL");
+  *out = nullptr;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count == 0)
+    return nd_fail(nullptr, ND_ERR_BACKEND, "no HIP device is available (%s)",
+                   hipGetErrorString(e));
+  if (device < 0 || device >= count)
+    return nd_fail(nullptr, ND_ERR_INVALID, "device %d is outside [0, %d)", device, count);
+  e = hipSetDevice(device);
+  if (e != hipSuccess)
+    return nd_fail(nullptr, ND_ERR_BACKEND, "hipSetDevice(%d): %s", device, hipGetErrorString(e));
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess)
+    return nd_fail(nullptr, ND_ERR_BACKEND, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return nd_fail(nullptr, ND_ERR_BACKEND, "device %d is %s; this library is built for gfx950",
+                   device, prop.gcnArchName);
+  nd_ctx* ctx = new nd_ctx();
+  ctx->device = device;
+  e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete ctx;
+    return nd_fail(nullptr, ND_ERR_BACKEND, "hipStreamCreate: %s", hipGetErrorString(e));
+  }
+  *out = ctx;
+  return ND_OK;
+}
+
+nd_status nd_destroy(nd_ctx* ctx) {
+  if (!ctx) return ND_OK;
+  hipSetDevice(ctx->device);
+  hipStreamSynchronize(ctx->stream);
+  for (nd_mat* m : ctx->mats) {
+    hipFree(m->w);
+    hipFree(m->scales);
+    delete m;
+  }
+  for (nd_kv* kv : ctx->kvs) {
+    hipFree(kv->k);
+    delete kv;
+  }
+  if (ctx->stage) hipFree(ctx->stage);
+  if (ctx->attn_partials) hipFree(ctx->attn_partials);
+  hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return ND_OK;
+}
+
+const char* nd_last_error(const nd_ctx* ctx) {
+  return ctx ? ctx->error.c_str() : g_create_error.c_str();
+}
+
+nd_status nd_sync(nd_ctx* ctx) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ND_OK;
+}
+
+void* nd_stream(nd_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+// ------------------------------------------------------------- matrices
+
+static nd_status check_mat_shape(nd_ctx* ctx, uint32_t n, uint32_t k, uint32_t g) {
+  if (n == 0 || k == 0 || g == 0)
+    return nd_fail(ctx, ND_ERR_INVALID, "matrix shape %ux%u with group %u is empty", n, k, g);
+  if (k % g != 0 || g % 16 != 0)
+    return nd_fail(ctx, ND_ERR_INVALID, "group size %u must divide k=%u and be a multiple of 16",
+                   g, k);
+  // The matvec kernel maps k / 16 segments onto a power-of-two lane count.
+  const uint32_t segs = k / 16;
+  if (k % 16 != 0 || (segs & (segs - 1)) != 0 || segs < 8 || segs > 512)
+    return nd_fail(ctx, ND_ERR_INVALID, "k=%u must be 16 * 2^j with 128 <= k <= 8192", k);
+  return ND_OK;
+}
+
+static nd_status upload(nd_ctx* ctx, const void* w, const void* s, uint32_t n, uint32_t k,
+                        uint32_t g, hipMemcpyKind kind, nd_mat** out) {
+  if (!ctx || !out || !w || !s) return nd_fail(ctx, ND_ERR_INVALID, "nd_mat_upload: NULL argument");
+  *out = nullptr;
+  nd_status st = check_mat_shape(ctx, n, k, g);
+  if (st != ND_OK) return st;
+  ND_HIP(ctx, hipSetDevice(ctx->device));
+  nd_mat* m = new nd_mat();
+  m->n = n;
+  m->k = k;
+  m->g = g;
+  const size_t wb = (size_t)n * k, sb = (size_t)n * (k / g) * sizeof(float);
+  hipError_t e = hipMalloc(&m->w, wb);
+  if (e == hipSuccess) e = hipMalloc(&m->scales, sb);
+  if (e == hipSuccess) e = hipMemcpyAsync(m->w, w, wb, kind, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(m->scales, s, sb, kind, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    hipFree(m->w);
+    hipFree(m->scales);
+    delete m;
+    return nd_hip_fail(ctx, e, "matrix upload");
+  }
+  ctx->mats.insert(m);
+  *out = m;
+  return ND_OK;
+}
+
+nd_status nd_mat_upload_i8(nd_ctx* ctx, const int8_t* w, const float* scales, uint32_t n,
+                           uint32_t k, uint32_t g, nd_mat** out) {
+  return upload(ctx, w, scales, n, k, g, hipMemcpyHostToDevice, out);
+}
+
+nd_status nd_mat_upload_i8_d(nd_ctx* ctx, const int8_t* w_dev, const float* scales_dev,
+                             uint32_t n, uint32_t k, uint32_t g, nd_mat** out) {
+  return upload(ctx, w_dev, scales_dev, n, k, g, hipMemcpyDeviceToDevice, out);
+}
+
+nd_status nd_mat_free(nd_ctx* ctx, nd_mat* m) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!m) return ND_OK;
+  if (!ctx->mats.erase(m)) return nd_fail(ctx, ND_ERR_INVALID, "matrix does not belong to context");
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  hipFree(m->w);
+  hipFree(m->scales);
+  delete m;
+  return ND_OK;
+}
+
+nd_status nd_mat_info(const nd_mat* m, const int8_t** w_dev, const float** scales_dev, uint32_t* n,
+                      uint32_t* k, uint32_t* g) {
+  if (!m) return ND_ERR_INVALID;
+  if (w_dev) *w_dev = m->w;
+  if (scales_dev) *scales_dev = m->scales;
+  if (n) *n = m->n;
+  if (k) *k = m->k;
+  if (g) *g = m->g;
+  return ND_OK;
+}
+
+// --------------------------------------------------------------- matvec
+
+static nd_status check_range(nd_ctx* ctx, const nd_mat* m, uint32_t row_start, uint32_t row_count) {
+  if (!m) return nd_fail(ctx, ND_ERR_INVALID, "matrix is NULL");
+  if ((uint64_t)row_start + row_count > m->n)
+    return nd_fail(ctx, ND_ERR_INVALID, "Invalid matrix row range %u:%llu", row_start,
+                   (unsigned long long)row_start + row_count);
+  return ND_OK;
+}
+
+nd_status nd_matvec_d(nd_ctx* ctx, const nd_mat* m, const float* x, uint32_t batch,
+                      uint32_t row_start, uint32_t row_count, float* y, void* stream) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_range(ctx, m, row_start, row_count);
+  if (st != ND_OK) return st;
+  if ((batch && (!x || !y)) || (reinterpret_cast<uintptr_t>(x) & 15))
+    return nd_fail(ctx, ND_ERR_INVALID, "x must be a 16-byte aligned device pointer");
+  ND_HIP(ctx, nd_launch_matvec(m, x, batch, m->k, row_start, row_count, y, row_count,
+                               nd_pick_stream(ctx, stream)));
+  return ND_OK;
+}
+
+nd_status nd_matvec(nd_ctx* ctx, const nd_mat* m, const float* x, uint32_t batch,
+                    uint32_t row_start, uint32_t row_count, float* y) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_range(ctx, m, row_start, row_count);
+  if (st != ND_OK) return st;
+  if (batch == 0 || row_count == 0) return ND_OK;
+  if (!x || !y) return nd_fail(ctx, ND_ERR_INVALID, "x or y is NULL");
+  const size_t xb = (size_t)batch * m->k * sizeof(float);
+  const size_t yb = (size_t)batch * row_count * sizeof(float);
+  st = ensure_stage(ctx, align256(xb) + yb);
+  if (st != ND_OK) return st;
+  float* dx = reinterpret_cast<float*>(ctx->stage);
+  float* dy = reinterpret_cast<float*>(reinterpret_cast<char*>(ctx->stage) + align256(xb));
+  ND_HIP(ctx, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
+  ND_HIP(ctx, nd_launch_matvec(m, dx, batch, m->k, row_start, row_count, dy, row_count, ctx->stream));
+  ND_HIP(ctx, hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ND_OK;
+}
+
+nd_status nd_matvec_batch(nd_ctx* ctx, const nd_matvec_job* jobs, uint32_t count) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (count == 0) return ND_OK;
+  if (!jobs) return nd_fail(ctx, ND_ERR_INVALID, "jobs is NULL");
+  size_t total = 0;
+  for (uint32_t i = 0; i < count; ++i) {
+    nd_status st = check_range(ctx, jobs[i].mat, jobs[i].row_start, jobs[i].row_count);
+    if (st != ND_OK) return st;
+    if (!jobs[i].x || (jobs[i].row_count && !jobs[i].y))
+      return nd_fail(ctx, ND_ERR_INVALID, "job %u has a NULL buffer", i);
+    total += align256((size_t)jobs[i].mat->k * 4) + align256((size_t)jobs[i].row_count * 4);
+  }
+  nd_status st = ensure_stage(ctx, total);
+  if (st != ND_OK) return st;
+  char* base = reinterpret_cast<char*>(ctx->stage);
+  std::vector<float*> dys(count);
+  size_t off = 0;
+  // Identical host inputs are uploaded once (the reference prepares each
+  // input once per geometry, backends/cpu.ts:18-26).
+  std::vector<std::pair<const float*, float*>> seen;
+  for (uint32_t i = 0; i < count; ++i) {
+    const nd_mat* m = jobs[i].mat;
+    float* dx = nullptr;
+    for (auto& pr : seen)
+      if (pr.first == jobs[i].x) dx = pr.second;
+    if (!dx) {
+      dx = reinterpret_cast<float*>(base + off);
+      off += align256((size_t)m->k * 4);
+      ND_HIP(ctx, hipMemcpyAsync(dx, jobs[i].x, (size_t)m->k * 4, hipMemcpyHostToDevice, ctx->stream));
+      seen.emplace_back(jobs[i].x, dx);
+    }
+    dys[i] = reinterpret_cast<float*>(base + off);
+    off += align256((size_t)jobs[i].row_count * 4);
+    ND_HIP(ctx, nd_launch_matvec(m, dx, 1, m->k, jobs[i].row_start, jobs[i].row_count, dys[i],
+                                 jobs[i].row_count, ctx->stream));
+  }
+  for (uint32_t i = 0; i < count; ++i)
+    if (jobs[i].row_count)
+      ND_HIP(ctx, hipMemcpyAsync(jobs[i].y, dys[i], (size_t)jobs[i].row_count * 4,
+                                 hipMemcpyDeviceToHost, ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ND_OK;
+}
+
+nd_status nd_row_d(nd_ctx* ctx, const nd_mat* m, uint32_t row, float* out, void* stream) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!m || row >= m->n) return nd_fail(ctx, ND_ERR_INVALID, "Matrix row %u is out of range", row);
+  if (!out) return nd_fail(ctx, ND_ERR_INVALID, "output is NULL");
+  ND_HIP(ctx, nd_launch_row(m, row, out, nd_pick_stream(ctx, stream)));
+  return ND_OK;
+}
+
+nd_status nd_row(nd_ctx* ctx, const nd_mat* m, uint32_t row, float* out) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!m || row >= m->n) return nd_fail(ctx, ND_ERR_INVALID, "Matrix row %u is out of range", row);
+  if (!out) return nd_fail(ctx, ND_ERR_INVALID, "output is NULL");
+  nd_status st = ensure_stage(ctx, (size_t)m->k * 4);
+  if (st != ND_OK) return st;
+  float* d = reinterpret_cast<float*>(ctx->stage);
+  ND_HIP(ctx, nd_launch_row(m, row, d, ctx->stream));
+  ND_HIP(ctx, hipMemcpyAsync(out, d, (size_t)m->k * 4, hipMemcpyDeviceToHost, ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ND_OK;
+}
+
+// -------------------------------------------------------------- KV cache
+
+nd_status nd_kv_create(nd_ctx* ctx, uint32_t layers, uint32_t kv_heads, uint32_t head_dim,
+                       uint32_t max_length, uint32_t sink, uint32_t window, uint32_t mode,
+                       nd_kv** out) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!out) return nd_fail(ctx, ND_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  if (head_dim != 64) return nd_fail(ctx, ND_ERR_INVALID, "head_dim %u is not 64", head_dim);
+  if (layers == 0 || kv_heads == 0 || max_length == 0)
+    return nd_fail(ctx, ND_ERR_INVALID, "empty KV cache geometry");
+  if (mode != ND_KV_INT8 && mode != ND_KV_FLOAT32)
+    return nd_fail(ctx, ND_ERR_INVALID, "unknown KV mode %u", mode);
+  nd_kv* kv = new nd_kv();
+  kv->layers = layers;
+  kv->kv_heads = kv_heads;
+  kv->head_dim = head_dim;
+  kv->max_length = max_length;
+  kv->sink = sink < max_length ? sink : max_length;
+  kv->window = window;
+  kv->alloc = window > 0 ? (max_length < kv->sink + window ? max_length : kv->sink + window)
+                         : max_length;
+  kv->mode = mode;
+  const size_t rows = (size_t)layers * kv_heads * kv->alloc;
+  const size_t code_bytes = rows * head_dim * (mode == ND_KV_FLOAT32 ? 4 : 1);
+  const size_t scale_bytes = rows * sizeof(float);
+  const size_t total = 2 * align256(code_bytes) + 2 * align256(scale_bytes);
+  char* base = nullptr;
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e == hipSuccess) e = hipMalloc(&base, total);
+  if (e == hipSuccess) e = hipMemsetAsync(base, 0, total, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    if (base) hipFree(base);
+    delete kv;
+    return nd_hip_fail(ctx, e, "KV cache allocation");
+  }
+  kv->k = base;
+  kv->v = base + align256(code_bytes);
+  kv->ks = reinterpret_cast<float*>(base + 2 * align256(code_bytes));
+  kv->vs = reinterpret_cast<float*>(base + 2 * align256(code_bytes) + align256(scale_bytes));
+  // Attention partials for the largest visible set of this cache, with up to
+  // 8 query heads per KV head.
+  const uint32_t max_visible = kv->alloc;
+  nd_status st = ensure_partials(ctx, nd_attention_partial_floats(kv_heads * 8, max_visible));
+  if (st != ND_OK) {
+    hipFree(base);
+    delete kv;
+    return st;
+  }
+  ctx->kvs.insert(kv);
+  *out = kv;
+  return ND_OK;
+}
+
+nd_status nd_kv_free(nd_ctx* ctx, nd_kv* kv) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!kv) return ND_OK;
+  if (!ctx->kvs.erase(kv)) return nd_fail(ctx, ND_ERR_INVALID, "cache does not belong to context");
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  hipFree(kv->k);
+  delete kv;
+  return ND_OK;
+}
+
+static size_t kv_total_bytes(const nd_kv* kv) {
+  const size_t rows = (size_t)kv->layers * kv->kv_heads * kv->alloc;
+  const size_t code_bytes = rows * kv->head_dim * (kv->mode == ND_KV_FLOAT32 ? 4 : 1);
+  return 2 * align256(code_bytes) + 2 * align256(rows * sizeof(float));
+}
+
+nd_status nd_kv_clear(nd_ctx* ctx, nd_kv* kv) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!kv) return nd_fail(ctx, ND_ERR_INVALID, "cache is NULL");
+  ND_HIP(ctx, hipMemsetAsync(kv->k, 0, kv_total_bytes(kv), ctx->stream));
+  return ND_OK;
+}
+
+nd_status nd_kv_info(const nd_kv* kv, uint32_t* alloc, void** k_codes, void** v_codes,
+                     float** k_scales, float** v_scales) {
+  if (!kv) return ND_ERR_INVALID;
+  if (alloc) *alloc = kv->alloc;
+  if (k_codes) *k_codes = kv->k;
+  if (v_codes) *v_codes = kv->v;
+  if (k_scales) *k_scales = kv->ks;
+  if (v_scales) *v_scales = kv->vs;
+  return ND_OK;
+}
+
+static nd_status check_store(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t position,
+                             uint32_t count) {
+  if (!kv) return nd_fail(ctx, ND_ERR_INVALID, "cache is NULL");
+  if (layer >= kv->layers)
+    return nd_fail(ctx, ND_ERR_INVALID, "layer %u is outside [0, %u)", layer, kv->layers);
+  if ((uint64_t)position + count > kv->max_length)
+    return nd_fail(ctx, ND_ERR_OVERFLOW, "Position %llu reached runtime limit %u",
+                   (unsigned long long)position + count - 1, kv->max_length);
+  return ND_OK;
+}
+
+nd_status nd_kv_store_d(nd_ctx* ctx, nd_kv* kv, uint32_t layer, uint32_t position, uint32_t count,
+                        const float* k, const float* v, void* stream) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_store(ctx, kv, layer, position, count);
+  if (st != ND_OK) return st;
+  if (count && (!k || !v)) return nd_fail(ctx, ND_ERR_INVALID, "k or v is NULL");
+  ND_HIP(ctx, nd_launch_kv_store(kv, layer, position, 0, count, k, v, nd_pick_stream(ctx, stream)));
+  return ND_OK;
+}
+
+nd_status nd_kv_store(nd_ctx* ctx, nd_kv* kv, uint32_t layer, uint32_t position, uint32_t count,
+                      const float* k, const float* v) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_store(ctx, kv, layer, position, count);
+  if (st != ND_OK) return st;
+  if (count == 0) return ND_OK;
+  if (!k || !v) return nd_fail(ctx, ND_ERR_INVALID, "k or v is NULL");
+  const size_t bytes = (size_t)count * kv->kv_heads * kv->head_dim * sizeof(float);
+  st = ensure_stage(ctx, 2 * align256(bytes));
+  if (st != ND_OK) return st;
+  float* dk = reinterpret_cast<float*>(ctx->stage);
+  float* dv = reinterpret_cast<float*>(reinterpret_cast<char*>(ctx->stage) + align256(bytes));
+  ND_HIP(ctx, hipMemcpyAsync(dk, k, bytes, hipMemcpyHostToDevice, ctx->stream));
+  ND_HIP(ctx, hipMemcpyAsync(dv, v, bytes, hipMemcpyHostToDevice, ctx->stream));
+  ND_HIP(ctx, nd_launch_kv_store(kv, layer, position, 0, count, dk, dv, ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ND_OK;
+}
+
+nd_status nd_kv_read(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t head, void* k_codes,
+                     void* v_codes, float* k_scales, float* v_scales) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!kv || layer >= kv->layers || head >= kv->kv_heads)
+    return nd_fail(ctx, ND_ERR_INVALID, "layer/head outside the cache");
+  const size_t row0 = ((size_t)layer * kv->kv_heads + head) * kv->alloc;
+  const size_t esz = kv->mode == ND_KV_FLOAT32 ? 4 : 1;
+  const size_t cb = (size_t)kv->alloc * kv->head_dim * esz;
+  const char* kc = reinterpret_cast<const char*>(kv->k) + row0 * kv->head_dim * esz;
+  const char* vc = reinterpret_cast<const char*>(kv->v) + row0 * kv->head_dim * esz;
+  if (k_codes) ND_HIP(ctx, hipMemcpyAsync(k_codes, kc, cb, hipMemcpyDeviceToHost, ctx->stream));
+  if (v_codes) ND_HIP(ctx, hipMemcpyAsync(v_codes, vc, cb, hipMemcpyDeviceToHost, ctx->stream));
+  if (k_scales)
+    ND_HIP(ctx, hipMemcpyAsync(k_scales, kv->ks + row0, kv->alloc * 4, hipMemcpyDeviceToHost, ctx->stream));
+  if (v_scales)
+    ND_HIP(ctx, hipMemcpyAsync(v_scales, kv->vs + row0, kv->alloc * 4, hipMemcpyDeviceToHost, ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ND_OK;
+}
+
+static nd_status check_attention(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t position,
+                                 uint32_t q_heads) {
+  if (!kv) return nd_fail(ctx, ND_ERR_INVALID, "cache is NULL");
+  if (layer >= kv->layers)
+    return nd_fail(ctx, ND_ERR_INVALID, "layer %u is outside [0, %u)", layer, kv->layers);
+  if (position >= kv->max_length)
+    return nd_fail(ctx, ND_ERR_OVERFLOW, "Position %u reached runtime limit %u", position,
+                   kv->max_length);
+  const uint32_t rep = q_heads / kv->kv_heads;
+  if (q_heads == 0 || q_heads % kv->kv_heads != 0 || (rep != 1 && rep != 2 && rep != 4 && rep != 8))
+    return nd_fail(ctx, ND_ERR_INVALID,
+                   "q_heads %u must be 1, 2, 4 or 8 times the %u KV heads", q_heads, kv->kv_heads);
+  return ND_OK;
+}
+
+nd_status nd_attention_d(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t position,
+                         const float* q, uint32_t q_heads, float* out, void* stream) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_attention(ctx, kv, layer, position, q_heads);
+  if (st != ND_OK) return st;
+  if (!q || !out || (reinterpret_cast<uintptr_t>(q) & 15))
+    return nd_fail(ctx, ND_ERR_INVALID, "q must be a 16-byte aligned device pointer");
+  const nd_visible vis = nd_kv_visible(kv, position);
+  const size_t need = nd_attention_partial_floats(q_heads, vis.count);
+  if (need > ctx->attn_partial_floats && nd_attention_chunks(vis.count) > 1)
+    return nd_fail(ctx, ND_ERR_INVALID, "attention partials too small (%zu > %zu floats)", need,
+                   ctx->attn_partial_floats);
+  ND_HIP(ctx, nd_launch_attention(kv, layer, position, q, q_heads, out, ctx->attn_partials,
+                                  nd_pick_stream(ctx, stream)));
+  return ND_OK;
+}
+
+nd_status nd_attention(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t position,
+                       const float* q, uint32_t q_heads, float* out) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_attention(ctx, kv, layer, position, q_heads);
+  if (st != ND_OK) return st;
+  if (!q || !out) return nd_fail(ctx, ND_ERR_INVALID, "q or out is NULL");
+  const nd_visible vis = nd_kv_visible(kv, position);
+  st = ensure_partials(ctx, nd_attention_partial_floats(q_heads, vis.count));
+  if (st != ND_OK) return st;
+  const size_t bytes = (size_t)q_heads * kv->head_dim * sizeof(float);
+  st = ensure_stage(ctx, 2 * align256(bytes));
+  if (st != ND_OK) return st;
+  float* dq = reinterpret_cast<float*>(ctx->stage);
+  float* dout = reinterpret_cast<float*>(reinterpret_cast<char*>(ctx->stage) + align256(bytes));
+  ND_HIP(ctx, hipMemcpyAsync(dq, q, bytes, hipMemcpyHostToDevice, ctx->stream));
+  ND_HIP(ctx, nd_launch_attention(kv, layer, position, dq, q_heads, dout, ctx->attn_partials,
+                                  ctx->stream));
+  ND_HIP(ctx, hipMemcpyAsync(out, dout, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ND_OK;
+}
+
+// -------------------------------------------------------------- selection
+
+nd_status nd_select(nd_ctx* ctx, const float* logits, uint32_t vocab, const uint32_t* allowed,
+                    uint32_t count, uint32_t* id, double* logprob) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!logits || !id || !logprob || vocab == 0)
+    return nd_fail(ctx, ND_ERR_INVALID, "nd_select: NULL argument or empty vocabulary");
+  if (allowed) {
+    if (count == 0) return nd_fail(ctx, ND_ERR_INVALID, "Allowed token set is empty");
+    for (uint32_t i = 0; i < count; ++i)
+      if (allowed[i] >= vocab)
+        return nd_fail(ctx, ND_ERR_INVALID, "Token %u is outside logits", allowed[i]);
+  }
+  const size_t lb = (size_t)vocab * 4, ab = allowed ? (size_t)count * 4 : 0;
+  nd_status st = ensure_stage(ctx, align256(lb) + align256(ab) + 256);
+  if (st != ND_OK) return st;
+  char* base = reinterpret_cast<char*>(ctx->stage);
+  float* dl = reinterpret_cast<float*>(base);
+  uint32_t* da = allowed ? reinterpret_cast<uint32_t*>(base + align256(lb)) : nullptr;
+  char* res = base + align256(lb) + align256(ab);
+  double* dlp = reinterpret_cast<double*>(res);
+  uint32_t* did = reinterpret_cast<uint32_t*>(res + 8);
+  ND_HIP(ctx, hipMemcpyAsync(dl, logits, lb, hipMemcpyHostToDevice, ctx->stream));
+  if (allowed) ND_HIP(ctx, hipMemcpyAsync(da, allowed, ab, hipMemcpyHostToDevice, ctx->stream));
+  ND_HIP(ctx, nd_launch_select_list(dl, vocab, da, count, did, dlp, ctx->stream));
+  ND_HIP(ctx, hipMemcpyAsync(logprob, dlp, 8, hipMemcpyDeviceToHost, ctx->stream));
+  ND_HIP(ctx, hipMemcpyAsync(id, did, 4, hipMemcpyDeviceToHost, ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ND_OK;
+}
+
+nd_status nd_select_mask_d(nd_ctx* ctx, const float* logits, uint32_t batch, uint32_t vocab,
+                           const uint32_t* mask, uint32_t* ids, double* logprobs, void* stream) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (batch && (!logits || !ids || !logprobs || vocab == 0))
+    return nd_fail(ctx, ND_ERR_INVALID, "nd_select_mask_d: NULL argument or empty vocabulary");
+  ND_HIP(ctx, nd_launch_select_mask(logits, batch, vocab, mask, ids, logprobs,
+                                    nd_pick_stream(ctx, stream)));
+  return ND_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,81 @@
+// Internal declarations shared by the libneedle_hip translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <set>
+#include <string>
+
+#include "needle_hip.h"
+
+struct nd_mat {
+  int8_t* w = nullptr;      // [n][k] int8 codes, row-major
+  float* scales = nullptr;  // [n][k / g]
+  uint32_t n = 0, k = 0, g = 0;
+};
+
+struct nd_kv {
+  uint32_t layers = 0, kv_heads = 0, head_dim = 0, max_length = 0;
+  uint32_t sink = 0, window = 0, alloc = 0, mode = ND_KV_INT8;
+  void* k = nullptr;  // [layers][kv_heads][alloc][head_dim] int8 (or f32)
+  void* v = nullptr;
+  float* ks = nullptr;  // [layers][kv_heads][alloc]
+  float* vs = nullptr;
+};
+
+struct nd_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string error;
+  // Device staging for the host-pointer entry points (grown on demand).
+  void* stage = nullptr;
+  size_t stage_bytes = 0;
+  // Split-context attention partials: [q_heads][chunks][2 + head_dim] f32.
+  float* attn_partials = nullptr;
+  size_t attn_partial_floats = 0;
+  std::set<nd_mat*> mats;
+  std::set<nd_kv*> kvs;
+};
+
+// Error helpers: record a message on the context and return a status.
+nd_status nd_fail(nd_ctx* ctx, nd_status code, const char* fmt, ...);
+nd_status nd_hip_fail(nd_ctx* ctx, hipError_t err, const char* what);
+
+#define ND_HIP(ctx, expr)                                  \
+  do {                                                     \
+    hipError_t _e = (expr);                                \
+    if (_e != hipSuccess) return nd_hip_fail(ctx, _e, #expr); \
+  } while (0)
+
+inline hipStream_t nd_pick_stream(nd_ctx* ctx, void* stream) {
+  return stream ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
+}
+
+// Kernel launchers (each validates nothing: callers check shapes first).
+hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uint32_t x_stride,
+                            uint32_t row_start, uint32_t row_count, float* y, uint32_t y_stride,
+                            hipStream_t s);
+hipError_t nd_launch_row(const nd_mat* m, uint32_t row, float* out, hipStream_t s);
+
+// Visible-position arithmetic of the attention window (runtime.ts:723-728).
+struct nd_visible {
+  uint32_t prefix;      // positions [0, prefix)
+  uint32_t recent_low;  // positions [recent_low, position]
+  uint32_t count;       // prefix + position - recent_low + 1
+};
+nd_visible nd_kv_visible(const nd_kv* kv, uint32_t position);
+uint32_t nd_attention_chunks(uint32_t count);
+size_t nd_attention_partial_floats(uint32_t q_heads, uint32_t count);
+
+hipError_t nd_launch_kv_store(const nd_kv* kv, uint32_t layer, uint32_t position, uint32_t first,
+                              uint32_t count, const float* k, const float* v, hipStream_t s);
+hipError_t nd_launch_attention(const nd_kv* kv, uint32_t layer, uint32_t position,
+                               const float* q, uint32_t q_heads, float* out, float* partials,
+                               hipStream_t s);
+hipError_t nd_launch_select_list(const float* logits, uint32_t vocab, const uint32_t* allowed,
+                                 uint32_t count, uint32_t* id, double* logprob, hipStream_t s);
+hipError_t nd_launch_select_mask(const float* logits, uint32_t batch, uint32_t vocab,
+                                 const uint32_t* mask, uint32_t* ids, double* logprobs,
+                                 hipStream_t s);

@@ -1,0 +1,21 @@
+"""needle_hip: MI355X (gfx950) decode backend for needle.js.
+
+Host-side mirror of needle.js's backend contract (backends/backend.ts) over
+the C ABI of libneedle_hip.so (include/needle_hip.h).  There is no CPU
+fallback: constructing HipBackend without the library or a gfx950 device
+raises NeedleError("BACKEND_UNAVAILABLE").
+"""
+
+from .backend import HipBackend, Int8Matrix, MatrixRowRange, MatvecRequest
+from .errors import NeedleError, invariant
+from .kv import HipKvCache
+
+__all__ = [
+    "HipBackend",
+    "HipKvCache",
+    "Int8Matrix",
+    "MatrixRowRange",
+    "MatvecRequest",
+    "NeedleError",
+    "invariant",
+]

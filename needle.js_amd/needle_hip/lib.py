@@ -1,0 +1,128 @@
+"""ctypes binding of libneedle_hip.so (declarations in include/needle_hip.h).
+
+This is the host-side equivalent of the bun:ffi `dlopen` a TypeScript host
+would use: every entry point is a plain C function over pointers and sizes.
+Loading fails loudly -- there is no CPU fallback behind this module.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+from .errors import NeedleError
+
+ND_OK = 0
+ND_ERR_INVALID = 1
+ND_ERR_BACKEND = 2
+ND_ERR_OVERFLOW = 3
+ND_ERR_NOMEM = 4
+ND_KV_INT8 = 0
+ND_KV_FLOAT32 = 1
+
+_STATUS_CODE = {
+    ND_ERR_INVALID: "INVALID_CACT",
+    ND_ERR_OVERFLOW: "CONTEXT_OVERFLOW",
+    ND_ERR_BACKEND: "BACKEND_UNAVAILABLE",
+    ND_ERR_NOMEM: "BACKEND_UNAVAILABLE",
+}
+
+PACKAGE_ROOT = Path(__file__).resolve().parent.parent
+DEFAULT_LIBRARY = PACKAGE_ROOT / "libneedle_hip.so"
+
+P = C.c_void_p
+U32 = C.c_uint32
+I32 = C.c_int32
+PP = C.POINTER(C.c_void_p)
+PU32 = C.POINTER(C.c_uint32)
+PF = C.POINTER(C.c_float)
+
+
+class MatvecJob(C.Structure):
+    _fields_ = [
+        ("mat", P),
+        ("x", P),
+        ("row_start", U32),
+        ("row_count", U32),
+        ("y", P),
+    ]
+
+
+# name -> (restype, argtypes).  Kept in the order of include/needle_hip.h.
+SIGNATURES = {
+    "nd_create": (I32, [I32, PP]),
+    "nd_destroy": (I32, [P]),
+    "nd_last_error": (C.c_char_p, [P]),
+    "nd_sync": (I32, [P]),
+    "nd_stream": (P, [P]),
+    "nd_mat_upload_i8": (I32, [P, P, P, U32, U32, U32, PP]),
+    "nd_mat_upload_i8_d": (I32, [P, P, P, U32, U32, U32, PP]),
+    "nd_mat_free": (I32, [P, P]),
+    "nd_mat_info": (I32, [P, PP, PP, PU32, PU32, PU32]),
+    "nd_matvec": (I32, [P, P, P, U32, U32, U32, P]),
+    "nd_matvec_d": (I32, [P, P, P, U32, U32, U32, P, P]),
+    "nd_matvec_batch": (I32, [P, C.POINTER(MatvecJob), U32]),
+    "nd_row": (I32, [P, P, U32, P]),
+    "nd_row_d": (I32, [P, P, U32, P, P]),
+    "nd_kv_create": (I32, [P, U32, U32, U32, U32, U32, U32, U32, PP]),
+    "nd_kv_free": (I32, [P, P]),
+    "nd_kv_clear": (I32, [P, P]),
+    "nd_kv_info": (I32, [P, PU32, PP, PP, PP, PP]),
+    "nd_kv_store": (I32, [P, P, U32, U32, U32, P, P]),
+    "nd_kv_store_d": (I32, [P, P, U32, U32, U32, P, P, P]),
+    "nd_kv_read": (I32, [P, P, U32, U32, P, P, P, P]),
+    "nd_attention": (I32, [P, P, U32, U32, P, U32, P]),
+    "nd_attention_d": (I32, [P, P, U32, U32, P, U32, P, P]),
+    "nd_select": (I32, [P, P, U32, P, U32, PU32, C.POINTER(C.c_double)]),
+    "nd_select_mask_d": (I32, [P, P, U32, U32, P, P, P, P]),
+}
+
+_LIB: C.CDLL | None = None
+
+
+def library_path() -> Path:
+    env = os.environ.get("NEEDLE_HIP_LIB")
+    return Path(env) if env else DEFAULT_LIBRARY
+
+
+def load_library() -> C.CDLL:
+    """Loads libneedle_hip.so once and declares every entry point."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = library_path()
+    if not path.exists():
+        raise NeedleError(
+            "BACKEND_UNAVAILABLE",
+            f"{path} is missing; build it with __graft_entry__.build() or make -C needle.js_amd/csrc",
+        )
+    try:
+        lib = C.CDLL(str(path))
+    except OSError as exc:  # pragma: no cover - depends on the host
+        raise NeedleError("BACKEND_UNAVAILABLE", f"cannot load {path}: {exc}", exc) from exc
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _LIB = lib
+    return lib
+
+
+def last_error(lib: C.CDLL, ctx) -> str:
+    msg = lib.nd_last_error(ctx)
+    return msg.decode(errors="replace") if msg else ""
+
+
+def check(lib: C.CDLL, ctx, status: int, what: str = "") -> None:
+    """Raises the NeedleError that a nonzero nd_status maps to."""
+    if status == ND_OK:
+        return
+    code = _STATUS_CODE.get(status, "BACKEND_UNAVAILABLE")
+    message = last_error(lib, ctx) or f"{what} failed with status {status}"
+    raise NeedleError(code, message)
+
+
+def ptr(array) -> int:
+    """Address of a numpy array's data (host pointer)."""
+    return array.ctypes.data

@@ -1,0 +1,483 @@
+/*
+ * needle_oracle.c -- CPU restatement of the needle.js decode hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker: only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.  The
+ * product path (needle.js_amd/) never links, loads or calls it.
+ *
+ * Every function restates the arithmetic of the reference TypeScript CPU
+ * path with JavaScript number semantics: all scalar arithmetic is IEEE
+ * binary64 evaluated left to right with no fused multiply-add (build with
+ * -ffp-contract=off), and every store into a Float32Array is a
+ * round-to-nearest-even conversion to binary32 (a C (float) cast).
+ * Reference paths are relative to packages/needle.js/src/ of needle.js.
+ *
+ * Parity pins (what checks each function beyond re-reading this file):
+ *   or_round_ties_even  Python round() on random and tie values; tests/.
+ *   or_kv_quantize      invariants |code|<=127, code(absmax)=+-127,
+ *                       |x-code*s|<=s/2 in exact rationals, tie cases,
+ *                       zero vector; golden vectors in tests/golden/.
+ *   or_matvec_i8        closed forms (W==c, x==e_k), dense float64 matmul
+ *                       (numpy) on random inputs, batch==single with row
+ *                       ranges (mirrors tests/cq.test.ts:74-99).
+ *   or_row_i8           elementwise product in numpy (exact).
+ *   or_attention        textbook softmax attention in float64 numpy,
+ *                       identical keys -> mean of values, L=1 -> V0.
+ *   or_select           brute force over allowed ids (Python), NaN and tie
+ *                       special cases, scipy logsumexp for log-probability.
+ *   or_fwht             Sylvester Hadamard matrix (scipy.linalg.hadamard)
+ *                       and self-inverse (tests/cq.test.ts:64-72).
+ *   or_rms_norm, or_rope, or_sigmoid, or_softmax, or_sinkhorn,
+ *   or_hadamard_mlp     closed forms in numpy float64 (unit RMS, rotation
+ *                       preserves norms and matches complex multiply,
+ *                       Sinkhorn output doubly stochastic, H-MLP equals
+ *                       explicit matrix products).
+ *   decoder steps       composition of the pinned primitives; checked for
+ *                       prefill == repeated step and batch == single.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define OR_OK 0
+#define OR_INVALID 1
+#define OR_OVERFLOW 3
+
+/* JavaScript Math.max of two numbers: NaN if either is NaN, +0 beats -0. */
+static double js_max(double a, double b) {
+  if (isnan(a) || isnan(b)) return NAN;
+  if (a == 0.0 && b == 0.0) return (signbit(a) && signbit(b)) ? -0.0 : 0.0;
+  return a > b ? a : b;
+}
+
+/* ToInt8 of an integral double (Int8Array store): NaN/inf -> 0, wrap mod 256. */
+static int8_t js_to_int8(double v) {
+  if (!isfinite(v)) return 0;
+  double t = trunc(v);
+  double m = fmod(t, 256.0);
+  if (m < 0) m += 256.0;
+  int iv = (int)m;
+  return (int8_t)(iv >= 128 ? iv - 256 : iv);
+}
+
+/* runtime.ts:901-907 roundTiesToEven (Math.floor based). */
+double or_round_ties_even(double value) {
+  double lower = floor(value);
+  double fraction = value - lower;
+  if (fraction < 0.5) return lower;
+  if (fraction > 0.5) return lower + 1;
+  /* (lower & 1) uses ToInt32 of lower; NaN & 1 == 0 keeps lower. */
+  if (isnan(lower)) return lower;
+  int64_t li = (int64_t)fmod(lower, 4294967296.0);
+  return ((li & 1) == 0) ? lower : lower + 1;
+}
+
+/* ---------------------------------------------------------------- math.ts */
+
+/* math.ts:3-10 */
+double or_sigmoid(double value) {
+  if (value >= 0) {
+    double e = exp(-value);
+    return 1 / (1 + e);
+  }
+  double e = exp(value);
+  return e / (1 + e);
+}
+
+/* math.ts:12-14 */
+double or_silu(double value) { return value * or_sigmoid(value); }
+
+/* math.ts:16-32 rmsNorm (zero-centred: scale stores the offset from 1). */
+void or_rms_norm(const float* input, const float* scale, uint32_t n, float* output) {
+  double sum_squares = 0;
+  for (uint32_t i = 0; i < n; i++) {
+    double v = input[i];
+    sum_squares += v * v;
+  }
+  double inverse = 1 / sqrt(sum_squares / n + 1e-6);
+  for (uint32_t i = 0; i < n; i++)
+    output[i] = (float)((1 + (double)scale[i]) * (double)input[i] * inverse);
+}
+
+/* math.ts:34-44 rmsUnit */
+void or_rms_unit(const float* input, uint32_t n, float* output) {
+  double sum_squares = 0;
+  for (uint32_t i = 0; i < n; i++) {
+    double v = input[i];
+    sum_squares += v * v;
+  }
+  double inverse = 1 / sqrt(sum_squares / n + 1e-6);
+  for (uint32_t i = 0; i < n; i++) output[i] = (float)((double)input[i] * inverse);
+}
+
+/* runtime.ts:647-657 #rmsNormSlice (in place, offset slice). */
+void or_rms_norm_slice(float* values, uint32_t offset, uint32_t length, const float* scale) {
+  double sum_squares = 0;
+  for (uint32_t i = 0; i < length; i++) {
+    double v = values[offset + i];
+    sum_squares += v * v;
+  }
+  double inverse = 1 / sqrt(sum_squares / length + 1e-6);
+  for (uint32_t i = 0; i < length; i++)
+    values[offset + i] = (float)((1 + (double)scale[i]) * (double)values[offset + i] * inverse);
+}
+
+/* math.ts:46-60 softmaxInPlace */
+void or_softmax(float* values, uint32_t length) {
+  if (length == 0) return;
+  double maximum = values[0];
+  for (uint32_t i = 1; i < length; i++) maximum = js_max(maximum, values[i]);
+  double total = 0;
+  for (uint32_t i = 0; i < length; i++) {
+    double v = exp((double)values[i] - maximum);
+    values[i] = (float)v;
+    total += v;
+  }
+  double inverse = total > 0 ? 1 / total : 0;
+  for (uint32_t i = 0; i < length; i++) values[i] = (float)((double)values[i] * inverse);
+}
+
+/* cq.ts:8-27 fastWalshHadamard on values[offset, offset+length). */
+int or_fwht(float* values, uint32_t offset, uint32_t length) {
+  if (length == 0 || (length & (length - 1)) != 0) return OR_INVALID;
+  for (uint32_t stride = 1; stride < length; stride <<= 1) {
+    uint32_t block = stride << 1;
+    for (uint32_t base = 0; base < length; base += block) {
+      for (uint32_t inner = 0; inner < stride; inner++) {
+        uint32_t li = offset + base + inner, ri = li + stride;
+        double left = values[li], right = values[ri];
+        values[li] = (float)(left + right);
+        values[ri] = (float)(left - right);
+      }
+    }
+  }
+  return OR_OK;
+}
+
+/* math.ts:62-92 sinkhorn (log-space, float64 working copy). */
+void or_sinkhorn(float* logits, uint32_t size, uint32_t iterations) {
+  uint32_t n = size * size;
+  double* v = (double*)malloc(sizeof(double) * n);
+  for (uint32_t i = 0; i < n; i++) v[i] = logits[i];
+  for (uint32_t it = 0; it < iterations; it++) {
+    for (uint32_t row = 0; row < size; row++) {
+      uint32_t off = row * size;
+      double maximum = v[off];
+      for (uint32_t c = 1; c < size; c++) maximum = js_max(maximum, v[off + c]);
+      double sum = 0;
+      for (uint32_t c = 0; c < size; c++) sum += exp(v[off + c] - maximum);
+      double log_sum = log(sum) + maximum;
+      for (uint32_t c = 0; c < size; c++) v[off + c] = v[off + c] - log_sum;
+    }
+    for (uint32_t c = 0; c < size; c++) {
+      double maximum = v[c];
+      for (uint32_t r = 1; r < size; r++) maximum = js_max(maximum, v[r * size + c]);
+      double sum = 0;
+      for (uint32_t r = 0; r < size; r++) sum += exp(v[r * size + c] - maximum);
+      double log_sum = log(sum) + maximum;
+      for (uint32_t r = 0; r < size; r++) v[r * size + c] = v[r * size + c] - log_sum;
+    }
+  }
+  for (uint32_t i = 0; i < n; i++) logits[i] = (float)exp(v[i]);
+  free(v);
+}
+
+/* math.ts:94-115 applyRope: half-split rotation, theta^(-2j/d). */
+void or_rope(float* vec, uint32_t heads, uint32_t head_dim, uint32_t position, double theta) {
+  uint32_t half = head_dim >> 1;
+  for (uint32_t h = 0; h < heads; h++) {
+    uint32_t off = h * head_dim;
+    for (uint32_t d = 0; d < half; d++) {
+      double frequency = pow(theta, -(2.0 * d) / head_dim);
+      double angle = position * frequency;
+      double c = cos(angle), s = sin(angle);
+      double first = vec[off + d], second = vec[off + d + half];
+      vec[off + d] = (float)(first * c - second * s);
+      vec[off + d + half] = (float)(second * c + first * s);
+    }
+  }
+}
+
+/* math.ts:117-138 hadamardMlp; output has `n` entries, hdim >= n. */
+int or_hadamard_mlp(const float* input, uint32_t n, const float* d1, const float* d2,
+                    const float* d3, uint32_t hdim, float* output) {
+  if (hdim < n) return OR_INVALID;
+  float* values = (float*)calloc(hdim, sizeof(float));
+  for (uint32_t i = 0; i < n; i++) values[i] = (float)((double)input[i] * (double)d1[i]);
+  double inverse_root = 1 / sqrt((double)hdim);
+  if (or_fwht(values, 0, hdim) != OR_OK) { free(values); return OR_INVALID; }
+  for (uint32_t i = 0; i < hdim; i++)
+    values[i] = (float)or_silu((double)values[i] * inverse_root * (double)d2[i]);
+  or_fwht(values, 0, hdim);
+  for (uint32_t i = 0; i < n; i++)
+    output[i] = (float)((double)values[i] * inverse_root * (double)d3[i]);
+  free(values);
+  return OR_OK;
+}
+
+/* math.ts:140-151 argmax: first maximum under strict '>'. */
+uint32_t or_argmax(const float* values, uint32_t n) {
+  uint32_t best = 0;
+  double best_value = n ? (double)values[0] : -INFINITY;
+  for (uint32_t i = 1; i < n; i++) {
+    double v = values[i];
+    if (v > best_value) { best_value = v; best = i; }
+  }
+  return best;
+}
+
+/* math.ts:153-160 logSoftmaxAt over the full vocabulary. */
+double or_log_softmax_at(const float* logits, uint32_t n, uint32_t token) {
+  double maximum = n ? (double)logits[0] : -INFINITY;
+  for (uint32_t i = 1; i < n; i++) maximum = js_max(maximum, logits[i]);
+  double sum = 0;
+  for (uint32_t i = 0; i < n; i++) sum += exp((double)logits[i] - maximum);
+  double at = token < n ? (double)logits[token] : -INFINITY;
+  return at - maximum - log(sum);
+}
+
+/* runtime.ts:880-899 selectToken.  allowed==NULL -> unconstrained argmax.
+ * Returns OR_INVALID for an empty list or an id outside the logits. */
+int or_select(const float* logits, uint32_t vocab, const uint32_t* allowed, uint32_t count,
+              uint32_t* out_id, double* out_logprob) {
+  uint32_t id;
+  if (!allowed) {
+    id = or_argmax(logits, vocab);
+  } else {
+    if (count == 0) return OR_INVALID;
+    id = allowed[0];
+    if (id >= vocab) return OR_INVALID;
+    double best = logits[id];
+    for (uint32_t i = 1; i < count; i++) {
+      uint32_t c = allowed[i];
+      if (c >= vocab) return OR_INVALID;
+      double v = logits[c];
+      if (v > best) { best = v; id = c; }
+    }
+  }
+  *out_id = id;
+  *out_logprob = or_log_softmax_at(logits, vocab, id);
+  return OR_OK;
+}
+
+/* Bitmask form of selectToken used by batched constrained decode: the allowed
+ * list is the ascending set of ids whose bit (mask[id>>5] >> (id&31)) & 1 is
+ * set, which is how agent.ts:164-183 builds it (ascending token order). */
+int or_select_mask(const float* logits, uint32_t vocab, const uint32_t* mask, uint32_t* out_id,
+                   double* out_logprob) {
+  int found = 0;
+  uint32_t id = 0;
+  double best = 0;
+  for (uint32_t c = 0; c < vocab; c++) {
+    if (!((mask[c >> 5] >> (c & 31)) & 1u)) continue;
+    double v = logits[c];
+    if (!found) { id = c; best = v; found = 1; }
+    else if (v > best) { best = v; id = c; }
+  }
+  if (!found) return OR_INVALID;
+  *out_id = id;
+  *out_logprob = or_log_softmax_at(logits, vocab, id);
+  return OR_OK;
+}
+
+/* ------------------------------------------------------- a1: int8 matvec */
+
+/* Int8 variant of CqMatrix: W int8 [N][K] row-major, scales f32 [N][K/G].
+ * Restates cqMatvecPrepared's loop shape (cq.ts:106-156): for each row a
+ * float64 `dot` per group, `total += norm * dot`, f32 store; the codebook
+ * lookup becomes the int8 value and the fp16 group norm the fp32 scale.
+ * x and y are [B][K] and [B][row_count]. */
+int or_matvec_i8(const int8_t* w, const float* scales, uint32_t n, uint32_t k, uint32_t g,
+                 const float* x, uint32_t batch, uint32_t row_start, uint32_t row_count,
+                 float* y) {
+  if (g == 0 || k % g != 0) return OR_INVALID;
+  if ((uint64_t)row_start + row_count > n) return OR_INVALID;
+  uint32_t groups = k / g;
+  for (uint32_t b = 0; b < batch; b++) {
+    const float* xb = x + (size_t)b * k;
+    for (uint32_t lr = 0; lr < row_count; lr++) {
+      uint32_t r = row_start + lr;
+      const int8_t* wr = w + (size_t)r * k;
+      double total = 0;
+      for (uint32_t grp = 0; grp < groups; grp++) {
+        double dot = 0;
+        for (uint32_t c = 0; c < g; c++) {
+          uint32_t col = grp * g + c;
+          dot += (double)wr[col] * (double)xb[col];
+        }
+        total += (double)scales[(size_t)r * groups + grp] * dot;
+      }
+      y[(size_t)b * row_count + lr] = (float)total;
+    }
+  }
+  return OR_OK;
+}
+
+/* dequantizeCqRow analogue (cq.ts:243-295): out[c] = f32(W[r][c] * s[r][c/G]). */
+int or_row_i8(const int8_t* w, const float* scales, uint32_t n, uint32_t k, uint32_t g,
+              uint32_t row, float* out) {
+  if (g == 0 || k % g != 0 || row >= n) return OR_INVALID;
+  uint32_t groups = k / g;
+  for (uint32_t c = 0; c < k; c++)
+    out[c] = (float)((double)w[(size_t)row * k + c] * (double)scales[(size_t)row * groups + c / g]);
+  return OR_OK;
+}
+
+/* ------------------------------------------------- a2: int8 KV quantizer */
+
+/* One vector of runtime.ts:697-714: m = max(1e-12, max|x|) in float64,
+ * s = m/127, stored scale f32(s), code = roundTiesToEven(x/s) as Int8. */
+void or_kv_quantize(const float* x, uint32_t n, int8_t* codes, float* scale_out) {
+  double maximum = 1e-12;
+  for (uint32_t i = 0; i < n; i++) maximum = js_max(maximum, fabs((double)x[i]));
+  double scale = maximum / 127;
+  *scale_out = (float)scale;
+  for (uint32_t i = 0; i < n; i++) codes[i] = js_to_int8(or_round_ties_even((double)x[i] / scale));
+}
+
+/* KV cache geometry and slot map, runtime.ts:150-205 and 659-677. */
+typedef struct {
+  uint32_t layers, kv_heads, head_dim, max_length, sink, window, alloc;
+  int float_mode; /* kvCache: "float32" stores raw values, scale 1 */
+  int8_t *k8, *v8;
+  float *kf, *vf, *ks, *vs;
+} or_kv;
+
+or_kv* or_kv_create(uint32_t layers, uint32_t kv_heads, uint32_t head_dim, uint32_t max_length,
+                    uint32_t sink, uint32_t window, int float_mode) {
+  or_kv* kv = (or_kv*)calloc(1, sizeof(or_kv));
+  kv->layers = layers; kv->kv_heads = kv_heads; kv->head_dim = head_dim;
+  kv->max_length = max_length;
+  kv->sink = sink > max_length ? max_length : sink;
+  kv->window = window;
+  kv->alloc = window > 0 ? (max_length < kv->sink + window ? max_length : kv->sink + window)
+                         : max_length;
+  kv->float_mode = float_mode;
+  size_t elems = (size_t)layers * kv_heads * kv->alloc * head_dim;
+  size_t scales = (size_t)layers * kv_heads * kv->alloc;
+  if (float_mode) {
+    kv->kf = (float*)calloc(elems, sizeof(float));
+    kv->vf = (float*)calloc(elems, sizeof(float));
+  } else {
+    kv->k8 = (int8_t*)calloc(elems, 1);
+    kv->v8 = (int8_t*)calloc(elems, 1);
+  }
+  kv->ks = (float*)calloc(scales, sizeof(float));
+  kv->vs = (float*)calloc(scales, sizeof(float));
+  return kv;
+}
+
+void or_kv_destroy(or_kv* kv) {
+  if (!kv) return;
+  free(kv->k8); free(kv->v8); free(kv->kf); free(kv->vf); free(kv->ks); free(kv->vs);
+  free(kv);
+}
+
+uint32_t or_kv_alloc(const or_kv* kv) { return kv->alloc; }
+
+/* runtime.ts:659-664 #kvSlot */
+uint32_t or_kv_slot(const or_kv* kv, uint32_t position) {
+  if (kv->window == 0) return position;
+  if (position < kv->sink) return position;
+  return kv->sink + (position - kv->sink) % kv->window;
+}
+
+static size_t kv_base(const or_kv* kv, uint32_t layer, uint32_t head, uint32_t slot) {
+  return (((size_t)layer * kv->kv_heads + head) * kv->alloc + slot) * kv->head_dim;
+}
+static size_t kv_scale_index(const or_kv* kv, uint32_t layer, uint32_t head, uint32_t slot) {
+  return ((size_t)layer * kv->kv_heads + head) * kv->alloc + slot;
+}
+
+/* runtime.ts:679-717 #storeKV: k, v are [kv_heads][head_dim]. */
+int or_kv_store(or_kv* kv, uint32_t layer, uint32_t position, const float* k, const float* v) {
+  if (layer >= kv->layers || position >= kv->max_length) return OR_INVALID;
+  uint32_t slot = or_kv_slot(kv, position);
+  for (uint32_t h = 0; h < kv->kv_heads; h++) {
+    const float* kh = k + (size_t)h * kv->head_dim;
+    const float* vh = v + (size_t)h * kv->head_dim;
+    size_t base = kv_base(kv, layer, h, slot), si = kv_scale_index(kv, layer, h, slot);
+    if (kv->float_mode) {
+      memcpy(kv->kf + base, kh, sizeof(float) * kv->head_dim);
+      memcpy(kv->vf + base, vh, sizeof(float) * kv->head_dim);
+      kv->ks[si] = 1; kv->vs[si] = 1;
+    } else {
+      or_kv_quantize(kh, kv->head_dim, kv->k8 + base, kv->ks + si);
+      or_kv_quantize(vh, kv->head_dim, kv->v8 + base, kv->vs + si);
+    }
+  }
+  return OR_OK;
+}
+
+/* Copies out the int8 codes and scales of one (layer, head) for tests. */
+void or_kv_export(const or_kv* kv, uint32_t layer, uint32_t head, int8_t* kcodes, int8_t* vcodes,
+                  float* kscales, float* vscales) {
+  size_t base = kv_base(kv, layer, head, 0), si = kv_scale_index(kv, layer, head, 0);
+  if (!kv->float_mode) {
+    memcpy(kcodes, kv->k8 + base, (size_t)kv->alloc * kv->head_dim);
+    memcpy(vcodes, kv->v8 + base, (size_t)kv->alloc * kv->head_dim);
+  }
+  memcpy(kscales, kv->ks + si, sizeof(float) * kv->alloc);
+  memcpy(vscales, kv->vs + si, sizeof(float) * kv->alloc);
+}
+
+/* ------------------------------------------- a3: single-query attention */
+
+/* runtime.ts:719-786 #attention with softmaxInPlace (math.ts:46-60).
+ * q is [q_heads][head_dim]; out is [q_heads][head_dim]. */
+int or_attention(const or_kv* kv, uint32_t layer, uint32_t position, const float* q,
+                 uint32_t q_heads, float* out) {
+  uint32_t hd = kv->head_dim;
+  if (q_heads % kv->kv_heads != 0 || layer >= kv->layers || position >= kv->max_length)
+    return OR_INVALID;
+  uint32_t reps = q_heads / kv->kv_heads;
+  uint32_t prefix = kv->sink < position + 1 ? kv->sink : position + 1;
+  uint32_t recent_low = prefix;
+  if (kv->window > 0 && position + 1 > kv->window && position + 1 - kv->window > prefix)
+    recent_low = position + 1 - kv->window;
+  uint32_t count = prefix + (position - recent_low + 1);
+  uint32_t* logical = (uint32_t*)malloc(sizeof(uint32_t) * count);
+  float* scores = (float*)malloc(sizeof(float) * count);
+  uint32_t t = 0;
+  for (uint32_t i = 0; i < prefix; i++) logical[t++] = i;
+  for (uint32_t i = recent_low; i <= position; i++) logical[t++] = i;
+  double inverse_root = 1 / sqrt((double)hd);
+  memset(out, 0, sizeof(float) * (size_t)q_heads * hd);
+  for (uint32_t kvh = 0; kvh < kv->kv_heads; kvh++) {
+    for (uint32_t rep = 0; rep < reps; rep++) {
+      uint32_t qh = kvh * reps + rep;
+      const float* qv = q + (size_t)qh * hd;
+      for (uint32_t ti = 0; ti < count; ti++) {
+        uint32_t slot = or_kv_slot(kv, logical[ti]);
+        size_t base = kv_base(kv, layer, kvh, slot), si = kv_scale_index(kv, layer, kvh, slot);
+        double ks = kv->ks[si];
+        double dot = 0;
+        if (kv->float_mode) {
+          for (uint32_t i = 0; i < hd; i++) dot += (double)qv[i] * (double)kv->kf[base + i];
+        } else {
+          for (uint32_t i = 0; i < hd; i++) dot += (double)qv[i] * (double)kv->k8[base + i] * ks;
+        }
+        scores[ti] = (float)(dot * inverse_root);
+      }
+      or_softmax(scores, count);
+      float* o = out + (size_t)qh * hd;
+      for (uint32_t ti = 0; ti < count; ti++) {
+        uint32_t slot = or_kv_slot(kv, logical[ti]);
+        size_t base = kv_base(kv, layer, kvh, slot), si = kv_scale_index(kv, layer, kvh, slot);
+        double w = scores[ti];
+        if (kv->float_mode) {
+          for (uint32_t i = 0; i < hd; i++)
+            o[i] = (float)((double)o[i] + w * (double)kv->vf[base + i]);
+        } else {
+          double vs = kv->vs[si];
+          for (uint32_t i = 0; i < hd; i++)
+            o[i] = (float)((double)o[i] + w * (double)kv->v8[base + i] * vs);
+        }
+      }
+    }
+  }
+  free(logical);
+  free(scores);
+  return OR_OK;
+}

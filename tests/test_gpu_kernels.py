@@ -1,0 +1,216 @@
+"""GPU parity of the four hot-path kernels against the oracle, through the C ABI.
+
+Bars: int8 KV codes, scales and selected ids bit-exact; matvec and attention
+outputs within 1e-3 relative / 1e-4 absolute (|gpu - ref| <= 1e-4 + 1e-3|ref|);
+log-probabilities within 1e-9 relative (float64 on both sides).
+"""
+
+import json
+import math
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import assert_close
+from needle_hip import HipKvCache, Int8Matrix, MatrixRowRange, MatvecRequest, NeedleError
+from needle_hip import synth
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+RTOL, ATOL = 1e-3, 1e-4
+
+
+def say(*args):
+    print("[case]", *args, file=sys.stderr, flush=True)
+
+
+def matrix(seed, n, k, g):
+    w, s = synth.int8_matrix(seed, f"w{n}x{k}g{g}", n, k, g)
+    return Int8Matrix(w, s, g)
+
+
+# ------------------------------------------------------------------ matvec
+
+@pytest.mark.parametrize("n,k,g,batch", [
+    (4096, 4096, 32, 1), (4096, 4096, 32, 8),      # isolated matvec workload
+    (512, 512, 512, 1), (256, 512, 512, 3), (2048, 512, 512, 1), (512, 2048, 2048, 2),
+    (8192, 512, 512, 1), (32768, 512, 512, 1), (100, 128, 32, 5), (33, 8192, 64, 4),
+    (1, 1024, 1024, 1), (7, 256, 16, 8),
+])
+def test_matvec_matches_oracle(hip, n, k, g, batch):
+    say("matvec", n, k, g, batch)
+    m = matrix(11, n, k, g)
+    x = synth.Stream(5, f"x{k}b{batch}").normal((batch, k))
+    got = hip.matvec(m, x)
+    ref = oracle.matvec_i8(m.codes, m.scales, g, x)
+    assert_close(got, ref, RTOL, ATOL, f"matvec {n}x{k} g{g} b{batch}")
+
+
+def test_matvec_ranges_and_batch_requests(hip):
+    say("matvec ranges")
+    m = matrix(3, 512, 512, 512)
+    m2 = matrix(4, 2048, 512, 512)
+    x = synth.Stream(2, "xr").normal((512,))
+    full = hip.matvec(m, x)
+    part = hip.matvec(m, x, MatrixRowRange(100, 37))
+    assert np.array_equal(part, full[100:137])
+    outs = hip.matvec_batch([MatvecRequest(m, x), MatvecRequest(m, x, MatrixRowRange(1, 1)),
+                             MatvecRequest(m2, x, MatrixRowRange(8, 16))])
+    assert np.array_equal(outs[0], full)
+    assert np.array_equal(outs[1], full[1:2])
+    assert_close(outs[2], oracle.matvec_i8(m2.codes, m2.scales, 512, x, 8, 16), RTOL, ATOL)
+    with pytest.raises(NeedleError) as e:
+        hip.matvec(m, x, MatrixRowRange(500, 20))
+    assert e.value.code == "INVALID_CACT"
+    with pytest.raises(NeedleError):
+        hip.matvec(m, np.zeros(100, np.float32))
+
+
+def test_row_is_bit_exact(hip):
+    say("row")
+    m = matrix(8, 300, 512, 32)
+    for r in (0, 1, 150, 299):
+        assert np.array_equal(hip.row(m, r), oracle.row_i8(m.codes, m.scales, 32, r))
+    with pytest.raises(NeedleError):
+        hip.row(m, 300)
+
+
+# -------------------------------------------------------------- KV quantize
+
+def test_kv_golden_vectors_bit_exact(hip):
+    say("kv golden")
+    cases = json.loads((GOLDEN / "kv_quant.json").read_text())
+    kv = HipKvCache(hip, 1, 1, max_length=len(cases))
+    for p, case in enumerate(cases):
+        x = np.array(case["x"], np.float32)
+        kv.store(0, p, x, -x)
+    kc, vc, ks, vs = kv.read(0, 0)
+    for p, case in enumerate(cases):
+        assert kc[p].tolist() == case["codes"], case["name"]
+        assert vc[p].tolist() == [-c for c in case["codes"]], case["name"]
+        assert int(ks[p].view(np.uint32)) == case["scale_bits"], case["name"]
+    kv.free()
+
+
+@pytest.mark.parametrize("sigma", [1e-14, 1e-3, 1.0, 1e4])
+def test_kv_store_bit_exact_random(hip, sigma):
+    say("kv random", sigma)
+    layers, heads, n = 2, 8, 300
+    kv = HipKvCache(hip, layers, heads, max_length=n)
+    ref = oracle.KvCache(layers, heads, max_length=n)
+    s = synth.Stream(9, f"kv{sigma}")
+    K = (s.normal((n, heads, 64)) * np.float32(sigma)).astype(np.float32)
+    V = (s.normal((n, heads, 64)) * np.float32(sigma)).astype(np.float32)
+    K[5, 3] = 0.0  # zero vector: 1e-12 floor
+    kv.store(1, 0, K[:200], V[:200])        # bulk append
+    for p in range(200, n):                  # decode appends
+        kv.store(1, p, K[p], V[p])
+    ref.store(1, 0, K, V)
+    for h in range(heads):
+        for a, b in zip(kv.read(1, h), ref.read(1, h)):
+            assert np.array_equal(a.view(np.uint8) if a.dtype == np.int8 else a.view(np.uint32),
+                                  b.view(np.uint8) if b.dtype == np.int8 else b.view(np.uint32))
+    kv.free()
+
+
+def test_kv_ring_window_and_bulk_overwrite(hip):
+    say("kv ring")
+    sink, window, n = 3, 5, 23
+    kv = HipKvCache(hip, 1, 2, max_length=40, sink=sink, window=window)
+    ref = oracle.KvCache(1, 2, max_length=40, sink=sink, window=window)
+    s = synth.Stream(4, "ring")
+    K, V = s.normal((n, 2, 64)), s.normal((n, 2, 64))
+    kv.store(0, 0, K, V)  # one call: later positions win their ring slots
+    ref.store(0, 0, K, V)
+    for h in range(2):
+        for a, b in zip(kv.read(0, h), ref.read(0, h)):
+            assert np.array_equal(a, b)
+    with pytest.raises(NeedleError) as e:
+        kv.store(0, 39, np.zeros((2, 2, 64), np.float32), np.zeros((2, 2, 64), np.float32))
+    assert e.value.code == "CONTEXT_OVERFLOW"
+    kv.free()
+
+
+# ---------------------------------------------------------------- attention
+
+def _fill(kv, ref, layer, n, heads, seed):
+    s = synth.Stream(seed, f"att{n}")
+    K, V = s.normal((n, heads, 64)), s.normal((n, heads, 64))
+    kv.store(layer, 0, K, V)
+    ref.store(layer, 0, K, V)
+    return s
+
+
+@pytest.mark.parametrize("length", [512, 2048, 8192])
+def test_attention_int8_mha_contexts(hip, length):
+    say("attention mha", length)
+    heads = 8
+    kv = HipKvCache(hip, 1, heads, max_length=length)
+    ref = oracle.KvCache(1, heads, max_length=length)
+    s = _fill(kv, ref, 0, length, heads, 21)
+    q = s.normal((heads * 64,))
+    for pos in (0, 1, 63, 64, length // 2 + 3, length - 1):
+        assert_close(kv.attention(0, pos, q), ref.attention(0, pos, q), RTOL, ATOL,
+                     f"attention L={length} pos={pos}")
+    kv.free()
+
+
+@pytest.mark.parametrize("sink,window,mode", [(0, 256, "int8"), (7, 256, "int8"), (3, 5, "int8"),
+                                              (0, 0, "float32"), (4, 16, "float32")])
+def test_attention_gqa_window_sink(hip, sink, window, mode):
+    say("attention gqa", sink, window, mode)
+    n, hkv, hq = 300, 4, 8
+    kv = HipKvCache(hip, 2, hkv, max_length=n, sink=sink, window=window, kv_cache=mode)
+    ref = oracle.KvCache(2, hkv, max_length=n, sink=sink, window=window, kv_cache=mode)
+    s = synth.Stream(8, f"gqa{sink}{window}{mode}")
+    for p in range(n):
+        k, v = s.normal((hkv, 64)), s.normal((hkv, 64))
+        kv.store(1, p, k, v)
+        ref.store(1, p, k, v)
+        if p in (0, 2, 5, 6, 100, 255, 256, 299):
+            q = s.normal((hq * 64,))
+            assert_close(kv.attention(1, p, q), ref.attention(1, p, q), RTOL, ATOL,
+                         f"gqa pos={p}")
+    kv.free()
+
+
+# ---------------------------------------------------------------- selection
+
+def test_select_golden_cases(hip):
+    say("select golden")
+    for case in json.loads((GOLDEN / "select.json").read_text()):
+        logits = np.array(case["logits"], np.float32)
+        allowed = None if case["allowed"] is None else np.array(case["allowed"], np.uint32)
+        got, lp = hip.select(logits, allowed)
+        assert got == case["id"], case["name"]
+        rid, rlp = oracle.select(logits, allowed)
+        assert got == rid
+        assert (math.isnan(lp) and math.isnan(rlp)) or abs(lp - rlp) <= 1e-9 * max(1, abs(rlp))
+
+
+@pytest.mark.parametrize("vocab", [8192, 32768])
+def test_select_random_bit_exact_ids(hip, vocab):
+    say("select random", vocab)
+    s = synth.Stream(12, f"sel{vocab}")
+    for trial in range(20):
+        logits = s.normal((vocab,)) * np.float32(4)
+        if trial % 2:
+            logits = np.round(logits).astype(np.float32)  # many ties
+        if trial % 3 == 0:
+            allowed = None
+        else:
+            bits = s.uniform01(vocab) < 0.02
+            allowed = np.flatnonzero(bits).astype(np.uint32)
+            if trial % 3 == 2:
+                allowed = allowed[::-1].copy()  # list order, not id order
+        got, lp = hip.select(logits, allowed)
+        rid, rlp = oracle.select(logits, allowed)
+        assert got == rid, trial
+        assert abs(lp - rlp) <= 1e-9 * max(1, abs(rlp))
+    with pytest.raises(NeedleError):
+        hip.select(np.zeros(10, np.float32), np.array([10], np.uint32))
+    with pytest.raises(NeedleError):
+        hip.select(np.zeros(10, np.float32), np.array([], np.uint32))
