@@ -94,6 +94,17 @@ nd_status nd_matvec(nd_ctx* ctx, const nd_mat* mat, const float* x, uint32_t bat
 nd_status nd_matvec_d(nd_ctx* ctx, const nd_mat* mat, const float* x_dev, uint32_t batch,
                       uint32_t row_start, uint32_t row_count, float* y_dev, void* stream);
 
+/* y[m][n] = s[n] * sum_c W[n][c] * x[m][c] for m < rows on int8 MFMA: the
+ * batched matvec of InferenceBackend.matvec over `rows` activation vectors
+ * (the skinny GEMM of batched decode and prefill).  Each fp32 row of x is
+ * split exactly into three int8 digit planes with a power-of-two scale
+ * (representation error <= 2^-22 of the row's largest magnitude) and every
+ * plane is multiplied with int32 accumulation.  Requires per-row scales
+ * (g == k), k % 64 == 0 and k <= 2048.  With accumulate != 0, y += instead. */
+nd_status nd_matmul(nd_ctx* ctx, const nd_mat* mat, const float* x, uint32_t rows, float* y);
+nd_status nd_matmul_d(nd_ctx* ctx, const nd_mat* mat, const float* x_dev, uint32_t rows,
+                      float* y_dev, uint32_t accumulate, void* stream);
+
 /* One matvec request of a batch: MatvecRequest (backends/backend.ts:11-15). */
 typedef struct nd_matvec_job {
   const nd_mat* mat;
@@ -186,6 +197,89 @@ nd_status nd_select(nd_ctx* ctx, const float* logits, uint32_t vocab, const uint
 nd_status nd_select_mask_d(nd_ctx* ctx, const float* logits_dev, uint32_t batch, uint32_t vocab,
                            const uint32_t* mask_dev, uint32_t* ids_dev,
                            double* log_probabilities_dev, void* stream);
+
+/* --------------------------------- batched decoder (int8 MFMA, int8 KV) */
+
+typedef struct nd_decoder nd_decoder;
+typedef struct nd_batch nd_batch;
+
+/* A decoder built from the reference's per-token primitives: embedding row
+ * x sqrt(dim) (model/runtime.ts:305-309); per layer a = rmsNorm(x, attn_norm)
+ * (model/math.ts:16-32), q/k/v = Wq/Wk/Wv a, per-head rmsNormSlice with
+ * q_norm/k_norm and half-split RoPE (model/runtime.ts:471-500,
+ * model/math.ts:94-115), #storeKV and #attention (model/runtime.ts:679-786),
+ * x += Wo o, x += Wdown silu(Wup rmsNorm(x, ffn_norm)) (model/math.ts:12-14);
+ * logits = embedding . rmsNorm(x, final_norm) (model/runtime.ts:570-577).
+ * All matrices are per-row-scaled int8 (g == k) uploaded with
+ * nd_mat_upload_i8; norm vectors are host arrays copied at creation.
+ * Limits: head_dim 64, heads * 64 == dim, dim and ffn multiples of 64 and at
+ * most 2048, heads / kv_heads in {1, 2, 4, 8}. */
+typedef struct nd_decoder_desc {
+  uint32_t layers, dim, heads, kv_heads, head_dim, ffn, vocab;
+  float rope_theta;
+  const nd_mat* embedding;            /* [vocab][dim]; tied output projection */
+  const nd_mat* const* wq;            /* layers entries, [heads*64][dim] */
+  const nd_mat* const* wk;            /* [kv_heads*64][dim] */
+  const nd_mat* const* wv;            /* [kv_heads*64][dim] */
+  const nd_mat* const* wo;            /* [dim][heads*64] */
+  const nd_mat* const* wup;           /* [ffn][dim] */
+  const nd_mat* const* wdown;         /* [dim][ffn] */
+  const float* attn_norm;             /* [layers][dim] */
+  const float* ffn_norm;              /* [layers][dim] */
+  const float* q_norm;                /* [layers][64] */
+  const float* k_norm;                /* [layers][64] */
+  const float* final_norm;            /* [dim] */
+} nd_decoder_desc;
+
+/* The matrices stay owned by the caller and must outlive the decoder. */
+nd_status nd_decoder_create(nd_ctx* ctx, const nd_decoder_desc* desc, nd_decoder** out);
+nd_status nd_decoder_free(nd_ctx* ctx, nd_decoder* dec);
+
+/* `batch` independent sequences decoding together (no batch API exists in the
+ * reference: one NeedleRuntime is one sequence, model/runtime.ts:108-140; this
+ * is the additive batch extension of the backend).  Owns an int8 KV cache of
+ * max_length positions per sequence (no window, no sinks) and all step
+ * buffers, allocated once here. */
+nd_status nd_batch_create(nd_ctx* ctx, nd_decoder* dec, uint32_t batch, uint32_t max_length,
+                          nd_batch** out);
+nd_status nd_batch_free(nd_ctx* ctx, nd_batch* batch);
+
+/* The batch's KV cache: sequence s, KV head h is cache head s * kv_heads + h
+ * (read it with nd_kv_read). */
+nd_kv* nd_batch_kv(nd_batch* batch);
+
+/* Fills positions [0, length) of sequence `seq` in every layer with
+ * synthetic int8 rows: for layer l, head h, position p, element i < 64 the
+ * code is ((z >> 32) * 255 >> 32) - 127 and the scale lo + (hi - lo) *
+ * (z' >> 40) * 2^-24 (float64, stored f32), where z is output ((l * kv_heads
+ * + h) * index_stride + p) * 65 + i of the splitmix64 stream of seed_k (K) or
+ * seed_v (V), and z' is output ... * 65 + 64. */
+nd_status nd_batch_fill_synthetic(nd_ctx* ctx, nd_batch* batch, uint32_t seq, uint64_t seed_k,
+                                  uint64_t seed_v, uint32_t length, uint32_t index_stride,
+                                  float lo, float hi);
+
+/* Sets each sequence's current token and position and the step counter. */
+nd_status nd_batch_set_state(nd_ctx* ctx, nd_batch* batch, const uint32_t* tokens,
+                             const uint32_t* positions, uint32_t step);
+
+/* Enqueues one decode step of every sequence (about 10 launches per layer, no
+ * allocation, no host synchronisation; capturable in a HIP graph): each
+ * sequence runs its current token at its position, appends K/V, and selects
+ * the next token with selectToken semantics (model/runtime.ts:880-899); the
+ * selected ids become the current tokens and positions advance by one.  With
+ * use_masks, the allowed set of sequence b at step t is the bitmask whose bit
+ * v is set iff (z_v >> 40) < threshold24 or v is the forced id ((z_vocab >>
+ * 32) * vocab >> 32), z being the splitmix64 stream seeded by output
+ * t * 65536 + b of the stream of mask_seed (t = the device step counter).
+ * max_position must bound every sequence's position in this step. */
+nd_status nd_batch_step(nd_ctx* ctx, nd_batch* batch, uint32_t max_position, uint32_t use_masks,
+                        uint64_t mask_seed, uint32_t threshold24, void* stream);
+
+/* Copies the current tokens (the last selected ids), positions, the last
+ * step's log-probabilities and (optionally) logits [batch][vocab] to the
+ * host and synchronises. */
+nd_status nd_batch_read(nd_ctx* ctx, nd_batch* batch, uint32_t* tokens, uint32_t* positions,
+                        double* log_probabilities, float* logits);
 
 #ifdef __cplusplus
 }

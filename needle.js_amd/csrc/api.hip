@@ -51,6 +51,12 @@ static nd_status ensure_partials(nd_ctx* ctx, size_t floats) {
   }
   ND_HIP(ctx, hipMalloc(&ctx->attn_partials, floats * sizeof(float)));
   ctx->attn_partial_floats = floats;
+  if (!ctx->attn_counters) {
+    ND_HIP(ctx, hipMalloc(&ctx->attn_counters, kMaxAttentionKvHeads * sizeof(uint32_t)));
+    ND_HIP(ctx, hipMemsetAsync(ctx->attn_counters, 0, kMaxAttentionKvHeads * sizeof(uint32_t),
+                               ctx->stream));
+    ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  }
   return ND_OK;
 }
 
@@ -104,6 +110,8 @@ nd_status nd_destroy(nd_ctx* ctx) {
   }
   if (ctx->stage) hipFree(ctx->stage);
   if (ctx->attn_partials) hipFree(ctx->attn_partials);
+  if (ctx->attn_counters) hipFree(ctx->attn_counters);
+  if (ctx->mm_scratch) hipFree(ctx->mm_scratch);
   hipStreamDestroy(ctx->stream);
   delete ctx;
   return ND_OK;
@@ -303,6 +311,67 @@ nd_status nd_row(nd_ctx* ctx, const nd_mat* m, uint32_t row, float* out) {
   return ND_OK;
 }
 
+// ------------------------------------------------ batched matvec (MFMA)
+
+static nd_status check_matmul(nd_ctx* ctx, const nd_mat* m) {
+  if (!m) return nd_fail(ctx, ND_ERR_INVALID, "matrix is NULL");
+  if (m->g != m->k || m->k % 64 != 0 || m->k > 2048)
+    return nd_fail(ctx, ND_ERR_INVALID,
+                   "nd_matmul needs per-row scales (g == k), k %% 64 == 0 and k <= 2048 "
+                   "(got k=%u g=%u)", m->k, m->g);
+  return ND_OK;
+}
+
+static nd_status ensure_mm_scratch(nd_ctx* ctx, size_t bytes) {
+  if (ctx->mm_scratch_bytes >= bytes) return ND_OK;
+  if (ctx->mm_scratch) {
+    ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    ND_HIP(ctx, hipFree(ctx->mm_scratch));
+    ctx->mm_scratch = nullptr;
+    ctx->mm_scratch_bytes = 0;
+  }
+  ND_HIP(ctx, hipMalloc(&ctx->mm_scratch, bytes));
+  ctx->mm_scratch_bytes = bytes;
+  return ND_OK;
+}
+
+nd_status nd_matmul_d(nd_ctx* ctx, const nd_mat* m, const float* x, uint32_t rows, float* y,
+                      uint32_t accumulate, void* stream) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_matmul(ctx, m);
+  if (st != ND_OK) return st;
+  if (rows == 0) return ND_OK;
+  if (!x || !y) return nd_fail(ctx, ND_ERR_INVALID, "x or y is NULL");
+  const size_t dbytes = align256((size_t)3 * rows * m->k);
+  st = ensure_mm_scratch(ctx, dbytes + align256((size_t)rows * 4));
+  if (st != ND_OK) return st;
+  int8_t* digits = reinterpret_cast<int8_t*>(ctx->mm_scratch);
+  float* fm = reinterpret_cast<float*>(reinterpret_cast<char*>(ctx->mm_scratch) + dbytes);
+  hipStream_t s = nd_pick_stream(ctx, stream);
+  ND_HIP(ctx, nd_launch_digitize(x, m->k, nullptr, nullptr, digits, fm, rows, m->k, s));
+  ND_HIP(ctx, nd_launch_gemm(m, digits, fm, y, m->n, rows, accumulate ? 1 : 0, s));
+  return ND_OK;
+}
+
+nd_status nd_matmul(nd_ctx* ctx, const nd_mat* m, const float* x, uint32_t rows, float* y) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_matmul(ctx, m);
+  if (st != ND_OK) return st;
+  if (rows == 0) return ND_OK;
+  if (!x || !y) return nd_fail(ctx, ND_ERR_INVALID, "x or y is NULL");
+  const size_t xb = (size_t)rows * m->k * 4, yb = (size_t)rows * m->n * 4;
+  st = ensure_stage(ctx, align256(xb) + yb);
+  if (st != ND_OK) return st;
+  float* dx = reinterpret_cast<float*>(ctx->stage);
+  float* dy = reinterpret_cast<float*>(reinterpret_cast<char*>(ctx->stage) + align256(xb));
+  ND_HIP(ctx, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
+  st = nd_matmul_d(ctx, m, dx, rows, dy, 0, ctx->stream);
+  if (st != ND_OK) return st;
+  ND_HIP(ctx, hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ND_OK;
+}
+
 // -------------------------------------------------------------- KV cache
 
 nd_status nd_kv_create(nd_ctx* ctx, uint32_t layers, uint32_t kv_heads, uint32_t head_dim,
@@ -314,6 +383,9 @@ nd_status nd_kv_create(nd_ctx* ctx, uint32_t layers, uint32_t kv_heads, uint32_t
   if (head_dim != 64) return nd_fail(ctx, ND_ERR_INVALID, "head_dim %u is not 64", head_dim);
   if (layers == 0 || kv_heads == 0 || max_length == 0)
     return nd_fail(ctx, ND_ERR_INVALID, "empty KV cache geometry");
+  if (kv_heads > kMaxAttentionKvHeads || max_length > kMaxAttentionPositions)
+    return nd_fail(ctx, ND_ERR_INVALID, "KV cache limits: at most %u heads and %u positions",
+                   kMaxAttentionKvHeads, kMaxAttentionPositions);
   if (mode != ND_KV_INT8 && mode != ND_KV_FLOAT32)
     return nd_fail(ctx, ND_ERR_INVALID, "unknown KV mode %u", mode);
   nd_kv* kv = new nd_kv();
@@ -347,7 +419,7 @@ nd_status nd_kv_create(nd_ctx* ctx, uint32_t layers, uint32_t kv_heads, uint32_t
   // Attention partials for the largest visible set of this cache, with up to
   // 8 query heads per KV head.
   const uint32_t max_visible = kv->alloc;
-  nd_status st = ensure_partials(ctx, nd_attention_partial_floats(kv_heads * 8, max_visible));
+  nd_status st = ensure_partials(ctx, nd_attention_partial_floats(kv_heads * 8, kv_heads, max_visible));
   if (st != ND_OK) {
     hipFree(base);
     delete kv;
@@ -475,12 +547,12 @@ nd_status nd_attention_d(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t 
   if (!q || !out || (reinterpret_cast<uintptr_t>(q) & 15))
     return nd_fail(ctx, ND_ERR_INVALID, "q must be a 16-byte aligned device pointer");
   const nd_visible vis = nd_kv_visible(kv, position);
-  const size_t need = nd_attention_partial_floats(q_heads, vis.count);
-  if (need > ctx->attn_partial_floats && nd_attention_chunks(vis.count) > 1)
+  const size_t need = nd_attention_partial_floats(q_heads, kv->kv_heads, vis.count);
+  if (need > ctx->attn_partial_floats && nd_attention_chunks(vis.count, kv->kv_heads) > 1)
     return nd_fail(ctx, ND_ERR_INVALID, "attention partials too small (%zu > %zu floats)", need,
                    ctx->attn_partial_floats);
   ND_HIP(ctx, nd_launch_attention(kv, layer, position, q, q_heads, out, ctx->attn_partials,
-                                  nd_pick_stream(ctx, stream)));
+                                  ctx->attn_counters, nd_pick_stream(ctx, stream)));
   return ND_OK;
 }
 
@@ -491,7 +563,7 @@ nd_status nd_attention(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t po
   if (st != ND_OK) return st;
   if (!q || !out) return nd_fail(ctx, ND_ERR_INVALID, "q or out is NULL");
   const nd_visible vis = nd_kv_visible(kv, position);
-  st = ensure_partials(ctx, nd_attention_partial_floats(q_heads, vis.count));
+  st = ensure_partials(ctx, nd_attention_partial_floats(q_heads, kv->kv_heads, vis.count));
   if (st != ND_OK) return st;
   const size_t bytes = (size_t)q_heads * kv->head_dim * sizeof(float);
   st = ensure_stage(ctx, 2 * align256(bytes));
@@ -500,7 +572,7 @@ nd_status nd_attention(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t po
   float* dout = reinterpret_cast<float*>(reinterpret_cast<char*>(ctx->stage) + align256(bytes));
   ND_HIP(ctx, hipMemcpyAsync(dq, q, bytes, hipMemcpyHostToDevice, ctx->stream));
   ND_HIP(ctx, nd_launch_attention(kv, layer, position, dq, q_heads, dout, ctx->attn_partials,
-                                  ctx->stream));
+                                  ctx->attn_counters, ctx->stream));
   ND_HIP(ctx, hipMemcpyAsync(out, dout, bytes, hipMemcpyDeviceToHost, ctx->stream));
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return ND_OK;

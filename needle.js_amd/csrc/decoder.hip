@@ -1,0 +1,530 @@
+// Batched int8 decoder on HBM-resident weights and KV: the synthetic decoder
+// of the batched constrained-decode and prefill workloads, composed from the
+// reference primitives (embedding row x sqrt(d), runtime.ts:305-309; per-head
+// zero-centred RMS norm and half-split RoPE, runtime.ts:471-500 with
+// math.ts:94-115; #storeKV/#attention, runtime.ts:679-786; residual matvecs;
+// SiLU MLP, math.ts:12-14; tied logits, runtime.ts:570-577; selectToken over
+// an allowed bitmask, runtime.ts:880-899).
+//
+// One decode step of B sequences is a fixed sequence of kernel launches on one
+// stream with no host synchronisation and no allocation, so a caller can
+// capture it in a HIP graph; tokens, positions and the step counter advance
+// in device memory.
+#include <cmath>
+#include <vector>
+
+#include "nd_internal.hpp"
+
+namespace {
+
+constexpr uint32_t kHd = 64;
+
+__device__ __forceinline__ uint64_t sm64_mix(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+__device__ __forceinline__ uint64_t sm64_at(uint64_t seed, uint64_t i) {
+  return sm64_mix(seed + (i + 1) * 0x9E3779B97F4A7C15ull);
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_absmax_js(float v) {
+  v = fabsf(v);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float w = __shfl_xor(v, o, 64);
+    v = (v != v || w != w) ? __builtin_nanf("") : (v > w ? v : w);
+  }
+  return v;
+}
+
+// x[m][:] = f32(f32(W[tok][:] * s[tok]) * sqrt(d)), the row() gather and
+// embedding scale of runtime.ts:305-309, in float64 like the reference.
+__global__ void embed_kernel(const int8_t* __restrict__ W, const float* __restrict__ S,
+                             const uint32_t* __restrict__ tokens, uint32_t vocab, uint32_t d,
+                             double scale, float* __restrict__ x) {
+  const uint32_t m = blockIdx.y, k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= d) return;
+  const uint32_t tok = tokens[m] < vocab ? tokens[m] : vocab - 1;  // ids are validated on entry
+  const float row = (float)W[(size_t)tok * d + k] * S[tok];
+  x[(size_t)m * d + k] = (float)((double)row * scale);
+}
+
+// One wave per (row m, head slot).  Slots [0, H) are query heads: zero-centred
+// RMS norm with q_norm, then RoPE, written to q_out.  Slots [H, H + Hkv) are
+// KV heads: k gets k_norm and RoPE, then k and v are quantized into the cache
+// at the row's position (#storeKV bit-exact semantics).  Norm and rotation run
+// in float64 with f32 stores, as the reference does.
+__global__ __launch_bounds__(64) void qk_rope_store_kernel(
+    const float* __restrict__ qkv, uint32_t ld, uint32_t heads, uint32_t kv_heads,
+    const float* __restrict__ q_norm, const float* __restrict__ k_norm,
+    const double* __restrict__ inv_freq, const uint32_t* __restrict__ positions,
+    uint32_t position0, float* __restrict__ q_out, int8_t* __restrict__ Kc,
+    int8_t* __restrict__ Vc, float* __restrict__ Ks, float* __restrict__ Vs, uint32_t layer,
+    uint32_t cache_heads, uint32_t alloc, uint32_t kv_head_stride) {
+  const uint32_t m = blockIdx.y, slot = blockIdx.x, lane = threadIdx.x;
+  const uint32_t pos = positions ? positions[m] : position0 + m;
+  const bool is_q = slot < heads;
+  const uint32_t h = is_q ? slot : slot - heads;
+  const float* src = qkv + (size_t)m * ld + (is_q ? h * kHd : heads * kHd + h * kHd);
+  const float* scale = is_q ? q_norm : k_norm;
+  double x = src[lane];
+  const double inv = 1.0 / sqrt(wave_sum_d(x * x) / kHd + 1e-6);
+  const float normed = (float)((1.0 + (double)scale[lane]) * x * inv);
+  // Half-split RoPE: pair (j, j + 32), angle = pos * theta^(-2j/64).
+  const uint32_t j = lane & 31;
+  const double angle = (double)pos * inv_freq[j];
+  double sn, cs;
+  sincos(angle, &sn, &cs);
+  const double mine = normed;
+  const double other = __shfl_xor((double)normed, 32, 64);
+  const float rot = lane < 32 ? (float)(mine * cs - other * sn) : (float)(mine * cs + other * sn);
+  if (is_q) {
+    q_out[((size_t)m * heads + h) * kHd + lane] = rot;
+    return;
+  }
+  if (pos >= alloc) return;  // positions are validated on entry; never write past the cache
+  // Cache head for row m: (m * kv_head_stride + h) when rows are sequences of
+  // a batch (stride = Hkv), or h when rows are consecutive positions.
+  const size_t row = ((size_t)layer * cache_heads + (size_t)m * kv_head_stride + h) * alloc + pos;
+  const float kv = rot;
+  const float vv = qkv[(size_t)m * ld + (heads + kv_heads) * kHd + h * kHd + lane];
+  const float ak = wave_absmax_js(kv), av = wave_absmax_js(vv);
+  const double mk = (ak != ak) ? (double)ak : fmax(1e-12, (double)ak);
+  const double mv = (av != av) ? (double)av : fmax(1e-12, (double)av);
+  const double sk = mk / 127.0, sv = mv / 127.0;
+  const double ck = rint((double)kv / sk), cv = rint((double)vv / sv);
+  Kc[row * kHd + lane] = ck != ck ? (int8_t)0 : (int8_t)(int)ck;
+  Vc[row * kHd + lane] = cv != cv ? (int8_t)0 : (int8_t)(int)cv;
+  if (lane == 0) {
+    Ks[row] = (float)sk;
+    Vs[row] = (float)sv;
+  }
+}
+
+// Allowed-token bitmask rows for decode step *step of sequence b: id v is
+// allowed iff (z_v >> 40) < threshold24 with z the splitmix64 stream seeded by
+// splitmix64_at(mask_seed, step * 65536 + b); the id (z_vocab >> 32) * vocab
+// >> 32 is always allowed.  One thread per 32-bit word.
+__global__ void gen_masks_kernel(uint64_t mask_seed, const uint32_t* __restrict__ step,
+                                 uint32_t batch, uint32_t vocab, uint32_t threshold24,
+                                 uint32_t* __restrict__ masks) {
+  const uint32_t words = (vocab + 31) / 32;
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= batch * words) return;
+  const uint32_t b = i / words, w = i % words;
+  const uint64_t seed = sm64_at(mask_seed, (uint64_t)(*step) * 65536 + b);
+  const uint32_t forced = (uint32_t)(((sm64_at(seed, vocab) >> 32) * (uint64_t)vocab) >> 32);
+  uint32_t bits = 0;
+  for (uint32_t e = 0; e < 32; ++e) {
+    const uint32_t v = w * 32 + e;
+    if (v >= vocab) break;
+    if ((uint32_t)(sm64_at(seed, v) >> 40) < threshold24 || v == forced) bits |= 1u << e;
+  }
+  masks[i] = bits;
+}
+
+// Synthetic prefix rows for sequence `seq`: codes ((z >> 32) * 255 >> 32) -
+// 127 and scale lo + (hi - lo) * (z >> 40) * 2^-24 from the stream of the K or
+// V seed at index ((l * Hkv + h) * index_stride + p) * 65 + i.
+__global__ __launch_bounds__(64) void fill_kv_kernel(uint64_t seed_k, uint64_t seed_v,
+                                                     uint32_t seq, uint32_t kv_heads,
+                                                     uint32_t cache_heads, uint32_t alloc,
+                                                     uint32_t index_stride, float lo, float hi,
+                                                     int8_t* __restrict__ Kc,
+                                                     int8_t* __restrict__ Vc,
+                                                     float* __restrict__ Ks,
+                                                     float* __restrict__ Vs) {
+  const uint32_t p = blockIdx.x, h = blockIdx.y, l = blockIdx.z, lane = threadIdx.x;
+  const uint64_t base = (((uint64_t)l * kv_heads + h) * index_stride + p) * (kHd + 1);
+  const size_t row = ((size_t)l * cache_heads + (size_t)seq * kv_heads + h) * alloc + p;
+  const uint64_t zk = sm64_at(seed_k, base + lane), zv = sm64_at(seed_v, base + lane);
+  Kc[row * kHd + lane] = (int8_t)((int)(((zk >> 32) * 255ull) >> 32) - 127);
+  Vc[row * kHd + lane] = (int8_t)((int)(((zv >> 32) * 255ull) >> 32) - 127);
+  if (lane == 0) {
+    const double uk = (double)(sm64_at(seed_k, base + kHd) >> 40) * (1.0 / 16777216.0);
+    const double uv = (double)(sm64_at(seed_v, base + kHd) >> 40) * (1.0 / 16777216.0);
+    Ks[row] = (float)((double)lo + ((double)hi - (double)lo) * uk);
+    Vs[row] = (float)((double)lo + ((double)hi - (double)lo) * uv);
+  }
+}
+
+// After selection: feed ids back as the next tokens, advance positions and the
+// step counter.
+__global__ void advance_kernel(const uint32_t* __restrict__ ids, uint32_t* __restrict__ tokens,
+                               uint32_t* __restrict__ positions, uint32_t* __restrict__ step,
+                               uint32_t batch) {
+  const uint32_t b = threadIdx.x + blockIdx.x * blockDim.x;
+  if (b < batch) {
+    tokens[b] = ids[b];
+    positions[b] += 1;
+  }
+  if (b == 0) *step += 1;
+}
+
+}  // namespace
+
+struct nd_decoder {
+  uint32_t layers = 0, dim = 0, heads = 0, kv_heads = 0, head_dim = 0, ffn = 0, vocab = 0;
+  const nd_mat* embedding = nullptr;
+  std::vector<nd_mat> wqkv;  // owned: rows q (heads*64), k (kv_heads*64), v (kv_heads*64)
+  std::vector<const nd_mat*> wo, wup, wdown;
+  float* norms = nullptr;  // attn [L][d], ffn [L][d], q [L][64], k [L][64], final [d]
+  double* inv_freq = nullptr;
+  size_t attn_off = 0, ffn_off = 0, q_off = 0, k_off = 0, final_off = 0;
+};
+
+struct nd_batch {
+  nd_decoder* dec = nullptr;
+  uint32_t batch = 0, max_length = 0;
+  nd_kv kv;  // kv_heads = batch * dec->kv_heads
+  char* arena = nullptr;
+  float *x = nullptr, *qkv = nullptr, *q = nullptr, *o = nullptr, *h = nullptr,
+        *logits = nullptr, *fm = nullptr, *partials = nullptr;
+  int8_t* digits = nullptr;
+  uint32_t *counters = nullptr, *masks = nullptr, *tokens = nullptr, *positions = nullptr,
+           *step = nullptr, *ids = nullptr;
+  double* logprobs = nullptr;
+};
+
+static inline size_t a256(size_t n) { return (n + 255) & ~size_t(255); }
+
+static nd_status check_weight(nd_ctx* ctx, const nd_mat* m, uint32_t n, uint32_t k,
+                              const char* what) {
+  if (!m) return nd_fail(ctx, ND_ERR_INVALID, "%s is NULL", what);
+  if (m->n != n || m->k != k || m->g != k)
+    return nd_fail(ctx, ND_ERR_INVALID, "%s is %ux%u (group %u); expected %ux%u per-row scaled",
+                   what, m->n, m->k, m->g, n, k);
+  return ND_OK;
+}
+
+extern "C" {
+
+nd_status nd_decoder_create(nd_ctx* ctx, const nd_decoder_desc* d, nd_decoder** out) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!d || !out) return nd_fail(ctx, ND_ERR_INVALID, "nd_decoder_create: NULL argument");
+  *out = nullptr;
+  if (d->head_dim != kHd || d->layers == 0 || d->heads == 0 || d->kv_heads == 0 ||
+      d->heads % d->kv_heads != 0 || d->dim % 64 != 0 || d->ffn % 64 != 0 || d->dim > 2048 ||
+      d->ffn > 2048 || d->heads * kHd != d->dim)
+    return nd_fail(ctx, ND_ERR_INVALID,
+                   "decoder geometry: head_dim 64, heads * 64 == dim, dim and ffn multiples of 64 "
+                   "and at most 2048");
+  const uint32_t rep = d->heads / d->kv_heads;
+  if (rep != 1 && rep != 2 && rep != 4 && rep != 8)
+    return nd_fail(ctx, ND_ERR_INVALID, "query heads per KV head must be 1, 2, 4 or 8");
+  nd_status st = check_weight(ctx, d->embedding, d->vocab, d->dim, "embedding");
+  if (st != ND_OK) return st;
+  for (uint32_t l = 0; l < d->layers; ++l) {
+    if ((st = check_weight(ctx, d->wq[l], d->heads * kHd, d->dim, "wq")) ||
+        (st = check_weight(ctx, d->wk[l], d->kv_heads * kHd, d->dim, "wk")) ||
+        (st = check_weight(ctx, d->wv[l], d->kv_heads * kHd, d->dim, "wv")) ||
+        (st = check_weight(ctx, d->wo[l], d->dim, d->heads * kHd, "wo")) ||
+        (st = check_weight(ctx, d->wup[l], d->ffn, d->dim, "wup")) ||
+        (st = check_weight(ctx, d->wdown[l], d->dim, d->ffn, "wdown")))
+      return st;
+  }
+  nd_decoder* dec = new nd_decoder();
+  dec->layers = d->layers;
+  dec->dim = d->dim;
+  dec->heads = d->heads;
+  dec->kv_heads = d->kv_heads;
+  dec->head_dim = d->head_dim;
+  dec->ffn = d->ffn;
+  dec->vocab = d->vocab;
+  dec->embedding = d->embedding;
+  const uint32_t qkv_rows = (d->heads + 2 * d->kv_heads) * kHd;
+  dec->wqkv.resize(d->layers);
+  hipError_t e = hipSuccess;
+  for (uint32_t l = 0; l < d->layers && e == hipSuccess; ++l) {
+    nd_mat& m = dec->wqkv[l];
+    m.n = qkv_rows;
+    m.k = d->dim;
+    m.g = d->dim;
+    e = hipMalloc(&m.w, (size_t)qkv_rows * d->dim);
+    if (e == hipSuccess) e = hipMalloc(&m.scales, (size_t)qkv_rows * 4);
+    const nd_mat* parts[3] = {d->wq[l], d->wk[l], d->wv[l]};
+    size_t row = 0;
+    for (const nd_mat* p : parts) {
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(m.w + row * d->dim, p->w, (size_t)p->n * d->dim, hipMemcpyDeviceToDevice,
+                           ctx->stream);
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(m.scales + row, p->scales, (size_t)p->n * 4, hipMemcpyDeviceToDevice,
+                           ctx->stream);
+      row += p->n;
+    }
+    dec->wo.push_back(d->wo[l]);
+    dec->wup.push_back(d->wup[l]);
+    dec->wdown.push_back(d->wdown[l]);
+  }
+  const size_t L = d->layers, D = d->dim;
+  dec->attn_off = 0;
+  dec->ffn_off = L * D;
+  dec->q_off = 2 * L * D;
+  dec->k_off = 2 * L * D + L * kHd;
+  dec->final_off = 2 * L * D + 2 * L * kHd;
+  const size_t nf = dec->final_off + D;
+  std::vector<float> host(nf);
+  for (size_t i = 0; i < L * D; ++i) {
+    host[dec->attn_off + i] = d->attn_norm[i];
+    host[dec->ffn_off + i] = d->ffn_norm[i];
+  }
+  for (size_t i = 0; i < L * kHd; ++i) {
+    host[dec->q_off + i] = d->q_norm[i];
+    host[dec->k_off + i] = d->k_norm[i];
+  }
+  for (size_t i = 0; i < D; ++i) host[dec->final_off + i] = d->final_norm[i];
+  // RoPE frequencies theta^(-2j/64) in float64 (math.ts:94-115).
+  std::vector<double> freq(kHd / 2);
+  for (uint32_t j = 0; j < kHd / 2; ++j)
+    freq[j] = std::pow((double)d->rope_theta, -(2.0 * j) / kHd);
+  if (e == hipSuccess) e = hipMalloc(&dec->norms, nf * 4);
+  if (e == hipSuccess) e = hipMalloc(&dec->inv_freq, freq.size() * 8);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(dec->norms, host.data(), nf * 4, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(dec->inv_freq, freq.data(), freq.size() * 8, hipMemcpyHostToDevice,
+                       ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    for (auto& m : dec->wqkv) {
+      hipFree(m.w);
+      hipFree(m.scales);
+    }
+    hipFree(dec->norms);
+    hipFree(dec->inv_freq);
+    delete dec;
+    return nd_hip_fail(ctx, e, "decoder upload");
+  }
+  *out = dec;
+  return ND_OK;
+}
+
+nd_status nd_decoder_free(nd_ctx* ctx, nd_decoder* dec) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!dec) return ND_OK;
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  for (auto& m : dec->wqkv) {
+    hipFree(m.w);
+    hipFree(m.scales);
+  }
+  hipFree(dec->norms);
+  hipFree(dec->inv_freq);
+  delete dec;
+  return ND_OK;
+}
+
+nd_status nd_batch_create(nd_ctx* ctx, nd_decoder* dec, uint32_t batch, uint32_t max_length,
+                          nd_batch** out) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!dec || !out || batch == 0 || max_length == 0)
+    return nd_fail(ctx, ND_ERR_INVALID, "nd_batch_create: bad argument");
+  if (max_length > kMaxAttentionPositions || batch * dec->kv_heads > kMaxAttentionKvHeads)
+    return nd_fail(ctx, ND_ERR_INVALID, "batch limits: %u positions, %u KV heads in total",
+                   kMaxAttentionPositions, kMaxAttentionKvHeads);
+  *out = nullptr;
+  nd_batch* b = new nd_batch();
+  b->dec = dec;
+  b->batch = batch;
+  b->max_length = max_length;
+  nd_kv& kv = b->kv;
+  kv.layers = dec->layers;
+  kv.kv_heads = batch * dec->kv_heads;
+  kv.head_dim = kHd;
+  kv.max_length = max_length;
+  kv.sink = 0;
+  kv.window = 0;
+  kv.alloc = max_length;
+  kv.mode = ND_KV_INT8;
+  const size_t rows = (size_t)kv.layers * kv.kv_heads * kv.alloc;
+  const uint32_t rep = dec->heads / dec->kv_heads;
+  const size_t pf = nd_attention_batch_partial_floats(batch, dec->kv_heads, rep, max_length);
+  const uint32_t kmax = dec->ffn > dec->dim ? dec->ffn : dec->dim;
+  const uint32_t qkv_rows = (dec->heads + 2 * dec->kv_heads) * kHd;
+  const uint32_t words = (dec->vocab + 31) / 32;
+  size_t sizes[] = {
+      a256(rows * kHd), a256(rows * kHd), a256(rows * 4), a256(rows * 4),   // K, V, scales
+      a256((size_t)batch * dec->dim * 4),                                    // x
+      a256((size_t)batch * qkv_rows * 4),                                    // qkv
+      a256((size_t)batch * dec->dim * 4),                                    // q
+      a256((size_t)batch * dec->dim * 4),                                    // o
+      a256((size_t)batch * dec->ffn * 4),                                    // h
+      a256((size_t)batch * dec->vocab * 4),                                  // logits
+      a256((size_t)batch * 4),                                               // fm
+      a256(pf * 4),                                                          // partials
+      a256((size_t)3 * batch * kmax),                                        // digits
+      a256((size_t)batch * dec->kv_heads * 4),                               // counters
+      a256((size_t)batch * words * 4),                                       // masks
+      a256((size_t)batch * 4), a256((size_t)batch * 4), a256(256),           // tokens, positions, step
+      a256((size_t)batch * 4), a256((size_t)batch * 8)};                     // ids, logprobs
+  size_t total = 0;
+  for (size_t v : sizes) total += v;
+  hipError_t e = hipMalloc(&b->arena, total);
+  if (e == hipSuccess) e = hipMemsetAsync(b->arena, 0, total, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    if (b->arena) hipFree(b->arena);
+    delete b;
+    return nd_hip_fail(ctx, e, "batch allocation");
+  }
+  char* p = b->arena;
+  size_t i = 0;
+  auto take = [&](void* dst_ptr) {
+    *reinterpret_cast<char**>(dst_ptr) = p;
+    p += sizes[i++];
+  };
+  take(&kv.k);
+  take(&kv.v);
+  take(&kv.ks);
+  take(&kv.vs);
+  take(&b->x);
+  take(&b->qkv);
+  take(&b->q);
+  take(&b->o);
+  take(&b->h);
+  take(&b->logits);
+  take(&b->fm);
+  take(&b->partials);
+  take(&b->digits);
+  take(&b->counters);
+  take(&b->masks);
+  take(&b->tokens);
+  take(&b->positions);
+  take(&b->step);
+  take(&b->ids);
+  take(&b->logprobs);
+  *out = b;
+  return ND_OK;
+}
+
+nd_status nd_batch_free(nd_ctx* ctx, nd_batch* b) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!b) return ND_OK;
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  hipFree(b->arena);
+  delete b;
+  return ND_OK;
+}
+
+nd_kv* nd_batch_kv(nd_batch* b) { return b ? &b->kv : nullptr; }
+
+nd_status nd_batch_fill_synthetic(nd_ctx* ctx, nd_batch* b, uint32_t seq, uint64_t seed_k,
+                                  uint64_t seed_v, uint32_t length, uint32_t index_stride,
+                                  float lo, float hi) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!b || seq >= b->batch || length > b->max_length)
+    return nd_fail(ctx, ND_ERR_INVALID, "nd_batch_fill_synthetic: bad sequence or length");
+  if (length == 0) return ND_OK;
+  const nd_decoder* dec = b->dec;
+  hipLaunchKernelGGL(fill_kv_kernel, dim3(length, dec->kv_heads, dec->layers), dim3(64), 0,
+                     ctx->stream, seed_k, seed_v, seq, dec->kv_heads, b->kv.kv_heads, b->kv.alloc,
+                     index_stride, lo, hi, (int8_t*)b->kv.k, (int8_t*)b->kv.v, b->kv.ks, b->kv.vs);
+  ND_HIP(ctx, hipGetLastError());
+  return ND_OK;
+}
+
+nd_status nd_batch_set_state(nd_ctx* ctx, nd_batch* b, const uint32_t* tokens,
+                             const uint32_t* positions, uint32_t step) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!b || !tokens || !positions) return nd_fail(ctx, ND_ERR_INVALID, "NULL argument");
+  for (uint32_t i = 0; i < b->batch; ++i) {
+    if (tokens[i] >= b->dec->vocab)
+      return nd_fail(ctx, ND_ERR_INVALID, "Token %u is outside the vocabulary", tokens[i]);
+    if (positions[i] >= b->max_length)
+      return nd_fail(ctx, ND_ERR_OVERFLOW, "Position %u reached runtime limit %u", positions[i],
+                     b->max_length);
+  }
+  ND_HIP(ctx, hipMemcpyAsync(b->tokens, tokens, b->batch * 4, hipMemcpyHostToDevice, ctx->stream));
+  ND_HIP(ctx, hipMemcpyAsync(b->positions, positions, b->batch * 4, hipMemcpyHostToDevice,
+                             ctx->stream));
+  ND_HIP(ctx, hipMemcpyAsync(b->step, &step, 4, hipMemcpyHostToDevice, ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ND_OK;
+}
+
+nd_status nd_batch_read(nd_ctx* ctx, nd_batch* b, uint32_t* tokens, uint32_t* positions,
+                        double* logprobs, float* logits) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!b) return nd_fail(ctx, ND_ERR_INVALID, "batch is NULL");
+  if (tokens)
+    ND_HIP(ctx, hipMemcpyAsync(tokens, b->tokens, b->batch * 4, hipMemcpyDeviceToHost, ctx->stream));
+  if (positions)
+    ND_HIP(ctx, hipMemcpyAsync(positions, b->positions, b->batch * 4, hipMemcpyDeviceToHost,
+                               ctx->stream));
+  if (logprobs)
+    ND_HIP(ctx, hipMemcpyAsync(logprobs, b->logprobs, b->batch * 8, hipMemcpyDeviceToHost,
+                               ctx->stream));
+  if (logits)
+    ND_HIP(ctx, hipMemcpyAsync(logits, b->logits, (size_t)b->batch * b->dec->vocab * 4,
+                               hipMemcpyDeviceToHost, ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ND_OK;
+}
+
+// One decode step for all sequences.  Reads tokens/positions/step from device
+// memory; with masks == 1 the step's allowed bitmasks are generated on the
+// device from mask_seed and applied, otherwise selection is unconstrained.
+// `max_position` bounds every sequence's position this step (sizes the
+// attention grid); positions beyond it are not read.
+nd_status nd_batch_step(nd_ctx* ctx, nd_batch* b, uint32_t max_position, uint32_t use_masks,
+                        uint64_t mask_seed, uint32_t threshold24, void* stream) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!b) return nd_fail(ctx, ND_ERR_INVALID, "batch is NULL");
+  if (max_position >= b->max_length)
+    return nd_fail(ctx, ND_ERR_OVERFLOW, "Position %u reached runtime limit %u", max_position,
+                   b->max_length);
+  hipStream_t s = nd_pick_stream(ctx, stream);
+  const nd_decoder* dec = b->dec;
+  const uint32_t B = b->batch, D = dec->dim, F = dec->ffn;
+  const uint32_t qkv_rows = (dec->heads + 2 * dec->kv_heads) * kHd;
+  const uint32_t rep = dec->heads / dec->kv_heads;
+  hipLaunchKernelGGL(embed_kernel, dim3((D + 255) / 256, B), dim3(256), 0, s, dec->embedding->w,
+                     dec->embedding->scales, b->tokens, dec->vocab, D, std::sqrt((double)D), b->x);
+  ND_HIP(ctx, hipGetLastError());
+  for (uint32_t l = 0; l < dec->layers; ++l) {
+    ND_HIP(ctx, nd_launch_digitize(b->x, D, dec->norms + dec->attn_off + (size_t)l * D, nullptr,
+                                   b->digits, b->fm, B, D, s));
+    ND_HIP(ctx, nd_launch_gemm(&dec->wqkv[l], b->digits, b->fm, b->qkv, qkv_rows, B, 0, s));
+    hipLaunchKernelGGL(qk_rope_store_kernel, dim3(dec->heads + dec->kv_heads, B), dim3(64), 0, s,
+                       b->qkv, qkv_rows, dec->heads, dec->kv_heads,
+                       dec->norms + dec->q_off + (size_t)l * kHd,
+                       dec->norms + dec->k_off + (size_t)l * kHd, dec->inv_freq, b->positions, 0u,
+                       b->q, (int8_t*)b->kv.k, (int8_t*)b->kv.v, b->kv.ks, b->kv.vs, l,
+                       b->kv.kv_heads, b->kv.alloc, dec->kv_heads);
+    ND_HIP(ctx, hipGetLastError());
+    ND_HIP(ctx, nd_launch_attention_batch(&b->kv, l, b->positions, B, dec->kv_heads, rep,
+                                          max_position, b->q, b->o, b->partials, b->counters, s));
+    ND_HIP(ctx, nd_launch_digitize(b->o, D, nullptr, nullptr, b->digits, b->fm, B, D, s));
+    ND_HIP(ctx, nd_launch_gemm(dec->wo[l], b->digits, b->fm, b->x, D, B, 1, s));
+    ND_HIP(ctx, nd_launch_digitize(b->x, D, dec->norms + dec->ffn_off + (size_t)l * D, nullptr,
+                                   b->digits, b->fm, B, D, s));
+    ND_HIP(ctx, nd_launch_gemm(dec->wup[l], b->digits, b->fm, b->h, F, B, 2, s));
+    ND_HIP(ctx, nd_launch_digitize(b->h, F, nullptr, nullptr, b->digits, b->fm, B, F, s));
+    ND_HIP(ctx, nd_launch_gemm(dec->wdown[l], b->digits, b->fm, b->x, D, B, 1, s));
+  }
+  ND_HIP(ctx, nd_launch_digitize(b->x, D, dec->norms + dec->final_off, nullptr, b->digits, b->fm,
+                                 B, D, s));
+  ND_HIP(ctx, nd_launch_gemm(dec->embedding, b->digits, b->fm, b->logits, dec->vocab, B, 0, s));
+  const uint32_t words = (dec->vocab + 31) / 32;
+  if (use_masks) {
+    const uint32_t n = B * words;
+    hipLaunchKernelGGL(gen_masks_kernel, dim3((n + 255) / 256), dim3(256), 0, s, mask_seed,
+                       b->step, B, dec->vocab, threshold24, b->masks);
+    ND_HIP(ctx, hipGetLastError());
+  }
+  ND_HIP(ctx, nd_launch_select_mask(b->logits, B, dec->vocab, use_masks ? b->masks : nullptr,
+                                    b->ids, b->logprobs, s));
+  hipLaunchKernelGGL(advance_kernel, dim3((B + 255) / 256), dim3(256), 0, s, b->ids, b->tokens,
+                     b->positions, b->step, B);
+  ND_HIP(ctx, hipGetLastError());
+  return ND_OK;
+}
+
+}  // extern "C"

@@ -83,6 +83,17 @@ __device__ __forceinline__ uint32_t logical_at(const Visible& vis, uint32_t t) {
   return t < vis.prefix ? t : vis.recent_low + (t - vis.prefix);
 }
 
+// Visible positions of query `position` (model/runtime.ts:723-728).
+__device__ __forceinline__ Visible visible_at(uint32_t position, uint32_t sink, uint32_t window) {
+  Visible v;
+  v.prefix = sink < position + 1 ? sink : position + 1;
+  v.recent_low = v.prefix;
+  if (window > 0 && position + 1 > window && position + 1 - window > v.prefix)
+    v.recent_low = position + 1 - window;
+  v.count = v.prefix + (position - v.recent_low + 1);
+  return v;
+}
+
 __device__ __forceinline__ void decode16(const uint4& w, float* out) {
   const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -93,41 +104,58 @@ __device__ __forceinline__ void decode16(const uint4& w, float* out) {
   }
 }
 
-// One wave per (kv head, chunk of 64 visible positions), serving all REP
-// query heads of the kv head so that each code byte is read once.
-// Lane l owns dims [16*(l&3), +16) of tokens chunk + (l>>2) + 16*k, k < 4.
-// Output per query head and chunk: (max score m, sum exp l, acc[64]) or, for
-// a single chunk, the normalized result directly.
+// One workgroup of W waves (W <= 4) per (kv head, chunk of 64*W visible
+// positions), serving all REP query heads of the kv head so that each code
+// byte is read once.  In wave w, lane l owns dims [16*(l&3), +16) of the
+// positions chunk*64W + 64w + (l>>2) + 16k, k < 4, so every 128-bit load of
+// the wave reads 16 consecutive 64-byte code rows (1 KiB contiguous).
+//
+// Each wave reduces its 64 positions to (max m, sum l, acc[64]) per query
+// head; the waves are merged through LDS.  With one chunk the workgroup
+// writes the normalized output.  Otherwise it writes its partial, and the
+// last workgroup of the kv head to finish (device-scope counter, reset by
+// that workgroup) merges all chunks with a log-sum-exp combine.
+constexpr int kMaxWaves = 4;
+
 template <int REP, bool F32>
-__global__ __launch_bounds__(64) void attention_chunk_kernel(
+__global__ __launch_bounds__(256) void attention_kernel(
     const void* __restrict__ Kc, const void* __restrict__ Vc, const float* __restrict__ Ks,
     const float* __restrict__ Vs, const float* __restrict__ Q, float* __restrict__ out,
-    float* __restrict__ partials, uint32_t layer, uint32_t kv_heads, uint32_t alloc, uint32_t sink,
-    uint32_t window, Visible vis, uint32_t nchunks, float score_scale) {
-  const uint32_t chunk = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x;
+    float* __restrict__ part_acc, float* __restrict__ part_ml, uint32_t* __restrict__ counters,
+    uint32_t layer, uint32_t kv_heads, uint32_t alloc, uint32_t sink, uint32_t window,
+    Visible vis, const uint32_t* __restrict__ positions, uint32_t seq_kv_heads,
+    uint32_t max_chunks, float score_scale) {
+  // blockIdx.z selects the sequence of a batch: its KV heads are cache heads
+  // [z * seq_kv_heads, +seq_kv_heads), its queries rows [z * Hq, +Hq), and its
+  // query position is positions[z] (or the single `vis` when positions is null).
+  const uint32_t chunk = blockIdx.x, z = blockIdx.z;
+  const uint32_t kvh_local = blockIdx.y;
+  const uint32_t kvh = z * seq_kv_heads + kvh_local;
+  const uint32_t hq = seq_kv_heads * REP;
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t nwaves = blockDim.x >> 6;
   const uint32_t quad = lane & 3, trow = lane >> 2;
-  const size_t head_base = ((size_t)layer * kv_heads + kvh) * alloc;
-
-  float q[REP][16];
-#pragma unroll
-  for (int h = 0; h < REP; ++h) {
-    const float4* qp = reinterpret_cast<const float4*>(Q + (size_t)(kvh * REP + h) * kHeadDim + quad * 16);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float4 f = qp[c];
-      q[h][4 * c + 0] = f.x;
-      q[h][4 * c + 1] = f.y;
-      q[h][4 * c + 2] = f.z;
-      q[h][4 * c + 3] = f.w;
-    }
+  if (positions) {
+    if (window == 0 && positions[z] >= alloc) return;  // validated on entry; stay in bounds
+    vis = visible_at(positions[z], sink, window);
   }
+  // The grid covers max_chunks; a position beyond the launch's bound is a
+  // caller error that must not turn into out-of-range partial writes.
+  uint32_t nchunks = (vis.count + kChunk * nwaves - 1) / (kChunk * nwaves);
+  if (nchunks > max_chunks) nchunks = max_chunks;
+  if (chunk >= nchunks) return;
+  Q += (size_t)z * hq * kHeadDim;
+  out += (size_t)z * hq * kHeadDim;
+  const size_t part_base = (size_t)z * hq * max_chunks;
+  const size_t head_base = ((size_t)layer * kv_heads + kvh) * alloc;
+  const uint32_t tok0 = (chunk * nwaves + wave) * kChunk;
 
   float kc[4][16], vc[4][16];
   float ks[4], vs[4];
   bool valid[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const uint32_t t = chunk * kChunk + trow + 16 * k;
+    const uint32_t t = tok0 + trow + 16 * k;
     valid[k] = t < vis.count;
     const uint32_t slot = kv_slot(logical_at(vis, valid[k] ? t : 0), sink, window);
     const size_t row = head_base + slot;
@@ -150,9 +178,26 @@ __global__ __launch_bounds__(64) void attention_chunk_kernel(
     }
   }
 
-  float m[REP], l[REP], p[REP][4];
+  float q[REP][16];
 #pragma unroll
   for (int h = 0; h < REP; ++h) {
+    const float4* qp = reinterpret_cast<const float4*>(Q + (size_t)(kvh_local * REP + h) * kHeadDim + quad * 16);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float4 f = qp[c];
+      q[h][4 * c + 0] = f.x;
+      q[h][4 * c + 1] = f.y;
+      q[h][4 * c + 2] = f.z;
+      q[h][4 * c + 3] = f.w;
+    }
+  }
+
+  __shared__ float s_m[kMaxWaves][REP], s_l[kMaxWaves][REP];
+  __shared__ float s_acc[kMaxWaves][REP * kHeadDim];
+
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+    float sc[4];
     float mh = -INFINITY;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -161,97 +206,141 @@ __global__ __launch_bounds__(64) void attention_chunk_kernel(
       for (int i = 0; i < 16; ++i) d = fmaf(q[h][i], kc[k][i], d);
       d += __shfl_xor(d, 1, 64);
       d += __shfl_xor(d, 2, 64);
-      const float s = valid[k] ? d * ks[k] * score_scale : -INFINITY;
-      p[h][k] = s;
-      mh = fmaxf(mh, s);
+      sc[k] = valid[k] ? d * ks[k] * score_scale : -INFINITY;
+      mh = fmaxf(mh, sc[k]);
     }
 #pragma unroll
     for (int o = 4; o <= 32; o <<= 1) mh = fmaxf(mh, __shfl_xor(mh, o, 64));
     float lh = 0.f;
+    float a[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) a[i] = 0.f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float e = valid[k] ? __expf(p[h][k] - mh) : 0.f;
-      p[h][k] = e;
+      const float e = valid[k] ? __expf(sc[k] - mh) : 0.f;
       lh += e;
+      const float ev = e * vs[k];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) a[i] = fmaf(ev, vc[k][i], a[i]);
     }
+    // Sum over the 16 token rows (lane bits 2..5); all lanes of a quad end
+    // with the full sums of their 16 dims.
 #pragma unroll
-    for (int o = 4; o <= 32; o <<= 1) lh += __shfl_xor(lh, o, 64);
-    m[h] = mh;
-    l[h] = lh;
-  }
-
-  // acc[h*16 + i]: this lane's token rows, dims quad*16 + i.
-  constexpr int V = REP * 16;
-  float acc[V];
+    for (int o = 4; o <= 32; o <<= 1) {
+      lh += __shfl_xor(lh, o, 64);
 #pragma unroll
-  for (int h = 0; h < REP; ++h) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float a = 0.f;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) a = fmaf(p[h][k] * vs[k], vc[k][i], a);
-      acc[h * 16 + i] = a;
+      for (int i = 0; i < 16; ++i) a[i] += __shfl_xor(a[i], o, 64);
     }
-  }
-  // Transposing butterfly over the 16 token rows (lane bits 2..5).
-  uint32_t idx_base = 0;
+    if (trow == 0) {
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const int c = V >> s;
-    const int half = c >> 1;
-    const bool upper = (trow >> s) & 1u;
-#pragma unroll
-    for (int i = 0; i < half; ++i) {
-      const float send = upper ? acc[i] : acc[i + half];
-      const float keep = upper ? acc[i + half] : acc[i];
-      acc[i] = keep + __shfl_xor(send, 4 << s, 64);
-    }
-    if (upper) idx_base += half;
-  }
-  // Each lane now holds REP finished sums: indices idx_base + i.
-#pragma unroll
-  for (int i = 0; i < REP; ++i) {
-    const uint32_t idx = idx_base + i;
-    const uint32_t h = idx / 16, dim = quad * 16 + (idx % 16);
-    const uint32_t qh = kvh * REP + h;
-    // Select the per-head m and l without dynamic register indexing.
-    float mh = m[0], lh = l[0];
-#pragma unroll
-    for (int hh = 1; hh < REP; ++hh) {
-      if (h == (uint32_t)hh) {
-        mh = m[hh];
-        lh = l[hh];
+      for (int i = 0; i < 16; ++i) s_acc[wave][h * kHeadDim + quad * 16 + i] = a[i];
+      if (quad == 0) {
+        s_m[wave][h] = mh;
+        s_l[wave][h] = lh;
       }
     }
+  }
+  __syncthreads();
+
+  // Merge the waves: thread t < REP*64 owns (h, dim).
+  const uint32_t t = threadIdx.x;
+  float mine_m = -INFINITY, mine_l = 0.f, mine_a = 0.f;
+  uint32_t h_t = 0, dim_t = 0;
+  for (uint32_t o = t; o < REP * kHeadDim; o += blockDim.x) {
+    h_t = o / kHeadDim;
+    dim_t = o % kHeadDim;
+    float mx = -INFINITY;
+    for (uint32_t w = 0; w < nwaves; ++w) mx = fmaxf(mx, s_m[w][h_t]);
+    float L = 0.f, A = 0.f;
+    for (uint32_t w = 0; w < nwaves; ++w) {
+      const float f = (s_m[w][h_t] == -INFINITY) ? 0.f : __expf(s_m[w][h_t] - mx);
+      L = fmaf(f, s_l[w][h_t], L);
+      A = fmaf(f, s_acc[w][h_t * kHeadDim + dim_t], A);
+    }
+    const uint32_t qh = kvh_local * REP + h_t;
     if (nchunks == 1) {
-      out[(size_t)qh * kHeadDim + dim] = acc[i] / lh;
+      out[(size_t)qh * kHeadDim + dim_t] = A / L;
     } else {
-      float* part = partials + ((size_t)qh * nchunks + chunk) * (2 + kHeadDim);
-      part[2 + dim] = acc[i];
-      if (dim == 0) {
-        part[0] = mh;
-        part[1] = lh;
+      const size_t pi = part_base + (size_t)qh * max_chunks + chunk;
+      part_acc[pi * kHeadDim + dim_t] = A;
+      if (dim_t == 0) {
+        part_ml[pi * 2 + 0] = mx;
+        part_ml[pi * 2 + 1] = L;
       }
     }
+    mine_m = mx;
+    mine_l = L;
+    mine_a = A;
   }
-}
+  (void)mine_m; (void)mine_l; (void)mine_a;
+  if (nchunks == 1) return;
 
-// Log-sum-exp merge of the chunk partials: one wave per query head, lane = dim.
-__global__ __launch_bounds__(64) void attention_merge_kernel(const float* __restrict__ partials,
-                                                             uint32_t nchunks,
-                                                             float* __restrict__ out) {
-  const uint32_t qh = blockIdx.x, dim = threadIdx.x;
-  const float* base = partials + (size_t)qh * nchunks * (2 + kHeadDim);
-  float mx = -INFINITY;
-  for (uint32_t c = 0; c < nchunks; ++c) mx = fmaxf(mx, base[(size_t)c * (2 + kHeadDim)]);
-  float total = 0.f, acc = 0.f;
-  for (uint32_t c = 0; c < nchunks; ++c) {
-    const float* part = base + (size_t)c * (2 + kHeadDim);
-    const float w = __expf(part[0] - mx);
-    total = fmaf(w, part[1], total);
-    acc = fmaf(w, part[2 + dim], acc);
+  // Last-arriving workgroup of this kv head merges every chunk.
+  __shared__ uint32_t s_last;
+  __threadfence();
+  __syncthreads();
+  if (t == 0) s_last = (atomicAdd(&counters[kvh], 1u) == nchunks - 1) ? 1u : 0u;
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  if (t == 0) counters[kvh] = 0;  // ready for the next call on this stream
+
+  __shared__ float s_w[1024];
+  __shared__ float s_red[16][kHeadDim];
+  __shared__ float s_scalar[2];
+  for (int h = 0; h < REP; ++h) {
+    const uint32_t qh = kvh_local * REP + h;
+    const float* ml = part_ml + (part_base + (size_t)qh * max_chunks) * 2;
+    // Maximum over chunks.
+    float mx = -INFINITY;
+    for (uint32_t c = t; c < nchunks; c += blockDim.x) mx = fmaxf(mx, ml[2 * c]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if (lane == 0) s_m[wave][0] = mx;
+    __syncthreads();
+    mx = s_m[0][0];
+    for (uint32_t w = 1; w < nwaves; ++w) mx = fmaxf(mx, s_m[w][0]);
+    __syncthreads();
+    // Chunk weights and the total.
+    float L = 0.f;
+    for (uint32_t c = t; c < nchunks; c += blockDim.x) {
+      const float f = __expf(ml[2 * c] - mx);
+      s_w[c] = f;
+      L = fmaf(f, ml[2 * c + 1], L);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o, 64);
+    if (lane == 0) s_l[wave][0] = L;
+    __syncthreads();
+    if (t == 0) {
+      float tot = 0.f;
+      for (uint32_t w = 0; w < nwaves; ++w) tot += s_l[w][0];
+      s_scalar[0] = tot;
+    }
+    // Weighted sum of chunk accumulators: 16 threads per chunk row (float4 each).
+    const uint32_t dq = t & 15, cg = t >> 4, ngroups = blockDim.x >> 4;
+    float4 a4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    const float* accs = part_acc + (part_base + (size_t)qh * max_chunks) * kHeadDim;
+    for (uint32_t c = cg; c < nchunks; c += ngroups) {
+      const float4 v = reinterpret_cast<const float4*>(accs + (size_t)c * kHeadDim)[dq];
+      const float f = s_w[c];
+      a4.x = fmaf(f, v.x, a4.x);
+      a4.y = fmaf(f, v.y, a4.y);
+      a4.z = fmaf(f, v.z, a4.z);
+      a4.w = fmaf(f, v.w, a4.w);
+    }
+    s_red[cg][dq * 4 + 0] = a4.x;
+    s_red[cg][dq * 4 + 1] = a4.y;
+    s_red[cg][dq * 4 + 2] = a4.z;
+    s_red[cg][dq * 4 + 3] = a4.w;
+    __syncthreads();
+    if (t < kHeadDim) {
+      float sum = 0.f;
+      for (uint32_t g2 = 0; g2 < ngroups; ++g2) sum += s_red[g2][t];
+      out[(size_t)qh * kHeadDim + t] = sum / s_scalar[0];
+    }
+    __syncthreads();
   }
-  out[(size_t)qh * kHeadDim + dim] = acc / total;
 }
 
 }  // namespace
@@ -266,10 +355,24 @@ nd_visible nd_kv_visible(const nd_kv* kv, uint32_t position) {
   return v;
 }
 
-uint32_t nd_attention_chunks(uint32_t count) { return (count + kChunk - 1) / kChunk; }
+// Waves per workgroup: enough workgroups to cover the GPU first, then up to
+// four waves (256 positions) per workgroup to keep the merge short.
+static uint32_t attention_waves(uint32_t count, uint32_t kv_heads) {
+  const uint32_t wave_units = (count + kChunk - 1) / kChunk;
+  uint32_t w = 1;
+  while (w < kMaxWaves && wave_units * kv_heads >= 2u * w * 256u) w <<= 1;
+  return w;
+}
 
-size_t nd_attention_partial_floats(uint32_t q_heads, uint32_t count) {
-  return (size_t)q_heads * nd_attention_chunks(count) * (2 + kHeadDim);
+uint32_t nd_attention_chunks(uint32_t count, uint32_t kv_heads) {
+  const uint32_t per = kChunk * attention_waves(count, kv_heads);
+  return (count + per - 1) / per;
+}
+
+// Upper bound for any visible count <= count (one wave per chunk at worst).
+size_t nd_attention_partial_floats(uint32_t q_heads, uint32_t kv_heads, uint32_t count) {
+  (void)kv_heads;
+  return (size_t)q_heads * ((count + kChunk - 1) / kChunk) * (kHeadDim + 2);
 }
 
 hipError_t nd_launch_kv_store(const nd_kv* kv, uint32_t layer, uint32_t position, uint32_t first,
@@ -286,23 +389,41 @@ hipError_t nd_launch_kv_store(const nd_kv* kv, uint32_t layer, uint32_t position
   return hipGetLastError();
 }
 
+struct AttnLaunch {
+  const nd_kv* kv;
+  uint32_t layer;
+  const float* q;
+  float* out;
+  float* partials;
+  uint32_t* counters;
+  Visible vis;                 // used when positions == nullptr
+  const uint32_t* positions;   // per-sequence query positions, or nullptr
+  uint32_t seq_kv_heads;       // KV heads of one sequence
+  uint32_t rep;                // query heads per KV head
+  uint32_t batch;
+  uint32_t max_chunks;
+  uint32_t waves;
+};
+
 template <int REP, bool F32>
-static void launch_chunks(const nd_kv* kv, uint32_t layer, const float* q, float* out,
-                          float* partials, const Visible& vis, uint32_t nchunks, hipStream_t s) {
-  hipLaunchKernelGGL((attention_chunk_kernel<REP, F32>), dim3(nchunks, kv->kv_heads), dim3(64), 0,
-                     s, kv->k, kv->v, kv->ks, kv->vs, q, out, partials, layer, kv->kv_heads,
-                     kv->alloc, kv->sink, kv->window, vis, nchunks, 0.125f);
+static void launch_attention(const AttnLaunch& a, hipStream_t s) {
+  const size_t q_rows = (size_t)a.batch * a.seq_kv_heads * REP;
+  float* part_acc = a.partials;
+  float* part_ml = a.partials + q_rows * a.max_chunks * kHeadDim;
+  hipLaunchKernelGGL((attention_kernel<REP, F32>), dim3(a.max_chunks, a.seq_kv_heads, a.batch),
+                     dim3(64 * a.waves), 0, s, a.kv->k, a.kv->v, a.kv->ks, a.kv->vs, a.q, a.out,
+                     part_acc, part_ml, a.counters, a.layer, a.kv->kv_heads, a.kv->alloc,
+                     a.kv->sink, a.kv->window, a.vis, a.positions, a.seq_kv_heads, a.max_chunks,
+                     0.125f);
 }
 
 template <bool F32>
-static hipError_t launch_rep(uint32_t rep, const nd_kv* kv, uint32_t layer, const float* q,
-                             float* out, float* partials, const Visible& vis, uint32_t nchunks,
-                             hipStream_t s) {
-  switch (rep) {
-    case 1: launch_chunks<1, F32>(kv, layer, q, out, partials, vis, nchunks, s); break;
-    case 2: launch_chunks<2, F32>(kv, layer, q, out, partials, vis, nchunks, s); break;
-    case 4: launch_chunks<4, F32>(kv, layer, q, out, partials, vis, nchunks, s); break;
-    case 8: launch_chunks<8, F32>(kv, layer, q, out, partials, vis, nchunks, s); break;
+static hipError_t launch_rep(const AttnLaunch& a, hipStream_t s) {
+  switch (a.rep) {
+    case 1: launch_attention<1, F32>(a, s); break;
+    case 2: launch_attention<2, F32>(a, s); break;
+    case 4: launch_attention<4, F32>(a, s); break;
+    case 8: launch_attention<8, F32>(a, s); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -310,15 +431,52 @@ static hipError_t launch_rep(uint32_t rep, const nd_kv* kv, uint32_t layer, cons
 
 hipError_t nd_launch_attention(const nd_kv* kv, uint32_t layer, uint32_t position,
                                const float* q, uint32_t q_heads, float* out, float* partials,
-                               hipStream_t s) {
+                               uint32_t* counters, hipStream_t s) {
   const nd_visible nv = nd_kv_visible(kv, position);
-  const Visible vis{nv.prefix, nv.recent_low, nv.count};
-  const uint32_t nchunks = nd_attention_chunks(nv.count);
-  const uint32_t rep = q_heads / kv->kv_heads;
-  hipError_t e = kv->mode == ND_KV_FLOAT32
-                     ? launch_rep<true>(rep, kv, layer, q, out, partials, vis, nchunks, s)
-                     : launch_rep<false>(rep, kv, layer, q, out, partials, vis, nchunks, s);
-  if (e != hipSuccess || nchunks == 1) return e;
-  hipLaunchKernelGGL(attention_merge_kernel, dim3(q_heads), dim3(64), 0, s, partials, nchunks, out);
-  return hipGetLastError();
+  AttnLaunch a{};
+  a.kv = kv;
+  a.layer = layer;
+  a.q = q;
+  a.out = out;
+  a.partials = partials;
+  a.counters = counters;
+  a.vis = Visible{nv.prefix, nv.recent_low, nv.count};
+  a.positions = nullptr;
+  a.seq_kv_heads = kv->kv_heads;
+  a.rep = q_heads / kv->kv_heads;
+  a.batch = 1;
+  a.waves = attention_waves(nv.count, kv->kv_heads);
+  a.max_chunks = (nv.count + kChunk * a.waves - 1) / (kChunk * a.waves);
+  return kv->mode == ND_KV_FLOAT32 ? launch_rep<true>(a, s) : launch_rep<false>(a, s);
+}
+
+// Batched form: sequence z owns cache heads [z * seq_kv_heads, +seq_kv_heads)
+// and queries q[z][seq_kv_heads * rep][64]; its query position is
+// positions[z] (device memory), at most max_position.
+hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint32_t* positions,
+                                     uint32_t batch, uint32_t seq_kv_heads, uint32_t rep,
+                                     uint32_t max_position, const float* q, float* out,
+                                     float* partials, uint32_t* counters, hipStream_t s) {
+  const nd_visible nv = nd_kv_visible(kv, max_position);
+  AttnLaunch a{};
+  a.kv = kv;
+  a.layer = layer;
+  a.q = q;
+  a.out = out;
+  a.partials = partials;
+  a.counters = counters;
+  a.vis = Visible{nv.prefix, nv.recent_low, nv.count};
+  a.positions = positions;
+  a.seq_kv_heads = seq_kv_heads;
+  a.rep = rep;
+  a.batch = batch;
+  a.waves = attention_waves(nv.count, seq_kv_heads * batch);
+  a.max_chunks = (nv.count + kChunk * a.waves - 1) / (kChunk * a.waves);
+  return kv->mode == ND_KV_FLOAT32 ? launch_rep<true>(a, s) : launch_rep<false>(a, s);
+}
+
+size_t nd_attention_batch_partial_floats(uint32_t batch, uint32_t seq_kv_heads, uint32_t rep,
+                                         uint32_t max_count) {
+  const uint32_t chunks = (max_count + kChunk - 1) / kChunk;  // bound for every launch
+  return (size_t)batch * seq_kv_heads * rep * chunks * (kHeadDim + 2);
 }

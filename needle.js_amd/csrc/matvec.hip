@@ -11,8 +11,7 @@
 // are streamed with non-temporal 128-bit loads.  Bytes are decoded with the
 // unsigned-byte converts: u = b + 128 (byte ^ 0x80), dot = sum u*x - 128*sum x.
 // Partial sums (RACC rows x B batch values per thread) are reduced across the
-// row's lanes with a transposing butterfly (each step halves the values a
-// lane carries), then across waves through LDS when a row spans >64 lanes.
+// row's threads through LDS followed by a short shuffle butterfly.
 #include "nd_internal.hpp"
 
 namespace {
@@ -24,7 +23,7 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
   return __shfl_xor(v, mask, 64);
 }
 
-template <int B, int SPT, int TPRW, int RACC>
+template <int B, int SPT, int RACC>
 __global__ __launch_bounds__(kThreads) void matvec_i8_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ S, const float* __restrict__ X,
     float* __restrict__ Y, uint32_t K, uint32_t groups, uint32_t g16, uint32_t row_start,
@@ -37,8 +36,27 @@ __global__ __launch_bounds__(kThreads) void matvec_i8_kernel(
   const uint32_t lk = t & (tpr - 1);
   const uint32_t row0 = blockIdx.x * rpp * RACC;
 
-  // Issue the weight and scale loads first so that they are in flight while
-  // x is fetched and summed.
+  // x first: its loads hit L2 and, since loads complete in issue order, the
+  // x sums then overlap the weight loads instead of waiting behind them.
+  float xr[B][SPT][16];
+  float xs[B][SPT];
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+#pragma unroll
+    for (int j = 0; j < SPT; ++j) {
+      const float4* xp = reinterpret_cast<const float4*>(X + (size_t)b * x_stride) + (lk + j * tpr) * 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float4 f = xp[q];
+        xr[b][j][4 * q + 0] = f.x;
+        xr[b][j][4 * q + 1] = f.y;
+        xr[b][j][4 * q + 2] = f.z;
+        xr[b][j][4 * q + 3] = f.w;
+      }
+    }
+  }
+
+  // Then, per row, the scale and the 16-byte weight segments.
   u32x4 wv[RACC][SPT];
   float sv[RACC][SPT];
   uint32_t grp[SPT];
@@ -51,28 +69,19 @@ __global__ __launch_bounds__(kThreads) void matvec_i8_kernel(
     const u32x4* wrow = reinterpret_cast<const u32x4*>(W + (size_t)r * K);
 #pragma unroll
     for (int j = 0; j < SPT; ++j) {
-      wv[p][j] = __builtin_nontemporal_load(wrow + lk + j * tpr);
       sv[p][j] = S[(size_t)r * groups + grp[j]];
+      wv[p][j] = __builtin_nontemporal_load(wrow + lk + j * tpr);
     }
   }
 
-  float xr[B][SPT][16];
-  float xs[B][SPT];
 #pragma unroll
   for (int b = 0; b < B; ++b) {
 #pragma unroll
     for (int j = 0; j < SPT; ++j) {
-      const float4* xp = reinterpret_cast<const float4*>(X + (size_t)b * x_stride) + (lk + j * tpr) * 4;
       float sum = 0.f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float4 f = xp[q];
-        xr[b][j][4 * q + 0] = f.x;
-        xr[b][j][4 * q + 1] = f.y;
-        xr[b][j][4 * q + 2] = f.z;
-        xr[b][j][4 * q + 3] = f.w;
-        sum += (f.x + f.y) + (f.z + f.w);
-      }
+      for (int q = 0; q < 4; ++q)
+        sum += (xr[b][j][4 * q] + xr[b][j][4 * q + 1]) + (xr[b][j][4 * q + 2] + xr[b][j][4 * q + 3]);
       xs[b][j] = sum;
     }
   }
@@ -104,59 +113,26 @@ __global__ __launch_bounds__(kThreads) void matvec_i8_kernel(
     }
   }
 
-  // Transposing butterfly over the TPRW lanes that share a row.
-  const uint32_t lane = t & 63;
-  constexpr int L = (TPRW == 64) ? 6 : (TPRW == 32) ? 5 : (TPRW == 16) ? 4 : 3;
-  uint32_t idx_base = 0;
-  uint32_t dup_mask = 0;
+  // Reduce each row's partial sums over its tpr threads through LDS.  red is
+  // [V][256]: thread t stores its V partials in column t.  Output o = (sub,
+  // v) is summed by T = 256 / (rpp * V) threads (a power of two <= 64 that
+  // divides 64), each over tpr / T columns, then by a T-lane butterfly.
+  __shared__ float red[V * kThreads];
 #pragma unroll
-  for (int s = 0; s < L; ++s) {
-    const int c = V >> s;
-    const bool upper = (lane >> s) & 1u;
-    if (c >= 2) {
-      const int half = c >> 1;
-#pragma unroll
-      for (int i = 0; i < half; ++i) {
-        const float send = upper ? acc[i] : acc[i + half];
-        const float keep = upper ? acc[i + half] : acc[i];
-        acc[i] = keep + shfl_xor_f(send, 1 << s);
-      }
-      if (upper) idx_base += half;
-    } else {
-      acc[0] += shfl_xor_f(acc[0], 1 << s);
-      dup_mask |= 1u << s;
-    }
-  }
-  constexpr int CF = (V >> L) > 0 ? (V >> L) : 1;
-  const bool writer = (lane & dup_mask) == 0;
-
-  if (tpr <= 64) {
-    if (writer) {
-#pragma unroll
-      for (int i = 0; i < CF; ++i) {
-        const uint32_t idx = idx_base + i;
-        const uint32_t p = idx / B, b = idx % B;
-        const uint32_t row = row0 + p * rpp + sub;
-        if (row < row_count) Y[(size_t)b * y_stride + row] = acc[i];
-      }
-    }
-  } else {
-    __shared__ float red[kThreads / 64][V];
-    const uint32_t wave = t >> 6;
-    if (writer) {
-#pragma unroll
-      for (int i = 0; i < CF; ++i) red[wave][idx_base + i] = acc[i];
-    }
-    __syncthreads();
-    const uint32_t wpr = tpr >> 6;  // waves per row
-    if (t < rpp * V) {
-      const uint32_t sub2 = t / V, idx = t % V;
-      float sum = 0.f;
-      for (uint32_t w = 0; w < wpr; ++w) sum += red[sub2 * wpr + w][idx];
-      const uint32_t p = idx / B, b = idx % B;
-      const uint32_t row = row0 + p * rpp + sub2;
-      if (row < row_count) Y[(size_t)b * y_stride + row] = sum;
-    }
+  for (int i = 0; i < V; ++i) red[i * kThreads + t] = acc[i];
+  __syncthreads();
+  const uint32_t outputs = rpp * V;
+  const uint32_t T = kThreads / outputs;
+  const uint32_t o = t / T, part = t % T;
+  const uint32_t osub = o / V, ov = o % V;
+  const float* col = red + ov * kThreads + osub * tpr;
+  float sum = 0.f;
+  for (uint32_t c = part; c < tpr; c += T) sum += col[c];
+  for (uint32_t m = T >> 1; m >= 1; m >>= 1) sum += shfl_xor_f(sum, m);
+  if (part == 0) {
+    const uint32_t p = ov / B, b = ov % B;
+    const uint32_t row = row0 + p * rpp + osub;
+    if (row < row_count) Y[(size_t)b * y_stride + row] = sum;
   }
 }
 
@@ -170,36 +146,21 @@ __global__ void row_kernel(const int8_t* __restrict__ W, const float* __restrict
 using MatvecFn = void (*)(const int8_t*, const float*, const float*, float*, uint32_t, uint32_t,
                           uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t);
 
-template <int B, int SPT, int TPRW, int RACC>
-constexpr MatvecFn fn() {
-  return &matvec_i8_kernel<B, SPT, TPRW, RACC>;
-}
-
-template <int B, int SPT, int RACC>
-MatvecFn pick_tprw(uint32_t tprw) {
-  switch (tprw) {
-    case 8: return fn<B, SPT, 8, RACC>();
-    case 16: return fn<B, SPT, 16, RACC>();
-    case 32: return fn<B, SPT, 32, RACC>();
-    default: return fn<B, SPT, 64, RACC>();
-  }
-}
-
 template <int B, int RACC>
-MatvecFn pick_spt(uint32_t spt, uint32_t tprw) {
+MatvecFn pick_spt(uint32_t spt) {
   if constexpr (B <= 4) {
-    if (spt == 2) return pick_tprw<B, 2, RACC>(tprw);
+    if (spt == 2) return &matvec_i8_kernel<B, 2, RACC>;
   }
-  return pick_tprw<B, 1, RACC>(tprw);
+  return &matvec_i8_kernel<B, 1, RACC>;
 }
 
 template <int RACC>
-MatvecFn pick_b(uint32_t b, uint32_t spt, uint32_t tprw) {
+MatvecFn pick_b(uint32_t b, uint32_t spt) {
   switch (b) {
-    case 1: return pick_spt<1, RACC>(spt, tprw);
-    case 2: return pick_spt<2, RACC>(spt, tprw);
-    case 4: return pick_spt<4, RACC>(spt, tprw);
-    default: return pick_spt<8, RACC>(spt, tprw);
+    case 1: return pick_spt<1, RACC>(spt);
+    case 2: return pick_spt<2, RACC>(spt);
+    case 4: return pick_spt<4, RACC>(spt);
+    default: return pick_spt<8, RACC>(spt);
   }
 }
 
@@ -216,18 +177,22 @@ hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uin
   const uint32_t tpr = segs / spt;
   uint32_t tpr_log2 = 0;
   while ((1u << tpr_log2) < tpr) ++tpr_log2;
-  const uint32_t tprw = tpr < 64 ? tpr : 64;
   const uint32_t rpp = kThreads / tpr;
-  const uint32_t racc = (row_count / rpp >= 1024) ? 4 : 1;
   const uint32_t bmax = 8 / spt;
   const uint32_t groups = m->k / m->g;
   const uint32_t g16 = m->g / 16;
-  const uint32_t blocks = (row_count + rpp * racc - 1) / (rpp * racc);
   uint32_t b0 = 0;
   while (b0 < batch) {
     uint32_t left = batch - b0, bc = 1;
     while (bc * 2 <= left && bc * 2 <= bmax) bc *= 2;
-    MatvecFn f = racc == 4 ? pick_b<4>(bc, spt, tprw) : pick_b<1>(bc, spt, tprw);
+    // Rows per pass x batch x passes must give 4..256 outputs per workgroup
+    // (the LDS reduction needs T = 256 / outputs <= 64).  8 passes amortize
+    // the per-workgroup x loads when there are enough rows.
+    uint32_t racc = (bc <= 2 && row_count >= 8 * rpp * 256) ? 8 : 4;
+    while (racc > 1 && rpp * racc * bc > kThreads) racc >>= 1;
+    const uint32_t blocks = (row_count + rpp * racc - 1) / (rpp * racc);
+    MatvecFn f = racc == 8 ? pick_b<8>(bc, spt) : racc == 4 ? pick_b<4>(bc, spt)
+               : racc == 2 ? pick_b<2>(bc, spt) : pick_b<1>(bc, spt);
     hipLaunchKernelGGL(f, dim3(blocks), dim3(kThreads), 0, s, m->w, m->scales,
                        x + (size_t)b0 * x_stride, y + (size_t)b0 * y_stride, m->k, groups, g16,
                        row_start, row_count, tpr_log2, x_stride, y_stride);

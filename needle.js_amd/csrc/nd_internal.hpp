@@ -32,9 +32,15 @@ struct nd_ctx {
   // Device staging for the host-pointer entry points (grown on demand).
   void* stage = nullptr;
   size_t stage_bytes = 0;
-  // Split-context attention partials: [q_heads][chunks][2 + head_dim] f32.
+  // Split-context attention partials: acc [q_heads][chunks][head_dim] then
+  // (max, sum) [q_heads][chunks][2], f32; and one arrival counter per KV head
+  // (zeroed at allocation, reset by the kernel that consumes it).
   float* attn_partials = nullptr;
   size_t attn_partial_floats = 0;
+  uint32_t* attn_counters = nullptr;
+  // Digit planes and row factors of nd_matmul_d (grown on demand).
+  void* mm_scratch = nullptr;
+  size_t mm_scratch_bytes = 0;
   std::set<nd_mat*> mats;
   std::set<nd_kv*> kvs;
 };
@@ -66,16 +72,33 @@ struct nd_visible {
   uint32_t count;       // prefix + position - recent_low + 1
 };
 nd_visible nd_kv_visible(const nd_kv* kv, uint32_t position);
-uint32_t nd_attention_chunks(uint32_t count);
-size_t nd_attention_partial_floats(uint32_t q_heads, uint32_t count);
+uint32_t nd_attention_chunks(uint32_t count, uint32_t kv_heads);
+size_t nd_attention_partial_floats(uint32_t q_heads, uint32_t kv_heads, uint32_t count);
+constexpr uint32_t kMaxAttentionKvHeads = 1024;
+constexpr uint32_t kMaxAttentionPositions = 262144;
 
 hipError_t nd_launch_kv_store(const nd_kv* kv, uint32_t layer, uint32_t position, uint32_t first,
                               uint32_t count, const float* k, const float* v, hipStream_t s);
 hipError_t nd_launch_attention(const nd_kv* kv, uint32_t layer, uint32_t position,
                                const float* q, uint32_t q_heads, float* out, float* partials,
-                               hipStream_t s);
+                               uint32_t* counters, hipStream_t s);
 hipError_t nd_launch_select_list(const float* logits, uint32_t vocab, const uint32_t* allowed,
                                  uint32_t count, uint32_t* id, double* logprob, hipStream_t s);
 hipError_t nd_launch_select_mask(const float* logits, uint32_t batch, uint32_t vocab,
                                  const uint32_t* mask, uint32_t* ids, double* logprobs,
                                  hipStream_t s);
+
+// Digit-sliced int8 MFMA GEMM (gemm.hip): y[m][n] (op)= s_w[n] * A[m] . W[n]
+// with A given as digits [3][M][K] and per-row factors fm (digitize first).
+// epilogue: 0 store, 1 add into y, 2 store silu.  K % 64 == 0, K <= 2048 for
+// digitize.
+hipError_t nd_launch_digitize(const float* x, uint32_t ldx, const float* norm, float* norm_out,
+                              int8_t* digits, float* fm, uint32_t M, uint32_t K, hipStream_t s);
+hipError_t nd_launch_gemm(const nd_mat* w, const int8_t* digits, const float* fm, float* y,
+                          uint32_t ldy, uint32_t M, int epilogue, hipStream_t s);
+hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint32_t* positions,
+                                     uint32_t batch, uint32_t seq_kv_heads, uint32_t rep,
+                                     uint32_t max_position, const float* q, float* out,
+                                     float* partials, uint32_t* counters, hipStream_t s);
+size_t nd_attention_batch_partial_floats(uint32_t batch, uint32_t seq_kv_heads, uint32_t rep,
+                                         uint32_t max_count);

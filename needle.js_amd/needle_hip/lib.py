@@ -76,7 +76,31 @@ SIGNATURES = {
     "nd_attention_d": (I32, [P, P, U32, U32, P, U32, P, P]),
     "nd_select": (I32, [P, P, U32, P, U32, PU32, C.POINTER(C.c_double)]),
     "nd_select_mask_d": (I32, [P, P, U32, U32, P, P, P, P]),
+    "nd_matmul": (I32, [P, P, P, U32, P]),
+    "nd_matmul_d": (I32, [P, P, P, U32, P, U32, P]),
+    "nd_decoder_create": (I32, [P, P, PP]),
+    "nd_decoder_free": (I32, [P, P]),
+    "nd_batch_create": (I32, [P, P, U32, U32, PP]),
+    "nd_batch_free": (I32, [P, P]),
+    "nd_batch_kv": (P, [P]),
+    "nd_batch_fill_synthetic": (I32, [P, P, U32, C.c_uint64, C.c_uint64, U32, U32, C.c_float,
+                                      C.c_float]),
+    "nd_batch_set_state": (I32, [P, P, P, P, U32]),
+    "nd_batch_step": (I32, [P, P, U32, U32, C.c_uint64, U32, P]),
+    "nd_batch_read": (I32, [P, P, P, P, P, P]),
 }
+
+
+class DecoderDesc(C.Structure):
+    """nd_decoder_desc of include/needle_hip.h."""
+
+    _fields_ = [
+        ("layers", U32), ("dim", U32), ("heads", U32), ("kv_heads", U32), ("head_dim", U32),
+        ("ffn", U32), ("vocab", U32), ("rope_theta", C.c_float),
+        ("embedding", P),
+        ("wq", PP), ("wk", PP), ("wv", PP), ("wo", PP), ("wup", PP), ("wdown", PP),
+        ("attn_norm", P), ("ffn_norm", P), ("q_norm", P), ("k_norm", P), ("final_norm", P),
+    ]
 
 _LIB: C.CDLL | None = None
 

@@ -244,3 +244,121 @@ class KvCache:
         out = np.empty_like(q)
         _ok(lib().or_attention(self.h, layer, position, _p(q), q.size // self.head_dim, _p(out)))
         return out
+
+
+# ------------------------------------------------------ synthetic decoder
+
+_SIG_MODEL = {
+    "or_splitmix64_at": (C.c_uint64, [C.c_uint64, C.c_uint64]),
+    "or_gen_mask": (None, [C.c_uint64, U32, U32, P]),
+    "or_gen_kv_row": (None, [C.c_uint64, C.c_uint64, U32, C.c_float, C.c_float, P, P]),
+    "or_kv_fill_synthetic": (None, [P, C.c_uint64, C.c_uint64, U32, C.c_float, C.c_float]),
+    "or_synth_step": (C.c_int, [P, P, U32, U32, P, P]),
+    "or_synth_decode_batch": (C.c_int, [P, P, P, P, U32, U32, C.c_uint64, U32, P, P, U32]),
+}
+
+
+def _model_lib():
+    h = lib()
+    if not getattr(h, "_model_bound", False):
+        for name, (res, args) in _SIG_MODEL.items():
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        h._model_bound = True
+    return h
+
+
+class _OrMat(C.Structure):
+    _fields_ = [("w", P), ("s", P), ("n", U32), ("k", U32)]
+
+
+class _OrSynth(C.Structure):
+    _fields_ = [("layers", U32), ("dim", U32), ("heads", U32), ("kv_heads", U32),
+                ("head_dim", U32), ("ffn", U32), ("vocab", U32), ("rope_theta", D),
+                ("embedding", _OrMat), ("wq", C.POINTER(_OrMat)), ("wk", C.POINTER(_OrMat)),
+                ("wv", C.POINTER(_OrMat)), ("wo", C.POINTER(_OrMat)), ("wup", C.POINTER(_OrMat)),
+                ("wdown", C.POINTER(_OrMat)), ("attn_norm", P), ("ffn_norm", P), ("q_norm", P),
+                ("k_norm", P), ("final_norm", P)]
+
+
+def splitmix64_at(seed: int, index: int) -> int:
+    return int(_model_lib().or_splitmix64_at(seed, index))
+
+
+def gen_mask(seed: int, vocab: int, threshold24: int):
+    mask = np.zeros((vocab + 31) // 32, dtype=np.uint32)
+    _model_lib().or_gen_mask(seed, vocab, threshold24, _p(mask))
+    return mask
+
+
+def gen_kv_row(seed: int, index: int, n: int, lo: float, hi: float):
+    codes = np.empty(n, np.int8)
+    scale = np.empty(1, np.float32)
+    _model_lib().or_gen_kv_row(seed, index, n, lo, hi, _p(codes), _p(scale))
+    return codes, float(scale[0])
+
+
+def kv_fill_synthetic(cache: "KvCache", seed_k: int, seed_v: int, length: int, lo: float,
+                      hi: float) -> None:
+    _model_lib().or_kv_fill_synthetic(cache.h, seed_k, seed_v, length, lo, hi)
+
+
+class SynthDecoder:
+    """The oracle's synthetic decoder over a DecoderWeights-like object."""
+
+    def __init__(self, weights):
+        g = weights.geometry
+        self.geometry = g
+        self._keep = []
+
+        def om(m):
+            c = np.ascontiguousarray(m.codes, np.int8)
+            s = np.ascontiguousarray(m.scales, np.float32)
+            self._keep += [c, s]
+            return _OrMat(_p(c), _p(s), c.shape[0], c.shape[1])
+
+        def arr(ms):
+            a = (_OrMat * len(ms))(*[om(m) for m in ms])
+            self._keep.append(a)
+            return a
+
+        def vec(v):
+            v = np.ascontiguousarray(v, np.float32)
+            self._keep.append(v)
+            return _p(v)
+
+        st = _OrSynth()
+        st.layers, st.dim, st.heads, st.kv_heads = g.layers, g.dim, g.heads, g.kv_heads
+        st.head_dim, st.ffn, st.vocab, st.rope_theta = g.head_dim, g.ffn, g.vocab, float(np.float32(g.rope_theta))
+        st.embedding = om(weights.embedding)
+        for name in ("wq", "wk", "wv", "wo", "wup", "wdown"):
+            setattr(st, name, C.cast(arr(getattr(weights, name)), C.POINTER(_OrMat)))
+        for name in ("attn_norm", "ffn_norm", "q_norm", "k_norm", "final_norm"):
+            setattr(st, name, vec(getattr(weights, name)))
+        self.struct = st
+        _model_lib()
+
+    def new_cache(self, max_length: int) -> KvCache:
+        g = self.geometry
+        return KvCache(g.layers, g.kv_heads, max_length)
+
+    def step(self, cache: KvCache, token: int, position: int, want_hidden: bool = False):
+        logits = np.empty(self.geometry.vocab, np.float32)
+        hidden = np.empty(self.geometry.dim, np.float32) if want_hidden else None
+        _ok(_model_lib().or_synth_step(C.byref(self.struct), cache.h, token, position, _p(logits),
+                                       _p(hidden) if want_hidden else None))
+        return (logits, hidden) if want_hidden else logits
+
+    def decode_batch(self, caches, tokens, start, steps: int, mask_seed: int, threshold24: int,
+                     threads: int = 1):
+        b = len(caches)
+        ptrs = (P * b)(*[c.h for c in caches])
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        start = np.ascontiguousarray(start, np.uint32)
+        ids = np.empty((steps, b), np.uint32)
+        lps = np.empty((steps, b), np.float64)
+        _ok(_model_lib().or_synth_decode_batch(C.byref(self.struct), ptrs, _p(tokens), _p(start),
+                                               b, steps, mask_seed, threshold24, _p(ids), _p(lps),
+                                               threads))
+        return ids, lps

@@ -36,6 +36,7 @@
  *                       prefill == repeated step and batch == single.
  */
 #include <math.h>
+#include <pthread.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -480,4 +481,214 @@ int or_attention(const or_kv* kv, uint32_t layer, uint32_t position, const float
   free(logical);
   free(scores);
   return OR_OK;
+}
+
+/* ------------------------------------------ seeded generators (integers) */
+
+/* splitmix64 output i (0-based) of the stream with 64-bit seed `seed`:
+ * mix(seed + (i + 1) * golden).  Shared spec with the synthetic-data module
+ * and the GPU generators; pure integer arithmetic, so bit-exact everywhere. */
+static uint64_t sm64_mix(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+uint64_t or_splitmix64_at(uint64_t seed, uint64_t i) {
+  return sm64_mix(seed + (i + 1) * 0x9E3779B97F4A7C15ull);
+}
+
+/* Allowed-token bitmask row: id v allowed iff (z_v >> 40) < threshold24,
+ * plus the forced id (z_vocab >> 32) * vocab >> 32. */
+void or_gen_mask(uint64_t seed, uint32_t vocab, uint32_t threshold24, uint32_t* mask) {
+  uint32_t words = (vocab + 31) / 32;
+  memset(mask, 0, sizeof(uint32_t) * words);
+  for (uint32_t v = 0; v < vocab; v++)
+    if ((uint32_t)(or_splitmix64_at(seed, v) >> 40) < threshold24) mask[v >> 5] |= 1u << (v & 31);
+  uint32_t forced = (uint32_t)(((or_splitmix64_at(seed, vocab) >> 32) * (uint64_t)vocab) >> 32);
+  mask[forced >> 5] |= 1u << (forced & 31);
+}
+
+/* Synthetic int8 KV row: code_i = ((z_i >> 32) * 255 >> 32) - 127 and scale
+ * = lo + (hi - lo) * (z_n >> 40) * 2^-24 (float64 then f32). */
+void or_gen_kv_row(uint64_t seed, uint64_t index, uint32_t n, float lo, float hi, int8_t* codes,
+                   float* scale) {
+  uint64_t base = index * (uint64_t)(n + 1);
+  for (uint32_t i = 0; i < n; i++) {
+    uint64_t z = or_splitmix64_at(seed, base + i);
+    codes[i] = (int8_t)((int)(((z >> 32) * 255ull) >> 32) - 127);
+  }
+  uint64_t z = or_splitmix64_at(seed, base + n);
+  double u = (double)(z >> 40) * (1.0 / 16777216.0);
+  *scale = (float)((double)lo + ((double)hi - (double)lo) * u);
+}
+
+/* ------------------------------------------ synthetic decoder (configs) */
+
+/* BASELINE-defined decoder composed from the reference primitives: per layer
+ *   a = rmsNorm(x, attn_norm)                      math.ts:16-32
+ *   q, k, v = Wq a, Wk a, Wv a                     cq.ts:106-156 (int8 form)
+ *   per-head rmsNormSlice(q, q_norm), (k, k_norm)  runtime.ts:471-486, 647-657
+ *   RoPE(q), RoPE(k) at the position               math.ts:94-115
+ *   #storeKV, #attention                            runtime.ts:679-786
+ *   x = x + Wo o
+ *   f = rmsNorm(x, ffn_norm); x = x + Wdown silu(Wup f)   math.ts:12-14
+ * embedding row x sqrt(d) in, tied embedding^T out (runtime.ts:305-309,
+ * 570-577).  Matrices are int8 with one f32 scale per row. */
+typedef struct {
+  const int8_t* w;
+  const float* s;
+  uint32_t n, k;
+} or_mat;
+
+typedef struct {
+  uint32_t layers, dim, heads, kv_heads, head_dim, ffn, vocab;
+  double rope_theta;
+  or_mat embedding;
+  const or_mat* wq;
+  const or_mat* wk;
+  const or_mat* wv;
+  const or_mat* wo;
+  const or_mat* wup;
+  const or_mat* wdown;
+  const float* attn_norm; /* [layers][dim] */
+  const float* ffn_norm;  /* [layers][dim] */
+  const float* q_norm;    /* [layers][head_dim] */
+  const float* k_norm;    /* [layers][head_dim] */
+  const float* final_norm;
+} or_synth;
+
+static void synth_matvec(const or_mat* m, const float* x, float* y) {
+  or_matvec_i8(m->w, m->s, m->n, m->k, m->k, x, 1, 0, m->n, y);
+}
+
+/* One decode step of one sequence at `position`; logits may be NULL. */
+int or_synth_step(const or_synth* md, or_kv* kv, uint32_t token, uint32_t position,
+                  float* logits, float* hidden_out) {
+  uint32_t d = md->dim, hd = md->head_dim;
+  uint32_t qw = md->heads * hd, kw = md->kv_heads * hd;
+  if (token >= md->vocab || position >= kv->max_length) return OR_INVALID;
+  float* x = (float*)malloc(sizeof(float) * d);
+  float* a = (float*)malloc(sizeof(float) * d);
+  float* q = (float*)malloc(sizeof(float) * qw);
+  float* k = (float*)malloc(sizeof(float) * kw);
+  float* v = (float*)malloc(sizeof(float) * kw);
+  float* o = (float*)malloc(sizeof(float) * qw);
+  float* p = (float*)malloc(sizeof(float) * d);
+  float* h = (float*)malloc(sizeof(float) * md->ffn);
+  or_row_i8(md->embedding.w, md->embedding.s, md->embedding.n, md->embedding.k,
+            md->embedding.k, token, x);
+  double es = sqrt((double)d);
+  for (uint32_t i = 0; i < d; i++) x[i] = (float)((double)x[i] * es);
+  for (uint32_t l = 0; l < md->layers; l++) {
+    or_rms_norm(x, md->attn_norm + (size_t)l * d, d, a);
+    synth_matvec(&md->wq[l], a, q);
+    synth_matvec(&md->wk[l], a, k);
+    synth_matvec(&md->wv[l], a, v);
+    for (uint32_t hh = 0; hh < md->heads; hh++)
+      or_rms_norm_slice(q, hh * hd, hd, md->q_norm + (size_t)l * hd);
+    for (uint32_t hh = 0; hh < md->kv_heads; hh++)
+      or_rms_norm_slice(k, hh * hd, hd, md->k_norm + (size_t)l * hd);
+    or_rope(q, md->heads, hd, position, md->rope_theta);
+    or_rope(k, md->kv_heads, hd, position, md->rope_theta);
+    or_kv_store(kv, l, position, k, v);
+    or_attention(kv, l, position, q, md->heads, o);
+    synth_matvec(&md->wo[l], o, p);
+    for (uint32_t i = 0; i < d; i++) x[i] = (float)((double)x[i] + (double)p[i]);
+    or_rms_norm(x, md->ffn_norm + (size_t)l * d, d, a);
+    synth_matvec(&md->wup[l], a, h);
+    for (uint32_t i = 0; i < md->ffn; i++) h[i] = (float)or_silu((double)h[i]);
+    synth_matvec(&md->wdown[l], h, p);
+    for (uint32_t i = 0; i < d; i++) x[i] = (float)((double)x[i] + (double)p[i]);
+  }
+  if (hidden_out) memcpy(hidden_out, x, sizeof(float) * d);
+  if (logits) {
+    or_rms_norm(x, md->final_norm, d, a);
+    synth_matvec(&md->embedding, a, logits);
+  }
+  free(x); free(a); free(q); free(k); free(v); free(o); free(p); free(h);
+  return OR_OK;
+}
+
+/* Writes positions [0, length) of every (layer, kv head) of `kv` with the
+ * synthetic prefix rows: K row (l, h, p) = or_gen_kv_row(seed_k, (l * H + h)
+ * * max_length + p, ...), V likewise with seed_v. */
+void or_kv_fill_synthetic(or_kv* kv, uint64_t seed_k, uint64_t seed_v, uint32_t length, float lo,
+                          float hi) {
+  for (uint32_t l = 0; l < kv->layers; l++)
+    for (uint32_t h = 0; h < kv->kv_heads; h++)
+      for (uint32_t p = 0; p < length; p++) {
+        uint64_t index = ((uint64_t)l * kv->kv_heads + h) * kv->max_length + p;
+        uint32_t slot = or_kv_slot(kv, p);
+        size_t base = kv_base(kv, l, h, slot), si = kv_scale_index(kv, l, h, slot);
+        or_gen_kv_row(seed_k, index, kv->head_dim, lo, hi, kv->k8 + base, kv->ks + si);
+        or_gen_kv_row(seed_v, index, kv->head_dim, lo, hi, kv->v8 + base, kv->vs + si);
+      }
+}
+
+/* Constrained batched greedy decode (BASELINE configuration 5 semantics):
+ * for step t and sequence b, run or_synth_step on the current token at
+ * position start[b] + t, build the allowed mask with seed
+ * or_splitmix64_at(mask_seed, t * 65536 + b), select with or_select_mask
+ * (selectToken over the ascending allowed list), and feed the id back.
+ * Sequences are independent and are spread over `threads` POSIX threads;
+ * each sequence's arithmetic is the single-sequence oracle's. */
+
+typedef struct {
+  const or_synth* md;
+  or_kv** kvs;
+  const uint32_t* tokens;
+  const uint32_t* start;
+  uint32_t batch, steps, threshold24;
+  uint64_t mask_seed;
+  uint32_t* out_ids;    /* [steps][batch] */
+  double* out_logprob;  /* [steps][batch] */
+  uint32_t next;        /* work counter */
+  pthread_mutex_t lock;
+  int status;
+} or_batch_job;
+
+static void* batch_worker(void* arg) {
+  or_batch_job* job = (or_batch_job*)arg;
+  const or_synth* md = job->md;
+  float* logits = (float*)malloc(sizeof(float) * md->vocab);
+  uint32_t* mask = (uint32_t*)malloc(sizeof(uint32_t) * ((md->vocab + 31) / 32));
+  for (;;) {
+    pthread_mutex_lock(&job->lock);
+    uint32_t b = job->next++;
+    pthread_mutex_unlock(&job->lock);
+    if (b >= job->batch) break;
+    uint32_t token = job->tokens[b];
+    for (uint32_t t = 0; t < job->steps; t++) {
+      if (or_synth_step(md, job->kvs[b], token, job->start[b] + t, logits, NULL) != OR_OK) {
+        job->status = OR_INVALID;
+        break;
+      }
+      or_gen_mask(or_splitmix64_at(job->mask_seed, (uint64_t)t * 65536 + b), md->vocab,
+                  job->threshold24, mask);
+      uint32_t id;
+      double lp;
+      or_select_mask(logits, md->vocab, mask, &id, &lp);
+      job->out_ids[(size_t)t * job->batch + b] = id;
+      job->out_logprob[(size_t)t * job->batch + b] = lp;
+      token = id;
+    }
+  }
+  free(logits);
+  free(mask);
+  return NULL;
+}
+
+int or_synth_decode_batch(const or_synth* md, or_kv** kvs, const uint32_t* tokens,
+                          const uint32_t* start, uint32_t batch, uint32_t steps,
+                          uint64_t mask_seed, uint32_t threshold24, uint32_t* out_ids,
+                          double* out_logprob, uint32_t threads) {
+  or_batch_job job = {md, kvs, tokens, start, batch, steps, threshold24, mask_seed,
+                      out_ids, out_logprob, 0, PTHREAD_MUTEX_INITIALIZER, OR_OK};
+  if (threads < 1) threads = 1;
+  if (threads > batch) threads = batch;
+  pthread_t* tid = (pthread_t*)malloc(sizeof(pthread_t) * threads);
+  for (uint32_t i = 0; i < threads; i++) pthread_create(&tid[i], NULL, batch_worker, &job);
+  for (uint32_t i = 0; i < threads; i++) pthread_join(tid[i], NULL);
+  free(tid);
+  return job.status;
 }
