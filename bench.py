@@ -149,6 +149,94 @@ def bench_attention(torch, hip, length, heads, steps, warmup, rotate=True):
             "ms_per_call": ms, "GBps": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
 
 
+def decoder_weight_bytes(g):
+    """int8 codes + f32 per-row scales read by one decode step (tied lm head)."""
+    per_layer = [(g.heads + 2 * g.kv_heads) * 64 * g.dim, g.dim * g.heads * 64, g.ffn * g.dim,
+                 g.dim * g.ffn]
+    rows = [(g.heads + 2 * g.kv_heads) * 64, g.dim, g.ffn, g.dim]
+    total = g.layers * (sum(per_layer) + 4 * sum(rows))
+    return total + g.vocab * g.dim + 4 * g.vocab
+
+
+def bench_constrained_decode(torch, hip, steps, warmup, check, threads, cpu_seconds):
+    """Batched constrained greedy decode: 64 sequences, ragged contexts
+    U{32..2048}, vocab 32768, ~2% allowed bitmask per sequence per step."""
+    import numpy as np
+
+    import oracle
+    from needle_hip.models import (MASK_THRESHOLD24, PREFIX_SCALE, ConstrainedWorkload,
+                                   DecoderGeometry, DecoderWeights, HipBatch, HipDecoder)
+
+    g = DecoderGeometry()
+    wl = ConstrainedWorkload(batch=64, steps=steps, min_context=32, max_context=2048,
+                             vocab=g.vocab)
+    weights = DecoderWeights(g, 2026)
+    dec = HipDecoder(hip, weights)
+    batch = HipBatch(dec, wl.batch, wl.max_length)
+    lengths, starts = wl.lengths, wl.start_tokens
+    for s in range(wl.batch):
+        batch.fill_synthetic(s, *wl.kv_seeds(s), int(lengths[s]), wl.max_length)
+    max_pos = int(lengths.max()) + steps - 1
+
+    def launch(stream):
+        batch.step(max_pos, mask_seed=wl.mask_seed, stream=stream)
+
+    batch.set_state(starts, lengths, 0)
+    timer = GraphTimer(torch, [launch])
+    batch.set_state(starts, lengths, 0)
+    for _ in range(warmup):
+        timer.graph.replay()
+    torch.cuda.synchronize()
+    batch.set_state(starts, lengths, 0)
+    ms_per_step = timer.time(steps, 0)
+    ids, lps = batch.history(0, steps)
+    tok_s = wl.batch / (ms_per_step * 1e-3)
+    kv_tokens = float(np.sum(lengths.astype(np.float64) + (steps + 1) / 2.0))
+    kv_bytes = kv_tokens * g.layers * g.kv_heads * (64 + 64 + 4 + 4)
+    step_bytes = kv_bytes + decoder_weight_bytes(g) + wl.batch * ((g.vocab + 31) // 32) * 4
+    gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+    part = {"sequences": wl.batch, "steps": steps, "ms_per_step": ms_per_step,
+            "tokens_per_s": tok_s, "context_mean": float(lengths.mean()),
+            "bytes_per_step": step_bytes, "GBps": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
+
+    def caches():
+        out = []
+        for s in range(wl.batch):
+            c = oracle.KvCache(g.layers, g.kv_heads, wl.max_length)
+            oracle.kv_fill_synthetic(c, *wl.kv_seeds(s), int(lengths[s]), *PREFIX_SCALE)
+            out.append(c)
+        return out
+
+    ref = oracle.SynthDecoder(weights)
+    cpu = None
+    if cpu_seconds > 0:
+        # One thread, a bounded sample: the first sequences, all in order.
+        sample_seqs = 2
+        sample_steps = max(1, min(steps, int(cpu_seconds / 0.09 / sample_seqs)))
+        cs = caches()[:sample_seqs]
+        t0 = time.perf_counter()
+        ref.decode_batch(cs, starts[:sample_seqs], lengths[:sample_seqs], sample_steps,
+                         wl.mask_seed, MASK_THRESHOLD24, threads=1)
+        el = time.perf_counter() - t0
+        cpu = {"value": sample_seqs * sample_steps / el, "unit": "tok/s", "cores": 1,
+               "kind": "port",
+               "sample": f"oracle decode of sequences 0-{sample_seqs - 1} x {sample_steps} steps "
+                         f"of the same workload ({el:.1f} s)"}
+        part["cpu_tokens_per_s"] = cpu["value"]
+        part["speedup_vs_cpu"] = tok_s / cpu["value"]
+    if check:
+        t0 = time.perf_counter()
+        want, want_lp = ref.decode_batch(caches(), starts, lengths, steps, wl.mask_seed,
+                                         MASK_THRESHOLD24, threads=threads)
+        part["greedy_identical"] = bool(np.array_equal(ids, want))
+        part["greedy_mismatches"] = int(np.sum(ids != want))
+        part["logprob_max_abs_err"] = float(np.max(np.abs(lps - want_lp)))
+        part["check_seconds"] = time.perf_counter() - t0
+    batch.free()
+    dec.free()
+    return part, cpu
+
+
 def cpu_baseline_matvec(n, k, g, seconds):
     """The oracle (one thread) on the same matvec workload, timed on this host."""
     import numpy as np
@@ -180,6 +268,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=3, help="untimed graph replays")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-decode", action="store_true")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the batched constrained decode part (for profiling)")
+    ap.add_argument("--decode-steps", type=int, default=128)
+    ap.add_argument("--no-check", action="store_true",
+                    help="skip the full-size greedy identity check against the oracle")
+    ap.add_argument("--check-threads", type=int, default=min(16, os.cpu_count() or 1))
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
@@ -193,6 +288,10 @@ def main():
     hip = HipBackend(device=0)
     n = k = 4096
     g = 32
+    if args.decode_only:
+        part, _ = bench_constrained_decode(torch, hip, args.decode_steps, 2, False, 1, 0)
+        print(json.dumps({"constrained_decode_b64": part}))
+        return
     main_mv = bench_matvec(torch, hip, n, k, g, 1, args.steps, args.warmup)
     print(f"[bench] matvec b1 HBM {main_mv['GBps']:.0f} GB/s "
           f"{main_mv['ms_per_launch'] * 1e3:.2f} us/launch", file=sys.stderr, flush=True)
@@ -209,6 +308,16 @@ def main():
               f"{parts[f'attention_L{length}_hbm']['GBps']:.0f} GB/s", file=sys.stderr, flush=True)
     parts["attention_L8192_mall"] = bench_attention(torch, hip, 8192, 8, args.steps // 2,
                                                     args.warmup, rotate=False)
+    if not args.skip_decode:
+        part, cpu_dec = bench_constrained_decode(
+            torch, hip, args.decode_steps, 2, not args.no_check, args.check_threads,
+            0 if args.skip_cpu else args.cpu_seconds)
+        parts["constrained_decode_b64"] = part
+        if cpu_dec:
+            parts["constrained_decode_b64"]["cpu_baseline"] = cpu_dec
+        print(f"[bench] constrained decode b64 {part['tokens_per_s']:.0f} tok/s "
+              f"{part['ms_per_step']:.3f} ms/step greedy_identical="
+              f"{part.get('greedy_identical')}", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.skip_cpu:

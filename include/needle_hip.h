@@ -281,6 +281,12 @@ nd_status nd_batch_step(nd_ctx* ctx, nd_batch* batch, uint32_t max_position, uin
 nd_status nd_batch_read(nd_ctx* ctx, nd_batch* batch, uint32_t* tokens, uint32_t* positions,
                         double* log_probabilities, float* logits);
 
+/* Every step records its selected ids and log-probabilities at row t (the
+ * step counter) of a [max_length][batch] history in HBM; copies rows
+ * [first_step, first_step + steps) to the host and synchronises. */
+nd_status nd_batch_history(nd_ctx* ctx, nd_batch* batch, uint32_t first_step, uint32_t steps,
+                           uint32_t* ids, double* log_probabilities);
+
 #ifdef __cplusplus
 }
 #endif

@@ -155,17 +155,25 @@ __global__ __launch_bounds__(64) void fill_kv_kernel(uint64_t seed_k, uint64_t s
   }
 }
 
-// After selection: feed ids back as the next tokens, advance positions and the
-// step counter.
-__global__ void advance_kernel(const uint32_t* __restrict__ ids, uint32_t* __restrict__ tokens,
-                               uint32_t* __restrict__ positions, uint32_t* __restrict__ step,
-                               uint32_t batch) {
-  const uint32_t b = threadIdx.x + blockIdx.x * blockDim.x;
-  if (b < batch) {
+// After selection (one workgroup): feed ids back as the next tokens, record
+// them and their log-probabilities in the per-step history, advance the
+// positions and then the step counter.
+__global__ __launch_bounds__(256) void advance_kernel(
+    const uint32_t* __restrict__ ids, const double* __restrict__ logprobs,
+    uint32_t* __restrict__ tokens, uint32_t* __restrict__ positions, uint32_t* __restrict__ step,
+    uint32_t* __restrict__ history, double* __restrict__ lp_history, uint32_t history_steps,
+    uint32_t batch) {
+  const uint32_t t = *step;
+  for (uint32_t b = threadIdx.x; b < batch; b += blockDim.x) {
     tokens[b] = ids[b];
     positions[b] += 1;
+    if (t < history_steps) {
+      history[(size_t)t * batch + b] = ids[b];
+      lp_history[(size_t)t * batch + b] = logprobs[b];
+    }
   }
-  if (b == 0) *step += 1;
+  __syncthreads();
+  if (threadIdx.x == 0) *step = t + 1;
 }
 
 }  // namespace
@@ -189,8 +197,8 @@ struct nd_batch {
         *logits = nullptr, *fm = nullptr, *partials = nullptr;
   int8_t* digits = nullptr;
   uint32_t *counters = nullptr, *masks = nullptr, *tokens = nullptr, *positions = nullptr,
-           *step = nullptr, *ids = nullptr;
-  double* logprobs = nullptr;
+           *step = nullptr, *ids = nullptr, *history = nullptr;
+  double *logprobs = nullptr, *lp_history = nullptr;  // history: [max_length][batch]
 };
 
 static inline size_t a256(size_t n) { return (n + 255) & ~size_t(255); }
@@ -363,7 +371,8 @@ nd_status nd_batch_create(nd_ctx* ctx, nd_decoder* dec, uint32_t batch, uint32_t
       a256((size_t)batch * dec->kv_heads * 4),                               // counters
       a256((size_t)batch * words * 4),                                       // masks
       a256((size_t)batch * 4), a256((size_t)batch * 4), a256(256),           // tokens, positions, step
-      a256((size_t)batch * 4), a256((size_t)batch * 8)};                     // ids, logprobs
+      a256((size_t)batch * 4), a256((size_t)batch * 8),                      // ids, logprobs
+      a256((size_t)max_length * batch * 4), a256((size_t)max_length * batch * 8)};  // history
   size_t total = 0;
   for (size_t v : sizes) total += v;
   hipError_t e = hipMalloc(&b->arena, total);
@@ -400,6 +409,8 @@ nd_status nd_batch_create(nd_ctx* ctx, nd_decoder* dec, uint32_t batch, uint32_t
   take(&b->step);
   take(&b->ids);
   take(&b->logprobs);
+  take(&b->history);
+  take(&b->lp_history);
   *out = b;
   return ND_OK;
 }
@@ -521,9 +532,25 @@ nd_status nd_batch_step(nd_ctx* ctx, nd_batch* b, uint32_t max_position, uint32_
   }
   ND_HIP(ctx, nd_launch_select_mask(b->logits, B, dec->vocab, use_masks ? b->masks : nullptr,
                                     b->ids, b->logprobs, s));
-  hipLaunchKernelGGL(advance_kernel, dim3((B + 255) / 256), dim3(256), 0, s, b->ids, b->tokens,
-                     b->positions, b->step, B);
+  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(256), 0, s, b->ids, b->logprobs, b->tokens,
+                     b->positions, b->step, b->history, b->lp_history, b->max_length, B);
   ND_HIP(ctx, hipGetLastError());
+  return ND_OK;
+}
+
+nd_status nd_batch_history(nd_ctx* ctx, nd_batch* b, uint32_t first_step, uint32_t steps,
+                           uint32_t* ids, double* log_probabilities) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!b) return nd_fail(ctx, ND_ERR_INVALID, "batch is NULL");
+  if ((uint64_t)first_step + steps > b->max_length)
+    return nd_fail(ctx, ND_ERR_INVALID, "history holds steps [0, %u)", b->max_length);
+  const size_t off = (size_t)first_step * b->batch, n = (size_t)steps * b->batch;
+  if (ids)
+    ND_HIP(ctx, hipMemcpyAsync(ids, b->history + off, n * 4, hipMemcpyDeviceToHost, ctx->stream));
+  if (log_probabilities)
+    ND_HIP(ctx, hipMemcpyAsync(log_probabilities, b->lp_history + off, n * 8,
+                               hipMemcpyDeviceToHost, ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return ND_OK;
 }
 

@@ -1,16 +1,18 @@
-// Int8 KV-cache append and split-context single-query decode attention.
+// Int8 KV-cache append and single-query decode attention.
 //
 // Cache layout in HBM (per nd_kv): codes [layers][kv_heads][alloc][64] int8,
 // scales [layers][kv_heads][alloc] f32, exactly NeedleRuntime's arrays
 // (model/runtime.ts:186-204, 666-677).  A 64-dim code row is 64 bytes, so a
-// 16-token x 64-dim tile is one contiguous 1 KiB run that a wave reads with
-// 128-bit loads.
+// 16-position x 64-dim tile is one contiguous 1 KiB run that a wave reads
+// with 128-bit loads.
 #include "nd_internal.hpp"
 
 namespace {
 
 constexpr uint32_t kHeadDim = 64;
-constexpr uint32_t kChunk = 64;  // visible positions per attention workgroup
+constexpr uint32_t kWavePositions = 64;  // positions a wave handles per iteration
+constexpr uint32_t kWaves = 4;           // waves per attention workgroup
+constexpr uint32_t kMinChunk = kWavePositions * kWaves;
 
 __device__ __forceinline__ uint32_t kv_slot(uint32_t position, uint32_t sink, uint32_t window) {
   if (window == 0 || position < sink) return position;
@@ -94,89 +96,104 @@ __device__ __forceinline__ Visible visible_at(uint32_t position, uint32_t sink, 
   return v;
 }
 
-__device__ __forceinline__ void decode16(const uint4& w, float* out) {
-  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+template <bool F32>
+struct Tile {
+  // Raw codes (or floats) of 4 positions x 16 dims for K and V, plus scales.
+  uint4 k[F32 ? 16 : 4], v[F32 ? 16 : 4];
+  float ks[4], vs[4];
+};
+
+template <bool F32>
+__device__ __forceinline__ void load_tile(Tile<F32>& tl, const void* Kc, const void* Vc,
+                                          const float* Ks, const float* Vs, size_t head_base,
+                                          const Visible& vis, uint32_t t0, uint32_t t_end,
+                                          uint32_t trow, uint32_t quad, uint32_t sink,
+                                          uint32_t window) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t t = t0 + trow + 16 * k;
+    const uint32_t slot = kv_slot(logical_at(vis, t < t_end ? t : t0), sink, window);
+    const size_t row = head_base + slot;
+    tl.ks[k] = Ks[row];
+    tl.vs[k] = Vs[row];
+    if constexpr (F32) {
+      const uint4* kp = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(Kc) + row * kHeadDim + quad * 16);
+      const uint4* vp = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(Vc) + row * kHeadDim + quad * 16);
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      out[4 * q + e] = (float)(int8_t)((words[q] >> (8 * e)) & 0xffu);
+      for (int c = 0; c < 4; ++c) {
+        tl.k[4 * k + c] = kp[c];
+        tl.v[4 * k + c] = vp[c];
+      }
+    } else {
+      tl.k[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const int8_t*>(Kc) + row * kHeadDim + quad * 16);
+      tl.v[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const int8_t*>(Vc) + row * kHeadDim + quad * 16);
+    }
   }
 }
 
-// One workgroup of W waves (W <= 4) per (kv head, chunk of 64*W visible
-// positions), serving all REP query heads of the kv head so that each code
-// byte is read once.  In wave w, lane l owns dims [16*(l&3), +16) of the
-// positions chunk*64W + 64w + (l>>2) + 16k, k < 4, so every 128-bit load of
-// the wave reads 16 consecutive 64-byte code rows (1 KiB contiguous).
-//
-// Each wave reduces its 64 positions to (max m, sum l, acc[64]) per query
-// head; the waves are merged through LDS.  With one chunk the workgroup
-// writes the normalized output.  Otherwise it writes its partial, and the
-// last workgroup of the kv head to finish (device-scope counter, reset by
-// that workgroup) merges all chunks with a log-sum-exp combine.
-constexpr int kMaxWaves = 4;
+template <bool F32>
+__device__ __forceinline__ void unpack(const Tile<F32>& tl, int k, bool is_v, float* out) {
+  if constexpr (F32) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint4 w = is_v ? tl.v[4 * k + c] : tl.k[4 * k + c];
+      out[4 * c + 0] = __uint_as_float(w.x);
+      out[4 * c + 1] = __uint_as_float(w.y);
+      out[4 * c + 2] = __uint_as_float(w.z);
+      out[4 * c + 3] = __uint_as_float(w.w);
+    }
+  } else {
+    const uint4 w = is_v ? tl.v[k] : tl.k[k];
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        out[4 * q + e] = (float)(int8_t)((words[q] >> (8 * e)) & 0xffu);
+    }
+  }
+}
 
+// Workgroup = 4 waves on one (sequence z, kv head, chunk of `chunk_positions`
+// visible positions), serving all REP query heads of the kv head so that each
+// code byte is read once.  Wave w walks 64-position tiles w, w+4, ... of the
+// chunk with a running (max, sum, acc) per query head (online softmax), and
+// prefetches its next tile before working on the current one.  In a tile,
+// lane l owns dims [16*(l&3), +16) of positions tile + (l>>2) + 16k, k < 4,
+// so each 128-bit load of the wave reads 16 consecutive 64-byte rows.
+//
+// The waves merge through LDS.  A sequence whose visible positions fit one
+// chunk gets its normalized output here; otherwise each chunk writes (max,
+// sum, acc[64]) per query head and attention_merge_kernel combines them.
+//
+// Scores: (q . k_codes) * k_scale / sqrt(64); softmax; out = sum w * v_codes *
+// v_scale -- NeedleRuntime.#attention (model/runtime.ts:719-786) with
+// softmaxInPlace (model/math.ts:46-60), evaluated in fp32.
 template <int REP, bool F32>
 __global__ __launch_bounds__(256) void attention_kernel(
     const void* __restrict__ Kc, const void* __restrict__ Vc, const float* __restrict__ Ks,
     const float* __restrict__ Vs, const float* __restrict__ Q, float* __restrict__ out,
-    float* __restrict__ part_acc, float* __restrict__ part_ml, uint32_t* __restrict__ counters,
-    uint32_t layer, uint32_t kv_heads, uint32_t alloc, uint32_t sink, uint32_t window,
-    Visible vis, const uint32_t* __restrict__ positions, uint32_t seq_kv_heads,
+    float* __restrict__ part_acc, float* __restrict__ part_ml, uint32_t layer, uint32_t kv_heads,
+    uint32_t alloc, uint32_t sink, uint32_t window, Visible vis,
+    const uint32_t* __restrict__ positions, uint32_t seq_kv_heads, uint32_t chunk_positions,
     uint32_t max_chunks, float score_scale) {
-  // blockIdx.z selects the sequence of a batch: its KV heads are cache heads
-  // [z * seq_kv_heads, +seq_kv_heads), its queries rows [z * Hq, +Hq), and its
-  // query position is positions[z] (or the single `vis` when positions is null).
-  const uint32_t chunk = blockIdx.x, z = blockIdx.z;
-  const uint32_t kvh_local = blockIdx.y;
+  const uint32_t chunk = blockIdx.x, kvh_local = blockIdx.y, z = blockIdx.z;
   const uint32_t kvh = z * seq_kv_heads + kvh_local;
   const uint32_t hq = seq_kv_heads * REP;
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const uint32_t nwaves = blockDim.x >> 6;
   const uint32_t quad = lane & 3, trow = lane >> 2;
   if (positions) {
     if (window == 0 && positions[z] >= alloc) return;  // validated on entry; stay in bounds
     vis = visible_at(positions[z], sink, window);
   }
-  // The grid covers max_chunks; a position beyond the launch's bound is a
-  // caller error that must not turn into out-of-range partial writes.
-  uint32_t nchunks = (vis.count + kChunk * nwaves - 1) / (kChunk * nwaves);
-  if (nchunks > max_chunks) nchunks = max_chunks;
+  uint32_t nchunks = (vis.count + chunk_positions - 1) / chunk_positions;
+  if (nchunks > max_chunks) nchunks = max_chunks;  // the grid bound; never write past it
   if (chunk >= nchunks) return;
+  const uint32_t c_begin = chunk * chunk_positions;
+  const uint32_t c_end = min(vis.count, c_begin + chunk_positions);
   Q += (size_t)z * hq * kHeadDim;
   out += (size_t)z * hq * kHeadDim;
-  const size_t part_base = (size_t)z * hq * max_chunks;
   const size_t head_base = ((size_t)layer * kv_heads + kvh) * alloc;
-  const uint32_t tok0 = (chunk * nwaves + wave) * kChunk;
-
-  float kc[4][16], vc[4][16];
-  float ks[4], vs[4];
-  bool valid[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const uint32_t t = tok0 + trow + 16 * k;
-    valid[k] = t < vis.count;
-    const uint32_t slot = kv_slot(logical_at(vis, valid[k] ? t : 0), sink, window);
-    const size_t row = head_base + slot;
-    ks[k] = Ks[row];
-    vs[k] = Vs[row];
-    if constexpr (F32) {
-      const float4* kp = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(Kc) + row * kHeadDim + quad * 16);
-      const float4* vp = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(Vc) + row * kHeadDim + quad * 16);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float4 a = kp[c], b = vp[c];
-        kc[k][4 * c + 0] = a.x; kc[k][4 * c + 1] = a.y; kc[k][4 * c + 2] = a.z; kc[k][4 * c + 3] = a.w;
-        vc[k][4 * c + 0] = b.x; vc[k][4 * c + 1] = b.y; vc[k][4 * c + 2] = b.z; vc[k][4 * c + 3] = b.w;
-      }
-    } else {
-      const uint4 a = *reinterpret_cast<const uint4*>(reinterpret_cast<const int8_t*>(Kc) + row * kHeadDim + quad * 16);
-      const uint4 b = *reinterpret_cast<const uint4*>(reinterpret_cast<const int8_t*>(Vc) + row * kHeadDim + quad * 16);
-      decode16(a, kc[k]);
-      decode16(b, vc[k]);
-    }
-  }
 
   float q[REP][16];
 #pragma unroll
@@ -192,154 +209,200 @@ __global__ __launch_bounds__(256) void attention_kernel(
     }
   }
 
-  __shared__ float s_m[kMaxWaves][REP], s_l[kMaxWaves][REP];
-  __shared__ float s_acc[kMaxWaves][REP * kHeadDim];
-
+  float m[REP], l[REP], acc[REP][16];
 #pragma unroll
   for (int h = 0; h < REP; ++h) {
-    float sc[4];
-    float mh = -INFINITY;
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[h][i] = 0.f;
+  }
+
+  Tile<F32> cur, nxt;
+  uint32_t t0 = c_begin + wave * kWavePositions;
+  if (t0 < c_end) load_tile<F32>(cur, Kc, Vc, Ks, Vs, head_base, vis, t0, c_end, trow, quad, sink, window);
+  for (; t0 < c_end; t0 += kWaves * kWavePositions) {
+    const uint32_t tn = t0 + kWaves * kWavePositions;
+    if (tn < c_end) load_tile<F32>(nxt, Kc, Vc, Ks, Vs, head_base, vis, tn, c_end, trow, quad, sink, window);
+    bool valid[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) valid[k] = t0 + trow + 16 * k < c_end;
+    float p[REP][4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      float d = 0.f;
+      float kc[16];
+      unpack<F32>(cur, k, false, kc);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) d = fmaf(q[h][i], kc[k][i], d);
-      d += __shfl_xor(d, 1, 64);
-      d += __shfl_xor(d, 2, 64);
-      sc[k] = valid[k] ? d * ks[k] * score_scale : -INFINITY;
-      mh = fmaxf(mh, sc[k]);
+      for (int h = 0; h < REP; ++h) {
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) d = fmaf(q[h][i], kc[i], d);
+        d += __shfl_xor(d, 1, 64);
+        d += __shfl_xor(d, 2, 64);
+        p[h][k] = valid[k] ? d * cur.ks[k] * score_scale : -INFINITY;
+      }
     }
 #pragma unroll
-    for (int o = 4; o <= 32; o <<= 1) mh = fmaxf(mh, __shfl_xor(mh, o, 64));
-    float lh = 0.f;
-    float a[16];
+    for (int h = 0; h < REP; ++h) {
+      float tile_max = fmaxf(fmaxf(p[h][0], p[h][1]), fmaxf(p[h][2], p[h][3]));
 #pragma unroll
-    for (int i = 0; i < 16; ++i) a[i] = 0.f;
+      for (int o = 4; o <= 32; o <<= 1) tile_max = fmaxf(tile_max, __shfl_xor(tile_max, o, 64));
+      const float m_new = fmaxf(m[h], tile_max);
+      const float alpha = __expf(m[h] - m_new);  // 0 on the first tile (m = -inf)
+      m[h] = m_new;
+      l[h] *= alpha;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[h][i] *= alpha;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float e = valid[k] ? __expf(p[h][k] - m_new) : 0.f;
+        p[h][k] = e;
+        l[h] += e;
+      }
+    }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float e = valid[k] ? __expf(sc[k] - mh) : 0.f;
-      lh += e;
-      const float ev = e * vs[k];
+      float vc[16];
+      unpack<F32>(cur, k, true, vc);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) a[i] = fmaf(ev, vc[k][i], a[i]);
+      for (int h = 0; h < REP; ++h) {
+        const float ev = p[h][k] * cur.vs[k];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[h][i] = fmaf(ev, vc[i], acc[h][i]);
+      }
     }
-    // Sum over the 16 token rows (lane bits 2..5); all lanes of a quad end
-    // with the full sums of their 16 dims.
+    cur = nxt;
+  }
+
+  // Per wave: sum l and acc over the 16 token rows (lane bits 2..5).
+  __shared__ float s_m[kWaves][REP], s_l[kWaves][REP];
+  __shared__ float s_acc[kWaves][REP * kHeadDim];
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
 #pragma unroll
     for (int o = 4; o <= 32; o <<= 1) {
-      lh += __shfl_xor(lh, o, 64);
+      l[h] += __shfl_xor(l[h], o, 64);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) a[i] += __shfl_xor(a[i], o, 64);
+      for (int i = 0; i < 16; ++i) acc[h][i] += __shfl_xor(acc[h][i], o, 64);
     }
     if (trow == 0) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s_acc[wave][h * kHeadDim + quad * 16 + i] = a[i];
+      for (int i = 0; i < 16; ++i) s_acc[wave][h * kHeadDim + quad * 16 + i] = acc[h][i];
       if (quad == 0) {
-        s_m[wave][h] = mh;
-        s_l[wave][h] = lh;
+        s_m[wave][h] = m[h];
+        s_l[wave][h] = l[h];
       }
     }
   }
   __syncthreads();
 
   // Merge the waves: thread t < REP*64 owns (h, dim).
-  const uint32_t t = threadIdx.x;
-  float mine_m = -INFINITY, mine_l = 0.f, mine_a = 0.f;
-  uint32_t h_t = 0, dim_t = 0;
-  for (uint32_t o = t; o < REP * kHeadDim; o += blockDim.x) {
-    h_t = o / kHeadDim;
-    dim_t = o % kHeadDim;
+  for (uint32_t o = threadIdx.x; o < REP * kHeadDim; o += blockDim.x) {
+    const uint32_t h = o / kHeadDim, dim = o % kHeadDim;
     float mx = -INFINITY;
-    for (uint32_t w = 0; w < nwaves; ++w) mx = fmaxf(mx, s_m[w][h_t]);
+#pragma unroll
+    for (uint32_t w = 0; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][h]);
     float L = 0.f, A = 0.f;
-    for (uint32_t w = 0; w < nwaves; ++w) {
-      const float f = (s_m[w][h_t] == -INFINITY) ? 0.f : __expf(s_m[w][h_t] - mx);
-      L = fmaf(f, s_l[w][h_t], L);
-      A = fmaf(f, s_acc[w][h_t * kHeadDim + dim_t], A);
+#pragma unroll
+    for (uint32_t w = 0; w < kWaves; ++w) {
+      const float f = (s_m[w][h] == -INFINITY) ? 0.f : __expf(s_m[w][h] - mx);
+      L = fmaf(f, s_l[w][h], L);
+      A = fmaf(f, s_acc[w][h * kHeadDim + dim], A);
     }
-    const uint32_t qh = kvh_local * REP + h_t;
+    const uint32_t qh = kvh_local * REP + h;
     if (nchunks == 1) {
-      out[(size_t)qh * kHeadDim + dim_t] = A / L;
+      out[(size_t)qh * kHeadDim + dim] = A / L;
     } else {
-      const size_t pi = part_base + (size_t)qh * max_chunks + chunk;
-      part_acc[pi * kHeadDim + dim_t] = A;
-      if (dim_t == 0) {
+      const size_t pi = ((size_t)z * hq + qh) * max_chunks + chunk;
+      part_acc[pi * kHeadDim + dim] = A;
+      if (dim == 0) {
         part_ml[pi * 2 + 0] = mx;
         part_ml[pi * 2 + 1] = L;
       }
     }
-    mine_m = mx;
-    mine_l = L;
-    mine_a = A;
   }
-  (void)mine_m; (void)mine_l; (void)mine_a;
-  if (nchunks == 1) return;
+}
 
-  // Last-arriving workgroup of this kv head merges every chunk.
-  __shared__ uint32_t s_last;
-  __threadfence();
-  __syncthreads();
-  if (t == 0) s_last = (atomicAdd(&counters[kvh], 1u) == nchunks - 1) ? 1u : 0u;
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  if (t == 0) counters[kvh] = 0;  // ready for the next call on this stream
+// Log-sum-exp combine of a sequence's chunk partials: one wave per (query
+// head, sequence), lane = dim.  Sequences that fit one chunk were finished by
+// attention_kernel and are skipped.
+__global__ __launch_bounds__(64) void attention_merge_kernel(
+    const float* __restrict__ part_acc, const float* __restrict__ part_ml,
+    float* __restrict__ out, uint32_t hq, uint32_t sink, uint32_t window, Visible vis,
+    const uint32_t* __restrict__ positions, uint32_t alloc, uint32_t chunk_positions,
+    uint32_t max_chunks) {
+  const uint32_t qh = blockIdx.x, z = blockIdx.y, dim = threadIdx.x;
+  if (positions) {
+    if (window == 0 && positions[z] >= alloc) return;
+    vis = visible_at(positions[z], sink, window);
+  }
+  uint32_t nchunks = (vis.count + chunk_positions - 1) / chunk_positions;
+  if (nchunks > max_chunks) nchunks = max_chunks;
+  if (nchunks <= 1) return;
+  const size_t base = ((size_t)z * hq + qh) * max_chunks;
+  float mx = -INFINITY;
+  for (uint32_t c = 0; c < nchunks; ++c) mx = fmaxf(mx, part_ml[(base + c) * 2]);
+  float total = 0.f, acc = 0.f;
+#pragma unroll 4
+  for (uint32_t c = 0; c < nchunks; ++c) {
+    const float w = __expf(part_ml[(base + c) * 2] - mx);
+    total = fmaf(w, part_ml[(base + c) * 2 + 1], total);
+    acc = fmaf(w, part_acc[(base + c) * kHeadDim + dim], acc);
+  }
+  out[((size_t)z * hq + qh) * kHeadDim + dim] = acc / total;
+}
 
-  __shared__ float s_w[1024];
-  __shared__ float s_red[16][kHeadDim];
-  __shared__ float s_scalar[2];
-  for (int h = 0; h < REP; ++h) {
-    const uint32_t qh = kvh_local * REP + h;
-    const float* ml = part_ml + (part_base + (size_t)qh * max_chunks) * 2;
-    // Maximum over chunks.
-    float mx = -INFINITY;
-    for (uint32_t c = t; c < nchunks; c += blockDim.x) mx = fmaxf(mx, ml[2 * c]);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    if (lane == 0) s_m[wave][0] = mx;
-    __syncthreads();
-    mx = s_m[0][0];
-    for (uint32_t w = 1; w < nwaves; ++w) mx = fmaxf(mx, s_m[w][0]);
-    __syncthreads();
-    // Chunk weights and the total.
-    float L = 0.f;
-    for (uint32_t c = t; c < nchunks; c += blockDim.x) {
-      const float f = __expf(ml[2 * c] - mx);
-      s_w[c] = f;
-      L = fmaf(f, ml[2 * c + 1], L);
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o, 64);
-    if (lane == 0) s_l[wave][0] = L;
-    __syncthreads();
-    if (t == 0) {
-      float tot = 0.f;
-      for (uint32_t w = 0; w < nwaves; ++w) tot += s_l[w][0];
-      s_scalar[0] = tot;
-    }
-    // Weighted sum of chunk accumulators: 16 threads per chunk row (float4 each).
-    const uint32_t dq = t & 15, cg = t >> 4, ngroups = blockDim.x >> 4;
-    float4 a4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    const float* accs = part_acc + (part_base + (size_t)qh * max_chunks) * kHeadDim;
-    for (uint32_t c = cg; c < nchunks; c += ngroups) {
-      const float4 v = reinterpret_cast<const float4*>(accs + (size_t)c * kHeadDim)[dq];
-      const float f = s_w[c];
-      a4.x = fmaf(f, v.x, a4.x);
-      a4.y = fmaf(f, v.y, a4.y);
-      a4.z = fmaf(f, v.z, a4.z);
-      a4.w = fmaf(f, v.w, a4.w);
-    }
-    s_red[cg][dq * 4 + 0] = a4.x;
-    s_red[cg][dq * 4 + 1] = a4.y;
-    s_red[cg][dq * 4 + 2] = a4.z;
-    s_red[cg][dq * 4 + 3] = a4.w;
-    __syncthreads();
-    if (t < kHeadDim) {
-      float sum = 0.f;
-      for (uint32_t g2 = 0; g2 < ngroups; ++g2) sum += s_red[g2][t];
-      out[(size_t)qh * kHeadDim + t] = sum / s_scalar[0];
-    }
-    __syncthreads();
+// Positions per chunk: the whole visible range when the (sequence, kv head)
+// pairs alone give ~1024 workgroups, else split so that they do; at least
+// one tile per wave.
+uint32_t chunk_positions_for(uint32_t max_count, uint32_t pairs) {
+  const uint32_t want_chunks = pairs >= 1024 ? 1 : (1024 + pairs - 1) / pairs;
+  uint32_t cp = (max_count + want_chunks - 1) / want_chunks;
+  cp = (cp + kMinChunk - 1) / kMinChunk * kMinChunk;
+  return cp < kMinChunk ? kMinChunk : cp;
+}
+
+struct AttnLaunch {
+  const nd_kv* kv;
+  uint32_t layer;
+  const float* q;
+  float* out;
+  float* partials;
+  Visible vis;                 // used when positions == nullptr
+  const uint32_t* positions;   // per-sequence query positions, or nullptr
+  uint32_t seq_kv_heads;       // KV heads of one sequence
+  uint32_t rep;                // query heads per KV head
+  uint32_t batch;
+  uint32_t max_count;          // bound on every sequence's visible count
+};
+
+template <int REP, bool F32>
+hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
+  const uint32_t cp = chunk_positions_for(a.max_count, a.batch * a.seq_kv_heads);
+  const uint32_t max_chunks = (a.max_count + cp - 1) / cp;
+  const uint32_t hq = a.seq_kv_heads * REP;
+  float* part_acc = a.partials;
+  float* part_ml = a.partials + (size_t)a.batch * hq * max_chunks * kHeadDim;
+  hipLaunchKernelGGL((attention_kernel<REP, F32>), dim3(max_chunks, a.seq_kv_heads, a.batch),
+                     dim3(64 * kWaves), 0, s, a.kv->k, a.kv->v, a.kv->ks, a.kv->vs, a.q, a.out,
+                     part_acc, part_ml, a.layer, a.kv->kv_heads, a.kv->alloc, a.kv->sink,
+                     a.kv->window, a.vis, a.positions, a.seq_kv_heads, cp, max_chunks, 0.125f);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || max_chunks == 1) return e;
+  hipLaunchKernelGGL(attention_merge_kernel, dim3(hq, a.batch), dim3(64), 0, s, part_acc,
+                     part_ml, a.out, hq, a.kv->sink, a.kv->window, a.vis, a.positions,
+                     a.kv->alloc, cp, max_chunks);
+  return hipGetLastError();
+}
+
+template <bool F32>
+hipError_t launch_rep(const AttnLaunch& a, hipStream_t s) {
+  switch (a.rep) {
+    case 1: return launch_attention<1, F32>(a, s);
+    case 2: return launch_attention<2, F32>(a, s);
+    case 4: return launch_attention<4, F32>(a, s);
+    case 8: return launch_attention<8, F32>(a, s);
+    default: return hipErrorInvalidValue;
   }
 }
 
@@ -355,24 +418,22 @@ nd_visible nd_kv_visible(const nd_kv* kv, uint32_t position) {
   return v;
 }
 
-// Waves per workgroup: enough workgroups to cover the GPU first, then up to
-// four waves (256 positions) per workgroup to keep the merge short.
-static uint32_t attention_waves(uint32_t count, uint32_t kv_heads) {
-  const uint32_t wave_units = (count + kChunk - 1) / kChunk;
-  uint32_t w = 1;
-  while (w < kMaxWaves && wave_units * kv_heads >= 2u * w * 256u) w <<= 1;
-  return w;
-}
-
 uint32_t nd_attention_chunks(uint32_t count, uint32_t kv_heads) {
-  const uint32_t per = kChunk * attention_waves(count, kv_heads);
-  return (count + per - 1) / per;
+  const uint32_t cp = chunk_positions_for(count, kv_heads);
+  return (count + cp - 1) / cp;
 }
 
-// Upper bound for any visible count <= count (one wave per chunk at worst).
+// Partials for any launch with visible counts <= count (chunks are at least
+// kMinChunk positions).
 size_t nd_attention_partial_floats(uint32_t q_heads, uint32_t kv_heads, uint32_t count) {
   (void)kv_heads;
-  return (size_t)q_heads * ((count + kChunk - 1) / kChunk) * (kHeadDim + 2);
+  return (size_t)q_heads * ((count + kMinChunk - 1) / kMinChunk) * (kHeadDim + 2);
+}
+
+size_t nd_attention_batch_partial_floats(uint32_t batch, uint32_t seq_kv_heads, uint32_t rep,
+                                         uint32_t max_count) {
+  return (size_t)batch * seq_kv_heads * rep * ((max_count + kMinChunk - 1) / kMinChunk) *
+         (kHeadDim + 2);
 }
 
 hipError_t nd_launch_kv_store(const nd_kv* kv, uint32_t layer, uint32_t position, uint32_t first,
@@ -389,49 +450,10 @@ hipError_t nd_launch_kv_store(const nd_kv* kv, uint32_t layer, uint32_t position
   return hipGetLastError();
 }
 
-struct AttnLaunch {
-  const nd_kv* kv;
-  uint32_t layer;
-  const float* q;
-  float* out;
-  float* partials;
-  uint32_t* counters;
-  Visible vis;                 // used when positions == nullptr
-  const uint32_t* positions;   // per-sequence query positions, or nullptr
-  uint32_t seq_kv_heads;       // KV heads of one sequence
-  uint32_t rep;                // query heads per KV head
-  uint32_t batch;
-  uint32_t max_chunks;
-  uint32_t waves;
-};
-
-template <int REP, bool F32>
-static void launch_attention(const AttnLaunch& a, hipStream_t s) {
-  const size_t q_rows = (size_t)a.batch * a.seq_kv_heads * REP;
-  float* part_acc = a.partials;
-  float* part_ml = a.partials + q_rows * a.max_chunks * kHeadDim;
-  hipLaunchKernelGGL((attention_kernel<REP, F32>), dim3(a.max_chunks, a.seq_kv_heads, a.batch),
-                     dim3(64 * a.waves), 0, s, a.kv->k, a.kv->v, a.kv->ks, a.kv->vs, a.q, a.out,
-                     part_acc, part_ml, a.counters, a.layer, a.kv->kv_heads, a.kv->alloc,
-                     a.kv->sink, a.kv->window, a.vis, a.positions, a.seq_kv_heads, a.max_chunks,
-                     0.125f);
-}
-
-template <bool F32>
-static hipError_t launch_rep(const AttnLaunch& a, hipStream_t s) {
-  switch (a.rep) {
-    case 1: launch_attention<1, F32>(a, s); break;
-    case 2: launch_attention<2, F32>(a, s); break;
-    case 4: launch_attention<4, F32>(a, s); break;
-    case 8: launch_attention<8, F32>(a, s); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
-}
-
 hipError_t nd_launch_attention(const nd_kv* kv, uint32_t layer, uint32_t position,
                                const float* q, uint32_t q_heads, float* out, float* partials,
                                uint32_t* counters, hipStream_t s) {
+  (void)counters;
   const nd_visible nv = nd_kv_visible(kv, position);
   AttnLaunch a{};
   a.kv = kv;
@@ -439,14 +461,12 @@ hipError_t nd_launch_attention(const nd_kv* kv, uint32_t layer, uint32_t positio
   a.q = q;
   a.out = out;
   a.partials = partials;
-  a.counters = counters;
   a.vis = Visible{nv.prefix, nv.recent_low, nv.count};
   a.positions = nullptr;
   a.seq_kv_heads = kv->kv_heads;
   a.rep = q_heads / kv->kv_heads;
   a.batch = 1;
-  a.waves = attention_waves(nv.count, kv->kv_heads);
-  a.max_chunks = (nv.count + kChunk * a.waves - 1) / (kChunk * a.waves);
+  a.max_count = nv.count;
   return kv->mode == ND_KV_FLOAT32 ? launch_rep<true>(a, s) : launch_rep<false>(a, s);
 }
 
@@ -457,6 +477,7 @@ hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint
                                      uint32_t batch, uint32_t seq_kv_heads, uint32_t rep,
                                      uint32_t max_position, const float* q, float* out,
                                      float* partials, uint32_t* counters, hipStream_t s) {
+  (void)counters;
   const nd_visible nv = nd_kv_visible(kv, max_position);
   AttnLaunch a{};
   a.kv = kv;
@@ -464,19 +485,11 @@ hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint
   a.q = q;
   a.out = out;
   a.partials = partials;
-  a.counters = counters;
   a.vis = Visible{nv.prefix, nv.recent_low, nv.count};
   a.positions = positions;
   a.seq_kv_heads = seq_kv_heads;
   a.rep = rep;
   a.batch = batch;
-  a.waves = attention_waves(nv.count, seq_kv_heads * batch);
-  a.max_chunks = (nv.count + kChunk * a.waves - 1) / (kChunk * a.waves);
+  a.max_count = nv.count;
   return kv->mode == ND_KV_FLOAT32 ? launch_rep<true>(a, s) : launch_rep<false>(a, s);
-}
-
-size_t nd_attention_batch_partial_floats(uint32_t batch, uint32_t seq_kv_heads, uint32_t rep,
-                                         uint32_t max_count) {
-  const uint32_t chunks = (max_count + kChunk - 1) / kChunk;  // bound for every launch
-  return (size_t)batch * seq_kv_heads * rep * chunks * (kHeadDim + 2);
 }

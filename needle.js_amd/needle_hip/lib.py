@@ -88,6 +88,7 @@ SIGNATURES = {
     "nd_batch_set_state": (I32, [P, P, P, P, U32]),
     "nd_batch_step": (I32, [P, P, U32, U32, C.c_uint64, U32, P]),
     "nd_batch_read": (I32, [P, P, P, P, P, P]),
+    "nd_batch_history": (I32, [P, P, U32, U32, P, P]),
 }
 
 

@@ -150,6 +150,15 @@ class HipBatch:
                                                    L.ptr(lg) if logits else None), "nd_batch_read")
         return t, p, lp, lg
 
+    def history(self, first_step: int, steps: int):
+        """Selected ids [steps][batch] and log-probabilities recorded on device."""
+        ids = np.empty((steps, self.batch), np.uint32)
+        lps = np.empty((steps, self.batch), np.float64)
+        self.backend._check(self.lib.nd_batch_history(self.backend.ctx, self.handle, first_step,
+                                                      steps, L.ptr(ids), L.ptr(lps)),
+                            "nd_batch_history")
+        return ids, lps
+
     def kv_read(self, layer: int, seq: int, head: int):
         """(k_codes, v_codes, k_scales, v_scales) of one sequence's KV head."""
         kv = self.lib.nd_batch_kv(self.handle)
