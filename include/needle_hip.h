@@ -281,6 +281,35 @@ nd_status nd_batch_step(nd_ctx* ctx, nd_batch* batch, uint32_t max_position, uin
 nd_status nd_batch_read(nd_ctx* ctx, nd_batch* batch, uint32_t* tokens, uint32_t* positions,
                         double* log_probabilities, float* logits);
 
+/* ------------------------------------------------------------------ prefill */
+
+typedef struct nd_prefill nd_prefill;
+
+/* Buffers for prompts of up to max_tokens positions ending at or before
+ * max_context.  The reference has no batched prefill: NeedleRuntime.prefill
+ * is one step() per prompt token (model/runtime.ts:227-243). */
+nd_status nd_prefill_create(nd_ctx* ctx, nd_decoder* dec, uint32_t max_tokens,
+                            uint32_t max_context, nd_prefill** out);
+nd_status nd_prefill_free(nd_ctx* ctx, nd_prefill* prefill);
+
+/* Runs `count` prompt tokens at positions [position0, position0 + count)
+ * through the decoder in one pass: M-row int8-MFMA GEMMs, every position's
+ * K/V quantized into `kv` (int8, window 0, the decoder's layers and KV heads)
+ * with #storeKV semantics, then causal attention of each position over [0,
+ * its position] of the int8 cache -- what `count` sequential steps read,
+ * since a step stores its own K/V before attending (model/runtime.ts:501-502).
+ * Writes the last position's logits [vocab] when logits != NULL. */
+nd_status nd_prefill_tokens(nd_ctx* ctx, nd_prefill* prefill, nd_kv* kv, const uint32_t* tokens,
+                            uint32_t count, uint32_t position0, float* logits);
+
+/* The same in three parts, for callers that time or capture the device work:
+ * upload the tokens, enqueue the pass (no allocation, no synchronisation),
+ * then copy the logits. */
+nd_status nd_prefill_set_tokens(nd_ctx* ctx, nd_prefill* prefill, const uint32_t* tokens,
+                                uint32_t count, uint32_t position0);
+nd_status nd_prefill_run_d(nd_ctx* ctx, nd_prefill* prefill, nd_kv* kv, void* stream);
+nd_status nd_prefill_logits(nd_ctx* ctx, nd_prefill* prefill, float* logits);
+
 /* Every step records its selected ids and log-probabilities at row t (the
  * step counter) of a [max_length][batch] history in HBM; copies rows
  * [first_step, first_step + steps) to the host and synchronises. */

@@ -510,8 +510,9 @@ nd_status nd_batch_step(nd_ctx* ctx, nd_batch* b, uint32_t max_position, uint32_
                        b->q, (int8_t*)b->kv.k, (int8_t*)b->kv.v, b->kv.ks, b->kv.vs, l,
                        b->kv.kv_heads, b->kv.alloc, dec->kv_heads);
     ND_HIP(ctx, hipGetLastError());
-    ND_HIP(ctx, nd_launch_attention_batch(&b->kv, l, b->positions, B, dec->kv_heads, rep,
-                                          max_position, b->q, b->o, b->partials, b->counters, s));
+    ND_HIP(ctx, nd_launch_attention_batch(&b->kv, l, b->positions, B, dec->kv_heads,
+                                          dec->kv_heads, rep, max_position, b->q, b->o,
+                                          b->partials, s));
     ND_HIP(ctx, nd_launch_digitize(b->o, D, nullptr, nullptr, b->digits, b->fm, B, D, s));
     ND_HIP(ctx, nd_launch_gemm(dec->wo[l], b->digits, b->fm, b->x, D, B, 1, s));
     ND_HIP(ctx, nd_launch_digitize(b->x, D, dec->norms + dec->ffn_off + (size_t)l * D, nullptr,
@@ -535,6 +536,183 @@ nd_status nd_batch_step(nd_ctx* ctx, nd_batch* b, uint32_t max_position, uint32_
   hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(256), 0, s, b->ids, b->logprobs, b->tokens,
                      b->positions, b->step, b->history, b->lp_history, b->max_length, B);
   ND_HIP(ctx, hipGetLastError());
+  return ND_OK;
+}
+
+// ----------------------------------------------------------------- prefill
+
+struct nd_prefill {
+  nd_decoder* dec = nullptr;
+  uint32_t max_tokens = 0, max_context = 0, count = 0, position0 = 0;
+  char* arena = nullptr;
+  float *x = nullptr, *qkv = nullptr, *q = nullptr, *o = nullptr, *h = nullptr, *fm = nullptr,
+        *partials = nullptr, *logits = nullptr;
+  int8_t* digits = nullptr;
+  uint32_t *tokens = nullptr, *positions = nullptr;
+  size_t partial_floats = 0;
+};
+
+nd_status nd_prefill_create(nd_ctx* ctx, nd_decoder* dec, uint32_t max_tokens,
+                            uint32_t max_context, nd_prefill** out) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!dec || !out || max_tokens == 0 || max_tokens > 65535 || max_context < max_tokens ||
+      max_context > kMaxAttentionPositions)
+    return nd_fail(ctx, ND_ERR_INVALID,
+                   "nd_prefill_create: 1..65535 tokens and max_context in [tokens, %u]",
+                   kMaxAttentionPositions);
+  *out = nullptr;
+  nd_prefill* p = new nd_prefill();
+  p->dec = dec;
+  p->max_tokens = max_tokens;
+  p->max_context = max_context;
+  const size_t M = max_tokens;
+  const uint32_t rep = dec->heads / dec->kv_heads;
+  const uint32_t qkv_rows = (dec->heads + 2 * dec->kv_heads) * kHd;
+  const uint32_t kmax = dec->ffn > dec->dim ? dec->ffn : dec->dim;
+  // Chunks of >= 256 positions over at most max_context positions.
+  p->partial_floats = nd_attention_batch_partial_floats(max_tokens, dec->kv_heads, rep,
+                                                        max_context);
+  const size_t sizes[] = {a256(M * dec->dim * 4),  a256(M * qkv_rows * 4), a256(M * dec->dim * 4),
+                          a256(M * dec->dim * 4),  a256(M * dec->ffn * 4), a256(M * 4),
+                          a256(p->partial_floats * 4), a256((size_t)dec->vocab * 4),
+                          a256(3 * M * kmax),      a256(M * 4),            a256(M * 4)};
+  size_t total = 0;
+  for (size_t v : sizes) total += v;
+  hipError_t e = hipMalloc(&p->arena, total);
+  if (e != hipSuccess) {
+    delete p;
+    return nd_hip_fail(ctx, e, "prefill allocation");
+  }
+  char* c = p->arena;
+  size_t i = 0;
+  auto take = [&](void* dst) {
+    *reinterpret_cast<char**>(dst) = c;
+    c += sizes[i++];
+  };
+  take(&p->x);
+  take(&p->qkv);
+  take(&p->q);
+  take(&p->o);
+  take(&p->h);
+  take(&p->fm);
+  take(&p->partials);
+  take(&p->logits);
+  take(&p->digits);
+  take(&p->tokens);
+  take(&p->positions);
+  *out = p;
+  return ND_OK;
+}
+
+nd_status nd_prefill_free(nd_ctx* ctx, nd_prefill* p) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!p) return ND_OK;
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  hipFree(p->arena);
+  delete p;
+  return ND_OK;
+}
+
+static nd_status check_prefill(nd_ctx* ctx, const nd_prefill* p, const nd_kv* kv, uint32_t count,
+                               uint32_t position0) {
+  if (!p || !kv) return nd_fail(ctx, ND_ERR_INVALID, "prefill or cache is NULL");
+  if (count == 0 || count > p->max_tokens)
+    return nd_fail(ctx, ND_ERR_INVALID, "prefill of %u tokens (session holds %u)", count,
+                   p->max_tokens);
+  if (kv->layers != p->dec->layers || kv->kv_heads != p->dec->kv_heads || kv->window != 0 ||
+      kv->mode != ND_KV_INT8 || kv->head_dim != kHd)
+    return nd_fail(ctx, ND_ERR_INVALID,
+                   "prefill cache must be int8, window 0, with the decoder's layers and KV heads");
+  if ((uint64_t)position0 + count > kv->max_length || (uint64_t)position0 + count > p->max_context)
+    return nd_fail(ctx, ND_ERR_OVERFLOW, "Prompt ends at %u but the runtime holds %u (session %u)",
+                   position0 + count, kv->max_length, p->max_context);
+  return ND_OK;
+}
+
+nd_status nd_prefill_set_tokens(nd_ctx* ctx, nd_prefill* p, const uint32_t* tokens, uint32_t count,
+                                uint32_t position0) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!p || !tokens || count == 0 || count > p->max_tokens)
+    return nd_fail(ctx, ND_ERR_INVALID, "nd_prefill_set_tokens: bad argument");
+  std::vector<uint32_t> pos(count);
+  for (uint32_t i = 0; i < count; ++i) {
+    if (tokens[i] >= p->dec->vocab)
+      return nd_fail(ctx, ND_ERR_INVALID, "Token %u is outside the vocabulary", tokens[i]);
+    pos[i] = position0 + i;
+  }
+  ND_HIP(ctx, hipMemcpyAsync(p->tokens, tokens, (size_t)count * 4, hipMemcpyHostToDevice, ctx->stream));
+  ND_HIP(ctx, hipMemcpyAsync(p->positions, pos.data(), (size_t)count * 4, hipMemcpyHostToDevice,
+                             ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  p->count = count;
+  p->position0 = position0;
+  return ND_OK;
+}
+
+// Enqueues the prefill of the tokens set by nd_prefill_set_tokens: every
+// layer runs as M-row GEMMs on int8 MFMA; all M positions' K/V are quantized
+// into the cache first, then each position attends causally over [0, its
+// position] of the int8 cache -- the same reads 2048 sequential steps make,
+// since a step stores its own K/V before its attention (runtime.ts:501-502).
+// The last position's logits stay in HBM (nd_prefill_logits copies them).
+nd_status nd_prefill_run_d(nd_ctx* ctx, nd_prefill* p, nd_kv* kv, void* stream) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_prefill(ctx, p, kv, p ? p->count : 0, p ? p->position0 : 0);
+  if (st != ND_OK) return st;
+  hipStream_t s = nd_pick_stream(ctx, stream);
+  const nd_decoder* dec = p->dec;
+  const uint32_t M = p->count, D = dec->dim, F = dec->ffn;
+  const uint32_t qkv_rows = (dec->heads + 2 * dec->kv_heads) * kHd;
+  const uint32_t rep = dec->heads / dec->kv_heads;
+  const uint32_t last = p->position0 + M - 1;
+  hipLaunchKernelGGL(embed_kernel, dim3((D + 255) / 256, M), dim3(256), 0, s, dec->embedding->w,
+                     dec->embedding->scales, p->tokens, dec->vocab, D, std::sqrt((double)D), p->x);
+  ND_HIP(ctx, hipGetLastError());
+  for (uint32_t l = 0; l < dec->layers; ++l) {
+    ND_HIP(ctx, nd_launch_digitize(p->x, D, dec->norms + dec->attn_off + (size_t)l * D, nullptr,
+                                   p->digits, p->fm, M, D, s));
+    ND_HIP(ctx, nd_launch_gemm(&dec->wqkv[l], p->digits, p->fm, p->qkv, qkv_rows, M, 0, s));
+    hipLaunchKernelGGL(qk_rope_store_kernel, dim3(dec->heads + dec->kv_heads, M), dim3(64), 0, s,
+                       p->qkv, qkv_rows, dec->heads, dec->kv_heads,
+                       dec->norms + dec->q_off + (size_t)l * kHd,
+                       dec->norms + dec->k_off + (size_t)l * kHd, dec->inv_freq, nullptr,
+                       p->position0, p->q, (int8_t*)kv->k, (int8_t*)kv->v, kv->ks, kv->vs, l,
+                       kv->kv_heads, kv->alloc, 0u);
+    ND_HIP(ctx, hipGetLastError());
+    ND_HIP(ctx, nd_launch_attention_batch(kv, l, p->positions, M, dec->kv_heads, 0u, rep, last,
+                                          p->q, p->o, p->partials, s));
+    ND_HIP(ctx, nd_launch_digitize(p->o, D, nullptr, nullptr, p->digits, p->fm, M, D, s));
+    ND_HIP(ctx, nd_launch_gemm(dec->wo[l], p->digits, p->fm, p->x, D, M, 1, s));
+    ND_HIP(ctx, nd_launch_digitize(p->x, D, dec->norms + dec->ffn_off + (size_t)l * D, nullptr,
+                                   p->digits, p->fm, M, D, s));
+    ND_HIP(ctx, nd_launch_gemm(dec->wup[l], p->digits, p->fm, p->h, F, M, 2, s));
+    ND_HIP(ctx, nd_launch_digitize(p->h, F, nullptr, nullptr, p->digits, p->fm, M, F, s));
+    ND_HIP(ctx, nd_launch_gemm(dec->wdown[l], p->digits, p->fm, p->x, D, M, 1, s));
+  }
+  ND_HIP(ctx, nd_launch_digitize(p->x + (size_t)(M - 1) * D, D, dec->norms + dec->final_off,
+                                 nullptr, p->digits, p->fm, 1, D, s));
+  ND_HIP(ctx, nd_launch_gemm(dec->embedding, p->digits, p->fm, p->logits, dec->vocab, 1, 0, s));
+  return ND_OK;
+}
+
+nd_status nd_prefill_logits(nd_ctx* ctx, nd_prefill* p, float* logits) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!p || !logits) return nd_fail(ctx, ND_ERR_INVALID, "NULL argument");
+  ND_HIP(ctx, hipMemcpyAsync(logits, p->logits, (size_t)p->dec->vocab * 4, hipMemcpyDeviceToHost,
+                             ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ND_OK;
+}
+
+nd_status nd_prefill_tokens(nd_ctx* ctx, nd_prefill* p, nd_kv* kv, const uint32_t* tokens,
+                            uint32_t count, uint32_t position0, float* logits) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_prefill(ctx, p, kv, count, position0);
+  if (st != ND_OK) return st;
+  if ((st = nd_prefill_set_tokens(ctx, p, tokens, count, position0)) != ND_OK) return st;
+  if ((st = nd_prefill_run_d(ctx, p, kv, nullptr)) != ND_OK) return st;
+  if (logits) return nd_prefill_logits(ctx, p, logits);
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return ND_OK;
 }
 

@@ -175,10 +175,13 @@ __global__ __launch_bounds__(256) void attention_kernel(
     const float* __restrict__ Vs, const float* __restrict__ Q, float* __restrict__ out,
     float* __restrict__ part_acc, float* __restrict__ part_ml, uint32_t layer, uint32_t kv_heads,
     uint32_t alloc, uint32_t sink, uint32_t window, Visible vis,
-    const uint32_t* __restrict__ positions, uint32_t seq_kv_heads, uint32_t chunk_positions,
-    uint32_t max_chunks, float score_scale) {
+    const uint32_t* __restrict__ positions, uint32_t seq_kv_heads, uint32_t kv_stride_z,
+    uint32_t chunk_positions, uint32_t max_chunks, float score_scale) {
+  // z indexes query rows: sequences of a batch (kv_stride_z = seq_kv_heads,
+  // each with its own cache heads) or positions of one prefill (kv_stride_z
+  // = 0, all reading the same cache heads).
   const uint32_t chunk = blockIdx.x, kvh_local = blockIdx.y, z = blockIdx.z;
-  const uint32_t kvh = z * seq_kv_heads + kvh_local;
+  const uint32_t kvh = z * kv_stride_z + kvh_local;
   const uint32_t hq = seq_kv_heads * REP;
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const uint32_t quad = lane & 3, trow = lane >> 2;
@@ -371,6 +374,7 @@ struct AttnLaunch {
   Visible vis;                 // used when positions == nullptr
   const uint32_t* positions;   // per-sequence query positions, or nullptr
   uint32_t seq_kv_heads;       // KV heads of one sequence
+  uint32_t kv_stride_z;        // cache-head offset between query rows z
   uint32_t rep;                // query heads per KV head
   uint32_t batch;
   uint32_t max_count;          // bound on every sequence's visible count
@@ -386,7 +390,8 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
   hipLaunchKernelGGL((attention_kernel<REP, F32>), dim3(max_chunks, a.seq_kv_heads, a.batch),
                      dim3(64 * kWaves), 0, s, a.kv->k, a.kv->v, a.kv->ks, a.kv->vs, a.q, a.out,
                      part_acc, part_ml, a.layer, a.kv->kv_heads, a.kv->alloc, a.kv->sink,
-                     a.kv->window, a.vis, a.positions, a.seq_kv_heads, cp, max_chunks, 0.125f);
+                     a.kv->window, a.vis, a.positions, a.seq_kv_heads, a.kv_stride_z, cp,
+                     max_chunks, 0.125f);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || max_chunks == 1) return e;
   hipLaunchKernelGGL(attention_merge_kernel, dim3(hq, a.batch), dim3(64), 0, s, part_acc,
@@ -464,20 +469,21 @@ hipError_t nd_launch_attention(const nd_kv* kv, uint32_t layer, uint32_t positio
   a.vis = Visible{nv.prefix, nv.recent_low, nv.count};
   a.positions = nullptr;
   a.seq_kv_heads = kv->kv_heads;
+  a.kv_stride_z = 0;
   a.rep = q_heads / kv->kv_heads;
   a.batch = 1;
   a.max_count = nv.count;
   return kv->mode == ND_KV_FLOAT32 ? launch_rep<true>(a, s) : launch_rep<false>(a, s);
 }
 
-// Batched form: sequence z owns cache heads [z * seq_kv_heads, +seq_kv_heads)
-// and queries q[z][seq_kv_heads * rep][64]; its query position is
+// Batched form: query row z reads cache heads [z * kv_stride_z, +seq_kv_heads)
+// (kv_stride_z = seq_kv_heads for a batch of sequences, 0 for the positions of
+// one prefill) with queries q[z][seq_kv_heads * rep][64] at position
 // positions[z] (device memory), at most max_position.
 hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint32_t* positions,
-                                     uint32_t batch, uint32_t seq_kv_heads, uint32_t rep,
-                                     uint32_t max_position, const float* q, float* out,
-                                     float* partials, uint32_t* counters, hipStream_t s) {
-  (void)counters;
+                                     uint32_t batch, uint32_t seq_kv_heads, uint32_t kv_stride_z,
+                                     uint32_t rep, uint32_t max_position, const float* q,
+                                     float* out, float* partials, hipStream_t s) {
   const nd_visible nv = nd_kv_visible(kv, max_position);
   AttnLaunch a{};
   a.kv = kv;
@@ -488,6 +494,7 @@ hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint
   a.vis = Visible{nv.prefix, nv.recent_low, nv.count};
   a.positions = positions;
   a.seq_kv_heads = seq_kv_heads;
+  a.kv_stride_z = kv_stride_z;
   a.rep = rep;
   a.batch = batch;
   a.max_count = nv.count;

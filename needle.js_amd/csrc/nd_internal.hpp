@@ -97,8 +97,8 @@ hipError_t nd_launch_digitize(const float* x, uint32_t ldx, const float* norm, f
 hipError_t nd_launch_gemm(const nd_mat* w, const int8_t* digits, const float* fm, float* y,
                           uint32_t ldy, uint32_t M, int epilogue, hipStream_t s);
 hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint32_t* positions,
-                                     uint32_t batch, uint32_t seq_kv_heads, uint32_t rep,
-                                     uint32_t max_position, const float* q, float* out,
-                                     float* partials, uint32_t* counters, hipStream_t s);
+                                     uint32_t batch, uint32_t seq_kv_heads, uint32_t kv_stride_z,
+                                     uint32_t rep, uint32_t max_position, const float* q,
+                                     float* out, float* partials, hipStream_t s);
 size_t nd_attention_batch_partial_floats(uint32_t batch, uint32_t seq_kv_heads, uint32_t rep,
                                          uint32_t max_count);

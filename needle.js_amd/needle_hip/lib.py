@@ -89,6 +89,12 @@ SIGNATURES = {
     "nd_batch_step": (I32, [P, P, U32, U32, C.c_uint64, U32, P]),
     "nd_batch_read": (I32, [P, P, P, P, P, P]),
     "nd_batch_history": (I32, [P, P, U32, U32, P, P]),
+    "nd_prefill_create": (I32, [P, P, U32, U32, PP]),
+    "nd_prefill_free": (I32, [P, P]),
+    "nd_prefill_tokens": (I32, [P, P, P, P, U32, U32, P]),
+    "nd_prefill_set_tokens": (I32, [P, P, P, U32, U32]),
+    "nd_prefill_run_d": (I32, [P, P, P, P]),
+    "nd_prefill_logits": (I32, [P, P, P]),
 }
 
 

@@ -178,6 +178,51 @@ class HipBatch:
         self.handle = None
 
 
+class HipPrefill:
+    """One-pass prompt prefill into an int8 KV cache (nd_prefill)."""
+
+    def __init__(self, decoder: HipDecoder, max_tokens: int, max_context: int):
+        self.decoder = decoder
+        self.backend = decoder.backend
+        self.lib = self.backend.lib
+        handle = C.c_void_p()
+        self.backend._check(self.lib.nd_prefill_create(self.backend.ctx, decoder.handle,
+                                                       max_tokens, max_context, C.byref(handle)),
+                            "nd_prefill_create")
+        self.handle = handle
+
+    def run(self, cache, tokens, position0: int = 0, want_logits: bool = True):
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        logits = np.empty(self.decoder.geometry.vocab, np.float32) if want_logits else None
+        self.backend._check(self.lib.nd_prefill_tokens(self.backend.ctx, self.handle,
+                                                       cache.handle, L.ptr(t), t.size, position0,
+                                                       L.ptr(logits) if want_logits else None),
+                            "nd_prefill_tokens")
+        return logits
+
+    def set_tokens(self, tokens, position0: int = 0) -> None:
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        self.backend._check(self.lib.nd_prefill_set_tokens(self.backend.ctx, self.handle,
+                                                           L.ptr(t), t.size, position0),
+                            "nd_prefill_set_tokens")
+
+    def launch(self, cache, stream=None) -> None:
+        self.backend._check(self.lib.nd_prefill_run_d(self.backend.ctx, self.handle, cache.handle,
+                                                      C.c_void_p(stream) if stream else None),
+                            "nd_prefill_run_d")
+
+    def logits(self):
+        out = np.empty(self.decoder.geometry.vocab, np.float32)
+        self.backend._check(self.lib.nd_prefill_logits(self.backend.ctx, self.handle,
+                                                       L.ptr(out)), "nd_prefill_logits")
+        return out
+
+    def free(self) -> None:
+        if self.handle is not None and self.backend.ctx is not None:
+            self.lib.nd_prefill_free(self.backend.ctx, self.handle)
+        self.handle = None
+
+
 @dataclass(frozen=True)
 class ConstrainedWorkload:
     """Seeded inputs of a batched constrained decode: per-sequence prefix
