@@ -237,6 +237,53 @@ def bench_constrained_decode(torch, hip, steps, warmup, check, threads, cpu_seco
     return part, cpu
 
 
+def bench_prefill(torch, hip, tokens_n, reps, cpu_seconds):
+    """Prefill of a 2048-token prompt through the synthetic 8-layer decoder."""
+    import numpy as np
+
+    import oracle
+    from needle_hip import HipKvCache, synth
+    from needle_hip.models import DecoderGeometry, DecoderWeights, HipDecoder, HipPrefill
+
+    g = DecoderGeometry()
+    weights = DecoderWeights(g, 2026)
+    dec = HipDecoder(hip, weights)
+    pre = HipPrefill(dec, tokens_n, tokens_n)
+    cache = HipKvCache(hip, g.layers, g.kv_heads, max_length=tokens_n)
+    tokens = synth.Stream(2026, "prefill-prompt").integers(tokens_n, 0, g.vocab - 1)
+    pre.set_tokens(tokens, 0)
+    timer = GraphTimer(torch, [lambda stream: pre.launch(cache, stream)])
+    ms = timer.time(reps, 1)
+    logits = pre.logits()
+    # Algorithmic int8 work: 2*M*N*K per projection (three digit planes are
+    # executed; the figure counts the contraction once).
+    per_layer = 2 * tokens_n * g.dim * ((g.heads + 2 * g.kv_heads) * 64 + g.dim + 2 * g.ffn)
+    gemm_ops = g.layers * per_layer + 2 * g.vocab * g.dim
+    attn_flops = g.layers * g.heads * 4 * 64 * tokens_n * (tokens_n + 1) / 2
+    part = {"tokens": tokens_n, "ms": ms, "tokens_per_s": tokens_n / (ms * 1e-3),
+            "gemm_int8_ops": gemm_ops, "attention_flops": attn_flops,
+            "effective_TOPS": (gemm_ops + attn_flops) / (ms * 1e-3) / 1e12,
+            "kv_bytes_written": g.layers * g.kv_heads * tokens_n * (64 * 2 + 8)}
+    cpu = None
+    if cpu_seconds > 0:
+        ref = oracle.SynthDecoder(weights)
+        rc = ref.new_cache(tokens_n)
+        t0 = time.perf_counter()
+        n = 0
+        while n < tokens_n and time.perf_counter() - t0 < cpu_seconds:
+            ref.step(rc, int(tokens[n]), n)
+            n += 1
+        el = time.perf_counter() - t0
+        cpu = {"value": n / el, "unit": "tok/s", "cores": 1, "kind": "port",
+               "sample": f"oracle sequential steps over the first {n} prompt tokens ({el:.1f} s)"}
+        part["cpu_tokens_per_s_first_positions"] = cpu["value"]
+    part["last_logit_argmax"] = int(np.argmax(logits))
+    pre.free()
+    cache.free()
+    dec.free()
+    return part, cpu
+
+
 def cpu_baseline_matvec(n, k, g, seconds):
     """The oracle (one thread) on the same matvec workload, timed on this host."""
     import numpy as np
@@ -269,8 +316,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-decode", action="store_true")
-    ap.add_argument("--decode-only", action="store_true",
-                    help="run only the batched constrained decode part (for profiling)")
+    ap.add_argument("--skip-prefill", action="store_true")
+    ap.add_argument("--only", choices=["matvec", "attention", "decode", "prefill"],
+                    help="run one part alone and print its JSON (for profiling)")
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--no-check", action="store_true",
                     help="skip the full-size greedy identity check against the oracle")
@@ -288,9 +336,16 @@ def main():
     hip = HipBackend(device=0)
     n = k = 4096
     g = 32
-    if args.decode_only:
-        part, _ = bench_constrained_decode(torch, hip, args.decode_steps, 2, False, 1, 0)
-        print(json.dumps({"constrained_decode_b64": part}))
+    if args.only:
+        if args.only == "matvec":
+            part = bench_matvec(torch, hip, n, k, g, 1, args.steps, args.warmup)
+        elif args.only == "attention":
+            part = bench_attention(torch, hip, 8192, 8, args.steps // 2, args.warmup)
+        elif args.only == "decode":
+            part, _ = bench_constrained_decode(torch, hip, args.decode_steps, 2, False, 1, 0)
+        else:
+            part, _ = bench_prefill(torch, hip, 2048, 5, 0)
+        print(json.dumps({args.only: part}))
         return
     main_mv = bench_matvec(torch, hip, n, k, g, 1, args.steps, args.warmup)
     print(f"[bench] matvec b1 HBM {main_mv['GBps']:.0f} GB/s "
@@ -318,6 +373,14 @@ def main():
         print(f"[bench] constrained decode b64 {part['tokens_per_s']:.0f} tok/s "
               f"{part['ms_per_step']:.3f} ms/step greedy_identical="
               f"{part.get('greedy_identical')}", file=sys.stderr, flush=True)
+
+    if not args.skip_prefill:
+        part, cpu_pre = bench_prefill(torch, hip, 2048, 5, 0 if args.skip_cpu else args.cpu_seconds)
+        if cpu_pre:
+            part["cpu_baseline"] = cpu_pre
+        parts["prefill_2048"] = part
+        print(f"[bench] prefill 2048 {part['ms']:.2f} ms {part['tokens_per_s']:.0f} tok/s "
+              f"{part['effective_TOPS']:.1f} TOPS", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.skip_cpu:
