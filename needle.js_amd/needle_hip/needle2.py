@@ -1,0 +1,88 @@
+"""Needle 2 geometry and seeded int8 weights.
+
+The shipped geometry (apps/website/src/content/docs/tutorials/model-structure.mdx:12-23;
+packages/needle.js/tests/model.integration.test.ts:175-180): vocab 8192,
+d 512, 27 layers, 8 query heads and 4 KV heads of 64, 4 mHC lanes, Hadamard
+512, KV window 256, maximum sequence 2048, engram orders {2, 3} at layers
+{2, 15} with 4 tables x 8192 slots x 128 and 4 taps.  The archive's RoPE
+theta is not documented; 10000 is used.  Every Cactus-Quant matrix becomes an
+int8 matrix with one fp32 scale per row (uniform codes in [-127, 127],
+scales ~U(0.001, 0.02)); dense vectors are seeded near neutral (norm offsets
+~U(-0.1, 0.1), Hadamard diagonals ~U(0.5, 1.5)).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import synth
+from .backend import Int8Matrix
+
+
+@dataclass(frozen=True)
+class Needle2Geometry:
+    vocab: int = 8192
+    dim: int = 512
+    heads: int = 8
+    kv_heads: int = 4
+    layers: int = 27
+    head_dim: int = 64
+    max_length: int = 2048
+    hadamard: int = 512
+    lanes: int = 4
+    engram_slots: int = 8192
+    engram_sub: int = 128
+    engram_tables: int = 4
+    engram_taps: int = 4
+    orders: tuple = (2, 3)
+    sites: tuple = (2, 15)
+    rope_theta: float = 10000.0
+    kv_window: int = 256
+
+
+class Needle2Weights:
+    def __init__(self, g: Needle2Geometry, run_seed: int = 2026):
+        self.geometry = g
+        L, d, hd = g.layers, g.dim, g.head_dim
+
+        def mat(name, n, k):
+            w, s = synth.int8_matrix(run_seed, name, n, k, k)
+            return Int8Matrix(w, s, k, name)
+
+        def u(name, shape, lo, hi):
+            return synth.Stream(run_seed, name).uniform(shape, lo, hi)
+
+        self.embedding = mat("n2.embedding", g.vocab, d)
+        self.wq = [mat(f"n2.l{l}.wq", g.heads * hd, d) for l in range(L)]
+        self.wk = [mat(f"n2.l{l}.wk", g.kv_heads * hd, d) for l in range(L)]
+        self.wv = [mat(f"n2.l{l}.wv", g.kv_heads * hd, d) for l in range(L)]
+        self.wgate = [mat(f"n2.l{l}.wgate", g.heads * hd, d) for l in range(L)]
+        self.wo = [mat(f"n2.l{l}.wo", d, g.heads * hd) for l in range(L)]
+        self.norm_input = u("n2.norm_input", (L, d), -0.1, 0.1)
+        self.query_norm = u("n2.query_norm", (L, hd), -0.1, 0.1)
+        self.key_norm = u("n2.key_norm", (L, hd), -0.1, 0.1)
+        self.post_attn_norm = u("n2.post_attn_norm", (L, d), -0.1, 0.1)
+        self.attention_gate = u("n2.attention_gate", (L,), -1.0, 1.0)
+        self.pre_hadamard_norm = u("n2.pre_hadamard_norm", (L, d), -0.1, 0.1)
+        self.d1 = u("n2.d1", (L, d), 0.5, 1.5)
+        self.d2 = u("n2.d2", (L, g.hadamard), 0.5, 1.5)
+        self.d3 = u("n2.d3", (L, d), 0.5, 1.5)
+        ln = g.lanes
+        self.phi_pre = mat("n2.phi_pre", L * ln, ln * d)
+        self.phi_post = mat("n2.phi_post", L * ln, ln * d)
+        self.phi_res = mat("n2.phi_res", L * ln * ln, ln * d)
+        self.a_pre = u("n2.a_pre", (L,), 0.02, 0.1)
+        self.a_post = u("n2.a_post", (L,), 0.02, 0.1)
+        self.a_res = u("n2.a_res", (L,), 0.02, 0.1)
+        self.b_pre = u("n2.b_pre", (L * ln,), -0.5, 0.5)
+        self.b_post = u("n2.b_post", (L * ln,), -0.5, 0.5)
+        self.b_res = u("n2.b_res", (L * ln * ln,), -0.5, 0.5)
+        cat = g.engram_tables * g.engram_sub
+        self.eg_tables = [mat(f"n2.e{s}.tables", g.engram_tables * g.engram_slots, g.engram_sub)
+                          for s in range(len(g.sites))]
+        self.eg_key = [mat(f"n2.e{s}.key", d, cat) for s in range(len(g.sites))]
+        self.eg_value = [mat(f"n2.e{s}.value", d, cat) for s in range(len(g.sites))]
+        self.eg_taps = u("n2.eg_taps", (len(g.sites), g.engram_taps, d), -0.5, 0.5)
+        self.final_norm = u("n2.final_norm", (d,), -0.1, 0.1)

@@ -362,3 +362,129 @@ class SynthDecoder:
                                                b, steps, mask_seed, threshold24, _p(ids), _p(lps),
                                                threads))
         return ids, lps
+
+
+# ------------------------------------------------------------------ Needle 2
+
+class _N2Mat(C.Structure):
+    _fields_ = [("w", P), ("s", P), ("n", U32), ("k", U32)]
+
+
+class _N2Model(C.Structure):
+    _fields_ = [
+        ("vocab", U32), ("dim", U32), ("heads", U32), ("kv_heads", U32), ("layers", U32),
+        ("head_dim", U32), ("max_length", U32), ("hadamard", U32), ("lanes", U32),
+        ("engram_slots", U32), ("engram_sub", U32), ("engram_tables", U32), ("engram_taps", U32),
+        ("n_orders", U32), ("n_sites", U32), ("orders", U32 * 4), ("sites", U32 * 4),
+        ("rope_theta", D), ("kv_window", U32), ("embedding", _N2Mat),
+        ("wq", C.POINTER(_N2Mat)), ("wk", C.POINTER(_N2Mat)), ("wv", C.POINTER(_N2Mat)),
+        ("wgate", C.POINTER(_N2Mat)), ("wo", C.POINTER(_N2Mat)),
+        ("norm_input", P), ("query_norm", P), ("key_norm", P), ("post_attn_norm", P),
+        ("attention_gate", P), ("pre_hadamard_norm", P), ("d1", P), ("d2", P), ("d3", P),
+        ("phi_pre", _N2Mat), ("phi_post", _N2Mat), ("phi_res", _N2Mat),
+        ("a_pre", P), ("a_post", P), ("a_res", P), ("b_pre", P), ("b_post", P), ("b_res", P),
+        ("eg_tables", C.POINTER(_N2Mat)), ("eg_key", C.POINTER(_N2Mat)),
+        ("eg_value", C.POINTER(_N2Mat)), ("eg_taps", P), ("final_norm", P),
+    ]
+
+
+_SIG_N2 = {
+    "or_n2_create": (P, [P, U32, U32]),
+    "or_n2_destroy": (None, [P]),
+    "or_n2_kv": (P, [P]),
+    "or_n2_step": (C.c_int, [P, U32, P]),
+}
+
+
+def _n2_lib():
+    h = lib()
+    if not getattr(h, "_n2_bound", False):
+        for name, (res, args) in _SIG_N2.items():
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        h._n2_bound = True
+    return h
+
+
+class Needle2:
+    """The oracle's Needle 2 model (NeedleRuntime.step on the CPU path)."""
+
+    def __init__(self, weights):
+        g = weights.geometry
+        self.geometry = g
+        self._keep = []
+
+        def om(m):
+            c = np.ascontiguousarray(m.codes, np.int8)
+            s = np.ascontiguousarray(m.scales, np.float32)
+            self._keep += [c, s]
+            return _N2Mat(_p(c), _p(s), c.shape[0], c.shape[1])
+
+        def arr(ms):
+            a = (_N2Mat * max(1, len(ms)))(*[om(m) for m in ms])
+            self._keep.append(a)
+            return C.cast(a, C.POINTER(_N2Mat))
+
+        def vec(v):
+            v = np.ascontiguousarray(v, np.float32)
+            self._keep.append(v)
+            return _p(v)
+
+        st = _N2Model()
+        for f in ("vocab", "dim", "heads", "kv_heads", "layers", "head_dim", "max_length",
+                  "hadamard", "lanes", "engram_slots", "engram_sub", "engram_tables",
+                  "engram_taps", "kv_window"):
+            setattr(st, f, getattr(g, f))
+        st.n_orders, st.n_sites = len(g.orders), len(g.sites)
+        for i, o in enumerate(g.orders):
+            st.orders[i] = o
+        for i, s in enumerate(g.sites):
+            st.sites[i] = s
+        st.rope_theta = float(np.float32(g.rope_theta))
+        st.embedding = om(weights.embedding)
+        for name in ("wq", "wk", "wv", "wgate", "wo", "eg_tables", "eg_key", "eg_value"):
+            setattr(st, name, arr(getattr(weights, name)))
+        for name in ("phi_pre", "phi_post", "phi_res"):
+            setattr(st, name, om(getattr(weights, name)))
+        for name in ("norm_input", "query_norm", "key_norm", "post_attn_norm", "attention_gate",
+                     "pre_hadamard_norm", "d1", "d2", "d3", "a_pre", "a_post", "a_res", "b_pre",
+                     "b_post", "b_res", "eg_taps", "final_norm"):
+            setattr(st, name, vec(getattr(weights, name)))
+        self.struct = st
+        _n2_lib()
+
+    def runtime(self, max_length: int, sink: int = 0) -> "Needle2Runtime":
+        return Needle2Runtime(self, max_length, sink)
+
+
+class Needle2Runtime:
+    """One sequence: reset(maximumLength, sinkLength) then step()."""
+
+    def __init__(self, model: Needle2, max_length: int, sink: int = 0):
+        self.model = model
+        self.h = _n2_lib().or_n2_create(C.byref(model.struct), max_length, sink)
+        if not self.h:
+            raise OracleError("bad runtime length")
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _n2_lib().or_n2_destroy(self.h)
+            self.h = None
+
+    def step(self, token: int, want_logits: bool = True):
+        logits = np.empty(self.model.geometry.vocab, np.float32) if want_logits else None
+        _ok(_n2_lib().or_n2_step(self.h, token, _p(logits) if want_logits else None))
+        return logits
+
+    def kv_read(self, layer: int, head: int):
+        cache = KvCache.__new__(KvCache)
+        g = self.model.geometry
+        cache.layers, cache.kv_heads, cache.head_dim = g.layers, g.kv_heads, g.head_dim
+        cache.float_mode = False
+        cache.h = _n2_lib().or_n2_kv(self.h)
+        cache.alloc = int(lib().or_kv_alloc(cache.h))
+        try:
+            return cache.read(layer, head)
+        finally:
+            cache.h = None  # owned by the runtime
