@@ -316,6 +316,109 @@ nd_status nd_prefill_logits(nd_ctx* ctx, nd_prefill* prefill, float* logits);
 nd_status nd_batch_history(nd_ctx* ctx, nd_batch* batch, uint32_t first_step, uint32_t steps,
                            uint32_t* ids, double* log_probabilities);
 
+/* ------------------------------------------------------- Needle 2 (batch 1) */
+
+typedef struct nd_needle nd_needle;
+
+/* Needle 2 geometry and weights (model/cact.ts geometry fields; the per-layer
+ * tensors read by NeedleRuntime.step, model/runtime.ts:280-583).  Every
+ * matrix is a per-row-scaled int8 matrix (g == k) uploaded with
+ * nd_mat_upload_i8 and owned by the caller (it must outlive the model);
+ * dense vectors are host arrays copied at creation.
+ *   embedding  [vocab][dim], tied output projection (runtime.ts:570-577)
+ *   wq, wgate  layers entries of [heads*64][dim]; wk, wv [kv_heads*64][dim]
+ *   wo         [dim][heads*64]
+ *   phi_pre    [layers*lanes][lanes*dim], phi_post likewise,
+ *   phi_res    [layers*lanes*lanes][lanes*dim] (runtime.ts:385-420)
+ *   eg_tables  n_sites entries of [engram_tables*engram_slots][engram_sub]
+ *   eg_key, eg_value  n_sites entries of [dim][engram_tables*engram_sub]
+ * Limits: head_dim 64, lanes <= 4, dim <= 512, hadamard a power of two in
+ * [dim, 1024], heads / kv_heads in {1, 2, 4, 8}, n_sites <= 4,
+ * engram_tables <= 16 and a multiple of n_orders. */
+typedef struct nd_needle_desc {
+  uint32_t vocab, dim, heads, kv_heads, layers, head_dim, max_length, hadamard, lanes;
+  uint32_t kv_window;                  /* 0 = no sliding window */
+  uint32_t engram_slots, engram_sub, engram_tables, engram_taps;
+  uint32_t n_orders, orders[4];        /* engram n-gram orders */
+  uint32_t n_sites, sites[4];          /* layers that inject an engram */
+  float rope_theta;
+  const nd_mat* embedding;
+  const nd_mat* const* wq;
+  const nd_mat* const* wk;
+  const nd_mat* const* wv;
+  const nd_mat* const* wgate;
+  const nd_mat* const* wo;
+  const nd_mat* phi_pre;
+  const nd_mat* phi_post;
+  const nd_mat* phi_res;
+  const nd_mat* const* eg_tables;
+  const nd_mat* const* eg_key;
+  const nd_mat* const* eg_value;
+  const float* norm_input;         /* [layers][dim] */
+  const float* query_norm;         /* [layers][64] */
+  const float* key_norm;           /* [layers][64] */
+  const float* post_attn_norm;     /* [layers][dim] */
+  const float* pre_hadamard_norm;  /* [layers][dim] */
+  const float* d1;                 /* [layers][dim] */
+  const float* d2;                 /* [layers][hadamard] */
+  const float* d3;                 /* [layers][dim] */
+  const float* attention_gate;     /* [layers] */
+  const float* a_pre;              /* [layers] */
+  const float* a_post;             /* [layers] */
+  const float* a_res;              /* [layers] */
+  const float* b_pre;              /* [layers][lanes] */
+  const float* b_post;             /* [layers][lanes] */
+  const float* b_res;              /* [layers][lanes][lanes] */
+  const float* eg_taps;            /* [n_sites][engram_taps][dim] */
+  const float* final_norm;         /* [dim] */
+} nd_needle_desc;
+
+nd_status nd_needle_create(nd_ctx* ctx, const nd_needle_desc* desc, nd_needle** out);
+nd_status nd_needle_free(nd_ctx* ctx, nd_needle* model);
+
+/* NeedleRuntime.reset (model/runtime.ts:150-225): position 0, empty history
+ * and engram ring, an int8 KV cache of min(max_length, sink + kv_window)
+ * slots per (layer, KV head) (max_length without a window).  Errors:
+ * CONTEXT_OVERFLOW when max_length is 0 or above the model's max_length.
+ * The first reset allocates the runtime state for the model's max_length;
+ * later resets only clear it. */
+nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* model, uint32_t max_length, uint32_t sink);
+
+/* The runtime's KV cache (read it with nd_kv_read), or NULL before reset. */
+nd_kv* nd_needle_kv(nd_needle* model);
+uint32_t nd_needle_position(const nd_needle* model);
+
+/* NeedleRuntime.step (model/runtime.ts:280-583): runs `token` at the current
+ * position and advances it; copies the logits [vocab] when logits != NULL.
+ * Errors: INVALID_CACT before reset or for token >= vocab, CONTEXT_OVERFLOW
+ * at the runtime limit (model/runtime.ts:288-298). */
+nd_status nd_needle_step(nd_ctx* ctx, nd_needle* model, uint32_t token, float* logits);
+
+/* NeedleRuntime.prefill (model/runtime.ts:227-243): `count` steps, the last
+ * one with logits. */
+nd_status nd_needle_prefill(nd_ctx* ctx, nd_needle* model, const uint32_t* tokens,
+                            uint32_t count, float* logits);
+
+/* NeedleRuntime.stepSelected (model/runtime.ts:257-278): the step, then
+ * selectToken (model/runtime.ts:880-899) over `allowed` (count ascending ids,
+ * or all ids when allowed == NULL) on the device; returns the id and its
+ * full-vocabulary log-probability. */
+nd_status nd_needle_step_select(nd_ctx* ctx, nd_needle* model, uint32_t token,
+                                const uint32_t* allowed, uint32_t count, uint32_t* id,
+                                double* log_probability);
+
+/* NeedleModel.generate at temperature 0 (model/model.ts:88-153) from token
+ * ids: reset(max(count, min(model max_length, count + max_new)), sink), prefill
+ * the prompt, then up to max_new greedy tokens, each the argmax of the last
+ * logits with its logSoftmaxAt, stepping the model with every token but the
+ * last; stops before an `eos` id (pass UINT32_MAX for none).  Every step after
+ * the prompt runs as a replay of one HIP graph whose kernels read the token
+ * and position from device memory, so the host issues no per-token copies
+ * or synchronisation.  Writes *generated ids and log-probabilities. */
+nd_status nd_needle_generate(nd_ctx* ctx, nd_needle* model, const uint32_t* prompt,
+                             uint32_t count, uint32_t max_new, uint32_t sink, uint32_t eos,
+                             uint32_t* ids, double* log_probabilities, uint32_t* generated);
+
 #ifdef __cplusplus
 }
 #endif

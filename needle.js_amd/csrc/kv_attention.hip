@@ -169,11 +169,15 @@ __device__ __forceinline__ void unpack(const Tile<F32>& tl, int k, bool is_v, fl
 // Scores: (q . k_codes) * k_scale / sqrt(64); softmax; out = sum w * v_codes *
 // v_scale -- NeedleRuntime.#attention (model/runtime.ts:719-786) with
 // softmaxInPlace (model/math.ts:46-60), evaluated in fp32.
+// Output gate of gated attention (model/runtime.ts:503-507): sigmoid(g).
+__device__ __forceinline__ float gate_factor(float g) { return 1.f / (1.f + __expf(-g)); }
+
 template <int REP, bool F32>
 __global__ __launch_bounds__(256) void attention_kernel(
     const void* __restrict__ Kc, const void* __restrict__ Vc, const float* __restrict__ Ks,
     const float* __restrict__ Vs, const float* __restrict__ Q, float* __restrict__ out,
-    float* __restrict__ part_acc, float* __restrict__ part_ml, uint32_t layer, uint32_t kv_heads,
+    const float* __restrict__ gate, float* __restrict__ part_acc, float* __restrict__ part_ml,
+    uint32_t layer, uint32_t kv_heads,
     uint32_t alloc, uint32_t sink, uint32_t window, Visible vis,
     const uint32_t* __restrict__ positions, uint32_t seq_kv_heads, uint32_t kv_stride_z,
     uint32_t chunk_positions, uint32_t max_chunks, float score_scale) {
@@ -314,7 +318,9 @@ __global__ __launch_bounds__(256) void attention_kernel(
     }
     const uint32_t qh = kvh_local * REP + h;
     if (nchunks == 1) {
-      out[(size_t)qh * kHeadDim + dim] = A / L;
+      float r = A / L;
+      if (gate) r *= gate_factor(gate[((size_t)z * hq + qh) * kHeadDim + dim]);
+      out[(size_t)qh * kHeadDim + dim] = r;
     } else {
       const size_t pi = ((size_t)z * hq + qh) * max_chunks + chunk;
       part_acc[pi * kHeadDim + dim] = A;
@@ -331,7 +337,7 @@ __global__ __launch_bounds__(256) void attention_kernel(
 // attention_kernel and are skipped.
 __global__ __launch_bounds__(64) void attention_merge_kernel(
     const float* __restrict__ part_acc, const float* __restrict__ part_ml,
-    float* __restrict__ out, uint32_t hq, uint32_t sink, uint32_t window, Visible vis,
+    float* __restrict__ out, const float* __restrict__ gate, uint32_t hq, uint32_t sink, uint32_t window, Visible vis,
     const uint32_t* __restrict__ positions, uint32_t alloc, uint32_t chunk_positions,
     uint32_t max_chunks) {
   const uint32_t qh = blockIdx.x, z = blockIdx.y, dim = threadIdx.x;
@@ -352,7 +358,10 @@ __global__ __launch_bounds__(64) void attention_merge_kernel(
     total = fmaf(w, part_ml[(base + c) * 2 + 1], total);
     acc = fmaf(w, part_acc[(base + c) * kHeadDim + dim], acc);
   }
-  out[((size_t)z * hq + qh) * kHeadDim + dim] = acc / total;
+  const size_t o = ((size_t)z * hq + qh) * kHeadDim + dim;
+  float r = acc / total;
+  if (gate) r *= gate_factor(gate[o]);
+  out[o] = r;
 }
 
 // Positions per chunk: the whole visible range when the (sequence, kv head)
@@ -370,6 +379,7 @@ struct AttnLaunch {
   uint32_t layer;
   const float* q;
   float* out;
+  const float* gate;           // optional: out *= sigmoid(gate), laid out like out
   float* partials;
   Visible vis;                 // used when positions == nullptr
   const uint32_t* positions;   // per-sequence query positions, or nullptr
@@ -389,13 +399,13 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
   float* part_ml = a.partials + (size_t)a.batch * hq * max_chunks * kHeadDim;
   hipLaunchKernelGGL((attention_kernel<REP, F32>), dim3(max_chunks, a.seq_kv_heads, a.batch),
                      dim3(64 * kWaves), 0, s, a.kv->k, a.kv->v, a.kv->ks, a.kv->vs, a.q, a.out,
-                     part_acc, part_ml, a.layer, a.kv->kv_heads, a.kv->alloc, a.kv->sink,
+                     a.gate, part_acc, part_ml, a.layer, a.kv->kv_heads, a.kv->alloc, a.kv->sink,
                      a.kv->window, a.vis, a.positions, a.seq_kv_heads, a.kv_stride_z, cp,
                      max_chunks, 0.125f);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || max_chunks == 1) return e;
   hipLaunchKernelGGL(attention_merge_kernel, dim3(hq, a.batch), dim3(64), 0, s, part_acc,
-                     part_ml, a.out, hq, a.kv->sink, a.kv->window, a.vis, a.positions,
+                     part_ml, a.out, a.gate, hq, a.kv->sink, a.kv->window, a.vis, a.positions,
                      a.kv->alloc, cp, max_chunks);
   return hipGetLastError();
 }
@@ -497,6 +507,28 @@ hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint
   a.kv_stride_z = kv_stride_z;
   a.rep = rep;
   a.batch = batch;
+  a.max_count = nv.count;
+  return kv->mode == ND_KV_FLOAT32 ? launch_rep<true>(a, s) : launch_rep<false>(a, s);
+}
+
+hipError_t nd_launch_attention_gated(const nd_kv* kv, uint32_t layer, const uint32_t* position,
+                                     uint32_t max_position, const float* q, uint32_t q_heads,
+                                     const float* gate, float* out, float* partials,
+                                     hipStream_t s) {
+  const nd_visible nv = nd_kv_visible(kv, max_position);
+  AttnLaunch a{};
+  a.kv = kv;
+  a.layer = layer;
+  a.q = q;
+  a.out = out;
+  a.gate = gate;
+  a.partials = partials;
+  a.vis = Visible{nv.prefix, nv.recent_low, nv.count};
+  a.positions = position;
+  a.seq_kv_heads = kv->kv_heads;
+  a.kv_stride_z = 0;
+  a.rep = q_heads / kv->kv_heads;
+  a.batch = 1;
   a.max_count = nv.count;
   return kv->mode == ND_KV_FLOAT32 ? launch_rep<true>(a, s) : launch_rep<false>(a, s);
 }

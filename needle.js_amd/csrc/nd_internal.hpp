@@ -100,5 +100,12 @@ hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint
                                      uint32_t batch, uint32_t seq_kv_heads, uint32_t kv_stride_z,
                                      uint32_t rep, uint32_t max_position, const float* q,
                                      float* out, float* partials, hipStream_t s);
+// One query row whose position is read from device memory (*position <=
+// max_position); out = attention * sigmoid(gate) elementwise when gate is set
+// (gated attention, model/runtime.ts:503-505).
+hipError_t nd_launch_attention_gated(const nd_kv* kv, uint32_t layer, const uint32_t* position,
+                                     uint32_t max_position, const float* q, uint32_t q_heads,
+                                     const float* gate, float* out, float* partials,
+                                     hipStream_t s);
 size_t nd_attention_batch_partial_floats(uint32_t batch, uint32_t seq_kv_heads, uint32_t rep,
                                          uint32_t max_count);

@@ -9,9 +9,17 @@ raises NeedleError("BACKEND_UNAVAILABLE").
 from .backend import HipBackend, Int8Matrix, MatrixRowRange, MatvecRequest
 from .errors import NeedleError, invariant
 from .kv import HipKvCache
+from .needle2 import Needle2Geometry, Needle2Weights
+from .runtime import GenerationResult, HipNeedleSession, NeedleModel, NeedleRuntime
 
 __all__ = [
+    "GenerationResult",
     "HipBackend",
+    "HipNeedleSession",
+    "Needle2Geometry",
+    "Needle2Weights",
+    "NeedleModel",
+    "NeedleRuntime",
     "HipKvCache",
     "Int8Matrix",
     "MatrixRowRange",

@@ -174,11 +174,13 @@ class HipBackend:
             return output
         return result
 
-    def create_resident_session(self):
-        from .session import HipResidentSession
+    def create_resident_session(self, weights):
+        """createResidentSession (backends/backend.ts:82-110): Needle 2
+        weights resident in HBM with one runtime state."""
+        from .runtime import HipNeedleSession
 
         self._alive()
-        return HipResidentSession(self)
+        return HipNeedleSession(self, weights)
 
     def dispose(self) -> None:
         if self._disposed:

@@ -95,6 +95,15 @@ SIGNATURES = {
     "nd_prefill_set_tokens": (I32, [P, P, P, U32, U32]),
     "nd_prefill_run_d": (I32, [P, P, P, P]),
     "nd_prefill_logits": (I32, [P, P, P]),
+    "nd_needle_create": (I32, [P, P, PP]),
+    "nd_needle_free": (I32, [P, P]),
+    "nd_needle_reset": (I32, [P, P, U32, U32]),
+    "nd_needle_kv": (P, [P]),
+    "nd_needle_position": (U32, [P]),
+    "nd_needle_step": (I32, [P, P, U32, P]),
+    "nd_needle_prefill": (I32, [P, P, P, U32, P]),
+    "nd_needle_step_select": (I32, [P, P, U32, P, U32, P, P]),
+    "nd_needle_generate": (I32, [P, P, P, U32, U32, U32, U32, P, P, P]),
 }
 
 
@@ -108,6 +117,26 @@ class DecoderDesc(C.Structure):
         ("wq", PP), ("wk", PP), ("wv", PP), ("wo", PP), ("wup", PP), ("wdown", PP),
         ("attn_norm", P), ("ffn_norm", P), ("q_norm", P), ("k_norm", P), ("final_norm", P),
     ]
+
+
+class NeedleDesc(C.Structure):
+    """nd_needle_desc of include/needle_hip.h."""
+
+    _fields_ = [
+        ("vocab", U32), ("dim", U32), ("heads", U32), ("kv_heads", U32), ("layers", U32),
+        ("head_dim", U32), ("max_length", U32), ("hadamard", U32), ("lanes", U32),
+        ("kv_window", U32), ("engram_slots", U32), ("engram_sub", U32), ("engram_tables", U32),
+        ("engram_taps", U32), ("n_orders", U32), ("orders", U32 * 4), ("n_sites", U32),
+        ("sites", U32 * 4), ("rope_theta", C.c_float),
+        ("embedding", P), ("wq", PP), ("wk", PP), ("wv", PP), ("wgate", PP), ("wo", PP),
+        ("phi_pre", P), ("phi_post", P), ("phi_res", P),
+        ("eg_tables", PP), ("eg_key", PP), ("eg_value", PP),
+        ("norm_input", P), ("query_norm", P), ("key_norm", P), ("post_attn_norm", P),
+        ("pre_hadamard_norm", P), ("d1", P), ("d2", P), ("d3", P), ("attention_gate", P),
+        ("a_pre", P), ("a_post", P), ("a_res", P), ("b_pre", P), ("b_post", P), ("b_res", P),
+        ("eg_taps", P), ("final_norm", P),
+    ]
+
 
 _LIB: C.CDLL | None = None
 

@@ -18,7 +18,7 @@ HEADER = ROOT / "include" / "needle_hip.h"
 
 def declared():
     text = HEADER.read_text()
-    return re.findall(r"^(?:nd_status|const char\*|void\*|nd_kv\*)\s+(nd_\w+)\(", text, re.M)
+    return re.findall(r"^(?:nd_status|const char\*|void\*|nd_kv\*|uint32_t)\s+(nd_\w+)\(", text, re.M)
 
 
 def test_header_declarations_are_bound_and_exported():

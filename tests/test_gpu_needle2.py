@@ -1,0 +1,189 @@
+"""GPU parity of the Needle 2 runtime (nd_needle_*) against the oracle's
+NeedleRuntime.step restatement, through the C ABI.
+
+Bars: logits within 1e-3 relative (normwise: one K/V code that rounds the
+other way at a boundary moves later outputs by ~1e-4 relative), appended
+KV codes within one code and mostly identical, greedy token sequences and
+selected ids identical, log-probabilities within 1e-3.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from needle_hip import NeedleError, NeedleModel, synth
+from needle_hip.needle2 import Needle2Geometry, Needle2Weights
+
+pytestmark = pytest.mark.gpu
+
+# Every engram site, lane, GQA group and a window that wraps; hadamard > dim
+# exercises the zero-padded transform.
+SMALL = Needle2Geometry(vocab=512, dim=128, heads=4, kv_heads=2, layers=3, head_dim=64,
+                        max_length=48, hadamard=256, lanes=4, engram_slots=64, engram_sub=128,
+                        engram_tables=4, engram_taps=4, orders=(2, 3), sites=(0, 2), kv_window=8)
+
+
+def say(*args):
+    print("[case]", *args, file=sys.stderr, flush=True)
+
+
+def close(got, want, what):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert err.max() <= 1e-3 * np.abs(want).max(), (what, float(err.max()))
+
+
+@pytest.fixture(scope="module")
+def small(hip):
+    w = Needle2Weights(SMALL, 31)
+    model = NeedleModel(hip, w)
+    yield w, model
+    model.dispose()
+
+
+@pytest.mark.parametrize("sink", [0, 3])
+def test_step_logits_and_kv_match_oracle(small, sink):
+    w, model = small
+    say("needle2 step sink", sink)
+    rt = model.create_runtime()
+    rt.reset(SMALL.max_length, sink)
+    ref = oracle.Needle2(w).runtime(SMALL.max_length, sink)
+    tokens = synth.Stream(5, f"n2tok{sink}").integers(30, 0, SMALL.vocab - 1)
+    tokens[7:10] = tokens[3:6]  # repeated n-grams hit the same engram rows
+    for i, t in enumerate(tokens):
+        want = ref.step(int(t))
+        got = rt.step(int(t))
+        close(got, want, (sink, i))
+        assert rt.position == i + 1
+    for layer in (0, SMALL.layers - 1):
+        for h in range(SMALL.kv_heads):
+            gk, gv, gks, gvs = model.session.kv_read(layer, h)
+            rk, rv, rks, rvs = ref.kv_read(layer, h)
+            assert gk.shape == rk.shape == (sink + SMALL.kv_window, 64)
+            for g, r in ((gk, rk), (gv, rv)):
+                d = np.abs(g.astype(int) - r.astype(int))
+                assert d.max() <= 1 and (d == 0).mean() > 0.95
+            for g, r in ((gks, rks), (gvs, rvs)):
+                np.testing.assert_allclose(g, r, rtol=1e-3)
+
+
+def test_prefill_and_step_selected(small):
+    w, model = small
+    say("needle2 prefill + step_selected")
+    rt = model.create_runtime()
+    rt.reset(40, 2)
+    ref = oracle.Needle2(w).runtime(40, 2)
+    prompt = synth.Stream(6, "n2prompt").integers(20, 0, SMALL.vocab - 1)
+    got = rt.prefill(prompt)
+    for t in prompt:
+        want = ref.step(int(t))
+    close(got, want, "prefill")
+    allowed = np.unique(synth.Stream(7, "n2allowed").integers(60, 0, SMALL.vocab - 1))
+    tok = int(prompt[-1])
+    for i in range(6):
+        gid, glp = rt.step_selected(tok, allowed if i % 2 else None)
+        logits = ref.step(tok)
+        rid, rlp = oracle.select(logits, allowed if i % 2 else None)
+        assert gid == rid, i
+        assert abs(glp - rlp) <= 1e-3 * max(1.0, abs(rlp)), i
+        tok = gid
+
+
+def test_generate_matches_stepwise_oracle(small):
+    w, model = small
+    say("needle2 generate small")
+    prompt = synth.Stream(8, "n2gen").integers(16, 3, SMALL.vocab - 1)
+    res = model.generate(prompt, max_new_tokens=20, sink_tokens=1, eos=None)
+    ref = oracle.Needle2(w).runtime(len(prompt) + 20, 1)
+    for t in prompt:
+        logits = ref.step(int(t))
+    ids, lps = [], []
+    for k in range(20):
+        tok = oracle.argmax(logits)
+        ids.append(tok)
+        lps.append(oracle.log_softmax_at(logits, tok))
+        if k + 1 < 20:
+            logits = ref.step(tok)
+    assert res.token_ids == ids
+    np.testing.assert_allclose(res.token_log_probabilities, lps, rtol=1e-3, atol=1e-3)
+    assert res.finish_reason == "length" and res.generated_tokens == 20
+    # Graph replays and direct launches give the same sequence.
+    rt = model.create_runtime()
+    rt.reset(len(prompt) + 20, 1)
+    logits = rt.prefill(prompt)
+    assert int(np.argmax(logits)) == ids[0]
+    tok = ids[0]
+    for k in range(1, 6):
+        tok, _ = rt.step_selected(tok)
+        assert tok == ids[k]
+
+
+def test_generate_stops_before_eos_and_at_limit(small):
+    w, model = small
+    say("needle2 generate eos/limit")
+    prompt = synth.Stream(9, "n2eos").integers(10, 3, SMALL.vocab - 1)
+    full = model.generate(prompt, max_new_tokens=12, eos=None)
+    stop = full.token_ids[4]
+    first = full.token_ids.index(stop)
+    cut = model.generate(prompt, max_new_tokens=12, eos=stop)
+    assert cut.token_ids == full.token_ids[:first] and cut.finish_reason == "eos"
+    # The context limit caps the count: 48 - 40 = 8 tokens.
+    long_prompt = synth.Stream(10, "n2lim").integers(40, 3, SMALL.vocab - 1)
+    lim = model.generate(long_prompt, max_new_tokens=30, eos=None)
+    assert lim.generated_tokens == 8
+    with pytest.raises(NeedleError) as e:
+        model.generate(synth.Stream(11, "n2over").integers(48, 3, SMALL.vocab - 1), 4, eos=None)
+    assert e.value.code == "CONTEXT_OVERFLOW"
+
+
+def test_runtime_errors(small):
+    w, model = small
+    say("needle2 errors")
+    rt = model.create_runtime()
+    with pytest.raises(NeedleError) as e:
+        rt.reset(SMALL.max_length + 1)
+    assert e.value.code == "CONTEXT_OVERFLOW"
+    rt.reset(2)
+    with pytest.raises(NeedleError) as e:
+        rt.step(SMALL.vocab)
+    assert e.value.code == "INVALID_CACT"
+    rt.step(1, want_logits=False)
+    rt.step(2, want_logits=False)
+    with pytest.raises(NeedleError) as e:
+        rt.step(3)
+    assert e.value.code == "CONTEXT_OVERFLOW"
+    with pytest.raises(NeedleError) as e:
+        rt.prefill([])
+    assert e.value.code == "INVALID_CACT"
+    rt.reset(5)
+    with pytest.raises(NeedleError) as e:
+        rt.step_selected(4, np.array([1, SMALL.vocab], np.uint32))
+    assert e.value.code == "INVALID_CACT"
+
+
+def test_generate_full_geometry_greedy_identical(hip):
+    """The shipped geometry (27 layers, vocab 8192, window 256): 128 prompt
+    tokens, 64 greedy tokens, identical to the oracle's greedy sequence."""
+    say("needle2 generate full geometry")
+    g = Needle2Geometry()
+    w = Needle2Weights(g, 2026)
+    model = NeedleModel(hip, w)
+    try:
+        prompt = synth.Stream(2026, "needle2.prompt").integers(128, 0, g.vocab - 1)
+        res = model.generate(prompt, max_new_tokens=64, eos=None)
+        ref = oracle.Needle2(w).runtime(128 + 64, 0)
+        for t in prompt[:-1]:
+            ref.step(int(t), want_logits=False)
+        logits = ref.step(int(prompt[-1]))
+        ids, lps = [], []
+        for k in range(64):
+            tok = oracle.argmax(logits)
+            ids.append(tok)
+            lps.append(oracle.log_softmax_at(logits, tok))
+            if k + 1 < 64:
+                logits = ref.step(tok)
+        assert res.token_ids == ids
+        np.testing.assert_allclose(res.token_log_probabilities, lps, rtol=1e-3, atol=1e-3)
+    finally:
+        model.dispose()
