@@ -13,6 +13,11 @@ int8-KV decode attention (8 heads x 64, contexts 512/2048/8192), each with
 its HBM roofline fraction (peak 8 TB/s) and, for reference, the same kernel
 on an Infinity-Cache-resident working set.
 
+`parts.needle2_generate_b1` is Needle 2 at the shipped geometry, batch 1:
+greedy generate of 64 tokens from a 128-token prompt (wall time of the whole
+call, as NeedleModel.generate reports tokensPerSecond), plus decode-only and
+prefill-only figures.
+
 `cpu_baseline` times the oracle (the C restatement of the reference CPU
 path, one thread) on a bounded sample of the same matvec workload.
 """
@@ -284,6 +289,102 @@ def bench_prefill(torch, hip, tokens_n, reps, cpu_seconds):
     return part, cpu
 
 
+def needle2_token_bytes(g, visible):
+    """HBM bytes one Needle 2 token reads: int8 codes + f32 row scales of every
+    matrix it multiplies, the engram rows it gathers and `visible` K/V rows
+    (64 + 64 codes + two f32 scales) per layer and KV head."""
+    qkvg = (2 * g.heads + 2 * g.kv_heads) * 64
+    per_layer = (qkvg * (g.dim + 4) + g.dim * (g.heads * 64 + 4)
+                 + (2 * g.lanes + g.lanes * g.lanes) * (g.lanes * g.dim + 4)
+                 + visible * g.kv_heads * (64 * 2 + 8))
+    cat = g.engram_tables * g.engram_sub
+    engram = len(g.sites) * (2 * g.dim * (cat + 4) + g.engram_tables * (g.engram_sub + 4))
+    return g.layers * per_layer + engram + g.vocab * (g.dim + 4)
+
+
+def bench_needle2(torch, hip, reps, check, cpu_seconds):
+    """Needle 2 at the shipped geometry (27 layers, vocab 8192, KV window
+    256), batch 1: NeedleModel.generate of 64 greedy tokens from a 128-token
+    prompt, tok/s as the reference reports it (generated tokens / wall time
+    of the whole call, prefill included)."""
+    import numpy as np
+
+    import oracle
+    from needle_hip import NeedleModel, synth
+    from needle_hip.needle2 import Needle2Geometry, Needle2Weights
+    from needle_hip.runtime import EOS_TOKEN_ID
+
+    g = Needle2Geometry()
+    weights = Needle2Weights(g, 2026)
+    model = NeedleModel(hip, weights)
+    prompt = synth.Stream(2026, "needle2.prompt").integers(128, 0, g.vocab - 1)
+    new = 64
+    model.generate(prompt, new, eos=EOS_TOKEN_ID)  # captures the step graphs
+    model.generate(prompt, 1, eos=EOS_TOKEN_ID)
+    walls, walls1 = [], []
+    res = None
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        res = model.generate(prompt, new, eos=EOS_TOKEN_ID)
+        walls.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        model.generate(prompt, 1, eos=EOS_TOKEN_ID)
+        walls1.append(time.perf_counter() - t0)
+    wall = float(np.median(walls))
+    wall1 = float(np.median(walls1))
+    n_gen = res.generated_tokens
+    decode_ms = (wall - wall1) * 1e3 / max(1, n_gen - 1)
+    prefill_ms = wall1 * 1e3
+    visible = min(g.kv_window, 128 + n_gen // 2)
+    bytes_tok = needle2_token_bytes(g, visible)
+    part = {"prompt_tokens": 128, "generated_tokens": n_gen, "reps": reps,
+            "wall_ms": wall * 1e3, "tokens_per_s": n_gen / wall,
+            "decode_ms_per_token": decode_ms, "decode_tokens_per_s": 1e3 / decode_ms,
+            "prefill_128_ms": prefill_ms, "prefill_tokens_per_s": 128 / wall1,
+            "bytes_per_token": bytes_tok,
+            "decode_GBps": bytes_tok / (decode_ms * 1e-3) / 1e9,
+            "launches_per_token": 6 * g.layers + 2 + len(g.sites) + 3}
+    part["decode_frac_hbm"] = part["decode_GBps"] / HBM_PEAK_GBS
+    ref = oracle.Needle2(weights)
+    cpu = None
+    if cpu_seconds > 0:
+        rt = ref.runtime(128 + new, 0)
+        t0 = time.perf_counter()
+        n = 0
+        while n < 128 and time.perf_counter() - t0 < cpu_seconds:
+            rt.step(int(prompt[n]), want_logits=n == 127)
+            n += 1
+        el = time.perf_counter() - t0
+        per_step = el / n
+        # generate = 128 prompt steps + (n_gen - 1) decode steps, all the same
+        # per-token graph (the decode steps' logits add one lm-head matvec).
+        cpu_tok_s = n_gen / (per_step * (128 + n_gen - 1))
+        cpu = {"value": cpu_tok_s, "unit": "tok/s", "cores": 1, "kind": "port",
+               "sample": f"oracle NeedleRuntime.step over the first {n} prompt tokens "
+                         f"({el:.1f} s, {per_step * 1e3:.1f} ms/step), scaled to the "
+                         f"{128 + n_gen - 1} steps of the generate call"}
+        part["cpu_tokens_per_s"] = cpu_tok_s
+        part["speedup_vs_cpu"] = part["tokens_per_s"] / cpu_tok_s
+    if check:
+        t0 = time.perf_counter()
+        rt = ref.runtime(128 + new, 0)
+        for t in prompt[:-1]:
+            rt.step(int(t), want_logits=False)
+        logits = rt.step(int(prompt[-1]))
+        ids = []
+        for k in range(new):
+            tok = oracle.argmax(logits)
+            if tok == EOS_TOKEN_ID:
+                break
+            ids.append(tok)
+            if k + 1 < new:
+                logits = rt.step(tok)
+        part["greedy_identical"] = ids == res.token_ids
+        part["check_seconds"] = time.perf_counter() - t0
+    model.dispose()
+    return part, cpu
+
+
 def cpu_baseline_matvec(n, k, g, seconds):
     """The oracle (one thread) on the same matvec workload, timed on this host."""
     import numpy as np
@@ -317,7 +418,9 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--skip-prefill", action="store_true")
-    ap.add_argument("--only", choices=["matvec", "attention", "decode", "prefill"],
+    ap.add_argument("--skip-needle2", action="store_true")
+    ap.add_argument("--needle2-reps", type=int, default=5)
+    ap.add_argument("--only", choices=["matvec", "attention", "decode", "prefill", "needle2"],
                     help="run one part alone and print its JSON (for profiling)")
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--no-check", action="store_true",
@@ -343,6 +446,8 @@ def main():
             part = bench_attention(torch, hip, 8192, 8, args.steps // 2, args.warmup)
         elif args.only == "decode":
             part, _ = bench_constrained_decode(torch, hip, args.decode_steps, 2, False, 1, 0)
+        elif args.only == "needle2":
+            part, _ = bench_needle2(torch, hip, args.needle2_reps, False, 0)
         else:
             part, _ = bench_prefill(torch, hip, 2048, 5, 0)
         print(json.dumps({args.only: part}))
@@ -381,6 +486,16 @@ def main():
         parts["prefill_2048"] = part
         print(f"[bench] prefill 2048 {part['ms']:.2f} ms {part['tokens_per_s']:.0f} tok/s "
               f"{part['effective_TOPS']:.1f} TOPS", file=sys.stderr, flush=True)
+
+    if not args.skip_needle2:
+        part, cpu_n2 = bench_needle2(torch, hip, args.needle2_reps, not args.no_check,
+                                     0 if args.skip_cpu else args.cpu_seconds)
+        if cpu_n2:
+            part["cpu_baseline"] = cpu_n2
+        parts["needle2_generate_b1"] = part
+        print(f"[bench] needle2 generate b1 {part['tokens_per_s']:.0f} tok/s, decode "
+              f"{part['decode_ms_per_token']:.3f} ms/token, greedy_identical="
+              f"{part.get('greedy_identical')}", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.skip_cpu:

@@ -1,0 +1,80 @@
+// Wave64 cross-lane helpers built on DPP moves and readlane, so that a
+// reduction costs a few VALU cycles per step instead of the LDS-crossbar
+// latency of ds_bpermute (__shfl_xor).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace nd {
+
+// DPP controls (GFX9 encoding).
+constexpr int kQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kHalfMirror = 0x141;  // lane i of 8 <- lane 7 - i
+constexpr int kRowMirror = 0x140;   // lane i of 16 <- lane 15 - i
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+template <int CTRL>
+__device__ __forceinline__ double dpp(double v) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_mov_dpp((int)b, CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_mov_dpp((int)(b >> 32), CTRL, 0xF, 0xF, false);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+__device__ __forceinline__ double readlane(double v, int lane) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)b, lane);
+  const int hi = __builtin_amdgcn_readlane((int)(b >> 32), lane);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+__device__ __forceinline__ float readlane(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Sum of each row of 16 lanes, in every lane of the row.
+template <typename T>
+__device__ __forceinline__ T row_sum(T v) {
+  v += dpp<kQuadXor1>(v);
+  v += dpp<kQuadXor2>(v);
+  v += dpp<kHalfMirror>(v);
+  v += dpp<kRowMirror>(v);
+  return v;
+}
+
+// Sum over the wave, the same value in every lane: rows of 16 by DPP, then
+// ((row0 + row1) + row2) + row3.
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+  v = row_sum(v);
+  return ((readlane(v, 0) + readlane(v, 16)) + readlane(v, 32)) + readlane(v, 48);
+}
+
+// JavaScript Math.max of two numbers (NaN if either is NaN).
+__device__ __forceinline__ float js_max(float a, float b) {
+  return (a != a || b != b) ? __builtin_nanf("") : (a > b ? a : b);
+}
+
+// JavaScript Math.max over the wave (NaN wins), in every lane.
+__device__ __forceinline__ float wave_max_js(float v) {
+  v = js_max(v, dpp<kQuadXor1>(v));
+  v = js_max(v, dpp<kQuadXor2>(v));
+  v = js_max(v, dpp<kHalfMirror>(v));
+  v = js_max(v, dpp<kRowMirror>(v));
+  return js_max(js_max(readlane(v, 0), readlane(v, 16)), js_max(readlane(v, 32), readlane(v, 48)));
+}
+
+// Sum over a quad of lanes (4 consecutive), in every lane of the quad.
+template <typename T>
+__device__ __forceinline__ T quad_sum(T v) {
+  v += dpp<kQuadXor1>(v);
+  v += dpp<kQuadXor2>(v);
+  return v;
+}
+
+}  // namespace nd

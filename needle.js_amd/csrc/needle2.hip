@@ -9,24 +9,29 @@
 // So one step's launches form a fixed sequence that is captured once as a
 // HIP graph and replayed per token with no host copies.
 //
-// Per layer the token runs six launches: mhc_pre (one workgroup: lane RMS,
-// the lanes*(2+lanes) phi rows, h-pre mix, engram injection, input norm), the
-// fused Q/K/V/gate matvec, qk norm + RoPE + KV append, attention with the
-// sigmoid(gate) epilogue, the Wo matvec, and mhc_post (one workgroup:
-// sandwich norm, Hadamard MLP, h-post, Sinkhorn routing, lane update).  The
-// one-workgroup kernels keep the reference's float64-with-f32-stores
-// arithmetic, which costs nothing at these sizes.
+// Per layer the token runs four launches: `mix` (one workgroup: the
+// post-attention half of the previous layer -- sandwich norm, Hadamard MLP,
+// h-post, Sinkhorn routing, lane update -- then this layer's pre-attention
+// half -- lane RMS, the lanes*(2+lanes) phi rows, h-pre mix, engram
+// injection, input norm), the Q/K/V/gate matvec with q/k norm + RoPE and the
+// KV append in its epilogue, attention with the sigmoid(gate) epilogue, and
+// the Wo matvec.  The one-workgroup arithmetic keeps the reference's
+// float64-with-f32-stores form except the Sinkhorn iterations (fp32).
 #include <algorithm>
 #include <cmath>
 #include <type_traits>
 #include <vector>
 
 #include "nd_internal.hpp"
+#include "nd_wave.hpp"
 
 namespace {
 
 constexpr uint32_t kHd = 64;
 constexpr int kWg = 1024;
+constexpr int kMixWg = 512;  // mix kernel: dim <= 512 values per thread role
+constexpr int kMixChunks = 6;  // 24 phi rows x 2048 / 16 bytes / kMixWg
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ double sigmoid_d(double v) {
   if (v >= 0) return 1.0 / (1.0 + exp(-v));
@@ -34,29 +39,21 @@ __device__ __forceinline__ double sigmoid_d(double v) {
   return e / (1.0 + e);
 }
 
-// Sum over a workgroup of kWg threads; every thread gets the total.
+// Sum over a workgroup of NT threads; every thread gets the total.
+template <int NT = kWg>
 __device__ __forceinline__ double block_sum_d(double v, double* red) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  v = nd::wave_sum(v);
   __syncthreads();
-  if (lane == 0) red[w] = v;
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   double r = 0.0;
-  for (int i = 0; i < kWg / 64; ++i) r += red[i];
+#pragma unroll
+  for (int i = 0; i < NT / 64; ++i) r += red[i];
   return r;
 }
 
 // JavaScript Math.max over |v| of a wave: NaN wins.
-__device__ __forceinline__ float wave_absmax_js(float v) {
-  v = fabsf(v);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const float w = __shfl_xor(v, o, 64);
-    v = (v != v || w != w) ? __builtin_nanf("") : (v > w ? v : w);
-  }
-  return v;
-}
+__device__ __forceinline__ float wave_absmax_js(float v) { return nd::wave_max_js(fabsf(v)); }
 
 // #kvSlot (model/runtime.ts:659-667).
 __device__ __forceinline__ uint32_t kv_slot(uint32_t p, uint32_t sink, uint32_t window) {
@@ -168,288 +165,453 @@ __global__ void n2_engram_conv_kernel(const uint32_t* __restrict__ st,
   mixed[(size_t)s * d + i] = m;
 }
 
-struct PreArgs {
-  const float* x;           // [lanes][d]
-  const int8_t* phi_pre;    // this layer's rows
-  const float* phi_pre_s;
-  const int8_t* phi_post;
-  const float* phi_post_s;
-  const int8_t* phi_res;
-  const float* phi_res_s;
-  float a_pre;
-  const float* b_pre;       // [lanes]
-  const float* ekey;        // engram key of this layer's site, or null
-  const float* evalue;
-  const float* norm_input;  // [d]
-  float* upd;               // out [d]
-  float* blk;               // out [d]
-  float* ain;               // out [d]
-  float* phi_post_out;      // out [lanes]
-  float* phi_res_out;       // out [lanes*lanes]
-  uint32_t d, lanes, own;
-};
-
-// mHC pre-mix (runtime.ts:385-420), engram injection (runtime.ts:422-438)
-// and the input norm (runtime.ts:441) in one workgroup.
-__global__ __launch_bounds__(kWg) void n2_mhc_pre_kernel(PreArgs a) {
-  __shared__ float nl[2048];
-  __shared__ float xs[2048];
-  __shared__ float phi[24];
-  __shared__ float hpre[4];
-  __shared__ double red[kWg / 64];
-  const uint32_t t = threadIdx.x, D = a.d, L = a.lanes, N = L * D;
-  // rmsUnit over all lanes (math.ts:34-44).
-  double ss = 0.0;
-  for (uint32_t i = t; i < N; i += kWg) {
-    const float v = a.x[i];
-    xs[i] = v;
-    ss += (double)v * (double)v;
+// Walsh-Hadamard transform of H = 64 * VPL values held by one wave (lane l
+// owns values [l * VPL, (l + 1) * VPL)), strides ascending, each butterfly
+// evaluated in float64 and stored as f32 -- fwht (math.ts) value for value.
+template <int VPL>
+__device__ __forceinline__ void fwht_wave(float (&v)[VPL], uint32_t lane) {
+#pragma unroll
+  for (int s = 1; s < VPL; s <<= 1) {
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+      if (!(j & s)) {
+        const double left = v[j], right = v[j | s];
+        v[j] = (float)(left + right);
+        v[j | s] = (float)(left - right);
+      }
   }
-  ss = block_sum_d(ss, red);
-  const double inv = 1.0 / sqrt(ss / N + 1e-6);
-  for (uint32_t i = t; i < N; i += kWg) nl[i] = (float)((double)xs[i] * inv);
-  __syncthreads();
-  // The phi rows (K = lanes * d): one wave per row, float64 dot, f32 store.
-  const uint32_t wave = t >> 6, lane = t & 63, nrows = 2 * L + L * L;
-  for (uint32_t r = wave; r < nrows; r += kWg / 64) {
-    const int8_t* w;
-    float sc;
-    if (r < L) {
-      w = a.phi_pre + (size_t)r * N;
-      sc = a.phi_pre_s[r];
-    } else if (r < 2 * L) {
-      w = a.phi_post + (size_t)(r - L) * N;
-      sc = a.phi_post_s[r - L];
-    } else {
-      w = a.phi_res + (size_t)(r - 2 * L) * N;
-      sc = a.phi_res_s[r - 2 * L];
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const float o = m == 1 ? nd::dpp<nd::kQuadXor1>(v[j])
+                      : m == 2 ? nd::dpp<nd::kQuadXor2>(v[j]) : __shfl_xor(v[j], m, 64);
+      const double mine = v[j], other = o;
+      v[j] = (lane & m) ? (float)(other - mine) : (float)(mine + other);
     }
-    double dot = 0.0;
-    for (uint32_t i = lane * 4; i < N; i += 256) {
-      const char4 c = *reinterpret_cast<const char4*>(w + i);
-      dot += (double)c.x * (double)nl[i] + (double)c.y * (double)nl[i + 1] +
-             (double)c.z * (double)nl[i + 2] + (double)c.w * (double)nl[i + 3];
+  }
+}
+
+// hadamardMlp (math.ts:117-138) on one wave up to the last scaling: FWHT(d1
+// x), SiLU(z / sqrt(H) * d2), FWHT.  hv holds d1 x zero-padded to H on entry
+// and the second transform on exit (the caller applies / sqrt(H) * d3); d2
+// is in LDS.
+template <int VPL>
+__device__ void hadamard_wave(float* hv, const float* d2, uint32_t lane) {
+  constexpr uint32_t H = 64 * VPL;
+  const double inv_root = 1.0 / sqrt((double)H);
+  float v[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) v[j] = hv[lane * VPL + j];
+  fwht_wave<VPL>(v, lane);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const double z = (double)v[j] * inv_root * (double)d2[lane * VPL + j];
+    v[j] = (float)(z * sigmoid_d(z));
+  }
+  fwht_wave<VPL>(v, lane);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) hv[lane * VPL + j] = v[j];
+}
+
+// sinkhorn (math.ts:62-92) of an L x L matrix (L <= 4) on the lanes of a
+// quad: lane q holds row q.  Each log-space row (column) step r -= logsumexp
+// is a division of exp(r) by its row (column) sum, so the twenty iterations
+// run on p = exp(r - max) in fp32 with reciprocals; a spread above 80
+// between the largest and smallest logit (where exp would underflow in fp32)
+// takes the float64 log-space form.  A NaN logit makes every entry NaN, as
+// the reference's Math.max does.  Reads the logits from and writes exp(r)
+// to io[q * L + c].
+__device__ void sinkhorn_quad(float* io, uint32_t L, uint32_t lane) {
+  const uint32_t q = lane & 3;
+  const bool row_ok = q < L;
+  float v[4];
+  float mx = -INFINITY, mn = INFINITY;
+  bool nan = false;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const bool ok = row_ok && (uint32_t)c < L;
+    v[c] = ok ? io[q * L + c] : 0.f;
+    if (ok) {
+      nan = nan || v[c] != v[c];
+      mx = fmaxf(mx, v[c]);
+      mn = fminf(mn, v[c]);
+    }
+  }
+  mx = fmaxf(mx, nd::dpp<nd::kQuadXor1>(mx));
+  mx = fmaxf(mx, nd::dpp<nd::kQuadXor2>(mx));
+  mn = fminf(mn, nd::dpp<nd::kQuadXor1>(mn));
+  mn = fminf(mn, nd::dpp<nd::kQuadXor2>(mn));
+  int any_nan = nan ? 1 : 0;
+  any_nan |= __builtin_amdgcn_mov_dpp(any_nan, nd::kQuadXor1, 0xF, 0xF, false);
+  any_nan |= __builtin_amdgcn_mov_dpp(any_nan, nd::kQuadXor2, 0xF, 0xF, false);
+  float p[4];
+  if (any_nan) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) p[c] = __builtin_nanf("");
+  } else if (mx - mn <= 80.f) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) p[c] = (row_ok && (uint32_t)c < L) ? __expf(v[c] - mx) : 0.f;
+    for (int it = 0; it < 20; ++it) {
+      const float rs = (p[0] + p[1]) + (p[2] + p[3]);
+      const float ri = row_ok ? __builtin_amdgcn_rcpf(rs) : 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) p[c] *= ri;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float cs = nd::quad_sum(p[c]);
+        p[c] *= (uint32_t)c < L ? __builtin_amdgcn_rcpf(cs) : 0.f;
+      }
+    }
+  } else {
+    double r[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r[c] = v[c];
+    for (int it = 0; it < 20; ++it) {
+      double m = -INFINITY, sum = 0.0;
+      for (uint32_t c = 0; c < L; ++c) m = fmax(m, r[c]);
+      for (uint32_t c = 0; c < L; ++c) sum += exp(r[c] - m);
+      const double ls = log(sum) + m;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) r[c] -= row_ok ? ls : 0.0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        double cm = row_ok ? r[c] : -INFINITY;
+        cm = fmax(cm, nd::dpp<nd::kQuadXor1>(cm));
+        cm = fmax(cm, nd::dpp<nd::kQuadXor2>(cm));
+        const double cs = nd::quad_sum(row_ok ? exp(r[c] - cm) : 0.0);
+        r[c] -= log(cs) + cm;
+      }
     }
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);
-    if (lane == 0) phi[r] = (float)((double)sc * dot);
+    for (int c = 0; c < 4; ++c) p[c] = (float)exp(r[c]);
+  }
+  if (lane < 4 && row_ok)
+    for (uint32_t c = 0; c < L; ++c) io[q * L + c] = p[c];
+}
+
+struct MixArgs {
+  float* x;  // [lanes][d]: read, and rewritten when has_post
+  uint32_t d, hdim, lanes;
+  // post-attention half of layer l - 1 (runtime.ts:509-542, #attentionDelta
+  // runtime.ts:585-611)
+  uint32_t has_post, own_post;
+  const float* proj;  // Wo output [d]
+  const float* post_norm;
+  const float* pre_h_norm;
+  const float* d1;
+  const float* d2;
+  const float* d3;
+  float attention_gate, a_post, a_res;
+  const float* b_post;
+  const float* b_res;
+  // pre-attention half of layer l (runtime.ts:385-441)
+  uint32_t has_pre, own_pre;
+  const int8_t* phi_w[3];  // phi_pre, phi_post, phi_res rows of layer l
+  const float* phi_s[3];
+  float a_pre;
+  const float* b_pre;
+  const float* ekey;  // engram key / mixed value of a site at layer l, or null
+  const float* evalue;
+  const float* norm_input;
+  // lane mean + final norm after the last layer (runtime.ts:570-576)
+  uint32_t has_final;
+  const float* final_norm;
+  float* fin;
+  // carried from pre(l) to post(l)
+  float* upd;       // [d]
+  float* blk;       // [d]
+  float* ain;       // [d]
+  float* phi_post;  // [lanes]
+  float* phi_res;   // [lanes * lanes]
+};
+
+// The one-workgroup part between two layers: post(l - 1), then pre(l) (or
+// the final norm).  Every global operand is loaded at entry -- the phi
+// weights of layer l, the lanes, the per-layer vectors -- so the kernel pays
+// one memory latency; after that it runs from registers and LDS.  The
+// Hadamard MLP (wave 0) and the Sinkhorn routing (wave 1) run side by side.
+__global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
+  __shared__ float nl[2048];
+  __shared__ float hv[512];
+  __shared__ float d2s[512];
+  __shared__ double part[kMixChunks * kMixWg];
+  __shared__ double red[kMixWg / 64];
+  __shared__ float phi[24], phi_sc[24], hpre[4], hpost[4], routing[16];
+  const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const uint32_t D = a.d, L = a.lanes, N = L * D, H = a.hdim;
+  const uint32_t nrows = 2 * L + L * L, cpr = N / 16, chunks = nrows * cpr;
+  const bool col = t < D;
+  // ---- loads
+  uint4 pw[kMixChunks];
+  if (a.has_pre) {
+#pragma unroll
+    for (int i = 0; i < kMixChunks; ++i) {
+      const uint32_t c = t + i * kMixWg;
+      if (c < chunks) {
+        const uint32_t r = c / cpr, m = r < L ? 0 : (r < 2 * L ? 1 : 2);
+        const uint32_t rr = m == 0 ? r : (m == 1 ? r - L : r - 2 * L);
+        pw[i] = *reinterpret_cast<const uint4*>(a.phi_w[m] + (size_t)rr * N + (c % cpr) * 16);
+      }
+    }
+  }
+  float xl[4];
+#pragma unroll
+  for (int l = 0; l < 4; ++l) xl[l] = (col && (uint32_t)l < L) ? a.x[(size_t)l * D + t] : 0.f;
+  float p = 0.f, blk = 0.f, upd = 0.f, post_norm = 0.f, pre_h = 0.f, d1 = 0.f, d3 = 0.f;
+  if (a.has_post) {
+    if (col) {
+      p = a.proj[t];
+      blk = a.blk[t];
+      upd = a.upd[t];
+      post_norm = a.post_norm[t];
+      pre_h = a.pre_h_norm[t];
+      d1 = a.d1[t];
+      d3 = a.d3[t];
+    }
+    if (t < H) d2s[t] = a.d2[t];
+    if (t < L * L)
+      routing[t] = (float)((double)a.a_res * (double)a.phi_res[t] + (double)a.b_res[t]);
+    if (t < L) {
+      const double off = t == a.own_post ? 0.0 : -4.0;
+      hpost[t] = (float)(2.0 * sigmoid_d((double)a.a_post * (double)a.phi_post[t] +
+                                         (double)a.b_post[t] + off));
+    }
+  }
+  float norm_in = 0.f, ekey = 0.f, evalue = 0.f, b_pre = 0.f, fnorm = 0.f;
+  if (a.has_pre) {
+    if (col) norm_in = a.norm_input[t];
+    if (col && a.ekey) {
+      ekey = a.ekey[t];
+      evalue = a.evalue[t];
+    }
+    if (t < L) b_pre = a.b_pre[t];
+    if (t < nrows) {
+      const uint32_t m = t < L ? 0 : (t < 2 * L ? 1 : 2);
+      phi_sc[t] = a.phi_s[m][m == 0 ? t : (m == 1 ? t - L : t - 2 * L)];
+    }
+  }
+  if (a.has_final && col) fnorm = a.final_norm[t];
+
+  // ---- post(l - 1)
+  if (a.has_post) {
+    const double sp = block_sum_d<kMixWg>(col ? (double)p * p : 0.0, red);
+    const double ip = 1.0 / sqrt(sp / D + 1e-6);
+    const double ascale = sigmoid_d((double)a.attention_gate);
+    float after = 0.f;
+    if (col) {
+      const float np = (float)((1.0 + (double)post_norm) * (double)p * ip);
+      after = (float)((double)blk + ascale * (double)np);
+    }
+    const double sa = block_sum_d<kMixWg>(col ? (double)after * after : 0.0, red);
+    const double ia = 1.0 / sqrt(sa / D + 1e-6);
+    if (col) {
+      const float pre = (float)((1.0 + (double)pre_h) * (double)after * ia);
+      hv[t] = (float)((double)pre * (double)d1);
+    }
+    for (uint32_t i = D + t; i < H; i += kMixWg) hv[i] = 0.f;
+    __syncthreads();
+    if (wave == 0) {
+      switch (H / 64) {
+        case 2: hadamard_wave<2>(hv, d2s, lane); break;
+        case 4: hadamard_wave<4>(hv, d2s, lane); break;
+        default: hadamard_wave<8>(hv, d2s, lane); break;
+      }
+    } else if (wave == 1) {
+      sinkhorn_quad(routing, L, lane);
+    }
+    __syncthreads();
+    if (col) {
+      const float mlp = (float)((double)hv[t] * (1.0 / sqrt((double)H)) * (double)d3);
+      const float delta = (float)((double)after + (double)mlp - (double)upd);
+      float nx[4];
+#pragma unroll
+      for (int l = 0; l < 4; ++l) {
+        if ((uint32_t)l >= L) break;
+        double sum = 0.0;
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2)
+          if ((uint32_t)s2 < L) sum += (double)routing[l * L + s2] * (double)xl[s2];
+        nx[l] = (float)(sum + (double)hpost[l] * (double)delta);
+      }
+#pragma unroll
+      for (int l = 0; l < 4; ++l)
+        if ((uint32_t)l < L) {
+          xl[l] = nx[l];
+          a.x[(size_t)l * D + t] = nx[l];
+        }
+    }
+  }
+  if (a.has_final) {
+    float m = 0.f;
+    if (col) {
+      double sum = 0.0;
+#pragma unroll
+      for (int l = 0; l < 4; ++l)
+        if ((uint32_t)l < L) sum += xl[l];
+      m = (float)(sum / L);
+    }
+    const double ss = block_sum_d<kMixWg>(col ? (double)m * m : 0.0, red);
+    const double inv = 1.0 / sqrt(ss / D + 1e-6);
+    if (col) a.fin[t] = (float)((1.0 + (double)fnorm) * (double)m * inv);
+  }
+  if (!a.has_pre) return;
+
+  // ---- pre(l): rmsUnit over all lanes (math.ts:34-44), then the phi rows.
+  double ss = 0.0;
+#pragma unroll
+  for (int l = 0; l < 4; ++l)
+    if ((uint32_t)l < L) ss += (double)xl[l] * (double)xl[l];
+  ss = block_sum_d<kMixWg>(col ? ss : 0.0, red);
+  const double inv = 1.0 / sqrt(ss / N + 1e-6);
+  if (col) {
+#pragma unroll
+    for (int l = 0; l < 4; ++l)
+      if ((uint32_t)l < L) nl[l * D + t] = (float)((double)xl[l] * inv);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kMixChunks; ++i) {
+    const uint32_t c = t + i * kMixWg;
+    if (c < chunks) {
+      const float4* xv = reinterpret_cast<const float4*>(nl + (c % cpr) * 16);
+      const uint32_t words[4] = {pw[i].x, pw[i].y, pw[i].z, pw[i].w};
+      double dot = 0.0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 f = xv[j];
+        const uint32_t wj = words[j];
+        dot += (double)(int8_t)(wj & 0xff) * (double)f.x;
+        dot += (double)(int8_t)((wj >> 8) & 0xff) * (double)f.y;
+        dot += (double)(int8_t)((wj >> 16) & 0xff) * (double)f.z;
+        dot += (double)(int8_t)(wj >> 24) * (double)f.w;
+      }
+      part[c] = dot;
+    }
+  }
+  __syncthreads();
+  for (uint32_t r = wave; r < nrows; r += kMixWg / 64) {
+    double sum = 0.0;
+    for (uint32_t i = lane; i < cpr; i += 64) sum += part[r * cpr + i];
+    sum = nd::wave_sum(sum);
+    if (lane == 0) phi[r] = (float)((double)phi_sc[r] * sum);
   }
   __syncthreads();
   if (t < L) {
-    const double off = t == a.own ? 4.0 : -4.0;
-    hpre[t] = (float)sigmoid_d((double)a.a_pre * (double)phi[t] + (double)a.b_pre[t] + off);
-    a.phi_post_out[t] = phi[L + t];
+    const double off = t == a.own_pre ? 4.0 : -4.0;
+    hpre[t] = (float)sigmoid_d((double)a.a_pre * (double)phi[t] + (double)b_pre + off);
+    a.phi_post[t] = phi[L + t];
   }
-  if (t < L * L) a.phi_res_out[t] = phi[2 * L + t];
+  if (t < L * L) a.phi_res[t] = phi[2 * L + t];
   __syncthreads();
   // updateInput = sum_lane hPre[lane] * x[lane].
   float u = 0.f;
-  if (t < D) {
+  if (col) {
     double sum = 0.0;
-    for (uint32_t l = 0; l < L; ++l) sum += (double)hpre[l] * (double)xs[l * D + t];
+#pragma unroll
+    for (int l = 0; l < 4; ++l)
+      if ((uint32_t)l < L) sum += (double)hpre[l] * (double)xl[l];
     u = (float)sum;
     a.upd[t] = u;
   }
   float b = u;
   if (a.ekey) {
     // alpha = sigmoid(rmsUnit(u) . rmsUnit(key) / sqrt(d)); block = u + alpha * value.
-    const float kk = t < D ? a.ekey[t] : 0.f;
-    const double su = block_sum_d(t < D ? (double)u * u : 0.0, red);
-    const double sk = block_sum_d(t < D ? (double)kk * kk : 0.0, red);
+    const double su = block_sum_d<kMixWg>(col ? (double)u * u : 0.0, red);
+    const double sk = block_sum_d<kMixWg>(col ? (double)ekey * ekey : 0.0, red);
     const double iu = 1.0 / sqrt(su / D + 1e-6), ik = 1.0 / sqrt(sk / D + 1e-6);
-    const float nu = (float)((double)u * iu), nk = (float)((double)kk * ik);
-    const double dot = block_sum_d(t < D ? (double)nu * (double)nk : 0.0, red);
+    const float nu = (float)((double)u * iu), nk = (float)((double)ekey * ik);
+    const double dot = block_sum_d<kMixWg>(col ? (double)nu * (double)nk : 0.0, red);
     const double alpha = sigmoid_d(dot / sqrt((double)D));
-    if (t < D) b = (float)((double)u + alpha * (double)a.evalue[t]);
+    if (col) b = (float)((double)u + alpha * (double)evalue);
   }
-  if (t < D) a.blk[t] = b;
+  if (col) a.blk[t] = b;
   // attentionInput = rmsNorm(block, normInput) (math.ts:16-32).
-  const double sb = block_sum_d(t < D ? (double)b * b : 0.0, red);
+  const double sb = block_sum_d<kMixWg>(col ? (double)b * b : 0.0, red);
   const double ib = 1.0 / sqrt(sb / D + 1e-6);
-  if (t < D) a.ain[t] = (float)((1.0 + (double)a.norm_input[t]) * (double)b * ib);
+  if (col) a.ain[t] = (float)((1.0 + (double)norm_in) * (double)b * ib);
 }
 
-// Query/key head norm + RoPE and the KV append at the ring slot
-// (runtime.ts:471-501, #storeKV runtime.ts:679-717).  One wave per head, lane
-// = dimension.  qkvg = [q (H*64) | k (Hkv*64) | v (Hkv*64) | gate (H*64)].
-__global__ __launch_bounds__(64) void n2_qk_rope_store_kernel(
-    const uint32_t* __restrict__ st, const float* __restrict__ qkvg, uint32_t heads,
-    uint32_t kv_heads, const float* __restrict__ q_norm, const float* __restrict__ k_norm,
-    const double* __restrict__ inv_freq, float* __restrict__ q_out, int8_t* __restrict__ Kc,
-    int8_t* __restrict__ Vc, float* __restrict__ Ks, float* __restrict__ Vs, uint32_t layer,
-    uint32_t alloc, uint32_t sink, uint32_t window) {
-  const uint32_t slot_h = blockIdx.x, lane = threadIdx.x;
-  const uint32_t pos = st[1];
-  const bool is_q = slot_h < heads;
-  const uint32_t h = is_q ? slot_h : slot_h - heads;
-  const float* src = qkvg + (is_q ? h * kHd : heads * kHd + h * kHd);
-  const float* scale = is_q ? q_norm : k_norm;
-  const double x = src[lane];
-  double ss = x * x;
+// The fused Q/K/V/gate projection of one layer (runtime.ts:465-470) with the
+// per-head norm + RoPE of q and k (runtime.ts:471-500) and #storeKV
+// (runtime.ts:679-717) in the epilogue.  Workgroup b computes rows [64 b,
+// 64 b + 64) of wqkvg = [q (H*64) | k (Hkv*64) | v (Hkv*64) | gate (H*64)]:
+// four threads per row, fp32 accumulation of int8 x fp32 like the matvec,
+// times the row scale.  q heads go to q_out, k and v heads are quantized into
+// the cache at the ring slot of the step's position, gate heads go to
+// gate_out as raw projections.
+__global__ __launch_bounds__(256) void n2_qkv_kernel(
+    const int8_t* __restrict__ W, const float* __restrict__ S, const float* __restrict__ x,
+    uint32_t d, uint32_t heads, uint32_t kv_heads, const uint32_t* __restrict__ st,
+    const float* __restrict__ q_norm, const float* __restrict__ k_norm,
+    const double* __restrict__ inv_freq, float* __restrict__ q_out, float* __restrict__ gate_out,
+    int8_t* __restrict__ Kc, int8_t* __restrict__ Vc, float* __restrict__ Ks,
+    float* __restrict__ Vs, uint32_t layer, uint32_t alloc, uint32_t sink, uint32_t window) {
+  __shared__ float xs[512];
+  __shared__ float rows[64];
+  const uint32_t b = blockIdx.x, t = threadIdx.x;
+  // Loads first: this thread's weight bytes, the row scale, the epilogue
+  // operands, then x.
+  const uint32_t r = t >> 2, q = t & 3, seg = d / 4;
+  const size_t row = (size_t)b * kHd + r;
+  const int8_t* w = W + row * d + q * seg;
+  i32x4 wv[8];
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-  const double inv = 1.0 / sqrt(ss / kHd + 1e-6);
-  const float normed = (float)((1.0 + (double)scale[lane]) * x * inv);
-  double sn, cs;
-  sincos((double)pos * inv_freq[lane & 31], &sn, &cs);
-  const double mine = normed;
-  const double other = __shfl_xor(mine, 32, 64);
-  const float rot = lane < 32 ? (float)(mine * cs - other * sn) : (float)(mine * cs + other * sn);
-  if (is_q) {
-    q_out[h * kHd + lane] = rot;
+  for (int k = 0; k < 8; ++k)
+    if ((uint32_t)k * 16 < seg) wv[k] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(w + k * 16));
+  const float srow = S[row];
+  const uint32_t pos = st[1];
+  const uint32_t lane = t & 63;
+  const float nscale = b < heads ? q_norm[lane] : k_norm[lane];
+  const double invf = inv_freq[lane & 31];
+  for (uint32_t i = t; i < d; i += 256) xs[i] = x[i];
+  __syncthreads();
+  const float* xv = xs + q * seg;
+  float acc = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if ((uint32_t)k * 16 >= seg) break;
+    int8_t cb[16];
+    __builtin_memcpy(cb, &wv[k], 16);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc = fmaf((float)cb[j], xv[k * 16 + j], acc);
+  }
+  acc = nd::quad_sum(acc);
+  if (q == 0) rows[r] = acc * srow;
+  __syncthreads();
+  if (t >= 64) return;
+  const float val = rows[lane];
+  const uint32_t nq = heads, nk = kv_heads;
+  if (b >= nq + 2 * nk) {  // gate head
+    gate_out[(size_t)(b - nq - 2 * nk) * kHd + lane] = val;
     return;
   }
+  const bool is_v = b >= nq + nk;
+  float out = val;
+  if (!is_v) {
+    const double xd = val;
+    const double ss = nd::wave_sum(xd * xd);
+    const double inv = 1.0 / sqrt(ss / kHd + 1e-6);
+    const double normed = (float)((1.0 + (double)nscale) * xd * inv);
+    double sn, cs;
+    sincos((double)pos * invf, &sn, &cs);
+    const double other = __shfl_xor(normed, 32, 64);
+    out = lane < 32 ? (float)(normed * cs - other * sn) : (float)(normed * cs + other * sn);
+    if (b < nq) {
+      q_out[(size_t)b * kHd + lane] = out;
+      return;
+    }
+  }
+  const uint32_t h = is_v ? b - nq - nk : b - nq;
   const uint32_t slot = kv_slot(pos, sink, window);
   if (slot >= alloc) return;  // the host keeps positions below the runtime limit
-  const size_t row = ((size_t)layer * kv_heads + h) * alloc + slot;
-  const float vv = qkvg[(heads + kv_heads) * kHd + h * kHd + lane];
-  const float ak = wave_absmax_js(rot), av = wave_absmax_js(vv);
-  const double mk = (ak != ak) ? (double)ak : fmax(1e-12, (double)ak);
-  const double mv = (av != av) ? (double)av : fmax(1e-12, (double)av);
-  const double sk = mk / 127.0, sv = mv / 127.0;
-  const double ck = rint((double)rot / sk), cv = rint((double)vv / sv);
-  Kc[row * kHd + lane] = ck != ck ? (int8_t)0 : (int8_t)(int)ck;
-  Vc[row * kHd + lane] = cv != cv ? (int8_t)0 : (int8_t)(int)cv;
-  if (lane == 0) {
-    Ks[row] = (float)sk;
-    Vs[row] = (float)sv;
-  }
-}
-
-struct PostArgs {
-  float* x;                 // [lanes][d], updated in place
-  const float* proj;        // Wo output [d]
-  const float* blk;
-  const float* upd;
-  const float* post_norm;   // [d]
-  const float* pre_h_norm;  // [d]
-  const float* d1;          // [d]
-  const float* d2;          // [hdim]
-  const float* d3;          // [d]
-  float attention_gate;
-  const float* phi_post;    // [lanes]
-  const float* phi_res;     // [lanes*lanes]
-  float a_post, a_res;
-  const float* b_post;      // [lanes]
-  const float* b_res;       // [lanes*lanes]
-  uint32_t d, hdim, lanes, own;
-};
-
-// runtime.ts:509-542 with #attentionDelta (runtime.ts:585-611), hadamardMlp
-// (math.ts:117-138), fwht (f32 store per butterfly) and sinkhorn
-// (math.ts:62-92), in one workgroup.
-__global__ __launch_bounds__(kWg) void n2_mhc_post_kernel(PostArgs a) {
-  __shared__ float hv[1024];
-  __shared__ double red[kWg / 64];
-  __shared__ float routing[16];
-  __shared__ float hpost[4];
-  const uint32_t t = threadIdx.x, D = a.d, H = a.hdim, L = a.lanes;
-  // afterAttention = block + sigmoid(gate) * rmsNorm(projected, postNorm).
-  const float p = t < D ? a.proj[t] : 0.f;
-  const double sp = block_sum_d(t < D ? (double)p * p : 0.0, red);
-  const double ip = 1.0 / sqrt(sp / D + 1e-6);
-  const double ascale = sigmoid_d((double)a.attention_gate);
-  float after = 0.f;
-  if (t < D) {
-    const float np = (float)((1.0 + (double)a.post_norm[t]) * (double)p * ip);
-    after = (float)((double)a.blk[t] + ascale * (double)np);
-  }
-  const double sa = block_sum_d(t < D ? (double)after * after : 0.0, red);
-  const double ia = 1.0 / sqrt(sa / D + 1e-6);
-  // Hadamard MLP: FWHT(d1 * x), SiLU(z / sqrt(H) * d2), FWHT, / sqrt(H) * d3.
-  if (t < H) {
-    float v = 0.f;
-    if (t < D) {
-      const float pre = (float)((1.0 + (double)a.pre_h_norm[t]) * (double)after * ia);
-      v = (float)((double)pre * (double)a.d1[t]);
-    }
-    hv[t] = v;
-  }
-  const double inv_root = 1.0 / sqrt((double)H);
-  for (int pass = 0; pass < 2; ++pass) {
-    __syncthreads();
-    for (uint32_t stride = 1; stride < H; stride <<= 1) {
-      if (t < H / 2) {
-        const uint32_t li = (t / stride) * 2 * stride + t % stride, ri = li + stride;
-        const double left = hv[li], right = hv[ri];
-        hv[li] = (float)(left + right);
-        hv[ri] = (float)(left - right);
-      }
-      __syncthreads();
-    }
-    if (pass == 0 && t < H) {
-      const double z = (double)hv[t] * inv_root * (double)a.d2[t];
-      hv[t] = (float)(z * sigmoid_d(z));
-    }
-  }
-  float delta = 0.f;
-  if (t < D) {
-    const float mlp = (float)((double)hv[t] * inv_root * (double)a.d3[t]);
-    delta = (float)((double)after + (double)mlp - (double)a.upd[t]);
-  }
-  if (t == 0) {
-    for (uint32_t l = 0; l < L; ++l) {
-      const double off = l == a.own ? 0.0 : -4.0;
-      hpost[l] = (float)(2.0 * sigmoid_d((double)a.a_post * (double)a.phi_post[l] +
-                                         (double)a.b_post[l] + off));
-    }
-    // Sinkhorn: twenty log-space row then column normalizations in float64.
-    double r[16];
-    for (uint32_t i = 0; i < L * L; ++i)
-      r[i] = (double)(float)((double)a.a_res * (double)a.phi_res[i] + (double)a.b_res[i]);
-    for (int it = 0; it < 20; ++it) {
-      for (uint32_t row = 0; row < L; ++row) {
-        double mx = r[row * L];
-        for (uint32_t c = 1; c < L; ++c) {
-          const double v = r[row * L + c];
-          mx = (mx != mx || v != v) ? (double)NAN : fmax(mx, v);
-        }
-        double sum = 0.0;
-        for (uint32_t c = 0; c < L; ++c) sum += exp(r[row * L + c] - mx);
-        const double ls = log(sum) + mx;
-        for (uint32_t c = 0; c < L; ++c) r[row * L + c] -= ls;
-      }
-      for (uint32_t c = 0; c < L; ++c) {
-        double mx = r[c];
-        for (uint32_t row = 1; row < L; ++row) {
-          const double v = r[row * L + c];
-          mx = (mx != mx || v != v) ? (double)NAN : fmax(mx, v);
-        }
-        double sum = 0.0;
-        for (uint32_t row = 0; row < L; ++row) sum += exp(r[row * L + c] - mx);
-        const double ls = log(sum) + mx;
-        for (uint32_t row = 0; row < L; ++row) r[row * L + c] -= ls;
-      }
-    }
-    for (uint32_t i = 0; i < L * L; ++i) routing[i] = (float)exp(r[i]);
-  }
-  __syncthreads();
-  if (t < D) {
-    float old[4];
-    for (uint32_t l = 0; l < L; ++l) old[l] = a.x[(size_t)l * D + t];
-    for (uint32_t l = 0; l < L; ++l) {
-      double sum = 0.0;
-      for (uint32_t src = 0; src < L; ++src) sum += (double)routing[l * L + src] * (double)old[src];
-      a.x[(size_t)l * D + t] = (float)(sum + (double)hpost[l] * (double)delta);
-    }
-  }
-}
-
-// runtime.ts:570-576: lane mean, then rmsNorm(finalNorm).
-__global__ __launch_bounds__(kWg) void n2_final_kernel(const float* __restrict__ x,
-                                                      const float* __restrict__ norm, uint32_t d,
-                                                      uint32_t lanes, float* __restrict__ out) {
-  __shared__ double red[kWg / 64];
-  const uint32_t t = threadIdx.x;
-  float m = 0.f;
-  if (t < d) {
-    double sum = 0.0;
-    for (uint32_t l = 0; l < lanes; ++l) sum += x[(size_t)l * d + t];
-    m = (float)(sum / lanes);
-  }
-  const double ss = block_sum_d(t < d ? (double)m * m : 0.0, red);
-  const double inv = 1.0 / sqrt(ss / d + 1e-6);
-  if (t < d) out[t] = (float)((1.0 + (double)norm[t]) * (double)m * inv);
+  const size_t crow = ((size_t)layer * kv_heads + h) * alloc + slot;
+  const float am = wave_absmax_js(out);
+  const double mx = (am != am) ? (double)am : fmax(1e-12, (double)am);
+  const double sc = mx / 127.0;
+  const double code = rint((double)out / sc);
+  (is_v ? Vc : Kc)[crow * kHd + lane] = code != code ? (int8_t)0 : (int8_t)(int)code;
+  if (lane == 0) (is_v ? Vs : Ks)[crow] = (float)sc;
 }
 
 size_t al(size_t n) { return (n + 255) & ~size_t(255); }
@@ -499,7 +661,7 @@ void drop_graphs(nd_needle* n) {
 hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want_logits,
                         bool select, const uint32_t* allowed, uint32_t count, hipStream_t s) {
   const nd_needle_desc& d = n->d;
-  const uint32_t D = d.dim, ln = d.lanes, qw = d.heads * kHd, kw = d.kv_heads * kHd;
+  const uint32_t D = d.dim, ln = d.lanes, qw = d.heads * kHd;
   BeginArgs b{};
   b.st = n->st;
   b.history = n->history;
@@ -542,76 +704,78 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   const size_t K = (size_t)ln * D;
-  for (uint32_t l = 0; l < d.layers; ++l) {
-    const uint32_t own = l % ln;
-    int site = -1;
-    for (uint32_t si = 0; si < d.n_sites; ++si)
-      if (d.sites[si] == l) site = (int)si;
-    PreArgs pa{};
-    pa.x = n->x;
-    pa.phi_pre = n->phi_pre->w + (size_t)l * ln * K;
-    pa.phi_pre_s = n->phi_pre->scales + (size_t)l * ln;
-    pa.phi_post = n->phi_post->w + (size_t)l * ln * K;
-    pa.phi_post_s = n->phi_post->scales + (size_t)l * ln;
-    pa.phi_res = n->phi_res->w + (size_t)l * ln * ln * K;
-    pa.phi_res_s = n->phi_res->scales + (size_t)l * ln * ln;
-    pa.a_pre = n->a_pre[l];
-    pa.b_pre = n->params + n->o_bpre + (size_t)l * ln;
-    pa.ekey = site >= 0 ? n->ekv_out + (size_t)site * 2 * D : nullptr;
-    pa.evalue = site >= 0 ? n->evals + (size_t)site * D : nullptr;
-    pa.norm_input = n->params + n->o_norm_input + (size_t)l * D;
-    pa.upd = n->upd;
-    pa.blk = n->blk;
-    pa.ain = n->ain;
-    pa.phi_post_out = n->phi_post_v;
-    pa.phi_res_out = n->phi_res_v;
-    pa.d = D;
-    pa.lanes = ln;
-    pa.own = own;
-    hipLaunchKernelGGL(n2_mhc_pre_kernel, dim3(1), dim3(kWg), 0, s, pa);
+  const bool tail = want_logits || select;
+  // Launch l (l <= layers) runs post(l - 1) and pre(l); the last one runs
+  // post(layers - 1) and the final norm, and only when logits are wanted
+  // (the lanes do not outlive the step).
+  for (uint32_t l = 0; l <= d.layers; ++l) {
+    const bool pre = l < d.layers;
+    if (!pre && !tail) break;
+    MixArgs m{};
+    m.x = n->x;
+    m.d = D;
+    m.hdim = d.hadamard;
+    m.lanes = ln;
+    m.upd = n->upd;
+    m.blk = n->blk;
+    m.ain = n->ain;
+    m.phi_post = n->phi_post_v;
+    m.phi_res = n->phi_res_v;
+    if (l > 0) {
+      const uint32_t p = l - 1;
+      m.has_post = 1;
+      m.own_post = p % ln;
+      m.proj = n->proj;
+      m.post_norm = n->params + n->o_post + (size_t)p * D;
+      m.pre_h_norm = n->params + n->o_preh + (size_t)p * D;
+      m.d1 = n->params + n->o_d1 + (size_t)p * D;
+      m.d2 = n->params + n->o_d2 + (size_t)p * d.hadamard;
+      m.d3 = n->params + n->o_d3 + (size_t)p * D;
+      m.attention_gate = n->attention_gate[p];
+      m.a_post = n->a_post[p];
+      m.a_res = n->a_res[p];
+      m.b_post = n->params + n->o_bpost + (size_t)p * ln;
+      m.b_res = n->params + n->o_bres + (size_t)p * ln * ln;
+    }
+    if (pre) {
+      int site = -1;
+      for (uint32_t si = 0; si < d.n_sites; ++si)
+        if (d.sites[si] == l) site = (int)si;
+      m.has_pre = 1;
+      m.own_pre = l % ln;
+      m.phi_w[0] = n->phi_pre->w + (size_t)l * ln * K;
+      m.phi_s[0] = n->phi_pre->scales + (size_t)l * ln;
+      m.phi_w[1] = n->phi_post->w + (size_t)l * ln * K;
+      m.phi_s[1] = n->phi_post->scales + (size_t)l * ln;
+      m.phi_w[2] = n->phi_res->w + (size_t)l * ln * ln * K;
+      m.phi_s[2] = n->phi_res->scales + (size_t)l * ln * ln;
+      m.a_pre = n->a_pre[l];
+      m.b_pre = n->params + n->o_bpre + (size_t)l * ln;
+      m.ekey = site >= 0 ? n->ekv_out + (size_t)site * 2 * D : nullptr;
+      m.evalue = site >= 0 ? n->evals + (size_t)site * D : nullptr;
+      m.norm_input = n->params + n->o_norm_input + (size_t)l * D;
+    } else {
+      m.has_final = 1;
+      m.final_norm = n->params + n->o_final;
+      m.fin = n->fin;
+    }
+    hipLaunchKernelGGL(n2_mix_kernel, dim3(1), dim3(kMixWg), 0, s, m);
     if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (!pre) break;
     const nd_mat& wm = n->wqkvg[l];
-    if ((e = nd_launch_matvec(&wm, n->ain, 1, D, 0, wm.n, n->qkvg, wm.n, s)) != hipSuccess)
-      return e;
-    hipLaunchKernelGGL(n2_qk_rope_store_kernel, dim3(d.heads + d.kv_heads), dim3(64), 0, s, n->st,
-                       n->qkvg, d.heads, d.kv_heads, n->params + n->o_qn + (size_t)l * kHd,
-                       n->params + n->o_kn + (size_t)l * kHd, n->inv_freq, n->q,
+    hipLaunchKernelGGL(n2_qkv_kernel, dim3(wm.n / kHd), dim3(256), 0, s, wm.w, wm.scales, n->ain,
+                       D, d.heads, d.kv_heads, n->st, n->params + n->o_qn + (size_t)l * kHd,
+                       n->params + n->o_kn + (size_t)l * kHd, n->inv_freq, n->q, n->qkvg,
                        (int8_t*)n->kv.k, (int8_t*)n->kv.v, n->kv.ks, n->kv.vs, l, n->kv.alloc,
                        n->kv.sink, n->kv.window);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    e = nd_launch_attention_gated(&n->kv, l, n->st + 1, n->max_length - 1, n->q, d.heads,
-                                  n->qkvg + qw + 2 * kw, n->att, n->partials, s);
+    e = nd_launch_attention_gated(&n->kv, l, n->st + 1, n->max_length - 1, n->q, d.heads, n->qkvg,
+                                  n->att, n->partials, s);
     if (e != hipSuccess) return e;
     if ((e = nd_launch_matvec(n->wo[l], n->att, 1, qw, 0, D, n->proj, D, s)) != hipSuccess)
       return e;
-    PostArgs qa{};
-    qa.x = n->x;
-    qa.proj = n->proj;
-    qa.blk = n->blk;
-    qa.upd = n->upd;
-    qa.post_norm = n->params + n->o_post + (size_t)l * D;
-    qa.pre_h_norm = n->params + n->o_preh + (size_t)l * D;
-    qa.d1 = n->params + n->o_d1 + (size_t)l * D;
-    qa.d2 = n->params + n->o_d2 + (size_t)l * d.hadamard;
-    qa.d3 = n->params + n->o_d3 + (size_t)l * D;
-    qa.attention_gate = n->attention_gate[l];
-    qa.phi_post = n->phi_post_v;
-    qa.phi_res = n->phi_res_v;
-    qa.a_post = n->a_post[l];
-    qa.a_res = n->a_res[l];
-    qa.b_post = n->params + n->o_bpost + (size_t)l * ln;
-    qa.b_res = n->params + n->o_bres + (size_t)l * ln * ln;
-    qa.d = D;
-    qa.hdim = d.hadamard;
-    qa.lanes = ln;
-    qa.own = own;
-    hipLaunchKernelGGL(n2_mhc_post_kernel, dim3(1), dim3(kWg), 0, s, qa);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  if (!want_logits && !select) return hipSuccess;
-  hipLaunchKernelGGL(n2_final_kernel, dim3(1), dim3(kWg), 0, s, n->x, n->params + n->o_final, D,
-                     ln, n->fin);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if (!tail) return hipSuccess;
   e = nd_launch_matvec(n->embedding, n->fin, 1, D, 0, d.vocab, n->logits, d.vocab, s);
   if (e != hipSuccess || !select) return e;
   return nd_launch_select_list(n->logits, d.vocab, allowed, count, n->sel_id, n->sel_lp, s);
@@ -670,7 +834,7 @@ nd_status nd_needle_create(nd_ctx* ctx, const nd_needle_desc* d, nd_needle** out
   if (!d || !out) return nd_fail(ctx, ND_ERR_INVALID, "nd_needle_create: NULL argument");
   *out = nullptr;
   if (d->head_dim != kHd || d->lanes == 0 || d->lanes > 4 || d->dim < 128 || d->dim > 512 ||
-      (d->dim & (d->dim - 1)) || d->hadamard > 1024 || d->hadamard < d->dim ||
+      (d->dim & (d->dim - 1)) || d->hadamard > 512 || d->hadamard < d->dim ||
       (d->hadamard & (d->hadamard - 1)) || d->heads == 0 || d->kv_heads == 0 ||
       d->heads % d->kv_heads || d->heads * kHd > 8192 || d->layers == 0 || d->vocab == 0 ||
       d->max_length == 0 || d->n_sites > 4 || d->n_orders > 4 ||
@@ -679,7 +843,7 @@ nd_status nd_needle_create(nd_ctx* ctx, const nd_needle_desc* d, nd_needle** out
       (d->n_sites && (d->engram_taps == 0 || d->engram_slots == 0 || d->engram_sub == 0)))
     return nd_fail(ctx, ND_ERR_INVALID,
                    "Needle geometry outside this kernel set: head_dim 64, lanes <= 4, dim a "
-                   "power of two in [128, 512], power-of-two hadamard in [dim, 1024], heads a "
+                   "power of two in [128, 512], power-of-two hadamard in [dim, 512], heads a "
                    "multiple of kv_heads, at most 4 engram sites and orders, tables a multiple "
                    "of orders");
   const uint32_t rep = d->heads / d->kv_heads;
