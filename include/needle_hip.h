@@ -332,8 +332,8 @@ typedef struct nd_needle nd_needle;
  *   phi_res    [layers*lanes*lanes][lanes*dim] (runtime.ts:385-420)
  *   eg_tables  n_sites entries of [engram_tables*engram_slots][engram_sub]
  *   eg_key, eg_value  n_sites entries of [dim][engram_tables*engram_sub]
- * Limits: head_dim 64, lanes <= 4, dim <= 512, hadamard a power of two in
- * [dim, 1024], heads / kv_heads in {1, 2, 4, 8}, n_sites <= 4,
+ * Limits: head_dim 64, lanes <= 4, dim a power of two in [128, 512],
+ * hadamard a power of two in [dim, 512], heads / kv_heads in {1, 2, 4, 8}, n_sites <= 4,
  * engram_tables <= 16 and a multiple of n_orders. */
 typedef struct nd_needle_desc {
   uint32_t vocab, dim, heads, kv_heads, layers, head_dim, max_length, hadamard, lanes;
