@@ -512,7 +512,7 @@ nd_status nd_batch_step(nd_ctx* ctx, nd_batch* b, uint32_t max_position, uint32_
     ND_HIP(ctx, hipGetLastError());
     ND_HIP(ctx, nd_launch_attention_batch(&b->kv, l, b->positions, B, dec->kv_heads,
                                           dec->kv_heads, rep, max_position, b->q, b->o,
-                                          b->partials, s));
+                                          b->partials, b->counters, s));
     ND_HIP(ctx, nd_launch_digitize(b->o, D, nullptr, nullptr, b->digits, b->fm, B, D, s));
     ND_HIP(ctx, nd_launch_gemm(dec->wo[l], b->digits, b->fm, b->x, D, B, 1, s));
     ND_HIP(ctx, nd_launch_digitize(b->x, D, dec->norms + dec->ffn_off + (size_t)l * D, nullptr,
@@ -548,7 +548,7 @@ struct nd_prefill {
   float *x = nullptr, *qkv = nullptr, *q = nullptr, *o = nullptr, *h = nullptr, *fm = nullptr,
         *partials = nullptr, *logits = nullptr;
   int8_t* digits = nullptr;
-  uint32_t *tokens = nullptr, *positions = nullptr;
+  uint32_t *tokens = nullptr, *positions = nullptr, *counters = nullptr;
   size_t partial_floats = 0;
 };
 
@@ -575,11 +575,15 @@ nd_status nd_prefill_create(nd_ctx* ctx, nd_decoder* dec, uint32_t max_tokens,
   const size_t sizes[] = {a256(M * dec->dim * 4),  a256(M * qkv_rows * 4), a256(M * dec->dim * 4),
                           a256(M * dec->dim * 4),  a256(M * dec->ffn * 4), a256(M * 4),
                           a256(p->partial_floats * 4), a256((size_t)dec->vocab * 4),
-                          a256(3 * M * kmax),      a256(M * 4),            a256(M * 4)};
+                          a256(3 * M * kmax),      a256(M * 4),            a256(M * 4),
+                          a256(M * dec->kv_heads * 4)};
   size_t total = 0;
   for (size_t v : sizes) total += v;
   hipError_t e = hipMalloc(&p->arena, total);
+  if (e == hipSuccess) e = hipMemsetAsync(p->arena, 0, total, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) {
+    if (p->arena) hipFree(p->arena);
     delete p;
     return nd_hip_fail(ctx, e, "prefill allocation");
   }
@@ -600,6 +604,7 @@ nd_status nd_prefill_create(nd_ctx* ctx, nd_decoder* dec, uint32_t max_tokens,
   take(&p->digits);
   take(&p->tokens);
   take(&p->positions);
+  take(&p->counters);
   *out = p;
   return ND_OK;
 }
@@ -680,7 +685,7 @@ nd_status nd_prefill_run_d(nd_ctx* ctx, nd_prefill* p, nd_kv* kv, void* stream) 
                        kv->kv_heads, kv->alloc, 0u);
     ND_HIP(ctx, hipGetLastError());
     ND_HIP(ctx, nd_launch_attention_batch(kv, l, p->positions, M, dec->kv_heads, 0u, rep, last,
-                                          p->q, p->o, p->partials, s));
+                                          p->q, p->o, p->partials, p->counters, s));
     ND_HIP(ctx, nd_launch_digitize(p->o, D, nullptr, nullptr, p->digits, p->fm, M, D, s));
     ND_HIP(ctx, nd_launch_gemm(dec->wo[l], p->digits, p->fm, p->x, D, M, 1, s));
     ND_HIP(ctx, nd_launch_digitize(p->x, D, dec->norms + dec->ffn_off + (size_t)l * D, nullptr,

@@ -163,8 +163,9 @@ __device__ __forceinline__ void unpack(const Tile<F32>& tl, int k, bool is_v, fl
 // so each 128-bit load of the wave reads 16 consecutive 64-byte rows.
 //
 // The waves merge through LDS.  A sequence whose visible positions fit one
-// chunk gets its normalized output here; otherwise each chunk writes (max,
-// sum, acc[64]) per query head and attention_merge_kernel combines them.
+// chunk gets its normalized output here; otherwise each chunk publishes
+// (max, sum, acc[64]) per query head and the last chunk to finish combines
+// them, so one launch always completes the attention.
 //
 // Scores: (q . k_codes) * k_scale / sqrt(64); softmax; out = sum w * v_codes *
 // v_scale -- NeedleRuntime.#attention (model/runtime.ts:719-786) with
@@ -176,8 +177,9 @@ template <int REP, bool F32>
 __global__ __launch_bounds__(256) void attention_kernel(
     const void* __restrict__ Kc, const void* __restrict__ Vc, const float* __restrict__ Ks,
     const float* __restrict__ Vs, const float* __restrict__ Q, float* __restrict__ out,
-    const float* __restrict__ gate, float* __restrict__ part_acc, float* __restrict__ part_ml,
-    uint32_t layer, uint32_t kv_heads,
+    const float* __restrict__ gate, uint32_t gate_ld, float* __restrict__ part_acc,
+    float* __restrict__ part_ml,
+    uint32_t* __restrict__ counters, uint32_t layer, uint32_t kv_heads,
     uint32_t alloc, uint32_t sink, uint32_t window, Visible vis,
     const uint32_t* __restrict__ positions, uint32_t seq_kv_heads, uint32_t kv_stride_z,
     uint32_t chunk_positions, uint32_t max_chunks, float score_scale) {
@@ -304,7 +306,9 @@ __global__ __launch_bounds__(256) void attention_kernel(
   __syncthreads();
 
   // Merge the waves: thread t < REP*64 owns (h, dim).
-  for (uint32_t o = threadIdx.x; o < REP * kHeadDim; o += blockDim.x) {
+  float w_m[2], w_l[2], w_a[2];
+  int n_own = 0;
+  for (uint32_t o = threadIdx.x; o < REP * kHeadDim; o += blockDim.x, ++n_own) {
     const uint32_t h = o / kHeadDim, dim = o % kHeadDim;
     float mx = -INFINITY;
 #pragma unroll
@@ -316,59 +320,94 @@ __global__ __launch_bounds__(256) void attention_kernel(
       L = fmaf(f, s_l[w][h], L);
       A = fmaf(f, s_acc[w][h * kHeadDim + dim], A);
     }
-    const uint32_t qh = kvh_local * REP + h;
-    if (nchunks == 1) {
-      float r = A / L;
-      if (gate) r *= gate_factor(gate[((size_t)z * hq + qh) * kHeadDim + dim]);
-      out[(size_t)qh * kHeadDim + dim] = r;
-    } else {
-      const size_t pi = ((size_t)z * hq + qh) * max_chunks + chunk;
-      part_acc[pi * kHeadDim + dim] = A;
+    w_m[n_own] = mx;
+    w_l[n_own] = L;
+    w_a[n_own] = A;
+  }
+  const size_t row0 = (size_t)z * hq + (size_t)kvh_local * REP;
+  if (nchunks == 1) {
+    int i = 0;
+    for (uint32_t o = threadIdx.x; o < REP * kHeadDim; o += blockDim.x, ++i) {
+      const size_t oi = (row0 + o / kHeadDim) * kHeadDim + o % kHeadDim;
+      float r = w_a[i] / w_l[i];
+      if (gate) r *= gate_factor(gate[(size_t)z * gate_ld + (oi - (size_t)z * hq * kHeadDim)]);
+      out[oi - (size_t)z * hq * kHeadDim] = r;
+    }
+    return;
+  }
+  // Several chunks: publish this chunk's (max, sum, acc) with agent-coherent
+  // stores, wait for them, count the chunk in; the last chunk of the (row,
+  // KV head) to arrive combines all of them (log-sum-exp) and resets the
+  // counter for the next launch.  No workgroup waits for another.
+  {
+    int i = 0;
+    for (uint32_t o = threadIdx.x; o < REP * kHeadDim; o += blockDim.x, ++i) {
+      const uint32_t h = o / kHeadDim, dim = o % kHeadDim;
+      const size_t pi = (row0 + h) * max_chunks + chunk;
+      __hip_atomic_store(part_acc + pi * kHeadDim + dim, w_a[i], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
       if (dim == 0) {
-        part_ml[pi * 2 + 0] = mx;
-        part_ml[pi * 2 + 1] = L;
+        __hip_atomic_store(part_ml + pi * 2, w_m[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(part_ml + pi * 2 + 1, w_l[i], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
+  __builtin_amdgcn_s_waitcnt(0);  // every store above has completed
+  __syncthreads();
+  __shared__ uint32_t s_last;
+  uint32_t* counter = counters + (size_t)z * seq_kv_heads + kvh_local;
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             nchunks - 1;
+  __syncthreads();
+  if (!s_last) return;
+  for (uint32_t o = threadIdx.x; o < REP * kHeadDim; o += blockDim.x) {
+    const uint32_t h = o / kHeadDim, dim = o % kHeadDim;
+    const size_t base = (row0 + h) * max_chunks;
+    float mx = -INFINITY, total = 0.f, acc = 0.f;
+    // Up to 32 chunks' loads in flight at a time.
+    for (uint32_t c0 = 0; c0 < nchunks; c0 += 32) {
+      float cm[32], cl[32], ca[32];
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        const uint32_t c = min(c0 + j, nchunks - 1);  // past the end: reread, then drop
+        cm[j] = __hip_atomic_load(part_ml + (base + c) * 2, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+        cl[j] = __hip_atomic_load(part_ml + (base + c) * 2 + 1, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+        ca[j] = __hip_atomic_load(part_acc + (base + c) * kHeadDim + dim, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int j = 0; j < 32; ++j)
+        if (c0 + j >= nchunks) cm[j] = -INFINITY, cl[j] = 0.f, ca[j] = 0.f;
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        const float m_new = fmaxf(mx, cm[j]);
+        const float f_old = mx == -INFINITY ? 0.f : __expf(mx - m_new);
+        const float f_new = cm[j] == -INFINITY ? 0.f : __expf(cm[j] - m_new);
+        total = total * f_old + cl[j] * f_new;
+        acc = acc * f_old + ca[j] * f_new;
+        mx = m_new;
+      }
+    }
+    const size_t oi = (row0 + h) * kHeadDim + dim;
+    float r = acc / total;
+    if (gate) r *= gate_factor(gate[(size_t)z * gate_ld + (oi - (size_t)z * hq * kHeadDim)]);
+    out[oi - (size_t)z * hq * kHeadDim] = r;
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Log-sum-exp combine of a sequence's chunk partials: one wave per (query
-// head, sequence), lane = dim.  Sequences that fit one chunk were finished by
-// attention_kernel and are skipped.
-__global__ __launch_bounds__(64) void attention_merge_kernel(
-    const float* __restrict__ part_acc, const float* __restrict__ part_ml,
-    float* __restrict__ out, const float* __restrict__ gate, uint32_t hq, uint32_t sink, uint32_t window, Visible vis,
-    const uint32_t* __restrict__ positions, uint32_t alloc, uint32_t chunk_positions,
-    uint32_t max_chunks) {
-  const uint32_t qh = blockIdx.x, z = blockIdx.y, dim = threadIdx.x;
-  if (positions) {
-    if (window == 0 && positions[z] >= alloc) return;
-    vis = visible_at(positions[z], sink, window);
-  }
-  uint32_t nchunks = (vis.count + chunk_positions - 1) / chunk_positions;
-  if (nchunks > max_chunks) nchunks = max_chunks;
-  if (nchunks <= 1) return;
-  const size_t base = ((size_t)z * hq + qh) * max_chunks;
-  float mx = -INFINITY;
-  for (uint32_t c = 0; c < nchunks; ++c) mx = fmaxf(mx, part_ml[(base + c) * 2]);
-  float total = 0.f, acc = 0.f;
-#pragma unroll 4
-  for (uint32_t c = 0; c < nchunks; ++c) {
-    const float w = __expf(part_ml[(base + c) * 2] - mx);
-    total = fmaf(w, part_ml[(base + c) * 2 + 1], total);
-    acc = fmaf(w, part_acc[(base + c) * kHeadDim + dim], acc);
-  }
-  const size_t o = ((size_t)z * hq + qh) * kHeadDim + dim;
-  float r = acc / total;
-  if (gate) r *= gate_factor(gate[o]);
-  out[o] = r;
-}
-
-// Positions per chunk: the whole visible range when the (sequence, kv head)
-// pairs alone give ~1024 workgroups, else split so that they do; at least
-// one tile per wave.
-uint32_t chunk_positions_for(uint32_t max_count, uint32_t pairs) {
-  const uint32_t want_chunks = pairs >= 1024 ? 1 : (1024 + pairs - 1) / pairs;
+// Positions per chunk: the whole visible range when the (row, kv head) pairs
+// alone give `target` workgroups, else split so that they do; at least one
+// tile per wave.  Splitting costs a publish + count + merge round trip at the
+// end, so a single query row aims at 128 workgroups (16 chunks of 512 per
+// head at 8 heads x 8192: the measured optimum), batches at 1024.
+constexpr uint32_t kTargetSingle = 128, kTargetBatch = 1024;
+uint32_t chunk_positions_for(uint32_t max_count, uint32_t pairs, uint32_t target) {
+  const uint32_t want_chunks = pairs >= target ? 1 : (target + pairs - 1) / pairs;
   uint32_t cp = (max_count + want_chunks - 1) / want_chunks;
   cp = (cp + kMinChunk - 1) / kMinChunk * kMinChunk;
   return cp < kMinChunk ? kMinChunk : cp;
@@ -379,8 +418,10 @@ struct AttnLaunch {
   uint32_t layer;
   const float* q;
   float* out;
-  const float* gate;           // optional: out *= sigmoid(gate), laid out like out
+  const float* gate;           // optional: out *= sigmoid(gate); row z at gate + z * gate_ld
+  uint32_t gate_ld;
   float* partials;
+  uint32_t* counters;          // batch * seq_kv_heads zeros, used when a row has >1 chunk
   Visible vis;                 // used when positions == nullptr
   const uint32_t* positions;   // per-sequence query positions, or nullptr
   uint32_t seq_kv_heads;       // KV heads of one sequence
@@ -392,21 +433,17 @@ struct AttnLaunch {
 
 template <int REP, bool F32>
 hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
-  const uint32_t cp = chunk_positions_for(a.max_count, a.batch * a.seq_kv_heads);
+  const uint32_t cp = chunk_positions_for(a.max_count, a.batch * a.seq_kv_heads,
+                                          a.batch == 1 ? kTargetSingle : kTargetBatch);
   const uint32_t max_chunks = (a.max_count + cp - 1) / cp;
   const uint32_t hq = a.seq_kv_heads * REP;
   float* part_acc = a.partials;
   float* part_ml = a.partials + (size_t)a.batch * hq * max_chunks * kHeadDim;
   hipLaunchKernelGGL((attention_kernel<REP, F32>), dim3(max_chunks, a.seq_kv_heads, a.batch),
                      dim3(64 * kWaves), 0, s, a.kv->k, a.kv->v, a.kv->ks, a.kv->vs, a.q, a.out,
-                     a.gate, part_acc, part_ml, a.layer, a.kv->kv_heads, a.kv->alloc, a.kv->sink,
-                     a.kv->window, a.vis, a.positions, a.seq_kv_heads, a.kv_stride_z, cp,
-                     max_chunks, 0.125f);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || max_chunks == 1) return e;
-  hipLaunchKernelGGL(attention_merge_kernel, dim3(hq, a.batch), dim3(64), 0, s, part_acc,
-                     part_ml, a.out, a.gate, hq, a.kv->sink, a.kv->window, a.vis, a.positions,
-                     a.kv->alloc, cp, max_chunks);
+                     a.gate, a.gate_ld, part_acc, part_ml, a.counters, a.layer, a.kv->kv_heads, a.kv->alloc,
+                     a.kv->sink, a.kv->window, a.vis, a.positions, a.seq_kv_heads, a.kv_stride_z,
+                     cp, max_chunks, 0.125f);
   return hipGetLastError();
 }
 
@@ -434,7 +471,7 @@ nd_visible nd_kv_visible(const nd_kv* kv, uint32_t position) {
 }
 
 uint32_t nd_attention_chunks(uint32_t count, uint32_t kv_heads) {
-  const uint32_t cp = chunk_positions_for(count, kv_heads);
+  const uint32_t cp = chunk_positions_for(count, kv_heads, kTargetSingle);
   return (count + cp - 1) / cp;
 }
 
@@ -468,7 +505,6 @@ hipError_t nd_launch_kv_store(const nd_kv* kv, uint32_t layer, uint32_t position
 hipError_t nd_launch_attention(const nd_kv* kv, uint32_t layer, uint32_t position,
                                const float* q, uint32_t q_heads, float* out, float* partials,
                                uint32_t* counters, hipStream_t s) {
-  (void)counters;
   const nd_visible nv = nd_kv_visible(kv, position);
   AttnLaunch a{};
   a.kv = kv;
@@ -476,6 +512,7 @@ hipError_t nd_launch_attention(const nd_kv* kv, uint32_t layer, uint32_t positio
   a.q = q;
   a.out = out;
   a.partials = partials;
+  a.counters = counters;
   a.vis = Visible{nv.prefix, nv.recent_low, nv.count};
   a.positions = nullptr;
   a.seq_kv_heads = kv->kv_heads;
@@ -493,14 +530,18 @@ hipError_t nd_launch_attention(const nd_kv* kv, uint32_t layer, uint32_t positio
 hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint32_t* positions,
                                      uint32_t batch, uint32_t seq_kv_heads, uint32_t kv_stride_z,
                                      uint32_t rep, uint32_t max_position, const float* q,
-                                     float* out, float* partials, hipStream_t s) {
+                                     float* out, float* partials, uint32_t* counters,
+                                     hipStream_t s, const float* gate, uint32_t gate_ld) {
   const nd_visible nv = nd_kv_visible(kv, max_position);
   AttnLaunch a{};
   a.kv = kv;
   a.layer = layer;
   a.q = q;
   a.out = out;
+  a.gate = gate;
+  a.gate_ld = gate_ld;
   a.partials = partials;
+  a.counters = counters;
   a.vis = Visible{nv.prefix, nv.recent_low, nv.count};
   a.positions = positions;
   a.seq_kv_heads = seq_kv_heads;
@@ -514,7 +555,7 @@ hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint
 hipError_t nd_launch_attention_gated(const nd_kv* kv, uint32_t layer, const uint32_t* position,
                                      uint32_t max_position, const float* q, uint32_t q_heads,
                                      const float* gate, float* out, float* partials,
-                                     hipStream_t s) {
+                                     uint32_t* counters, hipStream_t s) {
   const nd_visible nv = nd_kv_visible(kv, max_position);
   AttnLaunch a{};
   a.kv = kv;
@@ -523,6 +564,7 @@ hipError_t nd_launch_attention_gated(const nd_kv* kv, uint32_t layer, const uint
   a.out = out;
   a.gate = gate;
   a.partials = partials;
+  a.counters = counters;
   a.vis = Visible{nv.prefix, nv.recent_low, nv.count};
   a.positions = position;
   a.seq_kv_heads = kv->kv_heads;

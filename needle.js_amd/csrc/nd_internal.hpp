@@ -99,13 +99,20 @@ hipError_t nd_launch_gemm(const nd_mat* w, const int8_t* digits, const float* fm
 hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint32_t* positions,
                                      uint32_t batch, uint32_t seq_kv_heads, uint32_t kv_stride_z,
                                      uint32_t rep, uint32_t max_position, const float* q,
-                                     float* out, float* partials, hipStream_t s);
+                                     float* out, float* partials, uint32_t* counters,
+                                     hipStream_t s, const float* gate = nullptr,
+                                     uint32_t gate_ld = 0);
+// Attention launches take `counters`: one zero-initialized word per (query
+// row, KV head) -- index z * seq_kv_heads + kv head -- which a launch that
+// splits a row into several chunks uses to elect the chunk that merges them,
+// and leaves at zero again.
+//
 // One query row whose position is read from device memory (*position <=
 // max_position); out = attention * sigmoid(gate) elementwise when gate is set
 // (gated attention, model/runtime.ts:503-505).
 hipError_t nd_launch_attention_gated(const nd_kv* kv, uint32_t layer, const uint32_t* position,
                                      uint32_t max_position, const float* q, uint32_t q_heads,
                                      const float* gate, float* out, float* partials,
-                                     hipStream_t s);
+                                     uint32_t* counters, hipStream_t s);
 size_t nd_attention_batch_partial_floats(uint32_t batch, uint32_t seq_kv_heads, uint32_t rep,
                                          uint32_t max_count);

@@ -31,6 +31,7 @@ constexpr uint32_t kHd = 64;
 constexpr int kWg = 1024;
 constexpr int kMixWg = 512;  // mix kernel: dim <= 512 values per thread role
 constexpr int kMixChunks = 6;  // 24 phi rows x 2048 / 16 bytes / kMixWg
+constexpr uint32_t kPrefillRows = 512;  // positions per batched prefill pass
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ double sigmoid_d(double v) {
@@ -165,55 +166,6 @@ __global__ void n2_engram_conv_kernel(const uint32_t* __restrict__ st,
   mixed[(size_t)s * d + i] = m;
 }
 
-// Walsh-Hadamard transform of H = 64 * VPL values held by one wave (lane l
-// owns values [l * VPL, (l + 1) * VPL)), strides ascending, each butterfly
-// evaluated in float64 and stored as f32 -- fwht (math.ts) value for value.
-template <int VPL>
-__device__ __forceinline__ void fwht_wave(float (&v)[VPL], uint32_t lane) {
-#pragma unroll
-  for (int s = 1; s < VPL; s <<= 1) {
-#pragma unroll
-    for (int j = 0; j < VPL; ++j)
-      if (!(j & s)) {
-        const double left = v[j], right = v[j | s];
-        v[j] = (float)(left + right);
-        v[j | s] = (float)(left - right);
-      }
-  }
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      const float o = m == 1 ? nd::dpp<nd::kQuadXor1>(v[j])
-                      : m == 2 ? nd::dpp<nd::kQuadXor2>(v[j]) : __shfl_xor(v[j], m, 64);
-      const double mine = v[j], other = o;
-      v[j] = (lane & m) ? (float)(other - mine) : (float)(mine + other);
-    }
-  }
-}
-
-// hadamardMlp (math.ts:117-138) on one wave up to the last scaling: FWHT(d1
-// x), SiLU(z / sqrt(H) * d2), FWHT.  hv holds d1 x zero-padded to H on entry
-// and the second transform on exit (the caller applies / sqrt(H) * d3); d2
-// is in LDS.
-template <int VPL>
-__device__ void hadamard_wave(float* hv, const float* d2, uint32_t lane) {
-  constexpr uint32_t H = 64 * VPL;
-  const double inv_root = 1.0 / sqrt((double)H);
-  float v[VPL];
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) v[j] = hv[lane * VPL + j];
-  fwht_wave<VPL>(v, lane);
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const double z = (double)v[j] * inv_root * (double)d2[lane * VPL + j];
-    v[j] = (float)(z * sigmoid_d(z));
-  }
-  fwht_wave<VPL>(v, lane);
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) hv[lane * VPL + j] = v[j];
-}
-
 // sinkhorn (math.ts:62-92) of an L x L matrix (L <= 4) on the lanes of a
 // quad: lane q holds row q.  Each log-space row (column) step r -= logsumexp
 // is a division of exp(r) by its row (column) sum, so the twenty iterations
@@ -290,28 +242,59 @@ __device__ void sinkhorn_quad(float* io, uint32_t L, uint32_t lane) {
     for (uint32_t c = 0; c < L; ++c) io[q * L + c] = p[c];
 }
 
+struct RouteArgs {
+  const float* phi_post;  // [lanes], from pre(l)
+  const float* phi_res;   // [lanes * lanes]
+  float a_post, a_res;
+  const float* b_post;
+  const float* b_res;
+  uint32_t lanes, own;
+  float* route;  // out: [lanes * lanes] routing, then [lanes] h-post
+};
+
+// h-post and the Sinkhorn routing of layer l (runtime.ts:511-528) on one
+// wave; they depend only on pre(l)'s phi values, so they run beside the
+// Q/K/V projection instead of inside the next mix kernel.
+__device__ void route_wave(const RouteArgs& r, uint32_t lane, float* lds) {
+  const uint32_t L = r.lanes;
+  if (lane < L * L)
+    lds[lane] = (float)((double)r.a_res * (double)r.phi_res[lane] + (double)r.b_res[lane]);
+  float hp = 0.f;
+  if (lane < L) {
+    const double off = lane == r.own ? 0.0 : -4.0;
+    hp = (float)(2.0 * sigmoid_d((double)r.a_post * (double)r.phi_post[lane] +
+                                 (double)r.b_post[lane] + off));
+  }
+  __syncthreads();
+  if (lane < 64) sinkhorn_quad(lds, L, lane);
+  __syncthreads();
+  if (lane < L * L) r.route[lane] = lds[lane];
+  if (lane < L) r.route[L * L + lane] = hp;
+}
+
 struct MixArgs {
   float* x;  // [lanes][d]: read, and rewritten when has_post
   uint32_t d, hdim, lanes;
   // post-attention half of layer l - 1 (runtime.ts:509-542, #attentionDelta
-  // runtime.ts:585-611)
-  uint32_t has_post, own_post;
+  // runtime.ts:585-611); routing and h-post come from the route workgroup of
+  // the Q/K/V launch of layer l - 1
+  uint32_t has_post;
   const float* proj;  // Wo output [d]
   const float* post_norm;
   const float* pre_h_norm;
   const float* d1;
   const float* d2;
   const float* d3;
-  float attention_gate, a_post, a_res;
-  const float* b_post;
-  const float* b_res;
+  float attention_gate;
+  const float* route;  // [lanes * lanes] Sinkhorn routing, then [lanes] h-post
   // pre-attention half of layer l (runtime.ts:385-441)
   uint32_t has_pre, own_pre;
   const int8_t* phi_w[3];  // phi_pre, phi_post, phi_res rows of layer l
   const float* phi_s[3];
   float a_pre;
   const float* b_pre;
-  const float* ekey;  // engram key / mixed value of a site at layer l, or null
+  uint32_t has_site;  // an engram site injects at layer l
+  const float* ekey;  // engram key / mixed value of that site
   const float* evalue;
   const float* norm_input;
   // lane mean + final norm after the last layer (runtime.ts:570-576)
@@ -324,78 +307,120 @@ struct MixArgs {
   float* ain;       // [d]
   float* phi_post;  // [lanes]
   float* phi_res;   // [lanes * lanes]
+  // Batched prefill: workgroup m works on row m of every per-row buffer
+  // (row strides: x lanes * d; proj, blk, upd, ain d; route 20; phi_post
+  // lanes; phi_res lanes * lanes; ekey ek_ld; evalue ev_ld) and, with
+  // route_out set, also computes layer l's routing into route_out row m.
+  uint32_t ek_ld, ev_ld;
+  float* route_out;
+  float r_a_post, r_a_res;
+  const float* r_b_post;
+  const float* r_b_res;
 };
 
+// Sum over the kMixWg threads with one barrier: the partial sums alternate
+// between two LDS rows, so a row is rewritten only after the next call's
+// barrier, which every reader of the previous call has passed.
+__device__ __forceinline__ double mix_sum(double v, double (*red)[kMixWg / 64], int& phase) {
+  v = nd::wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[phase][threadIdx.x >> 6] = v;
+  __syncthreads();
+  double r = 0.0;
+#pragma unroll
+  for (int i = 0; i < kMixWg / 64; ++i) r += red[phase][i];
+  phase ^= 1;
+  return r;
+}
+
+// One FWHT butterfly stage across threads: thread t holds value t and
+// combines it with value t ^ s (fwht, f32 store of the float64 sum).
+__device__ __forceinline__ float butterfly(float mine, float other, uint32_t t, uint32_t s) {
+  const double m = mine, o = other;
+  return (t & s) ? (float)(o - m) : (float)(m + o);
+}
+
+// Walsh-Hadamard transform of hv[0, H) (H <= kMixWg a power of two), one
+// value per thread, strides ascending: DPP within quads, lane shuffles
+// within the wave, LDS across waves.  Every thread calls it; threads >= H
+// hold zeros.  Returns thread t's transformed value; v is its input.
+__device__ float fwht_block(float v, float* hv, uint32_t H, uint32_t t) {
+  v = butterfly(v, nd::dpp<nd::kQuadXor1>(v), t, 1);
+  if (H > 2) v = butterfly(v, nd::dpp<nd::kQuadXor2>(v), t, 2);
+  for (uint32_t s = 4; s < 64 && s < H; s <<= 1) v = butterfly(v, __shfl_xor(v, s, 64), t, s);
+  for (uint32_t s = 64; s < H; s <<= 1) {
+    __syncthreads();
+    hv[t] = v;
+    __syncthreads();
+    v = butterfly(v, hv[t ^ s], t, s);
+  }
+  return v;
+}
+
 // The one-workgroup part between two layers: post(l - 1), then pre(l) (or
-// the final norm).  Every global operand is loaded at entry -- the phi
-// weights of layer l, the lanes, the per-layer vectors -- so the kernel pays
-// one memory latency; after that it runs from registers and LDS.  The
-// Hadamard MLP (wave 0) and the Sinkhorn routing (wave 1) run side by side.
+// the final norm).  Every global operand is loaded at entry, the ones the
+// post half needs first and the 48 KB of phi weights last, so the kernel
+// pays about one memory latency; after that it runs from registers and LDS.
 __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
+  if (blockIdx.x) {
+    const uint32_t m = blockIdx.x, D0 = a.d, L0 = a.lanes;
+    a.x += (size_t)m * L0 * D0;
+    a.proj += (size_t)m * D0;
+    a.blk += (size_t)m * D0;
+    a.upd += (size_t)m * D0;
+    a.ain += (size_t)m * D0;
+    a.route += (size_t)m * 20;
+    a.phi_post += (size_t)m * L0;
+    a.phi_res += (size_t)m * L0 * L0;
+    a.ekey += (size_t)m * a.ek_ld;
+    a.evalue += (size_t)m * a.ev_ld;
+    if (a.route_out) a.route_out += (size_t)m * 20;
+  }
   __shared__ float nl[2048];
-  __shared__ float hv[512];
-  __shared__ float d2s[512];
+  __shared__ float hv[kMixWg];
   __shared__ double part[kMixChunks * kMixWg];
-  __shared__ double red[kMixWg / 64];
-  __shared__ float phi[24], phi_sc[24], hpre[4], hpost[4], routing[16];
+  __shared__ double red[2][kMixWg / 64];
+  __shared__ float phi[24], phi_sc[24], hpre[4], rt[20];
   const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const uint32_t D = a.d, L = a.lanes, N = L * D, H = a.hdim;
   const uint32_t nrows = 2 * L + L * L, cpr = N / 16, chunks = nrows * cpr;
   const bool col = t < D;
-  // ---- loads
-  uint4 pw[kMixChunks];
-  if (a.has_pre) {
-#pragma unroll
-    for (int i = 0; i < kMixChunks; ++i) {
-      const uint32_t c = t + i * kMixWg;
-      if (c < chunks) {
-        const uint32_t r = c / cpr, m = r < L ? 0 : (r < 2 * L ? 1 : 2);
-        const uint32_t rr = m == 0 ? r : (m == 1 ? r - L : r - 2 * L);
-        pw[i] = *reinterpret_cast<const uint4*>(a.phi_w[m] + (size_t)rr * N + (c % cpr) * 16);
-      }
-    }
-  }
+  int phase = 0;
+  // ---- loads, unconditional and in first-use order (every pointer is valid
+  // even for a half that is off, indices are clamped in bounds), so the
+  // post half waits for its own operands only: post operands and lanes, the
+  // phi weights, then the pre operands.  The three phi matrices are picked by
+  // uniform selection: indexing the argument block per lane would cost a
+  // dependent load.
+  const int8_t* const w0 = a.phi_w[0];
+  const int8_t* const w1 = a.phi_w[1];
+  const int8_t* const w2 = a.phi_w[2];
+  const float* const s0 = a.phi_s[0];
+  const float* const s1 = a.phi_s[1];
+  const float* const s2 = a.phi_s[2];
+  const uint32_t tc = min(t, D - 1);
+  const float p = a.proj[tc], blk = a.blk[tc], upd = a.upd[tc], post_norm = a.post_norm[tc],
+              pre_h = a.pre_h_norm[tc], d1 = a.d1[tc], d3 = a.d3[tc], d2 = a.d2[min(t, H - 1)],
+              route = a.route[min(t, L * L + L - 1)];
   float xl[4];
 #pragma unroll
-  for (int l = 0; l < 4; ++l) xl[l] = (col && (uint32_t)l < L) ? a.x[(size_t)l * D + t] : 0.f;
-  float p = 0.f, blk = 0.f, upd = 0.f, post_norm = 0.f, pre_h = 0.f, d1 = 0.f, d3 = 0.f;
-  if (a.has_post) {
-    if (col) {
-      p = a.proj[t];
-      blk = a.blk[t];
-      upd = a.upd[t];
-      post_norm = a.post_norm[t];
-      pre_h = a.pre_h_norm[t];
-      d1 = a.d1[t];
-      d3 = a.d3[t];
-    }
-    if (t < H) d2s[t] = a.d2[t];
-    if (t < L * L)
-      routing[t] = (float)((double)a.a_res * (double)a.phi_res[t] + (double)a.b_res[t]);
-    if (t < L) {
-      const double off = t == a.own_post ? 0.0 : -4.0;
-      hpost[t] = (float)(2.0 * sigmoid_d((double)a.a_post * (double)a.phi_post[t] +
-                                         (double)a.b_post[t] + off));
-    }
+  for (int l = 0; l < 4; ++l) xl[l] = a.x[(size_t)min((uint32_t)l, L - 1) * D + tc];
+  uint4 pw[kMixChunks];
+#pragma unroll
+  for (int i = 0; i < kMixChunks; ++i) {
+    const uint32_t c = min(t + i * kMixWg, chunks - 1);
+    const uint32_t r = c / cpr;
+    const int8_t* row = r < L ? w0 + (size_t)r * N
+                        : (r < 2 * L ? w1 + (size_t)(r - L) * N : w2 + (size_t)(r - 2 * L) * N);
+    pw[i] = *reinterpret_cast<const uint4*>(row + (c % cpr) * 16);
   }
-  float norm_in = 0.f, ekey = 0.f, evalue = 0.f, b_pre = 0.f, fnorm = 0.f;
-  if (a.has_pre) {
-    if (col) norm_in = a.norm_input[t];
-    if (col && a.ekey) {
-      ekey = a.ekey[t];
-      evalue = a.evalue[t];
-    }
-    if (t < L) b_pre = a.b_pre[t];
-    if (t < nrows) {
-      const uint32_t m = t < L ? 0 : (t < 2 * L ? 1 : 2);
-      phi_sc[t] = a.phi_s[m][m == 0 ? t : (m == 1 ? t - L : t - 2 * L)];
-    }
-  }
-  if (a.has_final && col) fnorm = a.final_norm[t];
+  const uint32_t tr = min(t, nrows - 1);
+  const float norm_in = a.norm_input[tc], ekey = a.ekey[tc], evalue = a.evalue[tc],
+              b_pre = a.b_pre[min(t, L - 1)], fnorm = a.final_norm[tc],
+              psc = tr < L ? s0[tr] : (tr < 2 * L ? s1[tr - L] : s2[tr - 2 * L]);
 
   // ---- post(l - 1)
   if (a.has_post) {
-    const double sp = block_sum_d<kMixWg>(col ? (double)p * p : 0.0, red);
+    const double sp = mix_sum(col ? (double)p * p : 0.0, red, phase);
     const double ip = 1.0 / sqrt(sp / D + 1e-6);
     const double ascale = sigmoid_d((double)a.attention_gate);
     float after = 0.f;
@@ -403,26 +428,27 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
       const float np = (float)((1.0 + (double)post_norm) * (double)p * ip);
       after = (float)((double)blk + ascale * (double)np);
     }
-    const double sa = block_sum_d<kMixWg>(col ? (double)after * after : 0.0, red);
+    if (t < L * L + L) rt[t] = route;  // visible after the next barrier
+    const double sa = mix_sum(col ? (double)after * after : 0.0, red, phase);
     const double ia = 1.0 / sqrt(sa / D + 1e-6);
+    // hadamardMlp (math.ts:117-138): FWHT(d1 x), SiLU(z / sqrt(H) * d2),
+    // FWHT, / sqrt(H) * d3.
+    float v = 0.f;
     if (col) {
       const float pre = (float)((1.0 + (double)pre_h) * (double)after * ia);
-      hv[t] = (float)((double)pre * (double)d1);
+      v = (float)((double)pre * (double)d1);
     }
-    for (uint32_t i = D + t; i < H; i += kMixWg) hv[i] = 0.f;
-    __syncthreads();
-    if (wave == 0) {
-      switch (H / 64) {
-        case 2: hadamard_wave<2>(hv, d2s, lane); break;
-        case 4: hadamard_wave<4>(hv, d2s, lane); break;
-        default: hadamard_wave<8>(hv, d2s, lane); break;
-      }
-    } else if (wave == 1) {
-      sinkhorn_quad(routing, L, lane);
+    const double inv_root = 1.0 / sqrt((double)H);
+    v = fwht_block(v, hv, H, t);
+    if (t < H) {
+      const double z = (double)v * inv_root * (double)d2;
+      v = (float)(z * sigmoid_d(z));
+    } else {
+      v = 0.f;
     }
-    __syncthreads();
+    v = fwht_block(v, hv, H, t);
     if (col) {
-      const float mlp = (float)((double)hv[t] * (1.0 / sqrt((double)H)) * (double)d3);
+      const float mlp = (float)((double)v * inv_root * (double)d3);
       const float delta = (float)((double)after + (double)mlp - (double)upd);
       float nx[4];
 #pragma unroll
@@ -431,8 +457,8 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
         double sum = 0.0;
 #pragma unroll
         for (int s2 = 0; s2 < 4; ++s2)
-          if ((uint32_t)s2 < L) sum += (double)routing[l * L + s2] * (double)xl[s2];
-        nx[l] = (float)(sum + (double)hpost[l] * (double)delta);
+          if ((uint32_t)s2 < L) sum += (double)rt[l * L + s2] * (double)xl[s2];
+        nx[l] = (float)(sum + (double)rt[L * L + l] * (double)delta);
       }
 #pragma unroll
       for (int l = 0; l < 4; ++l)
@@ -451,7 +477,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
         if ((uint32_t)l < L) sum += xl[l];
       m = (float)(sum / L);
     }
-    const double ss = block_sum_d<kMixWg>(col ? (double)m * m : 0.0, red);
+    const double ss = mix_sum(col ? (double)m * m : 0.0, red, phase);
     const double inv = 1.0 / sqrt(ss / D + 1e-6);
     if (col) a.fin[t] = (float)((1.0 + (double)fnorm) * (double)m * inv);
   }
@@ -462,31 +488,33 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
 #pragma unroll
   for (int l = 0; l < 4; ++l)
     if ((uint32_t)l < L) ss += (double)xl[l] * (double)xl[l];
-  ss = block_sum_d<kMixWg>(col ? ss : 0.0, red);
+  ss = mix_sum(col ? ss : 0.0, red, phase);
   const double inv = 1.0 / sqrt(ss / N + 1e-6);
   if (col) {
 #pragma unroll
     for (int l = 0; l < 4; ++l)
       if ((uint32_t)l < L) nl[l * D + t] = (float)((double)xl[l] * inv);
   }
+  if (t < nrows) phi_sc[t] = psc;
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < kMixChunks; ++i) {
     const uint32_t c = t + i * kMixWg;
     if (c < chunks) {
+      // fp32 over the chunk's 16 products, float64 across chunks.
       const float4* xv = reinterpret_cast<const float4*>(nl + (c % cpr) * 16);
       const uint32_t words[4] = {pw[i].x, pw[i].y, pw[i].z, pw[i].w};
-      double dot = 0.0;
+      float dot = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float4 f = xv[j];
         const uint32_t wj = words[j];
-        dot += (double)(int8_t)(wj & 0xff) * (double)f.x;
-        dot += (double)(int8_t)((wj >> 8) & 0xff) * (double)f.y;
-        dot += (double)(int8_t)((wj >> 16) & 0xff) * (double)f.z;
-        dot += (double)(int8_t)(wj >> 24) * (double)f.w;
+        dot = fmaf((float)(int8_t)(wj & 0xff), f.x, dot);
+        dot = fmaf((float)(int8_t)((wj >> 8) & 0xff), f.y, dot);
+        dot = fmaf((float)(int8_t)((wj >> 16) & 0xff), f.z, dot);
+        dot = fmaf((float)(int8_t)(wj >> 24), f.w, dot);
       }
-      part[c] = dot;
+      part[c] = (double)dot;
     }
   }
   __syncthreads();
@@ -515,21 +543,68 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     a.upd[t] = u;
   }
   float b = u;
-  if (a.ekey) {
+  if (a.has_site) {
     // alpha = sigmoid(rmsUnit(u) . rmsUnit(key) / sqrt(d)); block = u + alpha * value.
-    const double su = block_sum_d<kMixWg>(col ? (double)u * u : 0.0, red);
-    const double sk = block_sum_d<kMixWg>(col ? (double)ekey * ekey : 0.0, red);
+    const double su = mix_sum(col ? (double)u * u : 0.0, red, phase);
+    const double sk = mix_sum(col ? (double)ekey * ekey : 0.0, red, phase);
     const double iu = 1.0 / sqrt(su / D + 1e-6), ik = 1.0 / sqrt(sk / D + 1e-6);
     const float nu = (float)((double)u * iu), nk = (float)((double)ekey * ik);
-    const double dot = block_sum_d<kMixWg>(col ? (double)nu * (double)nk : 0.0, red);
+    const double dot = mix_sum(col ? (double)nu * (double)nk : 0.0, red, phase);
     const double alpha = sigmoid_d(dot / sqrt((double)D));
     if (col) b = (float)((double)u + alpha * (double)evalue);
   }
   if (col) a.blk[t] = b;
   // attentionInput = rmsNorm(block, normInput) (math.ts:16-32).
-  const double sb = block_sum_d<kMixWg>(col ? (double)b * b : 0.0, red);
+  const double sb = mix_sum(col ? (double)b * b : 0.0, red, phase);
   const double ib = 1.0 / sqrt(sb / D + 1e-6);
   if (col) a.ain[t] = (float)((1.0 + (double)norm_in) * (double)b * ib);
+  if (a.route_out) {
+    RouteArgs r{};
+    r.phi_post = phi + L;
+    r.phi_res = phi + 2 * L;
+    r.a_post = a.r_a_post;
+    r.a_res = a.r_a_res;
+    r.b_post = a.r_b_post;
+    r.b_res = a.r_b_res;
+    r.lanes = L;
+    r.own = a.own_pre;
+    r.route = a.route_out;
+    route_wave(r, t, rt);
+  }
+}
+
+// One head of the projection epilogue, one wave, lane = dimension: role 0
+// (query) and 1 (key) take the per-head rmsNorm with their scale and the
+// half-split RoPE at `pos` (runtime.ts:471-500, math.ts:94-115); role 0
+// writes q_dst, roles 1 and 2 (value) quantize into cache row
+// head_row + slot with #storeKV's arithmetic (runtime.ts:679-717).
+__device__ __forceinline__ void head_epilogue(float val, uint32_t lane, int role, uint32_t pos,
+                                              float nscale, double invf, float* q_dst,
+                                              int8_t* Kc, int8_t* Vc, float* Ks, float* Vs,
+                                              size_t head_row, uint32_t slot, uint32_t alloc) {
+  float out = val;
+  if (role != 2) {
+    const double xd = val;
+    const double ss = nd::wave_sum(xd * xd);
+    const double inv = 1.0 / sqrt(ss / kHd + 1e-6);
+    const double normed = (float)((1.0 + (double)nscale) * xd * inv);
+    double sn, cs;
+    sincos((double)pos * invf, &sn, &cs);
+    const double other = __shfl_xor(normed, 32, 64);
+    out = lane < 32 ? (float)(normed * cs - other * sn) : (float)(normed * cs + other * sn);
+    if (role == 0) {
+      q_dst[lane] = out;
+      return;
+    }
+  }
+  if (slot >= alloc) return;  // the host keeps positions below the runtime limit
+  const size_t crow = head_row + slot;
+  const float am = wave_absmax_js(out);
+  const double mx = (am != am) ? (double)am : fmax(1e-12, (double)am);
+  const double sc = mx / 127.0;
+  const double code = rint((double)out / sc);
+  (role == 2 ? Vc : Kc)[crow * kHd + lane] = code != code ? (int8_t)0 : (int8_t)(int)code;
+  if (lane == 0) (role == 2 ? Vs : Ks)[crow] = (float)sc;
 }
 
 // The fused Q/K/V/gate projection of one layer (runtime.ts:465-470) with the
@@ -539,17 +614,23 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
 // four threads per row, fp32 accumulation of int8 x fp32 like the matvec,
 // times the row scale.  q heads go to q_out, k and v heads are quantized into
 // the cache at the ring slot of the step's position, gate heads go to
-// gate_out as raw projections.
+// gate_out as raw projections.  One more workgroup computes the layer's
+// routing (route_wave).
 __global__ __launch_bounds__(256) void n2_qkv_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ S, const float* __restrict__ x,
     uint32_t d, uint32_t heads, uint32_t kv_heads, const uint32_t* __restrict__ st,
     const float* __restrict__ q_norm, const float* __restrict__ k_norm,
     const double* __restrict__ inv_freq, float* __restrict__ q_out, float* __restrict__ gate_out,
     int8_t* __restrict__ Kc, int8_t* __restrict__ Vc, float* __restrict__ Ks,
-    float* __restrict__ Vs, uint32_t layer, uint32_t alloc, uint32_t sink, uint32_t window) {
+    float* __restrict__ Vs, uint32_t layer, uint32_t alloc, uint32_t sink, uint32_t window,
+    RouteArgs route) {
   __shared__ float xs[512];
   __shared__ float rows[64];
   const uint32_t b = blockIdx.x, t = threadIdx.x;
+  if (b == 2 * (heads + kv_heads)) {
+    route_wave(route, t, rows);
+    return;
+  }
   // Loads first: this thread's weight bytes, the row scale, the epilogue
   // operands, then x.
   const uint32_t r = t >> 2, q = t & 3, seg = d / 4;
@@ -586,32 +667,124 @@ __global__ __launch_bounds__(256) void n2_qkv_kernel(
     gate_out[(size_t)(b - nq - 2 * nk) * kHd + lane] = val;
     return;
   }
-  const bool is_v = b >= nq + nk;
-  float out = val;
-  if (!is_v) {
-    const double xd = val;
-    const double ss = nd::wave_sum(xd * xd);
-    const double inv = 1.0 / sqrt(ss / kHd + 1e-6);
-    const double normed = (float)((1.0 + (double)nscale) * xd * inv);
-    double sn, cs;
-    sincos((double)pos * invf, &sn, &cs);
-    const double other = __shfl_xor(normed, 32, 64);
-    out = lane < 32 ? (float)(normed * cs - other * sn) : (float)(normed * cs + other * sn);
-    if (b < nq) {
-      q_out[(size_t)b * kHd + lane] = out;
-      return;
+  const int role = b < nq ? 0 : (b < nq + nk ? 1 : 2);
+  const uint32_t h = role == 0 ? b : (role == 1 ? b - nq : b - nq - nk);
+  head_epilogue(val, lane, role, pos, nscale, invf, q_out + (size_t)h * kHd, Kc, Vc, Ks, Vs,
+                ((size_t)layer * kv_heads + h) * alloc, kv_slot(pos, sink, window), alloc);
+}
+
+// ---------------------------------------------------------------- prefill
+// NeedleRuntime.prefill runs one step per prompt token (runtime.ts:227-243).
+// The batched form below gives each of M prompt positions its own row and
+// runs every layer for all of them at once: the projections become int8
+// MFMA GEMMs (digit-sliced, exact to 2^-22 of a row's largest entry), the
+// one-workgroup parts become one workgroup per position, and causal
+// attention reads the int8 cache, which holds every earlier position because
+// each position's K/V is appended before any attention of the layer runs.
+// It applies while the prompt's cache slots do not wrap (positions < slots),
+// which keeps every position a later query can see in the cache.
+
+// Per position: token from the prompt in `history`, engram hashes, scaled
+// embedding in every lane, concatenated engram rows; workgroup 0 advances the
+// position counters past the batch.
+__global__ __launch_bounds__(kWg) void n2_begin_batch_kernel(BeginArgs a, uint32_t p0,
+                                                             uint32_t count,
+                                                             uint32_t* __restrict__ positions) {
+  __shared__ uint32_t s_idx[16], s_valid[16];
+  const uint32_t m = blockIdx.x, t = threadIdx.x, pos = p0 + m;
+  const uint32_t tok = a.history[pos];
+  if (t == 0) {
+    positions[m] = pos;
+    if (m == 0) {
+      a.st[0] = p0 + count;
+      a.st[1] = p0 + count - 1;
     }
   }
-  const uint32_t h = is_v ? b - nq - nk : b - nq;
-  const uint32_t slot = kv_slot(pos, sink, window);
-  if (slot >= alloc) return;  // the host keeps positions below the runtime limit
-  const size_t crow = ((size_t)layer * kv_heads + h) * alloc + slot;
-  const float am = wave_absmax_js(out);
-  const double mx = (am != am) ? (double)am : fmax(1e-12, (double)am);
-  const double sc = mx / 127.0;
-  const double code = rint((double)out / sc);
-  (is_v ? Vc : Kc)[crow * kHd + lane] = code != code ? (int8_t)0 : (int8_t)(int)code;
-  if (lane == 0) (is_v ? Vs : Ks)[crow] = (float)sc;
+  if (t < a.tables) {
+    const uint32_t order = a.orders[t / a.per_order];
+    uint32_t hash = 0x9E3779B9u * (t + 1);
+    bool valid = true;
+    for (uint32_t off = 0; off < order; ++off) {
+      const bool in = off <= pos;
+      const uint32_t token = in ? a.history[pos - off] : 0u;
+      hash = (hash ^ token) * 0x01000193u;
+      if (off == order - 1) valid = in;
+    }
+    hash ^= hash >> 15;
+    s_idx[t] = hash % a.slots;
+    s_valid[t] = valid ? 1u : 0u;
+  }
+  __syncthreads();
+  float* x = a.x + (size_t)m * a.lanes * a.d;
+  for (uint32_t k = t; k < a.d; k += kWg) {
+    const float row = (float)a.emb[(size_t)tok * a.d + k] * a.emb_s[tok];
+    const float v = (float)((double)row * a.scale);
+    for (uint32_t l = 0; l < a.lanes; ++l) x[(size_t)l * a.d + k] = v;
+  }
+  const uint32_t per_site = a.tables * a.sub;
+  float* cat = a.cat + (size_t)m * a.n_sites * per_site;
+  for (uint32_t i = t; i < a.n_sites * per_site; i += kWg) {
+    const uint32_t s = i / per_site, j = i % per_site, tb = j / a.sub, c = j % a.sub;
+    float v = 0.f;
+    if (s_valid[tb]) {
+      const size_t row = (size_t)tb * a.slots + s_idx[tb];
+      v = (float)a.tw[s][row * a.sub + c] * a.ts[s][row];
+    }
+    cat[i] = v;
+  }
+}
+
+// The engram convolution of position p0 + m (runtime.ts:854-872): value rows
+// of batch positions come from this batch's projections ekv[m'][s] = [key |
+// value], older ones from the ring (which the batch does not touch here).
+__global__ void n2_conv_batch_kernel(const float* __restrict__ ekv, const float* __restrict__ ring,
+                                     const float* __restrict__ taps, uint32_t d, uint32_t depth,
+                                     uint32_t n_taps, uint32_t max_order, uint32_t n_sites,
+                                     uint32_t p0, float* __restrict__ mixed) {
+  const uint32_t m = blockIdx.x, s = blockIdx.y, i = threadIdx.x;
+  if (i >= d) return;
+  const uint32_t pos = p0 + m;
+  float acc = 0.f;
+  for (uint32_t tap = 0; tap < n_taps; ++tap) {
+    if (tap * max_order > pos) continue;
+    const uint32_t prev = pos - tap * max_order;
+    const float v = prev >= p0
+        ? ekv[((size_t)(prev - p0) * n_sites + s) * 2 * d + d + i]
+        : ring[((size_t)s * depth + prev % depth) * d + i];
+    acc = (float)((double)acc + (double)taps[((size_t)s * n_taps + tap) * d + i] * (double)v);
+  }
+  mixed[((size_t)m * n_sites + s) * d + i] = acc;
+}
+
+// After the convolution: the ring keeps the value rows of the batch's last
+// `depth` positions.
+__global__ void n2_ring_store_kernel(const float* __restrict__ ekv, float* __restrict__ ring,
+                                     uint32_t d, uint32_t depth, uint32_t n_sites, uint32_t p0,
+                                     uint32_t count) {
+  const uint32_t j = blockIdx.x, s = blockIdx.y, i = threadIdx.x;
+  const uint32_t first = count > depth ? count - depth : 0;
+  const uint32_t m = first + j;
+  if (i >= d || m >= count) return;
+  const uint32_t pos = p0 + m;
+  ring[((size_t)s * depth + pos % depth) * d + i] =
+      ekv[((size_t)m * n_sites + s) * 2 * d + d + i];
+}
+
+// Query/key norm + RoPE and the K/V append of every batch position: one wave
+// per (head, position); qkvg rows [q | k | v | gate] with stride ld.
+__global__ __launch_bounds__(64) void n2_rope_store_batch_kernel(
+    const float* __restrict__ qkvg, uint32_t ld, uint32_t heads, uint32_t kv_heads,
+    const float* __restrict__ q_norm, const float* __restrict__ k_norm,
+    const double* __restrict__ inv_freq, uint32_t p0, float* __restrict__ q_out,
+    int8_t* __restrict__ Kc, int8_t* __restrict__ Vc, float* __restrict__ Ks,
+    float* __restrict__ Vs, uint32_t layer, uint32_t alloc, uint32_t sink, uint32_t window) {
+  const uint32_t b = blockIdx.x, m = blockIdx.y, lane = threadIdx.x, pos = p0 + m;
+  const int role = b < heads ? 0 : (b < heads + kv_heads ? 1 : 2);
+  const uint32_t h = role == 0 ? b : (role == 1 ? b - heads : b - heads - kv_heads);
+  const float val = qkvg[(size_t)m * ld + (size_t)b * kHd + lane];
+  head_epilogue(val, lane, role, pos, role == 0 ? q_norm[lane] : k_norm[lane],
+                inv_freq[lane & 31], q_out + ((size_t)m * heads + h) * kHd, Kc, Vc, Ks, Vs,
+                ((size_t)layer * kv_heads + h) * alloc, kv_slot(pos, sink, window), alloc);
 }
 
 size_t al(size_t n) { return (n + 255) & ~size_t(255); }
@@ -634,13 +807,23 @@ struct nd_needle {
   nd_kv kv{};
   char* arena = nullptr;
   size_t state_bytes = 0;  // leading part of the arena cleared by reset
-  uint32_t *st = nullptr, *history = nullptr, *sel_id = nullptr, *allowed = nullptr;
+  uint32_t *st = nullptr, *history = nullptr, *sel_id = nullptr, *allowed = nullptr,
+           *counters = nullptr;
   double *lp_history = nullptr, *sel_lp = nullptr;
   float *ring = nullptr, *x = nullptr, *upd = nullptr, *blk = nullptr, *ain = nullptr,
         *qkvg = nullptr, *q = nullptr, *att = nullptr, *proj = nullptr, *phi_post_v = nullptr,
         *phi_res_v = nullptr, *fin = nullptr, *logits = nullptr, *cat = nullptr, *ekv_out = nullptr,
-        *evals = nullptr, *partials = nullptr;
+        *evals = nullptr, *partials = nullptr, *route = nullptr;
   uint32_t max_length = 0, sink = 0, position = 0;
+  // Batched prefill buffers (first prefill), for up to pf_cap positions a pass.
+  char* pf_arena = nullptr;
+  uint32_t pf_cap = 0;
+  float *pf_x = nullptr, *pf_upd = nullptr, *pf_blk = nullptr, *pf_ain = nullptr,
+        *pf_phi_post = nullptr, *pf_phi_res = nullptr, *pf_route = nullptr, *pf_qkvg = nullptr,
+        *pf_q = nullptr, *pf_att = nullptr, *pf_proj = nullptr, *pf_cat = nullptr,
+        *pf_ekv = nullptr, *pf_evals = nullptr, *pf_fm = nullptr, *pf_partials = nullptr;
+  int8_t* pf_digits = nullptr;
+  uint32_t *pf_positions = nullptr, *pf_counters = nullptr;
   // Step graphs, valid for (graph_alloc, graph_sink).
   hipGraphExec_t graphs[3] = {nullptr, nullptr, nullptr};
   uint32_t graph_alloc = 0, graph_sink = 0;
@@ -711,6 +894,12 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
   for (uint32_t l = 0; l <= d.layers; ++l) {
     const bool pre = l < d.layers;
     if (!pre && !tail) break;
+    // Every operand pointer is valid whether or not its half runs (the
+    // kernel loads them unconditionally): an absent layer reads layer 0's.
+    const uint32_t pl = l > 0 ? l - 1 : 0, ql = pre ? l : 0;
+    int site = -1;
+    for (uint32_t si = 0; si < d.n_sites; ++si)
+      if (pre && d.sites[si] == l) site = (int)si;
     MixArgs m{};
     m.x = n->x;
     m.d = D;
@@ -721,56 +910,54 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
     m.ain = n->ain;
     m.phi_post = n->phi_post_v;
     m.phi_res = n->phi_res_v;
-    if (l > 0) {
-      const uint32_t p = l - 1;
-      m.has_post = 1;
-      m.own_post = p % ln;
-      m.proj = n->proj;
-      m.post_norm = n->params + n->o_post + (size_t)p * D;
-      m.pre_h_norm = n->params + n->o_preh + (size_t)p * D;
-      m.d1 = n->params + n->o_d1 + (size_t)p * D;
-      m.d2 = n->params + n->o_d2 + (size_t)p * d.hadamard;
-      m.d3 = n->params + n->o_d3 + (size_t)p * D;
-      m.attention_gate = n->attention_gate[p];
-      m.a_post = n->a_post[p];
-      m.a_res = n->a_res[p];
-      m.b_post = n->params + n->o_bpost + (size_t)p * ln;
-      m.b_res = n->params + n->o_bres + (size_t)p * ln * ln;
-    }
-    if (pre) {
-      int site = -1;
-      for (uint32_t si = 0; si < d.n_sites; ++si)
-        if (d.sites[si] == l) site = (int)si;
-      m.has_pre = 1;
-      m.own_pre = l % ln;
-      m.phi_w[0] = n->phi_pre->w + (size_t)l * ln * K;
-      m.phi_s[0] = n->phi_pre->scales + (size_t)l * ln;
-      m.phi_w[1] = n->phi_post->w + (size_t)l * ln * K;
-      m.phi_s[1] = n->phi_post->scales + (size_t)l * ln;
-      m.phi_w[2] = n->phi_res->w + (size_t)l * ln * ln * K;
-      m.phi_s[2] = n->phi_res->scales + (size_t)l * ln * ln;
-      m.a_pre = n->a_pre[l];
-      m.b_pre = n->params + n->o_bpre + (size_t)l * ln;
-      m.ekey = site >= 0 ? n->ekv_out + (size_t)site * 2 * D : nullptr;
-      m.evalue = site >= 0 ? n->evals + (size_t)site * D : nullptr;
-      m.norm_input = n->params + n->o_norm_input + (size_t)l * D;
-    } else {
-      m.has_final = 1;
-      m.final_norm = n->params + n->o_final;
-      m.fin = n->fin;
-    }
+    m.has_post = l > 0;
+    m.proj = n->proj;
+    m.post_norm = n->params + n->o_post + (size_t)pl * D;
+    m.pre_h_norm = n->params + n->o_preh + (size_t)pl * D;
+    m.d1 = n->params + n->o_d1 + (size_t)pl * D;
+    m.d2 = n->params + n->o_d2 + (size_t)pl * d.hadamard;
+    m.d3 = n->params + n->o_d3 + (size_t)pl * D;
+    m.attention_gate = n->attention_gate[pl];
+    m.route = n->route;
+    m.has_pre = pre;
+    m.own_pre = ql % ln;
+    m.phi_w[0] = n->phi_pre->w + (size_t)ql * ln * K;
+    m.phi_s[0] = n->phi_pre->scales + (size_t)ql * ln;
+    m.phi_w[1] = n->phi_post->w + (size_t)ql * ln * K;
+    m.phi_s[1] = n->phi_post->scales + (size_t)ql * ln;
+    m.phi_w[2] = n->phi_res->w + (size_t)ql * ln * ln * K;
+    m.phi_s[2] = n->phi_res->scales + (size_t)ql * ln * ln;
+    m.a_pre = n->a_pre[ql];
+    m.b_pre = n->params + n->o_bpre + (size_t)ql * ln;
+    m.has_site = site >= 0;
+    m.ekey = n->ekv_out + (size_t)(site >= 0 ? site : 0) * 2 * D;
+    m.evalue = n->evals + (size_t)(site >= 0 ? site : 0) * D;
+    m.norm_input = n->params + n->o_norm_input + (size_t)ql * D;
+    m.has_final = !pre;
+    m.final_norm = n->params + n->o_final;
+    m.fin = n->fin;
     hipLaunchKernelGGL(n2_mix_kernel, dim3(1), dim3(kMixWg), 0, s, m);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (!pre) break;
     const nd_mat& wm = n->wqkvg[l];
-    hipLaunchKernelGGL(n2_qkv_kernel, dim3(wm.n / kHd), dim3(256), 0, s, wm.w, wm.scales, n->ain,
-                       D, d.heads, d.kv_heads, n->st, n->params + n->o_qn + (size_t)l * kHd,
-                       n->params + n->o_kn + (size_t)l * kHd, n->inv_freq, n->q, n->qkvg,
-                       (int8_t*)n->kv.k, (int8_t*)n->kv.v, n->kv.ks, n->kv.vs, l, n->kv.alloc,
-                       n->kv.sink, n->kv.window);
+    RouteArgs ra{};
+    ra.phi_post = n->phi_post_v;
+    ra.phi_res = n->phi_res_v;
+    ra.a_post = n->a_post[l];
+    ra.a_res = n->a_res[l];
+    ra.b_post = n->params + n->o_bpost + (size_t)l * ln;
+    ra.b_res = n->params + n->o_bres + (size_t)l * ln * ln;
+    ra.lanes = ln;
+    ra.own = l % ln;
+    ra.route = n->route;
+    hipLaunchKernelGGL(n2_qkv_kernel, dim3(wm.n / kHd + 1), dim3(256), 0, s, wm.w, wm.scales,
+                       n->ain, D, d.heads, d.kv_heads, n->st,
+                       n->params + n->o_qn + (size_t)l * kHd, n->params + n->o_kn + (size_t)l * kHd,
+                       n->inv_freq, n->q, n->qkvg, (int8_t*)n->kv.k, (int8_t*)n->kv.v, n->kv.ks,
+                       n->kv.vs, l, n->kv.alloc, n->kv.sink, n->kv.window, ra);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     e = nd_launch_attention_gated(&n->kv, l, n->st + 1, n->max_length - 1, n->q, d.heads, n->qkvg,
-                                  n->att, n->partials, s);
+                                  n->att, n->partials, n->counters, s);
     if (e != hipSuccess) return e;
     if ((e = nd_launch_matvec(n->wo[l], n->att, 1, qw, 0, D, n->proj, D, s)) != hipSuccess)
       return e;
@@ -811,6 +998,241 @@ nd_status launch_graph(nd_ctx* ctx, nd_needle* n, GraphKind kind) {
     }
   }
   ND_HIP(ctx, hipGraphLaunch(n->graphs[kind], s));
+  return ND_OK;
+}
+
+// Buffers of the batched prefill, for up to pf_cap positions per pass.
+nd_status ensure_prefill(nd_ctx* ctx, nd_needle* n) {
+  if (n->pf_arena) return ND_OK;
+  const nd_needle_desc& d = n->d;
+  const uint32_t cap = std::min<uint32_t>(d.max_length, kPrefillRows);
+  const uint32_t D = d.dim, ln = d.lanes, qw = d.heads * kHd, kw = d.kv_heads * kHd;
+  const uint32_t S = d.n_sites ? d.n_sites : 1, cat = d.n_sites ? d.engram_tables * d.engram_sub : 1;
+  const uint32_t kmax = std::max(std::max(D, qw), cat);
+  const size_t pf = nd_attention_batch_partial_floats(cap, d.kv_heads, d.heads / d.kv_heads,
+                                                      d.max_length);
+  const size_t sizes[] = {al((size_t)cap * ln * D * 4), al((size_t)cap * D * 4),
+                          al((size_t)cap * D * 4),      al((size_t)cap * D * 4),
+                          al((size_t)cap * ln * 4),     al((size_t)cap * ln * ln * 4),
+                          al((size_t)cap * 20 * 4),     al((size_t)cap * (2 * qw + 2 * kw) * 4),
+                          al((size_t)cap * qw * 4),     al((size_t)cap * qw * 4),
+                          al((size_t)cap * D * 4),      al((size_t)cap * S * cat * 4),
+                          al((size_t)cap * S * 2 * D * 4), al((size_t)cap * S * D * 4),
+                          al((size_t)cap * 4),          al(pf * 4),
+                          al((size_t)3 * cap * kmax),   al((size_t)cap * 4),
+                          al((size_t)cap * d.kv_heads * 4)};
+  size_t total = 0;
+  for (size_t v : sizes) total += v;
+  hipError_t e = hipMalloc(&n->pf_arena, total);
+  if (e == hipSuccess) e = hipMemsetAsync(n->pf_arena, 0, total, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    if (n->pf_arena) hipFree(n->pf_arena);
+    n->pf_arena = nullptr;
+    return nd_hip_fail(ctx, e, "Needle prefill allocation");
+  }
+  char* p = n->pf_arena;
+  size_t i = 0;
+  auto take = [&](auto** dst) {
+    *dst = reinterpret_cast<std::remove_reference_t<decltype(**dst)>*>(p);
+    p += sizes[i++];
+  };
+  take(&n->pf_x);
+  take(&n->pf_upd);
+  take(&n->pf_blk);
+  take(&n->pf_ain);
+  take(&n->pf_phi_post);
+  take(&n->pf_phi_res);
+  take(&n->pf_route);
+  take(&n->pf_qkvg);
+  take(&n->pf_q);
+  take(&n->pf_att);
+  take(&n->pf_proj);
+  take(&n->pf_cat);
+  take(&n->pf_ekv);
+  take(&n->pf_evals);
+  take(&n->pf_fm);
+  take(&n->pf_partials);
+  take(&n->pf_digits);
+  take(&n->pf_positions);
+  take(&n->pf_counters);
+  n->pf_cap = cap;
+  return ND_OK;
+}
+
+// Enqueues `count` prompt tokens (already in history at [position, position
+// + count)) as one batched pass; the host checks that the slots do not wrap
+// and that count <= pf_cap.  want_logits / select: the last position's
+// logits (and selection over all ids) as a step would produce them.
+hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool select,
+                           hipStream_t s) {
+  const nd_needle_desc& d = n->d;
+  const uint32_t D = d.dim, ln = d.lanes, qw = d.heads * kHd, kw = d.kv_heads * kHd;
+  const uint32_t M = count, p0 = n->position, N = ln * D;
+  const uint32_t S = d.n_sites ? d.n_sites : 1, cat = d.engram_tables * d.engram_sub;
+  const uint32_t qkv_ld = 2 * qw + 2 * kw;
+  BeginArgs b{};
+  b.st = n->st;
+  b.history = n->history;
+  b.emb = n->embedding->w;
+  b.emb_s = n->embedding->scales;
+  b.d = D;
+  b.lanes = ln;
+  b.scale = std::sqrt((double)D);
+  b.x = n->pf_x;
+  for (uint32_t si = 0; si < d.n_sites; ++si) {
+    b.tw[si] = n->eg_tables[si]->w;
+    b.ts[si] = n->eg_tables[si]->scales;
+  }
+  b.n_sites = d.n_sites;
+  b.tables = d.n_sites ? d.engram_tables : 0;
+  b.slots = d.engram_slots;
+  b.sub = d.engram_sub;
+  b.n_orders = d.n_orders;
+  b.per_order = d.n_orders ? d.engram_tables / d.n_orders : 1;
+  for (uint32_t i = 0; i < d.n_orders; ++i) b.orders[i] = d.orders[i];
+  b.cat = n->pf_cat;
+  hipLaunchKernelGGL(n2_begin_batch_kernel, dim3(M), dim3(kWg), 0, s, b, p0, M, n->pf_positions);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (d.n_sites) {
+    for (uint32_t si = 0; si < d.n_sites; ++si) {
+      if ((e = nd_launch_digitize(n->pf_cat + (size_t)si * cat, S * cat, nullptr, nullptr,
+                                  n->pf_digits, n->pf_fm, M, cat, s)) != hipSuccess)
+        return e;
+      if ((e = nd_launch_gemm(&n->ekv[si], n->pf_digits, n->pf_fm, n->pf_ekv + (size_t)si * 2 * D,
+                              S * 2 * D, M, 0, s)) != hipSuccess)
+        return e;
+    }
+    const uint32_t threads = (D + 63) / 64 * 64;
+    hipLaunchKernelGGL(n2_conv_batch_kernel, dim3(M, d.n_sites), dim3(threads), 0, s, n->pf_ekv,
+                       n->ring, n->params + n->o_taps, D, n->depth, d.engram_taps, n->max_order,
+                       d.n_sites, p0, n->pf_evals);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(n2_ring_store_kernel, dim3(std::min(M, n->depth), d.n_sites), dim3(threads),
+                       0, s, n->pf_ekv, n->ring, D, n->depth, d.n_sites, p0, M);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  const size_t K = (size_t)N;
+  for (uint32_t l = 0; l <= d.layers; ++l) {
+    const bool pre = l < d.layers;
+    if (!pre && !want_logits && !select) break;
+    const uint32_t pl = l > 0 ? l - 1 : 0, ql = pre ? l : 0;
+    const uint32_t rows = pre ? M : 1, r0 = pre ? 0 : M - 1;  // the final part: last row only
+    int site = -1;
+    for (uint32_t si = 0; si < d.n_sites; ++si)
+      if (pre && d.sites[si] == l) site = (int)si;
+    MixArgs m{};
+    m.x = n->pf_x + (size_t)r0 * N;
+    m.d = D;
+    m.hdim = d.hadamard;
+    m.lanes = ln;
+    m.upd = n->pf_upd + (size_t)r0 * D;
+    m.blk = n->pf_blk + (size_t)r0 * D;
+    m.ain = n->pf_ain + (size_t)r0 * D;
+    m.phi_post = n->pf_phi_post + (size_t)r0 * ln;
+    m.phi_res = n->pf_phi_res + (size_t)r0 * ln * ln;
+    m.has_post = l > 0;
+    m.proj = n->pf_proj + (size_t)r0 * D;
+    m.post_norm = n->params + n->o_post + (size_t)pl * D;
+    m.pre_h_norm = n->params + n->o_preh + (size_t)pl * D;
+    m.d1 = n->params + n->o_d1 + (size_t)pl * D;
+    m.d2 = n->params + n->o_d2 + (size_t)pl * d.hadamard;
+    m.d3 = n->params + n->o_d3 + (size_t)pl * D;
+    m.attention_gate = n->attention_gate[pl];
+    m.route = n->pf_route + (size_t)r0 * 20;
+    m.has_pre = pre;
+    m.own_pre = ql % ln;
+    m.phi_w[0] = n->phi_pre->w + (size_t)ql * ln * K;
+    m.phi_s[0] = n->phi_pre->scales + (size_t)ql * ln;
+    m.phi_w[1] = n->phi_post->w + (size_t)ql * ln * K;
+    m.phi_s[1] = n->phi_post->scales + (size_t)ql * ln;
+    m.phi_w[2] = n->phi_res->w + (size_t)ql * ln * ln * K;
+    m.phi_s[2] = n->phi_res->scales + (size_t)ql * ln * ln;
+    m.a_pre = n->a_pre[ql];
+    m.b_pre = n->params + n->o_bpre + (size_t)ql * ln;
+    m.has_site = site >= 0;
+    m.ekey = n->pf_ekv + (size_t)(site >= 0 ? site : 0) * 2 * D;
+    m.evalue = n->pf_evals + (size_t)(site >= 0 ? site : 0) * D;
+    m.ek_ld = S * 2 * D;
+    m.ev_ld = S * D;
+    m.norm_input = n->params + n->o_norm_input + (size_t)ql * D;
+    m.has_final = !pre;
+    m.final_norm = n->params + n->o_final;
+    m.fin = n->fin;
+    if (pre) {
+      m.route_out = n->pf_route;
+      m.r_a_post = n->a_post[l];
+      m.r_a_res = n->a_res[l];
+      m.r_b_post = n->params + n->o_bpost + (size_t)l * ln;
+      m.r_b_res = n->params + n->o_bres + (size_t)l * ln * ln;
+    }
+    hipLaunchKernelGGL(n2_mix_kernel, dim3(rows), dim3(kMixWg), 0, s, m);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (!pre) break;
+    if ((e = nd_launch_digitize(n->pf_ain, D, nullptr, nullptr, n->pf_digits, n->pf_fm, M, D, s)) !=
+        hipSuccess)
+      return e;
+    if ((e = nd_launch_gemm(&n->wqkvg[l], n->pf_digits, n->pf_fm, n->pf_qkvg, qkv_ld, M, 0, s)) !=
+        hipSuccess)
+      return e;
+    hipLaunchKernelGGL(n2_rope_store_batch_kernel, dim3(d.heads + 2 * d.kv_heads, M), dim3(64), 0,
+                       s, n->pf_qkvg, qkv_ld, d.heads, d.kv_heads,
+                       n->params + n->o_qn + (size_t)l * kHd, n->params + n->o_kn + (size_t)l * kHd,
+                       n->inv_freq, p0, n->pf_q, (int8_t*)n->kv.k, (int8_t*)n->kv.v, n->kv.ks,
+                       n->kv.vs, l, n->kv.alloc, n->kv.sink, n->kv.window);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    e = nd_launch_attention_batch(&n->kv, l, n->pf_positions, M, d.kv_heads, 0u,
+                                  d.heads / d.kv_heads, p0 + M - 1, n->pf_q, n->pf_att,
+                                  n->pf_partials, n->pf_counters, s, n->pf_qkvg + qw + 2 * kw,
+                                  qkv_ld);
+    if (e != hipSuccess) return e;
+    if ((e = nd_launch_digitize(n->pf_att, qw, nullptr, nullptr, n->pf_digits, n->pf_fm, M, qw,
+                                s)) != hipSuccess)
+      return e;
+    if ((e = nd_launch_gemm(n->wo[l], n->pf_digits, n->pf_fm, n->pf_proj, D, M, 0, s)) !=
+        hipSuccess)
+      return e;
+  }
+  if (!want_logits && !select) return hipSuccess;
+  e = nd_launch_matvec(n->embedding, n->fin, 1, D, 0, d.vocab, n->logits, d.vocab, s);
+  if (e != hipSuccess || !select) return e;
+  return nd_launch_select_list(n->logits, d.vocab, nullptr, 0, n->sel_id, n->sel_lp, s);
+}
+
+// Runs the prompt tokens already in history at [position, position + count):
+// batched passes while the cache slots do not wrap, steps after that.  The
+// last token produces logits (and a selection over all ids when select).
+nd_status run_prompt(nd_ctx* ctx, nd_needle* n, uint32_t count, bool want_logits, bool select,
+                     bool graphs) {
+  nd_status st = ensure_prefill(ctx, n);
+  if (st != ND_OK) return st;
+  hipStream_t s = ctx->stream;
+  uint32_t done = 0;
+  while (done < count) {
+    const uint32_t left = count - done;
+    const uint32_t room = n->kv.alloc > n->position ? n->kv.alloc - n->position : 0;
+    const uint32_t chunk = std::min(std::min(left, n->pf_cap), room);
+    const bool last_pass = chunk == left;
+    if (chunk > 0) {
+      ND_HIP(ctx, enqueue_prefill(n, chunk, last_pass && want_logits, last_pass && select, s));
+      n->position += chunk;
+      done += chunk;
+      continue;
+    }
+    // Slots wrap from here on: one step per token.
+    const bool last = left == 1;
+    if (graphs) {
+      if ((st = launch_graph(ctx, n, last && (want_logits || select) ? kGraphPromptSelect
+                                                                     : kGraphPrompt)) != ND_OK)
+        return st;
+    } else {
+      ND_HIP(ctx, enqueue_step(n, kTokenHistory, 0, last && want_logits, last && select, nullptr, 0,
+                               s));
+    }
+    ++n->position;
+    ++done;
+  }
   return ND_OK;
 }
 
@@ -985,6 +1407,7 @@ nd_status nd_needle_free(nd_ctx* ctx, nd_needle* n) {
   hipStreamSynchronize(ctx->stream);
   drop_graphs(n);
   if (n->arena) hipFree(n->arena);
+  if (n->pf_arena) hipFree(n->pf_arena);
   for (auto* v : {&n->wqkvg, &n->ekv})
     for (auto& m : *v) {
       if (m.w) hipFree(m.w);
@@ -1013,13 +1436,13 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     const uint32_t cat = d.n_sites ? d.engram_tables * d.engram_sub : 1;
     // State first (cleared by every reset), then scratch.
     const size_t sizes[] = {al(64), al((size_t)cap * 4), al((size_t)cap * 8),
-                            al((size_t)S * n->depth * D * 4), al(64), al(64),
+                            al((size_t)S * n->depth * D * 4), al((size_t)d.kv_heads * 4), al(64), al(64),
                             al((size_t)d.vocab * 4), al(rows * kHd), al(rows * kHd), al(rows * 4),
                             al(rows * 4), al((size_t)ln * D * 4), al(D * 4), al(D * 4), al(D * 4),
                             al((size_t)(2 * qw + 2 * kw) * 4), al(qw * 4), al(qw * 4), al(D * 4),
                             al(ln * 4), al(ln * ln * 4), al(D * 4), al((size_t)d.vocab * 4),
                             al((size_t)S * cat * 4), al((size_t)S * 2 * D * 4),
-                            al((size_t)S * D * 4), al(pf * 4)};
+                            al((size_t)S * D * 4), al(pf * 4), al(20 * 4)};
     size_t total = 0;
     for (size_t v : sizes) total += v;
     ND_HIP(ctx, hipMalloc(&n->arena, total));
@@ -1033,6 +1456,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     take(&n->history);
     take(&n->lp_history);
     take(&n->ring);
+    take(&n->counters);
     n->state_bytes = (size_t)(p - n->arena);
     take(&n->sel_id);
     take(&n->sel_lp);
@@ -1060,6 +1484,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     take(&n->ekv_out);
     take(&n->evals);
     take(&n->partials);
+    take(&n->route);
   }
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
   ND_HIP(ctx, hipMemsetAsync(n->arena, 0, n->state_bytes, ctx->stream));
@@ -1112,11 +1537,8 @@ nd_status nd_needle_prefill(nd_ctx* ctx, nd_needle* n, const uint32_t* tokens, u
       return nd_fail(ctx, ND_ERR_INVALID, "Token %u is outside the vocabulary", tokens[i]);
   ND_HIP(ctx, hipMemcpyAsync(n->history + n->position, tokens, (size_t)count * 4,
                              hipMemcpyHostToDevice, ctx->stream));
-  for (uint32_t i = 0; i < count; ++i) {
-    const bool last = i + 1 == count;
-    ND_HIP(ctx, enqueue_step(n, kTokenHistory, 0, last && logits, false, nullptr, 0, ctx->stream));
-    ++n->position;
-  }
+  nd_status st = run_prompt(ctx, n, count, logits != nullptr, false, false);
+  if (st != ND_OK) return st;
   if (logits)
     ND_HIP(ctx, hipMemcpyAsync(logits, n->logits, (size_t)n->d.vocab * 4, hipMemcpyDeviceToHost,
                                ctx->stream));
@@ -1172,12 +1594,7 @@ nd_status nd_needle_generate(nd_ctx* ctx, nd_needle* n, const uint32_t* prompt, 
   ND_HIP(ctx, hipMemcpyAsync(n->history, prompt, (size_t)count * 4, hipMemcpyHostToDevice,
                              ctx->stream));
   const uint32_t n_gen = max_new ? std::min(max_new, max_len - count) : 0;
-  for (uint32_t i = 0; i + 1 < count; ++i) {
-    if ((st = launch_graph(ctx, n, kGraphPrompt)) != ND_OK) return st;
-    ++n->position;
-  }
-  if ((st = launch_graph(ctx, n, n_gen ? kGraphPromptSelect : kGraphPrompt)) != ND_OK) return st;
-  ++n->position;
+  if ((st = run_prompt(ctx, n, count, false, n_gen > 0, true)) != ND_OK) return st;
   // Token k (k < n_gen - 1) is stepped by decode step k, which records it and
   // its log-probability at history[count + k]; the last one stays in the
   // selection buffers.

@@ -187,3 +187,44 @@ def test_generate_full_geometry_greedy_identical(hip):
         np.testing.assert_allclose(res.token_log_probabilities, lps, rtol=1e-3, atol=1e-3)
     finally:
         model.dispose()
+
+
+@pytest.mark.parametrize("window,sink,n_prompt", [(0, 0, 40), (16, 3, 30), (8, 0, 33)])
+def test_batched_prefill_then_steps(hip, window, sink, n_prompt):
+    """Prompt positions whose cache slots do not wrap run as one batched pass
+    (int8 MFMA projections, one mix workgroup per position), the rest as
+    steps; logits, every appended KV row and the engram ring handed to the
+    following steps must agree with the oracle's sequential steps."""
+    say("needle2 batched prefill", window, sink, n_prompt)
+    g = Needle2Geometry(**{**SMALL.__dict__, "kv_window": window, "max_length": 64})
+    w = Needle2Weights(g, 41)
+    model = NeedleModel(hip, w)
+    try:
+        rt = model.create_runtime()
+        rt.reset(g.max_length, sink)
+        ref = oracle.Needle2(w).runtime(g.max_length, sink)
+        prompt = synth.Stream(12, f"n2pf{window}").integers(n_prompt, 0, g.vocab - 1)
+        prompt[10:13] = prompt[2:5]
+        got = rt.prefill(prompt)
+        for t in prompt:
+            want = ref.step(int(t))
+        close(got, want, "prefill logits")
+        alloc = min(g.max_length, sink + window) if window else g.max_length
+        written = min(n_prompt, alloc)  # slots fill in order; the rest were never stored
+        for layer in (0, g.layers - 1):
+            for h in range(g.kv_heads):
+                for a_, b_ in zip(model.session.kv_read(layer, h), ref.kv_read(layer, h)):
+                    a_, b_ = a_[:written], b_[:written]
+                    if a_.dtype == np.int8:
+                        d = np.abs(a_.astype(int) - b_.astype(int))
+                        assert d.max() <= 1 and (d == 0).mean() > 0.95, (layer, h)
+                    else:
+                        np.testing.assert_allclose(a_, b_, rtol=1e-3)
+        tok = int(np.argmax(got))
+        for i in range(6):  # steps after the batch read its engram ring and cache
+            want = ref.step(tok)
+            got = rt.step(tok)
+            close(got, want, ("step after prefill", i))
+            tok = int(np.argmax(want))
+    finally:
+        model.dispose()
