@@ -639,7 +639,8 @@ __global__ __launch_bounds__(256) void n2_qkv_kernel(
   i32x4 wv[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k)
-    if ((uint32_t)k * 16 < seg) wv[k] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(w + k * 16));
+    wv[k] = __builtin_nontemporal_load(  // clamped: unconditional loads issue back to back
+        reinterpret_cast<const i32x4*>(w + min((uint32_t)k * 16, seg - 16)));
   const float srow = S[row];
   const uint32_t pos = st[1];
   const uint32_t lane = t & 63;

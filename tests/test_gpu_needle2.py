@@ -189,14 +189,16 @@ def test_generate_full_geometry_greedy_identical(hip):
         model.dispose()
 
 
-@pytest.mark.parametrize("window,sink,n_prompt", [(0, 0, 40), (16, 3, 30), (8, 0, 33)])
-def test_batched_prefill_then_steps(hip, window, sink, n_prompt):
+@pytest.mark.parametrize("window,sink,n_prompt,max_length",
+                         [(0, 0, 40, 64), (16, 3, 30, 64), (8, 0, 33, 64), (0, 0, 280, 300)])
+def test_batched_prefill_then_steps(hip, window, sink, n_prompt, max_length):
     """Prompt positions whose cache slots do not wrap run as one batched pass
     (int8 MFMA projections, one mix workgroup per position), the rest as
     steps; logits, every appended KV row and the engram ring handed to the
-    following steps must agree with the oracle's sequential steps."""
-    say("needle2 batched prefill", window, sink, n_prompt)
-    g = Needle2Geometry(**{**SMALL.__dict__, "kv_window": window, "max_length": 64})
+    following steps must agree with the oracle's sequential steps (the
+    300-position case batches a prompt longer than one attention chunk)."""
+    say("needle2 batched prefill", window, sink, n_prompt, max_length)
+    g = Needle2Geometry(**{**SMALL.__dict__, "kv_window": window, "max_length": max_length})
     w = Needle2Weights(g, 41)
     model = NeedleModel(hip, w)
     try:
