@@ -385,6 +385,54 @@ def bench_needle2(torch, hip, reps, check, cpu_seconds):
     return part, cpu
 
 
+def traffic_workload(torch, hip, n, k, g, launches=64):
+    """The launches a pair of rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE)
+    measure: a 256 MiB device-to-device tensor copy (known bytes, to scale
+    the counters) and `launches` batch-1 matvecs over rotated HBM replicas."""
+    import ctypes as C
+
+    from needle_hip import lib as L
+    from needle_hip import synth
+
+    src = torch.rand(64 << 20, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    per = matvec_bytes(n, k, g, 1)
+    replicas = max(1, math.ceil(ROTATE_BYTES / per))
+    w, sc = synth.int8_matrix(2026, f"bench-w{n}x{k}", n, k, g)
+    mats = []
+    for _ in range(replicas):
+        h = C.c_void_p()
+        hip._check(hip.lib.nd_mat_upload_i8(hip.ctx, L.ptr(w), L.ptr(sc), n, k, g, C.byref(h)))
+        mats.append(h)
+    x = torch.from_numpy(synth.Stream(2026, "bench-x").normal((1, k))).cuda()
+    y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    for i in range(launches):
+        hip._check(hip.lib.nd_matvec_d(hip.ctx, mats[i % replicas], x.data_ptr(), 1, 0, n,
+                                        y.data_ptr(), C.c_void_p(stream)))
+    torch.cuda.synchronize()
+    for h in mats:
+        hip.lib.nd_mat_free(hip.ctx, h)
+    return {"copy_bytes_each_way": src.numel() * 4, "copies": 4, "matvec_launches": launches,
+            "matvec_bytes_per_launch": per}
+
+
+def measured_traffic():
+    """HBM bytes per matvec launch from the committed rocprofv3 --pmc summary
+    (profiles/matvec_i8_4096x4096_g32_b1_traffic.md, line 'traffic_bytes_per_launch: N'),
+    or None when it is absent."""
+    path = ROOT / "profiles" / "matvec_i8_4096x4096_g32_b1_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
+
+
 def cpu_baseline_matvec(n, k, g, seconds):
     """The oracle (one thread) on the same matvec workload, timed on this host."""
     import numpy as np
@@ -420,7 +468,8 @@ def main():
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--skip-needle2", action="store_true")
     ap.add_argument("--needle2-reps", type=int, default=5)
-    ap.add_argument("--only", choices=["matvec", "attention", "decode", "prefill", "needle2"],
+    ap.add_argument("--only", choices=["matvec", "attention", "decode", "prefill", "needle2",
+                                       "traffic"],
                     help="run one part alone and print its JSON (for profiling)")
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--no-check", action="store_true",
@@ -448,6 +497,8 @@ def main():
             part, _ = bench_constrained_decode(torch, hip, args.decode_steps, 2, False, 1, 0)
         elif args.only == "needle2":
             part, _ = bench_needle2(torch, hip, args.needle2_reps, False, 0)
+        elif args.only == "traffic":
+            part = traffic_workload(torch, hip, n, k, g)
         else:
             part, _ = bench_prefill(torch, hip, 2048, 5, 0)
         print(json.dumps({args.only: part}))
@@ -518,7 +569,8 @@ def main():
         "config": {"workload": "int8 matvec N=4096 K=4096 G=32 batch 1 (fp32 scales, fp32 x/y)",
                    "rotation_replicas": main_mv["replicas"]},
         "roofline": {"bound": "hbm", "achieved": round(main_mv["GBps"], 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(main_mv["frac_hbm"], 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(main_mv["frac_hbm"], 4),
+                     "traffic": measured_traffic(),
                      "kernel": "matvec_i8_kernel<B=1,SPT=1,RACC=8>",
                      "bytes_per_launch": main_mv["bytes_per_launch"]},
         "cpu_baseline": cpu,
