@@ -289,6 +289,26 @@ def bench_prefill(torch, hip, tokens_n, reps, cpu_seconds):
     return part, cpu
 
 
+def bench_copy_ceiling(torch, bytes_moved, steps, warmup):
+    """The runtime's own device copy moving the same number of bytes per
+    launch (half read, half written) under the same rotation and graph
+    timing: what one launch of this size reaches on this GPU."""
+    half = bytes_moved // 2 // 4
+    replicas = max(1, math.ceil(ROTATE_BYTES / (half * 4)))
+    srcs = [torch.rand(half, device="cuda") for _ in range(replicas)]
+    dst = torch.empty(half, device="cuda")
+
+    def make(src):
+        return lambda stream: dst.copy_(src)
+
+    timer = GraphTimer(torch, [make(srcs[i % replicas]) for i in range(max(replicas, 32))])
+    replays = max(1, math.ceil(steps / timer.n))
+    ms = timer.time(replays, warmup)
+    gbs = half * 8 / (ms * 1e-3) / 1e9
+    return {"bytes_per_launch": half * 8, "replicas": replicas, "ms_per_launch": ms,
+            "GBps": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
+
+
 def needle2_token_bytes(g, visible):
     """HBM bytes one Needle 2 token reads: int8 codes + f32 row scales of every
     matrix it multiplies, the engram rows it gathers and `visible` K/V rows
@@ -343,7 +363,9 @@ def bench_needle2(torch, hip, reps, check, cpu_seconds):
             "prefill_128_ms": prefill_ms, "prefill_tokens_per_s": 128 / wall1,
             "bytes_per_token": bytes_tok,
             "decode_GBps": bytes_tok / (decode_ms * 1e-3) / 1e9,
-            "launches_per_token": 6 * g.layers + 2 + len(g.sites) + 3}
+            # begin, engram projections + convolution, per layer mix / QKV /
+            # attention / Wo, the final mix, lm head and selection
+            "launches_per_token": 2 + len(g.sites) + 4 * g.layers + 3}
     part["decode_frac_hbm"] = part["decode_GBps"] / HBM_PEAK_GBS
     ref = oracle.Needle2(weights)
     cpu = None
@@ -519,6 +541,12 @@ def main():
               f"{parts[f'attention_L{length}_hbm']['GBps']:.0f} GB/s", file=sys.stderr, flush=True)
     parts["attention_L8192_mall"] = bench_attention(torch, hip, 8192, 8, args.steps // 2,
                                                     args.warmup, rotate=False)
+    for name, nbytes in (("copy_ceiling_matvec_bytes", main_mv["bytes_per_launch"]),
+                         ("copy_ceiling_attention_L8192_bytes",
+                          parts["attention_L8192_hbm"]["bytes_per_call"])):
+        parts[name] = bench_copy_ceiling(torch, nbytes, args.steps, args.warmup)
+        print(f"[bench] {name}: {parts[name]['GBps']:.0f} GB/s "
+              f"({parts[name]['ms_per_launch'] * 1e3:.2f} us)", file=sys.stderr, flush=True)
     if not args.skip_decode:
         part, cpu_dec = bench_constrained_decode(
             torch, hip, args.decode_steps, 2, not args.no_check, args.check_threads,
