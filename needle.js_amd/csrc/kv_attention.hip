@@ -6,6 +6,7 @@
 // 16-position x 64-dim tile is one contiguous 1 KiB run that a wave reads
 // with 128-bit loads.
 #include "nd_internal.hpp"
+#include "nd_wave.hpp"
 
 namespace {
 
@@ -246,16 +247,17 @@ __global__ __launch_bounds__(256) void attention_kernel(
         float d = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) d = fmaf(q[h][i], kc[i], d);
-        d += __shfl_xor(d, 1, 64);
-        d += __shfl_xor(d, 2, 64);
+        d = nd::quad_sum(d);
         p[h][k] = valid[k] ? d * cur.ks[k] * score_scale : -INFINITY;
       }
     }
 #pragma unroll
     for (int h = 0; h < REP; ++h) {
       float tile_max = fmaxf(fmaxf(p[h][0], p[h][1]), fmaxf(p[h][2], p[h][3]));
-#pragma unroll
-      for (int o = 4; o <= 32; o <<= 1) tile_max = fmaxf(tile_max, __shfl_xor(tile_max, o, 64));
+      tile_max = fmaxf(tile_max, nd::lane_xor<4>(tile_max));
+      tile_max = fmaxf(tile_max, nd::lane_xor<8>(tile_max));
+      tile_max = fmaxf(tile_max, nd::lane_xor<16>(tile_max));
+      tile_max = fmaxf(tile_max, nd::lane_xor<32>(tile_max));
       const float m_new = fmaxf(m[h], tile_max);
       const float alpha = __expf(m[h] - m_new);  // 0 on the first tile (m = -inf)
       m[h] = m_new;
@@ -288,11 +290,16 @@ __global__ __launch_bounds__(256) void attention_kernel(
   __shared__ float s_acc[kWaves][REP * kHeadDim];
 #pragma unroll
   for (int h = 0; h < REP; ++h) {
+    l[h] += nd::lane_xor<4>(l[h]);
+    l[h] += nd::lane_xor<8>(l[h]);
+    l[h] += nd::lane_xor<16>(l[h]);
+    l[h] += nd::lane_xor<32>(l[h]);
 #pragma unroll
-    for (int o = 4; o <= 32; o <<= 1) {
-      l[h] += __shfl_xor(l[h], o, 64);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[h][i] += __shfl_xor(acc[h][i], o, 64);
+    for (int i = 0; i < 16; ++i) {
+      acc[h][i] += nd::lane_xor<4>(acc[h][i]);
+      acc[h][i] += nd::lane_xor<8>(acc[h][i]);
+      acc[h][i] += nd::lane_xor<16>(acc[h][i]);
+      acc[h][i] += nd::lane_xor<32>(acc[h][i]);
     }
     if (trow == 0) {
 #pragma unroll

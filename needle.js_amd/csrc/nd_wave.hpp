@@ -69,6 +69,27 @@ __device__ __forceinline__ float wave_max_js(float v) {
   return js_max(js_max(readlane(v, 0), readlane(v, 16)), js_max(readlane(v, 32), readlane(v, 48)));
 }
 
+// Row rotations (lane i of a row of 16 reads lane (i - n) mod 16), checked
+// on gfx950.
+constexpr int kRowRor4 = 0x124;
+constexpr int kRowRor8 = 0x128;   // = lane xor 8
+constexpr int kRowRor12 = 0x12C;
+
+// The value of lane (lane xor m), for m in {1, 2, 4, 8, 16, 32}: DPP within a
+// row of 16, ds_swizzle (no memory access) for 16, ds_bpermute for 32.
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+  if constexpr (M == 1) return dpp<kQuadXor1>(v);
+  else if constexpr (M == 2) return dpp<kQuadXor2>(v);
+  else if constexpr (M == 4) {
+    const float up = dpp<kRowRor12>(v), down = dpp<kRowRor4>(v);
+    return (__lane_id() & 4) ? down : up;
+  } else if constexpr (M == 8) return dpp<kRowRor8>(v);
+  else if constexpr (M == 16)
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+  else return __shfl_xor(v, 32, 64);
+}
+
 // Sum over a quad of lanes (4 consecutive), in every lane of the quad.
 template <typename T>
 __device__ __forceinline__ T quad_sum(T v) {

@@ -30,7 +30,9 @@ namespace {
 constexpr uint32_t kHd = 64;
 constexpr int kWg = 1024;
 constexpr int kMixWg = 512;  // mix kernel: dim <= 512 values per thread role
-constexpr int kMixChunks = 6;  // 24 phi rows x 2048 / 16 bytes / kMixWg
+// phi rows per wave (24 rows / 8 waves) and 16-byte chunks per lane and row
+// (2048 bytes / 16 / 64 lanes) of the mix kernel.
+constexpr int kMixRows = 3, kMixCols = 2;
 constexpr uint32_t kPrefillRows = 512;  // positions per batched prefill pass
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
@@ -346,7 +348,10 @@ __device__ __forceinline__ float butterfly(float mine, float other, uint32_t t, 
 __device__ float fwht_block(float v, float* hv, uint32_t H, uint32_t t) {
   v = butterfly(v, nd::dpp<nd::kQuadXor1>(v), t, 1);
   if (H > 2) v = butterfly(v, nd::dpp<nd::kQuadXor2>(v), t, 2);
-  for (uint32_t s = 4; s < 64 && s < H; s <<= 1) v = butterfly(v, __shfl_xor(v, s, 64), t, s);
+  if (H > 4) v = butterfly(v, nd::lane_xor<4>(v), t, 4);
+  if (H > 8) v = butterfly(v, nd::lane_xor<8>(v), t, 8);
+  if (H > 16) v = butterfly(v, nd::lane_xor<16>(v), t, 16);
+  if (H > 32) v = butterfly(v, nd::lane_xor<32>(v), t, 32);
   for (uint32_t s = 64; s < H; s <<= 1) {
     __syncthreads();
     hv[t] = v;
@@ -377,12 +382,11 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   }
   __shared__ float nl[2048];
   __shared__ float hv[kMixWg];
-  __shared__ double part[kMixChunks * kMixWg];
   __shared__ double red[2][kMixWg / 64];
   __shared__ float phi[24], phi_sc[24], hpre[4], rt[20];
   const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const uint32_t D = a.d, L = a.lanes, N = L * D, H = a.hdim;
-  const uint32_t nrows = 2 * L + L * L, cpr = N / 16, chunks = nrows * cpr;
+  const uint32_t nrows = 2 * L + L * L, cpr = N / 16;
   const bool col = t < D;
   int phase = 0;
   // ---- loads, unconditional and in first-use order (every pointer is valid
@@ -404,14 +408,17 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   float xl[4];
 #pragma unroll
   for (int l = 0; l < 4; ++l) xl[l] = a.x[(size_t)min((uint32_t)l, L - 1) * D + tc];
-  uint4 pw[kMixChunks];
+  // Wave w owns phi rows w, w + 8, w + 16; lane l their 16-byte chunks l and
+  // l + 64.
+  uint4 pw[kMixRows][kMixCols];
 #pragma unroll
-  for (int i = 0; i < kMixChunks; ++i) {
-    const uint32_t c = min(t + i * kMixWg, chunks - 1);
-    const uint32_t r = c / cpr;
+  for (int i = 0; i < kMixRows; ++i) {
+    const uint32_t r = min(wave + i * (kMixWg / 64), nrows - 1);
     const int8_t* row = r < L ? w0 + (size_t)r * N
                         : (r < 2 * L ? w1 + (size_t)(r - L) * N : w2 + (size_t)(r - 2 * L) * N);
-    pw[i] = *reinterpret_cast<const uint4*>(row + (c % cpr) * 16);
+#pragma unroll
+    for (int j = 0; j < kMixCols; ++j)
+      pw[i][j] = *reinterpret_cast<const uint4*>(row + min(lane + 64u * j, cpr - 1) * 16);
   }
   const uint32_t tr = min(t, nrows - 1);
   const float norm_in = a.norm_input[tc], ekey = a.ekey[tc], evalue = a.evalue[tc],
@@ -490,39 +497,45 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     if ((uint32_t)l < L) ss += (double)xl[l] * (double)xl[l];
   ss = mix_sum(col ? ss : 0.0, red, phase);
   const double inv = 1.0 / sqrt(ss / N + 1e-6);
+  // The normalized lanes go to LDS interleaved: the q-th float4 of 16-element
+  // chunk ch sits at float4 index q * cpr + ch, so that the lanes of a wave,
+  // which read consecutive chunks, read consecutive 16-byte words.
+  float4* nl4 = reinterpret_cast<float4*>(nl);
   if (col) {
 #pragma unroll
     for (int l = 0; l < 4; ++l)
-      if ((uint32_t)l < L) nl[l * D + t] = (float)((double)xl[l] * inv);
+      if ((uint32_t)l < L) {
+        const uint32_t e = l * D + t;
+        nl[((((e >> 2) & 3) * cpr) + (e >> 4)) * 4 + (e & 3)] = (float)((double)xl[l] * inv);
+      }
   }
   if (t < nrows) phi_sc[t] = psc;
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < kMixChunks; ++i) {
-    const uint32_t c = t + i * kMixWg;
-    if (c < chunks) {
-      // fp32 over the chunk's 16 products, float64 across chunks.
-      const float4* xv = reinterpret_cast<const float4*>(nl + (c % cpr) * 16);
-      const uint32_t words[4] = {pw[i].x, pw[i].y, pw[i].z, pw[i].w};
-      float dot = 0.f;
+  for (int i = 0; i < kMixRows; ++i) {
+    const uint32_t r = wave + i * (kMixWg / 64);
+    double rs = 0.0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float4 f = xv[j];
-        const uint32_t wj = words[j];
-        dot = fmaf((float)(int8_t)(wj & 0xff), f.x, dot);
-        dot = fmaf((float)(int8_t)((wj >> 8) & 0xff), f.y, dot);
-        dot = fmaf((float)(int8_t)((wj >> 16) & 0xff), f.z, dot);
-        dot = fmaf((float)(int8_t)(wj >> 24), f.w, dot);
+    for (int j = 0; j < kMixCols; ++j) {
+      const uint32_t c = lane + 64u * j;
+      if (r < nrows && c < cpr) {
+        // fp32 over the chunk's 16 products, float64 across chunks.
+        const uint32_t words[4] = {pw[i][j].x, pw[i][j].y, pw[i][j].z, pw[i][j].w};
+        float dot = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 f = nl4[q * cpr + c];
+          const uint32_t wq = words[q];
+          dot = fmaf((float)(int8_t)(wq & 0xff), f.x, dot);
+          dot = fmaf((float)(int8_t)((wq >> 8) & 0xff), f.y, dot);
+          dot = fmaf((float)(int8_t)((wq >> 16) & 0xff), f.z, dot);
+          dot = fmaf((float)(int8_t)(wq >> 24), f.w, dot);
+        }
+        rs += (double)dot;
       }
-      part[c] = (double)dot;
     }
-  }
-  __syncthreads();
-  for (uint32_t r = wave; r < nrows; r += kMixWg / 64) {
-    double sum = 0.0;
-    for (uint32_t i = lane; i < cpr; i += 64) sum += part[r * cpr + i];
-    sum = nd::wave_sum(sum);
-    if (lane == 0) phi[r] = (float)((double)phi_sc[r] * sum);
+    rs = nd::wave_sum(rs);
+    if (lane == 0 && r < nrows) phi[r] = (float)((double)phi_sc[r] * rs);
   }
   __syncthreads();
   if (t < L) {
