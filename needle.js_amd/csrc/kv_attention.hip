@@ -182,7 +182,8 @@ __global__ __launch_bounds__(256) void attention_kernel(
     float* __restrict__ part_ml,
     uint32_t* __restrict__ counters, uint32_t layer, uint32_t kv_heads,
     uint32_t alloc, uint32_t sink, uint32_t window, Visible vis,
-    const uint32_t* __restrict__ positions, uint32_t seq_kv_heads, uint32_t kv_stride_z,
+    const uint32_t* __restrict__ positions, uint32_t slot_space, uint32_t seq_kv_heads,
+    uint32_t kv_stride_z,
     uint32_t chunk_positions, uint32_t max_chunks, float score_scale) {
   // z indexes query rows: sequences of a batch (kv_stride_z = seq_kv_heads,
   // each with its own cache heads) or positions of one prefill (kv_stride_z
@@ -192,7 +193,15 @@ __global__ __launch_bounds__(256) void attention_kernel(
   const uint32_t hq = seq_kv_heads * REP;
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const uint32_t quad = lane & 3, trow = lane >> 2;
-  if (positions) {
+  // slot_space (one row, position in device memory): walk the cache slots
+  // [0, alloc) in slot order -- vis = {alloc, alloc, alloc} makes logical
+  // index = slot -- so the tile loads need not wait for the position; a slot
+  // holds a visible position iff slot <= position or the ring is full
+  // (position >= alloc).  Otherwise the visible range of the row's position.
+  uint32_t spos = 0;
+  if (slot_space) {
+    spos = positions[z];
+  } else if (positions) {
     if (window == 0 && positions[z] >= alloc) return;  // validated on entry; stay in bounds
     vis = visible_at(positions[z], sink, window);
   }
@@ -236,7 +245,10 @@ __global__ __launch_bounds__(256) void attention_kernel(
     if (tn < c_end) load_tile<F32>(nxt, Kc, Vc, Ks, Vs, head_base, vis, tn, c_end, trow, quad, sink, window);
     bool valid[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) valid[k] = t0 + trow + 16 * k < c_end;
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t ti = t0 + trow + 16 * k;
+      valid[k] = ti < c_end && (!slot_space || ti <= spos || spos >= alloc);
+    }
     float p[REP][4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -431,6 +443,7 @@ struct AttnLaunch {
   uint32_t* counters;          // batch * seq_kv_heads zeros, used when a row has >1 chunk
   Visible vis;                 // used when positions == nullptr
   const uint32_t* positions;   // per-sequence query positions, or nullptr
+  uint32_t slot_space;         // one row: iterate cache slots, mask by *positions
   uint32_t seq_kv_heads;       // KV heads of one sequence
   uint32_t kv_stride_z;        // cache-head offset between query rows z
   uint32_t rep;                // query heads per KV head
@@ -449,7 +462,8 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
   hipLaunchKernelGGL((attention_kernel<REP, F32>), dim3(max_chunks, a.seq_kv_heads, a.batch),
                      dim3(64 * kWaves), 0, s, a.kv->k, a.kv->v, a.kv->ks, a.kv->vs, a.q, a.out,
                      a.gate, a.gate_ld, part_acc, part_ml, a.counters, a.layer, a.kv->kv_heads, a.kv->alloc,
-                     a.kv->sink, a.kv->window, a.vis, a.positions, a.seq_kv_heads, a.kv_stride_z,
+                     a.kv->sink, a.kv->window, a.vis, a.positions, a.slot_space, a.seq_kv_heads,
+                     a.kv_stride_z,
                      cp, max_chunks, 0.125f);
   return hipGetLastError();
 }
@@ -563,7 +577,7 @@ hipError_t nd_launch_attention_gated(const nd_kv* kv, uint32_t layer, const uint
                                      uint32_t max_position, const float* q, uint32_t q_heads,
                                      const float* gate, float* out, float* partials,
                                      uint32_t* counters, hipStream_t s) {
-  const nd_visible nv = nd_kv_visible(kv, max_position);
+  (void)max_position;  // slot order covers every slot a position can see
   AttnLaunch a{};
   a.kv = kv;
   a.layer = layer;
@@ -572,12 +586,13 @@ hipError_t nd_launch_attention_gated(const nd_kv* kv, uint32_t layer, const uint
   a.gate = gate;
   a.partials = partials;
   a.counters = counters;
-  a.vis = Visible{nv.prefix, nv.recent_low, nv.count};
+  a.vis = Visible{kv->alloc, kv->alloc, kv->alloc};
   a.positions = position;
+  a.slot_space = 1;
   a.seq_kv_heads = kv->kv_heads;
   a.kv_stride_z = 0;
   a.rep = q_heads / kv->kv_heads;
   a.batch = 1;
-  a.max_count = nv.count;
+  a.max_count = kv->alloc;
   return kv->mode == ND_KV_FLOAT32 ? launch_rep<true>(a, s) : launch_rep<false>(a, s);
 }

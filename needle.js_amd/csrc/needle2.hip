@@ -83,6 +83,8 @@ struct BeginArgs {
   uint32_t n_sites, tables, slots, sub, per_order, n_orders;
   uint32_t orders[4];
   float* cat;
+  const double* inv_freq;  // [32]
+  double* rope;            // out: sin then cos of position * inv_freq[j]
 };
 
 // Token intake, engram hashing (runtime.ts:788-818), the scaled embedding
@@ -112,6 +114,13 @@ __global__ __launch_bounds__(kWg) void n2_begin_kernel(BeginArgs a) {
   }
   __syncthreads();
   const uint32_t tok = s_tok, pos = s_pos;
+  if (t < 32) {
+    // RoPE angles of this step (math.ts:94-115), shared by every layer.
+    double sn, cs;
+    sincos((double)pos * a.inv_freq[t], &sn, &cs);
+    a.rope[t] = sn;
+    a.rope[32 + t] = cs;
+  }
   if (t < a.tables) {
     const uint32_t order = a.orders[t / a.per_order];
     uint32_t hash = 0x9E3779B9u * (t + 1);
@@ -588,11 +597,12 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
 
 // One head of the projection epilogue, one wave, lane = dimension: role 0
 // (query) and 1 (key) take the per-head rmsNorm with their scale and the
-// half-split RoPE at `pos` (runtime.ts:471-500, math.ts:94-115); role 0
+// half-split RoPE by (sin, cos) of the lane's angle (runtime.ts:471-500,
+// math.ts:94-115); role 0
 // writes q_dst, roles 1 and 2 (value) quantize into cache row
 // head_row + slot with #storeKV's arithmetic (runtime.ts:679-717).
-__device__ __forceinline__ void head_epilogue(float val, uint32_t lane, int role, uint32_t pos,
-                                              float nscale, double invf, float* q_dst,
+__device__ __forceinline__ void head_epilogue(float val, uint32_t lane, int role, double sn,
+                                              double cs, float nscale, float* q_dst,
                                               int8_t* Kc, int8_t* Vc, float* Ks, float* Vs,
                                               size_t head_row, uint32_t slot, uint32_t alloc) {
   float out = val;
@@ -601,8 +611,6 @@ __device__ __forceinline__ void head_epilogue(float val, uint32_t lane, int role
     const double ss = nd::wave_sum(xd * xd);
     const double inv = 1.0 / sqrt(ss / kHd + 1e-6);
     const double normed = (float)((1.0 + (double)nscale) * xd * inv);
-    double sn, cs;
-    sincos((double)pos * invf, &sn, &cs);
     const double other = __shfl_xor(normed, 32, 64);
     out = lane < 32 ? (float)(normed * cs - other * sn) : (float)(normed * cs + other * sn);
     if (role == 0) {
@@ -633,7 +641,7 @@ __global__ __launch_bounds__(256) void n2_qkv_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ S, const float* __restrict__ x,
     uint32_t d, uint32_t heads, uint32_t kv_heads, const uint32_t* __restrict__ st,
     const float* __restrict__ q_norm, const float* __restrict__ k_norm,
-    const double* __restrict__ inv_freq, float* __restrict__ q_out, float* __restrict__ gate_out,
+    const double* __restrict__ rope, float* __restrict__ q_out, float* __restrict__ gate_out,
     int8_t* __restrict__ Kc, int8_t* __restrict__ Vc, float* __restrict__ Ks,
     float* __restrict__ Vs, uint32_t layer, uint32_t alloc, uint32_t sink, uint32_t window,
     RouteArgs route) {
@@ -658,7 +666,7 @@ __global__ __launch_bounds__(256) void n2_qkv_kernel(
   const uint32_t pos = st[1];
   const uint32_t lane = t & 63;
   const float nscale = b < heads ? q_norm[lane] : k_norm[lane];
-  const double invf = inv_freq[lane & 31];
+  const double rs = rope[lane & 31], rc = rope[32 + (lane & 31)];
   for (uint32_t i = t; i < d; i += 256) xs[i] = x[i];
   __syncthreads();
   const float* xv = xs + q * seg;
@@ -683,7 +691,7 @@ __global__ __launch_bounds__(256) void n2_qkv_kernel(
   }
   const int role = b < nq ? 0 : (b < nq + nk ? 1 : 2);
   const uint32_t h = role == 0 ? b : (role == 1 ? b - nq : b - nq - nk);
-  head_epilogue(val, lane, role, pos, nscale, invf, q_out + (size_t)h * kHd, Kc, Vc, Ks, Vs,
+  head_epilogue(val, lane, role, rs, rc, nscale, q_out + (size_t)h * kHd, Kc, Vc, Ks, Vs,
                 ((size_t)layer * kv_heads + h) * alloc, kv_slot(pos, sink, window), alloc);
 }
 
@@ -796,8 +804,10 @@ __global__ __launch_bounds__(64) void n2_rope_store_batch_kernel(
   const int role = b < heads ? 0 : (b < heads + kv_heads ? 1 : 2);
   const uint32_t h = role == 0 ? b : (role == 1 ? b - heads : b - heads - kv_heads);
   const float val = qkvg[(size_t)m * ld + (size_t)b * kHd + lane];
-  head_epilogue(val, lane, role, pos, role == 0 ? q_norm[lane] : k_norm[lane],
-                inv_freq[lane & 31], q_out + ((size_t)m * heads + h) * kHd, Kc, Vc, Ks, Vs,
+  double sn, cs;
+  sincos((double)pos * inv_freq[lane & 31], &sn, &cs);
+  head_epilogue(val, lane, role, sn, cs, role == 0 ? q_norm[lane] : k_norm[lane],
+                q_out + ((size_t)m * heads + h) * kHd, Kc, Vc, Ks, Vs,
                 ((size_t)layer * kv_heads + h) * alloc, kv_slot(pos, sink, window), alloc);
 }
 
@@ -828,6 +838,7 @@ struct nd_needle {
         *qkvg = nullptr, *q = nullptr, *att = nullptr, *proj = nullptr, *phi_post_v = nullptr,
         *phi_res_v = nullptr, *fin = nullptr, *logits = nullptr, *cat = nullptr, *ekv_out = nullptr,
         *evals = nullptr, *partials = nullptr, *route = nullptr;
+  double* rope = nullptr;
   uint32_t max_length = 0, sink = 0, position = 0;
   // Batched prefill buffers (first prefill), for up to pf_cap positions a pass.
   char* pf_arena = nullptr;
@@ -885,6 +896,8 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
   b.per_order = d.n_orders ? d.engram_tables / d.n_orders : 1;
   for (uint32_t i = 0; i < d.n_orders; ++i) b.orders[i] = d.orders[i];
   b.cat = n->cat;
+  b.inv_freq = n->inv_freq;
+  b.rope = n->rope;
   hipLaunchKernelGGL(n2_begin_kernel, dim3(1), dim3(kWg), 0, s, b);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -967,7 +980,7 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
     hipLaunchKernelGGL(n2_qkv_kernel, dim3(wm.n / kHd + 1), dim3(256), 0, s, wm.w, wm.scales,
                        n->ain, D, d.heads, d.kv_heads, n->st,
                        n->params + n->o_qn + (size_t)l * kHd, n->params + n->o_kn + (size_t)l * kHd,
-                       n->inv_freq, n->q, n->qkvg, (int8_t*)n->kv.k, (int8_t*)n->kv.v, n->kv.ks,
+                       n->rope, n->q, n->qkvg, (int8_t*)n->kv.k, (int8_t*)n->kv.v, n->kv.ks,
                        n->kv.vs, l, n->kv.alloc, n->kv.sink, n->kv.window, ra);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     e = nd_launch_attention_gated(&n->kv, l, n->st + 1, n->max_length - 1, n->q, d.heads, n->qkvg,
@@ -1456,7 +1469,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
                             al((size_t)(2 * qw + 2 * kw) * 4), al(qw * 4), al(qw * 4), al(D * 4),
                             al(ln * 4), al(ln * ln * 4), al(D * 4), al((size_t)d.vocab * 4),
                             al((size_t)S * cat * 4), al((size_t)S * 2 * D * 4),
-                            al((size_t)S * D * 4), al(pf * 4), al(20 * 4)};
+                            al((size_t)S * D * 4), al(pf * 4), al(20 * 4), al(64 * 8)};
     size_t total = 0;
     for (size_t v : sizes) total += v;
     ND_HIP(ctx, hipMalloc(&n->arena, total));
@@ -1499,6 +1512,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     take(&n->evals);
     take(&n->partials);
     take(&n->route);
+    take(&n->rope);
   }
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
   ND_HIP(ctx, hipMemsetAsync(n->arena, 0, n->state_bytes, ctx->stream));
