@@ -11,17 +11,14 @@
 // are streamed with non-temporal 128-bit loads.  Bytes are decoded with the
 // unsigned-byte converts: u = b + 128 (byte ^ 0x80), dot = sum u*x - 128*sum x.
 // Partial sums (RACC rows x B batch values per thread) are reduced across the
-// row's threads through LDS followed by a short shuffle butterfly.
+// row's threads through LDS followed by a short DPP butterfly.
 #include "nd_internal.hpp"
+#include "nd_wave.hpp"
 
 namespace {
 
 constexpr int kThreads = 256;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
-  return __shfl_xor(v, mask, 64);
-}
 
 template <int B, int SPT, int RACC>
 __global__ __launch_bounds__(kThreads) void matvec_i8_kernel(
@@ -128,7 +125,13 @@ __global__ __launch_bounds__(kThreads) void matvec_i8_kernel(
   const float* col = red + ov * kThreads + osub * tpr;
   float sum = 0.f;
   for (uint32_t c = part; c < tpr; c += T) sum += col[c];
-  for (uint32_t m = T >> 1; m >= 1; m >>= 1) sum += shfl_xor_f(sum, m);
+  // T-lane butterfly: DPP within rows of 16, swizzle / bpermute beyond.
+  if (T > 32) sum += nd::lane_xor<32>(sum);
+  if (T > 16) sum += nd::lane_xor<16>(sum);
+  if (T > 8) sum += nd::lane_xor<8>(sum);
+  if (T > 4) sum += nd::lane_xor<4>(sum);
+  if (T > 2) sum += nd::lane_xor<2>(sum);
+  if (T > 1) sum += nd::lane_xor<1>(sum);
   if (part == 0) {
     const uint32_t p = ov / B, b = ov % B;
     const uint32_t row = row0 + p * rpp + osub;

@@ -177,6 +177,26 @@ def test_attention_gqa_window_sink(hip, sink, window, mode):
     kv.free()
 
 
+@pytest.mark.parametrize("hkv,hq,sink,window", [(4, 8, 0, 0), (2, 8, 0, 0), (1, 8, 3, 1024),
+                                                (2, 16, 0, 0), (8, 8, 5, 700)])
+def test_attention_split_chunks_every_head_ratio(hip, hkv, hq, sink, window):
+    """Contexts long enough to split into several chunks per KV head, for 1, 2,
+    4 and 8 query heads per KV head: the cross-chunk merge at each grouping."""
+    say("attention split", hkv, hq, sink, window)
+    n = 1300
+    kv = HipKvCache(hip, 1, hkv, max_length=n, sink=sink, window=window)
+    ref = oracle.KvCache(1, hkv, max_length=n, sink=sink, window=window)
+    s = synth.Stream(31, f"split{hkv}{hq}{sink}{window}")
+    K, V = s.normal((n, hkv, 64)), s.normal((n, hkv, 64))
+    kv.store(0, 0, K, V)
+    ref.store(0, 0, K, V)
+    for pos in (511, 512, 777, n - 1):
+        q = s.normal((hq * 64,))
+        assert_close(kv.attention(0, pos, q), ref.attention(0, pos, q), RTOL, ATOL,
+                     f"split hkv={hkv} hq={hq} pos={pos}")
+    kv.free()
+
+
 # ---------------------------------------------------------------- selection
 
 def test_select_golden_cases(hip):
