@@ -91,6 +91,12 @@ nd_status nd_create(int32_t device, nd_ctx** out) {
     delete ctx;
     return nd_fail(nullptr, ND_ERR_BACKEND, "hipStreamCreate: %s", hipGetErrorString(e));
   }
+  e = hipMalloc(&ctx->mv_split, kMatvecSplitBytes);
+  if (e != hipSuccess) {
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return nd_fail(nullptr, ND_ERR_BACKEND, "hipMalloc(matvec split): %s", hipGetErrorString(e));
+  }
   *out = ctx;
   return ND_OK;
 }
@@ -112,6 +118,7 @@ nd_status nd_destroy(nd_ctx* ctx) {
   if (ctx->attn_partials) hipFree(ctx->attn_partials);
   if (ctx->attn_counters) hipFree(ctx->attn_counters);
   if (ctx->mm_scratch) hipFree(ctx->mm_scratch);
+  if (ctx->mv_split) hipFree(ctx->mv_split);
   hipStreamDestroy(ctx->stream);
   delete ctx;
   return ND_OK;
@@ -222,7 +229,7 @@ nd_status nd_matvec_d(nd_ctx* ctx, const nd_mat* m, const float* x, uint32_t bat
   if ((batch && (!x || !y)) || (reinterpret_cast<uintptr_t>(x) & 15))
     return nd_fail(ctx, ND_ERR_INVALID, "x must be a 16-byte aligned device pointer");
   ND_HIP(ctx, nd_launch_matvec(m, x, batch, m->k, row_start, row_count, y, row_count,
-                               nd_pick_stream(ctx, stream)));
+                               nd_pick_stream(ctx, stream), ctx->mv_split));
   return ND_OK;
 }
 
@@ -240,7 +247,8 @@ nd_status nd_matvec(nd_ctx* ctx, const nd_mat* m, const float* x, uint32_t batch
   float* dx = reinterpret_cast<float*>(ctx->stage);
   float* dy = reinterpret_cast<float*>(reinterpret_cast<char*>(ctx->stage) + align256(xb));
   ND_HIP(ctx, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
-  ND_HIP(ctx, nd_launch_matvec(m, dx, batch, m->k, row_start, row_count, dy, row_count, ctx->stream));
+  ND_HIP(ctx, nd_launch_matvec(m, dx, batch, m->k, row_start, row_count, dy, row_count, ctx->stream,
+                               ctx->mv_split));
   ND_HIP(ctx, hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, ctx->stream));
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return ND_OK;

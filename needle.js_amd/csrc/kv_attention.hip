@@ -283,15 +283,21 @@ __global__ __launch_bounds__(256) void attention_kernel(
         l[h] += e;
       }
     }
+    // Masked positions add exactly nothing, whatever their (possibly never
+    // written) slots hold: int8 codes are finite, so a zero weight suffices;
+    // float32 rows could hold NaN and are skipped per element.
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       float vc[16];
       unpack<F32>(cur, k, true, vc);
 #pragma unroll
       for (int h = 0; h < REP; ++h) {
-        const float ev = p[h][k] * cur.vs[k];
+        const float ev = valid[k] ? p[h][k] * cur.vs[k] : 0.f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[h][i] = fmaf(ev, vc[i], acc[h][i]);
+        for (int i = 0; i < 16; ++i) {
+          if constexpr (F32) acc[h][i] = valid[k] ? fmaf(ev, vc[i], acc[h][i]) : acc[h][i];
+          else acc[h][i] = fmaf(ev, vc[i], acc[h][i]);
+        }
       }
     }
     cur = nxt;

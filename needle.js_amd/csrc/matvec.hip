@@ -139,6 +139,392 @@ __global__ __launch_bounds__(kThreads) void matvec_i8_kernel(
   }
 }
 
+// Batched form on MFMA (up to 8 rows per launch, g % 32 == 0): fp16 operands with
+// the fp32 inputs split exactly enough.  mv_split_kernel writes, per batch
+// row b with e_b = the exponent of max_k |x[b][k]| (max < 2^e_b),
+//   x[b][k] * 2^-e_b = hi + lo,  hi = f16(x * 2^-e_b),  lo = f16(x * 2^-e_b - hi),
+// which leaves at most 2^-24 of the row's largest element unrepresented
+// (fp32's own rounding step).  Weights are int8, exact in fp16, and fp16 x
+// fp16 products are exact in the fp32 MFMA accumulator, so
+//   y[b][r] = 2^e_b * sum_g s[r][g] * (sum_{k in g} W[r][k] (hi + lo)[b][k])
+// differs from the fp32 dot product only by fp32 accumulation rounding.
+//
+// v_mfma_f32_16x16x32_f16 with A = the 16 split rows i = (b = i & 7, part =
+// i >> 3: hi, lo) and B = 16 weight rows: lane l supplies A row l % 16 and B
+// column l % 16, eight k of a 32-wide group, and receives D rows 4 (l / 16)
+// + [0, 4) of column l % 16 -- so each lane's four outputs belong to one
+// weight row and take one group scale.  Lane block kb = l / 16 holds the
+// group's k in [8 kOrder[kb], +8), kOrder = {0, 2, 1, 3}: the order in which
+// one 16-byte weight load per lane plus a lane-half swap delivers two groups
+// (see matvec_mfma_kernel).  The split rows are stored in operand order:
+// xs[group][lane] = 8 halves.
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+constexpr uint32_t kSplitRows = 8;
+// Batch 2 streams faster on the vector kernel (7.5 vs 11 us at 4096 x 4096);
+// from 3 rows on (two vector launches) the MFMA path wins.
+constexpr uint32_t kMfmaMinBatch = 3;
+
+// Lane block holding k block j of a group (kOrder is its own inverse).
+__device__ __forceinline__ uint32_t k_block_lanes(uint32_t j) { return j == 1 ? 2 : j == 2 ? 1 : j; }
+
+__global__ __launch_bounds__(256) void mv_split_kernel(const float* __restrict__ X,
+                                                       uint32_t x_stride, uint32_t bc, uint32_t K,
+                                                       uint4* __restrict__ xs,
+                                                       float* __restrict__ xf) {
+  const uint32_t b = blockIdx.x, t = threadIdx.x;
+  const uint32_t units = K / 8;  // unit u: k in [8u, 8u + 8) = group u / 4, k block u % 4
+  if (b >= bc) {  // rows past the batch multiply as zeros
+    for (uint32_t u = t; u < units; u += 256) {
+      const size_t e = (size_t)(u >> 2) * 64 + k_block_lanes(u & 3) * 16 + b;
+      xs[e] = make_uint4(0, 0, 0, 0);
+      xs[e + 8] = make_uint4(0, 0, 0, 0);
+    }
+    return;
+  }
+  const float4* x = reinterpret_cast<const float4*>(X + (size_t)b * x_stride);
+  float v[4][8];  // K <= 8192: at most 4 units per thread
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t u = t + 256 * i;
+    const uint32_t uu = u < units ? u : 0;
+    const float4 a = x[2 * uu], c = x[2 * uu + 1];
+    v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
+    v[i][4] = c.x; v[i][5] = c.y; v[i][6] = c.z; v[i][7] = c.w;
+    if (u < units)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) amax = fmaxf(amax, fabsf(v[i][q]));
+  }
+  __shared__ float red[4];
+  amax = fmaxf(amax, nd::lane_xor<1>(amax));
+  amax = fmaxf(amax, nd::lane_xor<2>(amax));
+  amax = fmaxf(amax, nd::lane_xor<4>(amax));
+  amax = fmaxf(amax, nd::lane_xor<8>(amax));
+  amax = fmaxf(amax, nd::lane_xor<16>(amax));
+  amax = fmaxf(amax, nd::lane_xor<32>(amax));
+  if ((t & 63) == 0) red[t >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = 0;
+  if (amax > 0.f && amax <= 3.4028235e38f) frexpf(amax, &e);  // amax < 2^e
+  const float down = ldexpf(1.f, -e);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t u = t + 256 * i;
+    if (u >= units) continue;
+    half8 hi, lo;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float xv = v[i][q] * down;
+      const _Float16 h = (_Float16)xv;
+      hi[q] = h;
+      lo[q] = (_Float16)(xv - (float)h);
+    }
+    const size_t at = (size_t)(u >> 2) * 64 + k_block_lanes(u & 3) * 16 + b;
+    xs[at] = __builtin_bit_cast(uint4, hi);
+    xs[at + 8] = __builtin_bit_cast(uint4, lo);
+  }
+  if (t == 0) xf[b] = ldexpf(1.f, e);
+}
+
+// Eight int8 codes -> eight exact fp16 values: 0x6500 | (c ^ 0x80) is the
+// fp16 number 1408 + c, and one packed subtraction per pair removes 1408.
+__device__ __forceinline__ half8 codes_to_half(u32x2 w) {
+  const uint32_t u0 = w.x ^ 0x80808080u, u1 = w.y ^ 0x80808080u;
+  const uint32_t k = 0x65656565u;
+  const half2v off = {(_Float16)-1408.f, (_Float16)-1408.f};
+  const half2v p0 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(k, u0, 0x04010400u)) + off;
+  const half2v p1 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(k, u0, 0x04030402u)) + off;
+  const half2v p2 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(k, u1, 0x04010400u)) + off;
+  const half2v p3 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(k, u1, 0x04030402u)) + off;
+  return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+constexpr uint32_t kMfmaWaves = 16;
+
+// Cross-wave sum of the MFMA accumulators and the store: every wave leaves
+// its four components in red ([wave][component][lane], 16 KB of LDS), then
+// wave c < 4 sums component c over the waves, adds the lo row to the hi row
+// (lanes l and l + 32) and scales by 2^e_b of its row b = 4 (l / 16) + c.
+// With RT row tiles per workgroup, tile r uses red + 4096 r and rows
+// row0 + 16 r.
+template <int RT>
+__device__ __forceinline__ void mfma_reduce_store(const float4v (&acc)[RT], float* red,
+                                                  uint32_t wave, uint32_t lane, uint32_t row0,
+                                                  uint32_t row_count, uint32_t bc, float fb,
+                                                  float* __restrict__ Y, uint32_t y_stride) {
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) red[r * 4096 + (wave * 4 + c) * 64 + lane] = acc[r][c];
+  __syncthreads();
+  if (wave >= 4) return;
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    float sum = 0.f;
+#pragma unroll
+    for (uint32_t w = 0; w < kMfmaWaves; ++w) sum += red[r * 4096 + (w * 4 + wave) * 64 + lane];
+    sum += nd::lane_xor<32>(sum);
+    const uint32_t b = (lane >> 4) * 4 + wave, row = row0 + 16 * r + (lane & 15);
+    if (lane < 32 && row < row_count && b < bc) Y[(size_t)b * y_stride + row] = sum * fb;
+  }
+}
+
+// One workgroup of kMfmaWaves waves per 16 weight rows.  The rows' group
+// scales are staged in LDS (coalesced loads).  Wave w takes pairs of 32-wide
+// groups p = w + kMfmaWaves i, NP pairs at a time, each lane loading 16
+// bytes of its row: lanes 0..31 (blocks 0, 1) bytes [16 kb, +16) of group
+// 2p, lanes 32..63 the same of group 2p + 1 -- 64 contiguous bytes per row.
+// v_permlane32_swap of (d0, d2) and of (d1, d3) then gives every lane eight
+// codes of group 2p (k blocks kOrder) and eight of group 2p + 1.  All loads
+// of a step are issued together and unconditionally (addresses clamped,
+// contributions weighted by zero), so each MFMA waits only for its operands.
+
+template <int NP>
+__global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_kernel(
+    const int8_t* __restrict__ W, const float* __restrict__ S, const uint4* __restrict__ xs,
+    const float* __restrict__ xf, float* __restrict__ Y, uint32_t K, uint32_t groups,
+    uint32_t gshift, uint32_t row_start, uint32_t row_count, uint32_t bc, uint32_t y_stride) {
+  const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const uint32_t r16 = lane & 15, kb = lane >> 4;
+  const uint32_t row0 = blockIdx.x * 16;
+  const uint32_t row = row0 + r16;
+  const uint32_t rr = row_start + (row < row_count ? row : row_count - 1);
+  const int8_t* wrow = W + (size_t)rr * K + (kb & 1) * 16 + (kb >> 1) * 32;
+  const uint32_t ng = K / 32;  // 32-wide groups
+  const uint32_t npairs = ng / 2;
+  const uint32_t per_wave = (npairs + kMfmaWaves - 1) / kMfmaWaves;
+
+  // Scales of the 16 rows, [row][group] with a padded row stride.
+  extern __shared__ float s_scale[];
+  const uint32_t sstride = groups + 1;
+  float sreg[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {  // 16 * groups <= 4096 = 4 per thread
+    const uint32_t e = t + 1024 * i;
+    const uint32_t r = e / groups, q = e % groups;
+    const uint32_t srow = row0 + r < row_count ? row0 + r : row_count - 1;
+    sreg[i] = e < 16 * groups ? S[(size_t)(row_start + srow) * groups + q] : 0.f;
+  }
+  // The output factor 2^e_b of the row this lane stores (b <= 7 is always
+  // inside xf).
+  const float fb = xf[(kb & 1) * 4 + (wave & 3)];
+
+  float4v acc = {0.f, 0.f, 0.f, 0.f};
+  u32x4 wv[NP];
+  uint4 xa[NP][2];
+  auto load = [&](uint32_t base) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const uint32_t p = wave + kMfmaWaves * (base + i);
+      const uint32_t pc = p < npairs ? p : 0;
+      wv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + (size_t)pc * 64));
+      xa[i][0] = xs[(size_t)(2 * pc) * 64 + lane];
+      xa[i][1] = xs[(size_t)(2 * pc + 1) * 64 + lane];
+    }
+  };
+  auto compute = [&](uint32_t base) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const uint32_t p = wave + kMfmaWaves * (base + i);
+      const uint32_t pc = p < npairs ? p : 0;
+      const auto lo = __builtin_amdgcn_permlane32_swap(wv[i].x, wv[i].z, false, false);
+      const auto hi = __builtin_amdgcn_permlane32_swap(wv[i].y, wv[i].w, false, false);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t g = 2 * pc + h;
+        const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            __builtin_bit_cast(half8, xa[i][h]), codes_to_half(u32x2{lo[h], hi[h]}),
+            float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        const float sv = p < npairs ? s_scale[r16 * sstride + (g >> gshift)] : 0.f;
+        acc[0] = fmaf(sv, d[0], acc[0]);
+        acc[1] = fmaf(sv, d[1], acc[1]);
+        acc[2] = fmaf(sv, d[2], acc[2]);
+        acc[3] = fmaf(sv, d[3], acc[3]);
+      }
+    }
+  };
+  // First step: its loads in flight behind the scale loads, then the scales
+  // to LDS, then the rest.
+  load(0);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t e = t + 1024 * i;
+    if (e < 16 * groups) s_scale[(e / groups) * sstride + e % groups] = sreg[i];
+  }
+  __syncthreads();
+  compute(0);
+  for (uint32_t base = NP; base < per_wave; base += NP) {
+    load(base);
+    compute(base);
+  }
+
+  __shared__ float red[kMfmaWaves * 4 * 64];
+  const float4v accs[1] = {acc};
+  mfma_reduce_store<1>(accs, red, wave, lane, row0, row_count, bc, fb, Y, y_stride);
+}
+
+// The same product with the split done in the workgroup (k <= 4096): every
+// workgroup reads x (an L2 hit after the first), takes each row's largest
+// magnitude, and writes the hi/lo image of x in operand order into LDS
+// (128 KB at k = 4096) while its weight loads stream in -- one launch, and
+// the split's VALU work overlaps the wait for HBM.  Entry e of group g sits
+// at g * 64 + (e ^ (g & 15)): a 16-lane write round (16 groups, see the unit
+// order below) then covers 16 distinct 16-byte slots, and a wave's read of
+// one group stays a permutation within each 256-byte block.
+constexpr uint32_t kFusedMaxK = 4096;
+constexpr int kFusedRT = 1;  // 16-row tiles per workgroup (2 measured slower: half the CUs)
+
+template <int NP, int RT>
+__global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_fused_kernel(
+    const int8_t* __restrict__ W, const float* __restrict__ S, const float* __restrict__ X,
+    uint32_t x_stride, float* __restrict__ Y, uint32_t K, uint32_t groups, uint32_t gshift,
+    uint32_t row_start, uint32_t row_count, uint32_t bc, uint32_t y_stride) {
+  __shared__ uint4 s_xs[kFusedMaxK / 32 * 64];
+  __shared__ float s_sc[16 * RT * (kFusedMaxK / 32 + 1)];
+  __shared__ float s_max[kMfmaWaves], s_f[kSplitRows];
+  const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const uint32_t r16 = lane & 15, kb = lane >> 4;
+  const uint32_t row0 = blockIdx.x * 16 * RT;
+  const int8_t* wrow[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    const uint32_t row = row0 + 16 * r + r16;
+    const uint32_t rr = row_start + (row < row_count ? row : row_count - 1);
+    wrow[r] = W + (size_t)rr * K + (kb & 1) * 16 + (kb >> 1) * 32;
+  }
+  const uint32_t ng = K / 32, npairs = ng / 2;
+  const uint32_t per_wave = (npairs + kMfmaWaves - 1) / kMfmaWaves;
+
+  // x: thread t holds row xb = t / 128 and 8-value units j = q + 128 i, with
+  // q = 64 h + 4 (l % 16) + l / 16 for lane l of half h of the row's threads.
+  const uint32_t xb = t >> 7, upr = K / 8;
+  const uint32_t xj = (t & 64) + (lane & 15) * 4 + (lane >> 4);
+  const float4* xrow = reinterpret_cast<const float4*>(X + (size_t)(xb < bc ? xb : 0) * x_stride);
+  float xv[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t j = xj + 128 * i;
+    const uint32_t jj = j < upr ? j : 0;
+    const float4 a = xrow[2 * jj], c = xrow[2 * jj + 1];
+    const bool ok = j < upr && xb < bc;  // rows past the batch multiply as zeros
+    xv[i][0] = ok ? a.x : 0.f; xv[i][1] = ok ? a.y : 0.f;
+    xv[i][2] = ok ? a.z : 0.f; xv[i][3] = ok ? a.w : 0.f;
+    xv[i][4] = ok ? c.x : 0.f; xv[i][5] = ok ? c.y : 0.f;
+    xv[i][6] = ok ? c.z : 0.f; xv[i][7] = ok ? c.w : 0.f;
+  }
+  // Scales of the 16 RT rows, [row][group] with a padded row stride.
+  const uint32_t sstride = groups + 1;
+  constexpr int kSc = RT * 2;  // 16 RT * groups <= 2048 RT here
+  float sreg[kSc];
+#pragma unroll
+  for (int i = 0; i < kSc; ++i) {
+    const uint32_t e = t + 1024 * i;
+    const uint32_t ee = e < 16 * RT * groups ? e : 0;
+    const uint32_t r = ee / groups, q = ee % groups;
+    const uint32_t srow = row0 + r < row_count ? row0 + r : row_count - 1;
+    sreg[i] = S[(size_t)(row_start + srow) * groups + q];
+  }
+
+  float4v acc[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r) acc[r] = float4v{0.f, 0.f, 0.f, 0.f};
+  u32x4 wv[RT][NP];
+  auto load = [&](uint32_t base) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const uint32_t p = wave + kMfmaWaves * (base + i);
+      const uint32_t pc = p < npairs ? p : 0;
+#pragma unroll
+      for (int r = 0; r < RT; ++r)
+        wv[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[r] + (size_t)pc * 64));
+    }
+  };
+  auto compute = [&](uint32_t base) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const uint32_t p = wave + kMfmaWaves * (base + i);
+      const uint32_t pc = p < npairs ? p : 0;
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        const auto lo = __builtin_amdgcn_permlane32_swap(wv[r][i].x, wv[r][i].z, false, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap(wv[r][i].y, wv[r][i].w, false, false);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t g = 2 * pc + h;
+          const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              __builtin_bit_cast(half8, s_xs[g * 64 + (lane ^ (g & 15))]),
+              codes_to_half(u32x2{lo[h], hi[h]}), float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          const float sv = p < npairs ? s_sc[(16 * r + r16) * sstride + (g >> gshift)] : 0.f;
+          acc[r][0] = fmaf(sv, d[0], acc[r][0]);
+          acc[r][1] = fmaf(sv, d[1], acc[r][1]);
+          acc[r][2] = fmaf(sv, d[2], acc[r][2]);
+          acc[r][3] = fmaf(sv, d[3], acc[r][3]);
+        }
+      }
+    }
+  };
+  // Row maxima (rows xb live in waves 2 xb and 2 xb + 1), the split, then
+  // the scales to LDS.  The weight loads are issued only once x is here:
+  // behind the weight stream x would arrive last and the split could not
+  // overlap anything.
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int q = 0; q < 8; ++q) mx = fmaxf(mx, fabsf(xv[i][q]));
+  __builtin_amdgcn_sched_barrier(0);
+  load(0);
+  mx = fmaxf(mx, nd::lane_xor<1>(mx));
+  mx = fmaxf(mx, nd::lane_xor<2>(mx));
+  mx = fmaxf(mx, nd::lane_xor<4>(mx));
+  mx = fmaxf(mx, nd::lane_xor<8>(mx));
+  mx = fmaxf(mx, nd::lane_xor<16>(mx));
+  mx = fmaxf(mx, nd::lane_xor<32>(mx));
+  if (lane == 0) s_max[wave] = mx;
+  __syncthreads();
+  const float amax = fmaxf(s_max[2 * xb], s_max[2 * xb + 1]);
+  int ex = 0;
+  if (amax > 0.f && amax <= 3.4028235e38f) frexpf(amax, &ex);  // amax < 2^ex
+  const float down = ldexpf(1.f, -ex);
+  if (xj == 0) s_f[xb] = ldexpf(1.f, ex);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t j = xj + 128 * i;
+    if (j >= upr) continue;
+    half8 hv, lv;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float v = xv[i][q] * down;
+      const _Float16 h = (_Float16)v;
+      hv[q] = h;
+      lv[q] = (_Float16)(v - (float)h);
+    }
+    const uint32_t g = j >> 2, e = k_block_lanes(j & 3) * 16 + xb;
+    s_xs[g * 64 + (e ^ (g & 15))] = __builtin_bit_cast(uint4, hv);
+    s_xs[g * 64 + ((e + 8) ^ (g & 15))] = __builtin_bit_cast(uint4, lv);
+  }
+#pragma unroll
+  for (int i = 0; i < kSc; ++i) {
+    const uint32_t e = t + 1024 * i;
+    if (e < 16 * RT * groups) s_sc[(e / groups) * sstride + e % groups] = sreg[i];
+  }
+  __syncthreads();
+
+  compute(0);
+  for (uint32_t base = NP; base < per_wave; base += NP) {
+    load(base);
+    compute(base);
+  }
+  const float fb = s_f[(kb & 1) * 4 + (wave & 3)];
+  __syncthreads();  // every wave is done with s_xs: reuse it for the sums
+  mfma_reduce_store<RT>(acc, reinterpret_cast<float*>(s_xs), wave, lane, row0, row_count, bc, fb,
+                        Y, y_stride);
+}
+
 __global__ void row_kernel(const int8_t* __restrict__ W, const float* __restrict__ S,
                            uint32_t K, uint32_t groups, uint32_t G, uint32_t row,
                            float* __restrict__ out) {
@@ -171,10 +557,50 @@ MatvecFn pick_b(uint32_t b, uint32_t spt) {
 
 // Host-side checks that the kernel's geometry fits the matrix were done by
 // the caller (k = 16 * 2^j with 128 <= k <= 8192, g % 16 == 0, k % g == 0).
+// With `split` (kMatvecSplitBytes of device memory), batches of 3 or more
+// rows of a matrix with g % 32 == 0 run on MFMA, 8 rows per launch (k <=
+// 4096: one fused launch; k = 8192: split kernel + MFMA kernel); otherwise
+// every row is streamed by the vector kernel.
 hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uint32_t x_stride,
                             uint32_t row_start, uint32_t row_count, float* y, uint32_t y_stride,
-                            hipStream_t s) {
+                            hipStream_t s, void* split) {
   if (row_count == 0 || batch == 0) return hipSuccess;
+  if (split && batch >= kMfmaMinBatch && m->g % 32 == 0) {
+    uint32_t gshift = 0;  // g = 32 << gshift (g divides k, a power of two)
+    while ((32u << gshift) < m->g) ++gshift;
+    uint4* xs = reinterpret_cast<uint4*>(split);
+    float* xf = reinterpret_cast<float*>(reinterpret_cast<char*>(split) + (size_t)m->k * 32);
+    const uint32_t pairs_per_wave = (m->k / 64 + kMfmaWaves - 1) / kMfmaWaves;
+    for (uint32_t b0 = 0; b0 < batch; b0 += kSplitRows) {
+      const uint32_t bc = batch - b0 < kSplitRows ? batch - b0 : kSplitRows;
+      if (m->k <= kFusedMaxK) {
+        const auto kern = pairs_per_wave >= 4 ? &matvec_mfma_fused_kernel<4, kFusedRT>
+                        : pairs_per_wave >= 2 ? &matvec_mfma_fused_kernel<2, kFusedRT>
+                                              : &matvec_mfma_fused_kernel<1, kFusedRT>;
+        hipLaunchKernelGGL(kern, dim3((row_count + 16 * kFusedRT - 1) / (16 * kFusedRT)),
+                           dim3(64 * kMfmaWaves), 0, s, m->w,
+                           m->scales, x + (size_t)b0 * x_stride, x_stride,
+                           y + (size_t)b0 * y_stride, m->k, m->k / m->g, gshift, row_start,
+                           row_count, bc, y_stride);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        continue;
+      }
+      hipLaunchKernelGGL(mv_split_kernel, dim3(kSplitRows), dim3(256), 0, s,
+                         x + (size_t)b0 * x_stride, x_stride, bc, m->k, xs, xf);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      const auto kern = pairs_per_wave >= 4 ? &matvec_mfma_kernel<4>
+                      : pairs_per_wave >= 2 ? &matvec_mfma_kernel<2> : &matvec_mfma_kernel<1>;
+      const size_t lds = (size_t)16 * (m->k / m->g + 1) * sizeof(float);
+      hipLaunchKernelGGL(kern, dim3((row_count + 15) / 16), dim3(64 * kMfmaWaves), lds, s, m->w,
+                         m->scales, xs, xf, y + (size_t)b0 * y_stride, m->k, m->k / m->g, gshift,
+                         row_start, row_count, bc, y_stride);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
   const uint32_t segs = m->k / 16;
   const uint32_t spt = segs > 256 ? segs / 256 : 1;
   const uint32_t tpr = segs / spt;

@@ -38,6 +38,8 @@ struct nd_ctx {
   float* attn_partials = nullptr;
   size_t attn_partial_floats = 0;
   uint32_t* attn_counters = nullptr;
+  // Split inputs of the batched MFMA matvec (kMatvecSplitBytes).
+  void* mv_split = nullptr;
   // Digit planes and row factors of nd_matmul_d (grown on demand).
   void* mm_scratch = nullptr;
   size_t mm_scratch_bytes = 0;
@@ -60,9 +62,13 @@ inline hipStream_t nd_pick_stream(nd_ctx* ctx, void* stream) {
 }
 
 // Kernel launchers (each validates nothing: callers check shapes first).
+// `split`: kMatvecSplitBytes of device memory that lets batches of 3 or more
+// run on MFMA (the fp16 split of x at k = 8192); nullptr keeps the vector
+// kernel.
+constexpr size_t kMatvecSplitBytes = 8192 * 32 + 256;
 hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uint32_t x_stride,
                             uint32_t row_start, uint32_t row_count, float* y, uint32_t y_stride,
-                            hipStream_t s);
+                            hipStream_t s, void* split = nullptr);
 hipError_t nd_launch_row(const nd_mat* m, uint32_t row, float* out, hipStream_t s);
 
 // Visible-position arithmetic of the attention window (runtime.ts:723-728).

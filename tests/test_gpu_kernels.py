@@ -49,6 +49,26 @@ def test_matvec_matches_oracle(hip, n, k, g, batch):
     assert_close(got, ref, RTOL, ATOL, f"matvec {n}x{k} g{g} b{batch}")
 
 
+def test_matvec_batched_magnitudes_ranges_and_chunks(hip):
+    """Batches run on MFMA with each input row split around its own largest
+    element: rows of very different magnitude, an all-zero row, elements
+    spread over six decades, a row range and a batch above eight."""
+    say("matvec batched magnitudes")
+    m = matrix(13, 600, 1024, 32)
+    s = synth.Stream(9, "xmag")
+    x = s.normal((12, 1024))
+    x[1] *= 1e-6
+    x[2] *= 1e4
+    x[3] = 0.0
+    x[4] *= np.power(10.0, s.uniform((1024,), -3.0, 3.0)).astype(np.float32)
+    got = hip.matvec(m, x)
+    assert np.all(got[3] == 0.0)
+    assert_close(got, oracle.matvec_i8(m.codes, m.scales, 32, x), RTOL, ATOL, "matvec b12")
+    part = hip.matvec(m, x[:3], MatrixRowRange(37, 300))
+    assert_close(part, oracle.matvec_i8(m.codes, m.scales, 32, x[:3], 37, 300), RTOL, ATOL,
+                 "matvec b3 rows 37..336")
+
+
 def test_matvec_ranges_and_batch_requests(hip):
     say("matvec ranges")
     m = matrix(3, 512, 512, 512)

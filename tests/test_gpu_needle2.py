@@ -68,6 +68,34 @@ def test_step_logits_and_kv_match_oracle(small, sink):
                 np.testing.assert_allclose(g, r, rtol=1e-3)
 
 
+def test_step_ignores_stale_nan_slots(small):
+    """A step's attention walks every ring slot and masks the ones its position
+    cannot see; such slots must add nothing even when they hold NaN (stale or
+    never-written memory).  The cache is poisoned with NaN rows (code 0, scale
+    NaN) before a fresh reset, and the steps must still match the oracle."""
+    import ctypes as C
+
+    from needle_hip import lib as L
+
+    w, model = small
+    say("needle2 stale NaN slots")
+    rt = model.create_runtime()
+    rt.reset(SMALL.max_length, 0)
+    sess = model.session
+    kv = sess.lib.nd_needle_kv(sess.handle)
+    alloc = C.c_uint32()
+    sess._check(sess.lib.nd_kv_info(kv, C.byref(alloc), None, None, None, None), "nd_kv_info")
+    poison = np.full((alloc.value, SMALL.kv_heads, 64), np.nan, np.float32)
+    for layer in range(SMALL.layers):
+        sess._check(sess.lib.nd_kv_store(sess.backend.ctx, kv, layer, 0, alloc.value,
+                                         L.ptr(poison), L.ptr(poison)), "nd_kv_store")
+    assert np.isnan(sess.kv_read(0, 0)[3]).all()
+    rt.reset(SMALL.max_length, 0)
+    ref = oracle.Needle2(w).runtime(SMALL.max_length, 0)
+    for i, t in enumerate(synth.Stream(6, "n2nan").integers(12, 0, SMALL.vocab - 1)):
+        close(rt.step(int(t)), ref.step(int(t)), ("nan slots", i))
+
+
 def test_prefill_and_step_selected(small):
     w, model = small
     say("needle2 prefill + step_selected")
