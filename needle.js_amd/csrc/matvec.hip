@@ -113,7 +113,8 @@ __global__ __launch_bounds__(kThreads) void matvec_i8_kernel(
   // Reduce each row's partial sums over its tpr threads through LDS.  red is
   // [V][256]: thread t stores its V partials in column t.  Output o = (sub,
   // v) is summed by T = 256 / (rpp * V) threads (a power of two <= 64 that
-  // divides 64), each over tpr / T columns, then by a T-lane butterfly.
+  // divides 64), each over tpr / T = V columns (all V reads in flight at
+  // once), then by a T-lane butterfly.
   __shared__ float red[V * kThreads];
 #pragma unroll
   for (int i = 0; i < V; ++i) red[i * kThreads + t] = acc[i];
@@ -123,8 +124,12 @@ __global__ __launch_bounds__(kThreads) void matvec_i8_kernel(
   const uint32_t o = t / T, part = t % T;
   const uint32_t osub = o / V, ov = o % V;
   const float* col = red + ov * kThreads + osub * tpr;
+  float cv[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) cv[i] = col[part + T * i];
   float sum = 0.f;
-  for (uint32_t c = part; c < tpr; c += T) sum += col[c];
+#pragma unroll
+  for (int i = 0; i < V; ++i) sum += cv[i];
   // T-lane butterfly: DPP within rows of 16, swizzle / bpermute beyond.
   if (T > 32) sum += nd::lane_xor<32>(sum);
   if (T > 16) sum += nd::lane_xor<16>(sum);
