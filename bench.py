@@ -490,8 +490,8 @@ def main():
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--skip-needle2", action="store_true")
     ap.add_argument("--needle2-reps", type=int, default=5)
-    ap.add_argument("--only", choices=["matvec", "attention", "decode", "prefill", "needle2",
-                                       "traffic"],
+    ap.add_argument("--only", choices=["matvec", "matvec8", "attention", "decode", "prefill",
+                                       "needle2", "traffic"],
                     help="run one part alone and print its JSON (for profiling)")
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--no-check", action="store_true",
@@ -513,6 +513,8 @@ def main():
     if args.only:
         if args.only == "matvec":
             part = bench_matvec(torch, hip, n, k, g, 1, args.steps, args.warmup)
+        elif args.only == "matvec8":
+            part = bench_matvec(torch, hip, n, k, g, 8, args.steps, args.warmup)
         elif args.only == "attention":
             part = bench_attention(torch, hip, 8192, 8, args.steps // 2, args.warmup)
         elif args.only == "decode":
