@@ -199,7 +199,13 @@ struct nd_batch {
   uint32_t *counters = nullptr, *masks = nullptr, *tokens = nullptr, *positions = nullptr,
            *step = nullptr, *ids = nullptr, *history = nullptr;
   double *logprobs = nullptr, *lp_history = nullptr;  // history: [max_length][batch]
+  nd_gemm_split gsplit{};  // split-k workspace of the step's GEMMs (zeroed counters)
 };
+
+// Split-k workspace of a batch: up to 512 tiles' worth of partials (16 x 64
+// outputs each) and 256 tile counters.
+constexpr size_t kSplitPartialFloats = (size_t)512 * 1024;
+constexpr uint32_t kSplitCounters = 256;
 
 static inline size_t a256(size_t n) { return (n + 255) & ~size_t(255); }
 
@@ -372,7 +378,8 @@ nd_status nd_batch_create(nd_ctx* ctx, nd_decoder* dec, uint32_t batch, uint32_t
       a256((size_t)batch * words * 4),                                       // masks
       a256((size_t)batch * 4), a256((size_t)batch * 4), a256(256),           // tokens, positions, step
       a256((size_t)batch * 4), a256((size_t)batch * 8),                      // ids, logprobs
-      a256((size_t)max_length * batch * 4), a256((size_t)max_length * batch * 8)};  // history
+      a256((size_t)max_length * batch * 4), a256((size_t)max_length * batch * 8),   // history
+      a256(kSplitPartialFloats * 4), a256((size_t)kSplitCounters * 4)};         // GEMM split-k
   size_t total = 0;
   for (size_t v : sizes) total += v;
   hipError_t e = hipMalloc(&b->arena, total);
@@ -411,6 +418,10 @@ nd_status nd_batch_create(nd_ctx* ctx, nd_decoder* dec, uint32_t batch, uint32_t
   take(&b->logprobs);
   take(&b->history);
   take(&b->lp_history);
+  take(&b->gsplit.partials);
+  take(&b->gsplit.counters);
+  b->gsplit.partial_floats = kSplitPartialFloats;
+  b->gsplit.counter_count = kSplitCounters;
   *out = b;
   return ND_OK;
 }
@@ -502,7 +513,7 @@ nd_status nd_batch_step(nd_ctx* ctx, nd_batch* b, uint32_t max_position, uint32_
   for (uint32_t l = 0; l < dec->layers; ++l) {
     ND_HIP(ctx, nd_launch_digitize(b->x, D, dec->norms + dec->attn_off + (size_t)l * D, nullptr,
                                    b->digits, b->fm, B, D, s));
-    ND_HIP(ctx, nd_launch_gemm(&dec->wqkv[l], b->digits, b->fm, b->qkv, qkv_rows, B, 0, s));
+    ND_HIP(ctx, nd_launch_gemm(&dec->wqkv[l], b->digits, b->fm, b->qkv, qkv_rows, B, 0, s, &b->gsplit));
     hipLaunchKernelGGL(qk_rope_store_kernel, dim3(dec->heads + dec->kv_heads, B), dim3(64), 0, s,
                        b->qkv, qkv_rows, dec->heads, dec->kv_heads,
                        dec->norms + dec->q_off + (size_t)l * kHd,
@@ -514,16 +525,17 @@ nd_status nd_batch_step(nd_ctx* ctx, nd_batch* b, uint32_t max_position, uint32_
                                           dec->kv_heads, rep, max_position, b->q, b->o,
                                           b->partials, b->counters, s));
     ND_HIP(ctx, nd_launch_digitize(b->o, D, nullptr, nullptr, b->digits, b->fm, B, D, s));
-    ND_HIP(ctx, nd_launch_gemm(dec->wo[l], b->digits, b->fm, b->x, D, B, 1, s));
+    ND_HIP(ctx, nd_launch_gemm(dec->wo[l], b->digits, b->fm, b->x, D, B, 1, s, &b->gsplit));
     ND_HIP(ctx, nd_launch_digitize(b->x, D, dec->norms + dec->ffn_off + (size_t)l * D, nullptr,
                                    b->digits, b->fm, B, D, s));
-    ND_HIP(ctx, nd_launch_gemm(dec->wup[l], b->digits, b->fm, b->h, F, B, 2, s));
+    ND_HIP(ctx, nd_launch_gemm(dec->wup[l], b->digits, b->fm, b->h, F, B, 2, s, &b->gsplit));
     ND_HIP(ctx, nd_launch_digitize(b->h, F, nullptr, nullptr, b->digits, b->fm, B, F, s));
-    ND_HIP(ctx, nd_launch_gemm(dec->wdown[l], b->digits, b->fm, b->x, D, B, 1, s));
+    ND_HIP(ctx, nd_launch_gemm(dec->wdown[l], b->digits, b->fm, b->x, D, B, 1, s, &b->gsplit));
   }
   ND_HIP(ctx, nd_launch_digitize(b->x, D, dec->norms + dec->final_off, nullptr, b->digits, b->fm,
                                  B, D, s));
-  ND_HIP(ctx, nd_launch_gemm(dec->embedding, b->digits, b->fm, b->logits, dec->vocab, B, 0, s));
+  ND_HIP(ctx, nd_launch_gemm(dec->embedding, b->digits, b->fm, b->logits, dec->vocab, B, 0, s,
+                             &b->gsplit));
   const uint32_t words = (dec->vocab + 31) / 32;
   if (use_masks) {
     const uint32_t n = B * words;

@@ -27,22 +27,34 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int kGemmThreads = 256;
 constexpr int kKChunk = 256;             // k per LDS stage
 constexpr int kLdsRow = kKChunk + 16;    // padded row stride (bank spread)
+constexpr int kMaxSplit = 8;             // k slices of a split launch
 
 __device__ __forceinline__ float silu_f(float v) { return v / (1.f + __expf(-v)); }
 
 // MS m-subtiles of 16 and NS n-subtiles of 16 per wave; 4 waves split n.
+// blockIdx.z selects the k slice [z * kslice, +kslice) (kslice = K without a
+// split).  Each 256-wide chunk issues its weight loads first and then stages
+// the digit planes through LDS, so one round trip serves both.  With
+// gridDim.z = S > 1 every workgroup stores its tile's partial sums (fp32 of
+// the three exact integer sums) with agent-coherent stores, counts itself in
+// on the tile's counter, and the last of the S to arrive adds the partials in
+// slice order (deterministic), applies the epilogue and resets the counter.
 template <int MS, int NS, int EPI>
 __global__ __launch_bounds__(kGemmThreads) void gemm_i8_digits_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ sw, const int8_t* __restrict__ D,
     const float* __restrict__ fm, float* __restrict__ Y, uint32_t M, uint32_t N, uint32_t K,
-    uint32_t ldy) {
+    uint32_t ldy, uint32_t kslice, float* __restrict__ part, uint32_t* __restrict__ counters) {
   constexpr int TM = 16 * MS;
   constexpr int TN = 4 * 16 * NS;
+  constexpr int kSlots = MS * NS * 4;  // outputs per thread
   __shared__ __attribute__((aligned(16))) int8_t lds[3][TM][kLdsRow];
 
   const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const uint32_t n0 = blockIdx.x * TN + wave * 16 * NS;
   const uint32_t m0 = blockIdx.y * TM;
+  const uint32_t S = gridDim.z;
+  const uint32_t k_begin = blockIdx.z * kslice;
+  const uint32_t k_end = K - k_begin < kslice ? K : k_begin + kslice;
   const size_t plane = (size_t)M * K;
 
   v4i acc[NS][MS][3];
@@ -54,8 +66,20 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_digits_kernel(
       for (int j = 0; j < 3; ++j) acc[a][b][j] = v4i{0, 0, 0, 0};
 
   const uint32_t lrow = lane & 15, lk = (lane >> 4) * 16;
-  for (uint32_t kc = 0; kc < K; kc += kKChunk) {
-    const uint32_t kw = (K - kc) < (uint32_t)kKChunk ? (K - kc) : (uint32_t)kKChunk;
+  for (uint32_t kc = k_begin; kc < k_end; kc += kKChunk) {
+    const uint32_t kw = (k_end - kc) < (uint32_t)kKChunk ? (k_end - kc) : (uint32_t)kKChunk;
+    // This chunk's weights (clamped addresses past kw, never used).
+    v4i wa[kKChunk / 64][NS];
+#pragma unroll
+    for (int q = 0; q < kKChunk / 64; ++q) {
+      const uint32_t ks = (uint32_t)q * 64 < kw ? q * 64 : 0;
+#pragma unroll
+      for (int a = 0; a < NS; ++a) {
+        const uint32_t n = n0 + a * 16 + lrow;
+        const uint32_t nn = n < N ? n : N - 1;
+        wa[q][a] = *reinterpret_cast<const v4i*>(W + (size_t)nn * K + kc + ks + lk);
+      }
+    }
     __syncthreads();
     // Stage digits of rows [m0, m0 + TM) and k [kc, kc + kw) into LDS.
     const uint32_t vec_per_row = kw / 16;
@@ -68,49 +92,85 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_digits_kernel(
       *reinterpret_cast<uint4*>(&lds[j][r][c * 16]) = v;
     }
     __syncthreads();
-    for (uint32_t ks = 0; ks < kw; ks += 64) {
-      v4i wa[NS];
 #pragma unroll
-      for (int a = 0; a < NS; ++a) {
-        const uint32_t n = n0 + a * 16 + lrow;
-        const uint32_t nn = n < N ? n : N - 1;
-        wa[a] = *reinterpret_cast<const v4i*>(W + (size_t)nn * K + kc + ks + lk);
-      }
+    for (int q = 0; q < kKChunk / 64; ++q) {
+      if ((uint32_t)q * 64 >= kw) break;
 #pragma unroll
       for (int b = 0; b < MS; ++b) {
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
-          const v4i db = *reinterpret_cast<const v4i*>(&lds[j][b * 16 + lrow][ks + lk]);
+          const v4i db = *reinterpret_cast<const v4i*>(&lds[j][b * 16 + lrow][q * 64 + lk]);
 #pragma unroll
           for (int a = 0; a < NS; ++a)
-            acc[a][b][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[a], db, acc[a][b][j], 0, 0, 0);
+            acc[a][b][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[q][a], db, acc[a][b][j], 0, 0, 0);
         }
       }
     }
   }
 
-  // Epilogue: lane l, element i -> n = n0 + 16a + 4(l/16) + i, m = m0 + 16b + l%16.
+  // Output (a, b, i) of lane l: n = n0 + 16a + 4(l/16) + i, m = m0 + 16b + l%16.
+  auto emit = [&](int a, int b, int i, float c) {
+    const uint32_t m = m0 + b * 16 + lrow;
+    const uint32_t n = n0 + a * 16 + (lane >> 4) * 4 + i;
+    if (m >= M || n >= N) return;
+    const float v = sw[n] * (fm[m] * c);
+    float* dst = Y + (size_t)m * ldy + n;
+    if constexpr (EPI == 0) *dst = v;
+    else if constexpr (EPI == 1) *dst = *dst + v;
+    else *dst = silu_f(v);
+  };
+  float cs[kSlots];
 #pragma unroll
-  for (int a = 0; a < NS; ++a) {
+  for (int a = 0; a < NS; ++a)
 #pragma unroll
-    for (int b = 0; b < MS; ++b) {
-      const uint32_t m = m0 + b * 16 + lrow;
-      if (m >= M) continue;
-      const float f = fm[m];
+    for (int b = 0; b < MS; ++b)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t n = n0 + a * 16 + (lane >> 4) * 4 + i;
-        if (n >= N) continue;
-        const float c = (float)acc[a][b][0][i] + 256.f * (float)acc[a][b][1][i] +
-                        65536.f * (float)acc[a][b][2][i];
-        const float v = sw[n] * (f * c);
-        float* dst = Y + (size_t)m * ldy + n;
-        if constexpr (EPI == 0) *dst = v;
-        else if constexpr (EPI == 1) *dst = *dst + v;
-        else *dst = silu_f(v);
-      }
+      for (int i = 0; i < 4; ++i)
+        cs[(a * MS + b) * 4 + i] = (float)acc[a][b][0][i] + 256.f * (float)acc[a][b][1][i] +
+                                   65536.f * (float)acc[a][b][2][i];
+  if constexpr (MS == 1 && NS == 1) {  // the decode tile; the launcher splits no other
+  if (S > 1) {
+    const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x;
+    float* mine = part + ((size_t)tile * S + blockIdx.z) * (TM * TN);
+#pragma unroll
+    for (int q = 0; q < kSlots; ++q)
+      __hip_atomic_store(mine + q * kGemmThreads + t, cs[q], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // every store above has completed
+    __syncthreads();
+    __shared__ uint32_t s_last;
+    if (t == 0)
+      s_last = __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+    __syncthreads();
+    if (!s_last) return;
+    const float* all = part + (size_t)tile * S * (TM * TN);
+    float pv[kMaxSplit][kSlots];
+#pragma unroll
+    for (int z = 0; z < kMaxSplit; ++z) {
+      const uint32_t zc = (uint32_t)z < S ? z : 0;  // past S: reread slice 0, then drop
+#pragma unroll
+      for (int q = 0; q < kSlots; ++q)
+        pv[z][q] = __hip_atomic_load(all + (size_t)zc * (TM * TN) + q * kGemmThreads + t,
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+#pragma unroll
+    for (int q = 0; q < kSlots; ++q) {
+      float sum = pv[0][q];
+#pragma unroll
+      for (int z = 1; z < kMaxSplit; ++z)
+        if ((uint32_t)z < S) sum += pv[z][q];
+      cs[q] = sum;
+    }
+    if (t == 0) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  }
+#pragma unroll
+  for (int a = 0; a < NS; ++a)
+#pragma unroll
+    for (int b = 0; b < MS; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) emit(a, b, i, cs[(a * MS + b) * 4 + i]);
 }
 
 // Row-wise digit split of A (optionally after the zero-centred RMS norm of
@@ -182,7 +242,7 @@ __global__ __launch_bounds__(256) void digitize_kernel(const float* __restrict__
 }
 
 using GemmFn = void (*)(const int8_t*, const float*, const int8_t*, const float*, float*, uint32_t,
-                        uint32_t, uint32_t, uint32_t);
+                        uint32_t, uint32_t, uint32_t, uint32_t, float*, uint32_t*);
 
 template <int EPI>
 GemmFn pick(uint32_t ms, uint32_t ns) {
@@ -202,15 +262,29 @@ hipError_t nd_launch_digitize(const float* x, uint32_t ldx, const float* norm, f
 
 // Tile choice: decode-sized M (<= 64) uses 16-row m tiles so that even
 // N = 512 spreads over 32+ workgroups; prefill-sized M uses 64 x 128 tiles.
+// With `split`, a grid of fewer than 256 tiles also splits k (K % 256 == 0)
+// into S = 2..8 slices until tiles * S reaches 256, within the workspace
+// (16 x 64 tiles only).
 hipError_t nd_launch_gemm(const nd_mat* w, const int8_t* digits, const float* fm, float* y,
-                          uint32_t ldy, uint32_t M, int epilogue, hipStream_t s) {
+                          uint32_t ldy, uint32_t M, int epilogue, hipStream_t s,
+                          const nd_gemm_split* split) {
   if (M == 0) return hipSuccess;
   const uint32_t ms = M > 64 ? 4 : 1;
   const uint32_t ns = (M > 64 || w->n >= 8192) ? 2 : 1;
   const uint32_t tm = 16 * ms, tn = 64 * ns;
   GemmFn f = epilogue == 0 ? pick<0>(ms, ns) : epilogue == 1 ? pick<1>(ms, ns) : pick<2>(ms, ns);
-  dim3 grid((w->n + tn - 1) / tn, (M + tm - 1) / tm);
+  dim3 grid((w->n + tn - 1) / tn, (M + tm - 1) / tm, 1);
+  const uint32_t tiles = grid.x * grid.y;
+  if (split && ms == 1 && ns == 1 && w->k % kKChunk == 0 && tiles <= split->counter_count) {
+    const uint32_t chunks = w->k / kKChunk;
+    uint32_t S = 1;
+    while (S * 2 <= (uint32_t)kMaxSplit && chunks % (S * 2) == 0 && tiles * S < 256 &&
+           (size_t)tiles * S * 2 * tm * tn <= split->partial_floats)
+      S *= 2;
+    grid.z = S;
+  }
   hipLaunchKernelGGL(f, grid, dim3(kGemmThreads), 0, s, w->w, w->scales, digits, fm, y, M, w->n,
-                     w->k, ldy);
+                     w->k, ldy, w->k / grid.z, split ? split->partials : nullptr,
+                     split ? split->counters : nullptr);
   return hipGetLastError();
 }

@@ -100,8 +100,19 @@ hipError_t nd_launch_select_mask(const float* logits, uint32_t batch, uint32_t v
 // digitize.
 hipError_t nd_launch_digitize(const float* x, uint32_t ldx, const float* norm, float* norm_out,
                               int8_t* digits, float* fm, uint32_t M, uint32_t K, hipStream_t s);
+// Split-k workspace of nd_launch_gemm: partial sums (partial_floats floats)
+// and counter_count arrival counters, zero when first used and left zero by
+// every launch that completes.  Launches that share a workspace must be
+// ordered (one stream).
+struct nd_gemm_split {
+  float* partials;
+  size_t partial_floats;
+  uint32_t* counters;
+  uint32_t counter_count;
+};
 hipError_t nd_launch_gemm(const nd_mat* w, const int8_t* digits, const float* fm, float* y,
-                          uint32_t ldy, uint32_t M, int epilogue, hipStream_t s);
+                          uint32_t ldy, uint32_t M, int epilogue, hipStream_t s,
+                          const nd_gemm_split* split = nullptr);
 hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint32_t* positions,
                                      uint32_t batch, uint32_t seq_kv_heads, uint32_t kv_stride_z,
                                      uint32_t rep, uint32_t max_position, const float* q,
