@@ -179,6 +179,89 @@ __global__ __launch_bounds__(kSelectThreads) void select_mask_kernel(
   }
 }
 
+// Register-resident form for vocab % 32 == 0 and vocab <= 32 * 1024: thread
+// t holds ids [32 t, 32 t + 32) -- eight 16-byte loads and one mask word --
+// so the row is read once, the masked argmax and the JavaScript max come out
+// of one pass and one LDS round, and the float64 exp sum runs from registers.
+// Same selection and log-probability as select_mask_kernel.
+__global__ __launch_bounds__(kSelectThreads) void select_mask_reg_kernel(
+    const float* __restrict__ logits_all, uint32_t vocab, const uint32_t* __restrict__ mask_all,
+    uint32_t* __restrict__ ids, double* __restrict__ logprobs) {
+  __shared__ float s_v[16], s_mx[16];
+  __shared__ uint32_t s_o[16], s_first[16];
+  __shared__ double s_sum[16];
+  const uint32_t r = blockIdx.x, t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const float* logits = logits_all + (size_t)r * vocab;
+  const uint32_t words = vocab / 32;
+  const bool mine = t < words;
+  const uint32_t tc = mine ? t : 0;
+  const float4* src = reinterpret_cast<const float4*>(logits + (size_t)tc * 32);
+  float v[32];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const float4 f = src[q];
+    v[4 * q] = f.x;
+    v[4 * q + 1] = f.y;
+    v[4 * q + 2] = f.z;
+    v[4 * q + 3] = f.w;
+  }
+  const uint32_t m = !mine ? 0u : mask_all ? mask_all[(size_t)r * words + tc] : 0xFFFFFFFFu;
+  Best b{-INFINITY, kNone};
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    mx = js_maxf(mx, v[j]);
+    if (((m >> j) & 1u) && v[j] == v[j] && (b.order == kNone || v[j] > b.v))
+      b = Best{v[j], t * 32 + j};
+  }
+  if (!mine) mx = -INFINITY;
+  uint32_t first = m ? t * 32 + (uint32_t)__builtin_ctz(m) : kNone;
+  for (int o = 32; o >= 1; o >>= 1) {
+    Best other{__shfl_xor(b.v, o, 64), (uint32_t)__shfl_xor((int)b.order, o, 64)};
+    if (better(other, b)) b = other;
+    mx = js_maxf(mx, __shfl_xor(mx, o, 64));
+    first = min(first, (uint32_t)__shfl_xor((int)first, o, 64));
+  }
+  if (lane == 0) {
+    s_v[w] = b.v;
+    s_o[w] = b.order;
+    s_mx[w] = mx;
+    s_first[w] = first;
+  }
+  __syncthreads();
+  mx = s_mx[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) mx = js_maxf(mx, s_mx[i]);
+  double sum = 0.0;
+  if (mine) {
+    const double md = (double)mx;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) sum += exp((double)v[j] - md);
+  }
+  for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  if (lane == 0) s_sum[w] = sum;
+  __syncthreads();
+  if (t != 0) return;
+  Best best{s_v[0], s_o[0]};
+  uint32_t f = s_first[0];
+  double total = s_sum[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) {
+    const Best other{s_v[i], s_o[i]};
+    if (better(other, best)) best = other;
+    f = min(f, s_first[i]);
+    total += s_sum[i];
+  }
+  if (f == kNone) {
+    ids[r] = kNone;
+    logprobs[r] = __builtin_nan("");
+    return;
+  }
+  const uint32_t id = (logits[f] != logits[f] || best.order == kNone) ? f : best.order;
+  ids[r] = id;
+  logprobs[r] = (double)logits[id] - (double)mx - log(total);
+}
+
 }  // namespace
 
 hipError_t nd_launch_select_list(const float* logits, uint32_t vocab, const uint32_t* allowed,
@@ -192,7 +275,11 @@ hipError_t nd_launch_select_mask(const float* logits, uint32_t batch, uint32_t v
                                  const uint32_t* mask, uint32_t* ids, double* logprobs,
                                  hipStream_t s) {
   if (batch == 0) return hipSuccess;
-  hipLaunchKernelGGL(select_mask_kernel, dim3(batch), dim3(kSelectThreads), 0, s, logits, vocab,
-                     mask, ids, logprobs);
+  if (vocab % 32 == 0 && vocab <= 32u * kSelectThreads)
+    hipLaunchKernelGGL(select_mask_reg_kernel, dim3(batch), dim3(kSelectThreads), 0, s, logits,
+                       vocab, mask, ids, logprobs);
+  else
+    hipLaunchKernelGGL(select_mask_kernel, dim3(batch), dim3(kSelectThreads), 0, s, logits, vocab,
+                       mask, ids, logprobs);
   return hipGetLastError();
 }

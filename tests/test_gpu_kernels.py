@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import oracle
-from helpers import assert_close
+from helpers import DeviceArray, assert_close
 from needle_hip import HipKvCache, Int8Matrix, MatrixRowRange, MatvecRequest, NeedleError
 from needle_hip import synth
 
@@ -218,6 +218,51 @@ def test_attention_split_chunks_every_head_ratio(hip, hkv, hq, sink, window):
 
 
 # ---------------------------------------------------------------- selection
+
+@pytest.mark.parametrize("vocab", [32768, 4096, 1000])
+def test_select_mask_batch_on_device(hip, vocab):
+    """Masked selection over a batch of rows in HBM (nd_select_mask_d): ids
+    bit-exact and log-probabilities to 1e-9, with ties, NaN logits inside and
+    outside the allowed set, a NaN first candidate and an empty mask.  1000
+    is not a multiple of 32 and takes the general kernel."""
+    say("select mask batch", vocab)
+    s = synth.Stream(17, f"selmask{vocab}")
+    B = 8
+    logits = (s.normal((B, vocab)) * 3.0).astype(np.float32)
+    words = (vocab + 31) // 32
+    allowed = s.uniform01(B * vocab).reshape(B, vocab) < 0.02
+    allowed[:, 5] = True  # every row but the empty one has candidates
+    allowed[1, 900] = True
+    logits[1, [5, 900]] = 50.0  # tie: the earlier id wins
+    logits[2, np.flatnonzero(allowed[2])[1]] = np.nan  # NaN candidate never wins
+    logits[3, np.flatnonzero(allowed[3])[0]] = np.nan  # NaN first candidate is kept
+    allowed[4] = False  # empty mask
+    logits[5, np.flatnonzero(~allowed[5])[3]] = np.nan  # NaN outside: log-prob NaN
+    masks = np.zeros((B, words), np.uint32)
+    for r in range(B):
+        for i in np.flatnonzero(allowed[r]):
+            masks[r, i >> 5] |= np.uint32(1 << (int(i) & 31))
+    bufs = [DeviceArray(a) for a in (logits, masks, np.zeros(B, np.uint32), np.zeros(B))]
+    dl, dm, ids, lps = bufs
+    hip._check(hip.lib.nd_select_mask_d(hip.ctx, dl.ptr, B, vocab, dm.ptr, ids.ptr, lps.ptr, None),
+               "nd_select_mask_d")
+    got_ids, got_lps = ids.read(), lps.read()
+    for b in bufs:
+        b.free()
+    for r in range(B):
+        if r == 4:  # empty set: the oracle refuses it, the batch kernel flags the row
+            with pytest.raises(oracle.OracleError):
+                oracle.select_mask(logits[r], masks[r])
+            assert int(got_ids[r]) == 0xFFFFFFFF and math.isnan(got_lps[r])
+            continue
+        want_id, want_lp = oracle.select_mask(logits[r], masks[r])
+        assert int(got_ids[r]) == want_id, (vocab, r)
+        if math.isnan(want_lp):
+            assert math.isnan(got_lps[r]), (vocab, r)
+        else:
+            assert abs(got_lps[r] - want_lp) <= 1e-9 * max(1.0, abs(want_lp)), (vocab, r)
+    assert int(got_ids[1]) == 5 and int(got_ids[4]) == 0xFFFFFFFF
+
 
 def test_select_golden_cases(hip):
     say("select golden")
