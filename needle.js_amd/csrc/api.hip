@@ -52,9 +52,9 @@ static nd_status ensure_partials(nd_ctx* ctx, size_t floats) {
   ND_HIP(ctx, hipMalloc(&ctx->attn_partials, floats * sizeof(float)));
   ctx->attn_partial_floats = floats;
   if (!ctx->attn_counters) {
-    ND_HIP(ctx, hipMalloc(&ctx->attn_counters, kMaxAttentionKvHeads * sizeof(uint32_t)));
-    ND_HIP(ctx, hipMemsetAsync(ctx->attn_counters, 0, kMaxAttentionKvHeads * sizeof(uint32_t),
-                               ctx->stream));
+    const size_t cbytes = (size_t)kMaxAttentionKvHeads * kAttnCounterStride * sizeof(uint32_t);
+    ND_HIP(ctx, hipMalloc(&ctx->attn_counters, cbytes));
+    ND_HIP(ctx, hipMemsetAsync(ctx->attn_counters, 0, cbytes, ctx->stream));
     ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
   }
   return ND_OK;

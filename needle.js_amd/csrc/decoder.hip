@@ -374,7 +374,7 @@ nd_status nd_batch_create(nd_ctx* ctx, nd_decoder* dec, uint32_t batch, uint32_t
       a256((size_t)batch * 4),                                               // fm
       a256(pf * 4),                                                          // partials
       a256((size_t)3 * batch * kmax),                                        // digits
-      a256((size_t)batch * dec->kv_heads * 4),                               // counters
+      a256((size_t)batch * dec->kv_heads * kAttnCounterStride * 4),          // counters
       a256((size_t)batch * words * 4),                                       // masks
       a256((size_t)batch * 4), a256((size_t)batch * 4), a256(256),           // tokens, positions, step
       a256((size_t)batch * 4), a256((size_t)batch * 8),                      // ids, logprobs
@@ -588,7 +588,7 @@ nd_status nd_prefill_create(nd_ctx* ctx, nd_decoder* dec, uint32_t max_tokens,
                           a256(M * dec->dim * 4),  a256(M * dec->ffn * 4), a256(M * 4),
                           a256(p->partial_floats * 4), a256((size_t)dec->vocab * 4),
                           a256(3 * M * kmax),      a256(M * 4),            a256(M * 4),
-                          a256(M * dec->kv_heads * 4)};
+                          a256(M * dec->kv_heads * kAttnCounterStride * 4)};
   size_t total = 0;
   for (size_t v : sizes) total += v;
   hipError_t e = hipMalloc(&p->arena, total);

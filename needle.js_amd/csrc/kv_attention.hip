@@ -14,6 +14,7 @@ constexpr uint32_t kHeadDim = 64;
 constexpr uint32_t kWavePositions = 64;  // positions a wave handles per iteration
 constexpr uint32_t kWaves = 4;           // waves per attention workgroup
 constexpr uint32_t kMinChunk = kWavePositions * kWaves;
+constexpr uint32_t kChunkGroup = 8;  // chunks per first-level arrival counter
 
 __device__ __forceinline__ uint32_t kv_slot(uint32_t position, uint32_t sink, uint32_t window) {
   if (window == 0 || position < sink) return position;
@@ -401,11 +402,32 @@ __global__ __launch_bounds__(256) void attention_kernel(
   }
   __builtin_amdgcn_s_waitcnt(0);  // every store above has completed
   __syncthreads();
+  // Election: rows of more than kChunkGroup chunks count in per group first
+  // and the last of each group then on the row's counter, so that no counter
+  // serializes more than kChunkGroup arrivals (atomics on one address
+  // complete ~70 ns apart).  Each counter is reset by its last arriver.
   __shared__ uint32_t s_last;
-  uint32_t* counter = counters + (size_t)z * seq_kv_heads + kvh_local;
-  if (threadIdx.x == 0)
-    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+  uint32_t* counter = counters + ((size_t)z * seq_kv_heads + kvh_local) * kAttnCounterStride;
+  if (threadIdx.x == 0) {
+    bool last;
+    if (nchunks <= kChunkGroup) {
+      last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
              nchunks - 1;
+    } else {
+      const uint32_t grp = chunk / kChunkGroup;
+      const uint32_t ngroups = (nchunks + kChunkGroup - 1) / kChunkGroup;
+      const uint32_t members = min(kChunkGroup, nchunks - grp * kChunkGroup);
+      uint32_t* gc = counter + 1 + grp;
+      last = false;
+      if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+          members - 1) {
+        __hip_atomic_store(gc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               ngroups - 1;
+      }
+    }
+    s_last = last;
+  }
   __syncthreads();
   if (!s_last) return;
 
@@ -482,12 +504,13 @@ __global__ __launch_bounds__(256) void attention_kernel(
 // Positions per chunk: the whole visible range when the (row, kv head) pairs
 // alone give `target` workgroups, else split so that they do; at least one
 // tile per wave.  Splitting costs a publish + count + merge round trip at the
-// end, so a single query row aims at 128 workgroups (16 chunks of 512 per
-// head at 8 heads x 8192: the measured optimum) and batches at 4096 (64
-// sequences x 8 heads at contexts up to 2048: 0.635 ms per decode step, vs
-// 0.698 at 1024 and 0.638 at 2048).
-constexpr uint32_t kTargetSingle = 128, kTargetBatch = 4096;
+// end, so a single query row aims at 256 workgroups (32 chunks of 256 per
+// head at 8 heads x 8192, elected in groups of 8: 8.1 us per call, vs 8.9 at
+// 128 workgroups) and batches at 4096 (64 sequences x 8 heads at contexts up
+// to 2048: 0.635 ms per decode step, vs 0.698 at 1024 and 0.638 at 2048).
+constexpr uint32_t kTargetSingle = 256, kTargetBatch = 4096;
 constexpr uint32_t kMaxChunks = 64;  // the merge holds one chunk per lane
+static_assert(1 + kMaxChunks / kChunkGroup <= kAttnCounterStride, "group counters fit the stride");
 uint32_t chunk_positions_for(uint32_t max_count, uint32_t pairs, uint32_t target) {
   uint32_t want_chunks = pairs >= target ? 1 : (target + pairs - 1) / pairs;
   // Up to two tiles per wave stay in one chunk: the merge round trips cost

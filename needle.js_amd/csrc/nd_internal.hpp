@@ -119,10 +119,12 @@ hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint
                                      float* out, float* partials, uint32_t* counters,
                                      hipStream_t s, const float* gate = nullptr,
                                      uint32_t gate_ld = 0);
-// Attention launches take `counters`: one zero-initialized word per (query
-// row, KV head) -- index z * seq_kv_heads + kv head -- which a launch that
-// splits a row into several chunks uses to elect the chunk that merges them,
-// and leaves at zero again.
+// Attention launches take `counters`: kAttnCounterStride zero-initialized
+// words per (query row, KV head) -- from (z * seq_kv_heads + kv head) *
+// kAttnCounterStride -- which a launch that splits a row into several chunks
+// uses to elect the chunk that merges them (a counter per group of chunks,
+// then one per row and head), and leaves at zero again.
+constexpr uint32_t kAttnCounterStride = 16;
 //
 // One query row whose position is read from device memory (*position <=
 // max_position); out = attention * sigmoid(gate) elementwise when gate is set

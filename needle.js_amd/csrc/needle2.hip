@@ -1047,7 +1047,7 @@ nd_status ensure_prefill(nd_ctx* ctx, nd_needle* n) {
                           al((size_t)cap * S * 2 * D * 4), al((size_t)cap * S * D * 4),
                           al((size_t)cap * 4),          al(pf * 4),
                           al((size_t)3 * cap * kmax),   al((size_t)cap * 4),
-                          al((size_t)cap * d.kv_heads * 4)};
+                          al((size_t)cap * d.kv_heads * kAttnCounterStride * 4)};
   size_t total = 0;
   for (size_t v : sizes) total += v;
   hipError_t e = hipMalloc(&n->pf_arena, total);
@@ -1463,7 +1463,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     const uint32_t cat = d.n_sites ? d.engram_tables * d.engram_sub : 1;
     // State first (cleared by every reset), then scratch.
     const size_t sizes[] = {al(64), al((size_t)cap * 4), al((size_t)cap * 8),
-                            al((size_t)S * n->depth * D * 4), al((size_t)d.kv_heads * 4), al(64), al(64),
+                            al((size_t)S * n->depth * D * 4), al((size_t)d.kv_heads * kAttnCounterStride * 4), al(64), al(64),
                             al((size_t)d.vocab * 4), al(rows * kHd), al(rows * kHd), al(rows * 4),
                             al(rows * 4), al((size_t)ln * D * 4), al(D * 4), al(D * 4), al(D * 4),
                             al((size_t)(2 * qw + 2 * kw) * 4), al(qw * 4), al(qw * 4), al(D * 4),
