@@ -510,10 +510,19 @@ nd_status nd_batch_step(nd_ctx* ctx, nd_batch* b, uint32_t max_position, uint32_
   hipLaunchKernelGGL(embed_kernel, dim3((D + 255) / 256, B), dim3(256), 0, s, dec->embedding->w,
                      dec->embedding->scales, b->tokens, dec->vocab, D, std::sqrt((double)D), b->x);
   ND_HIP(ctx, hipGetLastError());
+  // x (optionally normalized) times w into y: one launch that digitizes its
+  // own chunks where the shape allows, else digitize + GEMM.
+  auto product = [&](const nd_mat* w, const float* x, const float* norm, float* y, uint32_t ldy,
+                     int epi) -> hipError_t {
+    if (nd_gemm_f32_fits(w, x, w->k, norm != nullptr, B, &b->gsplit))
+      return nd_launch_gemm_f32(w, x, w->k, norm, y, ldy, B, epi, s, &b->gsplit);
+    hipError_t e = nd_launch_digitize(x, w->k, norm, nullptr, b->digits, b->fm, B, w->k, s);
+    if (e != hipSuccess) return e;
+    return nd_launch_gemm(w, b->digits, b->fm, y, ldy, B, epi, s, &b->gsplit);
+  };
   for (uint32_t l = 0; l < dec->layers; ++l) {
-    ND_HIP(ctx, nd_launch_digitize(b->x, D, dec->norms + dec->attn_off + (size_t)l * D, nullptr,
-                                   b->digits, b->fm, B, D, s));
-    ND_HIP(ctx, nd_launch_gemm(&dec->wqkv[l], b->digits, b->fm, b->qkv, qkv_rows, B, 0, s, &b->gsplit));
+    ND_HIP(ctx, product(&dec->wqkv[l], b->x, dec->norms + dec->attn_off + (size_t)l * D, b->qkv,
+                        qkv_rows, 0));
     hipLaunchKernelGGL(qk_rope_store_kernel, dim3(dec->heads + dec->kv_heads, B), dim3(64), 0, s,
                        b->qkv, qkv_rows, dec->heads, dec->kv_heads,
                        dec->norms + dec->q_off + (size_t)l * kHd,
@@ -524,18 +533,11 @@ nd_status nd_batch_step(nd_ctx* ctx, nd_batch* b, uint32_t max_position, uint32_
     ND_HIP(ctx, nd_launch_attention_batch(&b->kv, l, b->positions, B, dec->kv_heads,
                                           dec->kv_heads, rep, max_position, b->q, b->o,
                                           b->partials, b->counters, s));
-    ND_HIP(ctx, nd_launch_digitize(b->o, D, nullptr, nullptr, b->digits, b->fm, B, D, s));
-    ND_HIP(ctx, nd_launch_gemm(dec->wo[l], b->digits, b->fm, b->x, D, B, 1, s, &b->gsplit));
-    ND_HIP(ctx, nd_launch_digitize(b->x, D, dec->norms + dec->ffn_off + (size_t)l * D, nullptr,
-                                   b->digits, b->fm, B, D, s));
-    ND_HIP(ctx, nd_launch_gemm(dec->wup[l], b->digits, b->fm, b->h, F, B, 2, s, &b->gsplit));
-    ND_HIP(ctx, nd_launch_digitize(b->h, F, nullptr, nullptr, b->digits, b->fm, B, F, s));
-    ND_HIP(ctx, nd_launch_gemm(dec->wdown[l], b->digits, b->fm, b->x, D, B, 1, s, &b->gsplit));
+    ND_HIP(ctx, product(dec->wo[l], b->o, nullptr, b->x, D, 1));
+    ND_HIP(ctx, product(dec->wup[l], b->x, dec->norms + dec->ffn_off + (size_t)l * D, b->h, F, 2));
+    ND_HIP(ctx, product(dec->wdown[l], b->h, nullptr, b->x, D, 1));
   }
-  ND_HIP(ctx, nd_launch_digitize(b->x, D, dec->norms + dec->final_off, nullptr, b->digits, b->fm,
-                                 B, D, s));
-  ND_HIP(ctx, nd_launch_gemm(dec->embedding, b->digits, b->fm, b->logits, dec->vocab, B, 0, s,
-                             &b->gsplit));
+  ND_HIP(ctx, product(dec->embedding, b->x, dec->norms + dec->final_off, b->logits, dec->vocab, 0));
   const uint32_t words = (dec->vocab + 31) / 32;
   if (use_masks) {
     const uint32_t n = B * words;

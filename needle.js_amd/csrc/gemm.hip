@@ -19,6 +19,7 @@
 // column l%16 (activation row m).  Any k order shared by both operands gives
 // the same sum, so both are read straight from row-major memory.
 #include "nd_internal.hpp"
+#include "nd_wave.hpp"
 
 namespace {
 
@@ -28,6 +29,7 @@ constexpr int kGemmThreads = 256;
 constexpr int kKChunk = 256;             // k per LDS stage
 constexpr int kLdsRow = kKChunk + 16;    // padded row stride (bank spread)
 constexpr int kMaxSplit = 8;             // k slices of a split launch
+constexpr uint32_t kMaxNormK = 1024;     // rows the fused norm reads whole
 
 __device__ __forceinline__ float silu_f(float v) { return v / (1.f + __expf(-v)); }
 
@@ -241,6 +243,187 @@ __global__ __launch_bounds__(256) void digitize_kernel(const float* __restrict__
   if (t == 0) fm[m] = ldexpf(1.f, e - 21);
 }
 
+// Decode-shaped product (M <= 64 rows per launch, 16 x 64 output tiles) that
+// digitizes its own activations: workgroup (n tile, m tile, z) reads the fp32
+// rows of its 16 x 256 k chunk z (and, with NORM, the whole rows for the
+// zero-centred RMS norm of math.ts:16-32), writes the three digit planes of
+// that chunk with the chunk's own exponent -- 2^(E - 21), max |a| in
+// [2^E, 2^(E+1)) over the row's 256 values, so each value is carried to
+// 2^-22 of the chunk's largest -- and multiplies them as the kernel above.
+// Thread t of the staging holds row t / 16, columns [16 (t % 16), +16): a
+// row is one DPP row of 16 lanes, so its sum of squares and its maximum are
+// DPP reductions.  Slices (gridDim.z = K / 256) are combined as in the kernel
+// above, each partial already scaled by its chunk's factor.
+template <int EPI, bool NORM>
+__global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
+    const int8_t* __restrict__ W, const float* __restrict__ sw, const float* __restrict__ X,
+    uint32_t ldx, const float* __restrict__ norm, float* __restrict__ Y, uint32_t M, uint32_t N,
+    uint32_t K, uint32_t ldy, float* __restrict__ part, uint32_t* __restrict__ counters) {
+  __shared__ __attribute__((aligned(16))) int8_t lds[3][16][kLdsRow];
+  __shared__ float s_fm[16];
+  const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const uint32_t n0 = blockIdx.x * 64 + wave * 16;
+  const uint32_t m0 = blockIdx.y * 16;
+  const uint32_t S = gridDim.z, kc = blockIdx.z * kKChunk;
+  const uint32_t lrow = lane & 15, lk = (lane >> 4) * 16;
+
+  // Weights of the chunk first.
+  v4i wa[kKChunk / 64];
+  {
+    const uint32_t n = n0 + lrow;
+    const int8_t* wr = W + (size_t)(n < N ? n : N - 1) * K + kc + lk;
+#pragma unroll
+    for (int q = 0; q < kKChunk / 64; ++q) wa[q] = *reinterpret_cast<const v4i*>(wr + q * 64);
+  }
+  // Activations: row r of the tile, 16 values of the chunk (and the row's
+  // other chunks for the norm; K <= kMaxNormK then).
+  const uint32_t r = t >> 4, pc = t & 15;
+  const uint32_t m = m0 + r;
+  const float* xr = X + (size_t)(m < M ? m : M - 1) * ldx;
+  float v[16];
+  {
+    const float4* src = reinterpret_cast<const float4*>(xr + kc + pc * 16);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 f = src[q];
+      v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+    }
+  }
+  float4 wn[4];  // this chunk's norm weights, in flight with the activations
+  if constexpr (NORM) {
+    const float4* src = reinterpret_cast<const float4*>(norm + kc + pc * 16);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) wn[q] = src[q];
+  }
+  if constexpr (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ss = fmaf(v[i], v[i], ss);
+    for (uint32_t c0 = 0; c0 < K; c0 += kKChunk) {  // the row's other chunks
+      if (c0 == kc) continue;
+      const float4* o = reinterpret_cast<const float4*>(xr + c0 + pc * 16);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 f = o[q];
+        ss = fmaf(f.x, f.x, fmaf(f.y, f.y, fmaf(f.z, f.z, fmaf(f.w, f.w, ss))));
+      }
+    }
+    ss = nd::row_sum(ss);
+    const float inv = 1.f / sqrtf(ss / (float)K + 1e-6f);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 f = wn[q];
+      v[4 * q] = (1.f + f.x) * v[4 * q] * inv;
+      v[4 * q + 1] = (1.f + f.y) * v[4 * q + 1] * inv;
+      v[4 * q + 2] = (1.f + f.z) * v[4 * q + 2] * inv;
+      v[4 * q + 3] = (1.f + f.w) * v[4 * q + 3] * inv;
+    }
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = nd::row_max(amax);
+  int e = 0;
+  if (amax > 0.f) {
+    frexpf(amax, &e);  // amax in [2^(e-1), 2^e)
+    e -= 1;
+  }
+  const float up = ldexpf(1.f, 21 - e);
+  uint32_t d0w[4] = {0, 0, 0, 0}, d1w[4] = {0, 0, 0, 0}, d2w[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int X0 = (int)rintf(v[i] * up);  // |X0| < 2^22
+    const int d0 = ((X0 + 128) & 255) - 128;
+    const int X1 = (X0 - d0) >> 8;
+    const int d1 = ((X1 + 128) & 255) - 128;
+    const int d2 = (X1 - d1) >> 8;
+    d0w[i >> 2] |= (uint32_t)(d0 & 255) << (8 * (i & 3));
+    d1w[i >> 2] |= (uint32_t)(d1 & 255) << (8 * (i & 3));
+    d2w[i >> 2] |= (uint32_t)(d2 & 255) << (8 * (i & 3));
+  }
+  const bool live = m < M;  // rows past M multiply as zeros
+  *reinterpret_cast<uint4*>(&lds[0][r][pc * 16]) =
+      live ? make_uint4(d0w[0], d0w[1], d0w[2], d0w[3]) : make_uint4(0, 0, 0, 0);
+  *reinterpret_cast<uint4*>(&lds[1][r][pc * 16]) =
+      live ? make_uint4(d1w[0], d1w[1], d1w[2], d1w[3]) : make_uint4(0, 0, 0, 0);
+  *reinterpret_cast<uint4*>(&lds[2][r][pc * 16]) =
+      live ? make_uint4(d2w[0], d2w[1], d2w[2], d2w[3]) : make_uint4(0, 0, 0, 0);
+  if (pc == 0) s_fm[r] = ldexpf(1.f, e - 21);
+  __syncthreads();
+
+  v4i acc[3] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+#pragma unroll
+  for (int q = 0; q < kKChunk / 64; ++q) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const v4i db = *reinterpret_cast<const v4i*>(&lds[j][lrow][q * 64 + lk]);
+      acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[q], db, acc[j], 0, 0, 0);
+    }
+  }
+  // Lane l, element i: n = n0 + 4 (l / 16) + i, m = m0 + l % 16.
+  const float fm = s_fm[lrow];
+  float cs[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    cs[i] = fm * ((float)acc[0][i] + 256.f * (float)acc[1][i] + 65536.f * (float)acc[2][i]);
+  if (S > 1) {
+    const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x;
+    float* mine = part + ((size_t)tile * S + blockIdx.z) * 1024;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __hip_atomic_store(mine + i * kGemmThreads + t, cs[i], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // every store above has completed
+    __syncthreads();
+    __shared__ uint32_t s_last;
+    if (t == 0)
+      s_last = __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+    __syncthreads();
+    if (!s_last) return;
+    const float* all = part + (size_t)tile * S * 1024;
+    float pv[kMaxSplit][4];
+#pragma unroll
+    for (int z = 0; z < kMaxSplit; ++z) {
+      const uint32_t zc = (uint32_t)z < S ? z : 0;  // past S: reread slice 0, then drop
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        pv[z][i] = __hip_atomic_load(all + (size_t)zc * 1024 + i * kGemmThreads + t,
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float sum = pv[0][i];
+#pragma unroll
+      for (int z = 1; z < kMaxSplit; ++z)
+        if ((uint32_t)z < S) sum += pv[z][i];
+      cs[i] = sum;
+    }
+    if (t == 0) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const uint32_t mo = m0 + lrow;
+  if (mo >= M) return;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t n = n0 + (lane >> 4) * 4 + i;
+    if (n >= N) continue;
+    const float val = sw[n] * cs[i];
+    float* dst = Y + (size_t)mo * ldy + n;
+    if constexpr (EPI == 0) *dst = val;
+    else if constexpr (EPI == 1) *dst = *dst + val;
+    else *dst = silu_f(val);
+  }
+}
+
+using F32aFn = void (*)(const int8_t*, const float*, const float*, uint32_t, const float*, float*,
+                        uint32_t, uint32_t, uint32_t, uint32_t, float*, uint32_t*);
+
+template <bool NORM>
+F32aFn pick_f32a(int epilogue) {
+  return epilogue == 0 ? &gemm_i8_f32a_kernel<0, NORM>
+       : epilogue == 1 ? &gemm_i8_f32a_kernel<1, NORM> : &gemm_i8_f32a_kernel<2, NORM>;
+}
+
 using GemmFn = void (*)(const int8_t*, const float*, const int8_t*, const float*, float*, uint32_t,
                         uint32_t, uint32_t, uint32_t, uint32_t, float*, uint32_t*);
 
@@ -286,5 +469,34 @@ hipError_t nd_launch_gemm(const nd_mat* w, const int8_t* digits, const float* fm
   hipLaunchKernelGGL(f, grid, dim3(kGemmThreads), 0, s, w->w, w->scales, digits, fm, y, M, w->n,
                      w->k, ldy, w->k / grid.z, split ? split->partials : nullptr,
                      split ? split->counters : nullptr);
+  return hipGetLastError();
+}
+
+// Decode-shaped product on fp32 activations (optionally RMS-normalized with
+// `norm`): one launch instead of digitize + GEMM, for the shapes
+// nd_gemm_f32_fits accepts (M <= 64, K % 256 == 0 with K / 256 <= kMaxSplit
+// slices, K <= kMaxNormK with a norm, the slices' partials and counters
+// within the workspace, 16-byte aligned rows).
+bool nd_gemm_f32_fits(const nd_mat* w, const float* x, uint32_t ldx, bool norm, uint32_t M,
+                      const nd_gemm_split* split) {
+  const uint32_t S = w->k / kKChunk;
+  const uint32_t tiles = ((w->n + 63) / 64) * ((M + 15) / 16);
+  return M >= 1 && M <= 64 && w->k % kKChunk == 0 && S <= (uint32_t)kMaxSplit &&
+         (!norm || w->k <= kMaxNormK) && split &&
+         (S == 1 || (tiles <= split->counter_count &&
+                     (size_t)tiles * S * 1024 <= split->partial_floats)) &&
+         ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+}
+
+hipError_t nd_launch_gemm_f32(const nd_mat* w, const float* x, uint32_t ldx, const float* norm,
+                              float* y, uint32_t ldy, uint32_t M, int epilogue, hipStream_t s,
+                              const nd_gemm_split* split) {
+  if (M == 0) return hipSuccess;
+  if (!nd_gemm_f32_fits(w, x, ldx, norm != nullptr, M, split)) return hipErrorInvalidValue;
+  const uint32_t S = w->k / kKChunk;
+  const F32aFn f = norm ? pick_f32a<true>(epilogue) : pick_f32a<false>(epilogue);
+  hipLaunchKernelGGL(f, dim3((w->n + 63) / 64, (M + 15) / 16, S), dim3(kGemmThreads), 0, s, w->w,
+                     w->scales, x, ldx, norm, y, M, w->n, w->k, ldy, split->partials,
+                     split->counters);
   return hipGetLastError();
 }

@@ -113,6 +113,14 @@ struct nd_gemm_split {
 hipError_t nd_launch_gemm(const nd_mat* w, const int8_t* digits, const float* fm, float* y,
                           uint32_t ldy, uint32_t M, int epilogue, hipStream_t s,
                           const nd_gemm_split* split = nullptr);
+// The same product on fp32 rows x [M][ldx] (optionally RMS-normalized with
+// `norm`, math.ts:16-32), digitized per 256-wide chunk inside the launch;
+// only for the shapes nd_gemm_f32_fits accepts.
+bool nd_gemm_f32_fits(const nd_mat* w, const float* x, uint32_t ldx, bool norm, uint32_t M,
+                      const nd_gemm_split* split);
+hipError_t nd_launch_gemm_f32(const nd_mat* w, const float* x, uint32_t ldx, const float* norm,
+                              float* y, uint32_t ldy, uint32_t M, int epilogue, hipStream_t s,
+                              const nd_gemm_split* split);
 hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint32_t* positions,
                                      uint32_t batch, uint32_t seq_kv_heads, uint32_t kv_stride_z,
                                      uint32_t rep, uint32_t max_position, const float* q,

@@ -55,6 +55,15 @@ __device__ __forceinline__ T wave_sum(T v) {
   return ((readlane(v, 0) + readlane(v, 16)) + readlane(v, 32)) + readlane(v, 48);
 }
 
+// Maximum of each row of 16 lanes (fmaxf), in every lane of the row.
+__device__ __forceinline__ float row_max(float v) {
+  v = fmaxf(v, dpp<kQuadXor1>(v));
+  v = fmaxf(v, dpp<kQuadXor2>(v));
+  v = fmaxf(v, dpp<kHalfMirror>(v));
+  v = fmaxf(v, dpp<kRowMirror>(v));
+  return v;
+}
+
 // JavaScript Math.max of two numbers (NaN if either is NaN).
 __device__ __forceinline__ float js_max(float a, float b) {
   return (a != a || b != b) ? __builtin_nanf("") : (a > b ? a : b);
