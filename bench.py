@@ -122,6 +122,53 @@ def bench_matvec(torch, hip, n, k, g, batch, steps, warmup, rotate=True):
             "ms_per_launch": ms, "GBps": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
 
 
+def cq_matvec_bytes(n, k, g, bits, batch):
+    """Algorithmic bytes of one Cactus-Quant matvec call: packed codes,
+    binary16 norms, x and y (the rotated copy of x is the call's own
+    intermediate)."""
+    kpad = -(-k // g) * g
+    pb = 2 if bits == 5 else bits
+    return n * kpad * pb // 8 + n * (kpad // g) * 2 + batch * k * 4 + batch * n * 4
+
+
+def bench_cq_matvec(torch, hip, n, k, g, bits, batch, steps, warmup):
+    """nd_matvec_d on a CQ matrix (rotation kernel + matvec kernel per call),
+    weights rotated over enough HBM replicas to defeat the Infinity Cache."""
+    import ctypes as C
+
+    from needle_hip import lib as L
+    from needle_hip import synth
+
+    per = cq_matvec_bytes(n, k, g, bits, batch)
+    replicas = max(1, math.ceil(ROTATE_BYTES / per))
+    packed, norms = synth.cq_matrix(2026, f"bench-cq{n}x{k}g{g}b{bits}", n, k, g, bits)
+    codebook = synth.cq_codebook()
+    lo = {2: 0, 3: 4, 4: 12, 5: 0}[bits]
+    book = codebook[lo:]
+    mats = []
+    for _ in range(replicas):
+        h = C.c_void_p()
+        hip._check(hip.lib.nd_mat_upload_cq(hip.ctx, L.ptr(packed), L.ptr(norms), L.ptr(book), n,
+                                            k, g, bits, C.byref(h)))
+        mats.append(h)
+    x = torch.from_numpy(synth.Stream(2026, "bench-x").normal((batch, k))).cuda()
+    y = torch.empty((batch, n), dtype=torch.float32, device="cuda")
+
+    def make(h):
+        return lambda stream: hip._check(hip.lib.nd_matvec_d(
+            hip.ctx, h, x.data_ptr(), batch, 0, n, y.data_ptr(), C.c_void_p(stream)))
+
+    timer = GraphTimer(torch, [make(mats[i % replicas]) for i in range(max(replicas, 32))])
+    replays = max(1, math.ceil(steps / timer.n))
+    ms = timer.time(replays, warmup)
+    for h in mats:
+        hip.lib.nd_mat_free(hip.ctx, h)
+    gbs = per / (ms * 1e-3) / 1e9
+    return {"bits": bits, "group": g, "bytes_per_call": per, "replicas": replicas,
+            "calls": replays * timer.n, "ms_per_call": ms, "GBps": gbs,
+            "frac_hbm": gbs / HBM_PEAK_GBS}
+
+
 def bench_attention(torch, hip, length, heads, steps, warmup, rotate=True):
     import ctypes as C
 
@@ -491,7 +538,7 @@ def main():
     ap.add_argument("--skip-needle2", action="store_true")
     ap.add_argument("--needle2-reps", type=int, default=5)
     ap.add_argument("--only", choices=["matvec", "matvec8", "attention", "decode", "prefill",
-                                       "needle2", "traffic"],
+                                       "needle2", "traffic", "cq"],
                     help="run one part alone and print its JSON (for profiling)")
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--no-check", action="store_true",
@@ -523,6 +570,10 @@ def main():
             part, _ = bench_needle2(torch, hip, args.needle2_reps, False, 0)
         elif args.only == "traffic":
             part = traffic_workload(torch, hip, n, k, g)
+        elif args.only == "cq":
+            part = {f"cq{bits}_matvec_b1_hbm": bench_cq_matvec(torch, hip, n, k, g, bits, 1,
+                                                                 args.steps, args.warmup)
+                    for bits in (2, 3, 4, 5)}
         else:
             part, _ = bench_prefill(torch, hip, 2048, 5, 0)
         print(json.dumps({args.only: part}))
@@ -536,6 +587,11 @@ def main():
                                            rotate=False)
     print(f"[bench] matvec b8 {parts['matvec_b8_hbm']['GBps']:.0f} GB/s, b1 MALL "
           f"{parts['matvec_b1_mall']['GBps']:.0f} GB/s", file=sys.stderr, flush=True)
+    for bits in (2, 3, 4, 5):
+        part = bench_cq_matvec(torch, hip, n, k, g, bits, 1, args.steps, args.warmup)
+        parts[f"cq{bits}_matvec_b1_hbm"] = part
+        print(f"[bench] CQ{bits if bits < 5 else ' ternary'} matvec b1 {part['GBps']:.0f} GB/s "
+              f"{part['ms_per_call'] * 1e3:.2f} us/call", file=sys.stderr, flush=True)
     for length in (512, 2048, 8192):
         parts[f"attention_L{length}_hbm"] = bench_attention(torch, hip, length, 8,
                                                             args.steps // 2, args.warmup)

@@ -35,6 +35,7 @@ typedef int32_t nd_status;
 #define ND_ERR_BACKEND 2     /* HIP failure, no device, disposed: BACKEND_UNAVAILABLE */
 #define ND_ERR_OVERFLOW 3    /* position beyond the runtime length: CONTEXT_OVERFLOW */
 #define ND_ERR_NOMEM 4       /* HBM allocation failed: BACKEND_UNAVAILABLE */
+#define ND_ERR_UNSUPPORTED 5 /* valid record this backend does not run: UNSUPPORTED_CACT */
 
 typedef struct nd_ctx nd_ctx;
 typedef struct nd_mat nd_mat;
@@ -77,6 +78,31 @@ nd_status nd_mat_upload_i8_d(nd_ctx* ctx, const int8_t* w_dev, const float* scal
                              uint32_t n, uint32_t k, uint32_t g, nd_mat** out);
 
 nd_status nd_mat_free(nd_ctx* ctx, nd_mat* mat);
+
+/* Uploads one Cactus-Quant matrix as the archive stores it (CqMatrix,
+ * model/cact.ts:61-75, parsed at cact.ts:346-396): packed codes
+ * [n][row_bytes] with row_bytes = kpad * pb / 8 (kpad = k rounded up to a
+ * multiple of g, pb = bits, or 2 for the ternary width bits = 5), binary16
+ * norms [n][kpad / g], and the width's codebook (2^bits floats: the
+ * archive's entries [0, 4) for CQ2, [4, 12) for CQ3, [12, 28) for CQ4,
+ * cact.ts:272-276; ignored and may be NULL for ternary).  Codes are read
+ * low bits first; 3-bit rows are one little-endian bit stream.  The matrix
+ * works with nd_matvec / nd_matvec_d / nd_matvec_batch (cqMatvec,
+ * backends/cq.ts:106-231: per-group Walsh-Hadamard input rotation, then the
+ * codebook dot products times the group norms) and nd_row / nd_row_d
+ * (dequantizeCqRow, cq.ts:234-295); nd_matmul and the model builders take
+ * int8 matrices only.  g must be a power of two (else ND_ERR_UNSUPPORTED,
+ * as cact.ts:350-359); this backend further needs g >= 8 and kpad <= 8192
+ * after rounding up to a multiple of 32 (ND_ERR_UNSUPPORTED otherwise).
+ * Calls on one context share one buffer of rotated inputs: enqueue them on
+ * one stream. */
+nd_status nd_mat_upload_cq(nd_ctx* ctx, const uint8_t* packed, const uint16_t* norms,
+                           const float* codebook, uint32_t n, uint32_t k, uint32_t g,
+                           uint32_t bits, nd_mat** out);
+
+/* Width (0 for int8 matrices), stored row width in codes (kpad rounded up
+ * to a multiple of 32) and stored packed row bytes. */
+nd_status nd_mat_cq_info(const nd_mat* mat, uint32_t* bits, uint32_t* kpad, uint32_t* row_bytes);
 
 /* HBM addresses of a matrix's codes and scales (for building graphs). */
 nd_status nd_mat_info(const nd_mat* mat, const int8_t** w_dev, const float** scales_dev,

@@ -3,6 +3,7 @@
 // reference's invariants (backends/cq.ts:113-126, model/runtime.ts:150-160,
 // 289-299, 885-891) so that the host binding can raise the same NeedleError
 // codes.
+#include <cmath>
 #include <cstdarg>
 #include <cstring>
 #include <vector>
@@ -62,6 +63,14 @@ static nd_status ensure_partials(nd_ctx* ctx, size_t floats) {
 
 static inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
+static void free_mat_buffers(nd_mat* m) {
+  hipFree(m->w);
+  hipFree(m->scales);
+  hipFree(m->packed);
+  hipFree(m->norms);
+  delete m;
+}
+
 extern "C" {
 
 nd_status nd_create(int32_t device, nd_ctx** out) {
@@ -105,11 +114,7 @@ nd_status nd_destroy(nd_ctx* ctx) {
   if (!ctx) return ND_OK;
   hipSetDevice(ctx->device);
   hipStreamSynchronize(ctx->stream);
-  for (nd_mat* m : ctx->mats) {
-    hipFree(m->w);
-    hipFree(m->scales);
-    delete m;
-  }
+  for (nd_mat* m : ctx->mats) free_mat_buffers(m);
   for (nd_kv* kv : ctx->kvs) {
     hipFree(kv->k);
     delete kv;
@@ -119,6 +124,7 @@ nd_status nd_destroy(nd_ctx* ctx) {
   if (ctx->attn_counters) hipFree(ctx->attn_counters);
   if (ctx->mm_scratch) hipFree(ctx->mm_scratch);
   if (ctx->mv_split) hipFree(ctx->mv_split);
+  if (ctx->cq_prepared) hipFree(ctx->cq_prepared);
   hipStreamDestroy(ctx->stream);
   delete ctx;
   return ND_OK;
@@ -194,9 +200,90 @@ nd_status nd_mat_free(nd_ctx* ctx, nd_mat* m) {
   if (!m) return ND_OK;
   if (!ctx->mats.erase(m)) return nd_fail(ctx, ND_ERR_INVALID, "matrix does not belong to context");
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
-  hipFree(m->w);
-  hipFree(m->scales);
-  delete m;
+  free_mat_buffers(m);
+  return ND_OK;
+}
+
+// A Cactus-Quant record (model/cact.ts:346-396): shape [n][k], group g (a
+// power of two), bits 2, 3, 4 or 5 (ternary, packed as 2-bit crumbs), rows
+// of kpad = ceil(k / g) * g codes.  The kernels work in units of 32 codes:
+// rows are stored kstore = kpad rounded up to 32 codes wide, the extra
+// codes zero and their groups' norms zero (the rotated input is zero there
+// too, so they add nothing); they also need g >= 8 and kstore <= 8192.
+nd_status nd_mat_upload_cq(nd_ctx* ctx, const uint8_t* packed, const uint16_t* norms,
+                           const float* codebook, uint32_t n, uint32_t k, uint32_t g,
+                           uint32_t bits, nd_mat** out) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!out || !packed || !norms || (bits != 5 && !codebook))
+    return nd_fail(ctx, ND_ERR_INVALID, "nd_mat_upload_cq: NULL argument");
+  *out = nullptr;
+  if (n == 0 || k == 0) return nd_fail(ctx, ND_ERR_INVALID, "CQ matrix %ux%u is empty", n, k);
+  if (g == 0 || (g & (g - 1)) != 0)
+    return nd_fail(ctx, ND_ERR_UNSUPPORTED, "CQ matrix has non-power-of-two group %u", g);
+  if (bits < 2 || bits > 5)
+    return nd_fail(ctx, ND_ERR_UNSUPPORTED, "CQ matrix uses unsupported record width %u", bits);
+  const uint64_t kpad = ((uint64_t)k + g - 1) / g * g, kstore = (kpad + 31) / 32 * 32;
+  const uint32_t pb = bits == 5 ? 2 : bits;
+  if ((kpad * pb) % 8 != 0)
+    return nd_fail(ctx, ND_ERR_INVALID, "CQ matrix has a fractional packed row size");
+  if (g < 8 || kstore > kCqMaxKpad)
+    return nd_fail(ctx, ND_ERR_UNSUPPORTED,
+                   "CQ matrix k=%u with group %u: this backend needs group >= 8 and at most %u "
+                   "padded columns", k, g, kCqMaxKpad);
+  ND_HIP(ctx, hipSetDevice(ctx->device));
+  if (!ctx->cq_prepared)
+    ND_HIP(ctx, hipMalloc(&ctx->cq_prepared, (size_t)kCqPreparedRows * kCqMaxKpad * sizeof(float)));
+  nd_mat* m = new nd_mat();
+  m->n = n;
+  m->k = k;
+  m->g = g;
+  m->bits = bits;
+  m->kpad = (uint32_t)kstore;
+  m->row_bytes = (uint32_t)(kstore * pb / 8);
+  if (bits == 5) {
+    // cqMatvecPrepared's crumb table [0, c, 0, -c], c = 1.2240064 / sqrt(g)
+    // (backends/cq.ts:182-184), rounded to fp32 once.
+    const float c = (float)(1.2240064 / std::sqrt((double)g));
+    m->cb[1] = c;
+    m->cb[3] = -c;
+  } else {
+    for (uint32_t i = 0; i < (1u << bits); ++i) m->cb[i] = codebook[i];
+  }
+  const size_t pbytes = (size_t)n * m->row_bytes, nbytes = (size_t)n * (kstore / g) * 2;
+  const void* psrc = packed;
+  const void* nsrc = norms;
+  std::vector<uint8_t> ppad;
+  std::vector<uint16_t> npad;
+  if (kstore != kpad) {  // widen each row to kstore codes: zero codes, zero norms
+    const size_t src_row = kpad * pb / 8, src_groups = kpad / g, groups = kstore / g;
+    ppad.assign(pbytes, 0);
+    npad.assign((size_t)n * groups, 0);
+    for (size_t r = 0; r < n; ++r) {
+      std::memcpy(&ppad[r * m->row_bytes], packed + r * src_row, src_row);
+      std::memcpy(&npad[r * groups], norms + r * src_groups, src_groups * 2);
+    }
+    psrc = ppad.data();
+    nsrc = npad.data();
+  }
+  hipError_t e = hipMalloc(&m->packed, pbytes);
+  if (e == hipSuccess) e = hipMalloc(&m->norms, nbytes);
+  if (e == hipSuccess) e = hipMemcpyAsync(m->packed, psrc, pbytes, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(m->norms, nsrc, nbytes, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    free_mat_buffers(m);
+    return nd_hip_fail(ctx, e, "CQ matrix upload");
+  }
+  ctx->mats.insert(m);
+  *out = m;
+  return ND_OK;
+}
+
+nd_status nd_mat_cq_info(const nd_mat* m, uint32_t* bits, uint32_t* kpad, uint32_t* row_bytes) {
+  if (!m) return ND_ERR_INVALID;
+  if (bits) *bits = m->bits;
+  if (kpad) *kpad = m->kpad;
+  if (row_bytes) *row_bytes = m->row_bytes;
   return ND_OK;
 }
 
@@ -213,6 +300,16 @@ nd_status nd_mat_info(const nd_mat* m, const int8_t** w_dev, const float** scale
 
 // --------------------------------------------------------------- matvec
 
+// Either matrix form: int8 codes with scales, or Cactus-Quant.  y rows are
+// y_stride floats apart.
+static hipError_t launch_matvec_any(nd_ctx* ctx, const nd_mat* m, const float* x, uint32_t batch,
+                                    uint32_t row_start, uint32_t row_count, float* y,
+                                    uint32_t y_stride, hipStream_t s, void* split) {
+  if (!m->bits) return nd_launch_matvec(m, x, batch, m->k, row_start, row_count, y, y_stride, s, split);
+  return nd_launch_cq_matvec(m, x, batch, m->k, ctx->cq_prepared, row_start, row_count, y,
+                             y_stride, s);
+}
+
 static nd_status check_range(nd_ctx* ctx, const nd_mat* m, uint32_t row_start, uint32_t row_count) {
   if (!m) return nd_fail(ctx, ND_ERR_INVALID, "matrix is NULL");
   if ((uint64_t)row_start + row_count > m->n)
@@ -228,8 +325,8 @@ nd_status nd_matvec_d(nd_ctx* ctx, const nd_mat* m, const float* x, uint32_t bat
   if (st != ND_OK) return st;
   if ((batch && (!x || !y)) || (reinterpret_cast<uintptr_t>(x) & 15))
     return nd_fail(ctx, ND_ERR_INVALID, "x must be a 16-byte aligned device pointer");
-  ND_HIP(ctx, nd_launch_matvec(m, x, batch, m->k, row_start, row_count, y, row_count,
-                               nd_pick_stream(ctx, stream), ctx->mv_split));
+  ND_HIP(ctx, launch_matvec_any(ctx, m, x, batch, row_start, row_count, y, row_count,
+                                nd_pick_stream(ctx, stream), ctx->mv_split));
   return ND_OK;
 }
 
@@ -247,8 +344,8 @@ nd_status nd_matvec(nd_ctx* ctx, const nd_mat* m, const float* x, uint32_t batch
   float* dx = reinterpret_cast<float*>(ctx->stage);
   float* dy = reinterpret_cast<float*>(reinterpret_cast<char*>(ctx->stage) + align256(xb));
   ND_HIP(ctx, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
-  ND_HIP(ctx, nd_launch_matvec(m, dx, batch, m->k, row_start, row_count, dy, row_count, ctx->stream,
-                               ctx->mv_split));
+  ND_HIP(ctx, launch_matvec_any(ctx, m, dx, batch, row_start, row_count, dy, row_count,
+                                ctx->stream, ctx->mv_split));
   ND_HIP(ctx, hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, ctx->stream));
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return ND_OK;
@@ -287,8 +384,8 @@ nd_status nd_matvec_batch(nd_ctx* ctx, const nd_matvec_job* jobs, uint32_t count
     }
     dys[i] = reinterpret_cast<float*>(base + off);
     off += align256((size_t)jobs[i].row_count * 4);
-    ND_HIP(ctx, nd_launch_matvec(m, dx, 1, m->k, jobs[i].row_start, jobs[i].row_count, dys[i],
-                                 jobs[i].row_count, ctx->stream));
+    ND_HIP(ctx, launch_matvec_any(ctx, m, dx, 1, jobs[i].row_start, jobs[i].row_count, dys[i],
+                                  jobs[i].row_count, ctx->stream, nullptr));
   }
   for (uint32_t i = 0; i < count; ++i)
     if (jobs[i].row_count)
@@ -302,7 +399,8 @@ nd_status nd_row_d(nd_ctx* ctx, const nd_mat* m, uint32_t row, float* out, void*
   if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
   if (!m || row >= m->n) return nd_fail(ctx, ND_ERR_INVALID, "Matrix row %u is out of range", row);
   if (!out) return nd_fail(ctx, ND_ERR_INVALID, "output is NULL");
-  ND_HIP(ctx, nd_launch_row(m, row, out, nd_pick_stream(ctx, stream)));
+  hipStream_t s = nd_pick_stream(ctx, stream);
+  ND_HIP(ctx, m->bits ? nd_launch_cq_row(m, row, out, s) : nd_launch_row(m, row, out, s));
   return ND_OK;
 }
 
@@ -313,7 +411,7 @@ nd_status nd_row(nd_ctx* ctx, const nd_mat* m, uint32_t row, float* out) {
   nd_status st = ensure_stage(ctx, (size_t)m->k * 4);
   if (st != ND_OK) return st;
   float* d = reinterpret_cast<float*>(ctx->stage);
-  ND_HIP(ctx, nd_launch_row(m, row, d, ctx->stream));
+  ND_HIP(ctx, m->bits ? nd_launch_cq_row(m, row, d, ctx->stream) : nd_launch_row(m, row, d, ctx->stream));
   ND_HIP(ctx, hipMemcpyAsync(out, d, (size_t)m->k * 4, hipMemcpyDeviceToHost, ctx->stream));
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return ND_OK;
@@ -323,6 +421,7 @@ nd_status nd_row(nd_ctx* ctx, const nd_mat* m, uint32_t row, float* out) {
 
 static nd_status check_matmul(nd_ctx* ctx, const nd_mat* m) {
   if (!m) return nd_fail(ctx, ND_ERR_INVALID, "matrix is NULL");
+  if (m->bits) return nd_fail(ctx, ND_ERR_INVALID, "nd_matmul needs an int8 matrix");
   if (m->g != m->k || m->k % 64 != 0 || m->k > 2048)
     return nd_fail(ctx, ND_ERR_INVALID,
                    "nd_matmul needs per-row scales (g == k), k %% 64 == 0 and k <= 2048 "

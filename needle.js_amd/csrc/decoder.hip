@@ -212,7 +212,7 @@ static inline size_t a256(size_t n) { return (n + 255) & ~size_t(255); }
 static nd_status check_weight(nd_ctx* ctx, const nd_mat* m, uint32_t n, uint32_t k,
                               const char* what) {
   if (!m) return nd_fail(ctx, ND_ERR_INVALID, "%s is NULL", what);
-  if (m->n != n || m->k != k || m->g != k)
+  if (m->bits || m->n != n || m->k != k || m->g != k)
     return nd_fail(ctx, ND_ERR_INVALID, "%s is %ux%u (group %u); expected %ux%u per-row scaled",
                    what, m->n, m->k, m->g, n, k);
   return ND_OK;

@@ -14,7 +14,18 @@ struct nd_mat {
   int8_t* w = nullptr;      // [n][k] int8 codes, row-major
   float* scales = nullptr;  // [n][k / g]
   uint32_t n = 0, k = 0, g = 0;
+  // Cactus-Quant form (bits != 0; w and scales unused): packed codes
+  // [n][row_bytes], binary16 norms [n][kpad / g] and this width's codebook
+  // by code (ternary: 0, +c, 0, -c).
+  uint32_t bits = 0, kpad = 0, row_bytes = 0;
+  uint8_t* packed = nullptr;
+  uint16_t* norms = nullptr;
+  float cb[16] = {};
 };
+// Prepared (rotated) input rows of a Cactus-Quant matvec: the context holds
+// kCqPreparedRows rows of up to kCqMaxKpad floats, reused in stream order.
+constexpr uint32_t kCqPreparedRows = 8;
+constexpr uint32_t kCqMaxKpad = 8192;
 
 struct nd_kv {
   uint32_t layers = 0, kv_heads = 0, head_dim = 0, max_length = 0;
@@ -40,6 +51,7 @@ struct nd_ctx {
   uint32_t* attn_counters = nullptr;
   // Split inputs of the batched MFMA matvec (kMatvecSplitBytes).
   void* mv_split = nullptr;
+  float* cq_prepared = nullptr;  // [kCqPreparedRows][kCqMaxKpad], on the first CQ upload
   // Digit planes and row factors of nd_matmul_d (grown on demand).
   void* mm_scratch = nullptr;
   size_t mm_scratch_bytes = 0;
@@ -70,6 +82,16 @@ hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uin
                             uint32_t row_start, uint32_t row_count, float* y, uint32_t y_stride,
                             hipStream_t s, void* split = nullptr);
 hipError_t nd_launch_row(const nd_mat* m, uint32_t row, float* out, hipStream_t s);
+// Cactus-Quant matrices (csrc/cq.hip): prepareCqActivation of batch rows of
+// x into prepared [batch][kpad]; the matvec of batch rows of x (its own
+// input rotation; `prepared` is the context's kCqPreparedRows x kCqMaxKpad
+// buffer, used for groups wider than 2048); one dequantized row.
+hipError_t nd_launch_cq_prepare(const nd_mat* m, const float* x, uint32_t batch, uint32_t x_stride,
+                                float* prepared, hipStream_t s);
+hipError_t nd_launch_cq_matvec(const nd_mat* m, const float* x, uint32_t batch, uint32_t x_stride,
+                               float* prepared, uint32_t row_start, uint32_t row_count, float* y,
+                               uint32_t y_stride, hipStream_t s);
+hipError_t nd_launch_cq_row(const nd_mat* m, uint32_t row, float* out, hipStream_t s);
 
 // Visible-position arithmetic of the attention window (runtime.ts:723-728).
 struct nd_visible {

@@ -1309,7 +1309,7 @@ nd_status nd_needle_create(nd_ctx* ctx, const nd_needle_desc* d, nd_needle** out
     return nd_fail(ctx, ND_ERR_INVALID,
                    "engram tables x sub must be a power of two in [128, 8192]");
   auto check = [&](const nd_mat* m, uint32_t n, uint32_t k, const char* what) -> nd_status {
-    if (!m || m->n != n || m->k != k || m->g != k)
+    if (!m || m->bits || m->n != n || m->k != k || m->g != k)
       return nd_fail(ctx, ND_ERR_INVALID, "%s must be a per-row-scaled %ux%u int8 matrix", what,
                      n, k);
     return ND_OK;

@@ -7,12 +7,15 @@ raises NeedleError("BACKEND_UNAVAILABLE").
 """
 
 from .backend import HipBackend, Int8Matrix, MatrixRowRange, MatvecRequest
+from .cact import CactArchive, CqMatrix, pack_codes, parse_cact, write_cact
 from .errors import NeedleError, invariant
 from .kv import HipKvCache
 from .needle2 import Needle2Geometry, Needle2Weights
 from .runtime import GenerationResult, HipNeedleSession, NeedleModel, NeedleRuntime
 
 __all__ = [
+    "CactArchive",
+    "CqMatrix",
     "GenerationResult",
     "HipBackend",
     "HipNeedleSession",
@@ -26,4 +29,7 @@ __all__ = [
     "MatvecRequest",
     "NeedleError",
     "invariant",
+    "pack_codes",
+    "parse_cact",
+    "write_cact",
 ]

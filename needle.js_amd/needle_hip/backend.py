@@ -1,10 +1,13 @@
 """HipBackend: the InferenceBackend contract of needle.js over libneedle_hip.
 
 Mirrors backends/backend.ts:82-110 (kind, name, weights, matvec, matvecBatch,
-createResidentSession, row, dispose) with Python naming.  Matrices are the
-int8 form of CqMatrix (model/cact.ts:61-75): codes [n][k] int8 and one fp32
-scale per (row, group of g columns).  Each matrix is uploaded to HBM once, on
-first use, and cached by identity as backends/typegpu.ts:390-410 does.
+createResidentSession, row, dispose) with Python naming.  Matrices are either
+the archive's own Cactus-Quant form (cact.CqMatrix, model/cact.ts:61-75:
+packed 2/3/4-bit or ternary codes, binary16 group norms, a shared codebook)
+or its int8 form (codes [n][k] int8 and one fp32 scale per (row, group of g
+columns)), the form of the resident Needle 2 and batched decoders.  Each
+matrix is uploaded to HBM once, on first use, and cached by identity as
+backends/typegpu.ts:390-410 does.
 Results are fresh float32 arrays (backends/cpu.ts:12-16).
 """
 
@@ -98,10 +101,17 @@ class HipBackend:
         if entry is not None and entry[0] is matrix:
             return entry[1]
         handle = C.c_void_p()
-        n, k = matrix.codes.shape
-        self._check(self.lib.nd_mat_upload_i8(self.ctx, L.ptr(matrix.codes), L.ptr(matrix.scales),
-                                              n, k, matrix.group_size, C.byref(handle)),
-                    "nd_mat_upload_i8")
+        if getattr(matrix, "kind", None) == "cq":
+            cb = matrix.codebook
+            self._check(self.lib.nd_mat_upload_cq(
+                self.ctx, L.ptr(matrix.packed), L.ptr(matrix.norms),
+                None if cb is None else L.ptr(cb), matrix.output_size, matrix.input_size,
+                matrix.group_size, matrix.bits, C.byref(handle)), "nd_mat_upload_cq")
+        else:
+            n, k = matrix.codes.shape
+            self._check(self.lib.nd_mat_upload_i8(self.ctx, L.ptr(matrix.codes),
+                                                  L.ptr(matrix.scales), n, k, matrix.group_size,
+                                                  C.byref(handle)), "nd_mat_upload_i8")
         self._mats[id(matrix)] = (matrix, handle)
         return handle
 

@@ -18,6 +18,7 @@ ND_ERR_INVALID = 1
 ND_ERR_BACKEND = 2
 ND_ERR_OVERFLOW = 3
 ND_ERR_NOMEM = 4
+ND_ERR_UNSUPPORTED = 5
 ND_KV_INT8 = 0
 ND_KV_FLOAT32 = 1
 
@@ -26,6 +27,7 @@ _STATUS_CODE = {
     ND_ERR_OVERFLOW: "CONTEXT_OVERFLOW",
     ND_ERR_BACKEND: "BACKEND_UNAVAILABLE",
     ND_ERR_NOMEM: "BACKEND_UNAVAILABLE",
+    ND_ERR_UNSUPPORTED: "UNSUPPORTED_CACT",
 }
 
 PACKAGE_ROOT = Path(__file__).resolve().parent.parent
@@ -59,6 +61,8 @@ SIGNATURES = {
     "nd_mat_upload_i8": (I32, [P, P, P, U32, U32, U32, PP]),
     "nd_mat_upload_i8_d": (I32, [P, P, P, U32, U32, U32, PP]),
     "nd_mat_free": (I32, [P, P]),
+    "nd_mat_upload_cq": (I32, [P, P, P, P, U32, U32, U32, U32, PP]),
+    "nd_mat_cq_info": (I32, [P, PU32, PU32, PU32]),
     "nd_mat_info": (I32, [P, PP, PP, PU32, PU32, PU32]),
     "nd_matvec": (I32, [P, P, P, U32, U32, U32, P]),
     "nd_matvec_d": (I32, [P, P, P, U32, U32, U32, P, P]),

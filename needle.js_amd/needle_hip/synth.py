@@ -128,3 +128,31 @@ def int8_matrix(run_seed: int, name: str, n: int, k: int, g: int,
     w = s.int8((n, k))
     scales = s.uniform((n, k // g), scale_lo, scale_hi)
     return w, scales
+
+
+def cq_codebook() -> np.ndarray:
+    """A 28-entry archive codebook: CQ2 [0, 4), CQ3 [4, 12), CQ4 [12, 28),
+    each width's levels symmetric about zero (the shape of Lloyd-Max levels
+    for a rotated, unit-variance weight distribution)."""
+    cq2 = np.array([-1.51, -0.4528, 0.4528, 1.51])
+    cq3 = np.array([-2.152, -1.344, -0.756, -0.245, 0.245, 0.756, 1.344, 2.152])
+    cq4 = np.linspace(-2.7326, 2.7326, 16)
+    return np.concatenate([cq2, cq3, cq4]).astype(np.float32)
+
+
+def cq_matrix(run_seed: int, name: str, n: int, k: int, g: int, bits: int,
+              norm_lo: float = 0.01, norm_hi: float = 0.05):
+    """Packed Cactus-Quant matrix (packed uint8 [n][row_bytes], binary16
+    norms uint16 [n][kpad/g]) with uniform codes; the ternary width (5) draws
+    crumbs 0, 1 and 3 (zero, +c, -c) and a few reserved 2s (zero)."""
+    from .cact import pack_codes
+
+    s = Stream(run_seed, name)
+    kpad = -(-k // g) * g
+    if bits == 5:
+        codes = np.array([0, 1, 3, 0, 1, 3, 0, 1, 3, 2])[s.integers(n * kpad, 0, 9)]
+    else:
+        codes = s.integers(n * kpad, 0, (1 << bits) - 1)
+    packed = pack_codes(codes.reshape(n, kpad), bits)
+    norms = s.uniform((n, kpad // g), norm_lo, norm_hi).astype(np.float16).view(np.uint16)
+    return packed, norms

@@ -39,6 +39,10 @@ _SIG = {
     "or_select_mask": (C.c_int, [P, U32, P, C.POINTER(U32), C.POINTER(D)]),
     "or_matvec_i8": (C.c_int, [P, P, U32, U32, U32, P, U32, U32, U32, P]),
     "or_row_i8": (C.c_int, [P, P, U32, U32, U32, U32, P]),
+    "or_f16_to_f32": (C.c_float, [C.c_uint16]),
+    "or_cq_prepare": (C.c_int, [P, U32, U32, P]),
+    "or_cq_matvec": (C.c_int, [P, P, P, U32, U32, U32, U32, P, U32, U32, U32, P]),
+    "or_cq_row": (C.c_int, [P, P, P, U32, U32, U32, U32, U32, P]),
     "or_kv_quantize": (None, [P, U32, P, P]),
     "or_kv_create": (P, [U32, U32, U32, U32, U32, U32, C.c_int]),
     "or_kv_destroy": (None, [P]),
@@ -186,6 +190,49 @@ def matvec_i8(w, scales, g: int, x, row_start: int = 0, row_count=None):
     y = np.empty((batch, rc), dtype=np.float32)
     _ok(lib().or_matvec_i8(_p(w), _p(scales), n, k, g, _p(x), batch, row_start, rc, _p(y)))
     return y[0] if x.ndim == 1 else y
+
+
+def f16_to_f32(bits: int) -> float:
+    """float16ToNumber (fp16.ts:5-32) of one binary16 bit pattern."""
+    return float(lib().or_f16_to_f32(int(bits) & 0xFFFF))
+
+
+def cq_prepare(x, g: int):
+    """prepareCqActivation (cq.ts:30-46): padded, per-group FWHT / sqrt(g)."""
+    x = _f32(x).reshape(-1)
+    kpad = (x.size + g - 1) // g * g
+    out = np.empty(kpad, dtype=np.float32)
+    _ok(lib().or_cq_prepare(_p(x), x.size, g, _p(out)))
+    return out
+
+
+def _cq_args(packed, norms, codebook):
+    return (np.ascontiguousarray(packed, dtype=np.uint8),
+            np.ascontiguousarray(norms, dtype=np.uint16), _f32(codebook))
+
+
+def cq_matvec(packed, norms, codebook, k: int, g: int, bits: int, x, row_start: int = 0,
+              row_count=None):
+    """cqMatvec (cq.ts:107-240) over a packed CQ matrix [n][row_bytes] with
+    binary16 norms [n][groups] and the archive's 28-float codebook."""
+    packed, norms, codebook = _cq_args(packed, norms, codebook)
+    x = _f32(x)
+    n = packed.shape[0]
+    batch = 1 if x.ndim == 1 else x.shape[0]
+    rc = n - row_start if row_count is None else row_count
+    y = np.empty((batch, rc), dtype=np.float32)
+    _ok(lib().or_cq_matvec(_p(packed), _p(norms), _p(codebook), n, k, g, bits, _p(x), batch,
+                           row_start, rc, _p(y)))
+    return y[0] if x.ndim == 1 else y
+
+
+def cq_row(packed, norms, codebook, k: int, g: int, bits: int, row: int):
+    """dequantizeCqRow (cq.ts:243-295)."""
+    packed, norms, codebook = _cq_args(packed, norms, codebook)
+    out = np.empty(k, dtype=np.float32)
+    _ok(lib().or_cq_row(_p(packed), _p(norms), _p(codebook), packed.shape[0], k, g, bits, row,
+                        _p(out)))
+    return out
 
 
 def row_i8(w, scales, g: int, row: int):

@@ -27,6 +27,17 @@
  *                       special cases, scipy logsumexp for log-probability.
  *   or_fwht             Sylvester Hadamard matrix (scipy.linalg.hadamard)
  *                       and self-inverse (tests/cq.test.ts:64-72).
+ *   or_f16_to_f32       the binary16 patterns of tests/fp16.test.ts:4-20 and
+ *                       numpy's float16 decoding of all 65536 patterns.
+ *   or_cq_prepare       explicit Sylvester-matrix products per group.
+ *   or_cq_matvec        the fixtures of tests/cq.test.ts:20-61 (direct ==
+ *                       dequantized row dot, batch == single with a range),
+ *                       codes unpacked independently (numpy bit operations)
+ *                       times explicit Hadamard products, closed form for a
+ *                       constant code (sqrt(g) * x_0 per group).
+ *   or_cq_row           dequantized rows against explicit H (codebook .*
+ *                       norm) / sqrt(g); matvec == row . x (the reference
+ *                       test's identity).
  *   or_rms_norm, or_rope, or_sigmoid, or_softmax, or_sinkhorn,
  *   or_hadamard_mlp     closed forms in numpy float64 (unit RMS, rotation
  *                       preserves norms and matches complex multiply,
@@ -322,6 +333,167 @@ int or_row_i8(const int8_t* w, const float* scales, uint32_t n, uint32_t k, uint
   uint32_t groups = k / g;
   for (uint32_t c = 0; c < k; c++)
     out[c] = (float)((double)w[(size_t)row * k + c] * (double)scales[(size_t)row * groups + c / g]);
+  return OR_OK;
+}
+
+/* ------------------------------------- a1 (CQ): Cactus-Quant matrices */
+
+/* fp16.ts:5-32 float16ToNumber: binary16 bit pattern -> binary32 (exact). */
+float or_f16_to_f32(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  int32_t exponent = (h >> 10) & 0x1f;
+  uint32_t mantissa = h & 0x3ffu, bits;
+  if (exponent == 0) {
+    if (mantissa == 0) {
+      bits = sign;
+    } else {
+      exponent = 127 - 15 + 1;
+      while ((mantissa & 0x400u) == 0) {
+        mantissa <<= 1;
+        exponent--;
+      }
+      mantissa &= 0x3ffu;
+      bits = sign | ((uint32_t)exponent << 23) | (mantissa << 13);
+    }
+  } else if (exponent == 0x1f) {
+    bits = sign | 0x7f800000u | (mantissa << 13);
+  } else {
+    bits = sign | ((uint32_t)(exponent - 15 + 127) << 23) | (mantissa << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+#define OR_TERNARY_BITS 5
+static const double kTernaryCentroid = 1.2240064; /* cq.ts:6 */
+
+/* cact.ts:362-378: inputs padded to whole groups; ternary records pack 2-bit
+ * crumbs; row byte length = padded inputs * packed bits / 8. */
+static int cq_geometry(uint32_t k, uint32_t g, uint32_t bits, uint32_t* kpad, uint32_t* row_bytes) {
+  if (g == 0 || (g & (g - 1)) != 0) return OR_INVALID;
+  if (bits != 2 && bits != 3 && bits != 4 && bits != OR_TERNARY_BITS) return OR_INVALID;
+  uint32_t pb = bits == OR_TERNARY_BITS ? 2 : bits;
+  *kpad = (k + g - 1) / g * g;
+  if (((uint64_t)*kpad * pb) % 8 != 0) return OR_INVALID;
+  *row_bytes = (uint32_t)((uint64_t)*kpad * pb / 8);
+  return OR_OK;
+}
+
+/* Code (crumb, nibble or 3-bit field) of column c of a packed row: crumbs and
+ * nibbles low bits first (cq.ts:143, 169, 194), 3-bit rows one little-endian
+ * bitstream read through a 16-bit window (cq.ts:219-224). */
+static uint32_t cq_code(const uint8_t* row, uint32_t c, uint32_t bits) {
+  if (bits == 2 || bits == OR_TERNARY_BITS) return (row[c >> 2] >> ((c & 3) * 2)) & 3u;
+  if (bits == 4) return (row[c >> 1] >> ((c & 1) * 4)) & 15u;
+  uint32_t bit = c * 3, at = bit >> 3, shift = bit & 7;
+  uint32_t word = (uint32_t)row[at] | ((shift + 3 > 8) ? ((uint32_t)row[at + 1] << 8) : 0u);
+  return (word >> shift) & 7u;
+}
+
+/* cq.ts:30-46 prepareCqActivation: x zero-padded to kpad, fastWalshHadamard
+ * on each group (f32 store after every butterfly), then each value times
+ * 1/sqrt(g) in float64 with an f32 store.  out holds kpad values. */
+int or_cq_prepare(const float* x, uint32_t k, uint32_t g, float* out) {
+  if (g == 0 || (g & (g - 1)) != 0) return OR_INVALID;
+  uint32_t kpad = (k + g - 1) / g * g;
+  for (uint32_t i = 0; i < kpad; i++) out[i] = i < k ? x[i] : 0.0f;
+  const double inverse_root = 1.0 / sqrt((double)g);
+  for (uint32_t off = 0; off < kpad; off += g) {
+    or_fwht(out, off, g);
+    for (uint32_t i = 0; i < g; i++) out[off + i] = (float)((double)out[off + i] * inverse_root);
+  }
+  return OR_OK;
+}
+
+/* cq.ts:107-231 cqMatvecPrepared on or_cq_prepare(x), batch rows of x [B][k]
+ * into y [B][row_count].  codebook is the archive's 28 floats: CQ2 [0, 4),
+ * CQ3 [4, 12), CQ4 [12, 28) (cact.ts:272-276); norms are binary16 bit
+ * patterns [n][kpad / g].  Per row: float64 `dot` per group in the
+ * reference's summation order, `total += norm * dot`, f32 store. */
+int or_cq_matvec(const uint8_t* packed, const uint16_t* norms, const float* codebook, uint32_t n,
+                 uint32_t k, uint32_t g, uint32_t bits, const float* x, uint32_t batch,
+                 uint32_t row_start, uint32_t row_count, float* y) {
+  uint32_t kpad, row_bytes;
+  if (cq_geometry(k, g, bits, &kpad, &row_bytes) != OR_OK) return OR_INVALID;
+  if ((uint64_t)row_start + row_count > n) return OR_INVALID;
+  const uint32_t groups = kpad / g;
+  const double coefficient = kTernaryCentroid / sqrt((double)g);
+  const double crumbs[4] = {0.0, coefficient, 0.0, -coefficient};
+  const float* cb = bits == 2 ? codebook : bits == 3 ? codebook + 4 : codebook + 12;
+  float* prepared = (float*)malloc(sizeof(float) * kpad);
+  if (!prepared) return OR_INVALID;
+  for (uint32_t b = 0; b < batch; b++) {
+    or_cq_prepare(x + (size_t)b * k, k, g, prepared);
+    for (uint32_t lr = 0; lr < row_count; lr++) {
+      const uint32_t r = row_start + lr;
+      const uint8_t* row = packed + (size_t)r * row_bytes;
+      double total = 0;
+      for (uint32_t grp = 0; grp < groups; grp++) {
+        const float* p = prepared + (size_t)grp * g;
+        const uint32_t c0 = grp * g;
+        double dot = 0;
+        if (bits == 2 || bits == OR_TERNARY_BITS) {
+          for (uint32_t c = 0; c < g; c += 4) {
+            double v[4];
+            for (int j = 0; j < 4; j++) {
+              uint32_t code = cq_code(row, c0 + c + j, bits);
+              v[j] = bits == 2 ? (double)cb[code] : crumbs[code];
+            }
+            dot += ((v[0] * (double)p[c] + v[1] * (double)p[c + 1]) + v[2] * (double)p[c + 2]) +
+                   v[3] * (double)p[c + 3];
+          }
+        } else if (bits == 4) {
+          for (uint32_t c = 0; c < g; c += 2)
+            dot += (double)cb[cq_code(row, c0 + c, 4)] * (double)p[c] +
+                   (double)cb[cq_code(row, c0 + c + 1, 4)] * (double)p[c + 1];
+        } else {
+          for (uint32_t c = 0; c < g; c++) dot += (double)cb[cq_code(row, c0 + c, 3)] * (double)p[c];
+        }
+        total += (double)or_f16_to_f32(norms[(size_t)r * groups + grp]) * dot;
+      }
+      y[(size_t)b * row_count + lr] = (float)total;
+    }
+  }
+  free(prepared);
+  return OR_OK;
+}
+
+/* cq.ts:243-295 dequantizeCqRow: per group, f32(codebook[index] * norm) (the
+ * ternary codebook is Float32Array([-c, 0, c]) with c = 1.2240064/sqrt(g),
+ * crumb 3 -> index 0, crumb i -> i + 1, index 3 reads as 0), the FWHT, then
+ * f32(value * 1/sqrt(g)); the first k columns are written. */
+int or_cq_row(const uint8_t* packed, const uint16_t* norms, const float* codebook, uint32_t n,
+              uint32_t k, uint32_t g, uint32_t bits, uint32_t row, float* out) {
+  uint32_t kpad, row_bytes;
+  if (cq_geometry(k, g, bits, &kpad, &row_bytes) != OR_OK || row >= n) return OR_INVALID;
+  const uint32_t groups = kpad / g;
+  const double inverse_root = 1.0 / sqrt((double)g);
+  const float ternary[3] = {(float)(-kTernaryCentroid * inverse_root), 0.0f,
+                            (float)(kTernaryCentroid * inverse_root)};
+  const float* cb = bits == 2 ? codebook : bits == 3 ? codebook + 4 : codebook + 12;
+  const uint8_t* prow = packed + (size_t)row * row_bytes;
+  float* temporary = (float*)malloc(sizeof(float) * g);
+  if (!temporary) return OR_INVALID;
+  for (uint32_t grp = 0; grp < groups; grp++) {
+    const double norm = (double)or_f16_to_f32(norms[(size_t)row * groups + grp]);
+    for (uint32_t c = 0; c < g; c++) {
+      const uint32_t code = cq_code(prow, grp * g + c, bits);
+      double value;
+      if (bits == OR_TERNARY_BITS) {
+        const uint32_t index = code == 3 ? 0 : code + 1;
+        value = index < 3 ? (double)ternary[index] : 0.0;
+      } else {
+        value = (double)cb[code];
+      }
+      temporary[c] = (float)(value * norm);
+    }
+    or_fwht(temporary, 0, g);
+    const uint32_t count = g < k - grp * g ? g : k - grp * g;
+    for (uint32_t c = 0; c < count; c++)
+      out[grp * g + c] = (float)((double)temporary[c] * inverse_root);
+  }
+  free(temporary);
   return OR_OK;
 }
 
