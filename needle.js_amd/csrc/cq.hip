@@ -105,6 +105,21 @@ __global__ __launch_bounds__(kCqThreads) void cq_row_kernel(
     out[c] = (float)((double)v[c] * inverse_root);
 }
 
+// cb.v[i] for i < N by a select tree over the bits of i (constant indices
+// only).
+template <int N>
+__device__ __forceinline__ float pick_code(const Codebook& cb, uint32_t i) {
+  float v[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) v[j] = cb.v[j];
+#pragma unroll
+  for (int half = N / 2, bit = 0; half >= 1; half /= 2, ++bit) {
+#pragma unroll
+    for (int j = 0; j < half; ++j) v[j] = (i >> bit) & 1u ? v[2 * j + 1] : v[2 * j];
+  }
+  return v[0];
+}
+
 // Rotated inputs of unit u (32 consecutive columns) in registers: the
 // butterflies of fastWalshHadamard with strides 1 .. GS / 2 inside the unit
 // (GS = min(g, 32)), then strides 32, 64, ... as exchanges with the lanes
@@ -155,6 +170,10 @@ __device__ __forceinline__ void rotate_unit(float (&v)[32], uint32_t lanes_per_g
 // their latency; codes index an LDS copy of the codebook; fp32 dots per
 // group times the group norm; row sums through LDS and a DPP butterfly,
 // times out_scale (1/sqrt(g) for ROTATE, else 1).
+// Codes per table lookup for UB-byte units: entries of kE floats indexed by
+// kE packed codes.
+constexpr int lookup_codes(int ub) { return ub == 8 ? 4 : 2; }
+
 template <int UB, int NG, int RACC, bool ROTATE, bool VEC>
 __global__ __launch_bounds__(kCqThreads) void cq_matvec_kernel(
     const uint8_t* __restrict__ packed, const uint16_t* __restrict__ norms, Codebook cb,
@@ -162,10 +181,17 @@ __global__ __launch_bounds__(kCqThreads) void cq_matvec_kernel(
     uint32_t k, uint32_t kpad, uint32_t g_log2, uint32_t row_bytes, uint32_t row_start,
     uint32_t row_count, uint32_t tpr_log2, uint32_t lanes_per_group, float out_scale) {
   constexpr int kGs = 32 / NG;  // weights per group inside a unit
-  __shared__ float lut[16];
+  // Lookup table in LDS: entry i holds the codebook values of the kE codes
+  // packed in index i (kE * bits index bits), one read per kE weights.
+  constexpr int kPB = UB / 4;                  // bits per code
+  constexpr int kE = lookup_codes(UB);         // codes per lookup
+  constexpr int kLB = kPB * kE;                // bits per lookup index
+  constexpr int kEntries = 1 << kLB;
+  constexpr int kLookups = 32 / kE;            // per unit
+  constexpr int kPerGroup = kGs / kE;          // lookups per group
+  __shared__ __align__(16) float tab[kEntries * kE];
   __shared__ float red[RACC * kCqThreads];
   const uint32_t t = threadIdx.x;
-  if (t < 16) lut[t] = cb.v[t];
   const uint32_t tpr = 1u << tpr_log2, rpp = kCqThreads >> tpr_log2;
   const uint32_t sub = t >> tpr_log2, u = t & (tpr - 1);
   const uint32_t units = kpad / 32, groups = kpad >> g_log2;
@@ -174,7 +200,9 @@ __global__ __launch_bounds__(kCqThreads) void cq_matvec_kernel(
   const uint32_t row0 = blockIdx.x * rpp * RACC;
   const float* xb = x + (size_t)blockIdx.y * x_stride;
 
-  // x first (L2-resident, needed first), then the weights.
+  // x first (L2-resident, needed first), then the weights; nothing reads
+  // x until the weight loads are issued, so the wait for x leaves them in
+  // flight.
   float xv[32];
   const uint32_t c0 = u * 32, lim = ROTATE ? k : kpad;
   if constexpr (VEC) {
@@ -182,18 +210,16 @@ __global__ __launch_bounds__(kCqThreads) void cq_matvec_kernel(
     for (int q = 0; q < 8; ++q) {
       const uint32_t c = c0 + 4 * q;
       const float4 f = *reinterpret_cast<const float4*>(xb + (c < lim ? c : lim - 4));
-      const bool ok = c < lim;
-      xv[4 * q] = ok ? f.x : 0.f;
-      xv[4 * q + 1] = ok ? f.y : 0.f;
-      xv[4 * q + 2] = ok ? f.z : 0.f;
-      xv[4 * q + 3] = ok ? f.w : 0.f;
+      xv[4 * q] = f.x;
+      xv[4 * q + 1] = f.y;
+      xv[4 * q + 2] = f.z;
+      xv[4 * q + 3] = f.w;
     }
   } else {
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
       const uint32_t c = c0 + i;
-      const float f = xb[c < lim ? c : lim - 1];
-      xv[i] = c < lim ? f : 0.f;
+      xv[i] = xb[c < lim ? c : lim - 1];
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -219,31 +245,71 @@ __global__ __launch_bounds__(kCqThreads) void cq_matvec_kernel(
     }
   }
   __builtin_amdgcn_sched_barrier(0);
+  // The table, while the loads are in flight.  The codebook is read at
+  // constant indices (scalar loads of the kernel arguments) and each entry
+  // picked with a select tree: no per-lane loads from the argument segment.
+  if (t < (uint32_t)kEntries) {
+#pragma unroll
+    for (int e = 0; e < kE; ++e)
+      tab[t * kE + e] = pick_code<(1 << kPB)>(cb, (t >> (e * kPB)) & ((1u << kPB) - 1));
+  }
+  // Columns past the row (clamped loads above) read as zero.
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const uint32_t c = VEC ? c0 + (i & ~3) : c0 + i;
+    xv[i] = c < lim ? xv[i] : 0.f;
+  }
   if constexpr (ROTATE) rotate_unit<kGs>(xv, lanes_per_group);
-  __syncthreads();  // lut
+  __syncthreads();  // tab
 
+  // Codebook values of row r's 32 codes: kLookups table reads (bits
+  // kLB * i .. of the unit's 32 * kPB-bit stream).  Row r + 1's reads are
+  // issued before row r's products, so LDS latency overlaps the FMAs.
+  auto lookup_row = [&](int r, float (&tv)[32]) {
+#pragma unroll
+    for (int i = 0; i < kLookups; ++i) {
+      const int bit = kLB * i, w = bit >> 5, sh = bit & 31;
+      const uint32_t b = sh + kLB <= 32
+                             ? (raw[r][w] >> sh) & (kEntries - 1u)
+                             : ((raw[r][w] >> sh) | (raw[r][w + 1] << (32 - sh))) & (kEntries - 1u);
+      const char* at = reinterpret_cast<const char*>(tab) + b * (kE * 4);
+      if constexpr (kE == 4) {
+        const float4 f = *reinterpret_cast<const float4*>(at);
+        tv[4 * i] = f.x;
+        tv[4 * i + 1] = f.y;
+        tv[4 * i + 2] = f.z;
+        tv[4 * i + 3] = f.w;
+      } else if constexpr (kE == 2) {
+        const float2 f = *reinterpret_cast<const float2*>(at);
+        tv[2 * i] = f.x;
+        tv[2 * i + 1] = f.y;
+      } else {
+        tv[i] = *reinterpret_cast<const float*>(at);
+      }
+    }
+  };
   float acc[RACC];
+  float tv[2][32];
+  lookup_row(0, tv[0]);
 #pragma unroll
   for (int r = 0; r < RACC; ++r) {
+    if (r + 1 < RACC) lookup_row(r + 1, tv[(r + 1) & 1]);
+    __builtin_amdgcn_sched_barrier(0);
+    const float(&v)[32] = tv[r & 1];
     float total = 0.f;
 #pragma unroll
     for (int s = 0; s < NG; ++s) {
-      float dot = 0.f;
+      float d[kE];
+#pragma unroll
+      for (int e = 0; e < kE; ++e) d[e] = 0.f;
 #pragma unroll
       for (int jj = 0; jj < kGs; ++jj) {
         const int j = s * kGs + jj;
-        uint32_t code;
-        if constexpr (UB == 16) {
-          code = (raw[r][j >> 3] >> (4 * (j & 7))) & 15u;
-        } else if constexpr (UB == 8) {
-          code = (raw[r][j >> 4] >> (2 * (j & 15))) & 3u;
-        } else {  // 3-bit stream: 32 fields in 96 bits
-          const int bit = 3 * j, w = bit >> 5, sh = bit & 31;
-          code = sh <= 29 ? (raw[r][w] >> sh) & 7u
-                          : ((raw[r][w] >> sh) | (raw[r][w + 1] << (32 - sh))) & 7u;
-        }
-        dot = fmaf(lut[code], xv[j], dot);
+        d[jj % kE] = fmaf(v[j], xv[j], d[jj % kE]);
       }
+      float dot = d[0];
+      if constexpr (kE >= 2) dot += d[1];
+      if constexpr (kE == 4) dot += d[2] + d[3];
       const uint32_t h = NG == 1 ? nb[r][0] : (nb[r][s >> 1] >> (16 * (s & 1))) & 0xFFFFu;
       total = fmaf(half_bits_to_float(h), dot, total);
     }
