@@ -411,8 +411,11 @@ def bench_needle2(torch, hip, reps, check, cpu_seconds):
             "bytes_per_token": bytes_tok,
             "decode_GBps": bytes_tok / (decode_ms * 1e-3) / 1e9,
             # begin, engram projections + convolution, per layer mix / QKV /
-            # attention / Wo, the final mix, lm head and selection
-            "launches_per_token": 2 + len(g.sites) + 4 * g.layers + 3}
+            # attention / Wo, the final mix, lm head and selection, and the
+            # confidence pool (the head is on, as the reference's default)
+            "launches_per_token": 2 + len(g.sites) + 4 * g.layers + 3
+                                  + int(model.session.has_confidence),
+            "confidence_pool": model.session.has_confidence}
     part["decode_frac_hbm"] = part["decode_GBps"] / HBM_PEAK_GBS
     ref = oracle.Needle2(weights)
     cpu = None

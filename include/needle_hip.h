@@ -397,6 +397,16 @@ typedef struct nd_needle_desc {
   const float* b_res;              /* [layers][lanes][lanes] */
   const float* eg_taps;            /* [n_sites][engram_taps][dim] */
   const float* final_norm;         /* [dim] */
+  /* Confidence probe head (CactProbeHead, model/cact.ts:105-112), or
+   * probes == NULL for none: probes [probe_count][dim] (1..8), projection
+   * [probe_out][probe_count * dim], bias [probe_out].  With a head, every
+   * step pools the scaled embedding and each layer's lane mean on the
+   * device (OnlineProbePool.add, model/runtime.ts:64-91, fed at
+   * runtime.ts:310 and :550). */
+  const float* probes;
+  uint32_t probe_count, probe_out;
+  const float* probe_projection;
+  const float* probe_bias;
 } nd_needle_desc;
 
 nd_status nd_needle_create(nd_ctx* ctx, const nd_needle_desc* desc, nd_needle** out);
@@ -413,6 +423,13 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* model, uint32_t max_length, ui
 /* The runtime's KV cache (read it with nd_kv_read), or NULL before reset. */
 nd_kv* nd_needle_kv(nd_needle* model);
 uint32_t nd_needle_position(const nd_needle* model);
+
+/* The resident confidence (ResidentExecutionSession.residentConfidence,
+ * backends/backend.ts:77; computed as NeedleRuntime.confidence,
+ * model/runtime.ts:93-104, 641-645): sigmoid of output 0 of the probe head
+ * over everything pooled since the last reset.  INVALID_CACT when the model
+ * has no confidence head or before reset. */
+nd_status nd_needle_confidence(nd_ctx* ctx, nd_needle* model, double* confidence);
 
 /* NeedleRuntime.step (model/runtime.ts:280-583): runs `token` at the current
  * position and advances it; copies the logits [vocab] when logits != NULL.

@@ -85,6 +85,8 @@ struct BeginArgs {
   float* cat;
   const double* inv_freq;  // [32]
   double* rope;            // out: sin then cos of position * inv_freq[j]
+  float* cell0;            // confidence pool cell 0 (the scaled embedding), or null
+  uint32_t cell_ld;        // its row stride in the batched form
 };
 
 // Token intake, engram hashing (runtime.ts:788-818), the scaled embedding
@@ -140,6 +142,7 @@ __global__ __launch_bounds__(kWg) void n2_begin_kernel(BeginArgs a) {
     const float row = (float)a.emb[(size_t)tok * a.d + k] * a.emb_s[tok];
     const float v = (float)((double)row * a.scale);
     for (uint32_t l = 0; l < a.lanes; ++l) a.x[(size_t)l * a.d + k] = v;
+    if (a.cell0) a.cell0[k] = v;
   }
   const uint32_t per_site = a.tables * a.sub;
   for (uint32_t i = t; i < a.n_sites * per_site; i += kWg) {
@@ -327,6 +330,11 @@ struct MixArgs {
   float r_a_post, r_a_res;
   const float* r_b_post;
   const float* r_b_res;
+  // Confidence pool: after post(l - 1), the lane mean (runtime.ts:543-550)
+  // into cell [d] (row stride cell_ld), when not null.  Only workgroup
+  // final_row computes the final norm.
+  float* cell;
+  uint32_t cell_ld, final_row;
 };
 
 // Sum over the kMixWg threads with one barrier: the partial sums alternate
@@ -388,6 +396,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     a.ekey += (size_t)m * a.ek_ld;
     a.evalue += (size_t)m * a.ev_ld;
     if (a.route_out) a.route_out += (size_t)m * 20;
+    if (a.cell) a.cell += (size_t)m * a.cell_ld;
   }
   __shared__ float nl[2048];
   __shared__ float hv[kMixWg];
@@ -482,9 +491,16 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
           xl[l] = nx[l];
           a.x[(size_t)l * D + t] = nx[l];
         }
+      if (a.cell) {
+        double sum = 0.0;
+#pragma unroll
+        for (int l = 0; l < 4; ++l)
+          if ((uint32_t)l < L) sum += xl[l];
+        a.cell[t] = (float)(sum / L);
+      }
     }
   }
-  if (a.has_final) {
+  if (a.has_final && blockIdx.x == a.final_row) {
     float m = 0.f;
     if (col) {
       double sum = 0.0;
@@ -742,6 +758,7 @@ __global__ __launch_bounds__(kWg) void n2_begin_batch_kernel(BeginArgs a, uint32
     const float row = (float)a.emb[(size_t)tok * a.d + k] * a.emb_s[tok];
     const float v = (float)((double)row * a.scale);
     for (uint32_t l = 0; l < a.lanes; ++l) x[(size_t)l * a.d + k] = v;
+    if (a.cell0) a.cell0[(size_t)m * a.cell_ld + k] = v;
   }
   const uint32_t per_site = a.tables * a.sub;
   float* cat = a.cat + (size_t)m * a.n_sites * per_site;
@@ -811,6 +828,216 @@ __global__ __launch_bounds__(64) void n2_rope_store_batch_kernel(
                 ((size_t)layer * kv_heads + h) * alloc, kv_slot(pos, sink, window), alloc);
 }
 
+// Confidence pool state (OnlineProbePool, runtime.ts:48-62) for up to
+// kMaxProbes probes, float64.  The pool launch runs one workgroup per
+// (probe p, 64-column chunk j), and each keeps its own copy of the running
+// maximum and denominator ([p][j]: the copies are equal, every workgroup of
+// a probe computing them from the same scores) so that no workgroup reads
+// what another writes; weighted holds probe p's weighted cell sums.  A
+// denominator of 0 means no cell yet (every pooled cell adds at least
+// exp(0) = 1 through the maximum's own term).
+constexpr uint32_t kMaxProbes = 8;
+constexpr uint32_t kMaxChunks = 8;       // d <= 512
+struct PoolState {
+  double* max;       // [8][8]
+  double* den;       // [8][8]
+  double* weighted;  // [8][d]
+};
+
+// A lane's share of a d-vector (d <= 512): elements lane + 64 k, zero past
+// d, loaded together from clamped addresses.
+__device__ __forceinline__ void lane_share(const float* __restrict__ v, uint32_t D, uint32_t lane,
+                                           float (&out)[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t i = lane + 64u * k;
+    const float x = v[i < D ? i : D - 1];
+    out[k] = i < D ? x : 0.f;
+  }
+}
+
+// score = (cell . probe) / sqrt(d) in float64 (runtime.ts:66-72), from the
+// lane shares of both vectors.
+__device__ __forceinline__ double probe_score(const float (&cell)[8], const float (&probe)[8],
+                                              double scale) {
+  double sum = 0.0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) sum += (double)cell[k] * (double)probe[k];
+  return nd::wave_sum(sum) * scale;
+}
+
+// Scores of C cells for every probe into scores[c][p], one wave per cell
+// (the batched prefill's cells; a step's few cells are scored inside the
+// pool launch).
+__global__ __launch_bounds__(256) void n2_probe_scores_kernel(const float* __restrict__ cells,
+                                                              uint32_t C, uint32_t D,
+                                                              const float* __restrict__ probes,
+                                                              uint32_t P, double scale,
+                                                              double* __restrict__ scores) {
+  const uint32_t c = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (c >= C) return;
+  float cv[8];
+  lane_share(cells + (size_t)c * D, D, lane, cv);
+  for (uint32_t p = 0; p < P; ++p) {
+    float pv[8];
+    lane_share(probes + (size_t)p * D, D, lane, pv);
+    const double v = probe_score(cv, pv, scale);
+    if (lane == 0) scores[(size_t)c * kMaxProbes + p] = v;
+  }
+}
+
+// The online update of runtime.ts:73-90 over C cells at once, in its closed
+// form: M' = max(M, max_c s_c); every earlier term is rescaled by
+// exp(M - M') (0 before the first cell) and cell c enters with weight
+// exp(s_c - M').  Workgroup (p, j) updates probe p's weighted sums of
+// columns [64 j, 64 j + 64) and its copy of (M, denominator).
+__global__ __launch_bounds__(256) void n2_probe_pool_kernel(const float* __restrict__ cells,
+                                                            uint32_t C, uint32_t D,
+                                                            const double* __restrict__ scores,
+                                                            PoolState ps) {
+  constexpr uint32_t kChunk = 1024;
+  __shared__ double e[kChunk];
+  __shared__ double red[256];
+  const uint32_t p = blockIdx.x, j = blockIdx.y, t = threadIdx.x;
+  const uint32_t col = j * 64 + (t & 63), slice = t >> 6;
+  double* const my_max = ps.max + p * kMaxChunks + j;
+  double* const my_den = ps.den + p * kMaxChunks + j;
+  const double den_old = *my_den;
+  const double m_old = den_old > 0.0 ? *my_max : -INFINITY;
+  double mx = -INFINITY;
+  for (uint32_t c = t; c < C; c += 256) mx = fmax(mx, scores[(size_t)c * kMaxProbes + p]);
+  red[t] = mx;
+  __syncthreads();
+  for (uint32_t w = 128; w > 0; w >>= 1) {
+    if (t < w) red[t] = fmax(red[t], red[t + w]);
+    __syncthreads();
+  }
+  const double m_new = fmax(m_old, red[0]);
+  const double factor = m_old > -INFINITY ? exp(m_old - m_new) : 0.0;
+  __syncthreads();
+  double acc = 0.0, esum = 0.0;
+  for (uint32_t c0 = 0; c0 < C; c0 += kChunk) {
+    const uint32_t n = C - c0 < kChunk ? C - c0 : kChunk;
+    for (uint32_t c = t; c < n; c += 256) {
+      const double w = exp(scores[(size_t)(c0 + c) * kMaxProbes + p] - m_new);
+      e[c] = w;
+      esum += w;
+    }
+    __syncthreads();
+    if (col < D) {
+#pragma unroll 8
+      for (uint32_t c = slice; c < n; c += 4) acc += e[c] * (double)cells[(size_t)(c0 + c) * D + col];
+    }
+    __syncthreads();
+  }
+  red[t] = acc;
+  __syncthreads();
+  if (t < 64 && col < D) {
+    const double sum = ((red[t] + red[t + 64]) + red[t + 128]) + red[t + 192];
+    double* w = ps.weighted + (size_t)p * D + col;
+    *w = *w * factor + sum;
+  }
+  __syncthreads();
+  red[t] = esum;
+  __syncthreads();
+  for (uint32_t w = 128; w > 0; w >>= 1) {
+    if (t < w) red[t] += red[t + w];
+    __syncthreads();
+  }
+  if (t == 0) {
+    *my_den = den_old * factor + red[0];
+    *my_max = m_new;
+  }
+}
+
+// The same update for a step's C <= kStepCells cells, scored in the
+// launch: every load is issued first (wave w holds lane shares of cells w,
+// w + 4, ... and of probe p), the column chunk j of a cell is the share
+// element j of the wave that holds it, and the few exponentials are taken
+// once per cell.
+constexpr uint32_t kStepCells = 32;
+__global__ __launch_bounds__(256) void n2_probe_pool_step_kernel(const float* __restrict__ cells,
+                                                                 uint32_t C, uint32_t D,
+                                                                 const float* __restrict__ probes,
+                                                                 double scale, PoolState ps) {
+  constexpr int kPerWave = kStepCells / 4;
+  __shared__ double sc[kStepCells], wt[kStepCells];
+  __shared__ double part[4][64];
+  const uint32_t p = blockIdx.x, j = blockIdx.y, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  double* const my_max = ps.max + p * kMaxChunks + j;
+  double* const my_den = ps.den + p * kMaxChunks + j;
+  double* const my_w = ps.weighted + (size_t)p * D + j * 64 + lane;
+  const double den_old = *my_den, m_stored = *my_max;
+  const double w_old = j * 64 + lane < D ? *my_w : 0.0;
+  float pv[8], cv[kPerWave][8];
+  lane_share(probes + (size_t)p * D, D, lane, pv);
+#pragma unroll
+  for (int i = 0; i < kPerWave; ++i) {
+    const uint32_t c = wave + 4 * i;
+    lane_share(cells + (size_t)(c < C ? c : 0) * D, D, lane, cv[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < kPerWave; ++i) {
+    const uint32_t c = wave + 4 * i;
+    const double v = probe_score(cv[i], pv, scale);
+    if (lane == 0 && c < C) sc[c] = v;
+  }
+  __syncthreads();
+  const double m_old = den_old > 0.0 ? m_stored : -INFINITY;
+  double m_new = m_old;
+  for (uint32_t c = 0; c < C; ++c) m_new = fmax(m_new, sc[c]);
+  const double factor = m_old > -INFINITY ? exp(m_old - m_new) : 0.0;
+  if (wave == 0) {
+    const double w = lane < C ? exp(sc[lane] - m_new) : 0.0;
+    if (lane < C) wt[lane] = w;
+    const double esum = nd::wave_sum(w);
+    if (lane == 0) {
+      *my_den = den_old * factor + esum;
+      *my_max = m_new;
+    }
+  }
+  __syncthreads();
+  double acc = 0.0;
+#pragma unroll
+  for (int i = 0; i < kPerWave; ++i) {
+    const uint32_t c = wave + 4 * i;
+    float x = cv[i][0];
+#pragma unroll
+    for (int k = 1; k < 8; ++k) x = j == (uint32_t)k ? cv[i][k] : x;
+    if (c < C) acc += wt[c] * (double)x;
+  }
+  part[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && j * 64 + lane < D)
+    *my_w = w_old * factor + (((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane]);
+}
+
+// output() and confidence() (runtime.ts:93-104, 641-645): pooled =
+// f32(weighted / max(denominator, 1e-30)), output 0 = f32(bias + projection
+// row 0 . pooled) summed in float64, then its sigmoid in float64.
+__global__ __launch_bounds__(256) void n2_probe_head_kernel(PoolState ps, uint32_t P, uint32_t D,
+                                                            const float* __restrict__ projection,
+                                                            float bias, double* __restrict__ out) {
+  __shared__ double red[256];
+  const uint32_t t = threadIdx.x;
+  double sum = 0.0;
+  for (uint32_t j = t; j < P * D; j += 256) {
+    const double den = fmax(ps.den[(j / D) * kMaxChunks], 1e-30);
+    const float pooled = (float)(ps.weighted[j] / den);
+    sum += (double)projection[j] * (double)pooled;
+  }
+  red[t] = sum;
+  __syncthreads();
+  for (uint32_t w = 128; w > 0; w >>= 1) {
+    if (t < w) red[t] += red[t + w];
+    __syncthreads();
+  }
+  if (t == 0) {
+    const float o = (float)((double)bias + red[0]);
+    *out = 1.0 / (1.0 + exp(-(double)o));
+  }
+}
+
 size_t al(size_t n) { return (n + 255) & ~size_t(255); }
 
 }  // namespace
@@ -852,6 +1079,17 @@ struct nd_needle {
   // Step graphs, valid for (graph_alloc, graph_sink).
   hipGraphExec_t graphs[3] = {nullptr, nullptr, nullptr};
   uint32_t graph_alloc = 0, graph_sink = 0;
+  // Confidence probe head (absent when the description has no probes):
+  // probes [P][d] and projection row 0 [P * d] in params, the pool state in
+  // the arena's cleared part, cells of one step (or one prefill pass) and
+  // their scores as scratch.
+  bool conf = false;
+  uint32_t probe_count = 0;
+  size_t o_probes = 0, o_pproj = 0;
+  float probe_bias0 = 0.f;
+  PoolState pool{};
+  float *cells = nullptr, *pf_cells = nullptr;
+  double *scores = nullptr, *pf_scores = nullptr, *conf_out = nullptr;
 };
 
 namespace {
@@ -861,6 +1099,27 @@ void drop_graphs(nd_needle* n) {
     if (g) hipGraphExecDestroy(g);
     g = nullptr;
   }
+}
+
+// Pools C cells ([C][d]) into the confidence state: one launch that scores
+// a step's few cells itself, else a scoring launch and the update.
+hipError_t enqueue_pool(nd_needle* n, const float* cells, uint32_t C, double* scores,
+                        hipStream_t s) {
+  const uint32_t D = n->d.dim;
+  const double scale = 1.0 / std::sqrt((double)D);
+  const float* probes = n->params + n->o_probes;
+  const dim3 grid(n->probe_count, (D + 63) / 64);
+  if (C <= kStepCells) {
+    hipLaunchKernelGGL(n2_probe_pool_step_kernel, grid, dim3(256), 0, s, cells, C, D, probes,
+                       scale, n->pool);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL(n2_probe_scores_kernel, dim3((C + 3) / 4), dim3(256), 0, s, cells, C, D,
+                     probes, n->probe_count, scale, scores);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(n2_probe_pool_kernel, grid, dim3(256), 0, s, cells, C, D, scores, n->pool);
+  return hipGetLastError();
 }
 
 // Enqueues one token of NeedleRuntime.step (model/runtime.ts:280-583) on s.
@@ -898,6 +1157,7 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
   b.cat = n->cat;
   b.inv_freq = n->inv_freq;
   b.rope = n->rope;
+  b.cell0 = n->conf ? n->cells : nullptr;
   hipLaunchKernelGGL(n2_begin_kernel, dim3(1), dim3(kWg), 0, s, b);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -916,11 +1176,12 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
   const size_t K = (size_t)ln * D;
   const bool tail = want_logits || select;
   // Launch l (l <= layers) runs post(l - 1) and pre(l); the last one runs
-  // post(layers - 1) and the final norm, and only when logits are wanted
-  // (the lanes do not outlive the step).
+  // post(layers - 1) and the final norm, and only when logits are wanted or
+  // the confidence pool takes the last layer's lane mean (otherwise the
+  // lanes do not outlive the step).
   for (uint32_t l = 0; l <= d.layers; ++l) {
     const bool pre = l < d.layers;
-    if (!pre && !tail) break;
+    if (!pre && !tail && !n->conf) break;
     // Every operand pointer is valid whether or not its half runs (the
     // kernel loads them unconditionally): an absent layer reads layer 0's.
     const uint32_t pl = l > 0 ? l - 1 : 0, ql = pre ? l : 0;
@@ -960,9 +1221,10 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
     m.ekey = n->ekv_out + (size_t)(site >= 0 ? site : 0) * 2 * D;
     m.evalue = n->evals + (size_t)(site >= 0 ? site : 0) * D;
     m.norm_input = n->params + n->o_norm_input + (size_t)ql * D;
-    m.has_final = !pre;
+    m.has_final = !pre && tail;
     m.final_norm = n->params + n->o_final;
     m.fin = n->fin;
+    m.cell = n->conf && l > 0 ? n->cells + (size_t)l * D : nullptr;
     hipLaunchKernelGGL(n2_mix_kernel, dim3(1), dim3(kMixWg), 0, s, m);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (!pre) break;
@@ -989,6 +1251,8 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
     if ((e = nd_launch_matvec(n->wo[l], n->att, 1, qw, 0, D, n->proj, D, s)) != hipSuccess)
       return e;
   }
+  if (n->conf && (e = enqueue_pool(n, n->cells, d.layers + 1, n->scores, s)) != hipSuccess)
+    return e;
   if (!tail) return hipSuccess;
   e = nd_launch_matvec(n->embedding, n->fin, 1, D, 0, d.vocab, n->logits, d.vocab, s);
   if (e != hipSuccess || !select) return e;
@@ -1047,7 +1311,9 @@ nd_status ensure_prefill(nd_ctx* ctx, nd_needle* n) {
                           al((size_t)cap * S * 2 * D * 4), al((size_t)cap * S * D * 4),
                           al((size_t)cap * 4),          al(pf * 4),
                           al((size_t)3 * cap * kmax),   al((size_t)cap * 4),
-                          al((size_t)cap * d.kv_heads * kAttnCounterStride * 4)};
+                          al((size_t)cap * d.kv_heads * kAttnCounterStride * 4),
+                          n->conf ? al((size_t)cap * (d.layers + 1) * D * 4) : 0,
+                          n->conf ? al((size_t)cap * (d.layers + 1) * kMaxProbes * 8) : 0};
   size_t total = 0;
   for (size_t v : sizes) total += v;
   hipError_t e = hipMalloc(&n->pf_arena, total);
@@ -1083,6 +1349,8 @@ nd_status ensure_prefill(nd_ctx* ctx, nd_needle* n) {
   take(&n->pf_digits);
   take(&n->pf_positions);
   take(&n->pf_counters);
+  take(&n->pf_cells);
+  take(&n->pf_scores);
   n->pf_cap = cap;
   return ND_OK;
 }
@@ -1119,6 +1387,9 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
   b.per_order = d.n_orders ? d.engram_tables / d.n_orders : 1;
   for (uint32_t i = 0; i < d.n_orders; ++i) b.orders[i] = d.orders[i];
   b.cat = n->pf_cat;
+  const uint32_t cell_ld = (d.layers + 1) * D;  // cells of one position: [layers + 1][d]
+  b.cell0 = n->conf ? n->pf_cells : nullptr;
+  b.cell_ld = cell_ld;
   hipLaunchKernelGGL(n2_begin_batch_kernel, dim3(M), dim3(kWg), 0, s, b, p0, M, n->pf_positions);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -1141,11 +1412,14 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   const size_t K = (size_t)N;
+  const bool tail = want_logits || select;
   for (uint32_t l = 0; l <= d.layers; ++l) {
     const bool pre = l < d.layers;
-    if (!pre && !want_logits && !select) break;
+    if (!pre && !tail && !n->conf) break;
     const uint32_t pl = l > 0 ? l - 1 : 0, ql = pre ? l : 0;
-    const uint32_t rows = pre ? M : 1, r0 = pre ? 0 : M - 1;  // the final part: last row only
+    // The final part runs the last row only, unless the confidence pool
+    // needs every row's last lane mean.
+    const uint32_t rows = pre || n->conf ? M : 1, r0 = pre || n->conf ? 0 : M - 1;
     int site = -1;
     for (uint32_t si = 0; si < d.n_sites; ++si)
       if (pre && d.sites[si] == l) site = (int)si;
@@ -1184,9 +1458,12 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
     m.ek_ld = S * 2 * D;
     m.ev_ld = S * D;
     m.norm_input = n->params + n->o_norm_input + (size_t)ql * D;
-    m.has_final = !pre;
+    m.has_final = !pre && tail;
+    m.final_row = rows - 1;
     m.final_norm = n->params + n->o_final;
     m.fin = n->fin;
+    m.cell = n->conf && l > 0 ? n->pf_cells + (size_t)l * D : nullptr;
+    m.cell_ld = cell_ld;
     if (pre) {
       m.route_out = n->pf_route;
       m.r_a_post = n->a_post[l];
@@ -1221,7 +1498,10 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
         hipSuccess)
       return e;
   }
-  if (!want_logits && !select) return hipSuccess;
+  if (n->conf && (e = enqueue_pool(n, n->pf_cells, M * (d.layers + 1), n->pf_scores, s)) !=
+                     hipSuccess)
+    return e;
+  if (!tail) return hipSuccess;
   e = nd_launch_matvec(n->embedding, n->fin, 1, D, 0, d.vocab, n->logits, d.vocab, s);
   if (e != hipSuccess || !select) return e;
   return nd_launch_select_list(n->logits, d.vocab, nullptr, 0, n->sel_id, n->sel_lp, s);
@@ -1322,6 +1602,11 @@ nd_status nd_needle_create(nd_ctx* ctx, const nd_needle_desc* d, nd_needle** out
     return st;
   if (!d->wq || !d->wk || !d->wv || !d->wgate || !d->wo)
     return nd_fail(ctx, ND_ERR_INVALID, "layer matrix arrays must not be NULL");
+  if (d->probes && (d->probe_count == 0 || d->probe_count > kMaxProbes || d->probe_out == 0 ||
+                    !d->probe_projection || !d->probe_bias))
+    return nd_fail(ctx, ND_ERR_INVALID,
+                   "confidence head needs 1..%u probes, at least one output, a projection and a "
+                   "bias", kMaxProbes);
   for (uint32_t l = 0; l < L; ++l)
     if ((st = check(d->wq[l], qw, D, "wq")) || (st = check(d->wk[l], kw, D, "wk")) ||
         (st = check(d->wv[l], kw, D, "wv")) || (st = check(d->wgate[l], qw, D, "wgate")) ||
@@ -1402,6 +1687,13 @@ nd_status nd_needle_create(nd_ctx* ctx, const nd_needle_desc* d, nd_needle** out
   n->o_taps = put(d->n_sites ? d->eg_taps : nullptr,
                   (size_t)(d->n_sites ? d->n_sites * d->engram_taps : 1) * D);
   n->o_final = put(d->final_norm, D);
+  if (d->probes) {
+    n->conf = true;
+    n->probe_count = d->probe_count;
+    n->o_probes = put(d->probes, (size_t)d->probe_count * D);
+    n->o_pproj = put(d->probe_projection, (size_t)d->probe_count * D);  // row 0
+    n->probe_bias0 = d->probe_bias[0];
+  }
   n->attention_gate.assign(d->attention_gate, d->attention_gate + L);
   n->a_pre.assign(d->a_pre, d->a_pre + L);
   n->a_post.assign(d->a_post, d->a_post + L);
@@ -1462,14 +1754,20 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     const uint32_t S = d.n_sites ? d.n_sites : 1;
     const uint32_t cat = d.n_sites ? d.engram_tables * d.engram_sub : 1;
     // State first (cleared by every reset), then scratch.
+    const size_t P8 = kMaxProbes * 8, cb = n->conf ? 1 : 0;
     const size_t sizes[] = {al(64), al((size_t)cap * 4), al((size_t)cap * 8),
-                            al((size_t)S * n->depth * D * 4), al((size_t)d.kv_heads * kAttnCounterStride * 4), al(64), al(64),
+                            al((size_t)S * n->depth * D * 4),
+                            al((size_t)d.kv_heads * kAttnCounterStride * 4),
+                            cb * al(P8 * kMaxChunks), cb * al(P8 * kMaxChunks),
+                            cb * al(P8 * D), al(64), al(64),
                             al((size_t)d.vocab * 4), al(rows * kHd), al(rows * kHd), al(rows * 4),
                             al(rows * 4), al((size_t)ln * D * 4), al(D * 4), al(D * 4), al(D * 4),
                             al((size_t)(2 * qw + 2 * kw) * 4), al(qw * 4), al(qw * 4), al(D * 4),
                             al(ln * 4), al(ln * ln * 4), al(D * 4), al((size_t)d.vocab * 4),
                             al((size_t)S * cat * 4), al((size_t)S * 2 * D * 4),
-                            al((size_t)S * D * 4), al(pf * 4), al(20 * 4), al(64 * 8)};
+                            al((size_t)S * D * 4), al(pf * 4), al(20 * 4), al(64 * 8),
+                            cb * al((size_t)(d.layers + 1) * D * 4),
+                            cb * al((size_t)(d.layers + 1) * P8), cb * al(64)};
     size_t total = 0;
     for (size_t v : sizes) total += v;
     ND_HIP(ctx, hipMalloc(&n->arena, total));
@@ -1484,6 +1782,9 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     take(&n->lp_history);
     take(&n->ring);
     take(&n->counters);
+    take(&n->pool.max);
+    take(&n->pool.den);
+    take(&n->pool.weighted);
     n->state_bytes = (size_t)(p - n->arena);
     take(&n->sel_id);
     take(&n->sel_lp);
@@ -1513,6 +1814,9 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     take(&n->partials);
     take(&n->route);
     take(&n->rope);
+    take(&n->cells);
+    take(&n->scores);
+    take(&n->conf_out);
   }
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
   ND_HIP(ctx, hipMemsetAsync(n->arena, 0, n->state_bytes, ctx->stream));
@@ -1535,6 +1839,20 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
 nd_kv* nd_needle_kv(nd_needle* n) { return n && n->arena && n->max_length ? &n->kv : nullptr; }
 
 uint32_t nd_needle_position(const nd_needle* n) { return n ? n->position : 0; }
+
+nd_status nd_needle_confidence(nd_ctx* ctx, nd_needle* n, double* confidence) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!n || !confidence) return nd_fail(ctx, ND_ERR_INVALID, "nd_needle_confidence: NULL argument");
+  if (!n->conf) return nd_fail(ctx, ND_ERR_INVALID, "the model has no confidence head");
+  if (!n->arena || !n->max_length)
+    return nd_fail(ctx, ND_ERR_INVALID, "runtime is not reset");
+  hipLaunchKernelGGL(n2_probe_head_kernel, dim3(1), dim3(256), 0, ctx->stream, n->pool,
+                     n->probe_count, n->d.dim, n->params + n->o_pproj, n->probe_bias0, n->conf_out);
+  ND_HIP(ctx, hipGetLastError());
+  ND_HIP(ctx, hipMemcpyAsync(confidence, n->conf_out, 8, hipMemcpyDeviceToHost, ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ND_OK;
+}
 
 nd_status nd_needle_step(nd_ctx* ctx, nd_needle* n, uint32_t token, float* logits) {
   if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");

@@ -104,6 +104,7 @@ SIGNATURES = {
     "nd_needle_reset": (I32, [P, P, U32, U32]),
     "nd_needle_kv": (P, [P]),
     "nd_needle_position": (U32, [P]),
+    "nd_needle_confidence": (I32, [P, P, C.POINTER(C.c_double)]),
     "nd_needle_step": (I32, [P, P, U32, P]),
     "nd_needle_prefill": (I32, [P, P, P, U32, P]),
     "nd_needle_step_select": (I32, [P, P, U32, P, U32, P, P]),
@@ -139,6 +140,8 @@ class NeedleDesc(C.Structure):
         ("pre_hadamard_norm", P), ("d1", P), ("d2", P), ("d3", P), ("attention_gate", P),
         ("a_pre", P), ("a_post", P), ("a_res", P), ("b_pre", P), ("b_post", P), ("b_res", P),
         ("eg_taps", P), ("final_norm", P),
+        ("probes", P), ("probe_count", U32), ("probe_out", U32), ("probe_projection", P),
+        ("probe_bias", P),
     ]
 
 

@@ -8,7 +8,9 @@ d 512, 27 layers, 8 query heads and 4 KV heads of 64, 4 mHC lanes, Hadamard
 theta is not documented; 10000 is used.  Every Cactus-Quant matrix becomes an
 int8 matrix with one fp32 scale per row (uniform codes in [-127, 127],
 scales ~U(0.001, 0.02)); dense vectors are seeded near neutral (norm offsets
-~U(-0.1, 0.1), Hadamard diagonals ~U(0.5, 1.5)).
+~U(-0.1, 0.1), Hadamard diagonals ~U(0.5, 1.5)).  The confidence probe head
+has the shape the resident reference path accepts (resident/compatibility.ts:42-51):
+8 probes of d, one output.
 """
 
 from __future__ import annotations
@@ -40,6 +42,19 @@ class Needle2Geometry:
     sites: tuple = (2, 15)
     rope_theta: float = 10000.0
     kv_window: int = 256
+
+
+class ProbeHead:
+    """CactProbeHead (model/cact.ts:105-112): probes [count][dim],
+    projection [output_size][count * dim], bias [output_size]."""
+
+    def __init__(self, probes: np.ndarray, projection: np.ndarray, bias: np.ndarray):
+        self.probes = np.ascontiguousarray(probes, dtype=np.float32)
+        self.projection = np.ascontiguousarray(projection, dtype=np.float32)
+        self.bias = np.ascontiguousarray(bias, dtype=np.float32)
+        self.probe_count, dim = self.probes.shape
+        self.output_size = self.bias.shape[0]
+        assert self.projection.shape == (self.output_size, self.probe_count * dim)
 
 
 class Needle2Weights:
@@ -86,3 +101,6 @@ class Needle2Weights:
         self.eg_value = [mat(f"n2.e{s}.value", d, cat) for s in range(len(g.sites))]
         self.eg_taps = u("n2.eg_taps", (len(g.sites), g.engram_taps, d), -0.5, 0.5)
         self.final_norm = u("n2.final_norm", (d,), -0.1, 0.1)
+        self.confidence = ProbeHead(u("n2.conf.probes", (8, d), -0.1, 0.1),
+                                    u("n2.conf.projection", (1, 8 * d), -0.003, 0.003),
+                                    u("n2.conf.bias", (1,), -0.2, 0.2))

@@ -43,7 +43,8 @@ class HipNeedleSession:
     the role of the reference's ResidentExecutionSession
     (backends/backend.ts:66-80) for a whole token."""
 
-    def __init__(self, backend: HipBackend, weights: Needle2Weights):
+    def __init__(self, backend: HipBackend, weights: Needle2Weights,
+                 collect_confidence: bool = True):
         self.backend = backend
         self.weights = weights
         g = weights.geometry
@@ -85,6 +86,16 @@ class HipNeedleSession:
                      "pre_hadamard_norm", "d1", "d2", "d3", "attention_gate", "a_pre",
                      "a_post", "a_res", "b_pre", "b_post", "b_res", "eg_taps", "final_norm"):
             setattr(d, name, vec(getattr(w, name)))
+        # The confidence pool runs whenever the weights carry the head, as
+        # the reference's does unless collectConfidence is false
+        # (model/runtime.ts:215-224).
+        head = getattr(w, "confidence", None)
+        self.has_confidence = bool(collect_confidence and head is not None)
+        if self.has_confidence:
+            d.probes = vec(head.probes)
+            d.probe_count, d.probe_out = head.probe_count, head.output_size
+            d.probe_projection = vec(head.projection)
+            d.probe_bias = vec(head.bias)
         handle = C.c_void_p()
         backend._check(lib.nd_needle_create(backend.ctx, C.byref(d), C.byref(handle)),
                        "nd_needle_create")
@@ -93,6 +104,16 @@ class HipNeedleSession:
 
     def _check(self, status: int, what: str) -> None:
         self.backend._check(status, what)
+
+    def confidence(self) -> Optional[float]:
+        """residentConfidence (backends/backend.ts:77): the probe head over
+        every cell pooled since reset, or None without a head."""
+        if not self.has_confidence:
+            return None
+        out = C.c_double()
+        self._check(self.lib.nd_needle_confidence(self.backend.ctx, self.handle, C.byref(out)),
+                    "nd_needle_confidence")
+        return float(out.value)
 
     def reset(self, maximum_length: int, sink_length: int = 0) -> None:
         invariant(isinstance(maximum_length, (int, np.integer)) and maximum_length > 0,
@@ -221,6 +242,10 @@ class NeedleRuntime:
     def step_selected(self, token: int, allowed: Optional[np.ndarray] = None):
         return self.session.step_selected(token, allowed)
 
+    def resolve_confidence(self) -> Optional[float]:
+        """resolveConfidence (model/runtime.ts:634-639) from the resident pool."""
+        return self.session.confidence()
+
 
 @dataclass
 class GenerationResult:
@@ -238,10 +263,11 @@ class NeedleModel:
     token ids: prefill, then greedy argmax tokens with their logSoftmaxAt,
     stopping before EOS or after max_new_tokens."""
 
-    def __init__(self, backend: HipBackend, weights: Needle2Weights):
+    def __init__(self, backend: HipBackend, weights: Needle2Weights,
+                 collect_confidence: bool = True):
         self.backend = backend
         self.weights = weights
-        self.session = HipNeedleSession(backend, weights)
+        self.session = HipNeedleSession(backend, weights, collect_confidence)
 
     def create_runtime(self) -> NeedleRuntime:
         return NeedleRuntime(self.session)

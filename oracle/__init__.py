@@ -432,6 +432,8 @@ class _N2Model(C.Structure):
         ("a_pre", P), ("a_post", P), ("a_res", P), ("b_pre", P), ("b_post", P), ("b_res", P),
         ("eg_tables", C.POINTER(_N2Mat)), ("eg_key", C.POINTER(_N2Mat)),
         ("eg_value", C.POINTER(_N2Mat)), ("eg_taps", P), ("final_norm", P),
+        ("probes", P), ("probe_count", U32), ("probe_out", U32), ("probe_projection", P),
+        ("probe_bias", P),
     ]
 
 
@@ -440,6 +442,9 @@ _SIG_N2 = {
     "or_n2_destroy": (None, [P]),
     "or_n2_kv": (P, [P]),
     "or_n2_step": (C.c_int, [P, U32, P]),
+    "or_n2_confidence": (C.c_int, [P, C.POINTER(D)]),
+    "or_n2_record_cells": (None, [P, P, U32]),
+    "or_n2_recorded_cells": (U32, [P]),
 }
 
 
@@ -498,6 +503,13 @@ class Needle2:
                      "pre_hadamard_norm", "d1", "d2", "d3", "a_pre", "a_post", "a_res", "b_pre",
                      "b_post", "b_res", "eg_taps", "final_norm"):
             setattr(st, name, vec(getattr(weights, name)))
+        head = getattr(weights, "confidence", None)
+        if head is not None:
+            st.probes = vec(head.probes)
+            st.probe_count = head.probe_count
+            st.probe_out = head.output_size
+            st.probe_projection = vec(head.projection)
+            st.probe_bias = vec(head.bias)
         self.struct = st
         _n2_lib()
 
@@ -523,6 +535,21 @@ class Needle2Runtime:
         logits = np.empty(self.model.geometry.vocab, np.float32) if want_logits else None
         _ok(_n2_lib().or_n2_step(self.h, token, _p(logits) if want_logits else None))
         return logits
+
+    def confidence(self) -> float:
+        """resolveConfidence on the CPU path (runtime.ts:634-645)."""
+        out = D()
+        _ok(_n2_lib().or_n2_confidence(self.h, C.byref(out)))
+        return out.value
+
+    def record_cells(self, cap: int) -> np.ndarray:
+        """Buffer that receives the next `cap` pooled cells ([cap][dim])."""
+        self._cells = np.zeros((cap, self.model.geometry.dim), np.float32)
+        _n2_lib().or_n2_record_cells(self.h, _p(self._cells), cap)
+        return self._cells
+
+    def recorded_cells(self) -> int:
+        return int(_n2_lib().or_n2_recorded_cells(self.h))
 
     def kv_read(self, layer: int, head: int):
         cache = KvCache.__new__(KvCache)

@@ -8,7 +8,10 @@
  * Parity pins: the composition is checked against an independent float64
  * numpy model of the same graph (tests/test_oracle_needle2.py) on a reduced
  * geometry, and prefill == repeated step by construction; every primitive is
- * pinned in needle_oracle.c.
+ * pinned in needle_oracle.c.  The confidence pool (OnlineProbePool,
+ * runtime.ts:48-105) is checked against the closed form of its online
+ * update (a softmax over every pooled cell, scipy.special.softmax, then the
+ * projection and a sigmoid) on cells recorded from the same steps.
  */
 #include <math.h>
 #include <stdint.h>
@@ -82,6 +85,12 @@ typedef struct {
   const n2_mat* eg_value;
   const float* eg_taps;         /* [sites][taps][dim] */
   const float* final_norm;
+  /* Confidence probe head (CactProbeHead, cact.ts:105-112); probes == NULL
+   * when the archive has none. */
+  const float* probes;          /* [probe_count][dim] */
+  uint32_t probe_count, probe_out;
+  const float* probe_projection; /* [probe_out][probe_count * dim] */
+  const float* probe_bias;      /* [probe_out] */
 } n2_model;
 
 typedef struct {
@@ -93,6 +102,13 @@ typedef struct {
   float* ring;      /* [sites][depth][dim] */
   uint8_t* valid;   /* [sites][depth] */
   uint32_t depth, engram_position;
+  /* OnlineProbePool state (runtime.ts:48-62); cells_out, when set, records
+   * every pooled cell (for the closed-form check). */
+  double* pool_max;       /* [probe_count] */
+  double* pool_den;       /* [probe_count] */
+  double* pool_weighted;  /* [probe_count][dim] */
+  float* cells_out;
+  uint32_t cells_count, cells_cap;
 } n2_state;
 
 static void mv(const n2_mat* m, const float* x, uint32_t row_start, uint32_t rows, float* y) {
@@ -115,8 +131,74 @@ n2_state* or_n2_create(const n2_model* md, uint32_t max_length, uint32_t sink) {
   st->depth = (md->engram_taps - 1) * max_order + 1;
   st->ring = (float*)calloc((size_t)md->n_sites * st->depth * md->dim, sizeof(float));
   st->valid = (uint8_t*)calloc((size_t)md->n_sites * st->depth, 1);
+  if (md->probes && md->probe_count) {
+    st->pool_max = (double*)malloc(sizeof(double) * md->probe_count);
+    for (uint32_t p = 0; p < md->probe_count; p++) st->pool_max[p] = -INFINITY;
+    st->pool_den = (double*)calloc(md->probe_count, sizeof(double));
+    st->pool_weighted = (double*)calloc((size_t)md->probe_count * md->dim, sizeof(double));
+  }
   return st;
 }
+
+/* runtime.ts:64-91 OnlineProbePool.add: per probe, score = (cell . probe) /
+ * sqrt(dim) summed in float64, then the online softmax-weighted update of
+ * (maximum, denominator, weighted cell sum). */
+static void pool_add(n2_state* st, const float* cell) {
+  const n2_model* md = st->md;
+  if (!st->pool_max) return;
+  const uint32_t d = md->dim;
+  if (st->cells_out && st->cells_count < st->cells_cap)
+    memcpy(st->cells_out + (size_t)st->cells_count++ * d, cell, sizeof(float) * d);
+  const double scale = 1.0 / sqrt((double)d);
+  for (uint32_t p = 0; p < md->probe_count; p++) {
+    double score = 0;
+    const float* probe = md->probes + (size_t)p * d;
+    for (uint32_t i = 0; i < d; i++) score += (double)cell[i] * (double)probe[i];
+    score *= scale;
+    const double previous = st->pool_max[p];
+    double* w = st->pool_weighted + (size_t)p * d;
+    if (score <= previous) {
+      const double weight = exp(score - previous);
+      st->pool_den[p] = st->pool_den[p] + weight;
+      for (uint32_t i = 0; i < d; i++) w[i] = w[i] + weight * (double)cell[i];
+    } else {
+      const double old = isfinite(previous) ? exp(previous - score) : 0.0;
+      st->pool_den[p] = st->pool_den[p] * old + 1;
+      for (uint32_t i = 0; i < d; i++) w[i] = w[i] * old + (double)cell[i];
+      st->pool_max[p] = score;
+    }
+  }
+}
+
+/* runtime.ts:93-104 output() then runtime.ts:641-645 confidence():
+ * pooled = f32(weighted / max(denominator, 1e-30)), denseMatvec with the
+ * bias (backends/cq.ts:297-318: float64 sum from the bias, f32 store), and
+ * the sigmoid of output 0 in float64. */
+int or_n2_confidence(const n2_state* st, double* confidence) {
+  const n2_model* md = st->md;
+  if (!st->pool_max || md->probe_out == 0) return OR_INVALID;
+  const uint32_t d = md->dim, width = md->probe_count * d;
+  float* pooled = (float*)malloc(sizeof(float) * width);
+  for (uint32_t p = 0; p < md->probe_count; p++) {
+    double den = st->pool_den[p] > 1e-30 ? st->pool_den[p] : 1e-30;
+    for (uint32_t i = 0; i < d; i++)
+      pooled[(size_t)p * d + i] = (float)(st->pool_weighted[(size_t)p * d + i] / den);
+  }
+  double sum = (double)md->probe_bias[0];
+  for (uint32_t j = 0; j < width; j++) sum += (double)md->probe_projection[j] * (double)pooled[j];
+  free(pooled);
+  *confidence = or_sigmoid((double)(float)sum);
+  return OR_OK;
+}
+
+/* Records the next `cap` pooled cells into cells ([cap][dim]); count out. */
+void or_n2_record_cells(n2_state* st, float* cells, uint32_t cap) {
+  st->cells_out = cells;
+  st->cells_cap = cap;
+  st->cells_count = 0;
+}
+
+uint32_t or_n2_recorded_cells(const n2_state* st) { return st->cells_count; }
 
 void or_n2_destroy(n2_state* st) {
   if (!st) return;
@@ -124,6 +206,9 @@ void or_n2_destroy(n2_state* st) {
   free(st->history);
   free(st->ring);
   free(st->valid);
+  free(st->pool_max);
+  free(st->pool_den);
+  free(st->pool_weighted);
   free(st);
 }
 
@@ -191,6 +276,7 @@ int or_n2_step(n2_state* st, uint32_t token, float* logits) {
             md->embedding.k, token, emb);
   double es = sqrt((double)d);
   for (uint32_t i = 0; i < d; i++) emb[i] = (float)((double)emb[i] * es);
+  pool_add(st, emb); /* runtime.ts:310 */
   for (uint32_t ln = 0; ln < L; ln++) memcpy(x + ln * d, emb, sizeof(float) * d);
 
   /* runtime.ts:820-877 #engramStep */
@@ -304,6 +390,15 @@ int or_n2_step(n2_state* st, uint32_t token, float* logits) {
         nx[ln * d + c] = (float)(sum + (double)hpost[ln] * (double)delta[c]);
       }
     memcpy(x, nx, sizeof(float) * L * d);
+    /* runtime.ts:543-550: the lane mean after the layer joins the pool. */
+    if (st->pool_max) {
+      for (uint32_t c = 0; c < d; c++) {
+        double sum = 0;
+        for (uint32_t ln = 0; ln < L; ln++) sum += x[ln * d + c];
+        tmp[c] = (float)(sum / L);
+      }
+      pool_add(st, tmp);
+    }
   }
   st->position++;
   if (logits) {

@@ -34,6 +34,13 @@ def close(got, want, what):
     assert err.max() <= 1e-3 * np.abs(want).max(), (what, float(err.max()))
 
 
+def close_confidence(got, want, what):
+    """The probe head's sigmoid output: within 1e-3 relative of the oracle's
+    (the pooled cells carry the whole model's 1e-4-level differences)."""
+    assert got is not None and 0.0 < got < 1.0, (what, got)
+    assert abs(got - want) <= 1e-3 * want, (what, got, want)
+
+
 @pytest.fixture(scope="module")
 def small(hip):
     w = Needle2Weights(SMALL, 31)
@@ -56,6 +63,8 @@ def test_step_logits_and_kv_match_oracle(small, sink):
         got = rt.step(int(t))
         close(got, want, (sink, i))
         assert rt.position == i + 1
+        if i in (0, 9, len(tokens) - 1):
+            close_confidence(rt.resolve_confidence(), ref.confidence(), ("confidence", sink, i))
     for layer in (0, SMALL.layers - 1):
         for h in range(SMALL.kv_heads):
             gk, gv, gks, gvs = model.session.kv_read(layer, h)
@@ -107,6 +116,7 @@ def test_prefill_and_step_selected(small):
     for t in prompt:
         want = ref.step(int(t))
     close(got, want, "prefill")
+    close_confidence(rt.resolve_confidence(), ref.confidence(), "confidence after prefill")
     allowed = np.unique(synth.Stream(7, "n2allowed").integers(60, 0, SMALL.vocab - 1))
     tok = int(prompt[-1])
     for i in range(6):
@@ -116,6 +126,13 @@ def test_prefill_and_step_selected(small):
         assert gid == rid, i
         assert abs(glp - rlp) <= 1e-3 * max(1.0, abs(rlp)), i
         tok = gid
+    close_confidence(rt.resolve_confidence(), ref.confidence(), "confidence after selection")
+    # reset clears the pool: one token pools that token's cells only
+    rt.reset(40, 2)
+    ref = oracle.Needle2(w).runtime(40, 2)
+    rt.step(int(prompt[0]), want_logits=False)
+    ref.step(int(prompt[0]), want_logits=False)
+    close_confidence(rt.resolve_confidence(), ref.confidence(), "confidence after reset")
 
 
 def test_generate_matches_stepwise_oracle(small):
@@ -213,6 +230,25 @@ def test_generate_full_geometry_greedy_identical(hip):
                 logits = ref.step(tok)
         assert res.token_ids == ids
         np.testing.assert_allclose(res.token_log_probabilities, lps, rtol=1e-3, atol=1e-3)
+        # the graph-replayed steps pooled every token they ran
+        close_confidence(model.session.confidence(), ref.confidence(), "generate confidence")
+    finally:
+        model.dispose()
+
+
+def test_confidence_absent_or_disabled(hip):
+    say("needle2 confidence disabled")
+    w = Needle2Weights(SMALL, 32)
+    model = NeedleModel(hip, w, collect_confidence=False)
+    try:
+        rt = model.create_runtime()
+        rt.reset(8)
+        rt.step(3)
+        assert rt.resolve_confidence() is None
+        import ctypes as C
+        out = C.c_double()
+        st = hip.lib.nd_needle_confidence(hip.ctx, model.session.handle, C.byref(out))
+        assert st != 0 and b"no confidence head" in hip.lib.nd_last_error(hip.ctx)
     finally:
         model.dispose()
 
@@ -239,6 +275,7 @@ def test_batched_prefill_then_steps(hip, window, sink, n_prompt, max_length):
         for t in prompt:
             want = ref.step(int(t))
         close(got, want, "prefill logits")
+        close_confidence(rt.resolve_confidence(), ref.confidence(), "batched prefill confidence")
         alloc = min(g.max_length, sink + window) if window else g.max_length
         written = min(n_prompt, alloc)  # slots fill in order; the rest were never stored
         for layer in (0, g.layers - 1):
@@ -256,5 +293,6 @@ def test_batched_prefill_then_steps(hip, window, sink, n_prompt, max_length):
             got = rt.step(tok)
             close(got, want, ("step after prefill", i))
             tok = int(np.argmax(want))
+        close_confidence(rt.resolve_confidence(), ref.confidence(), "confidence after steps")
     finally:
         model.dispose()

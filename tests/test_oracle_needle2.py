@@ -42,6 +42,7 @@ class NumpyNeedle2:
         self.K = [[] for _ in range(g.layers)]  # dequantized rows by position
         self.V = [[] for _ in range(g.layers)]
         self.H = hadamard(g.hadamard) / np.sqrt(g.hadamard)
+        self.cells = []  # pooled cells: scaled embedding, then each layer's lane mean
 
     @staticmethod
     def rms(x, s=None):
@@ -80,6 +81,7 @@ class NumpyNeedle2:
         g, w = self.g, self.w
         self.history.append(token)
         x = np.tile(dense(w.embedding)[token] * np.sqrt(g.dim), (g.lanes, 1))
+        self.cells.append(x[0].copy())
         keys, vals = [], []
         idx, ok = self.lookup()
         for s in range(len(g.sites)):
@@ -155,6 +157,7 @@ class NumpyNeedle2:
                 r = r - logsumexp(r, axis=1, keepdims=True)
                 r = r - logsumexp(r, axis=0, keepdims=True)
             x = np.exp(r) @ x + hpost[:, None] * delta[None, :]
+            self.cells.append(x.mean(axis=0))
         self.pos += 1
         return dense(w.embedding) @ self.rms(x.mean(axis=0), w.final_norm)
 
@@ -192,3 +195,53 @@ def test_overflow_and_bad_token():
         rt.step(1)
     with pytest.raises(oracle.OracleError):
         oracle.Needle2(w).runtime(5).step(SMALL.vocab)
+
+
+def pooled_confidence(head, cells):
+    """Closed form of OnlineProbePool over `cells` (runtime.ts:48-105): per
+    probe a softmax over the cells' scores (cell . probe / sqrt(d)), the
+    softmax-weighted mean cell, the dense projection plus bias, sigmoid of
+    output 0 (runtime.ts:641-645)."""
+    from scipy.special import softmax
+
+    cells = np.asarray(cells, np.float64)
+    probes = head.probes.astype(np.float64)
+    scores = cells @ probes.T / np.sqrt(cells.shape[1])       # [cells][probes]
+    weights = softmax(scores, axis=0)
+    pooled = (weights.T @ cells).reshape(-1)                  # [probes * d]
+    out = head.bias.astype(np.float64) + head.projection.astype(np.float64) @ pooled
+    return float(expit(out[0]))
+
+
+@pytest.mark.parametrize("sink", [0, 3])
+def test_confidence_pool_matches_closed_form(sink):
+    w = Needle2Weights(SMALL, 12)
+    rt = oracle.Needle2(w).runtime(SMALL.max_length, sink)
+    ref = NumpyNeedle2(w, SMALL.max_length, sink)
+    tokens = [5, 200, 17, 17, 99, 3, 250, 17, 5]
+    cells = rt.record_cells(len(tokens) * (SMALL.layers + 1))
+    for t in tokens:
+        rt.step(t, want_logits=False)
+        ref.step(t)
+    assert rt.recorded_cells() == len(tokens) * (SMALL.layers + 1)
+    want = np.asarray(ref.cells)
+    for i, (got_c, want_c) in enumerate(zip(cells, want)):
+        assert np.abs(got_c - want_c).max() <= 1e-4 * np.abs(want_c).max(), i
+    # the online update equals the closed form on the same cells ...
+    conf = rt.confidence()
+    assert abs(conf - pooled_confidence(w.confidence, cells)) <= 1e-6 * conf
+    # ... and the independent model's cells give the same confidence
+    assert abs(conf - pooled_confidence(w.confidence, want)) <= 1e-4 * conf
+    assert 0.0 < conf < 1.0
+
+
+def test_confidence_single_cell_is_that_cell():
+    # One step: every probe's softmax pools the step's L + 1 cells; with one
+    # token the first cell is the scaled embedding row.
+    w = Needle2Weights(SMALL, 13)
+    rt = oracle.Needle2(w).runtime(SMALL.max_length)
+    cells = rt.record_cells(SMALL.layers + 1)
+    rt.step(7, want_logits=False)
+    emb = oracle.row_i8(w.embedding.codes, w.embedding.scales, SMALL.dim, 7)
+    assert np.array_equal(cells[0], (emb.astype(np.float64) * np.sqrt(SMALL.dim)).astype(np.float32))
+    assert abs(rt.confidence() - pooled_confidence(w.confidence, cells)) <= 1e-6
