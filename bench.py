@@ -169,6 +169,87 @@ def bench_cq_matvec(torch, hip, n, k, g, bits, batch, steps, warmup):
             "frac_hbm": gbs / HBM_PEAK_GBS}
 
 
+def bench_grammar_mask(torch, hip, reps, cpu_seconds):
+    """Allowed-token masks of the tool-call grammar over an 8192-piece
+    vocabulary, at every state along a complete two-call output of the demo
+    tools (longest-piece tokenization): the device kernel alone (states
+    resident in HBM, one launch per mask, HIP events), the host call with
+    its undecided pieces settled, and the agent's own loop (a grammar clone
+    fed per piece, tools/agent.ts:164-175) on the host as the CPU baseline."""
+    import ctypes as C
+
+    import numpy as np
+
+    from needle_hip import synth
+    from needle_hip.grammar import ToolCallGrammar, allowed_pieces
+    from needle_hip.maskgen import GrammarMasker, state_words
+
+    tools = synth.demo_tools()
+    pieces, eligible = synth.tool_pieces(7, 8192, tools)
+    masker = GrammarMasker(hip, tools, pieces, eligible)
+    target = synth.DEMO_TOOL_OUTPUT.encode()
+    g = ToolCallGrammar(tools, 4)
+    states, points, undecided = [], [], []
+    pos = 0
+    while pos < len(target):
+        allowed = masker.allowed(g, pos)
+        undecided.append(masker.last_undecided)
+        states.append(state_words(masker.program, g))
+        points.append((g.clone(), pos))
+        best = max((t for t in allowed if target.startswith(pieces[t], pos)),
+                   key=lambda t: len(pieces[t]))
+        g.feed(pieces[best])
+        pos += len(pieces[best])
+    width = max(s_.size for s_ in states)
+    host = np.zeros((len(states), width), np.uint32)
+    for i, s_ in enumerate(states):
+        host[i, : s_.size] = s_
+    dev_states = torch.from_numpy(host.view(np.int32)).cuda()
+    words = (len(pieces) + 31) // 32
+    allowed_d = torch.zeros(words, dtype=torch.int32, device="cuda")
+    undecided_d = torch.zeros(words, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def run_all():
+        for i in range(len(states)):
+            hip._check(hip.lib.nd_grammar_mask_d(
+                hip.ctx, masker._grammar, dev_states[i].data_ptr(), masker._pieces,
+                65536 - points[i][1], allowed_d.data_ptr(), undecided_d.data_ptr(),
+                C.c_void_p(stream.cuda_stream)))
+
+    run_all()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        run_all()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    kernel_ms = start.elapsed_time(stop) / (reps * len(states))
+    t0 = time.perf_counter()
+    for gg, p_ in points:
+        masker.allowed(gg, p_)
+    call_ms = (time.perf_counter() - t0) * 1e3 / len(points)
+    part = {"vocab": len(pieces), "states": len(states), "kernel_ms_per_mask": kernel_ms,
+            "host_call_ms_per_mask": call_ms, "mean_undecided": float(np.mean(undecided)),
+            "max_undecided": int(max(undecided))}
+    cpu = None
+    if cpu_seconds > 0:
+        t0, n = time.perf_counter(), 0
+        while n < len(points) and time.perf_counter() - t0 < cpu_seconds:
+            gg, p_ = points[(n * 7) % len(points)]
+            allowed_pieces(gg, pieces, eligible, p_)
+            n += 1
+        cpu_ms = (time.perf_counter() - t0) * 1e3 / max(1, n)
+        cpu = {"value": cpu_ms, "unit": "ms/mask", "cores": 1, "kind": "port",
+               "sample": f"{n} masks of the agent loop (grammar clone fed per piece) at states of "
+                         f"the same output"}
+        part["cpu_ms_per_mask"] = cpu_ms
+        part["speedup_vs_cpu_loop"] = cpu_ms / call_ms
+    masker.free()
+    return part, cpu
+
+
 def bench_attention(torch, hip, length, heads, steps, warmup, rotate=True):
     import ctypes as C
 
@@ -541,7 +622,7 @@ def main():
     ap.add_argument("--skip-needle2", action="store_true")
     ap.add_argument("--needle2-reps", type=int, default=5)
     ap.add_argument("--only", choices=["matvec", "matvec8", "attention", "decode", "prefill",
-                                       "needle2", "traffic", "cq"],
+                                       "needle2", "traffic", "cq", "grammar"],
                     help="run one part alone and print its JSON (for profiling)")
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--no-check", action="store_true",
@@ -573,6 +654,8 @@ def main():
             part, _ = bench_needle2(torch, hip, args.needle2_reps, False, 0)
         elif args.only == "traffic":
             part = traffic_workload(torch, hip, n, k, g)
+        elif args.only == "grammar":
+            part, _ = bench_grammar_mask(torch, hip, 20, 0 if args.skip_cpu else args.cpu_seconds)
         elif args.only == "cq":
             part = {f"cq{bits}_matvec_b1_hbm": bench_cq_matvec(torch, hip, n, k, g, bits, 1,
                                                                  args.steps, args.warmup)
@@ -636,6 +719,14 @@ def main():
         print(f"[bench] needle2 generate b1 {part['tokens_per_s']:.0f} tok/s, decode "
               f"{part['decode_ms_per_token']:.3f} ms/token, greedy_identical="
               f"{part.get('greedy_identical')}", file=sys.stderr, flush=True)
+
+    part, cpu_gm = bench_grammar_mask(torch, hip, 20, 0 if args.skip_cpu else 5.0)
+    if cpu_gm:
+        part["cpu_baseline"] = cpu_gm
+    parts["grammar_mask_v8192"] = part
+    print(f"[bench] grammar mask: kernel {part['kernel_ms_per_mask'] * 1e3:.1f} us/mask, host call "
+          f"{part['host_call_ms_per_mask']:.2f} ms/mask, agent loop "
+          f"{part.get('cpu_ms_per_mask', float('nan')):.1f} ms/mask", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.skip_cpu:

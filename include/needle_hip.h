@@ -462,6 +462,64 @@ nd_status nd_needle_generate(nd_ctx* ctx, nd_needle* model, const uint32_t* prom
                              uint32_t count, uint32_t max_new, uint32_t sink, uint32_t eos,
                              uint32_t* ids, double* log_probabilities, uint32_t* generated);
 
+/* ------------------------------ (f): schema-constrained token masks */
+
+typedef struct nd_pieces nd_pieces;
+typedef struct nd_grammar nd_grammar;
+
+/* The tokenizer's pieces for mask generation: piece t is bytes[offsets[t],
+ * offsets[t + 1]); eligible[t] = 1 for Normal and Byte pieces
+ * (tools/agent.ts:167-168; TokenPieceType, model/tokenizer.ts:21-27). */
+nd_status nd_pieces_upload(nd_ctx* ctx, const uint32_t* offsets, const uint8_t* bytes,
+                           const uint8_t* eligible, uint32_t vocab, nd_pieces** out);
+nd_status nd_pieces_free(nd_ctx* ctx, nd_pieces* pieces);
+
+/* A tool-call grammar program (ToolCallGrammar over its tools' JSON Schemas,
+ * tools/grammar.ts:256-797) compiled by the host, as 32-bit words:
+ *   header [16]: magic 0x4E444752; (count, word offset) of nodes [12 words
+ *     each], values [4], alternatives [1], properties [4], candidates [4],
+ *     tools [4]; byte offset and length of the byte pool.
+ *   node: possible-type bits (string 1, number 2, integer 4, boolean 8,
+ *     null 16, array 32, object 64); check flags (1 string constraints,
+ *     2 numeric constraints, 4 integer only, 8 enum/const/uniqueItems on an
+ *     array or object); minItems; maxItems; items value; property count
+ *     (<= 32); first property; required mask; minProperties; maxProperties.
+ *   value (a value frame's schema): kind 0 = alternatives (first, count:
+ *     node indices in oneOf/anyOf order), 1 = choice (first, count <= 32
+ *     candidates: every alternative is const/enum), 2 = too many candidates.
+ *   property: name (byte offset, length), value index.
+ *   candidate: JSON text (byte offset, length), value kind (0 string,
+ *     1 number, 2 boolean, 3 null, 4 array, 5 object).
+ *   tool: name (byte offset, length), the parameters' value index.
+ * Every index is checked at upload (INVALID_CACT when one points outside). */
+nd_status nd_grammar_upload(nd_ctx* ctx, const uint32_t* program, uint32_t n_words,
+                            nd_grammar** out);
+nd_status nd_grammar_free(nd_ctx* ctx, nd_grammar* grammar);
+
+/* The allowed-token mask of one grammar state: bit t of allowed[t / 32] is
+ * set when piece t is eligible, at most `budget` bytes long (65536 minus
+ * the output so far, agent.ts:169) and accepted by the grammar from
+ * `state`; bit t of undecided[t / 32] instead when the answer needs a check
+ * the device does not make (strings under length/pattern/format/enum/const,
+ * numbers under numeric constraints or with an exponent, arrays/objects
+ * under enum/const/uniqueItems) -- the host grammar settles those pieces.
+ * state: [16] tool-call phase (0 array-open .. 8 done), literal offset,
+ * live tool-name mask, name offset, current tool, used-tool mask, calls,
+ * maximum calls, tools, arguments present, arguments complete, the
+ * completed value's kind, frame depth (<= 24), 3 reserved; then 4 words per
+ * JSON frame, bottom first: kind | phase << 8 | flags << 16 (kinds 1 value,
+ * 2 string, 3 number, 4 literal, 5 choice, 6 array, 7 object, 8 key), a
+ * value or node index (literal: 0 true, 1 false, 2 null), a live/used mask,
+ * and an offset, count or current key.  Indices in the state are checked
+ * by the kernel.  The host-pointer form copies state in and both masks
+ * (ceil(vocab / 32) words each) out. */
+nd_status nd_grammar_mask(nd_ctx* ctx, const nd_grammar* grammar, const uint32_t* state,
+                          uint32_t n_state_words, const nd_pieces* pieces, uint32_t budget,
+                          uint32_t* allowed, uint32_t* undecided);
+nd_status nd_grammar_mask_d(nd_ctx* ctx, const nd_grammar* grammar, const uint32_t* state_dev,
+                            const nd_pieces* pieces, uint32_t budget, uint32_t* allowed_dev,
+                            uint32_t* undecided_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -119,6 +119,14 @@ nd_status nd_destroy(nd_ctx* ctx) {
     hipFree(kv->k);
     delete kv;
   }
+  for (nd_pieces* pc : ctx->pieces) {
+    hipFree(pc->offsets);
+    delete pc;
+  }
+  for (nd_grammar* g : ctx->grammars) {
+    hipFree(g->words);
+    delete g;
+  }
   if (ctx->stage) hipFree(ctx->stage);
   if (ctx->attn_partials) hipFree(ctx->attn_partials);
   if (ctx->attn_counters) hipFree(ctx->attn_counters);

@@ -57,7 +57,31 @@ struct nd_ctx {
   size_t mm_scratch_bytes = 0;
   std::set<nd_mat*> mats;
   std::set<nd_kv*> kvs;
+  std::set<nd_pieces*> pieces;
+  std::set<nd_grammar*> grammars;
 };
+
+// Token pieces in HBM: byte offsets [vocab + 1], bytes, eligibility [vocab].
+struct nd_pieces {
+  uint32_t* offsets = nullptr;
+  uint8_t* bytes = nullptr;
+  uint8_t* eligible = nullptr;
+  uint32_t vocab = 0;
+};
+
+// A compiled tool-call grammar program in HBM (layout in include/needle_hip.h):
+// word offsets of nodes, values, alternatives, properties, candidates and
+// tools, the byte offset of the name/candidate bytes, and the table sizes
+// the kernel checks state indices against.
+struct nd_grammar {
+  uint32_t* words = nullptr;
+  uint32_t off[6] = {};
+  uint32_t bytes_off = 0;
+  uint32_t n_nodes = 0, n_values = 0, n_tools = 0;
+};
+hipError_t nd_launch_grammar_mask(const nd_grammar* g, const uint32_t* state, const nd_pieces* pc,
+                                  uint32_t budget, uint32_t* allowed, uint32_t* undecided,
+                                  hipStream_t s);
 
 // Error helpers: record a message on the context and return a status.
 nd_status nd_fail(nd_ctx* ctx, nd_status code, const char* fmt, ...);

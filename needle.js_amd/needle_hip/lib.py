@@ -109,6 +109,12 @@ SIGNATURES = {
     "nd_needle_prefill": (I32, [P, P, P, U32, P]),
     "nd_needle_step_select": (I32, [P, P, U32, P, U32, P, P]),
     "nd_needle_generate": (I32, [P, P, P, U32, U32, U32, U32, P, P, P]),
+    "nd_pieces_upload": (I32, [P, P, P, P, U32, PP]),
+    "nd_pieces_free": (I32, [P, P]),
+    "nd_grammar_upload": (I32, [P, P, U32, PP]),
+    "nd_grammar_free": (I32, [P, P]),
+    "nd_grammar_mask": (I32, [P, P, P, U32, P, U32, P, P]),
+    "nd_grammar_mask_d": (I32, [P, P, P, P, U32, P, P, P]),
 }
 
 

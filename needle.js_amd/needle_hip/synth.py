@@ -156,3 +156,154 @@ def cq_matrix(run_seed: int, name: str, n: int, k: int, g: int, bits: int,
     packed = pack_codes(codes.reshape(n, kpad), bits)
     norms = s.uniform((n, kpad // g), norm_lo, norm_hi).astype(np.float16).view(np.uint16)
     return packed, norms
+
+
+def tool_pieces(run_seed: int, vocab: int, tools) -> tuple:
+    """A synthetic tokenizer vocabulary for tool-call decoding: (pieces,
+    eligible).  Ids 0-255 are the byte pieces; a few control pieces (not
+    eligible) and one empty piece follow; then JSON punctuation runs, the
+    literals and their halves, number fragments, the tools' names, property
+    names and enum texts (whole, split, quoted), escapes, UTF-8 characters
+    and broken sequences, and seeded words and byte strings up to `vocab`
+    pieces, no two alike."""
+    import json as _json
+
+    s = Stream(run_seed, "tool-pieces")
+    pieces = [bytes([b]) for b in range(256)]
+    eligible = [True] * 256
+    for ctl in (b"<s>", b"</s>", b"<|im_end|>", b"<unk>"):
+        pieces.append(ctl)
+        eligible.append(False)
+    pieces.append(b"")
+    eligible.append(True)
+    seen = set(pieces)
+
+    def add(p: bytes):
+        if p and p not in seen and len(pieces) < vocab:
+            seen.add(p)
+            pieces.append(p)
+            eligible.append(True)
+
+    punct = ['{"', '":"', '","', '"}', '"},', '}]', '},{"', '":', ':', ',"', '[{"name":"',
+             '","arguments":{', '"}}', '}}', '}}]', ']', '[', '[]', '{}', '"]', '"],"', '":[',
+             '":{', '":["', '":true', '":false', '":null', ',', '"', '],', '}', '{', '"]}',
+             '","arguments":', '"arguments":', '[{"', '{"name":"', '"name":"', ',"arguments":{}',
+             '":{}', '":[]', '":0', '":1', '":-', ']}', ']}]', '"}]', '"}}]']
+    for p in punct:
+        add(p.encode())
+    for lit in ("true", "false", "null"):
+        for i in range(1, len(lit) + 1):
+            add(lit[:i].encode())
+            add(lit[i:].encode())
+    for p in ["0", "1", "12", "123", "-", "-1", "-0", ".", ".5", "0.", "1.", "e", "E", "e5", "E-3",
+              "e+", "1e", "1e5", "2.5", "-2.5", "10", "100", "1000", "3,", "7}", "42]", "0.0",
+              "9e999", "1.e5", "00", "-.", "5e-1", "1E+2"]:
+        add(p.encode())
+    names = set()
+
+    def walk(schema):
+        if not isinstance(schema, dict):
+            return
+        for k, v in schema.get("properties", {}).items():
+            names.add(k)
+            walk(v)
+        for key in ("items", "additionalProperties"):
+            walk(schema.get(key))
+        for key in ("oneOf", "anyOf"):
+            for v in schema.get(key, []):
+                walk(v)
+        for key in ("$defs", "definitions"):
+            for v in schema.get(key, {}).values():
+                walk(v)
+        for v in schema.get("enum", []) + ([schema["const"]] if "const" in schema else []):
+            names.add(_json.dumps(v, separators=(",", ":")))
+
+    for t in tools:
+        names.add(t["name"])
+        walk(t["parameters"])
+    for n in sorted(names):
+        for p in (n, '"' + n, n + '"', '"' + n + '"', '"' + n + '":', n[: len(n) // 2],
+                  n[len(n) // 2:], n[:1], n[1:]):
+            add(p.encode())
+    for p in ["\\n", '\\"', "\\u", "\\u00", "\\u00e9", "\\", "\\x", "\\\\", "\\t", "\\ud83d",
+              "é", "中", "😀", "é\"", "naïve", "\\u00E9\""]:
+        add(p.encode())
+    for p in [b"\xc3", b"\xa9", b"\xe4\xb8", b"\xad", b"\xff", b"\xed\xa0\x80", b"\xf4\x90\x80\x80",
+              b"\xe0\x80\xaf", b"\xc0\xaf", b"\xf0\x9f", b"\x98\x80"]:
+        add(p)
+    letters = b"abcdefghijklmnopqrstuvwxyz"
+    alphabet = b'abcdefghijklmnopqrstuvwxyz0123456789 "{}[]:,.-_eE\\'
+    while len(pieces) < vocab:
+        n = int(s.integers(1, 1, 8)[0])
+        if s.uniform01(1)[0] < 0.6:
+            word = bytes(letters[i] for i in s.integers(n, 0, len(letters) - 1))
+            add((b" " if s.uniform01(1)[0] < 0.3 else b"") + word)
+        else:
+            add(bytes(alphabet[i] for i in s.integers(n, 0, len(alphabet) - 1)))
+    return pieces, eligible
+
+
+# The reference's grammar test schema (tests/grammar.test.ts:7-21).
+DEMO_PARAMETERS = {
+    "type": "object",
+    "properties": {
+        "enabled": {"type": "boolean"},
+        "level": {"type": "integer", "minimum": 0, "maximum": 10},
+        "mode": {"type": "string", "enum": ["eco", "boost"]},
+        "tags": {"type": "array", "items": {"type": "string", "minLength": 1}, "minItems": 1,
+                 "maxItems": 3},
+        "location": {"type": "object", "properties": {"lat": {"type": "number"},
+                                                      "lon": {"type": "number"}},
+                     "required": ["lat", "lon"]},
+    },
+    "required": ["enabled", "level", "mode", "tags"],
+}
+
+# A schema that uses every grammar feature: oneOf/anyOf, const, enums of
+# mixed types, $ref, nested arrays and objects, integer and number, bounds,
+# pattern, format, uniqueItems and type unions.
+DEMO_RICH = {
+    "type": "object",
+    "$defs": {"point": {"type": "object", "properties": {"x": {"type": "number"},
+                                                         "y": {"type": "integer"}},
+                        "required": ["x"]}},
+    "properties": {
+        "kind": {"oneOf": [{"const": "circle"}, {"const": "square"}]},
+        "count": {"type": "integer"},
+        "ratio": {"type": "number"},
+        "bounded": {"type": "integer", "minimum": 1, "maximum": 5},
+        "points": {"type": "array", "items": {"$ref": "#/$defs/point"}, "maxItems": 4},
+        "label": {"type": "string", "pattern": "^[a-z]+$"},
+        "note": {"type": "string"},
+        "flag": {"type": ["boolean", "null"]},
+        "mixed": {"enum": ["a", 1, True, None]},
+        "alt": {"anyOf": [{"type": "string"}, {"type": "number"},
+                          {"type": "array", "items": {"type": "integer"}}]},
+        "uniq": {"type": "array", "items": {"type": "string"}, "uniqueItems": True},
+        "nested": {"type": "object", "properties": {"deep": {"type": "object", "properties": {
+            "deeper": {"type": "array", "items": {"type": "array",
+                                                  "items": {"type": "boolean"}}}}}}},
+        "email": {"type": "string", "format": "email"},
+    },
+    "required": ["kind"],
+}
+
+DEMO_TOOL_OUTPUT = (
+    '[{"name":"get_weather","arguments":{"kind":"circle","count":-12,"ratio":2.5e3,'
+    '"bounded":3,"points":[{"x":1.5,"y":2},{"x":-0.0}],"label":"abc",'
+    '"note":"h\\u00e9llo \\"q\\" \u4e2d","flag":null,"mixed":true,"alt":[1,2],'
+    '"uniq":["a","b"],"nested":{"deep":{"deeper":[[true,false],[]]}},"email":"a@b.co"}},'
+    '{"name":"get_time","arguments":{"tz":"CET"}}]')
+
+
+def demo_tools():
+    """Three tools with shared name prefixes: get, get_weather (the rich
+    schema) and get_time."""
+    from .grammar import normalize_tools
+
+    return normalize_tools([
+        {"name": "get", "parameters": {"type": "object", "properties": {"q": {"type": "string"}}}},
+        {"name": "get_weather", "parameters": DEMO_RICH},
+        {"name": "get_time", "parameters": {"type": "object", "properties": {
+            "tz": {"enum": ["UTC", "CET"]}}, "required": ["tz"]}},
+    ])
