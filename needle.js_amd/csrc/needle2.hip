@@ -360,7 +360,11 @@ __device__ __forceinline__ float butterfly(float mine, float other, uint32_t t, 
 
 // Walsh-Hadamard transform of hv[0, H) (H <= kMixWg a power of two), one
 // value per thread, strides ascending: DPP within quads, lane shuffles
-// within the wave, LDS across waves.  Every thread calls it; threads >= H
+// within the wave for strides 1..32.  The strides 64, 128, 256 mix values
+// of different waves: after one exchange through LDS, thread t = g + 64 k
+// reads the H / 64 values g + 64 k' of its column and runs those stages on
+// them in registers (the same butterflies, in the same order, with the same
+// f32 rounding), keeping element k.  Every thread calls it; threads >= H
 // hold zeros.  Returns thread t's transformed value; v is its input.
 __device__ float fwht_block(float v, float* hv, uint32_t H, uint32_t t) {
   v = butterfly(v, nd::dpp<nd::kQuadXor1>(v), t, 1);
@@ -369,13 +373,30 @@ __device__ float fwht_block(float v, float* hv, uint32_t H, uint32_t t) {
   if (H > 8) v = butterfly(v, nd::lane_xor<8>(v), t, 8);
   if (H > 16) v = butterfly(v, nd::lane_xor<16>(v), t, 16);
   if (H > 32) v = butterfly(v, nd::lane_xor<32>(v), t, 32);
-  for (uint32_t s = 64; s < H; s <<= 1) {
-    __syncthreads();
-    hv[t] = v;
-    __syncthreads();
-    v = butterfly(v, hv[t ^ s], t, s);
+  if (H <= 64) return v;
+  __syncthreads();  // every read of the previous exchange is done
+  hv[t] = v;
+  __syncthreads();
+  const uint32_t G = H / 64, g = t & 63, k = t >> 6;  // G <= kMixWg / 64 = 8
+  float c[kMixWg / 64];
+#pragma unroll
+  for (uint32_t i = 0; i < kMixWg / 64; ++i) c[i] = i < G ? hv[g + 64 * i] : 0.f;
+#pragma unroll
+  for (uint32_t st = 1; st < kMixWg / 64; st <<= 1) {
+    if (st < G) {
+#pragma unroll
+      for (uint32_t i = 0; i < kMixWg / 64; ++i)
+        if (!(i & st)) {
+          const double a = c[i], b = c[i + st];
+          c[i] = (float)(a + b);
+          c[i + st] = (float)(a - b);
+        }
+    }
   }
-  return v;
+  float out = c[0];
+#pragma unroll
+  for (uint32_t i = 1; i < kMixWg / 64; ++i) out = k == i ? c[i] : out;
+  return out;
 }
 
 // The one-workgroup part between two layers: post(l - 1), then pre(l) (or

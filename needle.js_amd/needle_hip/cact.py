@@ -8,16 +8,21 @@ matrices stay views of the archive bytes, as the reference keeps them
 (cact.ts:183-186); HipBackend uploads a CqMatrix to HBM on first use and
 multiplies it there without expanding it.
 
-`write_cact` builds an archive from tensors: the inverse of `parse_cact`,
-for synthetic models and round-trip tests (there is no writer in the
-reference; the layout is the parser's).
+`parse_cact_weights` continues as parseCact does (cact.ts:398-562): the
+tensors in archive order become the named Needle 2 weights (embedding,
+layers, mHC, engram sites, final norm, probe heads, tokenizer blob) with
+the reference's kind, shape and manifest checks.  `write_cact` builds an
+archive from tensors: the inverse of `parse_cact`, for synthetic models and
+round-trip tests (there is no writer in the reference; the layout is the
+parser's); `synthetic_needle2_archive` writes one in the Needle 2 order.
 """
 
 from __future__ import annotations
 
+import math
 import struct
 from dataclasses import dataclass, field
-from typing import Optional, Sequence, Union
+from typing import List, Optional, Sequence, Union
 
 import numpy as np
 
@@ -310,3 +315,217 @@ def write_cact(geometry: dict, codebook: np.ndarray, tensors: Sequence[CactTenso
         body += payload
         cursor = start + len(payload)
     return bytes(header_bytes) + codebook.tobytes() + bytes(records) + bytes(body)
+
+
+# ------------------------------------------------------ named Needle 2 weights
+
+@dataclass
+class CactLayer:
+    norm_input: np.ndarray
+    query_projection: CqMatrix
+    key_projection: CqMatrix
+    value_projection: CqMatrix
+    query_norm: np.ndarray
+    key_norm: np.ndarray
+    gate_projection: CqMatrix
+    output_projection: CqMatrix
+    post_attention_norm: np.ndarray
+    attention_gate: float
+    pre_hadamard_norm: np.ndarray
+    hadamard_d1: np.ndarray
+    hadamard_d2: np.ndarray
+    hadamard_d3: np.ndarray
+
+
+@dataclass
+class CactEngramSite:
+    tables: CqMatrix
+    key_projection: CqMatrix
+    value_projection: CqMatrix
+    taps: np.ndarray
+
+
+@dataclass
+class CactProbeHead:
+    """CactProbeHead (cact.ts:105-112)."""
+
+    name: str
+    probes: np.ndarray
+    probe_count: int
+    projection: np.ndarray
+    output_size: int
+    bias: np.ndarray
+
+
+@dataclass
+class CactWeights:
+    """CactWeights (cact.ts:114-138)."""
+
+    geometry: dict
+    codebook: np.ndarray
+    tensors: list
+    embedding: CqMatrix
+    layers: List[CactLayer]
+    mhc_a_pre: np.ndarray
+    mhc_a_post: np.ndarray
+    mhc_a_residual: np.ndarray
+    mhc_b_pre: np.ndarray
+    mhc_b_post: np.ndarray
+    mhc_b_residual: np.ndarray
+    mhc_phi_pre: CqMatrix
+    mhc_phi_post: CqMatrix
+    mhc_phi_residual: CqMatrix
+    engrams: List[CactEngramSite]
+    final_norm: np.ndarray
+    heads: dict
+    tokenizer_blob: np.ndarray
+
+
+def parse_cact_weights(source) -> CactWeights:
+    """parseCact to the end (cact.ts:398-562)."""
+    archive = parse_cact(source)
+    geometry, tensors = archive.geometry, archive.tensors
+    cursor = 0
+
+    def take(name):
+        nonlocal cursor
+        invariant(cursor < len(tensors), "INVALID_CACT", f"Archive ended before {name}")
+        t = tensors[cursor]
+        cursor += 1
+        return t
+
+    def cq(t, name) -> CqMatrix:
+        invariant(t.kind == "cq", "INVALID_CACT", f"{name} must be a Cactus-Quant matrix")
+        return t
+
+    def dense(t, name) -> np.ndarray:
+        invariant(t.kind == "dense", "INVALID_CACT", f"{name} must be a dense tensor")
+        return t.data
+
+    embedding = cq(take("embedding"), "embedding")
+    invariant(embedding.output_size == geometry["vocabulary_size"]
+              and embedding.input_size == geometry["model_dimension"], "INVALID_CACT",
+              "Embedding shape does not match model geometry")
+    layers = []
+    for layer in range(geometry["number_of_layers"]):
+        pre = f"layer {layer}"
+        norm_input = dense(take(f"{pre} input norm"), f"{pre} input norm")
+        q = cq(take(f"{pre} query projection"), f"{pre} query projection")
+        k = cq(take(f"{pre} key projection"), f"{pre} key projection")
+        v = cq(take(f"{pre} value projection"), f"{pre} value projection")
+        qn = dense(take(f"{pre} query norm"), f"{pre} query norm")
+        kn = dense(take(f"{pre} key norm"), f"{pre} key norm")
+        gate = cq(take(f"{pre} gate projection"), f"{pre} gate projection")
+        out = cq(take(f"{pre} output projection"), f"{pre} output projection")
+        post = dense(take(f"{pre} post-attention norm"), f"{pre} post-attention norm")
+        ag = dense(take(f"{pre} attention gate"), f"{pre} attention gate")
+        preh = dense(take(f"{pre} pre-Hadamard norm"), f"{pre} pre-Hadamard norm")
+        d1 = dense(take(f"{pre} Hadamard d1"), f"{pre} Hadamard d1")
+        d2 = dense(take(f"{pre} Hadamard d2"), f"{pre} Hadamard d2")
+        d3 = dense(take(f"{pre} Hadamard d3"), f"{pre} Hadamard d3")
+        layers.append(CactLayer(norm_input, q, k, v, qn, kn, gate, out, post,
+                                float(ag[0]) if ag.size else 0.0, preh, d1, d2, d3))
+    mhc = [dense(take(f"mHC {n}"), f"mHC {n}")
+           for n in ("a_pre", "a_post", "a_res", "b_pre", "b_post", "b_res")]
+    phi = [cq(take(f"mHC {n}"), f"mHC {n}") for n in ("phi_pre", "phi_post", "phi_res")]
+    engrams = []
+    for site in range(len(geometry["engram_layers"])):
+        engrams.append(CactEngramSite(
+            cq(take(f"engram {site} tables"), f"engram {site} tables"),
+            cq(take(f"engram {site} key projection"), f"engram {site} key projection"),
+            cq(take(f"engram {site} value projection"), f"engram {site} value projection"),
+            dense(take(f"engram {site} taps"), f"engram {site} taps")))
+    final_norm = dense(take("final norm"), "final norm")
+    heads = {}
+    if cursor < len(tensors) and tensors[cursor].kind == "dense":
+        manifest = tensors[cursor].data
+        cursor += 1
+        for raw in manifest:
+            code = math.floor(float(raw) + 0.5)  # Math.round
+            name = "contrastive" if code == 1 else "confidence" if code == 2 else None
+            invariant(name is not None, "UNSUPPORTED_CACT", f"Unknown probe-head manifest code {code}")
+            pt, jt, bt = take(f"{name} probes"), take(f"{name} projection"), take(f"{name} bias")
+            probes, proj, bias = (dense(pt, f"{name} probes"), dense(jt, f"{name} projection"),
+                                  dense(bt, f"{name} bias"))
+            count = pt.shape[0] if pt.shape else 0
+            out = jt.shape[0] if jt.shape else bias.size
+            d = geometry["model_dimension"]
+            invariant(count > 0 and probes.size == count * d, "INVALID_CACT",
+                      f"{name} probe shape is inconsistent")
+            invariant(proj.size == out * count * d, "INVALID_CACT",
+                      f"{name} projection shape is inconsistent")
+            heads[name] = CactProbeHead(name, probes.reshape(count, d), count,
+                                        proj.reshape(out, count * d), out, bias)
+    blob = None
+    while cursor < len(tensors):
+        t = take("trailing tensor")
+        if t.kind == "raw":
+            invariant(blob is None, "INVALID_CACT", "Archive contains more than one RAW tokenizer tensor")
+            blob = t.data
+        else:
+            raise NeedleError("UNSUPPORTED_CACT", f"Unexpected trailing tensor {t.record.index}")
+    invariant(blob is not None, "INVALID_CACT", "Archive does not contain its RAW SentencePiece tokenizer")
+    return CactWeights(geometry, archive.codebook, tensors, embedding, layers, *mhc, *phi, engrams,
+                       final_norm, heads, blob)
+
+
+def synthetic_needle2_archive(geometry: dict, run_seed: int = 2026, bits: int = 4,
+                              group: int = 32, confidence: bool = True) -> bytes:
+    """A .cact archive in the Needle 2 tensor order (cact.ts:410-540) with
+    seeded Cactus-Quant matrices of one width, dense vectors near neutral,
+    an optional confidence head and a placeholder tokenizer blob."""
+    from . import synth
+
+    g = geometry
+    d, hd, L = g["model_dimension"], g["head_dimension"], g["number_of_layers"]
+    H, Hkv, ln = g["number_of_heads"], g["number_of_kv_heads"], g["mhc_lanes"]
+    codebook = synth.cq_codebook()
+    books = {b: codebook[lo:hi] for b, (lo, hi) in CODEBOOK_SLICES.items()}
+    tensors: list = []
+    count = [0]
+
+    def cqm(n, k):
+        count[0] += 1
+        packed, norms = synth.cq_matrix(run_seed, f"arch{count[0]}", n, k, group, bits)
+        tensors.append(CqMatrix(packed, norms, books, n, k, group, bits))
+
+    def vec(shape, lo, hi):
+        count[0] += 1
+        data = synth.Stream(run_seed, f"arch{count[0]}").uniform(shape, lo, hi).reshape(-1)
+        tensors.append(DenseTensor(tuple(shape), data.astype(np.float32)))
+
+    cqm(g["vocabulary_size"], d)
+    for _ in range(L):
+        vec((d,), -0.1, 0.1)
+        cqm(H * hd, d)
+        cqm(Hkv * hd, d)
+        cqm(Hkv * hd, d)
+        vec((hd,), -0.1, 0.1)
+        vec((hd,), -0.1, 0.1)
+        cqm(H * hd, d)
+        cqm(d, H * hd)
+        vec((d,), -0.1, 0.1)
+        vec((1,), -1.0, 1.0)
+        vec((d,), -0.1, 0.1)
+        vec((d,), 0.5, 1.5)
+        vec((g["hadamard_dimension"],), 0.5, 1.5)
+        vec((d,), 0.5, 1.5)
+    for shape in ((L,), (L,), (L,), (L * ln,), (L * ln,), (L * ln * ln,)):
+        vec(shape, 0.02, 0.1)
+    cqm(L * ln, ln * d)
+    cqm(L * ln, ln * d)
+    cqm(L * ln * ln, ln * d)
+    cat = g["number_of_engram_tables"] * g["engram_sub_dimension"]
+    for _ in g.get("engram_layers", []):
+        cqm(g["number_of_engram_tables"] * g["engram_slots"], g["engram_sub_dimension"])
+        cqm(d, cat)
+        cqm(d, cat)
+        vec((g["engram_convolution_taps"], d), -0.5, 0.5)
+    vec((d,), -0.1, 0.1)
+    if confidence:
+        tensors.append(DenseTensor((1,), np.array([2.0], np.float32)))
+        vec((8, d), -0.1, 0.1)
+        vec((1, 8 * d), -0.003, 0.003)
+        vec((1,), -0.2, 0.2)
+    tensors.append(RawTensor((16,), np.frombuffer(b"synthetic-sp-mdl", np.uint8)))
+    return write_cact(geometry, codebook, tensors)

@@ -1,8 +1,10 @@
 """.cact archive parsing and writing (host logic, CPU only).
 
 The first three cases are the reference's parser tests (tests/cact.test.ts:
-5-21); the rest check that every tensor kind survives write -> parse and
-that the parser's length and kind checks raise the reference's codes.
+5-21); the rest check that every tensor kind survives write -> parse, that
+the parser's length and kind checks raise the reference's codes, and that
+a Needle 2 archive parses into its named weights (cact.ts:398-562) with the
+reference's structure checks.
 """
 
 import struct
@@ -12,6 +14,7 @@ import pytest
 
 from needle_hip import CqMatrix, NeedleError, parse_cact, synth, write_cact
 from needle_hip import cact as K
+from needle_hip.cact import parse_cact_weights, synthetic_needle2_archive
 
 
 def test_rejects_truncated_header():
@@ -122,3 +125,63 @@ def test_rejects_out_of_range_blob_and_heads():
     bad = dict(GEOMETRY, number_of_heads=3, number_of_kv_heads=2)
     with pytest.raises(NeedleError, match="positive multiple of KV heads"):
         parse_cact(write_cact(bad, codebook, tensors[:1]))
+
+
+# ------------------------------------------------------ named Needle 2 weights
+
+N2_GEOMETRY = dict(kv_window=8, kv_bits=8, vocabulary_size=256, model_dimension=128,
+                   number_of_heads=4, number_of_kv_heads=2, number_of_layers=2, head_dimension=64,
+                   maximum_sequence_length=64, hadamard_dimension=128, mhc_lanes=4,
+                   engram_slots=64, engram_sub_dimension=32, number_of_engram_tables=4,
+                   engram_convolution_taps=4, engram_convolution_dilation=1,
+                   engram_orders=[2, 3], engram_layers=[0, 1], rope_theta=10000.0)
+
+
+def test_needle2_archive_named_structure():
+    w = parse_cact_weights(synthetic_needle2_archive(N2_GEOMETRY, 3))
+    g = N2_GEOMETRY
+    assert w.embedding.shape == (256, 128) and len(w.layers) == 2
+    layer = w.layers[1]
+    assert layer.query_projection.shape == (256, 128)
+    assert layer.key_projection.shape == (128, 128)
+    assert layer.output_projection.shape == (128, 256)
+    assert layer.query_norm.shape == (64,) and layer.hadamard_d2.shape == (128,)
+    assert isinstance(layer.attention_gate, float)
+    assert w.mhc_phi_residual.shape == (2 * 16, 4 * 128) and w.mhc_b_residual.shape == (32,)
+    assert len(w.engrams) == 2 and w.engrams[0].tables.shape == (4 * 64, 32)
+    assert w.engrams[1].taps.size == 4 * 128
+    head = w.heads["confidence"]
+    assert (head.probe_count, head.output_size) == (8, 1) and head.projection.shape == (1, 1024)
+    assert w.tokenizer_blob.tobytes() == b"synthetic-sp-mdl"
+    assert w.geometry["engram_layers"] == g["engram_layers"]
+
+
+def _rewrite(tensors_edit):
+    archive = K.parse_cact(synthetic_needle2_archive(N2_GEOMETRY, 4))
+    tensors = list(archive.tensors)
+    tensors_edit(tensors)
+    return write_cact(archive.geometry, archive.codebook, tensors)
+
+
+@pytest.mark.parametrize("edit,code,pattern", [
+    (lambda t: t.pop(), "INVALID_CACT", "tokenizer"),
+    (lambda t: t.append(K.RawTensor((1,), np.zeros(1, np.uint8))), "INVALID_CACT",
+     "more than one RAW"),
+    (lambda t: t.insert(len(t) - 1, K.DenseTensor((1,), np.ones(1, np.float32))),
+     "UNSUPPORTED_CACT", "Unexpected trailing tensor"),
+    (lambda t: t.__setitem__(0, t[1]), "INVALID_CACT", "embedding must be a Cactus-Quant"),
+    (lambda t: t.__setitem__(-5, K.DenseTensor((1,), np.array([3.0], np.float32))),
+     "UNSUPPORTED_CACT", "probe-head manifest code 3"),
+])
+def test_needle2_archive_checks(edit, code, pattern):
+    with pytest.raises(NeedleError, match=pattern) as e:
+        parse_cact_weights(_rewrite(edit))
+    assert e.value.code == code
+
+
+def test_needle2_archive_embedding_shape_checked():
+    g = dict(N2_GEOMETRY, vocabulary_size=300)
+    data = bytearray(synthetic_needle2_archive(N2_GEOMETRY, 5))
+    struct.pack_into("<I", data, 5 * 4, g["vocabulary_size"])
+    with pytest.raises(NeedleError, match="Embedding shape"):
+        parse_cact_weights(bytes(data))

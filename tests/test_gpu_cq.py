@@ -183,3 +183,26 @@ def test_cq_rejections(hip):
     with pytest.raises(NeedleError) as e:
         hip.matvec(m, np.zeros(64, np.float32), MatrixRowRange(60, 5))
     assert e.value.code == "INVALID_CACT"
+
+
+def test_needle2_archive_matrices_on_device(hip):
+    # A synthetic archive in the Needle 2 order: its parsed CQ matrices run
+    # on the device as the reference's backends would run them.
+    from needle_hip.cact import parse_cact_weights, synthetic_needle2_archive
+
+    say("needle2 archive matrices")
+    geo = dict(kv_window=8, kv_bits=8, vocabulary_size=256, model_dimension=128,
+               number_of_heads=4, number_of_kv_heads=2, number_of_layers=2, head_dimension=64,
+               maximum_sequence_length=64, hadamard_dimension=128, mhc_lanes=4, engram_slots=64,
+               engram_sub_dimension=32, number_of_engram_tables=4, engram_convolution_taps=4,
+               engram_convolution_dilation=1, engram_orders=[2, 3], engram_layers=[0, 1],
+               rope_theta=10000.0)
+    for bits in (3, 5):
+        w = parse_cact_weights(synthetic_needle2_archive(geo, 9, bits=bits, group=64))
+        x = np.random.default_rng(bits).standard_normal(128).astype(np.float32)
+        for m in (w.layers[0].query_projection, w.layers[1].key_projection, w.mhc_phi_pre,
+                  w.engrams[0].key_projection):
+            xx = np.resize(x, m.input_size).astype(np.float32)
+            assert_close(hip.matvec(m, xx), ref_matvec(m, xx), RTOL, ATOL, f"archive b{bits}")
+        for tok in (0, 255):
+            assert np.array_equal(hip.row(w.embedding, tok), ref_row(w.embedding, tok))
