@@ -188,7 +188,6 @@ __global__ __launch_bounds__(kCqThreads) void cq_matvec_kernel(
   constexpr int kLB = kPB * kE;                // bits per lookup index
   constexpr int kEntries = 1 << kLB;
   constexpr int kLookups = 32 / kE;            // per unit
-  constexpr int kPerGroup = kGs / kE;          // lookups per group
   __shared__ __align__(16) float tab[kEntries * kE];
   __shared__ float red[RACC * kCqThreads];
   const uint32_t t = threadIdx.x;

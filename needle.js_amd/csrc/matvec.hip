@@ -145,8 +145,8 @@ __global__ __launch_bounds__(kThreads) void matvec_i8_kernel(
 }
 
 // Batched form on MFMA (up to 8 rows per launch, g % 32 == 0): fp16 operands with
-// the fp32 inputs split exactly enough.  mv_split_kernel writes, per batch
-// row b with e_b = the exponent of max_k |x[b][k]| (max < 2^e_b),
+// the fp32 inputs split exactly enough.  Each workgroup writes into LDS, per
+// batch row b with e_b = the exponent of max_k |x[b][k]| (max < 2^e_b),
 //   x[b][k] * 2^-e_b = hi + lo,  hi = f16(x * 2^-e_b),  lo = f16(x * 2^-e_b - hi),
 // which leaves at most 2^-24 of the row's largest element unrepresented
 // (fp32's own rounding step).  Weights are int8, exact in fp16, and fp16 x
@@ -160,9 +160,15 @@ __global__ __launch_bounds__(kThreads) void matvec_i8_kernel(
 // + [0, 4) of column l % 16 -- so each lane's four outputs belong to one
 // weight row and take one group scale.  Lane block kb = l / 16 holds the
 // group's k in [8 kOrder[kb], +8), kOrder = {0, 2, 1, 3}: the order in which
-// one 16-byte weight load per lane plus a lane-half swap delivers two groups
-// (see matvec_mfma_kernel).  The split rows are stored in operand order:
-// xs[group][lane] = 8 halves.
+// one 16-byte weight load per lane plus a lane-half swap delivers two groups:
+// for a pair of 32-wide groups (2p, 2p + 1), lanes 0..31 (blocks 0, 1) load
+// bytes [16 kb, +16) of group 2p and lanes 32..63 the same of group 2p + 1 --
+// 64 contiguous bytes per row -- and v_permlane32_swap of (d0, d2) and of
+// (d1, d3) gives every lane eight codes of group 2p (k blocks kOrder) and
+// eight of group 2p + 1.  The split rows are stored in operand order:
+// xs[group][lane] = 8 halves.  Weight loads are issued together and
+// unconditionally (addresses clamped, contributions weighted by zero), so
+// each MFMA waits only for its operands.
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
@@ -174,66 +180,6 @@ constexpr uint32_t kMfmaMinBatch = 3;
 
 // Lane block holding k block j of a group (kOrder is its own inverse).
 __device__ __forceinline__ uint32_t k_block_lanes(uint32_t j) { return j == 1 ? 2 : j == 2 ? 1 : j; }
-
-__global__ __launch_bounds__(256) void mv_split_kernel(const float* __restrict__ X,
-                                                       uint32_t x_stride, uint32_t bc, uint32_t K,
-                                                       uint4* __restrict__ xs,
-                                                       float* __restrict__ xf) {
-  const uint32_t b = blockIdx.x, t = threadIdx.x;
-  const uint32_t units = K / 8;  // unit u: k in [8u, 8u + 8) = group u / 4, k block u % 4
-  if (b >= bc) {  // rows past the batch multiply as zeros
-    for (uint32_t u = t; u < units; u += 256) {
-      const size_t e = (size_t)(u >> 2) * 64 + k_block_lanes(u & 3) * 16 + b;
-      xs[e] = make_uint4(0, 0, 0, 0);
-      xs[e + 8] = make_uint4(0, 0, 0, 0);
-    }
-    return;
-  }
-  const float4* x = reinterpret_cast<const float4*>(X + (size_t)b * x_stride);
-  float v[4][8];  // K <= 8192: at most 4 units per thread
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t u = t + 256 * i;
-    const uint32_t uu = u < units ? u : 0;
-    const float4 a = x[2 * uu], c = x[2 * uu + 1];
-    v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
-    v[i][4] = c.x; v[i][5] = c.y; v[i][6] = c.z; v[i][7] = c.w;
-    if (u < units)
-#pragma unroll
-      for (int q = 0; q < 8; ++q) amax = fmaxf(amax, fabsf(v[i][q]));
-  }
-  __shared__ float red[4];
-  amax = fmaxf(amax, nd::lane_xor<1>(amax));
-  amax = fmaxf(amax, nd::lane_xor<2>(amax));
-  amax = fmaxf(amax, nd::lane_xor<4>(amax));
-  amax = fmaxf(amax, nd::lane_xor<8>(amax));
-  amax = fmaxf(amax, nd::lane_xor<16>(amax));
-  amax = fmaxf(amax, nd::lane_xor<32>(amax));
-  if ((t & 63) == 0) red[t >> 6] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  int e = 0;
-  if (amax > 0.f && amax <= 3.4028235e38f) frexpf(amax, &e);  // amax < 2^e
-  const float down = ldexpf(1.f, -e);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t u = t + 256 * i;
-    if (u >= units) continue;
-    half8 hi, lo;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const float xv = v[i][q] * down;
-      const _Float16 h = (_Float16)xv;
-      hi[q] = h;
-      lo[q] = (_Float16)(xv - (float)h);
-    }
-    const size_t at = (size_t)(u >> 2) * 64 + k_block_lanes(u & 3) * 16 + b;
-    xs[at] = __builtin_bit_cast(uint4, hi);
-    xs[at + 8] = __builtin_bit_cast(uint4, lo);
-  }
-  if (t == 0) xf[b] = ldexpf(1.f, e);
-}
 
 // Eight int8 codes -> eight exact fp16 values: 0x6500 | (c ^ 0x80) is the
 // fp16 number 1408 + c, and one packed subtraction per pair removes 1408.
@@ -250,85 +196,95 @@ __device__ __forceinline__ half8 codes_to_half(u32x2 w) {
 
 constexpr uint32_t kMfmaWaves = 16;
 
-// Cross-wave sum of the MFMA accumulators and the store: every wave leaves
-// its four components in red ([wave][component][lane], 16 KB of LDS), then
-// wave c < 4 sums component c over the waves, adds the lo row to the hi row
-// (lanes l and l + 32) and scales by 2^e_b of its row b = 4 (l / 16) + c.
-// With RT row tiles per workgroup, tile r uses red + 4096 r and rows
-// row0 + 16 r.
-template <int RT>
-__device__ __forceinline__ void mfma_reduce_store(const float4v (&acc)[RT], float* red,
-                                                  uint32_t wave, uint32_t lane, uint32_t row0,
-                                                  uint32_t row_count, uint32_t bc, float fb,
+// Cross-wave sum of the MFMA accumulators (already scaled by their split
+// exponents) and the store: every wave leaves its four components in red
+// ([wave][component][lane], 16 KB of LDS), then wave c < 4 sums component c
+// over the waves and adds the lo row to the hi row (lanes l and l + 32) for
+// batch row b = 4 (l / 16) + c.
+__device__ __forceinline__ void mfma_reduce_store(float4v acc, float* red, uint32_t wave,
+                                                  uint32_t lane, uint32_t row0,
+                                                  uint32_t row_count, uint32_t bc,
                                                   float* __restrict__ Y, uint32_t y_stride) {
 #pragma unroll
-  for (int r = 0; r < RT; ++r)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) red[r * 4096 + (wave * 4 + c) * 64 + lane] = acc[r][c];
+  for (int c = 0; c < 4; ++c) red[(wave * 4 + c) * 64 + lane] = acc[c];
   __syncthreads();
   if (wave >= 4) return;
+  float sum = 0.f;
 #pragma unroll
-  for (int r = 0; r < RT; ++r) {
-    float sum = 0.f;
-#pragma unroll
-    for (uint32_t w = 0; w < kMfmaWaves; ++w) sum += red[r * 4096 + (w * 4 + wave) * 64 + lane];
-    sum += nd::lane_xor<32>(sum);
-    const uint32_t b = (lane >> 4) * 4 + wave, row = row0 + 16 * r + (lane & 15);
-    if (lane < 32 && row < row_count && b < bc) Y[(size_t)b * y_stride + row] = sum * fb;
-  }
+  for (uint32_t w = 0; w < kMfmaWaves; ++w) sum += red[(w * 4 + wave) * 64 + lane];
+  sum += nd::lane_xor<32>(sum);
+  const uint32_t b = (lane >> 4) * 4 + wave, row = row0 + (lane & 15);
+  if (lane < 32 && row < row_count && b < bc) Y[(size_t)b * y_stride + row] = sum;
 }
 
-// One workgroup of kMfmaWaves waves per 16 weight rows.  The rows' group
-// scales are staged in LDS (coalesced loads).  Wave w takes pairs of 32-wide
-// groups p = w + kMfmaWaves i, NP pairs at a time, each lane loading 16
-// bytes of its row: lanes 0..31 (blocks 0, 1) bytes [16 kb, +16) of group
-// 2p, lanes 32..63 the same of group 2p + 1 -- 64 contiguous bytes per row.
-// v_permlane32_swap of (d0, d2) and of (d1, d3) then gives every lane eight
-// codes of group 2p (k blocks kOrder) and eight of group 2p + 1.  All loads
-// of a step are issued together and unconditionally (addresses clamped,
-// contributions weighted by zero), so each MFMA waits only for its operands.
+// k <= 2048: the split done in the workgroup over all of k.  Every
+// workgroup reads x (an L2 hit after the first), takes each row's largest
+// magnitude, and writes the hi/lo image of x in operand order into LDS (64
+// KB at k = 2048) while its weight loads stream in -- one launch, and the
+// split's VALU work overlaps the wait for HBM.  Wave w takes the pairs p = w
+// + kMfmaWaves i.  Entry e of group g sits
+// at g * 64 + (e ^ (g & 15)): a 16-lane write round (16 groups, see the unit
+// order below) then covers 16 distinct 16-byte slots, and a wave's read of
+// one group stays a permutation within each 256-byte block.
+constexpr uint32_t kFusedMaxK = 2048;
+constexpr int kXUnits = kFusedMaxK / 8 / 128;  // 8-value units of x per thread
 
 template <int NP>
-__global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_kernel(
-    const int8_t* __restrict__ W, const float* __restrict__ S, const uint4* __restrict__ xs,
-    const float* __restrict__ xf, float* __restrict__ Y, uint32_t K, uint32_t groups,
-    uint32_t gshift, uint32_t row_start, uint32_t row_count, uint32_t bc, uint32_t y_stride) {
+__global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_fused_kernel(
+    const int8_t* __restrict__ W, const float* __restrict__ S, const float* __restrict__ X,
+    uint32_t x_stride, float* __restrict__ Y, uint32_t K, uint32_t groups, uint32_t gshift,
+    uint32_t row_start, uint32_t row_count, uint32_t bc, uint32_t y_stride) {
+  __shared__ uint4 s_xs[kFusedMaxK / 32 * 64];
+  __shared__ float s_sc[16 * (kFusedMaxK / 32 + 1)];
+  __shared__ float s_max[kMfmaWaves];
+  __shared__ int s_e[kSplitRows];
   const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const uint32_t r16 = lane & 15, kb = lane >> 4;
   const uint32_t row0 = blockIdx.x * 16;
   const uint32_t row = row0 + r16;
-  const uint32_t rr = row_start + (row < row_count ? row : row_count - 1);
-  const int8_t* wrow = W + (size_t)rr * K + (kb & 1) * 16 + (kb >> 1) * 32;
-  const uint32_t ng = K / 32;  // 32-wide groups
-  const uint32_t npairs = ng / 2;
+  const int8_t* wrow = W + (size_t)(row_start + (row < row_count ? row : row_count - 1)) * K +
+                       (kb & 1) * 16 + (kb >> 1) * 32;
+  const uint32_t ng = K / 32, npairs = ng / 2;
   const uint32_t per_wave = (npairs + kMfmaWaves - 1) / kMfmaWaves;
 
-  // Scales of the 16 rows, [row][group] with a padded row stride.
-  extern __shared__ float s_scale[];
-  const uint32_t sstride = groups + 1;
-  float sreg[4];
+  // x: thread t holds row xb = t / 128 and 8-value units j = q + 128 i, with
+  // q = 64 h + 4 (l % 16) + l / 16 for lane l of half h of the row's threads.
+  const uint32_t xb = t >> 7, upr = K / 8;
+  const uint32_t xj = (t & 64) + (lane & 15) * 4 + (lane >> 4);
+  const float4* xrow = reinterpret_cast<const float4*>(X + (size_t)(xb < bc ? xb : 0) * x_stride);
+  float xv[kXUnits][8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {  // 16 * groups <= 4096 = 4 per thread
-    const uint32_t e = t + 1024 * i;
-    const uint32_t r = e / groups, q = e % groups;
-    const uint32_t srow = row0 + r < row_count ? row0 + r : row_count - 1;
-    sreg[i] = e < 16 * groups ? S[(size_t)(row_start + srow) * groups + q] : 0.f;
+  for (int i = 0; i < kXUnits; ++i) {
+    const uint32_t j = xj + 128 * i;
+    const uint32_t jj = j < upr ? j : 0;
+    const float4 a = xrow[2 * jj], c = xrow[2 * jj + 1];
+    const bool ok = j < upr && xb < bc;  // rows past the batch multiply as zeros
+    xv[i][0] = ok ? a.x : 0.f; xv[i][1] = ok ? a.y : 0.f;
+    xv[i][2] = ok ? a.z : 0.f; xv[i][3] = ok ? a.w : 0.f;
+    xv[i][4] = ok ? c.x : 0.f; xv[i][5] = ok ? c.y : 0.f;
+    xv[i][6] = ok ? c.z : 0.f; xv[i][7] = ok ? c.w : 0.f;
   }
-  // The output factor 2^e_b of the row this lane stores (b <= 7 is always
-  // inside xf).
-  const float fb = xf[(kb & 1) * 4 + (wave & 3)];
+  // Scales of the 16 rows, [row][group] with a padded row stride.
+  const uint32_t sstride = groups + 1;
+  constexpr int kSc = 2;  // 16 * groups <= 2048 here
+  float sreg[kSc];
+#pragma unroll
+  for (int i = 0; i < kSc; ++i) {
+    const uint32_t e = t + 1024 * i;
+    const uint32_t ee = e < 16 * groups ? e : 0;
+    const uint32_t r = ee / groups, q = ee % groups;
+    const uint32_t srow = row0 + r < row_count ? row0 + r : row_count - 1;
+    sreg[i] = S[(size_t)(row_start + srow) * groups + q];
+  }
 
   float4v acc = {0.f, 0.f, 0.f, 0.f};
   u32x4 wv[NP];
-  uint4 xa[NP][2];
   auto load = [&](uint32_t base) {
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
       const uint32_t p = wave + kMfmaWaves * (base + i);
       const uint32_t pc = p < npairs ? p : 0;
       wv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + (size_t)pc * 64));
-      xa[i][0] = xs[(size_t)(2 * pc) * 64 + lane];
-      xa[i][1] = xs[(size_t)(2 * pc + 1) * 64 + lane];
     }
   };
   auto compute = [&](uint32_t base) {
@@ -342,133 +298,13 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_kernel(
       for (int h = 0; h < 2; ++h) {
         const uint32_t g = 2 * pc + h;
         const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            __builtin_bit_cast(half8, xa[i][h]), codes_to_half(u32x2{lo[h], hi[h]}),
-            float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-        const float sv = p < npairs ? s_scale[r16 * sstride + (g >> gshift)] : 0.f;
+            __builtin_bit_cast(half8, s_xs[g * 64 + (lane ^ (g & 15))]),
+            codes_to_half(u32x2{lo[h], hi[h]}), float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        const float sv = p < npairs ? s_sc[r16 * sstride + (g >> gshift)] : 0.f;
         acc[0] = fmaf(sv, d[0], acc[0]);
         acc[1] = fmaf(sv, d[1], acc[1]);
         acc[2] = fmaf(sv, d[2], acc[2]);
         acc[3] = fmaf(sv, d[3], acc[3]);
-      }
-    }
-  };
-  // First step: its loads in flight behind the scale loads, then the scales
-  // to LDS, then the rest.
-  load(0);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t e = t + 1024 * i;
-    if (e < 16 * groups) s_scale[(e / groups) * sstride + e % groups] = sreg[i];
-  }
-  __syncthreads();
-  compute(0);
-  for (uint32_t base = NP; base < per_wave; base += NP) {
-    load(base);
-    compute(base);
-  }
-
-  __shared__ float red[kMfmaWaves * 4 * 64];
-  const float4v accs[1] = {acc};
-  mfma_reduce_store<1>(accs, red, wave, lane, row0, row_count, bc, fb, Y, y_stride);
-}
-
-// The same product with the split done in the workgroup (k <= 4096): every
-// workgroup reads x (an L2 hit after the first), takes each row's largest
-// magnitude, and writes the hi/lo image of x in operand order into LDS
-// (128 KB at k = 4096) while its weight loads stream in -- one launch, and
-// the split's VALU work overlaps the wait for HBM.  Entry e of group g sits
-// at g * 64 + (e ^ (g & 15)): a 16-lane write round (16 groups, see the unit
-// order below) then covers 16 distinct 16-byte slots, and a wave's read of
-// one group stays a permutation within each 256-byte block.
-constexpr uint32_t kFusedMaxK = 4096;
-constexpr int kFusedRT = 1;  // 16-row tiles per workgroup (2 measured slower: half the CUs)
-
-template <int NP, int RT>
-__global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_fused_kernel(
-    const int8_t* __restrict__ W, const float* __restrict__ S, const float* __restrict__ X,
-    uint32_t x_stride, float* __restrict__ Y, uint32_t K, uint32_t groups, uint32_t gshift,
-    uint32_t row_start, uint32_t row_count, uint32_t bc, uint32_t y_stride) {
-  __shared__ uint4 s_xs[kFusedMaxK / 32 * 64];
-  __shared__ float s_sc[16 * RT * (kFusedMaxK / 32 + 1)];
-  __shared__ float s_max[kMfmaWaves], s_f[kSplitRows];
-  const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
-  const uint32_t r16 = lane & 15, kb = lane >> 4;
-  const uint32_t row0 = blockIdx.x * 16 * RT;
-  const int8_t* wrow[RT];
-#pragma unroll
-  for (int r = 0; r < RT; ++r) {
-    const uint32_t row = row0 + 16 * r + r16;
-    const uint32_t rr = row_start + (row < row_count ? row : row_count - 1);
-    wrow[r] = W + (size_t)rr * K + (kb & 1) * 16 + (kb >> 1) * 32;
-  }
-  const uint32_t ng = K / 32, npairs = ng / 2;
-  const uint32_t per_wave = (npairs + kMfmaWaves - 1) / kMfmaWaves;
-
-  // x: thread t holds row xb = t / 128 and 8-value units j = q + 128 i, with
-  // q = 64 h + 4 (l % 16) + l / 16 for lane l of half h of the row's threads.
-  const uint32_t xb = t >> 7, upr = K / 8;
-  const uint32_t xj = (t & 64) + (lane & 15) * 4 + (lane >> 4);
-  const float4* xrow = reinterpret_cast<const float4*>(X + (size_t)(xb < bc ? xb : 0) * x_stride);
-  float xv[4][8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t j = xj + 128 * i;
-    const uint32_t jj = j < upr ? j : 0;
-    const float4 a = xrow[2 * jj], c = xrow[2 * jj + 1];
-    const bool ok = j < upr && xb < bc;  // rows past the batch multiply as zeros
-    xv[i][0] = ok ? a.x : 0.f; xv[i][1] = ok ? a.y : 0.f;
-    xv[i][2] = ok ? a.z : 0.f; xv[i][3] = ok ? a.w : 0.f;
-    xv[i][4] = ok ? c.x : 0.f; xv[i][5] = ok ? c.y : 0.f;
-    xv[i][6] = ok ? c.z : 0.f; xv[i][7] = ok ? c.w : 0.f;
-  }
-  // Scales of the 16 RT rows, [row][group] with a padded row stride.
-  const uint32_t sstride = groups + 1;
-  constexpr int kSc = RT * 2;  // 16 RT * groups <= 2048 RT here
-  float sreg[kSc];
-#pragma unroll
-  for (int i = 0; i < kSc; ++i) {
-    const uint32_t e = t + 1024 * i;
-    const uint32_t ee = e < 16 * RT * groups ? e : 0;
-    const uint32_t r = ee / groups, q = ee % groups;
-    const uint32_t srow = row0 + r < row_count ? row0 + r : row_count - 1;
-    sreg[i] = S[(size_t)(row_start + srow) * groups + q];
-  }
-
-  float4v acc[RT];
-#pragma unroll
-  for (int r = 0; r < RT; ++r) acc[r] = float4v{0.f, 0.f, 0.f, 0.f};
-  u32x4 wv[RT][NP];
-  auto load = [&](uint32_t base) {
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      const uint32_t p = wave + kMfmaWaves * (base + i);
-      const uint32_t pc = p < npairs ? p : 0;
-#pragma unroll
-      for (int r = 0; r < RT; ++r)
-        wv[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[r] + (size_t)pc * 64));
-    }
-  };
-  auto compute = [&](uint32_t base) {
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      const uint32_t p = wave + kMfmaWaves * (base + i);
-      const uint32_t pc = p < npairs ? p : 0;
-#pragma unroll
-      for (int r = 0; r < RT; ++r) {
-        const auto lo = __builtin_amdgcn_permlane32_swap(wv[r][i].x, wv[r][i].z, false, false);
-        const auto hi = __builtin_amdgcn_permlane32_swap(wv[r][i].y, wv[r][i].w, false, false);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint32_t g = 2 * pc + h;
-          const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-              __builtin_bit_cast(half8, s_xs[g * 64 + (lane ^ (g & 15))]),
-              codes_to_half(u32x2{lo[h], hi[h]}), float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-          const float sv = p < npairs ? s_sc[(16 * r + r16) * sstride + (g >> gshift)] : 0.f;
-          acc[r][0] = fmaf(sv, d[0], acc[r][0]);
-          acc[r][1] = fmaf(sv, d[1], acc[r][1]);
-          acc[r][2] = fmaf(sv, d[2], acc[r][2]);
-          acc[r][3] = fmaf(sv, d[3], acc[r][3]);
-        }
       }
     }
   };
@@ -478,7 +314,7 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_fused_kernel(
   // overlap anything.
   float mx = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kXUnits; ++i)
 #pragma unroll
     for (int q = 0; q < 8; ++q) mx = fmaxf(mx, fabsf(xv[i][q]));
   __builtin_amdgcn_sched_barrier(0);
@@ -490,14 +326,14 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_fused_kernel(
   mx = fmaxf(mx, nd::lane_xor<16>(mx));
   mx = fmaxf(mx, nd::lane_xor<32>(mx));
   if (lane == 0) s_max[wave] = mx;
-  __syncthreads();
+  nd::lds_barrier();  // the weight loads stay in flight
   const float amax = fmaxf(s_max[2 * xb], s_max[2 * xb + 1]);
   int ex = 0;
   if (amax > 0.f && amax <= 3.4028235e38f) frexpf(amax, &ex);  // amax < 2^ex
   const float down = ldexpf(1.f, -ex);
-  if (xj == 0) s_f[xb] = ldexpf(1.f, ex);
+  if (xj == 0) s_e[xb] = ex;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kXUnits; ++i) {
     const uint32_t j = xj + 128 * i;
     if (j >= upr) continue;
     half8 hv, lv;
@@ -515,19 +351,183 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_fused_kernel(
 #pragma unroll
   for (int i = 0; i < kSc; ++i) {
     const uint32_t e = t + 1024 * i;
-    if (e < 16 * RT * groups) s_sc[(e / groups) * sstride + e % groups] = sreg[i];
+    if (e < 16 * groups) s_sc[(e / groups) * sstride + e % groups] = sreg[i];
   }
-  __syncthreads();
+  nd::lds_barrier();
 
   compute(0);
   for (uint32_t base = NP; base < per_wave; base += NP) {
     load(base);
     compute(base);
   }
-  const float fb = s_f[(kb & 1) * 4 + (wave & 3)];
+  // Output c of lane l belongs to batch row (4 (l / 16) + c) % 8 (ldexp by
+  // its exponent: a product with 2^e overflows at e = 128).
+#pragma unroll
+  for (int c = 0; c < 4; ++c) acc[c] = ldexpf(acc[c], s_e[(4 * kb + c) & 7]);
   __syncthreads();  // every wave is done with s_xs: reuse it for the sums
-  mfma_reduce_store<RT>(acc, reinterpret_cast<float*>(s_xs), wave, lane, row0, row_count, bc, fb,
-                        Y, y_stride);
+  mfma_reduce_store(acc, reinterpret_cast<float*>(s_xs), wave, lane, row0, row_count, bc, Y,
+                    y_stride);
+}
+
+// K-split form of the batched product (k >= 4096): workgroup (row block,
+// slice) takes 64 weight rows (4 tiles of 16) over the k-slice [KS s, KS s +
+// KS), KS = 256 NP.  Every workgroup of a full-k design reads all of x (128
+// KB for 8 fp32 rows at k = 4096) for 64 KB of weights, and the rate at which
+// data enters a CU bounds the launch; slicing k cuts x to KS * 32 bytes per
+// workgroup (32 KB at KS = 1024) for the same 64 KB of weights.  The split
+// into hi/lo halves is taken per (batch row, slice): x * 2^-e_bs with e_bs
+// the exponent of the slice's largest magnitude, so the slice's partial sum
+// is 2^e_bs times the MFMA sum.  Wave w takes tile w % 4 and the contiguous
+// pairs [NP (w / 4), +NP) of the slice.  Partials go to
+// P[s][b][row - row_start] (plain stores); mv_slice_sum_kernel then adds the
+// slices in order s = 0, 1, ... -- the same sum on every run.
+template <int NP>
+__global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_slice_kernel(
+    const int8_t* __restrict__ W, const float* __restrict__ S, const float* __restrict__ X,
+    uint32_t x_stride, float* __restrict__ P, uint32_t K, uint32_t groups, uint32_t gshift,
+    uint32_t row_start, uint32_t row_count, uint32_t bc) {
+  constexpr uint32_t KS = 256 * NP, kUnits = KS / 8;  // 8-value units of one batch row
+  constexpr uint32_t kSg = KS / 32;                   // 32-wide groups of the slice
+  __shared__ uint4 s_xs[kSg * 64];                    // also the cross-wave sums (16 KB)
+  __shared__ float s_sc[64 * (kSg + 1)];
+  __shared__ float s_max[kMfmaWaves];
+  __shared__ int s_e[kSplitRows];
+  static_assert(kSg * 64 * 16 >= kMfmaWaves * 4 * 64 * 4, "the sums fit the x image");
+  const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const uint32_t r16 = lane & 15, kb = lane >> 4;
+  const uint32_t slice = blockIdx.y, k0 = slice * KS;
+  const uint32_t row0 = blockIdx.x * 64;
+  const uint32_t tile = wave & 3, wq = wave >> 2;
+
+  // x: thread t < 8 kUnits takes batch row xb = t / kUnits, unit j of the
+  // slice with j = 64 (u / 64) + 4 (l % 16) + l / 16 for u = t % kUnits, l =
+  // u % 64 -- a 16-lane write round then covers 16 distinct groups.
+  const bool has_x = t < kSplitRows * kUnits;
+  const uint32_t xb = t / kUnits, u = t % kUnits;
+  const uint32_t xj = (u & ~63u) + (lane & 15) * 4 + (lane >> 4);
+  const float4* xp = reinterpret_cast<const float4*>(
+                        X + (size_t)(has_x && xb < bc ? xb : 0) * x_stride + k0) + 2 * xj;
+  const float4 xa = xp[0], xc = xp[1];
+  // Scales of the 64 rows over the slice's groups, [row][group] padded.
+  const uint32_t gs = KS >> gshift >= 32 ? (KS >> gshift) / 32 : 1;  // groups in the slice
+  const uint32_t q0 = k0 / (32u << gshift);
+  const uint32_t sstride = kSg + 1;
+  constexpr int kSc = 64 * kSg / (64 * kMfmaWaves) > 0 ? 64 * kSg / (64 * kMfmaWaves) : 1;
+  float sreg[kSc];
+#pragma unroll
+  for (int i = 0; i < kSc; ++i) {
+    const uint32_t e = t + 64 * kMfmaWaves * i;
+    const uint32_t ee = e < 64 * gs ? e : 0;
+    const uint32_t r = ee / gs, q = ee % gs;
+    const uint32_t srow = row0 + r < row_count ? row0 + r : row_count - 1;
+    sreg[i] = S[(size_t)(row_start + srow) * groups + q0 + q];
+  }
+  // Weights: NP pairs of this wave's tile, all in flight at once, issued
+  // only after every wave has issued its x and scale loads (a CU serves its
+  // waves' loads roughly in issue order: behind the weight stream x would
+  // arrive last and the split could not overlap it).
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t row = row0 + 16 * tile + r16;
+  const int8_t* wrow = W + (size_t)(row_start + (row < row_count ? row : row_count - 1)) * K + k0 +
+                       (kb & 1) * 16 + (kb >> 1) * 32;
+  u32x4 wv[NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i)
+    wv[i] = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4*>(wrow + (size_t)(NP * wq + i) * 64));
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Slice maxima: a batch row spans kUnits / 64 waves.
+  const bool ok = has_x && xb < bc;  // rows past the batch multiply as zeros
+  const float xv[8] = {ok ? xa.x : 0.f, ok ? xa.y : 0.f, ok ? xa.z : 0.f, ok ? xa.w : 0.f,
+                       ok ? xc.x : 0.f, ok ? xc.y : 0.f, ok ? xc.z : 0.f, ok ? xc.w : 0.f};
+  float mx = 0.f;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) mx = fmaxf(mx, fabsf(xv[q]));
+  mx = fmaxf(mx, nd::lane_xor<1>(mx));
+  mx = fmaxf(mx, nd::lane_xor<2>(mx));
+  mx = fmaxf(mx, nd::lane_xor<4>(mx));
+  mx = fmaxf(mx, nd::lane_xor<8>(mx));
+  mx = fmaxf(mx, nd::lane_xor<16>(mx));
+  mx = fmaxf(mx, nd::lane_xor<32>(mx));
+  if (lane == 0) s_max[wave] = mx;
+  nd::lds_barrier();  // the weight loads stay in flight
+  if (has_x) {
+    constexpr uint32_t kWpr = kUnits / 64;  // waves per batch row
+    float amax = 0.f;
+#pragma unroll
+    for (uint32_t i = 0; i < kWpr; ++i) amax = fmaxf(amax, s_max[xb * kWpr + i]);
+    int ex = 0;
+    if (amax > 0.f && amax <= 3.4028235e38f) frexpf(amax, &ex);  // amax < 2^ex
+    const float down = ldexpf(1.f, -ex);
+    if (u == 0) s_e[xb] = ex;
+    half8 hv, lv;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float v = xv[q] * down;
+      const _Float16 h = (_Float16)v;
+      hv[q] = h;
+      lv[q] = (_Float16)(v - (float)h);
+    }
+    const uint32_t g = xj >> 2, e = k_block_lanes(xj & 3) * 16 + xb;
+    s_xs[g * 64 + (e ^ (g & 15))] = __builtin_bit_cast(uint4, hv);
+    s_xs[g * 64 + ((e + 8) ^ (g & 15))] = __builtin_bit_cast(uint4, lv);
+  }
+#pragma unroll
+  for (int i = 0; i < kSc; ++i) {
+    const uint32_t e = t + 64 * kMfmaWaves * i;
+    if (e < 64 * gs) s_sc[(e / gs) * sstride + e % gs] = sreg[i];
+  }
+  nd::lds_barrier();
+
+  float4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const uint32_t p = NP * wq + i;
+    const auto lo = __builtin_amdgcn_permlane32_swap(wv[i].x, wv[i].z, false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap(wv[i].y, wv[i].w, false, false);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t g = 2 * p + h;
+      const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+          __builtin_bit_cast(half8, s_xs[g * 64 + (lane ^ (g & 15))]),
+          codes_to_half(u32x2{lo[h], hi[h]}), float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+      const float sv = s_sc[(16 * tile + r16) * sstride + (g >> gshift)];
+      acc[0] = fmaf(sv, d[0], acc[0]);
+      acc[1] = fmaf(sv, d[1], acc[1]);
+      acc[2] = fmaf(sv, d[2], acc[2]);
+      acc[3] = fmaf(sv, d[3], acc[3]);
+    }
+  }
+  // Sum the 4 waves of each tile: red[wave][c][lane]; thread (tile, c, lane)
+  // adds its tile's waves, then the lo row onto the hi row (lane + 32).
+  float* red = reinterpret_cast<float*>(s_xs);
+  __syncthreads();  // every wave is done with the x image
+#pragma unroll
+  for (int c = 0; c < 4; ++c) red[(wave * 4 + c) * 64 + lane] = acc[c];
+  __syncthreads();
+  const uint32_t ot = t >> 8, oc = (t >> 6) & 3;
+  float sum = 0.f;
+#pragma unroll
+  for (uint32_t q = 0; q < 4; ++q) sum += red[((4 * q + ot) * 4 + oc) * 64 + lane];
+  sum += nd::lane_xor<32>(sum);
+  const uint32_t b = (lane >> 4) * 4 + oc, orow = row0 + 16 * ot + (lane & 15);
+  if (lane < 32 && orow < row_count && b < bc)
+    P[((size_t)slice * kSplitRows + b) * row_count + orow] = ldexpf(sum, s_e[b]);
+}
+
+// y[b][r] = sum over slices s = 0, 1, ... of P[s][b][r].
+__global__ __launch_bounds__(256) void mv_slice_sum_kernel(const float* __restrict__ P,
+                                                           uint32_t slices, uint32_t row_count,
+                                                           uint32_t bc, float* __restrict__ Y,
+                                                           uint32_t y_stride) {
+  const uint32_t r = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
+  if (r >= row_count || b >= bc) return;
+  float sum = 0.f;
+  for (uint32_t s = 0; s < slices; ++s) sum += P[((size_t)s * kSplitRows + b) * row_count + r];
+  Y[(size_t)b * y_stride + r] = sum;
 }
 
 __global__ void row_kernel(const int8_t* __restrict__ W, const float* __restrict__ S,
@@ -563,9 +563,11 @@ MatvecFn pick_b(uint32_t b, uint32_t spt) {
 // Host-side checks that the kernel's geometry fits the matrix were done by
 // the caller (k = 16 * 2^j with 128 <= k <= 8192, g % 16 == 0, k % g == 0).
 // With `split` (kMatvecSplitBytes of device memory), batches of 3 or more
-// rows of a matrix with g % 32 == 0 run on MFMA, 8 rows per launch (k <=
-// 4096: one fused launch; k = 8192: split kernel + MFMA kernel); otherwise
-// every row is streamed by the vector kernel.
+// rows of a matrix with g % 32 == 0 run on MFMA, 8 rows per launch: k <=
+// 2048 in one fused launch, k >= 4096 as k-slices plus the slice sum (9.98
+// vs 10.7 us at 4096 x 4096 and 15.3 vs 17.4 at 4096 x 8192, batch 8; 8.0 vs
+// 7.1 at 4096 x 2048, where the sum launch costs more than it saves);
+// otherwise every row is streamed by the vector kernel.
 hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uint32_t x_stride,
                             uint32_t row_start, uint32_t row_count, float* y, uint32_t y_stride,
                             hipStream_t s, void* split) {
@@ -573,36 +575,41 @@ hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uin
   if (split && batch >= kMfmaMinBatch && m->g % 32 == 0) {
     uint32_t gshift = 0;  // g = 32 << gshift (g divides k, a power of two)
     while ((32u << gshift) < m->g) ++gshift;
-    uint4* xs = reinterpret_cast<uint4*>(split);
-    float* xf = reinterpret_cast<float*>(reinterpret_cast<char*>(split) + (size_t)m->k * 32);
-    const uint32_t pairs_per_wave = (m->k / 64 + kMfmaWaves - 1) / kMfmaWaves;
     for (uint32_t b0 = 0; b0 < batch; b0 += kSplitRows) {
       const uint32_t bc = batch - b0 < kSplitRows ? batch - b0 : kSplitRows;
+      const float* xb = x + (size_t)b0 * x_stride;
+      float* yb = y + (size_t)b0 * y_stride;
       if (m->k <= kFusedMaxK) {
-        const auto kern = pairs_per_wave >= 4 ? &matvec_mfma_fused_kernel<4, kFusedRT>
-                        : pairs_per_wave >= 2 ? &matvec_mfma_fused_kernel<2, kFusedRT>
-                                              : &matvec_mfma_fused_kernel<1, kFusedRT>;
-        hipLaunchKernelGGL(kern, dim3((row_count + 16 * kFusedRT - 1) / (16 * kFusedRT)),
-                           dim3(64 * kMfmaWaves), 0, s, m->w,
-                           m->scales, x + (size_t)b0 * x_stride, x_stride,
-                           y + (size_t)b0 * y_stride, m->k, m->k / m->g, gshift, row_start,
+        const uint32_t pairs_per_wave = (m->k / 64 + kMfmaWaves - 1) / kMfmaWaves;
+        const auto kern = pairs_per_wave >= 2 ? &matvec_mfma_fused_kernel<2>
+                                              : &matvec_mfma_fused_kernel<1>;
+        hipLaunchKernelGGL(kern, dim3((row_count + 15) / 16), dim3(64 * kMfmaWaves), 0, s, m->w,
+                           m->scales, xb, x_stride, yb, m->k, m->k / m->g, gshift, row_start,
                            row_count, bc, y_stride);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         continue;
       }
-      hipLaunchKernelGGL(mv_split_kernel, dim3(kSplitRows), dim3(256), 0, s,
-                         x + (size_t)b0 * x_stride, x_stride, bc, m->k, xs, xf);
-      hipError_t e = hipGetLastError();
-      if (e != hipSuccess) return e;
-      const auto kern = pairs_per_wave >= 4 ? &matvec_mfma_kernel<4>
-                      : pairs_per_wave >= 2 ? &matvec_mfma_kernel<2> : &matvec_mfma_kernel<1>;
-      const size_t lds = (size_t)16 * (m->k / m->g + 1) * sizeof(float);
-      hipLaunchKernelGGL(kern, dim3((row_count + 15) / 16), dim3(64 * kMfmaWaves), lds, s, m->w,
-                         m->scales, xs, xf, y + (size_t)b0 * y_stride, m->k, m->k / m->g, gshift,
-                         row_start, row_count, bc, y_stride);
-      e = hipGetLastError();
-      if (e != hipSuccess) return e;
+      // Slices of 1024 when they give 256 workgroups, else of 512; partials
+      // of at most kMatvecSplitBytes per launch pair (row blocks of 64).
+      const bool wide = ((row_count + 63) / 64) * (m->k / 1024) >= 256;
+      const uint32_t ks = wide ? 1024 : 512, slices = m->k / ks;
+      const size_t cap = kMatvecSplitBytes / sizeof(float) / ((size_t)slices * kSplitRows);
+      const uint32_t block = (uint32_t)(cap / 64 * 64);
+      float* P = reinterpret_cast<float*>(split);
+      for (uint32_t r0 = 0; r0 < row_count; r0 += block) {
+        const uint32_t rc = row_count - r0 < block ? row_count - r0 : block;
+        const auto kern = wide ? &matvec_mfma_slice_kernel<4> : &matvec_mfma_slice_kernel<2>;
+        hipLaunchKernelGGL(kern, dim3((rc + 63) / 64, slices), dim3(64 * kMfmaWaves), 0, s, m->w,
+                           m->scales, xb, x_stride, P, m->k, m->k / m->g, gshift, row_start + r0,
+                           rc, bc);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(mv_slice_sum_kernel, dim3((rc + 255) / 256, bc), dim3(256), 0, s, P,
+                           slices, rc, bc, yb + r0, y_stride);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+      }
     }
     return hipSuccess;
   }

@@ -49,7 +49,7 @@ struct nd_ctx {
   float* attn_partials = nullptr;
   size_t attn_partial_floats = 0;
   uint32_t* attn_counters = nullptr;
-  // Split inputs of the batched MFMA matvec (kMatvecSplitBytes).
+  // Workspace of the batched MFMA matvec (kMatvecSplitBytes).
   void* mv_split = nullptr;
   float* cq_prepared = nullptr;  // [kCqPreparedRows][kCqMaxKpad], on the first CQ upload
   // Digit planes and row factors of nd_matmul_d (grown on demand).
@@ -99,9 +99,10 @@ inline hipStream_t nd_pick_stream(nd_ctx* ctx, void* stream) {
 
 // Kernel launchers (each validates nothing: callers check shapes first).
 // `split`: kMatvecSplitBytes of device memory that lets batches of 3 or more
-// run on MFMA (the fp16 split of x at k = 8192); nullptr keeps the vector
-// kernel.
-constexpr size_t kMatvecSplitBytes = 8192 * 32 + 256;
+// run on MFMA (it holds the per-slice partial sums at k >= 4096); nullptr
+// keeps the vector kernel.  Launches sharing one `split` must be ordered
+// (one stream).
+constexpr size_t kMatvecSplitBytes = size_t(4) << 20;
 hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uint32_t x_stride,
                             uint32_t row_start, uint32_t row_count, float* y, uint32_t y_stride,
                             hipStream_t s, void* split = nullptr);

@@ -99,6 +99,14 @@ __device__ __forceinline__ float lane_xor(float v) {
   else return __shfl_xor(v, 32, 64);
 }
 
+// Workgroup barrier for hand-offs through LDS only: waits for this wave's
+// LDS (and scalar) operations, not for its global loads.  __syncthreads()
+// also fences global memory, which waits for every load still in flight --
+// work that needs only LDS would then wait for a whole weight stream.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Sum over a quad of lanes (4 consecutive), in every lane of the quad.
 template <typename T>
 __device__ __forceinline__ T quad_sum(T v) {

@@ -69,6 +69,43 @@ def test_matvec_batched_magnitudes_ranges_and_chunks(hip):
                  "matvec b3 rows 37..336")
 
 
+def test_matvec_k_slices(hip):
+    """Batches at k >= 4096 run as k-slices, each input row split around its
+    largest element within the slice, and the slices summed in order: slices
+    of very different magnitude, an all-zero row, groups wider than a slice
+    and as wide as k, slices of 512 and of 1024, a row range, a batch above
+    eight, and a row count whose partial sums take two launch pairs."""
+    say("matvec k-slices magnitudes")
+    m = matrix(17, 300, 4096, 32)
+    s = synth.Stream(19, "xslices")
+    x = s.normal((11, 4096))
+    x[0, :512] *= 1e4
+    x[0, 1024:1536] *= 1e-5
+    x[1] = 0.0
+    x[2, 512:] = 0.0
+    x[5] *= np.power(10.0, s.uniform((4096,), -3.0, 3.0)).astype(np.float32)
+    got = hip.matvec(m, x)
+    assert np.all(got[1] == 0.0)
+    assert_close(got, oracle.matvec_i8(m.codes, m.scales, 32, x), RTOL, ATOL, "slices b11")
+    part = hip.matvec(m, x[:3], MatrixRowRange(5, 200))
+    assert_close(part, oracle.matvec_i8(m.codes, m.scales, 32, x[:3], 5, 200), RTOL, ATOL,
+                 "slices b3 rows 5..204")
+    for n, k, g, batch in [(640, 4096, 1024, 3), (96, 8192, 8192, 4), (4100, 4096, 64, 5),
+                           (2100, 8192, 128, 8)]:
+        say("matvec k-slices", n, k, g, batch)
+        mg = matrix(23, n, k, g)
+        xg = synth.Stream(29, f"xs{k}").normal((batch, k))
+        assert_close(hip.matvec(mg, xg), oracle.matvec_i8(mg.codes, mg.scales, g, xg), RTOL,
+                     ATOL, f"slices {n}x{k} g{g} b{batch}")
+    say("matvec k-slices two launch pairs")
+    w, sc = synth.int8_matrix(31, "w1028x8192", 1028, 8192, 32)  # rows repeat every 1028
+    big = Int8Matrix(np.tile(w, (16, 1))[:16448], np.tile(sc, (16, 1))[:16448], 32)
+    xb = synth.Stream(37, "xbig").normal((3, 8192))
+    got = hip.matvec(big, xb)
+    assert_close(got, oracle.matvec_i8(big.codes, big.scales, 32, xb), RTOL, ATOL,
+                 "slices 16448x8192 b3")
+
+
 def test_matvec_ranges_and_batch_requests(hip):
     say("matvec ranges")
     m = matrix(3, 512, 512, 512)
