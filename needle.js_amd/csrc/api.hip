@@ -101,7 +101,10 @@ nd_status nd_create(int32_t device, nd_ctx** out) {
     return nd_fail(nullptr, ND_ERR_BACKEND, "hipStreamCreate: %s", hipGetErrorString(e));
   }
   e = hipMalloc(&ctx->mv_split, kMatvecSplitBytes);
+  if (e == hipSuccess) e = hipMemsetAsync(ctx->mv_split, 0, kMatvecSplitBytes, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) {
+    if (ctx->mv_split) hipFree(ctx->mv_split);
     hipStreamDestroy(ctx->stream);
     delete ctx;
     return nd_fail(nullptr, ND_ERR_BACKEND, "hipMalloc(matvec split): %s", hipGetErrorString(e));

@@ -227,6 +227,7 @@ __device__ __forceinline__ void mfma_reduce_store(float4v acc, float* red, uint3
 // order below) then covers 16 distinct 16-byte slots, and a wave's read of
 // one group stays a permutation within each 256-byte block.
 constexpr uint32_t kFusedMaxK = 2048;
+constexpr uint32_t kMaxSlices = 16;  // k = 8192 in slices of 512
 constexpr int kXUnits = kFusedMaxK / 8 / 128;  // 8-value units of x per thread
 
 template <int NP>
@@ -379,12 +380,14 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_fused_kernel(
 // the exponent of the slice's largest magnitude, so the slice's partial sum
 // is 2^e_bs times the MFMA sum.  Wave w takes tile w % 4 and the contiguous
 // pairs [NP (w / 4), +NP) of the slice.  Partials go to
-// P[s][b][row - row_start] (plain stores); mv_slice_sum_kernel then adds the
-// slices in order s = 0, 1, ... -- the same sum on every run.
+// P[s][b][row - row_start] with agent-coherent stores; the last slice of a
+// row block to count itself in adds the slices in order s = 0, 1, ... (the
+// same sum on every run) -- no second launch.
 template <int NP>
 __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_slice_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ S, const float* __restrict__ X,
-    uint32_t x_stride, float* __restrict__ P, uint32_t K, uint32_t groups, uint32_t gshift,
+    uint32_t x_stride, float* __restrict__ P, uint32_t* __restrict__ counters,
+    float* __restrict__ Y, uint32_t y_stride, uint32_t K, uint32_t groups, uint32_t gshift,
     uint32_t row_start, uint32_t row_count, uint32_t bc) {
   constexpr uint32_t KS = 256 * NP, kUnits = KS / 8;  // 8-value units of one batch row
   constexpr uint32_t kSg = KS / 32;                   // 32-wide groups of the slice
@@ -515,19 +518,34 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_slice_kernel(
   sum += nd::lane_xor<32>(sum);
   const uint32_t b = (lane >> 4) * 4 + oc, orow = row0 + 16 * ot + (lane & 15);
   if (lane < 32 && orow < row_count && b < bc)
-    P[((size_t)slice * kSplitRows + b) * row_count + orow] = ldexpf(sum, s_e[b]);
-}
-
-// y[b][r] = sum over slices s = 0, 1, ... of P[s][b][r].
-__global__ __launch_bounds__(256) void mv_slice_sum_kernel(const float* __restrict__ P,
-                                                           uint32_t slices, uint32_t row_count,
-                                                           uint32_t bc, float* __restrict__ Y,
-                                                           uint32_t y_stride) {
-  const uint32_t r = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
-  if (r >= row_count || b >= bc) return;
-  float sum = 0.f;
-  for (uint32_t s = 0; s < slices; ++s) sum += P[((size_t)s * kSplitRows + b) * row_count + r];
-  Y[(size_t)b * y_stride + r] = sum;
+    __hip_atomic_store(P + ((size_t)slice * kSplitRows + b) * row_count + orow,
+                       ldexpf(sum, s_e[b]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Count the slice in once its partials are stored (agent-coherent stores,
+  // completed); the last slice of the row block adds all of them in order s
+  // = 0, 1, ... and resets the counter for the next launch.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __shared__ uint32_t s_last;
+  if (t == 0)
+    s_last = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT) == gridDim.y - 1;
+  __syncthreads();
+  if (!s_last) return;
+  const uint32_t fb = t >> 6, frow = row0 + (t & 63);
+  if (t < 64 * kSplitRows && fb < bc && frow < row_count) {
+    float v[kMaxSlices];
+#pragma unroll
+    for (uint32_t q = 0; q < kMaxSlices; ++q)
+      v[q] = q < gridDim.y ? __hip_atomic_load(P + ((size_t)q * kSplitRows + fb) * row_count + frow,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                           : 0.f;
+    float total = v[0];
+#pragma unroll
+    for (uint32_t q = 1; q < kMaxSlices; ++q)
+      if (q < gridDim.y) total += v[q];
+    Y[(size_t)fb * y_stride + frow] = total;
+  }
+  if (t == 0) __hip_atomic_store(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __global__ void row_kernel(const int8_t* __restrict__ W, const float* __restrict__ S,
@@ -564,9 +582,10 @@ MatvecFn pick_b(uint32_t b, uint32_t spt) {
 // the caller (k = 16 * 2^j with 128 <= k <= 8192, g % 16 == 0, k % g == 0).
 // With `split` (kMatvecSplitBytes of device memory), batches of 3 or more
 // rows of a matrix with g % 32 == 0 run on MFMA, 8 rows per launch: k <=
-// 2048 in one fused launch, k >= 4096 as k-slices plus the slice sum (9.98
-// vs 10.7 us at 4096 x 4096 and 15.3 vs 17.4 at 4096 x 8192, batch 8; 8.0 vs
-// 7.1 at 4096 x 2048, where the sum launch costs more than it saves);
+// 2048 in one fused launch, k >= 4096 as k-slices summed by the last slice
+// of each row block (9.2 vs 10.7 us for the fused form at 4096 x 4096 and
+// 12.9 vs 17.4 at 4096 x 8192, batch 8; at 4096 x 2048 the fused form wins,
+// 6.75 vs 7.1);
 // otherwise every row is streamed by the vector kernel.
 hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uint32_t x_stride,
                             uint32_t row_start, uint32_t row_count, float* y, uint32_t y_stride,
@@ -591,23 +610,21 @@ hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uin
         continue;
       }
       // Slices of 1024 when they give 256 workgroups, else of 512; partials
-      // of at most kMatvecSplitBytes per launch pair (row blocks of 64).
+      // of at most kMatvecPartialBytes per launch (row blocks of 64).
       const bool wide = ((row_count + 63) / 64) * (m->k / 1024) >= 256;
       const uint32_t ks = wide ? 1024 : 512, slices = m->k / ks;
-      const size_t cap = kMatvecSplitBytes / sizeof(float) / ((size_t)slices * kSplitRows);
+      const size_t cap = kMatvecPartialBytes / sizeof(float) / ((size_t)slices * kSplitRows);
       const uint32_t block = (uint32_t)(cap / 64 * 64);
       float* P = reinterpret_cast<float*>(split);
+      uint32_t* counters = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(split) +
+                                                       kMatvecPartialBytes);
       for (uint32_t r0 = 0; r0 < row_count; r0 += block) {
         const uint32_t rc = row_count - r0 < block ? row_count - r0 : block;
         const auto kern = wide ? &matvec_mfma_slice_kernel<4> : &matvec_mfma_slice_kernel<2>;
         hipLaunchKernelGGL(kern, dim3((rc + 63) / 64, slices), dim3(64 * kMfmaWaves), 0, s, m->w,
-                           m->scales, xb, x_stride, P, m->k, m->k / m->g, gshift, row_start + r0,
-                           rc, bc);
+                           m->scales, xb, x_stride, P, counters, yb + r0, y_stride, m->k,
+                           m->k / m->g, gshift, row_start + r0, rc, bc);
         hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(mv_slice_sum_kernel, dim3((rc + 255) / 256, bc), dim3(256), 0, s, P,
-                           slices, rc, bc, yb + r0, y_stride);
-        e = hipGetLastError();
         if (e != hipSuccess) return e;
       }
     }

@@ -99,10 +99,12 @@ inline hipStream_t nd_pick_stream(nd_ctx* ctx, void* stream) {
 
 // Kernel launchers (each validates nothing: callers check shapes first).
 // `split`: kMatvecSplitBytes of device memory that lets batches of 3 or more
-// run on MFMA (it holds the per-slice partial sums at k >= 4096); nullptr
-// keeps the vector kernel.  Launches sharing one `split` must be ordered
+// run on MFMA (it holds the per-slice partial sums at k >= 4096 and their
+// arrival counters, zero at allocation and left zero by every launch);
+// nullptr keeps the vector kernel.  Launches sharing one `split` must be ordered
 // (one stream).
-constexpr size_t kMatvecSplitBytes = size_t(4) << 20;
+constexpr size_t kMatvecPartialBytes = (size_t(4) << 20) - (size_t(64) << 10);
+constexpr size_t kMatvecSplitBytes = kMatvecPartialBytes + (size_t(64) << 10);  // + counters
 hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uint32_t x_stride,
                             uint32_t row_start, uint32_t row_count, float* y, uint32_t y_stride,
                             hipStream_t s, void* split = nullptr);
