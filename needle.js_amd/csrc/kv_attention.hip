@@ -272,7 +272,9 @@ __global__ __launch_bounds__(256) void attention_kernel(
       tile_max = fmaxf(tile_max, nd::lane_xor<16>(tile_max));
       tile_max = fmaxf(tile_max, nd::lane_xor<32>(tile_max));
       const float m_new = fmaxf(m[h], tile_max);
-      const float alpha = __expf(m[h] - m_new);  // 0 on the first tile (m = -inf)
+      // 0 on the first tile with a visible position (m = -inf); 1 while no
+      // position has been visible (a tile of unwritten slots: -inf - -inf).
+      const float alpha = m_new == -INFINITY ? 1.f : __expf(m[h] - m_new);
       m[h] = m_new;
       l[h] *= alpha;
 #pragma unroll

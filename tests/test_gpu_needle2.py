@@ -7,6 +7,7 @@ KV codes within one code and mostly identical, greedy token sequences and
 selected ids identical, log-probabilities within 1e-3.
 """
 
+import dataclasses
 import sys
 
 import numpy as np
@@ -75,6 +76,28 @@ def test_step_logits_and_kv_match_oracle(small, sink):
                 assert d.max() <= 1 and (d == 0).mean() > 0.95
             for g, r in ((gks, rks), (gvs, rvs)):
                 np.testing.assert_allclose(g, r, rtol=1e-3)
+
+
+@pytest.mark.parametrize("heads,kv_heads,window,length", [(2, 2, 8, 48), (4, 2, 0, 600)])
+def test_attention_group_sizes_and_chunked_slots(hip, heads, kv_heads, window, length):
+    """One query head per KV head, and a 600-slot cache without a window
+    whose three chunks are mostly unwritten slots at the first steps (a tile
+    with no visible position must leave its wave's softmax state empty, not
+    NaN): step logits agree with the oracle's."""
+    geo = dataclasses.replace(SMALL, heads=heads, kv_heads=kv_heads, kv_window=window,
+                              max_length=max(SMALL.max_length, length))
+    say("needle2 attention paths", heads, kv_heads, window, length)
+    w = Needle2Weights(geo, 41)
+    model = NeedleModel(hip, w)
+    try:
+        rt = model.create_runtime()
+        rt.reset(length, 0)
+        ref = oracle.Needle2(w).runtime(length, 0)
+        tokens = synth.Stream(6, f"n2paths{heads}{window}").integers(12, 0, geo.vocab - 1)
+        for i, t in enumerate(tokens):
+            close(rt.step(int(t)), ref.step(int(t)), (heads, window, i))
+    finally:
+        model.dispose()
 
 
 def test_step_ignores_stale_nan_slots(small):
