@@ -907,18 +907,21 @@ __global__ __launch_bounds__(256) void n2_probe_scores_kernel(const float* __res
   }
 }
 
+constexpr uint32_t kPoolThreads = 1024;  // 16 waves, each on every 16th cell
+
 // The online update of runtime.ts:73-90 over C cells at once, in its closed
 // form: M' = max(M, max_c s_c); every earlier term is rescaled by
 // exp(M - M') (0 before the first cell) and cell c enters with weight
 // exp(s_c - M').  Workgroup (p, j) updates probe p's weighted sums of
 // columns [64 j, 64 j + 64) and its copy of (M, denominator).
-__global__ __launch_bounds__(256) void n2_probe_pool_kernel(const float* __restrict__ cells,
+__global__ __launch_bounds__(kPoolThreads) void n2_probe_pool_kernel(const float* __restrict__ cells,
                                                             uint32_t C, uint32_t D,
                                                             const double* __restrict__ scores,
                                                             PoolState ps) {
   constexpr uint32_t kChunk = 1024;
   __shared__ double e[kChunk];
-  __shared__ double red[256];
+  __shared__ double red[kPoolThreads];
+  constexpr uint32_t kSlices = kPoolThreads / 64;
   const uint32_t p = blockIdx.x, j = blockIdx.y, t = threadIdx.x;
   const uint32_t col = j * 64 + (t & 63), slice = t >> 6;
   double* const my_max = ps.max + p * kMaxChunks + j;
@@ -926,10 +929,10 @@ __global__ __launch_bounds__(256) void n2_probe_pool_kernel(const float* __restr
   const double den_old = *my_den;
   const double m_old = den_old > 0.0 ? *my_max : -INFINITY;
   double mx = -INFINITY;
-  for (uint32_t c = t; c < C; c += 256) mx = fmax(mx, scores[(size_t)c * kMaxProbes + p]);
+  for (uint32_t c = t; c < C; c += kPoolThreads) mx = fmax(mx, scores[(size_t)c * kMaxProbes + p]);
   red[t] = mx;
   __syncthreads();
-  for (uint32_t w = 128; w > 0; w >>= 1) {
+  for (uint32_t w = kPoolThreads / 2; w > 0; w >>= 1) {
     if (t < w) red[t] = fmax(red[t], red[t + w]);
     __syncthreads();
   }
@@ -939,29 +942,32 @@ __global__ __launch_bounds__(256) void n2_probe_pool_kernel(const float* __restr
   double acc = 0.0, esum = 0.0;
   for (uint32_t c0 = 0; c0 < C; c0 += kChunk) {
     const uint32_t n = C - c0 < kChunk ? C - c0 : kChunk;
-    for (uint32_t c = t; c < n; c += 256) {
+    for (uint32_t c = t; c < n; c += kPoolThreads) {
       const double w = exp(scores[(size_t)(c0 + c) * kMaxProbes + p] - m_new);
       e[c] = w;
       esum += w;
     }
     __syncthreads();
     if (col < D) {
-#pragma unroll 8
-      for (uint32_t c = slice; c < n; c += 4) acc += e[c] * (double)cells[(size_t)(c0 + c) * D + col];
+#pragma unroll 16
+      for (uint32_t c = slice; c < n; c += kSlices)
+        acc += e[c] * (double)cells[(size_t)(c0 + c) * D + col];
     }
     __syncthreads();
   }
   red[t] = acc;
   __syncthreads();
   if (t < 64 && col < D) {
-    const double sum = ((red[t] + red[t + 64]) + red[t + 128]) + red[t + 192];
+    double sum = red[t];
+#pragma unroll
+    for (uint32_t q = 1; q < kSlices; ++q) sum += red[t + 64 * q];
     double* w = ps.weighted + (size_t)p * D + col;
     *w = *w * factor + sum;
   }
   __syncthreads();
   red[t] = esum;
   __syncthreads();
-  for (uint32_t w = 128; w > 0; w >>= 1) {
+  for (uint32_t w = kPoolThreads / 2; w > 0; w >>= 1) {
     if (t < w) red[t] += red[t + w];
     __syncthreads();
   }
@@ -1139,7 +1145,8 @@ hipError_t enqueue_pool(nd_needle* n, const float* cells, uint32_t C, double* sc
                      probes, n->probe_count, scale, scores);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(n2_probe_pool_kernel, grid, dim3(256), 0, s, cells, C, D, scores, n->pool);
+  hipLaunchKernelGGL(n2_probe_pool_kernel, grid, dim3(kPoolThreads), 0, s, cells, C, D, scores,
+                     n->pool);
   return hipGetLastError();
 }
 
