@@ -114,7 +114,10 @@ nd_status nd_mat_info(const nd_mat* mat, const int8_t** w_dev, const float** sca
  * rows [row_start, row_start + row_count) and b < batch; x is [batch][k],
  * y is [batch][row_count].  InferenceBackend.matvec with a MatrixRowRange
  * (backends/backend.ts:88-93, backends/cpu.ts:12-16; arithmetic of
- * backends/cq.ts:106-156).  batch > 1 is the batched-activation form. */
+ * backends/cq.ts:106-156).  batch > 1 is the batched-activation form.
+ * Batches of 3 or more on int8 matrices (g a multiple of 32) share the
+ * context's workspace of partial sums and arrival counters: enqueue such
+ * calls of one context on one stream. */
 nd_status nd_matvec(nd_ctx* ctx, const nd_mat* mat, const float* x, uint32_t batch,
                     uint32_t row_start, uint32_t row_count, float* y);
 nd_status nd_matvec_d(nd_ctx* ctx, const nd_mat* mat, const float* x_dev, uint32_t batch,
