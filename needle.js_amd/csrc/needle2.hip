@@ -690,15 +690,17 @@ __global__ __launch_bounds__(256) void n2_qkv_kernel(
     return;
   }
   // Loads first: this thread's weight bytes, the row scale, the epilogue
-  // operands, then x.
-  const uint32_t r = t >> 2, q = t & 3, seg = d / 4;
+  // operands, then x.  The 4 threads of a row read 64 contiguous bytes per
+  // load (thread q bytes [64 k + 16 q, +16)), so a wave's load covers 16
+  // rows x 64 bytes rather than 64 rows x 16.
+  const uint32_t r = t >> 2, q = t & 3, last = d / 64 - 1;
   const size_t row = (size_t)b * kHd + r;
-  const int8_t* w = W + row * d + q * seg;
+  const int8_t* w = W + row * d + q * 16;
   i32x4 wv[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k)
     wv[k] = __builtin_nontemporal_load(  // clamped: unconditional loads issue back to back
-        reinterpret_cast<const i32x4*>(w + min((uint32_t)k * 16, seg - 16)));
+        reinterpret_cast<const i32x4*>(w + min((uint32_t)k, last) * 64));
   const float srow = S[row];
   const uint32_t pos = st[1];
   const uint32_t lane = t & 63;
@@ -706,15 +708,15 @@ __global__ __launch_bounds__(256) void n2_qkv_kernel(
   const double rs = rope[lane & 31], rc = rope[32 + (lane & 31)];
   for (uint32_t i = t; i < d; i += 256) xs[i] = x[i];
   __syncthreads();
-  const float* xv = xs + q * seg;
+  const float* xv = xs + q * 16;
   float acc = 0.f;
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    if ((uint32_t)k * 16 >= seg) break;
+    if ((uint32_t)k > last) break;
     int8_t cb[16];
     __builtin_memcpy(cb, &wv[k], 16);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) acc = fmaf((float)cb[j], xv[k * 16 + j], acc);
+    for (int j = 0; j < 16; ++j) acc = fmaf((float)cb[j], xv[k * 64 + j], acc);
   }
   acc = nd::quad_sum(acc);
   if (q == 0) rows[r] = acc * srow;
