@@ -82,14 +82,31 @@ __device__ Best block_best(Best b, float* redv, uint32_t* redo) {
 }
 
 // Full-vocabulary max and sum of exp(logit - max), float64 accumulation.
+// The first kCache values of each thread (ids t + blockDim.x c) are loaded
+// together and kept in registers for the sum; larger vocabularies stream
+// the rest.  Each thread still adds its ids in increasing order.
+constexpr int kCache = 8;
 __device__ void log_normalizer(const float* __restrict__ logits, uint32_t vocab, float* redf,
                                double* redd, float* out_max, double* out_sum) {
+  float v[kCache];
+#pragma unroll
+  for (int c = 0; c < kCache; ++c) {
+    const uint32_t i = threadIdx.x + c * blockDim.x;
+    v[c] = i < vocab ? logits[i] : -INFINITY;
+  }
   float mx = -INFINITY;
-  for (uint32_t i = threadIdx.x; i < vocab; i += blockDim.x) mx = js_maxf(mx, logits[i]);
+#pragma unroll
+  for (int c = 0; c < kCache; ++c) mx = js_maxf(mx, v[c]);
+  for (uint32_t i = threadIdx.x + kCache * blockDim.x; i < vocab; i += blockDim.x)
+    mx = js_maxf(mx, logits[i]);
   mx = block_max_js(mx, redf);
   double sum = 0.0;
   const double md = (double)mx;
-  for (uint32_t i = threadIdx.x; i < vocab; i += blockDim.x) sum += exp((double)logits[i] - md);
+#pragma unroll
+  for (int c = 0; c < kCache; ++c)
+    if (threadIdx.x + c * blockDim.x < vocab) sum += exp((double)v[c] - md);
+  for (uint32_t i = threadIdx.x + kCache * blockDim.x; i < vocab; i += blockDim.x)
+    sum += exp((double)logits[i] - md);
   sum = block_sum_d(sum, redd);
   *out_max = mx;
   *out_sum = sum;
@@ -107,16 +124,31 @@ __global__ __launch_bounds__(kSelectThreads) void select_list_kernel(
   __syncthreads();
   const uint32_t n = allowed ? count : vocab;
   Best b{-INFINITY, kNone};
-  for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-    const uint32_t id = allowed ? allowed[i] : i;
-    if (id >= vocab) {
-      bad = 1;
-      continue;
+  // kCache candidates per thread per round: ids first, then their logits,
+  // all loads of a round in flight together (the winner does not depend on
+  // the order candidates are seen in: `better` is a total order).
+  for (uint32_t base = 0; base < n; base += kCache * blockDim.x) {
+    uint32_t ids[kCache];
+#pragma unroll
+    for (int c = 0; c < kCache; ++c) {
+      const uint32_t i = base + threadIdx.x + c * blockDim.x;
+      ids[c] = i < n ? (allowed ? allowed[i] : i) : kNone;
     }
-    const float v = logits[id];
-    if (v != v) continue;  // a NaN never beats anything
-    Best c{v, i};
-    if (better(c, b)) b = c;
+    float vals[kCache];
+#pragma unroll
+    for (int c = 0; c < kCache; ++c) vals[c] = ids[c] < vocab ? logits[ids[c]] : 0.f;
+#pragma unroll
+    for (int c = 0; c < kCache; ++c) {
+      const uint32_t i = base + threadIdx.x + c * blockDim.x;
+      if (i >= n) continue;
+      if (ids[c] >= vocab) {
+        bad = 1;
+        continue;
+      }
+      if (vals[c] != vals[c]) continue;  // a NaN never beats anything
+      const Best cand{vals[c], i};
+      if (better(cand, b)) b = cand;
+    }
   }
   b = block_best(b, redf, redo);
   float mx;
