@@ -648,6 +648,11 @@ hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uin
     // the per-workgroup x loads when there are enough rows.
     uint32_t racc = (bc <= 2 && row_count >= 8 * rpp * 256) ? 8 : 4;
     while (racc > 1 && rpp * racc * bc > kThreads) racc >>= 1;
+    // Small matrices: fewer passes while that adds workgroups (up to 256),
+    // keeping at least 4 outputs per workgroup.
+    while (racc > 1 && rpp * (racc / 2) * bc >= 4 &&
+           (row_count + rpp * racc - 1) / (rpp * racc) < 256)
+      racc >>= 1;
     const uint32_t blocks = (row_count + rpp * racc - 1) / (rpp * racc);
     MatvecFn f = racc == 8 ? pick_b<8>(bc, spt) : racc == 4 ? pick_b<4>(bc, spt)
                : racc == 2 ? pick_b<2>(bc, spt) : pick_b<1>(bc, spt);
