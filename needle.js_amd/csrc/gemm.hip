@@ -452,8 +452,12 @@ hipError_t nd_launch_gemm(const nd_mat* w, const int8_t* digits, const float* fm
                           uint32_t ldy, uint32_t M, int epilogue, hipStream_t s,
                           const nd_gemm_split* split) {
   if (M == 0) return hipSuccess;
-  const uint32_t ms = M > 64 ? 4 : 1;
-  const uint32_t ns = (M > 64 || w->n >= 8192) ? 2 : 1;
+  uint32_t ms = M > 64 ? 4 : 1;
+  uint32_t ns = (M > 64 || w->n >= 8192) ? 2 : 1;
+  // 64 x 128 tiles only while they still give 256 workgroups (a 128-row
+  // prompt through a 1536 x 512 projection would get 24); below that the
+  // 16 x 64 tiles spread the product over more CUs.
+  if (((w->n + 64 * ns - 1) / (64 * ns)) * ((M + 16 * ms - 1) / (16 * ms)) < 256) ms = ns = 1;
   const uint32_t tm = 16 * ms, tn = 64 * ns;
   GemmFn f = epilogue == 0 ? pick<0>(ms, ns) : epilogue == 1 ? pick<1>(ms, ns) : pick<2>(ms, ns);
   dim3 grid((w->n + tn - 1) / tn, (M + tm - 1) / tm, 1);
