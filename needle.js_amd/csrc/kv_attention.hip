@@ -175,7 +175,12 @@ __device__ __forceinline__ void unpack(const Tile<F32>& tl, int k, bool is_v, fl
 // Output gate of gated attention (model/runtime.ts:503-507): sigmoid(g).
 __device__ __forceinline__ float gate_factor(float g) { return 1.f / (1.f + __expf(-g)); }
 
-template <int REP, bool F32>
+// QB (prefill without a sliding window, one query head per KV head): the
+// REP rows are REP consecutive query positions z0 + r (z0 = REP blockIdx.z,
+// rows at or past `qrows` absent) of KV head blockIdx.y instead of REP heads
+// of one query, each row seeing cache positions [0, position]; every K/V
+// tile is then read once for REP queries.
+template <int REP, bool F32, bool QB = false>
 __global__ __launch_bounds__(256) void attention_kernel(
     const void* __restrict__ Kc, const void* __restrict__ Vc, const float* __restrict__ Ks,
     const float* __restrict__ Vs, const float* __restrict__ Q, float* __restrict__ out,
@@ -185,7 +190,7 @@ __global__ __launch_bounds__(256) void attention_kernel(
     uint32_t alloc, uint32_t sink, uint32_t window, Visible vis,
     const uint32_t* __restrict__ positions, uint32_t slot_space, uint32_t seq_kv_heads,
     uint32_t kv_stride_z,
-    uint32_t chunk_positions, uint32_t max_chunks, float score_scale) {
+    uint32_t chunk_positions, uint32_t max_chunks, float score_scale, uint32_t qrows) {
   // z indexes query rows: sequences of a batch (kv_stride_z = seq_kv_heads,
   // each with its own cache heads) or positions of one prefill (kv_stride_z
   // = 0, all reading the same cache heads).
@@ -200,7 +205,19 @@ __global__ __launch_bounds__(256) void attention_kernel(
   // holds a visible position iff slot <= position or the ring is full
   // (position >= alloc).  Otherwise the visible range of the row's position.
   uint32_t spos = 0;
-  if (slot_space) {
+  uint32_t rlim[QB ? REP : 1];  // QB: row r sees cache positions < rlim[r]
+  if constexpr (QB) {
+    uint32_t top = 0;
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      const uint32_t zr = z * REP + r;
+      const uint32_t pr = zr < qrows ? positions[zr] : 0;
+      if (zr < qrows && pr >= alloc) return;  // validated on entry; stay in bounds
+      rlim[r] = zr < qrows ? pr + 1 : 0;
+      top = max(top, rlim[r]);
+    }
+    vis = Visible{top, top, top};
+  } else if (slot_space) {
     spos = positions[z];
   } else if (positions) {
     if (window == 0 && positions[z] >= alloc) return;  // validated on entry; stay in bounds
@@ -211,14 +228,26 @@ __global__ __launch_bounds__(256) void attention_kernel(
   if (chunk >= nchunks) return;
   const uint32_t c_begin = chunk * chunk_positions;
   const uint32_t c_end = min(vis.count, c_begin + chunk_positions);
-  Q += (size_t)z * hq * kHeadDim;
-  out += (size_t)z * hq * kHeadDim;
+  if constexpr (!QB) {
+    Q += (size_t)z * hq * kHeadDim;
+    out += (size_t)z * hq * kHeadDim;
+  }
   const size_t head_base = ((size_t)layer * kv_heads + kvh) * alloc;
+  // Query row h: head h of this KV head, or (QB) query z REP + h (absent
+  // rows read query 0; they are never stored).
+  auto qrow = [&](int h) -> size_t {
+    if constexpr (QB) {
+      const uint32_t zr = z * REP + h;
+      return ((size_t)(zr < qrows ? zr : 0) * seq_kv_heads + kvh_local) * kHeadDim;
+    } else {
+      return (size_t)(kvh_local * REP + h) * kHeadDim;
+    }
+  };
 
   float q[REP][16];
 #pragma unroll
   for (int h = 0; h < REP; ++h) {
-    const float4* qp = reinterpret_cast<const float4*>(Q + (size_t)(kvh_local * REP + h) * kHeadDim + quad * 16);
+    const float4* qp = reinterpret_cast<const float4*>(Q + qrow(h) + quad * 16);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const float4 f = qp[c];
@@ -261,7 +290,9 @@ __global__ __launch_bounds__(256) void attention_kernel(
 #pragma unroll
         for (int i = 0; i < 16; ++i) d = fmaf(q[h][i], kc[i], d);
         d = nd::quad_sum(d);
-        p[h][k] = valid[k] ? d * cur.ks[k] * score_scale : -INFINITY;
+        bool ok = valid[k];
+        if constexpr (QB) ok = ok && t0 + trow + 16 * k < rlim[h];
+        p[h][k] = ok ? d * cur.ks[k] * score_scale : -INFINITY;
       }
     }
 #pragma unroll
@@ -281,7 +312,9 @@ __global__ __launch_bounds__(256) void attention_kernel(
       for (int i = 0; i < 16; ++i) acc[h][i] *= alpha;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const float e = valid[k] ? __expf(p[h][k] - m_new) : 0.f;
+        bool ok = valid[k];
+        if constexpr (QB) ok = ok && t0 + trow + 16 * k < rlim[h];
+        const float e = ok ? __expf(p[h][k] - m_new) : 0.f;
         p[h][k] = e;
         l[h] += e;
       }
@@ -372,6 +405,18 @@ __global__ __launch_bounds__(256) void attention_kernel(
   const size_t row0 = (size_t)z * hq + (size_t)kvh_local * REP;
   float* const out_z = out;  // already offset to row z
   const float* const gate_z = gate ? gate + (size_t)z * gate_ld : nullptr;
+  if constexpr (QB) {  // one chunk (the launch guarantees it), no gate
+    if (part == 0) {
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const uint32_t zr = z * REP + w_o[u] / kHeadDim;
+        if (zr < qrows)
+          out[((size_t)zr * seq_kv_heads + kvh_local) * kHeadDim + w_o[u] % kHeadDim] =
+              w_a[u] / w_l[u];
+      }
+    }
+    return;
+  }
   if (nchunks == 1) {
     if (part == 0) {
 #pragma unroll
@@ -543,10 +588,24 @@ struct AttnLaunch {
   uint32_t rep;                // query heads per KV head
   uint32_t batch;
   uint32_t max_count;          // bound on every sequence's visible count
+  bool qblock;                 // query blocks of a no-window prefill (rep 1, int8, no gate)
 };
 
 template <int REP, bool F32>
 hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
+  if constexpr (REP == 1 && !F32) {
+    // A prefill without a sliding window: 8 query positions per workgroup.
+    if (a.qblock) {
+      constexpr int kQb = 4;
+      hipLaunchKernelGGL((attention_kernel<kQb, false, true>),
+                         dim3(1, a.seq_kv_heads, (a.batch + kQb - 1) / kQb), dim3(64 * kWaves), 0,
+                         s, a.kv->k, a.kv->v, a.kv->ks, a.kv->vs, a.q, a.out, nullptr, 0u, nullptr,
+                         nullptr, nullptr, a.layer, a.kv->kv_heads, a.kv->alloc, a.kv->sink,
+                         a.kv->window, a.vis, a.positions, 0u, a.seq_kv_heads, 0u,
+                         a.max_count, 1u, 0.125f, a.batch);
+      return hipGetLastError();
+    }
+  }
   const uint32_t cp = chunk_positions_for(a.max_count, a.batch * a.seq_kv_heads,
                                           a.batch == 1 ? kTargetSingle : kTargetBatch);
   const uint32_t max_chunks = (a.max_count + cp - 1) / cp;
@@ -558,7 +617,7 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
                      a.gate, a.gate_ld, part_acc, part_ml, a.counters, a.layer, a.kv->kv_heads, a.kv->alloc,
                      a.kv->sink, a.kv->window, a.vis, a.positions, a.slot_space, a.seq_kv_heads,
                      a.kv_stride_z,
-                     cp, max_chunks, 0.125f);
+                     cp, max_chunks, 0.125f, a.batch);
   return hipGetLastError();
 }
 
@@ -664,6 +723,8 @@ hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint
   a.rep = rep;
   a.batch = batch;
   a.max_count = nv.count;
+  a.qblock = kv_stride_z == 0 && kv->window == 0 && rep == 1 && !gate &&
+             kv->mode != ND_KV_FLOAT32 && batch >= 64;
   return kv->mode == ND_KV_FLOAT32 ? launch_rep<true>(a, s) : launch_rep<false>(a, s);
 }
 
