@@ -175,11 +175,12 @@ __device__ __forceinline__ void unpack(const Tile<F32>& tl, int k, bool is_v, fl
 // Output gate of gated attention (model/runtime.ts:503-507): sigmoid(g).
 __device__ __forceinline__ float gate_factor(float g) { return 1.f / (1.f + __expf(-g)); }
 
-// QB (prefill without a sliding window, one query head per KV head): the
-// REP rows are REP consecutive query positions z0 + r (z0 = REP blockIdx.z,
-// rows at or past `qrows` absent) of KV head blockIdx.y instead of REP heads
-// of one query, each row seeing cache positions [0, position]; every K/V
-// tile is then read once for REP queries.
+// QB (a prefill whose positions all see [0, position]: no sliding window,
+// or a window no position outgrows): the REP rows are REP / G consecutive
+// query positions x the G = qgroup query heads of KV head blockIdx.y --
+// row r is query z0 + r / G (z0 = (REP / G) blockIdx.z, rows at or past
+// `qrows` absent), head G blockIdx.y + r % G, with its own causal limit --
+// so every K/V tile is read once for all of them.
 template <int REP, bool F32, bool QB = false>
 __global__ __launch_bounds__(256) void attention_kernel(
     const void* __restrict__ Kc, const void* __restrict__ Vc, const float* __restrict__ Ks,
@@ -190,7 +191,8 @@ __global__ __launch_bounds__(256) void attention_kernel(
     uint32_t alloc, uint32_t sink, uint32_t window, Visible vis,
     const uint32_t* __restrict__ positions, uint32_t slot_space, uint32_t seq_kv_heads,
     uint32_t kv_stride_z,
-    uint32_t chunk_positions, uint32_t max_chunks, float score_scale, uint32_t qrows) {
+    uint32_t chunk_positions, uint32_t max_chunks, float score_scale, uint32_t qrows,
+    uint32_t qgroup) {
   // z indexes query rows: sequences of a batch (kv_stride_z = seq_kv_heads,
   // each with its own cache heads) or positions of one prefill (kv_stride_z
   // = 0, all reading the same cache heads).
@@ -210,7 +212,7 @@ __global__ __launch_bounds__(256) void attention_kernel(
     uint32_t top = 0;
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
-      const uint32_t zr = z * REP + r;
+      const uint32_t zr = z * (REP / qgroup) + r / qgroup;
       const uint32_t pr = zr < qrows ? positions[zr] : 0;
       if (zr < qrows && pr >= alloc) return;  // validated on entry; stay in bounds
       rlim[r] = zr < qrows ? pr + 1 : 0;
@@ -237,8 +239,9 @@ __global__ __launch_bounds__(256) void attention_kernel(
   // rows read query 0; they are never stored).
   auto qrow = [&](int h) -> size_t {
     if constexpr (QB) {
-      const uint32_t zr = z * REP + h;
-      return ((size_t)(zr < qrows ? zr : 0) * seq_kv_heads + kvh_local) * kHeadDim;
+      const uint32_t zr = z * (REP / qgroup) + h / qgroup;
+      return ((size_t)(zr < qrows ? zr : 0) * seq_kv_heads * qgroup + kvh_local * qgroup +
+              h % qgroup) * kHeadDim;
     } else {
       return (size_t)(kvh_local * REP + h) * kHeadDim;
     }
@@ -405,14 +408,16 @@ __global__ __launch_bounds__(256) void attention_kernel(
   const size_t row0 = (size_t)z * hq + (size_t)kvh_local * REP;
   float* const out_z = out;  // already offset to row z
   const float* const gate_z = gate ? gate + (size_t)z * gate_ld : nullptr;
-  if constexpr (QB) {  // one chunk (the launch guarantees it), no gate
+  if constexpr (QB) {  // one chunk (the launch guarantees it)
     if (part == 0) {
 #pragma unroll
       for (int u = 0; u < kPer; ++u) {
-        const uint32_t zr = z * REP + w_o[u] / kHeadDim;
-        if (zr < qrows)
-          out[((size_t)zr * seq_kv_heads + kvh_local) * kHeadDim + w_o[u] % kHeadDim] =
-              w_a[u] / w_l[u];
+        const uint32_t r = w_o[u] / kHeadDim, zr = z * (REP / qgroup) + r / qgroup;
+        if (zr >= qrows) continue;
+        const uint32_t oi = (kvh_local * qgroup + r % qgroup) * kHeadDim + w_o[u] % kHeadDim;
+        float v = w_a[u] / w_l[u];
+        if (gate) v *= gate_factor(gate[(size_t)zr * gate_ld + oi]);
+        out[(size_t)zr * seq_kv_heads * qgroup * kHeadDim + oi] = v;
       }
     }
     return;
@@ -588,21 +593,22 @@ struct AttnLaunch {
   uint32_t rep;                // query heads per KV head
   uint32_t batch;
   uint32_t max_count;          // bound on every sequence's visible count
-  bool qblock;                 // query blocks of a no-window prefill (rep 1, int8, no gate)
+  bool qblock;                 // query blocks of a prefill whose positions see [0, position]
 };
 
 template <int REP, bool F32>
 hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
-  if constexpr (REP == 1 && !F32) {
-    // A prefill without a sliding window: 8 query positions per workgroup.
+  if constexpr ((REP == 1 || REP == 2) && !F32) {
+    // Query blocks: 4 rows per workgroup (4 positions x 1 head, or 2 x 2).
     if (a.qblock) {
       constexpr int kQb = 4;
       hipLaunchKernelGGL((attention_kernel<kQb, false, true>),
-                         dim3(1, a.seq_kv_heads, (a.batch + kQb - 1) / kQb), dim3(64 * kWaves), 0,
-                         s, a.kv->k, a.kv->v, a.kv->ks, a.kv->vs, a.q, a.out, nullptr, 0u, nullptr,
-                         nullptr, nullptr, a.layer, a.kv->kv_heads, a.kv->alloc, a.kv->sink,
-                         a.kv->window, a.vis, a.positions, 0u, a.seq_kv_heads, 0u,
-                         a.max_count, 1u, 0.125f, a.batch);
+                         dim3(1, a.seq_kv_heads, (a.batch + kQb / REP - 1) / (kQb / REP)),
+                         dim3(64 * kWaves), 0, s, a.kv->k, a.kv->v, a.kv->ks, a.kv->vs, a.q,
+                         a.out, a.gate, a.gate_ld, nullptr, nullptr, nullptr, a.layer,
+                         a.kv->kv_heads, a.kv->alloc, a.kv->sink, a.kv->window, a.vis,
+                         a.positions, 0u, a.seq_kv_heads, 0u, a.max_count, 1u, 0.125f, a.batch,
+                         (uint32_t)REP);
       return hipGetLastError();
     }
   }
@@ -617,7 +623,7 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
                      a.gate, a.gate_ld, part_acc, part_ml, a.counters, a.layer, a.kv->kv_heads, a.kv->alloc,
                      a.kv->sink, a.kv->window, a.vis, a.positions, a.slot_space, a.seq_kv_heads,
                      a.kv_stride_z,
-                     cp, max_chunks, 0.125f, a.batch);
+                     cp, max_chunks, 0.125f, a.batch, 1u);
   return hipGetLastError();
 }
 
@@ -723,8 +729,10 @@ hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint
   a.rep = rep;
   a.batch = batch;
   a.max_count = nv.count;
-  a.qblock = kv_stride_z == 0 && kv->window == 0 && rep == 1 && !gate &&
-             kv->mode != ND_KV_FLOAT32 && batch >= 64;
+  // Every position sees [0, position] when no window is outgrown (positions
+  // below the window also sit in their own slots).
+  a.qblock = kv_stride_z == 0 && (kv->window == 0 || max_position < kv->window) &&
+             (rep == 1 || rep == 2) && kv->mode != ND_KV_FLOAT32 && batch >= 64;
   return kv->mode == ND_KV_FLOAT32 ? launch_rep<true>(a, s) : launch_rep<false>(a, s);
 }
 
