@@ -100,6 +100,14 @@ nd_status nd_create(int32_t device, nd_ctx** out) {
     delete ctx;
     return nd_fail(nullptr, ND_ERR_BACKEND, "hipStreamCreate: %s", hipGetErrorString(e));
   }
+  // The fixed attention scratch of nd_attention_static_d, once per device.
+  e = nd_attention_scratch_setup(device);
+  if (e != hipSuccess) {
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return nd_fail(nullptr, ND_ERR_BACKEND, "attention scratch set-up on device %d: %s", device,
+                   hipGetErrorString(e));
+  }
   e = hipMalloc(&ctx->mv_split, kMatvecSplitBytes);
   if (e == hipSuccess) e = hipMemsetAsync(ctx->mv_split, 0, kMatvecSplitBytes, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
@@ -671,6 +679,36 @@ nd_status nd_attention_d(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t 
                    ctx->attn_partial_floats);
   ND_HIP(ctx, nd_launch_attention(kv, layer, position, q, q_heads, out, ctx->attn_partials,
                                   ctx->attn_counters, nd_pick_stream(ctx, stream)));
+  return ND_OK;
+}
+
+nd_status nd_attention_static_d(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t position,
+                                const float* q, uint32_t q_heads, float* out, void* stream) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_attention(ctx, kv, layer, position, q_heads);
+  if (st != ND_OK) return st;
+  if (!q || !out || (reinterpret_cast<uintptr_t>(q) & 15))
+    return nd_fail(ctx, ND_ERR_INVALID, "q must be a 16-byte aligned device pointer");
+  if (q_heads > kStaticAttnQHeads)
+    return nd_fail(ctx, ND_ERR_INVALID,
+                   "nd_attention_static_d: %u query heads exceed its fixed scratch (at most %u "
+                   "query heads; nd_attention_d has no such limit)",
+                   q_heads, kStaticAttnQHeads);
+  void* scratch = nd_attention_scratch(ctx->device);
+  if (!scratch)
+    return nd_fail(ctx, ND_ERR_BACKEND, "fixed attention scratch is not set up on device %d",
+                   ctx->device);
+  const nd_visible vis = nd_kv_visible(kv, position);
+  const size_t need =
+      (size_t)q_heads * nd_attention_chunks(vis.count, kv->kv_heads) * (kv->head_dim + 2);
+  if (need > kStaticAttnPartialWords)
+    return nd_fail(ctx, ND_ERR_INVALID,
+                   "nd_attention_static_d: %zu partial floats exceed its fixed scratch of %zu",
+                   need, kStaticAttnPartialWords);
+  float* partials = reinterpret_cast<float*>(scratch);
+  uint32_t* counters = reinterpret_cast<uint32_t*>(scratch) + kStaticAttnPartialWords;
+  ND_HIP(ctx, nd_launch_attention(kv, layer, position, q, q_heads, out, partials, counters,
+                                  nd_pick_stream(ctx, stream)));
   return ND_OK;
 }
 

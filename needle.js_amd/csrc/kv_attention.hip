@@ -5,6 +5,8 @@
 // (model/runtime.ts:186-204, 666-677).  A 64-dim code row is 64 bytes, so a
 // 16-position x 64-dim tile is one contiguous 1 KiB run that a wave reads
 // with 128-bit loads.
+#include <mutex>
+
 #include "nd_internal.hpp"
 #include "nd_wave.hpp"
 
@@ -639,6 +641,46 @@ hipError_t launch_rep(const AttnLaunch& a, hipStream_t s) {
 }
 
 }  // namespace
+
+// ------------------------------------------- fixed scratch (no allocation)
+//
+// The allocation-free attention entry point keeps its chunk partials and
+// arrival counters in this array instead of a context buffer.  Every GPU the
+// library runs on holds its own copy until the process ends.  Host code never
+// passes `scratch` itself to a kernel (in host code it names a host-side
+// stand-in): nd_attention_scratch_setup looks up each device's address once,
+// and launches take that address.  The counters are cleared at set-up and
+// every launch leaves them at zero; the partials are written before they are
+// read.  Launches that use the scratch on one GPU must not overlap.
+static_assert(kMaxChunks == 64, "the scratch holds 64 chunks per query head");
+static __device__ __align__(256) uint32_t scratch[kStaticAttnWords];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxScratchDevices] = {};
+}  // namespace
+
+hipError_t nd_attention_scratch_setup(int device) {
+  if (device < 0 || device >= kMaxScratchDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[device]) return hipSuccess;
+  void* p = nullptr;
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  if (!p) return hipErrorInvalidSymbol;
+  e = hipMemset(p, 0, kStaticAttnWords * sizeof(uint32_t));
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) return e;
+  g_scratch_dev[device] = p;
+  return hipSuccess;
+}
+
+void* nd_attention_scratch(int device) {
+  if (device < 0 || device >= kMaxScratchDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return g_scratch_dev[device];
+}
 
 nd_visible nd_kv_visible(const nd_kv* kv, uint32_t position) {
   nd_visible v;

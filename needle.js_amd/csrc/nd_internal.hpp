@@ -182,6 +182,18 @@ hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint
 // uses to elect the chunk that merges them (a counter per group of chunks,
 // then one per row and head), and leaves at zero again.
 constexpr uint32_t kAttnCounterStride = 16;
+// Fixed device scratch of nd_attention_static_d (kv_attention.hip): the chunk
+// partials of one query row -- acc [q_heads][chunks][64] then (max, sum)
+// [q_heads][chunks][2] -- for up to kStaticAttnQHeads query heads and the
+// kernel's 64 chunks, then kAttnCounterStride arrival counters per KV head.
+constexpr uint32_t kStaticAttnQHeads = 64;
+constexpr size_t kStaticAttnPartialWords = (size_t)kStaticAttnQHeads * 64 * (64 + 2);
+constexpr size_t kStaticAttnWords =
+    kStaticAttnPartialWords + (size_t)kStaticAttnQHeads * kAttnCounterStride;
+// Looks the scratch up on `device` (which must be current) once per device;
+// nd_attention_scratch returns its HBM address there (nullptr before set-up).
+hipError_t nd_attention_scratch_setup(int device);
+void* nd_attention_scratch(int device);
 //
 // One query row whose position is read from device memory (*position <=
 // max_position); out = attention * sigmoid(gate) elementwise when gate is set
