@@ -199,7 +199,10 @@ nd_status nd_kv_read(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t head
  * [q_heads][head_dim]; query head h reads KV head h / (q_heads / kv_heads);
  * scores are q.k * scale_k / sqrt(head_dim), softmax, out = sum w * v *
  * scale_v.  NeedleRuntime.#attention (model/runtime.ts:719-786) with
- * softmaxInPlace (model/math.ts:46-60). */
+ * softmaxInPlace (model/math.ts:46-60).  A long visible range is split over
+ * several workgroups whose partial results meet in the context's workspace
+ * (partials and arrival counters): enqueue the _d calls of one context on one
+ * stream. */
 nd_status nd_attention(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t position,
                        const float* q, uint32_t q_heads, float* out);
 nd_status nd_attention_d(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t position,
