@@ -325,6 +325,10 @@ nd_status nd_batch_step(nd_ctx* ctx, nd_batch* batch, uint32_t max_position, uin
 nd_status nd_batch_read(nd_ctx* ctx, nd_batch* batch, uint32_t* tokens, uint32_t* positions,
                         double* log_probabilities, float* logits);
 
+/* Copies the last layer's Q/K/V projections of the last step, [batch]
+ * [(heads + 2 kv_heads) * 64] f32 (as nd_prefill_read_projections). */
+nd_status nd_batch_read_projections(nd_ctx* ctx, nd_batch* batch, float* out);
+
 /* ------------------------------------------------------------------ prefill */
 
 typedef struct nd_prefill nd_prefill;
@@ -353,6 +357,13 @@ nd_status nd_prefill_set_tokens(nd_ctx* ctx, nd_prefill* prefill, const uint32_t
                                 uint32_t count, uint32_t position0);
 nd_status nd_prefill_run_d(nd_ctx* ctx, nd_prefill* prefill, nd_kv* kv, void* stream);
 nd_status nd_prefill_logits(nd_ctx* ctx, nd_prefill* prefill, float* logits);
+
+/* Copies the last layer's Q/K/V projections of the last pass -- [count]
+ * [(heads + 2 kv_heads) * 64] f32, rows q | k | v before the per-head norms
+ * and RoPE -- so that a caller can check that the codes stored for the last
+ * layer are #storeKV of the values this backend computed (no counterpart in
+ * the reference: a read-back of device state, like nd_kv_read). */
+nd_status nd_prefill_read_projections(nd_ctx* ctx, nd_prefill* prefill, float* out);
 
 /* Every step records its selected ids and log-probabilities at row t (the
  * step counter) of a [max_length][batch] history in HBM; copies rows

@@ -490,6 +490,16 @@ nd_status nd_batch_read(nd_ctx* ctx, nd_batch* b, uint32_t* tokens, uint32_t* po
   return ND_OK;
 }
 
+nd_status nd_batch_read_projections(nd_ctx* ctx, nd_batch* b, float* out) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!b || !out) return nd_fail(ctx, ND_ERR_INVALID, "NULL argument");
+  const size_t rows = (size_t)(b->dec->heads + 2 * b->dec->kv_heads) * kHd;
+  ND_HIP(ctx, hipMemcpyAsync(out, b->qkv, (size_t)b->batch * rows * 4, hipMemcpyDeviceToHost,
+                             ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ND_OK;
+}
+
 // One decode step for all sequences.  Reads tokens/positions/step from device
 // memory; with masks == 1 the step's allowed bitmasks are generated on the
 // device from mask_seed and applied, otherwise selection is unconstrained.
@@ -718,6 +728,17 @@ nd_status nd_prefill_logits(nd_ctx* ctx, nd_prefill* p, float* logits) {
   if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
   if (!p || !logits) return nd_fail(ctx, ND_ERR_INVALID, "NULL argument");
   ND_HIP(ctx, hipMemcpyAsync(logits, p->logits, (size_t)p->dec->vocab * 4, hipMemcpyDeviceToHost,
+                             ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return ND_OK;
+}
+
+nd_status nd_prefill_read_projections(nd_ctx* ctx, nd_prefill* p, float* out) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!p || !out) return nd_fail(ctx, ND_ERR_INVALID, "NULL argument");
+  if (p->count == 0) return nd_fail(ctx, ND_ERR_INVALID, "the prefill has not run");
+  const size_t rows = (size_t)(p->dec->heads + 2 * p->dec->kv_heads) * kHd;
+  ND_HIP(ctx, hipMemcpyAsync(out, p->qkv, (size_t)p->count * rows * 4, hipMemcpyDeviceToHost,
                              ctx->stream));
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return ND_OK;

@@ -93,6 +93,7 @@ SIGNATURES = {
     "nd_batch_set_state": (I32, [P, P, P, P, U32]),
     "nd_batch_step": (I32, [P, P, U32, U32, C.c_uint64, U32, P]),
     "nd_batch_read": (I32, [P, P, P, P, P, P]),
+    "nd_batch_read_projections": (I32, [P, P, P]),
     "nd_batch_history": (I32, [P, P, U32, U32, P, P]),
     "nd_prefill_create": (I32, [P, P, U32, U32, PP]),
     "nd_prefill_free": (I32, [P, P]),
@@ -100,6 +101,7 @@ SIGNATURES = {
     "nd_prefill_set_tokens": (I32, [P, P, P, U32, U32]),
     "nd_prefill_run_d": (I32, [P, P, P, P]),
     "nd_prefill_logits": (I32, [P, P, P]),
+    "nd_prefill_read_projections": (I32, [P, P, P]),
     "nd_needle_create": (I32, [P, P, PP]),
     "nd_needle_free": (I32, [P, P]),
     "nd_needle_reset": (I32, [P, P, U32, U32]),

@@ -150,6 +150,15 @@ class HipBatch:
                                                    L.ptr(lg) if logits else None), "nd_batch_read")
         return t, p, lp, lg
 
+    def read_projections(self):
+        """The last layer's Q/K/V projections of the last step, [batch][q|k|v]."""
+        g = self.decoder.geometry
+        out = np.empty((self.batch, (g.heads + 2 * g.kv_heads) * g.head_dim), np.float32)
+        self.backend._check(self.lib.nd_batch_read_projections(self.backend.ctx, self.handle,
+                                                               L.ptr(out)),
+                            "nd_batch_read_projections")
+        return out
+
     def history(self, first_step: int, steps: int):
         """Selected ids [steps][batch] and log-probabilities recorded on device."""
         ids = np.empty((steps, self.batch), np.uint32)
@@ -215,6 +224,15 @@ class HipPrefill:
         out = np.empty(self.decoder.geometry.vocab, np.float32)
         self.backend._check(self.lib.nd_prefill_logits(self.backend.ctx, self.handle,
                                                        L.ptr(out)), "nd_prefill_logits")
+        return out
+
+    def read_projections(self, count: int):
+        """The last layer's Q/K/V projections of the last run, [count][q|k|v]."""
+        g = self.decoder.geometry
+        out = np.empty((count, (g.heads + 2 * g.kv_heads) * g.head_dim), np.float32)
+        self.backend._check(self.lib.nd_prefill_read_projections(self.backend.ctx, self.handle,
+                                                                 L.ptr(out)),
+                            "nd_prefill_read_projections")
         return out
 
     def free(self) -> None:

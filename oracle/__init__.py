@@ -50,6 +50,8 @@ _SIG = {
     "or_kv_slot": (U32, [P, U32]),
     "or_kv_store": (C.c_int, [P, U32, U32, P, P]),
     "or_kv_export": (None, [P, U32, U32, P, P, P, P]),
+    "or_kv_capture": (C.c_int, [P, U32, U32]),
+    "or_kv_export_raw": (C.c_int, [P, U32, U32, U32, U32, P, P]),
     "or_attention": (C.c_int, [P, U32, U32, P, U32, P]),
 }
 
@@ -258,6 +260,7 @@ class KvCache:
                  head_dim=64):
         self.layers, self.kv_heads, self.head_dim = layers, kv_heads, head_dim
         self.float_mode = kv_cache == "float32"
+        self.max_length = max_length
         self.h = lib().or_kv_create(layers, kv_heads, head_dim, max_length, sink, window,
                                     1 if self.float_mode else 0)
         self.alloc = int(lib().or_kv_alloc(self.h))
@@ -277,6 +280,21 @@ class KvCache:
             kk = np.ascontiguousarray(k[i * per:(i + 1) * per])
             vv = np.ascontiguousarray(v[i * per:(i + 1) * per])
             _ok(lib().or_kv_store(self.h, layer, position + i, _p(kk), _p(vv)))
+
+    def capture(self, from_position: int = 0, count: int | None = None) -> None:
+        """Keep the K/V vectors stored from now on at positions [from_position,
+        +count) (their values before quantization; count defaults to the rest
+        of the cache)."""
+        n = int(self.max_length) - from_position if count is None else count
+        _ok(lib().or_kv_capture(self.h, from_position, n))
+
+    def read_raw(self, layer, head, from_position, count):
+        """Captured (k, v) vectors of positions [from_position, +count), each
+        [count][head_dim] float32."""
+        k = np.empty((count, self.head_dim), np.float32)
+        v = np.empty((count, self.head_dim), np.float32)
+        _ok(lib().or_kv_export_raw(self.h, layer, head, from_position, count, _p(k), _p(v)))
+        return k, v
 
     def read(self, layer, head):
         kc = np.zeros((self.alloc, self.head_dim), dtype=np.int8)
@@ -301,7 +319,9 @@ _SIG_MODEL = {
     "or_gen_kv_row": (None, [C.c_uint64, C.c_uint64, U32, C.c_float, C.c_float, P, P]),
     "or_kv_fill_synthetic": (None, [P, C.c_uint64, C.c_uint64, U32, C.c_float, C.c_float]),
     "or_synth_step": (C.c_int, [P, P, U32, U32, P, P]),
-    "or_synth_decode_batch": (C.c_int, [P, P, P, P, U32, U32, C.c_uint64, U32, P, P, U32]),
+    "or_synth_decode_batch": (C.c_int, [P, P, P, P, U32, U32, C.c_uint64, U32, P, P, U32, P,
+                                        U32, P]),
+    "or_synth_prefill": (C.c_int, [P, P, P, U32, U32, P, U32]),
 }
 
 
@@ -397,18 +417,36 @@ class SynthDecoder:
                                        _p(hidden) if want_hidden else None))
         return (logits, hidden) if want_hidden else logits
 
+    def prefill(self, cache: KvCache, tokens, position0: int = 0, threads: int = 1):
+        """NeedleRuntime.prefill: the logits of the last of `tokens` run at
+        positions [position0, +len(tokens)), bit-identical to that many
+        step() calls (evaluated layer by layer on `threads` threads)."""
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        logits = np.empty(self.geometry.vocab, np.float32)
+        _ok(_model_lib().or_synth_prefill(C.byref(self.struct), cache.h, _p(tokens), tokens.size,
+                                          position0, _p(logits), threads))
+        return logits
+
     def decode_batch(self, caches, tokens, start, steps: int, mask_seed: int, threshold24: int,
-                     threads: int = 1):
+                     threads: int = 1, check_steps=None):
+        """(ids [steps][b], log-probabilities [steps][b]), plus the logits
+        [len(check_steps)][b][vocab] of the listed steps when check_steps is
+        given."""
         b = len(caches)
         ptrs = (P * b)(*[c.h for c in caches])
         tokens = np.ascontiguousarray(tokens, np.uint32)
         start = np.ascontiguousarray(start, np.uint32)
         ids = np.empty((steps, b), np.uint32)
         lps = np.empty((steps, b), np.float64)
-        _ok(_model_lib().or_synth_decode_batch(C.byref(self.struct), ptrs, _p(tokens), _p(start),
-                                               b, steps, mask_seed, threshold24, _p(ids), _p(lps),
-                                               threads))
-        return ids, lps
+        checks = np.ascontiguousarray(check_steps if check_steps is not None else [], np.uint32)
+        check_logits = np.empty((checks.size, b, self.geometry.vocab), np.float32)
+        _ok(_model_lib().or_synth_decode_batch(
+            C.byref(self.struct), ptrs, _p(tokens), _p(start), b, steps, mask_seed, threshold24,
+            _p(ids), _p(lps), threads, _p(checks) if checks.size else None, checks.size,
+            _p(check_logits) if checks.size else None))
+        if check_steps is None:
+            return ids, lps
+        return ids, lps, check_logits
 
 
 # ------------------------------------------------------------------ Needle 2
@@ -551,7 +589,7 @@ class Needle2Runtime:
     def recorded_cells(self) -> int:
         return int(_n2_lib().or_n2_recorded_cells(self.h))
 
-    def kv_read(self, layer: int, head: int):
+    def _cache(self, fn):
         cache = KvCache.__new__(KvCache)
         g = self.model.geometry
         cache.layers, cache.kv_heads, cache.head_dim = g.layers, g.kv_heads, g.head_dim
@@ -559,6 +597,17 @@ class Needle2Runtime:
         cache.h = _n2_lib().or_n2_kv(self.h)
         cache.alloc = int(lib().or_kv_alloc(cache.h))
         try:
-            return cache.read(layer, head)
+            return fn(cache)
         finally:
             cache.h = None  # owned by the runtime
+
+    def kv_read(self, layer: int, head: int):
+        return self._cache(lambda c: c.read(layer, head))
+
+    def capture_kv(self, from_position: int, count: int) -> None:
+        """Keep the K/V vectors of positions [from_position, +count) before
+        quantization (see KvCache.capture)."""
+        self._cache(lambda c: c.capture(from_position, count))
+
+    def kv_read_raw(self, layer: int, head: int, from_position: int, count: int):
+        return self._cache(lambda c: c.read_raw(layer, head, from_position, count))

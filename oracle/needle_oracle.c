@@ -45,6 +45,12 @@
  *                       explicit matrix products).
  *   decoder steps       composition of the pinned primitives; checked for
  *                       prefill == repeated step and batch == single.
+ *   or_synth_prefill    bit-identical to repeated or_synth_step (codes,
+ *                       scales, captured vectors, logits) at several thread
+ *                       counts and start positions; tests/.
+ *   or_kv_capture,      storage only: the captured vectors equal the stored
+ *   or_kv_export_raw    inputs and re-quantize to the cache's codes; tests/.
+ *   decode checkpoints  equal to or_synth_step logits of the same steps.
  */
 #include <math.h>
 #include <pthread.h>
@@ -515,6 +521,11 @@ typedef struct {
   int float_mode; /* kvCache: "float32" stores raw values, scale 1 */
   int8_t *k8, *v8;
   float *kf, *vf, *ks, *vs;
+  /* Test capture: the f32 vectors handed to #storeKV for positions
+   * [raw_from, raw_from + raw_count), by position: [layers][kv_heads]
+   * [raw_count][head_dim]. */
+  float *kraw, *vraw;
+  uint32_t raw_from, raw_count;
 } or_kv;
 
 or_kv* or_kv_create(uint32_t layers, uint32_t kv_heads, uint32_t head_dim, uint32_t max_length,
@@ -544,7 +555,42 @@ or_kv* or_kv_create(uint32_t layers, uint32_t kv_heads, uint32_t head_dim, uint3
 void or_kv_destroy(or_kv* kv) {
   if (!kv) return;
   free(kv->k8); free(kv->v8); free(kv->kf); free(kv->vf); free(kv->ks); free(kv->vs);
+  free(kv->kraw); free(kv->vraw);
   free(kv);
+}
+
+/* Keeps, from now on, a copy of every K/V vector stored at a position in
+ * [from, from + count) (the values before quantization), for tests that check
+ * codes against the exact quotient x / s.  Not part of the reference;
+ * storage only. */
+int or_kv_capture(or_kv* kv, uint32_t from, uint32_t count) {
+  if (count == 0 || (uint64_t)from + count > kv->max_length) return OR_INVALID;
+  free(kv->kraw); free(kv->vraw);
+  size_t elems = (size_t)kv->layers * kv->kv_heads * count * kv->head_dim;
+  kv->kraw = (float*)calloc(elems, sizeof(float));
+  kv->vraw = (float*)calloc(elems, sizeof(float));
+  kv->raw_from = from;
+  kv->raw_count = count;
+  return (kv->kraw && kv->vraw) ? OR_OK : OR_INVALID;
+}
+
+static size_t kv_raw_base(const or_kv* kv, uint32_t layer, uint32_t head, uint32_t position) {
+  return (((size_t)layer * kv->kv_heads + head) * kv->raw_count + (position - kv->raw_from)) *
+         kv->head_dim;
+}
+
+/* Copies the captured vectors of positions [from, from + count) of one
+ * (layer, head): k, v are [count][head_dim]. */
+int or_kv_export_raw(const or_kv* kv, uint32_t layer, uint32_t head, uint32_t from, uint32_t count,
+                     float* k, float* v) {
+  if (!kv->kraw || from < kv->raw_from ||
+      (uint64_t)from + count > (uint64_t)kv->raw_from + kv->raw_count ||
+      layer >= kv->layers || head >= kv->kv_heads)
+    return OR_INVALID;
+  size_t base = kv_raw_base(kv, layer, head, from);
+  memcpy(k, kv->kraw + base, sizeof(float) * (size_t)count * kv->head_dim);
+  memcpy(v, kv->vraw + base, sizeof(float) * (size_t)count * kv->head_dim);
+  return OR_OK;
 }
 
 uint32_t or_kv_alloc(const or_kv* kv) { return kv->alloc; }
@@ -578,6 +624,11 @@ int or_kv_store(or_kv* kv, uint32_t layer, uint32_t position, const float* k, co
     } else {
       or_kv_quantize(kh, kv->head_dim, kv->k8 + base, kv->ks + si);
       or_kv_quantize(vh, kv->head_dim, kv->v8 + base, kv->vs + si);
+    }
+    if (kv->kraw && position >= kv->raw_from && position - kv->raw_from < kv->raw_count) {
+      size_t rb = kv_raw_base(kv, layer, h, position);
+      memcpy(kv->kraw + rb, kh, sizeof(float) * kv->head_dim);
+      memcpy(kv->vraw + rb, vh, sizeof(float) * kv->head_dim);
     }
   }
   return OR_OK;
@@ -733,6 +784,53 @@ static void synth_matvec(const or_mat* m, const float* x, float* y) {
   or_matvec_i8(m->w, m->s, m->n, m->k, m->k, x, 1, 0, m->n, y);
 }
 
+/* First half of layer l for one token at `position`: attention input, Q/K/V
+ * projections, per-head norms, RoPE, then #storeKV.  q receives the rotated
+ * query; a, k, v are scratch ([dim], [kv_heads * head_dim] x 2). */
+static void synth_layer_qkv(const or_synth* md, or_kv* kv, uint32_t l, uint32_t position,
+                            const float* x, float* a, float* q, float* k, float* v) {
+  uint32_t d = md->dim, hd = md->head_dim;
+  or_rms_norm(x, md->attn_norm + (size_t)l * d, d, a);
+  synth_matvec(&md->wq[l], a, q);
+  synth_matvec(&md->wk[l], a, k);
+  synth_matvec(&md->wv[l], a, v);
+  for (uint32_t hh = 0; hh < md->heads; hh++)
+    or_rms_norm_slice(q, hh * hd, hd, md->q_norm + (size_t)l * hd);
+  for (uint32_t hh = 0; hh < md->kv_heads; hh++)
+    or_rms_norm_slice(k, hh * hd, hd, md->k_norm + (size_t)l * hd);
+  or_rope(q, md->heads, hd, position, md->rope_theta);
+  or_rope(k, md->kv_heads, hd, position, md->rope_theta);
+  or_kv_store(kv, l, position, k, v);
+}
+
+/* Second half: #attention over the cache, x += Wo o, then the FFN residual.
+ * x is updated in place; a, o, p, h are scratch. */
+static void synth_layer_out(const or_synth* md, const or_kv* kv, uint32_t l, uint32_t position,
+                            float* x, const float* q, float* a, float* o, float* p, float* h) {
+  uint32_t d = md->dim;
+  or_attention(kv, l, position, q, md->heads, o);
+  synth_matvec(&md->wo[l], o, p);
+  for (uint32_t i = 0; i < d; i++) x[i] = (float)((double)x[i] + (double)p[i]);
+  or_rms_norm(x, md->ffn_norm + (size_t)l * d, d, a);
+  synth_matvec(&md->wup[l], a, h);
+  for (uint32_t i = 0; i < md->ffn; i++) h[i] = (float)or_silu((double)h[i]);
+  synth_matvec(&md->wdown[l], h, p);
+  for (uint32_t i = 0; i < d; i++) x[i] = (float)((double)x[i] + (double)p[i]);
+}
+
+static void synth_embed(const or_synth* md, uint32_t token, float* x) {
+  uint32_t d = md->dim;
+  or_row_i8(md->embedding.w, md->embedding.s, md->embedding.n, md->embedding.k,
+            md->embedding.k, token, x);
+  double es = sqrt((double)d);
+  for (uint32_t i = 0; i < d; i++) x[i] = (float)((double)x[i] * es);
+}
+
+static void synth_logits(const or_synth* md, const float* x, float* a, float* logits) {
+  or_rms_norm(x, md->final_norm, md->dim, a);
+  synth_matvec(&md->embedding, a, logits);
+}
+
 /* One decode step of one sequence at `position`; logits may be NULL. */
 int or_synth_step(const or_synth* md, or_kv* kv, uint32_t token, uint32_t position,
                   float* logits, float* hidden_out) {
@@ -747,37 +845,104 @@ int or_synth_step(const or_synth* md, or_kv* kv, uint32_t token, uint32_t positi
   float* o = (float*)malloc(sizeof(float) * qw);
   float* p = (float*)malloc(sizeof(float) * d);
   float* h = (float*)malloc(sizeof(float) * md->ffn);
-  or_row_i8(md->embedding.w, md->embedding.s, md->embedding.n, md->embedding.k,
-            md->embedding.k, token, x);
-  double es = sqrt((double)d);
-  for (uint32_t i = 0; i < d; i++) x[i] = (float)((double)x[i] * es);
+  synth_embed(md, token, x);
   for (uint32_t l = 0; l < md->layers; l++) {
-    or_rms_norm(x, md->attn_norm + (size_t)l * d, d, a);
-    synth_matvec(&md->wq[l], a, q);
-    synth_matvec(&md->wk[l], a, k);
-    synth_matvec(&md->wv[l], a, v);
-    for (uint32_t hh = 0; hh < md->heads; hh++)
-      or_rms_norm_slice(q, hh * hd, hd, md->q_norm + (size_t)l * hd);
-    for (uint32_t hh = 0; hh < md->kv_heads; hh++)
-      or_rms_norm_slice(k, hh * hd, hd, md->k_norm + (size_t)l * hd);
-    or_rope(q, md->heads, hd, position, md->rope_theta);
-    or_rope(k, md->kv_heads, hd, position, md->rope_theta);
-    or_kv_store(kv, l, position, k, v);
-    or_attention(kv, l, position, q, md->heads, o);
-    synth_matvec(&md->wo[l], o, p);
-    for (uint32_t i = 0; i < d; i++) x[i] = (float)((double)x[i] + (double)p[i]);
-    or_rms_norm(x, md->ffn_norm + (size_t)l * d, d, a);
-    synth_matvec(&md->wup[l], a, h);
-    for (uint32_t i = 0; i < md->ffn; i++) h[i] = (float)or_silu((double)h[i]);
-    synth_matvec(&md->wdown[l], h, p);
-    for (uint32_t i = 0; i < d; i++) x[i] = (float)((double)x[i] + (double)p[i]);
+    synth_layer_qkv(md, kv, l, position, x, a, q, k, v);
+    synth_layer_out(md, kv, l, position, x, q, a, o, p, h);
   }
   if (hidden_out) memcpy(hidden_out, x, sizeof(float) * d);
-  if (logits) {
-    or_rms_norm(x, md->final_norm, d, a);
-    synth_matvec(&md->embedding, a, logits);
-  }
+  if (logits) synth_logits(md, x, a, logits);
   free(x); free(a); free(q); free(k); free(v); free(o); free(p); free(h);
+  return OR_OK;
+}
+
+/* NeedleRuntime.prefill (runtime.ts:227-243) of `count` tokens at positions
+ * [position0, position0 + count): the same per-token arithmetic as `count`
+ * calls of or_synth_step, evaluated layer by layer -- first every token's
+ * Q/K/V and #storeKV, then every token's attention and residual updates --
+ * with the tokens of each half spread over `threads` POSIX threads.  The
+ * result is bit-identical to the sequential steps: a step stores its own
+ * K/V before it attends (runtime.ts:501-502) and attends to positions <= its
+ * own, all of which the first half has stored, and no two positions share a
+ * slot (position0 + count <= the cache's slots).  Writes the last position's
+ * logits when logits != NULL. */
+typedef struct {
+  const or_synth* md;
+  or_kv* kv;
+  const uint32_t* tokens;
+  uint32_t count, position0, layer, half;
+  float *X, *Q; /* [count][dim], [count][heads * head_dim] */
+  uint32_t next;
+  pthread_mutex_t lock;
+} or_prefill_job;
+
+static void* prefill_worker(void* arg) {
+  or_prefill_job* job = (or_prefill_job*)arg;
+  const or_synth* md = job->md;
+  uint32_t d = md->dim, qw = md->heads * md->head_dim, kw = md->kv_heads * md->head_dim;
+  float* a = (float*)malloc(sizeof(float) * d);
+  float* k = (float*)malloc(sizeof(float) * kw);
+  float* v = (float*)malloc(sizeof(float) * kw);
+  float* o = (float*)malloc(sizeof(float) * qw);
+  float* p = (float*)malloc(sizeof(float) * d);
+  float* h = (float*)malloc(sizeof(float) * md->ffn);
+  for (;;) {
+    pthread_mutex_lock(&job->lock);
+    uint32_t i = job->next++;
+    pthread_mutex_unlock(&job->lock);
+    if (i >= job->count) break;
+    float* x = job->X + (size_t)i * d;
+    float* q = job->Q + (size_t)i * qw;
+    uint32_t position = job->position0 + i;
+    if (job->half == 0) {
+      if (job->layer == 0) synth_embed(md, job->tokens[i], x);
+      synth_layer_qkv(md, job->kv, job->layer, position, x, a, q, k, v);
+    } else {
+      synth_layer_out(md, job->kv, job->layer, position, x, q, a, o, p, h);
+    }
+  }
+  free(a); free(k); free(v); free(o); free(p); free(h);
+  return NULL;
+}
+
+int or_synth_prefill(const or_synth* md, or_kv* kv, const uint32_t* tokens, uint32_t count,
+                     uint32_t position0, float* logits, uint32_t threads) {
+  if (count == 0 || (uint64_t)position0 + count > kv->alloc ||
+      (uint64_t)position0 + count > kv->max_length)
+    return OR_INVALID;
+  for (uint32_t i = 0; i < count; i++)
+    if (tokens[i] >= md->vocab) return OR_INVALID;
+  if (threads < 1) threads = 1;
+  if (threads > count) threads = count;
+  or_prefill_job job;
+  memset(&job, 0, sizeof job);
+  job.md = md;
+  job.kv = kv;
+  job.tokens = tokens;
+  job.count = count;
+  job.position0 = position0;
+  job.X = (float*)malloc(sizeof(float) * (size_t)count * md->dim);
+  job.Q = (float*)malloc(sizeof(float) * (size_t)count * md->heads * md->head_dim);
+  pthread_mutex_init(&job.lock, NULL);
+  pthread_t* tid = (pthread_t*)malloc(sizeof(pthread_t) * threads);
+  for (uint32_t l = 0; l < md->layers; l++) {
+    for (uint32_t half = 0; half < 2; half++) {
+      job.layer = l;
+      job.half = half;
+      job.next = 0;
+      for (uint32_t t = 0; t < threads; t++) pthread_create(&tid[t], NULL, prefill_worker, &job);
+      for (uint32_t t = 0; t < threads; t++) pthread_join(tid[t], NULL);
+    }
+  }
+  if (logits) {
+    float* a = (float*)malloc(sizeof(float) * md->dim);
+    synth_logits(md, job.X + (size_t)(count - 1) * md->dim, a, logits);
+    free(a);
+  }
+  pthread_mutex_destroy(&job.lock);
+  free(tid);
+  free(job.X);
+  free(job.Q);
   return OR_OK;
 }
 
@@ -814,6 +979,9 @@ typedef struct {
   uint64_t mask_seed;
   uint32_t* out_ids;    /* [steps][batch] */
   double* out_logprob;  /* [steps][batch] */
+  const uint32_t* check_steps; /* steps whose logits are kept (may be NULL) */
+  uint32_t n_check;
+  float* check_logits;  /* [n_check][batch][vocab] */
   uint32_t next;        /* work counter */
   pthread_mutex_t lock;
   int status;
@@ -835,6 +1003,10 @@ static void* batch_worker(void* arg) {
         job->status = OR_INVALID;
         break;
       }
+      for (uint32_t c = 0; c < job->n_check; c++)
+        if (job->check_steps[c] == t)
+          memcpy(job->check_logits + ((size_t)c * job->batch + b) * md->vocab, logits,
+                 sizeof(float) * md->vocab);
       or_gen_mask(or_splitmix64_at(job->mask_seed, (uint64_t)t * 65536 + b), md->vocab,
                   job->threshold24, mask);
       uint32_t id;
@@ -853,9 +1025,11 @@ static void* batch_worker(void* arg) {
 int or_synth_decode_batch(const or_synth* md, or_kv** kvs, const uint32_t* tokens,
                           const uint32_t* start, uint32_t batch, uint32_t steps,
                           uint64_t mask_seed, uint32_t threshold24, uint32_t* out_ids,
-                          double* out_logprob, uint32_t threads) {
+                          double* out_logprob, uint32_t threads, const uint32_t* check_steps,
+                          uint32_t n_check, float* check_logits) {
   or_batch_job job = {md, kvs, tokens, start, batch, steps, threshold24, mask_seed,
-                      out_ids, out_logprob, 0, PTHREAD_MUTEX_INITIALIZER, OR_OK};
+                      out_ids, out_logprob, check_steps, check_steps ? n_check : 0,
+                      check_logits, 0, PTHREAD_MUTEX_INITIALIZER, OR_OK};
   if (threads < 1) threads = 1;
   if (threads > batch) threads = batch;
   pthread_t* tid = (pthread_t*)malloc(sizeof(pthread_t) * threads);

@@ -1,10 +1,14 @@
 """GPU parity of the Needle 2 runtime (nd_needle_*) against the oracle's
 NeedleRuntime.step restatement, through the C ABI.
 
-Bars: logits within 1e-3 relative (normwise: one K/V code that rounds the
-other way at a boundary moves later outputs by ~1e-4 relative), appended
-KV codes within one code and mostly identical, greedy token sequences and
-selected ids identical, log-probabilities within 1e-3.
+Bars: logits within 1e-3 of the largest logit (one K/V code that rounds
+the other way at a boundary moves later outputs by ~1e-4 relative); greedy
+token sequences and selected ids identical; log-probabilities within 1e-3.
+Appended KV codes: in layer 0, whose inputs agree with the oracle's to fp32
+rounding, equal to the oracle's or one apart with the oracle's quotient
+x / s within 1e-4 of the rounding boundary between them; in every layer at
+most one code apart (deeper layers see inputs that drifted by the model's
+own fp32 rounding).
 """
 
 import dataclasses
@@ -14,6 +18,7 @@ import numpy as np
 import pytest
 
 import oracle
+from helpers import assert_codes_or_boundary_flips
 from needle_hip import NeedleError, NeedleModel, synth
 from needle_hip.needle2 import Needle2Geometry, Needle2Weights
 
@@ -33,6 +38,40 @@ def say(*args):
 def close(got, want, what):
     err = np.abs(got.astype(np.float64) - want.astype(np.float64))
     assert err.max() <= 1e-3 * np.abs(want).max(), (what, float(err.max()))
+
+
+def slot_positions(written, alloc, sink, window):
+    """The position whose K/V each cache slot holds once positions [0,
+    written) were stored (#kvSlot, model/runtime.ts:659-664); -1 if none."""
+    pos = np.full(alloc, -1)
+    for p in range(written):
+        pos[p if window == 0 or p < sink else sink + (p - sink) % window] = p
+    return pos
+
+
+def check_kv(model, ref, g, written, sink, what):
+    """The GPU cache against the oracle's (which captured its vectors before
+    quantization from position 0): see the module docstring for the bars."""
+    alloc = min(g.max_length, sink + g.kv_window) if g.kv_window else g.max_length
+    pos = slot_positions(written, alloc, sink, g.kv_window)
+    used = np.flatnonzero(pos >= 0)
+    for layer in range(g.layers):
+        for h in range(g.kv_heads):
+            gk, gv, gks, gvs = model.session.kv_read(layer, h)
+            rk, rv, rks, rvs = ref.kv_read(layer, h)
+            assert gk.shape == rk.shape
+            if layer == 0:
+                raw_k, raw_v = ref.kv_read_raw(0, h, 0, written)
+                for got, want, raw in ((gk, rk, raw_k), (gv, rv, raw_v)):
+                    assert_codes_or_boundary_flips(got[used], want[used], raw[pos[used]], 1e-4,
+                                                   f"{what} layer 0 head {h}")
+            else:
+                for got, want in ((gk, rk), (gv, rv)):
+                    d = np.abs(got[used].astype(int) - want[used].astype(int))
+                    assert d.max() <= 1, (what, layer, h)
+            tol = 1e-5 if layer == 0 else 1e-2
+            np.testing.assert_allclose(gks[used], rks[used], rtol=tol)
+            np.testing.assert_allclose(gvs[used], rvs[used], rtol=tol)
 
 
 def close_confidence(got, want, what):
@@ -57,6 +96,7 @@ def test_step_logits_and_kv_match_oracle(small, sink):
     rt = model.create_runtime()
     rt.reset(SMALL.max_length, sink)
     ref = oracle.Needle2(w).runtime(SMALL.max_length, sink)
+    ref.capture_kv(0, SMALL.max_length)
     tokens = synth.Stream(5, f"n2tok{sink}").integers(30, 0, SMALL.vocab - 1)
     tokens[7:10] = tokens[3:6]  # repeated n-grams hit the same engram rows
     for i, t in enumerate(tokens):
@@ -66,16 +106,8 @@ def test_step_logits_and_kv_match_oracle(small, sink):
         assert rt.position == i + 1
         if i in (0, 9, len(tokens) - 1):
             close_confidence(rt.resolve_confidence(), ref.confidence(), ("confidence", sink, i))
-    for layer in (0, SMALL.layers - 1):
-        for h in range(SMALL.kv_heads):
-            gk, gv, gks, gvs = model.session.kv_read(layer, h)
-            rk, rv, rks, rvs = ref.kv_read(layer, h)
-            assert gk.shape == rk.shape == (sink + SMALL.kv_window, 64)
-            for g, r in ((gk, rk), (gv, rv)):
-                d = np.abs(g.astype(int) - r.astype(int))
-                assert d.max() <= 1 and (d == 0).mean() > 0.95
-            for g, r in ((gks, rks), (gvs, rvs)):
-                np.testing.assert_allclose(g, r, rtol=1e-3)
+    assert model.session.kv_read(0, 0)[0].shape == (sink + SMALL.kv_window, 64)
+    check_kv(model, ref, SMALL, len(tokens), sink, f"steps sink {sink}")
 
 
 @pytest.mark.parametrize("heads,kv_heads,window,length", [(2, 2, 8, 48), (4, 2, 0, 600)])
@@ -241,6 +273,7 @@ def test_generate_full_geometry_greedy_identical(hip):
         prompt = synth.Stream(2026, "needle2.prompt").integers(128, 0, g.vocab - 1)
         res = model.generate(prompt, max_new_tokens=64, eos=None)
         ref = oracle.Needle2(w).runtime(128 + 64, 0)
+        ref.capture_kv(0, 128 + 64)
         for t in prompt[:-1]:
             ref.step(int(t), want_logits=False)
         logits = ref.step(int(prompt[-1]))
@@ -253,6 +286,9 @@ def test_generate_full_geometry_greedy_identical(hip):
                 logits = ref.step(tok)
         assert res.token_ids == ids
         np.testing.assert_allclose(res.token_log_probabilities, lps, rtol=1e-3, atol=1e-3)
+        # 128 prompt positions and 63 generated ones were stored (the last
+        # generated token is never run), over the 256-position window.
+        check_kv(model, ref, g, 128 + 63, 0, "generate")
         # the graph-replayed steps pooled every token they ran
         close_confidence(model.session.confidence(), ref.confidence(), "generate confidence")
     finally:
@@ -277,13 +313,16 @@ def test_confidence_absent_or_disabled(hip):
 
 
 @pytest.mark.parametrize("window,sink,n_prompt,max_length",
-                         [(0, 0, 40, 64), (16, 3, 30, 64), (8, 0, 33, 64), (0, 0, 280, 300)])
+                         [(0, 0, 40, 64), (16, 3, 30, 64), (8, 0, 33, 64), (0, 0, 280, 300),
+                          (128, 3, 100, 160)])
 def test_batched_prefill_then_steps(hip, window, sink, n_prompt, max_length):
     """Prompt positions whose cache slots do not wrap run as one batched pass
     (int8 MFMA projections, one mix workgroup per position), the rest as
     steps; logits, every appended KV row and the engram ring handed to the
     following steps must agree with the oracle's sequential steps (the
-    300-position case batches a prompt longer than one attention chunk)."""
+    300-position case batches a prompt longer than one attention chunk; the
+    100-token prompt under a 128-position window with 3 sinks runs the
+    query-block attention of a windowed cache with sinks)."""
     say("needle2 batched prefill", window, sink, n_prompt, max_length)
     g = Needle2Geometry(**{**SMALL.__dict__, "kv_window": window, "max_length": max_length})
     w = Needle2Weights(g, 41)
@@ -292,6 +331,7 @@ def test_batched_prefill_then_steps(hip, window, sink, n_prompt, max_length):
         rt = model.create_runtime()
         rt.reset(g.max_length, sink)
         ref = oracle.Needle2(w).runtime(g.max_length, sink)
+        ref.capture_kv(0, g.max_length)
         prompt = synth.Stream(12, f"n2pf{window}").integers(n_prompt, 0, g.vocab - 1)
         prompt[10:13] = prompt[2:5]
         got = rt.prefill(prompt)
@@ -299,17 +339,7 @@ def test_batched_prefill_then_steps(hip, window, sink, n_prompt, max_length):
             want = ref.step(int(t))
         close(got, want, "prefill logits")
         close_confidence(rt.resolve_confidence(), ref.confidence(), "batched prefill confidence")
-        alloc = min(g.max_length, sink + window) if window else g.max_length
-        written = min(n_prompt, alloc)  # slots fill in order; the rest were never stored
-        for layer in (0, g.layers - 1):
-            for h in range(g.kv_heads):
-                for a_, b_ in zip(model.session.kv_read(layer, h), ref.kv_read(layer, h)):
-                    a_, b_ = a_[:written], b_[:written]
-                    if a_.dtype == np.int8:
-                        d = np.abs(a_.astype(int) - b_.astype(int))
-                        assert d.max() <= 1 and (d == 0).mean() > 0.95, (layer, h)
-                    else:
-                        np.testing.assert_allclose(a_, b_, rtol=1e-3)
+        check_kv(model, ref, g, n_prompt, sink, "batched prefill")
         tok = int(np.argmax(got))
         for i in range(6):  # steps after the batch read its engram ring and cache
             want = ref.step(tok)

@@ -1,30 +1,44 @@
 """GPU parity of the one-pass prefill against the oracle's sequential steps.
 
 The oracle prefill is the reference's: one step per prompt token
-(model/runtime.ts:227-243).  Bars: KV codes identical except where a value
-sits on a rounding boundary (at most one code apart, at most 0.5% of the
-codes; layer 0 measures ~1e-5); the last position's logits within 1e-3
-relative normwise and the same greedy token; and a prefill split at any
-position equals the unsplit one exactly.
+(model/runtime.ts:227-243), evaluated layer by layer on several host threads
+(bit-identical to the sequential steps, pinned on the CPU).  Bars:
 
-Why normwise end to end: a K/V element whose x/s lies within ~1e-5 of a
-half-integer rounds to the other code when the GPU's fp32 projection differs
-from the oracle's float64 one in the last bits; one such code shifts later
-attention outputs by up to ~5e-4 relative (measured), so elementwise
-1e-3/1e-4 is the per-kernel bar (matvec, matmul, attention on identical
-inputs) and the whole model is held to the relative bar normwise.
+* layer 0, whose inputs agree with the oracle's to fp32 rounding: every K/V
+  code equals the oracle's, or is one apart with the oracle's exact quotient
+  x / s within 1e-4 of the half-integer between the two codes (a value on a
+  rounding boundary; measured <= 3e-5 at 2048 tokens);
+* the last layer, checked against the oracle's #storeKV of the backend's own
+  last-layer projections (runtime.ts:479-501 applied to what the GPU
+  computed): keys equal up to flips within 1e-5 of a boundary (the per-head
+  norm and rotation run in float64 on both sides, so their f32 results
+  agree to the last bit almost always), values and value scales bit-exact;
+* every layer: codes at most one apart from the oracle's.  Deeper layers see
+  inputs that have drifted from the oracle's (each layer's fp32 rounding and
+  the flipped codes of earlier layers, amplified by the random weights: the
+  key scales of layer 7 differ by up to 1.9e-3 relative at 2048 tokens), so
+  their codes differ from the oracle's more often (0.33% at layer 7), and
+  the last-layer check above is what shows such codes are the correct
+  rounding of the GPU's values;
+* the last position's logits within 1e-3 relative both normwise and
+  elementwise against the largest logit (measured 4.9e-5 and 3.7e-5 at 2048
+  tokens), and the same greedy token;
+* a prefill split at any position equals the unsplit one.
 """
 
+import os
 import sys
 
 import numpy as np
 import pytest
 
 import oracle
+from helpers import assert_codes_or_boundary_flips, storekv_of_projections
 from needle_hip import HipKvCache, NeedleError, synth
 from needle_hip.models import DecoderGeometry, DecoderWeights, HipDecoder, HipPrefill
 
 pytestmark = pytest.mark.gpu
+THREADS = min(16, os.cpu_count() or 1)
 
 
 def say(*args):
@@ -38,35 +52,47 @@ def compare(hip, g, n, seed):
     cache = HipKvCache(hip, g.layers, g.kv_heads, max_length=n)
     tokens = synth.Stream(seed, "prompt").integers(n, 0, g.vocab - 1)
     logits = pre.run(cache, tokens)
+    proj = pre.read_projections(n)
     ref = oracle.SynthDecoder(weights)
     rc = ref.new_cache(n)
-    want = None
-    for p, t in enumerate(tokens):
-        want = ref.step(rc, int(t), p)
-    total = differ = 0
+    rc.capture(0, n)
+    want = ref.prefill(rc, tokens, 0, threads=THREADS)
+    last = g.layers - 1
+    tf = storekv_of_projections(proj, g.heads, g.kv_heads, weights.k_norm[last],
+                                ref.struct.rope_theta, np.arange(n))
+    _, _, tk, tks, tv, tvs = tf
     for l in range(g.layers):
+        differ = 0
         for h in range(g.kv_heads):
             got_k, got_v, got_ks, got_vs = cache.read(l, h)
             ref_k, ref_v, ref_ks, ref_vs = rc.read(l, h)
-            for a, b in ((got_k, ref_k), (got_v, ref_v)):
-                d = np.abs(a.astype(int) - b.astype(int))
-                assert d.max() <= 1, (l, h)
-                total += d.size
-                differ += int((d != 0).sum())
-            np.testing.assert_allclose(got_ks, ref_ks, rtol=1e-3)
-            np.testing.assert_allclose(got_vs, ref_vs, rtol=1e-3)
-            if l == 0:  # inputs of layer 0 are bit-exact: scales agree to fp32
-                np.testing.assert_allclose(got_ks, ref_ks, rtol=1e-6)
-    # Layer 0 flips ~1e-5 of its codes; each flip perturbs later layers, whose
-    # flip rate measures ~1e-3 (2-layer GQA model: 310 of 204800).
-    assert differ <= max(8, total * 5e-3), (differ, total)
-    err = np.abs(logits.astype(np.float64) - want)
-    assert err.max() <= 1e-3 * np.abs(want).max(), err.max()
+            raw_k, raw_v = rc.read_raw(l, h, 0, n)
+            for a, b, raw in ((got_k, ref_k, raw_k), (got_v, ref_v, raw_v)):
+                if l == 0:
+                    differ += assert_codes_or_boundary_flips(a, b, raw, 1e-4, f"layer 0 head {h}")[0]
+                else:
+                    d = np.abs(a.astype(int) - b.astype(int))
+                    assert d.max() <= 1, (l, h)
+                    differ += int((d != 0).sum())
+            tol = 1e-6 if l == 0 else 1e-2
+            np.testing.assert_allclose(got_ks, ref_ks, rtol=tol)
+            np.testing.assert_allclose(got_vs, ref_vs, rtol=tol)
+            if l == last:
+                # The GPU's own values, quantized by the oracle.
+                k_tf, _, _, _, _, _ = tf
+                assert_codes_or_boundary_flips(got_k, tk[:, h], k_tf[:, h], 1e-5,
+                                               f"last layer keys head {h}")
+                np.testing.assert_allclose(got_ks, tks[:, h], rtol=1e-6)
+                assert np.array_equal(got_v, tv[:, h]), f"last layer values head {h}"
+                assert np.array_equal(got_vs.view(np.uint32), tvs[:, h].view(np.uint32))
+        assert differ <= 0.01 * n * g.kv_heads * 64 * 2, (l, differ)
+    w64, g64 = want.astype(np.float64), logits.astype(np.float64)
+    assert np.linalg.norm(g64 - w64) <= 1e-3 * np.linalg.norm(w64)
+    assert np.abs(g64 - w64).max() <= 1e-3 * np.abs(w64).max()
     assert int(np.argmax(logits)) == oracle.argmax(want)
     pre.free()
     cache.free()
     dec.free()
-    return differ, total
 
 
 def test_prefill_small_model(hip):
@@ -80,8 +106,15 @@ def test_prefill_gqa_model(hip):
 
 
 def test_prefill_full_geometry(hip):
-    say("prefill full geometry")
+    say("prefill full geometry 512")
     compare(hip, DecoderGeometry(), 512, 2026)
+
+
+def test_prefill_2048_tokens_full_geometry(hip):
+    """The prefill workload at its own size: a 2048-token prompt through the
+    8-layer decoder (d 512, 8 x 64 heads, FFN 2048, vocab 32768)."""
+    say("prefill full geometry 2048")
+    compare(hip, DecoderGeometry(), 2048, 2026)
 
 
 def test_prefill_split_equals_unsplit(hip):

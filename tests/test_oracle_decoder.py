@@ -135,3 +135,88 @@ def test_batch_driver_equals_sequential_steps():
             tok, lp = oracle.select_mask(logits, mask)
             assert tok == ids[t, b] and lp == lps[t, b]
             assert synth.unpack_bits(mask[None, :], g.vocab)[0, tok]
+
+
+def _bits(a):
+    return a.view(np.uint32) if a.dtype == np.float32 else a.view(np.uint8)
+
+
+@pytest.mark.parametrize("position0,threads", [(0, 1), (0, 3), (5, 4)])
+def test_prefill_is_bit_identical_to_sequential_steps(position0, threads):
+    """or_synth_prefill evaluates layer by layer on several threads; it must
+    equal the same tokens run through step() one at a time: last logits,
+    every K/V code and scale, and every captured pre-quantization vector."""
+    g = DecoderGeometry(layers=3, dim=256, heads=4, kv_heads=2, ffn=512, vocab=1024)
+    w = DecoderWeights(g, 9)
+    m = oracle.SynthDecoder(w)
+    toks = synth.Stream(7, "prefill-toks").integers(40, 0, g.vocab - 1)
+    lead = synth.Stream(8, "prefill-lead").integers(position0, 0, g.vocab - 1)
+    seq, par = m.new_cache(64), m.new_cache(64)
+    for c in (seq, par):
+        c.capture(0)
+        for p, t in enumerate(lead):
+            m.step(c, int(t), p)
+    for i, t in enumerate(toks):
+        want = m.step(seq, int(t), position0 + i)
+    got = m.prefill(par, toks, position0, threads=threads)
+    assert np.array_equal(_bits(got), _bits(want))
+    n = position0 + len(toks)
+    for layer in range(g.layers):
+        for h in range(g.kv_heads):
+            for a, b in zip(par.read(layer, h), seq.read(layer, h)):
+                assert np.array_equal(_bits(a), _bits(b))
+            for a, b in zip(par.read_raw(layer, h, 0, n), seq.read_raw(layer, h, 0, n)):
+                assert np.array_equal(_bits(a), _bits(b))
+
+
+def test_prefill_rejects_positions_past_the_cache():
+    g = DecoderGeometry(layers=1, dim=256, heads=4, kv_heads=4, ffn=512, vocab=512)
+    m = oracle.SynthDecoder(DecoderWeights(g, 1))
+    with pytest.raises(oracle.OracleError):
+        m.prefill(m.new_cache(8), np.arange(9), 0)
+    with pytest.raises(oracle.OracleError):
+        m.prefill(m.new_cache(8), [600], 0)
+
+
+def test_captured_vectors_are_the_stored_inputs_and_requantize_to_the_codes():
+    cache = oracle.KvCache(2, 3, max_length=20)
+    cache.capture(4)
+    s = synth.Stream(3, "capture")
+    K, V = s.normal((20, 3, 64)), s.normal((20, 3, 64))
+    cache.store(1, 0, K, V)
+    for h in range(3):
+        rk, rv = cache.read_raw(1, h, 4, 16)
+        assert np.array_equal(rk, K[4:, h]) and np.array_equal(rv, V[4:, h])
+        kc, vc, ks, vs = cache.read(1, h)
+        for p in range(4, 20):
+            c, sc = oracle.kv_quantize(rk[p - 4])
+            assert np.array_equal(c, kc[p]) and sc == ks[p]
+    with pytest.raises(oracle.OracleError):
+        cache.read_raw(1, 0, 3, 2)  # before the capture start
+
+
+def test_decode_checkpoint_logits_equal_the_step_logits():
+    g = DecoderGeometry(layers=2, dim=256, heads=4, kv_heads=4, ffn=512, vocab=2048)
+    w = DecoderWeights(g, 4)
+    m = oracle.SynthDecoder(w)
+    wl = ConstrainedWorkload(batch=2, steps=3, min_context=2, max_context=20, vocab=g.vocab)
+    lengths, starts = wl.lengths, wl.start_tokens
+
+    def caches():
+        out = []
+        for b in range(wl.batch):
+            c = m.new_cache(wl.max_length)
+            oracle.kv_fill_synthetic(c, *wl.kv_seeds(b), int(lengths[b]), *PREFIX_SCALE)
+            out.append(c)
+        return out
+
+    ids, _, chk = m.decode_batch(caches(), starts, lengths, wl.steps, wl.mask_seed,
+                                 MASK_THRESHOLD24, threads=2, check_steps=[0, 2])
+    cs = caches()
+    for b in range(wl.batch):
+        tok = int(starts[b])
+        for t in range(wl.steps):
+            logits = m.step(cs[b], tok, int(lengths[b]) + t)
+            if t in (0, 2):
+                assert np.array_equal(_bits(chk[[0, 2].index(t), b]), _bits(logits))
+            tok = int(ids[t, b])
