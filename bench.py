@@ -467,16 +467,16 @@ def bench_needle2(torch, hip, reps, check, cpu_seconds):
     model = NeedleModel(hip, weights)
     prompt = synth.Stream(2026, "needle2.prompt").integers(128, 0, g.vocab - 1)
     new = 64
-    model.generate(prompt, new, eos=EOS_TOKEN_ID)  # captures the step graphs
-    model.generate(prompt, 1, eos=EOS_TOKEN_ID)
+    model.generate_resident(prompt, new, eos=EOS_TOKEN_ID)  # captures the step graphs
+    model.generate_resident(prompt, 1, eos=EOS_TOKEN_ID)
     walls, walls1 = [], []
     res = None
     for _ in range(reps):
         t0 = time.perf_counter()
-        res = model.generate(prompt, new, eos=EOS_TOKEN_ID)
+        res = model.generate_resident(prompt, new, eos=EOS_TOKEN_ID)
         walls.append(time.perf_counter() - t0)
         t0 = time.perf_counter()
-        model.generate(prompt, 1, eos=EOS_TOKEN_ID)
+        model.generate_resident(prompt, 1, eos=EOS_TOKEN_ID)
         walls1.append(time.perf_counter() - t0)
     wall = float(np.median(walls))
     wall1 = float(np.median(walls1))
@@ -495,8 +495,8 @@ def bench_needle2(torch, hip, reps, check, cpu_seconds):
             # attention / Wo, the final mix, lm head and selection, and the
             # confidence pool (the head is on, as the reference's default)
             "launches_per_token": 2 + len(g.sites) + 4 * g.layers + 3
-                                  + int(model.session.has_confidence),
-            "confidence_pool": model.session.has_confidence}
+                                  + int(model.resident.has_confidence),
+            "confidence_pool": model.resident.has_confidence}
     part["decode_frac_hbm"] = part["decode_GBps"] / HBM_PEAK_GBS
     ref = oracle.Needle2(weights)
     cpu = None

@@ -441,13 +441,23 @@ typedef struct nd_needle_desc {
 nd_status nd_needle_create(nd_ctx* ctx, const nd_needle_desc* desc, nd_needle** out);
 nd_status nd_needle_free(nd_ctx* ctx, nd_needle* model);
 
-/* NeedleRuntime.reset (model/runtime.ts:150-225): position 0, empty history
- * and engram ring, an int8 KV cache of min(max_length, sink + kv_window)
- * slots per (layer, KV head) (max_length without a window).  Errors:
- * CONTEXT_OVERFLOW when max_length is 0 or above the model's max_length.
- * The first reset allocates the runtime state for the model's max_length;
- * later resets only clear it. */
-nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* model, uint32_t max_length, uint32_t sink);
+/* NeedleRuntime.reset (model/runtime.ts:150-225) and
+ * ResidentExecutionSession.reset (backends/backend.ts:17-22, 67): position
+ * 0, empty history and engram ring, a KV cache of min(max_length, sink +
+ * kv_window) slots per (layer, KV head) (max_length without a window) in
+ * the kvCache mode `kv_cache` (ND_KV_INT8 or ND_KV_FLOAT32), and the
+ * confidence pool on when collect_confidence != 0 and the model has a probe
+ * head.  Errors: CONTEXT_OVERFLOW when max_length is 0 or above the model's
+ * max_length; UNSUPPORTED_CACT for a kvCache mode this runtime does not keep
+ * (the session's reset() then returns false and the runtime keeps its own
+ * cache, runtime.ts:171-205).  The first reset allocates the runtime state
+ * for the model's max_length; later resets only clear it.  One reset is
+ * driven either by the whole-step calls (nd_needle_step, _prefill,
+ * _step_select, _generate) or by the session calls (nd_needle_begin_token
+ * ... nd_needle_forward): the first call after a reset decides, and a call
+ * of the other kind is INVALID_CACT until the next reset. */
+nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* model, uint32_t max_length, uint32_t sink,
+                          uint32_t kv_cache, uint32_t collect_confidence);
 
 /* The runtime's KV cache (read it with nd_kv_read), or NULL before reset. */
 nd_kv* nd_needle_kv(nd_needle* model);
@@ -457,7 +467,8 @@ uint32_t nd_needle_position(const nd_needle* model);
  * backends/backend.ts:77; computed as NeedleRuntime.confidence,
  * model/runtime.ts:93-104, 641-645): sigmoid of output 0 of the probe head
  * over everything pooled since the last reset.  INVALID_CACT when the model
- * has no confidence head or before reset. */
+ * has no confidence head, before reset, or when the reset turned
+ * collectConfidence off. */
 nd_status nd_needle_confidence(nd_ctx* ctx, nd_needle* model, double* confidence);
 
 /* NeedleRuntime.step (model/runtime.ts:280-583): runs `token` at the current
@@ -490,6 +501,86 @@ nd_status nd_needle_step_select(nd_ctx* ctx, nd_needle* model, uint32_t token,
 nd_status nd_needle_generate(nd_ctx* ctx, nd_needle* model, const uint32_t* prompt,
                              uint32_t count, uint32_t max_new, uint32_t sink, uint32_t eos,
                              uint32_t* ids, double* log_probabilities, uint32_t* generated);
+
+/* ---------------- ResidentExecutionSession methods (backends/backend.ts:65-80)
+ *
+ * The session API an unchanged NeedleRuntime.step drives (model/runtime.ts:
+ * 314-375, 444-463, 554-564).  The host keeps the position, the token
+ * history and the engram hashes; the device keeps the KV cache, the engram
+ * ring, the lanes and the confidence pool.  A resident token is
+ * nd_needle_prepare_engrams (optional), nd_needle_begin_token, then
+ * nd_needle_forward_token (or nd_needle_forward_layer for layers 0..L-1 in
+ * order), then nd_needle_finish_token or nd_needle_finish_token_for_selection
+ * + nd_needle_select_token.  Calls out of that order are INVALID_CACT. */
+
+/* beginResidentToken(lanes) (backend.ts:69; runtime.ts:327): lanes
+ * [lanes][dim], every lane the scaled embedding row (runtime.ts:305-313);
+ * lane 0 is the confidence pool's first cell of the token. */
+nd_status nd_needle_begin_token(nd_ctx* ctx, nd_needle* model, const float* lanes);
+
+/* prepareResidentEngrams({indices, valid, position}) (backend.ts:46-50, 70;
+ * runtime.ts:314-321): the engram lookup of #engramLookup (runtime.ts:
+ * 788-818) for `tables` tables; the device gathers the rows, projects the
+ * keys and values of every site, and updates and convolves the ring at
+ * `position` (#engramStep, runtime.ts:820-877).  Called before
+ * nd_needle_begin_token.  Errors: INVALID_CACT for a model without engram
+ * layers, a table count other than the model's or an index outside the
+ * slots of a valid table; CONTEXT_OVERFLOW at the runtime limit. */
+nd_status nd_needle_prepare_engrams(nd_ctx* ctx, nd_needle* model, const uint32_t* indices,
+                                    const uint32_t* valid, uint32_t tables, uint32_t position);
+
+/* forwardResidentLayer({layerIndex, position, engramKey?, engramValue?})
+ * (backend.ts:58-63, 72; runtime.ts:346-361): layer `layer` of the token at
+ * `position` -- the lane mix (runtime.ts:385-441), Q/K/V/gate with the
+ * per-head norms and RoPE, #storeKV, gated attention, Wo (:465-505), and the
+ * post-attention half of the layer before it (:509-551).  An engram layer
+ * takes the host's key and value [dim] (#engramStep results) when the token's
+ * engrams were not prepared on the device, and NULL otherwise. */
+nd_status nd_needle_forward_layer(nd_ctx* ctx, nd_needle* model, uint32_t layer,
+                                  uint32_t position, const float* engram_key,
+                                  const float* engram_value);
+
+/* forwardResidentToken({position, engramKeys, engramValues}) (backend.ts:
+ * 52-56, 71; runtime.ts:337-345): every layer; engram_keys and
+ * engram_values are [n_sites][dim] host arrays, or both NULL when the
+ * engrams were prepared on the device. */
+nd_status nd_needle_forward_token(nd_ctx* ctx, nd_needle* model, uint32_t position,
+                                  const float* engram_keys, const float* engram_values);
+
+/* finishResidentToken(wantLogits) (backend.ts:73; runtime.ts:371-374): the
+ * last layer's post half, the lane mean and final norm, the confidence pool,
+ * and with want_logits the logits [vocab] copied to `logits`
+ * (runtime.ts:570-577). */
+nd_status nd_needle_finish_token(nd_ctx* ctx, nd_needle* model, uint32_t want_logits,
+                                 float* logits);
+
+/* finishResidentTokenForSelection() (backend.ts:74; runtime.ts:363-369): the
+ * same with the logits kept on the device for nd_needle_select_token. */
+nd_status nd_needle_finish_token_for_selection(nd_ctx* ctx, nd_needle* model);
+
+/* selectResidentToken(allowedTokenIds?) (backend.ts:75; runtime.ts:555-563):
+ * selectToken (runtime.ts:880-899) over those logits -- `count` allowed ids
+ * in list order, or every id when allowed == NULL.  Errors: INVALID_CACT for
+ * an empty list or an id outside the logits; BACKEND_UNAVAILABLE without
+ * logits from nd_needle_finish_token_for_selection. */
+nd_status nd_needle_select_token(nd_ctx* ctx, nd_needle* model, const uint32_t* allowed,
+                                 uint32_t count, uint32_t* id, double* log_probability);
+
+/* readResidentLanes() (backend.ts:78): the lanes [lanes][dim] after the
+ * last layer run (applying its post half if it is still owed). */
+nd_status nd_needle_read_lanes(nd_ctx* ctx, nd_needle* model, float* lanes);
+
+/* forward(request) (backend.ts:24-39, 68; runtime.ts:444-463), the layer of a
+ * token that does not run resident: from the runtime's attention input
+ * [dim] (the normalized block input), block and update inputs [dim], lanes x
+ * [lanes][dim] and the layer's phi rows (phi_post [lanes], phi_residual
+ * [lanes][lanes]), runs Q/K/V/gate, norms and RoPE, #storeKV, gated attention
+ * and Wo, then the post half, and returns the next lanes ("nextX")
+ * [lanes][dim] in next_x. */
+nd_status nd_needle_forward(nd_ctx* ctx, nd_needle* model, uint32_t layer, uint32_t position,
+                            const float* input, const float* block_input,
+                            const float* update_input, const float* x, const float* phi_post,
+                            const float* phi_residual, float* next_x);
 
 /* ------------------------------ (f): schema-constrained token masks */
 

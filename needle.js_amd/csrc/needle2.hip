@@ -19,6 +19,7 @@
 // float64-with-f32-stores form except the Sinkhorn iterations (fp32).
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <type_traits>
 #include <vector>
 
@@ -178,6 +179,43 @@ __global__ void n2_engram_conv_kernel(const uint32_t* __restrict__ st,
                                 (double)r[(size_t)ps * d + i]);
   }
   mixed[(size_t)s * d + i] = m;
+}
+
+// A session step's position (ResidentTokenRequest.position,
+// backends/backend.ts:52-56): st[1] = position and st[0] = position + 1, as
+// a whole step's intake leaves them, and the RoPE angles of every layer at it
+// (math.ts:94-115).
+__global__ void n2_position_kernel(uint32_t* __restrict__ st, uint32_t position,
+                                   const double* __restrict__ inv_freq, double* __restrict__ rope) {
+  const uint32_t t = threadIdx.x;
+  if (t == 0) {
+    st[0] = position + 1;
+    st[1] = position;
+  }
+  if (t < 32) {
+    double sn, cs;
+    sincos((double)position * inv_freq[t], &sn, &cs);
+    rope[t] = sn;
+    rope[32 + t] = cs;
+  }
+}
+
+// The concatenated engram rows of every site (runtime.ts:828-836) for a
+// lookup the host computed (ResidentEngramRequest, backends/backend.ts:
+// 46-50: runtime.ts:788-818's indices and valid flags per table, indices
+// checked against the slot count on entry); zero for an invalid table.
+__global__ __launch_bounds__(kWg) void n2_gather_kernel(BeginArgs a,
+                                                         const uint32_t* __restrict__ lookup) {
+  const uint32_t per_site = a.tables * a.sub;
+  for (uint32_t i = threadIdx.x; i < a.n_sites * per_site; i += kWg) {
+    const uint32_t s = i / per_site, j = i % per_site, tb = j / a.sub, c = j % a.sub;
+    float v = 0.f;
+    if (lookup[a.tables + tb]) {
+      const size_t row = (size_t)tb * a.slots + lookup[tb];
+      v = (float)a.tw[s][row * a.sub + c] * a.ts[s][row];
+    }
+    a.cat[i] = v;
+  }
 }
 
 // sinkhorn (math.ts:62-92) of an L x L matrix (L <= 4) on the lanes of a
@@ -1071,6 +1109,16 @@ size_t al(size_t n) { return (n + 255) & ~size_t(255); }
 
 }  // namespace
 
+// Pinned staging slots of the session calls.
+enum StageSlot : uint32_t {
+  kStageLanes = 0,  // begin: lanes [lanes][dim]
+  kStageLookup,     // prepare engrams: indices and valid flags
+  kStageAllowed,    // selection: allowed ids [vocab]
+  kStageForward,    // fallback forward: input, block, update [3][dim], x, phi post, phi res
+  kStageEngram,     // host engram key (2 site) and value (2 site + 1) [dim], 4 sites
+  kStageSlots = kStageEngram + 8
+};
+
 struct nd_needle {
   nd_needle_desc d{};
   std::vector<nd_mat> wqkvg;  // owned: rows q | k | v | gate of each layer
@@ -1113,12 +1161,33 @@ struct nd_needle {
   // the arena's cleared part, cells of one step (or one prefill pass) and
   // their scores as scratch.
   bool conf = false;
+  bool collect = true;  // this reset's collectConfidence
   uint32_t probe_count = 0;
   size_t o_probes = 0, o_pproj = 0;
   float probe_bias0 = 0.f;
   PoolState pool{};
   float *cells = nullptr, *pf_cells = nullptr;
   double *scores = nullptr, *pf_scores = nullptr, *conf_out = nullptr;
+  // Which calls drive the runtime since the last reset: 0 none yet, 1 whole
+  // steps (nd_needle_step, _prefill, _step_select, _generate), 2 the session
+  // methods (ResidentExecutionSession, backends/backend.ts:65-80).
+  uint32_t api = 0;
+  // Session token in flight: begin called, the next layer to run and the
+  // token's position, the post half owed to the last layer run, engrams
+  // prepared on the device for this token, logits awaiting selection.
+  bool token_open = false, post_pending = false, engrams_ready = false, select_ready = false;
+  uint32_t next_layer = 0, token_position = 0;
+  uint32_t* lookup = nullptr;  // [2][engram_tables]: indices, valid flags
+  // Engram keys and values handed over by the host ([2][sites][dim]; read by
+  // the mix launches of the token instead of the device's own when set) and
+  // the fallback forward's inputs (input, block, update, x, phi post, phi res).
+  float *host_eng = nullptr, *fwd_in = nullptr;
+  bool host_engrams = false;
+  // Pinned staging of the session's host inputs, one slot per purpose; each
+  // slot's event marks the completion of its last copy to the device.
+  char* pinned = nullptr;
+  size_t stage_off[kStageSlots] = {}, stage_bytes[kStageSlots] = {};
+  hipEvent_t stage_done[kStageSlots] = {};
 };
 
 namespace {
@@ -1152,26 +1221,135 @@ hipError_t enqueue_pool(nd_needle* n, const float* cells, uint32_t C, double* sc
   return hipGetLastError();
 }
 
-// Enqueues one token of NeedleRuntime.step (model/runtime.ts:280-583) on s.
-// select: after the logits, selectToken over allowed[0..count) (all ids when
-// allowed is null) into sel_id / sel_lp.
-hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want_logits,
-                        bool select, const uint32_t* allowed, uint32_t count, hipStream_t s) {
+// Whether this reset pools the confidence cells (a probe head and
+// collectConfidence).
+inline bool pool_on(const nd_needle* n) { return n->conf && n->collect; }
+
+// Halves of a mix launch (enqueue_mix `parts`).
+enum MixPart : uint32_t { kMixPost = 1, kMixPre = 2, kMixFinal = 4, kMixCell = 8 };
+
+// Mix launch of layer slot l (l <= layers): post(l - 1) of the previous
+// layer with kMixPost (runtime.ts:509-542 with #attentionDelta, :585-611),
+// pre(l) of this one with kMixPre when l < layers (runtime.ts:385-441), the
+// lane mean plus final norm with kMixFinal (runtime.ts:570-576), and with
+// kMixCell (and kMixPost) the lane mean after post(l - 1) into confidence
+// cell l when the pool is on.
+hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s) {
+  const bool has_post = parts & kMixPost;
+  const nd_needle_desc& d = n->d;
+  const uint32_t D = d.dim, ln = d.lanes;
+  const size_t K = (size_t)ln * D;
+  const bool pre = l < d.layers;
+  // Every operand pointer is valid whether or not its half runs (the kernel
+  // loads them unconditionally): an absent layer reads layer 0's.
+  const uint32_t pl = l > 0 ? l - 1 : 0, ql = pre ? l : 0;
+  int site = -1;
+  for (uint32_t si = 0; si < d.n_sites; ++si)
+    if (pre && d.sites[si] == l) site = (int)si;
+  MixArgs m{};
+  m.x = n->x;
+  m.d = D;
+  m.hdim = d.hadamard;
+  m.lanes = ln;
+  m.upd = n->upd;
+  m.blk = n->blk;
+  m.ain = n->ain;
+  m.phi_post = n->phi_post_v;
+  m.phi_res = n->phi_res_v;
+  m.has_post = has_post;
+  m.proj = n->proj;
+  m.post_norm = n->params + n->o_post + (size_t)pl * D;
+  m.pre_h_norm = n->params + n->o_preh + (size_t)pl * D;
+  m.d1 = n->params + n->o_d1 + (size_t)pl * D;
+  m.d2 = n->params + n->o_d2 + (size_t)pl * d.hadamard;
+  m.d3 = n->params + n->o_d3 + (size_t)pl * D;
+  m.attention_gate = n->attention_gate[pl];
+  m.route = n->route;
+  m.has_pre = pre && (parts & kMixPre);
+  m.own_pre = ql % ln;
+  m.phi_w[0] = n->phi_pre->w + (size_t)ql * ln * K;
+  m.phi_s[0] = n->phi_pre->scales + (size_t)ql * ln;
+  m.phi_w[1] = n->phi_post->w + (size_t)ql * ln * K;
+  m.phi_s[1] = n->phi_post->scales + (size_t)ql * ln;
+  m.phi_w[2] = n->phi_res->w + (size_t)ql * ln * ln * K;
+  m.phi_s[2] = n->phi_res->scales + (size_t)ql * ln * ln;
+  m.a_pre = n->a_pre[ql];
+  m.b_pre = n->params + n->o_bpre + (size_t)ql * ln;
+  m.has_site = site >= 0;
+  const uint32_t es = site >= 0 ? (uint32_t)site : 0;
+  const uint32_t S = d.n_sites ? d.n_sites : 1;
+  m.ekey = n->host_engrams ? n->host_eng + (size_t)es * D : n->ekv_out + (size_t)es * 2 * D;
+  m.evalue = n->host_engrams ? n->host_eng + (size_t)(S + es) * D : n->evals + (size_t)es * D;
+  m.norm_input = n->params + n->o_norm_input + (size_t)ql * D;
+  m.has_final = (parts & kMixFinal) != 0;
+  m.final_norm = n->params + n->o_final;
+  m.fin = n->fin;
+  m.cell = pool_on(n) && has_post && (parts & kMixCell) ? n->cells + (size_t)l * D : nullptr;
+  hipLaunchKernelGGL(n2_mix_kernel, dim3(1), dim3(kMixWg), 0, s, m);
+  return hipGetLastError();
+}
+
+// The attention block of layer l on the input n->ain: Q/K/V/gate matvec with
+// the q/k norms, RoPE and the KV append in its epilogue (plus the layer's
+// Sinkhorn routing from the mix's phi rows), gated attention, and Wo into
+// n->proj (runtime.ts:465-505).
+hipError_t enqueue_block(nd_needle* n, uint32_t l, hipStream_t s) {
   const nd_needle_desc& d = n->d;
   const uint32_t D = d.dim, ln = d.lanes, qw = d.heads * kHd;
+  const nd_mat& wm = n->wqkvg[l];
+  RouteArgs ra{};
+  ra.phi_post = n->phi_post_v;
+  ra.phi_res = n->phi_res_v;
+  ra.a_post = n->a_post[l];
+  ra.a_res = n->a_res[l];
+  ra.b_post = n->params + n->o_bpost + (size_t)l * ln;
+  ra.b_res = n->params + n->o_bres + (size_t)l * ln * ln;
+  ra.lanes = ln;
+  ra.own = l % ln;
+  ra.route = n->route;
+  hipLaunchKernelGGL(n2_qkv_kernel, dim3(wm.n / kHd + 1), dim3(256), 0, s, wm.w, wm.scales,
+                     n->ain, D, d.heads, d.kv_heads, n->st, n->params + n->o_qn + (size_t)l * kHd,
+                     n->params + n->o_kn + (size_t)l * kHd, n->rope, n->q, n->qkvg,
+                     (int8_t*)n->kv.k, (int8_t*)n->kv.v, n->kv.ks, n->kv.vs, l, n->kv.alloc,
+                     n->kv.sink, n->kv.window, ra);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  e = nd_launch_attention_gated(&n->kv, l, n->st + 1, n->max_length - 1, n->q, d.heads, n->qkvg,
+                                n->att, n->partials, n->counters, s);
+  if (e != hipSuccess) return e;
+  return nd_launch_matvec(n->wo[l], n->att, 1, qw, 0, D, n->proj, D, s);
+}
+
+// After the final mix: the confidence pool of the step's cells, the logits
+// (tied embedding, runtime.ts:577) when tail, and selectToken over
+// allowed[0..count) (all ids when allowed is null) when select.
+hipError_t enqueue_final(nd_needle* n, bool tail, bool select, const uint32_t* allowed,
+                         uint32_t count, hipStream_t s) {
+  const nd_needle_desc& d = n->d;
+  hipError_t e;
+  if (pool_on(n) && (e = enqueue_pool(n, n->cells, d.layers + 1, n->scores, s)) != hipSuccess)
+    return e;
+  if (!tail) return hipSuccess;
+  e = nd_launch_matvec(n->embedding, n->fin, 1, d.dim, 0, d.vocab, n->logits, d.vocab, s);
+  if (e != hipSuccess || !select) return e;
+  return nd_launch_select_list(n->logits, d.vocab, allowed, count, n->sel_id, n->sel_lp, s);
+}
+
+// Arguments of the token intake and engram gathers of one step (the token
+// and its source are set by the caller).
+BeginArgs begin_args(nd_needle* n) {
+  const nd_needle_desc& d = n->d;
   BeginArgs b{};
   b.st = n->st;
   b.history = n->history;
   b.lp_history = n->lp_history;
   b.selected_id = n->sel_id;
   b.selected_lp = n->sel_lp;
-  b.token_arg = token;
-  b.source = source;
   b.emb = n->embedding->w;
   b.emb_s = n->embedding->scales;
-  b.d = D;
-  b.lanes = ln;
-  b.scale = std::sqrt((double)D);
+  b.d = d.dim;
+  b.lanes = d.lanes;
+  b.scale = std::sqrt((double)d.dim);
   b.x = n->x;
   for (uint32_t si = 0; si < d.n_sites; ++si) {
     b.tw[si] = n->eg_tables[si]->w;
@@ -1187,23 +1365,41 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
   b.cat = n->cat;
   b.inv_freq = n->inv_freq;
   b.rope = n->rope;
-  b.cell0 = n->conf ? n->cells : nullptr;
+  b.cell0 = pool_on(n) ? n->cells : nullptr;
+  return b;
+}
+
+// The engram projections of the gathered rows in n->cat (runtime.ts:837-843)
+// and the ring update and tap convolution at position st[1] (:854-872):
+// keys in n->ekv_out, mixed values in n->evals.
+hipError_t enqueue_engrams(nd_needle* n, hipStream_t s) {
+  const nd_needle_desc& d = n->d;
+  const uint32_t D = d.dim, cat = d.engram_tables * d.engram_sub;
+  for (uint32_t si = 0; si < d.n_sites; ++si) {
+    const hipError_t e = nd_launch_matvec(&n->ekv[si], n->cat + (size_t)si * cat, 1, cat, 0,
+                                          2 * D, n->ekv_out + (size_t)si * 2 * D, 2 * D, s);
+    if (e != hipSuccess) return e;
+  }
+  if (!d.n_sites) return hipSuccess;
+  hipLaunchKernelGGL(n2_engram_conv_kernel, dim3(d.n_sites), dim3((D + 63) / 64 * 64), 0, s, n->st,
+                     n->ekv_out, n->ring, n->params + n->o_taps, D, n->depth, d.engram_taps,
+                     n->max_order, n->evals);
+  return hipGetLastError();
+}
+
+// Enqueues one token of NeedleRuntime.step (model/runtime.ts:280-583) on s.
+// select: after the logits, selectToken over allowed[0..count) (all ids when
+// allowed is null) into sel_id / sel_lp.
+hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want_logits,
+                        bool select, const uint32_t* allowed, uint32_t count, hipStream_t s) {
+  const nd_needle_desc& d = n->d;
+  BeginArgs b = begin_args(n);
+  b.token_arg = token;
+  b.source = source;
   hipLaunchKernelGGL(n2_begin_kernel, dim3(1), dim3(kWg), 0, s, b);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const uint32_t cat = d.engram_tables * d.engram_sub;
-  for (uint32_t si = 0; si < d.n_sites; ++si) {
-    e = nd_launch_matvec(&n->ekv[si], n->cat + (size_t)si * cat, 1, cat, 0, 2 * D,
-                         n->ekv_out + (size_t)si * 2 * D, 2 * D, s);
-    if (e != hipSuccess) return e;
-  }
-  if (d.n_sites) {
-    hipLaunchKernelGGL(n2_engram_conv_kernel, dim3(d.n_sites), dim3((D + 63) / 64 * 64), 0, s,
-                       n->st, n->ekv_out, n->ring, n->params + n->o_taps, D, n->depth,
-                       d.engram_taps, n->max_order, n->evals);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
-  const size_t K = (size_t)ln * D;
+  if ((e = enqueue_engrams(n, s)) != hipSuccess) return e;
   const bool tail = want_logits || select;
   // Launch l (l <= layers) runs post(l - 1) and pre(l); the last one runs
   // post(layers - 1) and the final norm, and only when logits are wanted or
@@ -1211,82 +1407,13 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
   // lanes do not outlive the step).
   for (uint32_t l = 0; l <= d.layers; ++l) {
     const bool pre = l < d.layers;
-    if (!pre && !tail && !n->conf) break;
-    // Every operand pointer is valid whether or not its half runs (the
-    // kernel loads them unconditionally): an absent layer reads layer 0's.
-    const uint32_t pl = l > 0 ? l - 1 : 0, ql = pre ? l : 0;
-    int site = -1;
-    for (uint32_t si = 0; si < d.n_sites; ++si)
-      if (pre && d.sites[si] == l) site = (int)si;
-    MixArgs m{};
-    m.x = n->x;
-    m.d = D;
-    m.hdim = d.hadamard;
-    m.lanes = ln;
-    m.upd = n->upd;
-    m.blk = n->blk;
-    m.ain = n->ain;
-    m.phi_post = n->phi_post_v;
-    m.phi_res = n->phi_res_v;
-    m.has_post = l > 0;
-    m.proj = n->proj;
-    m.post_norm = n->params + n->o_post + (size_t)pl * D;
-    m.pre_h_norm = n->params + n->o_preh + (size_t)pl * D;
-    m.d1 = n->params + n->o_d1 + (size_t)pl * D;
-    m.d2 = n->params + n->o_d2 + (size_t)pl * d.hadamard;
-    m.d3 = n->params + n->o_d3 + (size_t)pl * D;
-    m.attention_gate = n->attention_gate[pl];
-    m.route = n->route;
-    m.has_pre = pre;
-    m.own_pre = ql % ln;
-    m.phi_w[0] = n->phi_pre->w + (size_t)ql * ln * K;
-    m.phi_s[0] = n->phi_pre->scales + (size_t)ql * ln;
-    m.phi_w[1] = n->phi_post->w + (size_t)ql * ln * K;
-    m.phi_s[1] = n->phi_post->scales + (size_t)ql * ln;
-    m.phi_w[2] = n->phi_res->w + (size_t)ql * ln * ln * K;
-    m.phi_s[2] = n->phi_res->scales + (size_t)ql * ln * ln;
-    m.a_pre = n->a_pre[ql];
-    m.b_pre = n->params + n->o_bpre + (size_t)ql * ln;
-    m.has_site = site >= 0;
-    m.ekey = n->ekv_out + (size_t)(site >= 0 ? site : 0) * 2 * D;
-    m.evalue = n->evals + (size_t)(site >= 0 ? site : 0) * D;
-    m.norm_input = n->params + n->o_norm_input + (size_t)ql * D;
-    m.has_final = !pre && tail;
-    m.final_norm = n->params + n->o_final;
-    m.fin = n->fin;
-    m.cell = n->conf && l > 0 ? n->cells + (size_t)l * D : nullptr;
-    hipLaunchKernelGGL(n2_mix_kernel, dim3(1), dim3(kMixWg), 0, s, m);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (!pre && !tail && !pool_on(n)) break;
+    const uint32_t parts = (l > 0 ? kMixPost | kMixCell : 0) | kMixPre | (!pre && tail ? kMixFinal : 0);
+    if ((e = enqueue_mix(n, l, parts, s)) != hipSuccess) return e;
     if (!pre) break;
-    const nd_mat& wm = n->wqkvg[l];
-    RouteArgs ra{};
-    ra.phi_post = n->phi_post_v;
-    ra.phi_res = n->phi_res_v;
-    ra.a_post = n->a_post[l];
-    ra.a_res = n->a_res[l];
-    ra.b_post = n->params + n->o_bpost + (size_t)l * ln;
-    ra.b_res = n->params + n->o_bres + (size_t)l * ln * ln;
-    ra.lanes = ln;
-    ra.own = l % ln;
-    ra.route = n->route;
-    hipLaunchKernelGGL(n2_qkv_kernel, dim3(wm.n / kHd + 1), dim3(256), 0, s, wm.w, wm.scales,
-                       n->ain, D, d.heads, d.kv_heads, n->st,
-                       n->params + n->o_qn + (size_t)l * kHd, n->params + n->o_kn + (size_t)l * kHd,
-                       n->rope, n->q, n->qkvg, (int8_t*)n->kv.k, (int8_t*)n->kv.v, n->kv.ks,
-                       n->kv.vs, l, n->kv.alloc, n->kv.sink, n->kv.window, ra);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    e = nd_launch_attention_gated(&n->kv, l, n->st + 1, n->max_length - 1, n->q, d.heads, n->qkvg,
-                                  n->att, n->partials, n->counters, s);
-    if (e != hipSuccess) return e;
-    if ((e = nd_launch_matvec(n->wo[l], n->att, 1, qw, 0, D, n->proj, D, s)) != hipSuccess)
-      return e;
+    if ((e = enqueue_block(n, l, s)) != hipSuccess) return e;
   }
-  if (n->conf && (e = enqueue_pool(n, n->cells, d.layers + 1, n->scores, s)) != hipSuccess)
-    return e;
-  if (!tail) return hipSuccess;
-  e = nd_launch_matvec(n->embedding, n->fin, 1, D, 0, d.vocab, n->logits, d.vocab, s);
-  if (e != hipSuccess || !select) return e;
-  return nd_launch_select_list(n->logits, d.vocab, allowed, count, n->sel_id, n->sel_lp, s);
+  return enqueue_final(n, tail, select, allowed, count, s);
 }
 
 enum GraphKind { kGraphPrompt = 0, kGraphPromptSelect = 1, kGraphDecodeSelect = 2 };
@@ -1418,7 +1545,7 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
   for (uint32_t i = 0; i < d.n_orders; ++i) b.orders[i] = d.orders[i];
   b.cat = n->pf_cat;
   const uint32_t cell_ld = (d.layers + 1) * D;  // cells of one position: [layers + 1][d]
-  b.cell0 = n->conf ? n->pf_cells : nullptr;
+  b.cell0 = pool_on(n) ? n->pf_cells : nullptr;
   b.cell_ld = cell_ld;
   hipLaunchKernelGGL(n2_begin_batch_kernel, dim3(M), dim3(kWg), 0, s, b, p0, M, n->pf_positions);
   hipError_t e = hipGetLastError();
@@ -1445,11 +1572,11 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
   const bool tail = want_logits || select;
   for (uint32_t l = 0; l <= d.layers; ++l) {
     const bool pre = l < d.layers;
-    if (!pre && !tail && !n->conf) break;
+    if (!pre && !tail && !pool_on(n)) break;
     const uint32_t pl = l > 0 ? l - 1 : 0, ql = pre ? l : 0;
     // The final part runs the last row only, unless the confidence pool
     // needs every row's last lane mean.
-    const uint32_t rows = pre || n->conf ? M : 1, r0 = pre || n->conf ? 0 : M - 1;
+    const uint32_t rows = pre || pool_on(n) ? M : 1, r0 = pre || pool_on(n) ? 0 : M - 1;
     int site = -1;
     for (uint32_t si = 0; si < d.n_sites; ++si)
       if (pre && d.sites[si] == l) site = (int)si;
@@ -1492,7 +1619,7 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
     m.final_row = rows - 1;
     m.final_norm = n->params + n->o_final;
     m.fin = n->fin;
-    m.cell = n->conf && l > 0 ? n->pf_cells + (size_t)l * D : nullptr;
+    m.cell = pool_on(n) && l > 0 ? n->pf_cells + (size_t)l * D : nullptr;
     m.cell_ld = cell_ld;
     if (pre) {
       m.route_out = n->pf_route;
@@ -1528,7 +1655,7 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
         hipSuccess)
       return e;
   }
-  if (n->conf && (e = enqueue_pool(n, n->pf_cells, M * (d.layers + 1), n->pf_scores, s)) !=
+  if (pool_on(n) && (e = enqueue_pool(n, n->pf_cells, M * (d.layers + 1), n->pf_scores, s)) !=
                      hipSuccess)
     return e;
   if (!tail) return hipSuccess;
@@ -1571,6 +1698,35 @@ nd_status run_prompt(nd_ctx* ctx, nd_needle* n, uint32_t count, bool want_logits
     ++done;
   }
   return ND_OK;
+}
+
+// One reset is driven either by whole-step calls or by the session methods:
+// they keep different parts of the runtime state on the device (the token
+// history for the engram hashes, or the host's lookups), so mixing them
+// would read stale state.
+nd_status use_api(nd_ctx* ctx, nd_needle* n, uint32_t api) {
+  static const char* const names[] = {"", "whole-step", "session"};
+  if (n->api && n->api != api)
+    return nd_fail(ctx, ND_ERR_INVALID,
+                   "this runtime is driven by %s calls since its reset; call reset() before "
+                   "switching to %s calls",
+                   names[n->api], names[api]);
+  n->api = api;
+  return ND_OK;
+}
+
+// Copies `bytes` of host memory to dst on s through pinned staging slot k
+// (waiting first for that slot's previous copy), so that the caller's buffer
+// is free again when this returns and the copy stays asynchronous.
+hipError_t stage_copy(nd_needle* n, StageSlot k, void* dst, const void* src, size_t bytes,
+                      size_t slot_offset, hipStream_t s) {
+  if (slot_offset + bytes > n->stage_bytes[k]) return hipErrorInvalidValue;
+  hipError_t e = hipEventSynchronize(n->stage_done[k]);
+  if (e != hipSuccess) return e;
+  char* slot = n->pinned + n->stage_off[k] + slot_offset;
+  std::memcpy(slot, src, bytes);
+  if ((e = hipMemcpyAsync(dst, slot, bytes, hipMemcpyHostToDevice, s)) != hipSuccess) return e;
+  return hipEventRecord(n->stage_done[k], s);
 }
 
 nd_status check_step(nd_ctx* ctx, const nd_needle* n, uint32_t token) {
@@ -1764,14 +1920,22 @@ nd_status nd_needle_free(nd_ctx* ctx, nd_needle* n) {
     }
   if (n->params) hipFree(n->params);
   if (n->inv_freq) hipFree(n->inv_freq);
+  if (n->pinned) hipHostFree(n->pinned);
+  for (auto& ev : n->stage_done)
+    if (ev) hipEventDestroy(ev);
   delete n;
   return ND_OK;
 }
 
-nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32_t sink) {
+nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32_t sink,
+                          uint32_t kv_cache, uint32_t collect_confidence) {
   if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
   if (!n) return nd_fail(ctx, ND_ERR_INVALID, "model is NULL");
   const nd_needle_desc& d = n->d;
+  if (kv_cache != ND_KV_INT8 && kv_cache != ND_KV_FLOAT32)
+    return nd_fail(ctx, ND_ERR_INVALID, "unknown kvCache mode %u", kv_cache);
+  if (kv_cache == ND_KV_FLOAT32)
+    return nd_fail(ctx, ND_ERR_UNSUPPORTED, "the resident Needle 2 runtime keeps an int8 KV cache");
   if (max_length == 0 || max_length > d.max_length)
     return nd_fail(ctx, ND_ERR_OVERFLOW, "Runtime length %u is outside model limit %u",
                    max_length, d.max_length);
@@ -1797,7 +1961,9 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
                             al((size_t)S * cat * 4), al((size_t)S * 2 * D * 4),
                             al((size_t)S * D * 4), al(pf * 4), al(20 * 4), al(64 * 8),
                             cb * al((size_t)(d.layers + 1) * D * 4),
-                            cb * al((size_t)(d.layers + 1) * P8), cb * al(64)};
+                            cb * al((size_t)(d.layers + 1) * P8), cb * al(64), al(32 * 4),
+                            al((size_t)2 * S * D * 4),
+                            al((size_t)(3 * D + ln * D + ln + ln * ln) * 4)};
     size_t total = 0;
     for (size_t v : sizes) total += v;
     ND_HIP(ctx, hipMalloc(&n->arena, total));
@@ -1847,6 +2013,27 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     take(&n->cells);
     take(&n->scores);
     take(&n->conf_out);
+    take(&n->lookup);
+    take(&n->host_eng);
+    take(&n->fwd_in);
+  }
+  if (!n->pinned) {
+    // Pinned staging of the session calls' host inputs.
+    const uint32_t S = d.n_sites ? d.n_sites : 1;
+    (void)S;
+    size_t slot_bytes[kStageSlots] = {al((size_t)ln * D * 4), al(32 * 4),
+                                      al((size_t)d.vocab * 4),
+                                      al((size_t)(3 * D + ln * D + ln + ln * ln) * 4)};
+    for (uint32_t k = kStageEngram; k < kStageSlots; ++k) slot_bytes[k] = al((size_t)D * 4);
+    size_t pinned = 0;
+    for (uint32_t k = 0; k < kStageSlots; ++k) {
+      n->stage_off[k] = pinned;
+      n->stage_bytes[k] = slot_bytes[k];
+      pinned += slot_bytes[k];
+    }
+    for (auto& ev : n->stage_done)
+      if (!ev) ND_HIP(ctx, hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    ND_HIP(ctx, hipHostMalloc(reinterpret_cast<void**>(&n->pinned), pinned));
   }
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
   ND_HIP(ctx, hipMemsetAsync(n->arena, 0, n->state_bytes, ctx->stream));
@@ -1854,6 +2041,10 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
   n->max_length = max_length;
   n->sink = std::min(sink, max_length);
   n->position = 0;
+  n->collect = collect_confidence != 0;
+  n->api = 0;
+  n->token_open = n->post_pending = n->engrams_ready = n->select_ready = false;
+  n->next_layer = n->token_position = 0;
   nd_kv& kv = n->kv;
   kv.layers = d.layers;
   kv.kv_heads = d.kv_heads;
@@ -1876,6 +2067,8 @@ nd_status nd_needle_confidence(nd_ctx* ctx, nd_needle* n, double* confidence) {
   if (!n->conf) return nd_fail(ctx, ND_ERR_INVALID, "the model has no confidence head");
   if (!n->arena || !n->max_length)
     return nd_fail(ctx, ND_ERR_INVALID, "runtime is not reset");
+  if (!n->collect)
+    return nd_fail(ctx, ND_ERR_INVALID, "this reset has collectConfidence off");
   hipLaunchKernelGGL(n2_probe_head_kernel, dim3(1), dim3(256), 0, ctx->stream, n->pool,
                      n->probe_count, n->d.dim, n->params + n->o_pproj, n->probe_bias0, n->conf_out);
   ND_HIP(ctx, hipGetLastError());
@@ -1888,7 +2081,7 @@ nd_status nd_needle_step(nd_ctx* ctx, nd_needle* n, uint32_t token, float* logit
   if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
   if (!n) return nd_fail(ctx, ND_ERR_INVALID, "model is NULL");
   nd_status st = check_step(ctx, n, token);
-  if (st != ND_OK) return st;
+  if (st != ND_OK || (st = use_api(ctx, n, 1)) != ND_OK) return st;
   ND_HIP(ctx, enqueue_step(n, kTokenArg, token, logits != nullptr, false, nullptr, 0, ctx->stream));
   ++n->position;
   if (logits)
@@ -1911,9 +2104,11 @@ nd_status nd_needle_prefill(nd_ctx* ctx, nd_needle* n, const uint32_t* tokens, u
   for (uint32_t i = 0; i < count; ++i)
     if (tokens[i] >= n->d.vocab)
       return nd_fail(ctx, ND_ERR_INVALID, "Token %u is outside the vocabulary", tokens[i]);
+  nd_status st = use_api(ctx, n, 1);
+  if (st != ND_OK) return st;
   ND_HIP(ctx, hipMemcpyAsync(n->history + n->position, tokens, (size_t)count * 4,
                              hipMemcpyHostToDevice, ctx->stream));
-  nd_status st = run_prompt(ctx, n, count, logits != nullptr, false, false);
+  st = run_prompt(ctx, n, count, logits != nullptr, false, false);
   if (st != ND_OK) return st;
   if (logits)
     ND_HIP(ctx, hipMemcpyAsync(logits, n->logits, (size_t)n->d.vocab * 4, hipMemcpyDeviceToHost,
@@ -1927,7 +2122,7 @@ nd_status nd_needle_step_select(nd_ctx* ctx, nd_needle* n, uint32_t token, const
   if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
   if (!n || !id || !logprob) return nd_fail(ctx, ND_ERR_INVALID, "NULL argument");
   nd_status st = check_step(ctx, n, token);
-  if (st != ND_OK) return st;
+  if (st != ND_OK || (st = use_api(ctx, n, 1)) != ND_OK) return st;
   if (allowed) {
     // selectToken (runtime.ts:880-899): a non-empty id list inside the logits.
     if (count == 0) return nd_fail(ctx, ND_ERR_INVALID, "Allowed token set is empty");
@@ -1965,8 +2160,8 @@ nd_status nd_needle_generate(nd_ctx* ctx, nd_needle* n, const uint32_t* prompt, 
   for (uint32_t i = 0; i < count; ++i)
     if (prompt[i] >= n->d.vocab)
       return nd_fail(ctx, ND_ERR_INVALID, "Token %u is outside the vocabulary", prompt[i]);
-  nd_status st = nd_needle_reset(ctx, n, std::max(count, max_len), sink);
-  if (st != ND_OK) return st;
+  nd_status st = nd_needle_reset(ctx, n, std::max(count, max_len), sink, ND_KV_INT8, n->collect);
+  if (st != ND_OK || (st = use_api(ctx, n, 1)) != ND_OK) return st;
   ND_HIP(ctx, hipMemcpyAsync(n->history, prompt, (size_t)count * 4, hipMemcpyHostToDevice,
                              ctx->stream));
   const uint32_t n_gen = max_new ? std::min(max_new, max_len - count) : 0;
@@ -1999,6 +2194,304 @@ nd_status nd_needle_generate(nd_ctx* ctx, nd_needle* n, const uint32_t* prompt, 
     logprobs[out] = lp[out];
   }
   *generated = out;
+  return ND_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------ session methods
+//
+// ResidentExecutionSession (backends/backend.ts:65-80) at method granularity,
+// as NeedleRuntime.step drives it (model/runtime.ts:314-375, 444-463,
+// 554-564): the host keeps the position, the token history and the engram
+// hashing; the device keeps the KV cache, the engram ring, the lanes and the
+// confidence pool.  A resident token is begin -> (prepare engrams) ->
+// forward token (or forward layer 0..L-1) -> finish -> (select).
+
+namespace {
+
+nd_status check_session(nd_ctx* ctx, nd_needle* n) {
+  if (!n) return nd_fail(ctx, ND_ERR_INVALID, "model is NULL");
+  if (!n->arena || !n->max_length)
+    return nd_fail(ctx, ND_ERR_INVALID, "Call runtime.reset() before decoding");
+  return use_api(ctx, n, 2);
+}
+
+int site_of(const nd_needle* n, uint32_t layer) {
+  for (uint32_t si = 0; si < n->d.n_sites; ++si)
+    if (n->d.sites[si] == layer) return (int)si;
+  return -1;
+}
+
+hipError_t enqueue_position(nd_needle* n, uint32_t position, hipStream_t s) {
+  hipLaunchKernelGGL(n2_position_kernel, dim3(1), dim3(64), 0, s, n->st, position, n->inv_freq,
+                     n->rope);
+  return hipGetLastError();
+}
+
+// The session's final mix (post of the last layer, the lane mean and final
+// norm when tail), the pool and the logits.
+hipError_t enqueue_session_final(nd_needle* n, bool tail, hipStream_t s) {
+  hipError_t e;
+  if (tail || pool_on(n)) {
+    const uint32_t parts = (n->post_pending ? kMixPost | kMixCell : 0) | (tail ? kMixFinal : 0);
+    if ((e = enqueue_mix(n, n->d.layers, parts, s)) != hipSuccess) return e;
+    n->post_pending = false;
+  }
+  return enqueue_final(n, tail, false, nullptr, 0, s);
+}
+
+void close_token(nd_needle* n) {
+  n->token_open = n->engrams_ready = n->host_engrams = false;
+  n->position = n->token_position + 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+nd_status nd_needle_begin_token(nd_ctx* ctx, nd_needle* n, const float* lanes) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_session(ctx, n);
+  if (st != ND_OK) return st;
+  if (!lanes) return nd_fail(ctx, ND_ERR_INVALID, "lanes is NULL");
+  // A token left open (a runtime that aborted between beginResidentToken and
+  // finish, runtime.ts:338-342) is dropped; its position was not advanced.
+  const size_t D = n->d.dim;
+  hipStream_t s = ctx->stream;
+  ND_HIP(ctx, stage_copy(n, kStageLanes, n->x, lanes, (size_t)n->d.lanes * D * 4, 0, s));
+  // Every lane holds the scaled embedding (runtime.ts:312-313): cell 0 of the
+  // confidence pool (runtime.ts:310).
+  if (pool_on(n))
+    ND_HIP(ctx, hipMemcpyAsync(n->cells, n->x, D * 4, hipMemcpyDeviceToDevice, s));
+  n->token_open = true;
+  n->post_pending = n->select_ready = false;
+  n->next_layer = 0;
+  return ND_OK;
+}
+
+nd_status nd_needle_prepare_engrams(nd_ctx* ctx, nd_needle* n, const uint32_t* indices,
+                                    const uint32_t* valid, uint32_t tables, uint32_t position) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_session(ctx, n);
+  if (st != ND_OK) return st;
+  const nd_needle_desc& d = n->d;
+  if (!d.n_sites) return nd_fail(ctx, ND_ERR_INVALID, "the model has no engram layers");
+  if (!indices || !valid) return nd_fail(ctx, ND_ERR_INVALID, "indices or valid is NULL");
+  if (tables != d.engram_tables)
+    return nd_fail(ctx, ND_ERR_INVALID, "%u engram lookups for %u tables", tables,
+                   d.engram_tables);
+  if (n->token_open)
+    return nd_fail(ctx, ND_ERR_INVALID, "engrams are prepared before the token begins");
+  if (position >= n->max_length)
+    return nd_fail(ctx, ND_ERR_OVERFLOW, "Position %u reached runtime limit %u", position,
+                   n->max_length);
+  uint32_t buf[32];
+  for (uint32_t t = 0; t < tables; ++t) {
+    if (valid[t] && indices[t] >= d.engram_slots)
+      return nd_fail(ctx, ND_ERR_INVALID, "engram index %u is outside %u slots", indices[t],
+                     d.engram_slots);
+    buf[t] = valid[t] ? indices[t] : 0;
+    buf[tables + t] = valid[t] ? 1 : 0;
+  }
+  hipStream_t s = ctx->stream;
+  ND_HIP(ctx, stage_copy(n, kStageLookup, n->lookup, buf, (size_t)2 * tables * 4, 0, s));
+  ND_HIP(ctx, enqueue_position(n, position, s));
+  hipLaunchKernelGGL(n2_gather_kernel, dim3(1), dim3(kWg), 0, s, begin_args(n), n->lookup);
+  ND_HIP(ctx, hipGetLastError());
+  ND_HIP(ctx, enqueue_engrams(n, s));
+  n->engrams_ready = true;
+  return ND_OK;
+}
+
+nd_status nd_needle_forward_layer(nd_ctx* ctx, nd_needle* n, uint32_t layer, uint32_t position,
+                                  const float* engram_key, const float* engram_value) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_session(ctx, n);
+  if (st != ND_OK) return st;
+  const nd_needle_desc& d = n->d;
+  if (!n->token_open) return nd_fail(ctx, ND_ERR_INVALID, "Resident layers run after beginResidentToken");
+  if (layer != n->next_layer)
+    return nd_fail(ctx, ND_ERR_INVALID, "layer %u forwarded out of order (next is %u)", layer,
+                   n->next_layer);
+  if (position >= n->max_length)
+    return nd_fail(ctx, ND_ERR_OVERFLOW, "Position %u reached runtime limit %u", position,
+                   n->max_length);
+  if (layer > 0 && position != n->token_position)
+    return nd_fail(ctx, ND_ERR_INVALID, "layer %u at position %u follows position %u", layer,
+                   position, n->token_position);
+  hipStream_t s = ctx->stream;
+  if (layer == 0) {
+    ND_HIP(ctx, enqueue_position(n, position, s));
+    n->token_position = position;
+  }
+  const int site = site_of(n, layer);
+  if (site >= 0) {
+    const size_t D = d.dim, S = d.n_sites;
+    if (engram_key && engram_value) {
+      // The host's #engramStep result (runtime.ts:820-877) for this site;
+      // the runtime hands these over only when the device did not prepare
+      // the token's engrams (runtime.ts:315-325).
+      if (n->engrams_ready)
+        return nd_fail(ctx, ND_ERR_INVALID, "the engrams of this token were prepared resident");
+      ND_HIP(ctx, stage_copy(n, (StageSlot)(kStageEngram + 2 * site), n->host_eng + site * D,
+                             engram_key, D * 4, 0, s));
+      ND_HIP(ctx, stage_copy(n, (StageSlot)(kStageEngram + 2 * site + 1),
+                             n->host_eng + (S + site) * D, engram_value, D * 4, 0, s));
+      n->host_engrams = true;
+    } else if (!n->engrams_ready) {
+      return nd_fail(ctx, ND_ERR_INVALID, "Missing engram values for layer %u", layer);
+    }
+  }
+  const uint32_t parts = (n->post_pending ? kMixPost | kMixCell : 0) | kMixPre;
+  ND_HIP(ctx, enqueue_mix(n, layer, parts, s));
+  ND_HIP(ctx, enqueue_block(n, layer, s));
+  n->post_pending = true;
+  ++n->next_layer;
+  return ND_OK;
+}
+
+nd_status nd_needle_forward_token(nd_ctx* ctx, nd_needle* n, uint32_t position,
+                                  const float* engram_keys, const float* engram_values) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!n) return nd_fail(ctx, ND_ERR_INVALID, "model is NULL");
+  if ((engram_keys == nullptr) != (engram_values == nullptr))
+    return nd_fail(ctx, ND_ERR_INVALID, "engram keys and values come together");
+  const size_t D = n->d.dim;
+  for (uint32_t l = 0; l < n->d.layers; ++l) {
+    const int site = site_of(n, l);
+    const float* k = engram_keys && site >= 0 ? engram_keys + site * D : nullptr;
+    const float* v = engram_values && site >= 0 ? engram_values + site * D : nullptr;
+    const nd_status st = nd_needle_forward_layer(ctx, n, l, position, k, v);
+    if (st != ND_OK) return st;
+  }
+  return ND_OK;
+}
+
+nd_status nd_needle_finish_token(nd_ctx* ctx, nd_needle* n, uint32_t want_logits, float* logits) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_session(ctx, n);
+  if (st != ND_OK) return st;
+  if (!n->token_open || n->next_layer != n->d.layers)
+    return nd_fail(ctx, ND_ERR_INVALID, "finishResidentToken after every layer (%u of %u ran)",
+                   n->token_open ? n->next_layer : 0, n->d.layers);
+  if (want_logits && !logits) return nd_fail(ctx, ND_ERR_INVALID, "logits is NULL");
+  hipStream_t s = ctx->stream;
+  ND_HIP(ctx, enqueue_session_final(n, want_logits != 0, s));
+  close_token(n);
+  if (!want_logits) return ND_OK;
+  ND_HIP(ctx, hipMemcpyAsync(logits, n->logits, (size_t)n->d.vocab * 4, hipMemcpyDeviceToHost, s));
+  ND_HIP(ctx, hipStreamSynchronize(s));
+  return ND_OK;
+}
+
+nd_status nd_needle_finish_token_for_selection(nd_ctx* ctx, nd_needle* n) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_session(ctx, n);
+  if (st != ND_OK) return st;
+  if (!n->token_open || n->next_layer != n->d.layers)
+    return nd_fail(ctx, ND_ERR_INVALID,
+                   "finishResidentTokenForSelection after every layer (%u of %u ran)",
+                   n->token_open ? n->next_layer : 0, n->d.layers);
+  ND_HIP(ctx, enqueue_session_final(n, true, ctx->stream));
+  close_token(n);
+  n->select_ready = true;
+  return ND_OK;
+}
+
+nd_status nd_needle_select_token(nd_ctx* ctx, nd_needle* n, const uint32_t* allowed,
+                                 uint32_t count, uint32_t* id, double* log_probability) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_session(ctx, n);
+  if (st != ND_OK) return st;
+  if (!id || !log_probability) return nd_fail(ctx, ND_ERR_INVALID, "NULL argument");
+  if (!n->select_ready)
+    return nd_fail(ctx, ND_ERR_BACKEND, "Token selection did not produce a result");
+  const uint32_t vocab = n->d.vocab;
+  hipStream_t s = ctx->stream;
+  if (allowed) {
+    // selectToken (runtime.ts:880-899): a non-empty id list inside the logits.
+    if (count == 0) return nd_fail(ctx, ND_ERR_INVALID, "Allowed token set is empty");
+    if (count > vocab)
+      return nd_fail(ctx, ND_ERR_INVALID, "Allowed token set is larger than the vocabulary");
+    for (uint32_t i = 0; i < count; ++i)
+      if (allowed[i] >= vocab)
+        return nd_fail(ctx, ND_ERR_INVALID, "Token %u is outside logits", allowed[i]);
+    ND_HIP(ctx, stage_copy(n, kStageAllowed, n->allowed, allowed, (size_t)count * 4, 0, s));
+  }
+  ND_HIP(ctx, nd_launch_select_list(n->logits, vocab, allowed ? n->allowed : nullptr,
+                                    allowed ? count : 0, n->sel_id, n->sel_lp, s));
+  n->select_ready = false;
+  ND_HIP(ctx, hipMemcpyAsync(id, n->sel_id, 4, hipMemcpyDeviceToHost, s));
+  ND_HIP(ctx, hipMemcpyAsync(log_probability, n->sel_lp, 8, hipMemcpyDeviceToHost, s));
+  ND_HIP(ctx, hipStreamSynchronize(s));
+  return ND_OK;
+}
+
+nd_status nd_needle_read_lanes(nd_ctx* ctx, nd_needle* n, float* lanes) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_session(ctx, n);
+  if (st != ND_OK) return st;
+  if (!lanes) return nd_fail(ctx, ND_ERR_INVALID, "lanes is NULL");
+  hipStream_t s = ctx->stream;
+  if (n->token_open && n->post_pending) {
+    // The post half owed to the last layer run: the lanes after it.
+    ND_HIP(ctx, enqueue_mix(n, n->next_layer, kMixPost | kMixCell, s));
+    n->post_pending = false;
+  }
+  ND_HIP(ctx, hipMemcpyAsync(lanes, n->x, (size_t)n->d.lanes * n->d.dim * 4,
+                             hipMemcpyDeviceToHost, s));
+  ND_HIP(ctx, hipStreamSynchronize(s));
+  return ND_OK;
+}
+
+nd_status nd_needle_forward(nd_ctx* ctx, nd_needle* n, uint32_t layer, uint32_t position,
+                            const float* input, const float* block_input,
+                            const float* update_input, const float* x, const float* phi_post,
+                            const float* phi_residual, float* next_x) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_session(ctx, n);
+  if (st != ND_OK) return st;
+  const nd_needle_desc& d = n->d;
+  if (!input || !block_input || !update_input || !x || !phi_post || !phi_residual || !next_x)
+    return nd_fail(ctx, ND_ERR_INVALID, "NULL argument");
+  if (n->token_open)
+    return nd_fail(ctx, ND_ERR_INVALID, "forward() runs a layer of a token not begun resident");
+  if (layer >= d.layers)
+    return nd_fail(ctx, ND_ERR_INVALID, "layer %u is outside [0, %u)", layer, d.layers);
+  if (position >= n->max_length)
+    return nd_fail(ctx, ND_ERR_OVERFLOW, "Position %u reached runtime limit %u", position,
+                   n->max_length);
+  const size_t D = d.dim, ln = d.lanes;
+  hipStream_t s = ctx->stream;
+  // One staged copy of every input, then their places on the device.
+  const float* parts[] = {input, block_input, update_input, x, phi_post, phi_residual};
+  float* dsts[] = {n->ain, n->blk, n->upd, n->x, n->phi_post_v, n->phi_res_v};
+  const size_t sizes[] = {D, D, D, ln * D, ln, ln * ln};
+  size_t off = 0;
+  ND_HIP(ctx, hipEventSynchronize(n->stage_done[kStageForward]));
+  float* slot = reinterpret_cast<float*>(n->pinned + n->stage_off[kStageForward]);
+  for (int i = 0; i < 6; ++i) {
+    std::memcpy(slot + off, parts[i], sizes[i] * 4);
+    off += sizes[i];
+  }
+  ND_HIP(ctx, hipMemcpyAsync(n->fwd_in, slot, off * 4, hipMemcpyHostToDevice, s));
+  ND_HIP(ctx, hipEventRecord(n->stage_done[kStageForward], s));
+  off = 0;
+  for (int i = 0; i < 6; ++i) {
+    ND_HIP(ctx, hipMemcpyAsync(dsts[i], n->fwd_in + off, sizes[i] * 4, hipMemcpyDeviceToDevice, s));
+    off += sizes[i];
+  }
+  ND_HIP(ctx, enqueue_position(n, position, s));
+  // Q/K/V/gate, norms and RoPE, #storeKV, gated attention, Wo (with the
+  // layer's routing from the host's phi rows), then the post half: sandwich
+  // norm, Hadamard MLP, h-post and the Sinkhorn routing of the lanes -- the
+  // next lanes ("nextX", runtime.ts:456-458).
+  ND_HIP(ctx, enqueue_block(n, layer, s));
+  ND_HIP(ctx, enqueue_mix(n, layer + 1, kMixPost, s));
+  ND_HIP(ctx, hipMemcpyAsync(next_x, n->x, ln * D * 4, hipMemcpyDeviceToHost, s));
+  ND_HIP(ctx, hipStreamSynchronize(s));
+  if (layer + 1 == d.layers) n->position = position + 1;
   return ND_OK;
 }
 

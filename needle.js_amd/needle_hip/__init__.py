@@ -11,18 +11,23 @@ from .cact import CactArchive, CqMatrix, pack_codes, parse_cact, write_cact
 from .errors import NeedleError, invariant
 from .kv import HipKvCache
 from .needle2 import Needle2Geometry, Needle2Weights
-from .runtime import GenerationResult, HipNeedleSession, NeedleModel, NeedleRuntime
+from .runtime import (AbortSignal, GenerationResult, HipNeedleSession, Needle2Resident,
+                      NeedleModel, NeedleRuntime, ResidentRuntime, RuntimeOptions)
 
 __all__ = [
+    "AbortSignal",
     "CactArchive",
     "CqMatrix",
     "GenerationResult",
     "HipBackend",
     "HipNeedleSession",
+    "Needle2Resident",
     "Needle2Geometry",
     "Needle2Weights",
     "NeedleModel",
     "NeedleRuntime",
+    "ResidentRuntime",
+    "RuntimeOptions",
     "HipKvCache",
     "Int8Matrix",
     "MatrixRowRange",

@@ -74,8 +74,9 @@ class HipBackend:
     kind = "hip"
     name = "MI355X HIP (gfx950)"
 
-    def __init__(self, weights=None, device: int = 0):
+    def __init__(self, weights=None, device: int = 0, resident_layers: bool = True):
         self.weights = weights
+        self.resident_layers = resident_layers
         self.lib = L.load_library()
         ctx = C.c_void_p()
         status = self.lib.nd_create(device, C.byref(ctx))
@@ -184,13 +185,19 @@ class HipBackend:
             return output
         return result
 
-    def create_resident_session(self, weights):
-        """createResidentSession (backends/backend.ts:82-110): Needle 2
-        weights resident in HBM with one runtime state."""
+    def create_resident_session(self):
+        """createResidentSession (backends/backend.ts:103-104): a
+        ResidentExecutionSession over this backend's Needle 2 weights (their
+        matrices resident in HBM with one runtime state), or None when the
+        backend serves no Needle 2 weights.  Sessions run whole tokens on the
+        device unless the backend was built with resident_layers=False."""
+        from .needle2 import Needle2Weights
         from .runtime import HipNeedleSession
 
         self._alive()
-        return HipNeedleSession(self, weights)
+        if not isinstance(self.weights, Needle2Weights):
+            return None
+        return HipNeedleSession(self, self.weights, self.resident_layers)
 
     def dispose(self) -> None:
         if self._disposed:

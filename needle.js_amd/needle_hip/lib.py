@@ -104,7 +104,7 @@ SIGNATURES = {
     "nd_prefill_read_projections": (I32, [P, P, P]),
     "nd_needle_create": (I32, [P, P, PP]),
     "nd_needle_free": (I32, [P, P]),
-    "nd_needle_reset": (I32, [P, P, U32, U32]),
+    "nd_needle_reset": (I32, [P, P, U32, U32, U32, U32]),
     "nd_needle_kv": (P, [P]),
     "nd_needle_position": (U32, [P]),
     "nd_needle_confidence": (I32, [P, P, C.POINTER(C.c_double)]),
@@ -112,6 +112,15 @@ SIGNATURES = {
     "nd_needle_prefill": (I32, [P, P, P, U32, P]),
     "nd_needle_step_select": (I32, [P, P, U32, P, U32, P, P]),
     "nd_needle_generate": (I32, [P, P, P, U32, U32, U32, U32, P, P, P]),
+    "nd_needle_begin_token": (I32, [P, P, P]),
+    "nd_needle_prepare_engrams": (I32, [P, P, P, P, U32, U32]),
+    "nd_needle_forward_layer": (I32, [P, P, U32, U32, P, P]),
+    "nd_needle_forward_token": (I32, [P, P, U32, P, P]),
+    "nd_needle_finish_token": (I32, [P, P, U32, P]),
+    "nd_needle_finish_token_for_selection": (I32, [P, P]),
+    "nd_needle_select_token": (I32, [P, P, P, U32, P, P]),
+    "nd_needle_read_lanes": (I32, [P, P, P]),
+    "nd_needle_forward": (I32, [P, P, U32, U32, P, P, P, P, P, P, P]),
     "nd_pieces_upload": (I32, [P, P, P, P, U32, PP]),
     "nd_pieces_free": (I32, [P, P]),
     "nd_grammar_upload": (I32, [P, P, U32, PP]),

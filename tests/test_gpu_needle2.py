@@ -57,7 +57,7 @@ def check_kv(model, ref, g, written, sink, what):
     used = np.flatnonzero(pos >= 0)
     for layer in range(g.layers):
         for h in range(g.kv_heads):
-            gk, gv, gks, gvs = model.session.kv_read(layer, h)
+            gk, gv, gks, gvs = model.resident.kv_read(layer, h)
             rk, rv, rks, rvs = ref.kv_read(layer, h)
             assert gk.shape == rk.shape
             if layer == 0:
@@ -93,7 +93,7 @@ def small(hip):
 def test_step_logits_and_kv_match_oracle(small, sink):
     w, model = small
     say("needle2 step sink", sink)
-    rt = model.create_runtime()
+    rt = model.create_resident_runtime()
     rt.reset(SMALL.max_length, sink)
     ref = oracle.Needle2(w).runtime(SMALL.max_length, sink)
     ref.capture_kv(0, SMALL.max_length)
@@ -106,7 +106,7 @@ def test_step_logits_and_kv_match_oracle(small, sink):
         assert rt.position == i + 1
         if i in (0, 9, len(tokens) - 1):
             close_confidence(rt.resolve_confidence(), ref.confidence(), ("confidence", sink, i))
-    assert model.session.kv_read(0, 0)[0].shape == (sink + SMALL.kv_window, 64)
+    assert model.resident.kv_read(0, 0)[0].shape == (sink + SMALL.kv_window, 64)
     check_kv(model, ref, SMALL, len(tokens), sink, f"steps sink {sink}")
 
 
@@ -122,7 +122,7 @@ def test_attention_group_sizes_and_chunked_slots(hip, heads, kv_heads, window, l
     w = Needle2Weights(geo, 41)
     model = NeedleModel(hip, w)
     try:
-        rt = model.create_runtime()
+        rt = model.create_resident_runtime()
         rt.reset(length, 0)
         ref = oracle.Needle2(w).runtime(length, 0)
         tokens = synth.Stream(6, f"n2paths{heads}{window}").integers(12, 0, geo.vocab - 1)
@@ -143,9 +143,9 @@ def test_step_ignores_stale_nan_slots(small):
 
     w, model = small
     say("needle2 stale NaN slots")
-    rt = model.create_runtime()
+    rt = model.create_resident_runtime()
     rt.reset(SMALL.max_length, 0)
-    sess = model.session
+    sess = model.resident
     kv = sess.lib.nd_needle_kv(sess.handle)
     alloc = C.c_uint32()
     sess._check(sess.lib.nd_kv_info(kv, C.byref(alloc), None, None, None, None), "nd_kv_info")
@@ -163,7 +163,7 @@ def test_step_ignores_stale_nan_slots(small):
 def test_prefill_and_step_selected(small):
     w, model = small
     say("needle2 prefill + step_selected")
-    rt = model.create_runtime()
+    rt = model.create_resident_runtime()
     rt.reset(40, 2)
     ref = oracle.Needle2(w).runtime(40, 2)
     prompt = synth.Stream(6, "n2prompt").integers(20, 0, SMALL.vocab - 1)
@@ -194,7 +194,7 @@ def test_generate_matches_stepwise_oracle(small):
     w, model = small
     say("needle2 generate small")
     prompt = synth.Stream(8, "n2gen").integers(16, 3, SMALL.vocab - 1)
-    res = model.generate(prompt, max_new_tokens=20, sink_tokens=1, eos=None)
+    res = model.generate_resident(prompt, max_new_tokens=20, sink_tokens=1, eos=None)
     ref = oracle.Needle2(w).runtime(len(prompt) + 20, 1)
     for t in prompt:
         logits = ref.step(int(t))
@@ -209,7 +209,7 @@ def test_generate_matches_stepwise_oracle(small):
     np.testing.assert_allclose(res.token_log_probabilities, lps, rtol=1e-3, atol=1e-3)
     assert res.finish_reason == "length" and res.generated_tokens == 20
     # Graph replays and direct launches give the same sequence.
-    rt = model.create_runtime()
+    rt = model.create_resident_runtime()
     rt.reset(len(prompt) + 20, 1)
     logits = rt.prefill(prompt)
     assert int(np.argmax(logits)) == ids[0]
@@ -223,24 +223,24 @@ def test_generate_stops_before_eos_and_at_limit(small):
     w, model = small
     say("needle2 generate eos/limit")
     prompt = synth.Stream(9, "n2eos").integers(10, 3, SMALL.vocab - 1)
-    full = model.generate(prompt, max_new_tokens=12, eos=None)
+    full = model.generate_resident(prompt, max_new_tokens=12, eos=None)
     stop = full.token_ids[4]
     first = full.token_ids.index(stop)
-    cut = model.generate(prompt, max_new_tokens=12, eos=stop)
+    cut = model.generate_resident(prompt, max_new_tokens=12, eos=stop)
     assert cut.token_ids == full.token_ids[:first] and cut.finish_reason == "eos"
     # The context limit caps the count: 48 - 40 = 8 tokens.
     long_prompt = synth.Stream(10, "n2lim").integers(40, 3, SMALL.vocab - 1)
-    lim = model.generate(long_prompt, max_new_tokens=30, eos=None)
+    lim = model.generate_resident(long_prompt, max_new_tokens=30, eos=None)
     assert lim.generated_tokens == 8
     with pytest.raises(NeedleError) as e:
-        model.generate(synth.Stream(11, "n2over").integers(48, 3, SMALL.vocab - 1), 4, eos=None)
+        model.generate_resident(synth.Stream(11, "n2over").integers(48, 3, SMALL.vocab - 1), 4, eos=None)
     assert e.value.code == "CONTEXT_OVERFLOW"
 
 
 def test_runtime_errors(small):
     w, model = small
     say("needle2 errors")
-    rt = model.create_runtime()
+    rt = model.create_resident_runtime()
     with pytest.raises(NeedleError) as e:
         rt.reset(SMALL.max_length + 1)
     assert e.value.code == "CONTEXT_OVERFLOW"
@@ -271,7 +271,7 @@ def test_generate_full_geometry_greedy_identical(hip):
     model = NeedleModel(hip, w)
     try:
         prompt = synth.Stream(2026, "needle2.prompt").integers(128, 0, g.vocab - 1)
-        res = model.generate(prompt, max_new_tokens=64, eos=None)
+        res = model.generate_resident(prompt, max_new_tokens=64, eos=None)
         ref = oracle.Needle2(w).runtime(128 + 64, 0)
         ref.capture_kv(0, 128 + 64)
         for t in prompt[:-1]:
@@ -290,7 +290,7 @@ def test_generate_full_geometry_greedy_identical(hip):
         # generated token is never run), over the 256-position window.
         check_kv(model, ref, g, 128 + 63, 0, "generate")
         # the graph-replayed steps pooled every token they ran
-        close_confidence(model.session.confidence(), ref.confidence(), "generate confidence")
+        close_confidence(model.resident.confidence(), ref.confidence(), "generate confidence")
     finally:
         model.dispose()
 
@@ -300,14 +300,14 @@ def test_confidence_absent_or_disabled(hip):
     w = Needle2Weights(SMALL, 32)
     model = NeedleModel(hip, w, collect_confidence=False)
     try:
-        rt = model.create_runtime()
+        rt = model.create_resident_runtime()
         rt.reset(8)
         rt.step(3)
         assert rt.resolve_confidence() is None
         import ctypes as C
         out = C.c_double()
-        st = hip.lib.nd_needle_confidence(hip.ctx, model.session.handle, C.byref(out))
-        assert st != 0 and b"no confidence head" in hip.lib.nd_last_error(hip.ctx)
+        st = hip.lib.nd_needle_confidence(hip.ctx, model.resident.handle, C.byref(out))
+        assert st != 0 and b"collectConfidence" in hip.lib.nd_last_error(hip.ctx)
     finally:
         model.dispose()
 
@@ -328,7 +328,7 @@ def test_batched_prefill_then_steps(hip, window, sink, n_prompt, max_length):
     w = Needle2Weights(g, 41)
     model = NeedleModel(hip, w)
     try:
-        rt = model.create_runtime()
+        rt = model.create_resident_runtime()
         rt.reset(g.max_length, sink)
         ref = oracle.Needle2(w).runtime(g.max_length, sink)
         ref.capture_kv(0, g.max_length)
