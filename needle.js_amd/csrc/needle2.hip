@@ -678,8 +678,9 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
 // head_row + slot with #storeKV's arithmetic (runtime.ts:679-717).
 __device__ __forceinline__ void head_epilogue(float val, uint32_t lane, int role, double sn,
                                               double cs, float nscale, float* q_dst,
-                                              int8_t* Kc, int8_t* Vc, float* Ks, float* Vs,
-                                              size_t head_row, uint32_t slot, uint32_t alloc) {
+                                              void* Kc, void* Vc, float* Ks, float* Vs,
+                                              size_t head_row, uint32_t slot, uint32_t alloc,
+                                              uint32_t f32) {
   float out = val;
   if (role != 2) {
     const double xd = val;
@@ -695,11 +696,17 @@ __device__ __forceinline__ void head_epilogue(float val, uint32_t lane, int role
   }
   if (slot >= alloc) return;  // the host keeps positions below the runtime limit
   const size_t crow = head_row + slot;
+  if (f32) {  // kvCache "float32": the value itself, scale 1 (runtime.ts:686-692)
+    reinterpret_cast<float*>(role == 2 ? Vc : Kc)[crow * kHd + lane] = out;
+    if (lane == 0) (role == 2 ? Vs : Ks)[crow] = 1.f;
+    return;
+  }
   const float am = wave_absmax_js(out);
   const double mx = (am != am) ? (double)am : fmax(1e-12, (double)am);
   const double sc = mx / 127.0;
   const double code = rint((double)out / sc);
-  (role == 2 ? Vc : Kc)[crow * kHd + lane] = code != code ? (int8_t)0 : (int8_t)(int)code;
+  reinterpret_cast<int8_t*>(role == 2 ? Vc : Kc)[crow * kHd + lane] =
+      code != code ? (int8_t)0 : (int8_t)(int)code;
   if (lane == 0) (role == 2 ? Vs : Ks)[crow] = (float)sc;
 }
 
@@ -717,9 +724,9 @@ __global__ __launch_bounds__(256) void n2_qkv_kernel(
     uint32_t d, uint32_t heads, uint32_t kv_heads, const uint32_t* __restrict__ st,
     const float* __restrict__ q_norm, const float* __restrict__ k_norm,
     const double* __restrict__ rope, float* __restrict__ q_out, float* __restrict__ gate_out,
-    int8_t* __restrict__ Kc, int8_t* __restrict__ Vc, float* __restrict__ Ks,
+    void* __restrict__ Kc, void* __restrict__ Vc, float* __restrict__ Ks,
     float* __restrict__ Vs, uint32_t layer, uint32_t alloc, uint32_t sink, uint32_t window,
-    RouteArgs route) {
+    uint32_t f32, RouteArgs route) {
   __shared__ float xs[512];
   __shared__ float rows[64];
   const uint32_t b = blockIdx.x, t = threadIdx.x;
@@ -769,7 +776,7 @@ __global__ __launch_bounds__(256) void n2_qkv_kernel(
   const int role = b < nq ? 0 : (b < nq + nk ? 1 : 2);
   const uint32_t h = role == 0 ? b : (role == 1 ? b - nq : b - nq - nk);
   head_epilogue(val, lane, role, rs, rc, nscale, q_out + (size_t)h * kHd, Kc, Vc, Ks, Vs,
-                ((size_t)layer * kv_heads + h) * alloc, kv_slot(pos, sink, window), alloc);
+                ((size_t)layer * kv_heads + h) * alloc, kv_slot(pos, sink, window), alloc, f32);
 }
 
 // ---------------------------------------------------------------- prefill
@@ -876,8 +883,9 @@ __global__ __launch_bounds__(64) void n2_rope_store_batch_kernel(
     const float* __restrict__ qkvg, uint32_t ld, uint32_t heads, uint32_t kv_heads,
     const float* __restrict__ q_norm, const float* __restrict__ k_norm,
     const double* __restrict__ inv_freq, uint32_t p0, float* __restrict__ q_out,
-    int8_t* __restrict__ Kc, int8_t* __restrict__ Vc, float* __restrict__ Ks,
-    float* __restrict__ Vs, uint32_t layer, uint32_t alloc, uint32_t sink, uint32_t window) {
+    void* __restrict__ Kc, void* __restrict__ Vc, float* __restrict__ Ks,
+    float* __restrict__ Vs, uint32_t layer, uint32_t alloc, uint32_t sink, uint32_t window,
+    uint32_t f32) {
   const uint32_t b = blockIdx.x, m = blockIdx.y, lane = threadIdx.x, pos = p0 + m;
   const int role = b < heads ? 0 : (b < heads + kv_heads ? 1 : 2);
   const uint32_t h = role == 0 ? b : (role == 1 ? b - heads : b - heads - kv_heads);
@@ -886,7 +894,7 @@ __global__ __launch_bounds__(64) void n2_rope_store_batch_kernel(
   sincos((double)pos * inv_freq[lane & 31], &sn, &cs);
   head_epilogue(val, lane, role, sn, cs, role == 0 ? q_norm[lane] : k_norm[lane],
                 q_out + ((size_t)m * heads + h) * kHd, Kc, Vc, Ks, Vs,
-                ((size_t)layer * kv_heads + h) * alloc, kv_slot(pos, sink, window), alloc);
+                ((size_t)layer * kv_heads + h) * alloc, kv_slot(pos, sink, window), alloc, f32);
 }
 
 // Confidence pool state (OnlineProbePool, runtime.ts:48-62) for up to
@@ -1155,7 +1163,7 @@ struct nd_needle {
   uint32_t *pf_positions = nullptr, *pf_counters = nullptr;
   // Step graphs, valid for (graph_alloc, graph_sink).
   hipGraphExec_t graphs[3] = {nullptr, nullptr, nullptr};
-  uint32_t graph_alloc = 0, graph_sink = 0;
+  uint32_t graph_alloc = 0, graph_sink = 0, graph_mode = 0;
   // Confidence probe head (absent when the description has no probes):
   // probes [P][d] and projection row 0 [P * d] in params, the pool state in
   // the arena's cleared part, cells of one step (or one prefill pass) and
@@ -1310,8 +1318,8 @@ hipError_t enqueue_block(nd_needle* n, uint32_t l, hipStream_t s) {
   hipLaunchKernelGGL(n2_qkv_kernel, dim3(wm.n / kHd + 1), dim3(256), 0, s, wm.w, wm.scales,
                      n->ain, D, d.heads, d.kv_heads, n->st, n->params + n->o_qn + (size_t)l * kHd,
                      n->params + n->o_kn + (size_t)l * kHd, n->rope, n->q, n->qkvg,
-                     (int8_t*)n->kv.k, (int8_t*)n->kv.v, n->kv.ks, n->kv.vs, l, n->kv.alloc,
-                     n->kv.sink, n->kv.window, ra);
+                     n->kv.k, n->kv.v, n->kv.ks, n->kv.vs, l, n->kv.alloc, n->kv.sink,
+                     n->kv.window, n->kv.mode == ND_KV_FLOAT32 ? 1u : 0u, ra);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   e = nd_launch_attention_gated(&n->kv, l, n->st + 1, n->max_length - 1, n->q, d.heads, n->qkvg,
@@ -1419,12 +1427,14 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
 enum GraphKind { kGraphPrompt = 0, kGraphPromptSelect = 1, kGraphDecodeSelect = 2 };
 
 // Launches the step graph of `kind`, capturing and instantiating it first if
-// the cached one was built for another cache geometry.
+// the cached one was built for another cache geometry, KV mode or pooling.
 nd_status launch_graph(nd_ctx* ctx, nd_needle* n, GraphKind kind) {
-  if (n->graph_alloc != n->kv.alloc || n->graph_sink != n->kv.sink) {
+  const uint32_t mode = n->kv.mode | (pool_on(n) ? 2u : 0u);
+  if (n->graph_alloc != n->kv.alloc || n->graph_sink != n->kv.sink || n->graph_mode != mode) {
     drop_graphs(n);
     n->graph_alloc = n->kv.alloc;
     n->graph_sink = n->kv.sink;
+    n->graph_mode = mode;
   }
   hipStream_t s = ctx->stream;
   if (!n->graphs[kind]) {
@@ -1640,8 +1650,9 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
     hipLaunchKernelGGL(n2_rope_store_batch_kernel, dim3(d.heads + 2 * d.kv_heads, M), dim3(64), 0,
                        s, n->pf_qkvg, qkv_ld, d.heads, d.kv_heads,
                        n->params + n->o_qn + (size_t)l * kHd, n->params + n->o_kn + (size_t)l * kHd,
-                       n->inv_freq, p0, n->pf_q, (int8_t*)n->kv.k, (int8_t*)n->kv.v, n->kv.ks,
-                       n->kv.vs, l, n->kv.alloc, n->kv.sink, n->kv.window);
+                       n->inv_freq, p0, n->pf_q, n->kv.k, n->kv.v, n->kv.ks, n->kv.vs, l,
+                       n->kv.alloc, n->kv.sink, n->kv.window,
+                       n->kv.mode == ND_KV_FLOAT32 ? 1u : 0u);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     e = nd_launch_attention_batch(&n->kv, l, n->pf_positions, M, d.kv_heads, 0u,
                                   d.heads / d.kv_heads, p0 + M - 1, n->pf_q, n->pf_att,
@@ -1934,8 +1945,6 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
   const nd_needle_desc& d = n->d;
   if (kv_cache != ND_KV_INT8 && kv_cache != ND_KV_FLOAT32)
     return nd_fail(ctx, ND_ERR_INVALID, "unknown kvCache mode %u", kv_cache);
-  if (kv_cache == ND_KV_FLOAT32)
-    return nd_fail(ctx, ND_ERR_UNSUPPORTED, "the resident Needle 2 runtime keeps an int8 KV cache");
   if (max_length == 0 || max_length > d.max_length)
     return nd_fail(ctx, ND_ERR_OVERFLOW, "Runtime length %u is outside model limit %u",
                    max_length, d.max_length);
@@ -1954,7 +1963,9 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
                             al((size_t)d.kv_heads * kAttnCounterStride * 4),
                             cb * al(P8 * kMaxChunks), cb * al(P8 * kMaxChunks),
                             cb * al(P8 * D), al(64), al(64),
-                            al((size_t)d.vocab * 4), al(rows * kHd), al(rows * kHd), al(rows * 4),
+                            // K and V sized for float32 rows (kvCache "float32")
+                            al((size_t)d.vocab * 4), al(rows * kHd * 4), al(rows * kHd * 4),
+                            al(rows * 4),
                             al(rows * 4), al((size_t)ln * D * 4), al(D * 4), al(D * 4), al(D * 4),
                             al((size_t)(2 * qw + 2 * kw) * 4), al(qw * 4), al(qw * 4), al(D * 4),
                             al(ln * 4), al(ln * ln * 4), al(D * 4), al((size_t)d.vocab * 4),
@@ -2053,7 +2064,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
   kv.sink = n->sink;
   kv.window = d.kv_window;
   kv.alloc = d.kv_window > 0 ? std::min(max_length, n->sink + d.kv_window) : max_length;
-  kv.mode = ND_KV_INT8;
+  kv.mode = kv_cache;
   return ND_OK;
 }
 

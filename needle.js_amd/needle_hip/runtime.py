@@ -111,6 +111,7 @@ class Needle2Resident:
         self.handle = handle
         self.lib = lib
         self.collect_confidence = True
+        self.kv_cache = "int8"
 
     @property
     def ctx(self):
@@ -148,6 +149,7 @@ class Needle2Resident:
             return False
         self._check(status, "nd_needle_reset")
         self.collect_confidence = bool(collect_confidence)
+        self.kv_cache = kv_cache
         return True
 
     @property
@@ -275,15 +277,17 @@ class Needle2Resident:
         return out
 
     def kv_read(self, layer: int, head: int):
-        """(k codes, v codes, k scales, v scales) of one (layer, KV head)."""
+        """(k codes, v codes, k scales, v scales) of one (layer, KV head);
+        float32 rows instead of codes in kvCache "float32" mode."""
         kv = self.lib.nd_needle_kv(self.handle)
         invariant(kv is not None, "INVALID_CACT", "Call runtime.reset() before decoding")
         alloc = C.c_uint32()
         self._check(self.lib.nd_kv_info(kv, C.byref(alloc), None, None, None, None), "nd_kv_info")
         alloc = alloc.value
         hd = self.geometry.head_dim
-        kc = np.empty((alloc, hd), np.int8)
-        vc = np.empty((alloc, hd), np.int8)
+        dt = np.float32 if self.kv_cache == "float32" else np.int8
+        kc = np.empty((alloc, hd), dt)
+        vc = np.empty((alloc, hd), dt)
         ks = np.empty(alloc, np.float32)
         vs = np.empty(alloc, np.float32)
         self._check(self.lib.nd_kv_read(self.ctx, kv, layer, head, L.ptr(kc), L.ptr(vc),
@@ -905,10 +909,12 @@ class ResidentRuntime:
     of prompt positions) is one launch sequence on nd_needle, with the token
     history and engram hashing on the device."""
 
-    def __init__(self, resident: Needle2Resident, collect_confidence: bool = True):
+    def __init__(self, resident: Needle2Resident, collect_confidence: bool = True,
+                 kv_cache: str = "int8"):
         self.resident = resident
         self.weights = resident.weights
         self.collect_confidence = collect_confidence
+        self.kv_cache = kv_cache
         self._maximum_length = 0
 
     @property
@@ -920,7 +926,7 @@ class ResidentRuntime:
         return self._maximum_length
 
     def reset(self, maximum_length: int, sink_length: int = 0) -> None:
-        self.resident.reset(maximum_length, sink_length, "int8", self.collect_confidence)
+        self.resident.reset(maximum_length, sink_length, self.kv_cache, self.collect_confidence)
         self._maximum_length = int(maximum_length)
 
     def prefill(self, tokens: Sequence[int]) -> np.ndarray:
@@ -1016,9 +1022,9 @@ class NeedleModel:
         self.backend.weights = self.weights  # the backend serves this model's weights
         return NeedleRuntime(self.weights, self.backend, RuntimeOptions(**merged))
 
-    def create_resident_runtime(self) -> ResidentRuntime:
+    def create_resident_runtime(self, kv_cache: str = "int8") -> ResidentRuntime:
         invariant(not self._disposed, "BACKEND_UNAVAILABLE", "Needle model has been disposed")
-        return ResidentRuntime(self.resident, self.runtime_options.collect_confidence)
+        return ResidentRuntime(self.resident, self.runtime_options.collect_confidence, kv_cache)
 
     def generate(self, prompt_ids: Sequence[int], max_new_tokens: int = 96,
                  temperature: float = 0.0, top_k: int = 0, seed: int = 0x6D2B79F5,

@@ -297,8 +297,10 @@ class KvCache:
         return k, v
 
     def read(self, layer, head):
-        kc = np.zeros((self.alloc, self.head_dim), dtype=np.int8)
-        vc = np.zeros((self.alloc, self.head_dim), dtype=np.int8)
+        """(k, v, k scales, v scales): int8 codes, or float32 rows in float mode."""
+        dt = np.float32 if self.float_mode else np.int8
+        kc = np.zeros((self.alloc, self.head_dim), dtype=dt)
+        vc = np.zeros((self.alloc, self.head_dim), dtype=dt)
         ks = np.empty(self.alloc, dtype=np.float32)
         vs = np.empty(self.alloc, dtype=np.float32)
         lib().or_kv_export(self.h, layer, head, _p(kc), _p(vc), _p(ks), _p(vs))
@@ -477,6 +479,7 @@ class _N2Model(C.Structure):
 
 _SIG_N2 = {
     "or_n2_create": (P, [P, U32, U32]),
+    "or_n2_create_kv": (P, [P, U32, U32, C.c_int]),
     "or_n2_destroy": (None, [P]),
     "or_n2_kv": (P, [P]),
     "or_n2_step": (C.c_int, [P, U32, P]),
@@ -551,16 +554,18 @@ class Needle2:
         self.struct = st
         _n2_lib()
 
-    def runtime(self, max_length: int, sink: int = 0) -> "Needle2Runtime":
-        return Needle2Runtime(self, max_length, sink)
+    def runtime(self, max_length: int, sink: int = 0, kv_cache: str = "int8") -> "Needle2Runtime":
+        return Needle2Runtime(self, max_length, sink, kv_cache)
 
 
 class Needle2Runtime:
     """One sequence: reset(maximumLength, sinkLength) then step()."""
 
-    def __init__(self, model: Needle2, max_length: int, sink: int = 0):
+    def __init__(self, model: Needle2, max_length: int, sink: int = 0, kv_cache: str = "int8"):
         self.model = model
-        self.h = _n2_lib().or_n2_create(C.byref(model.struct), max_length, sink)
+        self.float_kv = kv_cache == "float32"
+        self.h = _n2_lib().or_n2_create_kv(C.byref(model.struct), max_length, sink,
+                                           1 if self.float_kv else 0)
         if not self.h:
             raise OracleError("bad runtime length")
 
@@ -593,7 +598,7 @@ class Needle2Runtime:
         cache = KvCache.__new__(KvCache)
         g = self.model.geometry
         cache.layers, cache.kv_heads, cache.head_dim = g.layers, g.kv_heads, g.head_dim
-        cache.float_mode = False
+        cache.float_mode = self.float_kv
         cache.h = _n2_lib().or_n2_kv(self.h)
         cache.alloc = int(lib().or_kv_alloc(cache.h))
         try:

@@ -115,15 +115,22 @@ static void mv(const n2_mat* m, const float* x, uint32_t row_start, uint32_t row
   or_matvec_i8(m->w, m->s, m->n, m->k, m->k, x, 1, row_start, rows, y);
 }
 
-/* runtime.ts:150-225 reset: KV allocation, engram ring depth. */
+/* runtime.ts:150-225 reset: KV allocation (int8, or float32 with
+ * float_kv: kvCache "float32", runtime.ts:192-196, 686-692), engram ring
+ * depth. */
+n2_state* or_n2_create_kv(const n2_model* md, uint32_t max_length, uint32_t sink, int float_kv);
 n2_state* or_n2_create(const n2_model* md, uint32_t max_length, uint32_t sink) {
+  return or_n2_create_kv(md, max_length, sink, 0);
+}
+
+n2_state* or_n2_create_kv(const n2_model* md, uint32_t max_length, uint32_t sink, int float_kv) {
   if (max_length == 0 || max_length > md->max_length) return NULL;
   n2_state* st = (n2_state*)calloc(1, sizeof(n2_state));
   st->md = md;
   st->max_length = max_length;
   st->sink = sink < max_length ? sink : max_length;
   st->kv = or_kv_create(md->layers, md->kv_heads, md->head_dim, max_length, st->sink,
-                        md->kv_window, 0);
+                        md->kv_window, float_kv);
   st->history = (uint32_t*)calloc(max_length, sizeof(uint32_t));
   uint32_t max_order = 1;
   for (uint32_t i = 0; i < md->n_orders; i++)

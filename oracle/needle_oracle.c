@@ -634,13 +634,17 @@ int or_kv_store(or_kv* kv, uint32_t layer, uint32_t position, const float* k, co
   return OR_OK;
 }
 
-/* Copies out the int8 codes and scales of one (layer, head) for tests. */
-void or_kv_export(const or_kv* kv, uint32_t layer, uint32_t head, int8_t* kcodes, int8_t* vcodes,
+/* Copies out the codes (int8, or the float32 rows in float mode) and scales
+ * of one (layer, head) for tests. */
+void or_kv_export(const or_kv* kv, uint32_t layer, uint32_t head, void* kcodes, void* vcodes,
                   float* kscales, float* vscales) {
   size_t base = kv_base(kv, layer, head, 0), si = kv_scale_index(kv, layer, head, 0);
   if (!kv->float_mode) {
     memcpy(kcodes, kv->k8 + base, (size_t)kv->alloc * kv->head_dim);
     memcpy(vcodes, kv->v8 + base, (size_t)kv->alloc * kv->head_dim);
+  } else {
+    memcpy(kcodes, kv->kf + base, sizeof(float) * (size_t)kv->alloc * kv->head_dim);
+    memcpy(vcodes, kv->vf + base, sizeof(float) * (size_t)kv->alloc * kv->head_dim);
   }
   memcpy(kscales, kv->ks + si, sizeof(float) * kv->alloc);
   memcpy(vscales, kv->vs + si, sizeof(float) * kv->alloc);

@@ -249,3 +249,42 @@ def test_full_geometry_session_equals_whole_steps(hip):
         rt.dispose()
     finally:
         model.dispose()
+
+
+def test_float32_kv_cache(small):
+    """kvCache "float32" (model/runtime.ts:30-40, 186-204, 686-692): the
+    cache keeps the projected K/V values themselves with scale 1, through the
+    session methods and through whole steps with a batched prompt; logits
+    within 1e-3 of the oracle's float32-cache runtime, and layer 0's rows
+    equal to the oracle's values up to fp32 rounding."""
+    w, model = small
+    say("float32 kv cache")
+    rt = model.create_runtime(kv_cache="float32")
+    rt.reset(SMALL.max_length, 3)
+    ref = oracle.Needle2(w).runtime(SMALL.max_length, 3, kv_cache="float32")
+    tokens = synth.Stream(14, "f32kv").integers(20, 0, SMALL.vocab - 1)
+    for i, t in enumerate(tokens):
+        close(rt.step(int(t)), ref.step(int(t)), ("float32 session", i))
+    k, v, ks, vs = rt.session.kv_read(0, 1)
+    rk, rv, rks, rvs = ref.kv_read(0, 1)
+    assert k.dtype == np.float32 and np.all(ks == 1.0) and np.all(vs == 1.0)
+    np.testing.assert_allclose(k, rk, rtol=1e-5, atol=1e-5 * np.abs(rk).max())
+    np.testing.assert_allclose(v, rv, rtol=1e-5, atol=1e-5 * np.abs(rv).max())
+    rt.dispose()
+    whole = model.create_resident_runtime(kv_cache="float32")
+    whole.reset(40, 0)
+    ref = oracle.Needle2(w).runtime(40, 0, kv_cache="float32")
+    prompt = synth.Stream(15, "f32kv-prompt").integers(24, 0, SMALL.vocab - 1)
+    got = whole.prefill(prompt)
+    for t in prompt:
+        want = ref.step(int(t))
+    close(got, want, "float32 batched prefill")
+    tok = int(np.argmax(got))
+    for i in range(4):
+        close(whole.step(tok), ref.step(tok), ("float32 step", i))
+        tok = (tok * 7 + 3) % SMALL.vocab
+    # back to int8 on the next reset: the graphs and kernels follow the mode
+    whole = model.create_resident_runtime()
+    whole.reset(40, 0)
+    ref = oracle.Needle2(w).runtime(40, 0)
+    close(whole.prefill(prompt), [ref.step(int(t)) for t in prompt][-1], "int8 after float32")
