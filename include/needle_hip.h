@@ -152,6 +152,15 @@ nd_status nd_matvec_batch(nd_ctx* ctx, const nd_matvec_job* jobs, uint32_t count
 nd_status nd_row(nd_ctx* ctx, const nd_mat* mat, uint32_t row, float* out);
 nd_status nd_row_d(nd_ctx* ctx, const nd_mat* mat, uint32_t row, float* out_dev, void* stream);
 
+/* Calibration, no counterpart in the reference: reads `bytes` (a nonzero
+ * multiple of 16) at the 16-byte aligned device address src with the
+ * matvec's own load form (non-temporal 128-bit loads) over `blocks`
+ * workgroups of 256 threads, and writes one folded word per workgroup to
+ * out_dev[blocks].  Gives the read-only streaming rate the weight stream of
+ * nd_matvec_d is measured against. */
+nd_status nd_stream_read_d(nd_ctx* ctx, const void* src_dev, uint64_t bytes, uint32_t blocks,
+                           uint32_t* out_dev, void* stream);
+
 /* --------------------------------------- a2/a3: int8 KV cache, attention */
 
 #define ND_KV_INT8 0
@@ -357,6 +366,13 @@ nd_status nd_prefill_set_tokens(nd_ctx* ctx, nd_prefill* prefill, const uint32_t
                                 uint32_t count, uint32_t position0);
 nd_status nd_prefill_run_d(nd_ctx* ctx, nd_prefill* prefill, nd_kv* kv, void* stream);
 nd_status nd_prefill_logits(nd_ctx* ctx, nd_prefill* prefill, float* logits);
+
+/* Runs the pass once on the context's stream with an event after every
+ * kernel and returns the summed kernel times by kind: ms[0] the int8 GEMMs
+ * (projections and lm head), ms[1] the causal attention, ms[2] the rest
+ * (embedding, digit planes, norms, RoPE and the K/V store).  Synchronises.
+ * Calibration, no counterpart in the reference. */
+nd_status nd_prefill_phase_ms(nd_ctx* ctx, nd_prefill* prefill, nd_kv* kv, float* ms);
 
 /* Copies the last layer's Q/K/V projections of the last pass -- [count]
  * [(heads + 2 kv_heads) * 64] f32, rows q | k | v before the per-head norms

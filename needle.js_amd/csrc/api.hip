@@ -349,6 +349,18 @@ nd_status nd_matvec_d(nd_ctx* ctx, const nd_mat* m, const float* x, uint32_t bat
   return ND_OK;
 }
 
+nd_status nd_stream_read_d(nd_ctx* ctx, const void* src, uint64_t bytes, uint32_t blocks,
+                           uint32_t* out, void* stream) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!src || !out || bytes == 0 || (bytes & 15) || (reinterpret_cast<uintptr_t>(src) & 15) ||
+      blocks == 0 || blocks > 65535)
+    return nd_fail(ctx, ND_ERR_INVALID,
+                   "nd_stream_read_d: 16-byte aligned source, bytes a nonzero multiple of 16, "
+                   "1..65535 blocks");
+  ND_HIP(ctx, nd_launch_stream_read(src, bytes, blocks, out, nd_pick_stream(ctx, stream)));
+  return ND_OK;
+}
+
 nd_status nd_matvec(nd_ctx* ctx, const nd_mat* m, const float* x, uint32_t batch,
                     uint32_t row_start, uint32_t row_count, float* y) {
   if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");

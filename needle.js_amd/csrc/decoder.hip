@@ -678,6 +678,80 @@ nd_status nd_prefill_set_tokens(nd_ctx* ctx, nd_prefill* p, const uint32_t* toke
   return ND_OK;
 }
 
+// Phase marks of a timed prefill: an event recorded after each kernel,
+// with the kind of work that kernel did (GEMM, attention, other).
+struct PrefillMarks {
+  enum Kind { kGemm = 0, kAttention = 1, kOther = 2 };
+  std::vector<hipEvent_t> events;
+  std::vector<int> kinds;
+  hipError_t mark(int kind, hipStream_t s) {
+    hipEvent_t e;
+    hipError_t err = hipEventCreate(&e);
+    if (err != hipSuccess) return err;
+    events.push_back(e);
+    kinds.push_back(kind);
+    return hipEventRecord(e, s);
+  }
+  ~PrefillMarks() {
+    for (hipEvent_t e : events) hipEventDestroy(e);
+  }
+};
+
+static nd_status enqueue_prefill(nd_ctx* ctx, nd_prefill* p, nd_kv* kv, hipStream_t s,
+                                 PrefillMarks* marks) {
+  const nd_decoder* dec = p->dec;
+  const uint32_t M = p->count, D = dec->dim, F = dec->ffn;
+  const uint32_t qkv_rows = (dec->heads + 2 * dec->kv_heads) * kHd;
+  const uint32_t rep = dec->heads / dec->kv_heads;
+  const uint32_t last = p->position0 + M - 1;
+  auto mark = [&](int kind) -> hipError_t {
+    return marks ? marks->mark(kind, s) : hipSuccess;
+  };
+  constexpr int G = PrefillMarks::kGemm, A = PrefillMarks::kAttention, O = PrefillMarks::kOther;
+  ND_HIP(ctx, mark(O));
+  hipLaunchKernelGGL(embed_kernel, dim3((D + 255) / 256, M), dim3(256), 0, s, dec->embedding->w,
+                     dec->embedding->scales, p->tokens, dec->vocab, D, std::sqrt((double)D), p->x);
+  ND_HIP(ctx, hipGetLastError());
+  ND_HIP(ctx, mark(O));
+  for (uint32_t l = 0; l < dec->layers; ++l) {
+    ND_HIP(ctx, nd_launch_digitize(p->x, D, dec->norms + dec->attn_off + (size_t)l * D, nullptr,
+                                   p->digits, p->fm, M, D, s));
+    ND_HIP(ctx, mark(O));
+    ND_HIP(ctx, nd_launch_gemm(&dec->wqkv[l], p->digits, p->fm, p->qkv, qkv_rows, M, 0, s));
+    ND_HIP(ctx, mark(G));
+    hipLaunchKernelGGL(qk_rope_store_kernel, dim3(dec->heads + dec->kv_heads, M), dim3(64), 0, s,
+                       p->qkv, qkv_rows, dec->heads, dec->kv_heads,
+                       dec->norms + dec->q_off + (size_t)l * kHd,
+                       dec->norms + dec->k_off + (size_t)l * kHd, dec->inv_freq, nullptr,
+                       p->position0, p->q, (int8_t*)kv->k, (int8_t*)kv->v, kv->ks, kv->vs, l,
+                       kv->kv_heads, kv->alloc, 0u);
+    ND_HIP(ctx, hipGetLastError());
+    ND_HIP(ctx, mark(O));
+    ND_HIP(ctx, nd_launch_attention_batch(kv, l, p->positions, M, dec->kv_heads, 0u, rep, last,
+                                          p->q, p->o, p->partials, p->counters, s));
+    ND_HIP(ctx, mark(A));
+    ND_HIP(ctx, nd_launch_digitize(p->o, D, nullptr, nullptr, p->digits, p->fm, M, D, s));
+    ND_HIP(ctx, mark(O));
+    ND_HIP(ctx, nd_launch_gemm(dec->wo[l], p->digits, p->fm, p->x, D, M, 1, s));
+    ND_HIP(ctx, mark(G));
+    ND_HIP(ctx, nd_launch_digitize(p->x, D, dec->norms + dec->ffn_off + (size_t)l * D, nullptr,
+                                   p->digits, p->fm, M, D, s));
+    ND_HIP(ctx, mark(O));
+    ND_HIP(ctx, nd_launch_gemm(dec->wup[l], p->digits, p->fm, p->h, F, M, 2, s));
+    ND_HIP(ctx, mark(G));
+    ND_HIP(ctx, nd_launch_digitize(p->h, F, nullptr, nullptr, p->digits, p->fm, M, F, s));
+    ND_HIP(ctx, mark(O));
+    ND_HIP(ctx, nd_launch_gemm(dec->wdown[l], p->digits, p->fm, p->x, D, M, 1, s));
+    ND_HIP(ctx, mark(G));
+  }
+  ND_HIP(ctx, nd_launch_digitize(p->x + (size_t)(M - 1) * D, D, dec->norms + dec->final_off,
+                                 nullptr, p->digits, p->fm, 1, D, s));
+  ND_HIP(ctx, mark(O));
+  ND_HIP(ctx, nd_launch_gemm(dec->embedding, p->digits, p->fm, p->logits, dec->vocab, 1, 0, s));
+  ND_HIP(ctx, mark(G));
+  return ND_OK;
+}
+
 // Enqueues the prefill of the tokens set by nd_prefill_set_tokens: every
 // layer runs as M-row GEMMs on int8 MFMA; all M positions' K/V are quantized
 // into the cache first, then each position attends causally over [0, its
@@ -688,39 +762,24 @@ nd_status nd_prefill_run_d(nd_ctx* ctx, nd_prefill* p, nd_kv* kv, void* stream) 
   if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
   nd_status st = check_prefill(ctx, p, kv, p ? p->count : 0, p ? p->position0 : 0);
   if (st != ND_OK) return st;
-  hipStream_t s = nd_pick_stream(ctx, stream);
-  const nd_decoder* dec = p->dec;
-  const uint32_t M = p->count, D = dec->dim, F = dec->ffn;
-  const uint32_t qkv_rows = (dec->heads + 2 * dec->kv_heads) * kHd;
-  const uint32_t rep = dec->heads / dec->kv_heads;
-  const uint32_t last = p->position0 + M - 1;
-  hipLaunchKernelGGL(embed_kernel, dim3((D + 255) / 256, M), dim3(256), 0, s, dec->embedding->w,
-                     dec->embedding->scales, p->tokens, dec->vocab, D, std::sqrt((double)D), p->x);
-  ND_HIP(ctx, hipGetLastError());
-  for (uint32_t l = 0; l < dec->layers; ++l) {
-    ND_HIP(ctx, nd_launch_digitize(p->x, D, dec->norms + dec->attn_off + (size_t)l * D, nullptr,
-                                   p->digits, p->fm, M, D, s));
-    ND_HIP(ctx, nd_launch_gemm(&dec->wqkv[l], p->digits, p->fm, p->qkv, qkv_rows, M, 0, s));
-    hipLaunchKernelGGL(qk_rope_store_kernel, dim3(dec->heads + dec->kv_heads, M), dim3(64), 0, s,
-                       p->qkv, qkv_rows, dec->heads, dec->kv_heads,
-                       dec->norms + dec->q_off + (size_t)l * kHd,
-                       dec->norms + dec->k_off + (size_t)l * kHd, dec->inv_freq, nullptr,
-                       p->position0, p->q, (int8_t*)kv->k, (int8_t*)kv->v, kv->ks, kv->vs, l,
-                       kv->kv_heads, kv->alloc, 0u);
-    ND_HIP(ctx, hipGetLastError());
-    ND_HIP(ctx, nd_launch_attention_batch(kv, l, p->positions, M, dec->kv_heads, 0u, rep, last,
-                                          p->q, p->o, p->partials, p->counters, s));
-    ND_HIP(ctx, nd_launch_digitize(p->o, D, nullptr, nullptr, p->digits, p->fm, M, D, s));
-    ND_HIP(ctx, nd_launch_gemm(dec->wo[l], p->digits, p->fm, p->x, D, M, 1, s));
-    ND_HIP(ctx, nd_launch_digitize(p->x, D, dec->norms + dec->ffn_off + (size_t)l * D, nullptr,
-                                   p->digits, p->fm, M, D, s));
-    ND_HIP(ctx, nd_launch_gemm(dec->wup[l], p->digits, p->fm, p->h, F, M, 2, s));
-    ND_HIP(ctx, nd_launch_digitize(p->h, F, nullptr, nullptr, p->digits, p->fm, M, F, s));
-    ND_HIP(ctx, nd_launch_gemm(dec->wdown[l], p->digits, p->fm, p->x, D, M, 1, s));
+  return enqueue_prefill(ctx, p, kv, nd_pick_stream(ctx, stream), nullptr);
+}
+
+nd_status nd_prefill_phase_ms(nd_ctx* ctx, nd_prefill* p, nd_kv* kv, float* ms) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!ms) return nd_fail(ctx, ND_ERR_INVALID, "ms is NULL");
+  nd_status st = check_prefill(ctx, p, kv, p ? p->count : 0, p ? p->position0 : 0);
+  if (st != ND_OK) return st;
+  PrefillMarks marks;
+  st = enqueue_prefill(ctx, p, kv, ctx->stream, &marks);
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  if (st != ND_OK) return st;
+  ms[0] = ms[1] = ms[2] = 0.f;
+  for (size_t i = 1; i < marks.events.size(); ++i) {
+    float t = 0.f;
+    ND_HIP(ctx, hipEventElapsedTime(&t, marks.events[i - 1], marks.events[i]));
+    ms[marks.kinds[i]] += t;
   }
-  ND_HIP(ctx, nd_launch_digitize(p->x + (size_t)(M - 1) * D, D, dec->norms + dec->final_off,
-                                 nullptr, p->digits, p->fm, 1, D, s));
-  ND_HIP(ctx, nd_launch_gemm(dec->embedding, p->digits, p->fm, p->logits, dec->vocab, 1, 0, s));
   return ND_OK;
 }
 

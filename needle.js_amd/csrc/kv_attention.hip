@@ -598,9 +598,298 @@ struct AttnLaunch {
   bool qblock;                 // query blocks of a prefill whose positions see [0, position]
 };
 
+// Causal prefill attention on MFMA (a prefill whose positions all see [0,
+// position] in their own slots; int8 cache).  Workgroup = (block of 64 query
+// rows, query head h, KV head h / rep), 8 waves in two groups: wave w takes
+// rows [z0 + 16 (w % 4), +16), lane l the row 16 (w % 4) + l % 16, and group
+// g = w / 4 the key blocks g, g + 2, ... (64 keys each), so both groups walk
+// half of the row block's keys; their online-softmax states merge through
+// LDS at the end.  Each group streams its key blocks through its own pair of
+// LDS buffers (K codes as stored, V transposed to [dim][key]), one barrier
+// per step.  Per block and wave:
+//   S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = K codes (row = key, exact in
+//   fp16), B = Q^T split into fp16 halves hi + lo of q * 2^-e (e: the row's
+//   largest magnitude, < 2^e), which hold q to 2^-24 of the row maximum; the
+//   product lands as lane l holding keys 4 (l / 16) + c of each 16-key tile
+//   for its own row;
+//   scores = (S * k_scale / 8) * 2^e, causal mask, online softmax in fp32
+//   (__expf), as NeedleRuntime.#attention (model/runtime.ts:719-786,
+//   softmaxInPlace model/math.ts:46-60) evaluates them;
+//   O^T += V^T P'^T: B = P'^T with p' = p * v_scale * 2^f (fp16 halves; f
+//   puts the largest v_scale of the visible keys below 2^15 so that both
+//   halves stay normal down to 2^-18 of it), which is exactly the layout the
+//   S^T product left in the lane (8 keys per lane, the A operand reads V^T at
+//   the same keys); A = V^T codes (row = dim).
+// The output row is O / (l 2^f), gated when `gate` is set (runtime.ts:503-507).
+constexpr uint32_t kPfRows = 64, kPfKeys = 64, kPfThreads = 512;
+constexpr uint32_t kKStride = 80;   // LDS bytes per key row of K (16-byte aligned rows)
+constexpr uint32_t kVtStride = 68;  // LDS bytes per dim row of V^T
+struct PfBuf {
+  int8_t k[kPfKeys * kKStride];
+  int8_t vt[kHeadDim * kVtStride];
+  float ks[kPfKeys];  // k_scale / 8
+  float vs[kPfKeys];  // v_scale * 2^f
+};
+
+__global__ __launch_bounds__(kPfThreads) void prefill_attention_mfma_kernel(
+    const int8_t* __restrict__ Kc, const int8_t* __restrict__ Vc, const float* __restrict__ Ks,
+    const float* __restrict__ Vs, const float* __restrict__ Q, float* __restrict__ out,
+    const float* __restrict__ gate, uint32_t gate_ld, uint32_t layer, uint32_t kv_heads,
+    uint32_t alloc, const uint32_t* __restrict__ positions, uint32_t qrows, uint32_t q_heads,
+    uint32_t rep, float score_scale) {
+  using nd::half8;
+  using nd::float4v;
+  using nd::u32x2;
+  __shared__ __align__(16) PfBuf s_buf[2][2];  // [group][buffer]
+  __shared__ uint32_t s_top[8];
+  __shared__ float s_vmax[8];
+  const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const uint32_t grp = wave >> 2, wq = wave & 3, tg = t & 255;
+  const uint32_t r16 = lane & 15, kb = lane >> 4;
+  const uint32_t h = blockIdx.y, kvh = h / rep;
+  const uint32_t z0 = blockIdx.x * kPfRows;
+  const size_t head_base = ((size_t)layer * kv_heads + kvh) * alloc;
+
+  // Keys [0, top): top = 1 + the largest position of the block's rows.
+  uint32_t my_top = 0;
+  if (t < kPfRows && z0 + t < qrows) my_top = positions[z0 + t] + 1;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) my_top = max(my_top, (uint32_t)__shfl_xor((int)my_top, o, 64));
+  if (lane == 0) s_top[wave] = my_top;
+  // This lane's query row and its q values: dims 32 s + 8 kb + [0, 8).
+  const uint32_t zq = z0 + 16 * wq + r16;
+  const bool q_ok = zq < qrows;
+  const uint32_t pos = q_ok ? positions[zq] : 0;
+  const float* qp = Q + ((size_t)(q_ok ? zq : 0) * q_heads + h) * kHeadDim + 8 * kb;
+  float qv[2][8];
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) {
+    const float4 a = *reinterpret_cast<const float4*>(qp + 32 * s2);
+    const float4 b = *reinterpret_cast<const float4*>(qp + 32 * s2 + 4);
+    qv[s2][0] = a.x; qv[s2][1] = a.y; qv[s2][2] = a.z; qv[s2][3] = a.w;
+    qv[s2][4] = b.x; qv[s2][5] = b.y; qv[s2][6] = b.z; qv[s2][7] = b.w;
+  }
+  // The smallest position of the wave's rows: blocks wholly below it need no mask.
+  uint32_t wmin = q_ok ? pos : 0;
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) wmin = min(wmin, (uint32_t)__shfl_xor((int)wmin, o, 64));
+  wmin = __builtin_amdgcn_readfirstlane(wmin);
+  __syncthreads();
+  const uint32_t top = max(max(max(s_top[0], s_top[1]), max(s_top[2], s_top[3])),
+                           max(max(s_top[4], s_top[5]), max(s_top[6], s_top[7])));
+  if (top > alloc || top == 0) return;  // validated on entry; stay in bounds
+  const uint32_t nblocks = (top + kPfKeys - 1) / kPfKeys;
+
+  // The split of q: the row maximum over the four lanes holding the row.
+  float qmax = 0.f;
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qmax = fmaxf(qmax, fabsf(qv[s2][e]));
+  qmax = fmaxf(qmax, nd::lane_xor<16>(qmax));
+  qmax = fmaxf(qmax, nd::lane_xor<32>(qmax));
+  int qe = 0;
+  if (qmax > 0.f && qmax <= 3.4028235e38f) frexpf(qmax, &qe);  // qmax < 2^qe
+  const float qdown = ldexpf(1.f, -qe), qup = ldexpf(1.f, qe);
+  half8 qh[2], ql[2];
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = qv[s2][e] * qdown;
+      const _Float16 hv = (_Float16)v;
+      qh[s2][e] = hv;
+      ql[s2][e] = (_Float16)(v - (float)hv);
+    }
+
+  // The largest v_scale of the visible keys sets the p' scale 2^f.
+  float vmax = 0.f;
+  for (uint32_t k = t; k < top; k += kPfThreads) vmax = fmaxf(vmax, Vs[head_base + k]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, o, 64));
+  if (lane == 0) s_vmax[wave] = vmax;
+  __syncthreads();
+  float vsmax = 0.f;
+#pragma unroll
+  for (int w = 0; w < 8; ++w) vsmax = fmaxf(vsmax, s_vmax[w]);
+  int fe = 0;
+  if (vsmax > 0.f && vsmax <= 3.4028235e38f) frexpf(vsmax, &fe);  // vsmax < 2^fe
+  const float pup = ldexpf(1.f, 15 - fe), pdown = ldexpf(1.f, fe - 15);
+  const float ks_mul = score_scale;
+
+  // Block loads of the group: thread tg takes key tg / 4, bytes [16 (tg %
+  // 4), +16) of its K and V rows (keys past top read the last visible slot;
+  // they are masked).
+  const uint32_t lkey = tg >> 2, lpart = tg & 3;
+  uint4 kreg, vreg;
+  float ksr = 0.f, vsr = 0.f;
+  auto load_block = [&](uint32_t b) {
+    const uint32_t key = min(b * kPfKeys + lkey, top - 1);
+    const size_t row = head_base + key;
+    kreg = *reinterpret_cast<const uint4*>(Kc + row * kHeadDim + 16 * lpart);
+    vreg = *reinterpret_cast<const uint4*>(Vc + row * kHeadDim + 16 * lpart);
+    if (tg < kPfKeys) {
+      const size_t srow = head_base + min(b * kPfKeys + tg, top - 1);
+      ksr = Ks[srow];
+      vsr = Vs[srow];
+    }
+  };
+  auto store_block = [&](PfBuf& B) {
+    *reinterpret_cast<uint4*>(&B.k[lkey * kKStride + 16 * lpart]) = kreg;
+    const uint32_t words[4] = {vreg.x, vreg.y, vreg.z, vreg.w};
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      B.vt[(16 * lpart + e) * kVtStride + lkey] = (int8_t)(words[e >> 2] >> (8 * (e & 3)));
+    if (tg < kPfKeys) {
+      B.ks[tg] = ksr * ks_mul;
+      B.vs[tg] = vsr * pup;
+    }
+  };
+  const uint32_t steps = (nblocks + 1) / 2;  // both groups step together
+  if (grp < nblocks) {
+    load_block(grp);
+    store_block(s_buf[grp][0]);
+  }
+  nd::lds_barrier();
+
+  float m = -INFINITY, l = 0.f;
+  float4v o[4] = {};
+  for (uint32_t i = 0; i < steps; ++i) {
+    const uint32_t b = 2 * i + grp;
+    const bool has = b < nblocks, has_next = b + 2 < nblocks;
+    PfBuf& B = s_buf[grp][i & 1];
+    if (has_next) load_block(b + 2);
+    if (has) {
+      const uint32_t k0 = b * kPfKeys;
+      // S^T tiles j: keys k0 + 16 j + 4 kb + c of this lane's row.
+      float4v sc[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        sc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const u32x2 kw =
+              *reinterpret_cast<const u32x2*>(&B.k[(16 * j + r16) * kKStride + 32 * s2 + 8 * kb]);
+          const half8 ka = nd::codes_to_half(kw);
+          sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[s2], sc[j], 0, 0, 0);
+          sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[s2], sc[j], 0, 0, 0);
+        }
+      }
+      const bool masked = k0 + kPfKeys - 1 > wmin;  // uniform over the wave
+      float bmax = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 ks4 = *reinterpret_cast<const float4*>(&B.ks[16 * j + 4 * kb]);
+        const float ksv[4] = {ks4.x, ks4.y, ks4.z, ks4.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          float v = (sc[j][c] * ksv[c]) * qup;
+          if (masked) v = (q_ok && k0 + 16 * j + 4 * kb + c <= pos) ? v : -INFINITY;
+          sc[j][c] = v;
+          bmax = fmaxf(bmax, v);
+        }
+      }
+      bmax = fmaxf(bmax, nd::lane_xor<16>(bmax));
+      bmax = fmaxf(bmax, nd::lane_xor<32>(bmax));
+      const float m_new = fmaxf(m, bmax);
+      // 1 while no key has been visible (-inf - -inf), 0 on the first visible one.
+      const float alpha = m_new == -INFINITY ? 1.f : __expf(m - m_new);
+      m = m_new;
+      l *= alpha;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) o[d] *= alpha;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float e = sc[j][c] == -INFINITY ? 0.f : __expf(sc[j][c] - m_new);
+          sc[j][c] = e;
+          l += e;
+        }
+      // O^T += V^T P'^T over the two 32-key steps.
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const float4 va = *reinterpret_cast<const float4*>(&B.vs[32 * s2 + 4 * kb]);
+        const float4 vb = *reinterpret_cast<const float4*>(&B.vs[32 * s2 + 16 + 4 * kb]);
+        const float pv[8] = {sc[2 * s2][0] * va.x,     sc[2 * s2][1] * va.y,
+                             sc[2 * s2][2] * va.z,     sc[2 * s2][3] * va.w,
+                             sc[2 * s2 + 1][0] * vb.x, sc[2 * s2 + 1][1] * vb.y,
+                             sc[2 * s2 + 1][2] * vb.z, sc[2 * s2 + 1][3] * vb.w};
+        half8 ph, pl;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const _Float16 hv = (_Float16)pv[e];
+          ph[e] = hv;
+          pl[e] = (_Float16)(pv[e] - (float)hv);
+        }
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const int8_t* vt = &B.vt[(16 * d + r16) * kVtStride + 32 * s2 + 4 * kb];
+          const u32x2 vw = {*reinterpret_cast<const uint32_t*>(vt),
+                            *reinterpret_cast<const uint32_t*>(vt + 16)};
+          const half8 va8 = nd::codes_to_half(vw);
+          o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va8, ph, o[d], 0, 0, 0);
+          o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va8, pl, o[d], 0, 0, 0);
+        }
+      }
+    }
+    if (has_next) store_block(s_buf[grp][(i + 1) & 1]);
+    nd::lds_barrier();
+  }
+  // l over the row's four lanes; o[d][c] is dim 16 d + 4 kb + c of the row.
+  l += nd::lane_xor<16>(l);
+  l += nd::lane_xor<32>(l);
+  // Merge: group 1 leaves (m, l, o) in LDS (the key buffers are free), group
+  // 0 combines them with its own and stores the row.
+  float* xm = reinterpret_cast<float*>(&s_buf[0][0]);  // [wq][18][64]
+  if (grp == 1) {
+    float* dst = xm + wq * 18 * 64 + lane;
+    dst[0] = m;
+    dst[64] = l;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) dst[(2 + 4 * d + c) * 64] = o[d][c];
+  }
+  nd::lds_barrier();
+  if (grp == 1 || !q_ok) return;
+  {
+    const float* src = xm + wq * 18 * 64 + lane;
+    const float m1 = src[0], l1 = src[64];
+    const float mt = fmaxf(m, m1);
+    const float a0 = m == -INFINITY ? 0.f : __expf(m - mt);
+    const float a1 = m1 == -INFINITY ? 0.f : __expf(m1 - mt);
+    l = l * a0 + l1 * a1;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[d][c] = o[d][c] * a0 + src[(2 + 4 * d + c) * 64] * a1;
+  }
+  const size_t obase = ((size_t)zq * q_heads + h) * kHeadDim;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    float r[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      r[c] = (o[d][c] * pdown) / l;
+      if (gate) r[c] *= gate_factor(gate[(size_t)zq * gate_ld + h * kHeadDim + 16 * d + 4 * kb + c]);
+    }
+    *reinterpret_cast<float4*>(out + obase + 16 * d + 4 * kb) = make_float4(r[0], r[1], r[2], r[3]);
+  }
+}
+
 template <int REP, bool F32>
 hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
   if constexpr ((REP == 1 || REP == 2) && !F32) {
+    if (a.qblock) {
+      hipLaunchKernelGGL(prefill_attention_mfma_kernel,
+                         dim3((a.batch + kPfRows - 1) / kPfRows, a.seq_kv_heads * REP),
+                         dim3(kPfThreads), 0, s, reinterpret_cast<const int8_t*>(a.kv->k),
+                         reinterpret_cast<const int8_t*>(a.kv->v), a.kv->ks, a.kv->vs, a.q, a.out,
+                         a.gate, a.gate_ld, a.layer, a.kv->kv_heads, a.kv->alloc, a.positions,
+                         a.batch, a.seq_kv_heads * REP, (uint32_t)REP, 0.125f);
+      return hipGetLastError();
+    }
     // Query blocks: 4 rows per workgroup (4 positions x 1 head, or 2 x 2).
     if (a.qblock) {
       constexpr int kQb = 4;

@@ -169,10 +169,10 @@ __global__ __launch_bounds__(kThreads) void matvec_i8_kernel(
 // xs[group][lane] = 8 halves.  Weight loads are issued together and
 // unconditionally (addresses clamped, contributions weighted by zero), so
 // each MFMA waits only for its operands.
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
-typedef float float4v __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+using nd::half8;
+using nd::float4v;
+using nd::u32x2;
+using nd::codes_to_half;
 constexpr uint32_t kSplitRows = 8;
 // Batch 2 streams faster on the vector kernel (7.5 vs 11 us at 4096 x 4096);
 // from 3 rows on (two vector launches) the MFMA path wins.
@@ -180,19 +180,6 @@ constexpr uint32_t kMfmaMinBatch = 3;
 
 // Lane block holding k block j of a group (kOrder is its own inverse).
 __device__ __forceinline__ uint32_t k_block_lanes(uint32_t j) { return j == 1 ? 2 : j == 2 ? 1 : j; }
-
-// Eight int8 codes -> eight exact fp16 values: 0x6500 | (c ^ 0x80) is the
-// fp16 number 1408 + c, and one packed subtraction per pair removes 1408.
-__device__ __forceinline__ half8 codes_to_half(u32x2 w) {
-  const uint32_t u0 = w.x ^ 0x80808080u, u1 = w.y ^ 0x80808080u;
-  const uint32_t k = 0x65656565u;
-  const half2v off = {(_Float16)-1408.f, (_Float16)-1408.f};
-  const half2v p0 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(k, u0, 0x04010400u)) + off;
-  const half2v p1 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(k, u0, 0x04030402u)) + off;
-  const half2v p2 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(k, u1, 0x04010400u)) + off;
-  const half2v p3 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(k, u1, 0x04030402u)) + off;
-  return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-}
 
 constexpr uint32_t kMfmaWaves = 16;
 
@@ -548,6 +535,32 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_slice_kernel(
   if (t == 0) __hip_atomic_store(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Read-only stream over `units` 16-byte units: the matvec's own load form
+// (non-temporal 128-bit loads, four in flight per thread), folded by xor into
+// one word per workgroup so the loads cannot be dropped.
+__global__ __launch_bounds__(kThreads) void stream_read_kernel(const u32x4* __restrict__ src,
+                                                               uint64_t units,
+                                                               uint32_t* __restrict__ out) {
+  const uint64_t stride = (uint64_t)gridDim.x * kThreads;
+  uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  u32x4 f = {0u, 0u, 0u, 0u};
+  for (; i + 3 * stride < units; i += 4 * stride) {
+    const u32x4 a = __builtin_nontemporal_load(src + i);
+    const u32x4 b = __builtin_nontemporal_load(src + i + stride);
+    const u32x4 c = __builtin_nontemporal_load(src + i + 2 * stride);
+    const u32x4 d = __builtin_nontemporal_load(src + i + 3 * stride);
+    f ^= a ^ b ^ c ^ d;
+  }
+  for (; i < units; i += stride) f ^= __builtin_nontemporal_load(src + i);
+  uint32_t w = f.x ^ f.y ^ f.z ^ f.w;
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) w ^= (uint32_t)__shfl_xor((int)w, m, 64);
+  __shared__ uint32_t s_w[kThreads / 64];
+  if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = w;
+  __syncthreads();
+  if (threadIdx.x == 0) out[blockIdx.x] = s_w[0] ^ s_w[1] ^ s_w[2] ^ s_w[3];
+}
+
 __global__ void row_kernel(const int8_t* __restrict__ W, const float* __restrict__ S,
                            uint32_t K, uint32_t groups, uint32_t G, uint32_t row,
                            float* __restrict__ out) {
@@ -664,6 +677,13 @@ hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uin
     b0 += bc;
   }
   return hipSuccess;
+}
+
+hipError_t nd_launch_stream_read(const void* src, uint64_t bytes, uint32_t blocks, uint32_t* out,
+                                 hipStream_t s) {
+  hipLaunchKernelGGL(stream_read_kernel, dim3(blocks), dim3(kThreads), 0, s,
+                     reinterpret_cast<const u32x4*>(src), bytes / 16, out);
+  return hipGetLastError();
 }
 
 hipError_t nd_launch_row(const nd_mat* m, uint32_t row, float* out, hipStream_t s) {

@@ -109,6 +109,10 @@ hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uin
                             uint32_t row_start, uint32_t row_count, float* y, uint32_t y_stride,
                             hipStream_t s, void* split = nullptr);
 hipError_t nd_launch_row(const nd_mat* m, uint32_t row, float* out, hipStream_t s);
+// Read-only stream of `bytes` (a multiple of 16) at 16-byte aligned `src`:
+// `blocks` workgroups of 256 threads, one folded word each into out[blocks].
+hipError_t nd_launch_stream_read(const void* src, uint64_t bytes, uint32_t blocks, uint32_t* out,
+                                 hipStream_t s);
 // Cactus-Quant matrices (csrc/cq.hip): prepareCqActivation of batch rows of
 // x into prepared [batch][kpad]; the matvec of batch rows of x (its own
 // input rotation; `prepared` is the context's kCqPreparedRows x kCqMaxKpad

@@ -64,6 +64,25 @@ __device__ __forceinline__ float row_max(float v) {
   return v;
 }
 
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Eight int8 codes (bytes 0..7 of w, in order) -> eight exact fp16 values:
+// 0x6500 | (c ^ 0x80) is the fp16 number 1408 + c, and one packed
+// subtraction per pair removes 1408.
+__device__ __forceinline__ half8 codes_to_half(u32x2 w) {
+  const uint32_t u0 = w.x ^ 0x80808080u, u1 = w.y ^ 0x80808080u;
+  const uint32_t k = 0x65656565u;
+  const half2v off = {(_Float16)-1408.f, (_Float16)-1408.f};
+  const half2v p0 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(k, u0, 0x04010400u)) + off;
+  const half2v p1 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(k, u0, 0x04030402u)) + off;
+  const half2v p2 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(k, u1, 0x04010400u)) + off;
+  const half2v p3 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(k, u1, 0x04030402u)) + off;
+  return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
 // JavaScript Math.max of two numbers (NaN if either is NaN).
 __device__ __forceinline__ float js_max(float a, float b) {
   return (a != a || b != b) ? __builtin_nanf("") : (a > b ? a : b);

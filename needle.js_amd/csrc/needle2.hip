@@ -31,16 +31,19 @@ namespace {
 constexpr uint32_t kHd = 64;
 constexpr int kWg = 1024;
 constexpr int kMixWg = 512;  // mix kernel: dim <= 512 values per thread role
-// phi rows per wave (24 rows / 8 waves) and 16-byte chunks per lane and row
-// (2048 bytes / 16 / 64 lanes) of the mix kernel.
-constexpr int kMixRows = 3, kMixCols = 2;
 constexpr uint32_t kPrefillRows = 512;  // positions per batched prefill pass
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+using nd::half8;
+using nd::float4v;
+using nd::u32x2;
 
+// or_sigmoid / sigmoid (math.ts): 1 / (1 + e^-v) for v >= 0, e^v / (1 + e^v)
+// below, with one exp either way (e = e^-|v|), so lanes of either sign share
+// one instruction stream.
 __device__ __forceinline__ double sigmoid_d(double v) {
-  if (v >= 0) return 1.0 / (1.0 + exp(-v));
-  const double e = exp(v);
-  return e / (1.0 + e);
+  const double e = exp(-fabs(v));
+  return (v >= 0 ? 1.0 : e) / (1.0 + e);
 }
 
 // Sum over a workgroup of NT threads; every thread gets the total.
@@ -337,7 +340,8 @@ struct MixArgs {
   const float* d1;
   const float* d2;
   const float* d3;
-  float attention_gate;
+  double attention_scale;  // sigmoid(attentionGate[l - 1]), float64
+  double inv_root_h;       // 1 / sqrt(hdim), float64
   const float* route;  // [lanes * lanes] Sinkhorn routing, then [lanes] h-post
   // pre-attention half of layer l (runtime.ts:385-441)
   uint32_t has_pre, own_pre;
@@ -348,6 +352,9 @@ struct MixArgs {
   uint32_t has_site;  // an engram site injects at layer l
   const float* ekey;  // engram key / mixed value of that site
   const float* evalue;
+  double sqrt_d;      // sqrt(d), float64
+  float split_scale;  // 2^s with sqrt(lanes * d) * 2^s <= 2^15 (the phi operand split)
+  float split_unscale;
   const float* norm_input;
   // lane mean + final norm after the last layer (runtime.ts:570-576)
   uint32_t has_final;
@@ -375,13 +382,34 @@ struct MixArgs {
   uint32_t cell_ld, final_row;
 };
 
-// Sum over the kMixWg threads with one barrier: the partial sums alternate
-// between two LDS rows, so a row is rewritten only after the next call's
-// barrier, which every reader of the previous call has passed.
-__device__ __forceinline__ double mix_sum(double v, double (*red)[kMixWg / 64], int& phase) {
+// sigmoid in float64 as the kernels evaluate it (host side: the constants
+// a mix launch takes precomputed).
+inline double host_sigmoid(double v) {
+  if (v >= 0) return 1.0 / (1.0 + std::exp(-v));
+  const double e = std::exp(v);
+  return e / (1.0 + e);
+}
+
+// The mix launch constants derived from the geometry and the layer's gate.
+inline void mix_constants(MixArgs& m, uint32_t d, uint32_t hdim, uint32_t lanes, float gate) {
+  m.attention_scale = host_sigmoid((double)gate);
+  m.inv_root_h = 1.0 / std::sqrt((double)hdim);
+  m.sqrt_d = std::sqrt((double)d);
+  int s = 0;
+  while (std::sqrt((double)lanes * d) * std::ldexp(1.0, s + 1) <= 32768.0) ++s;
+  m.split_scale = std::ldexp(1.f, s);
+  m.split_unscale = std::ldexp(1.f, -s);
+}
+
+// Sums over the kMixWg threads with one LDS barrier each: the partial sums
+// alternate between two LDS rows, so a row is rewritten only after the next
+// call's barrier, which every reader of the previous call has passed (the
+// barrier waits for the wave's own LDS reads first).  mix_sum2 reduces two
+// values in the same round.
+__device__ __forceinline__ double mix_sum(double v, double (*red)[2 * (kMixWg / 64)], int& phase) {
   v = nd::wave_sum(v);
   if ((threadIdx.x & 63) == 0) red[phase][threadIdx.x >> 6] = v;
-  __syncthreads();
+  nd::lds_barrier();
   double r = 0.0;
 #pragma unroll
   for (int i = 0; i < kMixWg / 64; ++i) r += red[phase][i];
@@ -389,32 +417,54 @@ __device__ __forceinline__ double mix_sum(double v, double (*red)[kMixWg / 64], 
   return r;
 }
 
-// One FWHT butterfly stage across threads: thread t holds value t and
-// combines it with value t ^ s (fwht, f32 store of the float64 sum).
-__device__ __forceinline__ float butterfly(float mine, float other, uint32_t t, uint32_t s) {
-  const double m = mine, o = other;
-  return (t & s) ? (float)(o - m) : (float)(m + o);
+__device__ __forceinline__ void mix_sum2(double& v, double& w,
+                                         double (*red)[2 * (kMixWg / 64)], int& phase) {
+  v = nd::wave_sum(v);
+  w = nd::wave_sum(w);
+  if ((threadIdx.x & 63) == 0) {
+    red[phase][threadIdx.x >> 6] = v;
+    red[phase][kMixWg / 64 + (threadIdx.x >> 6)] = w;
+  }
+  nd::lds_barrier();
+  double r = 0.0, q = 0.0;
+#pragma unroll
+  for (int i = 0; i < kMixWg / 64; ++i) {
+    r += red[phase][i];
+    q += red[phase][kMixWg / 64 + i];
+  }
+  v = r;
+  w = q;
+  phase ^= 1;
+}
+
+// One FWHT butterfly (fwht, math.ts): the lower element takes mine + other,
+// the upper other - mine, each evaluated in float64 and stored as f32.  The
+// float64 sum or difference of two f32 values rounded to f32 is the f32 sum
+// or difference itself (53 >= 2 * 24 + 2 bits: the double rounding is
+// innocuous), so the butterflies run in f32 with the same results.
+__device__ __forceinline__ float butterfly(float mine, float other, bool upper) {
+  return upper ? other - mine : mine + other;
 }
 
 // Walsh-Hadamard transform of hv[0, H) (H <= kMixWg a power of two), one
-// value per thread, strides ascending: DPP within quads, lane shuffles
-// within the wave for strides 1..32.  The strides 64, 128, 256 mix values
-// of different waves: after one exchange through LDS, thread t = g + 64 k
-// reads the H / 64 values g + 64 k' of its column and runs those stages on
-// them in registers (the same butterflies, in the same order, with the same
-// f32 rounding), keeping element k.  Every thread calls it; threads >= H
-// hold zeros.  Returns thread t's transformed value; v is its input.
+// value per thread, strides ascending: DPP within rows, swizzle / bpermute
+// across them, for strides 1..32.  The strides 64, 128, 256 mix values of
+// different waves: after one exchange through the LDS buffer hv (a buffer no
+// earlier step of the launch has used), thread t = g + 64 k reads the H / 64
+// values g + 64 k' of its column and runs those stages on them in registers
+// (the same butterflies, in the same order), keeping element k.  Every
+// thread calls it; threads >= H hold zeros.  Returns thread t's transformed
+// value; v is its input.
 __device__ float fwht_block(float v, float* hv, uint32_t H, uint32_t t) {
-  v = butterfly(v, nd::dpp<nd::kQuadXor1>(v), t, 1);
-  if (H > 2) v = butterfly(v, nd::dpp<nd::kQuadXor2>(v), t, 2);
-  if (H > 4) v = butterfly(v, nd::lane_xor<4>(v), t, 4);
-  if (H > 8) v = butterfly(v, nd::lane_xor<8>(v), t, 8);
-  if (H > 16) v = butterfly(v, nd::lane_xor<16>(v), t, 16);
-  if (H > 32) v = butterfly(v, nd::lane_xor<32>(v), t, 32);
+  v = butterfly(v, nd::dpp<nd::kQuadXor1>(v), t & 1);
+  if (H > 2) v = butterfly(v, nd::dpp<nd::kQuadXor2>(v), t & 2);
+  if (H > 4) v = butterfly(v, nd::lane_xor<4>(v), t & 4);
+  if (H > 8) v = butterfly(v, nd::lane_xor<8>(v), t & 8);
+  if (H > 16) v = butterfly(v, nd::lane_xor<16>(v), t & 16);
+  if (H > 32) v = butterfly(v, nd::lane_xor<32>(v), t & 32);
   if (H <= 64) return v;
-  __syncthreads();  // every read of the previous exchange is done
   hv[t] = v;
-  __syncthreads();
+  nd::lds_barrier();
   const uint32_t G = H / 64, g = t & 63, k = t >> 6;  // G <= kMixWg / 64 = 8
   float c[kMixWg / 64];
 #pragma unroll
@@ -425,9 +475,9 @@ __device__ float fwht_block(float v, float* hv, uint32_t H, uint32_t t) {
 #pragma unroll
       for (uint32_t i = 0; i < kMixWg / 64; ++i)
         if (!(i & st)) {
-          const double a = c[i], b = c[i + st];
-          c[i] = (float)(a + b);
-          c[i + st] = (float)(a - b);
+          const float a = c[i], b = c[i + st];
+          c[i] = a + b;
+          c[i + st] = a - b;
         }
     }
   }
@@ -437,10 +487,31 @@ __device__ float fwht_block(float v, float* hv, uint32_t H, uint32_t t) {
   return out;
 }
 
+// phi operand tiling: the (2 + lanes) * lanes phi rows (<= 24) in tiles of
+// 16 weight rows, four waves per tile, each over up to kPhiPairs 64-wide
+// k-pairs of the lanes * dim (<= 2048) columns.
+constexpr int kPhiPairs = 8;
+
 // The one-workgroup part between two layers: post(l - 1), then pre(l) (or
 // the final norm).  Every global operand is loaded at entry, the ones the
-// post half needs first and the 48 KB of phi weights last, so the kernel
-// pays about one memory latency; after that it runs from registers and LDS.
+// post half needs first and the phi weights last, so the kernel pays about
+// one memory latency; after that it runs from registers and LDS, with
+// LDS-only barriers (a full barrier would also wait for the phi weight
+// stream and for every global store of the launch).
+//
+// The phi rows (runtime.ts:401-411) run on v_mfma_f32_16x16x32_f16: the
+// normalized lanes nl (|nl| < sqrt(lanes * d) by construction) are scaled by
+// the power of two split_scale and split into fp16 halves, hi = f16(v) and
+// lo = f16(v - hi), which hold v to 22 bits (2^-24 of split_scale absolute
+// below 2^-14); the int8 weights are exact in fp16 and the products exact in
+// the fp32 accumulator.  A = rows 0 (hi) and 1 (lo), zeros elsewhere; B = 16
+// weight rows of the tile; lane l supplies A row l % 16 and B column l % 16,
+// eight k of each 32-wide step: for k-pair p, lane block kb = l / 16 loads
+// the 16 weight bytes [64 p + 16 kb, +16) and the first MFMA of the pair
+// takes bytes [0, 8) of every block, the second [8, 16) (the A halves are
+// read at the same k).  D rows 0 and 1 (hi, lo) land in lanes 0..15, outputs
+// 0 and 1; the four waves of a tile meet in LDS and the sum is taken in
+// float64 times the row scale.
 __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   if (blockIdx.x) {
     const uint32_t m = blockIdx.x, D0 = a.d, L0 = a.lanes;
@@ -457,13 +528,14 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     if (a.route_out) a.route_out += (size_t)m * 20;
     if (a.cell) a.cell += (size_t)m * a.cell_ld;
   }
-  __shared__ float nl[2048];
-  __shared__ float hv[kMixWg];
-  __shared__ double red[2][kMixWg / 64];
-  __shared__ float phi[24], phi_sc[24], hpre[4], rt[20];
+  __shared__ __align__(16) _Float16 s_split[2][2048];  // hi, lo of the scaled nl
+  __shared__ float hv1[kMixWg], hv2[kMixWg];
+  __shared__ double red[2][2 * (kMixWg / 64)];
+  __shared__ __align__(16) float s_part[32][4][2];  // [phi row][wave of the tile][hi, lo]
+  __shared__ float phi[24], rt[20];
   const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const uint32_t D = a.d, L = a.lanes, N = L * D, H = a.hdim;
-  const uint32_t nrows = 2 * L + L * L, cpr = N / 16;
+  const uint32_t nrows = 2 * L + L * L;
   const bool col = t < D;
   int phase = 0;
   // ---- loads, unconditional and in first-use order (every pointer is valid
@@ -485,32 +557,42 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   float xl[4];
 #pragma unroll
   for (int l = 0; l < 4; ++l) xl[l] = a.x[(size_t)min((uint32_t)l, L - 1) * D + tc];
-  // Wave w owns phi rows w, w + 8, w + 16; lane l their 16-byte chunks l and
-  // l + 64.
-  uint4 pw[kMixRows][kMixCols];
+  // phi weights: wave w takes tile w & 1 and k-pairs [ppw (w >> 1), +ppw).
+  const uint32_t r16 = lane & 15, kb = lane >> 4;
+  const uint32_t tile = wave & 1, kq = wave >> 1;
+  const uint32_t prow = tile * 16 + r16;
+  const bool prow_ok = prow < nrows;
+  const uint32_t pairs = N / 64, ppw = (pairs + 3) / 4;
+  const uint32_t pr = prow_ok ? prow : 0;
+  const int8_t* wrow = (pr < L ? w0 + (size_t)pr * N
+                               : (pr < 2 * L ? w1 + (size_t)(pr - L) * N
+                                             : w2 + (size_t)(pr - 2 * L) * N)) + kb * 16;
+  // Unconditional loads at clamped (in-bounds) addresses: a predicated load
+  // would make the compiler wait for it (and for every older load) at its
+  // branch.  Pairs past the wave's share are skipped by the MFMA loop and
+  // rows past the phi rows are zeroed there.
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 pw[kPhiPairs];
 #pragma unroll
-  for (int i = 0; i < kMixRows; ++i) {
-    const uint32_t r = min(wave + i * (kMixWg / 64), nrows - 1);
-    const int8_t* row = r < L ? w0 + (size_t)r * N
-                        : (r < 2 * L ? w1 + (size_t)(r - L) * N : w2 + (size_t)(r - 2 * L) * N);
-#pragma unroll
-    for (int j = 0; j < kMixCols; ++j)
-      pw[i][j] = *reinterpret_cast<const uint4*>(row + min(lane + 64u * j, cpr - 1) * 16);
+  for (int i = 0; i < kPhiPairs; ++i) {
+    const uint32_t pp = min(kq * ppw + i, pairs - 1);
+    pw[i] = *reinterpret_cast<const u32x4*>(wrow + (size_t)pp * 64);
   }
+  __builtin_amdgcn_sched_barrier(0);
   const uint32_t tr = min(t, nrows - 1);
   const float norm_in = a.norm_input[tc], ekey = a.ekey[tc], evalue = a.evalue[tc],
-              b_pre = a.b_pre[min(t, L - 1)], fnorm = a.final_norm[tc],
+              fnorm = a.final_norm[tc],
               psc = tr < L ? s0[tr] : (tr < 2 * L ? s1[tr - L] : s2[tr - 2 * L]);
+  const float bpre = a.b_pre[min(lane, L - 1)], spre = s0[min(lane, L - 1)];
 
   // ---- post(l - 1)
   if (a.has_post) {
     const double sp = mix_sum(col ? (double)p * p : 0.0, red, phase);
     const double ip = 1.0 / sqrt(sp / D + 1e-6);
-    const double ascale = sigmoid_d((double)a.attention_gate);
     float after = 0.f;
     if (col) {
       const float np = (float)((1.0 + (double)post_norm) * (double)p * ip);
-      after = (float)((double)blk + ascale * (double)np);
+      after = (float)((double)blk + a.attention_scale * (double)np);
     }
     if (t < L * L + L) rt[t] = route;  // visible after the next barrier
     const double sa = mix_sum(col ? (double)after * after : 0.0, red, phase);
@@ -522,15 +604,15 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
       const float pre = (float)((1.0 + (double)pre_h) * (double)after * ia);
       v = (float)((double)pre * (double)d1);
     }
-    const double inv_root = 1.0 / sqrt((double)H);
-    v = fwht_block(v, hv, H, t);
+    const double inv_root = a.inv_root_h;
+    v = fwht_block(v, hv1, H, t);
     if (t < H) {
       const double z = (double)v * inv_root * (double)d2;
       v = (float)(z * sigmoid_d(z));
     } else {
       v = 0.f;
     }
-    v = fwht_block(v, hv, H, t);
+    v = fwht_block(v, hv2, H, t);
     if (col) {
       const float mlp = (float)((double)v * inv_root * (double)d3);
       const float delta = (float)((double)after + (double)mlp - (double)upd);
@@ -581,54 +663,63 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     if ((uint32_t)l < L) ss += (double)xl[l] * (double)xl[l];
   ss = mix_sum(col ? ss : 0.0, red, phase);
   const double inv = 1.0 / sqrt(ss / N + 1e-6);
-  // The normalized lanes go to LDS interleaved: the q-th float4 of 16-element
-  // chunk ch sits at float4 index q * cpr + ch, so that the lanes of a wave,
-  // which read consecutive chunks, read consecutive 16-byte words.
-  float4* nl4 = reinterpret_cast<float4*>(nl);
   if (col) {
 #pragma unroll
     for (int l = 0; l < 4; ++l)
       if ((uint32_t)l < L) {
-        const uint32_t e = l * D + t;
-        nl[((((e >> 2) & 3) * cpr) + (e >> 4)) * 4 + (e & 3)] = (float)((double)xl[l] * inv);
+        const float v = (float)((double)xl[l] * inv) * a.split_scale;
+        const _Float16 h = (_Float16)v;
+        s_split[0][l * D + t] = h;
+        s_split[1][l * D + t] = (_Float16)(v - (float)h);
       }
   }
-  if (t < nrows) phi_sc[t] = psc;
-  __syncthreads();
+  nd::lds_barrier();
+  float4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < kMixRows; ++i) {
-    const uint32_t r = wave + i * (kMixWg / 64);
-    double rs = 0.0;
+  for (int i = 0; i < kPhiPairs; ++i) {
+    const uint32_t pp = kq * ppw + i;
+    if ((uint32_t)i < ppw && pp < pairs) {  // uniform over the wave
 #pragma unroll
-    for (int j = 0; j < kMixCols; ++j) {
-      const uint32_t c = lane + 64u * j;
-      if (r < nrows && c < cpr) {
-        // fp32 over the chunk's 16 products, float64 across chunks.
-        const uint32_t words[4] = {pw[i][j].x, pw[i][j].y, pw[i][j].z, pw[i][j].w};
-        float dot = 0.f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float4 f = nl4[q * cpr + c];
-          const uint32_t wq = words[q];
-          dot = fmaf((float)(int8_t)(wq & 0xff), f.x, dot);
-          dot = fmaf((float)(int8_t)((wq >> 8) & 0xff), f.y, dot);
-          dot = fmaf((float)(int8_t)((wq >> 16) & 0xff), f.z, dot);
-          dot = fmaf((float)(int8_t)(wq >> 24), f.w, dot);
-        }
-        rs += (double)dot;
+      for (int h = 0; h < 2; ++h) {
+        half8 av = {};
+        if (r16 < 2)
+          av = *reinterpret_cast<const half8*>(&s_split[r16][pp * 64 + kb * 16 + h * 8]);
+        const u32x4 wv = prow_ok ? pw[i] : u32x4{0u, 0u, 0u, 0u};
+        const half8 bv = nd::codes_to_half(h ? u32x2{wv.z, wv.w} : u32x2{wv.x, wv.y});
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
       }
     }
-    rs = nd::wave_sum(rs);
-    if (lane == 0 && r < nrows) phi[r] = (float)((double)phi_sc[r] * rs);
   }
-  __syncthreads();
-  if (t < L) {
-    const double off = t == a.own_pre ? 4.0 : -4.0;
-    hpre[t] = (float)sigmoid_d((double)a.a_pre * (double)phi[t] + (double)b_pre + off);
-    a.phi_post[t] = phi[L + t];
+  if (lane < 16) {
+    s_part[prow][kq][0] = acc[0];
+    s_part[prow][kq][1] = acc[1];
   }
-  if (t < L * L) a.phi_res[t] = phi[2 * L + t];
-  __syncthreads();
+  nd::lds_barrier();
+  // phi row r = scale_r * 2^-s * sum over the tile's waves of (hi + lo), in
+  // float64; every thread takes the phi_pre rows itself (they feed hPre).
+  auto phi_row = [&](uint32_t r, float scale) -> float {
+    const float4 q0 = *reinterpret_cast<const float4*>(&s_part[r][0][0]);
+    const float4 q1 = *reinterpret_cast<const float4*>(&s_part[r][2][0]);
+    const double sum = (((double)q0.x + (double)q0.y) + ((double)q0.z + (double)q0.w)) +
+                       (((double)q1.x + (double)q1.y) + ((double)q1.z + (double)q1.w));
+    return (float)((double)scale * (sum * (double)a.split_unscale));
+  };
+  if (t < nrows) {
+    const float v = phi_row(t, psc);
+    phi[t] = v;  // read by route_wave after later barriers
+    if (t >= L && t < 2 * L) a.phi_post[t - L] = v;
+    if (t >= 2 * L) a.phi_res[t - 2 * L] = v;
+  }
+  // hPre (runtime.ts:412-417): lane l < lanes of every wave takes lane l's
+  // gate, and the wave shares them by readlane (no barrier).
+  float hp = 0.f;
+  if (lane < L) {
+    const double off = lane == a.own_pre ? 4.0 : -4.0;
+    hp = (float)sigmoid_d((double)a.a_pre * (double)phi_row(lane, spre) + (double)bpre + off);
+  }
+  float hpre[4];
+#pragma unroll
+  for (int l = 0; l < 4; ++l) hpre[l] = nd::readlane(hp, l);
   // updateInput = sum_lane hPre[lane] * x[lane].
   float u = 0.f;
   if (col) {
@@ -642,12 +733,12 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   float b = u;
   if (a.has_site) {
     // alpha = sigmoid(rmsUnit(u) . rmsUnit(key) / sqrt(d)); block = u + alpha * value.
-    const double su = mix_sum(col ? (double)u * u : 0.0, red, phase);
-    const double sk = mix_sum(col ? (double)ekey * ekey : 0.0, red, phase);
+    double su = col ? (double)u * u : 0.0, sk = col ? (double)ekey * ekey : 0.0;
+    mix_sum2(su, sk, red, phase);
     const double iu = 1.0 / sqrt(su / D + 1e-6), ik = 1.0 / sqrt(sk / D + 1e-6);
     const float nu = (float)((double)u * iu), nk = (float)((double)ekey * ik);
     const double dot = mix_sum(col ? (double)nu * (double)nk : 0.0, red, phase);
-    const double alpha = sigmoid_d(dot / sqrt((double)D));
+    const double alpha = sigmoid_d(dot / a.sqrt_d);
     if (col) b = (float)((double)u + alpha * (double)evalue);
   }
   if (col) a.blk[t] = b;
@@ -1271,7 +1362,7 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s) 
   m.d1 = n->params + n->o_d1 + (size_t)pl * D;
   m.d2 = n->params + n->o_d2 + (size_t)pl * d.hadamard;
   m.d3 = n->params + n->o_d3 + (size_t)pl * D;
-  m.attention_gate = n->attention_gate[pl];
+  mix_constants(m, D, d.hadamard, ln, n->attention_gate[pl]);
   m.route = n->route;
   m.has_pre = pre && (parts & kMixPre);
   m.own_pre = ql % ln;
@@ -1607,7 +1698,7 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
     m.d1 = n->params + n->o_d1 + (size_t)pl * D;
     m.d2 = n->params + n->o_d2 + (size_t)pl * d.hadamard;
     m.d3 = n->params + n->o_d3 + (size_t)pl * D;
-    m.attention_gate = n->attention_gate[pl];
+    mix_constants(m, D, d.hadamard, ln, n->attention_gate[pl]);
     m.route = n->pf_route + (size_t)r0 * 20;
     m.has_pre = pre;
     m.own_pre = ql % ln;

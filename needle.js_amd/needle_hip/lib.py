@@ -69,6 +69,7 @@ SIGNATURES = {
     "nd_matvec_batch": (I32, [P, C.POINTER(MatvecJob), U32]),
     "nd_row": (I32, [P, P, U32, P]),
     "nd_row_d": (I32, [P, P, U32, P, P]),
+    "nd_stream_read_d": (I32, [P, P, C.c_uint64, U32, P, P]),
     "nd_kv_create": (I32, [P, U32, U32, U32, U32, U32, U32, U32, PP]),
     "nd_kv_free": (I32, [P, P]),
     "nd_kv_clear": (I32, [P, P]),
@@ -101,6 +102,7 @@ SIGNATURES = {
     "nd_prefill_set_tokens": (I32, [P, P, P, U32, U32]),
     "nd_prefill_run_d": (I32, [P, P, P, P]),
     "nd_prefill_logits": (I32, [P, P, P]),
+    "nd_prefill_phase_ms": (I32, [P, P, P, P]),
     "nd_prefill_read_projections": (I32, [P, P, P]),
     "nd_needle_create": (I32, [P, P, PP]),
     "nd_needle_free": (I32, [P, P]),

@@ -220,6 +220,15 @@ class HipPrefill:
                                                       C.c_void_p(stream) if stream else None),
                             "nd_prefill_run_d")
 
+    def phase_ms(self, cache):
+        """One eager pass with an event after every kernel: summed ms of
+        (int8 GEMMs, causal attention, everything else)."""
+        ms = np.zeros(3, np.float32)
+        self.backend._check(self.lib.nd_prefill_phase_ms(self.backend.ctx, self.handle,
+                                                         cache.handle, L.ptr(ms)),
+                            "nd_prefill_phase_ms")
+        return float(ms[0]), float(ms[1]), float(ms[2])
+
     def logits(self):
         out = np.empty(self.decoder.geometry.vocab, np.float32)
         self.backend._check(self.lib.nd_prefill_logits(self.backend.ctx, self.handle,
