@@ -600,34 +600,38 @@ struct AttnLaunch {
 
 // Causal prefill attention on MFMA (a prefill whose positions all see [0,
 // position] in their own slots; int8 cache).  Workgroup = (block of 64 query
-// rows, query head h, KV head h / rep), 8 waves in two groups: wave w takes
-// rows [z0 + 16 (w % 4), +16), lane l the row 16 (w % 4) + l % 16, and group
-// g = w / 4 the key blocks g, g + 2, ... (64 keys each), so both groups walk
-// half of the row block's keys; their online-softmax states merge through
+// rows, query head h, KV head h / rep), 16 waves in four groups: wave w
+// takes rows [z0 + 16 (w % 4), +16), lane l the row 16 (w % 4) + l % 16, and
+// group g = w / 4 the key blocks g, g + 4, ... (64 keys each), so each group
+// walks a quarter of the row block's keys (the causal triangle gives the
+// last row blocks the most); the four online-softmax states merge through
 // LDS at the end.  Each group streams its key blocks through its own pair of
-// LDS buffers (K codes as stored, V transposed to [dim][key]), one barrier
-// per step.  Per block and wave:
+// LDS buffers, converting the codes to fp16 once on the way in (K as
+// stored, V transposed to [dim][key]), one barrier per step.  Per block and
+// wave:
 //   S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = K codes (row = key, exact in
 //   fp16), B = Q^T split into fp16 halves hi + lo of q * 2^-e (e: the row's
 //   largest magnitude, < 2^e), which hold q to 2^-24 of the row maximum; the
 //   product lands as lane l holding keys 4 (l / 16) + c of each 16-key tile
 //   for its own row;
-//   scores = (S * k_scale / 8) * 2^e, causal mask, online softmax in fp32
-//   (__expf), as NeedleRuntime.#attention (model/runtime.ts:719-786,
-//   softmaxInPlace model/math.ts:46-60) evaluates them;
+//   scores in base 2: (S * (k_scale / 8 * log2 e)) * 2^e, causal mask,
+//   online softmax in fp32 with v_exp_f32 (2^x; results below 2^-126 flush
+//   to zero, as with __expf) -- NeedleRuntime.#attention
+//   (model/runtime.ts:719-786, softmaxInPlace model/math.ts:46-60) with its
+//   exponentials taken as 2^(x log2 e);
 //   O^T += V^T P'^T: B = P'^T with p' = p * v_scale * 2^f (fp16 halves; f
 //   puts the largest v_scale of the visible keys below 2^15 so that both
 //   halves stay normal down to 2^-18 of it), which is exactly the layout the
 //   S^T product left in the lane (8 keys per lane, the A operand reads V^T at
 //   the same keys); A = V^T codes (row = dim).
 // The output row is O / (l 2^f), gated when `gate` is set (runtime.ts:503-507).
-constexpr uint32_t kPfRows = 64, kPfKeys = 64, kPfThreads = 512;
-constexpr uint32_t kKStride = 80;   // LDS bytes per key row of K (16-byte aligned rows)
-constexpr uint32_t kVtStride = 68;  // LDS bytes per dim row of V^T
+constexpr uint32_t kPfRows = 64, kPfKeys = 64, kPfGroups = 4, kPfThreads = 256 * kPfGroups;
+constexpr uint32_t kKStrideH = 72;   // halves per key row of K in LDS (16-byte aligned rows)
+constexpr uint32_t kVtStrideH = 68;  // halves per dim row of V^T in LDS (8-byte aligned rows)
 struct PfBuf {
-  int8_t k[kPfKeys * kKStride];
-  int8_t vt[kHeadDim * kVtStride];
-  float ks[kPfKeys];  // k_scale / 8
+  _Float16 k[kPfKeys * kKStrideH];
+  _Float16 vt[kHeadDim * kVtStrideH];
+  float ks[kPfKeys];  // k_scale / 8 * log2 e
   float vs[kPfKeys];  // v_scale * 2^f
 };
 
@@ -640,9 +644,10 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_mfma_kernel(
   using nd::half8;
   using nd::float4v;
   using nd::u32x2;
-  __shared__ __align__(16) PfBuf s_buf[2][2];  // [group][buffer]
-  __shared__ uint32_t s_top[8];
-  __shared__ float s_vmax[8];
+  typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+  __shared__ __align__(16) PfBuf s_buf[kPfGroups][2];  // [group][buffer]
+  __shared__ uint32_t s_top[kPfThreads / 64];
+  __shared__ float s_vmax[kPfThreads / 64];
   const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const uint32_t grp = wave >> 2, wq = wave & 3, tg = t & 255;
   const uint32_t r16 = lane & 15, kb = lane >> 4;
@@ -675,8 +680,9 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_mfma_kernel(
   for (int o = 8; o >= 1; o >>= 1) wmin = min(wmin, (uint32_t)__shfl_xor((int)wmin, o, 64));
   wmin = __builtin_amdgcn_readfirstlane(wmin);
   __syncthreads();
-  const uint32_t top = max(max(max(s_top[0], s_top[1]), max(s_top[2], s_top[3])),
-                           max(max(s_top[4], s_top[5]), max(s_top[6], s_top[7])));
+  uint32_t top = 0;
+#pragma unroll
+  for (uint32_t w = 0; w < kPfThreads / 64; ++w) top = max(top, s_top[w]);
   if (top > alloc || top == 0) return;  // validated on entry; stay in bounds
   const uint32_t nblocks = (top + kPfKeys - 1) / kPfKeys;
 
@@ -711,11 +717,11 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_mfma_kernel(
   __syncthreads();
   float vsmax = 0.f;
 #pragma unroll
-  for (int w = 0; w < 8; ++w) vsmax = fmaxf(vsmax, s_vmax[w]);
+  for (uint32_t w = 0; w < kPfThreads / 64; ++w) vsmax = fmaxf(vsmax, s_vmax[w]);
   int fe = 0;
   if (vsmax > 0.f && vsmax <= 3.4028235e38f) frexpf(vsmax, &fe);  // vsmax < 2^fe
   const float pup = ldexpf(1.f, 15 - fe), pdown = ldexpf(1.f, fe - 15);
-  const float ks_mul = score_scale;
+  const float ks_mul = score_scale * 1.4426950408889634f;  // scores in base 2
 
   // Block loads of the group: thread tg takes key tg / 4, bytes [16 (tg %
   // 4), +16) of its K and V rows (keys past top read the last visible slot;
@@ -735,30 +741,36 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_mfma_kernel(
     }
   };
   auto store_block = [&](PfBuf& B) {
-    *reinterpret_cast<uint4*>(&B.k[lkey * kKStride + 16 * lpart]) = kreg;
-    const uint32_t words[4] = {vreg.x, vreg.y, vreg.z, vreg.w};
+    const half8 k0 = nd::codes_to_half(u32x2{kreg.x, kreg.y});
+    const half8 k1 = nd::codes_to_half(u32x2{kreg.z, kreg.w});
+    *reinterpret_cast<half8*>(&B.k[lkey * kKStrideH + 16 * lpart]) = k0;
+    *reinterpret_cast<half8*>(&B.k[lkey * kKStrideH + 16 * lpart + 8]) = k1;
+    const half8 v0 = nd::codes_to_half(u32x2{vreg.x, vreg.y});
+    const half8 v1 = nd::codes_to_half(u32x2{vreg.z, vreg.w});
 #pragma unroll
-    for (int e = 0; e < 16; ++e)
-      B.vt[(16 * lpart + e) * kVtStride + lkey] = (int8_t)(words[e >> 2] >> (8 * (e & 3)));
+    for (int e = 0; e < 8; ++e) {
+      B.vt[(16 * lpart + e) * kVtStrideH + lkey] = v0[e];
+      B.vt[(16 * lpart + 8 + e) * kVtStrideH + lkey] = v1[e];
+    }
     if (tg < kPfKeys) {
       B.ks[tg] = ksr * ks_mul;
       B.vs[tg] = vsr * pup;
     }
   };
-  const uint32_t steps = (nblocks + 1) / 2;  // both groups step together
+  const uint32_t steps = (nblocks + kPfGroups - 1) / kPfGroups;  // the groups step together
   if (grp < nblocks) {
     load_block(grp);
     store_block(s_buf[grp][0]);
   }
   nd::lds_barrier();
 
-  float m = -INFINITY, l = 0.f;
+  float m = -INFINITY, l = 0.f;  // m in base 2
   float4v o[4] = {};
   for (uint32_t i = 0; i < steps; ++i) {
-    const uint32_t b = 2 * i + grp;
-    const bool has = b < nblocks, has_next = b + 2 < nblocks;
+    const uint32_t b = kPfGroups * i + grp;
+    const bool has = b < nblocks, has_next = b + kPfGroups < nblocks;
     PfBuf& B = s_buf[grp][i & 1];
-    if (has_next) load_block(b + 2);
+    if (has_next) load_block(b + kPfGroups);
     if (has) {
       const uint32_t k0 = b * kPfKeys;
       // S^T tiles j: keys k0 + 16 j + 4 kb + c of this lane's row.
@@ -768,9 +780,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_mfma_kernel(
         sc[j] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-          const u32x2 kw =
-              *reinterpret_cast<const u32x2*>(&B.k[(16 * j + r16) * kKStride + 32 * s2 + 8 * kb]);
-          const half8 ka = nd::codes_to_half(kw);
+          const half8 ka =
+              *reinterpret_cast<const half8*>(&B.k[(16 * j + r16) * kKStrideH + 32 * s2 + 8 * kb]);
           sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[s2], sc[j], 0, 0, 0);
           sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[s2], sc[j], 0, 0, 0);
         }
@@ -792,8 +803,10 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_mfma_kernel(
       bmax = fmaxf(bmax, nd::lane_xor<16>(bmax));
       bmax = fmaxf(bmax, nd::lane_xor<32>(bmax));
       const float m_new = fmaxf(m, bmax);
-      // 1 while no key has been visible (-inf - -inf), 0 on the first visible one.
-      const float alpha = m_new == -INFINITY ? 1.f : __expf(m - m_new);
+      // While no key has been visible m_new is -inf: subtract 0 instead, so
+      // that masked scores give exp2(-inf) = 0 and alpha = 1.
+      const float m_sub = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m - m_sub);
       m = m_new;
       l *= alpha;
 #pragma unroll
@@ -802,7 +815,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_mfma_kernel(
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const float e = sc[j][c] == -INFINITY ? 0.f : __expf(sc[j][c] - m_new);
+          const float e = __builtin_amdgcn_exp2f(sc[j][c] - m_sub);
           sc[j][c] = e;
           l += e;
         }
@@ -815,19 +828,24 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_mfma_kernel(
                              sc[2 * s2][2] * va.z,     sc[2 * s2][3] * va.w,
                              sc[2 * s2 + 1][0] * vb.x, sc[2 * s2 + 1][1] * vb.y,
                              sc[2 * s2 + 1][2] * vb.z, sc[2 * s2 + 1][3] * vb.w};
+        // hi = pv rounded toward zero to fp16, lo = fp16 of the (exact f32)
+        // remainder: |pv - hi - lo| <= 2^-22 |pv| while lo is normal.
         half8 ph, pl;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const _Float16 hv = (_Float16)pv[e];
-          ph[e] = hv;
-          pl[e] = (_Float16)(pv[e] - (float)hv);
+        for (int e = 0; e < 8; e += 2) {
+          const auto hv = __builtin_amdgcn_cvt_pkrtz(pv[e], pv[e + 1]);
+          const auto lv = __builtin_amdgcn_cvt_pkrtz(pv[e] - (float)hv[0], pv[e + 1] - (float)hv[1]);
+          ph[e] = hv[0];
+          ph[e + 1] = hv[1];
+          pl[e] = lv[0];
+          pl[e + 1] = lv[1];
         }
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-          const int8_t* vt = &B.vt[(16 * d + r16) * kVtStride + 32 * s2 + 4 * kb];
-          const u32x2 vw = {*reinterpret_cast<const uint32_t*>(vt),
-                            *reinterpret_cast<const uint32_t*>(vt + 16)};
-          const half8 va8 = nd::codes_to_half(vw);
+          const _Float16* vt = &B.vt[(16 * d + r16) * kVtStrideH + 32 * s2 + 4 * kb];
+          const half4 lo4 = *reinterpret_cast<const half4*>(vt);
+          const half4 hi4 = *reinterpret_cast<const half4*>(vt + 16);
+          const half8 va8 = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
           o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va8, ph, o[d], 0, 0, 0);
           o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va8, pl, o[d], 0, 0, 0);
         }
@@ -839,11 +857,12 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_mfma_kernel(
   // l over the row's four lanes; o[d][c] is dim 16 d + 4 kb + c of the row.
   l += nd::lane_xor<16>(l);
   l += nd::lane_xor<32>(l);
-  // Merge: group 1 leaves (m, l, o) in LDS (the key buffers are free), group
-  // 0 combines them with its own and stores the row.
-  float* xm = reinterpret_cast<float*>(&s_buf[0][0]);  // [wq][18][64]
-  if (grp == 1) {
-    float* dst = xm + wq * 18 * 64 + lane;
+  // Merge: groups 1.. leave (m, l, o) in LDS (the key buffers are free),
+  // group 0 combines them with its own and stores the row.
+  float* xm = reinterpret_cast<float*>(&s_buf[0][0]);  // [group - 1][wq][18][64]
+  static_assert((kPfGroups - 1) * 4 * 18 * 64 * 4 <= sizeof(PfBuf) * kPfGroups * 2, "merge fits");
+  if (grp > 0) {
+    float* dst = xm + ((grp - 1) * 4 + wq) * 18 * 64 + lane;
     dst[0] = m;
     dst[64] = l;
 #pragma unroll
@@ -852,18 +871,34 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_mfma_kernel(
       for (int c = 0; c < 4; ++c) dst[(2 + 4 * d + c) * 64] = o[d][c];
   }
   nd::lds_barrier();
-  if (grp == 1 || !q_ok) return;
+  if (grp > 0 || !q_ok) return;
   {
-    const float* src = xm + wq * 18 * 64 + lane;
-    const float m1 = src[0], l1 = src[64];
-    const float mt = fmaxf(m, m1);
-    const float a0 = m == -INFINITY ? 0.f : __expf(m - mt);
-    const float a1 = m1 == -INFINITY ? 0.f : __expf(m1 - mt);
-    l = l * a0 + l1 * a1;
+    float mg[kPfGroups], lg[kPfGroups];
+    mg[0] = m;
+    lg[0] = l;
+    float mt = m;
 #pragma unroll
-    for (int d = 0; d < 4; ++d)
+    for (uint32_t g = 1; g < kPfGroups; ++g) {
+      const float* src = xm + ((g - 1) * 4 + wq) * 18 * 64 + lane;
+      mg[g] = src[0];
+      lg[g] = src[64];
+      mt = fmaxf(mt, mg[g]);
+    }
+    float ag[kPfGroups];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) o[d][c] = o[d][c] * a0 + src[(2 + 4 * d + c) * 64] * a1;
+    for (uint32_t g = 0; g < kPfGroups; ++g) ag[g] = mg[g] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mg[g] - mt);
+    l = l * ag[0];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) o[d] *= ag[0];
+#pragma unroll
+    for (uint32_t g = 1; g < kPfGroups; ++g) {
+      const float* src = xm + ((g - 1) * 4 + wq) * 18 * 64 + lane;
+      l += lg[g] * ag[g];
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[d][c] += src[(2 + 4 * d + c) * 64] * ag[g];
+    }
   }
   const size_t obase = ((size_t)zq * q_heads + h) * kHeadDim;
 #pragma unroll
