@@ -41,7 +41,7 @@ __device__ __forceinline__ float silu_f(float v) { return v / (1.f + __expf(-v))
 // the three exact integer sums) with agent-coherent stores, counts itself in
 // on the tile's counter, and the last of the S to arrive adds the partials in
 // slice order (deterministic), applies the epilogue and resets the counter.
-template <int MS, int NS, int EPI>
+template <int MS, int NS, int EPI, bool PF>
 __global__ __launch_bounds__(kGemmThreads) void gemm_i8_digits_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ sw, const int8_t* __restrict__ D,
     const float* __restrict__ fm, float* __restrict__ Y, uint32_t M, uint32_t N, uint32_t K,
@@ -68,13 +68,21 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_digits_kernel(
       for (int j = 0; j < 3; ++j) acc[a][b][j] = v4i{0, 0, 0, 0};
 
   const uint32_t lrow = lane & 15, lk = (lane >> 4) * 16;
-  for (uint32_t kc = k_begin; kc < k_end; kc += kKChunk) {
+  // A chunk's operands in registers: the weights (lane: 16 k of row n) and
+  // this thread's share of the digit staging, kDv 16-byte pieces (plane j,
+  // row r, piece c of the chunk's 16), all issued together.  With PF the
+  // next chunk's are issued before the current chunk's products (one memory
+  // round trip overlaps the MFMA work, for twice the operand registers).
+  constexpr int kVec = kKChunk / 16;                       // 16-byte pieces per row and plane
+  constexpr int kDv = 3 * TM * kVec / kGemmThreads;         // pieces per thread
+  static_assert(3 * TM * kVec % kGemmThreads == 0, "the staging divides evenly");
+  v4i wa[kKChunk / 64][NS];
+  uint4 dv[kDv];
+  auto load_chunk = [&](uint32_t kc) {
     const uint32_t kw = (k_end - kc) < (uint32_t)kKChunk ? (k_end - kc) : (uint32_t)kKChunk;
-    // This chunk's weights (clamped addresses past kw, never used).
-    v4i wa[kKChunk / 64][NS];
 #pragma unroll
     for (int q = 0; q < kKChunk / 64; ++q) {
-      const uint32_t ks = (uint32_t)q * 64 < kw ? q * 64 : 0;
+      const uint32_t ks = (uint32_t)q * 64 < kw ? q * 64 : 0;  // clamped past kw, never used
 #pragma unroll
       for (int a = 0; a < NS; ++a) {
         const uint32_t n = n0 + a * 16 + lrow;
@@ -82,18 +90,34 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_digits_kernel(
         wa[q][a] = *reinterpret_cast<const v4i*>(W + (size_t)nn * K + kc + ks + lk);
       }
     }
-    __syncthreads();
-    // Stage digits of rows [m0, m0 + TM) and k [kc, kc + kw) into LDS.
-    const uint32_t vec_per_row = kw / 16;
-    for (uint32_t i = t; i < 3 * TM * vec_per_row; i += kGemmThreads) {
-      const uint32_t j = i / (TM * vec_per_row);
-      const uint32_t rem = i % (TM * vec_per_row);
-      const uint32_t r = rem / vec_per_row, c = rem % vec_per_row;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (m0 + r < M) v = *reinterpret_cast<const uint4*>(D + j * plane + (size_t)(m0 + r) * K + kc + c * 16);
-      *reinterpret_cast<uint4*>(&lds[j][r][c * 16]) = v;
+#pragma unroll
+    for (int u = 0; u < kDv; ++u) {
+      const uint32_t i = t + u * kGemmThreads;
+      const uint32_t j = i / (TM * kVec), r = (i / kVec) % TM, c = i % kVec;
+      const uint32_t rr = m0 + r < M ? m0 + r : M - 1;
+      const uint32_t cc = c * 16 < kw ? c * 16 : 0;
+      dv[u] = *reinterpret_cast<const uint4*>(D + j * plane + (size_t)rr * K + kc + cc);
     }
-    __syncthreads();
+  };
+  load_chunk(k_begin);
+  for (uint32_t kc = k_begin; kc < k_end; kc += kKChunk) {
+    const uint32_t kw = (k_end - kc) < (uint32_t)kKChunk ? (k_end - kc) : (uint32_t)kKChunk;
+    if (!PF && kc != k_begin) load_chunk(kc);
+    __syncthreads();  // every wave is done with the previous chunk's digits
+#pragma unroll
+    for (int u = 0; u < kDv; ++u) {
+      const uint32_t i = t + u * kGemmThreads;
+      const uint32_t j = i / (TM * kVec), r = (i / kVec) % TM, c = i % kVec;
+      // rows past M multiply as zeros (pieces past kw are never read)
+      *reinterpret_cast<uint4*>(&lds[j][r][c * 16]) = m0 + r < M ? dv[u] : make_uint4(0, 0, 0, 0);
+    }
+    v4i wc[kKChunk / 64][NS];
+#pragma unroll
+    for (int q = 0; q < kKChunk / 64; ++q)
+#pragma unroll
+      for (int a = 0; a < NS; ++a) wc[q][a] = wa[q][a];
+    if (PF && kc + kKChunk < k_end) load_chunk(kc + kKChunk);
+    nd::lds_barrier();
 #pragma unroll
     for (int q = 0; q < kKChunk / 64; ++q) {
       if ((uint32_t)q * 64 >= kw) break;
@@ -104,7 +128,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_digits_kernel(
           const v4i db = *reinterpret_cast<const v4i*>(&lds[j][b * 16 + lrow][q * 64 + lk]);
 #pragma unroll
           for (int a = 0; a < NS; ++a)
-            acc[a][b][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[q][a], db, acc[a][b][j], 0, 0, 0);
+            acc[a][b][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wc[q][a], db, acc[a][b][j], 0, 0, 0);
         }
       }
     }
@@ -428,9 +452,17 @@ using GemmFn = void (*)(const int8_t*, const float*, const int8_t*, const float*
                         uint32_t, uint32_t, uint32_t, uint32_t, float*, uint32_t*);
 
 template <int EPI>
-GemmFn pick(uint32_t ms, uint32_t ns) {
-  if (ms == 4) return ns == 2 ? &gemm_i8_digits_kernel<4, 2, EPI> : &gemm_i8_digits_kernel<4, 1, EPI>;
-  return ns == 2 ? &gemm_i8_digits_kernel<1, 2, EPI> : &gemm_i8_digits_kernel<1, 1, EPI>;
+GemmFn pick(uint32_t ms, uint32_t ns, bool pf) {
+  if (ms == 4) {
+    if (pf) return ns == 2 ? &gemm_i8_digits_kernel<4, 2, EPI, true> : &gemm_i8_digits_kernel<4, 1, EPI, true>;
+    return ns == 2 ? &gemm_i8_digits_kernel<4, 2, EPI, false> : &gemm_i8_digits_kernel<4, 1, EPI, false>;
+  }
+  if (ms == 2) {
+    if (pf) return ns == 2 ? &gemm_i8_digits_kernel<2, 2, EPI, true> : &gemm_i8_digits_kernel<2, 1, EPI, true>;
+    return ns == 2 ? &gemm_i8_digits_kernel<2, 2, EPI, false> : &gemm_i8_digits_kernel<2, 1, EPI, false>;
+  }
+  if (pf) return ns == 2 ? &gemm_i8_digits_kernel<1, 2, EPI, true> : &gemm_i8_digits_kernel<1, 1, EPI, true>;
+  return ns == 2 ? &gemm_i8_digits_kernel<1, 2, EPI, false> : &gemm_i8_digits_kernel<1, 1, EPI, false>;
 }
 
 }  // namespace
@@ -444,7 +476,10 @@ hipError_t nd_launch_digitize(const float* x, uint32_t ldx, const float* norm, f
 }
 
 // Tile choice: decode-sized M (<= 64) uses 16-row m tiles so that even
-// N = 512 spreads over 32+ workgroups; prefill-sized M uses 64 x 128 tiles.
+// N = 512 spreads over 32+ workgroups; prefill-sized M uses 32 x 64 tiles
+// (measured at M = 2048 with digitize: 24.2 / 45.3 / 15.7 / 27.9 us for N x K
+// = 1536 x 512, 4096 x 512, 512 x 512, 512 x 2048, against 38.9 / 65.3 /
+// 21.6 / 43.9 for 64 x 128 tiles and 30.6 / 58.9 / 16.3 / 33.3 for 16 x 64).
 // With `split`, a grid of fewer than 256 tiles also splits k (K % 256 == 0)
 // into S = 2..8 slices until tiles * S reaches 256, within the workspace
 // (16 x 64 tiles only).
@@ -452,14 +487,19 @@ hipError_t nd_launch_gemm(const nd_mat* w, const int8_t* digits, const float* fm
                           uint32_t ldy, uint32_t M, int epilogue, hipStream_t s,
                           const nd_gemm_split* split) {
   if (M == 0) return hipSuccess;
-  uint32_t ms = M > 64 ? 4 : 1;
-  uint32_t ns = (M > 64 || w->n >= 8192) ? 2 : 1;
-  // 64 x 128 tiles only while they still give 256 workgroups (a 128-row
-  // prompt through a 1536 x 512 projection would get 24); below that the
+  uint32_t ms = M > 64 ? 2 : 1;
+  uint32_t ns = w->n >= 8192 && M <= 64 ? 2 : 1;
+  // 32 x 64 tiles only while they still give 256 workgroups (a 128-row
+  // prompt through a 1536 x 512 projection would get 96); below that the
   // 16 x 64 tiles spread the product over more CUs.
   if (((w->n + 64 * ns - 1) / (64 * ns)) * ((M + 16 * ms - 1) / (16 * ms)) < 256) ms = ns = 1;
+  // The prefetch of the next k chunk pays on the 16-row tiles (split-k
+  // decode shapes: 31.2 vs 33.3 us at 512 x 2048); the larger tiles run more
+  // workgroups per CU without it.
+  const bool pf = ms == 1;
   const uint32_t tm = 16 * ms, tn = 64 * ns;
-  GemmFn f = epilogue == 0 ? pick<0>(ms, ns) : epilogue == 1 ? pick<1>(ms, ns) : pick<2>(ms, ns);
+  GemmFn f = epilogue == 0 ? pick<0>(ms, ns, pf) : epilogue == 1 ? pick<1>(ms, ns, pf)
+                                                 : pick<2>(ms, ns, pf);
   dim3 grid((w->n + tn - 1) / tn, (M + tm - 1) / tm, 1);
   const uint32_t tiles = grid.x * grid.y;
   if (split && ms == 1 && ns == 1 && w->k % kKChunk == 0 && tiles <= split->counter_count) {
