@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "nd_internal.hpp"
+#include "nd_wave.hpp"
 
 namespace {
 
@@ -28,21 +29,10 @@ __device__ __forceinline__ uint64_t sm64_at(uint64_t seed, uint64_t i) {
   return sm64_mix(seed + (i + 1) * 0x9E3779B97F4A7C15ull);
 }
 
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+// Wave reductions on DPP and readlane (every lane gets the same value).
+__device__ __forceinline__ double wave_sum_d(double v) { return nd::wave_sum(v); }
 
-__device__ __forceinline__ float wave_absmax_js(float v) {
-  v = fabsf(v);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const float w = __shfl_xor(v, o, 64);
-    v = (v != v || w != w) ? __builtin_nanf("") : (v > w ? v : w);
-  }
-  return v;
-}
+__device__ __forceinline__ float wave_absmax_js(float v) { return nd::wave_max_js(fabsf(v)); }
 
 // x[m][:] = f32(f32(W[tok][:] * s[tok]) * sqrt(d)), the row() gather and
 // embedding scale of runtime.ts:305-309, in float64 like the reference.
@@ -61,14 +51,15 @@ __global__ void embed_kernel(const int8_t* __restrict__ W, const float* __restri
 // KV heads: k gets k_norm and RoPE, then k and v are quantized into the cache
 // at the row's position (#storeKV bit-exact semantics).  Norm and rotation run
 // in float64 with f32 stores, as the reference does.
-__global__ __launch_bounds__(64) void qk_rope_store_kernel(
+__device__ __forceinline__ void qk_rope_store_item(
+    uint32_t m, uint32_t slot, uint32_t lane,
     const float* __restrict__ qkv, uint32_t ld, uint32_t heads, uint32_t kv_heads,
     const float* __restrict__ q_norm, const float* __restrict__ k_norm,
-    const double* __restrict__ inv_freq, const uint32_t* __restrict__ positions,
+    const double* __restrict__ inv_freq, const double2* __restrict__ rope_tab,
+    const uint32_t* __restrict__ positions,
     uint32_t position0, float* __restrict__ q_out, int8_t* __restrict__ Kc,
     int8_t* __restrict__ Vc, float* __restrict__ Ks, float* __restrict__ Vs, uint32_t layer,
     uint32_t cache_heads, uint32_t alloc, uint32_t kv_head_stride) {
-  const uint32_t m = blockIdx.y, slot = blockIdx.x, lane = threadIdx.x;
   const uint32_t pos = positions ? positions[m] : position0 + m;
   const bool is_q = slot < heads;
   const uint32_t h = is_q ? slot : slot - heads;
@@ -79,9 +70,14 @@ __global__ __launch_bounds__(64) void qk_rope_store_kernel(
   const float normed = (float)((1.0 + (double)scale[lane]) * x * inv);
   // Half-split RoPE: pair (j, j + 32), angle = pos * theta^(-2j/64).
   const uint32_t j = lane & 31;
-  const double angle = (double)pos * inv_freq[j];
   double sn, cs;
-  sincos(angle, &sn, &cs);
+  if (rope_tab) {  // rope_table_kernel's values for row m: the same sincos
+    const double2 sc = rope_tab[(size_t)m * 32 + j];
+    sn = sc.x;
+    cs = sc.y;
+  } else {
+    sincos((double)pos * inv_freq[j], &sn, &cs);
+  }
   const double mine = normed;
   const double other = __shfl_xor((double)normed, 32, 64);
   const float rot = lane < 32 ? (float)(mine * cs - other * sn) : (float)(mine * cs + other * sn);
@@ -106,6 +102,33 @@ __global__ __launch_bounds__(64) void qk_rope_store_kernel(
     Ks[row] = (float)sk;
     Vs[row] = (float)sv;
   }
+}
+
+// Workgroup (slot, row m): one wave.
+__global__ __launch_bounds__(64) void qk_rope_store_kernel(
+    const float* __restrict__ qkv, uint32_t ld, uint32_t heads, uint32_t kv_heads,
+    const float* __restrict__ q_norm, const float* __restrict__ k_norm,
+    const double* __restrict__ inv_freq, const double2* __restrict__ rope_tab,
+    const uint32_t* __restrict__ positions,
+    uint32_t position0, float* __restrict__ q_out, int8_t* __restrict__ Kc,
+    int8_t* __restrict__ Vc, float* __restrict__ Ks, float* __restrict__ Vs, uint32_t layer,
+    uint32_t cache_heads, uint32_t alloc, uint32_t kv_head_stride) {
+  qk_rope_store_item(blockIdx.y, blockIdx.x, threadIdx.x, qkv, ld, heads, kv_heads, q_norm,
+                     k_norm, inv_freq, rope_tab, positions, position0, q_out, Kc, Vc, Ks, Vs,
+                     layer, cache_heads, alloc, kv_head_stride);
+}
+
+// (sin, cos) of the RoPE angles pos * inv_freq[j], j < 32, of rows [0, M)
+// at positions position0 + m, evaluated as qk_rope_store_kernel evaluates
+// them, so that the prefill's layers and heads share one evaluation per row.
+__global__ void rope_table_kernel(const double* __restrict__ inv_freq, uint32_t position0,
+                                  uint32_t M, double2* __restrict__ tab) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M * 32) return;
+  const uint32_t m = i >> 5, j = i & 31;
+  double sn, cs;
+  sincos((double)(position0 + m) * inv_freq[j], &sn, &cs);
+  tab[i] = make_double2(sn, cs);
 }
 
 // Allowed-token bitmask rows for decode step *step of sequence b: id v is
@@ -536,7 +559,8 @@ nd_status nd_batch_step(nd_ctx* ctx, nd_batch* b, uint32_t max_position, uint32_
     hipLaunchKernelGGL(qk_rope_store_kernel, dim3(dec->heads + dec->kv_heads, B), dim3(64), 0, s,
                        b->qkv, qkv_rows, dec->heads, dec->kv_heads,
                        dec->norms + dec->q_off + (size_t)l * kHd,
-                       dec->norms + dec->k_off + (size_t)l * kHd, dec->inv_freq, b->positions, 0u,
+                       dec->norms + dec->k_off + (size_t)l * kHd, dec->inv_freq, nullptr,
+                       b->positions, 0u,
                        b->q, (int8_t*)b->kv.k, (int8_t*)b->kv.v, b->kv.ks, b->kv.vs, l,
                        b->kv.kv_heads, b->kv.alloc, dec->kv_heads);
     ND_HIP(ctx, hipGetLastError());
@@ -571,6 +595,7 @@ struct nd_prefill {
   char* arena = nullptr;
   float *x = nullptr, *qkv = nullptr, *q = nullptr, *o = nullptr, *h = nullptr, *fm = nullptr,
         *partials = nullptr, *logits = nullptr;
+  double2* rope = nullptr;  // [max_tokens][32] (sin, cos) of the pass's positions
   int8_t* digits = nullptr;
   uint32_t *tokens = nullptr, *positions = nullptr, *counters = nullptr;
   size_t partial_floats = 0;
@@ -600,7 +625,7 @@ nd_status nd_prefill_create(nd_ctx* ctx, nd_decoder* dec, uint32_t max_tokens,
                           a256(M * dec->dim * 4),  a256(M * dec->ffn * 4), a256(M * 4),
                           a256(p->partial_floats * 4), a256((size_t)dec->vocab * 4),
                           a256(3 * M * kmax),      a256(M * 4),            a256(M * 4),
-                          a256(M * dec->kv_heads * kAttnCounterStride * 4)};
+                          a256(M * dec->kv_heads * kAttnCounterStride * 4), a256(M * 32 * 16)};
   size_t total = 0;
   for (size_t v : sizes) total += v;
   hipError_t e = hipMalloc(&p->arena, total);
@@ -629,6 +654,7 @@ nd_status nd_prefill_create(nd_ctx* ctx, nd_decoder* dec, uint32_t max_tokens,
   take(&p->tokens);
   take(&p->positions);
   take(&p->counters);
+  take(&p->rope);
   *out = p;
   return ND_OK;
 }
@@ -712,6 +738,9 @@ static nd_status enqueue_prefill(nd_ctx* ctx, nd_prefill* p, nd_kv* kv, hipStrea
   hipLaunchKernelGGL(embed_kernel, dim3((D + 255) / 256, M), dim3(256), 0, s, dec->embedding->w,
                      dec->embedding->scales, p->tokens, dec->vocab, D, std::sqrt((double)D), p->x);
   ND_HIP(ctx, hipGetLastError());
+  hipLaunchKernelGGL(rope_table_kernel, dim3((M * 32 + 255) / 256), dim3(256), 0, s, dec->inv_freq,
+                     p->position0, M, p->rope);
+  ND_HIP(ctx, hipGetLastError());
   ND_HIP(ctx, mark(O));
   for (uint32_t l = 0; l < dec->layers; ++l) {
     ND_HIP(ctx, nd_launch_digitize(p->x, D, dec->norms + dec->attn_off + (size_t)l * D, nullptr,
@@ -722,9 +751,9 @@ static nd_status enqueue_prefill(nd_ctx* ctx, nd_prefill* p, nd_kv* kv, hipStrea
     hipLaunchKernelGGL(qk_rope_store_kernel, dim3(dec->heads + dec->kv_heads, M), dim3(64), 0, s,
                        p->qkv, qkv_rows, dec->heads, dec->kv_heads,
                        dec->norms + dec->q_off + (size_t)l * kHd,
-                       dec->norms + dec->k_off + (size_t)l * kHd, dec->inv_freq, nullptr,
-                       p->position0, p->q, (int8_t*)kv->k, (int8_t*)kv->v, kv->ks, kv->vs, l,
-                       kv->kv_heads, kv->alloc, 0u);
+                       dec->norms + dec->k_off + (size_t)l * kHd, dec->inv_freq, p->rope,
+                       nullptr, p->position0, p->q, (int8_t*)kv->k, (int8_t*)kv->v, kv->ks,
+                       kv->vs, l, kv->kv_heads, kv->alloc, 0u);
     ND_HIP(ctx, hipGetLastError());
     ND_HIP(ctx, mark(O));
     ND_HIP(ctx, nd_launch_attention_batch(kv, l, p->positions, M, dec->kv_heads, 0u, rep, last,
