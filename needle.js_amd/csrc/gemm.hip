@@ -269,62 +269,78 @@ __global__ __launch_bounds__(256) void digitize_kernel(const float* __restrict__
 
 // Decode-shaped product (M <= 64 rows per launch, 16 x 64 output tiles) that
 // digitizes its own activations: workgroup (n tile, m tile, z) reads the fp32
-// rows of its 16 x 256 k chunk z (and, with NORM, the whole rows for the
-// zero-centred RMS norm of math.ts:16-32), writes the three digit planes of
-// that chunk with the chunk's own exponent -- 2^(E - 21), max |a| in
-// [2^E, 2^(E+1)) over the row's 256 values, so each value is carried to
-// 2^-22 of the chunk's largest -- and multiplies them as the kernel above.
-// Thread t of the staging holds row t / 16, columns [16 (t % 16), +16): a
+// rows of its CPW 16 x 256 k chunks [CPW z, CPW z + CPW) (and, with NORM, the
+// whole rows for the zero-centred RMS norm of math.ts:16-32), writes the
+// three digit planes of each chunk with the chunk's own exponent -- 2^(E -
+// 21), max |a| in [2^E, 2^(E+1)) over the row's 256 values, so each value is
+// carried to 2^-22 of the chunk's largest -- and multiplies them as the
+// kernel above, adding the chunks' scaled sums in k order.  All of its
+// chunks' loads are issued together (one memory round trip).  Thread t of
+// the staging holds row t / 16, columns [16 (t % 16), +16) of each chunk: a
 // row is one DPP row of 16 lanes, so its sum of squares and its maximum are
-// DPP reductions.  Slices (gridDim.z = K / 256) are combined as in the kernel
-// above, each partial already scaled by its chunk's factor.
-template <int EPI, bool NORM>
+// DPP reductions.  Slices (gridDim.z = K / (256 CPW)) are combined as in the
+// kernel above, each partial already scaled by its chunks' factors.
+template <int EPI, bool NORM, int CPW>
 __global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ sw, const float* __restrict__ X,
     uint32_t ldx, const float* __restrict__ norm, float* __restrict__ Y, uint32_t M, uint32_t N,
     uint32_t K, uint32_t ldy, float* __restrict__ part, uint32_t* __restrict__ counters) {
-  __shared__ __attribute__((aligned(16))) int8_t lds[3][16][kLdsRow];
-  __shared__ float s_fm[16];
+  __shared__ __attribute__((aligned(16))) int8_t lds[CPW][3][16][kLdsRow];
+  __shared__ float s_fm[CPW][16];
   const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const uint32_t n0 = blockIdx.x * 64 + wave * 16;
   const uint32_t m0 = blockIdx.y * 16;
-  const uint32_t S = gridDim.z, kc = blockIdx.z * kKChunk;
+  const uint32_t S = gridDim.z, kc0 = blockIdx.z * CPW * kKChunk;
   const uint32_t lrow = lane & 15, lk = (lane >> 4) * 16;
 
-  // Weights of the chunk first.
-  v4i wa[kKChunk / 64];
+  // Weights of the chunks first.
+  v4i wa[CPW][kKChunk / 64];
   {
     const uint32_t n = n0 + lrow;
-    const int8_t* wr = W + (size_t)(n < N ? n : N - 1) * K + kc + lk;
+    const int8_t* wr = W + (size_t)(n < N ? n : N - 1) * K + kc0 + lk;
 #pragma unroll
-    for (int q = 0; q < kKChunk / 64; ++q) wa[q] = *reinterpret_cast<const v4i*>(wr + q * 64);
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+      for (int q = 0; q < kKChunk / 64; ++q)
+        wa[c][q] = *reinterpret_cast<const v4i*>(wr + c * kKChunk + q * 64);
   }
-  // Activations: row r of the tile, 16 values of the chunk (and the row's
+  // Activations: row r of the tile, 16 values of each chunk (and the row's
   // other chunks for the norm; K <= kMaxNormK then).
   const uint32_t r = t >> 4, pc = t & 15;
   const uint32_t m = m0 + r;
   const float* xr = X + (size_t)(m < M ? m : M - 1) * ldx;
-  float v[16];
-  {
-    const float4* src = reinterpret_cast<const float4*>(xr + kc + pc * 16);
+  float v[CPW][16];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const float4* src = reinterpret_cast<const float4*>(xr + kc0 + c * kKChunk + pc * 16);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const float4 f = src[q];
-      v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+      v[c][4 * q] = f.x; v[c][4 * q + 1] = f.y; v[c][4 * q + 2] = f.z; v[c][4 * q + 3] = f.w;
     }
   }
-  float4 wn[4];  // this chunk's norm weights, in flight with the activations
+  float4 wn[CPW][4];  // the chunks' norm weights, in flight with the activations
   if constexpr (NORM) {
-    const float4* src = reinterpret_cast<const float4*>(norm + kc + pc * 16);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) wn[q] = src[q];
+    for (int c = 0; c < CPW; ++c) {
+      const float4* src = reinterpret_cast<const float4*>(norm + kc0 + c * kKChunk + pc * 16);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) wn[c][q] = src[q];
+    }
   }
   if constexpr (NORM) {
+    // The row's sum of squares in k order of the chunks: own chunks from
+    // registers, the others read here.
     float ss = 0.f;
+    for (uint32_t c0 = 0; c0 < K; c0 += kKChunk) {
+      if (c0 >= kc0 && c0 < kc0 + CPW * kKChunk) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) ss = fmaf(v[i], v[i], ss);
-    for (uint32_t c0 = 0; c0 < K; c0 += kKChunk) {  // the row's other chunks
-      if (c0 == kc) continue;
+        for (int c = 0; c < CPW; ++c)
+          if (c0 == kc0 + c * kKChunk)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) ss = fmaf(v[c][i], v[c][i], ss);
+        continue;
+      }
       const float4* o = reinterpret_cast<const float4*>(xr + c0 + pc * 16);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -335,61 +351,71 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
     ss = nd::row_sum(ss);
     const float inv = 1.f / sqrtf(ss / (float)K + 1e-6f);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4 f = wn[q];
-      v[4 * q] = (1.f + f.x) * v[4 * q] * inv;
-      v[4 * q + 1] = (1.f + f.y) * v[4 * q + 1] * inv;
-      v[4 * q + 2] = (1.f + f.z) * v[4 * q + 2] * inv;
-      v[4 * q + 3] = (1.f + f.w) * v[4 * q + 3] * inv;
-    }
-  }
-  float amax = 0.f;
+    for (int c = 0; c < CPW; ++c)
 #pragma unroll
-  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  amax = nd::row_max(amax);
-  int e = 0;
-  if (amax > 0.f) {
-    frexpf(amax, &e);  // amax in [2^(e-1), 2^e)
-    e -= 1;
-  }
-  const float up = ldexpf(1.f, 21 - e);
-  uint32_t d0w[4] = {0, 0, 0, 0}, d1w[4] = {0, 0, 0, 0}, d2w[4] = {0, 0, 0, 0};
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int X0 = (int)rintf(v[i] * up);  // |X0| < 2^22
-    const int d0 = ((X0 + 128) & 255) - 128;
-    const int X1 = (X0 - d0) >> 8;
-    const int d1 = ((X1 + 128) & 255) - 128;
-    const int d2 = (X1 - d1) >> 8;
-    d0w[i >> 2] |= (uint32_t)(d0 & 255) << (8 * (i & 3));
-    d1w[i >> 2] |= (uint32_t)(d1 & 255) << (8 * (i & 3));
-    d2w[i >> 2] |= (uint32_t)(d2 & 255) << (8 * (i & 3));
+      for (int q = 0; q < 4; ++q) {
+        const float4 f = wn[c][q];
+        v[c][4 * q] = (1.f + f.x) * v[c][4 * q] * inv;
+        v[c][4 * q + 1] = (1.f + f.y) * v[c][4 * q + 1] * inv;
+        v[c][4 * q + 2] = (1.f + f.z) * v[c][4 * q + 2] * inv;
+        v[c][4 * q + 3] = (1.f + f.w) * v[c][4 * q + 3] * inv;
+      }
   }
   const bool live = m < M;  // rows past M multiply as zeros
-  *reinterpret_cast<uint4*>(&lds[0][r][pc * 16]) =
-      live ? make_uint4(d0w[0], d0w[1], d0w[2], d0w[3]) : make_uint4(0, 0, 0, 0);
-  *reinterpret_cast<uint4*>(&lds[1][r][pc * 16]) =
-      live ? make_uint4(d1w[0], d1w[1], d1w[2], d1w[3]) : make_uint4(0, 0, 0, 0);
-  *reinterpret_cast<uint4*>(&lds[2][r][pc * 16]) =
-      live ? make_uint4(d2w[0], d2w[1], d2w[2], d2w[3]) : make_uint4(0, 0, 0, 0);
-  if (pc == 0) s_fm[r] = ldexpf(1.f, e - 21);
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
+    amax = nd::row_max(amax);
+    int e = 0;
+    if (amax > 0.f) {
+      frexpf(amax, &e);  // amax in [2^(e-1), 2^e)
+      e -= 1;
+    }
+    const float up = ldexpf(1.f, 21 - e);
+    uint32_t d0w[4] = {0, 0, 0, 0}, d1w[4] = {0, 0, 0, 0}, d2w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int X0 = (int)rintf(v[c][i] * up);  // |X0| < 2^22
+      const int d0 = ((X0 + 128) & 255) - 128;
+      const int X1 = (X0 - d0) >> 8;
+      const int d1 = ((X1 + 128) & 255) - 128;
+      const int d2 = (X1 - d1) >> 8;
+      d0w[i >> 2] |= (uint32_t)(d0 & 255) << (8 * (i & 3));
+      d1w[i >> 2] |= (uint32_t)(d1 & 255) << (8 * (i & 3));
+      d2w[i >> 2] |= (uint32_t)(d2 & 255) << (8 * (i & 3));
+    }
+    *reinterpret_cast<uint4*>(&lds[c][0][r][pc * 16]) =
+        live ? make_uint4(d0w[0], d0w[1], d0w[2], d0w[3]) : make_uint4(0, 0, 0, 0);
+    *reinterpret_cast<uint4*>(&lds[c][1][r][pc * 16]) =
+        live ? make_uint4(d1w[0], d1w[1], d1w[2], d1w[3]) : make_uint4(0, 0, 0, 0);
+    *reinterpret_cast<uint4*>(&lds[c][2][r][pc * 16]) =
+        live ? make_uint4(d2w[0], d2w[1], d2w[2], d2w[3]) : make_uint4(0, 0, 0, 0);
+    if (pc == 0) s_fm[c][r] = ldexpf(1.f, e - 21);
+  }
   __syncthreads();
 
-  v4i acc[3] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+  // Lane l, element i: n = n0 + 4 (l / 16) + i, m = m0 + l % 16.
+  float cs[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int q = 0; q < kKChunk / 64; ++q) {
+  for (int c = 0; c < CPW; ++c) {
+    v4i acc[3] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      const v4i db = *reinterpret_cast<const v4i*>(&lds[j][lrow][q * 64 + lk]);
-      acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[q], db, acc[j], 0, 0, 0);
+    for (int q = 0; q < kKChunk / 64; ++q) {
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const v4i db = *reinterpret_cast<const v4i*>(&lds[c][j][lrow][q * 64 + lk]);
+        acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[c][q], db, acc[j], 0, 0, 0);
+      }
+    }
+    const float fm = s_fm[c][lrow];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float ci = fm * ((float)acc[0][i] + 256.f * (float)acc[1][i] + 65536.f * (float)acc[2][i]);
+      cs[i] = c == 0 ? ci : cs[i] + ci;
     }
   }
-  // Lane l, element i: n = n0 + 4 (l / 16) + i, m = m0 + l % 16.
-  const float fm = s_fm[lrow];
-  float cs[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    cs[i] = fm * ((float)acc[0][i] + 256.f * (float)acc[1][i] + 65536.f * (float)acc[2][i]);
   if (S > 1) {
     const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x;
     float* mine = part + ((size_t)tile * S + blockIdx.z) * 1024;
@@ -442,10 +468,10 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
 using F32aFn = void (*)(const int8_t*, const float*, const float*, uint32_t, const float*, float*,
                         uint32_t, uint32_t, uint32_t, uint32_t, float*, uint32_t*);
 
-template <bool NORM>
+template <bool NORM, int CPW>
 F32aFn pick_f32a(int epilogue) {
-  return epilogue == 0 ? &gemm_i8_f32a_kernel<0, NORM>
-       : epilogue == 1 ? &gemm_i8_f32a_kernel<1, NORM> : &gemm_i8_f32a_kernel<2, NORM>;
+  return epilogue == 0 ? &gemm_i8_f32a_kernel<0, NORM, CPW>
+       : epilogue == 1 ? &gemm_i8_f32a_kernel<1, NORM, CPW> : &gemm_i8_f32a_kernel<2, NORM, CPW>;
 }
 
 using GemmFn = void (*)(const int8_t*, const float*, const int8_t*, const float*, float*, uint32_t,
@@ -537,8 +563,14 @@ hipError_t nd_launch_gemm_f32(const nd_mat* w, const float* x, uint32_t ldx, con
                               const nd_gemm_split* split) {
   if (M == 0) return hipSuccess;
   if (!nd_gemm_f32_fits(w, x, ldx, norm != nullptr, M, split)) return hipErrorInvalidValue;
-  const uint32_t S = w->k / kKChunk;
-  const F32aFn f = norm ? pick_f32a<true>(epilogue) : pick_f32a<false>(epilogue);
+  // Two chunks per workgroup when k has an even number of them: at K = 512
+  // the product then needs no cross-workgroup sum, whose round trip costs
+  // more than streaming the second chunk.
+  const uint32_t chunks = w->k / kKChunk;
+  const bool pair = chunks % 2 == 0;
+  const uint32_t S = pair ? chunks / 2 : chunks;
+  const F32aFn f = pair ? (norm ? pick_f32a<true, 2>(epilogue) : pick_f32a<false, 2>(epilogue))
+                        : (norm ? pick_f32a<true, 1>(epilogue) : pick_f32a<false, 1>(epilogue));
   hipLaunchKernelGGL(f, dim3((w->n + 63) / 64, (M + 15) / 16, S), dim3(kGemmThreads), 0, s, w->w,
                      w->scales, x, ldx, norm, y, M, w->n, w->k, ldy, split->partials,
                      split->counters);
