@@ -42,6 +42,20 @@ static nd_status ensure_stage(nd_ctx* ctx, size_t bytes) {
   return ND_OK;
 }
 
+static nd_status ensure_host_stage(nd_ctx* ctx, size_t bytes) {
+  if (ctx->host_stage_bytes >= bytes) return ND_OK;
+  if (ctx->host_stage) {
+    ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    ND_HIP(ctx, hipHostFree(ctx->host_stage));
+    ctx->host_stage = nullptr;
+    ctx->host_stage_bytes = 0;
+  }
+  size_t want = bytes < (64u << 10) ? (64u << 10) : bytes;
+  ND_HIP(ctx, hipHostMalloc(&ctx->host_stage, want, hipHostMallocDefault));
+  ctx->host_stage_bytes = want;
+  return ND_OK;
+}
+
 static nd_status ensure_partials(nd_ctx* ctx, size_t floats) {
   if (ctx->attn_partial_floats >= floats) return ND_OK;
   if (ctx->attn_partials) {
@@ -139,6 +153,7 @@ nd_status nd_destroy(nd_ctx* ctx) {
     delete g;
   }
   if (ctx->stage) hipFree(ctx->stage);
+  if (ctx->host_stage) hipHostFree(ctx->host_stage);
   if (ctx->attn_partials) hipFree(ctx->attn_partials);
   if (ctx->attn_counters) hipFree(ctx->attn_counters);
   if (ctx->mm_scratch) hipFree(ctx->mm_scratch);
@@ -440,11 +455,15 @@ nd_status nd_row(nd_ctx* ctx, const nd_mat* m, uint32_t row, float* out) {
   if (!m || row >= m->n) return nd_fail(ctx, ND_ERR_INVALID, "Matrix row %u is out of range", row);
   if (!out) return nd_fail(ctx, ND_ERR_INVALID, "output is NULL");
   nd_status st = ensure_stage(ctx, (size_t)m->k * 4);
+  if (st == ND_OK) st = ensure_host_stage(ctx, (size_t)m->k * 4);
   if (st != ND_OK) return st;
   float* d = reinterpret_cast<float*>(ctx->stage);
   ND_HIP(ctx, m->bits ? nd_launch_cq_row(m, row, d, ctx->stream) : nd_launch_row(m, row, d, ctx->stream));
-  ND_HIP(ctx, hipMemcpyAsync(out, d, (size_t)m->k * 4, hipMemcpyDeviceToHost, ctx->stream));
+  // Through pinned memory: a pageable destination costs a staged copy.
+  ND_HIP(ctx, hipMemcpyAsync(ctx->host_stage, d, (size_t)m->k * 4, hipMemcpyDeviceToHost,
+                             ctx->stream));
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  std::memcpy(out, ctx->host_stage, (size_t)m->k * 4);
   return ND_OK;
 }
 

@@ -43,6 +43,9 @@ struct nd_ctx {
   // Device staging for the host-pointer entry points (grown on demand).
   void* stage = nullptr;
   size_t stage_bytes = 0;
+  // Pinned host staging for small device-to-host reads (grown on demand).
+  void* host_stage = nullptr;
+  size_t host_stage_bytes = 0;
   // Split-context attention partials: acc [q_heads][chunks][head_dim] then
   // (max, sum) [q_heads][chunks][2], f32; and one arrival counter per KV head
   // (zeroed at allocation, reset by the kernel that consumes it).

@@ -537,12 +537,13 @@ def log_softmax_at(logits: np.ndarray, token: int) -> float:
 
 
 def argmax(values: np.ndarray) -> int:
-    """math.ts:140-151: the first maximum (NaN never wins after index 0)."""
-    best, best_value = 0, float(values[0])
-    for i in np.flatnonzero(values > best_value):
-        if float(values[i]) > best_value:
-            best, best_value = int(i), float(values[i])
-    return best
+    """math.ts:140-151: the first maximum, scanning with `>` from index 0 --
+    so a NaN at index 0 wins (nothing compares greater than it) and a NaN
+    anywhere else never does."""
+    v = np.asarray(values)
+    if v.size == 0 or np.isnan(v[0]):
+        return 0
+    return int(np.argmax(np.where(np.isnan(v), -np.inf, v)))
 
 
 class OnlineProbePool:

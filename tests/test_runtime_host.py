@@ -59,6 +59,20 @@ def test_log_softmax_and_argmax():
     assert argmax(np.array([np.nan, 1, 2], np.float32)) == 0  # NaN first is kept
     assert argmax(np.array([0, np.nan, 2], np.float32)) == 2
 
+    def scan(values):  # the reference loop as written: `>` from index 0
+        best, best_value = 0, float(values[0])
+        for i in range(1, len(values)):
+            if float(values[i]) > best_value:
+                best, best_value = i, float(values[i])
+        return best
+
+    for _ in range(200):
+        v = rng.integers(-3, 4, size=int(rng.integers(1, 12))).astype(np.float32)
+        v[rng.random(v.size) < 0.2] = np.nan
+        v[rng.random(v.size) < 0.1] = -np.inf
+        v[rng.random(v.size) < 0.05] = np.inf
+        assert argmax(v) == scan(v), v
+
 
 def test_probe_pool_equals_softmax_pooling():
     """Online pooling equals the closed form: per probe, the softmax over
