@@ -267,6 +267,90 @@ __global__ __launch_bounds__(256) void digitize_kernel(const float* __restrict__
   if (t == 0) fm[m] = ldexpf(1.f, e - 21);
 }
 
+// The same split with one wave per row (4 rows per workgroup): lane l holds
+// the float4 units l + 64 i of the row (VEC units, K <= 256 VEC), so the
+// sum of squares and the maximum are wave reductions on DPP and no barrier
+// is needed; each unit's three digit bytes go out as one 32-bit word per
+// plane.  Requires 16-byte aligned rows and K % 4 == 0.
+template <int VEC>
+__global__ __launch_bounds__(256) void digitize_rows_kernel(const float* __restrict__ X,
+                                                            uint32_t ldx,
+                                                            const float* __restrict__ norm,
+                                                            float* __restrict__ norm_out,
+                                                            int8_t* __restrict__ D,
+                                                            float* __restrict__ fm, uint32_t M,
+                                                            uint32_t K) {
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  const float4* x = reinterpret_cast<const float4*>(X + (size_t)m * ldx);
+  const uint32_t units = K / 4;
+  float4 v[VEC];
+  float4 w[VEC];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    const uint32_t u = lane + 64 * i;
+    v[i] = u < units ? x[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (norm) w[i] = u < units ? reinterpret_cast<const float4*>(norm)[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (norm) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i)
+      ss = fmaf(v[i].x, v[i].x, fmaf(v[i].y, v[i].y, fmaf(v[i].z, v[i].z, fmaf(v[i].w, v[i].w, ss))));
+    ss = nd::wave_sum(ss);
+    const float inv = 1.f / sqrtf(ss / (float)K + 1e-6f);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      v[i].x = (1.f + w[i].x) * v[i].x * inv;
+      v[i].y = (1.f + w[i].y) * v[i].y * inv;
+      v[i].z = (1.f + w[i].z) * v[i].z * inv;
+      v[i].w = (1.f + w[i].w) * v[i].w * inv;
+      const uint32_t u = lane + 64 * i;
+      if (norm_out && u < units) reinterpret_cast<float4*>(norm_out + (size_t)m * K)[u] = v[i];
+    }
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i)
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+  amax = nd::row_max(amax);
+  amax = fmaxf(fmaxf(nd::readlane(amax, 0), nd::readlane(amax, 16)),
+               fmaxf(nd::readlane(amax, 32), nd::readlane(amax, 48)));
+  int e = 0;
+  if (amax > 0.f) {
+    frexpf(amax, &e);  // amax in [2^(e-1), 2^e)
+    e -= 1;
+  }
+  const float up = ldexpf(1.f, 21 - e);
+  const size_t plane = (size_t)M * K;
+  uint32_t* d0p = reinterpret_cast<uint32_t*>(D + (size_t)m * K);
+  uint32_t* d1p = reinterpret_cast<uint32_t*>(D + plane + (size_t)m * K);
+  uint32_t* d2p = reinterpret_cast<uint32_t*>(D + 2 * plane + (size_t)m * K);
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    const uint32_t u = lane + 64 * i;
+    if (u >= units) continue;
+    const float vals[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+    uint32_t w0 = 0, w1 = 0, w2 = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int X0 = (int)rintf(vals[c] * up);  // |X0| < 2^22
+      const int d0 = ((X0 + 128) & 255) - 128;
+      const int X1 = (X0 - d0) >> 8;
+      const int d1 = ((X1 + 128) & 255) - 128;
+      const int d2 = (X1 - d1) >> 8;
+      w0 |= (uint32_t)(d0 & 255) << (8 * c);
+      w1 |= (uint32_t)(d1 & 255) << (8 * c);
+      w2 |= (uint32_t)(d2 & 255) << (8 * c);
+    }
+    d0p[u] = w0;
+    d1p[u] = w1;
+    d2p[u] = w2;
+  }
+  if (lane == 0) fm[m] = ldexpf(1.f, e - 21);
+}
+
 // Decode-shaped product (M <= 64 rows per launch, 16 x 64 output tiles) that
 // digitizes its own activations: workgroup (n tile, m tile, z) reads the fp32
 // rows of its CPW 16 x 256 k chunks [CPW z, CPW z + CPW) (and, with NORM, the
@@ -496,6 +580,25 @@ GemmFn pick(uint32_t ms, uint32_t ns, bool pf) {
 hipError_t nd_launch_digitize(const float* x, uint32_t ldx, const float* norm, float* norm_out,
                               int8_t* digits, float* fm, uint32_t M, uint32_t K, hipStream_t s) {
   if (M == 0) return hipSuccess;
+  // One wave per row when rows are 16-byte aligned float4 runs (every caller
+  // here); the workgroup-per-row kernel otherwise.
+  const bool rows4 = K % 4 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                     (!norm || (reinterpret_cast<uintptr_t>(norm) & 15) == 0) &&
+                     (!norm_out || (reinterpret_cast<uintptr_t>(norm_out) & 15) == 0) &&
+                     (reinterpret_cast<uintptr_t>(digits) & 3) == 0 && K <= 2048;
+  if (rows4) {
+    const dim3 grid((M + 3) / 4);
+    if (K <= 512)
+      hipLaunchKernelGGL(digitize_rows_kernel<2>, grid, dim3(256), 0, s, x, ldx, norm, norm_out,
+                         digits, fm, M, K);
+    else if (K <= 1024)
+      hipLaunchKernelGGL(digitize_rows_kernel<4>, grid, dim3(256), 0, s, x, ldx, norm, norm_out,
+                         digits, fm, M, K);
+    else
+      hipLaunchKernelGGL(digitize_rows_kernel<8>, grid, dim3(256), 0, s, x, ldx, norm, norm_out,
+                         digits, fm, M, K);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(digitize_kernel, dim3(M), dim3(256), 0, s, x, ldx, norm, norm_out, digits, fm,
                      M, K);
   return hipGetLastError();
