@@ -616,8 +616,12 @@ hipError_t nd_launch_gemm(const nd_mat* w, const int8_t* digits, const float* fm
                           uint32_t ldy, uint32_t M, int epilogue, hipStream_t s,
                           const nd_gemm_split* split) {
   if (M == 0) return hipSuccess;
-  uint32_t ms = M > 64 ? 2 : 1;
-  uint32_t ns = w->n >= 8192 && M <= 64 ? 2 : 1;
+  // A wide product at decode M (the 32768-row lm head of a 64-row batch)
+  // takes 32 x 128 tiles: 16.1 us with digitize, against 21.2 for 16 x 128
+  // tiles with the k prefetch.
+  const bool wide = w->n >= 8192 && M <= 64;
+  uint32_t ms = M > 64 || wide ? 2 : 1;
+  uint32_t ns = wide ? 2 : 1;
   // 32 x 64 tiles only while they still give 256 workgroups (a 128-row
   // prompt through a 1536 x 512 projection would get 96); below that the
   // 16 x 64 tiles spread the product over more CUs.
