@@ -81,6 +81,24 @@ __device__ Best block_best(Best b, float* redv, uint32_t* redo) {
   return r;
 }
 
+// One term e^x, x = logit - max <= 0, of the float64 log-softmax sum: the
+// float64 exp while x >= -20, the f32 exp below.  The leading term is 1, so
+// the terms below e^-20 = 2.1e-9 together hold at most vocab * 2.1e-9 of the
+// sum, and f32's relative error (< 2.4e-7, with the rounding of x to f32)
+// moves the sum by at most vocab * 5e-16 -- 1.6e-11 at a 32768 vocabulary,
+// far below the float64 log's own use of the sum.  The float64 exp runs only
+// while some lane of the wave holds such a term, so a row whose logits
+// spread over tens of units (most of the vocabulary below max - 20) costs
+// the f32 exp per term.
+__device__ __forceinline__ double exp_term(float v, double md) {
+  const double x = (double)v - md;
+  double e = (double)__expf((float)x);
+  if (__any(x >= -20.0)) {
+    if (x >= -20.0) e = exp(x);
+  }
+  return e;
+}
+
 // Full-vocabulary max and sum of exp(logit - max), float64 accumulation.
 // The first kCache values of each thread (ids t + blockDim.x c) are loaded
 // together and kept in registers for the sum; larger vocabularies stream
@@ -103,10 +121,12 @@ __device__ void log_normalizer(const float* __restrict__ logits, uint32_t vocab,
   double sum = 0.0;
   const double md = (double)mx;
 #pragma unroll
-  for (int c = 0; c < kCache; ++c)
-    if (threadIdx.x + c * blockDim.x < vocab) sum += exp((double)v[c] - md);
+  for (int c = 0; c < kCache; ++c) {
+    const double e = exp_term(v[c], md);
+    if (threadIdx.x + c * blockDim.x < vocab) sum += e;
+  }
   for (uint32_t i = threadIdx.x + kCache * blockDim.x; i < vocab; i += blockDim.x)
-    sum += exp((double)logits[i] - md);
+    sum += exp_term(logits[i], md);
   sum = block_sum_d(sum, redd);
   *out_max = mx;
   *out_sum = sum;
@@ -265,10 +285,13 @@ __global__ __launch_bounds__(kSelectThreads) void select_mask_reg_kernel(
 #pragma unroll
   for (int i = 1; i < 16; ++i) mx = js_maxf(mx, s_mx[i]);
   double sum = 0.0;
-  if (mine) {
+  {
     const double md = (double)mx;
 #pragma unroll
-    for (int j = 0; j < 32; ++j) sum += exp((double)v[j] - md);
+    for (int j = 0; j < 32; ++j) {
+      const double e = exp_term(mine ? v[j] : -INFINITY, md);
+      if (mine) sum += e;
+    }
   }
   for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
   if (lane == 0) s_sum[w] = sum;
