@@ -183,8 +183,8 @@ __device__ __forceinline__ float gate_factor(float g) { return 1.f / (1.f + __ex
 // row r is query z0 + r / G (z0 = (REP / G) blockIdx.z, rows at or past
 // `qrows` absent), head G blockIdx.y + r % G, with its own causal limit --
 // so every K/V tile is read once for all of them.
-template <int REP, bool F32, bool QB = false>
-__global__ __launch_bounds__(256) void attention_kernel(
+template <int REP, bool F32, bool QB = false, int KW = 4>
+__global__ __launch_bounds__(64 * KW) void attention_kernel(
     const void* __restrict__ Kc, const void* __restrict__ Vc, const float* __restrict__ Ks,
     const float* __restrict__ Vs, const float* __restrict__ Q, float* __restrict__ out,
     const float* __restrict__ gate, uint32_t gate_ld, float* __restrict__ part_acc,
@@ -275,8 +275,8 @@ __global__ __launch_bounds__(256) void attention_kernel(
   Tile<F32> cur, nxt;
   uint32_t t0 = c_begin + wave * kWavePositions;
   if (t0 < c_end) load_tile<F32>(cur, Kc, Vc, Ks, Vs, head_base, vis, t0, c_end, trow, quad, sink, window);
-  for (; t0 < c_end; t0 += kWaves * kWavePositions) {
-    const uint32_t tn = t0 + kWaves * kWavePositions;
+  for (; t0 < c_end; t0 += (uint32_t)KW * kWavePositions) {
+    const uint32_t tn = t0 + (uint32_t)KW * kWavePositions;
     if (tn < c_end) load_tile<F32>(nxt, Kc, Vc, Ks, Vs, head_base, vis, tn, c_end, trow, quad, sink, window);
     bool valid[4];
 #pragma unroll
@@ -348,8 +348,8 @@ __global__ __launch_bounds__(256) void attention_kernel(
   // (lane bits 2..3) with DPP, leaving 4 row groups (lane bits 4..5) that go
   // to LDS; l is the same in the 4 lanes of a quad and m in the whole wave.
   constexpr int kOut = REP * kHeadDim;  // outputs (head, dim) of the workgroup
-  __shared__ float s_m[kWaves][REP], s_l[kWaves][REP];
-  __shared__ float s_part[kWaves * 4][kOut];
+  __shared__ float s_m[(uint32_t)KW][REP], s_l[(uint32_t)KW][REP];
+  __shared__ float s_part[(uint32_t)KW * 4][kOut];
 #pragma unroll
   for (int h = 0; h < REP; ++h) {
     const float lw = nd::wave_sum(quad == 0 ? l[h] : 0.f);
@@ -372,12 +372,12 @@ __global__ __launch_bounds__(256) void attention_kernel(
   __syncthreads();
 
   // Combine the waves: kT consecutive threads share output o (REP <= 2), each
-  // summing kWaves * 4 / kT rows scaled by exp(m_wave - max); REP >= 4 gives
+  // summing KW * 4 / kT rows scaled by exp(m_wave - max); REP >= 4 gives
   // every thread kPer whole outputs.
-  constexpr int kThreads = 64 * kWaves;
+  constexpr int kThreads = 64 * KW;
   constexpr int kT = kOut >= kThreads ? 1 : kThreads / kOut;
   constexpr int kPer = kOut >= kThreads ? kOut / kThreads : 1;
-  constexpr int kRows = kWaves * 4 / kT;
+  constexpr int kRows = KW * 4 / kT;
   const uint32_t part = threadIdx.x % kT;
   float w_m[kPer], w_l[kPer], w_a[kPer];
   uint32_t w_o[kPer];
@@ -387,10 +387,10 @@ __global__ __launch_bounds__(256) void attention_kernel(
     const uint32_t h = o / kHeadDim;
     float mx = -INFINITY;
 #pragma unroll
-    for (uint32_t w = 0; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][h]);
+    for (uint32_t w = 0; w < (uint32_t)KW; ++w) mx = fmaxf(mx, s_m[w][h]);
     float L = 0.f;
 #pragma unroll
-    for (uint32_t w = 0; w < kWaves; ++w)
+    for (uint32_t w = 0; w < (uint32_t)KW; ++w)
       L = fmaf((s_m[w][h] == -INFINITY) ? 0.f : __expf(s_m[w][h] - mx), s_l[w][h], L);
     float A = 0.f;
 #pragma unroll
@@ -400,8 +400,10 @@ __global__ __launch_bounds__(256) void attention_kernel(
 #pragma unroll
       for (int g = 0; g < 4; ++g) A = fmaf(fw, s_part[w * 4 + g][o], A);
     }
-    if constexpr (kT == 4) A = nd::quad_sum(A);
-    if constexpr (kT == 2) A += nd::lane_xor<1>(A);
+    static_assert(kT <= 8, "at most 8 threads share an output");
+    if constexpr (kT >= 2) A += nd::lane_xor<1>(A);
+    if constexpr (kT >= 4) A += nd::lane_xor<2>(A);
+    if constexpr (kT >= 8) A += nd::lane_xor<4>(A);
     w_m[u] = mx;
     w_l[u] = L;
     w_a[u] = A;
@@ -486,19 +488,19 @@ __global__ __launch_bounds__(256) void attention_kernel(
   if (!s_last) return;
 
   // Last chunk: wave w merges head w / kWph over chunks c = w % kWph + kWph j
-  // (REP < kWaves) or heads w, w + kWaves, ... over all chunks.  Lane c holds
+  // (REP < KW) or heads w, w + KW, ... over all chunks.  Lane c holds
   // chunk c's (max, sum) (nchunks <= 64, see chunk_positions_for); lane d
   // accumulates dim d.  The first batch of acc loads is issued together
   // with the (max, sum) loads, so one round trip serves the common case.
-  constexpr int kWph = REP >= (int)kWaves ? 1 : kWaves / REP;
-  constexpr int kHpw = REP > (int)kWaves ? REP / kWaves : 1;
+  constexpr int kWph = REP >= KW ? 1 : KW / REP;
+  constexpr int kHpw = REP > KW ? REP / KW : 1;
   constexpr int kBatch = 16;
-  __shared__ float s_fin[kWaves][kHeadDim];
+  __shared__ float s_fin[(uint32_t)KW][kHeadDim];
   const uint32_t wpart = wave % kWph;
   float fin_l = 0.f;
 #pragma unroll
   for (int hh = 0; hh < kHpw; ++hh) {
-    const uint32_t h = kWph > 1 ? wave / kWph : wave + hh * kWaves;
+    const uint32_t h = kWph > 1 ? wave / kWph : wave + hh * (uint32_t)KW;
     const size_t base = (row0 + h) * max_chunks;
     const uint32_t cl = lane < nchunks ? lane : nchunks - 1;
     float mc = __hip_atomic_load(part_ml + (base + cl) * 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
