@@ -549,6 +549,125 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
   }
 }
 
+// Prompt-sized product with the activations stationary (M >= 1024, K <=
+// 512 with K % 128 == 0, N % 128 == 0): workgroup (column group g, row tile m) copies the
+// three digit planes of its 64 rows over all of K into LDS once (LDS DMA,
+// global_load_lds_dwordx4, no registers) and then streams 128-column weight
+// strips through them.  Every weight strip is read by the M / 64 row tiles
+// and every digit plane by the N / NG column groups, against one read of
+// each per 32 x 64 tile pair for the tiled kernel above -- about a quarter
+// of its L2 traffic at 2048 x 2048 x 512.  8 waves in two groups take the
+// strips alternately (group h: strips h, h + 2, ...), so one group's weight
+// loads overlap the other's products; wave w % 4 of a group takes the
+// strip's columns [32 (w % 4), +32).  The integer sums are exact and the
+// epilogue is the tiled kernel's, so both give the same bits.
+//
+// LDS layout: 16-byte units, plane j, row r, unit slot p (K / 16 per row);
+// slot p holds k-unit p ^ (r & 7), which spreads a wave's reads of one
+// k-unit over 16 rows across the banks.
+constexpr uint32_t kAsRows = 64, kAsMaxK = 512, kAsStrip = 128;
+template <int EPI>
+__global__ __launch_bounds__(512) void gemm_i8_astat_kernel(
+    const int8_t* __restrict__ W, const float* __restrict__ sw, const int8_t* __restrict__ D,
+    const float* __restrict__ fm, float* __restrict__ Y, uint32_t M, uint32_t N, uint32_t K,
+    uint32_t ldy, uint32_t group_cols) {
+  __shared__ __attribute__((aligned(16))) int8_t lds[3 * kAsRows * kAsMaxK];
+  const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const uint32_t half = wave >> 2, wq = wave & 3;
+  const uint32_t m0 = blockIdx.y * kAsRows;
+  const uint32_t c0 = blockIdx.x * group_cols;
+  const uint32_t U = K / 16;  // units per row
+  const size_t plane = (size_t)M * K;
+
+  // Stage the tile: 3 * 64 * U units in chunks of 64 (one wave load each).
+  {
+    const uint32_t chunks = 3 * kAsRows * U / 64;
+    for (uint32_t c = wave; c < chunks; c += 8) {
+      const uint32_t L = c * 64 + lane;
+      const uint32_t j = L / (kAsRows * U), r = (L / U) % kAsRows, pslot = L % U;
+      const uint32_t u = pslot ^ (r & 7);
+      const uint32_t row = m0 + r < M ? m0 + r : M - 1;  // rows past M feed only rows past M
+      __builtin_amdgcn_global_load_lds(D + j * plane + (size_t)row * K + u * 16,
+                                       (__attribute__((address_space(3))) void*)(lds + c * 1024),
+                                       16, 0, 0);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  const uint32_t lrow = lane & 15, lk = lane >> 4;
+  const uint32_t steps = K / 64;
+  for (uint32_t s0 = half * kAsStrip; s0 < group_cols; s0 += 2 * kAsStrip) {
+    const uint32_t nb = c0 + s0 + 32 * wq;  // this wave's 32 columns
+    // The strip's weights for both 16-column tiles and every k step.
+    v4i wa[kAsMaxK / 64][2];
+#pragma unroll
+    for (int q = 0; q < (int)(kAsMaxK / 64); ++q)
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const uint32_t n = nb + 16 * a + lrow;
+        const uint32_t qs = (uint32_t)q < steps ? q : 0;
+        wa[q][a] = *reinterpret_cast<const v4i*>(W + (size_t)(n < N ? n : N - 1) * K + qs * 64 +
+                                                 lk * 16);
+      }
+    v4i acc[2][4][3];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int j = 0; j < 3; ++j) acc[a][b][j] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int q = 0; q < (int)(kAsMaxK / 64); ++q) {
+      if ((uint32_t)q >= steps) break;
+      const uint32_t u = 4 * q + lk;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t r = 16 * b + lrow;
+        const uint32_t pslot = u ^ (r & 7);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          const v4i db = *reinterpret_cast<const v4i*>(
+              &lds[((j * kAsRows + r) * U + pslot) * 16]);
+#pragma unroll
+          for (int a = 0; a < 2; ++a)
+            acc[a][b][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[q][a], db, acc[a][b][j], 0, 0, 0);
+        }
+      }
+    }
+    // Output (a, b, i) of lane l: n = nb + 16 a + 4 (l / 16) + i, m = m0 + 16 b + l % 16.
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const uint32_t n = nb + 16 * a + 4 * lk;
+      if (n >= N) continue;
+      const float4 s4 = *reinterpret_cast<const float4*>(sw + n);
+      const float swv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t m = m0 + 16 * b + lrow;
+        if (m >= M) continue;
+        const float f = fm[m];
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float c = (float)acc[a][b][0][i] + 256.f * (float)acc[a][b][1][i] +
+                          65536.f * (float)acc[a][b][2][i];
+          v[i] = swv[i] * (f * c);
+        }
+        float4* dst = reinterpret_cast<float4*>(Y + (size_t)m * ldy + n);
+        if constexpr (EPI == 1) {
+          const float4 o = *dst;
+          *dst = make_float4(o.x + v[0], o.y + v[1], o.z + v[2], o.w + v[3]);
+        } else if constexpr (EPI == 2) {
+          *dst = make_float4(silu_f(v[0]), silu_f(v[1]), silu_f(v[2]), silu_f(v[3]));
+        } else {
+          *dst = make_float4(v[0], v[1], v[2], v[3]);
+        }
+      }
+    }
+  }
+}
+
 using F32aFn = void (*)(const int8_t*, const float*, const float*, uint32_t, const float*, float*,
                         uint32_t, uint32_t, uint32_t, uint32_t, float*, uint32_t*);
 
@@ -616,6 +735,28 @@ hipError_t nd_launch_gemm(const nd_mat* w, const int8_t* digits, const float* fm
                           uint32_t ldy, uint32_t M, int epilogue, hipStream_t s,
                           const nd_gemm_split* split) {
   if (M == 0) return hipSuccess;
+  // Prompt-sized M with K <= 512: the activation tile stays in LDS.  Column
+  // groups of whole 128-column strips, as many as give the row tiles 256
+  // workgroups (or fewer when N has fewer strips).
+  if (M >= 1024 && w->k <= kAsMaxK && w->k % 128 == 0 && w->n % kAsStrip == 0 && ldy % 4 == 0 &&
+      (reinterpret_cast<uintptr_t>(y) & 15) == 0 && (reinterpret_cast<uintptr_t>(digits) & 15) == 0) {
+    const uint32_t mt = (M + kAsRows - 1) / kAsRows, strips = w->n / kAsStrip;
+    uint32_t groups = (256 + mt - 1) / mt;
+    if (groups > strips) groups = strips;
+    while (strips % groups) --groups;
+    const uint32_t gc = (strips / groups) * kAsStrip;
+    const dim3 grid(groups, mt);
+    if (epilogue == 0)
+      hipLaunchKernelGGL(gemm_i8_astat_kernel<0>, grid, dim3(512), 0, s, w->w, w->scales, digits,
+                         fm, y, M, w->n, w->k, ldy, gc);
+    else if (epilogue == 1)
+      hipLaunchKernelGGL(gemm_i8_astat_kernel<1>, grid, dim3(512), 0, s, w->w, w->scales, digits,
+                         fm, y, M, w->n, w->k, ldy, gc);
+    else
+      hipLaunchKernelGGL(gemm_i8_astat_kernel<2>, grid, dim3(512), 0, s, w->w, w->scales, digits,
+                         fm, y, M, w->n, w->k, ldy, gc);
+    return hipGetLastError();
+  }
   // A wide product at decode M (the 32768-row lm head of a 64-row batch)
   // takes 32 x 128 tiles: 16.1 us with digitize, against 21.2 for 16 x 128
   // tiles with the k prefetch.
