@@ -549,8 +549,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
   }
 }
 
-// Prompt-sized product with the activations stationary (M >= 1024, K <=
-// 512 with K % 128 == 0, N % 128 == 0): workgroup (column group g, row tile m) copies the
+// Prompt-sized product with the activations stationary (M >= 1024, K in
+// {128, 256, 512}, N % 128 == 0): workgroup (column group g, row tile m) copies the
 // three digit planes of its 64 rows over all of K into LDS once (LDS DMA,
 // global_load_lds_dwordx4, no registers) and then streams 128-column weight
 // strips through them.  Every weight strip is read by the M / 64 row tiles
@@ -562,10 +562,16 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
 // strip's columns [32 (w % 4), +32).  The integer sums are exact and the
 // epilogue is the tiled kernel's, so both give the same bits.
 //
-// LDS layout: 16-byte units, plane j, row r, unit slot p (K / 16 per row);
-// slot p holds k-unit p ^ (r & 7), which spreads a wave's reads of one
-// k-unit over 16 rows across the banks.
+// LDS layout: 16-byte units, plane j, row r, unit slot p (U = K / 16 per
+// row); slot p holds k-unit p ^ (4 (r % 4) & (U - 1)).  A wave's 16-byte
+// read takes k-units 4 q + (l / 16) of rows 16 b + l % 16: the rows' four
+// residues mod 4 move those units to four different 64-byte bank groups, so
+// the 64 lanes fall on all 16 groups of the 64 banks, four lanes each (the
+// minimum of four passes for 1 KiB).
 constexpr uint32_t kAsRows = 64, kAsMaxK = 512, kAsStrip = 128;
+__device__ __forceinline__ uint32_t as_slot(uint32_t u, uint32_t r, uint32_t U) {
+  return u ^ ((4u * (r & 3u)) & (U - 1u));
+}
 template <int EPI>
 __global__ __launch_bounds__(512) void gemm_i8_astat_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ sw, const int8_t* __restrict__ D,
@@ -585,7 +591,7 @@ __global__ __launch_bounds__(512) void gemm_i8_astat_kernel(
     for (uint32_t c = wave; c < chunks; c += 8) {
       const uint32_t L = c * 64 + lane;
       const uint32_t j = L / (kAsRows * U), r = (L / U) % kAsRows, pslot = L % U;
-      const uint32_t u = pslot ^ (r & 7);
+      const uint32_t u = as_slot(pslot, r, U);  // the slot map is its own inverse
       const uint32_t row = m0 + r < M ? m0 + r : M - 1;  // rows past M feed only rows past M
       __builtin_amdgcn_global_load_lds(D + j * plane + (size_t)row * K + u * 16,
                                        (__attribute__((address_space(3))) void*)(lds + c * 1024),
@@ -624,7 +630,7 @@ __global__ __launch_bounds__(512) void gemm_i8_astat_kernel(
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const uint32_t r = 16 * b + lrow;
-        const uint32_t pslot = u ^ (r & 7);
+        const uint32_t pslot = as_slot(u, r, U);
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
           const v4i db = *reinterpret_cast<const v4i*>(
@@ -738,7 +744,8 @@ hipError_t nd_launch_gemm(const nd_mat* w, const int8_t* digits, const float* fm
   // Prompt-sized M with K <= 512: the activation tile stays in LDS.  Column
   // groups of whole 128-column strips, as many as give the row tiles 256
   // workgroups (or fewer when N has fewer strips).
-  if (M >= 1024 && w->k <= kAsMaxK && w->k % 128 == 0 && w->n % kAsStrip == 0 && ldy % 4 == 0 &&
+  if (M >= 1024 && (w->k == 128 || w->k == 256 || w->k == 512) && w->n % kAsStrip == 0 &&
+      ldy % 4 == 0 &&
       (reinterpret_cast<uintptr_t>(y) & 15) == 0 && (reinterpret_cast<uintptr_t>(digits) & 15) == 0) {
     const uint32_t mt = (M + kAsRows - 1) / kAsRows, strips = w->n / kAsStrip;
     uint32_t groups = (256 + mt - 1) / mt;
