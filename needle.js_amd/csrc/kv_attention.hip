@@ -107,17 +107,39 @@ struct Tile {
   float ks[4], vs[4];
 };
 
+// Cache slot of visible index t without branches: slot = t below the prefix,
+// else r0 + wrap(b0 + t - prefix), wrap(x) = x >= w ? x - w : x.  A sliding
+// window (kv_slot) gives r0 = sink, b0 = (recent_low - sink) % window, w =
+// window -- the recent indices span fewer than `window` positions, so one
+// subtraction wraps them -- and no window r0 = recent_low, b0 = 0, w = 2^32 - 1.
+struct Ring {
+  uint32_t r0, b0, w;
+};
+
+__device__ __forceinline__ Ring ring_of(const Visible& vis, uint32_t sink, uint32_t window) {
+  if (window == 0 || vis.recent_low < sink) return Ring{vis.recent_low, 0u, 0xffffffffu};
+  return Ring{sink, (vis.recent_low - sink) % window, window};
+}
+
+__device__ __forceinline__ uint32_t ring_slot(const Visible& vis, const Ring& ring, uint32_t t) {
+  const uint32_t x = ring.b0 + (t - vis.prefix);
+  return t < vis.prefix ? t : ring.r0 + (x >= ring.w ? x - ring.w : x);
+}
+
 template <bool F32>
 __device__ __forceinline__ void load_tile(Tile<F32>& tl, const void* Kc, const void* Vc,
                                           const float* Ks, const float* Vs, size_t head_base,
-                                          const Visible& vis, uint32_t t0, uint32_t t_end,
-                                          uint32_t trow, uint32_t quad, uint32_t sink,
-                                          uint32_t window) {
+                                          const Visible& vis, const Ring& ring, uint32_t t0,
+                                          uint32_t t_end, uint32_t trow, uint32_t quad) {
+  uint32_t slots[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const uint32_t t = t0 + trow + 16 * k;
-    const uint32_t slot = kv_slot(logical_at(vis, t < t_end ? t : t0), sink, window);
-    const size_t row = head_base + slot;
+    slots[k] = ring_slot(vis, ring, t < t_end ? t : t0);
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const size_t row = head_base + slots[k];
     tl.ks[k] = Ks[row];
     tl.vs[k] = Vs[row];
     if constexpr (F32) {
@@ -183,7 +205,7 @@ __device__ __forceinline__ float gate_factor(float g) { return 1.f / (1.f + __ex
 // row r is query z0 + r / G (z0 = (REP / G) blockIdx.z, rows at or past
 // `qrows` absent), head G blockIdx.y + r % G, with its own causal limit --
 // so every K/V tile is read once for all of them.
-template <int REP, bool F32, bool QB = false, int KW = 4>
+template <int REP, bool F32, bool QB = false, int KW = 4, int TILES = 0>
 __global__ __launch_bounds__(64 * KW) void attention_kernel(
     const void* __restrict__ Kc, const void* __restrict__ Vc, const float* __restrict__ Ks,
     const float* __restrict__ Vs, const float* __restrict__ Q, float* __restrict__ out,
@@ -201,7 +223,9 @@ __global__ __launch_bounds__(64 * KW) void attention_kernel(
   const uint32_t chunk = blockIdx.x, kvh_local = blockIdx.y, z = blockIdx.z;
   const uint32_t kvh = z * kv_stride_z + kvh_local;
   const uint32_t hq = seq_kv_heads * REP;
-  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // The wave index is uniform: read it into a scalar register so that the
+  // tile loop below is scalar control flow.
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const uint32_t quad = lane & 3, trow = lane >> 2;
   // slot_space (one row, position in device memory): walk the cache slots
   // [0, alloc) in slot order -- vis = {alloc, alloc, alloc} makes logical
@@ -272,12 +296,13 @@ __global__ __launch_bounds__(64 * KW) void attention_kernel(
     for (int i = 0; i < 16; ++i) acc[h][i] = 0.f;
   }
 
-  Tile<F32> cur, nxt;
-  uint32_t t0 = c_begin + wave * kWavePositions;
-  if (t0 < c_end) load_tile<F32>(cur, Kc, Vc, Ks, Vs, head_base, vis, t0, c_end, trow, quad, sink, window);
-  for (; t0 < c_end; t0 += (uint32_t)KW * kWavePositions) {
-    const uint32_t tn = t0 + (uint32_t)KW * kWavePositions;
-    if (tn < c_end) load_tile<F32>(nxt, Kc, Vc, Ks, Vs, head_base, vis, tn, c_end, trow, quad, sink, window);
+  // The tile loads are issued under uniform control flow with a static count
+  // of outstanding loads, and no loaded tile is carried from one loop
+  // iteration to the next, so that the wait before a tile's math covers that
+  // tile only.  (A load under a per-lane condition, or a prefetched tile
+  // copied or carried into the next iteration, makes the compiler wait for
+  // every outstanding load: one memory round trip per tile.)
+  auto tile_math = [&](const Tile<F32>& cur, uint32_t t0) __attribute__((always_inline)) {
     bool valid[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -341,7 +366,33 @@ __global__ __launch_bounds__(64 * KW) void attention_kernel(
         }
       }
     }
-    cur = nxt;
+  };
+  constexpr uint32_t kStride = (uint32_t)KW * kWavePositions;
+  const Ring ring = ring_of(vis, sink, window);
+  const uint32_t t_first = c_begin + wave * kWavePositions;
+  // Tiles t_first + kStride j, j < n (n uniform), two per round: both tiles'
+  // loads are in flight before the first tile's math.  TILES = 1 or 2: the
+  // launch guarantees n <= TILES, and the code is straight-line.
+  if (t_first < c_end) {
+    Tile<F32> ta, tb;
+    if constexpr (TILES == 1) {
+      load_tile<F32>(ta, Kc, Vc, Ks, Vs, head_base, vis, ring, t_first, c_end, trow, quad);
+      tile_math(ta, t_first);
+    } else {
+      const uint32_t n = TILES == 2 ? 2u : (c_end - t_first + kStride - 1) / kStride;
+      for (uint32_t j = 0; j < n; j += 2) {
+        // Past the chunk end the second tile rereads the first one's rows and
+        // its math masks every position (it adds nothing); its math is not
+        // skipped, so that the compiler cannot sink its loads behind a branch.
+        const uint32_t t_a = t_first + j * kStride, t_b = t_a + kStride;
+        load_tile<F32>(ta, Kc, Vc, Ks, Vs, head_base, vis, ring, t_a, c_end, trow, quad);
+        load_tile<F32>(tb, Kc, Vc, Ks, Vs, head_base, vis, ring, t_b < c_end ? t_b : t_a, c_end,
+                       trow, quad);
+        __builtin_amdgcn_sched_barrier(0);  // every load issued before the math
+        tile_math(ta, t_a);
+        tile_math(tb, t_b);
+      }
+    }
   }
 
   // Per wave: fold the 16 token rows of each lane's partial sums 4 apart
@@ -560,10 +611,12 @@ __global__ __launch_bounds__(64 * KW) void attention_kernel(
 // Positions per chunk: the whole visible range when the (row, kv head) pairs
 // alone give `target` workgroups, else split so that they do; at least one
 // tile per wave.  Splitting costs a publish + count + merge round trip at the
-// end, so a single query row aims at 256 workgroups (32 chunks of 256 per
-// head at 8 heads x 8192, elected in groups of 8: 8.1 us per call, vs 8.9 at
-// 128 workgroups) and batches at 4096 (64 sequences x 8 heads at contexts up
-// to 2048: 0.635 ms per decode step, vs 0.698 at 1024 and 0.638 at 2048).
+// end, yet more, smaller workgroups win: a single query row aims at 256
+// workgroups (32 chunks of 256 per head at 8 heads x 8192, elected in groups
+// of 8: 7.95 us per call, vs 8.9 at 128 workgroups and 10.4 at 64) and
+// batches at 4096 (64 sequences x 8 heads at contexts up to 2048: 0.467 ms
+// per decode step, vs 0.491 at 2048 and 0.527 at 1024).  One tile per wave
+// also runs the leanest kernel form (73 VGPRs: 6 waves per SIMD).
 constexpr uint32_t kTargetSingle = 256, kTargetBatch = 4096;
 constexpr uint32_t kMaxChunks = 64;  // the merge holds one chunk per lane
 static_assert(1 + kMaxChunks / kChunkGroup <= kAttnCounterStride, "group counters fit the stride");
@@ -946,7 +999,12 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
   const uint32_t hq = a.seq_kv_heads * REP;
   float* part_acc = a.partials;
   float* part_ml = a.partials + (size_t)a.batch * hq * max_chunks * kHeadDim;
-  hipLaunchKernelGGL((attention_kernel<REP, F32>), dim3(max_chunks, a.seq_kv_heads, a.batch),
+  // Tiles per wave: cp / kMinChunk (cp is a multiple of it).
+  const uint32_t tiles = cp / kMinChunk;
+  auto kernel = tiles == 1   ? attention_kernel<REP, F32, false, kWaves, 1>
+                : tiles == 2 ? attention_kernel<REP, F32, false, kWaves, 2>
+                             : attention_kernel<REP, F32, false, kWaves, 0>;
+  hipLaunchKernelGGL(kernel, dim3(max_chunks, a.seq_kv_heads, a.batch),
                      dim3(64 * kWaves), 0, s, a.kv->k, a.kv->v, a.kv->ks, a.kv->vs, a.q, a.out,
                      a.gate, a.gate_ld, part_acc, part_ml, a.counters, a.layer, a.kv->kv_heads, a.kv->alloc,
                      a.kv->sink, a.kv->window, a.vis, a.positions, a.slot_space, a.seq_kv_heads,

@@ -254,6 +254,28 @@ def test_attention_split_chunks_every_head_ratio(hip, hkv, hq, sink, window):
     kv.free()
 
 
+
+@pytest.mark.parametrize("hq,sink,window,mode", [(8, 0, 0, "int8"), (1, 5, 40000, "int8"),
+                                                 (2, 0, 0, "float32")])
+def test_attention_long_context_several_tiles_per_wave(hip, hq, sink, window, mode):
+    """One KV head at 50000 positions: 64 chunks of 1024 positions, so that each
+    wave walks several 64-position tiles two at a time -- with an odd count in
+    the last chunk (one tile of the last pair masked whole) and, with a
+    window, the ring wrapping inside a chunk."""
+    say("attention long", hq, sink, window, mode)
+    n = 50000
+    kv = HipKvCache(hip, 1, 1, max_length=n, sink=sink, window=window, kv_cache=mode)
+    ref = oracle.KvCache(1, 1, max_length=n, sink=sink, window=window, kv_cache=mode)
+    s = synth.Stream(77, f"long{hq}{sink}{window}{mode}")
+    K, V = s.normal((n, 1, 64)), s.normal((n, 1, 64))
+    kv.store(0, 0, K, V)
+    ref.store(0, 0, K, V)
+    for pos in (n - 1, 33000, 40100):
+        q = s.normal((hq * 64,))
+        assert_close(kv.attention(0, pos, q), ref.attention(0, pos, q), RTOL, ATOL,
+                     f"long hq={hq} pos={pos}")
+    kv.free()
+
 # ---------------------------------------------------------------- selection
 
 @pytest.mark.parametrize("vocab", [32768, 4096, 1000])
