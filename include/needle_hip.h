@@ -246,7 +246,8 @@ nd_status nd_select(nd_ctx* ctx, const float* logits, uint32_t vocab, const uint
  * id>>5; NULL = unconstrained).  The bitmask is the ascending allowed list
  * that Needle.complete builds (tools/agent.ts:164-183).  Writes ids[batch]
  * and log_probabilities[batch] in HBM; a row whose mask is empty gets id
- * 0xFFFFFFFF and log-probability NaN. */
+ * 0xFFFFFFFF and log-probability NaN.  Calls on one context share its
+ * selection workspace: calls on different streams must not overlap. */
 nd_status nd_select_mask_d(nd_ctx* ctx, const float* logits_dev, uint32_t batch, uint32_t vocab,
                            const uint32_t* mask_dev, uint32_t* ids_dev,
                            double* log_probabilities_dev, void* stream);

@@ -157,6 +157,7 @@ nd_status nd_destroy(nd_ctx* ctx) {
   if (ctx->attn_partials) hipFree(ctx->attn_partials);
   if (ctx->attn_counters) hipFree(ctx->attn_counters);
   if (ctx->mm_scratch) hipFree(ctx->mm_scratch);
+  if (ctx->sel_split) hipFree(ctx->sel_split);
   if (ctx->mv_split) hipFree(ctx->mv_split);
   if (ctx->cq_prepared) hipFree(ctx->cq_prepared);
   hipStreamDestroy(ctx->stream);
@@ -801,8 +802,22 @@ nd_status nd_select_mask_d(nd_ctx* ctx, const float* logits, uint32_t batch, uin
   if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
   if (batch && (!logits || !ids || !logprobs || vocab == 0))
     return nd_fail(ctx, ND_ERR_INVALID, "nd_select_mask_d: NULL argument or empty vocabulary");
+  if (batch == 0) return ND_OK;
+  // Split-selection records and counters: grown (after every stream of the
+  // device has drained, as earlier calls may have used any) and zeroed here.
+  const size_t need = nd_select_split_bytes(batch);
+  if (ctx->sel_split_bytes < need) {
+    ND_HIP(ctx, hipDeviceSynchronize());
+    if (ctx->sel_split) ND_HIP(ctx, hipFree(ctx->sel_split));
+    ctx->sel_split = nullptr;
+    ctx->sel_split_bytes = 0;
+    ND_HIP(ctx, hipMalloc(&ctx->sel_split, need));
+    ND_HIP(ctx, hipMemset(ctx->sel_split, 0, need));
+    ND_HIP(ctx, hipDeviceSynchronize());
+    ctx->sel_split_bytes = need;
+  }
   ND_HIP(ctx, nd_launch_select_mask(logits, batch, vocab, mask, ids, logprobs,
-                                    nd_pick_stream(ctx, stream)));
+                                    nd_pick_stream(ctx, stream), ctx->sel_split));
   return ND_OK;
 }
 

@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "nd_internal.hpp"
+#include "nd_rope.hpp"
 #include "nd_wave.hpp"
 
 namespace {
@@ -65,9 +66,7 @@ __device__ __forceinline__ void qk_rope_store_item(
   const uint32_t h = is_q ? slot : slot - heads;
   const float* src = qkv + (size_t)m * ld + (is_q ? h * kHd : heads * kHd + h * kHd);
   const float* scale = is_q ? q_norm : k_norm;
-  double x = src[lane];
-  const double inv = 1.0 / sqrt(wave_sum_d(x * x) / kHd + 1e-6);
-  const float normed = (float)((1.0 + (double)scale[lane]) * x * inv);
+  const double x = src[lane];
   // Half-split RoPE: pair (j, j + 32), angle = pos * theta^(-2j/64).
   const uint32_t j = lane & 31;
   double sn, cs;
@@ -78,9 +77,7 @@ __device__ __forceinline__ void qk_rope_store_item(
   } else {
     sincos((double)pos * inv_freq[j], &sn, &cs);
   }
-  const double mine = normed;
-  const double other = __shfl_xor((double)normed, 32, 64);
-  const float rot = lane < 32 ? (float)(mine * cs - other * sn) : (float)(mine * cs + other * sn);
+  const float rot = nd::norm_rope(x, scale, lane, sn, cs);
   if (is_q) {
     q_out[((size_t)m * heads + h) * kHd + lane] = rot;
     return;
@@ -89,19 +86,9 @@ __device__ __forceinline__ void qk_rope_store_item(
   // Cache head for row m: (m * kv_head_stride + h) when rows are sequences of
   // a batch (stride = Hkv), or h when rows are consecutive positions.
   const size_t row = ((size_t)layer * cache_heads + (size_t)m * kv_head_stride + h) * alloc + pos;
-  const float kv = rot;
-  const float vv = qkv[(size_t)m * ld + (heads + kv_heads) * kHd + h * kHd + lane];
-  const float ak = wave_absmax_js(kv), av = wave_absmax_js(vv);
-  const double mk = (ak != ak) ? (double)ak : fmax(1e-12, (double)ak);
-  const double mv = (av != av) ? (double)av : fmax(1e-12, (double)av);
-  const double sk = mk / 127.0, sv = mv / 127.0;
-  const double ck = rint((double)kv / sk), cv = rint((double)vv / sv);
-  Kc[row * kHd + lane] = ck != ck ? (int8_t)0 : (int8_t)(int)ck;
-  Vc[row * kHd + lane] = cv != cv ? (int8_t)0 : (int8_t)(int)cv;
-  if (lane == 0) {
-    Ks[row] = (float)sk;
-    Vs[row] = (float)sv;
-  }
+  nd::quant_store(rot, row, lane, Kc, Ks);
+  nd::quant_store(qkv[(size_t)m * ld + (heads + kv_heads) * kHd + h * kHd + lane], row, lane, Vc,
+                  Vs);
 }
 
 // Workgroup (slot, row m): one wave.
@@ -223,6 +210,8 @@ struct nd_batch {
            *step = nullptr, *ids = nullptr, *history = nullptr;
   double *logprobs = nullptr, *lp_history = nullptr;  // history: [max_length][batch]
   nd_gemm_split gsplit{};  // split-k workspace of the step's GEMMs (zeroed counters)
+  void* sel_split = nullptr;  // split-selection records and counters (zeroed)
+  double2* rope_tab = nullptr;  // (sin, cos) of every cache position: [max_length][32]
 };
 
 // Split-k workspace of a batch: up to 512 tiles' worth of partials (16 x 64
@@ -402,7 +391,9 @@ nd_status nd_batch_create(nd_ctx* ctx, nd_decoder* dec, uint32_t batch, uint32_t
       a256((size_t)batch * 4), a256((size_t)batch * 4), a256(256),           // tokens, positions, step
       a256((size_t)batch * 4), a256((size_t)batch * 8),                      // ids, logprobs
       a256((size_t)max_length * batch * 4), a256((size_t)max_length * batch * 8),   // history
-      a256(kSplitPartialFloats * 4), a256((size_t)kSplitCounters * 4)};         // GEMM split-k
+      a256(kSplitPartialFloats * 4), a256((size_t)kSplitCounters * 4),          // GEMM split-k
+      a256(nd_select_split_bytes(batch)),                                    // selection
+      a256((size_t)max_length * 32 * sizeof(double2))};                      // rope table
   size_t total = 0;
   for (size_t v : sizes) total += v;
   hipError_t e = hipMalloc(&b->arena, total);
@@ -443,8 +434,21 @@ nd_status nd_batch_create(nd_ctx* ctx, nd_decoder* dec, uint32_t batch, uint32_t
   take(&b->lp_history);
   take(&b->gsplit.partials);
   take(&b->gsplit.counters);
+  take(&b->sel_split);
+  take(&b->rope_tab);
   b->gsplit.partial_floats = kSplitPartialFloats;
   b->gsplit.counter_count = kSplitCounters;
+  // RoPE angles of every position the cache holds, evaluated once here as
+  // the rope/store kernel evaluates them.
+  hipLaunchKernelGGL(rope_table_kernel, dim3((max_length * 32 + 255) / 256), dim3(256), 0,
+                     ctx->stream, dec->inv_freq, 0u, max_length, b->rope_tab);
+  e = hipGetLastError();
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    hipFree(b->arena);
+    delete b;
+    return nd_hip_fail(ctx, e, "batch rope table");
+  }
   *out = b;
   return ND_OK;
 }
@@ -554,16 +558,27 @@ nd_status nd_batch_step(nd_ctx* ctx, nd_batch* b, uint32_t max_position, uint32_
     return nd_launch_gemm(w, b->digits, b->fm, y, ldy, B, epi, s, &b->gsplit);
   };
   for (uint32_t l = 0; l < dec->layers; ++l) {
-    ND_HIP(ctx, product(&dec->wqkv[l], b->x, dec->norms + dec->attn_off + (size_t)l * D, b->qkv,
-                        qkv_rows, 0));
-    hipLaunchKernelGGL(qk_rope_store_kernel, dim3(dec->heads + dec->kv_heads, B), dim3(64), 0, s,
-                       b->qkv, qkv_rows, dec->heads, dec->kv_heads,
-                       dec->norms + dec->q_off + (size_t)l * kHd,
-                       dec->norms + dec->k_off + (size_t)l * kHd, dec->inv_freq, nullptr,
-                       b->positions, 0u,
-                       b->q, (int8_t*)b->kv.k, (int8_t*)b->kv.v, b->kv.ks, b->kv.vs, l,
-                       b->kv.kv_heads, b->kv.alloc, dec->kv_heads);
-    ND_HIP(ctx, hipGetLastError());
+    const float* attn_norm = dec->norms + dec->attn_off + (size_t)l * D;
+    const float* q_norm = dec->norms + dec->q_off + (size_t)l * kHd;
+    const float* k_norm = dec->norms + dec->k_off + (size_t)l * kHd;
+    if (nd_gemm_f32_fits(&dec->wqkv[l], b->x, D, true, B, &b->gsplit)) {
+      // q/k/v projection with norm, rope and the cache store in its epilogue;
+      // the last layer's projections are also kept (nd_batch_read_projections).
+      const nd::RopeStore rs{dec->heads, dec->kv_heads, q_norm, k_norm, b->rope_tab,
+                             b->positions, b->q, (int8_t*)b->kv.k, (int8_t*)b->kv.v, b->kv.ks,
+                             b->kv.vs, l, b->kv.kv_heads, b->kv.alloc, dec->kv_heads};
+      const bool keep = l + 1 == dec->layers;
+      ND_HIP(ctx, nd_launch_gemm_f32(&dec->wqkv[l], b->x, D, attn_norm, keep ? b->qkv : nullptr,
+                                     qkv_rows, B, 3, s, &b->gsplit, &rs));
+    } else {
+      ND_HIP(ctx, product(&dec->wqkv[l], b->x, attn_norm, b->qkv, qkv_rows, 0));
+      hipLaunchKernelGGL(qk_rope_store_kernel, dim3(dec->heads + dec->kv_heads, B), dim3(64), 0,
+                         s, b->qkv, qkv_rows, dec->heads, dec->kv_heads, q_norm, k_norm,
+                         dec->inv_freq, nullptr, b->positions, 0u, b->q, (int8_t*)b->kv.k,
+                         (int8_t*)b->kv.v, b->kv.ks, b->kv.vs, l, b->kv.kv_heads, b->kv.alloc,
+                         dec->kv_heads);
+      ND_HIP(ctx, hipGetLastError());
+    }
     ND_HIP(ctx, nd_launch_attention_batch(&b->kv, l, b->positions, B, dec->kv_heads,
                                           dec->kv_heads, rep, max_position, b->q, b->o,
                                           b->partials, b->counters, s));
@@ -579,11 +594,16 @@ nd_status nd_batch_step(nd_ctx* ctx, nd_batch* b, uint32_t max_position, uint32_
                        b->step, B, dec->vocab, threshold24, b->masks);
     ND_HIP(ctx, hipGetLastError());
   }
+  const nd_select_advance adv{b->tokens, b->positions, b->step, b->history, b->lp_history,
+                              b->max_length};
+  bool advanced = false;
   ND_HIP(ctx, nd_launch_select_mask(b->logits, B, dec->vocab, use_masks ? b->masks : nullptr,
-                                    b->ids, b->logprobs, s));
-  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(256), 0, s, b->ids, b->logprobs, b->tokens,
-                     b->positions, b->step, b->history, b->lp_history, b->max_length, B);
-  ND_HIP(ctx, hipGetLastError());
+                                    b->ids, b->logprobs, s, b->sel_split, &adv, &advanced));
+  if (!advanced) {
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(256), 0, s, b->ids, b->logprobs, b->tokens,
+                       b->positions, b->step, b->history, b->lp_history, b->max_length, B);
+    ND_HIP(ctx, hipGetLastError());
+  }
   return ND_OK;
 }
 

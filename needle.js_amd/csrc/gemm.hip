@@ -19,6 +19,7 @@
 // column l%16 (activation row m).  Any k order shared by both operands gives
 // the same sum, so both are read straight from row-major memory.
 #include "nd_internal.hpp"
+#include "nd_rope.hpp"
 #include "nd_wave.hpp"
 
 namespace {
@@ -368,7 +369,8 @@ template <int EPI, bool NORM, int CPW>
 __global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ sw, const float* __restrict__ X,
     uint32_t ldx, const float* __restrict__ norm, float* __restrict__ Y, uint32_t M, uint32_t N,
-    uint32_t K, uint32_t ldy, float* __restrict__ part, uint32_t* __restrict__ counters) {
+    uint32_t K, uint32_t ldy, float* __restrict__ part, uint32_t* __restrict__ counters,
+    nd::RopeStore rope) {
   __shared__ __attribute__((aligned(16))) int8_t lds[CPW][3][16][kLdsRow];
   __shared__ float s_fm[CPW][16];
   const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
@@ -411,6 +413,37 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
 #pragma unroll
       for (int q = 0; q < 4; ++q) wn[c][q] = src[q];
     }
+  }
+  // Epilogue 3's operands, loaded after the product's so that they do not
+  // delay them: wave w's rows m0 + 4 w + r (w uniform: scalar loads of the
+  // positions), the rope angles of this lane's pair and the head's norm
+  // weight.
+  uint32_t e_m[4] = {}, e_pos[4] = {};
+  bool e_live[4] = {};
+  double2 e_sc[4] = {};
+  float e_scale = 0.f;
+  if constexpr (EPI == 3) {
+    const uint32_t slot = blockIdx.x, wu = __builtin_amdgcn_readfirstlane(wave);
+    const bool rope_head = slot < rope.heads + rope.kv_heads;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      e_m[r] = m0 + wu * 4 + r;
+      e_live[r] = e_m[r] < M;
+    }
+    if (e_live[3] && (reinterpret_cast<uintptr_t>(rope.positions) & 15) == 0) {
+      // One 16-byte scalar load (m0 + 4 w is a multiple of 4).
+      const uint4 pv = *reinterpret_cast<const uint4*>(rope.positions + e_m[0]);
+      e_pos[0] = pv.x, e_pos[1] = pv.y, e_pos[2] = pv.z, e_pos[3] = pv.w;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) e_pos[r] = rope.positions[e_live[r] ? e_m[r] : M - 1];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t pc = e_pos[r] < rope.alloc ? e_pos[r] : rope.alloc - 1;
+      if (rope_head) e_sc[r] = rope.rope_tab[(size_t)pc * 32 + (lane & 31)];
+    }
+    if (rope_head) e_scale = (slot < rope.heads ? rope.q_norm : rope.k_norm)[lane];
   }
   if constexpr (NORM) {
     // The row's sum of squares in k order of the chunks: own chunks from
@@ -534,6 +567,29 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
       cs[i] = sum;
     }
     if (t == 0) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if constexpr (EPI == 3) {
+    // The tile is one head (column tile blockIdx.x) of 16 rows: through LDS
+    // to one row per wave pass, one dimension per lane, then norm, rope and
+    // the cache store as the rope/store kernel does from the stored tile.
+    // Y, when given, also receives the projections themselves.
+    __shared__ float s_head[16][65];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t n = n0 + (lane >> 4) * 4 + i;  // < N: N is a multiple of 64 here
+      const float val = sw[n] * cs[i];
+      s_head[lrow][wave * 16 + (lane >> 4) * 4 + i] = val;
+      if (Y && m0 + lrow < M) Y[(size_t)(m0 + lrow) * ldy + n] = val;
+    }
+    __syncthreads();
+    float ex[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ex[r] = s_head[wave * 4 + r][lane];
+    // Keep the norm weight's arithmetic here: hoisted next to its early
+    // load, it would make the wave wait for every outstanding load there.
+    asm volatile("" : "+v"(e_scale));
+    nd::rope_store_rows<4>(ex, e_m, e_live, e_pos, e_sc, e_scale, blockIdx.x, lane, rope);
+    return;
   }
   const uint32_t mo = m0 + lrow;
   if (mo >= M) return;
@@ -675,12 +731,13 @@ __global__ __launch_bounds__(512) void gemm_i8_astat_kernel(
 }
 
 using F32aFn = void (*)(const int8_t*, const float*, const float*, uint32_t, const float*, float*,
-                        uint32_t, uint32_t, uint32_t, uint32_t, float*, uint32_t*);
+                        uint32_t, uint32_t, uint32_t, uint32_t, float*, uint32_t*, nd::RopeStore);
 
 template <bool NORM, int CPW>
 F32aFn pick_f32a(int epilogue) {
   return epilogue == 0 ? &gemm_i8_f32a_kernel<0, NORM, CPW>
-       : epilogue == 1 ? &gemm_i8_f32a_kernel<1, NORM, CPW> : &gemm_i8_f32a_kernel<2, NORM, CPW>;
+       : epilogue == 1 ? &gemm_i8_f32a_kernel<1, NORM, CPW>
+       : epilogue == 2 ? &gemm_i8_f32a_kernel<2, NORM, CPW> : &gemm_i8_f32a_kernel<3, NORM, CPW>;
 }
 
 using GemmFn = void (*)(const int8_t*, const float*, const int8_t*, const float*, float*, uint32_t,
@@ -815,9 +872,12 @@ bool nd_gemm_f32_fits(const nd_mat* w, const float* x, uint32_t ldx, bool norm, 
 
 hipError_t nd_launch_gemm_f32(const nd_mat* w, const float* x, uint32_t ldx, const float* norm,
                               float* y, uint32_t ldy, uint32_t M, int epilogue, hipStream_t s,
-                              const nd_gemm_split* split) {
+                              const nd_gemm_split* split, const nd::RopeStore* rope) {
   if (M == 0) return hipSuccess;
   if (!nd_gemm_f32_fits(w, x, ldx, norm != nullptr, M, split)) return hipErrorInvalidValue;
+  if (epilogue == 3 &&
+      (!rope || w->n != (rope->heads + 2 * rope->kv_heads) * nd::kRopeHd))
+    return hipErrorInvalidValue;
   // Two chunks per workgroup when k has an even number of them: at K = 512
   // the product then needs no cross-workgroup sum, whose round trip costs
   // more than streaming the second chunk.
@@ -828,6 +888,6 @@ hipError_t nd_launch_gemm_f32(const nd_mat* w, const float* x, uint32_t ldx, con
                         : (norm ? pick_f32a<true, 1>(epilogue) : pick_f32a<false, 1>(epilogue));
   hipLaunchKernelGGL(f, dim3((w->n + 63) / 64, (M + 15) / 16, S), dim3(kGemmThreads), 0, s, w->w,
                      w->scales, x, ldx, norm, y, M, w->n, w->k, ldy, split->partials,
-                     split->counters);
+                     split->counters, rope ? *rope : nd::RopeStore{});
   return hipGetLastError();
 }

@@ -9,6 +9,7 @@
 #include <string>
 
 #include "needle_hip.h"
+#include "nd_rope.hpp"
 
 struct nd_mat {
   int8_t* w = nullptr;      // [n][k] int8 codes, row-major
@@ -58,6 +59,9 @@ struct nd_ctx {
   // Digit planes and row factors of nd_matmul_d (grown on demand).
   void* mm_scratch = nullptr;
   size_t mm_scratch_bytes = 0;
+  // Row records and counters of split selection (grown on demand, zeroed).
+  void* sel_split = nullptr;
+  size_t sel_split_bytes = 0;
   std::set<nd_mat*> mats;
   std::set<nd_kv*> kvs;
   std::set<nd_pieces*> pieces;
@@ -146,9 +150,27 @@ hipError_t nd_launch_attention(const nd_kv* kv, uint32_t layer, uint32_t positio
                                uint32_t* counters, hipStream_t s);
 hipError_t nd_launch_select_list(const float* logits, uint32_t vocab, const uint32_t* allowed,
                                  uint32_t count, uint32_t* id, double* logprob, hipStream_t s);
+// `split`: nd_select_split_bytes(batch) of device memory, zero when first
+// used and left zero by every launch, that lets each row's vocabulary be
+// split over several workgroups (vocab % 32 == 0); nullptr keeps one
+// workgroup per row.  Launches sharing one `split` must be ordered.  With
+// `adv` and the split form, the launch also advances a decode batch's state
+// (tokens[r] = id, positions[r] += 1, history[*step][r] = (id, log-prob) while
+// *step < history_steps, then *step += 1) and sets *advanced.
+struct nd_select_advance {
+  uint32_t* tokens;
+  uint32_t* positions;
+  uint32_t* step;
+  uint32_t* history;
+  double* lp_history;
+  uint32_t history_steps;
+};
+size_t nd_select_split_bytes(uint32_t batch);
 hipError_t nd_launch_select_mask(const float* logits, uint32_t batch, uint32_t vocab,
                                  const uint32_t* mask, uint32_t* ids, double* logprobs,
-                                 hipStream_t s);
+                                 hipStream_t s, void* split = nullptr,
+                                 const nd_select_advance* adv = nullptr,
+                                 bool* advanced = nullptr);
 
 // Digit-sliced int8 MFMA GEMM (gemm.hip): y[m][n] (op)= s_w[n] * A[m] . W[n]
 // with A given as digits [3][M][K] and per-row factors fm (digitize first).
@@ -171,12 +193,16 @@ hipError_t nd_launch_gemm(const nd_mat* w, const int8_t* digits, const float* fm
                           const nd_gemm_split* split = nullptr);
 // The same product on fp32 rows x [M][ldx] (optionally RMS-normalized with
 // `norm`, math.ts:16-32), digitized per 256-wide chunk inside the launch;
-// only for the shapes nd_gemm_f32_fits accepts.
+// only for the shapes nd_gemm_f32_fits accepts.  Epilogue 3 (the q/k/v
+// projection of a decode step, w->n = (heads + 2 kv_heads) * 64): instead of
+// storing y, each 64-column head goes through norm, rope and the cache store
+// that `rope` describes (nd_rope.hpp).
 bool nd_gemm_f32_fits(const nd_mat* w, const float* x, uint32_t ldx, bool norm, uint32_t M,
                       const nd_gemm_split* split);
 hipError_t nd_launch_gemm_f32(const nd_mat* w, const float* x, uint32_t ldx, const float* norm,
                               float* y, uint32_t ldy, uint32_t M, int epilogue, hipStream_t s,
-                              const nd_gemm_split* split);
+                              const nd_gemm_split* split,
+                              const nd::RopeStore* rope = nullptr);
 hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint32_t* positions,
                                      uint32_t batch, uint32_t seq_kv_heads, uint32_t kv_stride_z,
                                      uint32_t rep, uint32_t max_position, const float* q,

@@ -317,6 +317,172 @@ __global__ __launch_bounds__(kSelectThreads) void select_mask_reg_kernel(
   logprobs[r] = (double)logits[id] - (double)mx - log(total);
 }
 
+// Split form of the register-resident kernel for batches that leave most of
+// the chip idle at one workgroup per row: workgroup (sp, r) takes mask words
+// [sp * wps, (sp + 1) * wps) of row r (thread t one word: 32 ids), reduces
+// them to (best candidate, JavaScript max, first allowed id, float64 sum of
+// e^(logit - local max)), publishes that record with agent-coherent stores
+// and counts itself in; the last of the row's S workgroups merges the
+// records: max over maxima, sum of sum_w * e^(max_w - max) in float64 (a
+// part whose maximum is -inf holds only e^-inf = 0 terms), the best record
+// by (value, lower id), the smallest first id.  Selection and
+// log-probability as select_mask_reg_kernel; the float64 sum is the same
+// terms regrouped.  With `adv`, each row's merge also feeds its id back as
+// the row's next token, records id and log-probability in the step history,
+// advances the row's position, and the last row to finish advances the step
+// counter (what a separate advance pass would do).  Every call leaves the
+// counters at zero.
+constexpr uint32_t kSelSplitMax = 16;
+struct SelRecord {
+  float bv;
+  uint32_t bo;
+  float mx;
+  uint32_t first;
+  double sum;
+  double pad;
+};
+static_assert(sizeof(SelRecord) == 32, "record layout");
+
+__global__ __launch_bounds__(kSelectThreads) void select_mask_split_kernel(
+    const float* __restrict__ logits_all, uint32_t vocab, const uint32_t* __restrict__ mask_all,
+    uint32_t* __restrict__ ids, double* __restrict__ logprobs, uint32_t wps,
+    SelRecord* __restrict__ records, uint32_t* __restrict__ counters, nd_select_advance adv) {
+  __shared__ float s_v[16], s_mx[16];
+  __shared__ uint32_t s_o[16], s_first[16], s_last;
+  __shared__ double s_sum[16];
+  const uint32_t sp = blockIdx.x, S = gridDim.x, r = blockIdx.y;
+  const uint32_t t = threadIdx.x, w = t >> 6, lane = t & 63, nw = blockDim.x >> 6;
+  const float* logits = logits_all + (size_t)r * vocab;
+  const uint32_t words = vocab / 32;
+  const uint32_t word = sp * wps + t;
+  const bool mine = t < wps && word < words;
+  const uint32_t wc = mine ? word : 0;
+  const float4* src = reinterpret_cast<const float4*>(logits + (size_t)wc * 32);
+  float v[32];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const float4 f = src[q];
+    v[4 * q] = f.x;
+    v[4 * q + 1] = f.y;
+    v[4 * q + 2] = f.z;
+    v[4 * q + 3] = f.w;
+  }
+  const uint32_t m = !mine ? 0u : mask_all ? mask_all[(size_t)r * words + wc] : 0xFFFFFFFFu;
+  Best b{-INFINITY, kNone};
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    mx = js_maxf(mx, v[j]);
+    if (((m >> j) & 1u) && v[j] == v[j] && (b.order == kNone || v[j] > b.v))
+      b = Best{v[j], wc * 32 + j};
+  }
+  if (!mine) mx = -INFINITY;
+  uint32_t first = m ? wc * 32 + (uint32_t)__builtin_ctz(m) : kNone;
+  for (int o = 32; o >= 1; o >>= 1) {
+    Best other{__shfl_xor(b.v, o, 64), (uint32_t)__shfl_xor((int)b.order, o, 64)};
+    if (better(other, b)) b = other;
+    mx = js_maxf(mx, __shfl_xor(mx, o, 64));
+    first = min(first, (uint32_t)__shfl_xor((int)first, o, 64));
+  }
+  if (lane == 0) {
+    s_v[w] = b.v;
+    s_o[w] = b.order;
+    s_mx[w] = mx;
+    s_first[w] = first;
+  }
+  __syncthreads();
+  mx = s_mx[0];
+  for (uint32_t i = 1; i < nw; ++i) mx = js_maxf(mx, s_mx[i]);
+  double sum = 0.0;
+  {
+    const double md = (double)mx;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      const double e = exp_term(mine ? v[j] : -INFINITY, md);
+      if (mine) sum += e;
+    }
+  }
+  for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  if (lane == 0) s_sum[w] = sum;
+  __syncthreads();
+  if (t == 0) {
+    Best best{s_v[0], s_o[0]};
+    uint32_t f = s_first[0];
+    double total = s_sum[0];
+    for (uint32_t i = 1; i < nw; ++i) {
+      const Best other{s_v[i], s_o[i]};
+      if (better(other, best)) best = other;
+      f = min(f, s_first[i]);
+      total += s_sum[i];
+    }
+    SelRecord* rec = records + (size_t)r * kSelSplitMax + sp;
+    __hip_atomic_store(&rec->bv, best.v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&rec->bo, best.order, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&rec->mx, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&rec->first, f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&rec->sum, total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // the record has completed
+    const bool last =
+        __hip_atomic_fetch_add(counters + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        S - 1;
+    if (last) __hip_atomic_store(counters + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last || w != 0) return;
+
+  // Merge: lane j holds record j.
+  const SelRecord* rec = records + (size_t)r * kSelSplitMax + (lane < S ? lane : 0);
+  float bv = __hip_atomic_load(&rec->bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t bo = __hip_atomic_load(&rec->bo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float pm = __hip_atomic_load(&rec->mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t pf = __hip_atomic_load(&rec->first, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  double ps = __hip_atomic_load(&rec->sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane >= S) {
+    bv = -INFINITY;
+    bo = kNone;
+    pm = -INFINITY;
+    pf = kNone;
+    ps = 0.0;
+  }
+  Best best{bv, bo};
+  float gm = pm;
+  uint32_t f = pf;
+  for (int o = 32; o >= 1; o >>= 1) {
+    Best other{__shfl_xor(best.v, o, 64), (uint32_t)__shfl_xor((int)best.order, o, 64)};
+    if (better(other, best)) best = other;
+    gm = js_maxf(gm, __shfl_xor(gm, o, 64));
+    f = min(f, (uint32_t)__shfl_xor((int)f, o, 64));
+  }
+  double term = (lane < S && pm != -INFINITY) ? ps * exp((double)pm - (double)gm) : 0.0;
+  for (int o = 32; o >= 1; o >>= 1) term += __shfl_xor(term, o, 64);
+  if (lane != 0) return;
+  uint32_t id = kNone;
+  double lp = __builtin_nan("");
+  if (f != kNone) {
+    id = (logits[f] != logits[f] || best.order == kNone) ? f : best.order;
+    lp = (double)logits[id] - (double)gm - log(term);
+  }
+  ids[r] = id;
+  logprobs[r] = lp;
+  if (!adv.tokens) return;
+  const uint32_t batch = gridDim.y;
+  const uint32_t step = __hip_atomic_load(adv.step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  adv.tokens[r] = id;
+  adv.positions[r] += 1;
+  if (step < adv.history_steps) {
+    adv.history[(size_t)step * batch + r] = id;
+    adv.lp_history[(size_t)step * batch + r] = lp;
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this row's read of the step counter has completed
+  uint32_t* rows_done = counters + batch;
+  if (__hip_atomic_fetch_add(rows_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+      batch - 1) {
+    __hip_atomic_store(rows_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(adv.step, step + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 }  // namespace
 
 hipError_t nd_launch_select_list(const float* logits, uint32_t vocab, const uint32_t* allowed,
@@ -326,10 +492,37 @@ hipError_t nd_launch_select_list(const float* logits, uint32_t vocab, const uint
   return hipGetLastError();
 }
 
+size_t nd_select_split_bytes(uint32_t batch) {
+  return (size_t)batch * kSelSplitMax * sizeof(SelRecord) + ((size_t)batch + 1) * 4;
+}
+
 hipError_t nd_launch_select_mask(const float* logits, uint32_t batch, uint32_t vocab,
                                  const uint32_t* mask, uint32_t* ids, double* logprobs,
-                                 hipStream_t s) {
+                                 hipStream_t s, void* split, const nd_select_advance* adv,
+                                 bool* advanced) {
+  if (advanced) *advanced = false;
   if (batch == 0) return hipSuccess;
+  if (split && vocab % 32 == 0) {
+    // Parts per row: enough workgroups for ~512 in all, at least 64 words
+    // (one wave) per part and at most 1024 words (one workgroup).
+    const uint32_t words = vocab / 32;
+    uint32_t S = (512 + batch - 1) / batch;
+    if (S > words / 64) S = words / 64;
+    if (S > kSelSplitMax) S = kSelSplitMax;
+    if (S < (words + kSelectThreads - 1) / kSelectThreads)
+      S = (words + kSelectThreads - 1) / kSelectThreads;
+    if (S >= 2 && S <= kSelSplitMax) {
+      const uint32_t wps = (words + S - 1) / S;
+      const uint32_t threads = (wps + 63) / 64 * 64;
+      SelRecord* records = reinterpret_cast<SelRecord*>(split);
+      uint32_t* counters = reinterpret_cast<uint32_t*>(records + (size_t)batch * kSelSplitMax);
+      hipLaunchKernelGGL(select_mask_split_kernel, dim3(S, batch), dim3(threads), 0, s, logits,
+                         vocab, mask, ids, logprobs, wps, records, counters,
+                         adv ? *adv : nd_select_advance{});
+      if (advanced) *advanced = adv != nullptr;
+      return hipGetLastError();
+    }
+  }
   if (vocab % 32 == 0 && vocab <= 32u * kSelectThreads)
     hipLaunchKernelGGL(select_mask_reg_kernel, dim3(batch), dim3(kSelectThreads), 0, s, logits,
                        vocab, mask, ids, logprobs);

@@ -281,9 +281,10 @@ def test_attention_long_context_several_tiles_per_wave(hip, hq, sink, window, mo
 @pytest.mark.parametrize("vocab", [32768, 4096, 1000])
 def test_select_mask_batch_on_device(hip, vocab):
     """Masked selection over a batch of rows in HBM (nd_select_mask_d): ids
-    bit-exact and log-probabilities to 1e-9, with ties, NaN logits inside and
-    outside the allowed set, a NaN first candidate and an empty mask.  1000
-    is not a multiple of 32 and takes the general kernel."""
+    bit-exact and log-probabilities to 1e-9, with ties (also between the
+    parts of a row split over workgroups), NaN logits inside and outside the
+    allowed set, a NaN first candidate, an empty mask and half a row at -inf.
+    1000 is not a multiple of 32 and takes the general kernel."""
     say("select mask batch", vocab)
     s = synth.Stream(17, f"selmask{vocab}")
     B = 8
@@ -297,6 +298,10 @@ def test_select_mask_batch_on_device(hip, vocab):
     logits[3, np.flatnonzero(allowed[3])[0]] = np.nan  # NaN first candidate is kept
     allowed[4] = False  # empty mask
     logits[5, np.flatnonzero(~allowed[5])[3]] = np.nan  # NaN outside: log-prob NaN
+    far = vocab - 100  # in another workgroup's part of the row when the row is split
+    allowed[6, [7, far]] = True
+    logits[6, [7, far]] = 60.0  # tie across parts: the earlier id wins
+    logits[7, :vocab // 2] = -np.inf  # parts whose maximum is -inf add nothing
     masks = np.zeros((B, words), np.uint32)
     for r in range(B):
         for i in np.flatnonzero(allowed[r]):
@@ -320,7 +325,7 @@ def test_select_mask_batch_on_device(hip, vocab):
             assert math.isnan(got_lps[r]), (vocab, r)
         else:
             assert abs(got_lps[r] - want_lp) <= 1e-9 * max(1.0, abs(want_lp)), (vocab, r)
-    assert int(got_ids[1]) == 5 and int(got_ids[4]) == 0xFFFFFFFF
+    assert int(got_ids[1]) == 5 and int(got_ids[4]) == 0xFFFFFFFF and int(got_ids[6]) == 7
 
 
 def test_select_golden_cases(hip):
