@@ -614,10 +614,11 @@ __global__ __launch_bounds__(64 * KW) void attention_kernel(
 // end, yet more, smaller workgroups win: a single query row aims at 256
 // workgroups (32 chunks of 256 per head at 8 heads x 8192, elected in groups
 // of 8: 7.95 us per call, vs 8.9 at 128 workgroups and 10.4 at 64) and
-// batches at 4096 (64 sequences x 8 heads at contexts up to 2048: 0.467 ms
-// per decode step, vs 0.491 at 2048 and 0.527 at 1024).  One tile per wave
-// also runs the leanest kernel form (73 VGPRs: 6 waves per SIMD).
-constexpr uint32_t kTargetSingle = 256, kTargetBatch = 4096;
+// batches at 8192 (64 sequences x 8 heads at contexts up to 2176: chunks of
+// 256, 20.3 us per layer, vs 21.6 with chunks of 512 at 4096 workgroups).
+// One tile per wave also runs the leanest kernel form (73 VGPRs: 6 waves
+// per SIMD).
+constexpr uint32_t kTargetSingle = 256, kTargetBatch = 8192;
 constexpr uint32_t kMaxChunks = 64;  // the merge holds one chunk per lane
 static_assert(1 + kMaxChunks / kChunkGroup <= kAttnCounterStride, "group counters fit the stride");
 uint32_t chunk_positions_for(uint32_t max_count, uint32_t pairs, uint32_t target) {
