@@ -414,6 +414,20 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
       for (int q = 0; q < 4; ++q) wn[c][q] = src[q];
     }
   }
+  // Epilogue 1's addends (this lane's 4 outputs of y), loaded with the
+  // product's operands instead of after the product: no load round trip at
+  // the end.
+  float e_add[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (EPI == 1) {
+    const uint32_t mo = m0 + lrow;
+    if (mo < M) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t n = n0 + (lane >> 4) * 4 + i;
+        if (n < N) e_add[i] = Y[(size_t)mo * ldy + n];
+      }
+    }
+  }
   // Epilogue 3's operands, loaded after the product's so that they do not
   // delay them: wave w's rows m0 + 4 w + r (w uniform: scalar loads of the
   // positions), the rope angles of this lane's pair and the head's norm
@@ -600,7 +614,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
     const float val = sw[n] * cs[i];
     float* dst = Y + (size_t)mo * ldy + n;
     if constexpr (EPI == 0) *dst = val;
-    else if constexpr (EPI == 1) *dst = *dst + val;
+    else if constexpr (EPI == 1) *dst = e_add[i] + val;
     else *dst = silu_f(val);
   }
 }
