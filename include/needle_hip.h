@@ -394,9 +394,15 @@ typedef struct nd_needle nd_needle;
 
 /* Needle 2 geometry and weights (model/cact.ts geometry fields; the per-layer
  * tensors read by NeedleRuntime.step, model/runtime.ts:280-583).  Every
- * matrix is a per-row-scaled int8 matrix (g == k) uploaded with
- * nd_mat_upload_i8 and owned by the caller (it must outlive the model);
- * dense vectors are host arrays copied at creation.
+ * matrix takes one form, owned by the caller (it must outlive the model):
+ * either per-row-scaled int8 (g == k, nd_mat_upload_i8), or -- the shipped
+ * archive's form, model/cact.ts:398-562 -- Cactus-Quant (nd_mat_upload_cq),
+ * all of the embedding's width and group size, groups of at most 2048 and
+ * engram rows of at most 1024 padded codes; a Cactus-Quant model runs every
+ * product as cqMatvec and every row gather as dequantizeCqRow
+ * (backends/cq.ts:106-295), and its prompts step token by token as
+ * NeedleRuntime.prefill does.  Dense vectors are host arrays copied at
+ * creation.
  *   embedding  [vocab][dim], tied output projection (runtime.ts:570-577)
  *   wq, wgate  layers entries of [heads*64][dim]; wk, wv [kv_heads*64][dim]
  *   wo         [dim][heads*64]

@@ -23,6 +23,7 @@
 #include <type_traits>
 #include <vector>
 
+#include "nd_cq.hpp"
 #include "nd_internal.hpp"
 #include "nd_wave.hpp"
 
@@ -91,6 +92,9 @@ struct BeginArgs {
   double* rope;            // out: sin then cos of position * inv_freq[j]
   float* cell0;            // confidence pool cell 0 (the scaled embedding), or null
   uint32_t cell_ld;        // its row stride in the batched form
+  // Cactus-Quant model: the gathers run in n2_cq_rows_kernel, which reads
+  // [tables] indices, [tables] valid flags and the token from here.
+  uint32_t* cq_lookup;
 };
 
 // Token intake, engram hashing (runtime.ts:788-818), the scaled embedding
@@ -140,6 +144,14 @@ __global__ __launch_bounds__(kWg) void n2_begin_kernel(BeginArgs a) {
     hash ^= hash >> 15;
     s_idx[t] = hash % a.slots;
     s_valid[t] = valid ? 1u : 0u;
+    if (a.cq_lookup) {
+      a.cq_lookup[t] = s_idx[t];
+      a.cq_lookup[a.tables + t] = s_valid[t];
+    }
+  }
+  if (a.cq_lookup) {
+    if (t == 0) a.cq_lookup[2 * a.tables] = tok;
+    return;
   }
   __syncthreads();
   for (uint32_t k = t; k < a.d; k += kWg) {
@@ -219,6 +231,61 @@ __global__ __launch_bounds__(kWg) void n2_gather_kernel(BeginArgs a,
     }
     a.cat[i] = v;
   }
+}
+
+// The begin kernel's gathers for a Cactus-Quant model (runtime.ts:305-313,
+// 828-836), rows dequantized as dequantizeCqRow (cq.ts:243-295):
+// workgroup 0 puts the embedding row of *token, times sqrt(d) in float64,
+// into every lane (and cell 0 of the confidence pool); workgroup 1 + s *
+// tables + t writes table t's row lookup[t] of engram site s into cat, or
+// zeros when lookup[tables + t] is 0.
+constexpr uint32_t kCqRowMax = 1024;  // padded row width of the embedding and tables
+struct CqRowsArgs {
+  const uint8_t* emb_p;
+  const uint16_t* emb_n;
+  uint32_t emb_kpad, emb_row_bytes;
+  const uint8_t* tab_p[4];
+  const uint16_t* tab_n[4];
+  uint32_t tab_kpad, tab_row_bytes;
+  float cb[16];  // by code (ternary: 0, +c, 0, -c)
+  uint32_t g, bits;
+  double inverse_root;
+  const uint32_t* token;   // null: no embedding row (the session's lanes come from the host)
+  const uint32_t* lookup;  // [tables] indices, then [tables] valid flags
+  uint32_t d, lanes;
+  double scale;
+  float* x;
+  float* cell0;
+  uint32_t n_sites, tables, slots, sub;
+  float* cat;
+};
+
+__global__ __launch_bounds__(256) void n2_cq_rows_kernel(CqRowsArgs a) {
+  __shared__ float v[kCqRowMax];
+  const uint32_t b = blockIdx.x, t = threadIdx.x;
+  if (b == 0) {
+    if (!a.token) return;
+    const uint32_t tok = *a.token;
+    nd::cq_dequant_row(a.emb_p + (size_t)tok * a.emb_row_bytes,
+                       a.emb_n + (size_t)tok * (a.emb_kpad / a.g), a.cb, a.emb_kpad, a.g, a.bits,
+                       a.inverse_root, v);
+    for (uint32_t k = t; k < a.d; k += blockDim.x) {
+      const float val = (float)((double)v[k] * a.scale);
+      for (uint32_t l = 0; l < a.lanes; ++l) a.x[(size_t)l * a.d + k] = val;
+      if (a.cell0) a.cell0[k] = val;
+    }
+    return;
+  }
+  const uint32_t i = b - 1, s = i / a.tables, tb = i % a.tables;
+  float* out = a.cat + ((size_t)s * a.tables + tb) * a.sub;
+  if (!a.lookup[a.tables + tb]) {
+    for (uint32_t c = t; c < a.sub; c += blockDim.x) out[c] = 0.f;
+    return;
+  }
+  const size_t row = (size_t)tb * a.slots + a.lookup[tb];
+  nd::cq_dequant_row(a.tab_p[s] + row * a.tab_row_bytes, a.tab_n[s] + row * (a.tab_kpad / a.g),
+                     a.cb, a.tab_kpad, a.g, a.bits, a.inverse_root, v);
+  for (uint32_t c = t; c < a.sub; c += blockDim.x) out[c] = v[c];
 }
 
 // sinkhorn (math.ts:62-92) of an L x L matrix (L <= 4) on the lanes of a
@@ -347,6 +414,14 @@ struct MixArgs {
   uint32_t has_pre, own_pre;
   const int8_t* phi_w[3];  // phi_pre, phi_post, phi_res rows of layer l
   const float* phi_s[3];
+  // The same rows as Cactus-Quant matrices (n2_mix_kernel<true>): packed
+  // rows and binary16 norms of layer l's phi_pre, phi_post and phi_res, the
+  // codebook by code, width, group, bytes per row, norms per row, 1/sqrt(g).
+  const uint8_t* cq_p[3];
+  const uint16_t* cq_n[3];
+  float cq_cb[16];
+  uint32_t cq_bits, cq_g, cq_row_bytes, cq_groups;
+  double cq_inv_root;
   float a_pre;
   const float* b_pre;
   uint32_t has_site;  // an engram site injects at layer l
@@ -512,6 +587,7 @@ constexpr int kPhiPairs = 8;
 // read at the same k).  D rows 0 and 1 (hi, lo) land in lanes 0..15, outputs
 // 0 and 1; the four waves of a tile meet in LDS and the sum is taken in
 // float64 times the row scale.
+template <bool CQ>
 __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   if (blockIdx.x) {
     const uint32_t m = blockIdx.x, D0 = a.d, L0 = a.lanes;
@@ -573,17 +649,27 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   // rows past the phi rows are zeroed there.
   __builtin_amdgcn_sched_barrier(0);
   u32x4 pw[kPhiPairs];
+  if constexpr (!CQ) {
 #pragma unroll
-  for (int i = 0; i < kPhiPairs; ++i) {
-    const uint32_t pp = min(kq * ppw + i, pairs - 1);
-    pw[i] = *reinterpret_cast<const u32x4*>(wrow + (size_t)pp * 64);
+    for (int i = 0; i < kPhiPairs; ++i) {
+      const uint32_t pp = min(kq * ppw + i, pairs - 1);
+      pw[i] = *reinterpret_cast<const u32x4*>(wrow + (size_t)pp * 64);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   const uint32_t tr = min(t, nrows - 1);
   const float norm_in = a.norm_input[tc], ekey = a.ekey[tc], evalue = a.evalue[tc],
-              fnorm = a.final_norm[tc],
-              psc = tr < L ? s0[tr] : (tr < 2 * L ? s1[tr - L] : s2[tr - 2 * L]);
-  const float bpre = a.b_pre[min(lane, L - 1)], spre = s0[min(lane, L - 1)];
+              fnorm = a.final_norm[tc];
+  float psc = 0.f, spre = 0.f;
+  if constexpr (!CQ) {
+    psc = tr < L ? s0[tr] : (tr < 2 * L ? s1[tr - L] : s2[tr - 2 * L]);
+    spre = s0[min(lane, L - 1)];
+  }
+  const float bpre = a.b_pre[min(lane, L - 1)];
+  __shared__ float s_cb[16];
+  if constexpr (CQ) {
+    if (t < 16) s_cb[t] = a.cq_cb[t];
+  }
 
   // ---- post(l - 1)
   if (a.has_post) {
@@ -663,59 +749,106 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     if ((uint32_t)l < L) ss += (double)xl[l] * (double)xl[l];
   ss = mix_sum(col ? ss : 0.0, red, phase);
   const double inv = 1.0 / sqrt(ss / N + 1e-6);
-  if (col) {
+  float pre_phi = 0.f;  // phi_pre row `lane` (lane < lanes): feeds hPre
+  if constexpr (CQ) {
+    // phi = cqMatvec of the normalized lanes (backends/cq.ts:30-46, 107-231):
+    // prepareCqActivation in LDS -- per group the butterflies, then times
+    // 1/sqrt(g) -- and one wave per phi row, lane u taking the row's 32-code
+    // unit u: float64 dot per group times the group's norm, summed over the
+    // wave in float64.
+    float* s_nl = reinterpret_cast<float*>(&s_split[0][0]);  // N <= 2048 floats
+    if (col) {
 #pragma unroll
-    for (int l = 0; l < 4; ++l)
-      if ((uint32_t)l < L) {
-        const float v = (float)((double)xl[l] * inv) * a.split_scale;
-        const _Float16 h = (_Float16)v;
-        s_split[0][l * D + t] = h;
-        s_split[1][l * D + t] = (_Float16)(v - (float)h);
+      for (int l = 0; l < 4; ++l)
+        if ((uint32_t)l < L) s_nl[l * D + t] = (float)((double)xl[l] * inv);
+    }
+    __syncthreads();
+    nd::cq_fwht_groups(s_nl, N, a.cq_g);
+    for (uint32_t i = t; i < N; i += kMixWg) s_nl[i] = (float)((double)s_nl[i] * a.cq_inv_root);
+    __syncthreads();
+    for (uint32_t r = wave; r < nrows; r += kMixWg / 64) {
+      const uint32_t mat = r < L ? 0u : (r < 2 * L ? 1u : 2u);
+      const uint32_t rr = r - (mat == 0 ? 0u : (mat == 1 ? L : 2 * L));
+      const uint8_t* prow = a.cq_p[mat] + (size_t)rr * a.cq_row_bytes;
+      const uint16_t* nrow = a.cq_n[mat] + (size_t)rr * a.cq_groups;
+      double total = 0.0;
+      if (lane < N / 32) {
+        double dot = 0.0;
+        for (uint32_t j = 0; j < 32; ++j) {
+          const uint32_t c = lane * 32 + j;
+          dot += (double)s_cb[nd::cq_code(prow, c, a.cq_bits)] * (double)s_nl[c];
+          if ((c + 1) % a.cq_g == 0 || j == 31) {  // end of a group, or of the unit
+            total += (double)nd::cq_half(nrow[c / a.cq_g]) * dot;
+            dot = 0.0;
+          }
+        }
       }
-  }
-  nd::lds_barrier();
-  float4v acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < kPhiPairs; ++i) {
-    const uint32_t pp = kq * ppw + i;
-    if ((uint32_t)i < ppw && pp < pairs) {  // uniform over the wave
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        half8 av = {};
-        if (r16 < 2)
-          av = *reinterpret_cast<const half8*>(&s_split[r16][pp * 64 + kb * 16 + h * 8]);
-        const u32x4 wv = prow_ok ? pw[i] : u32x4{0u, 0u, 0u, 0u};
-        const half8 bv = nd::codes_to_half(h ? u32x2{wv.z, wv.w} : u32x2{wv.x, wv.y});
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+      total = nd::wave_sum(total);
+      if (lane == 0) phi[r] = (float)total;
+    }
+    __syncthreads();
+    if (t < nrows) {
+      const float v = phi[t];
+      if (t >= L && t < 2 * L) a.phi_post[t - L] = v;
+      if (t >= 2 * L) a.phi_res[t - 2 * L] = v;
+    }
+    pre_phi = phi[min(lane, L - 1)];
+  } else {
+    if (col) {
+  #pragma unroll
+      for (int l = 0; l < 4; ++l)
+        if ((uint32_t)l < L) {
+          const float v = (float)((double)xl[l] * inv) * a.split_scale;
+          const _Float16 h = (_Float16)v;
+          s_split[0][l * D + t] = h;
+          s_split[1][l * D + t] = (_Float16)(v - (float)h);
+        }
+    }
+    nd::lds_barrier();
+    float4v acc = {0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+    for (int i = 0; i < kPhiPairs; ++i) {
+      const uint32_t pp = kq * ppw + i;
+      if ((uint32_t)i < ppw && pp < pairs) {  // uniform over the wave
+  #pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          half8 av = {};
+          if (r16 < 2)
+            av = *reinterpret_cast<const half8*>(&s_split[r16][pp * 64 + kb * 16 + h * 8]);
+          const u32x4 wv = prow_ok ? pw[i] : u32x4{0u, 0u, 0u, 0u};
+          const half8 bv = nd::codes_to_half(h ? u32x2{wv.z, wv.w} : u32x2{wv.x, wv.y});
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+        }
       }
     }
-  }
-  if (lane < 16) {
-    s_part[prow][kq][0] = acc[0];
-    s_part[prow][kq][1] = acc[1];
-  }
-  nd::lds_barrier();
-  // phi row r = scale_r * 2^-s * sum over the tile's waves of (hi + lo), in
-  // float64; every thread takes the phi_pre rows itself (they feed hPre).
-  auto phi_row = [&](uint32_t r, float scale) -> float {
-    const float4 q0 = *reinterpret_cast<const float4*>(&s_part[r][0][0]);
-    const float4 q1 = *reinterpret_cast<const float4*>(&s_part[r][2][0]);
-    const double sum = (((double)q0.x + (double)q0.y) + ((double)q0.z + (double)q0.w)) +
-                       (((double)q1.x + (double)q1.y) + ((double)q1.z + (double)q1.w));
-    return (float)((double)scale * (sum * (double)a.split_unscale));
-  };
-  if (t < nrows) {
-    const float v = phi_row(t, psc);
-    phi[t] = v;  // read by route_wave after later barriers
-    if (t >= L && t < 2 * L) a.phi_post[t - L] = v;
-    if (t >= 2 * L) a.phi_res[t - 2 * L] = v;
+    if (lane < 16) {
+      s_part[prow][kq][0] = acc[0];
+      s_part[prow][kq][1] = acc[1];
+    }
+    nd::lds_barrier();
+    // phi row r = scale_r * 2^-s * sum over the tile's waves of (hi + lo), in
+    // float64; every thread takes the phi_pre rows itself (they feed hPre).
+    auto phi_row = [&](uint32_t r, float scale) -> float {
+      const float4 q0 = *reinterpret_cast<const float4*>(&s_part[r][0][0]);
+      const float4 q1 = *reinterpret_cast<const float4*>(&s_part[r][2][0]);
+      const double sum = (((double)q0.x + (double)q0.y) + ((double)q0.z + (double)q0.w)) +
+                         (((double)q1.x + (double)q1.y) + ((double)q1.z + (double)q1.w));
+      return (float)((double)scale * (sum * (double)a.split_unscale));
+    };
+    if (t < nrows) {
+      const float v = phi_row(t, psc);
+      phi[t] = v;  // read by route_wave after later barriers
+      if (t >= L && t < 2 * L) a.phi_post[t - L] = v;
+      if (t >= 2 * L) a.phi_res[t - 2 * L] = v;
+    }
+    pre_phi = phi_row(min(lane, L - 1), spre);
   }
   // hPre (runtime.ts:412-417): lane l < lanes of every wave takes lane l's
   // gate, and the wave shares them by readlane (no barrier).
   float hp = 0.f;
   if (lane < L) {
     const double off = lane == a.own_pre ? 4.0 : -4.0;
-    hp = (float)sigmoid_d((double)a.a_pre * (double)phi_row(lane, spre) + (double)bpre + off);
+    hp = (float)sigmoid_d((double)a.a_pre * (double)pre_phi + (double)bpre + off);
   }
   float hpre[4];
 #pragma unroll
@@ -817,12 +950,31 @@ __global__ __launch_bounds__(256) void n2_qkv_kernel(
     const double* __restrict__ rope, float* __restrict__ q_out, float* __restrict__ gate_out,
     void* __restrict__ Kc, void* __restrict__ Vc, float* __restrict__ Ks,
     float* __restrict__ Vs, uint32_t layer, uint32_t alloc, uint32_t sink, uint32_t window,
-    uint32_t f32, RouteArgs route) {
+    uint32_t f32, RouteArgs route, const float* __restrict__ projected) {
   __shared__ float xs[512];
   __shared__ float rows[64];
   const uint32_t b = blockIdx.x, t = threadIdx.x;
   if (b == 2 * (heads + kv_heads)) {
     route_wave(route, t, rows);
+    return;
+  }
+  if (projected) {
+    // Cactus-Quant model: the projections come from a CQ matvec of the
+    // same rows; only the per-head epilogue runs here.
+    if (t >= 64) return;
+    const float val = projected[(size_t)b * kHd + t];
+    const uint32_t nq = heads, nk = kv_heads;
+    if (b >= nq + 2 * nk) {  // gate head
+      gate_out[(size_t)(b - nq - 2 * nk) * kHd + t] = val;
+      return;
+    }
+    const uint32_t pos = st[1];
+    const float nscale = b < heads ? q_norm[t] : k_norm[t];
+    const double rs = rope[t & 31], rc = rope[32 + (t & 31)];
+    const int role = b < nq ? 0 : (b < nq + nk ? 1 : 2);
+    const uint32_t h = role == 0 ? b : (role == 1 ? b - nq : b - nq - nk);
+    head_epilogue(val, t, role, rs, rc, nscale, q_out + (size_t)h * kHd, Kc, Vc, Ks, Vs,
+                  ((size_t)layer * kv_heads + h) * alloc, kv_slot(pos, sink, window), alloc, f32);
     return;
   }
   // Loads first: this thread's weight bytes, the row scale, the epilogue
@@ -1220,6 +1372,7 @@ enum StageSlot : uint32_t {
 
 struct nd_needle {
   nd_needle_desc d{};
+  bool cq = false;  // every matrix in the Cactus-Quant form (else int8)
   std::vector<nd_mat> wqkvg;  // owned: rows q | k | v | gate of each layer
   std::vector<nd_mat> ekv;    // owned: rows key | value of each engram site
   std::vector<const nd_mat*> wo, eg_tables;
@@ -1237,6 +1390,8 @@ struct nd_needle {
   uint32_t *st = nullptr, *history = nullptr, *sel_id = nullptr, *allowed = nullptr,
            *counters = nullptr;
   double *lp_history = nullptr, *sel_lp = nullptr;
+  uint32_t* cq_lookup = nullptr;  // CQ model: a step's engram lookups and token
+  float* cq_proj = nullptr;       // CQ model: a layer's q | k | v | gate projections
   float *ring = nullptr, *x = nullptr, *upd = nullptr, *blk = nullptr, *ain = nullptr,
         *qkvg = nullptr, *q = nullptr, *att = nullptr, *proj = nullptr, *phi_post_v = nullptr,
         *phi_res_v = nullptr, *fin = nullptr, *logits = nullptr, *cat = nullptr, *ekv_out = nullptr,
@@ -1366,12 +1521,27 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s) 
   m.route = n->route;
   m.has_pre = pre && (parts & kMixPre);
   m.own_pre = ql % ln;
-  m.phi_w[0] = n->phi_pre->w + (size_t)ql * ln * K;
-  m.phi_s[0] = n->phi_pre->scales + (size_t)ql * ln;
-  m.phi_w[1] = n->phi_post->w + (size_t)ql * ln * K;
-  m.phi_s[1] = n->phi_post->scales + (size_t)ql * ln;
-  m.phi_w[2] = n->phi_res->w + (size_t)ql * ln * ln * K;
-  m.phi_s[2] = n->phi_res->scales + (size_t)ql * ln * ln;
+  if (n->cq) {
+    const nd_mat* pm[3] = {n->phi_pre, n->phi_post, n->phi_res};
+    const size_t first[3] = {(size_t)ql * ln, (size_t)ql * ln, (size_t)ql * ln * ln};
+    for (int i = 0; i < 3; ++i) {
+      m.cq_p[i] = pm[i]->packed + first[i] * pm[i]->row_bytes;
+      m.cq_n[i] = pm[i]->norms + first[i] * (pm[i]->kpad / pm[i]->g);
+    }
+    for (int i = 0; i < 16; ++i) m.cq_cb[i] = n->phi_pre->cb[i];
+    m.cq_bits = n->phi_pre->bits;
+    m.cq_g = n->phi_pre->g;
+    m.cq_row_bytes = n->phi_pre->row_bytes;
+    m.cq_groups = n->phi_pre->kpad / n->phi_pre->g;
+    m.cq_inv_root = 1.0 / std::sqrt((double)n->phi_pre->g);
+  } else {
+    m.phi_w[0] = n->phi_pre->w + (size_t)ql * ln * K;
+    m.phi_s[0] = n->phi_pre->scales + (size_t)ql * ln;
+    m.phi_w[1] = n->phi_post->w + (size_t)ql * ln * K;
+    m.phi_s[1] = n->phi_post->scales + (size_t)ql * ln;
+    m.phi_w[2] = n->phi_res->w + (size_t)ql * ln * ln * K;
+    m.phi_s[2] = n->phi_res->scales + (size_t)ql * ln * ln;
+  }
   m.a_pre = n->a_pre[ql];
   m.b_pre = n->params + n->o_bpre + (size_t)ql * ln;
   m.has_site = site >= 0;
@@ -1384,8 +1554,21 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s) 
   m.final_norm = n->params + n->o_final;
   m.fin = n->fin;
   m.cell = pool_on(n) && has_post && (parts & kMixCell) ? n->cells + (size_t)l * D : nullptr;
-  hipLaunchKernelGGL(n2_mix_kernel, dim3(1), dim3(kMixWg), 0, s, m);
+  if (n->cq)
+    hipLaunchKernelGGL(n2_mix_kernel<true>, dim3(1), dim3(kMixWg), 0, s, m);
+  else
+    hipLaunchKernelGGL(n2_mix_kernel<false>, dim3(1), dim3(kMixWg), 0, s, m);
   return hipGetLastError();
+}
+
+// y = m x (rows [row_start, +row_count) into y[0, row_count)) for either
+// matrix form: the int8 matvec, or the Cactus-Quant matvec with its input
+// rotation inside the launch (groups <= 2048, checked at create).
+hipError_t mv_any(const nd_mat* m, const float* x, uint32_t row_start, uint32_t row_count,
+                  float* y, hipStream_t s) {
+  if (m->bits)
+    return nd_launch_cq_matvec(m, x, 1, m->k, nullptr, row_start, row_count, y, row_count, s);
+  return nd_launch_matvec(m, x, 1, m->k, row_start, row_count, y, row_count, s);
 }
 
 // The attention block of layer l on the input n->ain: Q/K/V/gate matvec with
@@ -1406,17 +1589,22 @@ hipError_t enqueue_block(nd_needle* n, uint32_t l, hipStream_t s) {
   ra.lanes = ln;
   ra.own = l % ln;
   ra.route = n->route;
+  if (n->cq) {  // the Cactus-Quant projections first, then the per-head epilogue
+    const hipError_t e = mv_any(&wm, n->ain, 0, wm.n, n->cq_proj, s);
+    if (e != hipSuccess) return e;
+  }
   hipLaunchKernelGGL(n2_qkv_kernel, dim3(wm.n / kHd + 1), dim3(256), 0, s, wm.w, wm.scales,
                      n->ain, D, d.heads, d.kv_heads, n->st, n->params + n->o_qn + (size_t)l * kHd,
                      n->params + n->o_kn + (size_t)l * kHd, n->rope, n->q, n->qkvg,
                      n->kv.k, n->kv.v, n->kv.ks, n->kv.vs, l, n->kv.alloc, n->kv.sink,
-                     n->kv.window, n->kv.mode == ND_KV_FLOAT32 ? 1u : 0u, ra);
+                     n->kv.window, n->kv.mode == ND_KV_FLOAT32 ? 1u : 0u, ra,
+                     n->cq ? n->cq_proj : nullptr);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   e = nd_launch_attention_gated(&n->kv, l, n->st + 1, n->max_length - 1, n->q, d.heads, n->qkvg,
                                 n->att, n->partials, n->counters, s);
   if (e != hipSuccess) return e;
-  return nd_launch_matvec(n->wo[l], n->att, 1, qw, 0, D, n->proj, D, s);
+  return mv_any(n->wo[l], n->att, 0, D, n->proj, s);
 }
 
 // After the final mix: the confidence pool of the step's cells, the logits
@@ -1429,7 +1617,7 @@ hipError_t enqueue_final(nd_needle* n, bool tail, bool select, const uint32_t* a
   if (pool_on(n) && (e = enqueue_pool(n, n->cells, d.layers + 1, n->scores, s)) != hipSuccess)
     return e;
   if (!tail) return hipSuccess;
-  e = nd_launch_matvec(n->embedding, n->fin, 1, d.dim, 0, d.vocab, n->logits, d.vocab, s);
+  e = mv_any(n->embedding, n->fin, 0, d.vocab, n->logits, s);
   if (e != hipSuccess || !select) return e;
   return nd_launch_select_list(n->logits, d.vocab, allowed, count, n->sel_id, n->sel_lp, s);
 }
@@ -1465,7 +1653,52 @@ BeginArgs begin_args(nd_needle* n) {
   b.inv_freq = n->inv_freq;
   b.rope = n->rope;
   b.cell0 = pool_on(n) ? n->cells : nullptr;
+  b.cq_lookup = n->cq ? n->cq_lookup : nullptr;
   return b;
+}
+
+// The gathers of a Cactus-Quant model's step: the embedding row of *token
+// (token null: none) and the engram table rows of `lookup`.
+hipError_t enqueue_cq_rows(nd_needle* n, const uint32_t* token, const uint32_t* lookup,
+                           hipStream_t s) {
+  const nd_needle_desc& d = n->d;
+  CqRowsArgs a{};
+  const nd_mat* e = n->embedding;
+  a.emb_p = e->packed;
+  a.emb_n = e->norms;
+  a.emb_kpad = e->kpad;
+  a.emb_row_bytes = e->row_bytes;
+  a.g = e->g;
+  a.bits = e->bits;
+  a.inverse_root = 1.0 / std::sqrt((double)e->g);
+  for (int i = 0; i < 16; ++i) a.cb[i] = e->cb[i];
+  if (e->bits == nd::kCqTernaryBits) {  // dequantizeCqRow's table: c = f32(1.2240064 * 1/sqrt(g))
+    const float c = (float)(1.2240064 * a.inverse_root);
+    a.cb[0] = 0.f;
+    a.cb[1] = c;
+    a.cb[2] = 0.f;
+    a.cb[3] = -c;
+  }
+  for (uint32_t si = 0; si < d.n_sites; ++si) {
+    a.tab_p[si] = n->eg_tables[si]->packed;
+    a.tab_n[si] = n->eg_tables[si]->norms;
+    a.tab_kpad = n->eg_tables[si]->kpad;
+    a.tab_row_bytes = n->eg_tables[si]->row_bytes;
+  }
+  a.token = token;
+  a.lookup = lookup;
+  a.d = d.dim;
+  a.lanes = d.lanes;
+  a.scale = std::sqrt((double)d.dim);
+  a.x = n->x;
+  a.cell0 = pool_on(n) ? n->cells : nullptr;
+  a.n_sites = d.n_sites;
+  a.tables = d.engram_tables;
+  a.slots = d.engram_slots;
+  a.sub = d.engram_sub;
+  a.cat = n->cat;
+  hipLaunchKernelGGL(n2_cq_rows_kernel, dim3(1 + d.n_sites * d.engram_tables), dim3(256), 0, s, a);
+  return hipGetLastError();
 }
 
 // The engram projections of the gathered rows in n->cat (runtime.ts:837-843)
@@ -1475,8 +1708,8 @@ hipError_t enqueue_engrams(nd_needle* n, hipStream_t s) {
   const nd_needle_desc& d = n->d;
   const uint32_t D = d.dim, cat = d.engram_tables * d.engram_sub;
   for (uint32_t si = 0; si < d.n_sites; ++si) {
-    const hipError_t e = nd_launch_matvec(&n->ekv[si], n->cat + (size_t)si * cat, 1, cat, 0,
-                                          2 * D, n->ekv_out + (size_t)si * 2 * D, 2 * D, s);
+    const hipError_t e =
+        mv_any(&n->ekv[si], n->cat + (size_t)si * cat, 0, 2 * D, n->ekv_out + (size_t)si * 2 * D, s);
     if (e != hipSuccess) return e;
   }
   if (!d.n_sites) return hipSuccess;
@@ -1498,6 +1731,9 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
   hipLaunchKernelGGL(n2_begin_kernel, dim3(1), dim3(kWg), 0, s, b);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (n->cq && (e = enqueue_cq_rows(n, n->cq_lookup + 2 * b.tables, n->cq_lookup, s)) !=
+                   hipSuccess)
+    return e;
   if ((e = enqueue_engrams(n, s)) != hipSuccess) return e;
   const bool tail = want_logits || select;
   // Launch l (l <= layers) runs post(l - 1) and pre(l); the last one runs
@@ -1729,7 +1965,7 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
       m.r_b_post = n->params + n->o_bpost + (size_t)l * ln;
       m.r_b_res = n->params + n->o_bres + (size_t)l * ln * ln;
     }
-    hipLaunchKernelGGL(n2_mix_kernel, dim3(rows), dim3(kMixWg), 0, s, m);
+    hipLaunchKernelGGL(n2_mix_kernel<false>, dim3(rows), dim3(kMixWg), 0, s, m);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (!pre) break;
     if ((e = nd_launch_digitize(n->pf_ain, D, nullptr, nullptr, n->pf_digits, n->pf_fm, M, D, s)) !=
@@ -1777,7 +2013,10 @@ nd_status run_prompt(nd_ctx* ctx, nd_needle* n, uint32_t count, bool want_logits
   uint32_t done = 0;
   while (done < count) {
     const uint32_t left = count - done;
-    const uint32_t room = n->kv.alloc > n->position ? n->kv.alloc - n->position : 0;
+    // The batched passes run int8 GEMMs; a Cactus-Quant model steps every
+    // prompt token (as NeedleRuntime.prefill does, runtime.ts:227-243).
+    const uint32_t room =
+        !n->cq && n->kv.alloc > n->position ? n->kv.alloc - n->position : 0;
     const uint32_t chunk = std::min(std::min(left, n->pf_cap), room);
     const bool last_pass = chunk == left;
     if (chunk > 0) {
@@ -1876,7 +2115,19 @@ nd_status nd_needle_create(nd_ctx* ctx, const nd_needle_desc* d, nd_needle** out
   if (d->n_sites && (cat < 128 || cat > 8192 || (cat & (cat - 1))))
     return nd_fail(ctx, ND_ERR_INVALID,
                    "engram tables x sub must be a power of two in [128, 8192]");
+  // Every matrix in one form: per-row-scaled int8, or (the shipped archive,
+  // model/cact.ts:398-562) Cactus-Quant with groups of at most 2048 (rotated
+  // inside the matvec), all of one width and group size.
+  const bool cq = d->embedding && d->embedding->bits != 0;
   auto check = [&](const nd_mat* m, uint32_t n, uint32_t k, const char* what) -> nd_status {
+    if (cq) {
+      if (!m || !m->bits || m->n != n || m->k != k || m->g > 2048 ||
+          m->bits != d->embedding->bits || m->g != d->embedding->g)
+        return nd_fail(ctx, ND_ERR_INVALID,
+                       "%s must be a %ux%u Cactus-Quant matrix of the embedding's width and group "
+                       "(group <= 2048)", what, n, k);
+      return ND_OK;
+    }
     if (!m || m->bits || m->n != n || m->k != k || m->g != k)
       return nd_fail(ctx, ND_ERR_INVALID, "%s must be a per-row-scaled %ux%u int8 matrix", what,
                      n, k);
@@ -1902,6 +2153,8 @@ nd_status nd_needle_create(nd_ctx* ctx, const nd_needle_desc* d, nd_needle** out
       return st;
   if (d->n_sites && (!d->eg_tables || !d->eg_key || !d->eg_value || !d->eg_taps))
     return nd_fail(ctx, ND_ERR_INVALID, "engram arrays must not be NULL");
+  if (cq && d->n_sites && (d->engram_sub + 31) / 32 * 32 > kCqRowMax)
+    return nd_fail(ctx, ND_ERR_INVALID, "Cactus-Quant engram rows wider than %u", kCqRowMax);
   for (uint32_t s = 0; s < d->n_sites; ++s)
     if ((st = check(d->eg_tables[s], d->engram_tables * d->engram_slots, d->engram_sub,
                     "engram tables")) ||
@@ -1917,6 +2170,7 @@ nd_status nd_needle_create(nd_ctx* ctx, const nd_needle_desc* d, nd_needle** out
 
   nd_needle* n = new nd_needle();
   n->d = *d;
+  n->cq = cq;
   n->embedding = d->embedding;
   n->phi_pre = d->phi_pre;
   n->phi_post = d->phi_post;
@@ -1926,6 +2180,29 @@ nd_status nd_needle_create(nd_ctx* ctx, const nd_needle_desc* d, nd_needle** out
     m.n = 0;
     for (size_t i = 0; i < count; ++i) m.n += parts[i]->n;
     m.k = parts[0]->k;
+    if (cq) {  // rows of packed codes and of norms, one after the other
+      const nd_mat* p0 = parts[0];
+      m.g = p0->g;
+      m.bits = p0->bits;
+      m.kpad = p0->kpad;
+      m.row_bytes = p0->row_bytes;
+      for (int i = 0; i < 16; ++i) m.cb[i] = p0->cb[i];
+      const size_t nb = (size_t)(m.kpad / m.g) * 2;  // norm bytes per row
+      if (e == hipSuccess) e = hipMalloc(&m.packed, (size_t)m.n * m.row_bytes);
+      if (e == hipSuccess) e = hipMalloc(&m.norms, (size_t)m.n * nb);
+      size_t row = 0;
+      for (size_t i = 0; i < count; ++i) {
+        const nd_mat* p = parts[i];
+        if (e == hipSuccess)
+          e = hipMemcpyAsync(m.packed + row * m.row_bytes, p->packed, (size_t)p->n * m.row_bytes,
+                             hipMemcpyDeviceToDevice, ctx->stream);
+        if (e == hipSuccess)
+          e = hipMemcpyAsync(reinterpret_cast<char*>(m.norms) + row * nb, p->norms,
+                             (size_t)p->n * nb, hipMemcpyDeviceToDevice, ctx->stream);
+        row += p->n;
+      }
+      return;
+    }
     m.g = m.k;
     if (e == hipSuccess) e = hipMalloc(&m.w, (size_t)m.n * m.k);
     if (e == hipSuccess) e = hipMalloc(&m.scales, (size_t)m.n * 4);
@@ -2019,6 +2296,8 @@ nd_status nd_needle_free(nd_ctx* ctx, nd_needle* n) {
     for (auto& m : *v) {
       if (m.w) hipFree(m.w);
       if (m.scales) hipFree(m.scales);
+      if (m.packed) hipFree(m.packed);
+      if (m.norms) hipFree(m.norms);
     }
   if (n->params) hipFree(n->params);
   if (n->inv_freq) hipFree(n->inv_freq);
@@ -2065,7 +2344,8 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
                             cb * al((size_t)(d.layers + 1) * D * 4),
                             cb * al((size_t)(d.layers + 1) * P8), cb * al(64), al(32 * 4),
                             al((size_t)2 * S * D * 4),
-                            al((size_t)(3 * D + ln * D + ln + ln * ln) * 4)};
+                            al((size_t)(3 * D + ln * D + ln + ln * ln) * 4),
+                            al((2 * 16 + 1) * 4), al((size_t)(2 * qw + 2 * kw) * 4)};
     size_t total = 0;
     for (size_t v : sizes) total += v;
     ND_HIP(ctx, hipMalloc(&n->arena, total));
@@ -2118,6 +2398,8 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     take(&n->lookup);
     take(&n->host_eng);
     take(&n->fwd_in);
+    take(&n->cq_lookup);
+    take(&n->cq_proj);
   }
   if (!n->pinned) {
     // Pinned staging of the session calls' host inputs.
@@ -2399,8 +2681,12 @@ nd_status nd_needle_prepare_engrams(nd_ctx* ctx, nd_needle* n, const uint32_t* i
   hipStream_t s = ctx->stream;
   ND_HIP(ctx, stage_copy(n, kStageLookup, n->lookup, buf, (size_t)2 * tables * 4, 0, s));
   ND_HIP(ctx, enqueue_position(n, position, s));
-  hipLaunchKernelGGL(n2_gather_kernel, dim3(1), dim3(kWg), 0, s, begin_args(n), n->lookup);
-  ND_HIP(ctx, hipGetLastError());
+  if (n->cq) {
+    ND_HIP(ctx, enqueue_cq_rows(n, nullptr, n->lookup, s));
+  } else {
+    hipLaunchKernelGGL(n2_gather_kernel, dim3(1), dim3(kWg), 0, s, begin_args(n), n->lookup);
+    ND_HIP(ctx, hipGetLastError());
+  }
   ND_HIP(ctx, enqueue_engrams(n, s));
   n->engrams_ready = true;
   return ND_OK;

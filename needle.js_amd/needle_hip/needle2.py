@@ -58,11 +58,25 @@ class ProbeHead:
 
 
 class Needle2Weights:
-    def __init__(self, g: Needle2Geometry, run_seed: int = 2026):
+    """Seeded Needle 2 weights: every matrix per-row-scaled int8, or with
+    cq_bits (2, 3, 4, or 5 for ternary) the shipped archive's Cactus-Quant
+    form (model/cact.ts:398-562) of that width with groups of cq_group."""
+
+    def __init__(self, g: Needle2Geometry, run_seed: int = 2026, cq_bits: int = 0,
+                 cq_group: int = 32):
         self.geometry = g
         L, d, hd = g.layers, g.dim, g.head_dim
+        if cq_bits:
+            from .cact import CqMatrix
+
+            cb = synth.cq_codebook()
+            books = {2: cb[0:4], 3: cb[4:12], 4: cb[12:28]}
 
         def mat(name, n, k):
+            if cq_bits:
+                packed, norms = synth.cq_matrix(run_seed, name, n, k, cq_group, cq_bits,
+                                                norm_lo=0.05, norm_hi=0.25)
+                return CqMatrix(packed, norms, books, n, k, cq_group, cq_bits)
             w, s = synth.int8_matrix(run_seed, name, n, k, k)
             return Int8Matrix(w, s, k, name)
 

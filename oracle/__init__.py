@@ -454,7 +454,8 @@ class SynthDecoder:
 # ------------------------------------------------------------------ Needle 2
 
 class _N2Mat(C.Structure):
-    _fields_ = [("w", P), ("s", P), ("n", U32), ("k", U32)]
+    _fields_ = [("w", P), ("s", P), ("n", U32), ("k", U32), ("bits", U32), ("g", U32),
+                ("packed", P), ("norms", P), ("codebook", P)]
 
 
 class _N2Model(C.Structure):
@@ -509,10 +510,20 @@ class Needle2:
         self._keep = []
 
         def om(m):
+            if getattr(m, "kind", None) == "cq":  # the archive's Cactus-Quant matrix
+                cb = np.zeros(28, np.float32)  # CQ2 [0, 4), CQ3 [4, 12), CQ4 [12, 28)
+                for bits, off in ((2, 0), (3, 4), (4, 12)):
+                    if bits in m.codebooks:
+                        cb[off:off + (1 << bits)] = m.codebooks[bits]
+                packed = np.ascontiguousarray(m.packed, np.uint8)
+                norms = np.ascontiguousarray(m.norms, np.uint16)
+                self._keep += [cb, packed, norms]
+                return _N2Mat(None, None, m.output_size, m.input_size, m.bits, m.group_size,
+                              _p(packed), _p(norms), _p(cb))
             c = np.ascontiguousarray(m.codes, np.int8)
             s = np.ascontiguousarray(m.scales, np.float32)
             self._keep += [c, s]
-            return _N2Mat(_p(c), _p(s), c.shape[0], c.shape[1])
+            return _N2Mat(_p(c), _p(s), c.shape[0], c.shape[1], 0, 0, None, None, None)
 
         def arr(ms):
             a = (_N2Mat * max(1, len(ms)))(*[om(m) for m in ms])

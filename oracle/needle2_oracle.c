@@ -1,7 +1,9 @@
 /*
  * needle2_oracle.c -- CPU restatement of NeedleRuntime.step for the full
- * Needle 2 graph (model/runtime.ts:280-583 of needle.js, CPU path), with the
- * int8 form of every CQ matrix.  TEST INFRASTRUCTURE ONLY (see
+ * Needle 2 graph (model/runtime.ts:280-583 of needle.js, CPU path), each
+ * matrix either in the int8 form or as the archive's Cactus-Quant matrix
+ * (backends/cq.ts:106-295 through or_cq_matvec / or_cq_row).  TEST
+ * INFRASTRUCTURE ONLY (see
  * needle_oracle.c for the semantics rules: binary64, no contraction, f32
  * stores).  Builds into liboracle.so with needle_oracle.c.
  *
@@ -35,6 +37,11 @@ int or_matvec_i8(const int8_t* w, const float* scales, uint32_t n, uint32_t k, u
                  const float* x, uint32_t batch, uint32_t row_start, uint32_t row_count, float* y);
 int or_row_i8(const int8_t* w, const float* scales, uint32_t n, uint32_t k, uint32_t g,
               uint32_t row, float* out);
+int or_cq_matvec(const uint8_t* packed, const uint16_t* norms, const float* codebook, uint32_t n,
+                 uint32_t k, uint32_t g, uint32_t bits, const float* x, uint32_t batch,
+                 uint32_t row_start, uint32_t row_count, float* y);
+int or_cq_row(const uint8_t* packed, const uint16_t* norms, const float* codebook, uint32_t n,
+              uint32_t k, uint32_t g, uint32_t bits, uint32_t row, float* out);
 typedef struct or_kv or_kv;
 or_kv* or_kv_create(uint32_t layers, uint32_t kv_heads, uint32_t head_dim, uint32_t max_length,
                     uint32_t sink, uint32_t window, int float_mode);
@@ -43,10 +50,17 @@ int or_kv_store(or_kv* kv, uint32_t layer, uint32_t position, const float* k, co
 int or_attention(const or_kv* kv, uint32_t layer, uint32_t position, const float* q,
                  uint32_t q_heads, float* out);
 
+/* A matrix [n][k]: int8 codes w with per-row scales s, or (bits != 0) the
+ * archive's Cactus-Quant form -- packed rows, binary16 norms [n][kpad / g]
+ * and the 28-float codebook (CQ2, CQ3, CQ4) -- with w and s unused. */
 typedef struct {
   const int8_t* w;
   const float* s;
   uint32_t n, k;
+  uint32_t bits, g;
+  const uint8_t* packed;
+  const uint16_t* norms;
+  const float* codebook;
 } n2_mat;
 
 typedef struct {
@@ -111,8 +125,21 @@ typedef struct {
   uint32_t cells_count, cells_cap;
 } n2_state;
 
+/* matvec (backends/cpu.ts:12-26, or cq.ts:106-231 for a CQ matrix). */
 static void mv(const n2_mat* m, const float* x, uint32_t row_start, uint32_t rows, float* y) {
-  or_matvec_i8(m->w, m->s, m->n, m->k, m->k, x, 1, row_start, rows, y);
+  if (m->bits)
+    or_cq_matvec(m->packed, m->norms, m->codebook, m->n, m->k, m->g, m->bits, x, 1, row_start,
+                 rows, y);
+  else
+    or_matvec_i8(m->w, m->s, m->n, m->k, m->k, x, 1, row_start, rows, y);
+}
+
+/* row (backends/cpu.ts:28-31, or dequantizeCqRow, cq.ts:243-295). */
+static void mat_row(const n2_mat* m, uint32_t row, float* out) {
+  if (m->bits)
+    or_cq_row(m->packed, m->norms, m->codebook, m->n, m->k, m->g, m->bits, row, out);
+  else
+    or_row_i8(m->w, m->s, m->n, m->k, m->k, row, out);
 }
 
 /* runtime.ts:150-225 reset: KV allocation (int8, or float32 with
@@ -279,8 +306,7 @@ int or_n2_step(n2_state* st, uint32_t token, float* logits) {
   float* evals = (float*)calloc((size_t)md->n_sites * d, sizeof(float));
 
   /* runtime.ts:305-313 */
-  or_row_i8(md->embedding.w, md->embedding.s, md->embedding.n, md->embedding.k,
-            md->embedding.k, token, emb);
+  mat_row(&md->embedding, token, emb);
   double es = sqrt((double)d);
   for (uint32_t i = 0; i < d; i++) emb[i] = (float)((double)emb[i] * es);
   pool_add(st, emb); /* runtime.ts:310 */
@@ -298,8 +324,7 @@ int or_n2_step(n2_state* st, uint32_t token, float* logits) {
       for (uint32_t t = 0; t < md->engram_tables; t++)
         if (valid[t]) {
           const n2_mat* tb = &md->eg_tables[s];
-          or_row_i8(tb->w, tb->s, tb->n, tb->k, tb->k, t * md->engram_slots + indices[t],
-                    cat + t * md->engram_sub);
+          mat_row(tb, t * md->engram_slots + indices[t], cat + t * md->engram_sub);
         }
       mv(&md->eg_key[s], cat, 0, d, ekeys + s * d);
       float* value_now = tmp;

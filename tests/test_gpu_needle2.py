@@ -295,6 +295,59 @@ def test_generate_full_geometry_greedy_identical(hip):
         model.dispose()
 
 
+@pytest.mark.parametrize("cq_bits,sink", [(4, 3), (3, 0), (2, 0), (5, 3)])
+def test_cactus_quant_model_steps_prefill_and_generate(hip, cq_bits, sink):
+    """The resident runtime over Cactus-Quant matrices, the form every matrix
+    of the shipped archive takes (model/cact.ts:398-562, backends/cq.ts:106-295):
+    step logits, the cache and the confidence against the oracle's cqMatvec /
+    dequantizeCqRow restatement, a prompt (stepped, as the reference's
+    prefill does) and a greedy continuation with identical ids."""
+    say("needle2 cactus-quant", cq_bits, sink)
+    w = Needle2Weights(SMALL, 51, cq_bits=cq_bits)
+    model = NeedleModel(hip, w)
+    try:
+        rt = model.create_resident_runtime()
+        rt.reset(SMALL.max_length, sink)
+        ref = oracle.Needle2(w).runtime(SMALL.max_length, sink)
+        ref.capture_kv(0, SMALL.max_length)
+        tokens = synth.Stream(6, f"cq{cq_bits}").integers(14, 0, SMALL.vocab - 1)
+        tokens[8:10] = tokens[2:4]  # repeated n-grams hit the same engram rows
+        for i, t in enumerate(tokens):
+            close(rt.step(int(t)), ref.step(int(t)), ("cq step", cq_bits, i))
+        close_confidence(rt.resolve_confidence(), ref.confidence(), ("cq confidence", cq_bits))
+        check_kv(model, ref, SMALL, len(tokens), sink, f"cq{cq_bits} steps")
+        # A prompt and greedy tokens through the generate path (graph replays).
+        prompt = synth.Stream(7, f"cqp{cq_bits}").integers(12, 0, SMALL.vocab - 1)
+        res = model.generate_resident(prompt, max_new_tokens=10, eos=None)
+        ref2 = oracle.Needle2(w).runtime(12 + 10, 0)
+        for t in prompt[:-1]:
+            ref2.step(int(t), want_logits=False)
+        logits = ref2.step(int(prompt[-1]))
+        ids = []
+        for k in range(10):
+            tok = oracle.argmax(logits)
+            ids.append(tok)
+            if k + 1 < 10:
+                logits = ref2.step(tok)
+        assert res.token_ids == ids, (cq_bits, res.token_ids, ids)
+    finally:
+        model.dispose()
+
+
+def test_cactus_quant_model_rejects_mixed_forms(hip):
+    """Every matrix of a model takes one form: a Cactus-Quant embedding with
+    an int8 projection is refused with the matrix named."""
+    w = Needle2Weights(SMALL, 52, cq_bits=4)
+    w.wq[1] = Needle2Weights(SMALL, 52).wq[1]
+    model = NeedleModel(hip, w)
+    try:
+        with pytest.raises(NeedleError) as e:
+            model.create_resident_runtime()
+        assert "wq" in str(e.value) and "Cactus-Quant" in str(e.value)
+    finally:
+        model.dispose()
+
+
 def test_confidence_absent_or_disabled(hip):
     say("needle2 confidence disabled")
     w = Needle2Weights(SMALL, 32)

@@ -92,6 +92,31 @@ def test_session_token_equals_whole_step(small):
     rt.dispose()
 
 
+def test_session_token_equals_whole_step_cactus_quant(hip):
+    """The session methods over a Cactus-Quant model (the shipped archive's
+    form): the host-driven step (embedding row through nd_row, engram rows
+    gathered from the host's lookups) gives the whole step's logits bit for
+    bit, and both agree with the oracle."""
+    say("session token == whole step, cactus-quant")
+    w = Needle2Weights(SMALL, 61, cq_bits=4)
+    model = NeedleModel(hip, w)
+    try:
+        rt = model.create_runtime()
+        rt.reset(SMALL.max_length, 2)
+        whole = model.create_resident_runtime()
+        whole.reset(SMALL.max_length, 2)
+        ref = oracle.Needle2(w).runtime(SMALL.max_length, 2)
+        tokens = synth.Stream(8, "sess-cq").integers(16, 0, SMALL.vocab - 1)
+        tokens[9:11] = tokens[3:5]
+        for i, t in enumerate(tokens):
+            got = rt.step(int(t))
+            assert np.array_equal(bits(got), bits(whole.step(int(t)))), i
+            close(got, ref.step(int(t)), i)
+        rt.dispose()
+    finally:
+        model.dispose()
+
+
 def test_layer_granularity_and_lane_reads(small):
     """forward_resident_layer per layer, with readResidentLanes between two
     layers, gives the same token as forward_resident_token."""

@@ -25,7 +25,26 @@ SMALL = Needle2Geometry(vocab=256, dim=128, heads=4, kv_heads=2, layers=3, head_
 
 
 def dense(m):
-    return m.codes.astype(np.float64) * m.scales.astype(np.float64)
+    """The matrix a step multiplies by, float64: int8 codes times row scales,
+    or for a Cactus-Quant matrix (cq.ts:243-295 read as linear algebra) per
+    row and group H_g (codebook[code] * norm) / sqrt(g), H_g the Sylvester
+    Hadamard matrix -- the rotation cqMatvec applies to the input instead."""
+    if getattr(m, "kind", None) != "cq":
+        return m.codes.astype(np.float64) * m.scales.astype(np.float64)
+    n, kpad, g = m.output_size, m.input_size_padded, m.group_size
+    raw = np.unpackbits(m.packed.reshape(n, -1), axis=1, bitorder="little")
+    pb = 2 if m.bits == 5 else m.bits
+    codes = raw.reshape(n, kpad, pb) @ (1 << np.arange(pb))  # little-endian fields
+    if m.bits == 5:  # crumbs 0, 1, 2, 3 -> 0, +c, 0, -c, c = 1.2240064 / sqrt(g)
+        c = 1.2240064 / np.sqrt(g)
+        values = np.array([0.0, c, 0.0, -c])[codes]
+    else:
+        values = m.codebooks[m.bits].astype(np.float64)[codes]
+    norms = m.norms.view(np.float16).astype(np.float64)  # [n][kpad / g]
+    scaled = values * np.repeat(norms, g, axis=1)
+    h = hadamard(g).astype(np.float64) / np.sqrt(g)
+    rows = (scaled.reshape(n, kpad // g, g) @ h.T).reshape(n, kpad)
+    return rows[:, :m.input_size]
 
 
 class NumpyNeedle2:
@@ -162,9 +181,11 @@ class NumpyNeedle2:
         return dense(w.embedding) @ self.rms(x.mean(axis=0), w.final_norm)
 
 
-@pytest.mark.parametrize("sink", [0, 3])
-def test_step_matches_float64_model(sink):
-    w = Needle2Weights(SMALL, 9)
+@pytest.mark.parametrize("sink,cq_bits", [(0, 0), (3, 0), (0, 4), (3, 3), (0, 2), (0, 5)])
+def test_step_matches_float64_model(sink, cq_bits):
+    """Int8 weights, and the Cactus-Quant widths of the shipped archive (the
+    oracle runs cqMatvec / dequantizeCqRow on them)."""
+    w = Needle2Weights(SMALL, 9, cq_bits=cq_bits)
     model = oracle.Needle2(w)
     rt = model.runtime(SMALL.max_length, sink)
     ref = NumpyNeedle2(w, SMALL.max_length, sink)
