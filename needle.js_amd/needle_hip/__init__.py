@@ -10,7 +10,7 @@ from .backend import HipBackend, Int8Matrix, MatrixRowRange, MatvecRequest
 from .cact import CactArchive, CqMatrix, pack_codes, parse_cact, write_cact
 from .errors import NeedleError, invariant
 from .kv import HipKvCache
-from .needle2 import Needle2Geometry, Needle2Weights
+from .needle2 import Needle2Geometry, Needle2Weights, weights_from_cact
 from .runtime import (AbortSignal, GenerationResult, HipNeedleSession, Needle2Resident,
                       NeedleModel, NeedleRuntime, ResidentRuntime, RuntimeOptions)
 
@@ -24,6 +24,7 @@ __all__ = [
     "Needle2Resident",
     "Needle2Geometry",
     "Needle2Weights",
+    "weights_from_cact",
     "NeedleModel",
     "NeedleRuntime",
     "ResidentRuntime",

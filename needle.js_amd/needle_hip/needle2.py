@@ -57,6 +57,58 @@ class ProbeHead:
         assert self.projection.shape == (self.output_size, self.probe_count * dim)
 
 
+def weights_from_cact(w) -> "Needle2Weights":
+    """The runtime's weights from a parsed .cact archive (CactWeights,
+    cact.ts:114-138, from parse_cact_weights): the archive's Cactus-Quant
+    matrices as they are, the per-layer dense tensors stacked, the geometry
+    from the header (cact.ts:398-562, runtime.ts:150-225)."""
+    h = w.geometry
+    g = Needle2Geometry(
+        vocab=h["vocabulary_size"], dim=h["model_dimension"], heads=h["number_of_heads"],
+        kv_heads=h["number_of_kv_heads"], layers=h["number_of_layers"],
+        head_dim=h["head_dimension"], max_length=h["maximum_sequence_length"],
+        hadamard=h["hadamard_dimension"], lanes=h["mhc_lanes"], engram_slots=h["engram_slots"],
+        engram_sub=h["engram_sub_dimension"], engram_tables=h["number_of_engram_tables"],
+        engram_taps=h["engram_convolution_taps"], orders=tuple(h["engram_orders"]),
+        sites=tuple(h["engram_layers"]), rope_theta=float(h["rope_theta"]),
+        kv_window=h["kv_window"])
+    out = Needle2Weights.__new__(Needle2Weights)
+    out.geometry = g
+    out.embedding = w.embedding
+    layers = w.layers
+    out.wq = [l.query_projection for l in layers]
+    out.wk = [l.key_projection for l in layers]
+    out.wv = [l.value_projection for l in layers]
+    out.wgate = [l.gate_projection for l in layers]
+    out.wo = [l.output_projection for l in layers]
+
+    def stack(name):
+        return np.stack([np.asarray(getattr(l, name), np.float32).reshape(-1) for l in layers])
+
+    out.norm_input = stack("norm_input")
+    out.query_norm = stack("query_norm")
+    out.key_norm = stack("key_norm")
+    out.post_attn_norm = stack("post_attention_norm")
+    out.attention_gate = np.array([l.attention_gate for l in layers], np.float32)
+    out.pre_hadamard_norm = stack("pre_hadamard_norm")
+    out.d1, out.d2, out.d3 = stack("hadamard_d1"), stack("hadamard_d2"), stack("hadamard_d3")
+    out.phi_pre, out.phi_post, out.phi_res = w.mhc_phi_pre, w.mhc_phi_post, w.mhc_phi_residual
+    f32 = lambda v: np.asarray(v, np.float32).reshape(-1)  # noqa: E731
+    out.a_pre, out.a_post, out.a_res = f32(w.mhc_a_pre), f32(w.mhc_a_post), f32(w.mhc_a_residual)
+    out.b_pre, out.b_post, out.b_res = f32(w.mhc_b_pre), f32(w.mhc_b_post), f32(w.mhc_b_residual)
+    out.eg_tables = [e.tables for e in w.engrams]
+    out.eg_key = [e.key_projection for e in w.engrams]
+    out.eg_value = [e.value_projection for e in w.engrams]
+    out.eg_taps = (np.stack([np.asarray(e.taps, np.float32).reshape(g.engram_taps, g.dim)
+                             for e in w.engrams]) if w.engrams
+                   else np.zeros((0, g.engram_taps, g.dim), np.float32))
+    out.final_norm = np.asarray(w.final_norm, np.float32).reshape(-1)
+    head = w.heads.get("confidence")
+    out.confidence = (ProbeHead(head.probes, head.projection, np.asarray(head.bias).reshape(-1))
+                      if head is not None else None)
+    return out
+
+
 class Needle2Weights:
     """Seeded Needle 2 weights: every matrix per-row-scaled int8, or with
     cq_bits (2, 3, 4, or 5 for ternary) the shipped archive's Cactus-Quant

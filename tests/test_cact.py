@@ -16,6 +16,8 @@ from needle_hip import CqMatrix, NeedleError, parse_cact, synth, write_cact
 from needle_hip import cact as K
 from needle_hip.cact import parse_cact_weights, synthetic_needle2_archive
 
+import oracle
+
 
 def test_rejects_truncated_header():
     with pytest.raises(NeedleError, match="(?i)header") as e:
@@ -135,6 +137,25 @@ N2_GEOMETRY = dict(kv_window=8, kv_bits=8, vocabulary_size=256, model_dimension=
                    engram_slots=64, engram_sub_dimension=32, number_of_engram_tables=4,
                    engram_convolution_taps=4, engram_convolution_dilation=1,
                    engram_orders=[2, 3], engram_layers=[0, 1], rope_theta=10000.0)
+
+
+def test_archive_weights_for_the_runtime_step_on_the_oracle():
+    """weights_from_cact maps a parsed archive onto the runtime's weight
+    layout: the oracle steps it, and its float64 model (dequantized CQ
+    matrices) agrees."""
+    from needle_hip.needle2 import weights_from_cact
+    from test_oracle_needle2 import NumpyNeedle2
+
+    w = weights_from_cact(parse_cact_weights(synthetic_needle2_archive(N2_GEOMETRY, 3)))
+    g = w.geometry
+    assert (g.vocab, g.dim, g.layers, g.sites, g.orders) == (256, 128, 2, (0, 1), (2, 3))
+    assert w.norm_input.shape == (2, 128) and w.d2.shape == (2, 128) and len(w.eg_tables) == 2
+    assert w.confidence is not None and w.confidence.probe_count == 8
+    rt = oracle.Needle2(w).runtime(g.max_length, 0)
+    ref = NumpyNeedle2(w, g.max_length, 0)
+    for t in (5, 200, 17, 5, 200, 64):
+        got, want = rt.step(t), ref.step(t)
+        assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max(), t
 
 
 def test_needle2_archive_named_structure():

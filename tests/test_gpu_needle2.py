@@ -334,6 +334,50 @@ def test_cactus_quant_model_steps_prefill_and_generate(hip, cq_bits, sink):
         model.dispose()
 
 
+@pytest.mark.parametrize("bits", [4, 5])
+def test_cact_archive_through_the_resident_runtime(hip, bits):
+    """A .cact archive in the shipped layout (synthetic weights, the
+    reference's tensor order) parsed by parse_cact_weights and run as is --
+    Cactus-Quant matrices, its geometry, its confidence head: step logits and
+    confidence against the oracle on the same archive, then a greedy
+    generate."""
+    from needle_hip.cact import parse_cact_weights, synthetic_needle2_archive
+    from needle_hip.needle2 import weights_from_cact
+
+    say("needle2 cact archive", bits)
+    geo = dict(kv_window=8, kv_bits=8, vocabulary_size=512, model_dimension=128,
+               number_of_heads=4, number_of_kv_heads=2, number_of_layers=3, head_dimension=64,
+               maximum_sequence_length=48, hadamard_dimension=256, mhc_lanes=4,
+               engram_slots=64, engram_sub_dimension=128, number_of_engram_tables=4,
+               engram_convolution_taps=4, engram_convolution_dilation=1,
+               engram_orders=[2, 3], engram_layers=[0, 2], rope_theta=10000.0)
+    w = weights_from_cact(parse_cact_weights(synthetic_needle2_archive(geo, 17, bits=bits)))
+    g = w.geometry
+    model = NeedleModel(hip, w)
+    try:
+        rt = model.create_resident_runtime()
+        rt.reset(g.max_length, 2)
+        ref = oracle.Needle2(w).runtime(g.max_length, 2)
+        tokens = synth.Stream(9, f"cact{bits}").integers(12, 0, g.vocab - 1)
+        for i, t in enumerate(tokens):
+            close(rt.step(int(t)), ref.step(int(t)), ("archive step", bits, i))
+        close_confidence(rt.resolve_confidence(), ref.confidence(), ("archive confidence", bits))
+        prompt = synth.Stream(10, f"cactp{bits}").integers(10, 0, g.vocab - 1)
+        res = model.generate_resident(prompt, max_new_tokens=8, eos=None)
+        ref2 = oracle.Needle2(w).runtime(10 + 8, 0)
+        for t in prompt[:-1]:
+            ref2.step(int(t), want_logits=False)
+        logits = ref2.step(int(prompt[-1]))
+        ids = []
+        for k in range(8):
+            ids.append(oracle.argmax(logits))
+            if k + 1 < 8:
+                logits = ref2.step(ids[-1])
+        assert res.token_ids == ids
+    finally:
+        model.dispose()
+
+
 def test_cactus_quant_model_rejects_mixed_forms(hip):
     """Every matrix of a model takes one form: a Cactus-Quant embedding with
     an int8 projection is refused with the matrix named."""
