@@ -502,6 +502,66 @@ def needle2_token_bytes(g, visible):
     return g.layers * per_layer + engram + g.vocab * (g.dim + 4)
 
 
+def needle2_cq_token_bytes(g, visible, bits, group):
+    """HBM bytes one Needle 2 token reads with Cactus-Quant matrices of one
+    width: packed codes (bits per weight, ternary 2) + binary16 norms per
+    group of every matrix it multiplies, the engram rows it gathers and
+    `visible` K/V rows per layer and KV head."""
+    pb = 2 if bits == 5 else bits
+
+    def mat(n, k):
+        kpad = -(-k // group) * group
+        return n * (kpad * pb // 8 + kpad // group * 2)
+
+    qkvg = (2 * g.heads + 2 * g.kv_heads) * 64
+    per_layer = (mat(qkvg, g.dim) + mat(g.dim, g.heads * 64)
+                 + mat(2 * g.lanes + g.lanes * g.lanes, g.lanes * g.dim)
+                 + visible * g.kv_heads * (64 * 2 + 8))
+    cat = g.engram_tables * g.engram_sub
+    engram = len(g.sites) * (mat(2 * g.dim, cat) + mat(g.engram_tables, g.engram_sub))
+    return g.layers * per_layer + engram + mat(g.vocab, g.dim)
+
+
+def bench_needle2_cq(torch, hip, reps, bits=4, group=32):
+    """The same generate (shipped geometry, 128-token prompt, 64 greedy
+    tokens) with every matrix in the Cactus-Quant form of the shipped archive
+    (CQ4, groups of 32): products as cqMatvec, rows as dequantizeCqRow, the
+    prompt stepped token by token as NeedleRuntime.prefill does.  Timing only:
+    the GPU tests hold its parity with the oracle."""
+    import numpy as np
+
+    from needle_hip import NeedleModel, synth
+    from needle_hip.needle2 import Needle2Geometry, Needle2Weights
+    from needle_hip.runtime import EOS_TOKEN_ID
+
+    g = Needle2Geometry()
+    model = NeedleModel(hip, Needle2Weights(g, 2026, cq_bits=bits, cq_group=group))
+    prompt = synth.Stream(2026, "needle2.prompt").integers(128, 0, g.vocab - 1)
+    new = 64
+    model.generate_resident(prompt, new, eos=EOS_TOKEN_ID)
+    model.generate_resident(prompt, 1, eos=EOS_TOKEN_ID)
+    walls, walls1 = [], []
+    res = None
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        res = model.generate_resident(prompt, new, eos=EOS_TOKEN_ID)
+        walls.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        model.generate_resident(prompt, 1, eos=EOS_TOKEN_ID)
+        walls1.append(time.perf_counter() - t0)
+    wall, wall1 = float(np.median(walls)), float(np.median(walls1))
+    n_gen = res.generated_tokens
+    decode_ms = (wall - wall1) * 1e3 / max(1, n_gen - 1)
+    bytes_tok = needle2_cq_token_bytes(g, min(g.kv_window, 128 + n_gen // 2), bits, group)
+    part = {"bits": bits, "group": group, "prompt_tokens": 128, "generated_tokens": n_gen,
+            "reps": reps, "wall_ms": wall * 1e3, "tokens_per_s": n_gen / wall,
+            "decode_ms_per_token": decode_ms, "decode_tokens_per_s": 1e3 / decode_ms,
+            "prompt_128_stepped_ms": wall1 * 1e3, "bytes_per_token": bytes_tok,
+            "decode_GBps": bytes_tok / (decode_ms * 1e-3) / 1e9}
+    model.dispose()
+    return part
+
+
 def bench_needle2(torch, hip, reps, check, cpu_seconds):
     """Needle 2 at the shipped geometry (27 layers, vocab 8192, KV window
     256), batch 1: NeedleModel.generate of 64 greedy tokens from a 128-token
@@ -677,7 +737,8 @@ def main():
     ap.add_argument("--skip-needle2", action="store_true")
     ap.add_argument("--needle2-reps", type=int, default=5)
     ap.add_argument("--only", choices=["matvec", "matvec8", "attention", "decode", "prefill",
-                                       "needle2", "traffic", "cq", "grammar", "ceiling"],
+                                       "needle2", "needle2cq", "traffic", "cq", "grammar",
+                                       "ceiling"],
                     help="run one part alone and print its JSON (for profiling)")
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--no-check", action="store_true",
@@ -707,6 +768,8 @@ def main():
             part, _ = bench_constrained_decode(torch, hip, args.decode_steps, 2, False, 1, 0)
         elif args.only == "needle2":
             part, _ = bench_needle2(torch, hip, args.needle2_reps, False, 0)
+        elif args.only == "needle2cq":
+            part = bench_needle2_cq(torch, hip, args.needle2_reps)
         elif args.only == "ceiling":
             part = bench_read_ceiling(torch, hip)
         elif args.only == "traffic":
@@ -781,6 +844,10 @@ def main():
         print(f"[bench] needle2 generate b1 {part['tokens_per_s']:.0f} tok/s, decode "
               f"{part['decode_ms_per_token']:.3f} ms/token, greedy_identical="
               f"{part.get('greedy_identical')}", file=sys.stderr, flush=True)
+        part = bench_needle2_cq(torch, hip, args.needle2_reps)
+        parts["needle2_cq4_generate_b1"] = part
+        print(f"[bench] needle2 cq4 generate b1 {part['tokens_per_s']:.0f} tok/s, decode "
+              f"{part['decode_ms_per_token']:.3f} ms/token", file=sys.stderr, flush=True)
 
     part, cpu_gm = bench_grammar_mask(torch, hip, 20, 0 if args.skip_cpu else 5.0)
     if cpu_gm:

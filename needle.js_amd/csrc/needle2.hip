@@ -667,8 +667,36 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   }
   const float bpre = a.b_pre[min(lane, L - 1)];
   __shared__ float s_cb[16];
+  // Cactus-Quant phi rows: wave w takes rows w, w + 8 and w + 16, lane u the
+  // rows' 32-code unit u -- its packed words (UB / 4 of them) and the norms
+  // of its groups -- loaded here with the other operands.
+  uint32_t cw[3][4] = {}, cn[3][4] = {};
   if constexpr (CQ) {
-    if (t < 16) s_cb[t] = a.cq_cb[t];
+    if (t == 0) {  // constant indices into the argument block
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s_cb[i] = a.cq_cb[i];
+    }
+    const uint32_t ubw = a.cq_bits == 4 ? 4u : (a.cq_bits == 3 ? 3u : 2u);  // words per unit
+    const uint32_t gpu = a.cq_g >= 32 ? 1u : 32u / a.cq_g;               // groups per unit
+    const uint32_t ul = min(lane, N / 32 - 1);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const uint32_t r = min(wave + 8u * j, nrows - 1);
+      const uint32_t mat = r < L ? 0u : (r < 2 * L ? 1u : 2u);
+      const uint32_t rr = r - (mat == 0 ? 0u : (mat == 1 ? L : 2 * L));
+      // The matrix by selection (a runtime index into the argument block
+      // would copy it to scratch).
+      const uint8_t* pm = mat == 0 ? a.cq_p[0] : (mat == 1 ? a.cq_p[1] : a.cq_p[2]);
+      const uint16_t* nm = mat == 0 ? a.cq_n[0] : (mat == 1 ? a.cq_n[1] : a.cq_n[2]);
+      const uint32_t* prow =
+          reinterpret_cast<const uint32_t*>(pm + (size_t)rr * a.cq_row_bytes) + ul * ubw;
+      const uint16_t* nrow = nm + (size_t)rr * a.cq_groups + (ul * 32) / a.cq_g;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if ((uint32_t)k < ubw) cw[j][k] = prow[k];
+        if ((uint32_t)k < gpu) cn[j][k] = nrow[k];
+      }
+    }
   }
 
   // ---- post(l - 1)
@@ -754,8 +782,8 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     // phi = cqMatvec of the normalized lanes (backends/cq.ts:30-46, 107-231):
     // prepareCqActivation in LDS -- per group the butterflies, then times
     // 1/sqrt(g) -- and one wave per phi row, lane u taking the row's 32-code
-    // unit u: float64 dot per group times the group's norm, summed over the
-    // wave in float64.
+    // unit u (codes from the words loaded at entry): an fp32 dot per group
+    // times the group's norm, summed over the wave in float64.
     float* s_nl = reinterpret_cast<float*>(&s_split[0][0]);  // N <= 2048 floats
     if (col) {
 #pragma unroll
@@ -766,21 +794,35 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     nd::cq_fwht_groups(s_nl, N, a.cq_g);
     for (uint32_t i = t; i < N; i += kMixWg) s_nl[i] = (float)((double)s_nl[i] * a.cq_inv_root);
     __syncthreads();
-    for (uint32_t r = wave; r < nrows; r += kMixWg / 64) {
-      const uint32_t mat = r < L ? 0u : (r < 2 * L ? 1u : 2u);
-      const uint32_t rr = r - (mat == 0 ? 0u : (mat == 1 ? L : 2 * L));
-      const uint8_t* prow = a.cq_p[mat] + (size_t)rr * a.cq_row_bytes;
-      const uint16_t* nrow = a.cq_n[mat] + (size_t)rr * a.cq_groups;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const uint32_t r = wave + 8u * j;
+      if (r >= nrows) break;  // uniform over the wave
       double total = 0.0;
       if (lane < N / 32) {
-        double dot = 0.0;
-        for (uint32_t j = 0; j < 32; ++j) {
-          const uint32_t c = lane * 32 + j;
-          dot += (double)s_cb[nd::cq_code(prow, c, a.cq_bits)] * (double)s_nl[c];
-          if ((c + 1) % a.cq_g == 0 || j == 31) {  // end of a group, or of the unit
-            total += (double)nd::cq_half(nrow[c / a.cq_g]) * dot;
-            dot = 0.0;
+        // fp32 dots over the unit's four 8-code blocks, then each block times
+        // its group's norm (groups of 8, 16, or 32 and wider) in float64;
+        // every index is a constant, so the operands stay in registers.
+        const float* xu = s_nl + lane * 32;
+        float dot8[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (uint32_t c = 0; c < 32; ++c) {
+          uint32_t code;
+          if (a.cq_bits == 4) {
+            code = (cw[j][c >> 3] >> (4 * (c & 7))) & 15u;
+          } else if (a.cq_bits == 3) {
+            const uint32_t bit = 3 * c, w = bit >> 5, sh = bit & 31;
+            const uint32_t hi = sh > 29 ? cw[j][w + 1 < 4 ? w + 1 : 3] << (32 - sh) : 0u;
+            code = ((cw[j][w] >> sh) | hi) & 7u;
+          } else {  // 2-bit codes and ternary crumbs
+            code = (cw[j][c >> 4] >> (2 * (c & 15))) & 3u;
           }
+          dot8[c >> 3] = fmaf(s_cb[code], xu[c], dot8[c >> 3]);
+        }
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const uint32_t nb = a.cq_g == 8 ? cn[j][b] : (a.cq_g == 16 ? cn[j][b >> 1] : cn[j][0]);
+          total += (double)nd::cq_half(nb) * (double)dot8[b];
         }
       }
       total = nd::wave_sum(total);
