@@ -7,7 +7,8 @@ raises NeedleError("BACKEND_UNAVAILABLE").
 """
 
 from .backend import HipBackend, Int8Matrix, MatrixRowRange, MatvecRequest
-from .cact import CactArchive, CqMatrix, pack_codes, parse_cact, write_cact
+from .cact import (CactArchive, CqMatrix, pack_codes, parse_cact, parse_cact_weights,
+                   write_cact)
 from .errors import NeedleError, invariant
 from .kv import HipKvCache
 from .needle2 import Needle2Geometry, Needle2Weights, weights_from_cact
@@ -37,5 +38,6 @@ __all__ = [
     "invariant",
     "pack_codes",
     "parse_cact",
+    "parse_cact_weights",
     "write_cact",
 ]
