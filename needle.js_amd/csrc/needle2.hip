@@ -976,16 +976,54 @@ __device__ __forceinline__ void head_epilogue(float val, uint32_t lane, int role
   if (lane == 0) (role == 2 ? Vs : Ks)[crow] = (float)sc;
 }
 
+// Projection rows of the Q/K/V/gate launch: 64 rows of d <= 512 int8
+// columns per workgroup, kQkvTpr threads a row; thread q of row r holds
+// bytes [16 kQkvTpr k + 16 q, +16) of the row (k < 32 / kQkvTpr; clamped in
+// the row, blocks past d add nothing), so a wave's load covers whole
+// 16 kQkvTpr-byte row pieces.  qkv_row_dot takes the fp32 fmas against x in
+// LDS in that order and sums the row's threads.
+constexpr uint32_t kQkvTpr = 8;
+constexpr uint32_t kQkvLoads = 32 / kQkvTpr;
+constexpr int kQkvWg = 64 * kQkvTpr;
+
+__device__ __forceinline__ void qkv_row_loads(const int8_t* W, size_t row, uint32_t q,
+                                              uint32_t d, i32x4 (&w)[kQkvLoads]) {
+  const int8_t* p = W + row * d;
+#pragma unroll
+  for (uint32_t k = 0; k < kQkvLoads; ++k)
+    w[k] = __builtin_nontemporal_load(
+        reinterpret_cast<const i32x4*>(p + min(16u * kQkvTpr * k + 16u * q, d - 16)));
+}
+
+__device__ __forceinline__ float qkv_row_dot(const i32x4 (&w)[kQkvLoads], const float* xs,
+                                             uint32_t q, uint32_t d) {
+  float acc = 0.f;
+#pragma unroll
+  for (uint32_t k = 0; k < kQkvLoads; ++k) {
+    const uint32_t off = 16u * kQkvTpr * k + 16u * q;
+    if (off < d) {
+      int8_t cb[16];
+      __builtin_memcpy(cb, &w[k], 16);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc = fmaf((float)cb[j], xs[off + j], acc);
+    }
+  }
+  acc = nd::quad_sum(acc);
+  if constexpr (kQkvTpr >= 8) acc += nd::lane_xor<4>(acc);
+  if constexpr (kQkvTpr >= 16) acc += nd::lane_xor<8>(acc);
+  return acc;
+}
+
 // The fused Q/K/V/gate projection of one layer (runtime.ts:465-470) with the
 // per-head norm + RoPE of q and k (runtime.ts:471-500) and #storeKV
 // (runtime.ts:679-717) in the epilogue.  Workgroup b computes rows [64 b,
 // 64 b + 64) of wqkvg = [q (H*64) | k (Hkv*64) | v (Hkv*64) | gate (H*64)]:
-// four threads per row, fp32 accumulation of int8 x fp32 like the matvec,
-// times the row scale.  q heads go to q_out, k and v heads are quantized into
+// eight threads per row (qkv_row_dot), fp32 accumulation of int8 x fp32 like
+// the matvec, times the row scale.  q heads go to q_out, k and v heads are quantized into
 // the cache at the ring slot of the step's position, gate heads go to
 // gate_out as raw projections.  One more workgroup computes the layer's
 // routing (route_wave).
-__global__ __launch_bounds__(256) void n2_qkv_kernel(
+__global__ __launch_bounds__(kQkvWg) void n2_qkv_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ S, const float* __restrict__ x,
     uint32_t d, uint32_t heads, uint32_t kv_heads, const uint32_t* __restrict__ st,
     const float* __restrict__ q_norm, const float* __restrict__ k_norm,
@@ -1019,37 +1057,20 @@ __global__ __launch_bounds__(256) void n2_qkv_kernel(
                   ((size_t)layer * kv_heads + h) * alloc, kv_slot(pos, sink, window), alloc, f32);
     return;
   }
-  // Loads first: this thread's weight bytes, the row scale, the epilogue
-  // operands, then x.  The 4 threads of a row read 64 contiguous bytes per
-  // load (thread q bytes [64 k + 16 q, +16)), so a wave's load covers 16
-  // rows x 64 bytes rather than 64 rows x 16.
-  const uint32_t r = t >> 2, q = t & 3, last = d / 64 - 1;
-  const size_t row = (size_t)b * kHd + r;
-  const int8_t* w = W + row * d + q * 16;
-  i32x4 wv[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k)
-    wv[k] = __builtin_nontemporal_load(  // clamped: unconditional loads issue back to back
-        reinterpret_cast<const i32x4*>(w + min((uint32_t)k, last) * 64));
+  // Loads first: this thread's weight bytes (unconditional, clamped, so they
+  // issue back to back), the row scale, the epilogue operands, then x.
+  const size_t row = (size_t)b * kHd + t / kQkvTpr;
+  i32x4 wv[kQkvLoads];
+  qkv_row_loads(W, row, t % kQkvTpr, d, wv);
   const float srow = S[row];
   const uint32_t pos = st[1];
   const uint32_t lane = t & 63;
   const float nscale = b < heads ? q_norm[lane] : k_norm[lane];
   const double rs = rope[lane & 31], rc = rope[32 + (lane & 31)];
-  for (uint32_t i = t; i < d; i += 256) xs[i] = x[i];
+  for (uint32_t i = t; i < d; i += kQkvWg) xs[i] = x[i];
   __syncthreads();
-  const float* xv = xs + q * 16;
-  float acc = 0.f;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    if ((uint32_t)k > last) break;
-    int8_t cb[16];
-    __builtin_memcpy(cb, &wv[k], 16);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc = fmaf((float)cb[j], xv[k * 64 + j], acc);
-  }
-  acc = nd::quad_sum(acc);
-  if (q == 0) rows[r] = acc * srow;
+  const float acc = qkv_row_dot(wv, xs, t % kQkvTpr, d);
+  if (t % kQkvTpr == 0) rows[t / kQkvTpr] = acc * srow;
   __syncthreads();
   if (t >= 64) return;
   const float val = rows[lane];
@@ -1635,7 +1656,7 @@ hipError_t enqueue_block(nd_needle* n, uint32_t l, hipStream_t s) {
     const hipError_t e = mv_any(&wm, n->ain, 0, wm.n, n->cq_proj, s);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(n2_qkv_kernel, dim3(wm.n / kHd + 1), dim3(256), 0, s, wm.w, wm.scales,
+  hipLaunchKernelGGL(n2_qkv_kernel, dim3(wm.n / kHd + 1), dim3(kQkvWg), 0, s, wm.w, wm.scales,
                      n->ain, D, d.heads, d.kv_heads, n->st, n->params + n->o_qn + (size_t)l * kHd,
                      n->params + n->o_kn + (size_t)l * kHd, n->rope, n->q, n->qkvg,
                      n->kv.k, n->kv.v, n->kv.ks, n->kv.vs, l, n->kv.alloc, n->kv.sink,
