@@ -562,6 +562,52 @@ __device__ float fwht_block(float v, float* hv, uint32_t H, uint32_t t) {
   return out;
 }
 
+// Cactus-Quant phi rows of the mix kernel, for one code width (2-bit codes and
+// ternary crumbs: BITS = 2): wave w takes rows w, w + 8 and w + 16, lane u
+// the rows' 32-code unit u, from the packed words w[j] and group norms n[j]
+// it loaded at entry.  x holds the rotated lanes with one pad float after
+// every 32 (element e at e + e / 32): lane u's unit starts at 33 u, so the
+// wave's reads of element c of its units fall in distinct banks.  Each unit
+// takes fp32 dots over its four 8-code blocks, each block times its group's
+// norm (groups of 8, 16, or 32 and wider) in float64, summed over the wave.
+template <uint32_t BITS>
+__device__ __forceinline__ void cq_phi_rows(const uint32_t (&w)[3][4], const uint32_t (&n)[3][4],
+                                            const float* x, const float* cb, uint32_t g,
+                                            uint32_t units, uint32_t nrows, uint32_t wave,
+                                            uint32_t lane, float* phi) {
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const uint32_t r = wave + 8u * j;
+    if (r >= nrows) break;  // uniform over the wave
+    double total = 0.0;
+    if (lane < units) {
+      const float* xu = x + lane * 33;
+      float dot8[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (uint32_t c = 0; c < 32; ++c) {
+        uint32_t code;
+        if constexpr (BITS == 4) {
+          code = (w[j][c >> 3] >> (4 * (c & 7))) & 15u;
+        } else if constexpr (BITS == 3) {
+          const uint32_t bit = 3 * c, k = bit >> 5, sh = bit & 31;
+          const uint32_t hi = sh > 29 ? w[j][k + 1 < 4 ? k + 1 : 3] << (32 - sh) : 0u;
+          code = ((w[j][k] >> sh) | hi) & 7u;
+        } else {
+          code = (w[j][c >> 4] >> (2 * (c & 15))) & 3u;
+        }
+        dot8[c >> 3] = fmaf(cb[code], xu[c], dot8[c >> 3]);
+      }
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t nb = g == 8 ? n[j][b] : (g == 16 ? n[j][b >> 1] : n[j][0]);
+        total += (double)nd::cq_half(nb) * (double)dot8[b];
+      }
+    }
+    total = nd::wave_sum(total);
+    if (lane == 0) phi[r] = (float)total;
+  }
+}
+
 // phi operand tiling: the (2 + lanes) * lanes phi rows (<= 24) in tiles of
 // 16 weight rows, four waves per tile, each over up to kPhiPairs 64-wide
 // k-pairs of the lanes * dim (<= 2048) columns.
@@ -609,6 +655,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   __shared__ double red[2][2 * (kMixWg / 64)];
   __shared__ __align__(16) float s_part[32][4][2];  // [phi row][wave of the tile][hi, lo]
   __shared__ float phi[24], rt[20];
+  __shared__ float s_cqx[CQ ? 2048 + 2048 / 32 : 1];  // rotated lanes, padded
   const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const uint32_t D = a.d, L = a.lanes, N = L * D, H = a.hdim;
   const uint32_t nrows = 2 * L + L * L;
@@ -780,54 +827,36 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   float pre_phi = 0.f;  // phi_pre row `lane` (lane < lanes): feeds hPre
   if constexpr (CQ) {
     // phi = cqMatvec of the normalized lanes (backends/cq.ts:30-46, 107-231):
-    // prepareCqActivation in LDS -- per group the butterflies, then times
-    // 1/sqrt(g) -- and one wave per phi row, lane u taking the row's 32-code
-    // unit u (codes from the words loaded at entry): an fp32 dot per group
-    // times the group's norm, summed over the wave in float64.
-    float* s_nl = reinterpret_cast<float*>(&s_split[0][0]);  // N <= 2048 floats
+    // prepareCqActivation in LDS -- per group the butterflies (strides 1 ..
+    // g / 2, one fp32 add and subtract per pair, a barrier per stage), then
+    // times 1/sqrt(g) -- and the rows by code width (cq_phi_rows).
+    auto at = [](uint32_t e) { return e + (e >> 5); };  // padded LDS slot
     if (col) {
 #pragma unroll
       for (int l = 0; l < 4; ++l)
-        if ((uint32_t)l < L) s_nl[l * D + t] = (float)((double)xl[l] * inv);
+        if ((uint32_t)l < L) s_cqx[at(l * D + t)] = (float)((double)xl[l] * inv);
     }
     __syncthreads();
-    nd::cq_fwht_groups(s_nl, N, a.cq_g);
-    for (uint32_t i = t; i < N; i += kMixWg) s_nl[i] = (float)((double)s_nl[i] * a.cq_inv_root);
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      const uint32_t r = wave + 8u * j;
-      if (r >= nrows) break;  // uniform over the wave
-      double total = 0.0;
-      if (lane < N / 32) {
-        // fp32 dots over the unit's four 8-code blocks, then each block times
-        // its group's norm (groups of 8, 16, or 32 and wider) in float64;
-        // every index is a constant, so the operands stay in registers.
-        const float* xu = s_nl + lane * 32;
-        float dot8[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (uint32_t c = 0; c < 32; ++c) {
-          uint32_t code;
-          if (a.cq_bits == 4) {
-            code = (cw[j][c >> 3] >> (4 * (c & 7))) & 15u;
-          } else if (a.cq_bits == 3) {
-            const uint32_t bit = 3 * c, w = bit >> 5, sh = bit & 31;
-            const uint32_t hi = sh > 29 ? cw[j][w + 1 < 4 ? w + 1 : 3] << (32 - sh) : 0u;
-            code = ((cw[j][w] >> sh) | hi) & 7u;
-          } else {  // 2-bit codes and ternary crumbs
-            code = (cw[j][c >> 4] >> (2 * (c & 15))) & 3u;
-          }
-          dot8[c >> 3] = fmaf(s_cb[code], xu[c], dot8[c >> 3]);
-        }
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const uint32_t nb = a.cq_g == 8 ? cn[j][b] : (a.cq_g == 16 ? cn[j][b >> 1] : cn[j][0]);
-          total += (double)nd::cq_half(nb) * (double)dot8[b];
-        }
+    uint32_t sh = 0;
+    for (uint32_t stride = 1; stride < a.cq_g; stride <<= 1, ++sh) {
+      for (uint32_t i = t; i < N / 2; i += kMixWg) {
+        const uint32_t left = ((i >> sh) << (sh + 1)) | (i & (stride - 1));
+        const uint32_t pl = at(left), pr = at(left + stride);
+        const float x0 = s_cqx[pl], x1 = s_cqx[pr];
+        s_cqx[pl] = x0 + x1;
+        s_cqx[pr] = x0 - x1;
       }
-      total = nd::wave_sum(total);
-      if (lane == 0) phi[r] = (float)total;
+      __syncthreads();
     }
+    for (uint32_t i = t; i < N; i += kMixWg)
+      s_cqx[at(i)] = (float)((double)s_cqx[at(i)] * a.cq_inv_root);
+    __syncthreads();
+    if (a.cq_bits == 4)
+      cq_phi_rows<4>(cw, cn, s_cqx, s_cb, a.cq_g, N / 32, nrows, wave, lane, phi);
+    else if (a.cq_bits == 3)
+      cq_phi_rows<3>(cw, cn, s_cqx, s_cb, a.cq_g, N / 32, nrows, wave, lane, phi);
+    else  // 2-bit codes and ternary crumbs
+      cq_phi_rows<2>(cw, cn, s_cqx, s_cb, a.cq_g, N / 32, nrows, wave, lane, phi);
     __syncthreads();
     if (t < nrows) {
       const float v = phi[t];
