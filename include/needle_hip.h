@@ -400,9 +400,8 @@ typedef struct nd_needle nd_needle;
  * all of the embedding's width and group size, groups of at most 2048 and
  * engram rows of at most 1024 padded codes; a Cactus-Quant model runs every
  * product as cqMatvec and every row gather as dequantizeCqRow
- * (backends/cq.ts:106-295), and its prompts step token by token as
- * NeedleRuntime.prefill does.  Dense vectors are host arrays copied at
- * creation.
+ * (backends/cq.ts:106-295), its prompts in the same batched passes as an
+ * int8 model's.  Dense vectors are host arrays copied at creation.
  *   embedding  [vocab][dim], tied output projection (runtime.ts:570-577)
  *   wq, wgate  layers entries of [heads*64][dim]; wk, wv [kv_heads*64][dim]
  *   wo         [dim][heads*64]

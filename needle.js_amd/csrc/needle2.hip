@@ -258,11 +258,22 @@ struct CqRowsArgs {
   float* cell0;
   uint32_t n_sites, tables, slots, sub;
   float* cat;
+  // Batched prefill: position blockIdx.y reads its token and lookups
+  // lookup_ld further on and writes its lanes, pool cell and engram rows
+  // x_ld, cell_ld and cat_ld further on (all 0 for one step).
+  uint32_t lookup_ld, x_ld, cell_ld, cat_ld;
 };
 
 __global__ __launch_bounds__(256) void n2_cq_rows_kernel(CqRowsArgs a) {
   __shared__ float v[kCqRowMax];
-  const uint32_t b = blockIdx.x, t = threadIdx.x;
+  const uint32_t b = blockIdx.x, t = threadIdx.x, m = blockIdx.y;
+  if (m) {
+    a.lookup += (size_t)m * a.lookup_ld;
+    if (a.token) a.token += (size_t)m * a.lookup_ld;
+    a.x += (size_t)m * a.x_ld;
+    if (a.cell0) a.cell0 += (size_t)m * a.cell_ld;
+    a.cat += (size_t)m * a.cat_ld;
+  }
   if (b == 0) {
     if (!a.token) return;
     const uint32_t tok = *a.token;
@@ -1154,6 +1165,15 @@ __global__ __launch_bounds__(kWg) void n2_begin_batch_kernel(BeginArgs a, uint32
     hash ^= hash >> 15;
     s_idx[t] = hash % a.slots;
     s_valid[t] = valid ? 1u : 0u;
+    if (a.cq_lookup) {
+      uint32_t* lk = a.cq_lookup + (size_t)m * (2 * a.tables + 1);
+      lk[t] = s_idx[t];
+      lk[a.tables + t] = s_valid[t];
+    }
+  }
+  if (a.cq_lookup) {  // the rows come from n2_cq_rows_kernel
+    if (t == 0) a.cq_lookup[(size_t)m * (2 * a.tables + 1) + 2 * a.tables] = tok;
+    return;
   }
   __syncthreads();
   float* x = a.x + (size_t)m * a.lanes * a.d;
@@ -1499,6 +1519,7 @@ struct nd_needle {
         *pf_ekv = nullptr, *pf_evals = nullptr, *pf_fm = nullptr, *pf_partials = nullptr;
   int8_t* pf_digits = nullptr;
   uint32_t *pf_positions = nullptr, *pf_counters = nullptr;
+  uint32_t* pf_cq_lookup = nullptr;  // CQ model: each position's engram lookups and token
   // Step graphs, valid for (graph_alloc, graph_sink).
   hipGraphExec_t graphs[3] = {nullptr, nullptr, nullptr};
   uint32_t graph_alloc = 0, graph_sink = 0, graph_mode = 0;
@@ -1571,6 +1592,34 @@ hipError_t enqueue_pool(nd_needle* n, const float* cells, uint32_t C, double* sc
 // collectConfidence).
 inline bool pool_on(const nd_needle* n) { return n->conf && n->collect; }
 
+// The phi rows of layer ql in a mix launch's arguments, in the model's
+// matrix form.
+void set_phi(const nd_needle* n, uint32_t ql, MixArgs& m) {
+  const uint32_t ln = n->d.lanes;
+  const size_t K = (size_t)ln * n->d.dim;
+  if (n->cq) {
+    const nd_mat* pm[3] = {n->phi_pre, n->phi_post, n->phi_res};
+    const size_t first[3] = {(size_t)ql * ln, (size_t)ql * ln, (size_t)ql * ln * ln};
+    for (int i = 0; i < 3; ++i) {
+      m.cq_p[i] = pm[i]->packed + first[i] * pm[i]->row_bytes;
+      m.cq_n[i] = pm[i]->norms + first[i] * (pm[i]->kpad / pm[i]->g);
+    }
+    for (int i = 0; i < 16; ++i) m.cq_cb[i] = n->phi_pre->cb[i];
+    m.cq_bits = n->phi_pre->bits;
+    m.cq_g = n->phi_pre->g;
+    m.cq_row_bytes = n->phi_pre->row_bytes;
+    m.cq_groups = n->phi_pre->kpad / n->phi_pre->g;
+    m.cq_inv_root = 1.0 / std::sqrt((double)n->phi_pre->g);
+  } else {
+    m.phi_w[0] = n->phi_pre->w + (size_t)ql * ln * K;
+    m.phi_s[0] = n->phi_pre->scales + (size_t)ql * ln;
+    m.phi_w[1] = n->phi_post->w + (size_t)ql * ln * K;
+    m.phi_s[1] = n->phi_post->scales + (size_t)ql * ln;
+    m.phi_w[2] = n->phi_res->w + (size_t)ql * ln * ln * K;
+    m.phi_s[2] = n->phi_res->scales + (size_t)ql * ln * ln;
+  }
+}
+
 // Halves of a mix launch (enqueue_mix `parts`).
 enum MixPart : uint32_t { kMixPost = 1, kMixPre = 2, kMixFinal = 4, kMixCell = 8 };
 
@@ -1584,7 +1633,6 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s) 
   const bool has_post = parts & kMixPost;
   const nd_needle_desc& d = n->d;
   const uint32_t D = d.dim, ln = d.lanes;
-  const size_t K = (size_t)ln * D;
   const bool pre = l < d.layers;
   // Every operand pointer is valid whether or not its half runs (the kernel
   // loads them unconditionally): an absent layer reads layer 0's.
@@ -1613,27 +1661,7 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s) 
   m.route = n->route;
   m.has_pre = pre && (parts & kMixPre);
   m.own_pre = ql % ln;
-  if (n->cq) {
-    const nd_mat* pm[3] = {n->phi_pre, n->phi_post, n->phi_res};
-    const size_t first[3] = {(size_t)ql * ln, (size_t)ql * ln, (size_t)ql * ln * ln};
-    for (int i = 0; i < 3; ++i) {
-      m.cq_p[i] = pm[i]->packed + first[i] * pm[i]->row_bytes;
-      m.cq_n[i] = pm[i]->norms + first[i] * (pm[i]->kpad / pm[i]->g);
-    }
-    for (int i = 0; i < 16; ++i) m.cq_cb[i] = n->phi_pre->cb[i];
-    m.cq_bits = n->phi_pre->bits;
-    m.cq_g = n->phi_pre->g;
-    m.cq_row_bytes = n->phi_pre->row_bytes;
-    m.cq_groups = n->phi_pre->kpad / n->phi_pre->g;
-    m.cq_inv_root = 1.0 / std::sqrt((double)n->phi_pre->g);
-  } else {
-    m.phi_w[0] = n->phi_pre->w + (size_t)ql * ln * K;
-    m.phi_s[0] = n->phi_pre->scales + (size_t)ql * ln;
-    m.phi_w[1] = n->phi_post->w + (size_t)ql * ln * K;
-    m.phi_s[1] = n->phi_post->scales + (size_t)ql * ln;
-    m.phi_w[2] = n->phi_res->w + (size_t)ql * ln * ln * K;
-    m.phi_s[2] = n->phi_res->scales + (size_t)ql * ln * ln;
-  }
+  set_phi(n, ql, m);
   m.a_pre = n->a_pre[ql];
   m.b_pre = n->params + n->o_bpre + (size_t)ql * ln;
   m.has_site = site >= 0;
@@ -1669,7 +1697,7 @@ hipError_t mv_any(const nd_mat* m, const float* x, uint32_t row_start, uint32_t 
 // n->proj (runtime.ts:465-505).
 hipError_t enqueue_block(nd_needle* n, uint32_t l, hipStream_t s) {
   const nd_needle_desc& d = n->d;
-  const uint32_t D = d.dim, ln = d.lanes, qw = d.heads * kHd;
+  const uint32_t D = d.dim, ln = d.lanes;
   const nd_mat& wm = n->wqkvg[l];
   RouteArgs ra{};
   ra.phi_post = n->phi_post_v;
@@ -1751,8 +1779,10 @@ BeginArgs begin_args(nd_needle* n) {
 
 // The gathers of a Cactus-Quant model's step: the embedding row of *token
 // (token null: none) and the engram table rows of `lookup`.
+// batch: 0 for one step's rows (n->x, n->cells, n->cat), else the number of
+// batched prefill positions (their rows into the prefill buffers).
 hipError_t enqueue_cq_rows(nd_needle* n, const uint32_t* token, const uint32_t* lookup,
-                           hipStream_t s) {
+                           hipStream_t s, uint32_t batch = 0) {
   const nd_needle_desc& d = n->d;
   CqRowsArgs a{};
   const nd_mat* e = n->embedding;
@@ -1789,7 +1819,18 @@ hipError_t enqueue_cq_rows(nd_needle* n, const uint32_t* token, const uint32_t* 
   a.slots = d.engram_slots;
   a.sub = d.engram_sub;
   a.cat = n->cat;
-  hipLaunchKernelGGL(n2_cq_rows_kernel, dim3(1 + d.n_sites * d.engram_tables), dim3(256), 0, s, a);
+  if (batch) {  // the batched prefill's rows, positions in history order
+    const uint32_t per_site = d.engram_tables * d.engram_sub;
+    a.x = n->pf_x;
+    a.cell0 = pool_on(n) ? n->pf_cells : nullptr;
+    a.cat = n->pf_cat;
+    a.lookup_ld = 2 * d.engram_tables + 1;
+    a.x_ld = d.lanes * d.dim;
+    a.cell_ld = (d.layers + 1) * d.dim;
+    a.cat_ld = (d.n_sites ? d.n_sites : 1) * per_site;
+  }
+  hipLaunchKernelGGL(n2_cq_rows_kernel, dim3(1 + d.n_sites * d.engram_tables, batch ? batch : 1),
+                     dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1899,7 +1940,8 @@ nd_status ensure_prefill(nd_ctx* ctx, nd_needle* n) {
                           al((size_t)3 * cap * kmax),   al((size_t)cap * 4),
                           al((size_t)cap * d.kv_heads * kAttnCounterStride * 4),
                           n->conf ? al((size_t)cap * (d.layers + 1) * D * 4) : 0,
-                          n->conf ? al((size_t)cap * (d.layers + 1) * kMaxProbes * 8) : 0};
+                          n->conf ? al((size_t)cap * (d.layers + 1) * kMaxProbes * 8) : 0,
+                          n->cq ? al((size_t)cap * (2 * d.engram_tables + 1) * 4) : 0};
   size_t total = 0;
   for (size_t v : sizes) total += v;
   hipError_t e = hipMalloc(&n->pf_arena, total);
@@ -1937,6 +1979,7 @@ nd_status ensure_prefill(nd_ctx* ctx, nd_needle* n) {
   take(&n->pf_counters);
   take(&n->pf_cells);
   take(&n->pf_scores);
+  take(&n->pf_cq_lookup);
   n->pf_cap = cap;
   return ND_OK;
 }
@@ -1976,18 +2019,29 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
   const uint32_t cell_ld = (d.layers + 1) * D;  // cells of one position: [layers + 1][d]
   b.cell0 = pool_on(n) ? n->pf_cells : nullptr;
   b.cell_ld = cell_ld;
+  b.cq_lookup = n->cq ? n->pf_cq_lookup : nullptr;
   hipLaunchKernelGGL(n2_begin_batch_kernel, dim3(M), dim3(kWg), 0, s, b, p0, M, n->pf_positions);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  const uint32_t lk = 2 * d.engram_tables + 1;
+  if (n->cq && (e = enqueue_cq_rows(n, n->pf_cq_lookup + lk - 1, n->pf_cq_lookup, s, M)) !=
+                   hipSuccess)
+    return e;
+  // The batch's products: digit-sliced int8 GEMMs, or for a Cactus-Quant
+  // model the CQ matvec over the M rows (the step's arithmetic per row).
+  auto product = [&](const nd_mat* w, const float* x, uint32_t x_ld, uint32_t k, float* y,
+                     uint32_t y_ld) -> hipError_t {
+    if (w->bits)
+      return nd_launch_cq_matvec(w, x, M, x_ld, nullptr, 0, w->n, y, y_ld, s);
+    hipError_t r = nd_launch_digitize(x, x_ld, nullptr, nullptr, n->pf_digits, n->pf_fm, M, k, s);
+    if (r != hipSuccess) return r;
+    return nd_launch_gemm(w, n->pf_digits, n->pf_fm, y, y_ld, M, 0, s);
+  };
   if (d.n_sites) {
-    for (uint32_t si = 0; si < d.n_sites; ++si) {
-      if ((e = nd_launch_digitize(n->pf_cat + (size_t)si * cat, S * cat, nullptr, nullptr,
-                                  n->pf_digits, n->pf_fm, M, cat, s)) != hipSuccess)
+    for (uint32_t si = 0; si < d.n_sites; ++si)
+      if ((e = product(&n->ekv[si], n->pf_cat + (size_t)si * cat, S * cat, cat,
+                       n->pf_ekv + (size_t)si * 2 * D, S * 2 * D)) != hipSuccess)
         return e;
-      if ((e = nd_launch_gemm(&n->ekv[si], n->pf_digits, n->pf_fm, n->pf_ekv + (size_t)si * 2 * D,
-                              S * 2 * D, M, 0, s)) != hipSuccess)
-        return e;
-    }
     const uint32_t threads = (D + 63) / 64 * 64;
     hipLaunchKernelGGL(n2_conv_batch_kernel, dim3(M, d.n_sites), dim3(threads), 0, s, n->pf_ekv,
                        n->ring, n->params + n->o_taps, D, n->depth, d.engram_taps, n->max_order,
@@ -1997,7 +2051,6 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
                        0, s, n->pf_ekv, n->ring, D, n->depth, d.n_sites, p0, M);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  const size_t K = (size_t)N;
   const bool tail = want_logits || select;
   for (uint32_t l = 0; l <= d.layers; ++l) {
     const bool pre = l < d.layers;
@@ -2030,12 +2083,7 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
     m.route = n->pf_route + (size_t)r0 * 20;
     m.has_pre = pre;
     m.own_pre = ql % ln;
-    m.phi_w[0] = n->phi_pre->w + (size_t)ql * ln * K;
-    m.phi_s[0] = n->phi_pre->scales + (size_t)ql * ln;
-    m.phi_w[1] = n->phi_post->w + (size_t)ql * ln * K;
-    m.phi_s[1] = n->phi_post->scales + (size_t)ql * ln;
-    m.phi_w[2] = n->phi_res->w + (size_t)ql * ln * ln * K;
-    m.phi_s[2] = n->phi_res->scales + (size_t)ql * ln * ln;
+    set_phi(n, ql, m);
     m.a_pre = n->a_pre[ql];
     m.b_pre = n->params + n->o_bpre + (size_t)ql * ln;
     m.has_site = site >= 0;
@@ -2057,15 +2105,13 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
       m.r_b_post = n->params + n->o_bpost + (size_t)l * ln;
       m.r_b_res = n->params + n->o_bres + (size_t)l * ln * ln;
     }
-    hipLaunchKernelGGL(n2_mix_kernel<false>, dim3(rows), dim3(kMixWg), 0, s, m);
+    if (n->cq)
+      hipLaunchKernelGGL(n2_mix_kernel<true>, dim3(rows), dim3(kMixWg), 0, s, m);
+    else
+      hipLaunchKernelGGL(n2_mix_kernel<false>, dim3(rows), dim3(kMixWg), 0, s, m);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (!pre) break;
-    if ((e = nd_launch_digitize(n->pf_ain, D, nullptr, nullptr, n->pf_digits, n->pf_fm, M, D, s)) !=
-        hipSuccess)
-      return e;
-    if ((e = nd_launch_gemm(&n->wqkvg[l], n->pf_digits, n->pf_fm, n->pf_qkvg, qkv_ld, M, 0, s)) !=
-        hipSuccess)
-      return e;
+    if ((e = product(&n->wqkvg[l], n->pf_ain, D, D, n->pf_qkvg, qkv_ld)) != hipSuccess) return e;
     hipLaunchKernelGGL(n2_rope_store_batch_kernel, dim3(d.heads + 2 * d.kv_heads, M), dim3(64), 0,
                        s, n->pf_qkvg, qkv_ld, d.heads, d.kv_heads,
                        n->params + n->o_qn + (size_t)l * kHd, n->params + n->o_kn + (size_t)l * kHd,
@@ -2078,18 +2124,13 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
                                   n->pf_partials, n->pf_counters, s, n->pf_qkvg + qw + 2 * kw,
                                   qkv_ld);
     if (e != hipSuccess) return e;
-    if ((e = nd_launch_digitize(n->pf_att, qw, nullptr, nullptr, n->pf_digits, n->pf_fm, M, qw,
-                                s)) != hipSuccess)
-      return e;
-    if ((e = nd_launch_gemm(n->wo[l], n->pf_digits, n->pf_fm, n->pf_proj, D, M, 0, s)) !=
-        hipSuccess)
-      return e;
+    if ((e = product(n->wo[l], n->pf_att, qw, qw, n->pf_proj, D)) != hipSuccess) return e;
   }
   if (pool_on(n) && (e = enqueue_pool(n, n->pf_cells, M * (d.layers + 1), n->pf_scores, s)) !=
                      hipSuccess)
     return e;
   if (!tail) return hipSuccess;
-  e = nd_launch_matvec(n->embedding, n->fin, 1, D, 0, d.vocab, n->logits, d.vocab, s);
+  e = mv_any(n->embedding, n->fin, 0, d.vocab, n->logits, s);
   if (e != hipSuccess || !select) return e;
   return nd_launch_select_list(n->logits, d.vocab, nullptr, 0, n->sel_id, n->sel_lp, s);
 }
@@ -2105,10 +2146,7 @@ nd_status run_prompt(nd_ctx* ctx, nd_needle* n, uint32_t count, bool want_logits
   uint32_t done = 0;
   while (done < count) {
     const uint32_t left = count - done;
-    // The batched passes run int8 GEMMs; a Cactus-Quant model steps every
-    // prompt token (as NeedleRuntime.prefill does, runtime.ts:227-243).
-    const uint32_t room =
-        !n->cq && n->kv.alloc > n->position ? n->kv.alloc - n->position : 0;
+    const uint32_t room = n->kv.alloc > n->position ? n->kv.alloc - n->position : 0;
     const uint32_t chunk = std::min(std::min(left, n->pf_cap), room);
     const bool last_pass = chunk == left;
     if (chunk > 0) {

@@ -300,8 +300,9 @@ def test_cactus_quant_model_steps_prefill_and_generate(hip, cq_bits, sink):
     """The resident runtime over Cactus-Quant matrices, the form every matrix
     of the shipped archive takes (model/cact.ts:398-562, backends/cq.ts:106-295):
     step logits, the cache and the confidence against the oracle's cqMatvec /
-    dequantizeCqRow restatement, a prompt (stepped, as the reference's
-    prefill does) and a greedy continuation with identical ids."""
+    dequantizeCqRow restatement, a prompt (one batched pass while its cache
+    slots do not wrap, steps after) and a greedy continuation with identical
+    ids."""
     say("needle2 cactus-quant", cq_bits, sink)
     w = Needle2Weights(SMALL, 51, cq_bits=cq_bits)
     model = NeedleModel(hip, w)
@@ -409,20 +410,22 @@ def test_confidence_absent_or_disabled(hip):
         model.dispose()
 
 
-@pytest.mark.parametrize("window,sink,n_prompt,max_length",
-                         [(0, 0, 40, 64), (16, 3, 30, 64), (8, 0, 33, 64), (0, 0, 280, 300),
-                          (128, 3, 100, 160)])
-def test_batched_prefill_then_steps(hip, window, sink, n_prompt, max_length):
+@pytest.mark.parametrize("window,sink,n_prompt,max_length,cq_bits",
+                         [(0, 0, 40, 64, 0), (16, 3, 30, 64, 0), (8, 0, 33, 64, 0),
+                          (0, 0, 280, 300, 0), (128, 3, 100, 160, 0), (16, 3, 30, 64, 4),
+                          (0, 0, 280, 300, 4), (8, 0, 33, 64, 5)])
+def test_batched_prefill_then_steps(hip, window, sink, n_prompt, max_length, cq_bits):
     """Prompt positions whose cache slots do not wrap run as one batched pass
-    (int8 MFMA projections, one mix workgroup per position), the rest as
-    steps; logits, every appended KV row and the engram ring handed to the
-    following steps must agree with the oracle's sequential steps (the
-    300-position case batches a prompt longer than one attention chunk; the
-    100-token prompt under a 128-position window with 3 sinks runs the
-    query-block attention of a windowed cache with sinks)."""
-    say("needle2 batched prefill", window, sink, n_prompt, max_length)
+    (int8 MFMA projections, or the Cactus-Quant matvec over the batch's rows
+    for a CQ model; one mix workgroup per position), the rest as steps;
+    logits, every appended KV row and the engram ring handed to the following
+    steps must agree with the oracle's sequential steps (the 300-position
+    case batches a prompt longer than one attention chunk; the 100-token
+    prompt under a 128-position window with 3 sinks runs the query-block
+    attention of a windowed cache with sinks)."""
+    say("needle2 batched prefill", window, sink, n_prompt, max_length, cq_bits)
     g = Needle2Geometry(**{**SMALL.__dict__, "kv_window": window, "max_length": max_length})
-    w = Needle2Weights(g, 41)
+    w = Needle2Weights(g, 41, cq_bits=cq_bits)
     model = NeedleModel(hip, w)
     try:
         rt = model.create_resident_runtime()
