@@ -1054,15 +1054,124 @@ __device__ __forceinline__ float qkv_row_dot(const i32x4 (&w)[kQkvLoads], const 
   return acc;
 }
 
+// A Cactus-Quant matrix's rows as the projection launch reads them (rows of
+// kpad codes, binary16 norms per group, the width's codebook by code).
+struct CqRows {
+  const uint8_t* packed;
+  const uint16_t* norms;
+  float cb[16];
+  uint32_t g, g_log2, row_bytes, groups;
+  float out_scale;  // 1 / sqrt(g)
+};
+
+// Rows r and r + 32 of the workgroup's 64 (r = t / 16) of a Cactus-Quant
+// product with d <= 512 inputs (cqMatvec, backends/cq.ts:106-231): thread t
+// takes 32-code unit u = t % 16 of both rows.  xs holds x with one pad float
+// after every 32 (element e at e + e / 32, zeros past d), so the 16 units'
+// reads fall in distinct banks.  The unit's inputs are rotated in registers
+// -- the butterflies of fastWalshHadamard with strides below min(g, 32), then
+// strides 32 .. g / 2 across the lanes holding the group's other units --
+// each result one fp32 add or subtract of the reference's two operands; the
+// codes index the codebook in LDS; fp32 dots per group times the group's
+// norm, summed over the row's 16 lanes, times 1/sqrt(g).  Returns the two
+// row values in every lane of the row.
+template <uint32_t BITS>
+__device__ __forceinline__ float2 cq_rows_pair(const CqRows& q, size_t row0, uint32_t units,
+                                               const float* xs, const float* cb, uint32_t t) {
+  constexpr uint32_t kWords = BITS;  // 32 codes of BITS bits
+  const uint32_t u = t & 15, r = t >> 4;
+  const bool active = u < units;
+  const uint32_t uc = active ? u : 0;
+  uint32_t w[2][kWords];
+  uint32_t nb[2][4];
+  const uint32_t ng = q.g < 32 ? 32u >> q.g_log2 : 1u;  // groups in a unit
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const size_t row = row0 + r + 32u * i;
+    const uint32_t* src =
+        reinterpret_cast<const uint32_t*>(q.packed + row * q.row_bytes) + uc * kWords;
+#pragma unroll
+    for (uint32_t k = 0; k < kWords; ++k) w[i][k] = src[k];
+    const uint16_t* nrow = q.norms + row * q.groups + ((uc * 32) >> q.g_log2);
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) nb[i][k] = nrow[k < ng ? k : 0];
+  }
+  float v[32];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) v[c] = xs[uc * 33 + c];
+  const uint32_t gs = q.g < 32 ? q.g : 32u;
+#pragma unroll
+  for (uint32_t st = 1; st < 32; st <<= 1) {
+    if (st < gs) {
+#pragma unroll
+      for (uint32_t c = 0; c < 32; ++c)
+        if (!(c & st)) {
+          const float a = v[c], b = v[c + st];
+          v[c] = a + b;
+          v[c + st] = a - b;
+        }
+    }
+  }
+  auto cross = [&](auto m) {
+    constexpr int M = decltype(m)::value;
+    const bool right = (t & M) != 0;
+#pragma unroll
+    for (int c = 0; c < 32; ++c) {
+      const float other = nd::lane_xor<M>(v[c]);
+      v[c] = right ? other - v[c] : v[c] + other;
+    }
+  };
+  const uint32_t lpg = q.g > 32 ? q.g >> 5 : 1u;  // lanes of a group
+  if (lpg > 1) cross(std::integral_constant<int, 1>{});
+  if (lpg > 2) cross(std::integral_constant<int, 2>{});
+  if (lpg > 4) cross(std::integral_constant<int, 4>{});
+  if (lpg > 8) cross(std::integral_constant<int, 8>{});
+  float out[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    float total = 0.f, dot = 0.f;
+#pragma unroll
+    for (uint32_t c = 0; c < 32; ++c) {
+      uint32_t code;
+      if constexpr (BITS == 4) {
+        code = (w[i][c >> 3] >> (4 * (c & 7))) & 15u;
+      } else if constexpr (BITS == 3) {
+        const uint32_t bit = 3 * c, k = bit >> 5, sh = bit & 31;
+        const uint32_t hi = sh > 29 ? w[i][k + 1 < kWords ? k + 1 : kWords - 1] << (32 - sh) : 0u;
+        code = ((w[i][k] >> sh) | hi) & 7u;
+      } else {
+        code = (w[i][c >> 4] >> (2 * (c & 15))) & 3u;
+      }
+      dot = fmaf(cb[code], v[c], dot);
+      if ((c & 7) == 7) {  // a group of 8, 16 or 32 and wider may end here: by selection
+        const bool ends = c == 31 || q.g == 8 || (q.g == 16 && (c & 15) == 15);
+        const uint32_t h = q.g == 8 ? nb[i][c >> 3] : (q.g == 16 ? nb[i][c >> 4] : nb[i][0]);
+        const float with = fmaf(nd::cq_half(h), dot, total);
+        total = ends ? with : total;
+        dot = ends ? 0.f : dot;
+      }
+    }
+    total = active ? total : 0.f;
+    total += nd::lane_xor<1>(total);
+    total += nd::lane_xor<2>(total);
+    total += nd::lane_xor<4>(total);
+    total += nd::lane_xor<8>(total);
+    out[i] = total * q.out_scale;
+  }
+  return float2{out[0], out[1]};
+}
+
 // The fused Q/K/V/gate projection of one layer (runtime.ts:465-470) with the
 // per-head norm + RoPE of q and k (runtime.ts:471-500) and #storeKV
 // (runtime.ts:679-717) in the epilogue.  Workgroup b computes rows [64 b,
 // 64 b + 64) of wqkvg = [q (H*64) | k (Hkv*64) | v (Hkv*64) | gate (H*64)]:
-// eight threads per row (qkv_row_dot), fp32 accumulation of int8 x fp32 like
-// the matvec, times the row scale.  q heads go to q_out, k and v heads are quantized into
-// the cache at the ring slot of the step's position, gate heads go to
-// gate_out as raw projections.  One more workgroup computes the layer's
-// routing (route_wave).
+// for int8 rows (BITS 0) eight threads per row (qkv_row_dot), fp32
+// accumulation of int8 x fp32 like the matvec, times the row scale; for
+// Cactus-Quant rows (BITS 2, 3, 4; ternary crumbs as 2) cq_rows_pair.  q
+// heads go to q_out, k and v heads are quantized into the cache at the ring
+// slot of the step's position, gate heads go to gate_out as raw projections.
+// One more workgroup computes the layer's routing (route_wave).
+template <uint32_t BITS>
 __global__ __launch_bounds__(kQkvWg) void n2_qkv_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ S, const float* __restrict__ x,
     uint32_t d, uint32_t heads, uint32_t kv_heads, const uint32_t* __restrict__ st,
@@ -1070,47 +1179,44 @@ __global__ __launch_bounds__(kQkvWg) void n2_qkv_kernel(
     const double* __restrict__ rope, float* __restrict__ q_out, float* __restrict__ gate_out,
     void* __restrict__ Kc, void* __restrict__ Vc, float* __restrict__ Ks,
     float* __restrict__ Vs, uint32_t layer, uint32_t alloc, uint32_t sink, uint32_t window,
-    uint32_t f32, RouteArgs route, const float* __restrict__ projected) {
-  __shared__ float xs[512];
+    uint32_t f32, RouteArgs route, CqRows cq) {
+  __shared__ float xs[512 + 16];
   __shared__ float rows[64];
+  __shared__ float s_cb[16];
   const uint32_t b = blockIdx.x, t = threadIdx.x;
   if (b == 2 * (heads + kv_heads)) {
     route_wave(route, t, rows);
     return;
   }
-  if (projected) {
-    // Cactus-Quant model: the projections come from a CQ matvec of the
-    // same rows; only the per-head epilogue runs here.
-    if (t >= 64) return;
-    const float val = projected[(size_t)b * kHd + t];
-    const uint32_t nq = heads, nk = kv_heads;
-    if (b >= nq + 2 * nk) {  // gate head
-      gate_out[(size_t)(b - nq - 2 * nk) * kHd + t] = val;
-      return;
-    }
-    const uint32_t pos = st[1];
-    const float nscale = b < heads ? q_norm[t] : k_norm[t];
-    const double rs = rope[t & 31], rc = rope[32 + (t & 31)];
-    const int role = b < nq ? 0 : (b < nq + nk ? 1 : 2);
-    const uint32_t h = role == 0 ? b : (role == 1 ? b - nq : b - nq - nk);
-    head_epilogue(val, t, role, rs, rc, nscale, q_out + (size_t)h * kHd, Kc, Vc, Ks, Vs,
-                  ((size_t)layer * kv_heads + h) * alloc, kv_slot(pos, sink, window), alloc, f32);
-    return;
-  }
-  // Loads first: this thread's weight bytes (unconditional, clamped, so they
-  // issue back to back), the row scale, the epilogue operands, then x.
-  const size_t row = (size_t)b * kHd + t / kQkvTpr;
-  i32x4 wv[kQkvLoads];
-  qkv_row_loads(W, row, t % kQkvTpr, d, wv);
-  const float srow = S[row];
-  const uint32_t pos = st[1];
   const uint32_t lane = t & 63;
+  if constexpr (BITS == 0) {
+    // Loads first: this thread's weight bytes (unconditional, clamped, so
+    // they issue back to back), the row scale, then x.
+    const size_t row = (size_t)b * kHd + t / kQkvTpr;
+    i32x4 wv[kQkvLoads];
+    qkv_row_loads(W, row, t % kQkvTpr, d, wv);
+    const float srow = S[row];
+    for (uint32_t i = t; i < d; i += kQkvWg) xs[i] = x[i];
+    __syncthreads();
+    const float acc = qkv_row_dot(wv, xs, t % kQkvTpr, d);
+    if (t % kQkvTpr == 0) rows[t / kQkvTpr] = acc * srow;
+  } else {
+    if (t == 0) {  // constant indices into the argument block
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s_cb[i] = cq.cb[i];
+    }
+    const uint32_t kpad = (d + 31) & ~31u;
+    for (uint32_t i = t; i < kpad; i += kQkvWg) xs[i + (i >> 5)] = i < d ? x[i] : 0.f;
+    __syncthreads();
+    const float2 v = cq_rows_pair<BITS>(cq, (size_t)b * kHd, kpad / 32, xs, s_cb, t);
+    if ((t & 15) == 0) {
+      rows[t >> 4] = v.x;
+      rows[(t >> 4) + 32] = v.y;
+    }
+  }
+  const uint32_t pos = st[1];
   const float nscale = b < heads ? q_norm[lane] : k_norm[lane];
   const double rs = rope[lane & 31], rc = rope[32 + (lane & 31)];
-  for (uint32_t i = t; i < d; i += kQkvWg) xs[i] = x[i];
-  __syncthreads();
-  const float acc = qkv_row_dot(wv, xs, t % kQkvTpr, d);
-  if (t % kQkvTpr == 0) rows[t / kQkvTpr] = acc * srow;
   __syncthreads();
   if (t >= 64) return;
   const float val = rows[lane];
@@ -1503,7 +1609,6 @@ struct nd_needle {
            *counters = nullptr;
   double *lp_history = nullptr, *sel_lp = nullptr;
   uint32_t* cq_lookup = nullptr;  // CQ model: a step's engram lookups and token
-  float* cq_proj = nullptr;       // CQ model: a layer's q | k | v | gate projections
   float *ring = nullptr, *x = nullptr, *upd = nullptr, *blk = nullptr, *ain = nullptr,
         *qkvg = nullptr, *q = nullptr, *att = nullptr, *proj = nullptr, *phi_post_v = nullptr,
         *phi_res_v = nullptr, *fin = nullptr, *logits = nullptr, *cat = nullptr, *ekv_out = nullptr,
@@ -1709,16 +1814,24 @@ hipError_t enqueue_block(nd_needle* n, uint32_t l, hipStream_t s) {
   ra.lanes = ln;
   ra.own = l % ln;
   ra.route = n->route;
-  if (n->cq) {  // the Cactus-Quant projections first, then the per-head epilogue
-    const hipError_t e = mv_any(&wm, n->ain, 0, wm.n, n->cq_proj, s);
-    if (e != hipSuccess) return e;
+  CqRows cq{};
+  auto kern = &n2_qkv_kernel<0>;
+  if (n->cq) {
+    cq.packed = wm.packed;
+    cq.norms = wm.norms;
+    for (int i = 0; i < 16; ++i) cq.cb[i] = wm.cb[i];
+    cq.g = wm.g;
+    while ((1u << cq.g_log2) < wm.g) ++cq.g_log2;
+    cq.row_bytes = wm.row_bytes;
+    cq.groups = wm.kpad / wm.g;
+    cq.out_scale = (float)(1.0 / std::sqrt((double)wm.g));
+    kern = wm.bits == 4 ? &n2_qkv_kernel<4> : (wm.bits == 3 ? &n2_qkv_kernel<3> : &n2_qkv_kernel<2>);
   }
-  hipLaunchKernelGGL(n2_qkv_kernel, dim3(wm.n / kHd + 1), dim3(kQkvWg), 0, s, wm.w, wm.scales,
-                     n->ain, D, d.heads, d.kv_heads, n->st, n->params + n->o_qn + (size_t)l * kHd,
-                     n->params + n->o_kn + (size_t)l * kHd, n->rope, n->q, n->qkvg,
-                     n->kv.k, n->kv.v, n->kv.ks, n->kv.vs, l, n->kv.alloc, n->kv.sink,
-                     n->kv.window, n->kv.mode == ND_KV_FLOAT32 ? 1u : 0u, ra,
-                     n->cq ? n->cq_proj : nullptr);
+  hipLaunchKernelGGL(kern, dim3(wm.n / kHd + 1), dim3(kQkvWg), 0, s, wm.w, wm.scales, n->ain, D,
+                     d.heads, d.kv_heads, n->st, n->params + n->o_qn + (size_t)l * kHd,
+                     n->params + n->o_kn + (size_t)l * kHd, n->rope, n->q, n->qkvg, n->kv.k,
+                     n->kv.v, n->kv.ks, n->kv.vs, l, n->kv.alloc, n->kv.sink, n->kv.window,
+                     n->kv.mode == ND_KV_FLOAT32 ? 1u : 0u, ra, cq);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   e = nd_launch_attention_gated(&n->kv, l, n->st + 1, n->max_length - 1, n->q, d.heads, n->qkvg,
@@ -2475,7 +2588,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
                             cb * al((size_t)(d.layers + 1) * P8), cb * al(64), al(32 * 4),
                             al((size_t)2 * S * D * 4),
                             al((size_t)(3 * D + ln * D + ln + ln * ln) * 4),
-                            al((2 * 16 + 1) * 4), al((size_t)(2 * qw + 2 * kw) * 4)};
+                            al((2 * 16 + 1) * 4)};
     size_t total = 0;
     for (size_t v : sizes) total += v;
     ND_HIP(ctx, hipMalloc(&n->arena, total));
@@ -2529,7 +2642,6 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     take(&n->host_eng);
     take(&n->fwd_in);
     take(&n->cq_lookup);
-    take(&n->cq_proj);
   }
   if (!n->pinned) {
     // Pinned staging of the session calls' host inputs.
