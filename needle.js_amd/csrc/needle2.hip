@@ -576,14 +576,12 @@ __device__ float fwht_block(float v, float* hv, uint32_t H, uint32_t t) {
 // Cactus-Quant phi rows of the mix kernel, for one code width (2-bit codes and
 // ternary crumbs: BITS = 2): wave w takes rows w, w + 8 and w + 16, lane u
 // the rows' 32-code unit u, from the packed words w[j] and group norms n[j]
-// it loaded at entry.  x holds the rotated lanes with one pad float after
-// every 32 (element e at e + e / 32): lane u's unit starts at 33 u, so the
-// wave's reads of element c of its units fall in distinct banks.  Each unit
+// it loaded at entry, against xu, the lane's 32 rotated inputs.  Each unit
 // takes fp32 dots over its four 8-code blocks, each block times its group's
 // norm (groups of 8, 16, or 32 and wider) in float64, summed over the wave.
 template <uint32_t BITS>
 __device__ __forceinline__ void cq_phi_rows(const uint32_t (&w)[3][4], const uint32_t (&n)[3][4],
-                                            const float* x, const float* cb, uint32_t g,
+                                            const float (&xu)[32], const float* cb, uint32_t g,
                                             uint32_t units, uint32_t nrows, uint32_t wave,
                                             uint32_t lane, float* phi) {
 #pragma unroll
@@ -592,7 +590,6 @@ __device__ __forceinline__ void cq_phi_rows(const uint32_t (&w)[3][4], const uin
     if (r >= nrows) break;  // uniform over the wave
     double total = 0.0;
     if (lane < units) {
-      const float* xu = x + lane * 33;
       float dot8[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (uint32_t c = 0; c < 32; ++c) {
@@ -838,37 +835,65 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   float pre_phi = 0.f;  // phi_pre row `lane` (lane < lanes): feeds hPre
   if constexpr (CQ) {
     // phi = cqMatvec of the normalized lanes (backends/cq.ts:30-46, 107-231):
-    // prepareCqActivation in LDS -- per group the butterflies (strides 1 ..
-    // g / 2, one fp32 add and subtract per pair, a barrier per stage), then
-    // times 1/sqrt(g) -- and the rows by code width (cq_phi_rows).
-    auto at = [](uint32_t e) { return e + (e >> 5); };  // padded LDS slot
+    // prepareCqActivation -- per group the butterflies (strides 1 .. g / 2,
+    // one fp32 add and subtract per pair), then times 1/sqrt(g) -- and the
+    // rows by code width (cq_phi_rows).  The N <= 2048 normalized values are
+    // 64 units of 32, one per lane of a wave: each wave reads them from LDS
+    // (one pad float after every 32, so lane u's unit starts at 33 u and a
+    // wave's reads fall in distinct banks) and rotates its own copy in
+    // registers, strides below 32 inside the unit and strides 32 .. g / 2
+    // across the lanes holding the group's other units.
     if (col) {
 #pragma unroll
       for (int l = 0; l < 4; ++l)
-        if ((uint32_t)l < L) s_cqx[at(l * D + t)] = (float)((double)xl[l] * inv);
+        if ((uint32_t)l < L) {
+          const uint32_t e = l * D + t;
+          s_cqx[e + (e >> 5)] = (float)((double)xl[l] * inv);
+        }
     }
-    __syncthreads();
-    uint32_t sh = 0;
-    for (uint32_t stride = 1; stride < a.cq_g; stride <<= 1, ++sh) {
-      for (uint32_t i = t; i < N / 2; i += kMixWg) {
-        const uint32_t left = ((i >> sh) << (sh + 1)) | (i & (stride - 1));
-        const uint32_t pl = at(left), pr = at(left + stride);
-        const float x0 = s_cqx[pl], x1 = s_cqx[pr];
-        s_cqx[pl] = x0 + x1;
-        s_cqx[pr] = x0 - x1;
+    nd::lds_barrier();
+    const uint32_t units = N / 32, uc = lane < units ? lane : 0;
+    float xu[32];
+#pragma unroll
+    for (int c = 0; c < 32; ++c) xu[c] = s_cqx[uc * 33 + c];
+    const uint32_t gs = a.cq_g < 32 ? a.cq_g : 32u;
+#pragma unroll
+    for (uint32_t st = 1; st < 32; st <<= 1) {
+      if (st < gs) {
+#pragma unroll
+        for (uint32_t c = 0; c < 32; ++c)
+          if (!(c & st)) {
+            const float x0 = xu[c], x1 = xu[c + st];
+            xu[c] = x0 + x1;
+            xu[c + st] = x0 - x1;
+          }
       }
-      __syncthreads();
     }
-    for (uint32_t i = t; i < N; i += kMixWg)
-      s_cqx[at(i)] = (float)((double)s_cqx[at(i)] * a.cq_inv_root);
-    __syncthreads();
+    auto cross = [&](auto m) {
+      constexpr int M = decltype(m)::value;
+      const bool right = (lane & M) != 0;
+#pragma unroll
+      for (int c = 0; c < 32; ++c) {
+        const float other = nd::lane_xor<M>(xu[c]);
+        xu[c] = right ? other - xu[c] : xu[c] + other;
+      }
+    };
+    const uint32_t lpg = a.cq_g > 32 ? a.cq_g >> 5 : 1u;  // lanes of a group
+    if (lpg > 1) cross(std::integral_constant<int, 1>{});
+    if (lpg > 2) cross(std::integral_constant<int, 2>{});
+    if (lpg > 4) cross(std::integral_constant<int, 4>{});
+    if (lpg > 8) cross(std::integral_constant<int, 8>{});
+    if (lpg > 16) cross(std::integral_constant<int, 16>{});
+    if (lpg > 32) cross(std::integral_constant<int, 32>{});
+#pragma unroll
+    for (int c = 0; c < 32; ++c) xu[c] = (float)((double)xu[c] * a.cq_inv_root);
     if (a.cq_bits == 4)
-      cq_phi_rows<4>(cw, cn, s_cqx, s_cb, a.cq_g, N / 32, nrows, wave, lane, phi);
+      cq_phi_rows<4>(cw, cn, xu, s_cb, a.cq_g, units, nrows, wave, lane, phi);
     else if (a.cq_bits == 3)
-      cq_phi_rows<3>(cw, cn, s_cqx, s_cb, a.cq_g, N / 32, nrows, wave, lane, phi);
+      cq_phi_rows<3>(cw, cn, xu, s_cb, a.cq_g, units, nrows, wave, lane, phi);
     else  // 2-bit codes and ternary crumbs
-      cq_phi_rows<2>(cw, cn, s_cqx, s_cb, a.cq_g, N / 32, nrows, wave, lane, phi);
-    __syncthreads();
+      cq_phi_rows<2>(cw, cn, xu, s_cb, a.cq_g, units, nrows, wave, lane, phi);
+    nd::lds_barrier();
     if (t < nrows) {
       const float v = phi[t];
       if (t >= L && t < 2 * L) a.phi_post[t - L] = v;
