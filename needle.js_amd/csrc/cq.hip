@@ -354,18 +354,26 @@ using CqFn = void (*)(const uint8_t*, const uint16_t*, Codebook, const float*, u
 constexpr int kRacc = 8;  // rows per thread: rpp * 8 <= 256 outputs per workgroup
 constexpr uint32_t kMaxRotateGroup = 2048;  // 64 lanes of 32 codes
 
-template <int UB, bool ROTATE, bool VEC>
+template <int UB, int RACC, bool ROTATE, bool VEC>
 CqFn pick_ng(uint32_t g) {
-  return g >= 32   ? &cq_matvec_kernel<UB, 1, kRacc, ROTATE, VEC>
-         : g == 16 ? &cq_matvec_kernel<UB, 2, kRacc, ROTATE, VEC>
-                   : &cq_matvec_kernel<UB, 4, kRacc, ROTATE, VEC>;
+  return g >= 32   ? &cq_matvec_kernel<UB, 1, RACC, ROTATE, VEC>
+         : g == 16 ? &cq_matvec_kernel<UB, 2, RACC, ROTATE, VEC>
+                   : &cq_matvec_kernel<UB, 4, RACC, ROTATE, VEC>;
 }
 
+template <int RACC, bool ROTATE, bool VEC>
+CqFn pick_w(const nd_mat* m) {
+  return m->bits == 4   ? pick_ng<16, RACC, ROTATE, VEC>(m->g)
+         : m->bits == 3 ? pick_ng<12, RACC, ROTATE, VEC>(m->g)
+                        : pick_ng<8, RACC, ROTATE, VEC>(m->g);
+}
+
+// kRacc rows per thread, or one when kRacc would give the launch fewer than
+// 256 workgroups (small matrices: more workgroups, each on fewer rows) and a
+// row has at most 64 units.
 template <bool ROTATE, bool VEC>
-CqFn pick(const nd_mat* m) {
-  return m->bits == 4   ? pick_ng<16, ROTATE, VEC>(m->g)
-         : m->bits == 3 ? pick_ng<12, ROTATE, VEC>(m->g)
-                        : pick_ng<8, ROTATE, VEC>(m->g);
+CqFn pick(const nd_mat* m, uint32_t racc) {
+  return racc == 1 ? pick_w<1, ROTATE, VEC>(m) : pick_w<kRacc, ROTATE, VEC>(m);
 }
 
 }  // namespace
@@ -393,14 +401,20 @@ hipError_t nd_launch_cq_matvec(const nd_mat* m, const float* x, uint32_t batch, 
   uint32_t tpr_log2 = 3;  // at least 8 threads per row: rpp * kRacc <= 256 outputs
   while ((1u << tpr_log2) < units) ++tpr_log2;
   const uint32_t rpp = kCqThreads >> tpr_log2;
-  const uint32_t blocks = (row_count + rpp * kRacc - 1) / (rpp * kRacc);
+  // One row per thread keeps a row's threads in one wave (the row sum's
+  // butterfly spans T = tpr lanes): rows of at most 64 units.
+  const uint32_t racc =
+      tpr_log2 <= 6 && (uint64_t)((row_count + rpp * kRacc - 1) / (rpp * kRacc)) * batch < 256
+          ? 1u
+          : kRacc;
+  const uint32_t blocks = (row_count + rpp * racc - 1) / (rpp * racc);
   uint32_t g_log2 = 0;
   while ((1u << g_log2) < m->g) ++g_log2;
   const uint32_t lanes_per_group = m->g > 32 ? m->g / 32 : 1;
   if (m->g <= kMaxRotateGroup) {
     const bool vec = (m->k & 3) == 0 && (x_stride & 3) == 0 &&
                      (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-    const CqFn f = vec ? pick<true, true>(m) : pick<true, false>(m);
+    const CqFn f = vec ? pick<true, true>(m, racc) : pick<true, false>(m, racc);
     hipLaunchKernelGGL(f, dim3(blocks, batch), dim3(kCqThreads), 0, s, m->packed,
                        m->norms, codebook_of(m), x, x_stride, y, y_stride, m->k, m->kpad, g_log2,
                        m->row_bytes, row_start, row_count, tpr_log2, lanes_per_group,
@@ -411,7 +425,7 @@ hipError_t nd_launch_cq_matvec(const nd_mat* m, const float* x, uint32_t batch, 
     const uint32_t nb = batch - b0 < kCqPreparedRows ? batch - b0 : kCqPreparedRows;
     hipError_t e = nd_launch_cq_prepare(m, x + (size_t)b0 * x_stride, nb, x_stride, prepared, s);
     if (e != hipSuccess) return e;
-    const CqFn f = pick<false, true>(m);
+    const CqFn f = pick<false, true>(m, racc);
     hipLaunchKernelGGL(f, dim3(blocks, nb), dim3(kCqThreads), 0, s, m->packed,
                        m->norms, codebook_of(m), prepared, m->kpad, y + (size_t)b0 * y_stride,
                        y_stride, m->k, m->kpad, g_log2, m->row_bytes, row_start, row_count,
