@@ -21,7 +21,7 @@ JavaScript regular expressions (`pattern`, and the email/uuid `format`s) are
 evaluated with Python's `re`, which agrees with them on the common syntax.
 Parity unpinned for those two features: no test or fixture of the reference
 covers a schema with `pattern` or `format`, and where JavaScript's and
-Python's regex dialects differ (lookbehind forms, `\d` over Unicode digits,
+Python's regex dialects differ (lookbehind forms, digit classes over Unicode digits,
 the `u`/`v` flags) the allowed pieces can differ.
 """
 
