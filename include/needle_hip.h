@@ -221,7 +221,7 @@ nd_status nd_attention_d(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t 
  * device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  No counterpart in the reference.  Identical
  * arguments and results; the partial results and arrival counters live in a
- * fixed per-GPU array (1,085,440 bytes, set up by nd_create) instead of the
+ * fixed per-GPU array (1,089,536 bytes, set up by nd_create) instead of the
  * context's workspace, so q_heads is limited to 64 (ND_ERR_INVALID above).
  * Every call on one GPU shares that array: calls that overlap on one GPU --
  * from any context or stream -- race and must be ordered by the caller. */

@@ -205,7 +205,7 @@ __device__ __forceinline__ float gate_factor(float g) { return 1.f / (1.f + __ex
 // row r is query z0 + r / G (z0 = (REP / G) blockIdx.z, rows at or past
 // `qrows` absent), head G blockIdx.y + r % G, with its own causal limit --
 // so every K/V tile is read once for all of them.
-template <int REP, bool F32, bool QB = false, int KW = 4, int TILES = 0>
+template <int REP, bool F32, bool QB = false, int KW = 4, int TILES = 0, bool XL = false>
 __global__ __launch_bounds__(64 * KW) void attention_kernel(
     const void* __restrict__ Kc, const void* __restrict__ Vc, const float* __restrict__ Ks,
     const float* __restrict__ Vs, const float* __restrict__ Q, float* __restrict__ out,
@@ -220,7 +220,23 @@ __global__ __launch_bounds__(64 * KW) void attention_kernel(
   // z indexes query rows: sequences of a batch (kv_stride_z = seq_kv_heads,
   // each with its own cache heads) or positions of one prefill (kv_stride_z
   // = 0, all reading the same cache heads).
-  const uint32_t chunk = blockIdx.x, kvh_local = blockIdx.y, z = blockIdx.z;
+  uint32_t chunk, kvh_local, z;
+  if constexpr (XL) {
+    // A one-dimensional grid laid out so that every chunk of a (row, KV
+    // head) pair runs on one XCD: the dispatcher hands workgroup L to XCD
+    // L % 8, so pair g = 8 (L / 8 % gpx) + L % 8 (row g / seq_kv_heads) and
+    // chunk L / (8 gpx), gpx = ceil(pairs / 8).
+    const uint32_t pairs = qrows * seq_kv_heads, gpx = (pairs + 7) / 8;
+    const uint32_t L = blockIdx.x, sl = L >> 3, g = 8 * (sl % gpx) + (L & 7);
+    chunk = sl / gpx;
+    if (g >= pairs) return;
+    z = g / seq_kv_heads;
+    kvh_local = g % seq_kv_heads;
+  } else {
+    chunk = blockIdx.x;
+    kvh_local = blockIdx.y;
+    z = blockIdx.z;
+  }
   const uint32_t kvh = z * kv_stride_z + kvh_local;
   const uint32_t hq = seq_kv_heads * REP;
   // The wave index is uniform: read it into a scalar register so that the
@@ -492,18 +508,21 @@ __global__ __launch_bounds__(64 * KW) void attention_kernel(
   // Several chunks: publish this chunk's (max, sum, acc) with agent-coherent
   // stores, wait for them, count the chunk in; the last chunk of the (row,
   // KV head) to arrive combines all of them (log-sum-exp) and resets the
-  // counter for the next launch.  No workgroup waits for another.
+  // counter for the next launch.  No workgroup waits for another.  XL: all
+  // chunks of the head share one XCD, so the partials and counters stay in
+  // its L2 (plain stores, atomics performed there); the merge's agent-scope
+  // loads miss the CU's L1 and hit that L2.  Each head's counters fill
+  // 128-byte lines of their own.
+  constexpr int kPubScope = XL ? __HIP_MEMORY_SCOPE_WORKGROUP : __HIP_MEMORY_SCOPE_AGENT;
   if (part == 0) {
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
       const uint32_t h = w_o[u] / kHeadDim, dim = w_o[u] % kHeadDim;
       const size_t pi = (row0 + h) * max_chunks + chunk;
-      __hip_atomic_store(part_acc + pi * kHeadDim + dim, w_a[u], __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(part_acc + pi * kHeadDim + dim, w_a[u], __ATOMIC_RELAXED, kPubScope);
       if (dim == 0) {
-        __hip_atomic_store(part_ml + pi * 2, w_m[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(part_ml + pi * 2 + 1, w_l[u], __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(part_ml + pi * 2, w_m[u], __ATOMIC_RELAXED, kPubScope);
+        __hip_atomic_store(part_ml + pi * 2 + 1, w_l[u], __ATOMIC_RELAXED, kPubScope);
       }
     }
   }
@@ -511,26 +530,25 @@ __global__ __launch_bounds__(64 * KW) void attention_kernel(
   __syncthreads();
   // Election: rows of more than kChunkGroup chunks count in per group first
   // and the last of each group then on the row's counter, so that no counter
-  // serializes more than kChunkGroup arrivals (atomics on one address
-  // complete ~70 ns apart).  Each counter is reset by its last arriver.
+  // serializes more than kChunkGroup arrivals (agent-scope atomics on one
+  // address complete ~70 ns apart); XL counts every chunk on the row's
+  // counter (atomics in the XCD's L2 do not serialize so).  Each counter is
+  // reset by its last arriver.
   __shared__ uint32_t s_last;
   uint32_t* counter = counters + ((size_t)z * seq_kv_heads + kvh_local) * kAttnCounterStride;
   if (threadIdx.x == 0) {
     bool last;
-    if (nchunks <= kChunkGroup) {
-      last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-             nchunks - 1;
+    if (XL || nchunks <= kChunkGroup) {
+      last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, kPubScope) == nchunks - 1;
     } else {
       const uint32_t grp = chunk / kChunkGroup;
       const uint32_t ngroups = (nchunks + kChunkGroup - 1) / kChunkGroup;
       const uint32_t members = min(kChunkGroup, nchunks - grp * kChunkGroup);
       uint32_t* gc = counter + 1 + grp;
       last = false;
-      if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-          members - 1) {
-        __hip_atomic_store(gc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-               ngroups - 1;
+      if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, kPubScope) == members - 1) {
+        __hip_atomic_store(gc, 0u, __ATOMIC_RELAXED, kPubScope);
+        last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, kPubScope) == ngroups - 1;
       }
     }
     s_last = last;
@@ -605,17 +623,19 @@ __global__ __launch_bounds__(64 * KW) void attention_kernel(
       out_z[oi] = r;
     }
   }
-  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, kPubScope);
 }
 
 // Positions per chunk: the whole visible range when the (row, kv head) pairs
 // alone give `target` workgroups, else split so that they do; at least one
 // tile per wave.  Splitting costs a publish + count + merge round trip at the
 // end, yet more, smaller workgroups win: a single query row aims at 256
-// workgroups (32 chunks of 256 per head at 8 heads x 8192, elected in groups
-// of 8: 7.95 us per call, vs 8.9 at 128 workgroups and 10.4 at 64) and
-// batches at 8192 (64 sequences x 8 heads at contexts up to 2176: chunks of
-// 256, 20.3 us per layer, vs 21.6 with chunks of 512 at 4096 workgroups).
+// workgroups (32 chunks of 256 per head at 8 heads x 8192: 7.0 us per call
+// with the XCD-local merge, 7.95 with the agent-scope one elected in groups
+// of 8, 8.9 with that at 128 workgroups and 10.4 at 64) and batches at 8192
+// (64 sequences x 8 heads at contexts up to 2176: chunks of 256, 20.3 us per
+// layer, vs 21.6 with chunks of 512 at 4096 workgroups; the XCD-local
+// layout measured slower there, 0.453 against 0.442 ms per decode step).
 // One tile per wave also runs the leanest kernel form (73 VGPRs: 6 waves
 // per SIMD).
 constexpr uint32_t kTargetSingle = 256, kTargetBatch = 8192;
@@ -1002,6 +1022,20 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
   float* part_ml = a.partials + (size_t)a.batch * hq * max_chunks * kHeadDim;
   // Tiles per wave: cp / kMinChunk (cp is a multiple of it).
   const uint32_t tiles = cp / kMinChunk;
+  if (a.batch == 1 && max_chunks > 1) {
+    // One query row split into chunks: the XCD-local merge (grid laid out
+    // per XCD, see attention_kernel).
+    auto kernel = tiles == 1   ? attention_kernel<REP, F32, false, kWaves, 1, true>
+                  : tiles == 2 ? attention_kernel<REP, F32, false, kWaves, 2, true>
+                               : attention_kernel<REP, F32, false, kWaves, 0, true>;
+    const uint32_t gpx = (a.batch * a.seq_kv_heads + 7) / 8;
+    hipLaunchKernelGGL(kernel, dim3(8 * gpx * max_chunks), dim3(64 * kWaves), 0, s, a.kv->k,
+                       a.kv->v, a.kv->ks, a.kv->vs, a.q, a.out, a.gate, a.gate_ld, part_acc,
+                       part_ml, a.counters, a.layer, a.kv->kv_heads, a.kv->alloc, a.kv->sink,
+                       a.kv->window, a.vis, a.positions, a.slot_space, a.seq_kv_heads,
+                       a.kv_stride_z, cp, max_chunks, 0.125f, a.batch, 1u);
+    return hipGetLastError();
+  }
   auto kernel = tiles == 1   ? attention_kernel<REP, F32, false, kWaves, 1>
                 : tiles == 2 ? attention_kernel<REP, F32, false, kWaves, 2>
                              : attention_kernel<REP, F32, false, kWaves, 0>;

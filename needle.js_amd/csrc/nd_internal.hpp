@@ -214,7 +214,7 @@ hipError_t nd_launch_attention_batch(const nd_kv* kv, uint32_t layer, const uint
 // kAttnCounterStride -- which a launch that splits a row into several chunks
 // uses to elect the chunk that merges them (a counter per group of chunks,
 // then one per row and head), and leaves at zero again.
-constexpr uint32_t kAttnCounterStride = 16;
+constexpr uint32_t kAttnCounterStride = 32;  // 128 bytes: one L2 line per row and head
 // Fixed device scratch of nd_attention_static_d (kv_attention.hip): the chunk
 // partials of one query row -- acc [q_heads][chunks][64] then (max, sum)
 // [q_heads][chunks][2] -- for up to kStaticAttnQHeads query heads and the
