@@ -383,10 +383,20 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_slice_kernel(
   __shared__ float s_max[kMfmaWaves];
   __shared__ int s_e[kSplitRows];
   static_assert(kSg * 64 * 16 >= kMfmaWaves * 4 * 64 * 4, "the sums fit the x image");
+  // The grid is laid out so that every slice of a row block runs on one XCD
+  // (the dispatcher hands workgroup L to XCD L % 8): row block rb = 8 (L / 8
+  // % rpx) + L % 8, slice L / (8 rpx), rpx = ceil(blocks / 8).  The slice sum
+  // then stays in that XCD's L2: partials stored and counted at workgroup
+  // scope (plain stores, the atomic performed in the L2), read by the last
+  // slice with agent-scope loads, which miss the CU's L1 and hit the L2.
+  const uint32_t nblocks = (row_count + 63) / 64, rpx = (nblocks + 7) / 8;
+  const uint32_t L = blockIdx.x, sl = L >> 3, rb = 8 * (sl % rpx) + (L & 7);
+  const uint32_t nslices = gridDim.x / (8 * rpx);
+  if (rb >= nblocks) return;
   const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const uint32_t r16 = lane & 15, kb = lane >> 4;
-  const uint32_t slice = blockIdx.y, k0 = slice * KS;
-  const uint32_t row0 = blockIdx.x * 64;
+  const uint32_t slice = sl / rpx, k0 = slice * KS;
+  const uint32_t row0 = rb * 64;
   const uint32_t tile = wave & 3, wq = wave >> 2;
 
   // x: thread t < 8 kUnits takes batch row xb = t / kUnits, unit j of the
@@ -506,16 +516,18 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_slice_kernel(
   const uint32_t b = (lane >> 4) * 4 + oc, orow = row0 + 16 * ot + (lane & 15);
   if (lane < 32 && orow < row_count && b < bc)
     __hip_atomic_store(P + ((size_t)slice * kSplitRows + b) * row_count + orow,
-                       ldexpf(sum, s_e[b]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // Count the slice in once its partials are stored (agent-coherent stores,
-  // completed); the last slice of the row block adds all of them in order s
-  // = 0, 1, ... and resets the counter for the next launch.
+                       ldexpf(sum, s_e[b]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  // Count the slice in once its partials are stored (completed in the L2);
+  // the last slice of the row block adds all of them in order s = 0, 1, ...
+  // and resets the counter for the next launch.  Each row block's counter
+  // has a 128-byte line of its own.
+  uint32_t* const counter = counters + (size_t)rb * 32;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   __shared__ uint32_t s_last;
   if (t == 0)
-    s_last = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT) == gridDim.y - 1;
+    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
+             nslices - 1;
   __syncthreads();
   if (!s_last) return;
   const uint32_t fb = t >> 6, frow = row0 + (t & 63);
@@ -523,16 +535,16 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_slice_kernel(
     float v[kMaxSlices];
 #pragma unroll
     for (uint32_t q = 0; q < kMaxSlices; ++q)
-      v[q] = q < gridDim.y ? __hip_atomic_load(P + ((size_t)q * kSplitRows + fb) * row_count + frow,
-                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                           : 0.f;
+      v[q] = q < nslices ? __hip_atomic_load(P + ((size_t)q * kSplitRows + fb) * row_count + frow,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                         : 0.f;
     float total = v[0];
 #pragma unroll
     for (uint32_t q = 1; q < kMaxSlices; ++q)
-      if (q < gridDim.y) total += v[q];
+      if (q < nslices) total += v[q];
     Y[(size_t)fb * y_stride + frow] = total;
   }
-  if (t == 0) __hip_atomic_store(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (t == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // Read-only stream over `units` 16-byte units: the matvec's own load form
@@ -627,14 +639,18 @@ hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uin
       const bool wide = ((row_count + 63) / 64) * (m->k / 1024) >= 256;
       const uint32_t ks = wide ? 1024 : 512, slices = m->k / ks;
       const size_t cap = kMatvecPartialBytes / sizeof(float) / ((size_t)slices * kSplitRows);
-      const uint32_t block = (uint32_t)(cap / 64 * 64);
+      // Row blocks per launch: within the partials and within the counters
+      // (one 32-word line per row block in the split's last 64 KB).
+      constexpr size_t kCounterBlocks = (kMatvecSplitBytes - kMatvecPartialBytes) / (32 * 4);
+      const uint32_t block = (uint32_t)(std::min(cap / 64, kCounterBlocks) * 64);
       float* P = reinterpret_cast<float*>(split);
       uint32_t* counters = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(split) +
                                                        kMatvecPartialBytes);
       for (uint32_t r0 = 0; r0 < row_count; r0 += block) {
         const uint32_t rc = row_count - r0 < block ? row_count - r0 : block;
         const auto kern = wide ? &matvec_mfma_slice_kernel<4> : &matvec_mfma_slice_kernel<2>;
-        hipLaunchKernelGGL(kern, dim3((rc + 63) / 64, slices), dim3(64 * kMfmaWaves), 0, s, m->w,
+        const uint32_t rpx = ((rc + 63) / 64 + 7) / 8;  // row blocks per XCD
+        hipLaunchKernelGGL(kern, dim3(8 * rpx * slices), dim3(64 * kMfmaWaves), 0, s, m->w,
                            m->scales, xb, x_stride, P, counters, yb + r0, y_stride, m->k,
                            m->k / m->g, gshift, row_start + r0, rc, bc);
         hipError_t e = hipGetLastError();
