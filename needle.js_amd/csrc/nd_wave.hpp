@@ -150,5 +150,13 @@ __device__ __forceinline__ T quad_sum(T v) {
 // write-back and invalidate of the whole XCD L2) and measured +2.4 us per
 // attention call at 8 heads x 8192, +7.3 us per batch-8 4096x4096 matvec and
 // twice the batch-64 decode step, so they are not used.
+//
+// XCD-local form (single-row attention, batch matvec slices): the dispatcher
+// hands workgroup L of a launch to XCD L % 8, so a grid laid out with every
+// member of a merge group at the same L % 8 keeps the group on one XCD.  The
+// partials are then stored and counted at workgroup scope (plain stores;
+// the atomic, like every global atomic, performed in the L2) and read with
+// the agent-scope loads above, which miss the CU's L1 and hit that L2: the
+// round trips end in the XCD's L2 instead of the agent coherence point.
 
 }  // namespace nd
