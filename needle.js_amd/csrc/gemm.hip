@@ -549,17 +549,31 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
   }
   if (S > 1) {
     const uint32_t tile = blockIdx.y * gridDim.x + blockIdx.x;
+    // Workgroup (x, y, z) runs on XCD (tile + tiles z) % 8: with a multiple
+    // of 8 tiles every slice of a tile shares its XCD, and the slice sum
+    // stays in that XCD's L2 (workgroup-scope stores and counter; the
+    // agent-scope loads below miss the CU's L1 and hit the L2).
+    const bool xl = (gridDim.x * gridDim.y) % 8 == 0;
     float* mine = part + ((size_t)tile * S + blockIdx.z) * 1024;
+    if (xl) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __hip_atomic_store(mine + i * kGemmThreads + t, cs[i], __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+      for (int i = 0; i < 4; ++i)
+        __hip_atomic_store(mine + i * kGemmThreads + t, cs[i], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        __hip_atomic_store(mine + i * kGemmThreads + t, cs[i], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
     __builtin_amdgcn_s_waitcnt(0);  // every store above has completed
     __syncthreads();
     __shared__ uint32_t s_last;
     if (t == 0)
-      s_last = __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+      s_last = (xl ? __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_WORKGROUP)
+                   : __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT)) == S - 1;
     __syncthreads();
     if (!s_last) return;
     const float* all = part + (size_t)tile * S * 1024;
@@ -580,7 +594,12 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
         if ((uint32_t)z < S) sum += pv[z][i];
       cs[i] = sum;
     }
-    if (t == 0) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t == 0) {
+      if (xl)
+        __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      else
+        __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   if constexpr (EPI == 3) {
     // The tile is one head (column tile blockIdx.x) of 16 rows: through LDS
