@@ -643,7 +643,8 @@ __global__ __launch_bounds__(64 * KW) void attention_kernel(
 constexpr uint32_t kTargetSingle = 256, kTargetBatch = 8192;
 constexpr uint32_t kMaxChunks = 64;  // the merge holds one chunk per lane
 static_assert(1 + kMaxChunks / kChunkGroup <= kAttnCounterStride, "group counters fit the stride");
-uint32_t chunk_positions_for(uint32_t max_count, uint32_t pairs, uint32_t target) {
+uint32_t chunk_positions_for(uint32_t max_count, uint32_t pairs, uint32_t target,
+                             uint32_t min_chunk = kMinChunk) {
   uint32_t want_chunks = pairs >= target ? 1 : (target + pairs - 1) / pairs;
   // Up to two tiles per wave stay in one chunk: the merge round trips cost
   // more than streaming the second, prefetched tile (5.7 vs 6.3 us at 512
@@ -652,8 +653,8 @@ uint32_t chunk_positions_for(uint32_t max_count, uint32_t pairs, uint32_t target
   if (max_count <= 2 * kMinChunk) want_chunks = 1;
   if (want_chunks > kMaxChunks) want_chunks = kMaxChunks;
   uint32_t cp = (max_count + want_chunks - 1) / want_chunks;
-  cp = (cp + kMinChunk - 1) / kMinChunk * kMinChunk;
-  return cp < kMinChunk ? kMinChunk : cp;
+  cp = (cp + min_chunk - 1) / min_chunk * min_chunk;
+  return cp < min_chunk ? min_chunk : cp;
 }
 
 struct AttnLaunch {
@@ -1024,6 +1025,26 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
   float* part_ml = a.partials + (size_t)a.batch * hq * max_chunks * kHeadDim;
   // Tiles per wave: cp / kMinChunk (cp is a multiple of it).
   const uint32_t tiles = cp / kMinChunk;
+  if (a.batch == 1 && max_chunks > 1 && a.seq_kv_heads * max_chunks < kTargetSingle) {
+    // One row whose 256-position chunks leave the launch short of
+    // kTargetSingle workgroups (8 heads x 2048: 64): two-wave workgroups on
+    // 128-position chunks double them (5.85 against 6.28 us at 2048; at
+    // 8192, already 256 workgroups, the four-wave form stays faster).
+    constexpr uint32_t kHalf = kWavePositions * 2;
+    const uint32_t cp2 = chunk_positions_for(a.max_count, a.seq_kv_heads, kTargetSingle, kHalf);
+    const uint32_t mc2 = (a.max_count + cp2 - 1) / cp2;
+    if (cp2 == kHalf && mc2 <= kMaxChunks) {
+      float* pm2 = a.partials + (size_t)hq * mc2 * kHeadDim;
+      const uint32_t gpx = (a.seq_kv_heads + 7) / 8;
+      hipLaunchKernelGGL((attention_kernel<REP, F32, false, 2, 1, true>), dim3(8 * gpx * mc2),
+                         dim3(64 * 2), 0, s, a.kv->k, a.kv->v, a.kv->ks, a.kv->vs, a.q, a.out,
+                         a.gate, a.gate_ld, part_acc, pm2, a.counters, a.layer, a.kv->kv_heads,
+                         a.kv->alloc, a.kv->sink, a.kv->window, a.vis, a.positions,
+                         a.slot_space, a.seq_kv_heads, a.kv_stride_z, cp2, mc2, 0.125f, a.batch,
+                         1u);
+      return hipGetLastError();
+    }
+  }
   if (max_chunks > 1) {
     // Rows split into chunks: the XCD-local merge (grid laid out per XCD,
     // see attention_kernel).
@@ -1120,15 +1141,18 @@ uint32_t nd_attention_chunks(uint32_t count, uint32_t kv_heads) {
 
 // Partials for any launch with visible counts <= count (chunks are at least
 // kMinChunk positions).
+// A single row may take 128-position chunks (two-wave workgroups), batches
+// 256-position ones.
 size_t nd_attention_partial_floats(uint32_t q_heads, uint32_t kv_heads, uint32_t count) {
   (void)kv_heads;
-  return (size_t)q_heads * ((count + kMinChunk - 1) / kMinChunk) * (kHeadDim + 2);
+  const uint32_t unit = kWavePositions * 2;
+  return (size_t)q_heads * ((count + unit - 1) / unit) * (kHeadDim + 2);
 }
 
 size_t nd_attention_batch_partial_floats(uint32_t batch, uint32_t seq_kv_heads, uint32_t rep,
                                          uint32_t max_count) {
-  return (size_t)batch * seq_kv_heads * rep * ((max_count + kMinChunk - 1) / kMinChunk) *
-         (kHeadDim + 2);
+  const uint32_t unit = batch == 1 ? kWavePositions * 2 : kMinChunk;
+  return (size_t)batch * seq_kv_heads * rep * ((max_count + unit - 1) / unit) * (kHeadDim + 2);
 }
 
 hipError_t nd_launch_kv_store(const nd_kv* kv, uint32_t layer, uint32_t position, uint32_t first,
