@@ -215,6 +215,35 @@ def test_attention_int8_mha_contexts(hip, length):
     kv.free()
 
 
+def test_chunk_merges_repeat_bit_identically(hip):
+    """The launches whose workgroups merge partial results through arrival
+    counters -- single-row attention with each head's chunks on one XCD (8192
+    positions: 32 chunks of 256 per head; 2048: 16 chunks of 128 on two-wave
+    workgroups) and the batch-8 matvec's slice sum -- leave every counter at
+    zero: 24 launches in a row give the same bits, which match the oracle."""
+    heads = 8
+    for length in (8192, 2048):
+        say("attention repeat", length)
+        kv = HipKvCache(hip, 1, heads, max_length=length)
+        ref = oracle.KvCache(1, heads, max_length=length)
+        s = _fill(kv, ref, 0, length, heads, 31)
+        q = s.normal((heads * 64,))
+        first = np.asarray(kv.attention(0, length - 1, q), np.float32)
+        assert_close(first, ref.attention(0, length - 1, q), RTOL, ATOL, f"attention L={length}")
+        for i in range(24):
+            again = np.asarray(kv.attention(0, length - 1, q), np.float32)
+            assert np.array_equal(again.view(np.uint32), first.view(np.uint32)), (length, i)
+        kv.free()
+    say("matvec batch 8 repeat")
+    m = matrix(33, 4096, 4096, 32)
+    x = synth.Stream(6, "repeat-x").normal((8, 4096))
+    first = np.asarray(hip.matvec(m, x), np.float32)
+    assert_close(first, oracle.matvec_i8(m.codes, m.scales, 32, x), RTOL, ATOL, "matvec b8")
+    for i in range(24):
+        again = np.asarray(hip.matvec(m, x), np.float32)
+        assert np.array_equal(again.view(np.uint32), first.view(np.uint32)), ("matvec", i)
+
+
 @pytest.mark.parametrize("sink,window,mode", [(0, 256, "int8"), (7, 256, "int8"), (3, 5, "int8"),
                                               (0, 0, "float32"), (4, 16, "float32")])
 def test_attention_gqa_window_sink(hip, sink, window, mode):
