@@ -606,7 +606,7 @@ def bench_needle2(torch, hip, reps, check, cpu_seconds):
             # begin, engram projections + convolution, per layer mix / QKV /
             # attention / Wo, the final mix, lm head and selection, and the
             # confidence pool (the head is on, as the reference's default)
-            "launches_per_token": 2 + len(g.sites) + 4 * g.layers + 3
+            "launches_per_token": 2 + len(g.sites) + 3 * g.layers + 3
                                   + int(model.resident.has_confidence),
             "confidence_pool": model.resident.has_confidence}
     part["decode_frac_hbm"] = part["decode_GBps"] / HBM_PEAK_GBS

@@ -466,7 +466,75 @@ struct MixArgs {
   // final_row computes the final norm.
   float* cell;
   uint32_t cell_ld, final_row;
+  // Wo of layer l - 1 in the same launch (n2_mix_kernel<false, true>): proj =
+  // Wo att (codes [wo_n][wo_k], one scale per row), rows in wo_groups
+  // workgroups that count in on wo_count.
+  const int8_t* wo_w;
+  const float* wo_s;
+  const float* wo_x;
+  uint32_t wo_n, wo_k, wo_groups, wo_tpr_log2;
+  uint32_t* wo_count;
 };
+
+// Rows [rpw k, +rpw) of proj = Wo att in the fused Wo + mix launch, rpw =
+// kMixWg / tpr, tpr = wo_k / 16 threads a row.  Each thread's arithmetic is
+// matvec_i8_kernel's for one batch row with one 16-byte segment per thread
+// and one scale per row: the segment's 16 inputs and their sum, the codes
+// biased to unsigned bytes, d = -128 sum + the fmas, times the row scale;
+// the row's threads then add in the same butterfly (lanes 32, 16, ..., 1
+// apart, as far as tpr reaches).  So proj holds the bits the separate Wo
+// launch gives.  The rows are stored at workgroup scope and the workgroup
+// counts itself in: every one of these workgroups and the mix workgroup run
+// on one XCD (the launch uses workgroups L % 8 == 0 only), so both stay in
+// its L2.
+__device__ __forceinline__ void wo_rows(const MixArgs& a, uint32_t k) {
+  const uint32_t t = threadIdx.x, tpr_log2 = a.wo_tpr_log2, tpr = 1u << tpr_log2;
+  const uint32_t rpw = kMixWg >> tpr_log2, sub = t >> tpr_log2, lk = t & (tpr - 1);
+  const uint32_t row = k * rpw + sub;
+  const bool ok = row < a.wo_n;
+  const uint32_t r = ok ? row : 0;
+  float xr[16];
+  const float4* xp = reinterpret_cast<const float4*>(a.wo_x) + lk * 4;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 f = xp[q];
+    xr[4 * q] = f.x;
+    xr[4 * q + 1] = f.y;
+    xr[4 * q + 2] = f.z;
+    xr[4 * q + 3] = f.w;
+  }
+  const u32x4 wv = __builtin_nontemporal_load(
+      reinterpret_cast<const u32x4*>(a.wo_w + (size_t)r * a.wo_k) + lk);
+  const float sv = a.wo_s[r];
+  float xs = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) xs += (xr[4 * q] + xr[4 * q + 1]) + (xr[4 * q + 2] + xr[4 * q + 3]);
+  const uint32_t words[4] = {wv.x ^ 0x80808080u, wv.y ^ 0x80808080u, wv.z ^ 0x80808080u,
+                             wv.w ^ 0x80808080u};
+  float d = -128.f * xs;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) d = fmaf((float)((words[q] >> (8 * e)) & 0xffu), xr[4 * q + e], d);
+  float sum = 0.f;
+  sum += fmaf(sv, d, 0.f);
+  if (tpr > 32) sum += nd::lane_xor<32>(sum);
+  if (tpr > 16) sum += nd::lane_xor<16>(sum);
+  if (tpr > 8) sum += nd::lane_xor<8>(sum);
+  if (tpr > 4) sum += nd::lane_xor<4>(sum);
+  if (tpr > 2) sum += nd::lane_xor<2>(sum);
+  if (tpr > 1) sum += nd::lane_xor<1>(sum);
+  if (lk == 0 && ok)
+    __hip_atomic_store(const_cast<float*>(a.proj) + row, sum, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_WORKGROUP);
+  __builtin_amdgcn_s_waitcnt(0);  // the rows are in the L2
+  __syncthreads();
+  if (t == 0) __hip_atomic_fetch_add(a.wo_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Bound on the mix workgroup's wait for the Wo rows (a safety net: every Wo
+// workgroup is dispatched before it and none waits on anything).
+constexpr uint32_t kWoSpin = 1u << 16;
 
 // sigmoid in float64 as the kernels evaluate it (host side: the constants
 // a mix launch takes precomputed).
@@ -641,9 +709,19 @@ constexpr int kPhiPairs = 8;
 // read at the same k).  D rows 0 and 1 (hi, lo) land in lanes 0..15, outputs
 // 0 and 1; the four waves of a tile meet in LDS and the sum is taken in
 // float64 times the row scale.
-template <bool CQ>
+template <bool CQ, bool WO = false>
 __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
-  if (blockIdx.x) {
+  static_assert(!(CQ && WO), "the fused Wo takes int8 rows");
+  if constexpr (WO) {
+    // Workgroups L % 8 == 0 only (one XCD): L / 8 < wo_groups computes Wo
+    // rows, L / 8 == wo_groups (dispatched after all of them) runs the mix.
+    if (blockIdx.x & 7) return;
+    const uint32_t k = blockIdx.x >> 3;
+    if (k < a.wo_groups) {
+      wo_rows(a, k);
+      return;
+    }
+  } else if (blockIdx.x) {
     const uint32_t m = blockIdx.x, D0 = a.d, L0 = a.lanes;
     a.x += (size_t)m * L0 * D0;
     a.proj += (size_t)m * D0;
@@ -682,7 +760,8 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   const float* const s1 = a.phi_s[1];
   const float* const s2 = a.phi_s[2];
   const uint32_t tc = min(t, D - 1);
-  const float p = a.proj[tc], blk = a.blk[tc], upd = a.upd[tc], post_norm = a.post_norm[tc],
+  float p = WO ? 0.f : a.proj[tc];  // WO: read once the Wo rows are in
+  const float blk = a.blk[tc], upd = a.upd[tc], post_norm = a.post_norm[tc],
               pre_h = a.pre_h_norm[tc], d1 = a.d1[tc], d3 = a.d3[tc], d2 = a.d2[min(t, H - 1)],
               route = a.route[min(t, L * L + L - 1)];
   float xl[4];
@@ -754,6 +833,21 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     }
   }
 
+  if constexpr (WO) {
+    // Every operand above is in flight; wait for the Wo workgroups' count
+    // (read past the CU's L1 in the XCD's L2, where they add it), then read
+    // their rows the same way, and reset the count for the next launch.
+    if (t == 0) {
+      uint32_t it = 0;
+      while (__hip_atomic_load(a.wo_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+                 a.wo_groups &&
+             ++it < kWoSpin)
+        __builtin_amdgcn_s_sleep(2);
+    }
+    __syncthreads();
+    p = __hip_atomic_load(a.proj + tc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t == 0) __hip_atomic_store(a.wo_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
   // ---- post(l - 1)
   if (a.has_post) {
     const double sp = mix_sum(col ? (double)p * p : 0.0, red, phase);
@@ -810,7 +904,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
       }
     }
   }
-  if (a.has_final && blockIdx.x == a.final_row) {
+  if (a.has_final && (WO ? 0u : blockIdx.x) == a.final_row) {
     float m = 0.f;
     if (col) {
       double sum = 0.0;
@@ -1632,6 +1726,7 @@ struct nd_needle {
   size_t state_bytes = 0;  // leading part of the arena cleared by reset
   uint32_t *st = nullptr, *history = nullptr, *sel_id = nullptr, *allowed = nullptr,
            *counters = nullptr;
+  uint32_t* wo_count = nullptr;  // arrivals of the fused Wo launch (a line of its own)
   double *lp_history = nullptr, *sel_lp = nullptr;
   uint32_t* cq_lookup = nullptr;  // CQ model: a step's engram lookups and token
   float *ring = nullptr, *x = nullptr, *upd = nullptr, *blk = nullptr, *ain = nullptr,
@@ -1759,7 +1854,9 @@ enum MixPart : uint32_t { kMixPost = 1, kMixPre = 2, kMixFinal = 4, kMixCell = 8
 // lane mean plus final norm with kMixFinal (runtime.ts:570-576), and with
 // kMixCell (and kMixPost) the lane mean after post(l - 1) into confidence
 // cell l when the pool is on.
-hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s) {
+// wo: for an int8 model with the post half, layer l - 1's Wo runs in the
+// same launch (n2_mix_kernel<false, true>) instead of after its attention.
+hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, bool wo = false) {
   const bool has_post = parts & kMixPost;
   const nd_needle_desc& d = n->d;
   const uint32_t D = d.dim, ln = d.lanes;
@@ -1804,10 +1901,23 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s) 
   m.final_norm = n->params + n->o_final;
   m.fin = n->fin;
   m.cell = pool_on(n) && has_post && (parts & kMixCell) ? n->cells + (size_t)l * D : nullptr;
-  if (n->cq)
+  if (n->cq) {
     hipLaunchKernelGGL(n2_mix_kernel<true>, dim3(1), dim3(kMixWg), 0, s, m);
-  else
+  } else if (wo && has_post) {
+    const nd_mat* w = n->wo[pl];
+    m.wo_w = w->w;
+    m.wo_s = w->scales;
+    m.wo_x = n->att;
+    m.wo_n = w->n;
+    m.wo_k = w->k;
+    while ((1u << m.wo_tpr_log2) < w->k / 16) ++m.wo_tpr_log2;
+    m.wo_groups = (w->n + (kMixWg >> m.wo_tpr_log2) - 1) / (kMixWg >> m.wo_tpr_log2);
+    m.wo_count = n->wo_count;
+    hipLaunchKernelGGL((n2_mix_kernel<false, true>), dim3(8 * (m.wo_groups + 1)), dim3(kMixWg), 0,
+                       s, m);
+  } else {
     hipLaunchKernelGGL(n2_mix_kernel<false>, dim3(1), dim3(kMixWg), 0, s, m);
+  }
   return hipGetLastError();
 }
 
@@ -1825,7 +1935,8 @@ hipError_t mv_any(const nd_mat* m, const float* x, uint32_t row_start, uint32_t 
 // the q/k norms, RoPE and the KV append in its epilogue (plus the layer's
 // Sinkhorn routing from the mix's phi rows), gated attention, and Wo into
 // n->proj (runtime.ts:465-505).
-hipError_t enqueue_block(nd_needle* n, uint32_t l, hipStream_t s) {
+// with_wo false: Wo is left to the next mix launch (int8 decode steps).
+hipError_t enqueue_block(nd_needle* n, uint32_t l, hipStream_t s, bool with_wo = true) {
   const nd_needle_desc& d = n->d;
   const uint32_t D = d.dim, ln = d.lanes;
   const nd_mat& wm = n->wqkvg[l];
@@ -1861,7 +1972,7 @@ hipError_t enqueue_block(nd_needle* n, uint32_t l, hipStream_t s) {
   if (e != hipSuccess) return e;
   e = nd_launch_attention_gated(&n->kv, l, n->st + 1, n->max_length - 1, n->q, d.heads, n->qkvg,
                                 n->att, n->partials, n->counters, s);
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || !with_wo) return e;
   return mv_any(n->wo[l], n->att, 0, D, n->proj, s);
 }
 
@@ -2015,9 +2126,13 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
     const bool pre = l < d.layers;
     if (!pre && !tail && !pool_on(n)) break;
     const uint32_t parts = (l > 0 ? kMixPost | kMixCell : 0) | kMixPre | (!pre && tail ? kMixFinal : 0);
-    if ((e = enqueue_mix(n, l, parts, s)) != hipSuccess) return e;
+    // int8 models: layer l - 1's Wo runs inside mix launch l (one launch
+    // per layer fewer; when no last mix runs, the last Wo has no reader).
+    const uint32_t wo_tpr = n->d.heads * kHd / 16;  // Wo threads a row
+    const bool fuse = !n->cq && (wo_tpr & (wo_tpr - 1)) == 0 && wo_tpr <= (uint32_t)kMixWg;
+    if ((e = enqueue_mix(n, l, parts, s, fuse)) != hipSuccess) return e;
     if (!pre) break;
-    if ((e = enqueue_block(n, l, s)) != hipSuccess) return e;
+    if ((e = enqueue_block(n, l, s, !fuse)) != hipSuccess) return e;
   }
   return enqueue_final(n, tail, select, allowed, count, s);
 }
@@ -2598,7 +2713,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     const size_t P8 = kMaxProbes * 8, cb = n->conf ? 1 : 0;
     const size_t sizes[] = {al(64), al((size_t)cap * 4), al((size_t)cap * 8),
                             al((size_t)S * n->depth * D * 4),
-                            al((size_t)d.kv_heads * kAttnCounterStride * 4),
+                            al((size_t)d.kv_heads * kAttnCounterStride * 4), al(128),
                             cb * al(P8 * kMaxChunks), cb * al(P8 * kMaxChunks),
                             cb * al(P8 * D), al(64), al(64),
                             // K and V sized for float32 rows (kvCache "float32")
@@ -2628,6 +2743,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     take(&n->lp_history);
     take(&n->ring);
     take(&n->counters);
+    take(&n->wo_count);
     take(&n->pool.max);
     take(&n->pool.den);
     take(&n->pool.weighted);
