@@ -603,10 +603,12 @@ def bench_needle2(torch, hip, reps, check, cpu_seconds):
             "prefill_128_ms": prefill_ms, "prefill_tokens_per_s": 128 / wall1,
             "bytes_per_token": bytes_tok,
             "decode_GBps": bytes_tok / (decode_ms * 1e-3) / 1e9,
-            # begin, engram projections + convolution, per layer mix / QKV /
-            # attention / Wo, the final mix, lm head and selection, and the
-            # confidence pool (the head is on, as the reference's default)
-            "launches_per_token": 2 + len(g.sites) + 3 * g.layers + 3
+            # begin, engram projections + convolution, per layer the mix
+            # (with the previous layer's Wo and this layer's QKV) and the
+            # attention, the final mix (with the last Wo), lm head and
+            # selection, and the confidence pool (the head is on, as the
+            # reference's default)
+            "launches_per_token": 2 + len(g.sites) + 2 * g.layers + 3
                                   + int(model.resident.has_confidence),
             "confidence_pool": model.resident.has_confidence}
     part["decode_frac_hbm"] = part["decode_GBps"] / HBM_PEAK_GBS

@@ -405,6 +405,311 @@ __device__ void route_wave(const RouteArgs& r, uint32_t lane, float* lds) {
   if (lane < L) r.route[L * L + lane] = hp;
 }
 
+// One head of the projection epilogue, one wave, lane = dimension: role 0
+// (query) and 1 (key) take the per-head rmsNorm with their scale and the
+// half-split RoPE by (sin, cos) of the lane's angle (runtime.ts:471-500,
+// math.ts:94-115); role 0
+// writes q_dst, roles 1 and 2 (value) quantize into cache row
+// head_row + slot with #storeKV's arithmetic (runtime.ts:679-717).
+__device__ __forceinline__ void head_epilogue(float val, uint32_t lane, int role, double sn,
+                                              double cs, float nscale, float* q_dst,
+                                              void* Kc, void* Vc, float* Ks, float* Vs,
+                                              size_t head_row, uint32_t slot, uint32_t alloc,
+                                              uint32_t f32) {
+  float out = val;
+  if (role != 2) {
+    const double xd = val;
+    const double ss = nd::wave_sum(xd * xd);
+    const double inv = 1.0 / sqrt(ss / kHd + 1e-6);
+    const double normed = (float)((1.0 + (double)nscale) * xd * inv);
+    const double other = __shfl_xor(normed, 32, 64);
+    out = lane < 32 ? (float)(normed * cs - other * sn) : (float)(normed * cs + other * sn);
+    if (role == 0) {
+      q_dst[lane] = out;
+      return;
+    }
+  }
+  if (slot >= alloc) return;  // the host keeps positions below the runtime limit
+  const size_t crow = head_row + slot;
+  if (f32) {  // kvCache "float32": the value itself, scale 1 (runtime.ts:686-692)
+    reinterpret_cast<float*>(role == 2 ? Vc : Kc)[crow * kHd + lane] = out;
+    if (lane == 0) (role == 2 ? Vs : Ks)[crow] = 1.f;
+    return;
+  }
+  const float am = wave_absmax_js(out);
+  const double mx = (am != am) ? (double)am : fmax(1e-12, (double)am);
+  const double sc = mx / 127.0;
+  const double code = rint((double)out / sc);
+  reinterpret_cast<int8_t*>(role == 2 ? Vc : Kc)[crow * kHd + lane] =
+      code != code ? (int8_t)0 : (int8_t)(int)code;
+  if (lane == 0) (role == 2 ? Vs : Ks)[crow] = (float)sc;
+}
+
+// Projection rows of the Q/K/V/gate launch: 64 rows of d <= 512 int8
+// columns per workgroup, kQkvTpr threads a row; thread q of row r holds
+// bytes [16 kQkvTpr k + 16 q, +16) of the row (k < 32 / kQkvTpr; clamped in
+// the row, blocks past d add nothing), so a wave's load covers whole
+// 16 kQkvTpr-byte row pieces.  qkv_row_dot takes the fp32 fmas against x in
+// LDS in that order and sums the row's threads.
+constexpr uint32_t kQkvTpr = 8;
+constexpr uint32_t kQkvLoads = 32 / kQkvTpr;
+constexpr int kQkvWg = 64 * kQkvTpr;
+
+__device__ __forceinline__ void qkv_row_loads(const int8_t* W, size_t row, uint32_t q,
+                                              uint32_t d, i32x4 (&w)[kQkvLoads]) {
+  const int8_t* p = W + row * d;
+#pragma unroll
+  for (uint32_t k = 0; k < kQkvLoads; ++k)
+    w[k] = __builtin_nontemporal_load(
+        reinterpret_cast<const i32x4*>(p + min(16u * kQkvTpr * k + 16u * q, d - 16)));
+}
+
+__device__ __forceinline__ float qkv_row_dot(const i32x4 (&w)[kQkvLoads], const float* xs,
+                                             uint32_t q, uint32_t d) {
+  float acc = 0.f;
+#pragma unroll
+  for (uint32_t k = 0; k < kQkvLoads; ++k) {
+    const uint32_t off = 16u * kQkvTpr * k + 16u * q;
+    if (off < d) {
+      int8_t cb[16];
+      __builtin_memcpy(cb, &w[k], 16);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc = fmaf((float)cb[j], xs[off + j], acc);
+    }
+  }
+  acc = nd::quad_sum(acc);
+  if constexpr (kQkvTpr >= 8) acc += nd::lane_xor<4>(acc);
+  if constexpr (kQkvTpr >= 16) acc += nd::lane_xor<8>(acc);
+  return acc;
+}
+
+// A Cactus-Quant matrix's rows as the projection launch reads them (rows of
+// kpad codes, binary16 norms per group, the width's codebook by code).
+struct CqRows {
+  const uint8_t* packed;
+  const uint16_t* norms;
+  float cb[16];
+  uint32_t g, g_log2, row_bytes, groups;
+  float out_scale;  // 1 / sqrt(g)
+};
+
+// Rows r and r + 32 of the workgroup's 64 (r = t / 16) of a Cactus-Quant
+// product with d <= 512 inputs (cqMatvec, backends/cq.ts:106-231): thread t
+// takes 32-code unit u = t % 16 of both rows.  xs holds x with one pad float
+// after every 32 (element e at e + e / 32, zeros past d), so the 16 units'
+// reads fall in distinct banks.  The unit's inputs are rotated in registers
+// -- the butterflies of fastWalshHadamard with strides below min(g, 32), then
+// strides 32 .. g / 2 across the lanes holding the group's other units --
+// each result one fp32 add or subtract of the reference's two operands; the
+// codes index the codebook in LDS; fp32 dots per group times the group's
+// norm, summed over the row's 16 lanes, times 1/sqrt(g).  Returns the two
+// row values in every lane of the row.
+template <uint32_t BITS>
+__device__ __forceinline__ float2 cq_rows_pair(const CqRows& q, size_t row0, uint32_t units,
+                                               const float* xs, const float* cb, uint32_t t) {
+  constexpr uint32_t kWords = BITS;  // 32 codes of BITS bits
+  const uint32_t u = t & 15, r = t >> 4;
+  const bool active = u < units;
+  const uint32_t uc = active ? u : 0;
+  uint32_t w[2][kWords];
+  uint32_t nb[2][4];
+  const uint32_t ng = q.g < 32 ? 32u >> q.g_log2 : 1u;  // groups in a unit
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const size_t row = row0 + r + 32u * i;
+    const uint32_t* src =
+        reinterpret_cast<const uint32_t*>(q.packed + row * q.row_bytes) + uc * kWords;
+#pragma unroll
+    for (uint32_t k = 0; k < kWords; ++k) w[i][k] = src[k];
+    const uint16_t* nrow = q.norms + row * q.groups + ((uc * 32) >> q.g_log2);
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) nb[i][k] = nrow[k < ng ? k : 0];
+  }
+  float v[32];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) v[c] = xs[uc * 33 + c];
+  const uint32_t gs = q.g < 32 ? q.g : 32u;
+#pragma unroll
+  for (uint32_t st = 1; st < 32; st <<= 1) {
+    if (st < gs) {
+#pragma unroll
+      for (uint32_t c = 0; c < 32; ++c)
+        if (!(c & st)) {
+          const float a = v[c], b = v[c + st];
+          v[c] = a + b;
+          v[c + st] = a - b;
+        }
+    }
+  }
+  auto cross = [&](auto m) {
+    constexpr int M = decltype(m)::value;
+    const bool right = (t & M) != 0;
+#pragma unroll
+    for (int c = 0; c < 32; ++c) {
+      const float other = nd::lane_xor<M>(v[c]);
+      v[c] = right ? other - v[c] : v[c] + other;
+    }
+  };
+  const uint32_t lpg = q.g > 32 ? q.g >> 5 : 1u;  // lanes of a group
+  if (lpg > 1) cross(std::integral_constant<int, 1>{});
+  if (lpg > 2) cross(std::integral_constant<int, 2>{});
+  if (lpg > 4) cross(std::integral_constant<int, 4>{});
+  if (lpg > 8) cross(std::integral_constant<int, 8>{});
+  float out[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    float total = 0.f, dot = 0.f;
+#pragma unroll
+    for (uint32_t c = 0; c < 32; ++c) {
+      uint32_t code;
+      if constexpr (BITS == 4) {
+        code = (w[i][c >> 3] >> (4 * (c & 7))) & 15u;
+      } else if constexpr (BITS == 3) {
+        const uint32_t bit = 3 * c, k = bit >> 5, sh = bit & 31;
+        const uint32_t hi = sh > 29 ? w[i][k + 1 < kWords ? k + 1 : kWords - 1] << (32 - sh) : 0u;
+        code = ((w[i][k] >> sh) | hi) & 7u;
+      } else {
+        code = (w[i][c >> 4] >> (2 * (c & 15))) & 3u;
+      }
+      dot = fmaf(cb[code], v[c], dot);
+      if ((c & 7) == 7) {  // a group of 8, 16 or 32 and wider may end here: by selection
+        const bool ends = c == 31 || q.g == 8 || (q.g == 16 && (c & 15) == 15);
+        const uint32_t h = q.g == 8 ? nb[i][c >> 3] : (q.g == 16 ? nb[i][c >> 4] : nb[i][0]);
+        const float with = fmaf(nd::cq_half(h), dot, total);
+        total = ends ? with : total;
+        dot = ends ? 0.f : dot;
+      }
+    }
+    total = active ? total : 0.f;
+    total += nd::lane_xor<1>(total);
+    total += nd::lane_xor<2>(total);
+    total += nd::lane_xor<4>(total);
+    total += nd::lane_xor<8>(total);
+    out[i] = total * q.out_scale;
+  }
+  return float2{out[0], out[1]};
+}
+
+// The fused Q/K/V/gate projection of one layer (runtime.ts:465-470) with the
+// per-head norm + RoPE of q and k (runtime.ts:471-500) and #storeKV
+// (runtime.ts:679-717) in the epilogue.  Workgroup b computes rows [64 b,
+// 64 b + 64) of wqkvg = [q (H*64) | k (Hkv*64) | v (Hkv*64) | gate (H*64)]:
+// for int8 rows (BITS 0) eight threads per row (qkv_row_dot), fp32
+// accumulation of int8 x fp32 like the matvec, times the row scale; for
+// Cactus-Quant rows (BITS 2, 3, 4; ternary crumbs as 2) cq_rows_pair.  q
+// heads go to q_out, k and v heads are quantized into the cache at the ring
+// slot of the step's position, gate heads go to gate_out as raw projections.
+// One more workgroup computes the layer's routing (route_wave).
+// Bound on the waits of the fused mix launch (a safety net: a workgroup
+// waits only on workgroups dispatched before it, which wait on nothing
+// later).
+constexpr uint32_t kWoSpin = 1u << 16;
+
+// The projection launch's arguments.
+struct QkvParams {
+  const int8_t* W;
+  const float* S;
+  const float* x;
+  uint32_t d, heads, kv_heads;
+  const uint32_t* st;
+  const float* q_norm;
+  const float* k_norm;
+  const double* rope;
+  float* q_out;
+  float* gate_out;
+  void* Kc;
+  void* Vc;
+  float* Ks;
+  float* Vs;
+  uint32_t layer, alloc, sink, window, f32;
+  RouteArgs route;
+  CqRows cq;
+};
+
+// Workgroup b of the projection launch (b == 2 (heads + kv_heads): the
+// routing).  WAIT (inside the fused mix launch): issue the weight rows and
+// the epilogue operands, then wait until *flag != 0 -- the mix's signal
+// that x and the phi values are in the XCD's L2 -- before reading them (a
+// bounded spin).  Each of the `waiters` workgroups then counts itself on the
+// flag and the last one clears it, so every launch starts from zero.
+template <uint32_t BITS, bool WAIT>
+__device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_t* flag,
+                                         uint32_t waiters) {
+  __shared__ float xs[512 + 16];
+  __shared__ float rows[64];
+  __shared__ float s_cb[16];
+  const uint32_t t = threadIdx.x;
+  auto wait = [&]() {
+    if constexpr (WAIT) {
+      if (t == 0) {
+        uint32_t it = 0;
+        while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0 &&
+               ++it < kWoSpin)
+          __builtin_amdgcn_s_sleep(2);
+        if (__hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
+            waiters)
+          __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+      __syncthreads();
+    }
+  };
+  if (b == 2 * (p.heads + p.kv_heads)) {
+    wait();
+    route_wave(p.route, t, rows);
+    return;
+  }
+  const uint32_t lane = t & 63;
+  const uint32_t d = p.d;
+  if constexpr (BITS == 0) {
+    // Loads first: this thread's weight bytes (unconditional, clamped, so
+    // they issue back to back), the row scale, then x.
+    const size_t row = (size_t)b * kHd + t / kQkvTpr;
+    i32x4 wv[kQkvLoads];
+    qkv_row_loads(p.W, row, t % kQkvTpr, d, wv);
+    const float srow = p.S[row];
+    wait();
+    for (uint32_t i = t; i < d; i += kQkvWg) xs[i] = p.x[i];
+    __syncthreads();
+    const float acc = qkv_row_dot(wv, xs, t % kQkvTpr, d);
+    if (t % kQkvTpr == 0) rows[t / kQkvTpr] = acc * srow;
+  } else {
+    if (t == 0) {  // constant indices into the argument block
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s_cb[i] = p.cq.cb[i];
+    }
+    wait();
+    const uint32_t kpad = (d + 31) & ~31u;
+    for (uint32_t i = t; i < kpad; i += kQkvWg) xs[i + (i >> 5)] = i < d ? p.x[i] : 0.f;
+    __syncthreads();
+    const float2 v = cq_rows_pair<BITS>(p.cq, (size_t)b * kHd, kpad / 32, xs, s_cb, t);
+    if ((t & 15) == 0) {
+      rows[t >> 4] = v.x;
+      rows[(t >> 4) + 32] = v.y;
+    }
+  }
+  const uint32_t pos = p.st[1];
+  const float nscale = b < p.heads ? p.q_norm[lane] : p.k_norm[lane];
+  const double rs = p.rope[lane & 31], rc = p.rope[32 + (lane & 31)];
+  __syncthreads();
+  if (t >= 64) return;
+  const float val = rows[lane];
+  const uint32_t nq = p.heads, nk = p.kv_heads;
+  if (b >= nq + 2 * nk) {  // gate head
+    p.gate_out[(size_t)(b - nq - 2 * nk) * kHd + lane] = val;
+    return;
+  }
+  const int role = b < nq ? 0 : (b < nq + nk ? 1 : 2);
+  const uint32_t h = role == 0 ? b : (role == 1 ? b - nq : b - nq - nk);
+  head_epilogue(val, lane, role, rs, rc, nscale, p.q_out + (size_t)h * kHd, p.Kc, p.Vc, p.Ks, p.Vs,
+                ((size_t)p.layer * nk + h) * p.alloc, kv_slot(pos, p.sink, p.window), p.alloc,
+                p.f32);
+}
+
+template <uint32_t BITS>
+__global__ __launch_bounds__(kQkvWg) void n2_qkv_kernel(QkvParams p) {
+  qkv_body<BITS, false>(p, blockIdx.x, nullptr, 0);
+}
+
 struct MixArgs {
   float* x;  // [lanes][d]: read, and rewritten when has_post
   uint32_t d, hdim, lanes;
@@ -474,6 +779,13 @@ struct MixArgs {
   const float* wo_x;
   uint32_t wo_n, wo_k, wo_groups, wo_tpr_log2;
   uint32_t* wo_count;
+  // ... and layer l's projection: qkv_groups workgroups (qkv_body) after
+  // the mix, waiting on qkv_flag, which the mix sets to 1 once the
+  // attention input and the phi values are stored (cleared by the last
+  // of them).
+  QkvParams qkv;
+  uint32_t qkv_groups;
+  uint32_t* qkv_flag;
 };
 
 // Rows [rpw k, +rpw) of proj = Wo att in the fused Wo + mix launch, rpw =
@@ -532,9 +844,6 @@ __device__ __forceinline__ void wo_rows(const MixArgs& a, uint32_t k) {
   if (t == 0) __hip_atomic_fetch_add(a.wo_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Bound on the mix workgroup's wait for the Wo rows (a safety net: every Wo
-// workgroup is dispatched before it and none waits on anything).
-constexpr uint32_t kWoSpin = 1u << 16;
 
 // sigmoid in float64 as the kernels evaluate it (host side: the constants
 // a mix launch takes precomputed).
@@ -712,13 +1021,21 @@ constexpr int kPhiPairs = 8;
 template <bool CQ, bool WO = false>
 __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   static_assert(!(CQ && WO), "the fused Wo takes int8 rows");
+  static_assert(kQkvWg == kMixWg, "the fused projection runs on mix-sized workgroups");
   if constexpr (WO) {
     // Workgroups L % 8 == 0 only (one XCD): L / 8 < wo_groups computes Wo
-    // rows, L / 8 == wo_groups (dispatched after all of them) runs the mix.
+    // rows, L / 8 == wo_groups (dispatched after all of them) runs the mix,
+    // the qkv_groups after it the projection.  Each waits only on workgroups
+    // dispatched before it.
     if (blockIdx.x & 7) return;
     const uint32_t k = blockIdx.x >> 3;
     if (k < a.wo_groups) {
       wo_rows(a, k);
+      return;
+    }
+    if (k > a.wo_groups) {
+      const uint32_t qb = k - a.wo_groups - 1;
+      if (qb < a.qkv_groups) qkv_body<0, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups);
       return;
     }
   } else if (blockIdx.x) {
@@ -1080,6 +1397,14 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   const double sb = mix_sum(col ? (double)b * b : 0.0, red, phase);
   const double ib = 1.0 / sqrt(sb / D + 1e-6);
   if (col) a.ain[t] = (float)((1.0 + (double)norm_in) * (double)b * ib);
+  if constexpr (WO) {
+    if (a.qkv_groups) {  // the input and the phi values are in the L2: signal
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (t == 0)
+        __hip_atomic_store(a.qkv_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  }
   if (a.route_out) {
     RouteArgs r{};
     r.phi_post = phi + L;
@@ -1093,261 +1418,6 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     r.route = a.route_out;
     route_wave(r, t, rt);
   }
-}
-
-// One head of the projection epilogue, one wave, lane = dimension: role 0
-// (query) and 1 (key) take the per-head rmsNorm with their scale and the
-// half-split RoPE by (sin, cos) of the lane's angle (runtime.ts:471-500,
-// math.ts:94-115); role 0
-// writes q_dst, roles 1 and 2 (value) quantize into cache row
-// head_row + slot with #storeKV's arithmetic (runtime.ts:679-717).
-__device__ __forceinline__ void head_epilogue(float val, uint32_t lane, int role, double sn,
-                                              double cs, float nscale, float* q_dst,
-                                              void* Kc, void* Vc, float* Ks, float* Vs,
-                                              size_t head_row, uint32_t slot, uint32_t alloc,
-                                              uint32_t f32) {
-  float out = val;
-  if (role != 2) {
-    const double xd = val;
-    const double ss = nd::wave_sum(xd * xd);
-    const double inv = 1.0 / sqrt(ss / kHd + 1e-6);
-    const double normed = (float)((1.0 + (double)nscale) * xd * inv);
-    const double other = __shfl_xor(normed, 32, 64);
-    out = lane < 32 ? (float)(normed * cs - other * sn) : (float)(normed * cs + other * sn);
-    if (role == 0) {
-      q_dst[lane] = out;
-      return;
-    }
-  }
-  if (slot >= alloc) return;  // the host keeps positions below the runtime limit
-  const size_t crow = head_row + slot;
-  if (f32) {  // kvCache "float32": the value itself, scale 1 (runtime.ts:686-692)
-    reinterpret_cast<float*>(role == 2 ? Vc : Kc)[crow * kHd + lane] = out;
-    if (lane == 0) (role == 2 ? Vs : Ks)[crow] = 1.f;
-    return;
-  }
-  const float am = wave_absmax_js(out);
-  const double mx = (am != am) ? (double)am : fmax(1e-12, (double)am);
-  const double sc = mx / 127.0;
-  const double code = rint((double)out / sc);
-  reinterpret_cast<int8_t*>(role == 2 ? Vc : Kc)[crow * kHd + lane] =
-      code != code ? (int8_t)0 : (int8_t)(int)code;
-  if (lane == 0) (role == 2 ? Vs : Ks)[crow] = (float)sc;
-}
-
-// Projection rows of the Q/K/V/gate launch: 64 rows of d <= 512 int8
-// columns per workgroup, kQkvTpr threads a row; thread q of row r holds
-// bytes [16 kQkvTpr k + 16 q, +16) of the row (k < 32 / kQkvTpr; clamped in
-// the row, blocks past d add nothing), so a wave's load covers whole
-// 16 kQkvTpr-byte row pieces.  qkv_row_dot takes the fp32 fmas against x in
-// LDS in that order and sums the row's threads.
-constexpr uint32_t kQkvTpr = 8;
-constexpr uint32_t kQkvLoads = 32 / kQkvTpr;
-constexpr int kQkvWg = 64 * kQkvTpr;
-
-__device__ __forceinline__ void qkv_row_loads(const int8_t* W, size_t row, uint32_t q,
-                                              uint32_t d, i32x4 (&w)[kQkvLoads]) {
-  const int8_t* p = W + row * d;
-#pragma unroll
-  for (uint32_t k = 0; k < kQkvLoads; ++k)
-    w[k] = __builtin_nontemporal_load(
-        reinterpret_cast<const i32x4*>(p + min(16u * kQkvTpr * k + 16u * q, d - 16)));
-}
-
-__device__ __forceinline__ float qkv_row_dot(const i32x4 (&w)[kQkvLoads], const float* xs,
-                                             uint32_t q, uint32_t d) {
-  float acc = 0.f;
-#pragma unroll
-  for (uint32_t k = 0; k < kQkvLoads; ++k) {
-    const uint32_t off = 16u * kQkvTpr * k + 16u * q;
-    if (off < d) {
-      int8_t cb[16];
-      __builtin_memcpy(cb, &w[k], 16);
-#pragma unroll
-      for (int j = 0; j < 16; ++j) acc = fmaf((float)cb[j], xs[off + j], acc);
-    }
-  }
-  acc = nd::quad_sum(acc);
-  if constexpr (kQkvTpr >= 8) acc += nd::lane_xor<4>(acc);
-  if constexpr (kQkvTpr >= 16) acc += nd::lane_xor<8>(acc);
-  return acc;
-}
-
-// A Cactus-Quant matrix's rows as the projection launch reads them (rows of
-// kpad codes, binary16 norms per group, the width's codebook by code).
-struct CqRows {
-  const uint8_t* packed;
-  const uint16_t* norms;
-  float cb[16];
-  uint32_t g, g_log2, row_bytes, groups;
-  float out_scale;  // 1 / sqrt(g)
-};
-
-// Rows r and r + 32 of the workgroup's 64 (r = t / 16) of a Cactus-Quant
-// product with d <= 512 inputs (cqMatvec, backends/cq.ts:106-231): thread t
-// takes 32-code unit u = t % 16 of both rows.  xs holds x with one pad float
-// after every 32 (element e at e + e / 32, zeros past d), so the 16 units'
-// reads fall in distinct banks.  The unit's inputs are rotated in registers
-// -- the butterflies of fastWalshHadamard with strides below min(g, 32), then
-// strides 32 .. g / 2 across the lanes holding the group's other units --
-// each result one fp32 add or subtract of the reference's two operands; the
-// codes index the codebook in LDS; fp32 dots per group times the group's
-// norm, summed over the row's 16 lanes, times 1/sqrt(g).  Returns the two
-// row values in every lane of the row.
-template <uint32_t BITS>
-__device__ __forceinline__ float2 cq_rows_pair(const CqRows& q, size_t row0, uint32_t units,
-                                               const float* xs, const float* cb, uint32_t t) {
-  constexpr uint32_t kWords = BITS;  // 32 codes of BITS bits
-  const uint32_t u = t & 15, r = t >> 4;
-  const bool active = u < units;
-  const uint32_t uc = active ? u : 0;
-  uint32_t w[2][kWords];
-  uint32_t nb[2][4];
-  const uint32_t ng = q.g < 32 ? 32u >> q.g_log2 : 1u;  // groups in a unit
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const size_t row = row0 + r + 32u * i;
-    const uint32_t* src =
-        reinterpret_cast<const uint32_t*>(q.packed + row * q.row_bytes) + uc * kWords;
-#pragma unroll
-    for (uint32_t k = 0; k < kWords; ++k) w[i][k] = src[k];
-    const uint16_t* nrow = q.norms + row * q.groups + ((uc * 32) >> q.g_log2);
-#pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) nb[i][k] = nrow[k < ng ? k : 0];
-  }
-  float v[32];
-#pragma unroll
-  for (int c = 0; c < 32; ++c) v[c] = xs[uc * 33 + c];
-  const uint32_t gs = q.g < 32 ? q.g : 32u;
-#pragma unroll
-  for (uint32_t st = 1; st < 32; st <<= 1) {
-    if (st < gs) {
-#pragma unroll
-      for (uint32_t c = 0; c < 32; ++c)
-        if (!(c & st)) {
-          const float a = v[c], b = v[c + st];
-          v[c] = a + b;
-          v[c + st] = a - b;
-        }
-    }
-  }
-  auto cross = [&](auto m) {
-    constexpr int M = decltype(m)::value;
-    const bool right = (t & M) != 0;
-#pragma unroll
-    for (int c = 0; c < 32; ++c) {
-      const float other = nd::lane_xor<M>(v[c]);
-      v[c] = right ? other - v[c] : v[c] + other;
-    }
-  };
-  const uint32_t lpg = q.g > 32 ? q.g >> 5 : 1u;  // lanes of a group
-  if (lpg > 1) cross(std::integral_constant<int, 1>{});
-  if (lpg > 2) cross(std::integral_constant<int, 2>{});
-  if (lpg > 4) cross(std::integral_constant<int, 4>{});
-  if (lpg > 8) cross(std::integral_constant<int, 8>{});
-  float out[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    float total = 0.f, dot = 0.f;
-#pragma unroll
-    for (uint32_t c = 0; c < 32; ++c) {
-      uint32_t code;
-      if constexpr (BITS == 4) {
-        code = (w[i][c >> 3] >> (4 * (c & 7))) & 15u;
-      } else if constexpr (BITS == 3) {
-        const uint32_t bit = 3 * c, k = bit >> 5, sh = bit & 31;
-        const uint32_t hi = sh > 29 ? w[i][k + 1 < kWords ? k + 1 : kWords - 1] << (32 - sh) : 0u;
-        code = ((w[i][k] >> sh) | hi) & 7u;
-      } else {
-        code = (w[i][c >> 4] >> (2 * (c & 15))) & 3u;
-      }
-      dot = fmaf(cb[code], v[c], dot);
-      if ((c & 7) == 7) {  // a group of 8, 16 or 32 and wider may end here: by selection
-        const bool ends = c == 31 || q.g == 8 || (q.g == 16 && (c & 15) == 15);
-        const uint32_t h = q.g == 8 ? nb[i][c >> 3] : (q.g == 16 ? nb[i][c >> 4] : nb[i][0]);
-        const float with = fmaf(nd::cq_half(h), dot, total);
-        total = ends ? with : total;
-        dot = ends ? 0.f : dot;
-      }
-    }
-    total = active ? total : 0.f;
-    total += nd::lane_xor<1>(total);
-    total += nd::lane_xor<2>(total);
-    total += nd::lane_xor<4>(total);
-    total += nd::lane_xor<8>(total);
-    out[i] = total * q.out_scale;
-  }
-  return float2{out[0], out[1]};
-}
-
-// The fused Q/K/V/gate projection of one layer (runtime.ts:465-470) with the
-// per-head norm + RoPE of q and k (runtime.ts:471-500) and #storeKV
-// (runtime.ts:679-717) in the epilogue.  Workgroup b computes rows [64 b,
-// 64 b + 64) of wqkvg = [q (H*64) | k (Hkv*64) | v (Hkv*64) | gate (H*64)]:
-// for int8 rows (BITS 0) eight threads per row (qkv_row_dot), fp32
-// accumulation of int8 x fp32 like the matvec, times the row scale; for
-// Cactus-Quant rows (BITS 2, 3, 4; ternary crumbs as 2) cq_rows_pair.  q
-// heads go to q_out, k and v heads are quantized into the cache at the ring
-// slot of the step's position, gate heads go to gate_out as raw projections.
-// One more workgroup computes the layer's routing (route_wave).
-template <uint32_t BITS>
-__global__ __launch_bounds__(kQkvWg) void n2_qkv_kernel(
-    const int8_t* __restrict__ W, const float* __restrict__ S, const float* __restrict__ x,
-    uint32_t d, uint32_t heads, uint32_t kv_heads, const uint32_t* __restrict__ st,
-    const float* __restrict__ q_norm, const float* __restrict__ k_norm,
-    const double* __restrict__ rope, float* __restrict__ q_out, float* __restrict__ gate_out,
-    void* __restrict__ Kc, void* __restrict__ Vc, float* __restrict__ Ks,
-    float* __restrict__ Vs, uint32_t layer, uint32_t alloc, uint32_t sink, uint32_t window,
-    uint32_t f32, RouteArgs route, CqRows cq) {
-  __shared__ float xs[512 + 16];
-  __shared__ float rows[64];
-  __shared__ float s_cb[16];
-  const uint32_t b = blockIdx.x, t = threadIdx.x;
-  if (b == 2 * (heads + kv_heads)) {
-    route_wave(route, t, rows);
-    return;
-  }
-  const uint32_t lane = t & 63;
-  if constexpr (BITS == 0) {
-    // Loads first: this thread's weight bytes (unconditional, clamped, so
-    // they issue back to back), the row scale, then x.
-    const size_t row = (size_t)b * kHd + t / kQkvTpr;
-    i32x4 wv[kQkvLoads];
-    qkv_row_loads(W, row, t % kQkvTpr, d, wv);
-    const float srow = S[row];
-    for (uint32_t i = t; i < d; i += kQkvWg) xs[i] = x[i];
-    __syncthreads();
-    const float acc = qkv_row_dot(wv, xs, t % kQkvTpr, d);
-    if (t % kQkvTpr == 0) rows[t / kQkvTpr] = acc * srow;
-  } else {
-    if (t == 0) {  // constant indices into the argument block
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s_cb[i] = cq.cb[i];
-    }
-    const uint32_t kpad = (d + 31) & ~31u;
-    for (uint32_t i = t; i < kpad; i += kQkvWg) xs[i + (i >> 5)] = i < d ? x[i] : 0.f;
-    __syncthreads();
-    const float2 v = cq_rows_pair<BITS>(cq, (size_t)b * kHd, kpad / 32, xs, s_cb, t);
-    if ((t & 15) == 0) {
-      rows[t >> 4] = v.x;
-      rows[(t >> 4) + 32] = v.y;
-    }
-  }
-  const uint32_t pos = st[1];
-  const float nscale = b < heads ? q_norm[lane] : k_norm[lane];
-  const double rs = rope[lane & 31], rc = rope[32 + (lane & 31)];
-  __syncthreads();
-  if (t >= 64) return;
-  const float val = rows[lane];
-  const uint32_t nq = heads, nk = kv_heads;
-  if (b >= nq + 2 * nk) {  // gate head
-    gate_out[(size_t)(b - nq - 2 * nk) * kHd + lane] = val;
-    return;
-  }
-  const int role = b < nq ? 0 : (b < nq + nk ? 1 : 2);
-  const uint32_t h = role == 0 ? b : (role == 1 ? b - nq : b - nq - nk);
-  head_epilogue(val, lane, role, rs, rc, nscale, q_out + (size_t)h * kHd, Kc, Vc, Ks, Vs,
-                ((size_t)layer * kv_heads + h) * alloc, kv_slot(pos, sink, window), alloc, f32);
 }
 
 // ---------------------------------------------------------------- prefill
@@ -1727,6 +1797,7 @@ struct nd_needle {
   uint32_t *st = nullptr, *history = nullptr, *sel_id = nullptr, *allowed = nullptr,
            *counters = nullptr;
   uint32_t* wo_count = nullptr;  // arrivals of the fused Wo launch (a line of its own)
+  uint32_t* qkv_flags = nullptr;  // per layer: the fused launch's mix-done flag
   double *lp_history = nullptr, *sel_lp = nullptr;
   uint32_t* cq_lookup = nullptr;  // CQ model: a step's engram lookups and token
   float *ring = nullptr, *x = nullptr, *upd = nullptr, *blk = nullptr, *ain = nullptr,
@@ -1854,8 +1925,11 @@ enum MixPart : uint32_t { kMixPost = 1, kMixPre = 2, kMixFinal = 4, kMixCell = 8
 // lane mean plus final norm with kMixFinal (runtime.ts:570-576), and with
 // kMixCell (and kMixPost) the lane mean after post(l - 1) into confidence
 // cell l when the pool is on.
-// wo: for an int8 model with the post half, layer l - 1's Wo runs in the
-// same launch (n2_mix_kernel<false, true>) instead of after its attention.
+QkvParams qkv_params(const nd_needle* n, uint32_t l);
+
+// wo: for an int8 model, layer l - 1's Wo (with the post half) and layer
+// l's projection (with the pre half) run in the same launch
+// (n2_mix_kernel<false, true>) instead of beside the attention.
 hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, bool wo = false) {
   const bool has_post = parts & kMixPost;
   const nd_needle_desc& d = n->d;
@@ -1903,7 +1977,9 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, 
   m.cell = pool_on(n) && has_post && (parts & kMixCell) ? n->cells + (size_t)l * D : nullptr;
   if (n->cq) {
     hipLaunchKernelGGL(n2_mix_kernel<true>, dim3(1), dim3(kMixWg), 0, s, m);
-  } else if (wo && has_post) {
+  } else if (wo) {
+    // One launch on one XCD: layer l - 1's Wo (with the post half), the mix,
+    // layer l's projection (with the pre half).
     const nd_mat* w = n->wo[pl];
     m.wo_w = w->w;
     m.wo_s = w->scales;
@@ -1911,10 +1987,16 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, 
     m.wo_n = w->n;
     m.wo_k = w->k;
     while ((1u << m.wo_tpr_log2) < w->k / 16) ++m.wo_tpr_log2;
-    m.wo_groups = (w->n + (kMixWg >> m.wo_tpr_log2) - 1) / (kMixWg >> m.wo_tpr_log2);
+    m.wo_groups =
+        has_post ? (w->n + (kMixWg >> m.wo_tpr_log2) - 1) / (kMixWg >> m.wo_tpr_log2) : 0;
     m.wo_count = n->wo_count;
-    hipLaunchKernelGGL((n2_mix_kernel<false, true>), dim3(8 * (m.wo_groups + 1)), dim3(kMixWg), 0,
-                       s, m);
+    if (m.has_pre) {
+      m.qkv = qkv_params(n, l);
+      m.qkv_groups = n->wqkvg[l].n / kHd + 1;
+      m.qkv_flag = n->qkv_flags + 32 * (size_t)l;
+    }
+    hipLaunchKernelGGL((n2_mix_kernel<false, true>), dim3(8 * (m.wo_groups + 1 + m.qkv_groups)),
+                       dim3(kMixWg), 0, s, m);
   } else {
     hipLaunchKernelGGL(n2_mix_kernel<false>, dim3(1), dim3(kMixWg), 0, s, m);
   }
@@ -1935,12 +2017,35 @@ hipError_t mv_any(const nd_mat* m, const float* x, uint32_t row_start, uint32_t 
 // the q/k norms, RoPE and the KV append in its epilogue (plus the layer's
 // Sinkhorn routing from the mix's phi rows), gated attention, and Wo into
 // n->proj (runtime.ts:465-505).
-// with_wo false: Wo is left to the next mix launch (int8 decode steps).
-hipError_t enqueue_block(nd_needle* n, uint32_t l, hipStream_t s, bool with_wo = true) {
+// The projection launch of layer l: its arguments (input n->ain, the
+// routing from the phi values in n->phi_post_v / phi_res_v into n->route).
+QkvParams qkv_params(const nd_needle* n, uint32_t l) {
   const nd_needle_desc& d = n->d;
-  const uint32_t D = d.dim, ln = d.lanes;
+  const uint32_t ln = d.lanes;
   const nd_mat& wm = n->wqkvg[l];
-  RouteArgs ra{};
+  QkvParams p{};
+  p.W = wm.w;
+  p.S = wm.scales;
+  p.x = n->ain;
+  p.d = d.dim;
+  p.heads = d.heads;
+  p.kv_heads = d.kv_heads;
+  p.st = n->st;
+  p.q_norm = n->params + n->o_qn + (size_t)l * kHd;
+  p.k_norm = n->params + n->o_kn + (size_t)l * kHd;
+  p.rope = n->rope;
+  p.q_out = n->q;
+  p.gate_out = n->qkvg;
+  p.Kc = n->kv.k;
+  p.Vc = n->kv.v;
+  p.Ks = n->kv.ks;
+  p.Vs = n->kv.vs;
+  p.layer = l;
+  p.alloc = n->kv.alloc;
+  p.sink = n->kv.sink;
+  p.window = n->kv.window;
+  p.f32 = n->kv.mode == ND_KV_FLOAT32 ? 1u : 0u;
+  RouteArgs& ra = p.route;
   ra.phi_post = n->phi_post_v;
   ra.phi_res = n->phi_res_v;
   ra.a_post = n->a_post[l];
@@ -1950,9 +2055,8 @@ hipError_t enqueue_block(nd_needle* n, uint32_t l, hipStream_t s, bool with_wo =
   ra.lanes = ln;
   ra.own = l % ln;
   ra.route = n->route;
-  CqRows cq{};
-  auto kern = &n2_qkv_kernel<0>;
   if (n->cq) {
+    CqRows& cq = p.cq;
     cq.packed = wm.packed;
     cq.norms = wm.norms;
     for (int i = 0; i < 16; ++i) cq.cb[i] = wm.cb[i];
@@ -1961,19 +2065,30 @@ hipError_t enqueue_block(nd_needle* n, uint32_t l, hipStream_t s, bool with_wo =
     cq.row_bytes = wm.row_bytes;
     cq.groups = wm.kpad / wm.g;
     cq.out_scale = (float)(1.0 / std::sqrt((double)wm.g));
-    kern = wm.bits == 4 ? &n2_qkv_kernel<4> : (wm.bits == 3 ? &n2_qkv_kernel<3> : &n2_qkv_kernel<2>);
   }
-  hipLaunchKernelGGL(kern, dim3(wm.n / kHd + 1), dim3(kQkvWg), 0, s, wm.w, wm.scales, n->ain, D,
-                     d.heads, d.kv_heads, n->st, n->params + n->o_qn + (size_t)l * kHd,
-                     n->params + n->o_kn + (size_t)l * kHd, n->rope, n->q, n->qkvg, n->kv.k,
-                     n->kv.v, n->kv.ks, n->kv.vs, l, n->kv.alloc, n->kv.sink, n->kv.window,
-                     n->kv.mode == ND_KV_FLOAT32 ? 1u : 0u, ra, cq);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  e = nd_launch_attention_gated(&n->kv, l, n->st + 1, n->max_length - 1, n->q, d.heads, n->qkvg,
+  return p;
+}
+
+// with_wo false: Wo is left to the next mix launch (int8 decode steps);
+// with_qkv false: the projection runs inside the mix launch too.
+hipError_t enqueue_block(nd_needle* n, uint32_t l, hipStream_t s, bool with_wo = true,
+                         bool with_qkv = true) {
+  const nd_needle_desc& d = n->d;
+  const nd_mat& wm = n->wqkvg[l];
+  if (with_qkv) {
+    auto kern = &n2_qkv_kernel<0>;
+    if (n->cq)
+      kern = wm.bits == 4 ? &n2_qkv_kernel<4>
+                          : (wm.bits == 3 ? &n2_qkv_kernel<3> : &n2_qkv_kernel<2>);
+    hipLaunchKernelGGL(kern, dim3(wm.n / kHd + 1), dim3(kQkvWg), 0, s, qkv_params(n, l));
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  const hipError_t e =
+      nd_launch_attention_gated(&n->kv, l, n->st + 1, n->max_length - 1, n->q, d.heads, n->qkvg,
                                 n->att, n->partials, n->counters, s);
   if (e != hipSuccess || !with_wo) return e;
-  return mv_any(n->wo[l], n->att, 0, D, n->proj, s);
+  return mv_any(n->wo[l], n->att, 0, d.dim, n->proj, s);
 }
 
 // After the final mix: the confidence pool of the step's cells, the logits
@@ -2132,7 +2247,7 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
     const bool fuse = !n->cq && (wo_tpr & (wo_tpr - 1)) == 0 && wo_tpr <= (uint32_t)kMixWg;
     if ((e = enqueue_mix(n, l, parts, s, fuse)) != hipSuccess) return e;
     if (!pre) break;
-    if ((e = enqueue_block(n, l, s, !fuse)) != hipSuccess) return e;
+    if ((e = enqueue_block(n, l, s, !fuse, !fuse)) != hipSuccess) return e;
   }
   return enqueue_final(n, tail, select, allowed, count, s);
 }
@@ -2714,6 +2829,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     const size_t sizes[] = {al(64), al((size_t)cap * 4), al((size_t)cap * 8),
                             al((size_t)S * n->depth * D * 4),
                             al((size_t)d.kv_heads * kAttnCounterStride * 4), al(128),
+                            al((size_t)d.layers * 128),
                             cb * al(P8 * kMaxChunks), cb * al(P8 * kMaxChunks),
                             cb * al(P8 * D), al(64), al(64),
                             // K and V sized for float32 rows (kvCache "float32")
@@ -2744,6 +2860,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     take(&n->ring);
     take(&n->counters);
     take(&n->wo_count);
+    take(&n->qkv_flags);
     take(&n->pool.max);
     take(&n->pool.den);
     take(&n->pool.weighted);
