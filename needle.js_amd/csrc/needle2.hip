@@ -710,6 +710,49 @@ __global__ __launch_bounds__(kQkvWg) void n2_qkv_kernel(QkvParams p) {
   qkv_body<BITS, false>(p, blockIdx.x, nullptr, 0);
 }
 
+// A Cactus-Quant Wo (y = W x, x of k <= 512 values, n a multiple of 64
+// rows) by 64-row workgroups of cq_rows_pair: the standalone launch
+// (n2_wo_cq_kernel) and the fused mix launch run the same body, so both
+// give the same bits.
+struct WoCq {
+  const float* x;
+  float* y;
+  uint32_t n, k;
+  CqRows cq;
+};
+
+// Rows [64 k, +64) of w.  count (the fused launch): after the rows are in
+// the XCD's L2, add one to *count.
+template <uint32_t BITS>
+__device__ __forceinline__ void wo_cq_rows(const WoCq& w, uint32_t k, uint32_t* count) {
+  __shared__ float xs[512 + 16];
+  __shared__ float s_cb[16];
+  const uint32_t t = threadIdx.x;
+  if (t == 0) {  // constant indices into the argument block
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s_cb[i] = w.cq.cb[i];
+  }
+  const uint32_t kpad = (w.k + 31) & ~31u;
+  for (uint32_t i = t; i < kpad; i += kMixWg) xs[i + (i >> 5)] = i < w.k ? w.x[i] : 0.f;
+  __syncthreads();
+  const float2 v = cq_rows_pair<BITS>(w.cq, (size_t)k * 64, kpad / 32, xs, s_cb, t);
+  if ((t & 15) == 0) {
+    const uint32_t r = k * 64 + (t >> 4);
+    __hip_atomic_store(w.y + r, v.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_store(w.y + r + 32, v.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  if (count) {
+    __builtin_amdgcn_s_waitcnt(0);  // the rows are in the L2
+    __syncthreads();
+    if (t == 0) __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+}
+
+template <uint32_t BITS>
+__global__ __launch_bounds__(kMixWg) void n2_wo_cq_kernel(WoCq w) {
+  wo_cq_rows<BITS>(w, blockIdx.x, nullptr);
+}
+
 struct MixArgs {
   float* x;  // [lanes][d]: read, and rewritten when has_post
   uint32_t d, hdim, lanes;
@@ -786,6 +829,10 @@ struct MixArgs {
   QkvParams qkv;
   uint32_t qkv_groups;
   uint32_t* qkv_flag;
+  // A Cactus-Quant Wo in the same launch (n2_mix_kernel<true, true>):
+  // wo_groups workgroups of wo_cq_rows, codes of wo_bits bits.
+  WoCq wo_cq;
+  uint32_t wo_bits;
 };
 
 // Rows [rpw k, +rpw) of proj = Wo att in the fused Wo + mix launch, rpw =
@@ -1020,7 +1067,6 @@ constexpr int kPhiPairs = 8;
 // float64 times the row scale.
 template <bool CQ, bool WO = false>
 __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
-  static_assert(!(CQ && WO), "the fused Wo takes int8 rows");
   static_assert(kQkvWg == kMixWg, "the fused projection runs on mix-sized workgroups");
   if constexpr (WO) {
     // Workgroups L % 8 == 0 only (one XCD): L / 8 < wo_groups computes Wo
@@ -1030,12 +1076,23 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     if (blockIdx.x & 7) return;
     const uint32_t k = blockIdx.x >> 3;
     if (k < a.wo_groups) {
-      wo_rows(a, k);
+      if constexpr (CQ) {
+        if (a.wo_bits == 4)
+          wo_cq_rows<4>(a.wo_cq, k, a.wo_count);
+        else if (a.wo_bits == 3)
+          wo_cq_rows<3>(a.wo_cq, k, a.wo_count);
+        else
+          wo_cq_rows<2>(a.wo_cq, k, a.wo_count);
+      } else {
+        wo_rows(a, k);
+      }
       return;
     }
     if (k > a.wo_groups) {
-      const uint32_t qb = k - a.wo_groups - 1;
-      if (qb < a.qkv_groups) qkv_body<0, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups);
+      if constexpr (!CQ) {
+        const uint32_t qb = k - a.wo_groups - 1;
+        if (qb < a.qkv_groups) qkv_body<0, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups);
+      }
       return;
     }
   } else if (blockIdx.x) {
@@ -1926,11 +1983,14 @@ enum MixPart : uint32_t { kMixPost = 1, kMixPre = 2, kMixFinal = 4, kMixCell = 8
 // kMixCell (and kMixPost) the lane mean after post(l - 1) into confidence
 // cell l when the pool is on.
 QkvParams qkv_params(const nd_needle* n, uint32_t l);
+bool wo_cq_fits(const nd_mat& w);
+WoCq wo_cq_of(const nd_needle* n, const nd_mat& w);
 
 // wo: for an int8 model, layer l - 1's Wo (with the post half) and layer
 // l's projection (with the pre half) run in the same launch
 // (n2_mix_kernel<false, true>) instead of beside the attention.
-hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, bool wo = false) {
+hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, bool wo = false,
+                       bool qkv = false) {
   const bool has_post = parts & kMixPost;
   const nd_needle_desc& d = n->d;
   const uint32_t D = d.dim, ln = d.lanes;
@@ -1975,11 +2035,21 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, 
   m.final_norm = n->params + n->o_final;
   m.fin = n->fin;
   m.cell = pool_on(n) && has_post && (parts & kMixCell) ? n->cells + (size_t)l * D : nullptr;
-  if (n->cq) {
+  if (wo && n->cq) {
+    // One launch on one XCD: layer l - 1's Wo (with the post half), then
+    // the mix.
+    const nd_mat* w = n->wo[pl];
+    m.wo_cq = wo_cq_of(n, *w);
+    m.wo_bits = w->bits;
+    m.wo_groups = has_post ? w->n / 64 : 0;
+    m.wo_count = n->wo_count;
+    hipLaunchKernelGGL((n2_mix_kernel<true, true>), dim3(8 * (m.wo_groups + 1)), dim3(kMixWg), 0,
+                       s, m);
+  } else if (n->cq) {
     hipLaunchKernelGGL(n2_mix_kernel<true>, dim3(1), dim3(kMixWg), 0, s, m);
   } else if (wo) {
     // One launch on one XCD: layer l - 1's Wo (with the post half), the mix,
-    // layer l's projection (with the pre half).
+    // layer l's projection (with the pre half, when qkv).
     const nd_mat* w = n->wo[pl];
     m.wo_w = w->w;
     m.wo_s = w->scales;
@@ -1990,7 +2060,7 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, 
     m.wo_groups =
         has_post ? (w->n + (kMixWg >> m.wo_tpr_log2) - 1) / (kMixWg >> m.wo_tpr_log2) : 0;
     m.wo_count = n->wo_count;
-    if (m.has_pre) {
+    if (qkv && m.has_pre) {
       m.qkv = qkv_params(n, l);
       m.qkv_groups = n->wqkvg[l].n / kHd + 1;
       m.qkv_flag = n->qkv_flags + 32 * (size_t)l;
@@ -2019,6 +2089,32 @@ hipError_t mv_any(const nd_mat* m, const float* x, uint32_t row_start, uint32_t 
 // n->proj (runtime.ts:465-505).
 // The projection launch of layer l: its arguments (input n->ain, the
 // routing from the phi values in n->phi_post_v / phi_res_v into n->route).
+CqRows cq_rows_of(const nd_mat& wm) {
+  CqRows cq{};
+  cq.packed = wm.packed;
+  cq.norms = wm.norms;
+  for (int i = 0; i < 16; ++i) cq.cb[i] = wm.cb[i];
+  cq.g = wm.g;
+  while ((1u << cq.g_log2) < wm.g) ++cq.g_log2;
+  cq.row_bytes = wm.row_bytes;
+  cq.groups = wm.kpad / wm.g;
+  cq.out_scale = (float)(1.0 / std::sqrt((double)wm.g));
+  return cq;
+}
+
+// A Cactus-Quant Wo that wo_cq_rows takes (both launches of it use it).
+bool wo_cq_fits(const nd_mat& w) { return w.bits && w.k <= 512 && w.n % 64 == 0; }
+
+WoCq wo_cq_of(const nd_needle* n, const nd_mat& w) {
+  WoCq c{};
+  c.x = n->att;
+  c.y = n->proj;
+  c.n = w.n;
+  c.k = w.k;
+  c.cq = cq_rows_of(w);
+  return c;
+}
+
 QkvParams qkv_params(const nd_needle* n, uint32_t l) {
   const nd_needle_desc& d = n->d;
   const uint32_t ln = d.lanes;
@@ -2055,17 +2151,7 @@ QkvParams qkv_params(const nd_needle* n, uint32_t l) {
   ra.lanes = ln;
   ra.own = l % ln;
   ra.route = n->route;
-  if (n->cq) {
-    CqRows& cq = p.cq;
-    cq.packed = wm.packed;
-    cq.norms = wm.norms;
-    for (int i = 0; i < 16; ++i) cq.cb[i] = wm.cb[i];
-    cq.g = wm.g;
-    while ((1u << cq.g_log2) < wm.g) ++cq.g_log2;
-    cq.row_bytes = wm.row_bytes;
-    cq.groups = wm.kpad / wm.g;
-    cq.out_scale = (float)(1.0 / std::sqrt((double)wm.g));
-  }
+  if (n->cq) p.cq = cq_rows_of(wm);
   return p;
 }
 
@@ -2088,6 +2174,13 @@ hipError_t enqueue_block(nd_needle* n, uint32_t l, hipStream_t s, bool with_wo =
       nd_launch_attention_gated(&n->kv, l, n->st + 1, n->max_length - 1, n->q, d.heads, n->qkvg,
                                 n->att, n->partials, n->counters, s);
   if (e != hipSuccess || !with_wo) return e;
+  const nd_mat& w = *n->wo[l];
+  if (n->cq && wo_cq_fits(w)) {  // the fused launch's arithmetic
+    auto kern = w.bits == 4 ? &n2_wo_cq_kernel<4>
+                            : (w.bits == 3 ? &n2_wo_cq_kernel<3> : &n2_wo_cq_kernel<2>);
+    hipLaunchKernelGGL(kern, dim3(w.n / 64), dim3(kMixWg), 0, s, wo_cq_of(n, w));
+    return hipGetLastError();
+  }
   return mv_any(n->wo[l], n->att, 0, d.dim, n->proj, s);
 }
 
@@ -2241,13 +2334,16 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
     const bool pre = l < d.layers;
     if (!pre && !tail && !pool_on(n)) break;
     const uint32_t parts = (l > 0 ? kMixPost | kMixCell : 0) | kMixPre | (!pre && tail ? kMixFinal : 0);
-    // int8 models: layer l - 1's Wo runs inside mix launch l (one launch
-    // per layer fewer; when no last mix runs, the last Wo has no reader).
-    const uint32_t wo_tpr = n->d.heads * kHd / 16;  // Wo threads a row
-    const bool fuse = !n->cq && (wo_tpr & (wo_tpr - 1)) == 0 && wo_tpr <= (uint32_t)kMixWg;
-    if ((e = enqueue_mix(n, l, parts, s, fuse)) != hipSuccess) return e;
+    // Layer l - 1's Wo runs inside mix launch l, and for int8 models layer
+    // l's projection too (when no last mix runs, the last Wo has no
+    // reader).
+    const uint32_t wo_tpr = n->d.heads * kHd / 16;  // int8 Wo threads a row
+    const bool fuse = n->cq ? wo_cq_fits(*n->wo[0])
+                            : (wo_tpr & (wo_tpr - 1)) == 0 && wo_tpr <= (uint32_t)kMixWg;
+    const bool fuse_qkv = fuse && !n->cq;
+    if ((e = enqueue_mix(n, l, parts, s, fuse, fuse_qkv)) != hipSuccess) return e;
     if (!pre) break;
-    if ((e = enqueue_block(n, l, s, !fuse, !fuse)) != hipSuccess) return e;
+    if ((e = enqueue_block(n, l, s, !fuse, !fuse_qkv)) != hipSuccess) return e;
   }
   return enqueue_final(n, tail, select, allowed, count, s);
 }
