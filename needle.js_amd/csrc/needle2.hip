@@ -833,6 +833,7 @@ struct MixArgs {
   // wo_groups workgroups of wo_cq_rows, codes of wo_bits bits.
   WoCq wo_cq;
   uint32_t wo_bits;
+  uint32_t qkv_bits;  // the projection's code width (CQ launches)
 };
 
 // Rows [rpw k, +rpw) of proj = Wo att in the fused Wo + mix launch, rpw =
@@ -1089,9 +1090,18 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
       return;
     }
     if (k > a.wo_groups) {
-      if constexpr (!CQ) {
-        const uint32_t qb = k - a.wo_groups - 1;
-        if (qb < a.qkv_groups) qkv_body<0, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups);
+      const uint32_t qb = k - a.wo_groups - 1;
+      if (qb < a.qkv_groups) {
+        if constexpr (CQ) {
+          if (a.qkv_bits == 4)
+            qkv_body<4, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups);
+          else if (a.qkv_bits == 3)
+            qkv_body<3, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups);
+          else
+            qkv_body<2, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups);
+        } else {
+          qkv_body<0, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups);
+        }
       }
       return;
     }
@@ -2036,15 +2046,21 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, 
   m.fin = n->fin;
   m.cell = pool_on(n) && has_post && (parts & kMixCell) ? n->cells + (size_t)l * D : nullptr;
   if (wo && n->cq) {
-    // One launch on one XCD: layer l - 1's Wo (with the post half), then
-    // the mix.
+    // One launch on one XCD: layer l - 1's Wo (with the post half), the mix,
+    // layer l's projection (with the pre half, when qkv).
     const nd_mat* w = n->wo[pl];
     m.wo_cq = wo_cq_of(n, *w);
     m.wo_bits = w->bits;
     m.wo_groups = has_post ? w->n / 64 : 0;
     m.wo_count = n->wo_count;
-    hipLaunchKernelGGL((n2_mix_kernel<true, true>), dim3(8 * (m.wo_groups + 1)), dim3(kMixWg), 0,
-                       s, m);
+    if (qkv && m.has_pre) {
+      m.qkv = qkv_params(n, l);
+      m.qkv_groups = n->wqkvg[l].n / kHd + 1;
+      m.qkv_flag = n->qkv_flags + 32 * (size_t)l;
+      m.qkv_bits = n->wqkvg[l].bits;
+    }
+    hipLaunchKernelGGL((n2_mix_kernel<true, true>), dim3(8 * (m.wo_groups + 1 + m.qkv_groups)),
+                       dim3(kMixWg), 0, s, m);
   } else if (n->cq) {
     hipLaunchKernelGGL(n2_mix_kernel<true>, dim3(1), dim3(kMixWg), 0, s, m);
   } else if (wo) {
@@ -2334,16 +2350,14 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
     const bool pre = l < d.layers;
     if (!pre && !tail && !pool_on(n)) break;
     const uint32_t parts = (l > 0 ? kMixPost | kMixCell : 0) | kMixPre | (!pre && tail ? kMixFinal : 0);
-    // Layer l - 1's Wo runs inside mix launch l, and for int8 models layer
-    // l's projection too (when no last mix runs, the last Wo has no
-    // reader).
+    // Layer l - 1's Wo and layer l's projection run inside mix launch l
+    // (when no last mix runs, the last Wo has no reader).
     const uint32_t wo_tpr = n->d.heads * kHd / 16;  // int8 Wo threads a row
     const bool fuse = n->cq ? wo_cq_fits(*n->wo[0])
                             : (wo_tpr & (wo_tpr - 1)) == 0 && wo_tpr <= (uint32_t)kMixWg;
-    const bool fuse_qkv = fuse && !n->cq;
-    if ((e = enqueue_mix(n, l, parts, s, fuse, fuse_qkv)) != hipSuccess) return e;
+    if ((e = enqueue_mix(n, l, parts, s, fuse, fuse)) != hipSuccess) return e;
     if (!pre) break;
-    if ((e = enqueue_block(n, l, s, !fuse, !fuse_qkv)) != hipSuccess) return e;
+    if ((e = enqueue_block(n, l, s, !fuse, !fuse)) != hipSuccess) return e;
   }
   return enqueue_final(n, tail, select, allowed, count, s);
 }
