@@ -645,7 +645,7 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
         uint32_t it = 0;
         while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0 &&
                ++it < kWoSpin)
-          __builtin_amdgcn_s_sleep(2);
+          __builtin_amdgcn_s_sleep(1);
         if (__hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
             waiters)
           __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -1226,7 +1226,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
       while (__hip_atomic_load(a.wo_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
                  a.wo_groups &&
              ++it < kWoSpin)
-        __builtin_amdgcn_s_sleep(2);
+        __builtin_amdgcn_s_sleep(1);
     }
     __syncthreads();
     p = __hip_atomic_load(a.proj + tc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
