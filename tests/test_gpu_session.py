@@ -257,11 +257,14 @@ def test_generate_over_runtime(small):
     assert e.value.code == "GENERATION_ABORTED"
 
 
-def test_full_geometry_session_equals_whole_steps(hip):
-    """The shipped geometry (27 layers, engram sites 2 and 15, window 256):
-    twelve tokens through the session methods equal the whole steps."""
-    say("session full geometry")
-    w = Needle2Weights(Needle2Geometry(), 2026)
+@pytest.mark.parametrize("cq_bits", [0, 4])
+def test_full_geometry_session_equals_whole_steps(hip, cq_bits):
+    """The shipped geometry (27 layers, engram sites 2 and 15, window 256),
+    int8 and Cactus-Quant (CQ4) matrices: twelve tokens through the session
+    methods (one launch each for Wo, mix and projection) equal the whole
+    steps (Wo, mix and projection in one launch per layer)."""
+    say("session full geometry", cq_bits)
+    w = Needle2Weights(Needle2Geometry(), 2026, cq_bits=cq_bits)
     model = NeedleModel(hip, w)
     try:
         rt = model.create_runtime()
