@@ -133,6 +133,60 @@ def bench_matvec(torch, hip, n, k, g, batch, steps, warmup, rotate=True):
             "ms_per_launch": ms, "GBps": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
 
 
+def bench_matvec_span(torch, hip, n, k, g, steps, warmup):
+    """The batch-1 matvec workload of bench_matvec (same rotated replicas,
+    same graph timing) through nd_matvec_stamped_d: the same kernel body and
+    grid with every workgroup's entry and exit read from the GPU's 100 MHz
+    clock.  Per launch of the last replay: body span = latest exit - earliest
+    entry; interval = earliest entry of the next launch - earliest entry of
+    this one (the per-launch cadence the HIP events time).  Medians."""
+    import ctypes as C
+
+    import numpy as np
+
+    from needle_hip import lib as L
+    from needle_hip import synth
+
+    per = matvec_bytes(n, k, g, 1)
+    replicas = max(1, math.ceil(ROTATE_BYTES / per))
+    w, s = synth.int8_matrix(2026, f"bench-w{n}x{k}", n, k, g)
+    mats = []
+    for _ in range(replicas):
+        h = C.c_void_p()
+        hip._check(hip.lib.nd_mat_upload_i8(hip.ctx, L.ptr(w), L.ptr(s), n, k, g, C.byref(h)))
+        mats.append(h)
+    x = torch.from_numpy(synth.Stream(2026, "bench-x").normal((1, k))).cuda()
+    y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    launches = max(replicas, 32)
+    cap = 4096
+    stamps = torch.zeros((launches, cap, 2), dtype=torch.int64, device="cuda")
+    wgs = C.c_uint32(0)
+
+    def make(i):
+        h = mats[i % replicas]
+        return lambda stream: hip._check(hip.lib.nd_matvec_stamped_d(
+            hip.ctx, h, x.data_ptr(), 0, n, y.data_ptr(), stamps[i].data_ptr(), cap,
+            C.byref(wgs), C.c_void_p(stream)))
+
+    timer = GraphTimer(torch, [make(i) for i in range(launches)])
+    ms, timed = timer.time(math.ceil(steps / timer.n), warmup)
+    st = stamps[:, :wgs.value, :].cpu().numpy()
+    for h in mats:
+        hip.lib.nd_mat_free(hip.ctx, h)
+    first = st[:, :, 0].min(axis=1)
+    last_in = st[:, :, 0].max(axis=1)
+    last = st[:, :, 1].max(axis=1)
+    span_us = (last - first) * 0.01
+    entry_spread_us = (last_in - first) * 0.01
+    interval_us = np.diff(first) * 0.01
+    return {"workgroups": wgs.value, "launches": int(launches), "events_ms_per_launch": ms,
+            "body_span_us_median": float(np.median(span_us)),
+            "body_span_us_mean": float(np.mean(span_us)),
+            "entry_spread_us_median": float(np.median(entry_spread_us)),
+            "launch_interval_us_median": float(np.median(interval_us)),
+            "body_GBps": per / (float(np.median(span_us)) * 1e-6) / 1e9}
+
+
 def cq_matvec_bytes(n, k, g, bits, batch):
     """Algorithmic bytes of one Cactus-Quant matvec call: packed codes,
     binary16 norms, x and y (the rotated copy of x is the call's own
@@ -688,6 +742,45 @@ def traffic_workload(torch, hip, n, k, g, launches=64):
             "matvec_bytes_per_launch": per}
 
 
+def attention_traffic_workload(torch, hip, length=8192, heads=8, launches=64):
+    """The launches a pair of rocprofv3 --pmc passes measure for the
+    single-query attention: a 256 MiB device-to-device tensor copy (known
+    bytes, to scale the counters) and `launches` attention calls over rotated
+    HBM replicas of an 8-head cache of `length` positions."""
+    import ctypes as C
+
+    from needle_hip import HipKvCache, synth
+
+    src = torch.rand(64 << 20, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    per = attention_bytes(length, heads)
+    replicas = max(1, math.ceil(ROTATE_BYTES / per))
+    st = synth.Stream(7, f"bench-att{length}")
+    K, V = st.normal((length, heads, 64)), st.normal((length, heads, 64))
+    caches = []
+    for _ in range(replicas):
+        kv = HipKvCache(hip, 1, heads, max_length=length)
+        kv.store(0, 0, K, V)
+        caches.append(kv)
+    q = torch.from_numpy(st.normal((heads * 64,))).cuda()
+    out = torch.empty(heads * 64, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.Stream()  # not the default stream: its handle is null
+    torch.cuda.synchronize()
+    for i in range(launches):
+        hip._check(hip.lib.nd_attention_d(hip.ctx, caches[i % replicas].handle, 0, length - 1,
+                                          q.data_ptr(), heads, out.data_ptr(),
+                                          C.c_void_p(stream.cuda_stream)))
+    torch.cuda.synchronize()
+    for kv in caches:
+        kv.free()
+    return {"copy_bytes_each_way": 256 << 20, "copies": 4, "attention_launches": launches,
+            "attention_bytes_per_call": per}
+
+
 def measured_traffic():
     """HBM bytes per matvec launch from the committed rocprofv3 --pmc summary
     (profiles/matvec_i8_4096x4096_g32_b1_traffic.md, line 'traffic_bytes_per_launch: N'),
@@ -739,8 +832,8 @@ def main():
     ap.add_argument("--skip-needle2", action="store_true")
     ap.add_argument("--needle2-reps", type=int, default=5)
     ap.add_argument("--only", choices=["matvec", "matvec8", "attention", "decode", "prefill",
-                                       "needle2", "needle2cq", "traffic", "cq", "grammar",
-                                       "ceiling"],
+                                       "needle2", "needle2cq", "traffic", "attention_traffic", "cq",
+                                       "grammar", "ceiling", "matvec_span", "copy_matvec"],
                     help="run one part alone and print its JSON (for profiling)")
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--no-check", action="store_true",
@@ -776,6 +869,12 @@ def main():
             part = bench_read_ceiling(torch, hip)
         elif args.only == "traffic":
             part = traffic_workload(torch, hip, n, k, g)
+        elif args.only == "attention_traffic":
+            part = attention_traffic_workload(torch, hip)
+        elif args.only == "matvec_span":
+            part = bench_matvec_span(torch, hip, n, k, g, args.steps, args.warmup)
+        elif args.only == "copy_matvec":
+            part = bench_copy_ceiling(torch, matvec_bytes(n, k, g, 1), args.steps, args.warmup)
         elif args.only == "grammar":
             part, _ = bench_grammar_mask(torch, hip, 20, 0 if args.skip_cpu else args.cpu_seconds)
         elif args.only == "cq":

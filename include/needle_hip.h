@@ -161,6 +161,18 @@ nd_status nd_row_d(nd_ctx* ctx, const nd_mat* mat, uint32_t row, float* out_dev,
 nd_status nd_stream_read_d(nd_ctx* ctx, const void* src_dev, uint64_t bytes, uint32_t blocks,
                            uint32_t* out_dev, void* stream);
 
+/* Measurement, no counterpart in the reference: nd_matvec_d for batch 1 on
+ * an int8 matrix, the same kernel body and launch geometry, with each
+ * workgroup's entry time and the time its stores completed (the GPU's 100 MHz
+ * constant clock) written to stamps_dev[2 w], stamps_dev[2 w + 1].  The
+ * workgroup count goes to *workgroups; more than `capacity` workgroups is
+ * ND_ERR_INVALID with nothing launched.  The span from the earliest entry
+ * to the latest exit is the kernel's body time. */
+nd_status nd_matvec_stamped_d(nd_ctx* ctx, const nd_mat* mat, const float* x_dev,
+                              uint32_t row_start, uint32_t row_count, float* y_dev,
+                              uint64_t* stamps_dev, uint32_t capacity, uint32_t* workgroups,
+                              void* stream);
+
 /* --------------------------------------- a2/a3: int8 KV cache, attention */
 
 #define ND_KV_INT8 0

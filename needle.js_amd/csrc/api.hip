@@ -365,6 +365,26 @@ nd_status nd_matvec_d(nd_ctx* ctx, const nd_mat* m, const float* x, uint32_t bat
   return ND_OK;
 }
 
+nd_status nd_matvec_stamped_d(nd_ctx* ctx, const nd_mat* m, const float* x, uint32_t row_start,
+                              uint32_t row_count, float* y, uint64_t* stamps, uint32_t capacity,
+                              uint32_t* workgroups, void* stream) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_range(ctx, m, row_start, row_count);
+  if (st != ND_OK) return st;
+  if (m->bits || row_count == 0 || !x || !y || !stamps || !workgroups ||
+      (reinterpret_cast<uintptr_t>(x) & 15))
+    return nd_fail(ctx, ND_ERR_INVALID,
+                   "nd_matvec_stamped_d: an int8 matrix, rows, a 16-byte aligned x, y, stamps "
+                   "and workgroups");
+  const hipError_t e = nd_launch_matvec_stamped(m, x, row_start, row_count, y, stamps, capacity,
+                                                workgroups, nd_pick_stream(ctx, stream));
+  if (e == hipErrorInvalidValue)
+    return nd_fail(ctx, ND_ERR_INVALID, "nd_matvec_stamped_d: %u workgroups, room for %u stamps",
+                   *workgroups, capacity);
+  ND_HIP(ctx, e);
+  return ND_OK;
+}
+
 nd_status nd_stream_read_d(nd_ctx* ctx, const void* src, uint64_t bytes, uint32_t blocks,
                            uint32_t* out, void* stream) {
   if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");

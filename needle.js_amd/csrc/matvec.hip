@@ -21,7 +21,7 @@ constexpr int kThreads = 256;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <int B, int SPT, int RACC>
-__global__ __launch_bounds__(kThreads) void matvec_i8_kernel(
+__device__ __forceinline__ void matvec_i8_body(
     const int8_t* __restrict__ W, const float* __restrict__ S, const float* __restrict__ X,
     float* __restrict__ Y, uint32_t K, uint32_t groups, uint32_t g16, uint32_t row_start,
     uint32_t row_count, uint32_t tpr_log2, uint32_t x_stride, uint32_t y_stride) {
@@ -141,6 +141,39 @@ __global__ __launch_bounds__(kThreads) void matvec_i8_kernel(
     const uint32_t p = ov / B, b = ov % B;
     const uint32_t row = row0 + p * rpp + osub;
     if (row < row_count) Y[(size_t)b * y_stride + row] = sum;
+  }
+}
+
+template <int B, int SPT, int RACC>
+__global__ __launch_bounds__(kThreads) void matvec_i8_kernel(
+    const int8_t* __restrict__ W, const float* __restrict__ S, const float* __restrict__ X,
+    float* __restrict__ Y, uint32_t K, uint32_t groups, uint32_t g16, uint32_t row_start,
+    uint32_t row_count, uint32_t tpr_log2, uint32_t x_stride, uint32_t y_stride) {
+  matvec_i8_body<B, SPT, RACC>(W, S, X, Y, K, groups, g16, row_start, row_count, tpr_log2,
+                               x_stride, y_stride);
+}
+
+// The same body between two reads of the 100 MHz constant clock
+// (s_memrealtime): workgroup w writes its entry time and the time its
+// stores completed to stamps[2 w], stamps[2 w + 1].  Measurement only: the
+// span from the earliest entry to the latest exit is the kernel's body time,
+// which excludes the dispatch before its first workgroup and the end-of-
+// kernel processing after its last.
+template <int B, int SPT, int RACC>
+__global__ __launch_bounds__(kThreads) void matvec_i8_stamped_kernel(
+    const int8_t* __restrict__ W, const float* __restrict__ S, const float* __restrict__ X,
+    float* __restrict__ Y, uint32_t K, uint32_t groups, uint32_t g16, uint32_t row_start,
+    uint32_t row_count, uint32_t tpr_log2, uint32_t x_stride, uint32_t y_stride,
+    uint64_t* __restrict__ stamps) {
+  const uint64_t t0 = wall_clock64();
+  matvec_i8_body<B, SPT, RACC>(W, S, X, Y, K, groups, g16, row_start, row_count, tpr_log2,
+                               x_stride, y_stride);
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint64_t t1 = wall_clock64();
+    stamps[2 * blockIdx.x] = t0;
+    stamps[2 * blockIdx.x + 1] = t1;
   }
 }
 
@@ -601,6 +634,38 @@ MatvecFn pick_b(uint32_t b, uint32_t spt) {
   }
 }
 
+// The vector kernel's geometry for the next `left` batch rows of a launch
+// over row_count rows: bc batch rows (a power of two, at most 8 / spt),
+// spt 16-byte segments per thread, tpr = k / (16 spt) threads a row,
+// racc row passes and the workgroup count.
+struct VecPlan {
+  uint32_t bc, spt, tpr_log2, racc, blocks;
+};
+
+VecPlan plan_vector(const nd_mat* m, uint32_t left, uint32_t row_count) {
+  VecPlan p{};
+  const uint32_t segs = m->k / 16;
+  p.spt = segs > 256 ? segs / 256 : 1;
+  const uint32_t tpr = segs / p.spt;
+  while ((1u << p.tpr_log2) < tpr) ++p.tpr_log2;
+  const uint32_t rpp = kThreads / tpr;
+  const uint32_t bmax = 8 / p.spt;
+  p.bc = 1;
+  while (p.bc * 2 <= left && p.bc * 2 <= bmax) p.bc *= 2;
+  // Rows per pass x batch x passes must give 4..256 outputs per workgroup
+  // (the LDS reduction needs T = 256 / outputs <= 64).  8 passes amortize
+  // the per-workgroup x loads when there are enough rows.
+  p.racc = (p.bc <= 2 && row_count >= 8 * rpp * 256) ? 8 : 4;
+  while (p.racc > 1 && rpp * p.racc * p.bc > kThreads) p.racc >>= 1;
+  // Small matrices: fewer passes while that adds workgroups (up to 256),
+  // keeping at least 4 outputs per workgroup.
+  while (p.racc > 1 && rpp * (p.racc / 2) * p.bc >= 4 &&
+         (row_count + rpp * p.racc - 1) / (rpp * p.racc) < 256)
+    p.racc >>= 1;
+  p.blocks = (row_count + rpp * p.racc - 1) / (rpp * p.racc);
+  return p;
+}
+
 }  // namespace
 
 // Host-side checks that the kernel's geometry fits the matrix were done by
@@ -659,40 +724,43 @@ hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uin
     }
     return hipSuccess;
   }
-  const uint32_t segs = m->k / 16;
-  const uint32_t spt = segs > 256 ? segs / 256 : 1;
-  const uint32_t tpr = segs / spt;
-  uint32_t tpr_log2 = 0;
-  while ((1u << tpr_log2) < tpr) ++tpr_log2;
-  const uint32_t rpp = kThreads / tpr;
-  const uint32_t bmax = 8 / spt;
-  const uint32_t groups = m->k / m->g;
-  const uint32_t g16 = m->g / 16;
   uint32_t b0 = 0;
   while (b0 < batch) {
-    uint32_t left = batch - b0, bc = 1;
-    while (bc * 2 <= left && bc * 2 <= bmax) bc *= 2;
-    // Rows per pass x batch x passes must give 4..256 outputs per workgroup
-    // (the LDS reduction needs T = 256 / outputs <= 64).  8 passes amortize
-    // the per-workgroup x loads when there are enough rows.
-    uint32_t racc = (bc <= 2 && row_count >= 8 * rpp * 256) ? 8 : 4;
-    while (racc > 1 && rpp * racc * bc > kThreads) racc >>= 1;
-    // Small matrices: fewer passes while that adds workgroups (up to 256),
-    // keeping at least 4 outputs per workgroup.
-    while (racc > 1 && rpp * (racc / 2) * bc >= 4 &&
-           (row_count + rpp * racc - 1) / (rpp * racc) < 256)
-      racc >>= 1;
-    const uint32_t blocks = (row_count + rpp * racc - 1) / (rpp * racc);
-    MatvecFn f = racc == 8 ? pick_b<8>(bc, spt) : racc == 4 ? pick_b<4>(bc, spt)
-               : racc == 2 ? pick_b<2>(bc, spt) : pick_b<1>(bc, spt);
-    hipLaunchKernelGGL(f, dim3(blocks), dim3(kThreads), 0, s, m->w, m->scales,
-                       x + (size_t)b0 * x_stride, y + (size_t)b0 * y_stride, m->k, groups, g16,
-                       row_start, row_count, tpr_log2, x_stride, y_stride);
+    const VecPlan p = plan_vector(m, batch - b0, row_count);
+    MatvecFn f = p.racc == 8 ? pick_b<8>(p.bc, p.spt) : p.racc == 4 ? pick_b<4>(p.bc, p.spt)
+               : p.racc == 2 ? pick_b<2>(p.bc, p.spt) : pick_b<1>(p.bc, p.spt);
+    hipLaunchKernelGGL(f, dim3(p.blocks), dim3(kThreads), 0, s, m->w, m->scales,
+                       x + (size_t)b0 * x_stride, y + (size_t)b0 * y_stride, m->k, m->k / m->g,
+                       m->g / 16, row_start, row_count, p.tpr_log2, x_stride, y_stride);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    b0 += bc;
+    b0 += p.bc;
   }
   return hipSuccess;
+}
+
+hipError_t nd_launch_matvec_stamped(const nd_mat* m, const float* x, uint32_t row_start,
+                                    uint32_t row_count, float* y, uint64_t* stamps,
+                                    uint32_t capacity, uint32_t* workgroups, hipStream_t s) {
+  const VecPlan p = plan_vector(m, 1, row_count);
+  *workgroups = p.blocks;
+  if (p.blocks > capacity) return hipErrorInvalidValue;
+  decltype(&matvec_i8_stamped_kernel<1, 1, 1>) f;
+  const uint32_t key = p.racc * 4 + p.spt;
+  switch (key) {
+    case 8 * 4 + 2: f = &matvec_i8_stamped_kernel<1, 2, 8>; break;
+    case 4 * 4 + 2: f = &matvec_i8_stamped_kernel<1, 2, 4>; break;
+    case 2 * 4 + 2: f = &matvec_i8_stamped_kernel<1, 2, 2>; break;
+    case 1 * 4 + 2: f = &matvec_i8_stamped_kernel<1, 2, 1>; break;
+    case 8 * 4 + 1: f = &matvec_i8_stamped_kernel<1, 1, 8>; break;
+    case 4 * 4 + 1: f = &matvec_i8_stamped_kernel<1, 1, 4>; break;
+    case 2 * 4 + 1: f = &matvec_i8_stamped_kernel<1, 1, 2>; break;
+    default: f = &matvec_i8_stamped_kernel<1, 1, 1>; break;
+  }
+  hipLaunchKernelGGL(f, dim3(p.blocks), dim3(kThreads), 0, s, m->w, m->scales, x, y, m->k,
+                     m->k / m->g, m->g / 16, row_start, row_count, p.tpr_log2, m->k, row_count,
+                     stamps);
+  return hipGetLastError();
 }
 
 hipError_t nd_launch_stream_read(const void* src, uint64_t bytes, uint32_t blocks, uint32_t* out,

@@ -116,6 +116,13 @@ hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uin
                             uint32_t row_start, uint32_t row_count, float* y, uint32_t y_stride,
                             hipStream_t s, void* split = nullptr);
 hipError_t nd_launch_row(const nd_mat* m, uint32_t row, float* out, hipStream_t s);
+// Batch-1 vector matvec of an int8 matrix with the entry and exit time of
+// every workgroup (two uint64 per workgroup, 100 MHz clock) in stamps; the
+// workgroup count goes to *workgroups, and a launch needing more than
+// `capacity` workgroups is refused (hipErrorInvalidValue, nothing launched).
+hipError_t nd_launch_matvec_stamped(const nd_mat* m, const float* x, uint32_t row_start,
+                                    uint32_t row_count, float* y, uint64_t* stamps,
+                                    uint32_t capacity, uint32_t* workgroups, hipStream_t s);
 // Read-only stream of `bytes` (a multiple of 16) at 16-byte aligned `src`:
 // `blocks` workgroups of 256 threads, one folded word each into out[blocks].
 hipError_t nd_launch_stream_read(const void* src, uint64_t bytes, uint32_t blocks, uint32_t* out,

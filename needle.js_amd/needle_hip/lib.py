@@ -70,6 +70,7 @@ SIGNATURES = {
     "nd_row": (I32, [P, P, U32, P]),
     "nd_row_d": (I32, [P, P, U32, P, P]),
     "nd_stream_read_d": (I32, [P, P, C.c_uint64, U32, P, P]),
+    "nd_matvec_stamped_d": (I32, [P, P, P, U32, U32, P, P, U32, PU32, P]),
     "nd_kv_create": (I32, [P, U32, U32, U32, U32, U32, U32, U32, PP]),
     "nd_kv_free": (I32, [P, P]),
     "nd_kv_clear": (I32, [P, P]),
