@@ -536,6 +536,22 @@ nd_status nd_needle_generate(nd_ctx* ctx, nd_needle* model, const uint32_t* prom
                              uint32_t count, uint32_t max_new, uint32_t sink, uint32_t eos,
                              uint32_t* ids, double* log_probabilities, uint32_t* generated);
 
+/* The whole-step calls above run each layer's output projection, the layer
+ * mix and the next layer's projection in one launch whose workgroups hand
+ * over through bounded waits.  A wait that runs out sets a device status
+ * word and its workgroup stores nothing; the call then returns
+ * ND_ERR_BACKEND (BACKEND_UNAVAILABLE) with a message naming the wait, and
+ * every whole-step call fails the same way until nd_needle_reset clears the
+ * word with the launch's counters and flags.
+ *
+ * Test hook, no counterpart in the reference: makes the mix wait for
+ * `extra_arrivals` more output-projection workgroups than the launch has
+ * (so with extra_arrivals > 0 its wait runs out) and bounds every wait at
+ * `spin_rounds` sleep rounds (0 restores the default, 65536).  Takes effect
+ * from the next whole-step call; (0, 0) restores normal operation. */
+nd_status nd_needle_test_waits(nd_ctx* ctx, nd_needle* model, uint32_t extra_arrivals,
+                               uint32_t spin_rounds);
+
 /* ---------------- ResidentExecutionSession methods (backends/backend.ts:65-80)
  *
  * The session API an unchanged NeedleRuntime.step drives (model/runtime.ts:

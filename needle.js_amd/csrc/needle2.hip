@@ -602,8 +602,19 @@ __device__ __forceinline__ float2 cq_rows_pair(const CqRows& q, size_t row0, uin
 // One more workgroup computes the layer's routing (route_wave).
 // Bound on the waits of the fused mix launch (a safety net: a workgroup
 // waits only on workgroups dispatched before it, which wait on nothing
-// later).
+// later), in s_sleep(1) rounds.  A wait that runs out sets a bit of the
+// runtime's status word and skips every store that depends on it; the word
+// stays set until the next reset clears it with the counters and flags, and
+// the whole-step calls return an error while it is set (what later launches
+// compute from the skipped stores is never reported as a result).
 constexpr uint32_t kWoSpin = 1u << 16;
+constexpr uint32_t kStatusWoWait = 1u;   // the mix's wait for the Wo rows
+constexpr uint32_t kStatusQkvWait = 2u;  // a projection workgroup's wait for the mix
+// The mix's signal to the projection workgroups: 1 once its outputs are in
+// the L2, or kFlagAbort | 1 when it gave up (they then skip their stores).
+// The low 16 bits count the workgroups that have seen it.
+constexpr uint32_t kFlagAbort = 1u << 16;
+constexpr uint32_t kFlagCount = kFlagAbort - 1;
 
 // The projection launch's arguments.
 struct QkvParams {
@@ -629,32 +640,51 @@ struct QkvParams {
 // Workgroup b of the projection launch (b == 2 (heads + kv_heads): the
 // routing).  WAIT (inside the fused mix launch): issue the weight rows and
 // the epilogue operands, then wait until *flag != 0 -- the mix's signal
-// that x and the phi values are in the XCD's L2 -- before reading them (a
-// bounded spin).  Each of the `waiters` workgroups then counts itself on the
-// flag and the last one clears it, so every launch starts from zero.
+// that x and the phi values are in the XCD's L2 -- before reading them (at
+// most `spin` rounds).  Each of the `waiters` workgroups then counts itself
+// on the flag and the last one clears it, so every launch starts from zero.
+// A workgroup whose wait runs out sets kStatusQkvWait in *status; one that
+// finds kFlagAbort (the mix gave up) counts itself in; both return without
+// storing anything.
 template <uint32_t BITS, bool WAIT>
 __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_t* flag,
-                                         uint32_t waiters) {
+                                         uint32_t waiters, uint32_t* status = nullptr,
+                                         uint32_t spin = 0) {
   __shared__ float xs[512 + 16];
   __shared__ float rows[64];
   __shared__ float s_cb[16];
+  __shared__ uint32_t s_go;
   const uint32_t t = threadIdx.x;
-  auto wait = [&]() {
+  auto wait = [&]() -> bool {
     if constexpr (WAIT) {
       if (t == 0) {
-        uint32_t it = 0;
-        while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0 &&
-               ++it < kWoSpin)
+        uint32_t it = 0, f;
+        bool go = true;
+        while ((f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == 0) {
+          if (++it >= spin) {
+            go = false;
+            break;
+          }
           __builtin_amdgcn_s_sleep(1);
-        if (__hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
-            waiters)
-          __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        if (!go) {
+          __hip_atomic_fetch_or(status, kStatusQkvWait, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          if ((__hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) &
+               kFlagCount) == waiters)
+            __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          go = (f & kFlagAbort) == 0;
+        }
+        s_go = go;
       }
       __syncthreads();
+      return s_go != 0;
     }
+    return true;
   };
   if (b == 2 * (p.heads + p.kv_heads)) {
-    wait();
+    if (!wait()) return;
     route_wave(p.route, t, rows);
     return;
   }
@@ -667,7 +697,7 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
     i32x4 wv[kQkvLoads];
     qkv_row_loads(p.W, row, t % kQkvTpr, d, wv);
     const float srow = p.S[row];
-    wait();
+    if (!wait()) return;
     for (uint32_t i = t; i < d; i += kQkvWg) xs[i] = p.x[i];
     __syncthreads();
     const float acc = qkv_row_dot(wv, xs, t % kQkvTpr, d);
@@ -677,7 +707,7 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
 #pragma unroll
       for (int i = 0; i < 16; ++i) s_cb[i] = p.cq.cb[i];
     }
-    wait();
+    if (!wait()) return;
     const uint32_t kpad = (d + 31) & ~31u;
     for (uint32_t i = t; i < kpad; i += kQkvWg) xs[i + (i >> 5)] = i < d ? p.x[i] : 0.f;
     __syncthreads();
@@ -822,6 +852,11 @@ struct MixArgs {
   const float* wo_x;
   uint32_t wo_n, wo_k, wo_groups, wo_tpr_log2;
   uint32_t* wo_count;
+  // The mix waits for wo_target arrivals (wo_groups, or more when a test
+  // forces the wait to run out), each wait for at most spin rounds; a wait
+  // that runs out sets a bit of *status.
+  uint32_t wo_target, spin;
+  uint32_t* status;
   // ... and layer l's projection: qkv_groups workgroups (qkv_body) after
   // the mix, waiting on qkv_flag, which the mix sets to 1 once the
   // attention input and the phi values are stored (cleared by the last
@@ -1094,13 +1129,13 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
       if (qb < a.qkv_groups) {
         if constexpr (CQ) {
           if (a.qkv_bits == 4)
-            qkv_body<4, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups);
+            qkv_body<4, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups, a.status, a.spin);
           else if (a.qkv_bits == 3)
-            qkv_body<3, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups);
+            qkv_body<3, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups, a.status, a.spin);
           else
-            qkv_body<2, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups);
+            qkv_body<2, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups, a.status, a.spin);
         } else {
-          qkv_body<0, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups);
+          qkv_body<0, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups, a.status, a.spin);
         }
       }
       return;
@@ -1221,14 +1256,29 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     // Every operand above is in flight; wait for the Wo workgroups' count
     // (read past the CU's L1 in the XCD's L2, where they add it), then read
     // their rows the same way, and reset the count for the next launch.
+    // When the wait runs out: set the status bit, release the projection
+    // workgroups with the abort bit and store nothing.
+    __shared__ uint32_t s_go;
     if (t == 0) {
+      bool go = true;
       uint32_t it = 0;
       while (__hip_atomic_load(a.wo_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-                 a.wo_groups &&
-             ++it < kWoSpin)
+             a.wo_target) {
+        if (++it >= a.spin) {
+          __hip_atomic_fetch_or(a.status, kStatusWoWait, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+          go = false;
+          break;
+        }
         __builtin_amdgcn_s_sleep(1);
+      }
+      if (!go && a.qkv_groups)
+        __hip_atomic_store(a.qkv_flag, kFlagAbort | 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+      s_go = go;
     }
     __syncthreads();
+    if (!s_go) return;
     p = __hip_atomic_load(a.proj + tc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (t == 0) __hip_atomic_store(a.wo_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
@@ -1865,6 +1915,12 @@ struct nd_needle {
            *counters = nullptr;
   uint32_t* wo_count = nullptr;  // arrivals of the fused Wo launch (a line of its own)
   uint32_t* qkv_flags = nullptr;  // per layer: the fused launch's mix-done flag
+  // Give-ups of the fused launch's bounded waits (kStatus* bits; a line of
+  // its own, cleared by reset), its pinned host copy, and the test hook's
+  // extra Wo arrivals and spin bound (0: kWoSpin).
+  uint32_t* status = nullptr;
+  uint32_t* status_host = nullptr;
+  uint32_t dbg_extra = 0, dbg_spin = 0;
   double *lp_history = nullptr, *sel_lp = nullptr;
   uint32_t* cq_lookup = nullptr;  // CQ model: a step's engram lookups and token
   float *ring = nullptr, *x = nullptr, *upd = nullptr, *blk = nullptr, *ain = nullptr,
@@ -1983,6 +2039,14 @@ void set_phi(const nd_needle* n, uint32_t ql, MixArgs& m) {
   }
 }
 
+// The fused launch's waits: the arrivals the mix waits for, the spin bound
+// and the status word.
+void set_waits(const nd_needle* n, MixArgs& m) {
+  m.wo_target = m.wo_groups + n->dbg_extra;
+  m.spin = n->dbg_spin ? n->dbg_spin : kWoSpin;
+  m.status = n->status;
+}
+
 // Halves of a mix launch (enqueue_mix `parts`).
 enum MixPart : uint32_t { kMixPost = 1, kMixPre = 2, kMixFinal = 4, kMixCell = 8 };
 
@@ -2053,6 +2117,7 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, 
     m.wo_bits = w->bits;
     m.wo_groups = has_post ? w->n / 64 : 0;
     m.wo_count = n->wo_count;
+    set_waits(n, m);
     if (qkv && m.has_pre) {
       m.qkv = qkv_params(n, l);
       m.qkv_groups = n->wqkvg[l].n / kHd + 1;
@@ -2076,6 +2141,7 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, 
     m.wo_groups =
         has_post ? (w->n + (kMixWg >> m.wo_tpr_log2) - 1) / (kMixWg >> m.wo_tpr_log2) : 0;
     m.wo_count = n->wo_count;
+    set_waits(n, m);
     if (qkv && m.has_pre) {
       m.qkv = qkv_params(n, l);
       m.qkv_groups = n->wqkvg[l].n / kHd + 1;
@@ -2649,6 +2715,23 @@ nd_status run_prompt(nd_ctx* ctx, nd_needle* n, uint32_t count, bool want_logits
   return ND_OK;
 }
 
+// The fused launches' status word: its copy to the pinned host word is
+// enqueued before a whole-step call synchronizes, and read after.
+hipError_t enqueue_status(nd_needle* n, hipStream_t s) {
+  return hipMemcpyAsync(n->status_host, n->status, 4, hipMemcpyDeviceToHost, s);
+}
+
+nd_status check_waits(nd_ctx* ctx, const nd_needle* n) {
+  const uint32_t v = *n->status_host;
+  if (!v) return ND_OK;
+  return nd_fail(ctx, ND_ERR_BACKEND,
+                 "a bounded wait inside a fused layer launch ran out (%s%s%s): the results of "
+                 "this call are not valid, and every whole-step call fails until reset()",
+                 v & kStatusWoWait ? "the layer mix waiting for the output projection rows" : "",
+                 (v & kStatusWoWait) && (v & kStatusQkvWait) ? "; " : "",
+                 v & kStatusQkvWait ? "the projection waiting for the layer mix" : "");
+}
+
 // One reset is driven either by whole-step calls or by the session methods:
 // they keep different parts of the runtime state on the device (the token
 // history for the engram hashes, or the host's lookups), so mixing them
@@ -2910,6 +2993,7 @@ nd_status nd_needle_free(nd_ctx* ctx, nd_needle* n) {
   if (n->params) hipFree(n->params);
   if (n->inv_freq) hipFree(n->inv_freq);
   if (n->pinned) hipHostFree(n->pinned);
+  if (n->status_host) hipHostFree(n->status_host);
   for (auto& ev : n->stage_done)
     if (ev) hipEventDestroy(ev);
   delete n;
@@ -2939,7 +3023,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     const size_t sizes[] = {al(64), al((size_t)cap * 4), al((size_t)cap * 8),
                             al((size_t)S * n->depth * D * 4),
                             al((size_t)d.kv_heads * kAttnCounterStride * 4), al(128),
-                            al((size_t)d.layers * 128),
+                            al((size_t)d.layers * 128), al(128),
                             cb * al(P8 * kMaxChunks), cb * al(P8 * kMaxChunks),
                             cb * al(P8 * D), al(64), al(64),
                             // K and V sized for float32 rows (kvCache "float32")
@@ -2971,6 +3055,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     take(&n->counters);
     take(&n->wo_count);
     take(&n->qkv_flags);
+    take(&n->status);
     take(&n->pool.max);
     take(&n->pool.den);
     take(&n->pool.weighted);
@@ -3029,6 +3114,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
       if (!ev) ND_HIP(ctx, hipEventCreateWithFlags(&ev, hipEventDisableTiming));
     ND_HIP(ctx, hipHostMalloc(reinterpret_cast<void**>(&n->pinned), pinned));
   }
+  if (!n->status_host) ND_HIP(ctx, hipHostMalloc(reinterpret_cast<void**>(&n->status_host), 64));
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
   ND_HIP(ctx, hipMemsetAsync(n->arena, 0, n->state_bytes, ctx->stream));
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -3081,8 +3167,9 @@ nd_status nd_needle_step(nd_ctx* ctx, nd_needle* n, uint32_t token, float* logit
   if (logits)
     ND_HIP(ctx, hipMemcpyAsync(logits, n->logits, (size_t)n->d.vocab * 4, hipMemcpyDeviceToHost,
                                ctx->stream));
+  ND_HIP(ctx, enqueue_status(n, ctx->stream));
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
-  return ND_OK;
+  return check_waits(ctx, n);
 }
 
 nd_status nd_needle_prefill(nd_ctx* ctx, nd_needle* n, const uint32_t* tokens, uint32_t count,
@@ -3107,8 +3194,9 @@ nd_status nd_needle_prefill(nd_ctx* ctx, nd_needle* n, const uint32_t* tokens, u
   if (logits)
     ND_HIP(ctx, hipMemcpyAsync(logits, n->logits, (size_t)n->d.vocab * 4, hipMemcpyDeviceToHost,
                                ctx->stream));
+  ND_HIP(ctx, enqueue_status(n, ctx->stream));
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
-  return ND_OK;
+  return check_waits(ctx, n);
 }
 
 nd_status nd_needle_step_select(nd_ctx* ctx, nd_needle* n, uint32_t token, const uint32_t* allowed,
@@ -3133,8 +3221,9 @@ nd_status nd_needle_step_select(nd_ctx* ctx, nd_needle* n, uint32_t token, const
   ++n->position;
   ND_HIP(ctx, hipMemcpyAsync(id, n->sel_id, 4, hipMemcpyDeviceToHost, ctx->stream));
   ND_HIP(ctx, hipMemcpyAsync(logprob, n->sel_lp, 8, hipMemcpyDeviceToHost, ctx->stream));
+  ND_HIP(ctx, enqueue_status(n, ctx->stream));
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
-  return ND_OK;
+  return check_waits(ctx, n);
 }
 
 nd_status nd_needle_generate(nd_ctx* ctx, nd_needle* n, const uint32_t* prompt, uint32_t count,
@@ -3167,9 +3256,10 @@ nd_status nd_needle_generate(nd_ctx* ctx, nd_needle* n, const uint32_t* prompt, 
     if ((st = launch_graph(ctx, n, kGraphDecodeSelect)) != ND_OK) return st;
     ++n->position;
   }
+  ND_HIP(ctx, enqueue_status(n, ctx->stream));
   if (n_gen == 0) {
     ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    return ND_OK;
+    return check_waits(ctx, n);
   }
   std::vector<uint32_t> tok(n_gen);
   std::vector<double> lp(n_gen);
@@ -3182,12 +3272,25 @@ nd_status nd_needle_generate(nd_ctx* ctx, nd_needle* n, const uint32_t* prompt, 
   ND_HIP(ctx, hipMemcpyAsync(&tok[n_gen - 1], n->sel_id, 4, hipMemcpyDeviceToHost, ctx->stream));
   ND_HIP(ctx, hipMemcpyAsync(&lp[n_gen - 1], n->sel_lp, 8, hipMemcpyDeviceToHost, ctx->stream));
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  if ((st = check_waits(ctx, n)) != ND_OK) return st;
   uint32_t out = 0;
   for (; out < n_gen && tok[out] != eos; ++out) {
     ids[out] = tok[out];
     logprobs[out] = lp[out];
   }
   *generated = out;
+  return ND_OK;
+}
+
+nd_status nd_needle_test_waits(nd_ctx* ctx, nd_needle* n, uint32_t extra_arrivals,
+                               uint32_t spin_rounds) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!n) return nd_fail(ctx, ND_ERR_INVALID, "model is NULL");
+  if (extra_arrivals > 1024) return nd_fail(ctx, ND_ERR_INVALID, "at most 1024 extra arrivals");
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  drop_graphs(n);  // the launches' arguments change
+  n->dbg_extra = extra_arrivals;
+  n->dbg_spin = spin_rounds;
   return ND_OK;
 }
 

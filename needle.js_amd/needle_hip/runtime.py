@@ -199,6 +199,14 @@ class Needle2Resident:
         k = int(count.value)
         return out_ids[:k].copy(), out_lp[:k].copy()
 
+    def test_waits(self, extra_arrivals: int, spin_rounds: int) -> None:
+        """Test hook (nd_needle_test_waits): the fused layer launch's mix
+        waits for `extra_arrivals` more output-projection workgroups than it
+        has, every wait bounded at `spin_rounds` rounds (0: the default), so
+        that a whole-step call sees a wait run out; (0, 0) restores."""
+        self._check(self.lib.nd_needle_test_waits(self.ctx, self.handle, int(extra_arrivals),
+                                                  int(spin_rounds)), "nd_needle_test_waits")
+
     # -- session calls ---------------------------------------------------
     def begin_token(self, lanes: np.ndarray) -> None:
         x = _f32(lanes, self.geometry.lanes * self.geometry.dim, "Resident lane input")

@@ -262,6 +262,53 @@ def test_runtime_errors(small):
     assert e.value.code == "INVALID_CACT"
 
 
+def test_fused_wait_that_runs_out_is_reported_until_reset(small):
+    """The fused layer launch's bounded waits, made to run out from the host
+    (the test hook has the mix wait for one more output-projection workgroup
+    than the launch has, every wait bounded at 64 sleep rounds): step,
+    step_selected, a prefill whose slots wrap (stepped positions) and
+    generate each return BACKEND_UNAVAILABLE naming the wait, and every
+    kernel exits (the calls return).  The status stays set after the hook is
+    cleared until reset() clears it; then steps agree with the oracle."""
+    w, model = small
+    res = model.resident
+    rt = model.create_resident_runtime()
+    tokens = synth.Stream(8, "n2waits").integers(14, 0, SMALL.vocab - 1)
+    say("needle2 fused wait runs out")
+    try:
+        res.test_waits(1, 64)
+        calls = (("step", lambda: rt.step(int(tokens[0]))),
+                 ("step_selected", lambda: rt.step_selected(int(tokens[0]))),
+                 ("prefill", lambda: rt.prefill([int(t) for t in tokens[:12]])),
+                 ("generate", lambda: res.generate([int(t) for t in tokens[:4]], 3)))
+        for name, call in calls:
+            rt.reset(SMALL.max_length, 0)
+            with pytest.raises(NeedleError) as e:
+                call()
+            assert e.value.code == "BACKEND_UNAVAILABLE", name
+            assert "output projection rows" in str(e.value), (name, str(e.value))
+        res.test_waits(0, 0)
+        with pytest.raises(NeedleError) as e:  # still set: no reset since
+            rt.step(int(tokens[1]))
+        assert e.value.code == "BACKEND_UNAVAILABLE"
+    finally:
+        res.test_waits(0, 0)
+    rt.reset(SMALL.max_length, 0)
+    ref = oracle.Needle2(w).runtime(SMALL.max_length, 0)
+    for i, t in enumerate(tokens):
+        close(rt.step(int(t)), ref.step(int(t)), ("after reset", i))
+    ids, _ = res.generate([int(t) for t in tokens[:4]], 3, eos=None)
+    ref = oracle.Needle2(w).runtime(7, 0)
+    for t in tokens[:4]:
+        logits = ref.step(int(t))
+    want = []
+    for k in range(3):
+        want.append(oracle.argmax(logits))
+        if k < 2:
+            logits = ref.step(want[-1])
+    assert list(ids) == want
+
+
 def test_generate_full_geometry_greedy_identical(hip):
     """The shipped geometry (27 layers, vocab 8192, window 256): 128 prompt
     tokens, 64 greedy tokens, identical to the oracle's greedy sequence."""
