@@ -63,6 +63,20 @@ nd_status nd_sync(nd_ctx* ctx);
  * calls and time them with events. */
 void* nd_stream(nd_ctx* ctx);
 
+/* Workgroup placement, no counterpart in the reference.  Several kernels
+ * hand partial results between the workgroups of one launch through one
+ * XCD's L2 (the attention chunk merge, the k-slice matvec sum, the split-k
+ * GEMM sum, the Needle 2 fused layer launch); that needs the dispatcher to
+ * place workgroup L of a launch on the XCD of workgroup L % 8.  nd_create
+ * checks this on its device (every workgroup of three probe launches reads
+ * its XCC id); when it does not hold, those kernels run their agent-scope
+ * forms (and Needle 2 its separate layer launches) instead.  *probed
+ * (when not NULL) receives 1 when every device probed so far passed.
+ * Test hook: enable == 0 selects the agent-scope forms although the probe
+ * passed, enable == 1 restores the probe's choice; it applies to launches
+ * enqueued (and Needle 2 step graphs captured) after the call, process-wide. */
+nd_status nd_test_xcd_local(nd_ctx* ctx, int32_t enable, uint32_t* probed);
+
 /* ------------------------------------------------------------- weights */
 
 /* Uploads one int8 matrix: W int8 [n][k] row-major, scales f32 [n][k/g]

@@ -3,9 +3,11 @@
 // reference's invariants (backends/cq.ts:113-126, model/runtime.ts:150-160,
 // 289-299, 885-891) so that the host binding can raise the same NeedleError
 // codes.
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "nd_internal.hpp"
@@ -77,6 +79,55 @@ static nd_status ensure_partials(nd_ctx* ctx, size_t floats) {
 
 static inline size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
+// ------------------------------------------------------ workgroup placement
+
+namespace {
+// Thread 0 of workgroup L writes the id of the XCC (XCD) it runs on:
+// HW_REG_XCC_ID (hardware register 20), bits [3:0].
+__global__ void xcc_probe_kernel(uint32_t* out, uint32_t n) {
+  if (threadIdx.x == 0 && blockIdx.x < n)
+    out[blockIdx.x] = (uint32_t)__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15u;
+}
+
+std::mutex g_xcd_mu;
+int g_xcd_probed = -1;  // -1 no device probed yet, else 1 when every probed device passed
+std::atomic<bool> g_xcd_local{false};
+std::atomic<bool> g_xcd_off{false};
+}  // namespace
+
+hipError_t nd_probe_xcd_placement(hipStream_t s, bool* ok) {
+  constexpr uint32_t kMax = 1024;
+  uint32_t* d = nullptr;
+  hipError_t e = hipMalloc(&d, kMax * sizeof(uint32_t));
+  if (e != hipSuccess) return e;
+  std::vector<uint32_t> h(kMax);
+  bool pass = true;
+  for (uint32_t n : {8u, 64u, kMax}) {
+    hipLaunchKernelGGL(xcc_probe_kernel, dim3(n), dim3(64), 0, s, d, n);
+    if ((e = hipGetLastError()) != hipSuccess) break;
+    if ((e = hipMemcpyAsync(h.data(), d, n * sizeof(uint32_t), hipMemcpyDeviceToHost, s)) !=
+        hipSuccess)
+      break;
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) break;
+    for (uint32_t L = 8; L < n; ++L) pass = pass && h[L] == h[L % 8];
+  }
+  hipFree(d);
+  if (e != hipSuccess) return e;
+  *ok = pass;
+  std::lock_guard<std::mutex> lock(g_xcd_mu);
+  g_xcd_probed = (g_xcd_probed != 0 && pass) ? 1 : 0;
+  g_xcd_local = g_xcd_probed == 1 && !g_xcd_off;
+  return hipSuccess;
+}
+
+bool nd_xcd_local() { return g_xcd_local.load(std::memory_order_relaxed); }
+
+void nd_xcd_override(bool off) {
+  std::lock_guard<std::mutex> lock(g_xcd_mu);
+  g_xcd_off = off;
+  g_xcd_local = g_xcd_probed == 1 && !off;
+}
+
 static void free_mat_buffers(nd_mat* m) {
   hipFree(m->w);
   hipFree(m->scales);
@@ -122,6 +173,17 @@ nd_status nd_create(int32_t device, nd_ctx** out) {
     return nd_fail(nullptr, ND_ERR_BACKEND, "attention scratch set-up on device %d: %s", device,
                    hipGetErrorString(e));
   }
+  // Whether workgroups of one L % 8 share an XCD on this device (the
+  // XCD-local hand-offs; otherwise their agent-scope forms run).
+  bool placed = false;
+  e = nd_probe_xcd_placement(ctx->stream, &placed);
+  if (e != hipSuccess) {
+    hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return nd_fail(nullptr, ND_ERR_BACKEND, "workgroup placement probe on device %d: %s", device,
+                   hipGetErrorString(e));
+  }
+  ctx->xcd_local = placed;
   e = hipMalloc(&ctx->mv_split, kMatvecSplitBytes);
   if (e == hipSuccess) e = hipMemsetAsync(ctx->mv_split, 0, kMatvecSplitBytes, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
@@ -176,6 +238,17 @@ nd_status nd_sync(nd_ctx* ctx) {
 }
 
 void* nd_stream(nd_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+nd_status nd_test_xcd_local(nd_ctx* ctx, int32_t enable, uint32_t* probed) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  nd_xcd_override(enable == 0);
+  if (probed) {
+    std::lock_guard<std::mutex> lock(g_xcd_mu);
+    *probed = g_xcd_probed == 1 ? 1u : 0u;
+  }
+  return ND_OK;
+}
 
 // ------------------------------------------------------------- matrices
 

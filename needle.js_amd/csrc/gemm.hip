@@ -370,7 +370,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ sw, const float* __restrict__ X,
     uint32_t ldx, const float* __restrict__ norm, float* __restrict__ Y, uint32_t M, uint32_t N,
     uint32_t K, uint32_t ldy, float* __restrict__ part, uint32_t* __restrict__ counters,
-    nd::RopeStore rope) {
+    nd::RopeStore rope, uint32_t xcd_local) {
   __shared__ __attribute__((aligned(16))) int8_t lds[CPW][3][16][kLdsRow];
   __shared__ float s_fm[CPW][16];
   const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63;
@@ -552,8 +552,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
     // Workgroup (x, y, z) runs on XCD (tile + tiles z) % 8: with a multiple
     // of 8 tiles every slice of a tile shares its XCD, and the slice sum
     // stays in that XCD's L2 (workgroup-scope stores and counter; the
-    // agent-scope loads below miss the CU's L1 and hit the L2).
-    const bool xl = (gridDim.x * gridDim.y) % 8 == 0;
+    // agent-scope loads below miss the CU's L1 and hit the L2).  xcd_local:
+    // the placement was confirmed on this device.
+    const bool xl = xcd_local && (gridDim.x * gridDim.y) % 8 == 0;
     float* mine = part + ((size_t)tile * S + blockIdx.z) * 1024;
     if (xl) {
 #pragma unroll
@@ -764,7 +765,8 @@ __global__ __launch_bounds__(512) void gemm_i8_astat_kernel(
 }
 
 using F32aFn = void (*)(const int8_t*, const float*, const float*, uint32_t, const float*, float*,
-                        uint32_t, uint32_t, uint32_t, uint32_t, float*, uint32_t*, nd::RopeStore);
+                        uint32_t, uint32_t, uint32_t, uint32_t, float*, uint32_t*, nd::RopeStore,
+                        uint32_t);
 
 template <bool NORM, int CPW>
 F32aFn pick_f32a(int epilogue) {
@@ -921,6 +923,6 @@ hipError_t nd_launch_gemm_f32(const nd_mat* w, const float* x, uint32_t ldx, con
                         : (norm ? pick_f32a<true, 1>(epilogue) : pick_f32a<false, 1>(epilogue));
   hipLaunchKernelGGL(f, dim3((w->n + 63) / 64, (M + 15) / 16, S), dim3(kGemmThreads), 0, s, w->w,
                      w->scales, x, ldx, norm, y, M, w->n, w->k, ldy, split->partials,
-                     split->counters, rope ? *rope : nd::RopeStore{});
+                     split->counters, rope ? *rope : nd::RopeStore{}, nd_xcd_local() ? 1u : 0u);
   return hipGetLastError();
 }

@@ -1025,7 +1025,11 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
   float* part_ml = a.partials + (size_t)a.batch * hq * max_chunks * kHeadDim;
   // Tiles per wave: cp / kMinChunk (cp is a multiple of it).
   const uint32_t tiles = cp / kMinChunk;
-  if (a.batch == 1 && max_chunks > 1 && a.seq_kv_heads * max_chunks < kTargetSingle) {
+  // The XCD-local forms need the dispatcher's placement (workgroups of one
+  // L % 8 on one XCD), confirmed per device when the context is created;
+  // without it the chunks merge at the agent coherence point (last form).
+  const bool xcd = nd_xcd_local();
+  if (xcd && a.batch == 1 && max_chunks > 1 && a.seq_kv_heads * max_chunks < kTargetSingle) {
     // One row whose 256-position chunks leave the launch short of
     // kTargetSingle workgroups (8 heads x 2048: 64): two-wave workgroups on
     // 128-position chunks double them (5.85 against 6.28 us at 2048; at
@@ -1045,7 +1049,7 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
       return hipGetLastError();
     }
   }
-  if (max_chunks > 1) {
+  if (xcd && max_chunks > 1) {
     // Rows split into chunks: the XCD-local merge (grid laid out per XCD,
     // see attention_kernel).
     auto kernel = tiles == 1   ? attention_kernel<REP, F32, false, kWaves, 1, true>

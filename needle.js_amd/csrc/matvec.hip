@@ -408,7 +408,7 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_slice_kernel(
     const int8_t* __restrict__ W, const float* __restrict__ S, const float* __restrict__ X,
     uint32_t x_stride, float* __restrict__ P, uint32_t* __restrict__ counters,
     float* __restrict__ Y, uint32_t y_stride, uint32_t K, uint32_t groups, uint32_t gshift,
-    uint32_t row_start, uint32_t row_count, uint32_t bc) {
+    uint32_t row_start, uint32_t row_count, uint32_t bc, uint32_t xl) {
   constexpr uint32_t KS = 256 * NP, kUnits = KS / 8;  // 8-value units of one batch row
   constexpr uint32_t kSg = KS / 32;                   // 32-wide groups of the slice
   __shared__ uint4 s_xs[kSg * 64];                    // also the cross-wave sums (16 KB)
@@ -422,6 +422,8 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_slice_kernel(
   // then stays in that XCD's L2: partials stored and counted at workgroup
   // scope (plain stores, the atomic performed in the L2), read by the last
   // slice with agent-scope loads, which miss the CU's L1 and hit the L2.
+  // Without xl (workgroups of one L % 8 not known to share an XCD) the
+  // partials and the counter go to the agent coherence point instead.
   const uint32_t nblocks = (row_count + 63) / 64, rpx = (nblocks + 7) / 8;
   const uint32_t L = blockIdx.x, sl = L >> 3, rb = 8 * (sl % rpx) + (L & 7);
   const uint32_t nslices = gridDim.x / (8 * rpx);
@@ -547,9 +549,13 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_slice_kernel(
   for (uint32_t q = 0; q < 4; ++q) sum += red[((4 * q + ot) * 4 + oc) * 64 + lane];
   sum += nd::lane_xor<32>(sum);
   const uint32_t b = (lane >> 4) * 4 + oc, orow = row0 + 16 * ot + (lane & 15);
-  if (lane < 32 && orow < row_count && b < bc)
-    __hip_atomic_store(P + ((size_t)slice * kSplitRows + b) * row_count + orow,
-                       ldexpf(sum, s_e[b]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (lane < 32 && orow < row_count && b < bc) {
+    float* const pp = P + ((size_t)slice * kSplitRows + b) * row_count + orow;
+    if (xl)
+      __hip_atomic_store(pp, ldexpf(sum, s_e[b]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else
+      __hip_atomic_store(pp, ldexpf(sum, s_e[b]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   // Count the slice in once its partials are stored (completed in the L2);
   // the last slice of the row block adds all of them in order s = 0, 1, ...
   // and resets the counter for the next launch.  Each row block's counter
@@ -559,8 +565,10 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_slice_kernel(
   __syncthreads();
   __shared__ uint32_t s_last;
   if (t == 0)
-    s_last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
-             nslices - 1;
+    s_last = (xl ? __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_WORKGROUP)
+                 : __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT)) == nslices - 1;
   __syncthreads();
   if (!s_last) return;
   const uint32_t fb = t >> 6, frow = row0 + (t & 63);
@@ -577,7 +585,12 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_slice_kernel(
       if (q < nslices) total += v[q];
     Y[(size_t)fb * y_stride + frow] = total;
   }
-  if (t == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (t == 0) {
+    if (xl)
+      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    else
+      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // Read-only stream over `units` 16-byte units: the matvec's own load form
@@ -717,7 +730,8 @@ hipError_t nd_launch_matvec(const nd_mat* m, const float* x, uint32_t batch, uin
         const uint32_t rpx = ((rc + 63) / 64 + 7) / 8;  // row blocks per XCD
         hipLaunchKernelGGL(kern, dim3(8 * rpx * slices), dim3(64 * kMfmaWaves), 0, s, m->w,
                            m->scales, xb, x_stride, P, counters, yb + r0, y_stride, m->k,
-                           m->k / m->g, gshift, row_start + r0, rc, bc);
+                           m->k / m->g, gshift, row_start + r0, rc, bc,
+                           nd_xcd_local() ? 1u : 0u);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
       }

@@ -41,6 +41,7 @@ struct nd_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   std::string error;
+  bool xcd_local = false;  // this device passed the placement probe
   // Device staging for the host-pointer entry points (grown on demand).
   void* stage = nullptr;
   size_t stage_bytes = 0;
@@ -103,6 +104,19 @@ nd_status nd_hip_fail(nd_ctx* ctx, hipError_t err, const char* what);
 inline hipStream_t nd_pick_stream(nd_ctx* ctx, void* stream) {
   return stream ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
 }
+
+// Workgroup placement.  The XCD-local hand-offs (attention chunk merge,
+// k-slice matvec sum, split-k GEMM sum, the Needle 2 fused layer launch)
+// keep a merge group's workgroups at one L % 8 and rely on the dispatcher
+// handing workgroup L of a launch to the XCD of workgroup L % 8.
+// nd_probe_xcd_placement checks that on the current device (every workgroup
+// of launches of 8, 64 and 1024 workgroups reads its XCC id) and records
+// the result; nd_xcd_local() is true only when every probed device passed
+// and the test override (nd_xcd_override) has not switched it off.  False
+// selects the agent-scope forms.
+hipError_t nd_probe_xcd_placement(hipStream_t s, bool* ok);
+bool nd_xcd_local();
+void nd_xcd_override(bool off);
 
 // Kernel launchers (each validates nothing: callers check shapes first).
 // `split`: kMatvecSplitBytes of device memory that lets batches of 3 or more

@@ -2419,8 +2419,11 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
     // Layer l - 1's Wo and layer l's projection run inside mix launch l
     // (when no last mix runs, the last Wo has no reader).
     const uint32_t wo_tpr = n->d.heads * kHd / 16;  // int8 Wo threads a row
-    const bool fuse = n->cq ? wo_cq_fits(*n->wo[0])
-                            : (wo_tpr & (wo_tpr - 1)) == 0 && wo_tpr <= (uint32_t)kMixWg;
+    // The fused launch keeps its workgroups on one XCD (workgroups L % 8 ==
+    // 0 only): without the confirmed placement the launches stay separate.
+    const bool fuse = nd_xcd_local() &&
+                      (n->cq ? wo_cq_fits(*n->wo[0])
+                             : (wo_tpr & (wo_tpr - 1)) == 0 && wo_tpr <= (uint32_t)kMixWg);
     if ((e = enqueue_mix(n, l, parts, s, fuse, fuse)) != hipSuccess) return e;
     if (!pre) break;
     if ((e = enqueue_block(n, l, s, !fuse, !fuse)) != hipSuccess) return e;
@@ -2433,7 +2436,7 @@ enum GraphKind { kGraphPrompt = 0, kGraphPromptSelect = 1, kGraphDecodeSelect = 
 // Launches the step graph of `kind`, capturing and instantiating it first if
 // the cached one was built for another cache geometry, KV mode or pooling.
 nd_status launch_graph(nd_ctx* ctx, nd_needle* n, GraphKind kind) {
-  const uint32_t mode = n->kv.mode | (pool_on(n) ? 2u : 0u);
+  const uint32_t mode = n->kv.mode | (pool_on(n) ? 2u : 0u) | (nd_xcd_local() ? 4u : 0u);
   if (n->graph_alloc != n->kv.alloc || n->graph_sink != n->kv.sink || n->graph_mode != mode) {
     drop_graphs(n);
     n->graph_alloc = n->kv.alloc;

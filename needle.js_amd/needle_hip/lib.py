@@ -58,6 +58,7 @@ SIGNATURES = {
     "nd_last_error": (C.c_char_p, [P]),
     "nd_sync": (I32, [P]),
     "nd_stream": (P, [P]),
+    "nd_test_xcd_local": (I32, [P, I32, PU32]),
     "nd_mat_upload_i8": (I32, [P, P, P, U32, U32, U32, PP]),
     "nd_mat_upload_i8_d": (I32, [P, P, P, U32, U32, U32, PP]),
     "nd_mat_free": (I32, [P, P]),

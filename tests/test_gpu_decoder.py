@@ -4,9 +4,9 @@ decoder against the oracle, through the C ABI.
 Bars: matmul outputs within 1e-3 relative / 1e-4 absolute elementwise;
 selected ids (greedy, masked) identical at every step; synthetic prefix KV
 bit-exact; logits within 1e-3 relative both normwise and elementwise against
-the step's largest logit; log-probabilities within 2e-3 of the largest
-logit (|d lp| <= |d logit[id]| + |d logsumexp| <= 2 max|d logit|).  Appended
-K/V codes:
+the step's largest logit; log-probabilities within 0.05 absolute (the
+full-size workload measures 0.034 at logits up to ~146).  Appended K/V
+codes:
 
 * layer 0, whose inputs are the token's embedding on both sides: equal to the
   oracle's, or one apart with the oracle's quotient x / s within 1e-4 of the
@@ -16,7 +16,8 @@ K/V codes:
   1e-5, values bit-exact) -- the codes are the correct rounding of what the
   GPU computed;
 * every layer: at most one code from the oracle's (deeper layers see
-  drifted inputs, see test_gpu_prefill).
+  drifted inputs, see test_gpu_prefill), on at most 1% of a layer's
+  appended codes.
 """
 
 import ctypes as C
@@ -79,6 +80,8 @@ def check_last_layer(weights, ref_theta, proj, kc, vc, ks, vs, positions, what):
 def check_appended(caches, lengths, steps, kc, vc, ks, vs, g, what):
     """Appended rows [len_b, len_b + steps) of every sequence against the
     oracle's (which captured its pre-quantization vectors)."""
+    differ = np.zeros(g.layers, np.int64)
+    total = 0
     for b, c in enumerate(caches):
         p0 = int(lengths[b])
         for l in range(g.layers):
@@ -91,7 +94,13 @@ def check_appended(caches, lengths, steps, kc, vc, ks, vs, g, what):
                         assert_codes_or_boundary_flips(got, want, raw, 1e-4,
                                                        f"{what} layer 0 b={b} h={h}")
                     else:
-                        assert np.abs(got.astype(int) - want.astype(int)).max() <= 1, (what, l, b)
+                        d = np.abs(got.astype(int) - want.astype(int))
+                        assert d.max() <= 1, (what, l, b)
+                        differ[l] += int((d != 0).sum())
+                    if l == 0:
+                        total += got.size
+    say(f"[measure] {what}: codes differing per layer {differ.tolist()} of {total}")
+    assert (differ <= 0.01 * total).all(), (what, differ.tolist(), total)
 
 
 def matmul(hip, m, x):
@@ -165,7 +174,7 @@ def run_case(hip, geometry, wl, seed):
             want_id, want_lp = oracle.select_mask(want_logits, mask)
             check_logits(logits[b], want_logits, (t, b))
             assert int(ids[b]) == want_id, (t, b)
-            assert abs(lps[b] - want_lp) <= 2e-3 * np.abs(want_logits).max(), (t, b)
+            assert abs(lps[b] - want_lp) <= 0.05, (t, b, lps[b], want_lp)
             assert int(pos[b]) == p + 1
         cur = ids.astype(np.int64)
     kc, vc, kss, vss = batch_cache(hip, gpu, geometry)
@@ -235,9 +244,8 @@ def test_constrained_decode_full_size(hip):
         check_steps=checks)
     mism = np.argwhere(ids != want_ids)
     assert mism.size == 0, f"{len(mism)} ids differ, first (step, seq) {mism[:3].tolist()}"
-    scale = max(float(np.abs(want_logits[i, b]).max()) for i in range(len(checks))
-                for b in range(wl.batch))
-    assert np.abs(lps - want_lps).max() <= 2e-3 * scale
+    say(f"[measure] log-probability max |error| {float(np.abs(lps - want_lps).max()):.4f}")
+    assert np.abs(lps - want_lps).max() <= 0.05
     for i, t in enumerate(checks):
         for b in range(wl.batch):
             check_logits(got_logits[t][b], want_logits[i, b], (t, b))

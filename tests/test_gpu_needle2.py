@@ -6,9 +6,10 @@ the other way at a boundary moves later outputs by ~1e-4 relative); greedy
 token sequences and selected ids identical; log-probabilities within 1e-3.
 Appended KV codes: in layer 0, whose inputs agree with the oracle's to fp32
 rounding, equal to the oracle's or one apart with the oracle's quotient
-x / s within 1e-4 of the rounding boundary between them; in every layer at
-most one code apart (deeper layers see inputs that drifted by the model's
-own fp32 rounding).
+x / s within 1e-4 of the rounding boundary between them, scales within 1e-5
+relative; in deeper layers (inputs that drifted by the model's own fp32
+rounding) at most one code apart on at most 1% of a layer's codes, scales
+within 1e-3 relative.
 """
 
 import dataclasses
@@ -56,6 +57,8 @@ def check_kv(model, ref, g, written, sink, what):
     pos = slot_positions(written, alloc, sink, g.kv_window)
     used = np.flatnonzero(pos >= 0)
     for layer in range(g.layers):
+        differ = total = 0
+        worst = 0.0
         for h in range(g.kv_heads):
             gk, gv, gks, gvs = model.resident.kv_read(layer, h)
             rk, rv, rks, rvs = ref.kv_read(layer, h)
@@ -69,9 +72,17 @@ def check_kv(model, ref, g, written, sink, what):
                 for got, want in ((gk, rk), (gv, rv)):
                     d = np.abs(got[used].astype(int) - want[used].astype(int))
                     assert d.max() <= 1, (what, layer, h)
-            tol = 1e-5 if layer == 0 else 1e-2
-            np.testing.assert_allclose(gks[used], rks[used], rtol=tol)
-            np.testing.assert_allclose(gvs[used], rvs[used], rtol=tol)
+                    differ += int((d != 0).sum())
+                    total += d.size
+            tol = 1e-5 if layer == 0 else 1e-3
+            for got, want in ((gks, rks), (gvs, rvs)):
+                rel = np.abs(got[used].astype(np.float64) / want[used] - 1.0)
+                worst = max(worst, float(rel.max())) if layer else worst
+                assert rel.max() <= tol, (what, layer, h, float(rel.max()))
+        if layer:
+            say(f"[measure] {what} layer {layer}: {differ}/{total} codes differ, "
+                f"scale rel err max {worst:.2e}")
+            assert differ <= 0.01 * total, (what, layer, differ, total)
 
 
 def close_confidence(got, want, what):

@@ -16,10 +16,11 @@ The oracle prefill is the reference's: one step per prompt token
 * every layer: codes at most one apart from the oracle's.  Deeper layers see
   inputs that have drifted from the oracle's (each layer's fp32 rounding and
   the flipped codes of earlier layers, amplified by the random weights: the
-  key scales of layer 7 differ by up to 1.9e-3 relative at 2048 tokens), so
-  their codes differ from the oracle's more often (0.33% at layer 7), and
-  the last-layer check above is what shows such codes are the correct
-  rounding of the GPU's values;
+  scales of deeper layers differ by up to 9.4e-4 relative over these
+  prompts), so their codes differ from the oracle's more often (0.24% at
+  layer 7 of 2048 tokens; the bar is 1% of a layer's codes, scales within
+  1.5e-3 relative), and the last-layer check above is what shows such codes
+  are the correct rounding of the GPU's values;
 * the last position's logits within 1e-3 relative both normwise and
   elementwise against the largest logit (measured 4.9e-5 and 3.7e-5 at 2048
   tokens), and the same greedy token;
@@ -63,6 +64,7 @@ def compare(hip, g, n, seed):
     _, _, tk, tks, tv, tvs = tf
     for l in range(g.layers):
         differ = 0
+        worst = 0.0
         for h in range(g.kv_heads):
             got_k, got_v, got_ks, got_vs = cache.read(l, h)
             ref_k, ref_v, ref_ks, ref_vs = rc.read(l, h)
@@ -74,9 +76,11 @@ def compare(hip, g, n, seed):
                     d = np.abs(a.astype(int) - b.astype(int))
                     assert d.max() <= 1, (l, h)
                     differ += int((d != 0).sum())
-            tol = 1e-6 if l == 0 else 1e-2
-            np.testing.assert_allclose(got_ks, ref_ks, rtol=tol)
-            np.testing.assert_allclose(got_vs, ref_vs, rtol=tol)
+            tol = 1e-6 if l == 0 else 1.5e-3
+            for a, b in ((got_ks, ref_ks), (got_vs, ref_vs)):
+                rel = np.abs(a.astype(np.float64) / b - 1.0).max()
+                worst = max(worst, float(rel))
+                assert rel <= tol, (l, h, float(rel))
             if l == last:
                 # The GPU's own values, quantized by the oracle.
                 k_tf, _, _, _, _, _ = tf
@@ -85,6 +89,8 @@ def compare(hip, g, n, seed):
                 np.testing.assert_allclose(got_ks, tks[:, h], rtol=1e-6)
                 assert np.array_equal(got_v, tv[:, h]), f"last layer values head {h}"
                 assert np.array_equal(got_vs.view(np.uint32), tvs[:, h].view(np.uint32))
+        say(f"[measure] prefill {n} layer {l}: {differ} codes differ, scale rel err max "
+            f"{worst:.2e}")
         assert differ <= 0.01 * n * g.kv_heads * 64 * 2, (l, differ)
     w64, g64 = want.astype(np.float64), logits.astype(np.float64)
     assert np.linalg.norm(g64 - w64) <= 1e-3 * np.linalg.norm(w64)
