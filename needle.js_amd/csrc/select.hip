@@ -82,11 +82,14 @@ __device__ Best block_best(Best b, float* redv, uint32_t* redo) {
 }
 
 // One term e^x, x = logit - max <= 0, of the float64 log-softmax sum: the
-// float64 exp while x >= -20, the f32 exp below.  The leading term is 1, so
-// the terms below e^-20 = 2.1e-9 together hold at most vocab * 2.1e-9 of the
-// sum, and f32's relative error (< 2.4e-7, with the rounding of x to f32)
-// moves the sum by at most vocab * 5e-16 -- 1.6e-11 at a 32768 vocabulary,
-// far below the float64 log's own use of the sum.  The float64 exp runs only
+// float64 exp while x >= -20, the fast f32 exp below.  The leading term is 1,
+// so the terms below e^-20 = 2.1e-9 together hold at most vocab * 2.1e-9 of
+// the sum.  __expf is v_exp_f32 of x log2(e) rounded to f32: the rounding
+// moves the exponent by at most |x| 1.44 2^-24 (9e-6 at x = -104, where the
+// f32 result reaches 0), i.e. a relative error below 1e-5 with the
+// instruction's own ulp, and flushed subnormals lose terms below 1.2e-38.
+// Together that moves the sum by at most vocab * 2.1e-9 * 1e-5 -- 6.9e-10 at
+// a 32768 vocabulary -- and the log-probability by less than 7e-10.  The float64 exp runs only
 // while some lane of the wave holds such a term, so a row whose logits
 // spread over tens of units (most of the vocabulary below max - 20) costs
 // the f32 exp per term.

@@ -984,19 +984,38 @@ def xorshift32(seed: int) -> Callable[[], float]:
     return draw
 
 
+def _js_max(a: float, b: float) -> float:
+    """Math.max of two numbers: NaN when either is NaN."""
+    if math.isnan(a) or math.isnan(b):
+        return math.nan
+    return a if a >= b else b
+
+
 def sample(logits: np.ndarray, temperature: float, top_k: int, random: Callable[[], float]) -> int:
     """model/model.ts:213-240: argmax at temperature 0, else a draw from the
-    softmax of logits / temperature over the top_k largest (all when 0)."""
+    softmax of logits / temperature over the top_k largest (all when 0).
+    Edge cases as the reference evaluates them: 0 < top_k < 1 keeps no
+    candidate and returns 0 (indices[-1] ?? 0); a NaN logit makes the
+    maximum NaN (Math.max), so every probability is NaN, no threshold test
+    passes and the last candidate is returned (the last id when top_k keeps
+    every id).  With a NaN logit and fewer candidates than ids the
+    reference's comparator returns NaN, which leaves its sort order to the
+    engine: that case is parity unpinned."""
     if not temperature > 0:
         return argmax(logits)
     n = logits.size
     count = min(int(math.floor(top_k)), n) if top_k > 0 else n
     indices = list(range(n))
     if count < n:
-        indices.sort(key=lambda i: -float(logits[i]))  # stable, as Array.prototype.sort
+        # Array.prototype.sort is stable (a NaN logit sorts as 0 here).
+        indices.sort(key=lambda i: -float(logits[i]) if not math.isnan(logits[i]) else 0.0)
     indices = indices[:count]
+    if count == 0:
+        return 0
     scaled = logits[indices].astype(np.float64) / temperature
-    maximum = max(-math.inf, float(np.max(scaled)))
+    maximum = -math.inf
+    for v in scaled:
+        maximum = _js_max(maximum, float(v))
     probabilities = np.exp(scaled - maximum)
     threshold = random() * _seq_sum(probabilities)
     for i in range(count):

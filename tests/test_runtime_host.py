@@ -47,6 +47,23 @@ def test_sample_greedy_topk_and_distribution():
     assert sample(two, 1.0, 0, constant) == 0  # 0.5 * 2 - 1 <= 0
 
 
+def test_sample_edge_cases_follow_the_reference():
+    """model.ts:213-240 evaluated by hand: 0 < topK < 1 gives count 0, an
+    empty candidate list and `indices[count - 1] ?? 0` = 0; a NaN logit makes
+    Math.max NaN, every probability NaN, no `threshold <= 0` test passes and
+    the last candidate (the last id, topK keeping every id) is returned."""
+    logits = np.array([0.5, 2.0, -1.0, 0.25], np.float32)
+    assert sample(logits, 1.0, 0.5, xorshift32(4)) == 0
+    assert sample(logits, 0.7, 0.99, lambda: 0.0) == 0
+    nan = logits.copy()
+    nan[1] = np.nan
+    for draw in (0.0, 0.3, 0.999):
+        assert sample(nan, 1.0, 0, lambda: draw) == 3
+        assert sample(nan, 2.0, 4, lambda: draw) == 3
+    # Without NaN a draw of 0 returns the first candidate with nonzero mass.
+    assert sample(logits, 1.0, 0, lambda: 0.0) == 0
+
+
 def test_log_softmax_and_argmax():
     rng = np.random.default_rng(4)
     logits = (rng.normal(size=8192) * 20).astype(np.float32)
