@@ -556,39 +556,50 @@ def needle2_token_bytes(g, visible):
     return g.layers * per_layer + engram + g.vocab * (g.dim + 4)
 
 
-def needle2_cq_token_bytes(g, visible, bits, group):
-    """HBM bytes one Needle 2 token reads with Cactus-Quant matrices of one
-    width: packed codes (bits per weight, ternary 2) + binary16 norms per
-    group of every matrix it multiplies, the engram rows it gathers and
-    `visible` K/V rows per layer and KV head."""
-    pb = 2 if bits == 5 else bits
+def needle2_cq_token_bytes(g, visible, form):
+    """HBM bytes one Needle 2 token reads with Cactus-Quant matrices, each in
+    the (bits, group) that form(role, index) gives it: packed codes (bits per
+    weight, ternary 2) + binary16 norms per group of every matrix it
+    multiplies, the engram rows it gathers and `visible` K/V rows per layer
+    and KV head."""
 
-    def mat(n, k):
+    def mat(n, k, role, index=0):
+        bits, group = form(role, index)
+        pb = 2 if bits == 5 else bits
         kpad = -(-k // group) * group
         return n * (kpad * pb // 8 + kpad // group * 2)
 
-    qkvg = (2 * g.heads + 2 * g.kv_heads) * 64
-    per_layer = (mat(qkvg, g.dim) + mat(g.dim, g.heads * 64)
-                 + mat(2 * g.lanes + g.lanes * g.lanes, g.lanes * g.dim)
-                 + visible * g.kv_heads * (64 * 2 + 8))
+    total = 0
+    hd, ln = 64, g.lanes
+    for l in range(g.layers):
+        total += (mat(g.heads * hd, g.dim, "wq", l) + mat(g.kv_heads * hd, g.dim, "wk", l)
+                  + mat(g.kv_heads * hd, g.dim, "wv", l) + mat(g.heads * hd, g.dim, "wgate", l)
+                  + mat(g.dim, g.heads * hd, "wo", l) + mat(ln, ln * g.dim, "phi_pre")
+                  + mat(ln, ln * g.dim, "phi_post") + mat(ln * ln, ln * g.dim, "phi_res")
+                  + visible * g.kv_heads * (64 * 2 + 8))
     cat = g.engram_tables * g.engram_sub
-    engram = len(g.sites) * (mat(2 * g.dim, cat) + mat(g.engram_tables, g.engram_sub))
-    return g.layers * per_layer + engram + mat(g.vocab, g.dim)
+    for s in range(len(g.sites)):
+        total += (mat(g.dim, cat, "eg_key", s) + mat(g.dim, cat, "eg_value", s)
+                  + mat(g.engram_tables, g.engram_sub, "eg_tables", s))
+    return total + mat(g.vocab, g.dim, "embedding")
 
 
 def bench_needle2_cq(torch, hip, reps, bits=4, group=32):
     """The same generate (shipped geometry, 128-token prompt, 64 greedy
     tokens) with every matrix in the Cactus-Quant form of the shipped archive
-    (CQ4, groups of 32): products as cqMatvec, rows as dequantizeCqRow, the
+    (CQ4, groups of 32; bits "mixed": each matrix in its own width and group,
+    cact.mixed_form): products as cqMatvec, rows as dequantizeCqRow, the
     prompt as one batched pass (the CQ matvec over its 128 rows).  Timing
     only: the GPU tests hold its parity with the oracle."""
     import numpy as np
 
     from needle_hip import NeedleModel, synth
+    from needle_hip.cact import mixed_form
     from needle_hip.needle2 import Needle2Geometry, Needle2Weights
     from needle_hip.runtime import EOS_TOKEN_ID
 
     g = Needle2Geometry()
+    form = mixed_form if bits == "mixed" else (lambda role, index=0: (bits, group))
     model = NeedleModel(hip, Needle2Weights(g, 2026, cq_bits=bits, cq_group=group))
     prompt = synth.Stream(2026, "needle2.prompt").integers(128, 0, g.vocab - 1)
     new = 64
@@ -606,8 +617,9 @@ def bench_needle2_cq(torch, hip, reps, bits=4, group=32):
     wall, wall1 = float(np.median(walls)), float(np.median(walls1))
     n_gen = res.generated_tokens
     decode_ms = (wall - wall1) * 1e3 / max(1, n_gen - 1)
-    bytes_tok = needle2_cq_token_bytes(g, min(g.kv_window, 128 + n_gen // 2), bits, group)
-    part = {"bits": bits, "group": group, "prompt_tokens": 128, "generated_tokens": n_gen,
+    bytes_tok = needle2_cq_token_bytes(g, min(g.kv_window, 128 + n_gen // 2), form)
+    part = {"bits": bits, "group": group if bits != "mixed" else "mixed",
+            "prompt_tokens": 128, "generated_tokens": n_gen,
             "reps": reps, "wall_ms": wall * 1e3, "tokens_per_s": n_gen / wall,
             "decode_ms_per_token": decode_ms, "decode_tokens_per_s": 1e3 / decode_ms,
             "prefill_128_ms": wall1 * 1e3, "prefill_tokens_per_s": 128 / wall1, "bytes_per_token": bytes_tok,
@@ -832,7 +844,7 @@ def main():
     ap.add_argument("--skip-needle2", action="store_true")
     ap.add_argument("--needle2-reps", type=int, default=5)
     ap.add_argument("--only", choices=["matvec", "matvec8", "attention", "decode", "prefill",
-                                       "needle2", "needle2cq", "traffic", "attention_traffic", "cq",
+                                       "needle2", "needle2cq", "needle2mixed", "traffic", "attention_traffic", "cq",
                                        "grammar", "ceiling", "matvec_span", "copy_matvec"],
                     help="run one part alone and print its JSON (for profiling)")
     ap.add_argument("--decode-steps", type=int, default=128)
@@ -865,6 +877,8 @@ def main():
             part, _ = bench_needle2(torch, hip, args.needle2_reps, False, 0)
         elif args.only == "needle2cq":
             part = bench_needle2_cq(torch, hip, args.needle2_reps)
+        elif args.only == "needle2mixed":
+            part = bench_needle2_cq(torch, hip, args.needle2_reps, bits="mixed")
         elif args.only == "ceiling":
             part = bench_read_ceiling(torch, hip)
         elif args.only == "traffic":
@@ -948,6 +962,10 @@ def main():
         part = bench_needle2_cq(torch, hip, args.needle2_reps)
         parts["needle2_cq4_generate_b1"] = part
         print(f"[bench] needle2 cq4 generate b1 {part['tokens_per_s']:.0f} tok/s, decode "
+              f"{part['decode_ms_per_token']:.3f} ms/token", file=sys.stderr, flush=True)
+        part = bench_needle2_cq(torch, hip, args.needle2_reps, bits="mixed")
+        parts["needle2_cq_mixed_generate_b1"] = part
+        print(f"[bench] needle2 mixed-width generate b1 {part['tokens_per_s']:.0f} tok/s, decode "
               f"{part['decode_ms_per_token']:.3f} ms/token", file=sys.stderr, flush=True)
 
     part, cpu_gm = bench_grammar_mask(torch, hip, 20, 0 if args.skip_cpu else 5.0)

@@ -18,6 +18,7 @@
 // the Wo matvec.  The one-workgroup arithmetic keeps the reference's
 // float64-with-f32-stores form except the Sinkhorn iterations (fp32).
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstring>
 #include <type_traits>
@@ -240,16 +241,19 @@ __global__ __launch_bounds__(kWg) void n2_gather_kernel(BeginArgs a,
 // tables + t writes table t's row lookup[t] of engram site s into cat, or
 // zeros when lookup[tables + t] is 0.
 constexpr uint32_t kCqRowMax = 1024;  // padded row width of the embedding and tables
-struct CqRowsArgs {
-  const uint8_t* emb_p;
-  const uint16_t* emb_n;
-  uint32_t emb_kpad, emb_row_bytes;
-  const uint8_t* tab_p[4];
-  const uint16_t* tab_n[4];
-  uint32_t tab_kpad, tab_row_bytes;
-  float cb[16];  // by code (ternary: 0, +c, 0, -c)
-  uint32_t g, bits;
+// One matrix whose rows are dequantized: packed rows, binary16 norms,
+// padded width, bytes per row, group, code width, 1/sqrt(g) and the
+// codebook by code (ternary: 0, +c, 0, -c).
+struct CqSource {
+  const uint8_t* p;
+  const uint16_t* n;
+  uint32_t kpad, row_bytes, g, bits;
   double inverse_root;
+  float cb[16];
+};
+struct CqRowsArgs {
+  CqSource emb;     // the embedding
+  CqSource tab[4];  // each engram site's tables (their own formats)
   const uint32_t* token;   // null: no embedding row (the session's lanes come from the host)
   const uint32_t* lookup;  // [tables] indices, then [tables] valid flags
   uint32_t d, lanes;
@@ -274,12 +278,32 @@ __global__ __launch_bounds__(256) void n2_cq_rows_kernel(CqRowsArgs a) {
     if (a.cell0) a.cell0 += (size_t)m * a.cell_ld;
     a.cat += (size_t)m * a.cat_ld;
   }
+  // This workgroup's source, copied with constant indices (a runtime index
+  // into the argument block would copy it to scratch); its codebook in LDS.
+  const uint32_t i = b - 1, s = b ? i / a.tables : 0u, tb = b ? i % a.tables : 0u;
+  CqSource src;
+  if (b == 0) {
+    src = a.emb;
+  } else {
+    switch (s) {
+      case 0: src = a.tab[0]; break;
+      case 1: src = a.tab[1]; break;
+      case 2: src = a.tab[2]; break;
+      default: src = a.tab[3]; break;
+    }
+  }
+  __shared__ float s_cb[16];
+  if (t == 0) {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) s_cb[c] = src.cb[c];
+  }
+  __syncthreads();
   if (b == 0) {
     if (!a.token) return;
     const uint32_t tok = *a.token;
-    nd::cq_dequant_row(a.emb_p + (size_t)tok * a.emb_row_bytes,
-                       a.emb_n + (size_t)tok * (a.emb_kpad / a.g), a.cb, a.emb_kpad, a.g, a.bits,
-                       a.inverse_root, v);
+    nd::cq_dequant_row(src.p + (size_t)tok * src.row_bytes,
+                       src.n + (size_t)tok * (src.kpad / src.g), s_cb, src.kpad, src.g, src.bits,
+                       src.inverse_root, v);
     for (uint32_t k = t; k < a.d; k += blockDim.x) {
       const float val = (float)((double)v[k] * a.scale);
       for (uint32_t l = 0; l < a.lanes; ++l) a.x[(size_t)l * a.d + k] = val;
@@ -287,15 +311,14 @@ __global__ __launch_bounds__(256) void n2_cq_rows_kernel(CqRowsArgs a) {
     }
     return;
   }
-  const uint32_t i = b - 1, s = i / a.tables, tb = i % a.tables;
   float* out = a.cat + ((size_t)s * a.tables + tb) * a.sub;
   if (!a.lookup[a.tables + tb]) {
     for (uint32_t c = t; c < a.sub; c += blockDim.x) out[c] = 0.f;
     return;
   }
   const size_t row = (size_t)tb * a.slots + a.lookup[tb];
-  nd::cq_dequant_row(a.tab_p[s] + row * a.tab_row_bytes, a.tab_n[s] + row * (a.tab_kpad / a.g),
-                     a.cb, a.tab_kpad, a.g, a.bits, a.inverse_root, v);
+  nd::cq_dequant_row(src.p + row * src.row_bytes, src.n + row * (src.kpad / src.g), s_cb,
+                     src.kpad, src.g, src.bits, src.inverse_root, v);
   for (uint32_t c = t; c < a.sub; c += blockDim.x) out[c] = v[c];
 }
 
@@ -504,27 +527,54 @@ struct CqRows {
 // codes index the codebook in LDS; fp32 dots per group times the group's
 // norm, summed over the row's 16 lanes, times 1/sqrt(g).  Returns the two
 // row values in every lane of the row.
-template <uint32_t BITS>
-__device__ __forceinline__ float2 cq_rows_pair(const CqRows& q, size_t row0, uint32_t units,
-                                               const float* xs, const float* cb, uint32_t t) {
-  constexpr uint32_t kWords = BITS;  // 32 codes of BITS bits
-  const uint32_t u = t & 15, r = t >> 4;
-  const bool active = u < units;
-  const uint32_t uc = active ? u : 0;
-  uint32_t w[2][kWords];
+// The operands thread t loads for rows r and r + 32 (r = t / 16) of a
+// 64-row block, unit u = t % 16: the packed words (4, 3 or 2 by the code
+// width; ternary crumbs as 2) and the norms of the unit's groups.
+struct CqRowRegs {
+  uint32_t w[2][4];
   uint32_t nb[2][4];
+};
+
+__device__ __forceinline__ void cq_rows_load(const CqRows& q, uint32_t bits, size_t row0,
+                                             uint32_t units, uint32_t t, CqRowRegs& R) {
+  const uint32_t u = t & 15, r = t >> 4;
+  const uint32_t uc = u < units ? u : 0;
+  const uint32_t words = bits == 4 ? 4u : (bits == 3 ? 3u : 2u);
   const uint32_t ng = q.g < 32 ? 32u >> q.g_log2 : 1u;  // groups in a unit
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const size_t row = row0 + r + 32u * i;
     const uint32_t* src =
-        reinterpret_cast<const uint32_t*>(q.packed + row * q.row_bytes) + uc * kWords;
+        reinterpret_cast<const uint32_t*>(q.packed + row * q.row_bytes) + uc * words;
 #pragma unroll
-    for (uint32_t k = 0; k < kWords; ++k) w[i][k] = src[k];
+    for (uint32_t k = 0; k < 4; ++k) {
+      R.w[i][k] = 0u;
+      if (k < words) R.w[i][k] = src[k];
+    }
     const uint16_t* nrow = q.norms + row * q.groups + ((uc * 32) >> q.g_log2);
 #pragma unroll
-    for (uint32_t k = 0; k < 4; ++k) nb[i][k] = nrow[k < ng ? k : 0];
+    for (uint32_t k = 0; k < 4; ++k) R.nb[i][k] = nrow[k < ng ? k : 0];
   }
+}
+
+// Rows r and r + 32 of the workgroup's 64 (r = t / 16) of a Cactus-Quant
+// product with d <= 512 inputs (cqMatvec, backends/cq.ts:106-231) from the
+// operands cq_rows_load gave thread t (unit u = t % 16 of both rows).  xs
+// holds x with one pad float after every 32 (element e at e + e / 32, zeros
+// past d), so the 16 units' reads fall in distinct banks.  The unit's inputs
+// are rotated in registers -- the butterflies of fastWalshHadamard with
+// strides below min(g, 32), then strides 32 .. g / 2 across the lanes
+// holding the group's other units -- each result one fp32 add or subtract of
+// the reference's two operands; the codes index the codebook in LDS; fp32
+// dots per group times the group's norm, summed over the row's 16 lanes,
+// times 1/sqrt(g).  Returns the two row values in every lane of the row.
+template <uint32_t BITS>
+__device__ __forceinline__ float2 cq_rows_dot(const CqRows& q, const CqRowRegs& R,
+                                              uint32_t units, const float* xs, const float* cb,
+                                              uint32_t t) {
+  const uint32_t u = t & 15;
+  const bool active = u < units;
+  const uint32_t uc = active ? u : 0;
   float v[32];
 #pragma unroll
   for (int c = 0; c < 32; ++c) v[c] = xs[uc * 33 + c];
@@ -563,18 +613,19 @@ __device__ __forceinline__ float2 cq_rows_pair(const CqRows& q, size_t row0, uin
     for (uint32_t c = 0; c < 32; ++c) {
       uint32_t code;
       if constexpr (BITS == 4) {
-        code = (w[i][c >> 3] >> (4 * (c & 7))) & 15u;
+        code = (R.w[i][c >> 3] >> (4 * (c & 7))) & 15u;
       } else if constexpr (BITS == 3) {
         const uint32_t bit = 3 * c, k = bit >> 5, sh = bit & 31;
-        const uint32_t hi = sh > 29 ? w[i][k + 1 < kWords ? k + 1 : kWords - 1] << (32 - sh) : 0u;
-        code = ((w[i][k] >> sh) | hi) & 7u;
+        const uint32_t hi = sh > 29 ? R.w[i][k + 1 < 3 ? k + 1 : 2] << (32 - sh) : 0u;
+        code = ((R.w[i][k] >> sh) | hi) & 7u;
       } else {
-        code = (w[i][c >> 4] >> (2 * (c & 15))) & 3u;
+        code = (R.w[i][c >> 4] >> (2 * (c & 15))) & 3u;
       }
       dot = fmaf(cb[code], v[c], dot);
       if ((c & 7) == 7) {  // a group of 8, 16 or 32 and wider may end here: by selection
         const bool ends = c == 31 || q.g == 8 || (q.g == 16 && (c & 15) == 15);
-        const uint32_t h = q.g == 8 ? nb[i][c >> 3] : (q.g == 16 ? nb[i][c >> 4] : nb[i][0]);
+        const uint32_t h =
+            q.g == 8 ? R.nb[i][c >> 3] : (q.g == 16 ? R.nb[i][c >> 4] : R.nb[i][0]);
         const float with = fmaf(nd::cq_half(h), dot, total);
         total = ends ? with : total;
         dot = ends ? 0.f : dot;
@@ -588,6 +639,15 @@ __device__ __forceinline__ float2 cq_rows_pair(const CqRows& q, size_t row0, uin
     out[i] = total * q.out_scale;
   }
   return float2{out[0], out[1]};
+}
+
+// Both phases at once, for a block whose width is known at compile time.
+template <uint32_t BITS>
+__device__ __forceinline__ float2 cq_rows_pair(const CqRows& q, size_t row0, uint32_t units,
+                                               const float* xs, const float* cb, uint32_t t) {
+  CqRowRegs R;
+  cq_rows_load(q, BITS, row0, units, t, R);
+  return cq_rows_dot<BITS>(q, R, units, xs, cb, t);
 }
 
 // The fused Q/K/V/gate projection of one layer (runtime.ts:465-470) with the
@@ -634,11 +694,25 @@ struct QkvParams {
   float* Vs;
   uint32_t layer, alloc, sink, window, f32;
   RouteArgs route;
-  CqRows cq;
+  // Cactus-Quant models: the q, k, v and gate parts, each in its own format
+  // (code width cq_bits[i]; a mixed-width archive may differ per part).
+  CqRows cq[4];
+  uint32_t cq_bits[4];
 };
 
+// cq_rows_dot by code width (2-bit codes and ternary crumbs as 2).
+__device__ __forceinline__ float2 cq_rows_dot_any(uint32_t bits, const CqRows& q,
+                                                  const CqRowRegs& R, uint32_t units,
+                                                  const float* xs, const float* cb, uint32_t t) {
+  if (bits == 4) return cq_rows_dot<4>(q, R, units, xs, cb, t);
+  if (bits == 3) return cq_rows_dot<3>(q, R, units, xs, cb, t);
+  return cq_rows_dot<2>(q, R, units, xs, cb, t);
+}
+
 // Workgroup b of the projection launch (b == 2 (heads + kv_heads): the
-// routing).  WAIT (inside the fused mix launch): issue the weight rows and
+// routing).  CQ: the rows are Cactus-Quant, each 64-row block in its part's
+// format (q, k, v, gate).  WAIT (inside the fused mix launch): issue the
+// weight rows and
 // the epilogue operands, then wait until *flag != 0 -- the mix's signal
 // that x and the phi values are in the XCD's L2 -- before reading them (at
 // most `spin` rounds).  Each of the `waiters` workgroups then counts itself
@@ -646,7 +720,7 @@ struct QkvParams {
 // A workgroup whose wait runs out sets kStatusQkvWait in *status; one that
 // finds kFlagAbort (the mix gave up) counts itself in; both return without
 // storing anything.
-template <uint32_t BITS, bool WAIT>
+template <bool CQ, bool WAIT>
 __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_t* flag,
                                          uint32_t waiters, uint32_t* status = nullptr,
                                          uint32_t spin = 0) {
@@ -690,7 +764,7 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
   }
   const uint32_t lane = t & 63;
   const uint32_t d = p.d;
-  if constexpr (BITS == 0) {
+  if constexpr (!CQ) {
     // Loads first: this thread's weight bytes (unconditional, clamped, so
     // they issue back to back), the row scale, then x.
     const size_t row = (size_t)b * kHd + t / kQkvTpr;
@@ -703,15 +777,40 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
     const float acc = qkv_row_dot(wv, xs, t % kQkvTpr, d);
     if (t % kQkvTpr == 0) rows[t / kQkvTpr] = acc * srow;
   } else {
-    if (t == 0) {  // constant indices into the argument block
+    // The block's part and its first block; the part's descriptor field by
+    // field by selection (a runtime index into the argument block, or a copy
+    // of a whole descriptor, would go through scratch).
+    const uint32_t H = p.heads, K = p.kv_heads;
+    const uint32_t part = b < H ? 0u : (b < H + K ? 1u : (b < H + 2 * K ? 2u : 3u));
+    const uint32_t first = part == 0 ? 0u : (part == 1 ? H : (part == 2 ? H + K : H + 2 * K));
+    auto pick = [part](auto a, auto b, auto c, auto d) {
+      return part == 0 ? a : (part == 1 ? b : (part == 2 ? c : d));
+    };
+    CqRows q;
+    q.packed = pick(p.cq[0].packed, p.cq[1].packed, p.cq[2].packed, p.cq[3].packed);
+    q.norms = pick(p.cq[0].norms, p.cq[1].norms, p.cq[2].norms, p.cq[3].norms);
+    q.g = pick(p.cq[0].g, p.cq[1].g, p.cq[2].g, p.cq[3].g);
+    q.g_log2 = pick(p.cq[0].g_log2, p.cq[1].g_log2, p.cq[2].g_log2, p.cq[3].g_log2);
+    q.row_bytes = pick(p.cq[0].row_bytes, p.cq[1].row_bytes, p.cq[2].row_bytes,
+                       p.cq[3].row_bytes);
+    q.groups = pick(p.cq[0].groups, p.cq[1].groups, p.cq[2].groups, p.cq[3].groups);
+    q.out_scale = pick(p.cq[0].out_scale, p.cq[1].out_scale, p.cq[2].out_scale,
+                       p.cq[3].out_scale);
+    const uint32_t bits = pick(p.cq_bits[0], p.cq_bits[1], p.cq_bits[2], p.cq_bits[3]);
+    const uint32_t kpad = q.groups << q.g_log2;  // the part's padded row (<= 512)
+    // The rows' packed words and norms first (before the wait, as the int8
+    // rows), then the part's codebook into LDS.
+    CqRowRegs R;
+    cq_rows_load(q, bits, (size_t)(b - first) * kHd, kpad / 32, t, R);
+    if (t == 0) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s_cb[i] = p.cq.cb[i];
+      for (int i = 0; i < 16; ++i)
+        s_cb[i] = pick(p.cq[0].cb[i], p.cq[1].cb[i], p.cq[2].cb[i], p.cq[3].cb[i]);
     }
     if (!wait()) return;
-    const uint32_t kpad = (d + 31) & ~31u;
     for (uint32_t i = t; i < kpad; i += kQkvWg) xs[i + (i >> 5)] = i < d ? p.x[i] : 0.f;
     __syncthreads();
-    const float2 v = cq_rows_pair<BITS>(p.cq, (size_t)b * kHd, kpad / 32, xs, s_cb, t);
+    const float2 v = cq_rows_dot_any(bits, q, R, kpad / 32, xs, s_cb, t);
     if ((t & 15) == 0) {
       rows[t >> 4] = v.x;
       rows[(t >> 4) + 32] = v.y;
@@ -735,9 +834,9 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
                 p.f32);
 }
 
-template <uint32_t BITS>
+template <bool CQ>
 __global__ __launch_bounds__(kQkvWg) void n2_qkv_kernel(QkvParams p) {
-  qkv_body<BITS, false>(p, blockIdx.x, nullptr, 0);
+  qkv_body<CQ, false>(p, blockIdx.x, nullptr, 0);
 }
 
 // A Cactus-Quant Wo (y = W x, x of k <= 512 values, n a multiple of 64
@@ -758,14 +857,16 @@ __device__ __forceinline__ void wo_cq_rows(const WoCq& w, uint32_t k, uint32_t* 
   __shared__ float xs[512 + 16];
   __shared__ float s_cb[16];
   const uint32_t t = threadIdx.x;
+  const uint32_t kpad = w.cq.groups << w.cq.g_log2;  // the padded row (<= 512)
+  CqRowRegs R;  // the rows' packed words and norms first
+  cq_rows_load(w.cq, BITS, (size_t)k * 64, kpad / 32, t, R);
   if (t == 0) {  // constant indices into the argument block
 #pragma unroll
     for (int i = 0; i < 16; ++i) s_cb[i] = w.cq.cb[i];
   }
-  const uint32_t kpad = (w.k + 31) & ~31u;
   for (uint32_t i = t; i < kpad; i += kMixWg) xs[i + (i >> 5)] = i < w.k ? w.x[i] : 0.f;
   __syncthreads();
-  const float2 v = cq_rows_pair<BITS>(w.cq, (size_t)k * 64, kpad / 32, xs, s_cb, t);
+  const float2 v = cq_rows_dot<BITS>(w.cq, R, kpad / 32, xs, s_cb, t);
   if ((t & 15) == 0) {
     const uint32_t r = k * 64 + (t >> 4);
     __hip_atomic_store(w.y + r, v.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -803,14 +904,15 @@ struct MixArgs {
   uint32_t has_pre, own_pre;
   const int8_t* phi_w[3];  // phi_pre, phi_post, phi_res rows of layer l
   const float* phi_s[3];
-  // The same rows as Cactus-Quant matrices (n2_mix_kernel<true>): packed
-  // rows and binary16 norms of layer l's phi_pre, phi_post and phi_res, the
-  // codebook by code, width, group, bytes per row, norms per row, 1/sqrt(g).
+  // The same rows as Cactus-Quant matrices (n2_mix_kernel<true>): for layer
+  // l's phi_pre, phi_post and phi_res each, its packed rows and binary16
+  // norms, codebook by code, width, group, bytes per row, norms per row and
+  // 1/sqrt(g) (a mixed-width archive gives each matrix its own).
   const uint8_t* cq_p[3];
   const uint16_t* cq_n[3];
-  float cq_cb[16];
-  uint32_t cq_bits, cq_g, cq_row_bytes, cq_groups;
-  double cq_inv_root;
+  float cq_cb[3][16];
+  uint32_t cq_bits[3], cq_g[3], cq_row_bytes[3], cq_groups[3];
+  double cq_inv_root[3];
   float a_pre;
   const float* b_pre;
   uint32_t has_site;  // an engram site injects at layer l
@@ -868,7 +970,6 @@ struct MixArgs {
   // wo_groups workgroups of wo_cq_rows, codes of wo_bits bits.
   WoCq wo_cq;
   uint32_t wo_bits;
-  uint32_t qkv_bits;  // the projection's code width (CQ launches)
 };
 
 // Rows [rpw k, +rpw) of proj = Wo att in the fused Wo + mix launch, rpw =
@@ -1039,6 +1140,60 @@ __device__ float fwht_block(float v, float* hv, uint32_t H, uint32_t t) {
 // it loaded at entry, against xu, the lane's 32 rotated inputs.  Each unit
 // takes fp32 dots over its four 8-code blocks, each block times its group's
 // norm (groups of 8, 16, or 32 and wider) in float64, summed over the wave.
+// Element m (0, 1, 2) of a kernel-argument triple, by selection (a runtime
+// index into the argument block would copy it to scratch).
+template <typename T>
+__device__ __forceinline__ T sel3(uint32_t m, T a, T b, T c) {
+  return m == 0 ? a : (m == 1 ? b : c);
+}
+
+// One Cactus-Quant phi row on a wave: lane u < units holds the row's 32-code
+// unit u (packed words w, the norms n of its groups) and the rotated inputs
+// xu of that unit; each 8 codes are a dot in fp32 (code from the codebook
+// cb in LDS times the input), each group's dots times its binary16 norm in
+// float64.  Returns the lane's share of the row (the caller sums the wave).
+template <uint32_t BITS>
+__device__ __forceinline__ double cq_phi_row(const uint32_t (&w)[4], const uint32_t (&n)[4],
+                                             const float (&xu)[32], const float* cb, uint32_t g,
+                                             uint32_t units, uint32_t lane) {
+  double total = 0.0;
+  if (lane < units) {
+    float dot8[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (uint32_t c = 0; c < 32; ++c) {
+      uint32_t code;
+      if constexpr (BITS == 4) {
+        code = (w[c >> 3] >> (4 * (c & 7))) & 15u;
+      } else if constexpr (BITS == 3) {
+        const uint32_t bit = 3 * c, k = bit >> 5, sh = bit & 31;
+        const uint32_t hi = sh > 29 ? w[k + 1 < 4 ? k + 1 : 3] << (32 - sh) : 0u;
+        code = ((w[k] >> sh) | hi) & 7u;
+      } else {
+        code = (w[c >> 4] >> (2 * (c & 15))) & 3u;
+      }
+      dot8[c >> 3] = fmaf(cb[code], xu[c], dot8[c >> 3]);
+    }
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t nb = g == 8 ? n[b] : (g == 16 ? n[b >> 1] : n[0]);
+      total += (double)nd::cq_half(nb) * (double)dot8[b];
+    }
+  }
+  return total;
+}
+
+// cq_phi_row by the row's code width (2-bit codes and ternary crumbs as 2).
+__device__ __forceinline__ double cq_phi_row_any(uint32_t bits, const uint32_t (&w)[4],
+                                                 const uint32_t (&n)[4], const float (&xu)[32],
+                                                 const float* cb, uint32_t g, uint32_t units,
+                                                 uint32_t lane) {
+  if (bits == 4) return cq_phi_row<4>(w, n, xu, cb, g, units, lane);
+  if (bits == 3) return cq_phi_row<3>(w, n, xu, cb, g, units, lane);
+  return cq_phi_row<2>(w, n, xu, cb, g, units, lane);
+}
+
+// The wave's rows w, w + 8, w + 16 (below nrows) of phi matrices that share
+// one format: code width BITS, group g, the rotation xu and codebook cb.
 template <uint32_t BITS>
 __device__ __forceinline__ void cq_phi_rows(const uint32_t (&w)[3][4], const uint32_t (&n)[3][4],
                                             const float (&xu)[32], const float* cb, uint32_t g,
@@ -1048,32 +1203,49 @@ __device__ __forceinline__ void cq_phi_rows(const uint32_t (&w)[3][4], const uin
   for (int j = 0; j < 3; ++j) {
     const uint32_t r = wave + 8u * j;
     if (r >= nrows) break;  // uniform over the wave
-    double total = 0.0;
-    if (lane < units) {
-      float dot8[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (uint32_t c = 0; c < 32; ++c) {
-        uint32_t code;
-        if constexpr (BITS == 4) {
-          code = (w[j][c >> 3] >> (4 * (c & 7))) & 15u;
-        } else if constexpr (BITS == 3) {
-          const uint32_t bit = 3 * c, k = bit >> 5, sh = bit & 31;
-          const uint32_t hi = sh > 29 ? w[j][k + 1 < 4 ? k + 1 : 3] << (32 - sh) : 0u;
-          code = ((w[j][k] >> sh) | hi) & 7u;
-        } else {
-          code = (w[j][c >> 4] >> (2 * (c & 15))) & 3u;
-        }
-        dot8[c >> 3] = fmaf(cb[code], xu[c], dot8[c >> 3]);
-      }
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const uint32_t nb = g == 8 ? n[j][b] : (g == 16 ? n[j][b >> 1] : n[j][0]);
-        total += (double)nd::cq_half(nb) * (double)dot8[b];
-      }
-    }
-    total = nd::wave_sum(total);
+    const double total = nd::wave_sum(cq_phi_row<BITS>(w[j], n[j], xu, cb, g, units, lane));
     if (lane == 0) phi[r] = (float)total;
   }
+}
+
+// prepareCqActivation of one 32-value unit per lane (backends/cq.ts:30-46):
+// the butterflies of fastWalshHadamard with strides below min(g, 32) inside
+// the unit, strides 32 .. g / 2 across the lanes holding the group's other
+// units (each result one fp32 add or subtract of the reference's two
+// operands), then times 1/sqrt(g) in float64.
+__device__ __forceinline__ void cq_rotate_unit(float (&xu)[32], uint32_t g, double inv_root,
+                                               uint32_t lane) {
+  const uint32_t gs = g < 32 ? g : 32u;
+#pragma unroll
+  for (uint32_t st = 1; st < 32; st <<= 1) {
+    if (st < gs) {
+#pragma unroll
+      for (uint32_t c = 0; c < 32; ++c)
+        if (!(c & st)) {
+          const float x0 = xu[c], x1 = xu[c + st];
+          xu[c] = x0 + x1;
+          xu[c + st] = x0 - x1;
+        }
+    }
+  }
+  auto cross = [&](auto m) {
+    constexpr int M = decltype(m)::value;
+    const bool right = (lane & M) != 0;
+#pragma unroll
+    for (int c = 0; c < 32; ++c) {
+      const float other = nd::lane_xor<M>(xu[c]);
+      xu[c] = right ? other - xu[c] : xu[c] + other;
+    }
+  };
+  const uint32_t lpg = g > 32 ? g >> 5 : 1u;  // lanes of a group
+  if (lpg > 1) cross(std::integral_constant<int, 1>{});
+  if (lpg > 2) cross(std::integral_constant<int, 2>{});
+  if (lpg > 4) cross(std::integral_constant<int, 4>{});
+  if (lpg > 8) cross(std::integral_constant<int, 8>{});
+  if (lpg > 16) cross(std::integral_constant<int, 16>{});
+  if (lpg > 32) cross(std::integral_constant<int, 32>{});
+#pragma unroll
+  for (int c = 0; c < 32; ++c) xu[c] = (float)((double)xu[c] * inv_root);
 }
 
 // phi operand tiling: the (2 + lanes) * lanes phi rows (<= 24) in tiles of
@@ -1101,7 +1273,11 @@ constexpr int kPhiPairs = 8;
 // read at the same k).  D rows 0 and 1 (hi, lo) land in lanes 0..15, outputs
 // 0 and 1; the four waves of a tile meet in LDS and the sum is taken in
 // float64 times the row scale.
-template <bool CQ, bool WO = false>
+//
+// PU (Cactus-Quant): phi_pre, phi_post and phi_res share one format (width,
+// group, codebook), so one rotation and one width dispatch serve every row;
+// otherwise each row takes its own matrix's format.
+template <bool CQ, bool WO = false, bool PU = true>
 __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   static_assert(kQkvWg == kMixWg, "the fused projection runs on mix-sized workgroups");
   if constexpr (WO) {
@@ -1127,16 +1303,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     if (k > a.wo_groups) {
       const uint32_t qb = k - a.wo_groups - 1;
       if (qb < a.qkv_groups) {
-        if constexpr (CQ) {
-          if (a.qkv_bits == 4)
-            qkv_body<4, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups, a.status, a.spin);
-          else if (a.qkv_bits == 3)
-            qkv_body<3, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups, a.status, a.spin);
-          else
-            qkv_body<2, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups, a.status, a.spin);
-        } else {
-          qkv_body<0, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups, a.status, a.spin);
-        }
+        qkv_body<CQ, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups, a.status, a.spin);
       }
       return;
     }
@@ -1219,31 +1386,38 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     spre = s0[min(lane, L - 1)];
   }
   const float bpre = a.b_pre[min(lane, L - 1)];
-  __shared__ float s_cb[16];
-  // Cactus-Quant phi rows: wave w takes rows w, w + 8 and w + 16, lane u the
-  // rows' 32-code unit u -- its packed words (UB / 4 of them) and the norms
-  // of its groups -- loaded here with the other operands.
+  __shared__ float s_cb[3][16];
+  // Cactus-Quant phi rows: wave w takes rows w, w + 8 and w + 16 (rows of
+  // phi_pre, phi_post, phi_res in that order; rows w + 8 and w + 16 are
+  // always phi_res), lane u the rows' 32-code unit u -- its packed words
+  // (bits of them) and the norms of its groups -- loaded here with the
+  // other operands, each row in its own matrix's format.
   uint32_t cw[3][4] = {}, cn[3][4] = {};
   if constexpr (CQ) {
     if (t == 0) {  // constant indices into the argument block
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s_cb[i] = a.cq_cb[i];
+      for (int m = 0; m < (PU ? 1 : 3); ++m)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s_cb[m][i] = a.cq_cb[m][i];
     }
-    const uint32_t ubw = a.cq_bits == 4 ? 4u : (a.cq_bits == 3 ? 3u : 2u);  // words per unit
-    const uint32_t gpu = a.cq_g >= 32 ? 1u : 32u / a.cq_g;               // groups per unit
     const uint32_t ul = min(lane, N / 32 - 1);
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
       const uint32_t r = min(wave + 8u * j, nrows - 1);
       const uint32_t mat = r < L ? 0u : (r < 2 * L ? 1u : 2u);
       const uint32_t rr = r - (mat == 0 ? 0u : (mat == 1 ? L : 2 * L));
-      // The matrix by selection (a runtime index into the argument block
-      // would copy it to scratch).
-      const uint8_t* pm = mat == 0 ? a.cq_p[0] : (mat == 1 ? a.cq_p[1] : a.cq_p[2]);
-      const uint16_t* nm = mat == 0 ? a.cq_n[0] : (mat == 1 ? a.cq_n[1] : a.cq_n[2]);
-      const uint32_t* prow =
-          reinterpret_cast<const uint32_t*>(pm + (size_t)rr * a.cq_row_bytes) + ul * ubw;
-      const uint16_t* nrow = nm + (size_t)rr * a.cq_groups + (ul * 32) / a.cq_g;
+      const uint8_t* pm = sel3(mat, a.cq_p[0], a.cq_p[1], a.cq_p[2]);
+      const uint16_t* nm = sel3(mat, a.cq_n[0], a.cq_n[1], a.cq_n[2]);
+      const uint32_t bits = PU ? a.cq_bits[0] : sel3(mat, a.cq_bits[0], a.cq_bits[1], a.cq_bits[2]);
+      const uint32_t g = PU ? a.cq_g[0] : sel3(mat, a.cq_g[0], a.cq_g[1], a.cq_g[2]);
+      const uint32_t rb = PU ? a.cq_row_bytes[0]
+                             : sel3(mat, a.cq_row_bytes[0], a.cq_row_bytes[1], a.cq_row_bytes[2]);
+      const uint32_t ng = PU ? a.cq_groups[0]
+                             : sel3(mat, a.cq_groups[0], a.cq_groups[1], a.cq_groups[2]);
+      const uint32_t ubw = bits == 4 ? 4u : (bits == 3 ? 3u : 2u);  // words per unit
+      const uint32_t gpu = g >= 32 ? 1u : 32u / g;                  // groups per unit
+      const uint32_t* prow = reinterpret_cast<const uint32_t*>(pm + (size_t)rr * rb) + ul * ubw;
+      const uint16_t* nrow = nm + (size_t)rr * ng + (ul * 32) / g;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         if ((uint32_t)k < ubw) cw[j][k] = prow[k];
@@ -1365,7 +1539,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     // phi = cqMatvec of the normalized lanes (backends/cq.ts:30-46, 107-231):
     // prepareCqActivation -- per group the butterflies (strides 1 .. g / 2,
     // one fp32 add and subtract per pair), then times 1/sqrt(g) -- and the
-    // rows by code width (cq_phi_rows).  The N <= 2048 normalized values are
+    // rows by code width (cq_phi_row_any).  The N <= 2048 normalized values are
     // 64 units of 32, one per lane of a wave: each wave reads them from LDS
     // (one pad float after every 32, so lane u's unit starts at 33 u and a
     // wave's reads fall in distinct banks) and rotates its own copy in
@@ -1381,46 +1555,49 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     }
     nd::lds_barrier();
     const uint32_t units = N / 32, uc = lane < units ? lane : 0;
-    float xu[32];
+    if constexpr (PU) {
+      float xu[32];
 #pragma unroll
-    for (int c = 0; c < 32; ++c) xu[c] = s_cqx[uc * 33 + c];
-    const uint32_t gs = a.cq_g < 32 ? a.cq_g : 32u;
+      for (int c = 0; c < 32; ++c) xu[c] = s_cqx[uc * 33 + c];
+      cq_rotate_unit(xu, a.cq_g[0], a.cq_inv_root[0], lane);
+      if (a.cq_bits[0] == 4)
+        cq_phi_rows<4>(cw, cn, xu, s_cb[0], a.cq_g[0], units, nrows, wave, lane, phi);
+      else if (a.cq_bits[0] == 3)
+        cq_phi_rows<3>(cw, cn, xu, s_cb[0], a.cq_g[0], units, nrows, wave, lane, phi);
+      else  // 2-bit codes and ternary crumbs
+        cq_phi_rows<2>(cw, cn, xu, s_cb[0], a.cq_g[0], units, nrows, wave, lane, phi);
+    } else {
+    // Rows j = 0 take the rotation by their own matrix's group, rows j >= 1
+    // (phi_res) by phi_res's; one rotation serves both when the groups agree.
+    const uint32_t r0 = wave, mat0 = r0 < L ? 0u : (r0 < 2 * L ? 1u : 2u);
+    const uint32_t g0 = sel3(mat0, a.cq_g[0], a.cq_g[1], a.cq_g[2]), gr = a.cq_g[2];
+    const bool same = g0 == gr;
+    float xa[32], xb[32];
 #pragma unroll
-    for (uint32_t st = 1; st < 32; st <<= 1) {
-      if (st < gs) {
+    for (int c = 0; c < 32; ++c) xa[c] = s_cqx[uc * 33 + c];
+    cq_rotate_unit(xa, g0, sel3(mat0, a.cq_inv_root[0], a.cq_inv_root[1], a.cq_inv_root[2]),
+                   lane);
+    if (!same) {
 #pragma unroll
-        for (uint32_t c = 0; c < 32; ++c)
-          if (!(c & st)) {
-            const float x0 = xu[c], x1 = xu[c + st];
-            xu[c] = x0 + x1;
-            xu[c + st] = x0 - x1;
-          }
-      }
+      for (int c = 0; c < 32; ++c) xb[c] = s_cqx[uc * 33 + c];
+      cq_rotate_unit(xb, gr, a.cq_inv_root[2], lane);
     }
-    auto cross = [&](auto m) {
-      constexpr int M = decltype(m)::value;
-      const bool right = (lane & M) != 0;
 #pragma unroll
-      for (int c = 0; c < 32; ++c) {
-        const float other = nd::lane_xor<M>(xu[c]);
-        xu[c] = right ? other - xu[c] : xu[c] + other;
-      }
-    };
-    const uint32_t lpg = a.cq_g > 32 ? a.cq_g >> 5 : 1u;  // lanes of a group
-    if (lpg > 1) cross(std::integral_constant<int, 1>{});
-    if (lpg > 2) cross(std::integral_constant<int, 2>{});
-    if (lpg > 4) cross(std::integral_constant<int, 4>{});
-    if (lpg > 8) cross(std::integral_constant<int, 8>{});
-    if (lpg > 16) cross(std::integral_constant<int, 16>{});
-    if (lpg > 32) cross(std::integral_constant<int, 32>{});
-#pragma unroll
-    for (int c = 0; c < 32; ++c) xu[c] = (float)((double)xu[c] * a.cq_inv_root);
-    if (a.cq_bits == 4)
-      cq_phi_rows<4>(cw, cn, xu, s_cb, a.cq_g, units, nrows, wave, lane, phi);
-    else if (a.cq_bits == 3)
-      cq_phi_rows<3>(cw, cn, xu, s_cb, a.cq_g, units, nrows, wave, lane, phi);
-    else  // 2-bit codes and ternary crumbs
-      cq_phi_rows<2>(cw, cn, xu, s_cb, a.cq_g, units, nrows, wave, lane, phi);
+    for (int j = 0; j < 3; ++j) {
+      const uint32_t r = wave + 8u * j;
+      if (r >= nrows) break;  // uniform over the wave
+      const uint32_t mat = r < L ? 0u : (r < 2 * L ? 1u : 2u);
+      const uint32_t bits = sel3(mat, a.cq_bits[0], a.cq_bits[1], a.cq_bits[2]);
+      const uint32_t g = sel3(mat, a.cq_g[0], a.cq_g[1], a.cq_g[2]);
+      double total;
+      if (j == 0 || same)
+        total = cq_phi_row_any(bits, cw[j], cn[j], xa, s_cb[mat], g, units, lane);
+      else
+        total = cq_phi_row_any(bits, cw[j], cn[j], xb, s_cb[mat], g, units, lane);
+      total = nd::wave_sum(total);
+      if (lane == 0) phi[r] = (float)total;
+    }
+    }
     nd::lds_barrier();
     if (t < nrows) {
       const float v = phi[t];
@@ -1897,8 +2074,20 @@ enum StageSlot : uint32_t {
 struct nd_needle {
   nd_needle_desc d{};
   bool cq = false;  // every matrix in the Cactus-Quant form (else int8)
-  std::vector<nd_mat> wqkvg;  // owned: rows q | k | v | gate of each layer
-  std::vector<nd_mat> ekv;    // owned: rows key | value of each engram site
+  // Owned: rows q | k | v | gate of each layer and key | value of each
+  // engram site, concatenated when the parts share one format (int8, or
+  // Cactus-Quant of one width, group and padding); otherwise (a mixed-width
+  // archive) the entry keeps only its row count and the parts are owned
+  // copies in `owned_parts`.
+  std::vector<nd_mat> wqkvg;
+  std::vector<nd_mat> ekv;
+  // Cactus-Quant models: each part as a matrix of its own (views into the
+  // concatenation, or the owned copies).
+  std::vector<std::array<nd_mat, 4>> qkv_part;
+  std::vector<std::array<nd_mat, 2>> ekv_part;
+  std::vector<nd_mat> owned_parts;
+  bool wo_fused = true;  // every layer's Wo fits the fused launch's rows
+  bool phi_uniform = true;  // phi_pre, phi_post, phi_res share one format
   std::vector<const nd_mat*> wo, eg_tables;
   const nd_mat *embedding = nullptr, *phi_pre = nullptr, *phi_post = nullptr, *phi_res = nullptr;
   float* params = nullptr;  // dense vectors, offsets below (floats)
@@ -2023,12 +2212,14 @@ void set_phi(const nd_needle* n, uint32_t ql, MixArgs& m) {
       m.cq_p[i] = pm[i]->packed + first[i] * pm[i]->row_bytes;
       m.cq_n[i] = pm[i]->norms + first[i] * (pm[i]->kpad / pm[i]->g);
     }
-    for (int i = 0; i < 16; ++i) m.cq_cb[i] = n->phi_pre->cb[i];
-    m.cq_bits = n->phi_pre->bits;
-    m.cq_g = n->phi_pre->g;
-    m.cq_row_bytes = n->phi_pre->row_bytes;
-    m.cq_groups = n->phi_pre->kpad / n->phi_pre->g;
-    m.cq_inv_root = 1.0 / std::sqrt((double)n->phi_pre->g);
+    for (int i = 0; i < 3; ++i) {
+      for (int c = 0; c < 16; ++c) m.cq_cb[i][c] = pm[i]->cb[c];
+      m.cq_bits[i] = pm[i]->bits;
+      m.cq_g[i] = pm[i]->g;
+      m.cq_row_bytes[i] = pm[i]->row_bytes;
+      m.cq_groups[i] = pm[i]->kpad / pm[i]->g;
+      m.cq_inv_root[i] = 1.0 / std::sqrt((double)pm[i]->g);
+    }
   } else {
     m.phi_w[0] = n->phi_pre->w + (size_t)ql * ln * K;
     m.phi_s[0] = n->phi_pre->scales + (size_t)ql * ln;
@@ -2122,12 +2313,18 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, 
       m.qkv = qkv_params(n, l);
       m.qkv_groups = n->wqkvg[l].n / kHd + 1;
       m.qkv_flag = n->qkv_flags + 32 * (size_t)l;
-      m.qkv_bits = n->wqkvg[l].bits;
     }
-    hipLaunchKernelGGL((n2_mix_kernel<true, true>), dim3(8 * (m.wo_groups + 1 + m.qkv_groups)),
-                       dim3(kMixWg), 0, s, m);
+    if (n->phi_uniform)
+      hipLaunchKernelGGL((n2_mix_kernel<true, true, true>),
+                         dim3(8 * (m.wo_groups + 1 + m.qkv_groups)), dim3(kMixWg), 0, s, m);
+    else
+      hipLaunchKernelGGL((n2_mix_kernel<true, true, false>),
+                         dim3(8 * (m.wo_groups + 1 + m.qkv_groups)), dim3(kMixWg), 0, s, m);
   } else if (n->cq) {
-    hipLaunchKernelGGL(n2_mix_kernel<true>, dim3(1), dim3(kMixWg), 0, s, m);
+    if (n->phi_uniform)
+      hipLaunchKernelGGL((n2_mix_kernel<true, false, true>), dim3(1), dim3(kMixWg), 0, s, m);
+    else
+      hipLaunchKernelGGL((n2_mix_kernel<true, false, false>), dim3(1), dim3(kMixWg), 0, s, m);
   } else if (wo) {
     // One launch on one XCD: layer l - 1's Wo (with the post half), the mix,
     // layer l's projection (with the pre half, when qkv).
@@ -2185,7 +2382,7 @@ CqRows cq_rows_of(const nd_mat& wm) {
 }
 
 // A Cactus-Quant Wo that wo_cq_rows takes (both launches of it use it).
-bool wo_cq_fits(const nd_mat& w) { return w.bits && w.k <= 512 && w.n % 64 == 0; }
+bool wo_cq_fits(const nd_mat& w) { return w.bits && w.kpad <= 512 && w.n % 64 == 0; }
 
 WoCq wo_cq_of(const nd_needle* n, const nd_mat& w) {
   WoCq c{};
@@ -2233,7 +2430,11 @@ QkvParams qkv_params(const nd_needle* n, uint32_t l) {
   ra.lanes = ln;
   ra.own = l % ln;
   ra.route = n->route;
-  if (n->cq) p.cq = cq_rows_of(wm);
+  if (n->cq)
+    for (int i = 0; i < 4; ++i) {
+      p.cq[i] = cq_rows_of(n->qkv_part[l][i]);
+      p.cq_bits[i] = n->qkv_part[l][i].bits;
+    }
   return p;
 }
 
@@ -2244,10 +2445,7 @@ hipError_t enqueue_block(nd_needle* n, uint32_t l, hipStream_t s, bool with_wo =
   const nd_needle_desc& d = n->d;
   const nd_mat& wm = n->wqkvg[l];
   if (with_qkv) {
-    auto kern = &n2_qkv_kernel<0>;
-    if (n->cq)
-      kern = wm.bits == 4 ? &n2_qkv_kernel<4>
-                          : (wm.bits == 3 ? &n2_qkv_kernel<3> : &n2_qkv_kernel<2>);
+    auto kern = n->cq ? &n2_qkv_kernel<true> : &n2_qkv_kernel<false>;
     hipLaunchKernelGGL(kern, dim3(wm.n / kHd + 1), dim3(kQkvWg), 0, s, qkv_params(n, l));
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -2324,28 +2522,27 @@ hipError_t enqueue_cq_rows(nd_needle* n, const uint32_t* token, const uint32_t* 
                            hipStream_t s, uint32_t batch = 0) {
   const nd_needle_desc& d = n->d;
   CqRowsArgs a{};
-  const nd_mat* e = n->embedding;
-  a.emb_p = e->packed;
-  a.emb_n = e->norms;
-  a.emb_kpad = e->kpad;
-  a.emb_row_bytes = e->row_bytes;
-  a.g = e->g;
-  a.bits = e->bits;
-  a.inverse_root = 1.0 / std::sqrt((double)e->g);
-  for (int i = 0; i < 16; ++i) a.cb[i] = e->cb[i];
-  if (e->bits == nd::kCqTernaryBits) {  // dequantizeCqRow's table: c = f32(1.2240064 * 1/sqrt(g))
-    const float c = (float)(1.2240064 * a.inverse_root);
-    a.cb[0] = 0.f;
-    a.cb[1] = c;
-    a.cb[2] = 0.f;
-    a.cb[3] = -c;
-  }
-  for (uint32_t si = 0; si < d.n_sites; ++si) {
-    a.tab_p[si] = n->eg_tables[si]->packed;
-    a.tab_n[si] = n->eg_tables[si]->norms;
-    a.tab_kpad = n->eg_tables[si]->kpad;
-    a.tab_row_bytes = n->eg_tables[si]->row_bytes;
-  }
+  auto source = [](const nd_mat* m) {
+    CqSource c{};
+    c.p = m->packed;
+    c.n = m->norms;
+    c.kpad = m->kpad;
+    c.row_bytes = m->row_bytes;
+    c.g = m->g;
+    c.bits = m->bits;
+    c.inverse_root = 1.0 / std::sqrt((double)m->g);
+    for (int i = 0; i < 16; ++i) c.cb[i] = m->cb[i];
+    if (m->bits == nd::kCqTernaryBits) {  // dequantizeCqRow's table: c = f32(1.2240064 * 1/sqrt(g))
+      const float v = (float)(1.2240064 * c.inverse_root);
+      c.cb[0] = 0.f;
+      c.cb[1] = v;
+      c.cb[2] = 0.f;
+      c.cb[3] = -v;
+    }
+    return c;
+  };
+  a.emb = source(n->embedding);
+  for (uint32_t si = 0; si < d.n_sites; ++si) a.tab[si] = source(n->eg_tables[si]);
   a.token = token;
   a.lookup = lookup;
   a.d = d.dim;
@@ -2380,8 +2577,16 @@ hipError_t enqueue_engrams(nd_needle* n, hipStream_t s) {
   const nd_needle_desc& d = n->d;
   const uint32_t D = d.dim, cat = d.engram_tables * d.engram_sub;
   for (uint32_t si = 0; si < d.n_sites; ++si) {
-    const hipError_t e =
-        mv_any(&n->ekv[si], n->cat + (size_t)si * cat, 0, 2 * D, n->ekv_out + (size_t)si * 2 * D, s);
+    const float* x = n->cat + (size_t)si * cat;
+    float* y = n->ekv_out + (size_t)si * 2 * D;
+    const nd_mat& kv = n->ekv[si];
+    hipError_t e;
+    if (!kv.bits || kv.packed) {
+      e = mv_any(&kv, x, 0, 2 * D, y, s);
+    } else {  // key and value of different formats
+      e = mv_any(&n->ekv_part[si][0], x, 0, D, y, s);
+      if (e == hipSuccess) e = mv_any(&n->ekv_part[si][1], x, 0, D, y + D, s);
+    }
     if (e != hipSuccess) return e;
   }
   if (!d.n_sites) return hipSuccess;
@@ -2422,7 +2627,7 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
     // The fused launch keeps its workgroups on one XCD (workgroups L % 8 ==
     // 0 only): without the confirmed placement the launches stay separate.
     const bool fuse = nd_xcd_local() &&
-                      (n->cq ? wo_cq_fits(*n->wo[0])
+                      (n->cq ? n->wo_fused
                              : (wo_tpr & (wo_tpr - 1)) == 0 && wo_tpr <= (uint32_t)kMixWg);
     if ((e = enqueue_mix(n, l, parts, s, fuse, fuse)) != hipSuccess) return e;
     if (!pre) break;
@@ -2584,10 +2789,25 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
     if (r != hipSuccess) return r;
     return nd_launch_gemm(w, n->pf_digits, n->pf_fm, y, y_ld, M, 0, s);
   };
+  // Rows of parts concatenated when they share a format, else part by part
+  // into their columns of y.
+  auto parts_product = [&](const nd_mat& whole, const nd_mat* parts, size_t count,
+                           const float* x, uint32_t x_ld, uint32_t k, float* y,
+                           uint32_t y_ld) -> hipError_t {
+    if (!whole.bits || whole.packed) return product(&whole, x, x_ld, k, y, y_ld);
+    uint32_t col = 0;
+    for (size_t i = 0; i < count; ++i) {
+      const hipError_t r = product(&parts[i], x, x_ld, k, y + col, y_ld);
+      if (r != hipSuccess) return r;
+      col += parts[i].n;
+    }
+    return hipSuccess;
+  };
   if (d.n_sites) {
     for (uint32_t si = 0; si < d.n_sites; ++si)
-      if ((e = product(&n->ekv[si], n->pf_cat + (size_t)si * cat, S * cat, cat,
-                       n->pf_ekv + (size_t)si * 2 * D, S * 2 * D)) != hipSuccess)
+      if ((e = parts_product(n->ekv[si], n->cq ? n->ekv_part[si].data() : nullptr, 2,
+                             n->pf_cat + (size_t)si * cat, S * cat, cat,
+                             n->pf_ekv + (size_t)si * 2 * D, S * 2 * D)) != hipSuccess)
         return e;
     const uint32_t threads = (D + 63) / 64 * 64;
     hipLaunchKernelGGL(n2_conv_batch_kernel, dim3(M, d.n_sites), dim3(threads), 0, s, n->pf_ekv,
@@ -2652,13 +2872,15 @@ hipError_t enqueue_prefill(nd_needle* n, uint32_t count, bool want_logits, bool 
       m.r_b_post = n->params + n->o_bpost + (size_t)l * ln;
       m.r_b_res = n->params + n->o_bres + (size_t)l * ln * ln;
     }
-    if (n->cq)
-      hipLaunchKernelGGL(n2_mix_kernel<true>, dim3(rows), dim3(kMixWg), 0, s, m);
-    else
-      hipLaunchKernelGGL(n2_mix_kernel<false>, dim3(rows), dim3(kMixWg), 0, s, m);
+    auto mix = !n->cq ? &n2_mix_kernel<false>
+               : n->phi_uniform ? &n2_mix_kernel<true, false, true>
+                                : &n2_mix_kernel<true, false, false>;
+    hipLaunchKernelGGL(mix, dim3(rows), dim3(kMixWg), 0, s, m);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (!pre) break;
-    if ((e = product(&n->wqkvg[l], n->pf_ain, D, D, n->pf_qkvg, qkv_ld)) != hipSuccess) return e;
+    if ((e = parts_product(n->wqkvg[l], n->cq ? n->qkv_part[l].data() : nullptr, 4, n->pf_ain, D,
+                           D, n->pf_qkvg, qkv_ld)) != hipSuccess)
+      return e;
     hipLaunchKernelGGL(n2_rope_store_batch_kernel, dim3(d.heads + 2 * d.kv_heads, M), dim3(64), 0,
                        s, n->pf_qkvg, qkv_ld, d.heads, d.kv_heads,
                        n->params + n->o_qn + (size_t)l * kHd, n->params + n->o_kn + (size_t)l * kHd,
@@ -2810,16 +3032,24 @@ nd_status nd_needle_create(nd_ctx* ctx, const nd_needle_desc* d, nd_needle** out
     return nd_fail(ctx, ND_ERR_INVALID,
                    "engram tables x sub must be a power of two in [128, 8192]");
   // Every matrix in one form: per-row-scaled int8, or (the shipped archive,
-  // model/cact.ts:398-562) Cactus-Quant with groups of at most 2048 (rotated
-  // inside the matvec), all of one width and group size.
+  // model/cact.ts:398-562) Cactus-Quant, each matrix with its own width and
+  // group as the archive's records carry them (a mixed-bit archive,
+  // cact.ts:346-361), groups of at most 2048 (rotated inside the matvec).
+  // Rows padded to a multiple of the group must fit the kernel that
+  // consumes them: max_kpad codes (q, k, v, gate: 512, one row on 16 lanes
+  // of 32 codes; embedding and engram tables: kCqRowMax, a row in LDS; the
+  // phi matrices: exactly lanes x dim, the mix's units).
   const bool cq = d->embedding && d->embedding->bits != 0;
-  auto check = [&](const nd_mat* m, uint32_t n, uint32_t k, const char* what) -> nd_status {
+  auto check = [&](const nd_mat* m, uint32_t n, uint32_t k, const char* what,
+                   uint32_t max_kpad = kCqMaxKpad) -> nd_status {
     if (cq) {
-      if (!m || !m->bits || m->n != n || m->k != k || m->g > 2048 ||
-          m->bits != d->embedding->bits || m->g != d->embedding->g)
+      if (!m || !m->bits || m->n != n || m->k != k || m->g > 2048)
         return nd_fail(ctx, ND_ERR_INVALID,
-                       "%s must be a %ux%u Cactus-Quant matrix of the embedding's width and group "
-                       "(group <= 2048)", what, n, k);
+                       "%s must be a %ux%u Cactus-Quant matrix (group <= 2048)", what, n, k);
+      if (m->kpad > max_kpad)
+        return nd_fail(ctx, ND_ERR_UNSUPPORTED,
+                       "%s rows padded to %u codes (group %u); this runtime takes at most %u", what,
+                       m->kpad, m->g, max_kpad);
       return ND_OK;
     }
     if (!m || m->bits || m->n != n || m->k != k || m->g != k)
@@ -2828,10 +3058,10 @@ nd_status nd_needle_create(nd_ctx* ctx, const nd_needle_desc* d, nd_needle** out
     return ND_OK;
   };
   nd_status st;
-  if ((st = check(d->embedding, d->vocab, D, "embedding")) ||
-      (st = check(d->phi_pre, L * ln, ln * D, "phi_pre")) ||
-      (st = check(d->phi_post, L * ln, ln * D, "phi_post")) ||
-      (st = check(d->phi_res, L * ln * ln, ln * D, "phi_res")))
+  if ((st = check(d->embedding, d->vocab, D, "embedding", kCqRowMax)) ||
+      (st = check(d->phi_pre, L * ln, ln * D, "phi_pre", ln * D)) ||
+      (st = check(d->phi_post, L * ln, ln * D, "phi_post", ln * D)) ||
+      (st = check(d->phi_res, L * ln * ln, ln * D, "phi_res", ln * D)))
     return st;
   if (!d->wq || !d->wk || !d->wv || !d->wgate || !d->wo)
     return nd_fail(ctx, ND_ERR_INVALID, "layer matrix arrays must not be NULL");
@@ -2841,17 +3071,15 @@ nd_status nd_needle_create(nd_ctx* ctx, const nd_needle_desc* d, nd_needle** out
                    "confidence head needs 1..%u probes, at least one output, a projection and a "
                    "bias", kMaxProbes);
   for (uint32_t l = 0; l < L; ++l)
-    if ((st = check(d->wq[l], qw, D, "wq")) || (st = check(d->wk[l], kw, D, "wk")) ||
-        (st = check(d->wv[l], kw, D, "wv")) || (st = check(d->wgate[l], qw, D, "wgate")) ||
+    if ((st = check(d->wq[l], qw, D, "wq", 512)) || (st = check(d->wk[l], kw, D, "wk", 512)) ||
+        (st = check(d->wv[l], kw, D, "wv", 512)) || (st = check(d->wgate[l], qw, D, "wgate", 512)) ||
         (st = check(d->wo[l], D, qw, "wo")))
       return st;
   if (d->n_sites && (!d->eg_tables || !d->eg_key || !d->eg_value || !d->eg_taps))
     return nd_fail(ctx, ND_ERR_INVALID, "engram arrays must not be NULL");
-  if (cq && d->n_sites && (d->engram_sub + 31) / 32 * 32 > kCqRowMax)
-    return nd_fail(ctx, ND_ERR_INVALID, "Cactus-Quant engram rows wider than %u", kCqRowMax);
   for (uint32_t s = 0; s < d->n_sites; ++s)
     if ((st = check(d->eg_tables[s], d->engram_tables * d->engram_slots, d->engram_sub,
-                    "engram tables")) ||
+                    "engram tables", kCqRowMax)) ||
         (st = check(d->eg_key[s], D, cat, "engram key")) ||
         (st = check(d->eg_value[s], D, cat, "engram value")))
       return st;
@@ -2912,16 +3140,55 @@ nd_status nd_needle_create(nd_ctx* ctx, const nd_needle_desc* d, nd_needle** out
       row += p->n;
     }
   };
+  // Parts of one format are concatenated; a Cactus-Quant model also keeps
+  // every part as a matrix of its own (a view into the concatenation, or an
+  // owned copy when the parts' formats differ).
+  auto same_form = [](const nd_mat* a, const nd_mat* b) {
+    return a->bits == b->bits && a->g == b->g && a->kpad == b->kpad &&
+           a->row_bytes == b->row_bytes && std::memcmp(a->cb, b->cb, sizeof a->cb) == 0;
+  };
+  auto split = [&](nd_mat& whole, const nd_mat* const* parts, size_t count, nd_mat* out) {
+    bool uniform = true;
+    for (size_t i = 1; i < count; ++i) uniform = uniform && same_form(parts[0], parts[i]);
+    if (!cq || uniform) {
+      concat(whole, parts, count);
+      if (!cq) return;
+      size_t row = 0;
+      for (size_t i = 0; i < count; ++i) {
+        nd_mat v = whole;
+        v.n = parts[i]->n;
+        v.packed = whole.packed ? whole.packed + row * whole.row_bytes : nullptr;
+        v.norms = whole.norms ? whole.norms + row * (whole.kpad / whole.g) : nullptr;
+        out[i] = v;
+        row += parts[i]->n;
+      }
+      return;
+    }
+    whole.n = 0;
+    whole.k = parts[0]->k;
+    whole.bits = parts[0]->bits;  // Cactus-Quant, no concatenation (packed stays null)
+    for (size_t i = 0; i < count; ++i) {
+      whole.n += parts[i]->n;
+      nd_mat c;
+      concat(c, &parts[i], 1);
+      n->owned_parts.push_back(c);
+      out[i] = c;
+    }
+  };
+  n->phi_uniform = !cq || (same_form(d->phi_pre, d->phi_post) && same_form(d->phi_pre, d->phi_res));
   n->wqkvg.resize(L);
+  n->qkv_part.resize(L);
   for (uint32_t l = 0; l < L; ++l) {
     const nd_mat* parts[4] = {d->wq[l], d->wk[l], d->wv[l], d->wgate[l]};
-    concat(n->wqkvg[l], parts, 4);
+    split(n->wqkvg[l], parts, 4, n->qkv_part[l].data());
     n->wo.push_back(d->wo[l]);
+    n->wo_fused = n->wo_fused && (!cq || wo_cq_fits(*d->wo[l]));
   }
   n->ekv.resize(d->n_sites);
+  n->ekv_part.resize(d->n_sites);
   for (uint32_t s = 0; s < d->n_sites; ++s) {
     const nd_mat* parts[2] = {d->eg_key[s], d->eg_value[s]};
-    concat(n->ekv[s], parts, 2);
+    split(n->ekv[s], parts, 2, n->ekv_part[s].data());
     n->eg_tables.push_back(d->eg_tables[s]);
   }
   std::vector<float> h;
@@ -2986,7 +3253,7 @@ nd_status nd_needle_free(nd_ctx* ctx, nd_needle* n) {
   drop_graphs(n);
   if (n->arena) hipFree(n->arena);
   if (n->pf_arena) hipFree(n->pf_arena);
-  for (auto* v : {&n->wqkvg, &n->ekv})
+  for (auto* v : {&n->wqkvg, &n->ekv, &n->owned_parts})
     for (auto& m : *v) {
       if (m.w) hipFree(m.w);
       if (m.scales) hipFree(m.scales);

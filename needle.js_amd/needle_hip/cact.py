@@ -469,11 +469,41 @@ def parse_cact_weights(source) -> CactWeights:
                        final_norm, heads, blob)
 
 
+_MIXED_WIDTHS = (4, 3, 2, 5)
+
+
+def mixed_form(role: str, index: int = 0) -> tuple:
+    """(bits, group) of one matrix of the mixed-width Needle 2 used in tests
+    and the benchmark: the shipped archive is "mixed CQ2/CQ3/CQ4/ternary"
+    (packages/needle.js/README.md:21) with every record carrying its own
+    width and group (cact.ts:346-361).  Across layers every width (ternary
+    as 5) meets every kind of matrix; a layer's q, k, v and gate share their
+    group and Wo has groups of 128, as the reference's resident path expects
+    of the archive (resident/compatibility.ts:19-36).  `index` is the layer
+    (the engram site for the engram matrices)."""
+    w = _MIXED_WIDTHS
+    part = {"wq": 0, "wk": 1, "wv": 2, "wgate": 3}
+    if role in part:
+        return w[(index + part[role]) % 4], (32, 64)[index % 2]
+    return {
+        "embedding": (4, 32),
+        "wo": (w[(index + 2) % 4], 128),
+        "phi_pre": (2, 64),
+        "phi_post": (5, 32),
+        "phi_res": (3, 128),
+        "eg_tables": ((3, 64), (5, 64))[index % 2],
+        "eg_key": (2, 32),
+        "eg_value": (4, 64),
+    }[role]
+
+
 def synthetic_needle2_archive(geometry: dict, run_seed: int = 2026, bits: int = 4,
-                              group: int = 32, confidence: bool = True) -> bytes:
+                              group: int = 32, confidence: bool = True,
+                              mixed: bool = False) -> bytes:
     """A .cact archive in the Needle 2 tensor order (cact.ts:410-540) with
-    seeded Cactus-Quant matrices of one width, dense vectors near neutral,
-    an optional confidence head and a placeholder tokenizer blob."""
+    seeded Cactus-Quant matrices of one width and group (mixed: each matrix
+    in its mixed_form), dense vectors near neutral, an optional confidence
+    head and a placeholder tokenizer blob."""
     from . import synth
 
     g = geometry
@@ -484,26 +514,27 @@ def synthetic_needle2_archive(geometry: dict, run_seed: int = 2026, bits: int = 
     tensors: list = []
     count = [0]
 
-    def cqm(n, k):
+    def cqm(n, k, role="", index=0):
         count[0] += 1
-        packed, norms = synth.cq_matrix(run_seed, f"arch{count[0]}", n, k, group, bits)
-        tensors.append(CqMatrix(packed, norms, books, n, k, group, bits))
+        b, gr = mixed_form(role, index) if mixed else (bits, group)
+        packed, norms = synth.cq_matrix(run_seed, f"arch{count[0]}", n, k, gr, b)
+        tensors.append(CqMatrix(packed, norms, books, n, k, gr, b))
 
     def vec(shape, lo, hi):
         count[0] += 1
         data = synth.Stream(run_seed, f"arch{count[0]}").uniform(shape, lo, hi).reshape(-1)
         tensors.append(DenseTensor(tuple(shape), data.astype(np.float32)))
 
-    cqm(g["vocabulary_size"], d)
-    for _ in range(L):
+    cqm(g["vocabulary_size"], d, "embedding")
+    for layer in range(L):
         vec((d,), -0.1, 0.1)
-        cqm(H * hd, d)
-        cqm(Hkv * hd, d)
-        cqm(Hkv * hd, d)
+        cqm(H * hd, d, "wq", layer)
+        cqm(Hkv * hd, d, "wk", layer)
+        cqm(Hkv * hd, d, "wv", layer)
         vec((hd,), -0.1, 0.1)
         vec((hd,), -0.1, 0.1)
-        cqm(H * hd, d)
-        cqm(d, H * hd)
+        cqm(H * hd, d, "wgate", layer)
+        cqm(d, H * hd, "wo", layer)
         vec((d,), -0.1, 0.1)
         vec((1,), -1.0, 1.0)
         vec((d,), -0.1, 0.1)
@@ -512,14 +543,15 @@ def synthetic_needle2_archive(geometry: dict, run_seed: int = 2026, bits: int = 
         vec((d,), 0.5, 1.5)
     for shape in ((L,), (L,), (L,), (L * ln,), (L * ln,), (L * ln * ln,)):
         vec(shape, 0.02, 0.1)
-    cqm(L * ln, ln * d)
-    cqm(L * ln, ln * d)
-    cqm(L * ln * ln, ln * d)
+    cqm(L * ln, ln * d, "phi_pre")
+    cqm(L * ln, ln * d, "phi_post")
+    cqm(L * ln * ln, ln * d, "phi_res")
     cat = g["number_of_engram_tables"] * g["engram_sub_dimension"]
-    for _ in g.get("engram_layers", []):
-        cqm(g["number_of_engram_tables"] * g["engram_slots"], g["engram_sub_dimension"])
-        cqm(d, cat)
-        cqm(d, cat)
+    for site, _ in enumerate(g.get("engram_layers", [])):
+        cqm(g["number_of_engram_tables"] * g["engram_slots"], g["engram_sub_dimension"],
+            "eg_tables", site)
+        cqm(d, cat, "eg_key", site)
+        cqm(d, cat, "eg_value", site)
         vec((g["engram_convolution_taps"], d), -0.5, 0.5)
     vec((d,), -0.1, 0.1)
     if confidence:

@@ -112,35 +112,39 @@ def weights_from_cact(w) -> "Needle2Weights":
 class Needle2Weights:
     """Seeded Needle 2 weights: every matrix per-row-scaled int8, or with
     cq_bits (2, 3, 4, or 5 for ternary) the shipped archive's Cactus-Quant
-    form (model/cact.ts:398-562) of that width with groups of cq_group."""
+    form (model/cact.ts:398-562) of that width with groups of cq_group, or
+    with cq_bits "mixed" each matrix in its own width and group
+    (cact.mixed_form)."""
 
-    def __init__(self, g: Needle2Geometry, run_seed: int = 2026, cq_bits: int = 0,
+    def __init__(self, g: Needle2Geometry, run_seed: int = 2026, cq_bits=0,
                  cq_group: int = 32):
         self.geometry = g
         L, d, hd = g.layers, g.dim, g.head_dim
         if cq_bits:
-            from .cact import CqMatrix
+            from .cact import CqMatrix, mixed_form
 
             cb = synth.cq_codebook()
             books = {2: cb[0:4], 3: cb[4:12], 4: cb[12:28]}
 
-        def mat(name, n, k):
+        def mat(name, n, k, role="", index=0):
             if cq_bits:
-                packed, norms = synth.cq_matrix(run_seed, name, n, k, cq_group, cq_bits,
+                bits, group = (mixed_form(role, index) if cq_bits == "mixed"
+                               else (cq_bits, cq_group))
+                packed, norms = synth.cq_matrix(run_seed, name, n, k, group, bits,
                                                 norm_lo=0.05, norm_hi=0.25)
-                return CqMatrix(packed, norms, books, n, k, cq_group, cq_bits)
+                return CqMatrix(packed, norms, books, n, k, group, bits)
             w, s = synth.int8_matrix(run_seed, name, n, k, k)
             return Int8Matrix(w, s, k, name)
 
         def u(name, shape, lo, hi):
             return synth.Stream(run_seed, name).uniform(shape, lo, hi)
 
-        self.embedding = mat("n2.embedding", g.vocab, d)
-        self.wq = [mat(f"n2.l{l}.wq", g.heads * hd, d) for l in range(L)]
-        self.wk = [mat(f"n2.l{l}.wk", g.kv_heads * hd, d) for l in range(L)]
-        self.wv = [mat(f"n2.l{l}.wv", g.kv_heads * hd, d) for l in range(L)]
-        self.wgate = [mat(f"n2.l{l}.wgate", g.heads * hd, d) for l in range(L)]
-        self.wo = [mat(f"n2.l{l}.wo", d, g.heads * hd) for l in range(L)]
+        self.embedding = mat("n2.embedding", g.vocab, d, "embedding")
+        self.wq = [mat(f"n2.l{l}.wq", g.heads * hd, d, "wq", l) for l in range(L)]
+        self.wk = [mat(f"n2.l{l}.wk", g.kv_heads * hd, d, "wk", l) for l in range(L)]
+        self.wv = [mat(f"n2.l{l}.wv", g.kv_heads * hd, d, "wv", l) for l in range(L)]
+        self.wgate = [mat(f"n2.l{l}.wgate", g.heads * hd, d, "wgate", l) for l in range(L)]
+        self.wo = [mat(f"n2.l{l}.wo", d, g.heads * hd, "wo", l) for l in range(L)]
         self.norm_input = u("n2.norm_input", (L, d), -0.1, 0.1)
         self.query_norm = u("n2.query_norm", (L, hd), -0.1, 0.1)
         self.key_norm = u("n2.key_norm", (L, hd), -0.1, 0.1)
@@ -151,9 +155,9 @@ class Needle2Weights:
         self.d2 = u("n2.d2", (L, g.hadamard), 0.5, 1.5)
         self.d3 = u("n2.d3", (L, d), 0.5, 1.5)
         ln = g.lanes
-        self.phi_pre = mat("n2.phi_pre", L * ln, ln * d)
-        self.phi_post = mat("n2.phi_post", L * ln, ln * d)
-        self.phi_res = mat("n2.phi_res", L * ln * ln, ln * d)
+        self.phi_pre = mat("n2.phi_pre", L * ln, ln * d, "phi_pre")
+        self.phi_post = mat("n2.phi_post", L * ln, ln * d, "phi_post")
+        self.phi_res = mat("n2.phi_res", L * ln * ln, ln * d, "phi_res")
         self.a_pre = u("n2.a_pre", (L,), 0.02, 0.1)
         self.a_post = u("n2.a_post", (L,), 0.02, 0.1)
         self.a_res = u("n2.a_res", (L,), 0.02, 0.1)
@@ -161,10 +165,11 @@ class Needle2Weights:
         self.b_post = u("n2.b_post", (L * ln,), -0.5, 0.5)
         self.b_res = u("n2.b_res", (L * ln * ln,), -0.5, 0.5)
         cat = g.engram_tables * g.engram_sub
-        self.eg_tables = [mat(f"n2.e{s}.tables", g.engram_tables * g.engram_slots, g.engram_sub)
-                          for s in range(len(g.sites))]
-        self.eg_key = [mat(f"n2.e{s}.key", d, cat) for s in range(len(g.sites))]
-        self.eg_value = [mat(f"n2.e{s}.value", d, cat) for s in range(len(g.sites))]
+        self.eg_tables = [mat(f"n2.e{s}.tables", g.engram_tables * g.engram_slots, g.engram_sub,
+                              "eg_tables", s) for s in range(len(g.sites))]
+        self.eg_key = [mat(f"n2.e{s}.key", d, cat, "eg_key", s) for s in range(len(g.sites))]
+        self.eg_value = [mat(f"n2.e{s}.value", d, cat, "eg_value", s)
+                         for s in range(len(g.sites))]
         self.eg_taps = u("n2.eg_taps", (len(g.sites), g.engram_taps, d), -0.5, 0.5)
         self.final_norm = u("n2.final_norm", (d,), -0.1, 0.1)
         self.confidence = ProbeHead(u("n2.conf.probes", (8, d), -0.1, 0.1),

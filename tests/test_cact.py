@@ -158,6 +158,39 @@ def test_archive_weights_for_the_runtime_step_on_the_oracle():
         assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max(), t
 
 
+def test_mixed_width_archive_records_and_oracle_step():
+    """A mixed-width archive: every Cactus-Quant record keeps the width and
+    group mixed_form gives it through write and parse, every width appears,
+    and the oracle's step over the parsed weights agrees with the float64
+    model of the dequantized matrices."""
+    from needle_hip.cact import mixed_form
+    from needle_hip.needle2 import weights_from_cact
+    from test_oracle_needle2 import NumpyNeedle2
+
+    pw = parse_cact_weights(synthetic_needle2_archive(N2_GEOMETRY, 6, mixed=True))
+    seen = set()
+    for l, layer in enumerate(pw.layers):
+        for role, m in (("wq", layer.query_projection), ("wk", layer.key_projection),
+                        ("wv", layer.value_projection), ("wgate", layer.gate_projection),
+                        ("wo", layer.output_projection)):
+            assert (m.bits, m.group_size) == mixed_form(role, l), (role, l)
+            seen.add(m.bits)
+    for role, m in (("embedding", pw.embedding), ("phi_pre", pw.mhc_phi_pre),
+                    ("phi_post", pw.mhc_phi_post), ("phi_res", pw.mhc_phi_residual)):
+        assert (m.bits, m.group_size) == mixed_form(role), role
+    for s, e in enumerate(pw.engrams):
+        assert (e.tables.bits, e.tables.group_size) == mixed_form("eg_tables", s)
+        assert (e.key_projection.bits, e.key_projection.group_size) == mixed_form("eg_key", s)
+        assert (e.value_projection.bits, e.value_projection.group_size) == mixed_form("eg_value", s)
+    assert seen == {2, 3, 4, 5}
+    w = weights_from_cact(pw)
+    rt = oracle.Needle2(w).runtime(w.geometry.max_length, 0)
+    ref = NumpyNeedle2(w, w.geometry.max_length, 0)
+    for t in (5, 200, 17, 5, 200, 64):
+        got, want = rt.step(t), ref.step(t)
+        assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max(), t
+
+
 def test_needle2_archive_named_structure():
     w = parse_cact_weights(synthetic_needle2_archive(N2_GEOMETRY, 3))
     g = N2_GEOMETRY

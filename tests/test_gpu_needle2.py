@@ -353,11 +353,14 @@ def test_generate_full_geometry_greedy_identical(hip):
         model.dispose()
 
 
-@pytest.mark.parametrize("cq_bits,sink", [(4, 3), (3, 0), (2, 0), (5, 3)])
+@pytest.mark.parametrize("cq_bits,sink", [(4, 3), (3, 0), (2, 0), (5, 3), ("mixed", 3),
+                                          ("mixed", 0)])
 def test_cactus_quant_model_steps_prefill_and_generate(hip, cq_bits, sink):
     """The resident runtime over Cactus-Quant matrices, the form every matrix
-    of the shipped archive takes (model/cact.ts:398-562, backends/cq.ts:106-295):
-    step logits, the cache and the confidence against the oracle's cqMatvec /
+    of the shipped archive takes (model/cact.ts:398-562, backends/cq.ts:106-295),
+    one width for every matrix or each matrix its own width and group
+    (mixed: every width on every kind of matrix across the layers): step
+    logits, the cache and the confidence against the oracle's cqMatvec /
     dequantizeCqRow restatement, a prompt (one batched pass while its cache
     slots do not wrap, steps after) and a greedy continuation with identical
     ids."""
@@ -393,7 +396,7 @@ def test_cactus_quant_model_steps_prefill_and_generate(hip, cq_bits, sink):
         model.dispose()
 
 
-@pytest.mark.parametrize("bits", [4, 5])
+@pytest.mark.parametrize("bits", [4, 5, "mixed"])
 def test_cact_archive_through_the_resident_runtime(hip, bits):
     """A .cact archive in the shipped layout (synthetic weights, the
     reference's tensor order) parsed by parse_cact_weights and run as is --
@@ -410,7 +413,9 @@ def test_cact_archive_through_the_resident_runtime(hip, bits):
                engram_slots=64, engram_sub_dimension=128, number_of_engram_tables=4,
                engram_convolution_taps=4, engram_convolution_dilation=1,
                engram_orders=[2, 3], engram_layers=[0, 2], rope_theta=10000.0)
-    w = weights_from_cact(parse_cact_weights(synthetic_needle2_archive(geo, 17, bits=bits)))
+    archive = (synthetic_needle2_archive(geo, 17, mixed=True) if bits == "mixed"
+               else synthetic_needle2_archive(geo, 17, bits=bits))
+    w = weights_from_cact(parse_cact_weights(archive))
     g = w.geometry
     model = NeedleModel(hip, w)
     try:
@@ -433,6 +438,38 @@ def test_cact_archive_through_the_resident_runtime(hip, bits):
             if k + 1 < 8:
                 logits = ref2.step(ids[-1])
         assert res.token_ids == ids
+    finally:
+        model.dispose()
+
+
+def test_generate_full_geometry_mixed_width_greedy_identical(hip):
+    """The shipped geometry with every matrix in its own Cactus-Quant width
+    and group (the mixed archive's form): 128 prompt tokens and 64 greedy
+    tokens identical to the oracle's, log-probabilities within 1e-3, the
+    cache and the confidence within their bars."""
+    say("needle2 generate full geometry mixed widths")
+    g = Needle2Geometry()
+    w = Needle2Weights(g, 2027, cq_bits="mixed")
+    model = NeedleModel(hip, w)
+    try:
+        prompt = synth.Stream(2027, "needle2.prompt").integers(128, 0, g.vocab - 1)
+        res = model.generate_resident(prompt, max_new_tokens=64, eos=None)
+        ref = oracle.Needle2(w).runtime(128 + 64, 0)
+        ref.capture_kv(0, 128 + 64)
+        for t in prompt[:-1]:
+            ref.step(int(t), want_logits=False)
+        logits = ref.step(int(prompt[-1]))
+        ids, lps = [], []
+        for k in range(64):
+            tok = oracle.argmax(logits)
+            ids.append(tok)
+            lps.append(oracle.log_softmax_at(logits, tok))
+            if k + 1 < 64:
+                logits = ref.step(tok)
+        assert res.token_ids == ids
+        np.testing.assert_allclose(res.token_log_probabilities, lps, rtol=1e-3, atol=1e-3)
+        check_kv(model, ref, g, 128 + 63, 0, "mixed generate")
+        close_confidence(model.resident.confidence(), ref.confidence(), "mixed confidence")
     finally:
         model.dispose()
 

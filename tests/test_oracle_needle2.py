@@ -181,10 +181,12 @@ class NumpyNeedle2:
         return dense(w.embedding) @ self.rms(x.mean(axis=0), w.final_norm)
 
 
-@pytest.mark.parametrize("sink,cq_bits", [(0, 0), (3, 0), (0, 4), (3, 3), (0, 2), (0, 5)])
+@pytest.mark.parametrize("sink,cq_bits", [(0, 0), (3, 0), (0, 4), (3, 3), (0, 2), (0, 5),
+                                          (3, "mixed")])
 def test_step_matches_float64_model(sink, cq_bits):
     """Int8 weights, and the Cactus-Quant widths of the shipped archive (the
-    oracle runs cqMatvec / dequantizeCqRow on them)."""
+    oracle runs cqMatvec / dequantizeCqRow on them), one width for every
+    matrix or each matrix its own width and group (mixed)."""
     w = Needle2Weights(SMALL, 9, cq_bits=cq_bits)
     model = oracle.Needle2(w)
     rt = model.runtime(SMALL.max_length, sink)
