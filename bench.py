@@ -238,8 +238,10 @@ def bench_grammar_mask(torch, hip, reps, cpu_seconds):
     vocabulary, at every state along a complete two-call output of the demo
     tools (longest-piece tokenization): the device kernel alone (states
     resident in HBM, one launch per mask, HIP events), the host call with
-    its undecided pieces settled, and the agent's own loop (a grammar clone
-    fed per piece, tools/agent.ts:164-175) on the host as the CPU baseline."""
+    its undecided pieces settled and the allowed id list built, the same
+    with the mask kept in a model's mask buffer for the selection (no id
+    list), and the agent's own loop (a grammar clone fed per piece,
+    tools/agent.ts:164-175) on the host as the CPU baseline."""
     import ctypes as C
 
     import numpy as np
@@ -297,9 +299,29 @@ def bench_grammar_mask(torch, hip, reps, cpu_seconds):
     for gg, p_ in points:
         masker.allowed(gg, p_)
     call_ms = (time.perf_counter() - t0) * 1e3 / len(points)
+    # The resident loop's per-step host work: the mask into a model's mask
+    # buffer (nd_needle_grammar_mask, a one-layer model of the same
+    # vocabulary) and the undecided pieces settled; the selection then
+    # reads the mask on the device.
+    from needle_hip.needle2 import Needle2Geometry, Needle2Weights
+    from needle_hip.runtime import Needle2Resident
+
+    geo = Needle2Geometry(vocab=len(pieces), dim=128, heads=4, kv_heads=2, layers=1,
+                          max_length=16, hadamard=256, engram_slots=64, sites=(0,),
+                          kv_window=8)
+    rt = Needle2Resident(hip, Needle2Weights(geo, 5))
+    rt.reset(geo.max_length, 0)
+    for gg, p_ in points[:4]:
+        rt.grammar_mask(masker, masker.state(gg), 65536 - p_)
+    t0 = time.perf_counter()
+    for gg, p_ in points:
+        _, und = rt.grammar_mask(masker, masker.state(gg), 65536 - p_)
+        masker.settle(gg, und)
+    resident_ms = (time.perf_counter() - t0) * 1e3 / len(points)
+    rt.free()
     part = {"vocab": len(pieces), "states": len(states), "kernel_ms_per_mask": kernel_ms,
-            "host_call_ms_per_mask": call_ms, "mean_undecided": float(np.mean(undecided)),
-            "max_undecided": int(max(undecided))}
+            "host_call_ms_per_mask": call_ms, "resident_call_ms_per_mask": resident_ms,
+            "mean_undecided": float(np.mean(undecided)), "max_undecided": int(max(undecided))}
     cpu = None
     if cpu_seconds > 0:
         t0, n = time.perf_counter(), 0
@@ -973,7 +995,9 @@ def main():
         part["cpu_baseline"] = cpu_gm
     parts["grammar_mask_v8192"] = part
     print(f"[bench] grammar mask: kernel {part['kernel_ms_per_mask'] * 1e3:.1f} us/mask, host call "
-          f"{part['host_call_ms_per_mask']:.2f} ms/mask, agent loop "
+          f"{part['host_call_ms_per_mask']:.2f} ms/mask (resident "
+          f"{part['resident_call_ms_per_mask']:.3f}), undecided mean "
+          f"{part['mean_undecided']:.2f}, agent loop "
           f"{part.get('cpu_ms_per_mask', float('nan')):.1f} ms/mask", file=sys.stderr, flush=True)
 
     cpu = None

@@ -550,6 +550,17 @@ nd_status nd_needle_generate(nd_ctx* ctx, nd_needle* model, const uint32_t* prom
                              uint32_t count, uint32_t max_new, uint32_t sink, uint32_t eos,
                              uint32_t* ids, double* log_probabilities, uint32_t* generated);
 
+/* stepSelected (model/runtime.ts:257-278) with the allowed set held on the
+ * device: the model's mask buffer as nd_needle_grammar_mask left it, plus
+ * the `n_settled` ids in `settled` (the undecided pieces the host grammar
+ * accepted), then the step and selectToken over that bitmask (the ascending
+ * allowed list Needle.complete builds, tools/agent.ts:164-183).  No id list
+ * crosses to the device.  INVALID_CACT for a settled id outside the
+ * vocabulary, or, after the step as in the reference, for an empty set. */
+nd_status nd_needle_step_select_mask(nd_ctx* ctx, nd_needle* model, uint32_t token,
+                                     const uint32_t* settled, uint32_t n_settled, uint32_t* id,
+                                     double* log_probability);
+
 /* The whole-step calls above run each layer's output projection, the layer
  * mix and the next layer's projection in one launch whose workgroups hand
  * over through bounded waits.  A wait that runs out sets a device status
@@ -630,6 +641,12 @@ nd_status nd_needle_finish_token_for_selection(nd_ctx* ctx, nd_needle* model);
 nd_status nd_needle_select_token(nd_ctx* ctx, nd_needle* model, const uint32_t* allowed,
                                  uint32_t count, uint32_t* id, double* log_probability);
 
+/* selectResidentToken over the model's mask buffer plus `settled` (as
+ * nd_needle_step_select_mask), for the session methods. */
+nd_status nd_needle_select_token_mask(nd_ctx* ctx, nd_needle* model, const uint32_t* settled,
+                                      uint32_t n_settled, uint32_t* id,
+                                      double* log_probability);
+
 /* readResidentLanes() (backend.ts:78): the lanes [lanes][dim] after the
  * last layer run (applying its post half if it is still owed). */
 nd_status nd_needle_read_lanes(nd_ctx* ctx, nd_needle* model, float* lanes);
@@ -660,14 +677,30 @@ nd_status nd_pieces_free(nd_ctx* ctx, nd_pieces* pieces);
 
 /* A tool-call grammar program (ToolCallGrammar over its tools' JSON Schemas,
  * tools/grammar.ts:256-797) compiled by the host, as 32-bit words:
- *   header [16]: magic 0x4E444752; (count, word offset) of nodes [12 words
+ *   header [16]: magic 0x4E444752; (count, word offset) of nodes [28 words
  *     each], values [4], alternatives [1], properties [4], candidates [4],
- *     tools [4]; byte offset and length of the byte pool.
+ *     tools [4]; byte offset and length of the byte pool; word offset of the
+ *     pattern automata (0: none), which run up to the byte pool.
  *   node: possible-type bits (string 1, number 2, integer 4, boolean 8,
  *     null 16, array 32, object 64); check flags (1 string constraints,
- *     2 numeric constraints, 4 integer only, 8 enum/const/uniqueItems on an
- *     array or object); minItems; maxItems; items value; property count
- *     (<= 32); first property; required mask; minProperties; maxProperties.
+ *     2 numeric constraints, 4 integer only, 8 enum/const on an array or
+ *     object, 16 uniqueItems); minItems; maxItems; items value; property count
+ *     (<= 32); first property; required mask; minProperties; maxProperties;
+ *     2 reserved; then the value checks (grammar.ts:179-222): flags
+ *     (1 minLength, 2 maxLength, 4 format email, 8 format uuid, 16 a string
+ *     check the host makes: enum / const / a length that is not a count / a
+ *     pattern without an automaton, 32 pattern by its automaton; 256 minimum,
+ *     512 maximum, 1024 exclusiveMinimum, 2048 exclusiveMaximum,
+ *     4096 multipleOf, 8192 a numeric check the host makes: enum / const / a
+ *     bound that is not a number), minLength, maxLength, the pattern
+ *     automaton's word offset in the automata + 1 (0: none), minimum,
+ *     maximum, exclusiveMinimum, exclusiveMaximum and multipleOf as float64
+ *     (two words, low first), 2 reserved.
+ *   pattern automaton (`new RegExp(pattern).test(value)` over the value's
+ *     UTF-16 code units): states S (<= 1024), classes C, bounds B, 0; B
+ *     bounds (first code unit | class << 16, ascending from unit 0); S flags
+ *     (bit 0: the units read so far match); S x C next states.  State 0 is
+ *     the empty value.
  *   value (a value frame's schema): kind 0 = alternatives (first, count:
  *     node indices in oneOf/anyOf order), 1 = choice (first, count <= 32
  *     candidates: every alternative is const/enum), 2 = too many candidates.
@@ -684,16 +717,35 @@ nd_status nd_grammar_free(nd_ctx* ctx, nd_grammar* grammar);
  * set when piece t is eligible, at most `budget` bytes long (65536 minus
  * the output so far, agent.ts:169) and accepted by the grammar from
  * `state`; bit t of undecided[t / 32] instead when the answer needs a check
- * the device does not make (strings under length/pattern/format/enum/const,
- * numbers under numeric constraints or with an exponent, arrays/objects
- * under enum/const/uniqueItems) -- the host grammar settles those pieces.
- * state: [16] tool-call phase (0 array-open .. 8 done), literal offset,
+ * the device does not make (strings under enum/const or under a pattern
+ * with no automaton -- backreferences, lookaround, word boundaries --,
+ * numbers under enum/const or whose value is not exact in the fast path --
+ * more than 2^53 significant or a decimal exponent beyond +-22 --,
+ * arrays/objects under enum/const, an array under uniqueItems closing in
+ * the piece that completed one of its items, stacks deeper than 24) --
+ * the host grammar settles those pieces.  String lengths, patterns with an
+ * automaton, the email and uuid formats, and numeric bounds, multipleOf and
+ * integrality are decided on the device.
+ * state: [24] tool-call phase (0 array-open .. 8 done), literal offset,
  * live tool-name mask, name offset, current tool, used-tool mask, calls,
  * maximum calls, tools, arguments present, arguments complete, the
- * completed value's kind, frame depth (<= 24), 3 reserved; then 4 words per
+ * completed value's kind, frame depth (<= 24), 3 reserved; the running
+ * summary of the string or number in progress in the top frame (zeros
+ * otherwise): for a string, code points after the opening quote (an
+ * escaped surrogate pair counts once), word 1 = the \u value being read
+ * (bits 0-15) | an escaped high surrogate pending (16) | email state (17-19:
+ * 0 start, 1 local part, 2 after '@', 3 domain, 4 after a usable '.',
+ * 5 accepting, 6 dead) | uuid characters matched (20-25) | uuid mismatch
+ * (26), the UTF-8 code point being assembled, the pattern automaton's
+ * state (0 without one); for a number, the
+ * mantissa of its significant digits taken while below 10^18 (low, high),
+ * k (two's complement: value = mantissa 10^(k + exponent)), the exponent
+ * digits (saturating at 999999) | minus (24) | exponent minus (25) | a
+ * nonzero digit dropped (26); 4 reserved; then 4 words per
  * JSON frame, bottom first: kind | phase << 8 | flags << 16 (kinds 1 value,
  * 2 string, 3 number, 4 literal, 5 choice, 6 array, 7 object, 8 key), a
- * value or node index (literal: 0 true, 1 false, 2 null), a live/used mask,
+ * value or node index (literal: 0 true, 1 false, 2 null), a live/used mask
+ * (array: 1 its items are the state's, 2 they are distinct by JSON text),
  * and an offset, count or current key.  Indices in the state are checked
  * by the kernel.  The host-pointer form copies state in and both masks
  * (ceil(vocab / 32) words each) out. */
@@ -703,6 +755,19 @@ nd_status nd_grammar_mask(nd_ctx* ctx, const nd_grammar* grammar, const uint32_t
 nd_status nd_grammar_mask_d(nd_ctx* ctx, const nd_grammar* grammar, const uint32_t* state_dev,
                             const nd_pieces* pieces, uint32_t budget, uint32_t* allowed_dev,
                             uint32_t* undecided_dev, void* stream);
+
+/* nd_grammar_mask with the allowed mask kept on the device, in the model's
+ * mask buffer (pieces over the model's vocabulary), for
+ * nd_needle_step_select_mask / nd_needle_select_token_mask: the undecided
+ * bits (ceil(vocab / 32) words) and the number of allowed pieces come back
+ * to the host, which settles the undecided pieces with its grammar
+ * (tools/agent.ts:164-176), raises GRAMMAR_DEAD_END when the two counts sum
+ * to zero (agent.ts:177-182), and passes the accepted ids to the selection
+ * call.  The model must have been reset. */
+nd_status nd_needle_grammar_mask(nd_ctx* ctx, nd_needle* model, const nd_grammar* grammar,
+                                 const nd_pieces* pieces, const uint32_t* state,
+                                 uint32_t n_state_words, uint32_t budget, uint32_t* undecided,
+                                 uint32_t* n_allowed);
 
 #ifdef __cplusplus
 }

@@ -9,11 +9,19 @@
 // the JSON frame stack).  Layouts are the ones documented in
 // include/needle_hip.h.  The interpreter follows grammar.ts byte for byte,
 // including its retry limits; three outcomes per piece: accepted, rejected,
-// or undecided when the answer needs a check this kernel does not make
-// (a string closing under length/pattern/format/enum/const constraints, a
-// number completing under numeric constraints or with an exponent, a
-// composite value closing under enum/const/uniqueItems, or a stack deeper
-// than kMaxDepth).  The host grammar settles the undecided pieces.
+// or undecided when the answer needs a check this kernel does not make.  It
+// decides a closing string's minLength / maxLength (code points as
+// Array.from counts them), pattern (an automaton the host builds from the
+// JavaScript regular expression, stepped per UTF-16 code unit) and email /
+// uuid formats, and a completed number's finiteness, integrality, bounds and
+// multipleOf whenever its value is exact in the fast path (at most 2^53
+// significant, a decimal exponent within +-22); it leaves undecided a string
+// under enum / const or under a pattern with no automaton, a number under
+// enum / const or outside the fast path, a composite value closing under
+// enum / const, an array under uniqueItems closing in the piece that
+// completed an item (the host tells whether the items it holds are
+// distinct), and a stack deeper than kMaxDepth.  The host
+// grammar settles the undecided pieces.
 #include <cstring>
 #include <vector>
 
@@ -28,7 +36,23 @@ enum Kind : uint32_t { kValue = 1, kString, kNumber, kLiteral, kChoice, kArray, 
 enum VKind : uint32_t { vString = 0, vNumber, vBoolean, vNull, vArray, vObject };
 enum TypeBit : uint32_t { tString = 1, tNumber = 2, tInteger = 4, tBoolean = 8, tNull = 16,
                           tArray = 32, tObject = 64 };
-enum NodeFlag : uint32_t { fStrCheck = 1, fNumCheck = 2, fIntOnly = 4, fValueCheck = 8 };
+enum NodeFlag : uint32_t { fStrCheck = 1, fNumCheck = 2, fIntOnly = 4, fValueCheck = 8,
+                           fUnique = 16 };
+// An array frame's word 2: bit 0 = its items are the host state's (none
+// completed since), bit 1 = those items are pairwise distinct by their JSON
+// text (grammar.ts uniqueItems), as the host computed them.
+constexpr uint32_t kItemsHost = 1, kItemsUnique = 2;
+// A node's entry: words 0..11 its structure, words 12..27 its value checks
+// (flags below, minLength, maxLength, 0, then minimum, maximum,
+// exclusiveMinimum, exclusiveMaximum, multipleOf as float64, low word first).
+constexpr uint32_t kNodeWords = 28;
+enum Check : uint32_t {
+  kcMinLength = 1, kcMaxLength = 2, kcEmail = 4, kcUuid = 8, kcStringHost = 16, kcPattern = 32,
+  kcMinimum = 256, kcMaximum = 512, kcExclusiveMinimum = 1024, kcExclusiveMaximum = 2048,
+  kcMultipleOf = 4096, kcNumberHost = 8192
+};
+constexpr uint32_t kLengthMax = 0xFFFFFF;               // string lengths are counted up to this
+constexpr uint64_t kMantissaCap = 1000000000000000000ull;  // digits taken while below this
 enum Tool : uint32_t { pArrayOpen = 0, pCallOpen, pNameLiteral, pToolName, pArgsLiteral, pArgs,
                        pCallClose, pAfterCall, pDone };
 enum Res : int { rReject = 0, rOk = 1, rUndecided = 2 };
@@ -41,16 +65,56 @@ struct Program {
   const uint32_t* cands;   // [n][4]
   const uint32_t* tools;   // [n][4]
   const uint8_t* bytes;
+  const uint32_t* regex;  // pattern automata
   uint32_t n_nodes, n_values, n_tools;  // bounds for indices that come from the state
 };
 
 // Node fields.
-__device__ __forceinline__ uint32_t nd_types(const Program& p, uint32_t n) { return p.nodes[n * 12]; }
-__device__ __forceinline__ uint32_t nd_flags(const Program& p, uint32_t n) { return p.nodes[n * 12 + 1]; }
+__device__ __forceinline__ uint32_t nd_types(const Program& p, uint32_t n) {
+  return p.nodes[n * kNodeWords];
+}
+__device__ __forceinline__ uint32_t nd_flags(const Program& p, uint32_t n) {
+  return p.nodes[n * kNodeWords + 1];
+}
 
+// The pattern automaton of node n (node word 15 holds its offset in the
+// automata + 1, or 0).  An automaton: [states, classes, bounds, 0], then the
+// bounds (first code unit | class << 16, ascending from unit 0), a flag per
+// state (bit 0: the value read so far matches the pattern), and the next
+// state per (state, class).  State 0 is the start of a value.
+__device__ __forceinline__ const uint32_t* nd_regex(const Program& p, uint32_t n) {
+  const uint32_t o = p.nodes[n * kNodeWords + 15];
+  return o ? p.regex + (o - 1) : nullptr;
+}
+
+__device__ uint32_t regex_step(const uint32_t* rx, uint32_t state, uint32_t unit) {
+  const uint32_t nb = rx[2];
+  const uint32_t* b = rx + 4;
+  uint32_t lo = 0, hi = nb;  // the last bound whose first unit is <= unit
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if ((b[mid] & 0xFFFFu) <= unit)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  return rx[4 + nb + rx[0] + state * rx[1] + (b[lo] >> 16)];
+}
+
+// acc: the running summary of the string or number in progress (always the
+// top frame), zeroed when one starts.  String: code points so far (an
+// escaped high surrogate followed by an escaped low one counts once, as
+// Array.from counts the decoded value), word 1 = the \u value being read
+// (bits 0-15) | an escaped high surrogate pending (16) | email state
+// (17-19) | uuid position (20-25) | uuid mismatch (26), the UTF-8 code point
+// being assembled, the pattern automaton's state.  Number: mantissa m (words 0, 1) of the significant
+// digits taken while m < 10^18, k (word 2, two's complement) with value =
+// m 10^(k + exponent), word 3 = exponent digits (saturating at 999999) |
+// minus (24) | exponent minus (25) | a nonzero digit dropped (26).
 struct State {
   uint32_t phase, lit, name_live, name_off, cur_tool, used_tools, n_calls, max_calls, n_tools;
   uint32_t args_present, args_complete, args_kind, depth;
+  uint32_t acc[4];
   uint32_t fr[kMaxDepth][4];
 };
 
@@ -123,6 +187,139 @@ __device__ __forceinline__ uint32_t number_step(uint32_t s, uint32_t b) {
   }
 }
 
+// ECMAScript's \s: WhiteSpace (TAB, VT, FF, SP, NBSP, ZWNBSP, the Zs
+// category) and LineTerminator (LF, CR, LS, PS).
+__device__ __forceinline__ bool js_space(uint32_t c) {
+  return (c >= 0x09 && c <= 0x0D) || c == 0x20 || c == 0xA0 || c == 0x1680 ||
+         (c >= 0x2000 && c <= 0x200A) || c == 0x2028 || c == 0x2029 || c == 0x202F ||
+         c == 0x205F || c == 0x3000 || c == 0xFEFF;
+}
+
+// /^[^\s@]+@[^\s@]+\.[^\s@]+$/ (grammar.ts:191) one character at a time: 0
+// start, 1 local part, 2 after '@', 3 domain, 4 after a usable '.', 5
+// accepting, 6 dead.
+__device__ __forceinline__ uint32_t email_step(uint32_t s, uint32_t c) {
+  const bool at = c == 0x40, other = !at && !js_space(c);
+  switch (s) {
+    case 0: return other ? 1 : 6;
+    case 1: return other ? 1 : (at ? 2 : 6);
+    case 2: return other ? 3 : 6;
+    case 3: return other ? (c == 0x2E ? 4 : 3) : 6;
+    case 4:
+    case 5: return other ? 5 : 6;
+    default: return 6;
+  }
+}
+
+// /^[0-9a-f]{8}-[0-9a-f]{4}-[1-8][0-9a-f]{3}-[89ab][0-9a-f]{3}-[0-9a-f]{12}$/i
+// (grammar.ts:192-196): whether character c fits position p.
+__device__ __forceinline__ bool uuid_char(uint32_t p, uint32_t c) {
+  if (p == 8 || p == 13 || p == 18 || p == 23) return c == 0x2D;
+  if (p == 14) return c >= 0x31 && c <= 0x38;
+  if (p == 19) return c == 0x38 || c == 0x39 || c == 0x61 || c == 0x62 || c == 0x41 || c == 0x42;
+  return (c >= 0x30 && c <= 0x39) || (c >= 0x61 && c <= 0x66) || (c >= 0x41 && c <= 0x46);
+}
+
+// One UTF-16 code unit (or one code point above U+FFFF) of the string's
+// decoded value into acc; uesc: it came from a \u escape; rx: the string's
+// pattern automaton, which reads a code point above U+FFFF as its two
+// surrogates (RegExp without the u flag reads code units).
+__device__ void string_emit(uint32_t* acc, uint32_t cu, bool uesc, const uint32_t* rx) {
+  if (rx) {
+    if (cu > 0xFFFFu) {
+      acc[3] = regex_step(rx, acc[3], 0xD800u + ((cu - 0x10000u) >> 10));
+      acc[3] = regex_step(rx, acc[3], 0xDC00u + ((cu - 0x10000u) & 0x3FFu));
+    } else {
+      acc[3] = regex_step(rx, acc[3], cu);
+    }
+  }
+  uint32_t w = acc[1];
+  if (((w >> 16) & 1) && uesc && cu >= 0xDC00 && cu <= 0xDFFF) {
+    w &= ~(1u << 16);  // the low half of an escaped pair: one code point
+  } else {
+    if (acc[0] < kLengthMax) acc[0] += 1;
+    w = (w & ~(1u << 16)) | ((uesc && cu >= 0xD800 && cu <= 0xDBFF) ? 1u << 16 : 0u);
+  }
+  const uint32_t email = email_step((w >> 17) & 7, cu);
+  uint32_t pos = (w >> 20) & 63, miss = (w >> 26) & 1;
+  if (!miss) {
+    if (pos < 36 && uuid_char(pos, cu))
+      pos += 1;
+    else
+      miss = 1;
+  }
+  acc[1] = (w & 0x1FFFFu) | (email << 17) | (pos << 20) | (miss << 26);
+}
+
+// The checks of a string closing under node n (validateString,
+// grammar.ts:179-203) that the kernel makes; enum / const, and a pattern
+// without an automaton, are the host's.
+__device__ int string_checks(const Program& P, uint32_t n, const uint32_t* acc,
+                             const uint32_t* rx) {
+  const uint32_t* c = P.nodes + n * kNodeWords + 12;
+  const uint32_t cf = c[0], len = acc[0];
+  if (cf & kcStringHost) return rUndecided;
+  if ((cf & kcPattern) && !(rx[4 + rx[2] + acc[3]] & 1u)) return rReject;
+  if ((cf & (kcMinLength | kcMaxLength)) && len >= kLengthMax) return rUndecided;
+  if ((cf & kcMinLength) && len < c[1]) return rReject;
+  if ((cf & kcMaxLength) && len > c[2]) return rReject;
+  if ((cf & kcEmail) && ((acc[1] >> 17) & 7) != 5) return rReject;
+  if ((cf & kcUuid) && (((acc[1] >> 20) & 63) != 36 || ((acc[1] >> 26) & 1))) return rReject;
+  return rOk;
+}
+
+__constant__ const double kPow10[23] = {1e0,  1e1,  1e2,  1e3,  1e4,  1e5,  1e6,  1e7,
+                                        1e8,  1e9,  1e10, 1e11, 1e12, 1e13, 1e14, 1e15,
+                                        1e16, 1e17, 1e18, 1e19, 1e20, 1e21, 1e22};
+
+// Number(text) from the accumulator when it is exact in the fast path: a
+// mantissa of at most 2^53 times an exactly representable power of ten
+// (10^0 .. 10^22), one correctly rounded product or quotient -- the value
+// a correctly rounding Number() gives.  False: outside the fast path.
+__device__ bool number_value(const uint32_t* acc, double* v) {
+  const uint64_t m = (uint64_t)acc[0] | ((uint64_t)acc[1] << 32);
+  const uint32_t w = acc[3];
+  if (w & (1u << 26)) return false;
+  double r = 0.0;
+  if (m != 0) {
+    const int32_t e = (int32_t)(w & 0xFFFFFFu);
+    const int64_t K = (int64_t)(int32_t)acc[2] + (((w >> 25) & 1) ? -e : e);
+    if (m > (1ull << 53) || K < -22 || K > 22) return false;
+    r = K >= 0 ? (double)m * kPow10[K] : (double)m / kPow10[-K];
+  }
+  *v = ((w >> 24) & 1) ? -r : r;
+  return true;
+}
+
+__device__ __forceinline__ double word_double(const uint32_t* p) {
+  return __builtin_bit_cast(double, (uint64_t)p[0] | ((uint64_t)p[1] << 32));
+}
+
+// validateNumber (grammar.ts:205-222) of a finite value under node n.
+__device__ int number_checks(const Program& P, uint32_t n, uint32_t nf, double v) {
+  if ((nf & fIntOnly) && v != floor(v)) return rReject;  // Number.isInteger
+  if (!(nf & fNumCheck)) return rOk;
+  const uint32_t* c = P.nodes + n * kNodeWords + 12;
+  const uint32_t cf = c[0];
+  if (cf & kcNumberHost) return rUndecided;
+  if ((cf & kcMinimum) && v < word_double(c + 4)) return rReject;
+  if ((cf & kcMaximum) && v > word_double(c + 6)) return rReject;
+  if ((cf & kcExclusiveMinimum) && v <= word_double(c + 8)) return rReject;
+  if ((cf & kcExclusiveMaximum) && v >= word_double(c + 10)) return rReject;
+  if (cf & kcMultipleOf) {
+    const double q = v / word_double(c + 12);
+    double r = q;  // Math.round: nearest integer, ties toward +Infinity
+    if (isfinite(q)) {
+      r = floor(q);
+      if (q - r >= 0.5) r += 1.0;
+    }
+    const double aq = fabs(q);
+    const double scale = aq != aq ? aq : (aq > 1.0 ? aq : 1.0);  // Math.max(1, |q|)
+    if (fabs(q - r) > 1e-9 * scale) return rReject;
+  }
+  return rOk;
+}
+
 // #finish (grammar.ts:633-656): pop the frame; the parent takes the value
 // (the whole arguments value when the stack empties).
 __device__ int finish(State& st, uint32_t vkind) {
@@ -135,6 +332,7 @@ __device__ int finish(State& st, uint32_t vkind) {
   uint32_t* parent = st.fr[st.depth - 1];
   if (fkind(parent) == kArray && fphase(parent) == 2) {
     parent[3] += 1;
+    parent[2] &= ~kItemsHost;  // an item the host has not compared
     set_phase(parent, 3);
     return rOk;
   }
@@ -183,11 +381,13 @@ __device__ int json_byte(const Program& P, State& st, uint32_t b) {
           f[1] = node;
           f[2] = 0;
           f[3] = 0;
+          st.acc[0] = st.acc[1] = st.acc[2] = st.acc[3] = 0;
         } else if (want & tNumber) {
           f[0] = kNumber;  // DFA state 0 in the phase byte
           f[1] = node;
           f[2] = 0;
           f[3] = 0;
+          st.acc[0] = st.acc[1] = st.acc[2] = st.acc[3] = 0;
         } else if (want == tBoolean) {
           f[0] = kLiteral;
           f[1] = b == 0x74 ? 0 : 1;
@@ -219,11 +419,18 @@ __device__ int json_byte(const Program& P, State& st, uint32_t b) {
           f[0] = kString | (1u << 16);
           return rOk;
         }
-        const uint32_t u8 = utf8_step((flags >> 8) & 15, b);
+        const uint32_t* rx = nd_regex(P, f[1]);
+        if (rx && st.acc[3] >= rx[0]) return rReject;  // not a state of the automaton
+        const uint32_t prev8 = (flags >> 8) & 15, u8 = utf8_step(prev8, b);
         if (uni > 0) {
-          if (!((b >= 0x30 && b <= 0x39) || (b >= 0x41 && b <= 0x46) || (b >= 0x61 && b <= 0x66)))
-            return rReject;
+          const bool digit = b >= 0x30 && b <= 0x39, upper = b >= 0x41 && b <= 0x46,
+                     lower = b >= 0x61 && b <= 0x66;
+          if (!(digit || upper || lower)) return rReject;
           uni -= 1;
+          const uint32_t hv =
+              ((st.acc[1] << 4) | (digit ? b - 0x30 : (b | 0x20u) - 0x57)) & 0xFFFFu;
+          st.acc[1] = (st.acc[1] & ~0xFFFFu) | hv;
+          if (uni == 0) string_emit(st.acc, hv, true, rx);
           f[0] = kString | ((1u | (uni << 2) | (u8 << 8)) << 16);
           return rOk;
         }
@@ -232,6 +439,17 @@ __device__ int json_byte(const Program& P, State& st, uint32_t b) {
                 b == 0x72 || b == 0x74 || b == 0x75))
             return rReject;
           uni = b == 0x75 ? 4 : 0;
+          if (uni)
+            st.acc[1] &= ~0xFFFFu;
+          else  // the escape's character
+            string_emit(st.acc,
+                        b == 0x62   ? 0x08u
+                        : b == 0x66 ? 0x0Cu
+                        : b == 0x6E ? 0x0Au
+                        : b == 0x72 ? 0x0Du
+                        : b == 0x74 ? 0x09u
+                                    : b,
+                        false, rx);
           f[0] = kString | ((1u | (uni << 2) | (u8 << 8)) << 16);
           return rOk;
         }
@@ -241,13 +459,25 @@ __device__ int json_byte(const Program& P, State& st, uint32_t b) {
         }
         if (b < 0x20) return rReject;
         if (b != 0x22) {
+          if (prev8 == 0) {
+            if (b < 0x80)
+              string_emit(st.acc, b, false, rx);
+            else
+              st.acc[2] = b & (b < 0xE0 ? 0x1Fu : (b < 0xF0 ? 0x0Fu : 0x07u));
+          } else {
+            st.acc[2] = ((st.acc[2] << 6) | (b & 0x3Fu)) & 0x1FFFFFu;
+            if (u8 == 0) string_emit(st.acc, st.acc[2], false, rx);
+          }
           f[0] = kString | ((1u | (u8 << 8)) << 16);
           return rOk;
         }
         // Closing quote: the bytes must decode (fatal UTF-8), then the
         // string's schema checks.
         if (u8 != 0) return rReject;
-        if (nd_flags(P, f[1]) & fStrCheck) return rUndecided;
+        if (nd_flags(P, f[1]) & fStrCheck) {
+          const int r = string_checks(P, f[1], st.acc, rx);
+          if (r != rOk) return r;
+        }
         return finish(st, vString) == rOk ? rOk : rReject;
       }
       case kNumber: {
@@ -262,15 +492,52 @@ __device__ int json_byte(const Program& P, State& st, uint32_t b) {
           if (n == 5 && b != 0x30) flags |= 2;         // nonzero fraction digit
           if ((n == 2 || n == 3) && f[3] < 1000) f[3] += 1;  // integer digits
           f[0] = kNumber | (n << 8) | (flags << 16);
+          // The value: integer and fraction digits into m and k, the
+          // exponent's sign and digits.
+          const uint32_t dg = b - 0x30;
+          if (n == 1) {
+            st.acc[3] |= 1u << 24;
+          } else if ((n == 2 || n == 3) && (s == 0 || s == 1 || s == 3)) {
+            const uint64_t m = (uint64_t)st.acc[0] | ((uint64_t)st.acc[1] << 32);
+            if (m < kMantissaCap) {
+              const uint64_t m2 = m * 10 + dg;
+              st.acc[0] = (uint32_t)m2;
+              st.acc[1] = (uint32_t)(m2 >> 32);
+            } else {
+              if ((int32_t)st.acc[2] < (1 << 20)) st.acc[2] += 1;
+              if (dg) st.acc[3] |= 1u << 26;
+            }
+          } else if (n == 5) {
+            const uint64_t m = (uint64_t)st.acc[0] | ((uint64_t)st.acc[1] << 32);
+            if (m < kMantissaCap) {
+              const uint64_t m2 = m * 10 + dg;
+              st.acc[0] = (uint32_t)m2;
+              st.acc[1] = (uint32_t)(m2 >> 32);
+              if ((int32_t)st.acc[2] > -(1 << 20)) st.acc[2] -= 1;
+            } else if (dg) {
+              st.acc[3] |= 1u << 26;
+            }
+          } else if (n == 7 || n == 11) {
+            if (b == 0x2D) st.acc[3] |= 1u << 25;
+          } else if (n == 8 || n == 12) {
+            uint32_t e = (st.acc[3] & 0xFFFFFFu) * 10 + dg;
+            if (e > 999999) e = 999999;
+            st.acc[3] = (st.acc[3] & ~0xFFFFFFu) | e;
+          }
           return rOk;
         }
         if (!(s == 2 || s == 3 || s == 5 || s == 8)) return rReject;
         const uint32_t flags = f[0] >> 16, nf = nd_flags(P, f[1]);
-        // Number(text) must be finite and meet the schema: decided here
-        // without an exponent, at most 308 integer digits and no numeric
-        // constraints beyond "integer".
-        if ((flags & 1) || f[3] > 308 || (nf & fNumCheck)) return rUndecided;
-        if ((nf & fIntOnly) && (flags & 2)) return rReject;
+        // Number(text) must be finite and meet the schema.  Without an
+        // exponent, with at most 308 integer digits and no checks it is;
+        // otherwise the value in the fast path decides, and a value outside
+        // it is the host's.
+        if ((flags & 1) || f[3] > 308 || (nf & (fNumCheck | fIntOnly))) {
+          double v;
+          if (!number_value(st.acc, &v)) return rUndecided;
+          const int r = number_checks(P, f[1], nf, v);
+          if (r != rOk) return r;
+        }
         if (finish(st, vNumber) != rOk) return rReject;
         continue;
       }
@@ -301,7 +568,7 @@ __device__ int json_byte(const Program& P, State& st, uint32_t b) {
         continue;
       }
       case kArray: {
-        const uint32_t* nd = P.nodes + f[1] * 12;
+        const uint32_t* nd = P.nodes + f[1] * kNodeWords;
         const uint32_t ph = fphase(f), minimum = nd[2], maximum = nd[3];
         if (ph == 0) {
           if (b != 0x5B) return rReject;
@@ -337,6 +604,10 @@ __device__ int json_byte(const Program& P, State& st, uint32_t b) {
           }
           if (b == 0x5D && f[3] >= minimum) {
             if (nd[1] & fValueCheck) return rUndecided;
+            if (nd[1] & fUnique) {
+              if (!(f[2] & kItemsHost)) return rUndecided;
+              if (!(f[2] & kItemsUnique)) return rReject;
+            }
             return finish(st, vArray) == rOk ? rOk : rReject;
           }
           return rReject;
@@ -344,7 +615,7 @@ __device__ int json_byte(const Program& P, State& st, uint32_t b) {
         return rReject;
       }
       case kObject: {
-        const uint32_t* nd = P.nodes + f[1] * 12;
+        const uint32_t* nd = P.nodes + f[1] * kNodeWords;
         const uint32_t ph = fphase(f), nprops = nd[5], required = nd[7];
         const uint32_t minimum = nd[8], maximum = nd[9], used = f[2];
         const uint32_t nused = __builtin_popcount(used);
@@ -398,7 +669,7 @@ __device__ int json_byte(const Program& P, State& st, uint32_t b) {
         return rReject;
       }
       case kKey: {
-        const uint32_t* nd = P.nodes + f[1] * 12;
+        const uint32_t* nd = P.nodes + f[1] * kNodeWords;
         const uint32_t nprops = nd[5] < 32 ? nd[5] : 32;
         if (b == 0x22) {
           uint32_t done = 0xFFFFFFFFu;
@@ -581,8 +852,9 @@ __global__ __launch_bounds__(kGThreads) void grammar_mask_kernel(
       st.args_complete = state[10];
       st.args_kind = state[11];
       st.depth = state[12] < kMaxDepth ? state[12] : kMaxDepth;
+      for (int w = 0; w < 4; ++w) st.acc[w] = state[16 + w];
       for (uint32_t i = 0; i < st.depth; ++i)
-        for (int w = 0; w < 4; ++w) st.fr[i][w] = state[16 + i * 4 + w];
+        for (int w = 0; w < 4; ++w) st.fr[i][w] = state[24 + i * 4 + w];
       res = rOk;
       for (uint32_t i = begin; i < end && res == rOk; ++i) res = tool_byte(P, st, bytes[i]);
     }
@@ -612,6 +884,7 @@ hipError_t nd_launch_grammar_mask(const nd_grammar* g, const uint32_t* state,
   P.cands = g->words + g->off[4];
   P.tools = g->words + g->off[5];
   P.bytes = reinterpret_cast<const uint8_t*>(g->words) + g->bytes_off;
+  P.regex = g->words + g->regex_off;
   P.n_nodes = g->n_nodes;
   P.n_values = g->n_values;
   P.n_tools = g->n_tools;
@@ -626,14 +899,14 @@ hipError_t nd_launch_grammar_mask(const nd_grammar* g, const uint32_t* state,
 namespace {
 
 constexpr uint32_t kGrammarMagic = 0x4E444752u;  // "RGDN"
-constexpr uint32_t kStateHeaderWords = 16;
+constexpr uint32_t kStateHeaderWords = 24;
 
 // Every table reference inside the program stays inside the program, so that
 // the kernel's reads are in bounds for any state whose own indices it checks.
 const char* check_program(const uint32_t* w, uint32_t n, nd_grammar* g) {
   if (n < 16 || w[0] != kGrammarMagic) return "bad magic or header";
   const uint32_t counts[6] = {w[1], w[3], w[5], w[7], w[9], w[11]};
-  const uint32_t widths[6] = {12, 4, 1, 4, 4, 4};
+  const uint32_t widths[6] = {kNodeWords, 4, 1, 4, 4, 4};
   for (int i = 0; i < 6; ++i) {
     const uint64_t end = (uint64_t)w[2 + 2 * i] + (uint64_t)counts[i] * widths[i];
     if (w[2 + 2 * i] < 16 || end > n) return "table outside the program";
@@ -642,6 +915,27 @@ const char* check_program(const uint32_t* w, uint32_t n, nd_grammar* g) {
   const uint64_t bytes_end = (uint64_t)w[13] + w[14];
   if (w[13] < 64 || bytes_end > (uint64_t)n * 4) return "bytes outside the program";
   g->bytes_off = w[13];
+  // Pattern automata: the words from w[15] up to the bytes.
+  uint32_t rx_len = 0;
+  if (w[15]) {
+    if (w[15] < 16 || w[15] > w[13] / 4) return "pattern automata outside the program";
+    rx_len = w[13] / 4 - w[15];
+  }
+  g->regex_off = w[15];
+  auto regex_ok = [&](uint32_t entry) {
+    if ((uint64_t)entry + 4 > rx_len) return false;
+    const uint32_t* r = w + w[15] + entry;
+    const uint64_t ns = r[0], nc = r[1], nb = r[2];
+    if (ns == 0 || nc == 0 || nb == 0 || ns > 1024 || nc > 65536) return false;
+    if (entry + 4 + nb + ns + ns * nc > rx_len || (r[4] & 0xFFFFu) != 0) return false;
+    for (uint64_t i = 0; i < nb; ++i)
+      if ((r[4 + i] >> 16) >= nc || (i && (r[4 + i] & 0xFFFFu) <= (r[3 + i] & 0xFFFFu)))
+        return false;
+    const uint32_t* t = r + 4 + nb + ns;
+    for (uint64_t i = 0; i < ns * nc; ++i)
+      if (t[i] >= ns) return false;
+    return true;
+  };
   g->n_nodes = counts[0];
   g->n_values = counts[1];
   g->n_tools = counts[5];
@@ -652,9 +946,11 @@ const char* check_program(const uint32_t* w, uint32_t n, nd_grammar* g) {
     return (uint64_t)first + len <= w[14];
   };
   for (uint32_t i = 0; i < counts[0]; ++i) {
-    const uint32_t* nd = nodes + i * 12;
+    const uint32_t* nd = nodes + i * kNodeWords;
     if (nd[4] >= counts[1] || nd[5] > 32 || (uint64_t)nd[6] + nd[5] > counts[3])
       return "node references outside the tables";
+    if ((nd[15] && !regex_ok(nd[15] - 1)) || ((nd[12] & kcPattern) && !nd[15]))
+      return "pattern automaton outside the table";
   }
   for (uint32_t i = 0; i < counts[1]; ++i) {
     const uint32_t* v = values + i * 4;
@@ -676,6 +972,16 @@ const char* check_program(const uint32_t* w, uint32_t n, nd_grammar* g) {
 }
 
 }  // namespace
+
+nd_status nd_check_grammar_state(nd_ctx* ctx, const uint32_t* state, uint32_t n_state_words) {
+  if (n_state_words < kStateHeaderWords || state[12] > 24 ||
+      n_state_words < kStateHeaderWords + 4 * state[12])
+    return nd_fail(ctx, n_state_words >= kStateHeaderWords && state[12] > 24 ? ND_ERR_UNSUPPORTED
+                                                                              : ND_ERR_INVALID,
+                   "grammar state of %u words with depth %u (at most 24 frames)", n_state_words,
+                   n_state_words >= kStateHeaderWords ? state[12] : 0);
+  return ND_OK;
+}
 
 extern "C" {
 
@@ -780,11 +1086,8 @@ nd_status nd_grammar_mask(nd_ctx* ctx, const nd_grammar* g, const uint32_t* stat
   if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
   if (!g || !pc || !state || !allowed || !undecided)
     return nd_fail(ctx, ND_ERR_INVALID, "nd_grammar_mask: NULL argument");
-  if (n_state_words < kStateHeaderWords || state[12] > 24 ||
-      n_state_words < kStateHeaderWords + 4 * state[12])
-    return nd_fail(ctx, state[12] > 24 ? ND_ERR_UNSUPPORTED : ND_ERR_INVALID,
-                   "grammar state of %u words with depth %u (at most 24 frames)", n_state_words,
-                   n_state_words >= kStateHeaderWords ? state[12] : 0);
+  nd_status st = nd_check_grammar_state(ctx, state, n_state_words);
+  if (st != ND_OK) return st;
   const size_t words = ((size_t)pc->vocab + 31) / 32;
   const size_t sb = ((size_t)n_state_words * 4 + 255) & ~size_t(255);
   if (!ctx->stage || ctx->stage_bytes < sb + 2 * words * 4) {

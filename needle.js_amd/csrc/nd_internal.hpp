@@ -85,11 +85,15 @@ struct nd_grammar {
   uint32_t* words = nullptr;
   uint32_t off[6] = {};
   uint32_t bytes_off = 0;
+  uint32_t regex_off = 0;  // word offset of the pattern automata (0: none)
   uint32_t n_nodes = 0, n_values = 0, n_tools = 0;
 };
 hipError_t nd_launch_grammar_mask(const nd_grammar* g, const uint32_t* state, const nd_pieces* pc,
                                   uint32_t budget, uint32_t* allowed, uint32_t* undecided,
                                   hipStream_t s);
+// Whether a host grammar state's words hold its header and frames (at most
+// 24); records the error on ctx otherwise.
+nd_status nd_check_grammar_state(nd_ctx* ctx, const uint32_t* state, uint32_t n_state_words);
 
 // Error helpers: record a message on the context and return a status.
 nd_status nd_fail(nd_ctx* ctx, nd_status code, const char* fmt, ...);

@@ -2071,6 +2071,16 @@ enum StageSlot : uint32_t {
   kStageSlots = kStageEngram + 8
 };
 
+namespace {
+// mask |= bit ids[i] for i < n (the ids the host accepted among the
+// undecided pieces of a grammar mask).
+__global__ void n2_set_bits_kernel(uint32_t* __restrict__ mask, const uint32_t* __restrict__ ids,
+                                   uint32_t n) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) atomicOr(mask + (ids[i] >> 5), 1u << (ids[i] & 31));
+}
+}  // namespace
+
 struct nd_needle {
   nd_needle_desc d{};
   bool cq = false;  // every matrix in the Cactus-Quant form (else int8)
@@ -2102,6 +2112,10 @@ struct nd_needle {
   size_t state_bytes = 0;  // leading part of the arena cleared by reset
   uint32_t *st = nullptr, *history = nullptr, *sel_id = nullptr, *allowed = nullptr,
            *counters = nullptr;
+  // The allowed-token bitmask of the constrained selection calls: bit t of
+  // word t / 32 (nd_needle_grammar_mask fills it; the _mask calls add the
+  // ids the host accepted among the undecided ones).
+  uint32_t* mask = nullptr;
   uint32_t* wo_count = nullptr;  // arrivals of the fused Wo launch (a line of its own)
   uint32_t* qkv_flags = nullptr;  // per layer: the fused launch's mix-done flag
   // Give-ups of the fused launch's bounded waits (kStatus* bits; a line of
@@ -2468,7 +2482,7 @@ hipError_t enqueue_block(nd_needle* n, uint32_t l, hipStream_t s, bool with_wo =
 // (tied embedding, runtime.ts:577) when tail, and selectToken over
 // allowed[0..count) (all ids when allowed is null) when select.
 hipError_t enqueue_final(nd_needle* n, bool tail, bool select, const uint32_t* allowed,
-                         uint32_t count, hipStream_t s) {
+                         uint32_t count, hipStream_t s, const uint32_t* mask = nullptr) {
   const nd_needle_desc& d = n->d;
   hipError_t e;
   if (pool_on(n) && (e = enqueue_pool(n, n->cells, d.layers + 1, n->scores, s)) != hipSuccess)
@@ -2476,6 +2490,9 @@ hipError_t enqueue_final(nd_needle* n, bool tail, bool select, const uint32_t* a
   if (!tail) return hipSuccess;
   e = mv_any(n->embedding, n->fin, 0, d.vocab, n->logits, s);
   if (e != hipSuccess || !select) return e;
+  if (mask)  // the allowed set as a device bitmask (an empty one gives id 0xFFFFFFFF)
+    return nd_launch_select_mask(n->logits, 1, d.vocab, mask, n->sel_id, n->sel_lp, s, nullptr,
+                                 nullptr, nullptr);
   return nd_launch_select_list(n->logits, d.vocab, allowed, count, n->sel_id, n->sel_lp, s);
 }
 
@@ -2600,7 +2617,8 @@ hipError_t enqueue_engrams(nd_needle* n, hipStream_t s) {
 // select: after the logits, selectToken over allowed[0..count) (all ids when
 // allowed is null) into sel_id / sel_lp.
 hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want_logits,
-                        bool select, const uint32_t* allowed, uint32_t count, hipStream_t s) {
+                        bool select, const uint32_t* allowed, uint32_t count, hipStream_t s,
+                        const uint32_t* mask = nullptr) {
   const nd_needle_desc& d = n->d;
   BeginArgs b = begin_args(n);
   b.token_arg = token;
@@ -2633,7 +2651,7 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
     if (!pre) break;
     if ((e = enqueue_block(n, l, s, !fuse, !fuse)) != hipSuccess) return e;
   }
-  return enqueue_final(n, tail, select, allowed, count, s);
+  return enqueue_final(n, tail, select, allowed, count, s, mask);
 }
 
 enum GraphKind { kGraphPrompt = 0, kGraphPromptSelect = 1, kGraphDecodeSelect = 2 };
@@ -3297,7 +3315,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
                             cb * al(P8 * kMaxChunks), cb * al(P8 * kMaxChunks),
                             cb * al(P8 * D), al(64), al(64),
                             // K and V sized for float32 rows (kvCache "float32")
-                            al((size_t)d.vocab * 4), al(rows * kHd * 4), al(rows * kHd * 4),
+                            al((size_t)d.vocab * 4), al((size_t)(d.vocab + 31) / 32 * 4), al(rows * kHd * 4), al(rows * kHd * 4),
                             al(rows * 4),
                             al(rows * 4), al((size_t)ln * D * 4), al(D * 4), al(D * 4), al(D * 4),
                             al((size_t)(2 * qw + 2 * kw) * 4), al(qw * 4), al(qw * 4), al(D * 4),
@@ -3333,6 +3351,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     take(&n->sel_id);
     take(&n->sel_lp);
     take(&n->allowed);
+    take(&n->mask);
     int8_t *kc, *vc;
     take(&kc);
     take(&vc);
@@ -3494,6 +3513,83 @@ nd_status nd_needle_step_select(nd_ctx* ctx, nd_needle* n, uint32_t token, const
   ND_HIP(ctx, enqueue_status(n, ctx->stream));
   ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return check_waits(ctx, n);
+}
+
+nd_status nd_needle_grammar_mask(nd_ctx* ctx, nd_needle* n, const nd_grammar* g,
+                                 const nd_pieces* pc, const uint32_t* state,
+                                 uint32_t n_state_words, uint32_t budget, uint32_t* undecided,
+                                 uint32_t* n_allowed) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!n || !g || !pc || !state || !undecided || !n_allowed)
+    return nd_fail(ctx, ND_ERR_INVALID, "NULL argument");
+  if (!n->arena) return nd_fail(ctx, ND_ERR_INVALID, "Call runtime.reset() before decoding");
+  if (pc->vocab != n->d.vocab)
+    return nd_fail(ctx, ND_ERR_INVALID, "the pieces cover %u ids, the model %u", pc->vocab,
+                   n->d.vocab);
+  const size_t words = ((size_t)n->d.vocab + 31) / 32;
+  // The state through the allowed-id list's buffer (at least vocab words).
+  if (n_state_words > n->d.vocab)
+    return nd_fail(ctx, ND_ERR_INVALID, "grammar state of %u words", n_state_words);
+  nd_status st = nd_check_grammar_state(ctx, state, n_state_words);
+  if (st != ND_OK) return st;
+  hipStream_t s = ctx->stream;
+  ND_HIP(ctx, stage_copy(n, kStageAllowed, n->allowed, state, (size_t)n_state_words * 4, 0, s));
+  uint32_t* und = n->allowed + ((n_state_words + 63) & ~63u);
+  if ((size_t)((n_state_words + 63) & ~63u) + words > n->d.vocab)
+    return nd_fail(ctx, ND_ERR_INVALID, "vocabulary too small for the grammar state");
+  ND_HIP(ctx, nd_launch_grammar_mask(g, n->allowed, pc, budget, n->mask, und, s));
+  std::vector<uint32_t> bits(words);
+  ND_HIP(ctx, hipMemcpyAsync(bits.data(), n->mask, words * 4, hipMemcpyDeviceToHost, s));
+  ND_HIP(ctx, hipMemcpyAsync(undecided, und, words * 4, hipMemcpyDeviceToHost, s));
+  ND_HIP(ctx, hipStreamSynchronize(s));
+  uint32_t count = 0;
+  for (uint32_t w : bits) count += (uint32_t)__builtin_popcount(w);
+  *n_allowed = count;
+  return ND_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// The host's accepted ids among the undecided ones into the model's mask.
+nd_status settle_mask(nd_ctx* ctx, nd_needle* n, const uint32_t* settled, uint32_t n_settled) {
+  if (n_settled == 0) return ND_OK;
+  if (!settled) return nd_fail(ctx, ND_ERR_INVALID, "NULL settled ids");
+  if (n_settled > n->d.vocab)
+    return nd_fail(ctx, ND_ERR_INVALID, "more settled ids than the vocabulary");
+  for (uint32_t i = 0; i < n_settled; ++i)
+    if (settled[i] >= n->d.vocab)
+      return nd_fail(ctx, ND_ERR_INVALID, "Token %u is outside logits", settled[i]);
+  hipStream_t s = ctx->stream;
+  ND_HIP(ctx, stage_copy(n, kStageAllowed, n->allowed, settled, (size_t)n_settled * 4, 0, s));
+  hipLaunchKernelGGL(n2_set_bits_kernel, dim3((n_settled + 255) / 256), dim3(256), 0, s, n->mask,
+                     n->allowed, n_settled);
+  ND_HIP(ctx, hipGetLastError());
+  return ND_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+nd_status nd_needle_step_select_mask(nd_ctx* ctx, nd_needle* n, uint32_t token,
+                                     const uint32_t* settled, uint32_t n_settled, uint32_t* id,
+                                     double* logprob) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!n || !id || !logprob) return nd_fail(ctx, ND_ERR_INVALID, "NULL argument");
+  nd_status st = check_step(ctx, n, token);
+  if (st != ND_OK || (st = use_api(ctx, n, 1)) != ND_OK) return st;
+  if ((st = settle_mask(ctx, n, settled, n_settled)) != ND_OK) return st;
+  ND_HIP(ctx, enqueue_step(n, kTokenArg, token, true, true, nullptr, 0, ctx->stream, n->mask));
+  ++n->position;
+  ND_HIP(ctx, hipMemcpyAsync(id, n->sel_id, 4, hipMemcpyDeviceToHost, ctx->stream));
+  ND_HIP(ctx, hipMemcpyAsync(logprob, n->sel_lp, 8, hipMemcpyDeviceToHost, ctx->stream));
+  ND_HIP(ctx, enqueue_status(n, ctx->stream));
+  ND_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  if ((st = check_waits(ctx, n)) != ND_OK) return st;
+  if (*id == 0xFFFFFFFFu) return nd_fail(ctx, ND_ERR_INVALID, "Allowed token set is empty");
+  return ND_OK;
 }
 
 nd_status nd_needle_generate(nd_ctx* ctx, nd_needle* n, const uint32_t* prompt, uint32_t count,
@@ -3796,6 +3892,26 @@ nd_status nd_needle_select_token(nd_ctx* ctx, nd_needle* n, const uint32_t* allo
   ND_HIP(ctx, hipMemcpyAsync(id, n->sel_id, 4, hipMemcpyDeviceToHost, s));
   ND_HIP(ctx, hipMemcpyAsync(log_probability, n->sel_lp, 8, hipMemcpyDeviceToHost, s));
   ND_HIP(ctx, hipStreamSynchronize(s));
+  return ND_OK;
+}
+
+nd_status nd_needle_select_token_mask(nd_ctx* ctx, nd_needle* n, const uint32_t* settled,
+                                      uint32_t n_settled, uint32_t* id, double* log_probability) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_session(ctx, n);
+  if (st != ND_OK) return st;
+  if (!id || !log_probability) return nd_fail(ctx, ND_ERR_INVALID, "NULL argument");
+  if (!n->select_ready)
+    return nd_fail(ctx, ND_ERR_BACKEND, "Token selection did not produce a result");
+  if ((st = settle_mask(ctx, n, settled, n_settled)) != ND_OK) return st;
+  hipStream_t s = ctx->stream;
+  ND_HIP(ctx, nd_launch_select_mask(n->logits, 1, n->d.vocab, n->mask, n->sel_id, n->sel_lp, s,
+                                    nullptr, nullptr, nullptr));
+  n->select_ready = false;
+  ND_HIP(ctx, hipMemcpyAsync(id, n->sel_id, 4, hipMemcpyDeviceToHost, s));
+  ND_HIP(ctx, hipMemcpyAsync(log_probability, n->sel_lp, 8, hipMemcpyDeviceToHost, s));
+  ND_HIP(ctx, hipStreamSynchronize(s));
+  if (*id == 0xFFFFFFFFu) return nd_fail(ctx, ND_ERR_INVALID, "Allowed token set is empty");
   return ND_OK;
 }
 

@@ -17,12 +17,13 @@ restates that loop.  On the GPU, `maskgen` compiles the tools and each
 grammar state for the HIP mask kernel, which decides the same question for
 every piece in parallel.
 
-JavaScript regular expressions (`pattern`, and the email/uuid `format`s) are
-evaluated with Python's `re`, which agrees with them on the common syntax.
-Parity unpinned for those two features: no test or fixture of the reference
-covers a schema with `pattern` or `format`, and where JavaScript's and
-Python's regex dialects differ (lookbehind forms, digit classes over Unicode digits,
-the `u`/`v` flags) the allowed pieces can differ.
+JavaScript regular expressions keep JavaScript's semantics: a string's
+`pattern` runs on `jsregex` (RegExp without flags: Annex B syntax, UTF-16
+code units, ECMAScript's \\s and ASCII \\d/\\w), and the email and uuid
+`format`s on scanners of their two expressions with the same character
+sets and anchors.  The reference's tests hold no schema with `pattern` or
+`format`; these are pinned by the specification's own cases and by
+cross-checks against an independent matcher where the dialects agree.
 """
 
 from __future__ import annotations
@@ -32,13 +33,66 @@ import math
 import re
 from typing import Any, List, Optional, Sequence
 
+from . import jsregex
 from .errors import NeedleError, invariant
 
 _NAME_LITERAL = b'"name":"'  # grammar.ts:674
 _ARGUMENTS_LITERAL = b',"arguments":'  # grammar.ts:675
-_EMAIL = re.compile(r"^[^\s@]+@[^\s@]+\.[^\s@]+$")
-_UUID = re.compile(r"^[0-9a-f]{8}-[0-9a-f]{4}-[1-8][0-9a-f]{3}-[89ab][0-9a-f]{3}-[0-9a-f]{12}$",
-                   re.IGNORECASE)
+# The code points the \s class of an ECMAScript regular expression matches
+# (ECMA-262 WhiteSpace -- TAB, VT, FF, ZWNBSP and the Zs category -- and
+# LineTerminator -- LF, CR, LS, PS).  Python's \s differs (it matches
+# U+001C..U+001F and U+0085, not U+FEFF), so the format checks below are
+# written out with this set instead of using `re`.
+JS_SPACE = frozenset([0x09, 0x0A, 0x0B, 0x0C, 0x0D, 0x20, 0xA0, 0x1680, *range(0x2000, 0x200B),
+                      0x2028, 0x2029, 0x202F, 0x205F, 0x3000, 0xFEFF])
+
+
+def js_email(value: str) -> bool:
+    r"""/^[^\s@]+@[^\s@]+\.[^\s@]+$/.test(value) (grammar.ts:191), `$` at the
+    end of the input only: a local part, '@', then at least three characters
+    without whitespace or '@' with a '.' after the first of them and before
+    the last.  States: 0 start, 1 local part, 2 after '@', 3 domain, 4 after
+    a usable '.', 5 accepting, 6 dead.  Characters step one at a time (a
+    UTF-16 surrogate pair steps twice in JavaScript, through the same
+    'other' transitions)."""
+    state = 0
+    for ch in value:
+        c = ord(ch)
+        at = c == 0x40
+        other = not at and c not in JS_SPACE
+        if state == 0:
+            state = 1 if other else 6
+        elif state == 1:
+            state = 1 if other else (2 if at else 6)
+        elif state == 2:
+            state = 3 if other else 6
+        elif state == 3:
+            state = (4 if c == 0x2E else 3) if other else 6
+        elif state in (4, 5):
+            state = 5 if other else 6
+        else:
+            return False
+    return state == 5
+
+
+def js_uuid(value: str) -> bool:
+    """/^[0-9a-f]{8}-[0-9a-f]{4}-[1-8][0-9a-f]{3}-[89ab][0-9a-f]{3}-[0-9a-f]{12}$/i
+    .test(value) (grammar.ts:192-196): 36 characters, case-insensitive hex
+    (no character outside ASCII folds into these classes)."""
+    if len(value) != 36:
+        return False
+    for i, ch in enumerate(value):
+        if i in (8, 13, 18, 23):
+            ok = ch == "-"
+        elif i == 14:
+            ok = ch in "12345678"
+        elif i == 19:
+            ok = ch in "89abAB"
+        else:
+            ok = ch in "0123456789abcdefABCDEF"
+        if not ok:
+            return False
+    return True
 
 
 # ------------------------------------------------------------- JS semantics
@@ -139,7 +193,21 @@ def js_stringify(value: Any) -> str:
     raise TypeError(f"not a JSON value: {value!r}")
 
 
+def _js_divide(a: float, b: float) -> float:
+    """a / b in IEEE arithmetic as JavaScript evaluates it (Python raises on
+    a zero divisor instead)."""
+    if b == 0:
+        if a == 0 or math.isnan(a):
+            return math.nan
+        return math.copysign(math.inf, a) * math.copysign(1.0, b)
+    return a / b
+
+
 def _js_round(x: float) -> float:
+    """Math.round: the nearest integer, ties toward +Infinity; NaN and the
+    infinities unchanged."""
+    if not math.isfinite(x):
+        return x
     r = math.floor(x)
     return r + 1 if x - r >= 0.5 else r
 
@@ -252,14 +320,18 @@ def validate_string(value: str, schema: dict) -> bool:
         return False
     if "pattern" in schema:
         try:
-            if re.search(schema["pattern"], value) is None:
+            if not jsregex.test(schema["pattern"], value):
                 return False
-        except re.error as exc:
+        except jsregex.RegexSyntaxError as exc:
             raise NeedleError("INVALID_TOOL_SCHEMA",
                               f"Invalid JSON Schema pattern {schema['pattern']}", exc) from exc
-    if schema.get("format") == "email" and not _EMAIL.search(value):
+        except RecursionError as exc:
+            raise NeedleError("UNSUPPORTED_CACT",
+                              f"pattern {schema['pattern']} nests too deeply for this value",
+                              exc) from exc
+    if schema.get("format") == "email" and not js_email(value):
         return False
-    if schema.get("format") == "uuid" and not _UUID.search(value):
+    if schema.get("format") == "uuid" and not js_uuid(value):
         return False
     return validate_enum(value, schema)
 
@@ -280,7 +352,7 @@ def validate_number(value: float, schema: dict) -> bool:
     if "exclusiveMaximum" in schema and value >= schema["exclusiveMaximum"]:
         return False
     if "multipleOf" in schema:
-        q = value / schema["multipleOf"]
+        q = _js_divide(value, schema["multipleOf"])
         if abs(q - _js_round(q)) > 1e-9 * max(1.0, abs(q)):
             return False
     return validate_enum(value, schema)
@@ -336,18 +408,20 @@ class _Frame:
             setattr(self, k, kw.get(k))
 
     def clone(self) -> "_Frame":
-        f = _Frame(self.kind)
-        for k in self.__slots__[1:]:
-            v = getattr(self, k)
-            if k == "bytes" and v is not None:
-                v = list(v)
-            elif k == "candidates" and v is not None:
-                v = [list(c) for c in v]  # [bytes, value_or_name, offset]
-            elif k in ("values", "value") and isinstance(v, (list, dict)):
-                v = json.loads(json.dumps(v))
-            elif k == "used" and v is not None:
-                v = list(v)
-            setattr(f, k, v)
+        """A frame of its own.  The containers this frame fills (bytes,
+        candidates, items, properties) are copied; the completed values in
+        them are shared, as nothing modifies a value once it is complete."""
+        f = _Frame.__new__(_Frame)
+        f.kind, f.schema, f.started, f.escaped = self.kind, self.schema, self.started, self.escaped
+        f.unicode, f.text, f.offset, f.phase = self.unicode, self.text, self.offset, self.phase
+        f.current_key = self.current_key
+        f.bytes = None if self.bytes is None else list(self.bytes)
+        # [bytes, value_or_name, offset, index]
+        f.candidates = None if self.candidates is None else [list(c) for c in self.candidates]
+        v = self.value
+        f.value = dict(v) if isinstance(v, dict) else (list(v) if isinstance(v, list) else v)
+        f.values = None if self.values is None else list(self.values)
+        f.used = None if self.used is None else list(self.used)
         return f
 
 
@@ -387,7 +461,7 @@ class JsonSchemaGrammar:
         g.root_schema = self.root_schema
         g.stack = [f.clone() for f in self.stack]
         g._complete = self._complete
-        g._value = json.loads(json.dumps(self._value)) if self._value is not None else None
+        g._value = self._value  # complete: never modified
         return g
 
     def feed(self, data: bytes) -> bool:
@@ -675,7 +749,7 @@ class ToolCallGrammar:
         g.current_tool = self.current_tool
         g.used_tools = list(self.used_tools)
         g.arguments = self.arguments.clone() if self.arguments is not None else None
-        g.calls = json.loads(json.dumps(self.calls))
+        g.calls = list(self.calls)  # completed calls are never modified
         return g
 
     def feed(self, data: bytes) -> bool:

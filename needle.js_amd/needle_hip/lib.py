@@ -115,6 +115,7 @@ SIGNATURES = {
     "nd_needle_step": (I32, [P, P, U32, P]),
     "nd_needle_prefill": (I32, [P, P, P, U32, P]),
     "nd_needle_step_select": (I32, [P, P, U32, P, U32, P, P]),
+    "nd_needle_step_select_mask": (I32, [P, P, U32, P, U32, P, P]),
     "nd_needle_generate": (I32, [P, P, P, U32, U32, U32, U32, P, P, P]),
     "nd_needle_test_waits": (I32, [P, P, U32, U32]),
     "nd_needle_begin_token": (I32, [P, P, P]),
@@ -124,6 +125,7 @@ SIGNATURES = {
     "nd_needle_finish_token": (I32, [P, P, U32, P]),
     "nd_needle_finish_token_for_selection": (I32, [P, P]),
     "nd_needle_select_token": (I32, [P, P, P, U32, P, P]),
+    "nd_needle_select_token_mask": (I32, [P, P, P, U32, P, P]),
     "nd_needle_read_lanes": (I32, [P, P, P]),
     "nd_needle_forward": (I32, [P, P, U32, U32, P, P, P, P, P, P, P]),
     "nd_pieces_upload": (I32, [P, P, P, P, U32, PP]),
@@ -132,6 +134,7 @@ SIGNATURES = {
     "nd_grammar_free": (I32, [P, P]),
     "nd_grammar_mask": (I32, [P, P, P, U32, P, U32, P, P]),
     "nd_grammar_mask_d": (I32, [P, P, P, P, U32, P, P, P]),
+    "nd_needle_grammar_mask": (I32, [P, P, P, P, P, U32, U32, P, PU32]),
 }
 
 

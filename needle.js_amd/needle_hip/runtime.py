@@ -185,6 +185,30 @@ class Needle2Resident:
         self._check(st, "nd_needle_step_select")
         return int(out_id.value), float(out_lp.value)
 
+    def grammar_mask(self, masker, state: np.ndarray, budget: int):
+        """nd_needle_grammar_mask: the allowed mask of the grammar state
+        words `state` into the model's mask buffer; returns (the number of
+        allowed pieces, the undecided ids ascending)."""
+        st = np.ascontiguousarray(state, dtype=np.uint32)
+        words = (self.geometry.vocab + 31) // 32
+        und = np.zeros(words, np.uint32)
+        count = C.c_uint32()
+        self._check(self.lib.nd_needle_grammar_mask(self.ctx, self.handle, masker._grammar,
+                                                    masker._pieces, L.ptr(st), st.size,
+                                                    max(0, int(budget)), L.ptr(und),
+                                                    C.byref(count)), "nd_needle_grammar_mask")
+        bits = np.unpackbits(und.view(np.uint8), bitorder="little")[: self.geometry.vocab]
+        return int(count.value), np.flatnonzero(bits).astype(np.uint32)
+
+    def step_selected_mask(self, token: int, settled: Sequence[int] = ()):
+        """stepSelected over the mask buffer plus the `settled` ids."""
+        ids = np.ascontiguousarray(settled, dtype=np.uint32)
+        out_id, out_lp = C.c_uint32(), C.c_double()
+        self._check(self.lib.nd_needle_step_select_mask(
+            self.ctx, self.handle, _token(token), L.ptr(ids) if ids.size else None, ids.size,
+            C.byref(out_id), C.byref(out_lp)), "nd_needle_step_select_mask")
+        return int(out_id.value), float(out_lp.value)
+
     def generate(self, prompt: Sequence[int], max_new_tokens: int, sink: int = 0,
                  eos: Optional[int] = EOS_TOKEN_ID):
         ids = _ids(prompt)
@@ -259,6 +283,15 @@ class Needle2Resident:
             st = self.lib.nd_needle_select_token(self.ctx, self.handle, L.ptr(a), a.size,
                                                  C.byref(out_id), C.byref(out_lp))
         self._check(st, "nd_needle_select_token")
+        return int(out_id.value), float(out_lp.value)
+
+    def select_token_mask(self, settled: Sequence[int] = ()):
+        """selectResidentToken over the mask buffer plus the `settled` ids."""
+        ids = np.ascontiguousarray(settled, dtype=np.uint32)
+        out_id, out_lp = C.c_uint32(), C.c_double()
+        self._check(self.lib.nd_needle_select_token_mask(
+            self.ctx, self.handle, L.ptr(ids) if ids.size else None, ids.size, C.byref(out_id),
+            C.byref(out_lp)), "nd_needle_select_token_mask")
         return int(out_id.value), float(out_lp.value)
 
     def read_lanes(self) -> np.ndarray:
@@ -372,6 +405,14 @@ class SelectedToken:
 
 
 @dataclass(frozen=True)
+class DeviceMaskSelection:
+    """A selection request whose allowed set is the resident model's mask
+    buffer (nd_needle_grammar_mask) plus the host-settled ids."""
+
+    settled: List[int]
+
+
+@dataclass(frozen=True)
 class ResidentEngramRequest:
     """backends/backend.ts:46-50."""
 
@@ -462,7 +503,10 @@ class HipNeedleSession:
 
     def select_resident_token(self, allowed_token_ids: Optional[np.ndarray] = None) -> SelectedToken:
         self._on()
-        token, lp = self.resident.select_token(allowed_token_ids)
+        if isinstance(allowed_token_ids, DeviceMaskSelection):
+            token, lp = self.resident.select_token_mask(allowed_token_ids.settled)
+        else:
+            token, lp = self.resident.select_token(allowed_token_ids)
         return SelectedToken(token, lp)
 
     def resident_layers_enabled(self) -> bool:
@@ -722,6 +766,39 @@ class NeedleRuntime:
             self._selection_request = None
             self._selection_result = None
 
+    def step_constrained(self, token: int, masker, grammar, output_bytes: int = 0,
+                         limit: int = 65536, signal: Optional[AbortSignal] = None) -> SelectedToken:
+        """One step of the constrained agent loop (tools/agent.ts:164-183):
+        stepSelected over the grammar's allowed pieces.  With resident
+        layers the allowed set stays on the device (the grammar mask in the
+        model's mask buffer, its undecided pieces settled by clones of
+        `grammar`); otherwise it is the masker's id list."""
+        if not (self.session and self.session.resident_layers_enabled()):
+            allowed = masker.allowed(grammar, output_bytes, limit)
+            invariant(len(allowed) > 0, "GRAMMAR_DEAD_END",
+                      "No token can continue the schema-constrained tool call")
+            return self.step_selected(token, allowed, signal)
+        count, undecided = self.session.resident.grammar_mask(masker, masker.state(grammar),
+                                                              limit - output_bytes)
+        masker.last_undecided = int(undecided.size)
+        settled = masker.settle(grammar, undecided)
+        invariant(count + len(settled) > 0, "GRAMMAR_DEAD_END",
+                  "No token can continue the schema-constrained tool call")
+        invariant(not self._selection_active, "BACKEND_UNAVAILABLE", "Selection is already active")
+        self._selection_active = True
+        self._selection_request = DeviceMaskSelection(settled)
+        self._selection_result = None
+        try:
+            self.step(token, signal=signal)
+            result = self._selection_result
+            invariant(result is not None, "BACKEND_UNAVAILABLE",
+                      "Token selection did not produce a result")
+            return result
+        finally:
+            self._selection_active = False
+            self._selection_request = None
+            self._selection_result = None
+
     def step(self, token: int, want_logits: bool = True,
              signal: Optional[AbortSignal] = None) -> Optional[np.ndarray]:
         """runtime.ts:280-583."""
@@ -952,6 +1029,22 @@ class ResidentRuntime:
 
     def step_selected(self, token: int, allowed: Optional[np.ndarray] = None):
         return self.resident.step_selected(token, allowed)
+
+    def step_constrained(self, token: int, masker, grammar, output_bytes: int = 0,
+                         limit: int = 65536):
+        """One step of the constrained agent loop (tools/agent.ts:164-183)
+        with the allowed set built on the device: the grammar mask over the
+        model's vocabulary, its undecided pieces settled by clones of
+        `grammar`, then stepSelected over that mask.  (id, log-probability);
+        NeedleError INVALID_CACT "Allowed token set is empty" when nothing
+        is allowed."""
+        count, undecided = self.resident.grammar_mask(masker, masker.state(grammar),
+                                                      limit - output_bytes)
+        masker.last_undecided = int(undecided.size)
+        settled = masker.settle(grammar, undecided)
+        invariant(count + len(settled) > 0, "GRAMMAR_DEAD_END",
+                  "No token can continue the schema-constrained tool call")
+        return self.resident.step_selected_mask(token, settled)
 
     def resolve_confidence(self) -> Optional[float]:
         return self.resident.confidence()
