@@ -370,6 +370,71 @@ def bench_attention(torch, hip, length, heads, steps, warmup, rotate=True):
             "ms_per_call": ms, "GBps": gbs, "frac_hbm": gbs / HBM_PEAK_GBS}
 
 
+def bench_attention_span(torch, hip, length, heads, steps, warmup):
+    """The attention workload of bench_attention (same rotated replicas, same
+    graph timing) through nd_attention_stamped_d: the same launch with each
+    workgroup's thread 0 reading the 100 MHz clock at entry, after its
+    wave's tiles, after the waves' combine, after publishing the chunk's
+    partials, after counting in, and (the merging chunk) after the merge.
+    Per launch of the last replay, relative to its earliest entry: medians
+    over launches of the median and latest workgroup at each point, the
+    latest arrival, the merge's end, and the interval to the next launch."""
+    import ctypes as C
+
+    import numpy as np
+
+    from needle_hip import HipKvCache, synth
+
+    per = attention_bytes(length, heads)
+    replicas = max(1, math.ceil(ROTATE_BYTES / per))
+    st = synth.Stream(7, f"bench-att{length}")
+    K, V = st.normal((length, heads, 64)), st.normal((length, heads, 64))
+    caches = []
+    for _ in range(replicas):
+        kv = HipKvCache(hip, 1, heads, max_length=length)
+        kv.store(0, 0, K, V)
+        caches.append(kv)
+    q = torch.from_numpy(st.normal((heads * 64,))).cuda()
+    out = torch.empty(heads * 64, dtype=torch.float32, device="cuda")
+    launches = max(replicas, 32)
+    cap = 4096
+    stamps = torch.zeros((launches, cap, 8), dtype=torch.int64, device="cuda")
+    wgs = C.c_uint32(0)
+
+    def make(i):
+        kv = caches[i % replicas]
+        return lambda stream: hip._check(hip.lib.nd_attention_stamped_d(
+            hip.ctx, kv.handle, 0, length - 1, q.data_ptr(), heads, out.data_ptr(),
+            stamps[i].data_ptr(), cap, C.byref(wgs), C.c_void_p(stream)))
+
+    timer = GraphTimer(torch, [make(i) for i in range(launches)])
+    ms, _ = timer.time(math.ceil(steps / timer.n), warmup)
+    a = stamps[:, :wgs.value, :].cpu().numpy()
+    for kv in caches:
+        kv.free()
+    t0 = a[:, :, 0].min(axis=1)
+    rel = (a[:, :, :6] - t0[:, None, None]) * 0.01  # microseconds after the launch's first entry
+    merged = a[:, :, 6] == 1
+    names = ["entry", "tiles_done", "combined", "published", "counted"]
+    out_d = {"workgroups": wgs.value, "launches": int(launches), "events_ms_per_launch": ms}
+    for i, nm in enumerate(names):
+        out_d[f"{nm}_us_median_wg"] = float(np.median(np.median(rel[:, :, i], axis=1)))
+        out_d[f"{nm}_us_last_wg"] = float(np.median(rel[:, :, i].max(axis=1)))
+    merge_end = np.where(merged, rel[:, :, 5], 0).max(axis=1)
+    out_d["merge_end_us"] = float(np.median(merge_end))
+    out_d["merges_per_launch"] = float(np.median(merged.sum(axis=1)))
+    # per merging chunk: its own arrival to its merge end
+    gap = np.where(merged, rel[:, :, 5] - rel[:, :, 4], np.nan)
+    out_d["merge_phase_us_median"] = float(np.nanmedian(gap))
+    out_d["publish_phase_us_median"] = float(np.median(rel[:, :, 3] - rel[:, :, 2]))
+    out_d["count_phase_us_median"] = float(np.median(rel[:, :, 4] - rel[:, :, 3]))
+    out_d["combine_phase_us_median"] = float(np.median(rel[:, :, 2] - rel[:, :, 1]))
+    out_d["tiles_phase_us_median"] = float(np.median(rel[:, :, 1] - rel[:, :, 0]))
+    out_d["launch_interval_us_median"] = float(np.median(np.diff(t0) * 0.01))
+    out_d["xcc_ok"] = bool(np.all(a[:, :, 7] == (np.arange(wgs.value) % 8)[None, :]))
+    return out_d
+
+
 def decoder_weight_bytes(g):
     """int8 codes + f32 per-row scales read by one decode step (tied lm head)."""
     per_layer = [(g.heads + 2 * g.kv_heads) * 64 * g.dim, g.dim * g.heads * 64, g.ffn * g.dim,
@@ -867,7 +932,8 @@ def main():
     ap.add_argument("--needle2-reps", type=int, default=5)
     ap.add_argument("--only", choices=["matvec", "matvec8", "attention", "decode", "prefill",
                                        "needle2", "needle2cq", "needle2mixed", "traffic", "attention_traffic", "cq",
-                                       "grammar", "ceiling", "matvec_span", "copy_matvec"],
+                                       "grammar", "ceiling", "matvec_span", "copy_matvec",
+                                       "attention_span"],
                     help="run one part alone and print its JSON (for profiling)")
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--no-check", action="store_true",
@@ -909,6 +975,8 @@ def main():
             part = attention_traffic_workload(torch, hip)
         elif args.only == "matvec_span":
             part = bench_matvec_span(torch, hip, n, k, g, args.steps, args.warmup)
+        elif args.only == "attention_span":
+            part = bench_attention_span(torch, hip, 8192, 8, args.steps, args.warmup)
         elif args.only == "copy_matvec":
             part = bench_copy_ceiling(torch, matvec_bytes(n, k, g, 1), args.steps, args.warmup)
         elif args.only == "grammar":

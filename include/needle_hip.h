@@ -243,6 +243,21 @@ nd_status nd_attention(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t po
 nd_status nd_attention_d(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t position,
                          const float* q_dev, uint32_t q_heads, float* out_dev, void* stream);
 
+/* Measurement, no counterpart in the reference: nd_attention_d's own launch
+ * when it takes the XCD-local form with one tile per wave (8 heads x 8192
+ * positions does), with thread 0 of each workgroup L reading the GPU's
+ * 100 MHz constant clock at entry, after its wave's tiles, after the waves'
+ * combine, once the chunk's partials are published, once its arrival is
+ * counted and, for the chunk that merges, after the merge, written with
+ * the chunk's role (0 counted in, 1 merged) and its XCC id to
+ * stamps_dev[8 L .. 8 L + 7].  The workgroup count goes to *workgroups;
+ * another launch form, or more than `capacity` workgroups, is
+ * ND_ERR_UNSUPPORTED with nothing launched. */
+nd_status nd_attention_stamped_d(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t position,
+                                 const float* q_dev, uint32_t q_heads, float* out_dev,
+                                 uint64_t* stamps_dev, uint32_t capacity, uint32_t* workgroups,
+                                 void* stream);
+
 /* nd_attention_d without any allocation, for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  No counterpart in the reference.  Identical

@@ -807,6 +807,33 @@ nd_status nd_attention_d(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t 
   return ND_OK;
 }
 
+nd_status nd_attention_stamped_d(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t position,
+                                 const float* q, uint32_t q_heads, float* out, uint64_t* stamps,
+                                 uint32_t capacity, uint32_t* workgroups, void* stream) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  nd_status st = check_attention(ctx, kv, layer, position, q_heads);
+  if (st != ND_OK) return st;
+  if (!q || !out || !stamps || !workgroups || (reinterpret_cast<uintptr_t>(q) & 15))
+    return nd_fail(ctx, ND_ERR_INVALID,
+                   "nd_attention_stamped_d: a 16-byte aligned q, out, stamps and workgroups");
+  const nd_visible vis = nd_kv_visible(kv, position);
+  const size_t need = nd_attention_partial_floats(q_heads, kv->kv_heads, vis.count);
+  if (need > ctx->attn_partial_floats)
+    return nd_fail(ctx, ND_ERR_INVALID, "attention partials too small (%zu > %zu floats)", need,
+                   ctx->attn_partial_floats);
+  *workgroups = 0;
+  const hipError_t e =
+      nd_launch_attention(kv, layer, position, q, q_heads, out, ctx->attn_partials,
+                          ctx->attn_counters, nd_pick_stream(ctx, stream), stamps, capacity,
+                          workgroups);
+  if (e == hipErrorInvalidValue)
+    return nd_fail(ctx, ND_ERR_UNSUPPORTED,
+                   "nd_attention_stamped_d: only the XCD-local one-tile form is stamped, and "
+                   "%u workgroups need room for as many stamps (%u)", *workgroups, capacity);
+  ND_HIP(ctx, e);
+  return ND_OK;
+}
+
 nd_status nd_attention_static_d(nd_ctx* ctx, const nd_kv* kv, uint32_t layer, uint32_t position,
                                 const float* q, uint32_t q_heads, float* out, void* stream) {
   if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");

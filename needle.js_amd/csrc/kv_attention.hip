@@ -100,6 +100,8 @@ __device__ __forceinline__ Visible visible_at(uint32_t position, uint32_t sink, 
   return v;
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 template <bool F32>
 struct Tile {
   // Raw codes (or floats) of 4 positions x 16 dims for K and V, plus scales.
@@ -151,8 +153,14 @@ __device__ __forceinline__ void load_tile(Tile<F32>& tl, const void* Kc, const v
         tl.v[4 * k + c] = vp[c];
       }
     } else {
-      tl.k[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const int8_t*>(Kc) + row * kHeadDim + quad * 16);
-      tl.v[k] = *reinterpret_cast<const uint4*>(reinterpret_cast<const int8_t*>(Vc) + row * kHeadDim + quad * 16);
+      // Codes are read once per call: non-temporal loads (6.35 against
+      // 7.02 us per call at 8 heads x 8192 positions).
+      const u32x4 kk = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+          reinterpret_cast<const int8_t*>(Kc) + row * kHeadDim + quad * 16));
+      const u32x4 vv = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+          reinterpret_cast<const int8_t*>(Vc) + row * kHeadDim + quad * 16));
+      tl.k[k] = make_uint4(kk[0], kk[1], kk[2], kk[3]);
+      tl.v[k] = make_uint4(vv[0], vv[1], vv[2], vv[3]);
     }
   }
 }
@@ -205,7 +213,13 @@ __device__ __forceinline__ float gate_factor(float g) { return 1.f / (1.f + __ex
 // row r is query z0 + r / G (z0 = (REP / G) blockIdx.z, rows at or past
 // `qrows` absent), head G blockIdx.y + r % G, with its own causal limit --
 // so every K/V tile is read once for all of them.
-template <int REP, bool F32, bool QB = false, int KW = 4, int TILES = 0, bool XL = false>
+// STAMP (measurement only): thread 0 reads the 100 MHz constant clock at
+// entry, after its wave's tiles, after the waves' combine, once the chunk's
+// partials are published, once its arrival is counted and (the last chunk)
+// after the merge, and writes them with the chunk's role (0 counted in,
+// 1 merged) and its XCC id to stamps[8 L .. 8 L + 7] for workgroup L.
+template <int REP, bool F32, bool QB = false, int KW = 4, int TILES = 0, bool XL = false,
+          bool STAMP = false>
 __global__ __launch_bounds__(64 * KW) void attention_kernel(
     const void* __restrict__ Kc, const void* __restrict__ Vc, const float* __restrict__ Ks,
     const float* __restrict__ Vs, const float* __restrict__ Q, float* __restrict__ out,
@@ -216,7 +230,20 @@ __global__ __launch_bounds__(64 * KW) void attention_kernel(
     const uint32_t* __restrict__ positions, uint32_t slot_space, uint32_t seq_kv_heads,
     uint32_t kv_stride_z,
     uint32_t chunk_positions, uint32_t max_chunks, float score_scale, uint32_t qrows,
-    uint32_t qgroup) {
+    uint32_t qgroup, uint64_t* __restrict__ stamps) {
+  uint64_t stamp[6] = {};
+  if constexpr (STAMP) stamp[0] = wall_clock64();
+  auto put_stamps = [&](uint32_t role) {
+    if constexpr (STAMP) {
+      if (threadIdx.x == 0) {
+        uint64_t* o = stamps + 8 * (size_t)blockIdx.x;
+#pragma unroll
+        for (int i = 0; i < 6; ++i) o[i] = stamp[i];
+        o[6] = role;
+        o[7] = (uint32_t)__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15u;
+      }
+    }
+  };
   // z indexes query rows: sequences of a batch (kv_stride_z = seq_kv_heads,
   // each with its own cache heads) or positions of one prefill (kv_stride_z
   // = 0, all reading the same cache heads).
@@ -411,6 +438,7 @@ __global__ __launch_bounds__(64 * KW) void attention_kernel(
       }
     }
   }
+  if constexpr (STAMP) stamp[1] = wall_clock64();
 
   // Per wave: fold the 16 token rows of each lane's partial sums 4 apart
   // (lane bits 2..3) with DPP, leaving 4 row groups (lane bits 4..5) that go
@@ -438,6 +466,7 @@ __global__ __launch_bounds__(64 * KW) void attention_kernel(
     }
   }
   __syncthreads();
+  if constexpr (STAMP) stamp[2] = wall_clock64();
 
   // Combine the waves: kT consecutive threads share output o (REP <= 2), each
   // summing KW * 4 / kT rows scaled by exp(m_wave - max); REP >= 4 gives
@@ -529,6 +558,7 @@ __global__ __launch_bounds__(64 * KW) void attention_kernel(
   }
   __builtin_amdgcn_s_waitcnt(0);  // every store above has completed
   __syncthreads();
+  if constexpr (STAMP) stamp[3] = wall_clock64();
   // Election: rows of more than kChunkGroup chunks count in per group first
   // and the last of each group then on the row's counter, so that no counter
   // serializes more than kChunkGroup arrivals (agent-scope atomics on one
@@ -555,7 +585,11 @@ __global__ __launch_bounds__(64 * KW) void attention_kernel(
     s_last = last;
   }
   __syncthreads();
-  if (!s_last) return;
+  if constexpr (STAMP) stamp[4] = wall_clock64();
+  if (!s_last) {
+    put_stamps(0);
+    return;
+  }
 
   // Last chunk: wave w merges head w / kWph over chunks c = w % kWph + kWph j
   // (REP < KW) or heads w, w + KW, ... over all chunks.  Lane c holds
@@ -625,6 +659,11 @@ __global__ __launch_bounds__(64 * KW) void attention_kernel(
     }
   }
   if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, kPubScope);
+  if constexpr (STAMP) {
+    __builtin_amdgcn_s_waitcnt(0);  // the outputs are stored
+    stamp[5] = wall_clock64();
+  }
+  put_stamps(1);
 }
 
 // Positions per chunk: the whole visible range when the (row, kv head) pairs
@@ -675,6 +714,9 @@ struct AttnLaunch {
   uint32_t batch;
   uint32_t max_count;          // bound on every sequence's visible count
   bool qblock;                 // query blocks of a prefill whose positions see [0, position]
+  uint64_t* stamps;            // measurement form: 8 stamps per workgroup, or nullptr
+  uint32_t stamp_capacity;     // workgroups the stamps hold
+  uint32_t* stamp_workgroups;  // out: workgroups launched
 };
 
 // Causal prefill attention on MFMA (a prefill whose positions all see [0,
@@ -1013,7 +1055,7 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
                          a.out, a.gate, a.gate_ld, nullptr, nullptr, nullptr, a.layer,
                          a.kv->kv_heads, a.kv->alloc, a.kv->sink, a.kv->window, a.vis,
                          a.positions, 0u, a.seq_kv_heads, 0u, a.max_count, 1u, 0.125f, a.batch,
-                         (uint32_t)REP);
+                         (uint32_t)REP, nullptr);
       return hipGetLastError();
     }
   }
@@ -1038,6 +1080,7 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
     const uint32_t cp2 = chunk_positions_for(a.max_count, a.seq_kv_heads, kTargetSingle, kHalf);
     const uint32_t mc2 = (a.max_count + cp2 - 1) / cp2;
     if (cp2 == kHalf && mc2 <= kMaxChunks) {
+      if (a.stamps) return hipErrorInvalidValue;  // no measurement form of the two-wave kernel
       float* pm2 = a.partials + (size_t)hq * mc2 * kHeadDim;
       const uint32_t gpx = (a.seq_kv_heads + 7) / 8;
       hipLaunchKernelGGL((attention_kernel<REP, F32, false, 2, 1, true>), dim3(8 * gpx * mc2),
@@ -1045,7 +1088,7 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
                          a.gate, a.gate_ld, part_acc, pm2, a.counters, a.layer, a.kv->kv_heads,
                          a.kv->alloc, a.kv->sink, a.kv->window, a.vis, a.positions,
                          a.slot_space, a.seq_kv_heads, a.kv_stride_z, cp2, mc2, 0.125f, a.batch,
-                         1u);
+                         1u, nullptr);
       return hipGetLastError();
     }
   }
@@ -1056,13 +1099,19 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
                   : tiles == 2 ? attention_kernel<REP, F32, false, kWaves, 2, true>
                                : attention_kernel<REP, F32, false, kWaves, 0, true>;
     const uint32_t gpx = (a.batch * a.seq_kv_heads + 7) / 8;
+    if (a.stamps) {  // the measurement form of the same launch (one tile per wave)
+      if (tiles != 1 || 8 * gpx * max_chunks > a.stamp_capacity) return hipErrorInvalidValue;
+      kernel = attention_kernel<REP, F32, false, kWaves, 1, true, true>;
+      *a.stamp_workgroups = 8 * gpx * max_chunks;
+    }
     hipLaunchKernelGGL(kernel, dim3(8 * gpx * max_chunks), dim3(64 * kWaves), 0, s, a.kv->k,
                        a.kv->v, a.kv->ks, a.kv->vs, a.q, a.out, a.gate, a.gate_ld, part_acc,
                        part_ml, a.counters, a.layer, a.kv->kv_heads, a.kv->alloc, a.kv->sink,
                        a.kv->window, a.vis, a.positions, a.slot_space, a.seq_kv_heads,
-                       a.kv_stride_z, cp, max_chunks, 0.125f, a.batch, 1u);
+                       a.kv_stride_z, cp, max_chunks, 0.125f, a.batch, 1u, a.stamps);
     return hipGetLastError();
   }
+  if (a.stamps) return hipErrorInvalidValue;
   auto kernel = tiles == 1   ? attention_kernel<REP, F32, false, kWaves, 1>
                 : tiles == 2 ? attention_kernel<REP, F32, false, kWaves, 2>
                              : attention_kernel<REP, F32, false, kWaves, 0>;
@@ -1071,7 +1120,7 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
                      a.gate, a.gate_ld, part_acc, part_ml, a.counters, a.layer, a.kv->kv_heads, a.kv->alloc,
                      a.kv->sink, a.kv->window, a.vis, a.positions, a.slot_space, a.seq_kv_heads,
                      a.kv_stride_z,
-                     cp, max_chunks, 0.125f, a.batch, 1u);
+                     cp, max_chunks, 0.125f, a.batch, 1u, nullptr);
   return hipGetLastError();
 }
 
@@ -1175,9 +1224,13 @@ hipError_t nd_launch_kv_store(const nd_kv* kv, uint32_t layer, uint32_t position
 
 hipError_t nd_launch_attention(const nd_kv* kv, uint32_t layer, uint32_t position,
                                const float* q, uint32_t q_heads, float* out, float* partials,
-                               uint32_t* counters, hipStream_t s) {
+                               uint32_t* counters, hipStream_t s, uint64_t* stamps,
+                               uint32_t stamp_capacity, uint32_t* stamp_workgroups) {
   const nd_visible nv = nd_kv_visible(kv, position);
   AttnLaunch a{};
+  a.stamps = stamps;
+  a.stamp_capacity = stamp_capacity;
+  a.stamp_workgroups = stamp_workgroups;
   a.kv = kv;
   a.layer = layer;
   a.q = q;

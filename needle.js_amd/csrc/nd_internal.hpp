@@ -170,9 +170,14 @@ constexpr uint32_t kMaxAttentionPositions = 262144;
 
 hipError_t nd_launch_kv_store(const nd_kv* kv, uint32_t layer, uint32_t position, uint32_t first,
                               uint32_t count, const float* k, const float* v, hipStream_t s);
+// stamps (measurement form, the XCD-local one-tile launch only): 8 clock
+// stamps per workgroup, room for stamp_capacity workgroups; the launch's
+// workgroup count goes to *stamp_workgroups (hipErrorInvalidValue when the
+// launch takes another form or does not fit).
 hipError_t nd_launch_attention(const nd_kv* kv, uint32_t layer, uint32_t position,
                                const float* q, uint32_t q_heads, float* out, float* partials,
-                               uint32_t* counters, hipStream_t s);
+                               uint32_t* counters, hipStream_t s, uint64_t* stamps = nullptr,
+                               uint32_t stamp_capacity = 0, uint32_t* stamp_workgroups = nullptr);
 hipError_t nd_launch_select_list(const float* logits, uint32_t vocab, const uint32_t* allowed,
                                  uint32_t count, uint32_t* id, double* logprob, hipStream_t s);
 // `split`: nd_select_split_bytes(batch) of device memory, zero when first

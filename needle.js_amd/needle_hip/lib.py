@@ -81,6 +81,7 @@ SIGNATURES = {
     "nd_kv_read": (I32, [P, P, U32, U32, P, P, P, P]),
     "nd_attention": (I32, [P, P, U32, U32, P, U32, P]),
     "nd_attention_d": (I32, [P, P, U32, U32, P, U32, P, P]),
+    "nd_attention_stamped_d": (I32, [P, P, U32, U32, P, U32, P, P, U32, PU32, P]),
     "nd_attention_static_d": (I32, [P, P, U32, U32, P, U32, P, P]),
     "nd_select": (I32, [P, P, U32, P, U32, PU32, C.POINTER(C.c_double)]),
     "nd_select_mask_d": (I32, [P, P, U32, U32, P, P, P, P]),
