@@ -25,6 +25,7 @@
 #include <vector>
 
 #include "nd_cq.hpp"
+#include "nd_attention.hpp"
 #include "nd_internal.hpp"
 #include "nd_wave.hpp"
 
@@ -670,6 +671,7 @@ __device__ __forceinline__ float2 cq_rows_pair(const CqRows& q, size_t row0, uin
 constexpr uint32_t kWoSpin = 1u << 16;
 constexpr uint32_t kStatusWoWait = 1u;   // the mix's wait for the Wo rows
 constexpr uint32_t kStatusQkvWait = 2u;  // a projection workgroup's wait for the mix
+constexpr uint32_t kStatusAttWait = 4u;  // an attention workgroup's wait for the projection
 // The mix's signal to the projection workgroups: 1 once its outputs are in
 // the L2, or kFlagAbort | 1 when it gave up (they then skip their stores).
 // The low 16 bits count the workgroups that have seen it.
@@ -720,10 +722,14 @@ __device__ __forceinline__ float2 cq_rows_dot_any(uint32_t bits, const CqRows& q
 // A workgroup whose wait runs out sets kStatusQkvWait in *status; one that
 // finds kFlagAbort (the mix gave up) counts itself in; both return without
 // storing anything.
+//
+// att_count (inside the fused launch that also runs layer l's attention):
+// every head workgroup counts itself in once its stores (q, the cache row,
+// the gate) have completed, or with kFlagAbort when it stores nothing.
 template <bool CQ, bool WAIT>
 __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_t* flag,
                                          uint32_t waiters, uint32_t* status = nullptr,
-                                         uint32_t spin = 0) {
+                                         uint32_t spin = 0, uint32_t* att_count = nullptr) {
   __shared__ float xs[512 + 16];
   __shared__ float rows[64];
   __shared__ float s_cb[16];
@@ -757,6 +763,14 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
     }
     return true;
   };
+  auto count_in = [&](bool stored) {
+    if (att_count) {
+      if (!stored)
+        __hip_atomic_fetch_or(att_count, kFlagAbort, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_WORKGROUP);
+      __hip_atomic_fetch_add(att_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  };
   if (b == 2 * (p.heads + p.kv_heads)) {
     if (!wait()) return;
     route_wave(p.route, t, rows);
@@ -771,7 +785,10 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
     i32x4 wv[kQkvLoads];
     qkv_row_loads(p.W, row, t % kQkvTpr, d, wv);
     const float srow = p.S[row];
-    if (!wait()) return;
+    if (!wait()) {
+      if (t == 0) count_in(false);
+      return;
+    }
     for (uint32_t i = t; i < d; i += kQkvWg) xs[i] = p.x[i];
     __syncthreads();
     const float acc = qkv_row_dot(wv, xs, t % kQkvTpr, d);
@@ -807,7 +824,10 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
       for (int i = 0; i < 16; ++i)
         s_cb[i] = pick(p.cq[0].cb[i], p.cq[1].cb[i], p.cq[2].cb[i], p.cq[3].cb[i]);
     }
-    if (!wait()) return;
+    if (!wait()) {
+      if (t == 0) count_in(false);
+      return;
+    }
     for (uint32_t i = t; i < kpad; i += kQkvWg) xs[i + (i >> 5)] = i < d ? p.x[i] : 0.f;
     __syncthreads();
     const float2 v = cq_rows_dot_any(bits, q, R, kpad / 32, xs, s_cb, t);
@@ -825,6 +845,10 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
   const uint32_t nq = p.heads, nk = p.kv_heads;
   if (b >= nq + 2 * nk) {  // gate head
     p.gate_out[(size_t)(b - nq - 2 * nk) * kHd + lane] = val;
+    if (att_count) {
+      __builtin_amdgcn_s_waitcnt(0);  // the wave's stores have completed
+      if (lane == 0) count_in(true);
+    }
     return;
   }
   const int role = b < nq ? 0 : (b < nq + nk ? 1 : 2);
@@ -832,6 +856,10 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
   head_epilogue(val, lane, role, rs, rc, nscale, p.q_out + (size_t)h * kHd, p.Kc, p.Vc, p.Ks, p.Vs,
                 ((size_t)p.layer * nk + h) * p.alloc, kv_slot(pos, p.sink, p.window), p.alloc,
                 p.f32);
+  if (att_count) {
+    __builtin_amdgcn_s_waitcnt(0);  // the wave's stores have completed
+    if (lane == 0) count_in(true);
+  }
 }
 
 template <bool CQ>
@@ -883,6 +911,22 @@ template <uint32_t BITS>
 __global__ __launch_bounds__(kMixWg) void n2_wo_cq_kernel(WoCq w) {
   wo_cq_rows<BITS>(w, blockIdx.x, nullptr);
 }
+
+// Layer l's attention inside the fused launch (n2_mix_kernel<*, true>):
+// the gated single-chunk attention of nd_launch_attention_gated over an
+// int8 cache whose ring fits one 512-position chunk, two query heads per KV
+// head -- the same attention_body instance, so the same bits.
+struct AttArgs {
+  const void* Kc;
+  const void* Vc;
+  const float* Ks;
+  const float* Vs;
+  const float* q;
+  float* out;
+  const float* gate;
+  const uint32_t* position;
+  uint32_t layer, kv_heads, alloc, sink, window;
+};
 
 struct MixArgs {
   float* x;  // [lanes][d]: read, and rewritten when has_post
@@ -970,6 +1014,13 @@ struct MixArgs {
   // wo_groups workgroups of wo_cq_rows, codes of wo_bits bits.
   WoCq wo_cq;
   uint32_t wo_bits;
+  // ... and layer l's attention: att_groups workgroups (one per KV head)
+  // after the projection, each waiting until att_target projection
+  // workgroups have counted in on att_count; they count themselves in
+  // after the wait and the last clears the count.
+  AttArgs att;
+  uint32_t att_groups, att_target;
+  uint32_t* att_count;
 };
 
 // Rows [rpw k, +rpw) of proj = Wo att in the fused Wo + mix launch, rpw =
@@ -1277,14 +1328,53 @@ constexpr int kPhiPairs = 8;
 // PU (Cactus-Quant): phi_pre, phi_post and phi_res share one format (width,
 // group, codebook), so one rotation and one width dispatch serve every row;
 // otherwise each row takes its own matrix's format.
+// Attention workgroup ah (KV head ah) of the fused launch: wait until every
+// projection head workgroup has counted in (q, this position's cache rows
+// and the gate are in the XCD's L2), count in (the last clears the count),
+// then the gated attention of the KV head with nd_launch_attention_gated's
+// instance and arguments for a ring of at most kGatedChunk positions.  A
+// wait that runs out sets kStatusAttWait; an abort from the projection
+// stores nothing.
+__device__ __forceinline__ void attention_role(const MixArgs& a, uint32_t ah) {
+  __shared__ uint32_t s_att_go;
+  if (threadIdx.x == 0) {
+    bool go = true;
+    uint32_t it = 0, v;
+    while (((v = __hip_atomic_load(a.att_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) &
+            kFlagCount) < a.att_target &&
+           !(v & kFlagAbort)) {
+      if (++it >= a.spin) {
+        __hip_atomic_fetch_or(a.status, kStatusAttWait, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+        go = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (v & kFlagAbort) go = false;
+    if ((__hip_atomic_fetch_add(a.att_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) &
+         kFlagCount) == a.att_target + a.att_groups - 1)
+      __hip_atomic_store(a.att_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    s_att_go = go;
+  }
+  __syncthreads();
+  if (!s_att_go) return;
+  const AttArgs& g = a.att;
+  nd::att::attention_body<2, false, false, kMixWg / 64, 1, false, false, false>(
+      0u, ah, 0u, g.Kc, g.Vc, g.Ks, g.Vs, g.q, g.out, g.gate, 0u, nullptr, nullptr, nullptr,
+      g.layer, g.kv_heads, g.alloc, g.sink, g.window,
+      nd::att::Visible{g.alloc, g.alloc, g.alloc}, g.position, 1u, g.kv_heads, 0u,
+      nd::att::kGatedChunk, 1u, 0.125f, 1u, 1u, nullptr);
+}
+
 template <bool CQ, bool WO = false, bool PU = true>
 __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   static_assert(kQkvWg == kMixWg, "the fused projection runs on mix-sized workgroups");
   if constexpr (WO) {
     // Workgroups L % 8 == 0 only (one XCD): L / 8 < wo_groups computes Wo
     // rows, L / 8 == wo_groups (dispatched after all of them) runs the mix,
-    // the qkv_groups after it the projection.  Each waits only on workgroups
-    // dispatched before it.
+    // the qkv_groups after it the projection, the att_groups after those
+    // the attention.  Each waits only on workgroups dispatched before it.
     if (blockIdx.x & 7) return;
     const uint32_t k = blockIdx.x >> 3;
     if (k < a.wo_groups) {
@@ -1303,7 +1393,10 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     if (k > a.wo_groups) {
       const uint32_t qb = k - a.wo_groups - 1;
       if (qb < a.qkv_groups) {
-        qkv_body<CQ, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups, a.status, a.spin);
+        qkv_body<CQ, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups, a.status, a.spin,
+                           a.att_groups ? a.att_count : nullptr);
+      } else if (qb - a.qkv_groups < a.att_groups) {
+        attention_role(a, qb - a.qkv_groups);
       }
       return;
     }
@@ -2116,7 +2209,9 @@ struct nd_needle {
   // word t / 32 (nd_needle_grammar_mask fills it; the _mask calls add the
   // ids the host accepted among the undecided ones).
   uint32_t* mask = nullptr;
-  uint32_t* wo_count = nullptr;  // arrivals of the fused Wo launch (a line of its own)
+  // arrivals of the fused launch's Wo rows (word 0) and projection heads
+  // (word 32): a 128-byte line each
+  uint32_t* wo_count = nullptr;
   uint32_t* qkv_flags = nullptr;  // per layer: the fused launch's mix-done flag
   // Give-ups of the fused launch's bounded waits (kStatus* bits; a line of
   // its own, cleared by reset), its pinned host copy, and the test hook's
@@ -2265,11 +2360,30 @@ QkvParams qkv_params(const nd_needle* n, uint32_t l);
 bool wo_cq_fits(const nd_mat& w);
 WoCq wo_cq_of(const nd_needle* n, const nd_mat& w);
 
+// Whether layer attention can run inside the fused launch: an int8 cache
+// whose ring fits the gated attention's one chunk, two query heads per KV
+// head (attention_role's instance).
+bool att_fusable(const nd_needle* n) {
+  return n->kv.mode == ND_KV_INT8 && n->d.heads == 2 * n->d.kv_heads &&
+         n->kv.alloc <= nd::att::kGatedChunk;
+}
+
+// Layer l's attention in the fused launch (attention_role), with the
+// arguments nd_launch_attention_gated gives its kernel.
+void set_att(nd_needle* n, uint32_t l, MixArgs& m) {
+  m.att = AttArgs{n->kv.k, n->kv.v, n->kv.ks, n->kv.vs, n->q, n->att, n->qkvg, n->st + 1,
+                  l, n->d.kv_heads, n->kv.alloc, n->kv.sink, n->kv.window};
+  m.att_groups = n->d.kv_heads;
+  m.att_target = m.qkv_groups - 1;  // every projection workgroup but the routing
+  m.att_count = n->wo_count + 32;
+}
+
 // wo: for an int8 model, layer l - 1's Wo (with the post half) and layer
 // l's projection (with the pre half) run in the same launch
-// (n2_mix_kernel<false, true>) instead of beside the attention.
+// (n2_mix_kernel<false, true>) instead of beside the attention; att (with
+// qkv): layer l's attention too.
 hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, bool wo = false,
-                       bool qkv = false) {
+                       bool qkv = false, bool att = false) {
   const bool has_post = parts & kMixPost;
   const nd_needle_desc& d = n->d;
   const uint32_t D = d.dim, ln = d.lanes;
@@ -2327,13 +2441,13 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, 
       m.qkv = qkv_params(n, l);
       m.qkv_groups = n->wqkvg[l].n / kHd + 1;
       m.qkv_flag = n->qkv_flags + 32 * (size_t)l;
+      if (att) set_att(n, l, m);
     }
+    const dim3 grid(8 * (m.wo_groups + 1 + m.qkv_groups + m.att_groups));
     if (n->phi_uniform)
-      hipLaunchKernelGGL((n2_mix_kernel<true, true, true>),
-                         dim3(8 * (m.wo_groups + 1 + m.qkv_groups)), dim3(kMixWg), 0, s, m);
+      hipLaunchKernelGGL((n2_mix_kernel<true, true, true>), grid, dim3(kMixWg), 0, s, m);
     else
-      hipLaunchKernelGGL((n2_mix_kernel<true, true, false>),
-                         dim3(8 * (m.wo_groups + 1 + m.qkv_groups)), dim3(kMixWg), 0, s, m);
+      hipLaunchKernelGGL((n2_mix_kernel<true, true, false>), grid, dim3(kMixWg), 0, s, m);
   } else if (n->cq) {
     if (n->phi_uniform)
       hipLaunchKernelGGL((n2_mix_kernel<true, false, true>), dim3(1), dim3(kMixWg), 0, s, m);
@@ -2357,9 +2471,11 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, 
       m.qkv = qkv_params(n, l);
       m.qkv_groups = n->wqkvg[l].n / kHd + 1;
       m.qkv_flag = n->qkv_flags + 32 * (size_t)l;
+      if (att) set_att(n, l, m);
     }
-    hipLaunchKernelGGL((n2_mix_kernel<false, true>), dim3(8 * (m.wo_groups + 1 + m.qkv_groups)),
-                       dim3(kMixWg), 0, s, m);
+    hipLaunchKernelGGL((n2_mix_kernel<false, true>),
+                       dim3(8 * (m.wo_groups + 1 + m.qkv_groups + m.att_groups)), dim3(kMixWg),
+                       0, s, m);
   } else {
     hipLaunchKernelGGL(n2_mix_kernel<false>, dim3(1), dim3(kMixWg), 0, s, m);
   }
@@ -2647,8 +2763,11 @@ hipError_t enqueue_step(nd_needle* n, uint32_t source, uint32_t token, bool want
     const bool fuse = nd_xcd_local() &&
                       (n->cq ? n->wo_fused
                              : (wo_tpr & (wo_tpr - 1)) == 0 && wo_tpr <= (uint32_t)kMixWg);
-    if ((e = enqueue_mix(n, l, parts, s, fuse, fuse)) != hipSuccess) return e;
+    // ... and layer l's attention too when its ring fits one chunk.
+    const bool att = fuse && att_fusable(n);
+    if ((e = enqueue_mix(n, l, parts, s, fuse, fuse, att)) != hipSuccess) return e;
     if (!pre) break;
+    if (att) continue;
     if ((e = enqueue_block(n, l, s, !fuse, !fuse)) != hipSuccess) return e;
   }
   return enqueue_final(n, tail, select, allowed, count, s, mask);
@@ -2968,11 +3087,13 @@ nd_status check_waits(nd_ctx* ctx, const nd_needle* n) {
   const uint32_t v = *n->status_host;
   if (!v) return ND_OK;
   return nd_fail(ctx, ND_ERR_BACKEND,
-                 "a bounded wait inside a fused layer launch ran out (%s%s%s): the results of "
-                 "this call are not valid, and every whole-step call fails until reset()",
+                 "a bounded wait inside a fused layer launch ran out (%s%s%s%s%s): the results "
+                 "of this call are not valid, and every whole-step call fails until reset()",
                  v & kStatusWoWait ? "the layer mix waiting for the output projection rows" : "",
-                 (v & kStatusWoWait) && (v & kStatusQkvWait) ? "; " : "",
-                 v & kStatusQkvWait ? "the projection waiting for the layer mix" : "");
+                 (v & kStatusWoWait) && (v & (kStatusQkvWait | kStatusAttWait)) ? "; " : "",
+                 v & kStatusQkvWait ? "the projection waiting for the layer mix" : "",
+                 (v & kStatusQkvWait) && (v & kStatusAttWait) ? "; " : "",
+                 v & kStatusAttWait ? "the attention waiting for the projection" : "");
 }
 
 // One reset is driven either by whole-step calls or by the session methods:
@@ -3310,7 +3431,7 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     const size_t P8 = kMaxProbes * 8, cb = n->conf ? 1 : 0;
     const size_t sizes[] = {al(64), al((size_t)cap * 4), al((size_t)cap * 8),
                             al((size_t)S * n->depth * D * 4),
-                            al((size_t)d.kv_heads * kAttnCounterStride * 4), al(128),
+                            al((size_t)d.kv_heads * kAttnCounterStride * 4), al(256),
                             al((size_t)d.layers * 128), al(128),
                             cb * al(P8 * kMaxChunks), cb * al(P8 * kMaxChunks),
                             cb * al(P8 * D), al(64), al(64),
