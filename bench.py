@@ -435,6 +435,59 @@ def bench_attention_span(torch, hip, length, heads, steps, warmup):
     return out_d
 
 
+def bench_needle2_span(torch, hip, steps):
+    """Needle 2 at the shipped geometry (int8), batch 1, after a 128-token
+    prompt: `steps` direct whole-step calls with the fused layer launches in
+    their measurement form (nd_needle_test_stamps).  Per layer launch of the
+    last step, microseconds after its first workgroup's entry: the Wo rows
+    done, the mix's Wo wait over, the mix's signal to the projection, the
+    projection done, the attention done, the launch's last exit; and the gap
+    from that exit to the next launch's first entry.  Medians over layers."""
+    import numpy as np
+
+    from needle_hip import NeedleModel, synth
+    from needle_hip.needle2 import Needle2Geometry, Needle2Weights
+
+    g = Needle2Geometry()
+    model = NeedleModel(hip, Needle2Weights(g, 2026))
+    rt = model.create_resident_runtime()
+    prompt = synth.Stream(2026, "needle2.prompt").integers(128, 0, g.vocab - 1)
+    rt.reset(len(prompt) + steps + 1, 0)
+    rt.prefill(prompt)
+    cap = (g.layers + 1) * 64 * 4
+    stamps = torch.zeros(cap, dtype=torch.int64, device="cuda")
+    res = model.resident
+    hip._check(hip.lib.nd_needle_test_stamps(hip.ctx, res.handle, stamps.data_ptr(), cap))
+    tok = int(prompt[-1])
+    for _ in range(steps):
+        rt.step(tok, want_logits=False)
+    torch.cuda.synchronize()
+    a = stamps.view(g.layers + 1, 64, 4).cpu().numpy().astype(np.int64)
+    hip._check(hip.lib.nd_needle_test_stamps(hip.ctx, res.handle, None, 0))
+    model.dispose()
+    W = g.dim // (512 // (g.heads * 64 // 16))  # Wo workgroups (16 rows each at d 512)
+    Q = 2 * (g.heads + g.kv_heads) + 1
+    A = g.kv_heads
+    rows = []
+    for l in range(1, g.layers):
+        e = a[l]
+        act = e[: W + 1 + Q + A]
+        t0 = act[:, 0].min()
+        us = lambda v: float(v - t0) * 0.01
+        mix = e[W]
+        rows.append({"wo_done": us(e[:W, 3].max()), "mix_entry": us(mix[0]),
+                     "mix_wo_wait_done": us(mix[1]), "mix_signal": us(mix[2]),
+                     "mix_exit": us(mix[3]), "qkv_done": us(e[W + 1: W + 1 + Q, 3].max()),
+                     "att_done": us(e[W + 1 + Q: W + 1 + Q + A, 3].max()),
+                     "launch_last_exit": us(act[:, 3].max()),
+                     "gap_to_next_us": float(a[l + 1][: W + 1 + Q + A, 0][
+                         a[l + 1][: W + 1 + Q + A, 0] > 0].min() - act[:, 3].max()) * 0.01})
+    out = {k: float(np.median([r[k] for r in rows])) for k in rows[0]}
+    out["layers"] = len(rows)
+    out["step_span_us"] = float(a[g.layers][:, 3].max() - a[0][a[0][:, 0] > 0][:, 0].min()) * 0.01
+    return out
+
+
 def decoder_weight_bytes(g):
     """int8 codes + f32 per-row scales read by one decode step (tied lm head)."""
     per_layer = [(g.heads + 2 * g.kv_heads) * 64 * g.dim, g.dim * g.heads * 64, g.ffn * g.dim,
@@ -933,7 +986,7 @@ def main():
     ap.add_argument("--only", choices=["matvec", "matvec8", "attention", "decode", "prefill",
                                        "needle2", "needle2cq", "needle2mixed", "traffic", "attention_traffic", "cq",
                                        "grammar", "ceiling", "matvec_span", "copy_matvec",
-                                       "attention_span"],
+                                       "attention_span", "needle2_span"],
                     help="run one part alone and print its JSON (for profiling)")
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--no-check", action="store_true",
@@ -975,6 +1028,8 @@ def main():
             part = attention_traffic_workload(torch, hip)
         elif args.only == "matvec_span":
             part = bench_matvec_span(torch, hip, n, k, g, args.steps, args.warmup)
+        elif args.only == "needle2_span":
+            part = bench_needle2_span(torch, hip, 8)
         elif args.only == "attention_span":
             part = bench_attention_span(torch, hip, 8192, 8, args.steps, args.warmup)
         elif args.only == "copy_matvec":

@@ -152,12 +152,26 @@ __device__ __forceinline__ float gate_factor(float g) { return 1.f / (1.f + __ex
 // partials are published, once its arrival is counted and (the last chunk)
 // after the merge, and writes them with the chunk's role (0 counted in,
 // 1 merged) and its XCC id to stamps[8 L .. 8 L + 7] for workgroup L.
+// The default of attention_body's `hook`: nothing between the loads and
+// the math.
+struct NoHook {
+  static constexpr bool kActive = false;
+  __device__ bool wait() const { return true; }
+  __device__ uint32_t fresh_slot() const { return 0xFFFFFFFFu; }
+};
+
+// hook (kActive, one tile per wave, int8 cache): the workgroup issues its
+// tile loads, then every thread calls hook.wait() (false: return without
+// storing), then the rows of cache slot hook.fresh_slot() -- written by
+// another workgroup of the same launch while the loads were in flight -- are
+// read again past the CU's L1, and the query rows are read; then the math.
+//
 // GRID: the workgroup's (chunk, KV head local to its row, row z) come from
 // the grid (the arguments of those names are ignored); otherwise from the
 // arguments (a caller that runs one workgroup per (chunk, KV head, row) of
 // its own).
 template <int REP, bool F32, bool QB = false, int KW = 4, int TILES = 0, bool XL = false,
-          bool STAMP = false, bool GRID = true>
+          bool STAMP = false, bool GRID = true, class Hook = NoHook>
 __device__ __forceinline__ void attention_body(
     uint32_t chunk_arg, uint32_t kvh_arg, uint32_t z_arg, const void* Kc, const void* Vc, const float* Ks,
     const float* Vs, const float* Q, float* out,
@@ -168,7 +182,9 @@ __device__ __forceinline__ void attention_body(
     const uint32_t* positions, uint32_t slot_space, uint32_t seq_kv_heads,
     uint32_t kv_stride_z,
     uint32_t chunk_positions, uint32_t max_chunks, float score_scale, uint32_t qrows,
-    uint32_t qgroup, uint64_t* stamps) {
+    uint32_t qgroup, uint64_t* stamps, const Hook& hook = Hook()) {
+  static_assert(!Hook::kActive || (TILES == 1 && !F32 && !QB),
+                "the hook serves the one-tile int8 single-row form");
   uint64_t stamp[6] = {};
   if constexpr (STAMP) stamp[0] = wall_clock64();
   auto put_stamps = [&](uint32_t role) {
@@ -260,18 +276,21 @@ __device__ __forceinline__ void attention_body(
   };
 
   float q[REP][16];
+  auto load_q = [&]() __attribute__((always_inline)) {
 #pragma unroll
-  for (int h = 0; h < REP; ++h) {
-    const float4* qp = reinterpret_cast<const float4*>(Q + qrow(h) + quad * 16);
+    for (int h = 0; h < REP; ++h) {
+      const float4* qp = reinterpret_cast<const float4*>(Q + qrow(h) + quad * 16);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float4 f = qp[c];
-      q[h][4 * c + 0] = f.x;
-      q[h][4 * c + 1] = f.y;
-      q[h][4 * c + 2] = f.z;
-      q[h][4 * c + 3] = f.w;
+      for (int c = 0; c < 4; ++c) {
+        const float4 f = qp[c];
+        q[h][4 * c + 0] = f.x;
+        q[h][4 * c + 1] = f.y;
+        q[h][4 * c + 2] = f.z;
+        q[h][4 * c + 3] = f.w;
+      }
     }
-  }
+  };
+  if constexpr (!Hook::kActive) load_q();
 
   float m[REP], l[REP], acc[REP][16];
 #pragma unroll
@@ -359,7 +378,37 @@ __device__ __forceinline__ void attention_body(
   // Tiles t_first + kStride j, j < n (n uniform), two per round: both tiles'
   // loads are in flight before the first tile's math.  TILES = 1 or 2: the
   // launch guarantees n <= TILES, and the code is straight-line.
-  if (t_first < c_end) {
+  if constexpr (Hook::kActive) {
+    Tile<F32> ta;
+    const bool has = t_first < c_end;
+    if (has) load_tile<F32>(ta, Kc, Vc, Ks, Vs, head_base, vis, ring, t_first, c_end, trow, quad);
+    if (!hook.wait()) return;
+    // The fresh slot's rows, past the CU's L1 (agent-scope loads hit the L2
+    // its writer stored to); slot order: row k holds slot t_first + trow + 16 k.
+    const uint32_t fresh = hook.fresh_slot();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (has && t_first + trow + 16 * k == fresh) {
+        const size_t row = head_base + fresh;
+        const uint32_t* kp = reinterpret_cast<const uint32_t*>(
+            reinterpret_cast<const int8_t*>(Kc) + row * kHeadDim + quad * 16);
+        const uint32_t* vp = reinterpret_cast<const uint32_t*>(
+            reinterpret_cast<const int8_t*>(Vc) + row * kHeadDim + quad * 16);
+        uint32_t kw[4], vw[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          kw[c] = __hip_atomic_load(kp + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          vw[c] = __hip_atomic_load(vp + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        ta.k[k] = make_uint4(kw[0], kw[1], kw[2], kw[3]);
+        ta.v[k] = make_uint4(vw[0], vw[1], vw[2], vw[3]);
+        ta.ks[k] = __hip_atomic_load(Ks + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ta.vs[k] = __hip_atomic_load(Vs + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    load_q();
+    if (has) tile_math(ta, t_first);
+  } else if (t_first < c_end) {
     Tile<F32> ta, tb;
     if constexpr (TILES == 1) {
       load_tile<F32>(ta, Kc, Vc, Ks, Vs, head_base, vis, ring, t_first, c_end, trow, quad);

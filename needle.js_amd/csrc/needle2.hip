@@ -1021,6 +1021,10 @@ struct MixArgs {
   AttArgs att;
   uint32_t att_groups, att_target;
   uint32_t* att_count;
+  // Measurement (n2_mix_kernel<..., STAMP>): 4 clock stamps per active
+  // workgroup k (L / 8) at stamps[4 k]: entry, the mix's Wo wait done, the
+  // mix's signal to the projection, exit (0 where a role has no such point).
+  uint64_t* stamps;
 };
 
 // Rows [rpw k, +rpw) of proj = Wo att in the fused Wo + mix launch, rpw =
@@ -1328,48 +1332,73 @@ constexpr int kPhiPairs = 8;
 // PU (Cactus-Quant): phi_pre, phi_post and phi_res share one format (width,
 // group, codebook), so one rotation and one width dispatch serve every row;
 // otherwise each row takes its own matrix's format.
-// Attention workgroup ah (KV head ah) of the fused launch: wait until every
-// projection head workgroup has counted in (q, this position's cache rows
-// and the gate are in the XCD's L2), count in (the last clears the count),
-// then the gated attention of the KV head with nd_launch_attention_gated's
-// instance and arguments for a ring of at most kGatedChunk positions.  A
-// wait that runs out sets kStatusAttWait; an abort from the projection
-// stores nothing.
+// Attention workgroup ah (KV head ah) of the fused launch.  It issues its
+// cache tiles at once (every row but this position's is final before the
+// launch), then waits until every projection head workgroup has counted in
+// (q, this position's cache rows and the gate are in the XCD's L2), counts
+// in (the last clears the count), reads the fresh rows again past its L1,
+// and runs the gated attention of the KV head with nd_launch_attention_gated's
+// instance and arguments for a ring of at most kGatedChunk positions -- the
+// same values in the same order, so the same bits.  A wait that runs out
+// sets kStatusAttWait; an abort from the projection stores nothing.
+struct AttWait {
+  static constexpr bool kActive = true;
+  const MixArgs* a;
+  uint32_t* go;  // an LDS word
+  uint32_t slot;
+  __device__ bool wait() const {
+    if (threadIdx.x == 0) {
+      bool ok = true;
+      uint32_t it = 0, v;
+      while (((v = __hip_atomic_load(a->att_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) &
+              kFlagCount) < a->att_target &&
+             !(v & kFlagAbort)) {
+        if (++it >= a->spin) {
+          __hip_atomic_fetch_or(a->status, kStatusAttWait, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+          ok = false;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (v & kFlagAbort) ok = false;
+      if ((__hip_atomic_fetch_add(a->att_count, 1u, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_WORKGROUP) &
+           kFlagCount) == a->att_target + a->att_groups - 1)
+        __hip_atomic_store(a->att_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      *go = ok;
+    }
+    __syncthreads();
+    return *go != 0;
+  }
+  __device__ uint32_t fresh_slot() const { return slot; }
+};
+
 __device__ __forceinline__ void attention_role(const MixArgs& a, uint32_t ah) {
   __shared__ uint32_t s_att_go;
-  if (threadIdx.x == 0) {
-    bool go = true;
-    uint32_t it = 0, v;
-    while (((v = __hip_atomic_load(a.att_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) &
-            kFlagCount) < a.att_target &&
-           !(v & kFlagAbort)) {
-      if (++it >= a.spin) {
-        __hip_atomic_fetch_or(a.status, kStatusAttWait, __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_AGENT);
-        go = false;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
-    if (v & kFlagAbort) go = false;
-    if ((__hip_atomic_fetch_add(a.att_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) &
-         kFlagCount) == a.att_target + a.att_groups - 1)
-      __hip_atomic_store(a.att_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    s_att_go = go;
-  }
-  __syncthreads();
-  if (!s_att_go) return;
   const AttArgs& g = a.att;
-  nd::att::attention_body<2, false, false, kMixWg / 64, 1, false, false, false>(
+  const AttWait w{&a, &s_att_go, kv_slot(g.position[0], g.sink, g.window)};
+  nd::att::attention_body<2, false, false, kMixWg / 64, 1, false, false, false, AttWait>(
       0u, ah, 0u, g.Kc, g.Vc, g.Ks, g.Vs, g.q, g.out, g.gate, 0u, nullptr, nullptr, nullptr,
       g.layer, g.kv_heads, g.alloc, g.sink, g.window,
       nd::att::Visible{g.alloc, g.alloc, g.alloc}, g.position, 1u, g.kv_heads, 0u,
-      nd::att::kGatedChunk, 1u, 0.125f, 1u, 1u, nullptr);
+      nd::att::kGatedChunk, 1u, 0.125f, 1u, 1u, nullptr, w);
 }
 
-template <bool CQ, bool WO = false, bool PU = true>
+template <bool CQ, bool WO = false, bool PU = true, bool STAMP = false>
 __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   static_assert(kQkvWg == kMixWg, "the fused projection runs on mix-sized workgroups");
+  uint64_t stamp[4] = {};
+  if constexpr (STAMP) stamp[0] = wall_clock64();
+  auto put_stamps = [&](uint32_t k) {
+    if constexpr (STAMP) {
+      if (threadIdx.x == 0) {
+        stamp[3] = wall_clock64();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a.stamps[4 * k + i] = stamp[i];
+      }
+    }
+  };
   if constexpr (WO) {
     // Workgroups L % 8 == 0 only (one XCD): L / 8 < wo_groups computes Wo
     // rows, L / 8 == wo_groups (dispatched after all of them) runs the mix,
@@ -1388,6 +1417,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
       } else {
         wo_rows(a, k);
       }
+      put_stamps(k);
       return;
     }
     if (k > a.wo_groups) {
@@ -1398,6 +1428,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
       } else if (qb - a.qkv_groups < a.att_groups) {
         attention_role(a, qb - a.qkv_groups);
       }
+      put_stamps(k);
       return;
     }
   } else if (blockIdx.x) {
@@ -1546,6 +1577,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     }
     __syncthreads();
     if (!s_go) return;
+    if constexpr (STAMP) stamp[1] = wall_clock64();
     p = __hip_atomic_load(a.proj + tc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (t == 0) __hip_atomic_store(a.wo_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
@@ -1790,6 +1822,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
       __syncthreads();
       if (t == 0)
         __hip_atomic_store(a.qkv_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if constexpr (STAMP) stamp[2] = wall_clock64();
     }
   }
   if (a.route_out) {
@@ -1805,6 +1838,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     r.route = a.route_out;
     route_wave(r, t, rt);
   }
+  if constexpr (WO) put_stamps(blockIdx.x >> 3);
 }
 
 // ---------------------------------------------------------------- prefill
@@ -2219,6 +2253,7 @@ struct nd_needle {
   uint32_t* status = nullptr;
   uint32_t* status_host = nullptr;
   uint32_t dbg_extra = 0, dbg_spin = 0;
+  uint64_t* dbg_stamps = nullptr;  // measurement: the int8 fused launches' clock stamps
   double *lp_history = nullptr, *sel_lp = nullptr;
   uint32_t* cq_lookup = nullptr;  // CQ model: a step's engram lookups and token
   float *ring = nullptr, *x = nullptr, *upd = nullptr, *blk = nullptr, *ain = nullptr,
@@ -2473,9 +2508,13 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, 
       m.qkv_flag = n->qkv_flags + 32 * (size_t)l;
       if (att) set_att(n, l, m);
     }
-    hipLaunchKernelGGL((n2_mix_kernel<false, true>),
-                       dim3(8 * (m.wo_groups + 1 + m.qkv_groups + m.att_groups)), dim3(kMixWg),
-                       0, s, m);
+    const dim3 grid(8 * (m.wo_groups + 1 + m.qkv_groups + m.att_groups));
+    if (n->dbg_stamps && grid.x <= 8 * 64) {  // measurement: 64 workgroups' stamps per layer
+      m.stamps = n->dbg_stamps + (size_t)l * 64 * 4;
+      hipLaunchKernelGGL((n2_mix_kernel<false, true, true, true>), grid, dim3(kMixWg), 0, s, m);
+    } else {
+      hipLaunchKernelGGL((n2_mix_kernel<false, true>), grid, dim3(kMixWg), 0, s, m);
+    }
   } else {
     hipLaunchKernelGGL(n2_mix_kernel<false>, dim3(1), dim3(kMixWg), 0, s, m);
   }
@@ -3778,6 +3817,17 @@ nd_status nd_needle_test_waits(nd_ctx* ctx, nd_needle* n, uint32_t extra_arrival
   drop_graphs(n);  // the launches' arguments change
   n->dbg_extra = extra_arrivals;
   n->dbg_spin = spin_rounds;
+  return ND_OK;
+}
+
+nd_status nd_needle_test_stamps(nd_ctx* ctx, nd_needle* n, uint64_t* stamps, uint32_t capacity) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!n) return nd_fail(ctx, ND_ERR_INVALID, "NULL model");
+  if (stamps && (n->cq || capacity < (n->d.layers + 1) * 64 * 4))
+    return nd_fail(ctx, ND_ERR_INVALID,
+                   "nd_needle_test_stamps: an int8 model and room for %u stamps",
+                   (n->d.layers + 1) * 64 * 4);
+  n->dbg_stamps = stamps;
   return ND_OK;
 }
 
