@@ -454,7 +454,7 @@ def bench_needle2_span(torch, hip, steps):
     prompt = synth.Stream(2026, "needle2.prompt").integers(128, 0, g.vocab - 1)
     rt.reset(len(prompt) + steps + 1, 0)
     rt.prefill(prompt)
-    cap = (g.layers + 1) * 64 * 4
+    cap = (g.layers + 1) * 64 * 16
     stamps = torch.zeros(cap, dtype=torch.int64, device="cuda")
     res = model.resident
     hip._check(hip.lib.nd_needle_test_stamps(hip.ctx, res.handle, stamps.data_ptr(), cap))
@@ -462,7 +462,7 @@ def bench_needle2_span(torch, hip, steps):
     for _ in range(steps):
         rt.step(tok, want_logits=False)
     torch.cuda.synchronize()
-    a = stamps.view(g.layers + 1, 64, 4).cpu().numpy().astype(np.int64)
+    a = stamps.view(g.layers + 1, 64, 16).cpu().numpy().astype(np.int64)
     hip._check(hip.lib.nd_needle_test_stamps(hip.ctx, res.handle, None, 0))
     model.dispose()
     W = g.dim // (512 // (g.heads * 64 // 16))  # Wo workgroups (16 rows each at d 512)
@@ -475,7 +475,11 @@ def bench_needle2_span(torch, hip, steps):
         t0 = act[:, 0].min()
         us = lambda v: float(v - t0) * 0.01
         mix = e[W]
-        rows.append({"wo_done": us(e[:W, 3].max()), "mix_entry": us(mix[0]),
+        phases = {f"mix_{nm}": us(mix[i]) for i, nm in
+                  ((4, "post_norms"), (5, "fwht1"), (6, "fwht2"), (7, "lanes"), (8, "pre_norm"),
+                   (9, "phi"), (10, "engram"), (11, "input_norm"), (12, "phi_split"),
+                   (13, "phi_mfma"), (14, "phi_part"))}
+        rows.append({**phases, "wo_done": us(e[:W, 3].max()), "mix_entry": us(mix[0]),
                      "mix_wo_wait_done": us(mix[1]), "mix_signal": us(mix[2]),
                      "mix_exit": us(mix[3]), "qkv_done": us(e[W + 1: W + 1 + Q, 3].max()),
                      "att_done": us(e[W + 1 + Q: W + 1 + Q + A, 3].max()),

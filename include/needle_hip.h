@@ -593,14 +593,16 @@ nd_status nd_needle_test_waits(nd_ctx* ctx, nd_needle* model, uint32_t extra_arr
                                uint32_t spin_rounds);
 
 /* Measurement, no counterpart in the reference: while stamps_dev is set
- * (capacity >= (layers + 1) x 256 words, an int8 model), the fused layer
+ * (capacity >= (layers + 1) x 1024 words, an int8 model), the fused layer
  * launches of direct (not graph-replayed) whole-step calls (nd_needle_step,
  * nd_needle_step_select) run their measurement form: thread 0 of active
  * workgroup k of launch l writes the GPU's 100 MHz clock at entry, when the
  * mix's wait for the output-projection rows ended, when the mix signalled
- * the projection, and at exit to stamps_dev[(64 l + k) x 4 .. + 3] (0 where
- * the role has no such point; workgroups are Wo rows, then the mix, the
- * projection, the attention).  NULL turns it off. */
+ * the projection, and at exit to stamps_dev[(64 l + k) x 16 .. + 3], and
+ * the mix workgroup after its post norms, each FWHT, the lane update, the
+ * pre norm, the phi products, the engram gate and the input norm to words
+ * 4 .. 11 (0 where the role has no such point; workgroups are Wo rows, then
+ * the mix, the projection, the attention).  NULL turns it off. */
 nd_status nd_needle_test_stamps(nd_ctx* ctx, nd_needle* model, uint64_t* stamps_dev,
                                 uint32_t capacity);
 

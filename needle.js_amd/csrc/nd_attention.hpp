@@ -378,6 +378,11 @@ __device__ __forceinline__ void attention_body(
   // Tiles t_first + kStride j, j < n (n uniform), two per round: both tiles'
   // loads are in flight before the first tile's math.  TILES = 1 or 2: the
   // launch guarantees n <= TILES, and the code is straight-line.
+  // Hook: each thread's output gates (the combine's output mapping below),
+  // read together with q once the wait is over.
+  constexpr int kGateT = REP * kHeadDim >= 64 * KW ? 1 : 64 * KW / (REP * kHeadDim);
+  constexpr int kGatePer = REP * kHeadDim >= 64 * KW ? REP * kHeadDim / (64 * KW) : 1;
+  float gate_pre[Hook::kActive ? kGatePer : 1];
   if constexpr (Hook::kActive) {
     Tile<F32> ta;
     const bool has = t_first < c_end;
@@ -407,6 +412,12 @@ __device__ __forceinline__ void attention_body(
       }
     }
     load_q();
+    if (gate) {
+#pragma unroll
+      for (int u = 0; u < kGatePer; ++u)
+        gate_pre[u] = gate[(size_t)z * gate_ld + kvh_local * (REP * kHeadDim) +
+                           threadIdx.x / kGateT + u * (64 * KW / kGateT)];
+    }
     if (has) tile_math(ta, t_first);
   } else if (t_first < c_end) {
     Tile<F32> ta, tb;
@@ -521,7 +532,7 @@ __device__ __forceinline__ void attention_body(
       for (int u = 0; u < kPer; ++u) {
         const uint32_t oi = kvh_local * kOut + w_o[u];
         float r = w_a[u] / w_l[u];
-        if (gate_z) r *= gate_factor(gate_z[oi]);
+        if (gate_z) r *= gate_factor(Hook::kActive ? gate_pre[u] : gate_z[oi]);
         out_z[oi] = r;
       }
     }

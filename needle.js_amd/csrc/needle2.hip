@@ -735,33 +735,41 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
   __shared__ float s_cb[16];
   __shared__ uint32_t s_go;
   const uint32_t t = threadIdx.x;
+  // s_go: 0 the wait ran out, 1 go, 2 the flag carried the abort bit.  A
+  // workgroup that saw the flag counts itself on it when it is done
+  // (release): the flag is next read by this layer's launch of the next
+  // step, so the count stays off this launch's path.
   auto wait = [&]() -> bool {
     if constexpr (WAIT) {
       if (t == 0) {
         uint32_t it = 0, f;
-        bool go = true;
+        uint32_t go = 1;
         while ((f = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == 0) {
           if (++it >= spin) {
-            go = false;
+            go = 0;
             break;
           }
           __builtin_amdgcn_s_sleep(1);
         }
-        if (!go) {
+        if (!go)
           __hip_atomic_fetch_or(status, kStatusQkvWait, __ATOMIC_RELAXED,
                                 __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-          if ((__hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) &
-               kFlagCount) == waiters)
-            __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-          go = (f & kFlagAbort) == 0;
-        }
+        else if (f & kFlagAbort)
+          go = 2;
         s_go = go;
       }
       __syncthreads();
-      return s_go != 0;
+      return s_go == 1;
     }
     return true;
+  };
+  auto release = [&]() {
+    if constexpr (WAIT) {
+      if (t == 0 && s_go != 0 &&
+          (__hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) &
+           kFlagCount) == waiters)
+        __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
   };
   auto count_in = [&](bool stored) {
     if (att_count) {
@@ -772,8 +780,8 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
     }
   };
   if (b == 2 * (p.heads + p.kv_heads)) {
-    if (!wait()) return;
-    route_wave(p.route, t, rows);
+    if (wait()) route_wave(p.route, t, rows);
+    release();
     return;
   }
   const uint32_t lane = t & 63;
@@ -787,6 +795,7 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
     const float srow = p.S[row];
     if (!wait()) {
       if (t == 0) count_in(false);
+      release();
       return;
     }
     for (uint32_t i = t; i < d; i += kQkvWg) xs[i] = p.x[i];
@@ -826,6 +835,7 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
     }
     if (!wait()) {
       if (t == 0) count_in(false);
+      release();
       return;
     }
     for (uint32_t i = t; i < kpad; i += kQkvWg) xs[i + (i >> 5)] = i < d ? p.x[i] : 0.f;
@@ -849,6 +859,7 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
       __builtin_amdgcn_s_waitcnt(0);  // the wave's stores have completed
       if (lane == 0) count_in(true);
     }
+    release();
     return;
   }
   const int role = b < nq ? 0 : (b < nq + nk ? 1 : 2);
@@ -860,6 +871,7 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
     __builtin_amdgcn_s_waitcnt(0);  // the wave's stores have completed
     if (lane == 0) count_in(true);
   }
+  release();
 }
 
 template <bool CQ>
@@ -1021,9 +1033,11 @@ struct MixArgs {
   AttArgs att;
   uint32_t att_groups, att_target;
   uint32_t* att_count;
-  // Measurement (n2_mix_kernel<..., STAMP>): 4 clock stamps per active
-  // workgroup k (L / 8) at stamps[4 k]: entry, the mix's Wo wait done, the
-  // mix's signal to the projection, exit (0 where a role has no such point).
+  // Measurement (n2_mix_kernel<..., STAMP>): 16 clock stamps per active
+  // workgroup k (L / 8) at stamps[16 k]: entry, the mix's Wo wait done, the
+  // mix's signal to the projection, exit, then the mix's phases (after the
+  // post norms, each FWHT, the lane update, the pre norm, the phi products,
+  // the engram gate, the input norm) -- 0 where a role has no such point.
   uint64_t* stamps;
 };
 
@@ -1335,26 +1349,30 @@ constexpr int kPhiPairs = 8;
 // Attention workgroup ah (KV head ah) of the fused launch.  It issues its
 // cache tiles at once (every row but this position's is final before the
 // launch), then waits until every projection head workgroup has counted in
-// (q, this position's cache rows and the gate are in the XCD's L2), counts
-// in (the last clears the count), reads the fresh rows again past its L1,
+// (q, this position's cache rows and the gate are in the XCD's L2), reads
+// the fresh rows again past its L1 (counting itself in at the end; the last
+// clears the count),
 // and runs the gated attention of the KV head with nd_launch_attention_gated's
 // instance and arguments for a ring of at most kGatedChunk positions -- the
 // same values in the same order, so the same bits.  A wait that runs out
 // sets kStatusAttWait; an abort from the projection stores nothing.
+// (The hook holds copies of the launch arguments it needs: the address of
+// the argument block itself would cost a private copy of it.)
 struct AttWait {
   static constexpr bool kActive = true;
-  const MixArgs* a;
+  uint32_t* count;
+  uint32_t* status;
   uint32_t* go;  // an LDS word
-  uint32_t slot;
+  uint32_t target, groups, spin, slot;
   __device__ bool wait() const {
     if (threadIdx.x == 0) {
       bool ok = true;
       uint32_t it = 0, v;
-      while (((v = __hip_atomic_load(a->att_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) &
-              kFlagCount) < a->att_target &&
+      while (((v = __hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) &
+              kFlagCount) < target &&
              !(v & kFlagAbort)) {
-        if (++it >= a->spin) {
-          __hip_atomic_fetch_or(a->status, kStatusAttWait, __ATOMIC_RELAXED,
+        if (++it >= spin) {
+          __hip_atomic_fetch_or(status, kStatusAttWait, __ATOMIC_RELAXED,
                                 __HIP_MEMORY_SCOPE_AGENT);
           ok = false;
           break;
@@ -1362,40 +1380,49 @@ struct AttWait {
         __builtin_amdgcn_s_sleep(1);
       }
       if (v & kFlagAbort) ok = false;
-      if ((__hip_atomic_fetch_add(a->att_count, 1u, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_WORKGROUP) &
-           kFlagCount) == a->att_target + a->att_groups - 1)
-        __hip_atomic_store(a->att_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       *go = ok;
     }
     __syncthreads();
     return *go != 0;
   }
   __device__ uint32_t fresh_slot() const { return slot; }
+  // After the attention (off its path): thread 0 counts the workgroup in;
+  // the last of them clears the count for the next launch.
+  __device__ void release() const {
+    if (threadIdx.x == 0 &&
+        (__hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) &
+         kFlagCount) == target + groups - 1)
+      __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
 };
 
 __device__ __forceinline__ void attention_role(const MixArgs& a, uint32_t ah) {
   __shared__ uint32_t s_att_go;
   const AttArgs& g = a.att;
-  const AttWait w{&a, &s_att_go, kv_slot(g.position[0], g.sink, g.window)};
+  const AttWait w{a.att_count, a.status, &s_att_go, a.att_target, a.att_groups, a.spin,
+                  kv_slot(g.position[0], g.sink, g.window)};
   nd::att::attention_body<2, false, false, kMixWg / 64, 1, false, false, false, AttWait>(
       0u, ah, 0u, g.Kc, g.Vc, g.Ks, g.Vs, g.q, g.out, g.gate, 0u, nullptr, nullptr, nullptr,
       g.layer, g.kv_heads, g.alloc, g.sink, g.window,
       nd::att::Visible{g.alloc, g.alloc, g.alloc}, g.position, 1u, g.kv_heads, 0u,
       nd::att::kGatedChunk, 1u, 0.125f, 1u, 1u, nullptr, w);
+  w.release();
 }
 
 template <bool CQ, bool WO = false, bool PU = true, bool STAMP = false>
 __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   static_assert(kQkvWg == kMixWg, "the fused projection runs on mix-sized workgroups");
-  uint64_t stamp[4] = {};
+  uint64_t stamp[16] = {};
   if constexpr (STAMP) stamp[0] = wall_clock64();
+  auto mark = [&](int i) {
+    if constexpr (STAMP) stamp[i] = wall_clock64();
+  };
   auto put_stamps = [&](uint32_t k) {
     if constexpr (STAMP) {
       if (threadIdx.x == 0) {
         stamp[3] = wall_clock64();
 #pragma unroll
-        for (int i = 0; i < 4; ++i) a.stamps[4 * k + i] = stamp[i];
+        for (int i = 0; i < 16; ++i) a.stamps[16 * k + i] = stamp[i];
       }
     }
   };
@@ -1593,6 +1620,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     if (t < L * L + L) rt[t] = route;  // visible after the next barrier
     const double sa = mix_sum(col ? (double)after * after : 0.0, red, phase);
     const double ia = 1.0 / sqrt(sa / D + 1e-6);
+    mark(4);
     // hadamardMlp (math.ts:117-138): FWHT(d1 x), SiLU(z / sqrt(H) * d2),
     // FWHT, / sqrt(H) * d3.
     float v = 0.f;
@@ -1602,6 +1630,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     }
     const double inv_root = a.inv_root_h;
     v = fwht_block(v, hv1, H, t);
+    mark(5);
     if (t < H) {
       const double z = (double)v * inv_root * (double)d2;
       v = (float)(z * sigmoid_d(z));
@@ -1609,6 +1638,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
       v = 0.f;
     }
     v = fwht_block(v, hv2, H, t);
+    mark(6);
     if (col) {
       const float mlp = (float)((double)v * inv_root * (double)d3);
       const float delta = (float)((double)after + (double)mlp - (double)upd);
@@ -1650,6 +1680,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     const double inv = 1.0 / sqrt(ss / D + 1e-6);
     if (col) a.fin[t] = (float)((1.0 + (double)fnorm) * (double)m * inv);
   }
+  mark(7);
   if (!a.has_pre) return;
 
   // ---- pre(l): rmsUnit over all lanes (math.ts:34-44), then the phi rows.
@@ -1659,6 +1690,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     if ((uint32_t)l < L) ss += (double)xl[l] * (double)xl[l];
   ss = mix_sum(col ? ss : 0.0, red, phase);
   const double inv = 1.0 / sqrt(ss / N + 1e-6);
+  mark(8);
   float pre_phi = 0.f;  // phi_pre row `lane` (lane < lanes): feeds hPre
   if constexpr (CQ) {
     // phi = cqMatvec of the normalized lanes (backends/cq.ts:30-46, 107-231):
@@ -1742,6 +1774,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
         }
     }
     nd::lds_barrier();
+    mark(12);
     float4v acc = {0.f, 0.f, 0.f, 0.f};
   #pragma unroll
     for (int i = 0; i < kPhiPairs; ++i) {
@@ -1758,11 +1791,13 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
         }
       }
     }
+    mark(13);
     if (lane < 16) {
       s_part[prow][kq][0] = acc[0];
       s_part[prow][kq][1] = acc[1];
     }
     nd::lds_barrier();
+    mark(14);
     // phi row r = scale_r * 2^-s * sum over the tile's waves of (hi + lo), in
     // float64; every thread takes the phi_pre rows itself (they feed hPre).
     auto phi_row = [&](uint32_t r, float scale) -> float {
@@ -1782,6 +1817,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   }
   // hPre (runtime.ts:412-417): lane l < lanes of every wave takes lane l's
   // gate, and the wave shares them by readlane (no barrier).
+  mark(9);
   float hp = 0.f;
   if (lane < L) {
     const double off = lane == a.own_pre ? 4.0 : -4.0;
@@ -1811,11 +1847,13 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     const double alpha = sigmoid_d(dot / a.sqrt_d);
     if (col) b = (float)((double)u + alpha * (double)evalue);
   }
+  mark(10);
   if (col) a.blk[t] = b;
   // attentionInput = rmsNorm(block, normInput) (math.ts:16-32).
   const double sb = mix_sum(col ? (double)b * b : 0.0, red, phase);
   const double ib = 1.0 / sqrt(sb / D + 1e-6);
   if (col) a.ain[t] = (float)((1.0 + (double)norm_in) * (double)b * ib);
+  mark(11);
   if constexpr (WO) {
     if (a.qkv_groups) {  // the input and the phi values are in the L2: signal
       __builtin_amdgcn_s_waitcnt(0);
@@ -2510,7 +2548,7 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, 
     }
     const dim3 grid(8 * (m.wo_groups + 1 + m.qkv_groups + m.att_groups));
     if (n->dbg_stamps && grid.x <= 8 * 64) {  // measurement: 64 workgroups' stamps per layer
-      m.stamps = n->dbg_stamps + (size_t)l * 64 * 4;
+      m.stamps = n->dbg_stamps + (size_t)l * 64 * 16;
       hipLaunchKernelGGL((n2_mix_kernel<false, true, true, true>), grid, dim3(kMixWg), 0, s, m);
     } else {
       hipLaunchKernelGGL((n2_mix_kernel<false, true>), grid, dim3(kMixWg), 0, s, m);
@@ -3823,10 +3861,10 @@ nd_status nd_needle_test_waits(nd_ctx* ctx, nd_needle* n, uint32_t extra_arrival
 nd_status nd_needle_test_stamps(nd_ctx* ctx, nd_needle* n, uint64_t* stamps, uint32_t capacity) {
   if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
   if (!n) return nd_fail(ctx, ND_ERR_INVALID, "NULL model");
-  if (stamps && (n->cq || capacity < (n->d.layers + 1) * 64 * 4))
+  if (stamps && (n->cq || capacity < (n->d.layers + 1) * 64 * 16))
     return nd_fail(ctx, ND_ERR_INVALID,
                    "nd_needle_test_stamps: an int8 model and room for %u stamps",
-                   (n->d.layers + 1) * 64 * 4);
+                   (n->d.layers + 1) * 64 * 16);
   n->dbg_stamps = stamps;
   return ND_OK;
 }
