@@ -34,6 +34,29 @@ constexpr uint32_t kMaxNormK = 1024;     // rows the fused norm reads whole
 
 __device__ __forceinline__ float silu_f(float v) { return v / (1.f + __expf(-v)); }
 
+// Digit split of X = rint(v up), |X| <= 2^22, into signed base-256 digits
+// X = d0 + 256 d1 + 65536 d2 (d0 = X - 256 round(X / 256) with halves
+// rounded up, and so on; d2 in [-64, 64]).  v up + 1.5 2^23 rounds to the
+// integer 1.5 2^23 + X (to even on ties, as rint: 1.5 2^23 is even), whose
+// bit pattern over [2^23, 2^24] is 0x4B400000 + X; plus 0x408080 its low 24
+// bits are X + 0x808080, whose bytes are d_i + 128 -- the digits' bytes
+// with bit 7 flipped (no carry crosses a byte).  up = 0 gives zero digits.
+__device__ __forceinline__ uint32_t digit_bias(float v, float up) {
+  return __float_as_uint(fmaf(v, up, 12582912.f)) + 0x408080u;
+}
+// Four values' digit_bias words to one word per digit plane (value i in
+// byte i): byte permutes, then the bit-7 flips.
+__device__ __forceinline__ void digit_words(uint32_t a, uint32_t b, uint32_t c, uint32_t d,
+                                            uint32_t& w0, uint32_t& w1, uint32_t& w2) {
+  const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x05010400u);   // a0 b0 a1 b1
+  const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x05010400u);   // c0 d0 c1 d1
+  const uint32_t ab2 = __builtin_amdgcn_perm(b, a, 0x0c0c0602u);  // a2 b2 0 0
+  const uint32_t cd2 = __builtin_amdgcn_perm(d, c, 0x0c0c0602u);  // c2 d2 0 0
+  w0 = __builtin_amdgcn_perm(cd, ab, 0x05040100u) ^ 0x80808080u;
+  w1 = __builtin_amdgcn_perm(cd, ab, 0x07060302u) ^ 0x80808080u;
+  w2 = __builtin_amdgcn_perm(cd2, ab2, 0x05040100u) ^ 0x80808080u;
+}
+
 // MS m-subtiles of 16 and NS n-subtiles of 16 per wave; 4 waves split n.
 // blockIdx.z selects the k slice [z * kslice, +kslice) (kslice = K without a
 // split).  Each 256-wide chunk issues its weight loads first and then stages
@@ -255,14 +278,10 @@ __global__ __launch_bounds__(256) void digitize_kernel(const float* __restrict__
   for (uint32_t i = 0; i < 8; ++i) {
     const uint32_t k = t + i * 256;
     if (i < per && k < K) {
-      const int X0 = (int)rintf(v[i] * up);  // |X0| < 2^22
-      const int d0 = ((X0 + 128) & 255) - 128;
-      const int X1 = (X0 - d0) >> 8;
-      const int d1 = ((X1 + 128) & 255) - 128;
-      const int d2 = (X1 - d1) >> 8;
-      D[(size_t)m * K + k] = (int8_t)d0;
-      D[plane + (size_t)m * K + k] = (int8_t)d1;
-      D[2 * plane + (size_t)m * K + k] = (int8_t)d2;
+      const uint32_t u = digit_bias(v[i], up);
+      D[(size_t)m * K + k] = (int8_t)(u ^ 0x80u);
+      D[plane + (size_t)m * K + k] = (int8_t)((u >> 8) ^ 0x80u);
+      D[2 * plane + (size_t)m * K + k] = (int8_t)((u >> 16) ^ 0x80u);
     }
   }
   if (t == 0) fm[m] = ldexpf(1.f, e - 21);
@@ -332,19 +351,9 @@ __global__ __launch_bounds__(256) void digitize_rows_kernel(const float* __restr
   for (int i = 0; i < VEC; ++i) {
     const uint32_t u = lane + 64 * i;
     if (u >= units) continue;
-    const float vals[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-    uint32_t w0 = 0, w1 = 0, w2 = 0;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int X0 = (int)rintf(vals[c] * up);  // |X0| < 2^22
-      const int d0 = ((X0 + 128) & 255) - 128;
-      const int X1 = (X0 - d0) >> 8;
-      const int d1 = ((X1 + 128) & 255) - 128;
-      const int d2 = (X1 - d1) >> 8;
-      w0 |= (uint32_t)(d0 & 255) << (8 * c);
-      w1 |= (uint32_t)(d1 & 255) << (8 * c);
-      w2 |= (uint32_t)(d2 & 255) << (8 * c);
-    }
+    uint32_t w0, w1, w2;
+    digit_words(digit_bias(v[i].x, up), digit_bias(v[i].y, up), digit_bias(v[i].z, up),
+                digit_bias(v[i].w, up), w0, w1, w2);
     d0p[u] = w0;
     d1p[u] = w1;
     d2p[u] = w2;
@@ -504,25 +513,16 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_i8_f32a_kernel(
       frexpf(amax, &e);  // amax in [2^(e-1), 2^e)
       e -= 1;
     }
-    const float up = ldexpf(1.f, 21 - e);
-    uint32_t d0w[4] = {0, 0, 0, 0}, d1w[4] = {0, 0, 0, 0}, d2w[4] = {0, 0, 0, 0};
+    const float up = live ? ldexpf(1.f, 21 - e) : 0.f;
+    uint32_t d0w[4], d1w[4], d2w[4];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int X0 = (int)rintf(v[c][i] * up);  // |X0| < 2^22
-      const int d0 = ((X0 + 128) & 255) - 128;
-      const int X1 = (X0 - d0) >> 8;
-      const int d1 = ((X1 + 128) & 255) - 128;
-      const int d2 = (X1 - d1) >> 8;
-      d0w[i >> 2] |= (uint32_t)(d0 & 255) << (8 * (i & 3));
-      d1w[i >> 2] |= (uint32_t)(d1 & 255) << (8 * (i & 3));
-      d2w[i >> 2] |= (uint32_t)(d2 & 255) << (8 * (i & 3));
-    }
-    *reinterpret_cast<uint4*>(&lds[c][0][r][pc * 16]) =
-        live ? make_uint4(d0w[0], d0w[1], d0w[2], d0w[3]) : make_uint4(0, 0, 0, 0);
-    *reinterpret_cast<uint4*>(&lds[c][1][r][pc * 16]) =
-        live ? make_uint4(d1w[0], d1w[1], d1w[2], d1w[3]) : make_uint4(0, 0, 0, 0);
-    *reinterpret_cast<uint4*>(&lds[c][2][r][pc * 16]) =
-        live ? make_uint4(d2w[0], d2w[1], d2w[2], d2w[3]) : make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < 4; ++j)
+      digit_words(digit_bias(v[c][4 * j], up), digit_bias(v[c][4 * j + 1], up),
+                  digit_bias(v[c][4 * j + 2], up), digit_bias(v[c][4 * j + 3], up), d0w[j],
+                  d1w[j], d2w[j]);
+    *reinterpret_cast<uint4*>(&lds[c][0][r][pc * 16]) = make_uint4(d0w[0], d0w[1], d0w[2], d0w[3]);
+    *reinterpret_cast<uint4*>(&lds[c][1][r][pc * 16]) = make_uint4(d1w[0], d1w[1], d1w[2], d1w[3]);
+    *reinterpret_cast<uint4*>(&lds[c][2][r][pc * 16]) = make_uint4(d2w[0], d2w[1], d2w[2], d2w[3]);
     if (pc == 0) s_fm[c][r] = ldexpf(1.f, e - 21);
   }
   __syncthreads();
