@@ -442,7 +442,9 @@ def bench_needle2_span(torch, hip, steps):
     last step, microseconds after its first workgroup's entry: the Wo rows
     done, the mix's Wo wait over, the mix's signal to the projection, the
     projection done, the attention done, the launch's last exit; and the gap
-    from that exit to the next launch's first entry.  Medians over layers."""
+    from that exit to the next launch's first entry; the projection and
+    attention workgroups' phases (median and latest workgroup).  Medians
+    over layers."""
     import numpy as np
 
     from needle_hip import NeedleModel, synth
@@ -484,6 +486,16 @@ def bench_needle2_span(torch, hip, steps):
                      "mix_exit": us(mix[3]), "qkv_done": us(e[W + 1: W + 1 + Q, 3].max()),
                      "att_done": us(e[W + 1 + Q: W + 1 + Q + A, 3].max()),
                      "launch_last_exit": us(act[:, 3].max()),
+                     # the head projection workgroups (the routing one has no
+                     # marks): wait over, input staged, rows computed, stores
+                     # complete; the attention workgroups: wait over, q and
+                     # gates issued, tile math done, waves combined, stored
+                     **{f"qkv_{nm}_{fn.__name__}": us(fn(e[W + 1: W + Q, i])) for i, nm in
+                        ((4, "wait_over"), (5, "staged"), (6, "rows"), (7, "stored"))
+                        for fn in (np.median, np.max)},
+                     **{f"att_{nm}_{fn.__name__}": us(fn(e[W + 1 + Q: W + 1 + Q + A, i]))
+                        for i, nm in ((4, "wait_over"), (5, "issued"), (6, "tiles"), (7, "combined"),
+                                      (8, "stored")) for fn in (np.median, np.max)},
                      "gap_to_next_us": float(a[l + 1][: W + 1 + Q + A, 0][
                          a[l + 1][: W + 1 + Q + A, 0] > 0].min() - act[:, 3].max()) * 0.01})
     out = {k: float(np.median([r[k] for r in rows])) for k in rows[0]}
@@ -767,7 +779,8 @@ def bench_needle2_cq(torch, hip, reps, bits=4, group=32):
             "reps": reps, "wall_ms": wall * 1e3, "tokens_per_s": n_gen / wall,
             "decode_ms_per_token": decode_ms, "decode_tokens_per_s": 1e3 / decode_ms,
             "prefill_128_ms": wall1 * 1e3, "prefill_tokens_per_s": 128 / wall1, "bytes_per_token": bytes_tok,
-            "decode_GBps": bytes_tok / (decode_ms * 1e-3) / 1e9}
+            "decode_GBps": bytes_tok / (decode_ms * 1e-3) / 1e9,
+            "launches_per_token": model.resident.step_launches()}
     model.dispose()
     return part
 
@@ -813,13 +826,12 @@ def bench_needle2(torch, hip, reps, check, cpu_seconds):
             "prefill_128_ms": prefill_ms, "prefill_tokens_per_s": 128 / wall1,
             "bytes_per_token": bytes_tok,
             "decode_GBps": bytes_tok / (decode_ms * 1e-3) / 1e9,
-            # begin, engram projections + convolution, per layer the mix
-            # (with the previous layer's Wo and this layer's QKV) and the
-            # attention, the final mix (with the last Wo), lm head and
-            # selection, and the confidence pool (the head is on, as the
-            # reference's default)
-            "launches_per_token": 2 + len(g.sites) + 2 * g.layers + 3
-                                  + int(model.resident.has_confidence),
+            # counted in the decode-step graph: begin, engram projections +
+            # convolution, per layer one launch (the previous layer's Wo,
+            # the mix, this layer's QKV and attention), the final mix (with
+            # the last Wo), lm head and selection, and the confidence pool
+            # (the head is on, as the reference's default)
+            "launches_per_token": model.resident.step_launches(),
             "confidence_pool": model.resident.has_confidence}
     part["decode_frac_hbm"] = part["decode_GBps"] / HBM_PEAK_GBS
     # The same call through NeedleRuntime driving the session methods

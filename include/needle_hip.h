@@ -592,6 +592,11 @@ nd_status nd_needle_step_select_mask(nd_ctx* ctx, nd_needle* model, uint32_t tok
 nd_status nd_needle_test_waits(nd_ctx* ctx, nd_needle* model, uint32_t extra_arrivals,
                                uint32_t spin_rounds);
 
+/* Measurement, no counterpart in the reference: the kernel launches of the
+ * decode-step graph (a step with selection, as nd_needle_generate replays
+ * it), counted when it was captured; 0 before the first such step. */
+nd_status nd_needle_step_launches(nd_ctx* ctx, nd_needle* model, uint32_t* launches);
+
 /* Measurement, no counterpart in the reference: while stamps_dev is set
  * (capacity >= (layers + 1) x 1024 words, an int8 model), the fused layer
  * launches of direct (not graph-replayed) whole-step calls (nd_needle_step,
@@ -601,8 +606,13 @@ nd_status nd_needle_test_waits(nd_ctx* ctx, nd_needle* model, uint32_t extra_arr
  * the projection, and at exit to stamps_dev[(64 l + k) x 16 .. + 3], and
  * the mix workgroup after its post norms, each FWHT, the lane update, the
  * pre norm, the phi products, the engram gate and the input norm to words
- * 4 .. 11 (0 where the role has no such point; workgroups are Wo rows, then
- * the mix, the projection, the attention).  NULL turns it off. */
+ * 4 .. 11; a projection workgroup when its wait ended, its input was
+ * staged, its rows were computed and its stores had completed to words
+ * 4 .. 7; an attention workgroup when its wait ended, q and the gates were
+ * issued, the tile math and the waves' combine were done and its output
+ * stores had completed to words 4 .. 8 (0 where the role has no such point;
+ * workgroups are Wo rows, then the mix, the projection, the attention).
+ * NULL turns it off. */
 nd_status nd_needle_test_stamps(nd_ctx* ctx, nd_needle* model, uint64_t* stamps_dev,
                                 uint32_t capacity);
 

@@ -156,8 +156,10 @@ __device__ __forceinline__ float gate_factor(float g) { return 1.f / (1.f + __ex
 // the math.
 struct NoHook {
   static constexpr bool kActive = false;
+  static constexpr bool kStamp = false;  // measurement marks (hook.mark(i))
   __device__ bool wait() const { return true; }
   __device__ uint32_t fresh_slot() const { return 0xFFFFFFFFu; }
+  __device__ void mark(int) const {}
 };
 
 // hook (kActive, one tile per wave, int8 cache): the workgroup issues its
@@ -388,28 +390,30 @@ __device__ __forceinline__ void attention_body(
     const bool has = t_first < c_end;
     if (has) load_tile<F32>(ta, Kc, Vc, Ks, Vs, head_base, vis, ring, t_first, c_end, trow, quad);
     if (!hook.wait()) return;
-    // The fresh slot's rows, past the CU's L1 (agent-scope loads hit the L2
-    // its writer stored to); slot order: row k holds slot t_first + trow + 16 k.
+    // The fresh slot's row, past the CU's L1 (device-scope loads hit the L2
+    // its writer stored to), issued with q and the gates so that one round
+    // trip serves all three.  Slot order: row k of lane group trow holds
+    // slot t_first + trow + 16 k, so in the one wave whose tile holds the
+    // slot (uniform test) the lanes of row (fresh - t_first) % 16 take it
+    // at k = (fresh - t_first) / 16 (uniform); every lane of that wave loads
+    // its quad's codes of the row.
     const uint32_t fresh = hook.fresh_slot();
+    const bool wave_fresh = has && fresh - t_first < kWavePositions;
+    uint32_t fk[4] = {0, 0, 0, 0}, fv[4] = {0, 0, 0, 0};
+    float fks = 0.f, fvs = 0.f;
+    if (wave_fresh) {
+      const size_t row = head_base + fresh;
+      const uint32_t* kp = reinterpret_cast<const uint32_t*>(
+          reinterpret_cast<const int8_t*>(Kc) + row * kHeadDim + quad * 16);
+      const uint32_t* vp = reinterpret_cast<const uint32_t*>(
+          reinterpret_cast<const int8_t*>(Vc) + row * kHeadDim + quad * 16);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      if (has && t_first + trow + 16 * k == fresh) {
-        const size_t row = head_base + fresh;
-        const uint32_t* kp = reinterpret_cast<const uint32_t*>(
-            reinterpret_cast<const int8_t*>(Kc) + row * kHeadDim + quad * 16);
-        const uint32_t* vp = reinterpret_cast<const uint32_t*>(
-            reinterpret_cast<const int8_t*>(Vc) + row * kHeadDim + quad * 16);
-        uint32_t kw[4], vw[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          kw[c] = __hip_atomic_load(kp + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          vw[c] = __hip_atomic_load(vp + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        ta.k[k] = make_uint4(kw[0], kw[1], kw[2], kw[3]);
-        ta.v[k] = make_uint4(vw[0], vw[1], vw[2], vw[3]);
-        ta.ks[k] = __hip_atomic_load(Ks + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ta.vs[k] = __hip_atomic_load(Vs + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int c = 0; c < 4; ++c) {
+        fk[c] = __hip_atomic_load(kp + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        fv[c] = __hip_atomic_load(vp + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
+      fks = __hip_atomic_load(Ks + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      fvs = __hip_atomic_load(Vs + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     load_q();
     if (gate) {
@@ -418,7 +422,22 @@ __device__ __forceinline__ void attention_body(
         gate_pre[u] = gate[(size_t)z * gate_ld + kvh_local * (REP * kHeadDim) +
                            threadIdx.x / kGateT + u * (64 * KW / kGateT)];
     }
+    if (wave_fresh) {
+      const uint32_t kf = (fresh - t_first) >> 4;
+      const bool mine = trow == ((fresh - t_first) & 15u);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if ((uint32_t)k == kf && mine) {
+          ta.k[k] = make_uint4(fk[0], fk[1], fk[2], fk[3]);
+          ta.v[k] = make_uint4(fv[0], fv[1], fv[2], fv[3]);
+          ta.ks[k] = fks;
+          ta.vs[k] = fvs;
+        }
+      }
+    }
+    if constexpr (Hook::kStamp) hook.mark(1);
     if (has) tile_math(ta, t_first);
+    if constexpr (Hook::kStamp) hook.mark(2);
   } else if (t_first < c_end) {
     Tile<F32> ta, tb;
     if constexpr (TILES == 1) {
@@ -470,6 +489,7 @@ __device__ __forceinline__ void attention_body(
   }
   __syncthreads();
   if constexpr (STAMP) stamp[2] = wall_clock64();
+  if constexpr (Hook::kStamp) hook.mark(3);
 
   // Combine the waves: kT consecutive threads share output o (REP <= 2), each
   // summing KW * 4 / kT rows scaled by exp(m_wave - max); REP >= 4 gives

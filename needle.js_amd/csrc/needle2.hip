@@ -9,14 +9,17 @@
 // So one step's launches form a fixed sequence that is captured once as a
 // HIP graph and replayed per token with no host copies.
 //
-// Per layer the token runs four launches: `mix` (one workgroup: the
-// post-attention half of the previous layer -- sandwich norm, Hadamard MLP,
-// h-post, Sinkhorn routing, lane update -- then this layer's pre-attention
-// half -- lane RMS, the lanes*(2+lanes) phi rows, h-pre mix, engram
-// injection, input norm), the Q/K/V/gate matvec with q/k norm + RoPE and the
-// KV append in its epilogue, attention with the sigmoid(gate) epilogue, and
-// the Wo matvec.  The one-workgroup arithmetic keeps the reference's
-// float64-with-f32-stores form except the Sinkhorn iterations (fp32).
+// Per layer the token runs four stages: the previous layer's Wo matvec,
+// `mix` (one workgroup: the post-attention half of the previous layer --
+// sandwich norm, Hadamard MLP, h-post, Sinkhorn routing, lane update -- then
+// this layer's pre-attention half -- lane RMS, the lanes*(2+lanes) phi rows,
+// h-pre mix, engram injection, input norm), the Q/K/V/gate matvec with q/k
+// norm + RoPE and the KV append in its epilogue, and attention with the
+// sigmoid(gate) epilogue.  Where the placement is confirmed they share one
+// launch per layer (workgroups on one XCD handing over through its L2),
+// else they run as separate launches.  The one-workgroup arithmetic keeps
+// the reference's float64-with-f32-stores form except the Sinkhorn
+// iterations (fp32).
 #include <algorithm>
 #include <array>
 #include <cmath>
@@ -677,6 +680,9 @@ constexpr uint32_t kStatusAttWait = 4u;  // an attention workgroup's wait for th
 // The low 16 bits count the workgroups that have seen it.
 constexpr uint32_t kFlagAbort = 1u << 16;
 constexpr uint32_t kFlagCount = kFlagAbort - 1;
+// Words between the attention workgroups' per-KV-head counters (128 bytes:
+// no two share an L2 line, so their atomics do not queue on one address).
+constexpr uint32_t kAttStride = 32;
 
 // The projection launch's arguments.
 struct QkvParams {
@@ -724,17 +730,28 @@ __device__ __forceinline__ float2 cq_rows_dot_any(uint32_t bits, const CqRows& q
 // storing anything.
 //
 // att_count (inside the fused launch that also runs layer l's attention):
-// every head workgroup counts itself in once its stores (q, the cache row,
-// the gate) have completed, or with kFlagAbort when it stores nothing.
-template <bool CQ, bool WAIT>
+// every head workgroup counts itself in on its KV head's counter
+// (att_count + kAttStride kv head: the query and gate heads of that KV head,
+// its key and its value) once its stores (q, the cache row, the gate) have
+// completed, or with kFlagAbort when it stores nothing.
+// STAMP (measurement form of the fused launch): thread 0 writes the 100 MHz
+// clock to marks[0..3] (LDS) when the wait ended, the input was staged, the
+// rows were computed and the stores had completed.
+template <bool CQ, bool WAIT, bool STAMP = false>
 __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_t* flag,
                                          uint32_t waiters, uint32_t* status = nullptr,
-                                         uint32_t spin = 0, uint32_t* att_count = nullptr) {
+                                         uint32_t spin = 0, uint32_t* att_count = nullptr,
+                                         uint64_t* marks = nullptr) {
   __shared__ float xs[512 + 16];
   __shared__ float rows[64];
   __shared__ float s_cb[16];
   __shared__ uint32_t s_go;
   const uint32_t t = threadIdx.x;
+  auto mark = [&](int i) {
+    if constexpr (STAMP) {
+      if (t == 0) marks[i] = wall_clock64();
+    }
+  };
   // s_go: 0 the wait ran out, 1 go, 2 the flag carried the abort bit.  A
   // workgroup that saw the flag counts itself on it when it is done
   // (release): the flag is next read by this layer's launch of the next
@@ -759,6 +776,7 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
         s_go = go;
       }
       __syncthreads();
+      mark(0);
       return s_go == 1;
     }
     return true;
@@ -773,10 +791,14 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
   };
   auto count_in = [&](bool stored) {
     if (att_count) {
+      const uint32_t H = p.heads, K = p.kv_heads, rep = H / K;
+      const uint32_t kvh = b < H ? b / rep
+                         : b < H + K ? b - H
+                         : b < H + 2 * K ? b - H - K : (b - H - 2 * K) / rep;
+      uint32_t* c = att_count + kAttStride * kvh;
       if (!stored)
-        __hip_atomic_fetch_or(att_count, kFlagAbort, __ATOMIC_RELAXED,
-                              __HIP_MEMORY_SCOPE_WORKGROUP);
-      __hip_atomic_fetch_add(att_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __hip_atomic_fetch_or(c, kFlagAbort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   };
   if (b == 2 * (p.heads + p.kv_heads)) {
@@ -786,6 +808,11 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
   }
   const uint32_t lane = t & 63;
   const uint32_t d = p.d;
+  // The epilogue's operands (written before this launch) are issued here,
+  // ahead of the wait, so that they are in registers when the rows are.
+  const uint32_t pos = p.st[1];
+  const float nscale = b < p.heads ? p.q_norm[lane] : p.k_norm[lane];
+  const double rs = p.rope[lane & 31], rc = p.rope[32 + (lane & 31)];
   if constexpr (!CQ) {
     // Loads first: this thread's weight bytes (unconditional, clamped, so
     // they issue back to back), the row scale, then x.
@@ -800,6 +827,7 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
     }
     for (uint32_t i = t; i < d; i += kQkvWg) xs[i] = p.x[i];
     __syncthreads();
+    mark(1);
     const float acc = qkv_row_dot(wv, xs, t % kQkvTpr, d);
     if (t % kQkvTpr == 0) rows[t / kQkvTpr] = acc * srow;
   } else {
@@ -846,10 +874,8 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
       rows[(t >> 4) + 32] = v.y;
     }
   }
-  const uint32_t pos = p.st[1];
-  const float nscale = b < p.heads ? p.q_norm[lane] : p.k_norm[lane];
-  const double rs = p.rope[lane & 31], rc = p.rope[32 + (lane & 31)];
   __syncthreads();
+  mark(2);
   if (t >= 64) return;
   const float val = rows[lane];
   const uint32_t nq = p.heads, nk = p.kv_heads;
@@ -857,6 +883,7 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
     p.gate_out[(size_t)(b - nq - 2 * nk) * kHd + lane] = val;
     if (att_count) {
       __builtin_amdgcn_s_waitcnt(0);  // the wave's stores have completed
+      mark(3);
       if (lane == 0) count_in(true);
     }
     release();
@@ -869,6 +896,7 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
                 p.f32);
   if (att_count) {
     __builtin_amdgcn_s_waitcnt(0);  // the wave's stores have completed
+    mark(3);
     if (lane == 0) count_in(true);
   }
   release();
@@ -1027,9 +1055,10 @@ struct MixArgs {
   WoCq wo_cq;
   uint32_t wo_bits;
   // ... and layer l's attention: att_groups workgroups (one per KV head)
-  // after the projection, each waiting until att_target projection
-  // workgroups have counted in on att_count; they count themselves in
-  // after the wait and the last clears the count.
+  // after the projection, each waiting until the att_target projection
+  // workgroups of its KV head have counted in on its counter (att_count +
+  // kAttStride kv head); it counts itself in after its work and clears the
+  // count.
   AttArgs att;
   uint32_t att_groups, att_target;
   uint32_t* att_count;
@@ -1348,8 +1377,9 @@ constexpr int kPhiPairs = 8;
 // otherwise each row takes its own matrix's format.
 // Attention workgroup ah (KV head ah) of the fused launch.  It issues its
 // cache tiles at once (every row but this position's is final before the
-// launch), then waits until every projection head workgroup has counted in
-// (q, this position's cache rows and the gate are in the XCD's L2), reads
+// launch), then waits until the projection workgroups of its KV head (its
+// query and gate heads, key and value) have counted in on its counter (q,
+// this position's cache rows and the gate are in the XCD's L2), reads
 // the fresh rows again past its L1 (counting itself in at the end; the last
 // clears the count),
 // and runs the gated attention of the KV head with nd_launch_attention_gated's
@@ -1358,12 +1388,22 @@ constexpr int kPhiPairs = 8;
 // sets kStatusAttWait; an abort from the projection stores nothing.
 // (The hook holds copies of the launch arguments it needs: the address of
 // the argument block itself would cost a private copy of it.)
-struct AttWait {
+// STAMP: thread 0 writes the clock to marks[i] (LDS): 0 when the wait
+// ended, then at the attention body's marks (hook.mark(i)).
+template <bool STAMP = false>
+struct AttWaitT {
   static constexpr bool kActive = true;
+  static constexpr bool kStamp = STAMP;
   uint32_t* count;
   uint32_t* status;
   uint32_t* go;  // an LDS word
   uint32_t target, groups, spin, slot;
+  uint64_t* marks;
+  __device__ void mark(int i) const {
+    if constexpr (STAMP) {
+      if (threadIdx.x == 0) marks[i] = wall_clock64();
+    }
+  }
   __device__ bool wait() const {
     if (threadIdx.x == 0) {
       bool ok = true;
@@ -1381,6 +1421,7 @@ struct AttWait {
       }
       if (v & kFlagAbort) ok = false;
       *go = ok;
+      if constexpr (STAMP) marks[0] = wall_clock64();
     }
     __syncthreads();
     return *go != 0;
@@ -1396,16 +1437,25 @@ struct AttWait {
   }
 };
 
-__device__ __forceinline__ void attention_role(const MixArgs& a, uint32_t ah) {
+// STAMP: marks[0] when the wait ended, [1] when q and the gates were
+// issued, [2] after the tile math, [3] after the waves' combine, [4] when the
+// output stores had completed (thread 0, LDS).
+template <bool STAMP = false>
+__device__ __forceinline__ void attention_role(const MixArgs& a, uint32_t ah,
+                                               uint64_t* marks = nullptr) {
   __shared__ uint32_t s_att_go;
   const AttArgs& g = a.att;
-  const AttWait w{a.att_count, a.status, &s_att_go, a.att_target, a.att_groups, a.spin,
-                  kv_slot(g.position[0], g.sink, g.window)};
-  nd::att::attention_body<2, false, false, kMixWg / 64, 1, false, false, false, AttWait>(
+  const AttWaitT<STAMP> w{a.att_count + kAttStride * ah, a.status, &s_att_go, a.att_target, 1u,
+                          a.spin, kv_slot(g.position[0], g.sink, g.window), marks};
+  nd::att::attention_body<2, false, false, kMixWg / 64, 1, false, false, false, AttWaitT<STAMP>>(
       0u, ah, 0u, g.Kc, g.Vc, g.Ks, g.Vs, g.q, g.out, g.gate, 0u, nullptr, nullptr, nullptr,
       g.layer, g.kv_heads, g.alloc, g.sink, g.window,
       nd::att::Visible{g.alloc, g.alloc, g.alloc}, g.position, 1u, g.kv_heads, 0u,
       nd::att::kGatedChunk, 1u, 0.125f, 1u, 1u, nullptr, w);
+  if constexpr (STAMP) {
+    __builtin_amdgcn_s_waitcnt(0);
+    if (threadIdx.x == 0) marks[4] = wall_clock64();
+  }
   w.release();
 }
 
@@ -1449,11 +1499,17 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     }
     if (k > a.wo_groups) {
       const uint32_t qb = k - a.wo_groups - 1;
+      __shared__ uint64_t s_marks[STAMP ? 8 : 1];
       if (qb < a.qkv_groups) {
-        qkv_body<CQ, true>(a.qkv, qb, a.qkv_flag, a.qkv_groups, a.status, a.spin,
-                           a.att_groups ? a.att_count : nullptr);
+        qkv_body<CQ, true, STAMP>(a.qkv, qb, a.qkv_flag, a.qkv_groups, a.status, a.spin,
+                                  a.att_groups ? a.att_count : nullptr, s_marks);
       } else if (qb - a.qkv_groups < a.att_groups) {
-        attention_role(a, qb - a.qkv_groups);
+        attention_role<STAMP>(a, qb - a.qkv_groups, s_marks);
+      }
+      if constexpr (STAMP) {
+        __syncthreads();
+        if (threadIdx.x == 0)
+          for (int i = 0; i < 8; ++i) stamp[4 + i] = s_marks[i];
       }
       put_stamps(k);
       return;
@@ -2312,6 +2368,7 @@ struct nd_needle {
   uint32_t* pf_cq_lookup = nullptr;  // CQ model: each position's engram lookups and token
   // Step graphs, valid for (graph_alloc, graph_sink).
   hipGraphExec_t graphs[3] = {nullptr, nullptr, nullptr};
+  uint32_t graph_kernels[3] = {0, 0, 0};  // kernel launches each graph holds
   uint32_t graph_alloc = 0, graph_sink = 0, graph_mode = 0;
   // Confidence probe head (absent when the description has no probes):
   // probes [P][d] and projection row 0 [P * d] in params, the pool state in
@@ -2447,8 +2504,9 @@ void set_att(nd_needle* n, uint32_t l, MixArgs& m) {
   m.att = AttArgs{n->kv.k, n->kv.v, n->kv.ks, n->kv.vs, n->q, n->att, n->qkvg, n->st + 1,
                   l, n->d.kv_heads, n->kv.alloc, n->kv.sink, n->kv.window};
   m.att_groups = n->d.kv_heads;
-  m.att_target = m.qkv_groups - 1;  // every projection workgroup but the routing
-  m.att_count = n->wo_count + 32;
+  // per KV head: its query and gate heads, its key and its value
+  m.att_target = 2 * (n->d.heads / n->d.kv_heads) + 2;
+  m.att_count = n->wo_count + kAttStride;
 }
 
 // wo: for an int8 model, layer l - 1's Wo (with the post half) and layer
@@ -2874,7 +2932,18 @@ nd_status launch_graph(nd_ctx* ctx, nd_needle* n, GraphKind kind) {
       if (g) hipGraphDestroy(g);
       return nd_hip_fail(ctx, e != hipSuccess ? e : e2, "Needle step capture");
     }
-    const hipError_t e3 = hipGraphInstantiate(&n->graphs[kind], g, nullptr, nullptr, 0);
+    size_t count = 0;
+    hipError_t e3 = hipGraphGetNodes(g, nullptr, &count);
+    std::vector<hipGraphNode_t> nodes(count);
+    if (e3 == hipSuccess && count) e3 = hipGraphGetNodes(g, nodes.data(), &count);
+    uint32_t kernels = 0;
+    for (size_t i = 0; e3 == hipSuccess && i < count; ++i) {
+      hipGraphNodeType type;
+      e3 = hipGraphNodeGetType(nodes[i], &type);
+      kernels += type == hipGraphNodeTypeKernel;
+    }
+    n->graph_kernels[kind] = kernels;
+    if (e3 == hipSuccess) e3 = hipGraphInstantiate(&n->graphs[kind], g, nullptr, nullptr, 0);
     hipGraphDestroy(g);
     if (e3 != hipSuccess) {
       n->graphs[kind] = nullptr;
@@ -3508,7 +3577,8 @@ nd_status nd_needle_reset(nd_ctx* ctx, nd_needle* n, uint32_t max_length, uint32
     const size_t P8 = kMaxProbes * 8, cb = n->conf ? 1 : 0;
     const size_t sizes[] = {al(64), al((size_t)cap * 4), al((size_t)cap * 8),
                             al((size_t)S * n->depth * D * 4),
-                            al((size_t)d.kv_heads * kAttnCounterStride * 4), al(256),
+                            al((size_t)d.kv_heads * kAttnCounterStride * 4),
+                            al((size_t)(1 + d.kv_heads) * kAttStride * 4),
                             al((size_t)d.layers * 128), al(128),
                             cb * al(P8 * kMaxChunks), cb * al(P8 * kMaxChunks),
                             cb * al(P8 * D), al(64), al(64),
@@ -3855,6 +3925,13 @@ nd_status nd_needle_test_waits(nd_ctx* ctx, nd_needle* n, uint32_t extra_arrival
   drop_graphs(n);  // the launches' arguments change
   n->dbg_extra = extra_arrivals;
   n->dbg_spin = spin_rounds;
+  return ND_OK;
+}
+
+nd_status nd_needle_step_launches(nd_ctx* ctx, nd_needle* n, uint32_t* launches) {
+  if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
+  if (!n || !launches) return nd_fail(ctx, ND_ERR_INVALID, "NULL argument");
+  *launches = n->graphs[kGraphDecodeSelect] ? n->graph_kernels[kGraphDecodeSelect] : 0;
   return ND_OK;
 }
 

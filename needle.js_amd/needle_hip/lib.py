@@ -119,6 +119,7 @@ SIGNATURES = {
     "nd_needle_step_select_mask": (I32, [P, P, U32, P, U32, P, P]),
     "nd_needle_generate": (I32, [P, P, P, U32, U32, U32, U32, P, P, P]),
     "nd_needle_test_waits": (I32, [P, P, U32, U32]),
+    "nd_needle_step_launches": (I32, [P, P, PU32]),
     "nd_needle_test_stamps": (I32, [P, P, P, U32]),
     "nd_needle_begin_token": (I32, [P, P, P]),
     "nd_needle_prepare_engrams": (I32, [P, P, P, P, U32, U32]),

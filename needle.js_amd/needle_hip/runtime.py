@@ -223,6 +223,14 @@ class Needle2Resident:
         k = int(count.value)
         return out_ids[:k].copy(), out_lp[:k].copy()
 
+    def step_launches(self) -> int:
+        """Kernel launches of the decode-step graph (nd_needle_step_launches;
+        0 before the first generate step)."""
+        n = C.c_uint32()
+        self._check(self.lib.nd_needle_step_launches(self.ctx, self.handle, C.byref(n)),
+                    "nd_needle_step_launches")
+        return int(n.value)
+
     def test_waits(self, extra_arrivals: int, spin_rounds: int) -> None:
         """Test hook (nd_needle_test_waits): the fused layer launch's mix
         waits for `extra_arrivals` more output-projection workgroups than it

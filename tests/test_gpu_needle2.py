@@ -349,6 +349,10 @@ def test_generate_full_geometry_greedy_identical(hip):
         check_kv(model, ref, g, 128 + 63, 0, "generate")
         # the graph-replayed steps pooled every token they ran
         close_confidence(model.resident.confidence(), ref.confidence(), "generate confidence")
+        # one launch per layer (Wo, mix, projection and attention together)
+        # plus begin, the engram launches, the final mix, lm head, selection
+        # and the pool
+        assert model.resident.step_launches() == 2 + len(g.sites) + g.layers + 3 + 1
     finally:
         model.dispose()
 
