@@ -493,6 +493,9 @@ def bench_needle2_span(torch, hip, steps):
                      **{f"qkv_{nm}_{fn.__name__}": us(fn(e[W + 1: W + Q, i])) for i, nm in
                         ((4, "wait_over"), (5, "staged"), (6, "rows"), (7, "stored"))
                         for fn in (np.median, np.max)},
+                     **{f"wo_{nm}_{fn.__name__}": us(fn(e[:W, i])) for i, nm in
+                        ((0, "entry"), (4, "o_in"), (5, "w_in"), (6, "stored"))
+                        for fn in (np.median, np.max)},
                      **{f"att_{nm}_{fn.__name__}": us(fn(e[W + 1 + Q: W + 1 + Q + A, i]))
                         for i, nm in ((4, "wait_over"), (5, "issued"), (6, "tiles"), (7, "combined"),
                                       (8, "stored")) for fn in (np.median, np.max)},

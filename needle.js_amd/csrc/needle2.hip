@@ -1081,8 +1081,16 @@ struct MixArgs {
 // counts itself in: every one of these workgroups and the mix workgroup run
 // on one XCD (the launch uses workgroups L % 8 == 0 only), so both stay in
 // its L2.
-__device__ __forceinline__ void wo_rows(const MixArgs& a, uint32_t k) {
+// STAMP (measurement form): thread 0 writes the clock to marks[0..2] (LDS)
+// when o had arrived, the weights had arrived, and the rows were stored.
+template <bool STAMP = false>
+__device__ __forceinline__ void wo_rows(const MixArgs& a, uint32_t k, uint64_t* marks = nullptr) {
   const uint32_t t = threadIdx.x, tpr_log2 = a.wo_tpr_log2, tpr = 1u << tpr_log2;
+  auto mark = [&](int i) {
+    if constexpr (STAMP) {
+      if (t == 0) marks[i] = wall_clock64();
+    }
+  };
   const uint32_t rpw = kMixWg >> tpr_log2, sub = t >> tpr_log2, lk = t & (tpr - 1);
   const uint32_t row = k * rpw + sub;
   const bool ok = row < a.wo_n;
@@ -1103,6 +1111,10 @@ __device__ __forceinline__ void wo_rows(const MixArgs& a, uint32_t k) {
   float xs = 0.f;
 #pragma unroll
   for (int q = 0; q < 4; ++q) xs += (xr[4 * q] + xr[4 * q + 1]) + (xr[4 * q + 2] + xr[4 * q + 3]);
+  if constexpr (STAMP) {
+    asm volatile("" ::"v"(xs));
+    mark(0);
+  }
   const uint32_t words[4] = {wv.x ^ 0x80808080u, wv.y ^ 0x80808080u, wv.z ^ 0x80808080u,
                              wv.w ^ 0x80808080u};
   float d = -128.f * xs;
@@ -1110,6 +1122,10 @@ __device__ __forceinline__ void wo_rows(const MixArgs& a, uint32_t k) {
   for (int q = 0; q < 4; ++q)
 #pragma unroll
     for (int e = 0; e < 4; ++e) d = fmaf((float)((words[q] >> (8 * e)) & 0xffu), xr[4 * q + e], d);
+  if constexpr (STAMP) {
+    asm volatile("" ::"v"(d));
+    mark(1);
+  }
   float sum = 0.f;
   sum += fmaf(sv, d, 0.f);
   if (tpr > 32) sum += nd::lane_xor<32>(sum);
@@ -1122,6 +1138,7 @@ __device__ __forceinline__ void wo_rows(const MixArgs& a, uint32_t k) {
     __hip_atomic_store(const_cast<float*>(a.proj) + row, sum, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_WORKGROUP);
   __builtin_amdgcn_s_waitcnt(0);  // the rows are in the L2
+  mark(2);
   __syncthreads();
   if (t == 0) __hip_atomic_fetch_add(a.wo_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
@@ -1492,7 +1509,12 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
         else
           wo_cq_rows<2>(a.wo_cq, k, a.wo_count);
       } else {
-        wo_rows(a, k);
+        __shared__ uint64_t s_wo_marks[STAMP ? 4 : 1];
+        wo_rows<STAMP>(a, k, s_wo_marks);
+        if constexpr (STAMP) {
+          if (threadIdx.x == 0)
+            for (int i = 0; i < 3; ++i) stamp[4 + i] = s_wo_marks[i];
+        }
       }
       put_stamps(k);
       return;
