@@ -435,7 +435,7 @@ def bench_attention_span(torch, hip, length, heads, steps, warmup):
     return out_d
 
 
-def bench_needle2_span(torch, hip, steps):
+def bench_needle2_span(torch, hip, steps, cq_bits=None):
     """Needle 2 at the shipped geometry (int8), batch 1, after a 128-token
     prompt: `steps` direct whole-step calls with the fused layer launches in
     their measurement form (nd_needle_test_stamps).  Per layer launch of the
@@ -451,7 +451,8 @@ def bench_needle2_span(torch, hip, steps):
     from needle_hip.needle2 import Needle2Geometry, Needle2Weights
 
     g = Needle2Geometry()
-    model = NeedleModel(hip, Needle2Weights(g, 2026))
+    model = NeedleModel(hip, Needle2Weights(g, 2026, cq_bits=cq_bits, cq_group=32)
+                        if cq_bits else Needle2Weights(g, 2026))
     rt = model.create_resident_runtime()
     prompt = synth.Stream(2026, "needle2.prompt").integers(128, 0, g.vocab - 1)
     rt.reset(len(prompt) + steps + 1, 0)
@@ -467,7 +468,8 @@ def bench_needle2_span(torch, hip, steps):
     a = stamps.view(g.layers + 1, 64, 16).cpu().numpy().astype(np.int64)
     hip._check(hip.lib.nd_needle_test_stamps(hip.ctx, res.handle, None, 0))
     model.dispose()
-    W = g.dim // (512 // (g.heads * 64 // 16))  # Wo workgroups (16 rows each at d 512)
+    # Wo workgroups: int8 16 rows each at d 512, Cactus-Quant 64 rows each
+    W = g.dim // 64 if cq_bits else g.dim // (512 // (g.heads * 64 // 16))
     Q = 2 * (g.heads + g.kv_heads) + 1
     A = g.kv_heads
     rows = []
@@ -1005,7 +1007,7 @@ def main():
     ap.add_argument("--only", choices=["matvec", "matvec8", "attention", "decode", "prefill",
                                        "needle2", "needle2cq", "needle2mixed", "traffic", "attention_traffic", "cq",
                                        "grammar", "ceiling", "matvec_span", "copy_matvec",
-                                       "attention_span", "needle2_span"],
+                                       "attention_span", "needle2_span", "needle2_span_cq4"],
                     help="run one part alone and print its JSON (for profiling)")
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--no-check", action="store_true",
@@ -1049,6 +1051,8 @@ def main():
             part = bench_matvec_span(torch, hip, n, k, g, args.steps, args.warmup)
         elif args.only == "needle2_span":
             part = bench_needle2_span(torch, hip, 8)
+        elif args.only == "needle2_span_cq4":
+            part = bench_needle2_span(torch, hip, 8, cq_bits=4)
         elif args.only == "attention_span":
             part = bench_attention_span(torch, hip, 8192, 8, args.steps, args.warmup)
         elif args.only == "copy_matvec":

@@ -598,7 +598,8 @@ nd_status nd_needle_test_waits(nd_ctx* ctx, nd_needle* model, uint32_t extra_arr
 nd_status nd_needle_step_launches(nd_ctx* ctx, nd_needle* model, uint32_t* launches);
 
 /* Measurement, no counterpart in the reference: while stamps_dev is set
- * (capacity >= (layers + 1) x 1024 words, an int8 model), the fused layer
+ * (capacity >= (layers + 1) x 1024 words; an int8 model, or a Cactus-Quant
+ * one whose phi matrices share one format), the fused layer
  * launches of direct (not graph-replayed) whole-step calls (nd_needle_step,
  * nd_needle_step_select) run their measurement form: thread 0 of active
  * workgroup k of launch l writes the GPU's 100 MHz clock at entry, when the

@@ -2369,7 +2369,7 @@ struct nd_needle {
   uint32_t* status = nullptr;
   uint32_t* status_host = nullptr;
   uint32_t dbg_extra = 0, dbg_spin = 0;
-  uint64_t* dbg_stamps = nullptr;  // measurement: the int8 fused launches' clock stamps
+  uint64_t* dbg_stamps = nullptr;  // measurement: the fused launches' clock stamps
   double *lp_history = nullptr, *sel_lp = nullptr;
   uint32_t* cq_lookup = nullptr;  // CQ model: a step's engram lookups and token
   float *ring = nullptr, *x = nullptr, *upd = nullptr, *blk = nullptr, *ain = nullptr,
@@ -2597,10 +2597,14 @@ hipError_t enqueue_mix(nd_needle* n, uint32_t l, uint32_t parts, hipStream_t s, 
       if (att) set_att(n, l, m);
     }
     const dim3 grid(8 * (m.wo_groups + 1 + m.qkv_groups + m.att_groups));
-    if (n->phi_uniform)
+    if (n->dbg_stamps && n->phi_uniform && grid.x <= 8 * 64) {  // measurement form
+      m.stamps = n->dbg_stamps + (size_t)l * 64 * 16;
+      hipLaunchKernelGGL((n2_mix_kernel<true, true, true, true>), grid, dim3(kMixWg), 0, s, m);
+    } else if (n->phi_uniform) {
       hipLaunchKernelGGL((n2_mix_kernel<true, true, true>), grid, dim3(kMixWg), 0, s, m);
-    else
+    } else {
       hipLaunchKernelGGL((n2_mix_kernel<true, true, false>), grid, dim3(kMixWg), 0, s, m);
+    }
   } else if (n->cq) {
     if (n->phi_uniform)
       hipLaunchKernelGGL((n2_mix_kernel<true, false, true>), dim3(1), dim3(kMixWg), 0, s, m);
@@ -3960,9 +3964,10 @@ nd_status nd_needle_step_launches(nd_ctx* ctx, nd_needle* n, uint32_t* launches)
 nd_status nd_needle_test_stamps(nd_ctx* ctx, nd_needle* n, uint64_t* stamps, uint32_t capacity) {
   if (!ctx) return nd_fail(nullptr, ND_ERR_BACKEND, "context is NULL");
   if (!n) return nd_fail(ctx, ND_ERR_INVALID, "NULL model");
-  if (stamps && (n->cq || capacity < (n->d.layers + 1) * 64 * 16))
+  if (stamps && ((n->cq && !n->phi_uniform) || capacity < (n->d.layers + 1) * 64 * 16))
     return nd_fail(ctx, ND_ERR_INVALID,
-                   "nd_needle_test_stamps: an int8 model and room for %u stamps",
+                   "nd_needle_test_stamps: an int8 model or a Cactus-Quant one whose phi "
+                   "matrices share one format, and room for %u stamps",
                    (n->d.layers + 1) * 64 * 16);
   n->dbg_stamps = stamps;
   return ND_OK;
