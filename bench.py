@@ -481,8 +481,11 @@ def bench_needle2_span(torch, hip, steps, cq_bits=None):
         mix = e[W]
         phases = {f"mix_{nm}": us(mix[i]) for i, nm in
                   ((4, "post_norms"), (5, "fwht1"), (6, "fwht2"), (7, "lanes"), (8, "pre_norm"),
-                   (9, "phi"), (10, "engram"), (11, "input_norm"), (12, "phi_split"),
-                   (13, "phi_mfma"), (14, "phi_part"))}
+                   (9, "phi"), (10, "engram"), (11, "input_norm"),
+                   # int8 phi rows: split into LDS, MFMA done, wave partials
+                   # met; Cactus-Quant: lanes in LDS, rotated, rows done
+                   *(((12, "phi_staged"), (13, "phi_rotated"), (14, "phi_rows")) if cq_bits
+                     else ((12, "phi_split"), (13, "phi_mfma"), (14, "phi_part"))))}
         rows.append({**phases, "wo_done": us(e[:W, 3].max()), "mix_entry": us(mix[0]),
                      "mix_wo_wait_done": us(mix[1]), "mix_signal": us(mix[2]),
                      "mix_exit": us(mix[3]), "qkv_done": us(e[W + 1: W + 1 + Q, 3].max()),
@@ -495,8 +498,11 @@ def bench_needle2_span(torch, hip, steps, cq_bits=None):
                      **{f"qkv_{nm}_{fn.__name__}": us(fn(e[W + 1: W + Q, i])) for i, nm in
                         ((4, "wait_over"), (5, "staged"), (6, "rows"), (7, "stored"))
                         for fn in (np.median, np.max)},
+                     # the Wo workgroups: int8 o in, weights in, stored;
+                     # Cactus-Quant input staged, rows computed, stored
                      **{f"wo_{nm}_{fn.__name__}": us(fn(e[:W, i])) for i, nm in
-                        ((0, "entry"), (4, "o_in"), (5, "w_in"), (6, "stored"))
+                        ((0, "entry"), *(((4, "staged"), (5, "rows"), (6, "stored")) if cq_bits
+                                         else ((4, "o_in"), (5, "w_in"), (6, "stored"))))
                         for fn in (np.median, np.max)},
                      **{f"att_{nm}_{fn.__name__}": us(fn(e[W + 1 + Q: W + 1 + Q + A, i]))
                         for i, nm in ((4, "wait_over"), (5, "issued"), (6, "tiles"), (7, "combined"),

@@ -561,18 +561,51 @@ __device__ __forceinline__ void cq_rows_load(const CqRows& q, uint32_t bits, siz
   }
 }
 
+// The butterflies of fastWalshHadamard (backends/cq.ts:8-27) with strides
+// below min(g, 64) over values held one per lane, element e in lane e % 64
+// (groups of g are aligned, so a group below 64 values lies in one wave):
+// stride s pairs lane i with lane i ^ s, the lower lane takes a + b and the
+// upper a - b of the reference's two operands (a the lower element), one
+// fp32 add or subtract each.  Every lane of the wave must take part.
+__device__ __forceinline__ float cq_rotate_lanes(float v, uint32_t g, uint32_t lane) {
+  auto stage = [&](auto m) {
+    constexpr int M = decltype(m)::value;
+    const float other = nd::lane_xor<M>(v);
+    v = (lane & M) ? other - v : v + other;
+  };
+  if (g > 1) stage(std::integral_constant<int, 1>{});
+  if (g > 2) stage(std::integral_constant<int, 2>{});
+  if (g > 4) stage(std::integral_constant<int, 4>{});
+  if (g > 8) stage(std::integral_constant<int, 8>{});
+  if (g > 16) stage(std::integral_constant<int, 16>{});
+  if (g > 32) stage(std::integral_constant<int, 32>{});
+  return v;
+}
+
+// x (d <= kpad <= 512 values, zeros past d) into xs for cq_rows_dot, by a
+// 512-thread workgroup, one element per thread: element e at e + e / 32 (one
+// pad float after every 32, so that the 16 units' reads fall in distinct
+// banks), the strides below min(g, 64) of the per-group rotation applied
+// (cq_rotate_lanes).  The caller's barrier publishes xs.
+__device__ __forceinline__ void cq_stage_rotated(const float* x, uint32_t d, uint32_t kpad,
+                                                 uint32_t g, float* xs, uint32_t t) {
+  static_assert(kQkvWg == 512 && kMixWg == 512, "one input element per thread");
+  float v = t < d ? x[t] : 0.f;
+  v = cq_rotate_lanes(v, g, t & 63);
+  if (t < kpad) xs[t + (t >> 5)] = v;
+}
+
 // Rows r and r + 32 of the workgroup's 64 (r = t / 16) of a Cactus-Quant
 // product with d <= 512 inputs (cqMatvec, backends/cq.ts:106-231) from the
-// operands cq_rows_load gave thread t (unit u = t % 16 of both rows).  xs
-// holds x with one pad float after every 32 (element e at e + e / 32, zeros
-// past d), so the 16 units' reads fall in distinct banks.  The unit's inputs
-// are rotated in registers -- the butterflies of fastWalshHadamard with
-// strides below min(g, 32), then strides 32 .. g / 2 across the lanes
-// holding the group's other units -- each result one fp32 add or subtract of
-// the reference's two operands; the codes index the codebook in LDS; fp32
-// dots per group times the group's norm, summed over the row's 16 lanes,
-// times 1/sqrt(g).  Returns the two row values in every lane of the row.
-template <uint32_t BITS>
+// operands cq_rows_load gave thread t (unit u = t % 16 of both rows) and
+// the input cq_stage_rotated left in xs.  The group's remaining strides
+// (64 .. g / 2, g > 64) run across the lanes holding the group's other
+// units, each result one fp32 add or subtract of the reference's two
+// operands; the codes index the codebook in LDS; fp32 dots per group times
+// the group's norm, summed over the row's 16 lanes, times 1/sqrt(g).
+// Returns the two row values in every lane of the row.  G32: g >= 32 (one
+// group end per unit); otherwise g is 8 or 16.
+template <uint32_t BITS, bool G32>
 __device__ __forceinline__ float2 cq_rows_dot(const CqRows& q, const CqRowRegs& R,
                                               uint32_t units, const float* xs, const float* cb,
                                               uint32_t t) {
@@ -582,54 +615,48 @@ __device__ __forceinline__ float2 cq_rows_dot(const CqRows& q, const CqRowRegs& 
   float v[32];
 #pragma unroll
   for (int c = 0; c < 32; ++c) v[c] = xs[uc * 33 + c];
-  const uint32_t gs = q.g < 32 ? q.g : 32u;
+  if constexpr (G32) {
+    auto cross = [&](auto m) {
+      constexpr int M = decltype(m)::value;
+      const bool right = (t & M) != 0;
 #pragma unroll
-  for (uint32_t st = 1; st < 32; st <<= 1) {
-    if (st < gs) {
-#pragma unroll
-      for (uint32_t c = 0; c < 32; ++c)
-        if (!(c & st)) {
-          const float a = v[c], b = v[c + st];
-          v[c] = a + b;
-          v[c + st] = a - b;
-        }
-    }
+      for (int c = 0; c < 32; ++c) {
+        const float other = nd::lane_xor<M>(v[c]);
+        v[c] = right ? other - v[c] : v[c] + other;
+      }
+    };
+    if (q.g > 64) cross(std::integral_constant<int, 2>{});
+    if (q.g > 128) cross(std::integral_constant<int, 4>{});
+    if (q.g > 256) cross(std::integral_constant<int, 8>{});
   }
-  auto cross = [&](auto m) {
-    constexpr int M = decltype(m)::value;
-    const bool right = (t & M) != 0;
-#pragma unroll
-    for (int c = 0; c < 32; ++c) {
-      const float other = nd::lane_xor<M>(v[c]);
-      v[c] = right ? other - v[c] : v[c] + other;
-    }
-  };
-  const uint32_t lpg = q.g > 32 ? q.g >> 5 : 1u;  // lanes of a group
-  if (lpg > 1) cross(std::integral_constant<int, 1>{});
-  if (lpg > 2) cross(std::integral_constant<int, 2>{});
-  if (lpg > 4) cross(std::integral_constant<int, 4>{});
-  if (lpg > 8) cross(std::integral_constant<int, 8>{});
   float out[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     float total = 0.f, dot = 0.f;
 #pragma unroll
     for (uint32_t c = 0; c < 32; ++c) {
-      uint32_t code;
+      float w;
       if constexpr (BITS == 4) {
-        code = (R.w[i][c >> 3] >> (4 * (c & 7))) & 15u;
+        // The entry's byte offset code * 4: nibble k of a word sits at bits
+        // 2..5 of byte k / 2 of the word shifted left by 2 (k even) or right
+        // by 2 (k odd).
+        const uint32_t word = R.w[i][c >> 3];
+        const uint32_t sh = (c & 1) ? word >> 2 : word << 2;
+        w = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(cb) +
+                                            ((sh >> (8 * ((c & 7) >> 1))) & 0x3cu));
       } else if constexpr (BITS == 3) {
         const uint32_t bit = 3 * c, k = bit >> 5, sh = bit & 31;
         const uint32_t hi = sh > 29 ? R.w[i][k + 1 < 3 ? k + 1 : 2] << (32 - sh) : 0u;
-        code = ((R.w[i][k] >> sh) | hi) & 7u;
+        w = cb[((R.w[i][k] >> sh) | hi) & 7u];
       } else {
-        code = (R.w[i][c >> 4] >> (2 * (c & 15))) & 3u;
+        w = cb[(R.w[i][c >> 4] >> (2 * (c & 15))) & 3u];
       }
-      dot = fmaf(cb[code], v[c], dot);
-      if ((c & 7) == 7) {  // a group of 8, 16 or 32 and wider may end here: by selection
-        const bool ends = c == 31 || q.g == 8 || (q.g == 16 && (c & 15) == 15);
-        const uint32_t h =
-            q.g == 8 ? R.nb[i][c >> 3] : (q.g == 16 ? R.nb[i][c >> 4] : R.nb[i][0]);
+      dot = fmaf(w, v[c], dot);
+      if constexpr (G32) {
+        if (c == 31) total = fmaf(nd::cq_half(R.nb[i][0]), dot, total);
+      } else if ((c & 7) == 7) {  // a group of 8 or 16 may end here: by selection
+        const bool ends = q.g == 8 || (c & 15) == 15;
+        const uint32_t h = q.g == 8 ? R.nb[i][c >> 3] : R.nb[i][c >> 4];
         const float with = fmaf(nd::cq_half(h), dot, total);
         total = ends ? with : total;
         dot = ends ? 0.f : dot;
@@ -645,13 +672,14 @@ __device__ __forceinline__ float2 cq_rows_dot(const CqRows& q, const CqRowRegs& 
   return float2{out[0], out[1]};
 }
 
-// Both phases at once, for a block whose width is known at compile time.
+// cq_rows_dot by code width (2-bit codes and ternary crumbs as 2) and group
+// class.
 template <uint32_t BITS>
-__device__ __forceinline__ float2 cq_rows_pair(const CqRows& q, size_t row0, uint32_t units,
-                                               const float* xs, const float* cb, uint32_t t) {
-  CqRowRegs R;
-  cq_rows_load(q, BITS, row0, units, t, R);
-  return cq_rows_dot<BITS>(q, R, units, xs, cb, t);
+__device__ __forceinline__ float2 cq_rows_dot_g(const CqRows& q, const CqRowRegs& R,
+                                                uint32_t units, const float* xs, const float* cb,
+                                                uint32_t t) {
+  if (q.g >= 32) return cq_rows_dot<BITS, true>(q, R, units, xs, cb, t);
+  return cq_rows_dot<BITS, false>(q, R, units, xs, cb, t);
 }
 
 // The fused Q/K/V/gate projection of one layer (runtime.ts:465-470) with the
@@ -708,13 +736,14 @@ struct QkvParams {
   uint32_t cq_bits[4];
 };
 
-// cq_rows_dot by code width (2-bit codes and ternary crumbs as 2).
+// cq_rows_dot by code width (2-bit codes and ternary crumbs as 2) and group
+// class.
 __device__ __forceinline__ float2 cq_rows_dot_any(uint32_t bits, const CqRows& q,
                                                   const CqRowRegs& R, uint32_t units,
                                                   const float* xs, const float* cb, uint32_t t) {
-  if (bits == 4) return cq_rows_dot<4>(q, R, units, xs, cb, t);
-  if (bits == 3) return cq_rows_dot<3>(q, R, units, xs, cb, t);
-  return cq_rows_dot<2>(q, R, units, xs, cb, t);
+  if (bits == 4) return cq_rows_dot_g<4>(q, R, units, xs, cb, t);
+  if (bits == 3) return cq_rows_dot_g<3>(q, R, units, xs, cb, t);
+  return cq_rows_dot_g<2>(q, R, units, xs, cb, t);
 }
 
 // Workgroup b of the projection launch (b == 2 (heads + kv_heads): the
@@ -866,8 +895,9 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
       release();
       return;
     }
-    for (uint32_t i = t; i < kpad; i += kQkvWg) xs[i + (i >> 5)] = i < d ? p.x[i] : 0.f;
+    cq_stage_rotated(p.x, d, kpad, q.g, xs, t);
     __syncthreads();
+    mark(1);
     const float2 v = cq_rows_dot_any(bits, q, R, kpad / 32, xs, s_cb, t);
     if ((t & 15) == 0) {
       rows[t >> 4] = v.x;
@@ -919,12 +949,20 @@ struct WoCq {
 };
 
 // Rows [64 k, +64) of w.  count (the fused launch): after the rows are in
-// the XCD's L2, add one to *count.
-template <uint32_t BITS>
-__device__ __forceinline__ void wo_cq_rows(const WoCq& w, uint32_t k, uint32_t* count) {
+// the XCD's L2, add one to *count.  STAMP (measurement form): thread 0
+// writes the clock to marks[0..2] (LDS) when the input was staged, the rows
+// were computed and the rows were stored.
+template <uint32_t BITS, bool STAMP = false>
+__device__ __forceinline__ void wo_cq_rows(const WoCq& w, uint32_t k, uint32_t* count,
+                                           uint64_t* marks = nullptr) {
   __shared__ float xs[512 + 16];
   __shared__ float s_cb[16];
   const uint32_t t = threadIdx.x;
+  auto mark = [&](int i) {
+    if constexpr (STAMP) {
+      if (t == 0) marks[i] = wall_clock64();
+    }
+  };
   const uint32_t kpad = w.cq.groups << w.cq.g_log2;  // the padded row (<= 512)
   CqRowRegs R;  // the rows' packed words and norms first
   cq_rows_load(w.cq, BITS, (size_t)k * 64, kpad / 32, t, R);
@@ -932,9 +970,14 @@ __device__ __forceinline__ void wo_cq_rows(const WoCq& w, uint32_t k, uint32_t* 
 #pragma unroll
     for (int i = 0; i < 16; ++i) s_cb[i] = w.cq.cb[i];
   }
-  for (uint32_t i = t; i < kpad; i += kMixWg) xs[i + (i >> 5)] = i < w.k ? w.x[i] : 0.f;
+  cq_stage_rotated(w.x, w.k, kpad, w.cq.g, xs, t);
   __syncthreads();
-  const float2 v = cq_rows_dot<BITS>(w.cq, R, kpad / 32, xs, s_cb, t);
+  mark(0);
+  const float2 v = cq_rows_dot_g<BITS>(w.cq, R, kpad / 32, xs, s_cb, t);
+  if constexpr (STAMP) {
+    asm volatile("" ::"v"(v.x), "v"(v.y));
+    mark(1);
+  }
   if ((t & 15) == 0) {
     const uint32_t r = k * 64 + (t >> 4);
     __hip_atomic_store(w.y + r, v.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -942,6 +985,7 @@ __device__ __forceinline__ void wo_cq_rows(const WoCq& w, uint32_t k, uint32_t* 
   }
   if (count) {
     __builtin_amdgcn_s_waitcnt(0);  // the rows are in the L2
+    mark(2);
     __syncthreads();
     if (t == 0) __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
@@ -1501,20 +1545,20 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     if (blockIdx.x & 7) return;
     const uint32_t k = blockIdx.x >> 3;
     if (k < a.wo_groups) {
+      __shared__ uint64_t s_wo_marks[STAMP ? 4 : 1];
       if constexpr (CQ) {
         if (a.wo_bits == 4)
-          wo_cq_rows<4>(a.wo_cq, k, a.wo_count);
+          wo_cq_rows<4, STAMP>(a.wo_cq, k, a.wo_count, s_wo_marks);
         else if (a.wo_bits == 3)
-          wo_cq_rows<3>(a.wo_cq, k, a.wo_count);
+          wo_cq_rows<3, STAMP>(a.wo_cq, k, a.wo_count, s_wo_marks);
         else
-          wo_cq_rows<2>(a.wo_cq, k, a.wo_count);
+          wo_cq_rows<2, STAMP>(a.wo_cq, k, a.wo_count, s_wo_marks);
       } else {
-        __shared__ uint64_t s_wo_marks[STAMP ? 4 : 1];
         wo_rows<STAMP>(a, k, s_wo_marks);
-        if constexpr (STAMP) {
-          if (threadIdx.x == 0)
-            for (int i = 0; i < 3; ++i) stamp[4 + i] = s_wo_marks[i];
-        }
+      }
+      if constexpr (STAMP) {
+        if (threadIdx.x == 0)
+          for (int i = 0; i < 3; ++i) stamp[4 + i] = s_wo_marks[i];
       }
       put_stamps(k);
       return;
@@ -1789,18 +1833,25 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
         }
     }
     nd::lds_barrier();
+    mark(12);
     const uint32_t units = N / 32, uc = lane < units ? lane : 0;
     if constexpr (PU) {
       float xu[32];
 #pragma unroll
       for (int c = 0; c < 32; ++c) xu[c] = s_cqx[uc * 33 + c];
       cq_rotate_unit(xu, a.cq_g[0], a.cq_inv_root[0], lane);
+      if constexpr (STAMP) {
+#pragma unroll
+        for (int c = 0; c < 32; ++c) asm volatile("" ::"v"(xu[c]));
+        mark(13);
+      }
       if (a.cq_bits[0] == 4)
         cq_phi_rows<4>(cw, cn, xu, s_cb[0], a.cq_g[0], units, nrows, wave, lane, phi);
       else if (a.cq_bits[0] == 3)
         cq_phi_rows<3>(cw, cn, xu, s_cb[0], a.cq_g[0], units, nrows, wave, lane, phi);
       else  // 2-bit codes and ternary crumbs
         cq_phi_rows<2>(cw, cn, xu, s_cb[0], a.cq_g[0], units, nrows, wave, lane, phi);
+      mark(14);
     } else {
     // Rows j = 0 take the rotation by their own matrix's group, rows j >= 1
     // (phi_res) by phi_res's; one rotation serves both when the groups agree.

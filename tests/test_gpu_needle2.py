@@ -357,9 +357,10 @@ def test_generate_full_geometry_greedy_identical(hip):
         model.dispose()
 
 
-@pytest.mark.parametrize("cq_bits,sink", [(4, 3), (3, 0), (2, 0), (5, 3), ("mixed", 3),
-                                          ("mixed", 0)])
-def test_cactus_quant_model_steps_prefill_and_generate(hip, cq_bits, sink):
+@pytest.mark.parametrize("cq_bits,sink,group", [(4, 3, 32), (3, 0, 32), (2, 0, 32), (5, 3, 32),
+                                                ("mixed", 3, 32), ("mixed", 0, 32), (4, 0, 16),
+                                                (3, 3, 8)])
+def test_cactus_quant_model_steps_prefill_and_generate(hip, cq_bits, sink, group):
     """The resident runtime over Cactus-Quant matrices, the form every matrix
     of the shipped archive takes (model/cact.ts:398-562, backends/cq.ts:106-295),
     one width for every matrix or each matrix its own width and group
@@ -367,9 +368,9 @@ def test_cactus_quant_model_steps_prefill_and_generate(hip, cq_bits, sink):
     logits, the cache and the confidence against the oracle's cqMatvec /
     dequantizeCqRow restatement, a prompt (one batched pass while its cache
     slots do not wrap, steps after) and a greedy continuation with identical
-    ids."""
-    say("needle2 cactus-quant", cq_bits, sink)
-    w = Needle2Weights(SMALL, 51, cq_bits=cq_bits)
+    ids.  Groups of 8 and 16 put several groups in each 32-code unit."""
+    say("needle2 cactus-quant", cq_bits, sink, group)
+    w = Needle2Weights(SMALL, 51, cq_bits=cq_bits, cq_group=group)
     model = NeedleModel(hip, w)
     try:
         rt = model.create_resident_runtime()
