@@ -1320,17 +1320,20 @@ __device__ __forceinline__ double cq_phi_row(const uint32_t (&w)[4], const uint3
     float dot8[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (uint32_t c = 0; c < 32; ++c) {
-      uint32_t code;
+      float e;
       if constexpr (BITS == 4) {
-        code = (w[c >> 3] >> (4 * (c & 7))) & 15u;
+        // The entry's byte offset code * 4 (as in cq_rows_dot).
+        const uint32_t sh = (c & 1) ? w[c >> 3] >> 2 : w[c >> 3] << 2;
+        e = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(cb) +
+                                            ((sh >> (8 * ((c & 7) >> 1))) & 0x3cu));
       } else if constexpr (BITS == 3) {
         const uint32_t bit = 3 * c, k = bit >> 5, sh = bit & 31;
         const uint32_t hi = sh > 29 ? w[k + 1 < 4 ? k + 1 : 3] << (32 - sh) : 0u;
-        code = ((w[k] >> sh) | hi) & 7u;
+        e = cb[((w[k] >> sh) | hi) & 7u];
       } else {
-        code = (w[c >> 4] >> (2 * (c & 15))) & 3u;
+        e = cb[(w[c >> 4] >> (2 * (c & 15))) & 3u];
       }
-      dot8[c >> 3] = fmaf(cb[code], xu[c], dot8[c >> 3]);
+      dot8[c >> 3] = fmaf(e, xu[c], dot8[c >> 3]);
     }
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -1403,6 +1406,31 @@ __device__ __forceinline__ void cq_rotate_unit(float (&xu)[32], uint32_t g, doub
   if (lpg > 8) cross(std::integral_constant<int, 8>{});
   if (lpg > 16) cross(std::integral_constant<int, 16>{});
   if (lpg > 32) cross(std::integral_constant<int, 32>{});
+#pragma unroll
+  for (int c = 0; c < 32; ++c) xu[c] = (float)((double)xu[c] * inv_root);
+}
+
+// The strides 64 .. g / 2 (g > 64) of prepareCqActivation over one 32-value
+// unit per lane (stride 64 pairs the units two lanes apart), each result one
+// fp32 add or subtract of the reference's two operands, then times
+// 1/sqrt(g) in float64: the end of cq_rotate_unit for a unit whose strides
+// below 64 are done.
+__device__ __forceinline__ void cq_rotate_wide(float (&xu)[32], uint32_t g, double inv_root,
+                                               uint32_t lane) {
+  auto cross = [&](auto m) {
+    constexpr int M = decltype(m)::value;
+    const bool right = (lane & M) != 0;
+#pragma unroll
+    for (int c = 0; c < 32; ++c) {
+      const float other = nd::lane_xor<M>(xu[c]);
+      xu[c] = right ? other - xu[c] : xu[c] + other;
+    }
+  };
+  if (g > 64) cross(std::integral_constant<int, 2>{});
+  if (g > 128) cross(std::integral_constant<int, 4>{});
+  if (g > 256) cross(std::integral_constant<int, 8>{});
+  if (g > 512) cross(std::integral_constant<int, 16>{});
+  if (g > 1024) cross(std::integral_constant<int, 32>{});
 #pragma unroll
   for (int c = 0; c < 32; ++c) xu[c] = (float)((double)xu[c] * inv_root);
 }
@@ -1824,12 +1852,26 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     // wave's reads fall in distinct banks) and rotates its own copy in
     // registers, strides below 32 inside the unit and strides 32 .. g / 2
     // across the lanes holding the group's other units.
+    // PU with d a multiple of 64: thread t holds element l d + t of every
+    // lane l, so a group below 64 values lies in one wave and its strides
+    // run across the wave's lanes once (cq_rotate_lanes), then times
+    // 1/sqrt(g) when the group ends there; each wave then takes the wider
+    // groups' strides 64 .. g / 2 across the lanes holding the group's other
+    // units, and their scaling.  The same operations on the same operands
+    // as cq_rotate_unit, done once instead of once per wave.
+    const uint32_t g0 = a.cq_g[0];
+    const bool lanes_rot = PU && (D & 63u) == 0;
     if (col) {
 #pragma unroll
       for (int l = 0; l < 4; ++l)
         if ((uint32_t)l < L) {
           const uint32_t e = l * D + t;
-          s_cqx[e + (e >> 5)] = (float)((double)xl[l] * inv);
+          float v = (float)((double)xl[l] * inv);
+          if (lanes_rot) {
+            v = cq_rotate_lanes(v, g0, lane);
+            if (g0 <= 64) v = (float)((double)v * a.cq_inv_root[0]);
+          }
+          s_cqx[e + (e >> 5)] = v;
         }
     }
     nd::lds_barrier();
@@ -1839,7 +1881,11 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
       float xu[32];
 #pragma unroll
       for (int c = 0; c < 32; ++c) xu[c] = s_cqx[uc * 33 + c];
-      cq_rotate_unit(xu, a.cq_g[0], a.cq_inv_root[0], lane);
+      if (lanes_rot) {
+        if (g0 > 64) cq_rotate_wide(xu, g0, a.cq_inv_root[0], lane);
+      } else {
+        cq_rotate_unit(xu, g0, a.cq_inv_root[0], lane);
+      }
       if constexpr (STAMP) {
 #pragma unroll
         for (int c = 0; c < 32; ++c) asm volatile("" ::"v"(xu[c]));
