@@ -335,8 +335,10 @@ __device__ __forceinline__ void attention_body(
 #pragma unroll
     for (int h = 0; h < REP; ++h) {
       float tile_max = fmaxf(fmaxf(p[h][0], p[h][1]), fmaxf(p[h][2], p[h][3]));
-      tile_max = fmaxf(tile_max, nd::lane_xor<4>(tile_max));
-      tile_max = fmaxf(tile_max, nd::lane_xor<8>(tile_max));
+      // rows rotated by 4, then 8: the max over lanes i, i - 4, i - 8, i - 12
+      // of each 16-lane row, the set lane xor 4 and 8 span
+      tile_max = fmaxf(tile_max, nd::dpp<nd::kRowRor4>(tile_max));
+      tile_max = fmaxf(tile_max, nd::dpp<nd::kRowRor8>(tile_max));
       tile_max = fmaxf(tile_max, nd::lane_xor<16>(tile_max));
       tile_max = fmaxf(tile_max, nd::lane_xor<32>(tile_max));
       const float m_new = fmaxf(m[h], tile_max);
@@ -465,6 +467,10 @@ __device__ __forceinline__ void attention_body(
   // Per wave: fold the 16 token rows of each lane's partial sums 4 apart
   // (lane bits 2..3) with DPP, leaving 4 row groups (lane bits 4..5) that go
   // to LDS; l is the same in the 4 lanes of a quad and m in the whole wave.
+  // The fold adds the row rotated by 4, then by 8 (one DPP add each): lane
+  // j + 12 of a 16-lane row (j < 4) ends with (a[j+12] + a[j+8]) + (a[j+4] +
+  // a[j]), the sums a fold by lane xor 4 then 8 leaves in lane j, operand for
+  // operand (each add commutes exactly), and it is the lane that stores.
   constexpr int kOut = REP * kHeadDim;  // outputs (head, dim) of the workgroup
   __shared__ float s_m[(uint32_t)KW][REP], s_l[(uint32_t)KW][REP];
   __shared__ float s_part[(uint32_t)KW * 4][kOut];
@@ -473,10 +479,10 @@ __device__ __forceinline__ void attention_body(
     const float lw = nd::wave_sum(quad == 0 ? l[h] : 0.f);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      acc[h][i] += nd::lane_xor<4>(acc[h][i]);
-      acc[h][i] += nd::lane_xor<8>(acc[h][i]);
+      acc[h][i] += nd::dpp<nd::kRowRor4>(acc[h][i]);
+      acc[h][i] += nd::dpp<nd::kRowRor8>(acc[h][i]);
     }
-    if ((trow & 3) == 0) {
+    if ((trow & 3) == 3) {
       float4* dst = reinterpret_cast<float4*>(&s_part[wave * 4 + (lane >> 4)][h * kHeadDim + quad * 16]);
 #pragma unroll
       for (int c = 0; c < 4; ++c)

@@ -13,9 +13,13 @@ constexpr int kQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
 constexpr int kHalfMirror = 0x141;  // lane i of 8 <- lane 7 - i
 constexpr int kRowMirror = 0x140;   // lane i of 16 <- lane 15 - i
 
+// Every control used here is a full permutation (each lane reads a lane of
+// its own row), so bound_ctrl never applies; given as an update with it set,
+// the move folds into the VALU operation that consumes it (v_add_f32_dpp
+// and the like: one instruction per reduction step).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
 template <int CTRL>
