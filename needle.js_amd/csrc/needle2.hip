@@ -1015,6 +1015,9 @@ struct AttArgs {
 struct MixArgs {
   float* x;  // [lanes][d]: read, and rewritten when has_post
   uint32_t d, hdim, lanes;
+  // log2 of d, lanes * d and lanes when a power of two, else -1 (means over
+  // them scale exactly: div_pow2)
+  int32_t d_log2, n_log2, l_log2;
   // post-attention half of layer l - 1 (runtime.ts:509-542, #attentionDelta
   // runtime.ts:585-611); routing and h-post come from the route workgroup of
   // the Q/K/V launch of layer l - 1
@@ -1196,8 +1199,19 @@ inline double host_sigmoid(double v) {
   return e / (1.0 + e);
 }
 
+// log2 of n when n is a power of two, else -1.
+inline int32_t log2_exact(uint32_t n) {
+  if (n == 0 || (n & (n - 1))) return -1;
+  int32_t k = 0;
+  while ((1u << k) < n) ++k;
+  return k;
+}
+
 // The mix launch constants derived from the geometry and the layer's gate.
 inline void mix_constants(MixArgs& m, uint32_t d, uint32_t hdim, uint32_t lanes, float gate) {
+  m.d_log2 = log2_exact(d);
+  m.n_log2 = log2_exact(lanes * d);
+  m.l_log2 = log2_exact(lanes);
   m.attention_scale = host_sigmoid((double)gate);
   m.inv_root_h = 1.0 / std::sqrt((double)hdim);
   m.sqrt_d = std::sqrt((double)d);
@@ -1212,6 +1226,12 @@ inline void mix_constants(MixArgs& m, uint32_t d, uint32_t hdim, uint32_t lanes,
 // call's barrier, which every reader of the previous call has passed (the
 // barrier waits for the wave's own LDS reads first).  mix_sum2 reduces two
 // values in the same round.
+// s / n in float64: for n = 2^k (log2n = k >= 0) the exact scaling ldexp(s,
+// -k), which is the correctly rounded quotient itself; a division otherwise.
+__device__ __forceinline__ double div_pow2(double s, int32_t log2n, uint32_t n) {
+  return log2n >= 0 ? ldexp(s, -log2n) : s / (double)n;
+}
+
 __device__ __forceinline__ double mix_sum(double v, double (*red)[2 * (kMixWg / 64)], int& phase) {
   v = nd::wave_sum(v);
   if ((threadIdx.x & 63) == 0) red[phase][threadIdx.x >> 6] = v;
@@ -1761,7 +1781,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   // ---- post(l - 1)
   if (a.has_post) {
     const double sp = mix_sum(col ? (double)p * p : 0.0, red, phase);
-    const double ip = 1.0 / sqrt(sp / D + 1e-6);
+    const double ip = 1.0 / sqrt(div_pow2(sp, a.d_log2, D) + 1e-6);
     float after = 0.f;
     if (col) {
       const float np = (float)((1.0 + (double)post_norm) * (double)p * ip);
@@ -1769,7 +1789,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     }
     if (t < L * L + L) rt[t] = route;  // visible after the next barrier
     const double sa = mix_sum(col ? (double)after * after : 0.0, red, phase);
-    const double ia = 1.0 / sqrt(sa / D + 1e-6);
+    const double ia = 1.0 / sqrt(div_pow2(sa, a.d_log2, D) + 1e-6);
     mark(4);
     // hadamardMlp (math.ts:117-138): FWHT(d1 x), SiLU(z / sqrt(H) * d2),
     // FWHT, / sqrt(H) * d3.
@@ -1813,7 +1833,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
 #pragma unroll
         for (int l = 0; l < 4; ++l)
           if ((uint32_t)l < L) sum += xl[l];
-        a.cell[t] = (float)(sum / L);
+        a.cell[t] = (float)div_pow2(sum, a.l_log2, L);
       }
     }
   }
@@ -1824,10 +1844,10 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
 #pragma unroll
       for (int l = 0; l < 4; ++l)
         if ((uint32_t)l < L) sum += xl[l];
-      m = (float)(sum / L);
+      m = (float)div_pow2(sum, a.l_log2, L);
     }
     const double ss = mix_sum(col ? (double)m * m : 0.0, red, phase);
-    const double inv = 1.0 / sqrt(ss / D + 1e-6);
+    const double inv = 1.0 / sqrt(div_pow2(ss, a.d_log2, D) + 1e-6);
     if (col) a.fin[t] = (float)((1.0 + (double)fnorm) * (double)m * inv);
   }
   mark(7);
@@ -1839,7 +1859,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   for (int l = 0; l < 4; ++l)
     if ((uint32_t)l < L) ss += (double)xl[l] * (double)xl[l];
   ss = mix_sum(col ? ss : 0.0, red, phase);
-  const double inv = 1.0 / sqrt(ss / N + 1e-6);
+  const double inv = 1.0 / sqrt(div_pow2(ss, a.n_log2, N) + 1e-6);
   mark(8);
   float pre_phi = 0.f;  // phi_pre row `lane` (lane < lanes): feeds hPre
   if constexpr (CQ) {
@@ -2016,7 +2036,8 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
     // alpha = sigmoid(rmsUnit(u) . rmsUnit(key) / sqrt(d)); block = u + alpha * value.
     double su = col ? (double)u * u : 0.0, sk = col ? (double)ekey * ekey : 0.0;
     mix_sum2(su, sk, red, phase);
-    const double iu = 1.0 / sqrt(su / D + 1e-6), ik = 1.0 / sqrt(sk / D + 1e-6);
+    const double iu = 1.0 / sqrt(div_pow2(su, a.d_log2, D) + 1e-6),
+                 ik = 1.0 / sqrt(div_pow2(sk, a.d_log2, D) + 1e-6);
     const float nu = (float)((double)u * iu), nk = (float)((double)ekey * ik);
     const double dot = mix_sum(col ? (double)nu * (double)nk : 0.0, red, phase);
     const double alpha = sigmoid_d(dot / a.sqrt_d);
@@ -2026,7 +2047,7 @@ __global__ __launch_bounds__(kMixWg) void n2_mix_kernel(MixArgs a) {
   if (col) a.blk[t] = b;
   // attentionInput = rmsNorm(block, normInput) (math.ts:16-32).
   const double sb = mix_sum(col ? (double)b * b : 0.0, red, phase);
-  const double ib = 1.0 / sqrt(sb / D + 1e-6);
+  const double ib = 1.0 / sqrt(div_pow2(sb, a.d_log2, D) + 1e-6);
   if (col) a.ain[t] = (float)((1.0 + (double)norm_in) * (double)b * ib);
   mark(11);
   if constexpr (WO) {
