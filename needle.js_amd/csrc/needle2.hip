@@ -1489,12 +1489,11 @@ constexpr int kPhiPairs = 8;
 // launch), then waits until the projection workgroups of its KV head (its
 // query and gate heads, key and value) have counted in on its counter (q,
 // this position's cache rows and the gate are in the XCD's L2), reads
-// the fresh rows again past its L1 (counting itself in at the end; the last
-// clears the count),
-// and runs the gated attention of the KV head with nd_launch_attention_gated's
+// the fresh rows again past its L1, runs the gated attention of the KV head with nd_launch_attention_gated's
 // instance and arguments for a ring of at most kGatedChunk positions -- the
-// same values in the same order, so the same bits.  A wait that runs out
-// sets kStatusAttWait; an abort from the projection stores nothing.
+// same values in the same order, so the same bits -- and clears its counter
+// for the next launch.  A wait that runs out sets kStatusAttWait; an abort
+// from the projection stores nothing.
 // (The hook holds copies of the launch arguments it needs: the address of
 // the argument block itself would cost a private copy of it.)
 // STAMP: thread 0 writes the clock to marks[i] (LDS): 0 when the wait
@@ -1506,7 +1505,7 @@ struct AttWaitT {
   uint32_t* count;
   uint32_t* status;
   uint32_t* go;  // an LDS word
-  uint32_t target, groups, spin, slot;
+  uint32_t target, spin, slot;
   uint64_t* marks;
   __device__ void mark(int i) const {
     if constexpr (STAMP) {
@@ -1536,12 +1535,14 @@ struct AttWaitT {
     return *go != 0;
   }
   __device__ uint32_t fresh_slot() const { return slot; }
-  // After the attention (off its path): thread 0 counts the workgroup in;
-  // the last of them clears the count for the next launch.
+  // After the attention: clear the count for the next launch.  The
+  // workgroup is its counter's one waiter, and every arrival
+  // it waited for has landed, so a plain store does it, with no returning
+  // atomic (a round trip through the L2) at the end of the launch's last
+  // workgroups.  (After an abort, arrivals may still land; the status bit
+  // is then set and the next reset clears the counters.)
   __device__ void release() const {
-    if (threadIdx.x == 0 &&
-        (__hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) &
-         kFlagCount) == target + groups - 1)
+    if (threadIdx.x == 0)
       __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 };
@@ -1554,7 +1555,7 @@ __device__ __forceinline__ void attention_role(const MixArgs& a, uint32_t ah,
                                                uint64_t* marks = nullptr) {
   __shared__ uint32_t s_att_go;
   const AttArgs& g = a.att;
-  const AttWaitT<STAMP> w{a.att_count + kAttStride * ah, a.status, &s_att_go, a.att_target, 1u,
+  const AttWaitT<STAMP> w{a.att_count + kAttStride * ah, a.status, &s_att_go, a.att_target,
                           a.spin, kv_slot(g.position[0], g.sink, g.window), marks};
   nd::att::attention_body<2, false, false, kMixWg / 64, 1, false, false, false, AttWaitT<STAMP>>(
       0u, ah, 0u, g.Kc, g.Vc, g.Ks, g.Vs, g.q, g.out, g.gate, 0u, nullptr, nullptr, nullptr,
