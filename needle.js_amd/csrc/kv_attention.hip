@@ -519,18 +519,23 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
   // L % 8 on one XCD), confirmed per device when the context is created;
   // without it the chunks merge at the agent coherence point (last form).
   const bool xcd = nd_xcd_local();
-  if (xcd && a.batch == 1 && max_chunks > 1 && a.seq_kv_heads * max_chunks < kTargetSingle) {
-    // One row whose 256-position chunks leave the launch short of
-    // kTargetSingle workgroups (8 heads x 2048: 64): two-wave workgroups on
-    // 128-position chunks double them (5.85 against 6.28 us at 2048; at
-    // 8192, already 256 workgroups, the four-wave form stays faster).
+  if (xcd && max_chunks > 1 && (a.batch > 1 || a.seq_kv_heads * max_chunks < kTargetSingle)) {
+    // Two-wave workgroups on 128-position chunks.  One row whose
+    // 256-position chunks leave the launch short of kTargetSingle workgroups
+    // (8 heads x 2048: 64) gets twice as many (5.85 against 6.28 us at 2048;
+    // at 8192, already 256 workgroups, the four-wave form stays faster).  A
+    // batch takes them whenever its rows fit 64 such chunks: ragged rows
+    // spread more evenly (64 rows of 32..2048 positions: 0.397 against
+    // 0.401 ms per decode step).
     constexpr uint32_t kHalf = kWavePositions * 2;
-    const uint32_t cp2 = chunk_positions_for(a.max_count, a.seq_kv_heads, kTargetSingle, kHalf);
+    const uint32_t cp2 = a.batch == 1
+                             ? chunk_positions_for(a.max_count, a.seq_kv_heads, kTargetSingle, kHalf)
+                             : kHalf;
     const uint32_t mc2 = (a.max_count + cp2 - 1) / cp2;
     if (cp2 == kHalf && mc2 <= kMaxChunks) {
       if (a.stamps) return hipErrorInvalidValue;  // no measurement form of the two-wave kernel
-      float* pm2 = a.partials + (size_t)hq * mc2 * kHeadDim;
-      const uint32_t gpx = (a.seq_kv_heads + 7) / 8;
+      float* pm2 = a.partials + (size_t)a.batch * hq * mc2 * kHeadDim;
+      const uint32_t gpx = (a.batch * a.seq_kv_heads + 7) / 8;
       hipLaunchKernelGGL((attention_kernel<REP, F32, false, 2, 1, true>), dim3(8 * gpx * mc2),
                          dim3(64 * 2), 0, s, a.kv->k, a.kv->v, a.kv->ks, a.kv->vs, a.q, a.out,
                          a.gate, a.gate_ld, part_acc, pm2, a.counters, a.layer, a.kv->kv_heads,
@@ -652,7 +657,7 @@ size_t nd_attention_partial_floats(uint32_t q_heads, uint32_t kv_heads, uint32_t
 
 size_t nd_attention_batch_partial_floats(uint32_t batch, uint32_t seq_kv_heads, uint32_t rep,
                                          uint32_t max_count) {
-  const uint32_t unit = batch == 1 ? kWavePositions * 2 : kMinChunk;
+  const uint32_t unit = kWavePositions * 2;  // the two-wave form's chunks
   return (size_t)batch * seq_kv_heads * rep * ((max_count + unit - 1) / unit) * (kHeadDim + 2);
 }
 
