@@ -607,8 +607,11 @@ nd_status nd_needle_step_launches(nd_ctx* ctx, nd_needle* model, uint32_t* launc
  * the projection, and at exit to stamps_dev[(64 l + k) x 16 .. + 3], and
  * the mix workgroup after its post norms, each FWHT, the lane update, the
  * pre norm, the phi products, the engram gate and the input norm to words
- * 4 .. 11; a Wo workgroup when its input and its weights had arrived and
- * its rows were stored to words 4 .. 6; a projection workgroup when its
+ * 4 .. 11, and inside the phi products to words 12 .. 14 (int8: the fp16
+ * split in LDS, the MFMA chain, the partial rows; Cactus-Quant: the lanes
+ * staged, rotated, the rows done); an int8 Wo workgroup when its input and
+ * its weights had arrived and its rows were stored to words 4 .. 6 (a
+ * Cactus-Quant one: input staged, rows computed, rows stored); a projection workgroup when its
  * wait ended, its input was staged, its rows were computed and its stores had completed to words
  * 4 .. 7; an attention workgroup when its wait ended, q and the gates were
  * issued, the tile math and the waves' combine were done and its output
