@@ -565,6 +565,19 @@ hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) {
     return hipGetLastError();
   }
   if (a.stamps) return hipErrorInvalidValue;
+  if constexpr (REP <= 2 && !F32) {
+    if (max_chunks == 1 && tiles == 2) {
+      // One 512-position chunk per (row, KV head): eight waves of one tile
+      // each instead of four of two.
+      hipLaunchKernelGGL((attention_kernel<REP, F32, false, 8, 1>),
+                         dim3(1, a.seq_kv_heads, a.batch), dim3(64 * 8), 0, s, a.kv->k, a.kv->v,
+                         a.kv->ks, a.kv->vs, a.q, a.out, a.gate, a.gate_ld, part_acc, part_ml,
+                         a.counters, a.layer, a.kv->kv_heads, a.kv->alloc, a.kv->sink,
+                         a.kv->window, a.vis, a.positions, a.slot_space, a.seq_kv_heads,
+                         a.kv_stride_z, cp, max_chunks, 0.125f, a.batch, 1u, nullptr);
+      return hipGetLastError();
+    }
+  }
   auto kernel = tiles == 1   ? attention_kernel<REP, F32, false, kWaves, 1>
                 : tiles == 2 ? attention_kernel<REP, F32, false, kWaves, 2>
                              : attention_kernel<REP, F32, false, kWaves, 0>;
