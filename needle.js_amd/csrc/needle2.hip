@@ -570,7 +570,19 @@ __device__ __forceinline__ void cq_rows_load(const CqRows& q, uint32_t bits, siz
 __device__ __forceinline__ float cq_rotate_lanes(float v, uint32_t g, uint32_t lane) {
   auto stage = [&](auto m) {
     constexpr int M = decltype(m)::value;
-    const float other = nd::lane_xor<M>(v);
+    float other;
+    if constexpr (M >= 16) {
+      // Lane i ^ M through gfx950's row / half swaps (VALU): given the value
+      // twice, the 16-swap returns {rows 0, 0, 2, 2; rows 1, 1, 3, 3} and the
+      // 32-swap {lanes 0..31 twice; lanes 32..63 twice}.
+      const auto r = M == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(v),
+                                                                __float_as_uint(v), false, false)
+                             : __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+                                                                __float_as_uint(v), false, false);
+      other = __uint_as_float((lane & M) ? r[0] : r[1]);
+    } else {
+      other = nd::lane_xor<M>(v);
+    }
     v = (lane & M) ? other - v : v + other;
   };
   if (g > 1) stage(std::integral_constant<int, 1>{});
