@@ -594,15 +594,15 @@ __device__ __forceinline__ float cq_rotate_lanes(float v, uint32_t g, uint32_t l
   return v;
 }
 
-// x (d <= kpad <= 512 values, zeros past d) into xs for cq_rows_dot, by a
-// 512-thread workgroup, one element per thread: element e at e + e / 32 (one
-// pad float after every 32, so that the 16 units' reads fall in distinct
-// banks), the strides below min(g, 64) of the per-group rotation applied
-// (cq_rotate_lanes).  The caller's barrier publishes xs.
-__device__ __forceinline__ void cq_stage_rotated(const float* x, uint32_t d, uint32_t kpad,
-                                                 uint32_t g, float* xs, uint32_t t) {
+// x (kpad <= 512 values: v is thread t's element, zero past the input)
+// into xs for cq_rows_dot, by a 512-thread workgroup, one element per
+// thread: element e at e + e / 32 (one pad float after every 32, so that the
+// 16 units' reads fall in distinct banks), the strides below min(g, 64) of
+// the per-group rotation applied (cq_rotate_lanes).  The caller's barrier
+// publishes xs.
+__device__ __forceinline__ void cq_stage_rotated(float v, uint32_t kpad, uint32_t g, float* xs,
+                                                 uint32_t t) {
   static_assert(kQkvWg == 512 && kMixWg == 512, "one input element per thread");
-  float v = t < d ? x[t] : 0.f;
   v = cq_rotate_lanes(v, g, t & 63);
   if (t < kpad) xs[t + (t >> 5)] = v;
 }
@@ -907,7 +907,7 @@ __device__ __forceinline__ void qkv_body(const QkvParams& p, uint32_t b, uint32_
       release();
       return;
     }
-    cq_stage_rotated(p.x, d, kpad, q.g, xs, t);
+    cq_stage_rotated(t < d ? p.x[t] : 0.f, kpad, q.g, xs, t);
     __syncthreads();
     mark(1);
     const float2 v = cq_rows_dot_any(bits, q, R, kpad / 32, xs, s_cb, t);
@@ -976,13 +976,19 @@ __device__ __forceinline__ void wo_cq_rows(const WoCq& w, uint32_t k, uint32_t* 
     }
   };
   const uint32_t kpad = w.cq.groups << w.cq.g_log2;  // the padded row (<= 512)
-  CqRowRegs R;  // the rows' packed words and norms first
+  // The input first (it is in the L2), then the rows' packed words and
+  // norms: the rotation's wait for the input then leaves the weight loads in
+  // flight.
+  const float xv = t < w.k ? w.x[t] : 0.f;
+  __builtin_amdgcn_sched_barrier(0);
+  CqRowRegs R;
   cq_rows_load(w.cq, BITS, (size_t)k * 64, kpad / 32, t, R);
+  __builtin_amdgcn_sched_barrier(0);
   if (t == 0) {  // constant indices into the argument block
 #pragma unroll
     for (int i = 0; i < 16; ++i) s_cb[i] = w.cq.cb[i];
   }
-  cq_stage_rotated(w.x, w.k, kpad, w.cq.g, xs, t);
+  cq_stage_rotated(xv, kpad, w.cq.g, xs, t);
   __syncthreads();
   mark(0);
   const float2 v = cq_rows_dot_g<BITS>(w.cq, R, kpad / 32, xs, s_cb, t);
