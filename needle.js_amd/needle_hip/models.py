@@ -1,7 +1,7 @@
 """Synthetic int8 decoder (weights, HBM-resident decoder, batched sessions).
 
-The decoder is the one BASELINE's batched constrained-decode and prefill
-workloads name (8 layers, d_model 512, 8 heads x 64, FFN 2048, int8 weights
+The decoder is the synthetic model of the batched constrained-decode and
+prefill workloads (8 layers, d_model 512, 8 heads x 64, FFN 2048, int8 weights
 with per-row fp32 scales, vocab 32768), composed from the reference's own
 per-token primitives -- the layer recipe is spelled out in
 include/needle_hip.h (nd_decoder_desc) and restated by the oracle.

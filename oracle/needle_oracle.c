@@ -749,9 +749,9 @@ void or_gen_kv_row(uint64_t seed, uint64_t index, uint32_t n, float lo, float hi
   *scale = (float)((double)lo + ((double)hi - (double)lo) * u);
 }
 
-/* ------------------------------------------ synthetic decoder (configs) */
+/* ------------------------------------------ synthetic decoder */
 
-/* BASELINE-defined decoder composed from the reference primitives: per layer
+/* The synthetic 8-layer decoder, composed from the reference primitives: per layer
  *   a = rmsNorm(x, attn_norm)                      math.ts:16-32
  *   q, k, v = Wq a, Wk a, Wv a                     cq.ts:106-156 (int8 form)
  *   per-head rmsNormSlice(q, q_norm), (k, k_norm)  runtime.ts:471-486, 647-657
@@ -966,7 +966,7 @@ void or_kv_fill_synthetic(or_kv* kv, uint64_t seed_k, uint64_t seed_v, uint32_t 
       }
 }
 
-/* Constrained batched greedy decode (BASELINE configuration 5 semantics):
+/* Constrained batched greedy decode (64 ragged sequences, a seeded allowed-token mask per step):
  * for step t and sequence b, run or_synth_step on the current token at
  * position start[b] + t, build the allowed mask with seed
  * or_splitmix64_at(mask_seed, t * 65536 + b), select with or_select_mask
