@@ -344,8 +344,8 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_fused_kernel(
   mx = fmaxf(mx, nd::lane_xor<2>(mx));
   mx = fmaxf(mx, nd::lane_xor<4>(mx));
   mx = fmaxf(mx, nd::lane_xor<8>(mx));
-  mx = fmaxf(mx, nd::lane_xor<16>(mx));
-  mx = fmaxf(mx, nd::lane_xor<32>(mx));
+  mx = nd::max_xor<16>(mx);
+  mx = nd::max_xor<32>(mx);
   if (lane == 0) s_max[wave] = mx;
   nd::lds_barrier();  // the weight loads stay in flight
   const float amax = fmaxf(s_max[2 * xb], s_max[2 * xb + 1]);
@@ -485,8 +485,8 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_slice_kernel(
   mx = fmaxf(mx, nd::lane_xor<2>(mx));
   mx = fmaxf(mx, nd::lane_xor<4>(mx));
   mx = fmaxf(mx, nd::lane_xor<8>(mx));
-  mx = fmaxf(mx, nd::lane_xor<16>(mx));
-  mx = fmaxf(mx, nd::lane_xor<32>(mx));
+  mx = nd::max_xor<16>(mx);
+  mx = nd::max_xor<32>(mx);
   if (lane == 0) s_max[wave] = mx;
   nd::lds_barrier();  // the weight loads stay in flight
   if (has_x) {

@@ -339,8 +339,8 @@ __device__ __forceinline__ void attention_body(
       // of each 16-lane row, the set lane xor 4 and 8 span
       tile_max = fmaxf(tile_max, nd::dpp<nd::kRowRor4>(tile_max));
       tile_max = fmaxf(tile_max, nd::dpp<nd::kRowRor8>(tile_max));
-      tile_max = fmaxf(tile_max, nd::lane_xor<16>(tile_max));
-      tile_max = fmaxf(tile_max, nd::lane_xor<32>(tile_max));
+      tile_max = nd::max_xor<16>(tile_max);
+      tile_max = nd::max_xor<32>(tile_max);
       const float m_new = fmaxf(m[h], tile_max);
       // 0 on the first tile with a visible position (m = -inf); 1 while no
       // position has been visible (a tile of unwritten slots: -inf - -inf).
@@ -655,8 +655,8 @@ __device__ __forceinline__ void attention_body(
         mx = fmaxf(mx, nd::lane_xor<2>(mx));
         mx = fmaxf(mx, nd::lane_xor<4>(mx));
         mx = fmaxf(mx, nd::lane_xor<8>(mx));
-        mx = fmaxf(mx, nd::lane_xor<16>(mx));
-        mx = fmaxf(mx, nd::lane_xor<32>(mx));
+        mx = nd::max_xor<16>(mx);
+        mx = nd::max_xor<32>(mx);
         f = mc == -INFINITY ? 0.f : __expf(mc - mx);
         fin_l = nd::wave_sum(f * lc);
       }

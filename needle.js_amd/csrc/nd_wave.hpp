@@ -122,6 +122,21 @@ __device__ __forceinline__ float lane_xor(float v) {
   else return __shfl_xor(v, 32, 64);
 }
 
+// max(v, v of lane i ^ m) for m = 16 or 32 through gfx950's row / half
+// swaps (VALU, no trip through the LDS unit): given the value twice, the
+// 16-swap returns {rows 0, 0, 2, 2; rows 1, 1, 3, 3} and the 32-swap {lanes
+// 0..31 twice; lanes 32..63 twice} (checked on gfx950), so the two results
+// hold each lane's value and its partner's in some order, and fmaxf does
+// not depend on the order.
+template <int M>
+__device__ __forceinline__ float max_xor(float v) {
+  static_assert(M == 16 || M == 32, "max_xor takes 16 or 32");
+  const uint32_t b = __float_as_uint(v);
+  const auto r = M == 16 ? __builtin_amdgcn_permlane16_swap(b, b, false, false)
+                         : __builtin_amdgcn_permlane32_swap(b, b, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // Workgroup barrier for hand-offs through LDS only: waits for this wave's
 // LDS (and scalar) operations, not for its global loads.  __syncthreads()
 // also fences global memory, which waits for every load still in flight --
