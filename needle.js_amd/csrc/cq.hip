@@ -329,8 +329,8 @@ __global__ __launch_bounds__(kCqThreads) void cq_matvec_kernel(
   float sum = 0.f;
 #pragma unroll
   for (int i = 0; i < RACC; ++i) sum += col[part + T * i];
-  if (T > 32) sum += nd::lane_xor<32>(sum);
-  if (T > 16) sum += nd::lane_xor<16>(sum);
+  if (T > 32) sum = nd::sum_xor<32>(sum);
+  if (T > 16) sum = nd::sum_xor<16>(sum);
   if (T > 8) sum += nd::lane_xor<8>(sum);
   if (T > 4) sum += nd::lane_xor<4>(sum);
   if (T > 2) sum += nd::lane_xor<2>(sum);

@@ -247,8 +247,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_mfma_kernel(
   for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
     for (int e = 0; e < 8; ++e) qmax = fmaxf(qmax, fabsf(qv[s2][e]));
-  qmax = fmaxf(qmax, nd::lane_xor<16>(qmax));
-  qmax = fmaxf(qmax, nd::lane_xor<32>(qmax));
+  qmax = nd::max_xor<16>(qmax);
+  qmax = nd::max_xor<32>(qmax);
   int qe = 0;
   if (qmax > 0.f && qmax <= 3.4028235e38f) frexpf(qmax, &qe);  // qmax < 2^qe
   const float qdown = ldexpf(1.f, -qe), qup = ldexpf(1.f, qe);
@@ -355,8 +355,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_mfma_kernel(
           bmax = fmaxf(bmax, v);
         }
       }
-      bmax = fmaxf(bmax, nd::lane_xor<16>(bmax));
-      bmax = fmaxf(bmax, nd::lane_xor<32>(bmax));
+      bmax = nd::max_xor<16>(bmax);
+      bmax = nd::max_xor<32>(bmax);
       const float m_new = fmaxf(m, bmax);
       // While no key has been visible m_new is -inf: subtract 0 instead, so
       // that masked scores give exp2(-inf) = 0 and alpha = 1.
@@ -410,8 +410,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_mfma_kernel(
     nd::lds_barrier();
   }
   // l over the row's four lanes; o[d][c] is dim 16 d + 4 kb + c of the row.
-  l += nd::lane_xor<16>(l);
-  l += nd::lane_xor<32>(l);
+  l = nd::sum_xor<16>(l);
+  l = nd::sum_xor<32>(l);
   // Merge: groups 1.. leave (m, l, o) in LDS (the key buffers are free),
   // group 0 combines them with its own and stores the row.
   float* xm = reinterpret_cast<float*>(&s_buf[0][0]);  // [group - 1][wq][18][64]

@@ -131,8 +131,8 @@ __device__ __forceinline__ void matvec_i8_body(
 #pragma unroll
   for (int i = 0; i < V; ++i) sum += cv[i];
   // T-lane butterfly: DPP within rows of 16, swizzle / bpermute beyond.
-  if (T > 32) sum += nd::lane_xor<32>(sum);
-  if (T > 16) sum += nd::lane_xor<16>(sum);
+  if (T > 32) sum = nd::sum_xor<32>(sum);
+  if (T > 16) sum = nd::sum_xor<16>(sum);
   if (T > 8) sum += nd::lane_xor<8>(sum);
   if (T > 4) sum += nd::lane_xor<4>(sum);
   if (T > 2) sum += nd::lane_xor<2>(sum);
@@ -232,7 +232,7 @@ __device__ __forceinline__ void mfma_reduce_store(float4v acc, float* red, uint3
   float sum = 0.f;
 #pragma unroll
   for (uint32_t w = 0; w < kMfmaWaves; ++w) sum += red[(w * 4 + wave) * 64 + lane];
-  sum += nd::lane_xor<32>(sum);
+  sum = nd::sum_xor<32>(sum);
   const uint32_t b = (lane >> 4) * 4 + wave, row = row0 + (lane & 15);
   if (lane < 32 && row < row_count && b < bc) Y[(size_t)b * y_stride + row] = sum;
 }
@@ -547,7 +547,7 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void matvec_mfma_slice_kernel(
   float sum = 0.f;
 #pragma unroll
   for (uint32_t q = 0; q < 4; ++q) sum += red[((4 * q + ot) * 4 + oc) * 64 + lane];
-  sum += nd::lane_xor<32>(sum);
+  sum = nd::sum_xor<32>(sum);
   const uint32_t b = (lane >> 4) * 4 + oc, orow = row0 + 16 * ot + (lane & 15);
   if (lane < 32 && orow < row_count && b < bc) {
     float* const pp = P + ((size_t)slice * kSplitRows + b) * row_count + orow;

@@ -137,6 +137,18 @@ __device__ __forceinline__ float max_xor(float v) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// v + (v of lane i ^ m) for m = 16 or 32 through the same swaps: each lane
+// adds its own value and its partner's, in one order or the other, which an
+// fp32 add does not depend on -- the same sums as v + lane_xor<m>(v).
+template <int M>
+__device__ __forceinline__ float sum_xor(float v) {
+  static_assert(M == 16 || M == 32, "sum_xor takes 16 or 32");
+  const uint32_t b = __float_as_uint(v);
+  const auto r = M == 16 ? __builtin_amdgcn_permlane16_swap(b, b, false, false)
+                         : __builtin_amdgcn_permlane32_swap(b, b, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Workgroup barrier for hand-offs through LDS only: waits for this wave's
 // LDS (and scalar) operations, not for its global loads.  __syncthreads()
 // also fences global memory, which waits for every load still in flight --

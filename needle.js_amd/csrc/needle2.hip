@@ -1193,8 +1193,8 @@ __device__ __forceinline__ void wo_rows(const MixArgs& a, uint32_t k, uint64_t* 
   }
   float sum = 0.f;
   sum += fmaf(sv, d, 0.f);
-  if (tpr > 32) sum += nd::lane_xor<32>(sum);
-  if (tpr > 16) sum += nd::lane_xor<16>(sum);
+  if (tpr > 32) sum = nd::sum_xor<32>(sum);
+  if (tpr > 16) sum = nd::sum_xor<16>(sum);
   if (tpr > 8) sum += nd::lane_xor<8>(sum);
   if (tpr > 4) sum += nd::lane_xor<4>(sum);
   if (tpr > 2) sum += nd::lane_xor<2>(sum);
