@@ -567,22 +567,27 @@ __device__ __forceinline__ void cq_rows_load(const CqRows& q, uint32_t bits, siz
 // stride s pairs lane i with lane i ^ s, the lower lane takes a + b and the
 // upper a - b of the reference's two operands (a the lower element), one
 // fp32 add or subtract each.  Every lane of the wave must take part.
+// The value of lane (lane ^ M): DPP below 16; for 16 and 32 gfx950's row /
+// half swaps (VALU): given the value twice, the 16-swap returns {rows 0, 0,
+// 2, 2; rows 1, 1, 3, 3} and the 32-swap {lanes 0..31 twice; lanes 32..63
+// twice}.
+template <int M>
+__device__ __forceinline__ float xor_partner(float v, uint32_t lane) {
+  if constexpr (M >= 16) {
+    const auto r = M == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(v),
+                                                              __float_as_uint(v), false, false)
+                           : __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+                                                              __float_as_uint(v), false, false);
+    return __uint_as_float((lane & M) ? r[0] : r[1]);
+  } else {
+    return nd::lane_xor<M>(v);
+  }
+}
+
 __device__ __forceinline__ float cq_rotate_lanes(float v, uint32_t g, uint32_t lane) {
   auto stage = [&](auto m) {
     constexpr int M = decltype(m)::value;
-    float other;
-    if constexpr (M >= 16) {
-      // Lane i ^ M through gfx950's row / half swaps (VALU): given the value
-      // twice, the 16-swap returns {rows 0, 0, 2, 2; rows 1, 1, 3, 3} and the
-      // 32-swap {lanes 0..31 twice; lanes 32..63 twice}.
-      const auto r = M == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(v),
-                                                                __float_as_uint(v), false, false)
-                             : __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
-                                                                __float_as_uint(v), false, false);
-      other = __uint_as_float((lane & M) ? r[0] : r[1]);
-    } else {
-      other = nd::lane_xor<M>(v);
-    }
+    const float other = xor_partner<M>(v, lane);
     v = (lane & M) ? other - v : v + other;
   };
   if (g > 1) stage(std::integral_constant<int, 1>{});
@@ -1304,8 +1309,8 @@ __device__ float fwht_block(float v, float* hv, uint32_t H, uint32_t t) {
   if (H > 2) v = butterfly(v, nd::dpp<nd::kQuadXor2>(v), t & 2);
   if (H > 4) v = butterfly(v, nd::lane_xor<4>(v), t & 4);
   if (H > 8) v = butterfly(v, nd::lane_xor<8>(v), t & 8);
-  if (H > 16) v = butterfly(v, nd::lane_xor<16>(v), t & 16);
-  if (H > 32) v = butterfly(v, nd::lane_xor<32>(v), t & 32);
+  if (H > 16) v = butterfly(v, xor_partner<16>(v, t), t & 16);
+  if (H > 32) v = butterfly(v, xor_partner<32>(v, t), t & 32);
   if (H <= 64) return v;
   hv[t] = v;
   nd::lds_barrier();
