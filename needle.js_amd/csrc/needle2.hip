@@ -432,6 +432,23 @@ __device__ void route_wave(const RouteArgs& r, uint32_t lane, float* lds) {
   if (lane < L) r.route[L * L + lane] = hp;
 }
 
+// The value of lane (lane ^ M): DPP below 16; for 16 and 32 gfx950's row /
+// half swaps (VALU): given the value twice, the 16-swap returns {rows 0, 0,
+// 2, 2; rows 1, 1, 3, 3} and the 32-swap {lanes 0..31 twice; lanes 32..63
+// twice}.
+template <int M>
+__device__ __forceinline__ float xor_partner(float v, uint32_t lane) {
+  if constexpr (M >= 16) {
+    const auto r = M == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(v),
+                                                              __float_as_uint(v), false, false)
+                           : __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+                                                              __float_as_uint(v), false, false);
+    return __uint_as_float((lane & M) ? r[0] : r[1]);
+  } else {
+    return nd::lane_xor<M>(v);
+  }
+}
+
 // One head of the projection epilogue, one wave, lane = dimension: role 0
 // (query) and 1 (key) take the per-head rmsNorm with their scale and the
 // half-split RoPE by (sin, cos) of the lane's angle (runtime.ts:471-500,
@@ -448,8 +465,8 @@ __device__ __forceinline__ void head_epilogue(float val, uint32_t lane, int role
     const double xd = val;
     const double ss = nd::wave_sum(xd * xd);
     const double inv = 1.0 / sqrt(ss / kHd + 1e-6);
-    const double normed = (float)((1.0 + (double)nscale) * xd * inv);
-    const double other = __shfl_xor(normed, 32, 64);
+    const float nf = (float)((1.0 + (double)nscale) * xd * inv);
+    const double normed = nf, other = xor_partner<32>(nf, lane);  // float values, exact in double
     out = lane < 32 ? (float)(normed * cs - other * sn) : (float)(normed * cs + other * sn);
     if (role == 0) {
       q_dst[lane] = out;
@@ -567,23 +584,6 @@ __device__ __forceinline__ void cq_rows_load(const CqRows& q, uint32_t bits, siz
 // stride s pairs lane i with lane i ^ s, the lower lane takes a + b and the
 // upper a - b of the reference's two operands (a the lower element), one
 // fp32 add or subtract each.  Every lane of the wave must take part.
-// The value of lane (lane ^ M): DPP below 16; for 16 and 32 gfx950's row /
-// half swaps (VALU): given the value twice, the 16-swap returns {rows 0, 0,
-// 2, 2; rows 1, 1, 3, 3} and the 32-swap {lanes 0..31 twice; lanes 32..63
-// twice}.
-template <int M>
-__device__ __forceinline__ float xor_partner(float v, uint32_t lane) {
-  if constexpr (M >= 16) {
-    const auto r = M == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(v),
-                                                              __float_as_uint(v), false, false)
-                           : __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
-                                                              __float_as_uint(v), false, false);
-    return __uint_as_float((lane & M) ? r[0] : r[1]);
-  } else {
-    return nd::lane_xor<M>(v);
-  }
-}
-
 __device__ __forceinline__ float cq_rotate_lanes(float v, uint32_t g, uint32_t lane) {
   auto stage = [&](auto m) {
     constexpr int M = decltype(m)::value;
